@@ -1,0 +1,529 @@
+// Dense GEMM for gfx950: C[M,N] = A[M,K] · B[K,N], row-major, fp32 accumulation on MFMA.
+//
+// Semantics follow Frame's matmul (reference: src/backends/cpu/kernels/matmul.cpp:92-185): dtype in = out,
+// products accumulated in fp32, one round-to-nearest-even store. The optional epilogue applies the
+// elementwise segments Frame's graph would run next (bias add, ReLU, ...) on the rounded product before
+// the single store, rounding between segments exactly like the unfused graph.
+//
+// Tile kernel layout (one workgroup = 4 waves = 256 threads):
+//   * Block tile BM x BN, K staged in slices of 128 bytes per row (64 bf16/f16 or 32 fp32 values).
+//   * A slice is stored in LDS row-major [BM][128 B]; B slice is stored transposed [BN][128 B] so both MFMA
+//     operands read 16-byte k-contiguous fragments. B is transposed in registers (E x E blocks) between
+//     the global load and the LDS store, so global reads stay fully coalesced.
+//   * Every 16-byte chunk is XOR-swizzled inside its row by ((row ^ row>>3) & 7): fragment reads, A stores
+//     and transposed B stores are all bank-conflict free.
+//   * Two LDS stages: the global loads of slice k+1 are in flight while the MFMAs consume slice k.
+//   * Waves are laid out 2 x 2; each owns a (BM/2) x (BN/2) sub-tile of 32x32 MFMA tiles.
+//   * Workgroup ids are remapped so that consecutive tiles land on the same XCD (blocks are dispatched
+//     round-robin over the 8 XCDs) and tiles are visited in groups of rows for L2 reuse.
+#include <hip/hip_runtime.h>
+
+#include <string>
+
+#include "fh_common.h"
+
+namespace fh {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+template <typename T>
+struct GemmTraits;
+template <>
+struct GemmTraits<bf16_t> {
+  static constexpr int E = 8;  // elements per 16-byte chunk
+};
+template <>
+struct GemmTraits<f16_t> {
+  static constexpr int E = 8;
+};
+template <>
+struct GemmTraits<float> {
+  static constexpr int E = 4;
+};
+
+struct EpilogueArgs {
+  int32_t nseg;
+  int32_t round_between;
+  uint8_t ops[FH_MAX_SEGMENTS];
+  const void* ins[FH_MAX_SEGMENTS];
+};
+
+struct GemmArgs {
+  const void* A;
+  const void* B;
+  void* C;
+  int64_t M, N, K;
+  int64_t lda, ldb, ldc;             // row strides in elements
+  int64_t stride_a, stride_b, stride_c;  // batch strides in elements (blockIdx.y)
+  int32_t tiles_m, tiles_n;
+  EpilogueArgs ep;
+};
+
+__device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row ^ (row >> 3)) & 7); }
+
+// Applies the epilogue program to one rounded product value at (row, col).
+template <typename T>
+__device__ __forceinline__ float apply_epilogue(const EpilogueArgs& ep, float v, int64_t idx) {
+  using S = typename Io<T>::storage;
+  for (int s = 0; s < ep.nseg; ++s) {
+    const uint8_t op = ep.ops[s];
+    if (ew_is_binary(op)) {
+      const float e = Io<T>::load(static_cast<const S*>(ep.ins[s])[idx]);
+      v = ew_binary(op, v, e);
+    } else {
+      v = ew_unary(op, v);
+    }
+    if (ep.round_between) v = Io<T>::round(v);
+  }
+  return v;
+}
+
+// Transposes an E x E block of 16-bit values held as E rows of 16 bytes.
+__device__ __forceinline__ void transpose8x8_u16(const uint4 (&in)[8], uint4 (&out)[8]) {
+  const uint32_t* src = reinterpret_cast<const uint32_t*>(in);  // src[r*4 + d]
+  uint32_t* dst = reinterpret_cast<uint32_t*>(out);
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t a = src[(2 * q) * 4 + (c >> 1)];
+      const uint32_t b = src[(2 * q + 1) * 4 + (c >> 1)];
+      dst[c * 4 + q] = (c & 1) ? ((a >> 16) | (b & 0xffff0000u)) : ((a & 0xffffu) | (b << 16));
+    }
+  }
+}
+
+__device__ __forceinline__ void transpose4x4_u32(const uint4 (&in)[4], uint4 (&out)[4]) {
+  const uint32_t* src = reinterpret_cast<const uint32_t*>(in);
+  uint32_t* dst = reinterpret_cast<uint32_t*>(out);
+#pragma unroll
+  for (int c = 0; c < 4; ++c)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dst[c * 4 + r] = src[r * 4 + c];
+}
+
+template <typename T>
+__device__ __forceinline__ void mfma_step(const uint4& a, const uint4& b, f32x16_t& acc);
+
+template <>
+__device__ __forceinline__ void mfma_step<bf16_t>(const uint4& a, const uint4& b, f32x16_t& acc) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                acc, 0, 0, 0);
+}
+template <>
+__device__ __forceinline__ void mfma_step<f16_t>(const uint4& a, const uint4& b, f32x16_t& acc) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b),
+                                               acc, 0, 0, 0);
+}
+// fp32: one 16-byte chunk holds 4 k-values; lane halves read different chunks and both operands use the
+// same k assignment, so four 32x32x2 MFMAs consume the pair of chunks.
+template <>
+__device__ __forceinline__ void mfma_step<float>(const uint4& a, const uint4& b, f32x16_t& acc) {
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.x), __uint_as_float(b.x), acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.y), __uint_as_float(b.y), acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.z), __uint_as_float(b.z), acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a.w), __uint_as_float(b.w), acc, 0, 0, 0);
+}
+
+template <typename T, int BM, int BN, bool kGuard>
+__global__ __launch_bounds__(256) void gemm_tile_kernel(GemmArgs args) {
+  using S = typename Io<T>::storage;
+  constexpr int E = GemmTraits<T>::E;
+  constexpr int BK = 8 * E;  // 128 bytes of K per row
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int A_LOADS = BM * 8 / 256;
+  constexpr int B_BLOCKS = 8 * BN / E;  // E x E blocks in a K slice
+  constexpr int B_ITERS = (B_BLOCKS + 255) / 256;
+  constexpr int NB_PER_ROW = BN / E;
+  static_assert(A_LOADS >= 1, "BM too small");
+
+  __shared__ uint4 lds[2][(BM + BN) * 8];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+
+  // --- tile scheduling: XCD-aware remap, then grouped row-major order ---
+  const int tiles = args.tiles_m * args.tiles_n;
+  int bid = blockIdx.x;
+  if ((tiles & 7) == 0) bid = (bid & 7) * (tiles >> 3) + (bid >> 3);
+  constexpr int GROUP_M = 4;
+  const int group = bid / (GROUP_M * args.tiles_n);
+  const int first_m = group * GROUP_M;
+  const int gsize = min(args.tiles_m - first_m, GROUP_M);
+  const int tm = first_m + (bid % gsize);
+  const int tn = (bid % (GROUP_M * args.tiles_n)) / gsize;
+  const int64_t m0 = static_cast<int64_t>(tm) * BM;
+  const int64_t n0 = static_cast<int64_t>(tn) * BN;
+
+  const S* __restrict__ A = static_cast<const S*>(args.A) + blockIdx.y * args.stride_a;
+  const S* __restrict__ B = static_cast<const S*>(args.B) + blockIdx.y * args.stride_b;
+  S* __restrict__ C = static_cast<S*>(args.C) + blockIdx.y * args.stride_c;
+  const int64_t M = args.M, N = args.N, K = args.K;
+  const int64_t lda = args.lda, ldb = args.ldb, ldc = args.ldc;
+
+  uint4 ra[A_LOADS];
+  uint4 rb[B_ITERS][E];
+
+  auto load_slice = [&](int kt) {
+    const int64_t k0 = static_cast<int64_t>(kt) * BK;
+#pragma unroll
+    for (int i = 0; i < A_LOADS; ++i) {
+      const int id = tid + 256 * i;
+      const int row = id >> 3, c = id & 7;
+      const int64_t gr = m0 + row, gk = k0 + c * E;
+      if (!kGuard || (gr < M && gk < K)) {
+        ra[i] = *reinterpret_cast<const uint4*>(A + gr * lda + gk);
+      } else {
+        ra[i] = make_uint4(0, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < B_ITERS; ++j) {
+      const int blk = tid + 256 * j;
+      const int kb = blk / NB_PER_ROW, nb = blk % NB_PER_ROW;
+      const int64_t gn = n0 + nb * E;
+#pragma unroll
+      for (int r = 0; r < E; ++r) {
+        const int64_t gk = k0 + kb * E + r;
+        if ((B_BLOCKS % 256 == 0 || blk < B_BLOCKS) && (!kGuard || (gk < K && gn < N))) {
+          rb[j][r] = *reinterpret_cast<const uint4*>(B + gk * ldb + gn);
+        } else {
+          rb[j][r] = make_uint4(0, 0, 0, 0);
+        }
+      }
+    }
+  };
+
+  auto store_slice = [&](int buf) {
+    uint4* As = lds[buf];
+    uint4* Bs = lds[buf] + BM * 8;
+#pragma unroll
+    for (int i = 0; i < A_LOADS; ++i) {
+      const int id = tid + 256 * i;
+      const int row = id >> 3, c = id & 7;
+      As[row * 8 + swz(row, c)] = ra[i];
+    }
+#pragma unroll
+    for (int j = 0; j < B_ITERS; ++j) {
+      const int blk = tid + 256 * j;
+      if (B_BLOCKS % 256 != 0 && blk >= B_BLOCKS) continue;
+      const int kb = blk / NB_PER_ROW, nb = blk % NB_PER_ROW;
+      uint4 t[E];
+      if constexpr (E == 8) {
+        transpose8x8_u16(rb[j], t);
+      } else {
+        transpose4x4_u32(rb[j], t);
+      }
+#pragma unroll
+      for (int c = 0; c < E; ++c) {
+        const int n = nb * E + c;
+        Bs[n * 8 + swz(n, kb)] = t[c];
+      }
+    }
+  };
+
+  f32x16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  const int KT = static_cast<int>((K + BK - 1) / BK);
+  const int half = lane >> 5;
+  const int l32 = lane & 31;
+
+  load_slice(0);
+  store_slice(0);
+  __syncthreads();
+
+  for (int kt = 0; kt < KT; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < KT) load_slice(kt + 1);
+    const uint4* As = lds[cur];
+    const uint4* Bs = lds[cur] + BM * 8;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int chunk = 2 * ks + half;
+      uint4 a[TM], b[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int row = wm * WM + i * 32 + l32;
+        a[i] = As[row * 8 + swz(row, chunk)];
+      }
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int row = wn * WN + j * 32 + l32;
+        b[j] = Bs[row * 8 + swz(row, chunk)];
+      }
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) mfma_step<T>(a[i], b[j], acc[i][j]);
+    }
+    if (kt + 1 < KT) store_slice(cur ^ 1);
+    __syncthreads();
+  }
+
+  // --- epilogue: stage the rounded tile through LDS (free after the last barrier), then each wave runs the
+  // elementwise program on 16-byte vectors and stores them coalesced. Rounding the product to T before
+  // staging loses nothing: the epilogue starts from the rounded product anyway. ---
+  constexpr int V = 16 / static_cast<int>(sizeof(S));       // elements per 16-byte vector
+  constexpr int CAP = (BM + BN) * 64 / static_cast<int>(sizeof(S));  // LDS elements owned by one wave
+  constexpr int RP_RAW = (CAP / WN) / 32 * 32;
+  constexpr int RP = RP_RAW < WM ? RP_RAW : WM;               // wave rows staged per pass
+  constexpr int PASSES = WM / RP;
+  constexpr int LPR = WN / V;                                  // lanes per staged row
+  constexpr int RPI = 64 / LPR;                                // staged rows per wave-wide access
+  static_assert(RP >= 32 && WM % RP == 0 && 64 % LPR == 0, "epilogue staging shape");
+  S* wl = reinterpret_cast<S*>(&lds[0][0]) + wave * CAP;
+#pragma unroll
+  for (int p = 0; p < PASSES; ++p) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      if (i / (RP / 32) != p) continue;
+      const int rbase = (i % (RP / 32)) * 32;
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int rr = rbase + 8 * (r >> 2) + 4 * half + (r & 3);
+          wl[rr * WN + j * 32 + l32] = Io<T>::store(acc[i][j][r]);
+        }
+    }
+    __syncthreads();
+    const int c = (lane % LPR) * V;
+    const int64_t col = n0 + wn * WN + c;
+#pragma unroll 4
+    for (int it = 0; it < RP / RPI; ++it) {
+      const int rr = it * RPI + lane / LPR;
+      const int64_t row = m0 + wm * WM + p * RP + rr;
+      if (kGuard && (row >= M || col >= N)) continue;
+      uint4 packed = *reinterpret_cast<const uint4*>(wl + rr * WN + c);
+      const int64_t idx = row * ldc + col;
+      if (args.ep.nseg > 0) {
+        S vals[V];
+        __builtin_memcpy(vals, &packed, 16);
+        float v[V];
+#pragma unroll
+        for (int e = 0; e < V; ++e) v[e] = Io<T>::load(vals[e]);
+        for (int s = 0; s < args.ep.nseg; ++s) {
+          const uint8_t op = args.ep.ops[s];
+          if (ew_is_binary(op)) {
+            const uint4 in = *reinterpret_cast<const uint4*>(static_cast<const S*>(args.ep.ins[s]) + idx);
+            S ivals[V];
+            __builtin_memcpy(ivals, &in, 16);
+#pragma unroll
+            for (int e = 0; e < V; ++e) v[e] = ew_binary(op, v[e], Io<T>::load(ivals[e]));
+          } else {
+#pragma unroll
+            for (int e = 0; e < V; ++e) v[e] = ew_unary(op, v[e]);
+          }
+          if (args.ep.round_between) {
+#pragma unroll
+            for (int e = 0; e < V; ++e) v[e] = Io<T>::round(v[e]);
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < V; ++e) vals[e] = Io<T>::store(v[e]);
+        __builtin_memcpy(&packed, vals, 16);
+      }
+      *reinterpret_cast<uint4*>(C + idx) = packed;
+    }
+    if (p + 1 < PASSES) __syncthreads();
+  }
+}
+
+// Generic fallback for shapes the tile kernel does not accept (unaligned rows, N or K not a multiple of the
+// chunk width). Plain fp32 arithmetic with k summed in increasing order, like the reference CPU kernel.
+template <typename T>
+__global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs args) {
+  using S = typename Io<T>::storage;
+  constexpr int TB = 64, KB = 16;
+  __shared__ float As[KB][TB + 1];
+  __shared__ float Bs[KB][TB + 1];
+  const S* A = static_cast<const S*>(args.A) + blockIdx.z * args.stride_a;
+  const S* B = static_cast<const S*>(args.B) + blockIdx.z * args.stride_b;
+  S* C = static_cast<S*>(args.C) + blockIdx.z * args.stride_c;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * TB;
+  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * TB;
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  float acc[4][4] = {};
+  for (int64_t k0 = 0; k0 < args.K; k0 += KB) {
+    for (int e = threadIdx.x; e < KB * TB; e += 256) {
+      const int kk = e / TB, mm = e % TB;
+      const int64_t gm = m0 + mm, gk = k0 + kk;
+      As[kk][mm] = (gm < args.M && gk < args.K) ? Io<T>::load(A[gm * args.lda + gk]) : 0.0f;
+      const int nn = e % TB;
+      const int64_t gn = n0 + nn;
+      Bs[kk][nn] = (gk < args.K && gn < args.N) ? Io<T>::load(B[gk * args.ldb + gn]) : 0.0f;
+    }
+    __syncthreads();
+    const int kmax = static_cast<int>(min<int64_t>(KB, args.K - k0));
+    for (int kk = 0; kk < kmax; ++kk) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += As[kk][ty * 4 + i] * Bs[kk][tx * 4 + j];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t row = m0 + ty * 4 + i;
+    if (row >= args.M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t col = n0 + tx * 4 + j;
+      if (col >= args.N) continue;
+      float v = Io<T>::round(acc[i][j]);
+      const int64_t idx = row * args.ldc + col;
+      if (args.ep.nseg > 0) v = apply_epilogue<T>(args.ep, v, idx);
+      C[idx] = Io<T>::store(v);
+    }
+  }
+}
+
+template <typename T, int BM, int BN>
+fh_status launch_tile(GemmArgs args, int64_t batch, hipStream_t stream) {
+  args.tiles_m = static_cast<int32_t>((args.M + BM - 1) / BM);
+  args.tiles_n = static_cast<int32_t>((args.N + BN - 1) / BN);
+  constexpr int BK = 8 * GemmTraits<T>::E;
+  const bool full = (args.M % BM == 0) && (args.N % BN == 0) && (args.K % BK == 0);
+  dim3 grid(static_cast<uint32_t>(args.tiles_m) * static_cast<uint32_t>(args.tiles_n),
+            static_cast<uint32_t>(batch));
+  if (full) {
+    hipLaunchKernelGGL((gemm_tile_kernel<T, BM, BN, false>), grid, dim3(256), 0, stream, args);
+  } else {
+    hipLaunchKernelGGL((gemm_tile_kernel<T, BM, BN, true>), grid, dim3(256), 0, stream, args);
+  }
+  return launch_status("gemm_tile_kernel launch");
+}
+
+bool epilogue_aligned(const EpilogueArgs& ep) {
+  for (int s = 0; s < ep.nseg; ++s)
+    if (ew_is_binary(ep.ops[s]) && reinterpret_cast<uintptr_t>(ep.ins[s]) % 16 != 0) return false;
+  return true;
+}
+
+template <typename T>
+fh_status dispatch_gemm(GemmArgs args, int64_t batch, hipStream_t stream) {
+  constexpr int E = GemmTraits<T>::E;
+  const size_t esz = sizeof(typename Io<T>::storage);
+  const bool aligned = (reinterpret_cast<uintptr_t>(args.A) % 16 == 0) &&
+                       (reinterpret_cast<uintptr_t>(args.B) % 16 == 0) && (args.K % E == 0) &&
+                       (args.N % E == 0) && (args.lda % E == 0) && (args.ldb % E == 0) &&
+                       ((args.stride_a * esz) % 16 == 0) && ((args.stride_b * esz) % 16 == 0) &&
+                       (reinterpret_cast<uintptr_t>(args.C) % 16 == 0) && (args.ldc % E == 0) &&
+                       ((args.stride_c * esz) % 16 == 0) && epilogue_aligned(args.ep);
+  if (!aligned) {
+    dim3 grid(static_cast<uint32_t>((args.N + 63) / 64), static_cast<uint32_t>((args.M + 63) / 64),
+              static_cast<uint32_t>(batch));
+    hipLaunchKernelGGL((gemm_generic_kernel<T>), grid, dim3(256), 0, stream, args);
+    return launch_status("gemm_generic_kernel launch");
+  }
+  const int cus = device_cu_count();
+  auto tiles = [&](int64_t t) { return ((args.M + t - 1) / t) * ((args.N + t - 1) / t) * batch; };
+  if (tiles(256) >= cus) return launch_tile<T, 256, 256>(args, batch, stream);
+  if (tiles(128) >= cus / 2) return launch_tile<T, 128, 128>(args, batch, stream);
+  return launch_tile<T, 64, 64>(args, batch, stream);
+}
+
+fh_status run_gemm(int32_t dtype, GemmArgs args, int64_t batch, hipStream_t stream) {
+  switch (dtype) {
+    case FH_F32:
+      return dispatch_gemm<float>(args, batch, stream);
+    case FH_BF16:
+      return dispatch_gemm<bf16_t>(args, batch, stream);
+    case FH_F16:
+      return dispatch_gemm<f16_t>(args, batch, stream);
+    default:
+      return fail(FH_UNIMPLEMENTED, "fh_gemm: unsupported dtype code " + std::to_string(dtype));
+  }
+}
+
+fh_status copy_epilogue(const fh_epilogue* in, EpilogueArgs& out) {
+  out = EpilogueArgs{};
+  if (in == nullptr) return FH_OK;
+  if (in->nseg < 0 || in->nseg > FH_MAX_SEGMENTS)
+    return fail(FH_INVALID_ARGUMENT, "epilogue: nseg out of range: " + std::to_string(in->nseg));
+  out.nseg = in->nseg;
+  out.round_between = in->round_between;
+  for (int s = 0; s < in->nseg; ++s) {
+    const uint8_t op = in->ops[s];
+    if (op < FH_EW_ADD || op > FH_EW_GELU)
+      return fail(FH_INVALID_ARGUMENT, "epilogue: unknown op code " + std::to_string(op));
+    if (ew_is_binary(op) && in->ins[s] == nullptr)
+      return fail(FH_INVALID_ARGUMENT, "epilogue: binary segment " + std::to_string(s) + " has no operand");
+    out.ops[s] = op;
+    out.ins[s] = in->ins[s];
+  }
+  return FH_OK;
+}
+
+}  // namespace
+
+fh_status gemm_with_epilogue_args(int32_t dtype, const void* A, const void* B, void* C, int64_t M, int64_t N,
+                                  int64_t K, const fh_epilogue* epilogue, hipStream_t stream) {
+  if (!is_supported_float(dtype)) return fail(FH_UNIMPLEMENTED, "fh_gemm: unsupported dtype");
+  if (M < 0 || N < 0 || K < 0) return fail(FH_INVALID_ARGUMENT, "fh_gemm: negative dimension");
+  if (M == 0 || N == 0) return FH_OK;
+  if (A == nullptr || B == nullptr || C == nullptr) {
+    if (K > 0 || C == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_gemm: null operand");
+  }
+  GemmArgs args{};
+  args.A = A;
+  args.B = B;
+  args.C = C;
+  args.M = M;
+  args.N = N;
+  args.K = K;
+  args.lda = K;
+  args.ldb = N;
+  args.ldc = N;
+  fh_status st = copy_epilogue(epilogue, args.ep);
+  if (st != FH_OK) return st;
+  return run_gemm(dtype, args, 1, stream);
+}
+
+}  // namespace fh
+
+extern "C" fh_status fh_gemm(int32_t dtype, const void* A, const void* B, void* C, int64_t M, int64_t N,
+                             int64_t K, const fh_epilogue* epilogue, void* stream) {
+  return fh::gemm_with_epilogue_args(dtype, A, B, C, M, N, K, epilogue, static_cast<hipStream_t>(stream));
+}
+
+extern "C" fh_status fh_gemm_batched(int32_t dtype, const void* A, const void* B, void* C, int64_t M,
+                                     int64_t N, int64_t K, int64_t lda, int64_t ldb, int64_t ldc,
+                                     int64_t stride_a, int64_t stride_b, int64_t stride_c, int64_t batch,
+                                     void* stream) {
+  using namespace fh;
+  if (!is_supported_float(dtype)) return fail(FH_UNIMPLEMENTED, "fh_gemm_batched: unsupported dtype");
+  if (M < 0 || N < 0 || K < 0 || batch < 0)
+    return fail(FH_INVALID_ARGUMENT, "fh_gemm_batched: negative dimension");
+  if (M == 0 || N == 0 || batch == 0) return FH_OK;
+  if (lda < K || ldb < N || ldc < N)
+    return fail(FH_INVALID_ARGUMENT, "fh_gemm_batched: leading dimension smaller than the row width");
+  if (batch > 65535) return fail(FH_INVALID_ARGUMENT, "fh_gemm_batched: batch above 65535");
+  GemmArgs args{};
+  args.A = A;
+  args.B = B;
+  args.C = C;
+  args.M = M;
+  args.N = N;
+  args.K = K;
+  args.lda = lda;
+  args.ldb = ldb;
+  args.ldc = ldc;
+  args.stride_a = stride_a;
+  args.stride_b = stride_b;
+  args.stride_c = stride_c;
+  return run_gemm(dtype, args, batch, static_cast<hipStream_t>(stream));
+}

@@ -1,0 +1,174 @@
+/*
+ * frame_hip_abi.h — the C ABI of the MI355X (gfx950) kernel library `libframe_hip_kernels.so`.
+ *
+ * This is the thin boundary between Frame's C++20 host side (the `hip` backend plugin: HipBackend,
+ * HipStream, HipEvent, HipAllocator, HipExecutable and its KernelFn wrappers) and hand-written HIP
+ * code. No C++ type crosses it: only plain pointers, sizes, enums and POD structs.
+ *
+ * Conventions
+ *  - Every function returns fh_status. On failure a thread-local message is available from
+ *    fh_last_error(). Codes equal frame::ErrorCode ordinals (reference: include/frame/core/status.h:18-27).
+ *  - Device pointers are caller-owned. Kernel entry points only enqueue work on `stream`
+ *    (NULL = the device's null stream); they never allocate, never free and never synchronize.
+ *  - Argument validation (shapes, alignment, dtype) happens on the host before any launch and
+ *    returns FH_INVALID_ARGUMENT / FH_UNIMPLEMENTED synchronously.
+ *  - All floating-point arithmetic is fp32; 16-bit results are rounded once to nearest-even with the
+ *    reference's quiet-NaN rule (reference: include/frame/core/dtype.h:51-131).
+ *  - Tensors are dense row-major (reference: include/frame/core/tensor.h:64-66).
+ */
+#ifndef FRAME_HIP_ABI_H_
+#define FRAME_HIP_ABI_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FH_ABI_VERSION 1
+
+typedef enum fh_status {
+  FH_OK = 0,
+  FH_INVALID_ARGUMENT = 1,
+  FH_NOT_FOUND = 2,
+  FH_UNIMPLEMENTED = 4,
+  FH_OUT_OF_MEMORY = 5,
+  FH_INTERNAL = 6,
+  FH_DEVICE_ERROR = 7
+} fh_status;
+
+/* Equal to frame::DTypeCode ordinals (reference: include/frame/core/dtype.h:17-29). */
+typedef enum fh_dtype { FH_F32 = 0, FH_F16 = 2, FH_BF16 = 3 } fh_dtype;
+
+/* Elementwise sub-op codes understood by fh_ew_program and the GEMM/conv epilogues.
+ * add/mul/relu/square are the reference's fusable ops (reference: src/ops/schemas/elementwise.cpp:667-707);
+ * gelu is this build's addition (exact erf form). */
+typedef enum fh_ew_op {
+  FH_EW_ADD = 1,
+  FH_EW_MUL = 2,
+  FH_EW_RELU = 3,
+  FH_EW_SQUARE = 4,
+  FH_EW_GELU = 5
+} fh_ew_op;
+
+#define FH_MAX_SEGMENTS 8
+#define FH_MAX_EW_INPUTS 9
+
+/* memcpy directions */
+typedef enum fh_copy_kind { FH_H2H = 0, FH_H2D = 1, FH_D2H = 2, FH_D2D = 3 } fh_copy_kind;
+
+/* ---------------------------------------------------------------------------------------------
+ * Diagnostics
+ * ------------------------------------------------------------------------------------------- */
+const char* fh_last_error(void);
+int32_t fh_abi_version(void);
+
+/* ---------------------------------------------------------------------------------------------
+ * Runtime shims behind the HAL objects.
+ * Replace: cuda_backend.cpp:42-163 (device count, cudaMalloc/cudaFree, streams, events, cudaMemcpy[Async]),
+ *          cuda_allocator.cpp:26-66, cuda_backend.cpp:118-128 (event), cuda_backend.cpp:185-204 (copy).
+ * ------------------------------------------------------------------------------------------- */
+fh_status fh_device_count(int32_t* count);
+fh_status fh_set_device(int32_t device);
+fh_status fh_malloc(void** ptr, size_t bytes, int32_t device);
+fh_status fh_free(void* ptr);
+fh_status fh_host_alloc(void** ptr, size_t bytes); /* pinned host memory */
+fh_status fh_host_free(void* ptr);
+/* stream == NULL: synchronous copy. Otherwise enqueued on `stream`. */
+fh_status fh_memcpy(void* dst, const void* src, size_t bytes, int32_t kind, void* stream);
+fh_status fh_stream_create(void** stream, int32_t device);
+fh_status fh_stream_destroy(void* stream);
+fh_status fh_stream_synchronize(void* stream);
+fh_status fh_device_synchronize(void);
+fh_status fh_event_create(void** event, int32_t device);
+fh_status fh_event_destroy(void* event);
+fh_status fh_event_record(void* event, void* stream);
+fh_status fh_stream_wait_event(void* stream, void* event);
+fh_status fh_event_query(void* event, int32_t* done);
+fh_status fh_event_synchronize(void* event);
+fh_status fh_event_elapsed_ms(void* start, void* stop, float* ms);
+
+/* ---------------------------------------------------------------------------------------------
+ * Kernels
+ * ------------------------------------------------------------------------------------------- */
+
+/* Elementwise epilogue applied to a contraction's rounded output before the single store.
+ * Segment i consumes the previous value as its first operand and, for binary ops, the next
+ * external operand from `ins` (each a dense tensor of the output's shape and dtype).
+ * When round_between != 0 each segment's result is rounded to the output dtype before the next
+ * segment reads it, which is what Frame's unfused graph computes (reference:
+ * src/ops/fused_elementwise_utils.cpp:122-206). */
+typedef struct fh_epilogue {
+  int32_t nseg; /* 0 = plain store */
+  int32_t round_between;
+  uint8_t ops[FH_MAX_SEGMENTS];
+  const void* ins[FH_MAX_SEGMENTS];
+} fh_epilogue;
+
+/* C[M,N] = A[M,K] · B[K,N] (row-major, dtype in = out, fp32 accumulate), then the epilogue.
+ * Replaces the cuBLASLt call in matmul_cuda_kernel (reference: src/backends/cuda/kernels/matmul.cpp:90-276)
+ * and the CPU semantics of matmul_compute (reference: src/backends/cpu/kernels/matmul.cpp:92-185). */
+fh_status fh_gemm(int32_t dtype, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
+                  const fh_epilogue* epilogue, void* stream);
+
+/* Batched GEMM over `batch` independent problems with element strides between problems.
+ * Used by the fused attention lowering of per-(batch, head) matmuls (no reference counterpart in one
+ * call: the reference launches one matmul per (batch, head), reference: src/nn/layers.cpp:1014-1080). */
+fh_status fh_gemm_batched(int32_t dtype, const void* A, const void* B, void* C, int64_t M, int64_t N,
+                          int64_t K, int64_t lda, int64_t ldb, int64_t ldc, int64_t stride_a,
+                          int64_t stride_b, int64_t stride_c, int64_t batch, void* stream);
+
+/* Conv2d forward, NCHW, optional [Cout] bias added inside the fp32 accumulator, then the epilogue
+ * (e.g. ReLU). geom = {N, Cin, H, W, Cout, KH, KW, stride_h, stride_w, pad_h, pad_w, groups}.
+ * Replaces cuDNN conv + cudnnAddTensor (reference: src/backends/cuda/kernels/conv.cpp:385-520) with the
+ * CPU semantics of conv2d_forward_compute (reference: src/backends/cpu/kernels/conv.cpp:223-314). */
+fh_status fh_conv2d_fwd(int32_t dtype, const void* x, const void* w, const void* bias, void* y,
+                        const int64_t geom[12], const fh_epilogue* epilogue, void* stream);
+
+/* One-pass fused elementwise program over `numel` elements.
+ * ops/arities follow the fused_elementwise_internal attrs (reference: src/ops/fused_elementwise_utils.cpp:17-120);
+ * ins are the node's external inputs in order. Single add/mul/relu nodes are programs with nseg = 1.
+ * Replaces elementwise.cu:139-360 and execute_fused_chain (reference: src/ops/fused_elementwise_utils.cpp:122-206). */
+fh_status fh_ew_program(int32_t dtype, int32_t nseg, const uint8_t* ops, const int8_t* arities,
+                        const void* const* ins, int32_t nin, void* out, int64_t numel,
+                        int32_t round_between, void* stream);
+
+/* Row softmax over the last axis of [rows, cols].
+ * Replaces cudnnSoftmaxForward (reference: src/backends/cuda/kernels/sequence.cpp:108-178);
+ * semantics of softmax_cpu_kernel (reference: src/backends/cpu/kernels/sequence.cpp:114-174). */
+fh_status fh_softmax_rows(int32_t dtype, const void* x, void* y, int64_t rows, int64_t cols, void* stream);
+
+/* Row LayerNorm: y = gamma * (x - mean) * (1 / sqrt(var + eps)) + beta.
+ * Replaces layer_norm_kernel (reference: src/backends/cuda/kernels/sequence.cu:103-160);
+ * semantics of layer_norm_cpu_kernel (reference: src/backends/cpu/kernels/sequence.cpp:182-279). */
+fh_status fh_layer_norm_rows(int32_t dtype, const void* x, const void* gamma, const void* beta, void* y,
+                             int64_t rows, int64_t cols, float eps, void* stream);
+
+/* 2-D pooling, NCHW. mode 0 = max (-inf padding, first max wins), 1 = average (include padding).
+ * geom = {N, C, H, W, KH, KW, stride_h, stride_w, pad_h, pad_w}.
+ * Replaces cudnnPoolingForward (reference: src/backends/cuda/kernels/pool.cpp:172-244);
+ * semantics of pool.cpp (reference: src/backends/cpu/kernels/pool.cpp:8-350). */
+fh_status fh_pool2d(int32_t dtype, int32_t mode, const void* x, void* y, const int64_t geom[10], void* stream);
+
+/* out[i0..] = x[perm-gathered], rank <= 8, itemsize in {1,2,4,8}. out_dims are the output dims;
+ * in_strides_permuted[d] is the input element stride of the input axis that output axis d reads.
+ * Replaces transpose_kernel (reference: src/backends/cuda/kernels/shape.cu:65-192). */
+fh_status fh_permute(int32_t itemsize, const void* x, void* y, int32_t rank, const int64_t* out_dims,
+                     const int64_t* in_strides_permuted, void* stream);
+
+/* Strided 2-D byte copy (rows of width_bytes). Backs slice/concat/reshape.
+ * Replaces the per-segment cudaMemcpyAsync loops (reference: src/backends/cuda/kernels/shape.cpp:52-355). */
+fh_status fh_copy2d(void* dst, int64_t dst_pitch, const void* src, int64_t src_pitch, int64_t width_bytes,
+                    int64_t rows, void* stream);
+
+/* Fill `count` elements of `itemsize` bytes with the bit pattern `pattern` (little-endian low bytes).
+ * Used for constant materialisation (reference: src/backends/cuda/kernels/constant.cpp:23-73) and to clear
+ * memory without hipMemsetAsync. */
+fh_status fh_fill(void* dst, int32_t itemsize, uint64_t pattern, int64_t count, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FRAME_HIP_ABI_H_ */

@@ -1,0 +1,80 @@
+/*
+ * TEST INFRASTRUCTURE — the parity oracle. Only tests/, __graft_entry__.smoke() and bench.py's
+ * cpu_baseline leg may load this library; the product (frame-public_amd/) never links or calls it.
+ *
+ * A single-threaded C++ restatement of the arithmetic of Frame's reference CPU backend for the compiled-graph
+ * forward path. Every function cites the reference file:line it follows. Summation orders, the position of
+ * every rounding and the special-value behaviour (NaN, -0.0, padding) are kept identical so that, given the
+ * same inputs, the outputs are bit-identical to the reference CPU kernels (pinned by tests/test_oracle_*.py
+ * against oracle/_ref, the reference built from its own sources, and against the reference tests' known
+ * answers).
+ *
+ * dtype codes follow frame::DTypeCode: 0 = float32, 2 = float16, 3 = bfloat16. Buffers are host memory,
+ * dense row-major. Return value 0 = success, non-zero = invalid arguments.
+ */
+#ifndef FRAME_ORACLE_CPU_KERNELS_H_
+#define FRAME_ORACLE_CPU_KERNELS_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype bridge (reference: include/frame/core/dtype.h:51-131) */
+uint16_t oracle_float_to_bf16(float v);
+float oracle_bf16_to_float(uint16_t b);
+uint16_t oracle_float_to_f16(float v);
+float oracle_f16_to_float(uint16_t h);
+void oracle_f32_to_bf16_array(const float* in, uint16_t* out, int64_t n);
+void oracle_f32_to_f16_array(const float* in, uint16_t* out, int64_t n);
+
+/* matmul (reference: src/backends/cpu/kernels/matmul.cpp:92-129) */
+int oracle_matmul(int dtype, const void* a, const void* b, void* c, int64_t m, int64_t n, int64_t k);
+/* The same per-element formula evaluated only at (rows[i], cols[i]); out holds `count` values of dtype. */
+int oracle_matmul_sample(int dtype, const void* a, const void* b, int64_t m, int64_t n, int64_t k,
+                         const int64_t* rows, const int64_t* cols, int64_t count, void* out);
+
+/* conv2d forward (reference: src/backends/cpu/kernels/conv.cpp:174-251).
+ * geom = {N, Cin, H, W, Cout, KH, KW, stride_h, stride_w, pad_h, pad_w, groups}; bias may be NULL. */
+int oracle_conv2d(int dtype, const void* x, const void* w, const void* bias, void* y, const int64_t* geom);
+/* Only the flat output indices idx[i]. */
+int oracle_conv2d_sample(int dtype, const void* x, const void* w, const void* bias, const int64_t* geom,
+                         const int64_t* idx, int64_t count, void* out);
+
+/* Fused elementwise chain (reference: src/ops/fused_elementwise_utils.cpp:122-206 for segment order and
+ * per-segment rounding; sub-op arithmetic: src/backends/cpu/kernels/elementwise.cpp:146-331).
+ * op codes: 1 add, 2 mul, 3 relu, 4 square, 5 gelu. */
+int oracle_ew_program(int dtype, int nseg, const uint8_t* ops, const int8_t* arities, const void* const* ins,
+                      int nin, void* out, int64_t numel);
+
+/* softmax over the last axis (reference: src/backends/cpu/kernels/sequence.cpp:114-174) */
+int oracle_softmax(int dtype, const void* x, void* y, int64_t rows, int64_t cols);
+
+/* layer_norm over the last axis (reference: src/backends/cpu/kernels/sequence.cpp:182-279) */
+int oracle_layer_norm(int dtype, const void* x, const void* gamma, const void* beta, void* y, int64_t rows,
+                      int64_t cols, double eps);
+
+/* pooling (reference: src/backends/cpu/kernels/pool.cpp:178-306). mode 0 = max, 1 = avg.
+ * geom = {N, C, H, W, KH, KW, stride_h, stride_w, pad_h, pad_w}. Returns 2 when a max window is empty. */
+int oracle_pool2d(int dtype, int mode, const void* x, void* y, const int64_t* geom);
+
+/* transpose (reference: src/backends/cpu/kernels/shape.cpp:72-165): out.dims[i] = in.dims[perm[i]] */
+int oracle_transpose(int itemsize, const void* x, void* y, int rank, const int64_t* in_dims, const int64_t* perm);
+/* slice along axis to [start, stop) (reference: src/backends/cpu/kernels/shape.cpp:275-392) */
+int oracle_slice(int itemsize, const void* x, void* y, int rank, const int64_t* in_dims, int64_t axis,
+                 int64_t start, int64_t stop);
+/* concat of `count` inputs along axis (reference: src/backends/cpu/kernels/shape.cpp:170-270);
+ * dims is count x rank, row per input */
+int oracle_concat(int itemsize, const void* const* xs, int count, void* y, int rank, const int64_t* dims,
+                  int64_t axis);
+
+/* constant materialisation: value[i % nvalues] cast to dtype (reference: src/ops/constant_utils.cpp) */
+int oracle_constant(int dtype, const double* values, int64_t nvalues, void* out, int64_t numel);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,289 @@
+"""Kernel-level parity: every C-ABI kernel of libframe_hip_kernels.so against the oracle on identical seeded
+inputs. Tolerances are stated per test (criterion in tests/tolerance.py); data movement, max-pool selections
+and single elementwise ops are compared bit-for-bit."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle_lib as orc
+from frame_hip import synth
+from tolerance import assert_bitwise, assert_close
+
+pytestmark = pytest.mark.gpu
+
+F32, F16, BF16 = 0, 2, 3
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def dev(hip, a):
+    return hip.to_device(np.ascontiguousarray(a))
+
+
+def run_gemm(hip, dtype, a, b, epilogue_segments=None):
+    m, k = a.shape
+    n = b.shape[1]
+    da, db = dev(hip, a), dev(hip, b)
+    dc = hip.DeviceBuffer(m * n * a.itemsize)
+    ep = None
+    keep = []
+    if epilogue_segments:
+        segs = []
+        for op, operand in epilogue_segments:
+            if operand is None:
+                segs.append((op, None))
+            else:
+                d = dev(hip, operand)
+                keep.append(d)
+                segs.append((op, d.value))
+        ep = ctypes.byref(hip.make_epilogue(segs))
+    hip.check(hip.lib().fh_gemm(dtype, da.value, db.value, dc.value, m, n, k, ep, None), "fh_gemm")
+    hip.check(hip.lib().fh_device_synchronize())
+    return dc.download((m, n), a.dtype)
+
+
+GEMM_SHAPES = [
+    (64, 784, 256),   # C1 layer 1 (tile kernel, guarded: 64 rows)
+    (64, 256, 10),    # C1 layer 2 (generic kernel: N not a multiple of the chunk width)
+    (128, 128, 128),
+    (300, 264, 200),  # ragged: every edge guarded
+    (1, 8, 8),
+    (512, 64, 512),   # attention scores shape
+    (512, 512, 64),   # attention context shape
+    (17, 3, 4096),    # tiny N, long K
+]
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16, F16])
+@pytest.mark.parametrize("shape", GEMM_SHAPES)
+def test_gemm_matches_oracle(hip, dtype, shape):
+    m, k, n = shape
+    say(f"gemm dtype={dtype} m={m} k={k} n={n}")
+    a = synth.tensor(11, (m, k), dtype, "uniform")
+    b = synth.tensor(12, (k, n), dtype, "uniform")
+    got = run_gemm(hip, dtype, a, b)
+    want = orc.matmul(dtype, a, b)
+    assert_close(got, want, dtype, what=f"gemm {shape}")
+
+
+def test_gemm_known_answer(hip):
+    # reference: tests/cpp/ops/test_op_matmul.cpp:208-230 — [[1,2],[3,4]]·[[5,6],[7,8]] = [[19,22],[43,50]]
+    a = np.array([[1, 2], [3, 4]], np.float32)
+    b = np.array([[5, 6], [7, 8]], np.float32)
+    got = run_gemm(hip, F32, a, b)
+    assert_bitwise(got, np.array([[19, 22], [43, 50]], np.float32), "matmul known answer")
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16])
+@pytest.mark.parametrize("n", [1024, 2048])
+def test_gemm_square_full(hip, dtype, n):
+    say(f"gemm square full dtype={dtype} n={n}")
+    a = synth.tensor(21, (n, n), dtype, "uniform")
+    b = synth.tensor(22, (n, n), dtype, "uniform")
+    got = run_gemm(hip, dtype, a, b)
+    if n <= 1024:
+        want = orc.matmul(dtype, a, b)
+        assert_close(got, want, dtype, what=f"gemm {n}")
+    else:
+        rng = np.random.default_rng(5)
+        rows, cols = rng.integers(0, n, 4096), rng.integers(0, n, 4096)
+        want = orc.matmul_sample(dtype, a, b, rows, cols)
+        assert_close(got[rows, cols], want, dtype, what=f"gemm {n} sampled")
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16])
+def test_gemm_4096_sampled(hip, dtype):
+    n = 4096
+    say(f"gemm 4096 sampled dtype={dtype}")
+    a = synth.tensor(31, (n, n), dtype, "uniform")
+    b = synth.tensor(32, (n, n), dtype, "uniform")
+    got = run_gemm(hip, dtype, a, b)
+    rng = np.random.default_rng(7)
+    rows, cols = rng.integers(0, n, 4096), rng.integers(0, n, 4096)
+    want = orc.matmul_sample(dtype, a, b, rows, cols)
+    assert_close(got[rows, cols], want, dtype, what="gemm 4096 sampled")
+    # size-independent property: C = A·B implies C·1 = A·(B·1); checked on 8 rows in float64
+    ones = np.ones(n)
+    af, bf, cf = (synth.to_float(x, dtype).astype(np.float64) for x in (a, b, got))
+    lhs = cf[:8] @ ones
+    rhs = af[:8] @ (bf @ ones)
+    scale = np.abs(af[:8]) @ (np.abs(bf) @ ones)
+    assert np.all(np.abs(lhs - rhs) <= 1e-2 * scale), "row-sum identity"
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16])
+def test_gemm_epilogue_add_relu(hip, dtype):
+    # matmul -> add(bias[M,N]) -> relu, as Frame's Linear + fused add;relu computes it (rounded between segments)
+    m, k, n = 256, 192, 512
+    say(f"gemm epilogue add;relu dtype={dtype}")
+    a = synth.tensor(41, (m, k), dtype, "normal")
+    b = synth.tensor(42, (k, n), dtype, "normal", 0.1)
+    bias = synth.tensor(43, (m, n), dtype, "normal")
+    got = run_gemm(hip, dtype, a, b, [(hip.EW_ADD, bias), (hip.EW_RELU, None)])
+    mm = orc.matmul(dtype, a, b)
+    want = orc.ew_program(dtype, [1, 3], [2, 1], [mm, bias])
+    assert_close(got, want, dtype, what="gemm epilogue")
+
+
+def run_ew(hip, dtype, ops, arities, ins):
+    dins = [dev(hip, x) for x in ins]
+    out = hip.DeviceBuffer(ins[0].nbytes)
+    o = (ctypes.c_uint8 * len(ops))(*ops)
+    ar = (ctypes.c_int8 * len(arities))(*arities)
+    ptrs = (ctypes.c_void_p * len(dins))(*[d.value for d in dins])
+    hip.check(hip.lib().fh_ew_program(dtype, len(ops), o, ar, ptrs, len(dins), out.value, ins[0].size, 1, None))
+    hip.check(hip.lib().fh_device_synchronize())
+    return out.download(ins[0].shape, ins[0].dtype)
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16, F16])
+@pytest.mark.parametrize("numel", [1, 7, 4096, 100003])
+def test_ew_programs_bitwise(hip, dtype, numel):
+    say(f"ew dtype={dtype} numel={numel}")
+    x = synth.tensor(51, (numel,), dtype)
+    y = synth.tensor(52, (numel,), dtype)
+    z = synth.tensor(53, (numel,), dtype)
+    for ops, ar, ins in [([1], [2], [x, y]), ([2], [2], [x, y]), ([3], [1], [x]), ([1, 3], [2, 1], [x, y]),
+                         ([1, 2, 3], [2, 2, 1], [x, y, z]), ([4, 1], [1, 2], [x, y])]:
+        got = run_ew(hip, dtype, ops, ar, ins)
+        want = orc.ew_program(dtype, ops, ar, ins)
+        assert_bitwise(got, want, f"ew {ops}")
+
+
+def test_ew_special_values(hip):
+    # relu keeps NaN and -0.0 like std::max(x, 0.0f) (reference: src/backends/cpu/kernels/elementwise.cpp:323-330)
+    x = np.array([np.nan, -0.0, 0.0, -1.5, 2.5, np.inf, -np.inf, 1e-40], np.float32)
+    got = run_ew(hip, F32, [3], [1], [x])
+    want = orc.ew_program(F32, [3], [1], [x])
+    assert_bitwise(got, want, "relu special values")
+    assert np.signbit(got[1]) and np.isnan(got[0])
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16])
+def test_gelu(hip, dtype):
+    x = synth.tensor(55, (50000,), dtype, "normal", 3.0)
+    got = run_ew(hip, dtype, [5], [1], [x])
+    want = orc.ew_program(dtype, [5], [1], [x])
+    # erff differs between libm and the device library by at most a few float32 ulps
+    assert_close(got, want, dtype, rtol=1e-5 if dtype == F32 else 1e-2, atol=1e-6, what="gelu")
+
+
+@pytest.mark.parametrize("dtype,rows,cols", [(F32, 64, 10), (BF16, 512, 512), (F32, 3, 3000), (BF16, 8, 1),
+                                             (F32, 2, 2)])
+def test_softmax(hip, dtype, rows, cols):
+    say(f"softmax dtype={dtype} {rows}x{cols}")
+    x = synth.tensor(61, (rows, cols), dtype, "normal", 2.0)
+    dx, dy = dev(hip, x), hip.DeviceBuffer(x.nbytes)
+    hip.check(hip.lib().fh_softmax_rows(dtype, dx.value, dy.value, rows, cols, None))
+    got = dy.download(x.shape, x.dtype)
+    want = orc.softmax(dtype, x)
+    assert_close(got, want, dtype, atol=1e-7 if dtype == F32 else 1e-4, what="softmax")
+
+
+def test_softmax_known_answer(hip):
+    # reference: tests/cpp/ops/test_op_softmax.cpp:123-162
+    x = np.array([[1, 2], [3, 4]], np.float32)
+    dx, dy = dev(hip, x), hip.DeviceBuffer(x.nbytes)
+    hip.check(hip.lib().fh_softmax_rows(F32, dx.value, dy.value, 2, 2, None))
+    got = dy.download((2, 2), np.float32)
+    np.testing.assert_allclose(got, [[0.26894142, 0.73105858]] * 2, rtol=1e-6)
+
+
+@pytest.mark.parametrize("dtype,rows,cols", [(F32, 2, 5), (BF16, 4096, 1024), (F32, 3, 5000), (BF16, 7, 33)])
+def test_layer_norm(hip, dtype, rows, cols):
+    say(f"layer_norm dtype={dtype} {rows}x{cols}")
+    x = synth.tensor(71, (rows, cols), dtype, "normal")
+    g = synth.tensor(72, (cols,), dtype, "normal")
+    b = synth.tensor(73, (cols,), dtype, "normal")
+    dx, dg, db, dy = dev(hip, x), dev(hip, g), dev(hip, b), hip.DeviceBuffer(x.nbytes)
+    hip.check(hip.lib().fh_layer_norm_rows(dtype, dx.value, dg.value, db.value, dy.value, rows, cols, 1e-5, None))
+    got = dy.download(x.shape, x.dtype)
+    want = orc.layer_norm(dtype, x, g, b, 1e-5)
+    assert_close(got, want, dtype, what="layer_norm")
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16])
+@pytest.mark.parametrize("mode,geom", [
+    (0, (2, 3, 17, 17, 3, 3, 2, 2, 1, 1)),     # ResNet stem max-pool geometry, small
+    (0, (1, 2, 9, 9, 3, 3, 2, 2, 1, 1)),
+    (1, (2, 8, 7, 7, 7, 7, 1, 1, 0, 0)),       # global average pool
+    (1, (1, 2, 6, 6, 3, 3, 2, 2, 1, 1)),       # average with padding counted
+])
+def test_pool2d(hip, dtype, mode, geom):
+    say(f"pool mode={mode} dtype={dtype} {geom}")
+    n, c, h, w = geom[:4]
+    x = synth.tensor(81, (n, c, h, w), dtype, "normal")
+    want = orc.pool2d(dtype, mode, x, geom)
+    dx, dy = dev(hip, x), hip.DeviceBuffer(want.nbytes)
+    hip.check(hip.lib().fh_pool2d(dtype, mode, dx.value, dy.value, hip.i64_array(geom), None))
+    got = dy.download(want.shape, want.dtype)
+    assert_bitwise(got, want, f"pool mode={mode}")
+
+
+def test_maxpool_ties_and_neg_inf_padding(hip):
+    # first maximum wins; padding never selected (reference: tests/cpp/ops/test_pool2d.cpp:361-600)
+    x = np.full((1, 1, 4, 4), -5.0, np.float32)
+    x[0, 0, 1, 1] = 7.0
+    x[0, 0, 2, 2] = 7.0
+    geom = (1, 1, 4, 4, 3, 3, 1, 1, 1, 1)
+    want = orc.pool2d(F32, 0, x, geom)
+    dx, dy = dev(hip, x), hip.DeviceBuffer(want.nbytes)
+    hip.check(hip.lib().fh_pool2d(F32, 0, dx.value, dy.value, hip.i64_array(geom), None))
+    assert_bitwise(dy.download(want.shape, np.float32), want, "maxpool ties")
+
+
+def test_permute_copy_fill(hip):
+    x = np.arange(2 * 3 * 4 * 5, dtype=np.uint16).reshape(2, 3, 4, 5)
+    for perm in [(1, 0, 2, 3), (0, 2, 1, 3), (3, 2, 1, 0)]:
+        want = np.ascontiguousarray(np.transpose(x, perm))
+        in_strides = np.array(x.strides) // x.itemsize
+        dx, dy = dev(hip, x), hip.DeviceBuffer(x.nbytes)
+        hip.check(hip.lib().fh_permute(2, dx.value, dy.value, 4, hip.i64_array(want.shape),
+                                       hip.i64_array([in_strides[p] for p in perm]), None))
+        assert_bitwise(dy.download(want.shape, np.uint16), want, f"permute {perm}")
+    # rank-2 tiled transpose
+    t = synth.tensor(91, (512, 64), BF16)
+    dx, dy = dev(hip, t), hip.DeviceBuffer(t.nbytes)
+    hip.check(hip.lib().fh_permute(2, dx.value, dy.value, 2, hip.i64_array([64, 512]), hip.i64_array([1, 64]), None))
+    assert_bitwise(dy.download((64, 512), np.uint16), np.ascontiguousarray(t.T), "transpose2d")
+    # column slice [512,1024] -> [512,64] at column 128 through copy2d
+    s = synth.tensor(92, (512, 1024), BF16)
+    ds, dd = dev(hip, s), hip.DeviceBuffer(512 * 64 * 2)
+    hip.check(hip.lib().fh_copy2d(dd.value, 128, ds.value + 128 * 2, 2048, 128, 512, None))
+    assert_bitwise(dd.download((512, 64), np.uint16), np.ascontiguousarray(s[:, 128:192]), "copy2d slice")
+    # fill
+    dfb = hip.DeviceBuffer(1000 * 2)
+    hip.check(hip.lib().fh_fill(dfb.value, 2, 0x3E00, 1000, None))
+    assert np.all(dfb.download((1000,), np.uint16) == 0x3E00)
+
+
+CONV_CASES = [
+    # N, Cin, H, W, Cout, KH, KW, sh, sw, ph, pw, groups, bias
+    ((2, 3, 9, 9, 4, 7, 7, 2, 2, 3, 3, 1), True),
+    ((2, 8, 7, 7, 8, 3, 3, 1, 1, 1, 1, 1), True),
+    ((2, 8, 7, 7, 8, 3, 3, 1, 1, 1, 1, 2), False),     # groups
+    ((1, 16, 14, 14, 32, 1, 1, 2, 2, 0, 0, 1), False), # 1x1 stride-2 downsample
+    ((2, 64, 12, 12, 64, 3, 3, 1, 1, 1, 1, 1), True),
+]
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16])
+@pytest.mark.parametrize("geom,with_bias", CONV_CASES)
+def test_conv2d(hip, dtype, geom, with_bias):
+    say(f"conv dtype={dtype} {geom} bias={with_bias}")
+    n, cin, h, w, cout, kh, kw = geom[:7]
+    groups = geom[11]
+    x = synth.tensor(101, (n, cin, h, w), dtype, "normal")
+    wt = synth.tensor(102, (cout, cin // groups, kh, kw), dtype, "normal", (2.0 / (cin // groups * kh * kw)) ** 0.5)
+    bias = synth.tensor(103, (cout,), dtype, "normal", 0.1) if with_bias else None
+    want = orc.conv2d(dtype, x, wt, bias, geom)
+    dx, dw = dev(hip, x), dev(hip, wt)
+    db = dev(hip, bias) if with_bias else None
+    dy = hip.DeviceBuffer(want.nbytes)
+    hip.check(hip.lib().fh_conv2d_fwd(dtype, dx.value, dw.value, db.value if db else None, dy.value,
+                                      hip.i64_array(geom), None, None))
+    got = dy.download(want.shape, want.dtype)
+    assert_close(got, want, dtype, what=f"conv {geom}")
