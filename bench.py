@@ -1,0 +1,131 @@
+"""Benchmark of the `hip` backend's compiled-graph hot path on one MI355X.
+
+Workload (the dense GEMM sweep, at its largest size): C = A·B, row-major
+A[4096,4096]·B[4096,4096], bfloat16 inputs, fp32 accumulation, bfloat16 output; entries U(-1,1) from the
+build's seeded generator. One step = one forward pass of that graph on inputs already resident in HBM.
+
+Prints ONE JSON line with the metric (TFLOP/s), the dominant kernel's roofline fraction (its average duration
+measured with HIP events on the stream it runs on) and a CPU baseline: the reference's own CPU backend
+(oracle/_ref, single-threaded) timed on a bounded row-sample of the same GEMM on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+REPO = os.path.dirname(os.path.abspath(__file__))
+for p in (os.path.join(REPO, "frame-public_amd"), os.path.join(REPO, "tests")):
+    if p not in sys.path:
+        sys.path.insert(0, p)
+
+import numpy as np  # noqa: E402
+
+PEAK_BF16_TFLOPS = 2516.6  # dense bf16 MFMA, 256 CU x 2.4 GHz x 4096 FLOP/clk/CU
+PEAK_HBM_GBS = 8000.0
+
+N = 4096
+BF16 = 3
+
+
+def gemm_flops(m, n, k):
+    return 2.0 * m * n * k
+
+
+def run_gpu(steps: int, warmup: int):
+    from frame_hip import abi, synth
+
+    lib = abi.lib()
+    a = synth.tensor(31, (N, N), BF16, "uniform")
+    b = synth.tensor(32, (N, N), BF16, "uniform")
+    da, db = abi.to_device(a), abi.to_device(b)
+    dc = abi.DeviceBuffer(N * N * 2)
+    stream = abi.Stream()
+    start, stop = abi.Event(), abi.Event()
+
+    def step():
+        abi.check(lib.fh_gemm(BF16, da.value, db.value, dc.value, N, N, N, None, stream.ptr), "fh_gemm")
+
+    for _ in range(warmup):
+        step()
+    stream.synchronize()
+    abi.check(lib.fh_device_synchronize())
+    t0 = time.perf_counter()
+    start.record(stream)
+    for _ in range(steps):
+        step()
+    stop.record(stream)
+    stop.synchronize()
+    abi.check(lib.fh_device_synchronize())
+    wall = time.perf_counter() - t0
+    ms = start.elapsed_ms(stop) / steps
+    return ms, wall
+
+
+def cpu_baseline(rows: int):
+    """Reference CPU backend (single thread) on rows x 4096 x 4096 of the same GEMM."""
+    import oracle_lib as orc
+    from frame_hip import synth
+
+    a = synth.tensor(31, (N, N), BF16, "uniform")[:rows].copy()
+    b = synth.tensor(32, (N, N), BF16, "uniform")
+    if orc.ref_available():
+        text = (f"%0 = graph_input() : bfloat16[{rows},{N}]@cpu:0\n"
+                f"%1 = graph_input() : bfloat16[{N},{N}]@cpu:0\n"
+                f"%2 = matmul(%0, %1) : bfloat16[{rows},{N}]@cpu:0\n"
+                f"graph_output(%2)\n")
+        t0 = time.perf_counter()
+        orc.ref_run_graph(text, [a, b], [((rows, N), np.uint16)])
+        dt = time.perf_counter() - t0
+        kind = "reference"
+    else:
+        t0 = time.perf_counter()
+        orc.matmul(BF16, a, b)
+        dt = time.perf_counter() - t0
+        kind = "port"
+    return {"value": gemm_flops(rows, N, N) / dt / 1e12, "unit": "TFLOP/s", "cores": 1, "kind": kind,
+            "sample": f"{rows} of {N} output rows of the bf16 {N}^3 GEMM ({gemm_flops(rows, N, N) / 1e9:.1f} GFLOP), "
+                      f"{dt:.1f} s single-threaded"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--cpu-rows", type=int, default=128)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py: this build measures one MI355X only (no multi-GPU path); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    ms, wall = run_gpu(args.steps, args.warmup)
+    tflops = gemm_flops(N, N, N) / (ms * 1e-3) / 1e12
+    line = {
+        "metric": "GEMM/Conv2d TFLOP/s & % MFMA peak; fused-op GB/s; compiled-graph fwd latency",
+        "value": round(tflops, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "dense GEMM C=A·B, M=N=K=4096, bf16 in/out, fp32 accumulate (configs[1])",
+                   "M": N, "N": N, "K": N},
+        "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None},
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(args.cpu_rows)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
