@@ -1,0 +1,120 @@
+// The MI355X `hip` backend: HAL objects over the C ABI of libframe_hip_kernels.so (include/frame_hip_abi.h).
+// Modelled on the plugin contract of the reference (include/frame/hal/backend.h:77-109); the design analog
+// being replaced is src/backends/cuda/cuda_backend.{h,cpp}.
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <map>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <vector>
+
+#include <frame/core/device.h>
+#include <frame/core/status.h>
+#include <frame/hal/allocator.h>
+#include <frame/hal/backend.h>
+#include <frame/hal/event.h>
+#include <frame/hal/executable.h>
+#include <frame/hal/stream.h>
+#include <frame/ops/kernel_registry.h>
+
+#include "frame_hip_abi.h"
+
+namespace frame::backends::hip {
+
+// fh_status -> Status (the ABI's codes are frame::ErrorCode ordinals); the message comes from fh_last_error.
+Status from_fh(fh_status code, std::string_view what);
+
+#define FRAME_HIP_RETURN_IF_ERROR(expr, what)                                 \
+  do {                                                                        \
+    const fh_status frame_hip_st_ = (expr);                                   \
+    if (frame_hip_st_ != FH_OK) return ::frame::backends::hip::from_fh(frame_hip_st_, (what)); \
+  } while (0)
+
+class HipStream final : public hal::Stream {
+ public:
+  HipStream(void* handle, int32_t device) : handle_(handle), device_(device) {}
+  ~HipStream() override;
+  Status synchronize() override;
+  Status record(hal::Event& event) override;
+  Status wait(const hal::Event& event) override;
+  void* native_handle() override { return handle_; }
+  int32_t device() const { return device_; }
+
+ private:
+  void* handle_;
+  int32_t device_;
+};
+
+class HipEvent final : public hal::Event {
+ public:
+  HipEvent(void* handle, int32_t device) : handle_(handle), device_(device) {}
+  ~HipEvent() override;
+  bool query() const override;
+  Status synchronize() override;
+  void* handle() const { return handle_; }
+  bool recorded() const { return recorded_; }
+  void mark_recorded() { recorded_ = true; }
+
+ private:
+  void* handle_;
+  int32_t device_;
+  bool recorded_ = false;  // an event never recorded counts as complete
+};
+
+// Device memory with a size-class cache: freed blocks go back to per-size free lists and are handed out again
+// without calling hipMalloc. Memory returned to the cache may be reused by the next allocate(); callers free a
+// block only after the work that uses it is ordered before any later use (same stream or synchronised), which
+// is how the executor and the runtime use it.
+class HipAllocator final : public hal::Allocator {
+ public:
+  explicit HipAllocator(int32_t device) : device_(device) {}
+  ~HipAllocator() override;
+  Result<void*> allocate(size_t bytes, size_t alignment) override;
+  void deallocate(void* ptr) override;
+  static constexpr size_t kGuaranteedAlignment = 256;
+
+ private:
+  static size_t size_class(size_t bytes);
+  int32_t device_;
+  std::mutex mu_;
+  std::unordered_map<void*, size_t> live_;           // pointer -> size class
+  std::map<size_t, std::vector<void*>> free_lists_;  // size class -> cached blocks
+};
+
+class HipBackend final : public hal::Backend {
+ public:
+  HipBackend();
+  ~HipBackend() override;
+  std::string_view name() const override { return kHipBackendName; }
+  Result<int32_t> device_count() const override;
+  Result<std::unique_ptr<hal::Stream>> create_stream(Device device) override;
+  Result<std::unique_ptr<hal::Event>> create_event(Device device) override;
+  hal::Allocator* allocator(Device device) override;
+  Status copy(void* dst, Device dst_device, const void* src, Device src_device, size_t bytes,
+              hal::Stream* stream) override;
+  Result<std::unique_ptr<hal::Executable>> compile(const ir::Graph& graph, const hal::CompileOptions& options) override;
+  Status launch(const hal::KernelInvocation& invocation, hal::Stream* stream) override;
+
+ private:
+  Status check_device(Device device) const;
+  std::mutex mu_;
+  std::vector<std::unique_ptr<HipAllocator>> allocators_;
+};
+
+// The stream handle a kernel enqueues on (nullptr = the device's null stream).
+inline void* stream_handle(const ops::KernelContext& ctx) {
+  return ctx.stream == nullptr ? nullptr : ctx.stream->native_handle();
+}
+
+// Internal op names produced by HipBackend::compile's epilogue lowering (never user-visible).
+inline constexpr std::string_view kGemmEpilogueOp = "hip_matmul_epilogue_internal";
+inline constexpr std::string_view kConvEpilogueOp = "hip_conv2d_epilogue_internal";
+
+// Elementwise op name -> fh_ew_op code (0 when the op has no device code).
+uint8_t ew_code(std::string_view op);
+
+}  // namespace frame::backends::hip

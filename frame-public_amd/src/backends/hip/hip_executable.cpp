@@ -1,0 +1,240 @@
+// HipExecutable and the backend-internal lowering done by HipBackend::compile.
+//
+// Executor (design analog replaced: src/backends/cuda/cuda_executable.cpp:41-128, which allocates the arena
+// and every graph output per run and copies outputs device-to-device afterwards):
+//  * the arena is allocated once per stream and reused by later runs on that stream;
+//  * steps that produce a graph output write straight into the caller's output tensor;
+//  * constants are materialised on the device once, at compile time.
+//
+// Lowering (allowed inside Backend::compile by the HAL contract, include/frame/hal/backend.h:45-63): a matmul
+// or conv2d whose only consumer is an elementwise node (add, mul, relu, square, gelu or a fused chain) that
+// takes the contraction result as its first operand is replaced by one internal node that applies the
+// consumer's program in the contraction's epilogue. The epilogue rounds to the storage dtype after the
+// product and after every segment, so results equal the unfused graph's bit for bit. The rewrite runs on a
+// private copy of the graph before planning, so the memory plan sees the fused node's real lifetimes.
+#include <algorithm>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+#include <unordered_set>
+#include <utility>
+#include <vector>
+
+#include <frame/ir/graph.h>
+#include <frame/ops/constant_utils.h>
+#include <frame/ops/executable_plan.h>
+#include <frame/ops/fused_elementwise_utils.h>
+#include <frame/ops/op_registry.h>
+
+#include "hip_backend.h"
+
+namespace frame::backends::hip {
+
+namespace {
+
+// Consumer program as fh_ew_op codes, or empty when the consumer cannot become an epilogue.
+// `operand_index` is the position of the contraction result among the consumer's inputs.
+std::vector<int64_t> epilogue_program(const ir::Node* consumer, size_t operand_index) {
+  std::vector<int64_t> codes;
+  if (consumer->op() == ops::kFusedElementwiseOpName) {
+    ops::FusedElementwiseChain chain;
+    if (!ops::decode_and_validate_fused_chain(consumer->attrs(), static_cast<int64_t>(consumer->inputs().size()), chain)
+             .is_ok())
+      return {};
+    for (size_t i = 0; i < chain.sub_ops.size(); ++i) {
+      const uint8_t c = ew_code(chain.sub_ops[i]);
+      if (c == 0 || chain.arities[i] > 2) return {};
+      codes.push_back(c);
+    }
+    if (chain.arities[0] != (FH_EW_ADD == codes[0] || FH_EW_MUL == codes[0] ? 2 : 1)) return {};
+  } else {
+    const uint8_t c = ew_code(consumer->op());
+    if (c == 0) return {};
+    codes.push_back(c);
+  }
+  // The result must feed segment 0's first operand; add/mul are commutative, so the second slot also works.
+  if (operand_index == 0) return codes;
+  if (operand_index == 1 && (codes[0] == FH_EW_ADD || codes[0] == FH_EW_MUL)) return codes;
+  return {};
+}
+
+Status lower_epilogues(ir::Graph& g) {
+  std::unordered_map<const ir::Value*, int> uses;
+  for (const ir::Node* n : g.topological_order())
+    for (const ir::Value* v : n->inputs()) ++uses[v];
+  for (const ir::Value* v : g.outputs()) uses[v] += 1000;  // graph outputs are never folded away
+  const std::vector<ir::Node*> snapshot = g.topological_order();
+  std::unordered_set<const ir::Node*> erased;
+  for (ir::Node* c : snapshot) {
+    if (erased.count(c) || c->outputs().size() != 1) continue;
+    for (size_t idx = 0; idx < std::min<size_t>(2, c->inputs().size()); ++idx) {
+      ir::Value* v = c->inputs()[idx];
+      ir::Node* p = v->producer();
+      if (p == nullptr || erased.count(p) || uses[v] != 1) continue;
+      const bool is_mm = p->op() == "matmul", is_conv = p->op() == "conv2d";
+      if (!is_mm && !is_conv) continue;
+      if (!(p->outputs()[0].type().dtype == c->outputs()[0].type().dtype)) continue;
+      std::vector<int64_t> prog = epilogue_program(c, idx);
+      if (prog.empty() || prog.size() > FH_MAX_SEGMENTS) continue;
+      std::vector<ir::Value*> ins(p->inputs().begin(), p->inputs().end());
+      const size_t n_main = ins.size();
+      for (size_t j = 0; j < c->inputs().size(); ++j)
+        if (j != idx) ins.push_back(c->inputs()[j]);
+      if (ins.size() - n_main > FH_MAX_SEGMENTS) continue;
+      Result<ir::Node*> f = g.create_node(std::string(is_mm ? kGemmEpilogueOp : kConvEpilogueOp), ins,
+                                          {c->outputs()[0].type()});
+      if (!f.is_ok()) return f.status();
+      for (const auto& [k, a] : p->attrs()) f.value()->set_attr(k, a);
+      f.value()->set_attr("ep_ops", ir::AttrValue{prog});
+      f.value()->set_attr("n_main_inputs", ir::AttrValue{static_cast<int64_t>(n_main)});
+      FRAME_RETURN_IF_ERROR(g.replace_all_uses(c->output(0), f.value()->output(0)));
+      FRAME_RETURN_IF_ERROR(g.erase_node(c));
+      FRAME_RETURN_IF_ERROR(g.erase_node(p));
+      erased.insert(c);
+      erased.insert(p);
+      break;
+    }
+  }
+  return Status::ok();
+}
+
+class HipExecutable final : public hal::Executable {
+ public:
+  HipExecutable(ops::ExecutablePlan plan, HipAllocator& alloc, Device device, hal::CompileOptions options)
+      : plan_(std::move(plan)), alloc_(&alloc), device_(device), options_(std::move(options)) {
+    for (const auto& t : plan_.input_types) in_sig_.push_back({t.dtype, t.shape});
+    for (const auto& t : plan_.output_types) out_sig_.push_back({t.dtype, t.shape});
+  }
+
+  Status materialize_constants() {
+    for (size_t i = 0; i < plan_.steps.size(); ++i) {
+      const ops::ExecutablePlanStep& s = plan_.steps[i];
+      if (s.op != ops::kConstantOpName) continue;
+      const ir::TensorType& t = s.output_types[0];
+      const size_t bytes = static_cast<size_t>(t.shape.numel()) * t.dtype.itemsize();
+      std::vector<unsigned char> host(std::max<size_t>(bytes, 1));
+      Result<Tensor> dev = Tensor::empty(t.shape, t.dtype, device_, *alloc_);
+      if (!dev.is_ok()) return dev.status();
+      // fill_tensor_from_constant_attrs writes through raw_data(); give it a host tensor over `host`.
+      struct HostAlloc final : hal::Allocator {
+        void* p;
+        explicit HostAlloc(void* q) : p(q) {}
+        Result<void*> allocate(size_t, size_t) override { return p; }
+        void deallocate(void*) override {}
+      } ha(host.data());
+      Result<Tensor> h = Tensor::empty(t.shape, t.dtype, cpu_device(), ha);
+      if (!h.is_ok()) return h.status();
+      FRAME_RETURN_IF_ERROR(ops::fill_tensor_from_constant_attrs(s.attrs, h.value()));
+      if (bytes > 0)
+        FRAME_HIP_RETURN_IF_ERROR(fh_memcpy(dev.value().raw_data(), host.data(), bytes, FH_H2D, nullptr),
+                                  "HipExecutable: constant upload");
+      constants_.emplace(i, dev.value());
+    }
+    return Status::ok();
+  }
+
+  Status run(std::span<const Tensor> inputs, std::span<Tensor> outputs, hal::Stream& stream) override {
+    FRAME_RETURN_IF_ERROR(hal::validate_io_signature(inputs, in_sig_, "HipExecutable::run: input"));
+    FRAME_RETURN_IF_ERROR(hal::validate_io_signature(outputs, out_sig_, "HipExecutable::run: output"));
+    FRAME_RETURN_IF_ERROR(hal::validate_tensor_devices(inputs, device_, "HipExecutable::run: input"));
+    FRAME_RETURN_IF_ERROR(hal::validate_tensor_devices(outputs, device_, "HipExecutable::run: output"));
+    void* sh = stream.native_handle();
+    std::shared_ptr<Storage> arena;
+    if (plan_.arena_total_bytes > 0) {
+      std::lock_guard<std::mutex> lock(mu_);
+      auto& a = arenas_[sh];
+      if (!a) {
+        Result<std::shared_ptr<Storage>> st = Storage::allocate(*alloc_, plan_.arena_total_bytes, kDefaultAlignment, device_);
+        if (!st.is_ok()) return st.status();
+        a = st.value();
+      }
+      arena = a;
+    }
+    std::vector<Tensor> slots(static_cast<size_t>(plan_.slot_count));
+    for (size_t i = 0; i < inputs.size(); ++i) slots[i] = inputs[i];
+    // A slot that is a graph output is produced directly in the first caller tensor naming it.
+    std::unordered_map<int32_t, size_t> direct;
+    for (size_t i = 0; i < plan_.output_slots.size(); ++i) direct.try_emplace(plan_.output_slots[i], i);
+
+    std::vector<Tensor> step_in, step_out;
+    for (size_t si = 0; si < plan_.steps.size(); ++si) {
+      const ops::ExecutablePlanStep& s = plan_.steps[si];
+      if (auto c = constants_.find(si); c != constants_.end()) {
+        const int32_t slot = s.output_slots[0];
+        auto d = direct.find(slot);
+        if (d == direct.end()) {
+          slots[static_cast<size_t>(slot)] = c->second;
+        } else {
+          Tensor& dst = outputs[d->second];
+          const size_t bytes = static_cast<size_t>(dst.numel()) * dst.dtype().itemsize();
+          FRAME_HIP_RETURN_IF_ERROR(fh_memcpy(dst.raw_data(), c->second.raw_data(), bytes, FH_D2D, sh),
+                                    "HipExecutable: constant output copy");
+          slots[static_cast<size_t>(slot)] = dst;
+        }
+        continue;
+      }
+      step_in.clear();
+      step_out.clear();
+      for (int32_t slot : s.input_slots) step_in.push_back(slots[static_cast<size_t>(slot)]);
+      for (size_t j = 0; j < s.output_types.size(); ++j) {
+        const ir::TensorType& t = s.output_types[j];
+        auto d = direct.find(s.output_slots[j]);
+        if (d != direct.end()) {
+          step_out.push_back(outputs[d->second]);
+        } else if (s.output_arena_offsets[j].has_value() && t.shape.numel() > 0) {
+          step_out.push_back(Tensor::from_storage_slice(arena, *s.output_arena_offsets[j], t.shape, t.dtype, device_));
+        } else {
+          Result<Tensor> e = Tensor::empty(t.shape, t.dtype, device_, *alloc_);
+          if (!e.is_ok()) return e.status();
+          step_out.push_back(e.value());
+        }
+      }
+      ops::KernelContext ctx{step_in, step_out, &s.attrs, device_, &stream, &options_};
+      Status st = s.kernel(ctx);
+      if (!st.is_ok())
+        return Status::make(st.code(), "HipExecutable::run: op '" + s.op + "' kernel failed: " + std::string(st.message()));
+      for (size_t j = 0; j < s.output_slots.size(); ++j) slots[static_cast<size_t>(s.output_slots[j])] = step_out[j];
+    }
+    // Outputs that were not written in place: graph inputs passed through, or a value listed twice.
+    for (size_t i = 0; i < plan_.output_slots.size(); ++i) {
+      const Tensor& src = slots[static_cast<size_t>(plan_.output_slots[i])];
+      Tensor& dst = outputs[i];
+      if (src.raw_data() == dst.raw_data()) continue;
+      const size_t bytes = static_cast<size_t>(src.numel()) * src.dtype().itemsize();
+      if (bytes > 0)
+        FRAME_HIP_RETURN_IF_ERROR(fh_memcpy(dst.raw_data(), src.raw_data(), bytes, FH_D2D, sh),
+                                  "HipExecutable: output copy");
+    }
+    return Status::ok();
+  }
+
+  std::vector<hal::IoSpec> input_signature() const override { return in_sig_; }
+  std::vector<hal::IoSpec> output_signature() const override { return out_sig_; }
+
+ private:
+  ops::ExecutablePlan plan_;
+  HipAllocator* alloc_;
+  Device device_;
+  hal::CompileOptions options_;
+  std::vector<hal::IoSpec> in_sig_, out_sig_;
+  std::unordered_map<size_t, Tensor> constants_;  // step index -> device tensor
+  std::mutex mu_;
+  std::unordered_map<void*, std::shared_ptr<Storage>> arenas_;  // per stream
+};
+
+}  // namespace
+
+Result<std::unique_ptr<hal::Executable>> compile_hip_executable(const ir::Graph& graph, const hal::CompileOptions& options,
+                                                                 HipAllocator& allocator, Device device) {
+  Result<ir::Graph> work = ir::clone_graph(graph);
+  if (!work.is_ok()) return work.status();
+  if (options.opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_epilogues(work.value()));
+  Result<ops::ExecutablePlan> plan = ops::build_executable_plan(work.value(), kHipBackendName);
+  if (!plan.is_ok()) return plan.status();
+  auto exe = std::make_unique<HipExecutable>(std::move(plan.value()), allocator, device, options);
+  FRAME_RETURN_IF_ERROR(exe->materialize_constants());
+  return std::unique_ptr<hal::Executable>(std::move(exe));
+}
+
+}  // namespace frame::backends::hip

@@ -1,0 +1,385 @@
+// KernelFn wrappers of the `hip` backend: argument checks on the host, then one enqueue through the C ABI of
+// libframe_hip_kernels.so on the context's stream. Registered with FRAME_REGISTER_KERNEL(op, "hip", fn) like
+// every Frame backend's kernels (reference: include/frame/ops/kernel_registry.h:104-107). The design analogs
+// replaced are the cuda kernels under src/backends/cuda/kernels/ (cuBLASLt, cuDNN and the .cu files).
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include <frame/core/tensor.h>
+#include <frame/ops/constant_utils.h>
+#include <frame/ops/fused_elementwise_utils.h>
+#include <frame/ops/kernel_registry.h>
+
+#include "../hip_backend.h"
+
+namespace frame::backends::hip {
+namespace {
+
+using ops::KernelContext;
+
+Status invalid(const std::string& op, const std::string& msg) {
+  return Status::make(ErrorCode::kInvalidArgument, "op '" + op + "' (hip): " + msg);
+}
+
+// fh dtype code of a floating-point tensor, or an kUnimplemented status.
+Result<int32_t> float_code(const std::string& op, DType d) {
+  switch (d.code()) {
+    case DTypeCode::kFloat32: return static_cast<int32_t>(FH_F32);
+    case DTypeCode::kFloat16: return static_cast<int32_t>(FH_F16);
+    case DTypeCode::kBFloat16: return static_cast<int32_t>(FH_BF16);
+    default:
+      return Status::make(ErrorCode::kUnimplemented,
+                          "op '" + op + "' on backend 'hip' does not support dtype '" + std::string(d.name()) + "'");
+  }
+}
+
+Status arity(const KernelContext& ctx, const std::string& op, size_t n_in, size_t n_out) {
+  if (ctx.inputs.size() != n_in) return invalid(op, "expects " + std::to_string(n_in) + " input(s), got " + std::to_string(ctx.inputs.size()));
+  if (ctx.outputs.size() != n_out) return invalid(op, "expects " + std::to_string(n_out) + " output(s), got " + std::to_string(ctx.outputs.size()));
+  return Status::ok();
+}
+
+Status same_dtype(const KernelContext& ctx, const std::string& op) {
+  const DType d = ctx.outputs[0].dtype();
+  for (const Tensor& t : ctx.inputs)
+    if (!(t.dtype() == d)) return invalid(op, "input dtype '" + std::string(t.dtype().name()) + "' differs from output dtype '" + std::string(d.name()) + "'");
+  return Status::ok();
+}
+
+template <typename T>
+const T* attr(const KernelContext& ctx, const char* name) {
+  if (ctx.attrs == nullptr) return nullptr;
+  auto it = ctx.attrs->find(name);
+  return it == ctx.attrs->end() ? nullptr : std::get_if<T>(&it->second);
+}
+
+// ---- elementwise ------------------------------------------------------------------------------------------
+
+Status run_program(const KernelContext& ctx, const std::string& op, const std::vector<uint8_t>& codes,
+                   const std::vector<int8_t>& arities) {
+  FRAME_RETURN_IF_ERROR(same_dtype(ctx, op));
+  Result<int32_t> dt = float_code(op, ctx.outputs[0].dtype());
+  if (!dt.is_ok()) return dt.status();
+  const int64_t n = ctx.outputs[0].numel();
+  std::vector<const void*> ins;
+  for (const Tensor& t : ctx.inputs) {
+    if (t.numel() != n) return invalid(op, "operand element count " + std::to_string(t.numel()) + " differs from output " + std::to_string(n));
+    ins.push_back(t.raw_data());
+  }
+  FRAME_HIP_RETURN_IF_ERROR(fh_ew_program(dt.value(), static_cast<int32_t>(codes.size()), codes.data(), arities.data(),
+                                          ins.data(), static_cast<int32_t>(ins.size()), ctx.outputs[0].raw_data(), n,
+                                          /*round_between=*/1, stream_handle(ctx)),
+                            "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
+template <uint8_t Code, int Arity>
+Status ew_kernel(KernelContext& ctx) {
+  static const std::string names[] = {"", "add", "mul", "relu", "square", "gelu"};
+  const std::string& op = names[Code];
+  FRAME_RETURN_IF_ERROR(arity(ctx, op, Arity, 1));
+  return run_program(ctx, op, {Code}, {static_cast<int8_t>(Arity)});
+}
+
+Status fused_kernel(KernelContext& ctx) {
+  const std::string op(ops::kFusedElementwiseOpName);
+  if (ctx.outputs.size() != 1) return invalid(op, "expects 1 output");
+  if (ctx.attrs == nullptr) return invalid(op, "requires attrs");
+  ops::FusedElementwiseChain chain;
+  FRAME_RETURN_IF_ERROR(ops::decode_and_validate_fused_chain(*ctx.attrs, static_cast<int64_t>(ctx.inputs.size()), chain));
+  if (chain.sub_ops.size() > FH_MAX_SEGMENTS || ctx.inputs.size() > FH_MAX_EW_INPUTS)
+    return Status::make(ErrorCode::kUnimplemented, "op '" + op + "' (hip): chain longer than " + std::to_string(FH_MAX_SEGMENTS) + " segments");
+  std::vector<uint8_t> codes;
+  std::vector<int8_t> ar;
+  for (size_t i = 0; i < chain.sub_ops.size(); ++i) {
+    const uint8_t c = ew_code(chain.sub_ops[i]);
+    if (c == 0)
+      return Status::make(ErrorCode::kUnimplemented, "op '" + op + "' (hip): sub-op '" + chain.sub_ops[i] + "' has no device kernel");
+    codes.push_back(c);
+    ar.push_back(static_cast<int8_t>(chain.arities[i]));
+  }
+  return run_program(ctx, op, codes, ar);
+}
+
+// ---- contractions -----------------------------------------------------------------------------------------
+
+// Epilogue operands are ctx.inputs[first..]; binary segments consume them in order.
+Result<fh_epilogue> make_epilogue(const KernelContext& ctx, const std::string& op, size_t first) {
+  fh_epilogue ep{};
+  const auto* prog = attr<std::vector<int64_t>>(ctx, "ep_ops");
+  if (prog == nullptr) return ep;
+  if (prog->size() > FH_MAX_SEGMENTS) return invalid(op, "epilogue longer than " + std::to_string(FH_MAX_SEGMENTS) + " segments");
+  ep.nseg = static_cast<int32_t>(prog->size());
+  ep.round_between = 1;
+  size_t next = first;
+  const int64_t n = ctx.outputs[0].numel();
+  for (size_t s = 0; s < prog->size(); ++s) {
+    ep.ops[s] = static_cast<uint8_t>((*prog)[s]);
+    if (ep.ops[s] == FH_EW_ADD || ep.ops[s] == FH_EW_MUL) {
+      if (next >= ctx.inputs.size()) return invalid(op, "epilogue operand missing");
+      const Tensor& t = ctx.inputs[next++];
+      if (t.numel() != n || !(t.dtype() == ctx.outputs[0].dtype())) return invalid(op, "epilogue operand has the wrong shape or dtype");
+      ep.ins[s] = t.raw_data();
+    }
+  }
+  if (next != ctx.inputs.size()) return invalid(op, "unused epilogue operands");
+  return ep;
+}
+
+Status gemm_impl(KernelContext& ctx, const std::string& op, size_t n_main) {
+  if (ctx.inputs.size() < n_main || ctx.outputs.size() != 1) return invalid(op, "bad operand count");
+  const Tensor& a = ctx.inputs[0];
+  const Tensor& b = ctx.inputs[1];
+  Tensor& c = ctx.outputs[0];
+  if (a.shape().rank() != 2 || b.shape().rank() != 2 || c.shape().rank() != 2) return invalid(op, "operands must be rank-2");
+  const int64_t m = a.shape().dim(0), k = a.shape().dim(1), n = b.shape().dim(1);
+  if (b.shape().dim(0) != k || c.shape().dim(0) != m || c.shape().dim(1) != n)
+    return invalid(op, "shape mismatch " + a.shape().to_string() + " x " + b.shape().to_string() + " -> " + c.shape().to_string());
+  FRAME_RETURN_IF_ERROR(same_dtype(ctx, op));
+  Result<int32_t> dt = float_code(op, c.dtype());
+  if (!dt.is_ok()) return dt.status();
+  Result<fh_epilogue> ep = make_epilogue(ctx, op, n_main);
+  if (!ep.is_ok()) return ep.status();
+  FRAME_HIP_RETURN_IF_ERROR(fh_gemm(dt.value(), a.raw_data(), b.raw_data(), c.raw_data(), m, n, k,
+                                    ep.value().nseg > 0 ? &ep.value() : nullptr, stream_handle(ctx)),
+                            "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
+Status matmul_kernel(KernelContext& ctx) {
+  FRAME_RETURN_IF_ERROR(arity(ctx, "matmul", 2, 1));
+  return gemm_impl(ctx, "matmul", 2);
+}
+
+Status gemm_epilogue_kernel(KernelContext& ctx) {
+  const auto* n_main = attr<int64_t>(ctx, "n_main_inputs");
+  return gemm_impl(ctx, std::string(kGemmEpilogueOp), n_main ? static_cast<size_t>(*n_main) : 2);
+}
+
+Status conv_impl(KernelContext& ctx, const std::string& op, size_t n_main) {
+  if (ctx.inputs.size() < n_main || n_main < 2 || n_main > 3 || ctx.outputs.size() != 1) return invalid(op, "bad operand count");
+  const Tensor& x = ctx.inputs[0];
+  const Tensor& w = ctx.inputs[1];
+  const Tensor* bias = n_main == 3 ? &ctx.inputs[2] : nullptr;
+  Tensor& y = ctx.outputs[0];
+  const auto* stride = attr<std::vector<int64_t>>(ctx, "stride");
+  const auto* pad = attr<std::vector<int64_t>>(ctx, "padding");
+  const auto* groups = attr<int64_t>(ctx, "groups");
+  if (stride == nullptr || pad == nullptr || groups == nullptr || stride->size() != 2 || pad->size() != 2)
+    return invalid(op, "missing or malformed stride/padding/groups attributes");
+  if (x.shape().rank() != 4 || w.shape().rank() != 4 || y.shape().rank() != 4) return invalid(op, "operands must be rank-4");
+  for (size_t i = 0; i < n_main; ++i)
+    if (!(ctx.inputs[i].dtype() == y.dtype())) return invalid(op, "operand dtypes differ");
+  Result<int32_t> dt = float_code(op, y.dtype());
+  if (!dt.is_ok()) return dt.status();
+  const int64_t geom[12] = {x.shape().dim(0), x.shape().dim(1), x.shape().dim(2), x.shape().dim(3),
+                            w.shape().dim(0), w.shape().dim(2), w.shape().dim(3), (*stride)[0],
+                            (*stride)[1],     (*pad)[0],        (*pad)[1],        *groups};
+  const int64_t oh = (geom[2] + 2 * geom[9] - geom[5]) / geom[7] + 1;
+  const int64_t ow = (geom[3] + 2 * geom[10] - geom[6]) / geom[8] + 1;
+  if (y.shape() != Shape({geom[0], geom[4], oh, ow})) return invalid(op, "output shape " + y.shape().to_string() + " does not match the geometry");
+  if (w.shape().dim(1) * geom[11] != geom[1]) return invalid(op, "filter channels do not match Cin/groups");
+  if (bias != nullptr && (bias->shape().rank() != 1 || bias->shape().dim(0) != geom[4])) return invalid(op, "bias must be [Cout]");
+  Result<fh_epilogue> ep = make_epilogue(ctx, op, n_main);
+  if (!ep.is_ok()) return ep.status();
+  FRAME_HIP_RETURN_IF_ERROR(fh_conv2d_fwd(dt.value(), x.raw_data(), w.raw_data(), bias ? bias->raw_data() : nullptr,
+                                          y.raw_data(), geom, ep.value().nseg > 0 ? &ep.value() : nullptr, stream_handle(ctx)),
+                            "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
+Status conv2d_kernel(KernelContext& ctx) {
+  if (ctx.inputs.size() != 2 && ctx.inputs.size() != 3) return invalid("conv2d", "expects 2 or 3 inputs");
+  return conv_impl(ctx, "conv2d", ctx.inputs.size());
+}
+
+Status conv_epilogue_kernel(KernelContext& ctx) {
+  const auto* n_main = attr<int64_t>(ctx, "n_main_inputs");
+  return conv_impl(ctx, std::string(kConvEpilogueOp), n_main ? static_cast<size_t>(*n_main) : 2);
+}
+
+// ---- row reductions ---------------------------------------------------------------------------------------
+
+Status softmax_kernel(KernelContext& ctx) {
+  FRAME_RETURN_IF_ERROR(arity(ctx, "softmax", 1, 1));
+  FRAME_RETURN_IF_ERROR(same_dtype(ctx, "softmax"));
+  const Tensor& x = ctx.inputs[0];
+  if (x.shape().rank() != 2 || !(ctx.outputs[0].shape() == x.shape())) return invalid("softmax", "expects matching rank-2 tensors");
+  Result<int32_t> dt = float_code("softmax", x.dtype());
+  if (!dt.is_ok()) return dt.status();
+  FRAME_HIP_RETURN_IF_ERROR(fh_softmax_rows(dt.value(), x.raw_data(), ctx.outputs[0].raw_data(), x.shape().dim(0),
+                                            x.shape().dim(1), stream_handle(ctx)),
+                            "op 'softmax' (hip)");
+  return Status::ok();
+}
+
+Status layer_norm_kernel(KernelContext& ctx) {
+  FRAME_RETURN_IF_ERROR(arity(ctx, "layer_norm", 3, 1));
+  FRAME_RETURN_IF_ERROR(same_dtype(ctx, "layer_norm"));
+  const Tensor& x = ctx.inputs[0];
+  const auto* eps = attr<double>(ctx, "eps");
+  if (eps == nullptr) return invalid("layer_norm", "missing attribute 'eps'");
+  if (x.shape().rank() != 2 || ctx.inputs[1].numel() != x.shape().dim(1) || ctx.inputs[2].numel() != x.shape().dim(1))
+    return invalid("layer_norm", "expects x [N, D], gamma [D], beta [D]");
+  Result<int32_t> dt = float_code("layer_norm", x.dtype());
+  if (!dt.is_ok()) return dt.status();
+  FRAME_HIP_RETURN_IF_ERROR(fh_layer_norm_rows(dt.value(), x.raw_data(), ctx.inputs[1].raw_data(), ctx.inputs[2].raw_data(),
+                                               ctx.outputs[0].raw_data(), x.shape().dim(0), x.shape().dim(1),
+                                               static_cast<float>(*eps), stream_handle(ctx)),
+                            "op 'layer_norm' (hip)");
+  return Status::ok();
+}
+
+template <int Mode>
+Status pool_kernel(KernelContext& ctx) {
+  const std::string op = Mode == 0 ? "max_pool2d" : "avg_pool2d";
+  FRAME_RETURN_IF_ERROR(arity(ctx, op, 1, 1));
+  FRAME_RETURN_IF_ERROR(same_dtype(ctx, op));
+  const auto* k = attr<std::vector<int64_t>>(ctx, "kernel");
+  const auto* s = attr<std::vector<int64_t>>(ctx, "stride");
+  const auto* p = attr<std::vector<int64_t>>(ctx, "padding");
+  if (!k || !s || !p || k->size() != 2 || s->size() != 2 || p->size() != 2) return invalid(op, "missing or malformed attributes");
+  const Tensor& x = ctx.inputs[0];
+  if (x.shape().rank() != 4) return invalid(op, "expects rank-4 input");
+  Result<int32_t> dt = float_code(op, x.dtype());
+  if (!dt.is_ok()) return dt.status();
+  const int64_t geom[10] = {x.shape().dim(0), x.shape().dim(1), x.shape().dim(2), x.shape().dim(3), (*k)[0],
+                            (*k)[1],          (*s)[0],          (*s)[1],          (*p)[0],          (*p)[1]};
+  const int64_t oh = (geom[2] + 2 * geom[8] - geom[4]) / geom[6] + 1;
+  const int64_t ow = (geom[3] + 2 * geom[9] - geom[5]) / geom[7] + 1;
+  if (ctx.outputs[0].shape() != Shape({geom[0], geom[1], oh, ow})) return invalid(op, "output shape does not match the geometry");
+  FRAME_HIP_RETURN_IF_ERROR(fh_pool2d(dt.value(), Mode, x.raw_data(), ctx.outputs[0].raw_data(), geom, stream_handle(ctx)),
+                            "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
+// ---- data movement (bit-exact, any dtype) -----------------------------------------------------------------
+
+Status reshape_kernel(KernelContext& ctx) {
+  FRAME_RETURN_IF_ERROR(arity(ctx, "reshape", 1, 1));
+  const Tensor& x = ctx.inputs[0];
+  Tensor& y = ctx.outputs[0];
+  if (x.numel() != y.numel() || !(x.dtype() == y.dtype())) return invalid("reshape", "element count or dtype differs");
+  FRAME_HIP_RETURN_IF_ERROR(fh_memcpy(y.raw_data(), x.raw_data(), static_cast<size_t>(x.numel()) * x.dtype().itemsize(),
+                                      FH_D2D, stream_handle(ctx)),
+                            "op 'reshape' (hip)");
+  return Status::ok();
+}
+
+Status transpose_kernel(KernelContext& ctx) {
+  FRAME_RETURN_IF_ERROR(arity(ctx, "transpose", 1, 1));
+  const Tensor& x = ctx.inputs[0];
+  const auto* perm = attr<std::vector<int64_t>>(ctx, "perm");
+  const int64_t r = x.shape().rank();
+  if (perm == nullptr || static_cast<int64_t>(perm->size()) != r || r > 8) return invalid("transpose", "bad 'perm' or rank above 8");
+  const auto& st = x.strides().values();
+  std::vector<int64_t> out_dims, in_strides;
+  for (int64_t d = 0; d < r; ++d) {
+    const int64_t p = (*perm)[static_cast<size_t>(d)];
+    if (p < 0 || p >= r) return invalid("transpose", "perm entry out of range");
+    out_dims.push_back(x.shape().dim(p));
+    in_strides.push_back(st[static_cast<size_t>(p)]);
+  }
+  if (ctx.outputs[0].shape() != Shape(out_dims)) return invalid("transpose", "output shape does not match perm");
+  if (x.numel() == 0) return Status::ok();
+  FRAME_HIP_RETURN_IF_ERROR(fh_permute(static_cast<int32_t>(x.dtype().itemsize()), x.raw_data(), ctx.outputs[0].raw_data(),
+                                       static_cast<int32_t>(r), out_dims.data(), in_strides.data(), stream_handle(ctx)),
+                            "op 'transpose' (hip)");
+  return Status::ok();
+}
+
+// Row-major tensor seen as [outer, dim(axis) * inner] bytes around `axis`.
+void split_at_axis(const Shape& s, int64_t axis, size_t item, int64_t& outer, int64_t& inner_bytes) {
+  outer = 1;
+  for (int64_t d = 0; d < axis; ++d) outer *= s.dim(d);
+  int64_t inner = 1;
+  for (int64_t d = axis + 1; d < s.rank(); ++d) inner *= s.dim(d);
+  inner_bytes = inner * static_cast<int64_t>(item);
+}
+
+Status slice_kernel(KernelContext& ctx) {
+  FRAME_RETURN_IF_ERROR(arity(ctx, "slice", 1, 1));
+  const Tensor& x = ctx.inputs[0];
+  const auto* axis = attr<int64_t>(ctx, "axis");
+  const auto* start = attr<int64_t>(ctx, "start");
+  const auto* stop = attr<int64_t>(ctx, "stop");
+  if (!axis || !start || !stop || *axis < 0 || *axis >= x.shape().rank() || !(0 <= *start && *start < *stop && *stop <= x.shape().dim(*axis)))
+    return invalid("slice", "bad axis/start/stop");
+  int64_t outer = 0, inner = 0;
+  split_at_axis(x.shape(), *axis, x.dtype().itemsize(), outer, inner);
+  const int64_t src_pitch = x.shape().dim(*axis) * inner;
+  const int64_t width = (*stop - *start) * inner;
+  if (ctx.outputs[0].numel() * static_cast<int64_t>(x.dtype().itemsize()) != outer * width) return invalid("slice", "output size mismatch");
+  FRAME_HIP_RETURN_IF_ERROR(fh_copy2d(ctx.outputs[0].raw_data(), width, static_cast<const char*>(x.raw_data()) + *start * inner,
+                                      src_pitch, width, outer, stream_handle(ctx)),
+                            "op 'slice' (hip)");
+  return Status::ok();
+}
+
+Status concat_kernel(KernelContext& ctx) {
+  if (ctx.inputs.empty() || ctx.outputs.size() != 1) return invalid("concat", "expects >= 1 input and 1 output");
+  const auto* axis = attr<int64_t>(ctx, "axis");
+  Tensor& y = ctx.outputs[0];
+  if (axis == nullptr || *axis < 0 || *axis >= y.shape().rank()) return invalid("concat", "bad axis");
+  int64_t outer = 0, inner = 0;
+  split_at_axis(y.shape(), *axis, y.dtype().itemsize(), outer, inner);
+  const int64_t dst_pitch = y.shape().dim(*axis) * inner;
+  int64_t offset = 0;
+  for (const Tensor& x : ctx.inputs) {
+    if (!(x.dtype() == y.dtype()) || x.shape().rank() != y.shape().rank()) return invalid("concat", "operand dtype/rank differs");
+    const int64_t width = x.shape().dim(*axis) * inner;
+    if (offset + width > dst_pitch) return invalid("concat", "operands exceed the output along the axis");
+    if (width > 0 && outer > 0)
+      FRAME_HIP_RETURN_IF_ERROR(fh_copy2d(static_cast<char*>(y.raw_data()) + offset, dst_pitch, x.raw_data(), width, width,
+                                          outer, stream_handle(ctx)),
+                                "op 'concat' (hip)");
+    offset += width;
+  }
+  if (offset != dst_pitch) return invalid("concat", "operands do not fill the output");
+  return Status::ok();
+}
+
+// Eager constant: host fill, then a synchronous upload. Compiled graphs materialise constants at compile time.
+Status constant_kernel(KernelContext& ctx) {
+  FRAME_RETURN_IF_ERROR(arity(ctx, "constant", 0, 1));
+  if (ctx.attrs == nullptr) return invalid("constant", "requires attrs");
+  Tensor& y = ctx.outputs[0];
+  const size_t bytes = static_cast<size_t>(y.numel()) * y.dtype().itemsize();
+  std::vector<unsigned char> host(std::max<size_t>(bytes, 1));
+  struct HostAlloc final : hal::Allocator {
+    void* p;
+    explicit HostAlloc(void* q) : p(q) {}
+    Result<void*> allocate(size_t, size_t) override { return p; }
+    void deallocate(void*) override {}
+  } ha(host.data());
+  Result<Tensor> h = Tensor::empty(y.shape(), y.dtype(), cpu_device(), ha);
+  if (!h.is_ok()) return h.status();
+  FRAME_RETURN_IF_ERROR(ops::fill_tensor_from_constant_attrs(*ctx.attrs, h.value()));
+  if (bytes > 0) FRAME_HIP_RETURN_IF_ERROR(fh_memcpy(y.raw_data(), host.data(), bytes, FH_H2D, nullptr), "op 'constant' (hip)");
+  return Status::ok();
+}
+
+}  // namespace
+
+FRAME_REGISTER_KERNEL("add", kHipBackendName, (&ew_kernel<FH_EW_ADD, 2>));
+FRAME_REGISTER_KERNEL("mul", kHipBackendName, (&ew_kernel<FH_EW_MUL, 2>));
+FRAME_REGISTER_KERNEL("relu", kHipBackendName, (&ew_kernel<FH_EW_RELU, 1>));
+FRAME_REGISTER_KERNEL("square", kHipBackendName, (&ew_kernel<FH_EW_SQUARE, 1>));
+FRAME_REGISTER_KERNEL("gelu", kHipBackendName, (&ew_kernel<FH_EW_GELU, 1>));
+FRAME_REGISTER_KERNEL(ops::kFusedElementwiseOpName, kHipBackendName, &fused_kernel);
+FRAME_REGISTER_KERNEL("matmul", kHipBackendName, &matmul_kernel);
+FRAME_REGISTER_KERNEL(kGemmEpilogueOp, kHipBackendName, &gemm_epilogue_kernel);
+FRAME_REGISTER_KERNEL("conv2d", kHipBackendName, &conv2d_kernel);
+FRAME_REGISTER_KERNEL(kConvEpilogueOp, kHipBackendName, &conv_epilogue_kernel);
+FRAME_REGISTER_KERNEL("softmax", kHipBackendName, &softmax_kernel);
+FRAME_REGISTER_KERNEL("layer_norm", kHipBackendName, &layer_norm_kernel);
+FRAME_REGISTER_KERNEL("max_pool2d", kHipBackendName, &pool_kernel<0>);
+FRAME_REGISTER_KERNEL("avg_pool2d", kHipBackendName, &pool_kernel<1>);
+FRAME_REGISTER_KERNEL("reshape", kHipBackendName, &reshape_kernel);
+FRAME_REGISTER_KERNEL("transpose", kHipBackendName, &transpose_kernel);
+FRAME_REGISTER_KERNEL("slice", kHipBackendName, &slice_kernel);
+FRAME_REGISTER_KERNEL("concat", kHipBackendName, &concat_kernel);
+FRAME_REGISTER_KERNEL(ops::kConstantOpName, kHipBackendName, &constant_kernel);
+
+}  // namespace frame::backends::hip

@@ -1,0 +1,269 @@
+// C entry points of libframe.so (include/frame_capi.h) over the C++20 host API.
+#pragma GCC visibility push(default)
+#include "frame_capi.h"
+#pragma GCC visibility pop
+
+#include <cstring>
+#include <memory>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include <frame/compiler/pipeline.h>
+#include <frame/core/tensor.h>
+#include <frame/hal/allocator.h>
+#include <frame/hal/backend.h>
+#include <frame/hal/event.h>
+#include <frame/hal/executable.h>
+#include <frame/hal/stream.h>
+#include <frame/ir/graph.h>
+#include <frame/ir/memory_plan.h>
+#include <frame/ir/serialization.h>
+#include <frame/runtime/compile.h>
+
+struct frame_tensor {
+  frame::Tensor t;
+  frame::hal::Backend* backend;
+};
+struct frame_stream {
+  std::unique_ptr<frame::hal::Stream> s;
+};
+struct frame_event {
+  std::unique_ptr<frame::hal::Event> e;
+};
+struct frame_executable {
+  std::shared_ptr<frame::hal::Executable> exe;
+  std::string backend;
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+int fail(const frame::Status& s) {
+  g_error = std::string(s.message());
+  const int code = static_cast<int>(s.code());
+  return code == 0 ? static_cast<int>(frame::ErrorCode::kInternal) : code;
+}
+
+int fail_msg(const std::string& m) {
+  g_error = m;
+  return static_cast<int>(frame::ErrorCode::kInvalidArgument);
+}
+
+int text_out(const std::string& s, char* out, int64_t cap, int64_t* needed) {
+  if (needed != nullptr) *needed = static_cast<int64_t>(s.size()) + 1;
+  if (out == nullptr || cap < static_cast<int64_t>(s.size()) + 1) return -1;
+  std::memcpy(out, s.c_str(), s.size() + 1);
+  return 0;
+}
+
+frame::Result<frame::hal::Backend*> backend_of(const char* name) {
+  if (name == nullptr) return frame::Status::make(frame::ErrorCode::kInvalidArgument, "backend name is null");
+  return frame::hal::BackendRegistry::instance().get(name);
+}
+
+std::vector<frame::Tensor> unwrap(frame_tensor* const* ts, int32_t n) {
+  std::vector<frame::Tensor> v;
+  for (int32_t i = 0; i < n; ++i) v.push_back(ts[i]->t);
+  return v;
+}
+
+}  // namespace
+
+#pragma GCC visibility push(default)
+extern "C" {
+
+const char* frame_last_error(void) { return g_error.c_str(); }
+
+int frame_backends(char* out, int64_t cap, int64_t* needed) {
+  std::string s;
+  for (std::string_view n : frame::hal::BackendRegistry::instance().available()) s += (s.empty() ? "" : ",") + std::string(n);
+  return text_out(s, out, cap, needed);
+}
+
+int frame_device_count(const char* backend, int32_t* count) {
+  auto b = backend_of(backend);
+  if (!b.is_ok()) return fail(b.status());
+  auto n = b.value()->device_count();
+  if (!n.is_ok()) return fail(n.status());
+  *count = n.value();
+  return 0;
+}
+
+int frame_tensor_empty(const char* backend, int32_t device, int32_t dtype, const int64_t* dims, int32_t rank,
+                       frame_tensor** out) {
+  if (out == nullptr || rank < 0 || (rank > 0 && dims == nullptr)) return fail_msg("frame_tensor_empty: bad arguments");
+  if (dtype < 0 || dtype >= static_cast<int32_t>(frame::DTypeCode::kCount)) return fail_msg("frame_tensor_empty: bad dtype");
+  auto b = backend_of(backend);
+  if (!b.is_ok()) return fail(b.status());
+  const frame::Device dev{b.value()->name(), device};
+  frame::hal::Allocator* a = b.value()->allocator(dev);
+  if (a == nullptr) return fail_msg("frame_tensor_empty: backend has no allocator for device " + std::to_string(device));
+  auto t = frame::Tensor::empty(frame::Shape(std::vector<int64_t>(dims, dims + rank)),
+                                frame::DType(static_cast<frame::DTypeCode>(dtype)), dev, *a);
+  if (!t.is_ok()) return fail(t.status());
+  *out = new frame_tensor{t.value(), b.value()};
+  return 0;
+}
+
+void frame_tensor_free(frame_tensor* t) { delete t; }
+void* frame_tensor_data(frame_tensor* t) { return t == nullptr ? nullptr : t->t.raw_data(); }
+int64_t frame_tensor_nbytes(const frame_tensor* t) {
+  return t == nullptr ? 0 : t->t.numel() * static_cast<int64_t>(t->t.dtype().itemsize());
+}
+
+int frame_tensor_upload(frame_tensor* t, const void* host, size_t bytes) {
+  if (t == nullptr || static_cast<int64_t>(bytes) != frame_tensor_nbytes(t)) return fail_msg("frame_tensor_upload: size mismatch");
+  frame::Status s = t->backend->copy(t->t.raw_data(), t->t.device(), host, frame::cpu_device(), bytes, nullptr);
+  return s.is_ok() ? 0 : fail(s);
+}
+
+int frame_tensor_download(const frame_tensor* t, void* host, size_t bytes) {
+  if (t == nullptr || static_cast<int64_t>(bytes) != frame_tensor_nbytes(t)) return fail_msg("frame_tensor_download: size mismatch");
+  frame::Status s = t->backend->copy(host, frame::cpu_device(), t->t.raw_data(), t->t.device(), bytes, nullptr);
+  return s.is_ok() ? 0 : fail(s);
+}
+
+int frame_stream_create(const char* backend, int32_t device, frame_stream** out) {
+  auto b = backend_of(backend);
+  if (!b.is_ok()) return fail(b.status());
+  auto s = b.value()->create_stream(frame::Device{b.value()->name(), device});
+  if (!s.is_ok()) return fail(s.status());
+  *out = new frame_stream{std::move(s.value())};
+  return 0;
+}
+void frame_stream_destroy(frame_stream* s) { delete s; }
+int frame_stream_synchronize(frame_stream* s) {
+  frame::Status st = s->s->synchronize();
+  return st.is_ok() ? 0 : fail(st);
+}
+void* frame_stream_native(frame_stream* s) { return s->s->native_handle(); }
+
+int frame_event_create(const char* backend, int32_t device, frame_event** out) {
+  auto b = backend_of(backend);
+  if (!b.is_ok()) return fail(b.status());
+  auto e = b.value()->create_event(frame::Device{b.value()->name(), device});
+  if (!e.is_ok()) return fail(e.status());
+  *out = new frame_event{std::move(e.value())};
+  return 0;
+}
+void frame_event_destroy(frame_event* e) { delete e; }
+int frame_event_record(frame_event* e, frame_stream* s) {
+  frame::Status st = s->s->record(*e->e);
+  return st.is_ok() ? 0 : fail(st);
+}
+int frame_event_synchronize(frame_event* e) {
+  frame::Status st = e->e->synchronize();
+  return st.is_ok() ? 0 : fail(st);
+}
+
+int frame_compile(const char* ir_text, const char* backend, int32_t opt_level, frame_executable** out) {
+  if (ir_text == nullptr || backend == nullptr || out == nullptr) return fail_msg("frame_compile: null argument");
+  auto g = frame::ir::parse_text(ir_text);
+  if (!g.is_ok()) return fail(g.status());
+  frame::hal::CompileOptions opts;
+  opts.opt_level = opt_level;
+  auto e = frame::runtime::compile(g.value(), backend, opts);
+  if (!e.is_ok()) return fail(e.status());
+  *out = new frame_executable{e.value(), backend};
+  return 0;
+}
+
+void frame_executable_free(frame_executable* e) { delete e; }
+int32_t frame_executable_num_inputs(const frame_executable* e) {
+  return static_cast<int32_t>(e->exe->input_signature().size());
+}
+int32_t frame_executable_num_outputs(const frame_executable* e) {
+  return static_cast<int32_t>(e->exe->output_signature().size());
+}
+
+int frame_executable_io_spec(const frame_executable* e, int32_t is_output, int32_t index, int32_t* dtype, int64_t* dims,
+                             int32_t* rank) {
+  const auto sig = is_output ? e->exe->output_signature() : e->exe->input_signature();
+  if (index < 0 || index >= static_cast<int32_t>(sig.size())) return fail_msg("frame_executable_io_spec: index out of range");
+  const auto& s = sig[static_cast<size_t>(index)];
+  if (s.shape.rank() > 8) return fail_msg("frame_executable_io_spec: rank above 8");
+  *dtype = static_cast<int32_t>(s.dtype.code());
+  *rank = static_cast<int32_t>(s.shape.rank());
+  for (int64_t i = 0; i < s.shape.rank(); ++i) dims[i] = s.shape.dim(i);
+  return 0;
+}
+
+int frame_executable_run(frame_executable* e, frame_tensor* const* inputs, int32_t n_in, frame_tensor* const* outputs,
+                         int32_t n_out, frame_stream* stream) {
+  if (e == nullptr || stream == nullptr) return fail_msg("frame_executable_run: null argument");
+  std::vector<frame::Tensor> ins = unwrap(inputs, n_in), outs = unwrap(outputs, n_out);
+  frame::Status s = e->exe->run(ins, outs, *stream->s);
+  return s.is_ok() ? 0 : fail(s);
+}
+
+int frame_run_with_allocated_outputs(frame_executable* e, frame_tensor* const* inputs, int32_t n_in,
+                                     frame_tensor** outputs, int32_t n_out) {
+  std::vector<frame::Tensor> ins = unwrap(inputs, n_in);
+  auto r = frame::runtime::run_with_allocated_outputs(*e->exe, e->backend, ins);
+  if (!r.is_ok()) return fail(r.status());
+  if (static_cast<int32_t>(r.value().size()) != n_out) return fail_msg("frame_run_with_allocated_outputs: output count mismatch");
+  auto b = backend_of(e->backend.c_str());
+  for (int32_t i = 0; i < n_out; ++i) outputs[i] = new frame_tensor{r.value()[static_cast<size_t>(i)], b.value()};
+  return 0;
+}
+
+int64_t frame_compile_cache_size(void) { return static_cast<int64_t>(frame::runtime::compilation_cache_size()); }
+
+int frame_transform_text(const char* ir_text, const char* pass_name, char* out, int64_t cap, int64_t* needed) {
+  auto g = frame::ir::parse_text(ir_text);
+  if (!g.is_ok()) return fail(g.status());
+  frame::compiler::PassManager pm;
+  if (pass_name != nullptr && pass_name[0] != '\0') {
+    pm.add(pass_name);
+  } else {
+    auto p = frame::compiler::standard_pipeline("");
+    if (!p.is_ok()) return fail(p.status());
+    pm = std::move(p.value());
+  }
+  frame::Status s = pm.run(g.value());
+  if (!s.is_ok()) return fail(s);
+  return text_out(frame::ir::dump_text(g.value()), out, cap, needed);
+}
+
+int frame_roundtrip_text(const char* ir_text, char* out, int64_t cap, int64_t* needed) {
+  auto g = frame::ir::parse_text(ir_text);
+  if (!g.is_ok()) return fail(g.status());
+  return text_out(frame::ir::dump_text(g.value()), out, cap, needed);
+}
+
+int frame_memory_plan_text(const char* ir_text, char* out, int64_t cap, int64_t* needed) {
+  auto g = frame::ir::parse_text(ir_text);
+  if (!g.is_ok()) return fail(g.status());
+  auto plan = frame::ir::compute_memory_plan(g.value());
+  if (!plan.is_ok()) return fail(plan.status());
+  std::ostringstream os;
+  for (const auto& [k, e] : plan.value().entries)
+    os << k.first << ' ' << k.second << ' ' << e.byte_offset << ' ' << e.size_bytes << ' ' << e.def_index << ' '
+       << e.last_use_index << '\n';
+  os << "total " << plan.value().total_bytes << '\n';
+  return text_out(os.str(), out, cap, needed);
+}
+
+int frame_launch(const char* node_ir_text, const char* backend, frame_tensor* const* inputs, int32_t n_in,
+                 frame_tensor* const* outputs, int32_t n_out, frame_stream* stream) {
+  auto g = frame::ir::parse_text(node_ir_text);
+  if (!g.is_ok()) return fail(g.status());
+  const frame::ir::Node* node = nullptr;
+  for (const frame::ir::Node* n : g.value().topological_order()) {
+    if (n->op() == frame::ir::kGraphInputOp) continue;
+    if (node != nullptr) return fail_msg("frame_launch: the text holds more than one operator node");
+    node = n;
+  }
+  if (node == nullptr) return fail_msg("frame_launch: the text holds no operator node");
+  auto b = backend_of(backend);
+  if (!b.is_ok()) return fail(b.status());
+  std::vector<frame::Tensor> ins = unwrap(inputs, n_in), outs = unwrap(outputs, n_out);
+  frame::hal::KernelInvocation inv{node->op(), ins, outs, &node->attrs(), frame::Device{b.value()->name(), 0}};
+  frame::Status s = b.value()->launch(inv, stream ? stream->s.get() : nullptr);
+  return s.is_ok() ? 0 : fail(s);
+}
+
+}  // extern "C"
+#pragma GCC visibility pop

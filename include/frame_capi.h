@@ -1,0 +1,86 @@
+/*
+ * frame_capi.h — C entry points of the Frame host library (libframe.so) for foreign-function callers.
+ *
+ * It is the C counterpart of the reference's Python binding surface for the compiled-graph path
+ * (reference: python/src/bind_runtime.cpp:30-56 — compile(graph, backend) and Executable.run over
+ * runtime::run_with_allocated_outputs — and python/src/bind_core.cpp for tensors): graphs cross the boundary
+ * as Frame IR text (the dump_text format), tensors and executables as opaque handles. No C++ type crosses it.
+ *
+ * Every function returning int returns 0 on success or a frame::ErrorCode ordinal; the message of the last
+ * failure on the calling thread is frame_last_error(). Text outputs use the (out, cap, needed) convention:
+ * *needed receives the size including the terminating NUL; with out == NULL or cap too small the call returns
+ * -1 and writes nothing.
+ */
+#ifndef FRAME_CAPI_H_
+#define FRAME_CAPI_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct frame_tensor frame_tensor;
+typedef struct frame_stream frame_stream;
+typedef struct frame_event frame_event;
+typedef struct frame_executable frame_executable;
+
+const char* frame_last_error(void);
+
+/* Registered backend names, comma-separated (BackendRegistry::available). */
+int frame_backends(char* out, int64_t cap, int64_t* needed);
+int frame_device_count(const char* backend, int32_t* count);
+
+/* Tensors: dtype codes are frame::DTypeCode ordinals (0 float32, 2 float16, 3 bfloat16, ...). */
+int frame_tensor_empty(const char* backend, int32_t device, int32_t dtype, const int64_t* dims, int32_t rank,
+                       frame_tensor** out);
+void frame_tensor_free(frame_tensor* t);
+void* frame_tensor_data(frame_tensor* t);
+int64_t frame_tensor_nbytes(const frame_tensor* t);
+int frame_tensor_upload(frame_tensor* t, const void* host, size_t bytes);   /* synchronous */
+int frame_tensor_download(const frame_tensor* t, void* host, size_t bytes); /* synchronous */
+
+/* Streams and events of a backend (hal::Stream / hal::Event). */
+int frame_stream_create(const char* backend, int32_t device, frame_stream** out);
+void frame_stream_destroy(frame_stream* s);
+int frame_stream_synchronize(frame_stream* s);
+void* frame_stream_native(frame_stream* s); /* hipStream_t for the hip backend */
+int frame_event_create(const char* backend, int32_t device, frame_event** out);
+void frame_event_destroy(frame_event* e);
+int frame_event_record(frame_event* e, frame_stream* s);
+int frame_event_synchronize(frame_event* e);
+
+/* runtime::compile of IR text for `backend` (opt_level as hal::CompileOptions::opt_level). */
+int frame_compile(const char* ir_text, const char* backend, int32_t opt_level, frame_executable** out);
+void frame_executable_free(frame_executable* e);
+int32_t frame_executable_num_inputs(const frame_executable* e);
+int32_t frame_executable_num_outputs(const frame_executable* e);
+/* dims must hold 8 entries; writes dtype code and rank. */
+int frame_executable_io_spec(const frame_executable* e, int32_t is_output, int32_t index, int32_t* dtype, int64_t* dims,
+                             int32_t* rank);
+/* Executable::run on `stream` (enqueue only). */
+int frame_executable_run(frame_executable* e, frame_tensor* const* inputs, int32_t n_in, frame_tensor* const* outputs,
+                         int32_t n_out, frame_stream* stream);
+/* runtime::run_with_allocated_outputs: allocates outputs on device 0 of the backend, runs, synchronises. */
+int frame_run_with_allocated_outputs(frame_executable* e, frame_tensor* const* inputs, int32_t n_in,
+                                     frame_tensor** outputs, int32_t n_out);
+/* Number of entries in the compile cache. */
+int64_t frame_compile_cache_size(void);
+
+/* Compiler observability: the standard pipeline (pass_name NULL or "") or one named pass applied to the
+ * parsed text, dump_text round trip, and the memory plan as lines "topo out offset size def last" + "total N". */
+int frame_transform_text(const char* ir_text, const char* pass_name, char* out, int64_t cap, int64_t* needed);
+int frame_roundtrip_text(const char* ir_text, char* out, int64_t cap, int64_t* needed);
+int frame_memory_plan_text(const char* ir_text, char* out, int64_t cap, int64_t* needed);
+
+/* Eager single-op launch (Backend::launch) of the one operator node in `node_ir_text` (a graph whose
+ * non-input nodes are exactly one op) on the given tensors. */
+int frame_launch(const char* node_ir_text, const char* backend, frame_tensor* const* inputs, int32_t n_in,
+                 frame_tensor* const* outputs, int32_t n_out, frame_stream* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FRAME_CAPI_H_ */

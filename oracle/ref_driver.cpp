@@ -39,6 +39,7 @@ int copy_text(const std::string& s, char* out, int64_t cap, int64_t* needed) {
 
 }  // namespace
 
+#pragma GCC visibility push(default)
 extern "C" {
 
 const char* ref_last_error(void) { return g_error.c_str(); }
@@ -145,3 +146,4 @@ int ref_memory_plan_text(const char* ir_text, char* out, int64_t cap, int64_t* n
 }
 
 }  // extern "C"
+#pragma GCC visibility pop

@@ -52,6 +52,28 @@ def oracle() -> ctypes.CDLL:
     return _oracle
 
 
+_cpu_backend = None
+
+
+def load_cpu_backend() -> None:
+    """Registers the oracle as Frame's `cpu` backend inside the already-loaded libframe.so."""
+    global _cpu_backend
+    if _cpu_backend is None:
+        from frame_hip import host
+
+        host.lib()
+        _cpu_backend = ctypes.CDLL(ORACLE_CPU_BACKEND, mode=ctypes.RTLD_GLOBAL)
+
+
+def run_graph_cpu(graph, inputs, opt_level: int = 1):
+    """Compiles `graph` (a graphs.Graph on device 'cpu', or IR text) through runtime::compile for the oracle's
+    cpu backend and runs it on host arrays."""
+    from frame_hip import host
+
+    load_cpu_backend()
+    return host.compile(graph, "cpu", opt_level).run(inputs)
+
+
 def ref_available() -> bool:
     return os.path.exists(REF_LIB)
 

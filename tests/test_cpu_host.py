@@ -1,0 +1,172 @@
+"""The C++20 host side (libframe.so) on the CPU: the C ABI surface, the nine-pass pipeline against the
+reference's own golden IR fixtures (tests/golden/compiler, copied from the reference's
+tests/cpp/compiler/testdata) and against the reference pipeline itself, the memory plan, the compile cache and
+the error contract. No GPU is touched: graphs here live on the oracle's `cpu` backend, and hip graphs stop
+before Backend::compile."""
+import os
+import re
+import subprocess
+
+import pytest
+
+import oracle_lib as orc
+from frame_hip import abi, graphs, host
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+GOLDEN = os.path.join(REPO, "tests", "golden", "compiler")
+needs_ref = pytest.mark.skipif(not orc.ref_available(), reason="oracle/_ref not built (no /root/reference here)")
+
+PASS_OF_PREFIX = {
+    "add_passthrough": "backend_lowering",
+    "canonicalize": "canonicalize",
+    "constant_folding": "constant_folding",
+    "cse": "common_subexpression_elimination",
+    "dne": "dead_node_elimination",
+    "layout_assignment": "layout_assignment",
+    "memory_planning": "memory_planning",
+    "operator_fusion": "operator_fusion",
+}
+
+
+def golden_cases():
+    cases = []
+    for f in sorted(os.listdir(GOLDEN)):
+        if not f.endswith("_input.txt"):
+            continue
+        stem = f[: -len("_input.txt")]
+        expected = os.path.join(GOLDEN, stem + "_expected.txt")
+        if not os.path.exists(expected):
+            continue
+        prefix = next(p for p in PASS_OF_PREFIX if stem.startswith(p))
+        cases.append((stem, PASS_OF_PREFIX[prefix]))
+    return cases
+
+
+def read(name):
+    with open(os.path.join(GOLDEN, name)) as fh:
+        return fh.read()
+
+
+def declared(header, pattern):
+    with open(os.path.join(REPO, "include", header)) as fh:
+        text = fh.read()
+    return sorted(set(re.findall(pattern, text)))
+
+
+def exported(lib_path):
+    out = subprocess.run(["nm", "-D", "--defined-only", lib_path], check=True, capture_output=True, text=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if line.strip()}
+
+
+def test_kernel_abi_library_exports_every_declared_symbol():
+    syms = declared("frame_hip_abi.h", r"\b(fh_[a-z0-9_]+)\s*\(")
+    assert len(syms) >= 25
+    have = exported(abi.KERNELS_LIB)
+    assert not [s for s in syms if s not in have], "missing kernel ABI symbols"
+    abi.lib()  # loads (no device call)
+    assert set(abi.exported_symbols()) <= set(syms)
+
+
+def test_host_library_exports_every_declared_symbol():
+    syms = declared("frame_capi.h", r"\b(frame_[a-z0-9_]+)\s*\(")
+    assert len(syms) >= 25
+    have = exported(host.HOST_LIB)
+    assert not [s for s in syms if s not in have], "missing host C API symbols"
+    host.lib()
+    assert set(host.exported_symbols()) == set(syms)
+
+
+def test_hip_backend_is_registered_through_the_hal():
+    assert "hip" in host.backends()
+
+
+@pytest.fixture(scope="module")
+def cpu_backend():
+    orc.load_cpu_backend()
+
+
+@pytest.mark.parametrize("stem,pass_name", golden_cases())
+def test_pass_matches_reference_golden(cpu_backend, stem, pass_name):
+    if stem.startswith("dne_side_effect"):
+        pytest.skip("needs the reference's test-only op test_side_effect_op")
+    got = host.transform(read(stem + "_input.txt"), pass_name)
+    assert got == read(stem + "_expected.txt")
+
+
+@pytest.mark.parametrize("stem", [s for s, _ in golden_cases()])
+def test_text_round_trip(stem):
+    text = read(stem + "_input.txt")
+    if "test_side_effect_op" in text:
+        pytest.skip("test-only op")
+    assert host.roundtrip(text) == text
+
+
+def sample_graph_texts():
+    g1 = graphs.mlp(batch=8, dtype=0, device="cpu").text()
+    g2, _ = graphs.resnet18(batch=1, dtype=3, device="cpu", image=32, classes=10)
+    g3, _ = graphs.transformer_block(batch=2, seq=16, d_model=32, heads=2, ffn=64, dtype=3, device="cpu")
+    g4 = graphs.conv(0, device="cpu", n=1, cin=4, h=6, w=6, cout=4).text()
+    return {"mlp": g1, "resnet": g2.text(), "transformer_relu": g3.text().replace(" gelu(", " relu("), "conv": g4}
+
+
+@needs_ref
+@pytest.mark.parametrize("name", ["mlp", "resnet", "transformer_relu", "conv"])
+def test_standard_pipeline_matches_reference(cpu_backend, name):
+    text = sample_graph_texts()[name]
+    assert host.transform(text) == orc.ref_transform(text)
+
+
+@needs_ref
+@pytest.mark.parametrize("name", ["mlp", "resnet", "transformer_relu", "conv"])
+def test_memory_plan_matches_reference(cpu_backend, name):
+    text = host.transform(sample_graph_texts()[name])
+    assert host.memory_plan(text) == orc.ref_memory_plan(text)
+
+
+def test_gelu_chain_fuses_on_hip():
+    # add(matmul, bias) -> gelu becomes one fused group for the hip backend
+    g, _ = graphs.transformer_block(batch=1, seq=8, d_model=16, heads=2, ffn=32, dtype=3, device="hip")
+    out = host.transform(g.text())
+    assert 'ops="add;gelu"' in out and 'ops="add;add"' in out
+    assert out.count("constant(") == 1  # CSE merged the per-head scale constants
+
+
+def test_compile_cache_hits(cpu_backend):
+    text = graphs.mlp(batch=4, dtype=0, device="cpu").text()
+    host.compile(text, "cpu")
+    n = host.compile_cache_size()
+    host.compile(text, "cpu")
+    assert host.compile_cache_size() == n
+    host.compile(text, "cpu", opt_level=0)  # options are part of the key
+    assert host.compile_cache_size() == n + 1
+
+
+def test_unknown_backend_is_not_found():
+    with pytest.raises(host.FrameError) as e:
+        host.compile(graphs.mlp(batch=2, device="cpu").text(), "no_such_backend")
+    assert e.value.code == host.CODES["invalid_argument"]  # device/backend mismatch is checked first
+    g = graphs.Graph("cpu")
+    x = g.input(0, (2,))
+    g.output(g.relu(x))
+    with pytest.raises(host.FrameError) as e:
+        host.transform(g.text().replace("@cpu:0", "@ascend:0"))
+    assert e.value.code == host.CODES["not_found"]
+
+
+def test_op_without_hip_kernel_is_unimplemented_with_its_name():
+    g = graphs.Graph("hip")
+    x = g.input(0, (4,))
+    g.output(g.op("sigmoid", [x], (4,)))
+    with pytest.raises(host.FrameError) as e:
+        host.compile(g.text(), "hip")
+    assert e.value.code == host.CODES["unimplemented"] and "sigmoid" in str(e.value)
+
+
+def test_shape_inference_rejects_inconsistent_types():
+    g = graphs.Graph("cpu")
+    a = g.input(0, (2, 3))
+    b = g.input(0, (4, 5))
+    g.output(g.op("matmul", [a, b], (2, 5)))
+    with pytest.raises(host.FrameError) as e:
+        host.transform(g.text())
+    assert "contraction dimension mismatch" in str(e.value)

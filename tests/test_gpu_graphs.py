@@ -1,0 +1,197 @@
+"""Compiled-graph parity on the MI355X: every configuration of BASELINE.json goes through
+runtime::compile(graph, "hip") -> HipBackend::compile -> HipExecutable::run (the product path, C ABI kernels
+underneath) and is compared with the same graph compiled for the oracle's `cpu` backend on identical seeded
+inputs. Tolerances (stated per test) follow the north star: rtol 1e-5 for float32, 1e-2 for bfloat16, with
+atol = rtol * rms(expected) (tests/tolerance.py). Full-size configurations that the single-threaded oracle
+cannot finish in seconds are checked on sampled outputs recomputed with the oracle's per-element formula, or on
+independent batch rows (each image / sequence of a batch is computed independently by every op on the path).
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle_lib as orc
+from frame_hip import graphs, host, synth
+from tolerance import assert_bitwise, assert_close
+
+pytestmark = pytest.mark.gpu
+F32, F16, BF16 = 0, 2, 3
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+@pytest.fixture(scope="module")
+def dev():
+    n = host.device_count("hip")
+    assert n >= 1, "no hip device"
+    orc.load_cpu_backend()
+    return n
+
+
+def run_hip(g, ins, opt_level=1):
+    return host.compile(g, "hip", opt_level).run(ins)
+
+
+def retarget(g, device):
+    return g.text().replace("@hip:0", f"@{device}:0")
+
+
+# ---- HAL conformance (reference: tests/cpp/hal_conformance/test_hal_conformance.cpp:65-275) ---------------
+
+def test_hal_conformance(dev):
+    lib = host.lib()
+    s = host.Stream("hip")
+    ev = ctypes.c_void_p()
+    host.check(lib.frame_event_create(b"hip", 0, ctypes.byref(ev)))
+    host.check(lib.frame_event_synchronize(ev))  # never recorded: complete
+    host.check(lib.frame_event_record(ev, s.handle))
+    host.check(lib.frame_event_synchronize(ev))
+    lib.frame_event_destroy(ev)
+    a = np.arange(16, dtype=np.float32)  # 64 bytes through H2D / D2H
+    t = host.Tensor.from_numpy("hip", F32, a)
+    assert_bitwise(t.numpy(), a, "allocator round trip")
+    assert t.data_ptr % 256 == 0
+
+
+def test_eager_launch_add(dev):
+    g = graphs.Graph("hip")
+    x, y = g.input(F32, (1000,)), g.input(F32, (1000,))
+    g.output(g.add(x, y))
+    a, b = synth.tensor(1, (1000,), F32), synth.tensor(2, (1000,), F32)
+    ta, tb = host.Tensor.from_numpy("hip", F32, a), host.Tensor.from_numpy("hip", F32, b)
+    out = host.Tensor("hip", F32, (1000,))
+    s = host.Stream("hip")
+    host.launch(g.text(), "hip", [ta, tb], [out], s)
+    s.synchronize()
+    assert_bitwise(out.numpy(), a + b, "eager add")
+
+
+# ---- C1 --------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("batch", [64, 3])
+def test_c1_mlp(dev, batch):
+    say(f"C1 mlp f32 batch={batch}")
+    g = graphs.mlp(batch=batch, dtype=F32, device="hip")
+    ins = graphs.mlp_inputs(batch=batch, dtype=F32, seed=7)
+    (got,) = run_hip(g, ins)
+    (want,) = orc.run_graph_cpu(retarget(g, "cpu"), ins)
+    assert_close(got, want, F32, what="C1 mlp")  # rtol 1e-5, atol 1e-5 * rms
+    np.testing.assert_allclose(got.sum(1), 1.0, rtol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16])
+def test_epilogue_fusion_is_exact(dev, dtype):
+    # opt_level 1 folds add;relu / add into the GEMM epilogue; opt_level 0 runs the unfused kernels: equal bits
+    say(f"epilogue exactness dtype={dtype}")
+    g = graphs.mlp(batch=64, dtype=dtype, device="hip")
+    ins = graphs.mlp_inputs(batch=64, dtype=dtype, seed=9)
+    assert_bitwise(run_hip(g, ins, 1)[0], run_hip(g, ins, 0)[0], "opt1 vs opt0")
+
+
+# ---- C2 --------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [F32, BF16])
+@pytest.mark.parametrize("n", [1024, 2048, 4096])
+def test_c2_gemm(dev, dtype, n):
+    say(f"C2 gemm n={n} dtype={dtype}")
+    g = graphs.gemm(n, dtype, device="hip")
+    a, b = graphs.gemm_inputs(n, dtype)
+    (got,) = run_hip(g, [a, b])
+    if n == 1024:
+        want = orc.matmul(dtype, a, b)
+        assert_close(got, want, dtype, what=f"gemm {n}")
+    else:
+        rng = np.random.default_rng(n)
+        rows, cols = rng.integers(0, n, 4096), rng.integers(0, n, 4096)
+        want = orc.matmul_sample(dtype, a, b, rows, cols)
+        # atol from the rms of the full product (U(-1,1) entries: rms = sqrt(n/9))
+        assert_close(got[rows, cols], want, dtype, atol=(1e-5 if dtype == F32 else 1e-2) * np.sqrt(n / 9.0),
+                     what=f"gemm {n} sampled")
+
+
+def test_c2_gemm_odd_shapes(dev):
+    for (m, k, n) in [(1, 1, 1), (7, 13, 5), (300, 264, 200), (17, 4096, 3), (65, 8, 1000)]:
+        for dtype in (F32, BF16):
+            say(f"gemm odd m={m} k={k} n={n} dtype={dtype}")
+            g = graphs.gemm(n, dtype, device="hip", m=m, k=k)
+            ins = graphs.gemm_inputs(n, dtype, m=m, k=k)
+            assert_close(run_hip(g, ins)[0], orc.matmul(dtype, *ins), dtype, what=f"gemm {m}x{k}x{n}")
+
+
+# ---- C3 --------------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", [F32, BF16])
+def test_c3_conv_small_full(dev, dtype):
+    for cfg in (dict(n=2, cin=64, h=12, w=12, cout=64, k=3), dict(n=2, cin=3, h=20, w=20, cout=16, k=7, stride=2, pad=3)):
+        say(f"C3 conv small {cfg} dtype={dtype}")
+        g = graphs.conv(dtype, device="hip", **cfg)
+        ins = graphs.conv_inputs(dtype, n=cfg["n"], cin=cfg["cin"], h=cfg["h"], w=cfg["w"], cout=cfg["cout"], k=cfg["k"])
+        (got,) = run_hip(g, ins)
+        (want,) = orc.run_graph_cpu(retarget(g, "cpu"), ins)
+        assert_close(got, want, dtype, what="conv small")
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16])
+def test_c3_conv_full_sampled(dev, dtype):
+    say(f"C3 conv full dtype={dtype}")
+    g = graphs.conv(dtype, device="hip")
+    x, w, b = graphs.conv_inputs(dtype)
+    (got,) = run_hip(g, [x, w, b])
+    assert got.shape == (32, 64, 56, 56)
+    idx = np.random.default_rng(3).integers(0, got.size, 4096)
+    pre = orc.conv2d_sample(dtype, x, w, b, (32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1), idx)
+    want = orc.ew_program(dtype, [3], [1], [pre])  # relu after the rounded conv output
+    assert_close(got.reshape(-1)[idx], want, dtype, atol=(1e-5 if dtype == F32 else 1e-2) * 1.4, what="conv C3 sampled")
+
+
+# ---- C4 --------------------------------------------------------------------------------------------------
+
+def test_c4_resnet_small_full(dev):
+    say("C4 resnet18 bf16 batch=2 image=64")
+    g, specs = graphs.resnet18(batch=2, dtype=BF16, device="hip", image=64)
+    ins = graphs.resnet18_inputs(specs, batch=2, dtype=BF16, image=64)
+    (got,) = run_hip(g, ins)
+    (want,) = orc.run_graph_cpu(retarget(g, "cpu"), ins)
+    assert_close(got, want, BF16, what="resnet18 64px")
+
+
+def test_c4_resnet_full_rows(dev):
+    # Full configuration on the GPU; the oracle recomputes images 0 and 1 (a batch-2 graph with the same weights
+    # and the first two rows of the [64,1000] classifier bias).
+    say("C4 resnet18 bf16 batch=64 image=224 (rows 0-1 checked)")
+    g, specs = graphs.resnet18(batch=64, dtype=BF16, device="hip")
+    ins = graphs.resnet18_inputs(specs, batch=64, dtype=BF16)
+    (got,) = run_hip(g, ins)
+    assert got.shape == (64, 1000) and np.isfinite(synth.to_float(got, BF16)).all()
+    g2, specs2 = graphs.resnet18(batch=2, dtype=BF16, device="cpu")
+    ins2 = [ins[0][:2]] + ins[1:-1] + [ins[-1][:2]]
+    (want,) = orc.run_graph_cpu(g2, ins2)
+    assert_close(got[:2], want, BF16, what="resnet18 224px rows 0-1")
+
+
+# ---- C5 --------------------------------------------------------------------------------------------------
+
+def test_c5_transformer_small_full(dev):
+    say("C5 transformer bf16 small")
+    g, shapes = graphs.transformer_block(batch=2, seq=64, d_model=128, heads=4, ffn=512, dtype=BF16, device="hip")
+    ins = graphs.transformer_inputs(shapes, rows=128, d_model=128, dtype=BF16)
+    (got,) = run_hip(g, ins)
+    (want,) = orc.run_graph_cpu(retarget(g, "cpu"), ins)
+    assert_close(got, want, BF16, what="transformer small")
+
+
+def test_c5_transformer_full_rows(dev):
+    say("C5 transformer bf16 batch=8 seq=512 (sequence 0 checked)")
+    g, shapes = graphs.transformer_block(dtype=BF16, device="hip")
+    ins = graphs.transformer_inputs(shapes, dtype=BF16)
+    (got,) = run_hip(g, ins)
+    assert got.shape == (4096, 1024) and np.isfinite(synth.to_float(got, BF16)).all()
+    g1, shapes1 = graphs.transformer_block(batch=1, dtype=BF16, device="cpu")
+    # x and the full-shape biases (bq, bk, bv, bo, b1, b2) are per-row; weights and LayerNorm parameters are shared
+    per_row = {0, 4, 6, 8, 10, 14, 16}
+    ins1 = [a[:512] if i in per_row else a for i, a in enumerate(ins)]
+    (want,) = orc.run_graph_cpu(g1, ins1)
+    assert_close(got[:512], want, BF16, what="transformer sequence 0")
