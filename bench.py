@@ -34,31 +34,36 @@ def gemm_flops(m, n, k):
     return 2.0 * m * n * k
 
 
+class _NativeStream:
+    """The hipStream_t under a hal::Stream, for HIP events recorded on the stream the kernels run on."""
+
+    def __init__(self, ptr):
+        self.ptr = ptr
+
+
 def run_gpu(steps: int, warmup: int):
-    from frame_hip import abi, synth
+    """Times `steps` runs of the compiled GEMM graph (runtime::compile(graph, "hip") -> Executable::run) on one
+    persistent stream, inputs and outputs resident in HBM."""
+    from frame_hip import abi, graphs, host
 
-    lib = abi.lib()
-    a = synth.tensor(31, (N, N), BF16, "uniform")
-    b = synth.tensor(32, (N, N), BF16, "uniform")
-    da, db = abi.to_device(a), abi.to_device(b)
-    dc = abi.DeviceBuffer(N * N * 2)
-    stream = abi.Stream()
+    g = graphs.gemm(N, BF16, device="hip")
+    exe = host.compile(g, "hip")
+    ins = exe.upload_inputs(graphs.gemm_inputs(N, BF16))
+    outs = exe.alloc_outputs()
+    stream = host.Stream("hip")
+    native = _NativeStream(stream.native)
     start, stop = abi.Event(), abi.Event()
-
-    def step():
-        abi.check(lib.fh_gemm(BF16, da.value, db.value, dc.value, N, N, N, None, stream.ptr), "fh_gemm")
-
     for _ in range(warmup):
-        step()
+        exe.run_tensors(ins, outs, stream)
     stream.synchronize()
-    abi.check(lib.fh_device_synchronize())
+    abi.check(abi.lib().fh_device_synchronize())
     t0 = time.perf_counter()
-    start.record(stream)
+    start.record(native)
     for _ in range(steps):
-        step()
-    stop.record(stream)
+        exe.run_tensors(ins, outs, stream)
+    stop.record(native)
     stop.synchronize()
-    abi.check(lib.fh_device_synchronize())
+    stream.synchronize()
     wall = time.perf_counter() - t0
     ms = start.elapsed_ms(stop) / steps
     return ms, wall

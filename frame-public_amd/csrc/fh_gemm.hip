@@ -19,8 +19,10 @@
 #include <hip/hip_runtime.h>
 
 #include <string>
+#include <type_traits>
 
 #include "fh_common.h"
+#include "fh_gemm.h"
 
 namespace fh {
 namespace {
@@ -42,24 +44,6 @@ struct GemmTraits<f16_t> {
 template <>
 struct GemmTraits<float> {
   static constexpr int E = 4;
-};
-
-struct EpilogueArgs {
-  int32_t nseg;
-  int32_t round_between;
-  uint8_t ops[FH_MAX_SEGMENTS];
-  const void* ins[FH_MAX_SEGMENTS];
-};
-
-struct GemmArgs {
-  const void* A;
-  const void* B;
-  void* C;
-  int64_t M, N, K;
-  int64_t lda, ldb, ldc;             // row strides in elements
-  int64_t stride_a, stride_b, stride_c;  // batch strides in elements (blockIdx.y)
-  int32_t tiles_m, tiles_n;
-  EpilogueArgs ep;
 };
 
 __device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row ^ (row >> 3)) & 7); }
@@ -416,6 +400,10 @@ bool epilogue_aligned(const EpilogueArgs& ep) {
 template <typename T>
 fh_status dispatch_gemm(GemmArgs args, int64_t batch, hipStream_t stream) {
   constexpr int E = GemmTraits<T>::E;
+  if constexpr (!std::is_same_v<T, float>) {
+    fh_status st = FH_OK;
+    if (gemm16_try_launch(std::is_same_v<T, bf16_t> ? FH_BF16 : FH_F16, args, batch, stream, &st)) return st;
+  }
   const size_t esz = sizeof(typename Io<T>::storage);
   const bool aligned = (reinterpret_cast<uintptr_t>(args.A) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(args.B) % 16 == 0) && (args.K % E == 0) &&
