@@ -21,6 +21,7 @@
 
 #include <string>
 #include <type_traits>
+#include <utility>
 
 #include "fh_common.h"
 #include "fh_gemm.h"
@@ -38,8 +39,9 @@ typedef float f32x16_t __attribute__((ext_vector_type(16)));
 constexpr int kBK = 32;      // k per stage
 constexpr int kStages = 4;   // LDS ring depth
 
-template <typename T>
-__device__ __forceinline__ void mfma32(const uint4& a, const uint4& b, f32x16_t& acc) {
+template <typename T, typename V>
+__device__ __forceinline__ void mfma32(const V& a, const V& b, f32x16_t& acc) {
+  static_assert(sizeof(V) == 16, "8 x 16-bit fragments");
   if constexpr (std::is_same_v<T, bf16_t>) {
     acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
                                                   acc, 0, 0, 0);
@@ -57,14 +59,103 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 
-__device__ __forceinline__ uint4 lds_load128(const FH_LDS unsigned char* p) {
-  const u32x4_t v = *(const FH_LDS u32x4_t*)p;
-  return make_uint4(v[0], v[1], v[2], v[3]);
+// Fragment reads are written as inline asm without a memory clobber. The compiler's LDS-DMA wait tracking does
+// not follow the stage ring across the loop (it either waits for every in-flight prefetch or, on other paths,
+// for nothing), so the main loop orders LDS itself: explicit vmcnt waits + s_barrier before a stage is read,
+// and fragment_fence() (lgkmcnt(0), tied to the fragment registers) before the MFMAs consume them.
+template <int OFF>
+__device__ __forceinline__ u32x4_t lds_read_b128(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+  u32x4_t v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF));
+  return v;
+}
+
+template <int OFF>
+__device__ __forceinline__ u32x2_t lds_read_tr16_b64(uint32_t addr) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+  u32x2_t v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF));
+  return v;
+}
+
+// Keeps an accumulator's MFMA above later fences: VGPR or AGPR constraint, wherever the accumulators live.
+template <bool IN_AGPR>
+__device__ __forceinline__ void pin(f32x16_t& acc) {
+  if constexpr (IN_AGPR) {
+    asm volatile("" : "+a"(acc));
+  } else {
+    asm volatile("" : "+v"(acc));
+  }
+}
+
+// Waits until at most PENDING LDS reads are outstanding (they complete in order), then ties the fragment
+// registers to the wait so no consumer is scheduled above it.
+template <int PENDING, int TM, int TN>
+__device__ __forceinline__ void fragment_fence(u32x4_t (&a)[TM], u32x4_t (&b)[TN]) {
+  static_assert(PENDING >= 0 && PENDING <= 15, "lgkmcnt range");
+  asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(PENDING) : "memory");
+#pragma unroll
+  for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(a[i]));
+#pragma unroll
+  for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(b[j]));
+}
+
+__device__ __forceinline__ uint32_t lds_addr(const FH_LDS void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
 }
 
 __device__ __forceinline__ void global_to_lds16(const void* g, FH_LDS void* lds_wave_base) {
   __builtin_amdgcn_global_load_lds(g, lds_wave_base, 16, 0, 0);
+}
+
+// Runs the epilogue program on 8 rounded outputs (one 16-byte vector) at flat output index idx.
+template <typename T>
+__device__ __forceinline__ uint4 apply_epilogue_vec(const EpilogueArgs& ep, uint4 packed, int64_t idx) {
+  using S = uint16_t;
+  S vals[8];
+  __builtin_memcpy(vals, &packed, 16);
+  float v[8];
+#pragma unroll
+  for (int x = 0; x < 8; ++x) v[x] = Io<T>::load(vals[x]);
+  for (int sg = 0; sg < ep.nseg; ++sg) {
+    const uint8_t op = ep.ops[sg];
+    if (ew_is_binary(op)) {
+      const uint4 in = *reinterpret_cast<const uint4*>(static_cast<const S*>(ep.ins[sg]) + idx);
+      S iv[8];
+      __builtin_memcpy(iv, &in, 16);
+#pragma unroll
+      for (int x = 0; x < 8; ++x) v[x] = ew_binary(op, v[x], Io<T>::load(iv[x]));
+    } else {
+#pragma unroll
+      for (int x = 0; x < 8; ++x) v[x] = ew_unary(op, v[x]);
+    }
+    if (ep.round_between) {
+#pragma unroll
+      for (int x = 0; x < 8; ++x) v[x] = Io<T>::round(v[x]);
+    }
+  }
+#pragma unroll
+  for (int x = 0; x < 8; ++x) vals[x] = Io<T>::store(v[x]);
+  __builtin_memcpy(&packed, vals, 16);
+  return packed;
+}
+
+// XOR swizzles of the 16-byte chunks of an LDS row (gfx950 LDS: 64 banks of 4 bytes, 256 B per cycle).
+// A rows are 64 B (4 chunks); XOR with (row >> 2) & 3 makes the ds_read_b128 fragment reads (32 consecutive
+// rows, one chunk each) conflict-free. B rows are BN*2 B: the 4 consecutive k rows of one transpose-read group
+// get disjoint 64-byte windows. Both were chosen by measuring SQ_LDS_BANK_CONFLICT for candidate patterns on
+// an MI355X (zero conflict cycles per instruction for both).
+__device__ __forceinline__ int a_swizzle(int row) { return (row >> 2) & 3; }
+template <int B_CHUNKS>
+__device__ __forceinline__ int b_swizzle(int krow) {
+  if constexpr (B_CHUNKS >= 16) {
+    return (2 * (krow & 3)) ^ (8 * (krow & 1));
+  } else {
+    return 2 * (krow & 3);
+  }
 }
 
 template <typename T, int BM, int BN, int WAVES_M, int WAVES_N>
@@ -133,7 +224,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
 #pragma unroll
   for (int j = 0; j < A_PER_WAVE; ++j) {
     const int row = (wave * A_PER_WAVE + j) * 16 + (lane >> 2);  // 16 rows of 64 B per instruction
-    const int chunk = (lane & 3) ^ ((row >> 1) & 3);
+    const int chunk = (lane & 3) ^ a_swizzle(row);
     const int64_t grow = min(m0 + row, M - 1);
     a_src[j] = grow * lda + chunk * 8;
   }
@@ -141,14 +232,16 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
 #pragma unroll
   for (int j = 0; j < B_PER_WAVE; ++j) {
     const int krow = (wave * B_PER_WAVE + j) * B_ROWS_PER_INSTR + lane / B_CHUNKS;
-    const int chunk = (lane % B_CHUNKS) ^ (2 * (krow & 3));
+    const int chunk = (lane % B_CHUNKS) ^ b_swizzle<B_CHUNKS>(krow);
     const int64_t gcol = min(n0 + chunk * 8, N - 8);
     b_src[j] = static_cast<int64_t>(krow) * ldb + gcol;
   }
 
+  // Stages past the end re-load the last stage (into a buffer nobody reads again), so every step issues the
+  // same number of loads and the vmcnt bookkeeping is identical on every path.
   auto issue_stage = [&]<int SI>(int kt) {
     unsigned char* st = stage_mem.template operator()<SI>();
-    const int64_t k0 = static_cast<int64_t>(kt) * kBK;
+    const int64_t k0 = static_cast<int64_t>(min(kt, KT - 1)) * kBK;
 #pragma unroll
     for (int j = 0; j < A_PER_WAVE; ++j)
       global_to_lds16(A + a_src[j] + k0, (FH_LDS void*)(st + (wave * A_PER_WAVE + j) * 1024));
@@ -157,31 +250,27 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
       global_to_lds16(B + b_src[j] + k0 * ldb, (FH_LDS void*)(st + A_BYTES + (wave * B_PER_WAVE + j) * 1024));
   };
 
-  // ---- per-lane LDS read offsets (bytes within a stage) ----
+  // ---- per-lane LDS read offsets (bytes within a stage). Tile i of A adds i*32 rows (the swizzle depends on
+  // row bits 2-3 only, so it is a constant 2048 B); k-half s and 4-k group h of B add whole rows. ----
   const int l32 = lane & 31, hi = lane >> 5;
-  int a_off[TM][2];
+  int a_off[2];
+  {
+    const int row = wm * WM + l32;
 #pragma unroll
-  for (int i = 0; i < TM; ++i) {
-    const int row = wm * WM + i * 32 + l32;
-#pragma unroll
-    for (int s = 0; s < 2; ++s) a_off[i][s] = row * 64 + (((2 * s + hi) ^ ((row >> 1) & 3)) * 16);
+    for (int s = 0; s < 2; ++s) a_off[s] = row * 64 + (((2 * s + hi) ^ a_swizzle(row)) * 16);
   }
   // transpose reads: group g = lane/16 covers 16 columns and 4 k; lane r = q + 4e of the group points at
   // row (kbase + e), columns n + 4q .. n + 4q + 3
   const int g = lane >> 4, r = lane & 15, q = r & 3, e = r >> 2;
-  int b_off[TN][2][2];
+  int b_off[TN];
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
     const int ncol = wn * WN + j * 32 + 16 * (g & 1) + 4 * q;
-#pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int krow = 16 * s + 8 * (g >> 1) + 4 * h + e;
-        const int chunk = (ncol >> 3) ^ (2 * (krow & 3));
-        b_off[j][s][h] = A_BYTES + krow * (BN * 2) + chunk * 16 + (ncol & 7) * 2;
-      }
+    const int krow = 8 * (g >> 1) + e;  // + 16 s + 4 h (immediates): krow & 3 and krow & 1 are unchanged
+    const int chunk = (ncol >> 3) ^ b_swizzle<B_CHUNKS>(krow);
+    b_off[j] = A_BYTES + krow * (BN * 2) + chunk * 16 + (ncol & 7) * 2;
   }
+  constexpr int B_S = 16 * BN * 2, B_H = 4 * BN * 2;
 
   f32x16_t acc[TM][TN];
 #pragma unroll
@@ -194,44 +283,50 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
   // One k step on stage SI (= kt % kStages): wait for this wave's part of the stage, barrier (every wave's
   // part has landed and the stage refilled next was consumed by all), refill it kStages-1 steps ahead, multiply.
   auto step = [&]<int SI>(int kt) {
-    const int later = min(KT - 1 - kt, kStages - 2);
-    if (later >= 2) {
-      wait_vmcnt<2 * LOADS>();
-    } else if (later == 1) {
-      wait_vmcnt<LOADS>();
-    } else {
-      wait_vmcnt<0>();
-    }
+    wait_vmcnt<2 * LOADS>();  // this wave's loads of stage kt are done; stages kt+1, kt+2 may be in flight
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    if (kt + kStages - 1 < KT) issue_stage.template operator()<(SI + kStages - 1) % kStages>(kt + kStages - 1);
-    const FH_LDS unsigned char* st = (const FH_LDS unsigned char*)stage_mem.template operator()<SI>();
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      uint4 af[TM], bfr[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i) af[i] = lds_load128(st + a_off[i][s]);
+    issue_stage.template operator()<(SI + kStages - 1) % kStages>(kt + kStages - 1);
+    const uint32_t base = lds_addr((const FH_LDS void*)stage_mem.template operator()<SI>());
+    u32x4_t af[2][TM], bfr[2][TN];
+    auto read = [&]<int S>() {
+      const uint32_t abase = base + a_off[S];
+      [&]<int... I>(std::integer_sequence<int, I...>) {
+        ((af[S][I] = lds_read_b128<I * 2048>(abase)), ...);
+      }(std::make_integer_sequence<int, TM>{});
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
-        const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FH_LDS s16x4_t*)(st + b_off[j][s][0]));
-        const s16x4_t hi4 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FH_LDS s16x4_t*)(st + b_off[j][s][1]));
-        bfr[j] = make_uint4(static_cast<uint16_t>(lo[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(lo[1])) << 16),
-                            static_cast<uint16_t>(lo[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(lo[3])) << 16),
-                            static_cast<uint16_t>(hi4[0]) | (static_cast<uint32_t>(static_cast<uint16_t>(hi4[1])) << 16),
-                            static_cast<uint16_t>(hi4[2]) | (static_cast<uint32_t>(static_cast<uint16_t>(hi4[3])) << 16));
+        const u32x2_t lo = lds_read_tr16_b64<S * B_S>(base + b_off[j]);
+        const u32x2_t hi2 = lds_read_tr16_b64<S * B_S + B_H>(base + b_off[j]);
+        bfr[S][j] = u32x4_t{lo[0], lo[1], hi2[0], hi2[1]};
       }
+    };
+    // both k16 halves are requested up front; the second half's reads are in flight (and write registers
+    // distinct from the first half's) while the first half is multiplied
+    constexpr int READS = TM + 2 * TN;
+    constexpr bool ACC_IN_AGPR = TM * TN * 16 > 128;
+    read.template operator()<0>();
+    read.template operator()<1>();
+    fragment_fence<READS, TM, TN>(af[0], bfr[0]);
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
+    for (int i = 0; i < TM; ++i)
 #pragma unroll
-        for (int j = 0; j < TN; ++j) mfma32<T>(af[i], bfr[j], acc[i][j]);
-    }
+      for (int j = 0; j < TN; ++j) {
+        mfma32<T>(af[0][i], bfr[0][j], acc[i][j]);
+        pin<ACC_IN_AGPR>(acc[i][j]);  // keeps the first half's MFMAs above the second fence
+      }
+    fragment_fence<0, TM, TN>(af[1], bfr[1]);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) mfma32<T>(af[1][i], bfr[1][j], acc[i][j]);
   };
 
   // ---- prologue: stages 0..kStages-2 in flight ----
-  if (0 < KT) issue_stage.template operator()<0>(0);
-  if (1 < KT) issue_stage.template operator()<1>(1);
-  if (2 < KT) issue_stage.template operator()<2>(2);
+  issue_stage.template operator()<0>(0);
+  issue_stage.template operator()<1>(1);
+  issue_stage.template operator()<2>(2);
 
   for (int kt = 0; kt < KT; kt += kStages) {
     step.template operator()<0>(kt);
@@ -241,12 +336,13 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
   }
 
   // ---- epilogue: round, stage the whole wave tile in LDS, then 16-byte coalesced read-modify-store ----
+  wait_vmcnt<0>();  // the trailing re-loads must land before the ring is reused
   __syncthreads();  // all waves are done with the ring; reuse it
+  // The whole wave tile is staged (rounded) in LDS, then read back row-wise as 16-byte vectors. Each wave's
+  // tile lies inside one stage object.
   constexpr int WTILE_BYTES = WM * WN * 2;
-  static_assert(WTILE_BYTES <= STAGE, "a wave tile fits in one stage");
-  // each wave's tile lies inside one stage object (the objects need not be contiguous)
   constexpr int PER_STAGE = STAGE / WTILE_BYTES;
-  static_assert(NW <= kStages * PER_STAGE, "the wave tiles fit in the ring");
+  static_assert(PER_STAGE >= 1 && NW <= kStages * PER_STAGE, "the wave tiles fit in the ring");
   const int slot = wave / PER_STAGE;
   unsigned char* tile_base = slot == 0 ? st0 : slot == 1 ? st1 : slot == 2 ? st2 : st3;
   S* wl = reinterpret_cast<S*>(tile_base + (wave % PER_STAGE) * WTILE_BYTES);
@@ -259,7 +355,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
         const int rr = i * 32 + 8 * (x >> 2) + 4 * hi + (x & 3);
         wl[rr * WN + j * 32 + l32] = Io<T>::store(acc[i][j][x]);
       }
-  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's LDS writes are done (wave-private region)
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's tile is in LDS (wave-private region)
   __builtin_amdgcn_wave_barrier();
   constexpr int V = 8;           // elements per 16-byte vector
   constexpr int LPR = WN / V;    // lanes per staged row
@@ -270,37 +366,12 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
   for (int it = 0; it < WM / RPI; ++it) {
     const int rr = it * RPI + lane / LPR;
     const int64_t row = m0 + wm * WM + rr;
-    if (row >= M || col >= N) continue;
-    uint4 packed = *reinterpret_cast<const uint4*>(wl + rr * WN + c);
-    const int64_t idx = row * ldc + col;
-    if (args.ep.nseg > 0) {
-      S vals[V];
-      __builtin_memcpy(vals, &packed, 16);
-      float v[V];
-#pragma unroll
-      for (int x = 0; x < V; ++x) v[x] = Io<T>::load(vals[x]);
-      for (int sg = 0; sg < args.ep.nseg; ++sg) {
-        const uint8_t op = args.ep.ops[sg];
-        if (ew_is_binary(op)) {
-          const uint4 in = *reinterpret_cast<const uint4*>(static_cast<const S*>(args.ep.ins[sg]) + idx);
-          S iv[V];
-          __builtin_memcpy(iv, &in, 16);
-#pragma unroll
-          for (int x = 0; x < V; ++x) v[x] = ew_binary(op, v[x], Io<T>::load(iv[x]));
-        } else {
-#pragma unroll
-          for (int x = 0; x < V; ++x) v[x] = ew_unary(op, v[x]);
-        }
-        if (args.ep.round_between) {
-#pragma unroll
-          for (int x = 0; x < V; ++x) v[x] = Io<T>::round(v[x]);
-        }
-      }
-#pragma unroll
-      for (int x = 0; x < V; ++x) vals[x] = Io<T>::store(v[x]);
-      __builtin_memcpy(&packed, vals, 16);
+    if (row < M && col < N) {
+      uint4 packed = *reinterpret_cast<const uint4*>(wl + rr * WN + c);
+      const int64_t idx = row * ldc + col;
+      if (args.ep.nseg > 0) packed = apply_epilogue_vec<T>(args.ep, packed, idx);
+      *reinterpret_cast<uint4*>(C + idx) = packed;
     }
-    *reinterpret_cast<uint4*>(C + idx) = packed;
   }
 }
 
@@ -319,7 +390,7 @@ template <typename T>
 fh_status dispatch(const GemmArgs& args, int64_t batch, hipStream_t stream) {
   const int cus = device_cu_count();
   auto tiles = [&](int64_t bm, int64_t bn) { return ((args.M + bm - 1) / bm) * ((args.N + bn - 1) / bn) * batch; };
-  if (args.M >= 256 && args.N >= 256 && tiles(256, 256) >= cus) return launch<T, 256, 256, 2, 4>(args, batch, stream);
+  if (args.M >= 256 && args.N >= 256 && tiles(256, 256) >= cus) return launch<T, 256, 256, 4, 2>(args, batch, stream);
   if (args.M >= 128 && args.N >= 128 && tiles(128, 128) >= cus / 2) return launch<T, 128, 128, 2, 2>(args, batch, stream);
   if (args.N >= 128 && tiles(64, 128) >= cus / 2) return launch<T, 64, 128, 1, 2>(args, batch, stream);
   return launch<T, 64, 64, 2, 2>(args, batch, stream);
