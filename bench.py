@@ -13,6 +13,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -69,6 +70,34 @@ def run_gpu(steps: int, warmup: int):
     return ms, wall
 
 
+TRAFFIC_SUMMARY = os.path.join(REPO, "profiles", "gemm16_bf16_4096_hbm_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the GEMM kernel, from the committed FETCH_SIZE / WRITE_SIZE counter passes
+    (scaled by the same counters on a plain copy of known size); None where no such summary exists."""
+    try:
+        with open(TRAFFIC_SUMMARY) as f:
+            m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", f.read(), re.M)
+    except OSError:
+        return None
+    return int(m.group(1)) if m else None
+
+
+def copy_calibration(mib: int, reps: int):
+    """Launches copy2d_kernel (fh_copy2d, one 16-byte load and store per lane) over `mib` MiB, `reps` times:
+    the known-size copy that scales the FETCH_SIZE / WRITE_SIZE counters of the traffic passes."""
+    from frame_hip import abi
+
+    nbytes = mib << 20
+    src, dst = abi.DeviceBuffer(nbytes), abi.DeviceBuffer(nbytes)
+    abi.check(abi.lib().fh_fill(src.ptr, 4, 0x3F800000, nbytes // 4, None), "fh_fill")
+    for _ in range(reps):
+        abi.check(abi.lib().fh_copy2d(dst.ptr, nbytes, src.ptr, nbytes, nbytes, 1, None), "fh_copy2d")
+    abi.check(abi.lib().fh_device_synchronize(), "fh_device_synchronize")
+    print(json.dumps({"copy_calibration_bytes": nbytes, "launches": reps}), flush=True)
+
+
 def cpu_baseline(rows: int):
     """Reference CPU backend (single thread) on rows x 4096 x 4096 of the same GEMM."""
     import oracle_lib as orc
@@ -102,10 +131,15 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-rows", type=int, default=128)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="only run the known-size copy used to scale HBM traffic counters")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one MI355X only (no multi-GPU path); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.copy_calibration_mib > 0:
+        copy_calibration(args.copy_calibration_mib, args.steps)
+        return
 
     ms, wall = run_gpu(args.steps, args.warmup)
     tflops = gemm_flops(N, N, N) / (ms * 1e-3) / 1e12
@@ -125,7 +159,7 @@ def main():
         "config": {"workload": "dense GEMM C=A·B, M=N=K=4096, bf16 in/out, fp32 accumulate (configs[1])",
                    "M": N, "N": N, "K": N},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": None},
+                     "frac": round(tflops / PEAK_BF16_TFLOPS, 4), "traffic": measured_traffic()},
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_rows)
