@@ -29,7 +29,6 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
 template <typename T>
 struct GemmTraits;
@@ -219,6 +218,7 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(GemmArgs args) {
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+  acc_to_agpr(acc);
 
   const int KT = static_cast<int>((K + BK - 1) / BK);
   const int half = lane >> 5;
@@ -255,6 +255,7 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(GemmArgs args) {
     if (kt + 1 < KT) store_slice(cur ^ 1);
     __syncthreads();
   }
+  drain_accumulators(acc);
 
   // --- epilogue: stage the rounded tile through LDS (free after the last barrier), then each wave runs the
   // elementwise program on 16-byte vectors and stores them coalesced. Rounding the product to T before

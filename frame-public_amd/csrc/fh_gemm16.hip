@@ -6,14 +6,16 @@
 //  * Operands go global -> LDS with global_load_lds_dwordx4 (no VGPR staging): every wave instruction writes
 //    1 KB of LDS contiguously, lane L at +16*L. The lane -> global address map applies an XOR swizzle of the
 //    16-byte chunks inside each LDS row, so the fragment reads below are bank-conflict free.
-//  * A tile: [BM rows][32 k] bf16 = 64 B per row, chunk swizzle c ^ ((row >> 1) & 3). A fragments are
-//    ds_read_b128 (8 consecutive k of one row per lane), the MFMA's A layout.
-//  * B tile: [32 k rows][BN n] bf16 kept n-contiguous as in memory, chunk swizzle c ^ (2 * (k & 3)).
-//    B fragments need 8 consecutive k of one column per lane; ds_read_b64_tr_b16 (gfx950 LDS transpose read)
-//    delivers them in two reads of 4 k each, with no register transposes.
-//  * A ring of 4 LDS stages of BK = 32: loads for stage kt+3 are issued while stage kt is multiplied, so about
-//    three stages of MFMA work cover the global-load latency. Waits use explicit vmcnt counts and a bare
-//    s_barrier, so prefetched stages are never waited for early.
+//  * A tile: [BM rows][32 k] bf16 = 64 B per row. A fragments are ds_read_b128 (8 consecutive k of one row
+//    per lane), the MFMA's A layout.
+//  * B tile: [32 k rows][BN n] bf16 kept n-contiguous as in memory. B fragments need 8 consecutive k of one
+//    column per lane; ds_read_b64_tr_b16 (gfx950 LDS transpose read) delivers them in two reads of 4 k each,
+//    with no register transposes.
+//  * A ring of 4 LDS stages of BK = 32, refilled three stages ahead.
+//  * Software pipeline: each stage is multiplied as two k16 halves, and the fragments of the next half are
+//    read from LDS while the current half's MFMAs run. The reads (and, after the barrier, the global->LDS
+//    loads of the stage three ahead) are placed between the MFMAs in fixed program order (sched_barrier), so
+//    the matrix pipe is fed while LDS and global traffic are in flight. One s_barrier per stage.
 //  * Workgroups are remapped XCD-aware (consecutive tile ids on one XCD) and grouped along M for L2 reuse.
 //  * Epilogue: the rounded tile is staged through LDS per wave and written with 16-byte stores; epilogue
 //    operands are read with matching 16-byte loads.
@@ -31,17 +33,16 @@ namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
-typedef short s16x4_t __attribute__((ext_vector_type(4)));
-typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 
 #define FH_LDS __attribute__((address_space(3)))
 
 constexpr int kBK = 32;      // k per stage
 constexpr int kStages = 4;   // LDS ring depth
 
-template <typename T, typename V>
-__device__ __forceinline__ void mfma32(const V& a, const V& b, f32x16_t& acc) {
-  static_assert(sizeof(V) == 16, "8 x 16-bit fragments");
+template <typename T>
+__device__ __forceinline__ void mfma32(const u32x4_t& a, const u32x4_t& b, f32x16_t& acc) {
   if constexpr (std::is_same_v<T, bf16_t>) {
     acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
                                                   acc, 0, 0, 0);
@@ -58,13 +59,10 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
-
-// Fragment reads are written as inline asm without a memory clobber. The compiler's LDS-DMA wait tracking does
-// not follow the stage ring across the loop (it either waits for every in-flight prefetch or, on other paths,
-// for nothing), so the main loop orders LDS itself: explicit vmcnt waits + s_barrier before a stage is read,
-// and fragment_fence() (lgkmcnt(0), tied to the fragment registers) before the MFMAs consume them.
+// Fragment reads are inline asm without a memory clobber: the compiler's LDS-DMA wait tracking does not follow
+// the stage ring across the loop (it either waits for every in-flight prefetch or, on other paths, for
+// nothing), so the kernel orders LDS itself: explicit vmcnt waits + s_barrier before a stage is read, and
+// fence_fragments() (lgkmcnt(0), tied to the fragment registers) before the MFMAs consume them.
 template <int OFF>
 __device__ __forceinline__ u32x4_t lds_read_b128(uint32_t addr) {
   static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
@@ -81,34 +79,33 @@ __device__ __forceinline__ u32x2_t lds_read_tr16_b64(uint32_t addr) {
   return v;
 }
 
-// Keeps an accumulator's MFMA above later fences: VGPR or AGPR constraint, wherever the accumulators live.
-template <bool IN_AGPR>
-__device__ __forceinline__ void pin(f32x16_t& acc) {
-  if constexpr (IN_AGPR) {
-    asm volatile("" : "+a"(acc));
-  } else {
-    asm volatile("" : "+v"(acc));
-  }
-}
-
-// Waits until at most PENDING LDS reads are outstanding (they complete in order), then ties the fragment
-// registers to the wait so no consumer is scheduled above it.
-template <int PENDING, int TM, int TN>
-__device__ __forceinline__ void fragment_fence(u32x4_t (&a)[TM], u32x4_t (&b)[TN]) {
-  static_assert(PENDING >= 0 && PENDING <= 15, "lgkmcnt range");
-  asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(PENDING) : "memory");
-#pragma unroll
-  for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(a[i]));
-#pragma unroll
-  for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(b[j]));
-}
-
 __device__ __forceinline__ uint32_t lds_addr(const FH_LDS void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(p));
 }
 
 __device__ __forceinline__ void global_to_lds16(const void* g, FH_LDS void* lds_wave_base) {
   __builtin_amdgcn_global_load_lds(g, lds_wave_base, 16, 0, 0);
+}
+
+// The fragments of one k16 half of a wave tile.
+template <int TM, int TN>
+struct Fragments {
+  u32x4_t a[TM];
+  u32x2_t bl[TN], bh[TN];  // B fragment = 4 k from the low transpose read, 4 k from the high one
+};
+
+// Waits for every outstanding LDS read (they complete in order), then ties the fragment registers to the wait
+// so no consumer is scheduled above it. The B halves are combined into MFMA operands only after this point.
+template <int TM, int TN>
+__device__ __forceinline__ void fence_fragments(Fragments<TM, TN>& f) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(f.a[i]));
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    asm volatile("" : "+v"(f.bl[j]));
+    asm volatile("" : "+v"(f.bh[j]));
+  }
 }
 
 // Runs the epilogue program on 8 rounded outputs (one 16-byte vector) at flat output index idx.
@@ -158,44 +155,46 @@ __device__ __forceinline__ int b_swizzle(int krow) {
   }
 }
 
+// Number of items issued right after MFMA m when n items are spread over the first r MFMAs of a half, and the
+// index of the first of them.
+constexpr int share(int m, int n, int r) { return m < r ? (m + 1) * n / r - m * n / r : 0; }
+constexpr int first(int m, int n, int r) { return (m < r ? m : r) * n / r; }
+
+// One workgroup = WAVES_M x WAVES_N waves computing a BM x BN tile; each wave owns (BM/WAVES_M) x (BN/WAVES_N)
+// as TM x TN MFMA tiles of 32 x 32.
+//
+// Per stage kt (ring slot kt % 4), with f0 / f1 the fragment buffers of the two k16 halves:
+//   fence(f0); MFMA(kt, half 0) || read(kt, half 1) -> f1;
+//   wait vmcnt (this wave's loads of stage kt+1); s_barrier;
+//   fence(f1); MFMA(kt, half 1) || read(kt+1, half 0) -> f0 || load stage kt+3 into the slot of stage kt-1.
+// Ordering: stage kt+1 is read only after the barrier that follows every wave's vmcnt wait for it. The slot
+// refilled after the barrier of step kt held stage kt-1, whose reads every wave fenced (lgkmcnt(0)) before
+// arriving at that barrier. Stages past the end re-load the last stage (nobody reads them), so every step
+// issues the same number of loads and the vmcnt counts hold on every path.
 template <typename T, int BM, int BN, int WAVES_M, int WAVES_N>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs args) {
   using S = uint16_t;
-  constexpr int NT = WAVES_M * WAVES_N * 64;
   constexpr int NW = WAVES_M * WAVES_N;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int A_BYTES = BM * kBK * 2;        // one stage of A
-  constexpr int B_BYTES = BN * kBK * 2;        // one stage of B
+  constexpr int A_BYTES = BM * kBK * 2;
+  constexpr int B_BYTES = BN * kBK * 2;
   constexpr int STAGE = A_BYTES + B_BYTES;
-  constexpr int A_INSTR = A_BYTES / 1024;      // wave instructions per stage
-  constexpr int B_INSTR = B_BYTES / 1024;
-  constexpr int A_PER_WAVE = A_INSTR / NW;
-  constexpr int B_PER_WAVE = B_INSTR / NW;
-  constexpr int LOADS = A_PER_WAVE + B_PER_WAVE;  // vmcnt units per stage per wave
-  constexpr int B_CHUNKS = BN / 8;               // 16-byte chunks per B row
+  constexpr int A_PER_WAVE = A_BYTES / 1024 / NW;  // global->LDS instructions per wave and stage
+  constexpr int B_PER_WAVE = B_BYTES / 1024 / NW;
+  constexpr int LOADS = A_PER_WAVE + B_PER_WAVE;
+  constexpr int B_CHUNKS = BN / 8;  // 16-byte chunks per B row
   constexpr int B_ROWS_PER_INSTR = 64 / B_CHUNKS;
-  static_assert(A_INSTR % NW == 0 && B_INSTR % NW == 0, "stage loads must split evenly over the waves");
+  static_assert((A_BYTES / 1024) % NW == 0 && (B_BYTES / 1024) % NW == 0, "stage loads split evenly over waves");
   static_assert(B_CHUNKS >= 8 && B_CHUNKS <= 64, "BN in [64, 512]");
   static_assert(TM >= 1 && TN >= 1, "wave tile at least 32x32");
+  static_assert(2 * LOADS <= 63, "vmcnt range");
 
-  // One LDS object per stage: the compiler's LDS-DMA wait tracking then distinguishes the stages and waits
-  // only for the stage being read, not for the prefetches still in flight.
-  __shared__ __attribute__((aligned(1024))) unsigned char st0[STAGE];
-  __shared__ __attribute__((aligned(1024))) unsigned char st1[STAGE];
-  __shared__ __attribute__((aligned(1024))) unsigned char st2[STAGE];
-  __shared__ __attribute__((aligned(1024))) unsigned char st3[STAGE];
-  static_assert(kStages == 4, "one LDS object per stage");
-  auto stage_mem = [&]<int SI>() -> unsigned char* {
-    if constexpr (SI == 0) return st0;
-    else if constexpr (SI == 1) return st1;
-    else if constexpr (SI == 2) return st2;
-    else return st3;
-  };
+  __shared__ __attribute__((aligned(1024))) unsigned char ring[kStages * STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: LDS destinations become scalar math
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
 
   // ---- tile id: XCD-aware remap, then GROUP_M-row groups ----
@@ -225,29 +224,31 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
   for (int j = 0; j < A_PER_WAVE; ++j) {
     const int row = (wave * A_PER_WAVE + j) * 16 + (lane >> 2);  // 16 rows of 64 B per instruction
     const int chunk = (lane & 3) ^ a_swizzle(row);
-    const int64_t grow = min(m0 + row, M - 1);
-    a_src[j] = grow * lda + chunk * 8;
+    a_src[j] = min(m0 + row, M - 1) * lda + chunk * 8;
   }
   int64_t b_src[B_PER_WAVE];
 #pragma unroll
   for (int j = 0; j < B_PER_WAVE; ++j) {
     const int krow = (wave * B_PER_WAVE + j) * B_ROWS_PER_INSTR + lane / B_CHUNKS;
     const int chunk = (lane % B_CHUNKS) ^ b_swizzle<B_CHUNKS>(krow);
-    const int64_t gcol = min(n0 + chunk * 8, N - 8);
-    b_src[j] = static_cast<int64_t>(krow) * ldb + gcol;
+    b_src[j] = static_cast<int64_t>(krow) * ldb + min(n0 + chunk * 8, N - 8);
   }
 
-  // Stages past the end re-load the last stage (into a buffer nobody reads again), so every step issues the
-  // same number of loads and the vmcnt bookkeeping is identical on every path.
-  auto issue_stage = [&]<int SI>(int kt) {
-    unsigned char* st = stage_mem.template operator()<SI>();
+  // Load instruction J (< LOADS) of this wave's share of stage kt, into ring slot kt % kStages.
+  auto load_one = [&]<int J>(int kt) {
+    unsigned char* st = ring + (kt & (kStages - 1)) * STAGE;
     const int64_t k0 = static_cast<int64_t>(min(kt, KT - 1)) * kBK;
-#pragma unroll
-    for (int j = 0; j < A_PER_WAVE; ++j)
-      global_to_lds16(A + a_src[j] + k0, (FH_LDS void*)(st + (wave * A_PER_WAVE + j) * 1024));
-#pragma unroll
-    for (int j = 0; j < B_PER_WAVE; ++j)
-      global_to_lds16(B + b_src[j] + k0 * ldb, (FH_LDS void*)(st + A_BYTES + (wave * B_PER_WAVE + j) * 1024));
+    if constexpr (J < A_PER_WAVE) {
+      global_to_lds16(A + a_src[J] + k0, (FH_LDS void*)(st + (wave * A_PER_WAVE + J) * 1024));
+    } else {
+      constexpr int JB = J - A_PER_WAVE;
+      global_to_lds16(B + b_src[JB] + k0 * ldb, (FH_LDS void*)(st + A_BYTES + (wave * B_PER_WAVE + JB) * 1024));
+    }
+  };
+  auto issue_stage = [&](int kt) {
+    [&]<int... J>(std::integer_sequence<int, J...>) {
+      (load_one.template operator()<J>(kt), ...);
+    }(std::make_integer_sequence<int, LOADS>{});
   };
 
   // ---- per-lane LDS read offsets (bytes within a stage). Tile i of A adds i*32 rows (the swizzle depends on
@@ -271,6 +272,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
     b_off[j] = A_BYTES + krow * (BN * 2) + chunk * 16 + (ncol & 7) * 2;
   }
   constexpr int B_S = 16 * BN * 2, B_H = 4 * BN * 2;
+  const uint32_t ring_addr = lds_addr((const FH_LDS void*)ring);
 
   f32x16_t acc[TM][TN];
 #pragma unroll
@@ -279,73 +281,82 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int x = 0; x < 16; ++x) acc[i][j][x] = 0.0f;
+  acc_to_agpr(acc);
 
-  // One k step on stage SI (= kt % kStages): wait for this wave's part of the stage, barrier (every wave's
-  // part has landed and the stage refilled next was consumed by all), refill it kStages-1 steps ahead, multiply.
-  auto step = [&]<int SI>(int kt) {
-    wait_vmcnt<2 * LOADS>();  // this wave's loads of stage kt are done; stages kt+1, kt+2 may be in flight
+  Fragments<TM, TN> f0, f1;
+  constexpr int NREAD = TM + 2 * TN;  // LDS reads per half
+  constexpr int NMFMA = TM * TN;      // MFMAs per half
+
+  // Read number R of half H of the stage at `base` into f.
+  auto read_one = [&]<int H, int R>(uint32_t base, Fragments<TM, TN>& f) {
+    if constexpr (R < TM) {
+      f.a[R] = lds_read_b128<R * 2048>(base + a_off[H]);
+    } else if constexpr ((R - TM) % 2 == 0) {
+      f.bl[(R - TM) / 2] = lds_read_tr16_b64<H * B_S>(base + b_off[(R - TM) / 2]);
+    } else {
+      f.bh[(R - TM) / 2] = lds_read_tr16_b64<H * B_S + B_H>(base + b_off[(R - TM) / 2]);
+    }
+  };
+  // The MFMAs of the half held in `cur`. After each come some of the reads of half H of the stage at `base`
+  // into `nxt` (all within the first three quarters of the MFMAs, so they land before the half ends) and, with
+  // LOADS_TOO, some of the global->LDS loads of stage load_kt (within the first half of the MFMAs).
+  constexpr int R_SPAN = NMFMA * 3 / 4 > 0 ? NMFMA * 3 / 4 : 1;
+  constexpr int L_SPAN = NMFMA / 2 > 0 ? NMFMA / 2 : 1;
+  auto multiply_and_read = [&]<int H, bool LOADS_TOO>(Fragments<TM, TN>& cur, uint32_t base, Fragments<TM, TN>& nxt,
+                                                      int load_kt) {
+    [&]<int... M_>(std::integer_sequence<int, M_...>) {
+      (
+          [&] {
+            constexpr int i = M_ / TN, j = M_ % TN;
+            mfma32<T>(cur.a[i], u32x4_t{cur.bl[j][0], cur.bl[j][1], cur.bh[j][0], cur.bh[j][1]}, acc[i][j]);
+            constexpr int r0 = first(M_, NREAD, R_SPAN);
+            [&]<int... R_>(std::integer_sequence<int, R_...>) {
+              (read_one.template operator()<H, r0 + R_>(base, nxt), ...);
+            }(std::make_integer_sequence<int, share(M_, NREAD, R_SPAN)>{});
+            if constexpr (LOADS_TOO) {
+              constexpr int l0 = first(M_, LOADS, L_SPAN);
+              [&]<int... L_>(std::integer_sequence<int, L_...>) {
+                (load_one.template operator()<l0 + L_>(load_kt), ...);
+              }(std::make_integer_sequence<int, share(M_, LOADS, L_SPAN)>{});
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }(),
+          ...);
+    }(std::make_integer_sequence<int, NMFMA>{});
+  };
+
+  // ---- prologue: stages 0..2 in flight, half 0 of stage 0 in f0 ----
+  issue_stage(0);
+  issue_stage(1);
+  issue_stage(2);
+  wait_vmcnt<2 * LOADS>();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  [&]<int... R_>(std::integer_sequence<int, R_...>) {
+    (read_one.template operator()<0, R_>(ring_addr, f0), ...);
+  }(std::make_integer_sequence<int, NREAD>{});
+
+  for (int kt = 0; kt < KT; ++kt) {
+    const uint32_t cur = ring_addr + (kt & (kStages - 1)) * STAGE;
+    const uint32_t nxt = ring_addr + ((kt + 1) & (kStages - 1)) * STAGE;
+    fence_fragments(f0);
+    multiply_and_read.template operator()<1, false>(f0, cur, f1, 0);
+    wait_vmcnt<LOADS>();  // this wave's part of stage kt+1 has landed (stage kt+2 may be in flight)
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
-    issue_stage.template operator()<(SI + kStages - 1) % kStages>(kt + kStages - 1);
-    const uint32_t base = lds_addr((const FH_LDS void*)stage_mem.template operator()<SI>());
-    u32x4_t af[2][TM], bfr[2][TN];
-    auto read = [&]<int S>() {
-      const uint32_t abase = base + a_off[S];
-      [&]<int... I>(std::integer_sequence<int, I...>) {
-        ((af[S][I] = lds_read_b128<I * 2048>(abase)), ...);
-      }(std::make_integer_sequence<int, TM>{});
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const u32x2_t lo = lds_read_tr16_b64<S * B_S>(base + b_off[j]);
-        const u32x2_t hi2 = lds_read_tr16_b64<S * B_S + B_H>(base + b_off[j]);
-        bfr[S][j] = u32x4_t{lo[0], lo[1], hi2[0], hi2[1]};
-      }
-    };
-    // both k16 halves are requested up front; the second half's reads are in flight (and write registers
-    // distinct from the first half's) while the first half is multiplied
-    constexpr int READS = TM + 2 * TN;
-    constexpr bool ACC_IN_AGPR = TM * TN * 16 > 128;
-    read.template operator()<0>();
-    read.template operator()<1>();
-    fragment_fence<READS, TM, TN>(af[0], bfr[0]);
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        mfma32<T>(af[0][i], bfr[0][j], acc[i][j]);
-        pin<ACC_IN_AGPR>(acc[i][j]);  // keeps the first half's MFMAs above the second fence
-      }
-    fragment_fence<0, TM, TN>(af[1], bfr[1]);
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j) mfma32<T>(af[1][i], bfr[1][j], acc[i][j]);
-  };
-
-  // ---- prologue: stages 0..kStages-2 in flight ----
-  issue_stage.template operator()<0>(0);
-  issue_stage.template operator()<1>(1);
-  issue_stage.template operator()<2>(2);
-
-  for (int kt = 0; kt < KT; kt += kStages) {
-    step.template operator()<0>(kt);
-    if (kt + 1 < KT) step.template operator()<1>(kt + 1);
-    if (kt + 2 < KT) step.template operator()<2>(kt + 2);
-    if (kt + 3 < KT) step.template operator()<3>(kt + 3);
+    fence_fragments(f1);
+    multiply_and_read.template operator()<0, true>(f1, nxt, f0, kt + kStages - 1);
   }
+  drain_accumulators(acc);
 
-  // ---- epilogue: round, stage the whole wave tile in LDS, then 16-byte coalesced read-modify-store ----
+  // ---- epilogue: round, stage each wave tile in LDS, then 16-byte coalesced read-modify-store ----
   wait_vmcnt<0>();  // the trailing re-loads must land before the ring is reused
-  __syncthreads();  // all waves are done with the ring; reuse it
-  // The whole wave tile is staged (rounded) in LDS, then read back row-wise as 16-byte vectors. Each wave's
-  // tile lies inside one stage object.
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __syncthreads();
   constexpr int WTILE_BYTES = WM * WN * 2;
-  constexpr int PER_STAGE = STAGE / WTILE_BYTES;
-  static_assert(PER_STAGE >= 1 && NW <= kStages * PER_STAGE, "the wave tiles fit in the ring");
-  const int slot = wave / PER_STAGE;
-  unsigned char* tile_base = slot == 0 ? st0 : slot == 1 ? st1 : slot == 2 ? st2 : st3;
-  S* wl = reinterpret_cast<S*>(tile_base + (wave % PER_STAGE) * WTILE_BYTES);
+  static_assert(NW * WTILE_BYTES <= kStages * STAGE, "the wave tiles fit in the ring");
+  S* wl = reinterpret_cast<S*>(ring + wave * WTILE_BYTES);
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -386,13 +397,15 @@ fh_status launch(GemmArgs args, int64_t batch, hipStream_t stream) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// Largest tile that still gives every CU a workgroup (measured on MI355X, bf16 U(-1,1), M=N=K:
+// 4096: 256x256/8 waves 1164 TFLOP/s; 2048: 128x128/8 waves 711-724; 1024: 64x64/4 waves 282).
 template <typename T>
 fh_status dispatch(const GemmArgs& args, int64_t batch, hipStream_t stream) {
   const int cus = device_cu_count();
   auto tiles = [&](int64_t bm, int64_t bn) { return ((args.M + bm - 1) / bm) * ((args.N + bn - 1) / bn) * batch; };
   if (args.M >= 256 && args.N >= 256 && tiles(256, 256) >= cus) return launch<T, 256, 256, 4, 2>(args, batch, stream);
-  if (args.M >= 128 && args.N >= 128 && tiles(128, 128) >= cus / 2) return launch<T, 128, 128, 2, 2>(args, batch, stream);
-  if (args.N >= 128 && tiles(64, 128) >= cus / 2) return launch<T, 64, 128, 1, 2>(args, batch, stream);
+  if (args.M >= 128 && args.N >= 128 && tiles(128, 128) >= cus) return launch<T, 128, 128, 2, 4>(args, batch, stream);
+  if (args.N >= 128 && tiles(64, 128) >= cus) return launch<T, 64, 128, 2, 2>(args, batch, stream);
   return launch<T, 64, 64, 2, 2>(args, batch, stream);
 }
 
