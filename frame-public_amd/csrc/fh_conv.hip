@@ -2,14 +2,14 @@
 //
 // conv2d_direct_kernel: one thread per output element, products summed over (ci, kh, kw) in the reference's
 // order, bias added last inside the fp32 accumulator, one rounding. It serves every geometry (groups,
-// strides, padding, odd channel counts). Faster implicit-GEMM paths for ungrouped convolutions live in
-// fh_conv_igemm.hip and are selected by fh_conv2d_fwd when the shape allows.
+// strides, padding, odd channel counts, fp32) on NCHW operands. The MFMA implicit-GEMM path over
+// channels-last operands is fh_conv2d_nhwc_fwd (fh_conv_igemm.hip), selected at graph compile time.
 #include <hip/hip_runtime.h>
 
 #include <string>
 
 #include "fh_common.h"
-#include "fh_conv_igemm.h"
+#include "fh_conv_direct.h"
 
 namespace fh {
 namespace {
@@ -67,7 +67,6 @@ fh_status launch_direct(const void* x, const void* w, const void* bias, void* y,
 template <typename T>
 fh_status conv_typed(const void* x, const void* w, const void* bias, void* y, const ConvGeom& g,
                      const ConvEpilogue& ep, hipStream_t s) {
-  if (conv_igemm_supported<T>(g, x, w, y, ep)) return conv_igemm_launch<T>(x, w, bias, y, g, ep, s);
   return launch_direct<T>(x, w, bias, y, g, ep, s);
 }
 

@@ -1,4 +1,4 @@
-// Shared conv2d definitions: geometry, the elementwise epilogue, and the implicit-GEMM entry points.
+// Conv2d definitions of the direct (NCHW) path: geometry and the per-element elementwise epilogue.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -33,13 +33,5 @@ __device__ __forceinline__ float conv_epilogue(const ConvEpilogue& ep, float v, 
   }
   return v;
 }
-
-// Implicit-GEMM conv (MFMA). Returns whether the shape and pointers are accepted by the fast path.
-template <typename T>
-bool conv_igemm_supported(const ConvGeom& g, const void* x, const void* w, const void* y, const ConvEpilogue& ep);
-
-template <typename T>
-fh_status conv_igemm_launch(const void* x, const void* w, const void* bias, void* y, const ConvGeom& g,
-                            const ConvEpilogue& ep, hipStream_t stream);
 
 }  // namespace fh

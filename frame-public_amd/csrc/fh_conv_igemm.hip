@@ -1,30 +1,470 @@
-// Implicit-GEMM conv2d on MFMA (placeholder selection: not yet enabled for any shape).
-#include "fh_conv_igemm.h"
+// Conv2d as an implicit GEMM on MFMA, over channels-last operands (reference semantics:
+// src/backends/cpu/kernels/conv.cpp:223-314 — out = round(sum_{ci,kh,kw} x*w + bias[co]) in fp32, then the
+// fused elementwise chain).
+//
+// The graph keeps Frame's NCHW layout. HipBackend::compile lowers an eligible conv2d to
+//   x_nhwc = transpose_batched(x: batch N,    [Cin][H*W]   -> [H*W][Cin])
+//   w_khwc = transpose_batched(w: batch Cout, [Cin][KH*KW] -> [KH*KW][Cin])
+//   y      = conv2d_nhwc(x_nhwc, w_khwc, bias)   (y written NCHW)
+// so the transposed tensors are ordinary arena intermediates of the memory plan.
+//
+// GEMM view: M = Cout, N = P = batch*Ho*Wo output pixels, K = KH*KW*Cin ordered (kh, kw, ci). With
+// Cin % 32 == 0 every BK = 32 stage is one filter position (kh, kw) and 32 consecutive channels, so both
+// operands are k-contiguous 64-byte rows:
+//  * A rows = w_khwc[co] (row-major [Cout][K]), loaded with global_load_lds_dwordx4 like the GEMM's A;
+//  * B rows = one output pixel's receptive-field slice x_nhwc[img, oh*sh-ph+kh, ow*sw-pw+kw, ci0..ci0+31],
+//    loaded with buffer_load_dwordx4 ... lds. Positions in the zero padding get an offset past the buffer's
+//    size, and the buffer bounds check returns zeros, so padding costs nothing.
+// Both operands use the A-operand LDS layout ([rows][32 k], 16-byte chunks XOR-swizzled) and ds_read_b128
+// fragments. The main loop is the same software pipeline as the bf16 GEMM (fh_gemm16.hip): a 4-stage ring
+// refilled three stages ahead, fragment reads of the next k16 half interleaved with the current half's MFMAs,
+// one barrier per stage. The filter position (kh, kw, ci0) of the next stage to load advances with scalar
+// counters, not divisions.
+//
+// Epilogue: bias is added to the fp32 accumulator, the sum is rounded once, the chain runs on the rounded
+// value (rounding after every segment), and the tile is written NCHW — 16-byte stores along the pixel axis
+// when Ho*Wo % 8 == 0, element stores otherwise.
+#include <hip/hip_runtime.h>
+
+#include <string>
+#include <utility>
+
+#include "fh_common.h"
+#include "fh_gemm.h"
+#include "fh_mfma16.h"
 
 namespace fh {
+namespace {
 
-template <typename T>
-bool conv_igemm_supported(const ConvGeom&, const void*, const void*, const void*, const ConvEpilogue&) {
-  return false;
+using namespace mfma16;
+
+struct ConvNhwcArgs {
+  const void* x;     // [N][H][W][Cin]
+  const void* w;     // [Cout][KH][KW][Cin]
+  const void* bias;  // [Cout] or nullptr
+  void* y;           // [N][Cout][Ho][Wo]
+  int32_t cin, h, w_in, cout, kw, sh, sw, ph, pw, wo, howo;
+  int32_t k;         // KH*KW*Cin
+  int64_t p;         // N*Ho*Wo
+  uint32_t x_bytes;
+  int32_t tiles_m, tiles_n;
+  int32_t vec_store;  // Ho*Wo % 8 == 0 and 16-byte aligned output / epilogue operands
+  EpilogueArgs ep;
+};
+
+template <int TM, int TN>
+struct KFragments {
+  u32x4_t a[TM];
+  u32x4_t b[TN];
+};
+
+template <int TM, int TN>
+__device__ __forceinline__ void fence_kfragments(KFragments<TM, TN>& f) {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(f.a[i]));
+#pragma unroll
+  for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(f.b[j]));
 }
 
 template <typename T>
-fh_status conv_igemm_launch(const void*, const void*, const void*, void*, const ConvGeom&, const ConvEpilogue&,
-                            hipStream_t) {
-  return fail(FH_UNIMPLEMENTED, "conv implicit GEMM not available for this shape");
+__device__ __forceinline__ float apply_epilogue_one(const EpilogueArgs& ep, float v, int64_t idx) {
+  using S = uint16_t;
+  for (int s = 0; s < ep.nseg; ++s) {
+    const uint8_t op = ep.ops[s];
+    if (ew_is_binary(op)) {
+      v = ew_binary(op, v, Io<T>::load(static_cast<const S*>(ep.ins[s])[idx]));
+    } else {
+      v = ew_unary(op, v);
+    }
+    if (ep.round_between) v = Io<T>::round(v);
+  }
+  return v;
 }
 
-template bool conv_igemm_supported<float>(const ConvGeom&, const void*, const void*, const void*,
-                                          const ConvEpilogue&);
-template bool conv_igemm_supported<bf16_t>(const ConvGeom&, const void*, const void*, const void*,
-                                           const ConvEpilogue&);
-template bool conv_igemm_supported<f16_t>(const ConvGeom&, const void*, const void*, const void*,
-                                          const ConvEpilogue&);
-template fh_status conv_igemm_launch<float>(const void*, const void*, const void*, void*, const ConvGeom&,
-                                            const ConvEpilogue&, hipStream_t);
-template fh_status conv_igemm_launch<bf16_t>(const void*, const void*, const void*, void*, const ConvGeom&,
-                                             const ConvEpilogue&, hipStream_t);
-template fh_status conv_igemm_launch<f16_t>(const void*, const void*, const void*, void*, const ConvGeom&,
-                                            const ConvEpilogue&, hipStream_t);
+template <typename T, int BM, int BN, int WAVES_M, int WAVES_N>
+__global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNhwcArgs args) {
+  using S = uint16_t;
+  constexpr int NW = WAVES_M * WAVES_N;
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int A_BYTES = BM * kBK * 2;
+  constexpr int B_BYTES = BN * kBK * 2;
+  constexpr int STAGE = A_BYTES + B_BYTES;
+  constexpr int A_PER_WAVE = A_BYTES / 1024 / NW;
+  constexpr int B_PER_WAVE = B_BYTES / 1024 / NW;
+  constexpr int LOADS = A_PER_WAVE + B_PER_WAVE;
+  static_assert((A_BYTES / 1024) % NW == 0 && A_PER_WAVE >= 1, "A stage loads split evenly over waves");
+  static_assert((B_BYTES / 1024) % NW == 0 && B_PER_WAVE >= 1, "B stage loads split evenly over waves");
+  static_assert(TM >= 1 && TN >= 1, "wave tile at least 32x32");
+  static_assert(2 * LOADS <= 63, "vmcnt range");
 
+  __shared__ __attribute__((aligned(1024))) unsigned char ring[kStages * STAGE];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+
+  const int tiles = args.tiles_m * args.tiles_n;
+  int bid = blockIdx.x;
+  if ((tiles & 7) == 0) bid = (bid & 7) * (tiles >> 3) + (bid >> 3);
+  constexpr int GROUP_M = 8;
+  const int group = bid / (GROUP_M * args.tiles_n);
+  const int first_m = group * GROUP_M;
+  const int gsize = min(args.tiles_m - first_m, GROUP_M);
+  const int tm = first_m + (bid % gsize);
+  const int tn = (bid % (GROUP_M * args.tiles_n)) / gsize;
+  const int m0 = tm * BM;                              // first output channel of the tile
+  const int64_t n0 = static_cast<int64_t>(tn) * BN;   // first output pixel of the tile
+
+  const S* __restrict__ W = static_cast<const S*>(args.w);
+  const int cin = args.cin, K = args.k;
+  const int KT = K / kBK;
+
+  // ---- A (filter) sources: row co, clamped to the last channel ----
+  int64_t a_src[A_PER_WAVE];
+#pragma unroll
+  for (int j = 0; j < A_PER_WAVE; ++j) {
+    const int row = (wave * A_PER_WAVE + j) * 16 + (lane >> 2);
+    const int chunk = (lane & 3) ^ a_swizzle(row);
+    a_src[j] = static_cast<int64_t>(min(m0 + row, args.cout - 1)) * K + chunk * 8;
+  }
+  // ---- B (im2col) sources: per load row, the pixel's window origin (element offset in x_nhwc, possibly
+  // outside the image) and its top-left input coordinates ----
+  int32_t b_org[B_PER_WAVE], b_ih[B_PER_WAVE], b_iw[B_PER_WAVE];
+#pragma unroll
+  for (int j = 0; j < B_PER_WAVE; ++j) {
+    const int row = (wave * B_PER_WAVE + j) * 16 + (lane >> 2);
+    const int chunk = (lane & 3) ^ a_swizzle(row);
+    const int64_t p = min(n0 + row, args.p - 1);
+    const int img = static_cast<int>(p / args.howo);
+    const int rem = static_cast<int>(p - static_cast<int64_t>(img) * args.howo);
+    const int oh = rem / args.wo, ow = rem - (rem / args.wo) * args.wo;
+    b_ih[j] = oh * args.sh - args.ph;
+    b_iw[j] = ow * args.sw - args.pw;
+    b_org[j] = ((img * args.h + b_ih[j]) * args.w_in + b_iw[j]) * cin + chunk * 8;
+  }
+  const __amdgpu_buffer_rsrc_t xr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(args.x), static_cast<short>(0), static_cast<int>(args.x_bytes),
+                                        0x00020000);
+
+  // Filter position of the next stage to load; stays on the last stage once every stage has been issued.
+  // ld_off = the stage's element offset from a window origin, (kh * W + kw) * Cin + ci0.
+  int ld_kh = 0, ld_kw = 0, ld_ci = 0, ld_next = 0, ld_off = 0;
+  auto advance = [&]() {
+    if (ld_next + 1 < KT) {
+      ++ld_next;
+      ld_ci += kBK;
+      if (ld_ci == cin) {
+        ld_ci = 0;
+        if (++ld_kw == args.kw) {
+          ld_kw = 0;
+          ++ld_kh;
+        }
+      }
+      ld_off = (ld_kh * args.w_in + ld_kw) * cin + ld_ci;
+    }
+  };
+
+  // Load instruction J of this wave's share of stage kt (filter position = the ld_* counters).
+  auto load_one = [&]<int J>(int kt) {
+    unsigned char* st = ring + (kt & (kStages - 1)) * STAGE;
+    if constexpr (J < A_PER_WAVE) {
+      const int64_t k0 = static_cast<int64_t>(min(kt, KT - 1)) * kBK;
+      global_to_lds16(W + a_src[J] + k0, (FH_LDS void*)(st + (wave * A_PER_WAVE + J) * 1024));
+    } else {
+      constexpr int JB = J - A_PER_WAVE;
+      const int ih = b_ih[JB] + ld_kh, iw = b_iw[JB] + ld_kw;
+      const bool inside = static_cast<unsigned>(ih) < static_cast<unsigned>(args.h) &&
+                          static_cast<unsigned>(iw) < static_cast<unsigned>(args.w_in);
+      // computed unconditionally so the padding case is a select, not a branch
+      const uint32_t at = static_cast<uint32_t>(b_org[JB] + ld_off) * 2u;
+      const uint32_t voff = inside ? at : 0x80000000u;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (FH_LDS void*)(st + A_BYTES + (wave * B_PER_WAVE + JB) * 1024), 16,
+                                               static_cast<int>(voff), 0, 0, 0);
+    }
+  };
+  auto issue_stage = [&](int kt) {
+    [&]<int... J>(std::integer_sequence<int, J...>) {
+      (load_one.template operator()<J>(kt), ...);
+    }(std::make_integer_sequence<int, LOADS>{});
+    advance();
+  };
+
+  const int l32 = lane & 31, hi = lane >> 5;
+  int a_off[2], b_off[2];
+  {
+    const int arow = wm * WM + l32, brow = wn * WN + l32;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      a_off[s] = arow * 64 + (((2 * s + hi) ^ a_swizzle(arow)) * 16);
+      b_off[s] = A_BYTES + brow * 64 + (((2 * s + hi) ^ a_swizzle(brow)) * 16);
+    }
+  }
+  const uint32_t ring_addr = lds_addr((const FH_LDS void*)ring);
+
+  f32x16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int x = 0; x < 16; ++x) acc[i][j][x] = 0.0f;
+  acc_to_agpr(acc);
+
+  KFragments<TM, TN> f0, f1;
+  constexpr int NREAD = TM + TN;
+  constexpr int NMFMA = TM * TN;
+  auto read_one = [&]<int H, int R>(uint32_t base, KFragments<TM, TN>& f) {
+    if constexpr (R < TM) {
+      f.a[R] = lds_read_b128<R * 2048>(base + a_off[H]);
+    } else {
+      f.b[R - TM] = lds_read_b128<(R - TM) * 2048>(base + b_off[H]);
+    }
+  };
+  constexpr int R_SPAN = NMFMA * 3 / 4 > 0 ? NMFMA * 3 / 4 : 1;
+  constexpr int L_SPAN = NMFMA / 2 > 0 ? NMFMA / 2 : 1;
+  auto multiply_and_read = [&]<int H, bool LOADS_TOO>(KFragments<TM, TN>& cur, uint32_t base,
+                                                      KFragments<TM, TN>& nxt, int load_kt) {
+    [&]<int... M_>(std::integer_sequence<int, M_...>) {
+      (
+          [&] {
+            constexpr int i = M_ / TN, j = M_ % TN;
+            mfma32<T>(cur.a[i], cur.b[j], acc[i][j]);
+            constexpr int r0 = first(M_, NREAD, R_SPAN);
+            [&]<int... R_>(std::integer_sequence<int, R_...>) {
+              (read_one.template operator()<H, r0 + R_>(base, nxt), ...);
+            }(std::make_integer_sequence<int, share(M_, NREAD, R_SPAN)>{});
+            if constexpr (LOADS_TOO) {
+              constexpr int l0 = first(M_, LOADS, L_SPAN);
+              [&]<int... L_>(std::integer_sequence<int, L_...>) {
+                (load_one.template operator()<l0 + L_>(load_kt), ...);
+              }(std::make_integer_sequence<int, share(M_, LOADS, L_SPAN)>{});
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }(),
+          ...);
+    }(std::make_integer_sequence<int, NMFMA>{});
+  };
+
+  issue_stage(0);
+  issue_stage(1);
+  issue_stage(2);
+  wait_vmcnt<2 * LOADS>();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  [&]<int... R_>(std::integer_sequence<int, R_...>) {
+    (read_one.template operator()<0, R_>(ring_addr, f0), ...);
+  }(std::make_integer_sequence<int, NREAD>{});
+
+  for (int kt = 0; kt < KT; ++kt) {
+    const uint32_t cur = ring_addr + (kt & (kStages - 1)) * STAGE;
+    const uint32_t nxt = ring_addr + ((kt + 1) & (kStages - 1)) * STAGE;
+    fence_kfragments(f0);
+    multiply_and_read.template operator()<1, false>(f0, cur, f1, 0);
+    wait_vmcnt<LOADS>();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    fence_kfragments(f1);
+    multiply_and_read.template operator()<0, true>(f1, nxt, f0, kt + kStages - 1);
+    advance();
+  }
+  drain_accumulators(acc);
+
+  // ---- epilogue ----
+  wait_vmcnt<0>();
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __syncthreads();
+  constexpr int WTILE_BYTES = WM * WN * 2;
+  static_assert(NW * WTILE_BYTES <= kStages * STAGE, "the wave tiles fit in the ring");
+  S* wl = reinterpret_cast<S*>(ring + wave * WTILE_BYTES);
+  const S* bias = static_cast<const S*>(args.bias);
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      const int rr = i * 32 + 8 * (x >> 2) + 4 * hi + (x & 3);
+      const float bv = bias != nullptr ? Io<T>::load(bias[min(m0 + wm * WM + rr, args.cout - 1)]) : 0.0f;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) wl[rr * WN + j * 32 + l32] = Io<T>::store(acc[i][j][x] + bv);
+    }
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+  constexpr int V = 8;
+  constexpr int LPR = WN / V;
+  constexpr int RPI = 64 / LPR;
+  static_assert(64 % LPR == 0 && WM % RPI == 0, "epilogue access shape");
+  S* __restrict__ Y = static_cast<S*>(args.y);
+  const int c = (lane % LPR) * V;
+  const int64_t p0 = n0 + wn * WN + c;
+  for (int it = 0; it < WM / RPI; ++it) {
+    const int rr = it * RPI + lane / LPR;
+    const int co = m0 + wm * WM + rr;
+    if (co >= args.cout || p0 >= args.p) continue;
+    uint4 packed = *reinterpret_cast<const uint4*>(wl + rr * WN + c);
+    if (args.vec_store && p0 + V <= args.p) {
+      const int64_t img = p0 / args.howo;
+      const int64_t idx = (img * args.cout + co) * args.howo + (p0 - img * args.howo);
+      if (args.ep.nseg > 0) packed = apply_epilogue_vec<T>(args.ep, packed, idx);
+      *reinterpret_cast<uint4*>(Y + idx) = packed;
+    } else {
+      S vals[8];
+      __builtin_memcpy(vals, &packed, 16);
+      for (int e = 0; e < V && p0 + e < args.p; ++e) {
+        const int64_t p = p0 + e;
+        const int64_t img = p / args.howo;
+        const int64_t idx = (img * args.cout + co) * args.howo + (p - img * args.howo);
+        S v = vals[e];
+        if (args.ep.nseg > 0) v = Io<T>::store(apply_epilogue_one<T>(args.ep, Io<T>::load(v), idx));
+        Y[idx] = v;
+      }
+    }
+  }
+}
+
+template <typename T, int BM, int BN, int WAVES_M, int WAVES_N>
+fh_status launch_conv(ConvNhwcArgs a, hipStream_t stream) {
+  a.tiles_m = (a.cout + BM - 1) / BM;
+  a.tiles_n = static_cast<int32_t>((a.p + BN - 1) / BN);
+  const dim3 grid(static_cast<uint32_t>(a.tiles_m) * static_cast<uint32_t>(a.tiles_n));
+  hipLaunchKernelGGL((conv_nhwc_kernel<T, BM, BN, WAVES_M, WAVES_N>), grid, dim3(WAVES_M * WAVES_N * 64), 0, stream, a);
+  return launch_status("conv_nhwc_kernel launch");
+}
+
+// Largest tile that still gives every CU a workgroup; otherwise the one with the most workgroups.
+template <typename T>
+fh_status dispatch_conv(const ConvNhwcArgs& a, hipStream_t stream) {
+  const int64_t cus = device_cu_count();
+  auto tiles = [&](int64_t bm, int64_t bn) { return ((a.cout + bm - 1) / bm) * ((a.p + bn - 1) / bn); };
+  if (a.cout >= 128 && tiles(128, 256) >= cus) return launch_conv<T, 128, 256, 2, 4>(a, stream);
+  if (a.cout >= 128 && tiles(128, 128) >= cus) return launch_conv<T, 128, 128, 2, 4>(a, stream);
+  if (tiles(64, 256) >= cus) return launch_conv<T, 64, 256, 1, 4>(a, stream);
+  if (tiles(64, 128) >= cus) return launch_conv<T, 64, 128, 2, 2>(a, stream);
+  return launch_conv<T, 64, 64, 2, 2>(a, stream);
+}
+
+// Batched transpose through a 64 x 64 LDS tile: y[b][c][r] = x[b][r][c]; reads and writes are coalesced.
+template <typename E>
+__global__ __launch_bounds__(256) void transpose_batched_kernel(const E* __restrict__ x, E* __restrict__ y,
+                                                                int64_t rows, int64_t cols) {
+  __shared__ E tile[64][65];
+  const int64_t b = blockIdx.z;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64, c0 = static_cast<int64_t>(blockIdx.x) * 64;
+  const E* xb = x + b * rows * cols;
+  E* yb = y + b * rows * cols;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int r = ty; r < 64; r += 4) {
+    const int64_t gr = r0 + r, gc = c0 + tx;
+    if (gr < rows && gc < cols) tile[r][tx] = xb[gr * cols + gc];
+  }
+  __syncthreads();
+  for (int c = ty; c < 64; c += 4) {
+    const int64_t gc = c0 + c, gr = r0 + tx;
+    if (gc < cols && gr < rows) yb[gc * rows + gr] = tile[tx][c];
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
+// Geometry accepted by the channels-last MFMA path.
+bool nhwc_supported(int32_t dtype, const int64_t* g) {
+  if (dtype != FH_BF16 && dtype != FH_F16) return false;
+  const int64_t n = g[0], cin = g[1], h = g[2], w = g[3], cout = g[4], kh = g[5], kw = g[6], sh = g[7], sw = g[8],
+                ph = g[9], pw = g[10], groups = g[11];
+  if (groups != 1 || cin % kBK != 0 || n <= 0 || h <= 0 || w <= 0 || cout <= 0 || kh <= 0 || kw <= 0) return false;
+  if (sh <= 0 || sw <= 0 || ph < 0 || pw < 0 || h + 2 * ph < kh || w + 2 * pw < kw) return false;
+  const int64_t oh = (h + 2 * ph - kh) / sh + 1, ow = (w + 2 * pw - kw) / sw + 1;
+  // 32-bit offsets inside the kernel: input bytes, window origins and filter rows
+  if (n * h * w * cin * 2 >= (int64_t{1} << 31)) return false;
+  if (kh * kw * cin >= (int64_t{1} << 24) || n * oh * ow >= (int64_t{1} << 31)) return false;
+  return true;
+}
+
+}  // namespace
 }  // namespace fh
+
+using namespace fh;
+
+extern "C" fh_status fh_transpose_batched(int32_t itemsize, const void* x, void* y, int64_t batch, int64_t rows,
+                                          int64_t cols, void* stream) {
+  if (batch < 0 || rows < 0 || cols < 0) return fail(FH_INVALID_ARGUMENT, "fh_transpose_batched: negative size");
+  if (batch == 0 || rows == 0 || cols == 0) return FH_OK;
+  if (x == nullptr || y == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_transpose_batched: null pointer");
+  if (batch > 65535) return fail(FH_UNIMPLEMENTED, "fh_transpose_batched: batch above 65535");
+  if ((rows + 63) / 64 > 65535) return fail(FH_UNIMPLEMENTED, "fh_transpose_batched: too many row tiles");
+  const dim3 grid(static_cast<uint32_t>((cols + 63) / 64), static_cast<uint32_t>((rows + 63) / 64),
+                  static_cast<uint32_t>(batch));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (itemsize) {
+    case 2:
+      hipLaunchKernelGGL(transpose_batched_kernel<uint16_t>, grid, dim3(256), 0, s, static_cast<const uint16_t*>(x),
+                         static_cast<uint16_t*>(y), rows, cols);
+      break;
+    case 4:
+      hipLaunchKernelGGL(transpose_batched_kernel<uint32_t>, grid, dim3(256), 0, s, static_cast<const uint32_t*>(x),
+                         static_cast<uint32_t*>(y), rows, cols);
+      break;
+    default:
+      return fail(FH_INVALID_ARGUMENT, "fh_transpose_batched: itemsize must be 2 or 4");
+  }
+  return launch_status("transpose_batched_kernel launch");
+}
+
+extern "C" int32_t fh_conv2d_nhwc_supported(int32_t dtype, const int64_t geom[12]) {
+  return geom != nullptr && nhwc_supported(dtype, geom) ? 1 : 0;
+}
+
+extern "C" fh_status fh_conv2d_nhwc_fwd(int32_t dtype, const void* x_nhwc, const void* w_khwc, const void* bias, void* y,
+                                        const int64_t geom[12], const fh_epilogue* epilogue, void* stream) {
+  if (geom == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd: null geometry");
+  if (!nhwc_supported(dtype, geom))
+    return fail(FH_UNIMPLEMENTED, "fh_conv2d_nhwc_fwd: geometry or dtype not supported by the channels-last path "
+                                  "(needs bf16/f16, groups 1, Cin % 32 == 0)");
+  if (x_nhwc == nullptr || w_khwc == nullptr || y == nullptr)
+    return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd: null pointer");
+  if (!aligned16(x_nhwc) || !aligned16(w_khwc)) return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd: operands must be 16-byte aligned");
+  ConvNhwcArgs a{};
+  a.x = x_nhwc;
+  a.w = w_khwc;
+  a.bias = bias;
+  a.y = y;
+  a.cin = static_cast<int32_t>(geom[1]);
+  a.h = static_cast<int32_t>(geom[2]);
+  a.w_in = static_cast<int32_t>(geom[3]);
+  a.cout = static_cast<int32_t>(geom[4]);
+  a.kw = static_cast<int32_t>(geom[6]);
+  a.sh = static_cast<int32_t>(geom[7]);
+  a.sw = static_cast<int32_t>(geom[8]);
+  a.ph = static_cast<int32_t>(geom[9]);
+  a.pw = static_cast<int32_t>(geom[10]);
+  const int64_t oh = (geom[2] + 2 * geom[9] - geom[5]) / geom[7] + 1;
+  const int64_t ow = (geom[3] + 2 * geom[10] - geom[6]) / geom[8] + 1;
+  a.wo = static_cast<int32_t>(ow);
+  a.howo = static_cast<int32_t>(oh * ow);
+  a.k = static_cast<int32_t>(geom[5] * geom[6] * geom[1]);
+  a.p = geom[0] * oh * ow;
+  a.x_bytes = static_cast<uint32_t>(geom[0] * geom[2] * geom[3] * geom[1] * 2);
+  if (epilogue != nullptr) {
+    if (epilogue->nseg < 0 || epilogue->nseg > FH_MAX_SEGMENTS)
+      return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd: epilogue nseg out of range");
+    a.ep.nseg = epilogue->nseg;
+    a.ep.round_between = epilogue->round_between;
+    for (int s = 0; s < a.ep.nseg; ++s) {
+      const uint8_t op = epilogue->ops[s];
+      if (op < FH_EW_ADD || op > FH_EW_GELU) return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd: unknown epilogue op");
+      if (ew_is_binary(op) && epilogue->ins[s] == nullptr)
+        return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd: binary epilogue segment without operand");
+      a.ep.ops[s] = op;
+      a.ep.ins[s] = epilogue->ins[s];
+    }
+  }
+  bool vec = a.howo % 8 == 0 && aligned16(y);
+  for (int s = 0; s < a.ep.nseg; ++s)
+    if (ew_is_binary(a.ep.ops[s]) && !aligned16(a.ep.ins[s])) vec = false;
+  a.vec_store = vec ? 1 : 0;
+  if (a.p == 0) return FH_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return dtype == FH_BF16 ? dispatch_conv<bf16_t>(a, s) : dispatch_conv<f16_t>(a, s);
+}

@@ -110,9 +110,13 @@ inline void* stream_handle(const ops::KernelContext& ctx) {
   return ctx.stream == nullptr ? nullptr : ctx.stream->native_handle();
 }
 
-// Internal op names produced by HipBackend::compile's epilogue lowering (never user-visible).
+// Internal op names produced by HipBackend::compile's lowering (never user-visible).
 inline constexpr std::string_view kGemmEpilogueOp = "hip_matmul_epilogue_internal";
 inline constexpr std::string_view kConvEpilogueOp = "hip_conv2d_epilogue_internal";
+// [d0, d1, d2, d3] -> [d0, d2, d3, d1]: NCHW activations to NHWC, [Cout][Cin][KH][KW] filters to [Cout][KH][KW][Cin].
+inline constexpr std::string_view kChannelsLastOp = "hip_channels_last_internal";
+// conv2d (optionally with an epilogue program) on channels-last operands; output NCHW.
+inline constexpr std::string_view kConvNhwcOp = "hip_conv2d_nhwc_internal";
 
 // Elementwise op name -> fh_ew_op code (0 when the op has no device code).
 uint8_t ew_code(std::string_view op);

@@ -6,12 +6,15 @@
 //  * steps that produce a graph output write straight into the caller's output tensor;
 //  * constants are materialised on the device once, at compile time.
 //
-// Lowering (allowed inside Backend::compile by the HAL contract, include/frame/hal/backend.h:45-63): a matmul
+// Lowering (allowed inside Backend::compile by the HAL contract, include/frame/hal/backend.h:45-63):
+//  * epilogue fusion (opt_level >= 1): a matmul
 // or conv2d whose only consumer is an elementwise node (add, mul, relu, square, gelu or a fused chain) that
 // takes the contraction result as its first operand is replaced by one internal node that applies the
 // consumer's program in the contraction's epilogue. The epilogue rounds to the storage dtype after the
-// product and after every segment, so results equal the unfused graph's bit for bit. The rewrite runs on a
-// private copy of the graph before planning, so the memory plan sees the fused node's real lifetimes.
+// product and after every segment, so results equal the unfused graph's bit for bit.
+//  * channels-last conv (every opt_level): a bf16/f16 conv that the MFMA implicit-GEMM path accepts becomes
+// channels_last(x), channels_last(w) and conv2d_nhwc (see lower_convs).
+// The rewrites run on a private copy of the graph before planning, so the memory plan sees the real lifetimes.
 #include <algorithm>
 #include <cstring>
 #include <mutex>
@@ -97,6 +100,79 @@ Status lower_epilogues(ir::Graph& g) {
     }
   }
   return Status::ok();
+}
+
+// Lowers every conv2d / conv epilogue node that the channels-last MFMA path accepts (fh_conv2d_nhwc_supported)
+// to  x_nhwc = channels_last(x); w_khwc = channels_last(w); y = conv2d_nhwc(x_nhwc, w_khwc, bias?, ep...).
+// The graph is rebuilt in topological order with the three nodes emitted in the conv's place, so the transposed
+// operands become ordinary intermediates that the memory plan places and recycles.
+Result<ir::Graph> lower_convs(const ir::Graph& src) {
+  std::unordered_map<const ir::Value*, ir::Value*> map;
+  ir::Graph out{std::string(src.name())};
+  auto channels_last = [&](ir::Value* v) -> Result<ir::Value*> {
+    ir::TensorType t = v->type();
+    const Shape& s = t.shape;
+    t.shape = Shape({s.dim(0), s.dim(2), s.dim(3), s.dim(1)});
+    Result<ir::Node*> n = out.create_node(std::string(kChannelsLastOp), {v}, {t});
+    if (!n.is_ok()) return n.status();
+    return n.value()->output(0);
+  };
+  for (const ir::Node* n : src.topological_order()) {
+    if (n->op() == ir::kGraphInputOp) {
+      Result<ir::Value*> v = out.add_graph_input(n->outputs()[0].type());
+      if (!v.is_ok()) return v.status();
+      map[&n->outputs()[0]] = v.value();
+      continue;
+    }
+    std::vector<ir::Value*> ins;
+    for (const ir::Value* in : n->inputs()) ins.push_back(map.at(in));
+    const bool is_conv = n->op() == "conv2d" || n->op() == kConvEpilogueOp;
+    bool lowered = false;
+    if (is_conv && n->outputs().size() == 1 && ins.size() >= 2) {
+      const ir::TensorType& xt = n->inputs()[0]->type();
+      const ir::TensorType& wt = n->inputs()[1]->type();
+      auto get = [&](const char* k) -> const ir::AttrValue* {
+        auto it = n->attrs().find(k);
+        return it == n->attrs().end() ? nullptr : &it->second;
+      };
+      const auto* stride = get("stride") ? std::get_if<std::vector<int64_t>>(get("stride")) : nullptr;
+      const auto* pad = get("padding") ? std::get_if<std::vector<int64_t>>(get("padding")) : nullptr;
+      const auto* groups = get("groups") ? std::get_if<int64_t>(get("groups")) : nullptr;
+      const int32_t dt = xt.dtype.code() == DTypeCode::kBFloat16  ? FH_BF16
+                         : xt.dtype.code() == DTypeCode::kFloat16 ? FH_F16
+                                                                  : -1;
+      if (stride && pad && groups && stride->size() == 2 && pad->size() == 2 && dt >= 0 && xt.shape.rank() == 4 &&
+          wt.shape.rank() == 4 && wt.dtype == xt.dtype) {
+        const int64_t geom[12] = {xt.shape.dim(0), xt.shape.dim(1), xt.shape.dim(2), xt.shape.dim(3),
+                                  wt.shape.dim(0), wt.shape.dim(2), wt.shape.dim(3), (*stride)[0],
+                                  (*stride)[1],    (*pad)[0],       (*pad)[1],       *groups};
+        if (wt.shape.dim(1) == xt.shape.dim(1) && fh_conv2d_nhwc_supported(dt, geom) == 1) {
+          Result<ir::Value*> x_cl = channels_last(ins[0]);
+          if (!x_cl.is_ok()) return x_cl.status();
+          Result<ir::Value*> w_cl = channels_last(ins[1]);
+          if (!w_cl.is_ok()) return w_cl.status();
+          std::vector<ir::Value*> conv_ins = ins;
+          conv_ins[0] = x_cl.value();
+          conv_ins[1] = w_cl.value();
+          Result<ir::Node*> c = out.create_node(std::string(kConvNhwcOp), std::move(conv_ins), {n->outputs()[0].type()});
+          if (!c.is_ok()) return c.status();
+          for (const auto& [k, v] : n->attrs()) c.value()->set_attr(k, v);
+          if (n->op() == "conv2d") c.value()->set_attr("n_main_inputs", ir::AttrValue{static_cast<int64_t>(ins.size())});
+          map[&n->outputs()[0]] = c.value()->output(0);
+          lowered = true;
+        }
+      }
+    }
+    if (lowered) continue;
+    std::vector<ir::TensorType> types;
+    for (const ir::Value& o : n->outputs()) types.push_back(o.type());
+    Result<ir::Node*> c = out.create_node(std::string(n->op()), std::move(ins), std::move(types));
+    if (!c.is_ok()) return c.status();
+    for (const auto& [k, v] : n->attrs()) c.value()->set_attr(k, v);
+    for (size_t i = 0; i < n->outputs().size(); ++i) map[&n->outputs()[i]] = c.value()->output(static_cast<int32_t>(i));
+  }
+  for (const ir::Value* o : src.outputs()) FRAME_RETURN_IF_ERROR(out.mark_output(map.at(o)));
+  return out;
 }
 
 class HipExecutable final : public hal::Executable {
@@ -230,7 +306,10 @@ Result<std::unique_ptr<hal::Executable>> compile_hip_executable(const ir::Graph&
   Result<ir::Graph> work = ir::clone_graph(graph);
   if (!work.is_ok()) return work.status();
   if (options.opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_epilogues(work.value()));
-  Result<ops::ExecutablePlan> plan = ops::build_executable_plan(work.value(), kHipBackendName);
+  // Channels-last conv lowering runs at every level, so the conv numerics do not depend on the level.
+  Result<ir::Graph> lowered = lower_convs(work.value());
+  if (!lowered.is_ok()) return lowered.status();
+  Result<ops::ExecutablePlan> plan = ops::build_executable_plan(lowered.value(), kHipBackendName);
   if (!plan.is_ok()) return plan.status();
   auto exe = std::make_unique<HipExecutable>(std::move(plan.value()), allocator, device, options);
   FRAME_RETURN_IF_ERROR(exe->materialize_constants());

@@ -189,6 +189,58 @@ Status conv_impl(KernelContext& ctx, const std::string& op, size_t n_main) {
   return Status::ok();
 }
 
+// x_nhwc [N,H,W,Cin], w_khwc [Cout,KH,KW,Cin], optional bias [Cout], then the epilogue operands; y NCHW.
+Status conv_nhwc_kernel(KernelContext& ctx) {
+  const std::string op(kConvNhwcOp);
+  const auto* n_main_attr = attr<int64_t>(ctx, "n_main_inputs");
+  const size_t n_main = n_main_attr ? static_cast<size_t>(*n_main_attr) : 2;
+  if (ctx.inputs.size() < n_main || n_main < 2 || n_main > 3 || ctx.outputs.size() != 1) return invalid(op, "bad operand count");
+  const Tensor& x = ctx.inputs[0];
+  const Tensor& w = ctx.inputs[1];
+  const Tensor* bias = n_main == 3 ? &ctx.inputs[2] : nullptr;
+  Tensor& y = ctx.outputs[0];
+  const auto* stride = attr<std::vector<int64_t>>(ctx, "stride");
+  const auto* pad = attr<std::vector<int64_t>>(ctx, "padding");
+  const auto* groups = attr<int64_t>(ctx, "groups");
+  if (stride == nullptr || pad == nullptr || groups == nullptr || stride->size() != 2 || pad->size() != 2)
+    return invalid(op, "missing or malformed stride/padding/groups attributes");
+  if (x.shape().rank() != 4 || w.shape().rank() != 4 || y.shape().rank() != 4) return invalid(op, "operands must be rank-4");
+  for (size_t i = 0; i < n_main; ++i)
+    if (!(ctx.inputs[i].dtype() == y.dtype())) return invalid(op, "operand dtypes differ");
+  Result<int32_t> dt = float_code(op, y.dtype());
+  if (!dt.is_ok()) return dt.status();
+  const int64_t geom[12] = {x.shape().dim(0), x.shape().dim(3), x.shape().dim(1), x.shape().dim(2),
+                            w.shape().dim(0), w.shape().dim(1), w.shape().dim(2), (*stride)[0],
+                            (*stride)[1],     (*pad)[0],        (*pad)[1],        *groups};
+  if (w.shape().dim(3) != geom[1]) return invalid(op, "filter channels do not match the input's");
+  const int64_t oh = (geom[2] + 2 * geom[9] - geom[5]) / geom[7] + 1;
+  const int64_t ow = (geom[3] + 2 * geom[10] - geom[6]) / geom[8] + 1;
+  if (y.shape() != Shape({geom[0], geom[4], oh, ow})) return invalid(op, "output shape " + y.shape().to_string() + " does not match the geometry");
+  if (bias != nullptr && (bias->shape().rank() != 1 || bias->shape().dim(0) != geom[4])) return invalid(op, "bias must be [Cout]");
+  Result<fh_epilogue> ep = make_epilogue(ctx, op, n_main);
+  if (!ep.is_ok()) return ep.status();
+  FRAME_HIP_RETURN_IF_ERROR(fh_conv2d_nhwc_fwd(dt.value(), x.raw_data(), w.raw_data(), bias ? bias->raw_data() : nullptr,
+                                               y.raw_data(), geom, ep.value().nseg > 0 ? &ep.value() : nullptr,
+                                               stream_handle(ctx)),
+                            "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
+// [d0, d1, d2, d3] -> [d0, d2, d3, d1]
+Status channels_last_kernel(KernelContext& ctx) {
+  const std::string op(kChannelsLastOp);
+  FRAME_RETURN_IF_ERROR(arity(ctx, op, 1, 1));
+  const Tensor& x = ctx.inputs[0];
+  Tensor& y = ctx.outputs[0];
+  if (x.shape().rank() != 4 || !(x.dtype() == y.dtype())) return invalid(op, "expects a rank-4 input of the output's dtype");
+  const Shape& s = x.shape();
+  if (y.shape() != Shape({s.dim(0), s.dim(2), s.dim(3), s.dim(1)})) return invalid(op, "output shape does not match [d0,d2,d3,d1]");
+  FRAME_HIP_RETURN_IF_ERROR(fh_transpose_batched(static_cast<int32_t>(x.dtype().itemsize()), x.raw_data(), y.raw_data(),
+                                                 s.dim(0), s.dim(1), s.dim(2) * s.dim(3), stream_handle(ctx)),
+                            "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
 Status conv2d_kernel(KernelContext& ctx) {
   if (ctx.inputs.size() != 2 && ctx.inputs.size() != 3) return invalid("conv2d", "expects 2 or 3 inputs");
   return conv_impl(ctx, "conv2d", ctx.inputs.size());
@@ -372,6 +424,8 @@ FRAME_REGISTER_KERNEL("matmul", kHipBackendName, &matmul_kernel);
 FRAME_REGISTER_KERNEL(kGemmEpilogueOp, kHipBackendName, &gemm_epilogue_kernel);
 FRAME_REGISTER_KERNEL("conv2d", kHipBackendName, &conv2d_kernel);
 FRAME_REGISTER_KERNEL(kConvEpilogueOp, kHipBackendName, &conv_epilogue_kernel);
+FRAME_REGISTER_KERNEL(kConvNhwcOp, kHipBackendName, &conv_nhwc_kernel);
+FRAME_REGISTER_KERNEL(kChannelsLastOp, kHipBackendName, &channels_last_kernel);
 FRAME_REGISTER_KERNEL("softmax", kHipBackendName, &softmax_kernel);
 FRAME_REGISTER_KERNEL("layer_norm", kHipBackendName, &layer_norm_kernel);
 FRAME_REGISTER_KERNEL("max_pool2d", kHipBackendName, &pool_kernel<0>);

@@ -126,6 +126,25 @@ fh_status fh_gemm_batched(int32_t dtype, const void* A, const void* B, void* C, 
 fh_status fh_conv2d_fwd(int32_t dtype, const void* x, const void* w, const void* bias, void* y,
                         const int64_t geom[12], const fh_epilogue* epilogue, void* stream);
 
+/* Conv2d forward as an implicit GEMM on MFMA over channels-last operands: x_nhwc [N,H,W,Cin],
+ * w_khwc [Cout,KH,KW,Cin], bias [Cout] or NULL; y is written NCHW [N,Cout,Ho,Wo]. Same semantics and geom as
+ * fh_conv2d_fwd (bias inside the fp32 accumulator, one rounding, then the epilogue). The operands come from
+ * fh_transpose_batched; HipBackend::compile inserts those steps. Replaces the same cuDNN call
+ * (reference: src/backends/cuda/kernels/conv.cpp:385-520) for the geometries fh_conv2d_nhwc_supported accepts. */
+fh_status fh_conv2d_nhwc_fwd(int32_t dtype, const void* x_nhwc, const void* w_khwc, const void* bias, void* y,
+                             const int64_t geom[12], const fh_epilogue* epilogue, void* stream);
+
+/* 1 if fh_conv2d_nhwc_fwd accepts dtype and geom (bf16/f16, groups 1, Cin % 32 == 0, 32-bit offsets), else 0.
+ * Host-only query used at graph compile time; no counterpart in the reference. */
+int32_t fh_conv2d_nhwc_supported(int32_t dtype, const int64_t geom[12]);
+
+/* Batched transpose y[b][c][r] = x[b][r][c] (b < batch, r < rows, c < cols), itemsize 2 or 4.
+ * Lays out the channels-last conv operands: x NCHW -> NHWC is (batch N, rows Cin, cols H*W); w
+ * [Cout][Cin][KH][KW] -> [Cout][KH][KW][Cin] is (batch Cout, rows Cin, cols KH*KW). The reference has no
+ * such step (cuDNN consumes NCHW, reference: src/backends/cuda/kernels/conv.cpp:385-520). */
+fh_status fh_transpose_batched(int32_t itemsize, const void* x, void* y, int64_t batch, int64_t rows, int64_t cols,
+                               void* stream);
+
 /* One-pass fused elementwise program over `numel` elements.
  * ops/arities follow the fused_elementwise_internal attrs (reference: src/ops/fused_elementwise_utils.cpp:17-120);
  * ins are the node's external inputs in order. Single add/mul/relu nodes are programs with nseg = 1.

@@ -114,6 +114,24 @@ def test_gemm_4096_sampled(hip, dtype):
     assert np.all(np.abs(lhs - rhs) <= 1e-2 * scale), "row-sum identity"
 
 
+@pytest.mark.parametrize("dtype", [BF16, F16])
+@pytest.mark.parametrize("n", [64, 96])
+def test_gemm_many_workgroups_per_cu(hip, dtype, n):
+    # N < 128 selects the 64x64 tile; M = 65536 gives 1024 workgroups, four per CU, so several waves share each
+    # SIMD. Regression test for the accumulator drain: without it the first accumulator read after the main
+    # loop intermittently returned a stale value in this configuration. Three runs must agree bit for bit.
+    m, k = 65536, 256
+    say(f"gemm many workgroups per CU dtype={dtype} m={m} k={k} n={n}")
+    a = synth.tensor(51, (m, k), dtype, "uniform")
+    b = synth.tensor(52, (k, n), dtype, "uniform")
+    runs = [run_gemm(hip, dtype, a, b) for _ in range(3)]
+    for r in runs[1:]:
+        assert_bitwise(r, runs[0], "repeat runs")
+    rows = np.arange(0, m, 7)
+    want = orc.matmul(dtype, a[rows], b)
+    assert_close(runs[0][rows], want, dtype, what="gemm many workgroups per CU")
+
+
 @pytest.mark.parametrize("dtype", [F32, BF16])
 def test_gemm_epilogue_add_relu(hip, dtype):
     # matmul -> add(bias[M,N]) -> relu, as Frame's Linear + fused add;relu computes it (rounded between segments)
@@ -287,3 +305,78 @@ def test_conv2d(hip, dtype, geom, with_bias):
                                       hip.i64_array(geom), None, None))
     got = dy.download(want.shape, want.dtype)
     assert_close(got, want, dtype, what=f"conv {geom}")
+
+
+@pytest.mark.parametrize("itemsize,shape", [(2, (3, 64, 3136)), (2, (5, 70, 9)), (4, (2, 33, 130)), (2, (64, 64, 9))])
+def test_transpose_batched(hip, itemsize, shape):
+    b, r, c = shape
+    say(f"transpose_batched itemsize={itemsize} {shape}")
+    dt = np.uint16 if itemsize == 2 else np.uint32
+    x = np.random.default_rng(3).integers(0, np.iinfo(dt).max, size=shape, dtype=dt)
+    dx, dy = dev(hip, x), hip.DeviceBuffer(x.nbytes)
+    hip.check(hip.lib().fh_transpose_batched(itemsize, dx.value, dy.value, b, r, c, None))
+    got = dy.download((b, c, r), dt)
+    assert_bitwise(got, np.ascontiguousarray(x.transpose(0, 2, 1)), "batched transpose")
+
+
+NHWC_CASES = [
+    # N, Cin, H, W, Cout, KH, KW, sh, sw, ph, pw, groups, bias
+    ((2, 64, 12, 12, 64, 3, 3, 1, 1, 1, 1, 1), True),
+    ((2, 64, 7, 7, 128, 3, 3, 1, 1, 1, 1, 1), True),      # Ho*Wo = 49: element stores
+    ((1, 128, 14, 14, 256, 3, 3, 2, 2, 1, 1, 1), False),  # stride 2, Ho*Wo = 49
+    ((2, 64, 14, 14, 128, 1, 1, 2, 2, 0, 0, 1), False),   # 1x1 stride-2 downsample
+    ((1, 32, 9, 11, 40, 3, 5, 1, 2, 2, 0, 1), True),      # rectangular, Cout not a tile multiple
+    ((3, 96, 8, 8, 64, 3, 3, 1, 1, 1, 1, 1), True),       # Cin = 3 stages per filter position
+]
+
+
+def to_nhwc(x):
+    return np.ascontiguousarray(x.transpose(0, 2, 3, 1))
+
+
+@pytest.mark.parametrize("dtype", [BF16, F16])
+@pytest.mark.parametrize("geom,with_bias", NHWC_CASES)
+def test_conv2d_nhwc(hip, dtype, geom, with_bias):
+    say(f"conv nhwc dtype={dtype} {geom} bias={with_bias}")
+    n, cin, h, w, cout, kh, kw = geom[:7]
+    assert hip.lib().fh_conv2d_nhwc_supported(dtype, hip.i64_array(geom)) == 1
+    x = synth.tensor(111, (n, cin, h, w), dtype, "normal")
+    wt = synth.tensor(112, (cout, cin, kh, kw), dtype, "normal", (2.0 / (cin * kh * kw)) ** 0.5)
+    bias = synth.tensor(113, (cout,), dtype, "normal", 0.1) if with_bias else None
+    want = orc.conv2d(dtype, x, wt, bias, geom)
+    dx, dw = dev(hip, to_nhwc(x)), dev(hip, to_nhwc(wt))
+    db = dev(hip, bias) if with_bias else None
+    dy = hip.DeviceBuffer(want.nbytes)
+    hip.check(hip.lib().fh_conv2d_nhwc_fwd(dtype, dx.value, dw.value, db.value if db else None, dy.value,
+                                           hip.i64_array(geom), None, None))
+    got = dy.download(want.shape, want.dtype)
+    assert_close(got, want, dtype, what=f"conv nhwc {geom}")
+
+
+@pytest.mark.parametrize("dtype", [BF16])
+def test_conv2d_nhwc_epilogue_add_relu(hip, dtype):
+    # conv + bias, then the residual add;relu of a ResNet basic block, rounded between segments
+    geom = (2, 64, 14, 14, 64, 3, 3, 1, 1, 1, 1, 1)
+    say(f"conv nhwc epilogue add;relu dtype={dtype}")
+    x = synth.tensor(121, geom[:4], dtype, "normal")
+    wt = synth.tensor(122, (64, 64, 3, 3), dtype, "normal", (2.0 / 576) ** 0.5)
+    bias = synth.tensor(123, (64,), dtype, "normal", 0.1)
+    res = synth.tensor(124, (2, 64, 14, 14), dtype, "normal")
+    conv = orc.conv2d(dtype, x, wt, bias, geom)
+    want = orc.ew_program(dtype, [1, 3], [2, 1], [conv, res])
+    dx, dw, db, dr = dev(hip, to_nhwc(x)), dev(hip, to_nhwc(wt)), dev(hip, bias), dev(hip, res)
+    dy = hip.DeviceBuffer(want.nbytes)
+    ep = hip.make_epilogue([(hip.EW_ADD, dr.value), (hip.EW_RELU, None)])
+    hip.check(hip.lib().fh_conv2d_nhwc_fwd(dtype, dx.value, dw.value, db.value, dy.value, hip.i64_array(geom),
+                                           ctypes.byref(ep), None))
+    got = dy.download(want.shape, want.dtype)
+    assert_close(got, want, dtype, what="conv nhwc epilogue")
+
+
+def test_conv2d_nhwc_rejects_unsupported(hip):
+    # Cin % 32 != 0, grouped and fp32 convolutions stay on the direct path
+    for dtype, geom in [(BF16, (1, 3, 9, 9, 4, 3, 3, 1, 1, 1, 1, 1)), (BF16, (1, 64, 9, 9, 64, 3, 3, 1, 1, 1, 1, 2)),
+                        (F32, (1, 64, 9, 9, 64, 3, 3, 1, 1, 1, 1, 1))]:
+        assert hip.lib().fh_conv2d_nhwc_supported(dtype, hip.i64_array(geom)) == 0
+        status = hip.lib().fh_conv2d_nhwc_fwd(dtype, None, None, None, None, hip.i64_array(geom), None, None)
+        assert status == 4, status  # FH_UNIMPLEMENTED
