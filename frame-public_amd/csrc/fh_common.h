@@ -93,12 +93,19 @@ struct Io<float> {
   __device__ static float round(float v) { return v; }
 };
 
+// Device narrowing to bf16 on gfx950's v_cvt_pk_bf16_f32 (round-to-nearest-even). Checked exhaustively on an
+// MI355X against float_to_bf16_bits above for all 2^32 float bit patterns, NaNs and denormals included: zero
+// differences, so it is the reference's narrowing.
+__device__ inline uint16_t float_to_bf16_bits_hw(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+
 template <>
 struct Io<bf16_t> {
   using storage = uint16_t;
   __device__ static float load(uint16_t v) { return bf16_bits_to_float(v); }
-  __device__ static uint16_t store(float v) { return float_to_bf16_bits(v); }
-  __device__ static float round(float v) { return bf16_bits_to_float(float_to_bf16_bits(v)); }
+  __device__ static uint16_t store(float v) { return float_to_bf16_bits_hw(v); }
+  __device__ static float round(float v) { return bf16_bits_to_float(float_to_bf16_bits_hw(v)); }
 };
 
 template <>

@@ -211,7 +211,6 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int x = 0; x < 16; ++x) acc[i][j][x] = 0.0f;
-  acc_to_agpr(acc);
 
   KFragments<TM, TN> f0, f1;
   constexpr int NREAD = TM + TN;
@@ -271,7 +270,10 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
     multiply_and_read.template operator()<0, true>(f1, nxt, f0, kt + kStages - 1);
     advance();
   }
-  drain_accumulators(acc);
+  // The last step read the next half's fragments (past the end: unused). Those LDS reads are still in flight
+  // and would write their registers after the compiler has reused them in the epilogue, so they are fenced with
+  // the registers tied before anything else may use them.
+  fence_kfragments(f0);
 
   // ---- epilogue ----
   wait_vmcnt<0>();

@@ -89,6 +89,132 @@ __global__ __launch_bounds__(kEwThreads) void ew_program_kernel(EwArgs a) {
   }
 }
 
+// ---- fast path: 16-byte vectors, NIN external inputs known at compile time ----------------------------------
+// Per vector: the NIN input loads are issued first (non-temporal: each element is read once), then the program
+// runs with the segment switch outside the element loop, then one non-temporal 16-byte store. Rounding between
+// segments is skipped where it is provably the identity: after the last segment (the store rounds) and after
+// relu of an already rounded value (relu returns its input or zero, both representable).
+typedef unsigned int ew_u4 __attribute__((ext_vector_type(4)));
+
+template <typename T>
+struct Lanes;
+template <>
+struct Lanes<float> {
+  static constexpr int V = 4;
+  __device__ static void unpack(const ew_u4& w, float (&v)[4]) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = __uint_as_float(w[e]);
+  }
+  __device__ static ew_u4 pack(const float (&v)[4]) {
+    return ew_u4{__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
+  }
+  __device__ static void round(float (&)[4]) {}
+};
+template <>
+struct Lanes<bf16_t> {
+  static constexpr int V = 8;
+  __device__ static void unpack(const ew_u4& w, float (&v)[8]) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      v[2 * d] = __uint_as_float(w[d] << 16);
+      v[2 * d + 1] = __uint_as_float(w[d] & 0xffff0000u);
+    }
+  }
+  __device__ static ew_u4 pack(const float (&v)[8]) {
+    ew_u4 w;
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+      w[d] = static_cast<uint32_t>(float_to_bf16_bits_hw(v[2 * d])) |
+             (static_cast<uint32_t>(float_to_bf16_bits_hw(v[2 * d + 1])) << 16);
+    return w;
+  }
+  __device__ static void round(float (&v)[8]) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = Io<bf16_t>::round(v[e]);
+  }
+};
+template <>
+struct Lanes<f16_t> {
+  static constexpr int V = 8;
+  __device__ static void unpack(const ew_u4& w, float (&v)[8]) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      v[2 * d] = f16_bits_to_float(static_cast<uint16_t>(w[d] & 0xffffu));
+      v[2 * d + 1] = f16_bits_to_float(static_cast<uint16_t>(w[d] >> 16));
+    }
+  }
+  __device__ static ew_u4 pack(const float (&v)[8]) {
+    ew_u4 w;
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+      w[d] = static_cast<uint32_t>(float_to_f16_bits(v[2 * d])) | (static_cast<uint32_t>(float_to_f16_bits(v[2 * d + 1])) << 16);
+    return w;
+  }
+  __device__ static void round(float (&v)[8]) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = Io<f16_t>::round(v[e]);
+  }
+};
+
+template <typename T, int NIN>
+__global__ __launch_bounds__(kEwThreads) void ew_vec_kernel(EwArgs a) {
+  using L = Lanes<T>;
+  constexpr int V = L::V;
+  const int64_t nvec = a.numel / V;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kEwThreads;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kEwThreads + threadIdx.x; i < nvec; i += stride) {
+    ew_u4 in[NIN];
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) in[k] = __builtin_nontemporal_load(static_cast<const ew_u4*>(a.ins[k]) + i);
+    float v[V], w[V];
+    L::unpack(in[0], v);
+    int next = 1;
+    bool rounded = true;  // v holds storage-representable values (it starts as a loaded input)
+    for (int s = 0; s < a.nseg; ++s) {
+      const uint8_t op = a.ops[s];
+      const bool last = s + 1 == a.nseg;
+      switch (op) {
+        case FH_EW_ADD:
+        case FH_EW_MUL: {
+          ew_u4 t = in[0];
+#pragma unroll
+          for (int k = 1; k < NIN; ++k)
+            if (k == next) t = in[k];
+          ++next;
+          L::unpack(t, w);
+          if (op == FH_EW_ADD) {
+#pragma unroll
+            for (int e = 0; e < V; ++e) v[e] = v[e] + w[e];
+          } else {
+#pragma unroll
+            for (int e = 0; e < V; ++e) v[e] = v[e] * w[e];
+          }
+          rounded = false;
+          break;
+        }
+        case FH_EW_RELU:
+#pragma unroll
+          for (int e = 0; e < V; ++e) v[e] = (v[e] < 0.0f) ? 0.0f : v[e];
+          break;  // relu of a rounded value is rounded
+        default:
+#pragma unroll
+          for (int e = 0; e < V; ++e) v[e] = ew_unary(op, v[e]);
+          rounded = false;
+          break;
+      }
+      if (a.round_between && !last && !rounded) {
+        L::round(v);
+        rounded = true;
+      }
+    }
+    __builtin_nontemporal_store(L::pack(v), static_cast<ew_u4*>(a.out) + i);
+  }
+  // scalar tail (numel % V elements) on the first threads of the grid
+  const int64_t tail_start = nvec * V;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kEwThreads + threadIdx.x;
+  if (tail_start + t < a.numel) ew_eval<T, 1>(a, tail_start + t);
+}
+
 template <typename T>
 fh_status launch_ew(const EwArgs& a, hipStream_t stream) {
   using S = typename Io<T>::storage;
@@ -100,17 +226,28 @@ fh_status launch_ew(const EwArgs& a, hipStream_t stream) {
   const int64_t per_thread = aligned ? V : 1;
   const int64_t work = (a.numel + per_thread - 1) / per_thread;
   int64_t blocks = (work + kEwThreads - 1) / kEwThreads;
-  const int64_t cap = static_cast<int64_t>(device_cu_count()) * 16;
+  const int64_t cap = static_cast<int64_t>(device_cu_count()) * 16;  // measured best for 25-100 MB operands
   if (blocks > cap) blocks = cap;
   if (blocks < 1) blocks = 1;
-  if (aligned) {
-    hipLaunchKernelGGL((ew_program_kernel<T, V>), dim3(static_cast<uint32_t>(blocks)), dim3(kEwThreads), 0,
-                       stream, a);
+  const dim3 grid(static_cast<uint32_t>(blocks));
+  if (aligned && nin >= 1 && nin <= 3) {
+    switch (nin) {
+      case 1:
+        hipLaunchKernelGGL((ew_vec_kernel<T, 1>), grid, dim3(kEwThreads), 0, stream, a);
+        break;
+      case 2:
+        hipLaunchKernelGGL((ew_vec_kernel<T, 2>), grid, dim3(kEwThreads), 0, stream, a);
+        break;
+      default:
+        hipLaunchKernelGGL((ew_vec_kernel<T, 3>), grid, dim3(kEwThreads), 0, stream, a);
+        break;
+    }
+  } else if (aligned) {
+    hipLaunchKernelGGL((ew_program_kernel<T, V>), grid, dim3(kEwThreads), 0, stream, a);
   } else {
-    hipLaunchKernelGGL((ew_program_kernel<T, 1>), dim3(static_cast<uint32_t>(blocks)), dim3(kEwThreads), 0,
-                       stream, a);
+    hipLaunchKernelGGL((ew_program_kernel<T, 1>), grid, dim3(kEwThreads), 0, stream, a);
   }
-  return launch_status("ew_program_kernel launch");
+  return launch_status("ew kernel launch");
 }
 
 // ---------------------------------------------------------------------------------------------

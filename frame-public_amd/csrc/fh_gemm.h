@@ -28,29 +28,6 @@ struct GemmArgs {
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));
 
-// Accumulator drain between a GEMM main loop and its epilogue. Measured on MI355X: when several waves share a
-// SIMD, a VALU read of an MFMA result placed at the compiler's minimum distance after the MFMA (12 wait states
-// for v_mfma_f32_32x32x16_bf16) can return the accumulator's previous value. Each accumulator is tied to an
-// AGPR-resident asm statement so no copy or read of it can be scheduled earlier; the first one carries 24 wait
-// states. Call acc_to_agpr() once before the main loop (keeps the accumulators in AGPRs for the whole loop,
-// so the ties below add no copies) and drain_accumulators() right after it.
-template <int TM, int TN>
-__device__ __forceinline__ void acc_to_agpr(f32x16_t (&acc)[TM][TN]) {
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) asm volatile("" : "+a"(acc[i][j]));
-}
-
-template <int TM, int TN>
-__device__ __forceinline__ void drain_accumulators(f32x16_t (&acc)[TM][TN]) {
-  asm volatile("s_nop 7\n s_nop 7\n s_nop 7" : "+a"(acc[0][0]));
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j) asm volatile("" : "+a"(acc[i][j]));
-}
-
 // bf16 / f16 GEMM on 32x32x16 MFMA with direct-to-LDS operand loads (fh_gemm16.hip).
 // Accepts: K % 32 == 0, N % 8 == 0, lda/ldb/ldc % 8 == 0, 16-byte aligned base pointers and batch strides,
 // 16-byte aligned epilogue operands. Returns false (and launches nothing) otherwise.

@@ -218,7 +218,6 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(GemmArgs args) {
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
-  acc_to_agpr(acc);
 
   const int KT = static_cast<int>((K + BK - 1) / BK);
   const int half = lane >> 5;
@@ -255,7 +254,6 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(GemmArgs args) {
     if (kt + 1 < KT) store_slice(cur ^ 1);
     __syncthreads();
   }
-  drain_accumulators(acc);
 
   // --- epilogue: stage the rounded tile through LDS (free after the last barrier), then each wave runs the
   // elementwise program on 16-byte vectors and stores them coalesced. Rounding the product to T before

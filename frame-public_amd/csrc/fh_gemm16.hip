@@ -176,7 +176,6 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
     for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int x = 0; x < 16; ++x) acc[i][j][x] = 0.0f;
-  acc_to_agpr(acc);
 
   Fragments<TM, TN> f0, f1;
   constexpr int NREAD = TM + 2 * TN;  // LDS reads per half
@@ -243,7 +242,10 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
     fence_fragments(f1);
     multiply_and_read.template operator()<0, true>(f1, nxt, f0, kt + kStages - 1);
   }
-  drain_accumulators(acc);
+  // The last step read the next half's fragments (past the end: unused). Those LDS reads are still in flight
+  // and would write their registers after the compiler has reused them in the epilogue, so they are fenced with
+  // the registers tied before anything else may use them.
+  fence_fragments(f0);
 
   // ---- epilogue: round, stage each wave tile in LDS, then 16-byte coalesced read-modify-store ----
   wait_vmcnt<0>();  // the trailing re-loads must land before the ring is reused

@@ -117,9 +117,11 @@ def test_gemm_4096_sampled(hip, dtype):
 @pytest.mark.parametrize("dtype", [BF16, F16])
 @pytest.mark.parametrize("n", [64, 96])
 def test_gemm_many_workgroups_per_cu(hip, dtype, n):
-    # N < 128 selects the 64x64 tile; M = 65536 gives 1024 workgroups, four per CU, so several waves share each
-    # SIMD. Regression test for the accumulator drain: without it the first accumulator read after the main
-    # loop intermittently returned a stale value in this configuration. Three runs must agree bit for bit.
+    # N < 128 selects the 64x64 tile (one MFMA per k16 half); M = 65536 gives 1024 workgroups, four per CU.
+    # Regression test for the post-loop fragment fence: the last step's LDS reads (inline asm) are still in flight
+    # when the loop ends, and without the fence the compiler reused their destination registers for the first
+    # epilogue values, which the landing reads then overwrote (a few hundred wrong outputs per run, varying from
+    # run to run). Three runs must agree bit for bit and match the oracle.
     m, k = 65536, 256
     say(f"gemm many workgroups per CU dtype={dtype} m={m} k={k} n={n}")
     a = synth.tensor(51, (m, k), dtype, "uniform")
