@@ -10,6 +10,7 @@
 #include <hip/hip_runtime.h>
 
 #include <string>
+#include <utility>
 
 #include "fh_common.h"
 
@@ -120,17 +121,25 @@ struct Lanes<bf16_t> {
       v[2 * d + 1] = __uint_as_float(w[d] & 0xffff0000u);
     }
   }
+  // two floats -> one packed pair with a single v_cvt_pk_bf16_f32 (the hardware narrowing, see fh_common.h)
+  __device__ static uint32_t pack2(float lo, float hi) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{lo, hi}, b2));
+  }
   __device__ static ew_u4 pack(const float (&v)[8]) {
     ew_u4 w;
 #pragma unroll
-    for (int d = 0; d < 4; ++d)
-      w[d] = static_cast<uint32_t>(float_to_bf16_bits_hw(v[2 * d])) |
-             (static_cast<uint32_t>(float_to_bf16_bits_hw(v[2 * d + 1])) << 16);
+    for (int d = 0; d < 4; ++d) w[d] = pack2(v[2 * d], v[2 * d + 1]);
     return w;
   }
   __device__ static void round(float (&v)[8]) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = Io<bf16_t>::round(v[e]);
+    for (int d = 0; d < 4; ++d) {
+      const uint32_t p = pack2(v[2 * d], v[2 * d + 1]);
+      v[2 * d] = __uint_as_float(p << 16);
+      v[2 * d + 1] = __uint_as_float(p & 0xffff0000u);
+    }
   }
 };
 template <>
@@ -156,30 +165,59 @@ struct Lanes<f16_t> {
   }
 };
 
+// The segment op codes as one scalar word: a runtime-indexed a.ops[s] becomes a per-iteration vector load of the
+// kernel argument followed by a vmcnt(0) wait, which also drains the in-flight input loads.
+__device__ __forceinline__ uint64_t ops_as_word(const EwArgs& a) {
+  uint64_t w;
+  __builtin_memcpy(&w, a.ops, sizeof(w));
+  static_assert(sizeof(a.ops) == sizeof(w), "eight one-byte op codes");
+  return w;
+}
+
+// Issues the NIN input loads of vector i. The empty asm statements take the loaded registers as operands, so all
+// NIN loads are issued before the first wait (the compiler would otherwise sink a load to its first use).
+template <int NIN>
+__device__ __forceinline__ void ew_load(const EwArgs& a, int64_t i, ew_u4 (&in)[NIN]) {
+#pragma unroll
+  for (int k = 0; k < NIN; ++k) in[k] = __builtin_nontemporal_load(static_cast<const ew_u4*>(a.ins[k]) + i);
+}
+
+template <int NIN>
+__device__ __forceinline__ void ew_issued(ew_u4 (&in)[NIN]) {
+#pragma unroll
+  for (int k = 0; k < NIN; ++k) asm volatile("" : "+v"(in[k]));
+}
+
 template <typename T, int NIN>
 __global__ __launch_bounds__(kEwThreads) void ew_vec_kernel(EwArgs a) {
   using L = Lanes<T>;
   constexpr int V = L::V;
+  const uint64_t ops_word = ops_as_word(a);
   const int64_t nvec = a.numel / V;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kEwThreads;
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * kEwThreads + threadIdx.x; i < nvec; i += stride) {
-    ew_u4 in[NIN];
-#pragma unroll
-    for (int k = 0; k < NIN; ++k) in[k] = __builtin_nontemporal_load(static_cast<const ew_u4*>(a.ins[k]) + i);
+  int64_t i = static_cast<int64_t>(blockIdx.x) * kEwThreads + threadIdx.x;
+  // one vector of look-ahead: the next grid-stride vector's loads are in flight while this one is computed
+  ew_u4 cur[NIN], nxt[NIN];
+  if (i < nvec) ew_load<NIN>(a, i, cur);
+  for (; i < nvec; i += stride) {
+    // unconditional (index clamped to the last vector, result unused past the end): a load under a per-lane
+    // condition would make the wait counts unknowable and force a wait for every outstanding load
+    ew_load<NIN>(a, min(i + stride, nvec - 1), nxt);
+    ew_issued<NIN>(cur);
     float v[V], w[V];
-    L::unpack(in[0], v);
+    L::unpack(cur[0], v);
     int next = 1;
     bool rounded = true;  // v holds storage-representable values (it starts as a loaded input)
     for (int s = 0; s < a.nseg; ++s) {
-      const uint8_t op = a.ops[s];
+      const uint8_t op = static_cast<uint8_t>(ops_word >> (8 * s));
       const bool last = s + 1 == a.nseg;
       switch (op) {
         case FH_EW_ADD:
         case FH_EW_MUL: {
-          ew_u4 t = in[0];
+          ew_u4 t = cur[0];
 #pragma unroll
           for (int k = 1; k < NIN; ++k)
-            if (k == next) t = in[k];
+            if (k == next) t = cur[k];
           ++next;
           L::unpack(t, w);
           if (op == FH_EW_ADD) {
@@ -208,11 +246,105 @@ __global__ __launch_bounds__(kEwThreads) void ew_vec_kernel(EwArgs a) {
       }
     }
     __builtin_nontemporal_store(L::pack(v), static_cast<ew_u4*>(a.out) + i);
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) cur[k] = nxt[k];
   }
   // scalar tail (numel % V elements) on the first threads of the grid
   const int64_t tail_start = nvec * V;
   const int64_t t = static_cast<int64_t>(blockIdx.x) * kEwThreads + threadIdx.x;
   if (tail_start + t < a.numel) ew_eval<T, 1>(a, tail_start + t);
+}
+
+// Programs known at compile time (the common fused groups): no segment loop, no op switch, each segment's
+// input fixed. OPS are fh_ew_op codes; NIN = 1 + the number of binary segments.
+template <uint8_t... OPS>
+constexpr int ew_inputs() {
+  return 1 + ((OPS == FH_EW_ADD || OPS == FH_EW_MUL ? 1 : 0) + ... + 0);
+}
+
+template <typename T, uint8_t... OPS>
+__global__ __launch_bounds__(kEwThreads) void ew_fixed_kernel(EwArgs a) {
+  using L = Lanes<T>;
+  constexpr int V = L::V;
+  constexpr int NIN = ew_inputs<OPS...>();
+  constexpr uint8_t ops[] = {OPS...};
+  constexpr int NSEG = sizeof...(OPS);
+  const int64_t nvec = a.numel / V;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kEwThreads;
+  int64_t i = static_cast<int64_t>(blockIdx.x) * kEwThreads + threadIdx.x;
+  ew_u4 cur[NIN], nxt[NIN];
+  if (i < nvec) ew_load<NIN>(a, i, cur);
+  for (; i < nvec; i += stride) {
+    ew_load<NIN>(a, min(i + stride, nvec - 1), nxt);
+    ew_issued<NIN>(cur);
+    float v[V], w[V];
+    L::unpack(cur[0], v);
+    [&]<int... S>(std::integer_sequence<int, S...>) {
+      (
+          [&] {
+            constexpr uint8_t op = ops[S];
+            constexpr bool binary = op == FH_EW_ADD || op == FH_EW_MUL;
+            // input of segment S: 1 + the binary segments before it
+            constexpr int in_idx = [] {
+              int n = 1;
+              for (int q = 0; q < S; ++q) n += (ops[q] == FH_EW_ADD || ops[q] == FH_EW_MUL) ? 1 : 0;
+              return n;
+            }();
+            if constexpr (binary) {
+              L::unpack(cur[in_idx], w);
+#pragma unroll
+              for (int e = 0; e < V; ++e) v[e] = op == FH_EW_ADD ? v[e] + w[e] : v[e] * w[e];
+            } else if constexpr (op == FH_EW_RELU) {
+#pragma unroll
+              for (int e = 0; e < V; ++e) v[e] = (v[e] < 0.0f) ? 0.0f : v[e];
+            } else {
+#pragma unroll
+              for (int e = 0; e < V; ++e) v[e] = ew_unary(op, v[e]);
+            }
+            // Rounded after every segment but the last (the store rounds). Every segment's input is representable
+            // (a loaded value or a rounded / relu'd result), and relu returns its input or zero, so rounding after
+            // relu is the identity as well.
+            constexpr bool skip = S + 1 == NSEG || op == FH_EW_RELU;
+            if constexpr (!skip) L::round(v);
+          }(),
+          ...);
+    }(std::make_integer_sequence<int, NSEG>{});
+    __builtin_nontemporal_store(L::pack(v), static_cast<ew_u4*>(a.out) + i);
+#pragma unroll
+    for (int k = 0; k < NIN; ++k) cur[k] = nxt[k];
+  }
+  const int64_t tail_start = nvec * V;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kEwThreads + threadIdx.x;
+  if (tail_start + t < a.numel) ew_eval<T, 1>(a, tail_start + t);
+}
+
+// Launches the compile-time kernel for a.ops when it is one of the common programs; false otherwise.
+template <typename T>
+bool launch_fixed(const EwArgs& a, dim3 grid, hipStream_t stream) {
+  const uint8_t o0 = a.ops[0], o1 = a.nseg > 1 ? a.ops[1] : 0;
+#define FH_EW_FIXED(...)                                                                       \
+  do {                                                                                         \
+    hipLaunchKernelGGL((ew_fixed_kernel<T, __VA_ARGS__>), grid, dim3(kEwThreads), 0, stream, a); \
+    return true;                                                                               \
+  } while (0)
+  if (a.nseg == 1) {
+    switch (o0) {
+      case FH_EW_ADD: FH_EW_FIXED(FH_EW_ADD);
+      case FH_EW_MUL: FH_EW_FIXED(FH_EW_MUL);
+      case FH_EW_RELU: FH_EW_FIXED(FH_EW_RELU);
+      case FH_EW_GELU: FH_EW_FIXED(FH_EW_GELU);
+      case FH_EW_SQUARE: FH_EW_FIXED(FH_EW_SQUARE);
+      default: return false;
+    }
+  }
+  if (a.nseg == 2) {
+    if (o0 == FH_EW_ADD && o1 == FH_EW_RELU) FH_EW_FIXED(FH_EW_ADD, FH_EW_RELU);
+    if (o0 == FH_EW_ADD && o1 == FH_EW_GELU) FH_EW_FIXED(FH_EW_ADD, FH_EW_GELU);
+    if (o0 == FH_EW_ADD && o1 == FH_EW_ADD) FH_EW_FIXED(FH_EW_ADD, FH_EW_ADD);
+    if (o0 == FH_EW_MUL && o1 == FH_EW_ADD) FH_EW_FIXED(FH_EW_MUL, FH_EW_ADD);
+  }
+#undef FH_EW_FIXED
+  return false;
 }
 
 template <typename T>
@@ -230,7 +362,10 @@ fh_status launch_ew(const EwArgs& a, hipStream_t stream) {
   if (blocks > cap) blocks = cap;
   if (blocks < 1) blocks = 1;
   const dim3 grid(static_cast<uint32_t>(blocks));
-  if (aligned && nin >= 1 && nin <= 3) {
+  // compile-time programs need round_between (always set for 16-bit storage; rounding is the identity for fp32)
+  if (aligned && (a.round_between || sizeof(S) == 4) && launch_fixed<T>(a, grid, stream)) {
+    // launched
+  } else if (aligned && nin >= 1 && nin <= 3) {
     switch (nin) {
       case 1:
         hipLaunchKernelGGL((ew_vec_kernel<T, 1>), grid, dim3(kEwThreads), 0, stream, a);
