@@ -25,10 +25,11 @@ for p in (os.path.join(REPO, "frame-public_amd"), os.path.join(REPO, "tests")):
 import numpy as np  # noqa: E402
 
 PEAK_BF16_TFLOPS = 2516.6  # dense bf16 MFMA, 256 CU x 2.4 GHz x 4096 FLOP/clk/CU
+PEAK_F32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 
 N = 4096
-BF16 = 3
+F32, BF16 = 0, 3
 
 
 def gemm_flops(m, n, k):
@@ -98,6 +99,97 @@ def copy_calibration(mib: int, reps: int):
     print(json.dumps({"copy_calibration_bytes": nbytes, "launches": reps}), flush=True)
 
 
+# ---- secondary measurements of the same metric (GEMM/Conv2d TFLOP/s, fused-op GB/s, graph latency) --
+
+def _time_graph(graph_text, input_sets, steps, warmup):
+    """ms per Executable::run of the compiled graph, rotating over input_sets (lists of numpy arrays), HIP events
+    on the executable's own stream."""
+    from frame_hip import abi, host
+
+    exe = host.compile(graph_text, "hip")
+    sets = [exe.upload_inputs(s) for s in input_sets]
+    outs = exe.alloc_outputs()
+    stream = host.Stream("hip")
+    native = _NativeStream(stream.native)
+    start, stop = abi.Event(), abi.Event()
+    for i in range(warmup):
+        exe.run_tensors(sets[i % len(sets)], outs, stream)
+    stream.synchronize()
+    start.record(native)
+    for i in range(steps):
+        exe.run_tensors(sets[i % len(sets)], outs, stream)
+    stop.record(native)
+    stop.synchronize()
+    return start.elapsed_ms(stop) / steps
+
+
+def extras(steps):
+    """Each entry: the config, its work, and the measured rate; failures are reported, not raised."""
+    from frame_hip import graphs, synth
+
+    out = {}
+
+    def guard(name, fn):
+        try:
+            out[name] = fn()
+        except Exception as e:  # a secondary measurement must not cost the bench line
+            out[name] = {"error": f"{type(e).__name__}: {e}"}
+
+    def fused():
+        # C4's residual add;relu at layer-1 shape, bf16; 8 input sets (616 MB) so every run reads from HBM
+        shape = (64, 64, 56, 56)
+        g = graphs.Graph("hip")
+        x, y = g.input(BF16, shape), g.input(BF16, shape)
+        g.output(g.relu(g.add(x, y)))
+        sets = [[synth.tensor(900 + 2 * i, shape, BF16), synth.tensor(901 + 2 * i, shape, BF16)] for i in range(8)]
+        ms = _time_graph(g.text(), sets, max(steps, 40), 8)
+        by = 3 * int(np.prod(shape)) * 2
+        return {"workload": "fused add;relu bf16 [64,64,56,56], cold (8 rotating input sets)", "us": round(ms * 1e3, 2),
+                "GB/s": round(by / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(by / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+
+    def conv(dtype):
+        flops = 2 * 32 * 64 * 56 * 56 * 64 * 9
+        ms = _time_graph(graphs.conv(dtype).text(), [graphs.conv_inputs(dtype)], max(3, steps // 5), 2)
+        tf = flops / (ms * 1e-3) / 1e12
+        peak = PEAK_BF16_TFLOPS if dtype == BF16 else PEAK_F32_TFLOPS
+        return {"workload": f"C3 conv2d+bias+relu {'bf16' if dtype == BF16 else 'f32'} [32,64,56,56]*[64,64,3,3], whole compiled graph",
+                "us": round(ms * 1e3, 1), "TFLOP/s": round(tf, 1), "frac_mfma": round(tf / peak, 4)}
+
+    def gemm(n, dtype):
+        ms = _time_graph(graphs.gemm(n, dtype).text(), [graphs.gemm_inputs(n, dtype)], max(10, steps // 2), 3)
+        tf = gemm_flops(n, n, n) / (ms * 1e-3) / 1e12
+        peak = PEAK_BF16_TFLOPS if dtype == BF16 else PEAK_F32_TFLOPS
+        return {"TFLOP/s": round(tf, 1), "frac_mfma": round(tf / peak, 4), "us": round(ms * 1e3, 1)}
+
+    def mlp():
+        ms = _time_graph(graphs.mlp(64, F32).text(), [graphs.mlp_inputs(64, F32)], max(50, steps), 10)
+        return {"workload": "C1 MLP f32 batch 64, compiled graph", "us": round(ms * 1e3, 1)}
+
+    def resnet():
+        g, specs = graphs.resnet18(batch=64, dtype=BF16)
+        ms = _time_graph(g.text(), [graphs.resnet18_inputs(specs, batch=64, dtype=BF16)], max(5, steps // 5), 2)
+        return {"workload": "C4 ResNet-18 bf16 batch 64 224px, compiled graph", "ms": round(ms, 3),
+                "TFLOP/s": round(232.2e9 / (ms * 1e-3) / 1e12, 1)}
+
+    def transformer():
+        g, shapes = graphs.transformer_block(dtype=BF16)
+        ms = _time_graph(g.text(), [graphs.transformer_inputs(shapes, dtype=BF16)], max(5, steps // 5), 2)
+        return {"workload": "C5 transformer block bf16 8x512x1024, 16 heads, FFN 4096, compiled graph", "ms": round(ms, 3),
+                "TFLOP/s": round(111.67e9 / (ms * 1e-3) / 1e12, 1)}
+
+    guard("fused_elementwise", fused)
+    guard("conv_c3_bf16", lambda: conv(BF16))
+    guard("conv_c3_f32", lambda: conv(F32))
+    for n in (1024, 2048):
+        guard(f"gemm_bf16_{n}", lambda n=n: gemm(n, BF16))
+    for n in (1024, 2048, 4096):
+        guard(f"gemm_f32_{n}", lambda n=n: gemm(n, F32))
+    guard("c1_mlp_latency", mlp)
+    guard("c4_resnet18", resnet)
+    guard("c5_transformer", transformer)
+    return out
+
+
 def cpu_baseline(rows: int):
     """Reference CPU backend (single thread) on rows x 4096 x 4096 of the same GEMM."""
     import oracle_lib as orc
@@ -131,6 +223,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--cpu-rows", type=int, default=128)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extras", action="store_true", help="only the headline GEMM (and the CPU baseline)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="only run the known-size copy used to scale HBM traffic counters")
     args = ap.parse_args()
@@ -163,6 +256,8 @@ def main():
     }
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(args.cpu_rows)
+    if not args.no_extras:
+        line["extras"] = extras(args.steps)
     print(json.dumps(line), flush=True)
 
 

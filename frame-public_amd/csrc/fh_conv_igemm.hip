@@ -21,6 +21,11 @@
 // one barrier per stage. The filter position (kh, kw, ci0) of the next stage to load advances with scalar
 // counters, not divisions.
 //
+// C8 mode (Cin <= 8, e.g. an RGB stem): x is packed channels-last with the channels zero-padded to 8, so one
+// 16-byte chunk is one filter position's 8 channels, and a BK = 32 stage covers four consecutive filter positions
+// (K = KH*KW*8 rounded up to 32, the filter packed to match with zeros). Each B-load lane then follows its own
+// filter position, advancing by four per stage; positions past KH*KW load zeros like the padding does.
+//
 // Epilogue: bias is added to the fp32 accumulator, the sum is rounded once, the chain runs on the rounded
 // value (rounding after every segment), and the tile is written NCHW — 16-byte stores along the pixel axis
 // when Ho*Wo % 8 == 0, element stores otherwise.
@@ -43,7 +48,7 @@ struct ConvNhwcArgs {
   const void* w;     // [Cout][KH][KW][Cin]
   const void* bias;  // [Cout] or nullptr
   void* y;           // [N][Cout][Ho][Wo]
-  int32_t cin, h, w_in, cout, kw, sh, sw, ph, pw, wo, howo;
+  int32_t cin, h, w_in, cout, kh, kw, sh, sw, ph, pw, wo, howo;
   int32_t k;         // KH*KW*Cin
   int64_t p;         // N*Ho*Wo
   uint32_t x_bytes;
@@ -82,7 +87,7 @@ __device__ __forceinline__ float apply_epilogue_one(const EpilogueArgs& ep, floa
   return v;
 }
 
-template <typename T, int BM, int BN, int WAVES_M, int WAVES_N>
+template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, bool C8>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNhwcArgs args) {
   using S = uint16_t;
   constexpr int NW = WAVES_M * WAVES_N;
@@ -143,7 +148,23 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
     const int oh = rem / args.wo, ow = rem - (rem / args.wo) * args.wo;
     b_ih[j] = oh * args.sh - args.ph;
     b_iw[j] = ow * args.sw - args.pw;
-    b_org[j] = ((img * args.h + b_ih[j]) * args.w_in + b_iw[j]) * cin + chunk * 8;
+    b_org[j] = ((img * args.h + b_ih[j]) * args.w_in + b_iw[j]) * cin + (C8 ? 0 : chunk * 8);
+  }
+  // C8 mode: filter position (kh, kw) of this lane's chunk in each B load, for the next stage to load
+  // (stage s, chunk c -> position 4s + c); c8_live is false once the position is past KH*KW.
+  int32_t c8_kh[B_PER_WAVE], c8_kw[B_PER_WAVE];
+  if constexpr (C8) {
+#pragma unroll
+    for (int j = 0; j < B_PER_WAVE; ++j) {
+      const int row = (wave * B_PER_WAVE + j) * 16 + (lane >> 2);
+      const int c = (lane & 3) ^ a_swizzle(row);
+      c8_kh[j] = 0;
+      c8_kw[j] = c;
+      while (c8_kw[j] >= args.kw) {
+        c8_kw[j] -= args.kw;
+        ++c8_kh[j];
+      }
+    }
   }
   const __amdgpu_buffer_rsrc_t xr =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(args.x), static_cast<short>(0), static_cast<int>(args.x_bytes),
@@ -155,6 +176,17 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
   auto advance = [&]() {
     if (ld_next + 1 < KT) {
       ++ld_next;
+      if constexpr (C8) {
+#pragma unroll
+        for (int j = 0; j < B_PER_WAVE; ++j) {
+          c8_kw[j] += 4;
+          while (c8_kw[j] >= args.kw) {
+            c8_kw[j] -= args.kw;
+            ++c8_kh[j];
+          }
+        }
+        return;
+      }
       ld_ci += kBK;
       if (ld_ci == cin) {
         ld_ci = 0;
@@ -175,11 +207,13 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
       global_to_lds16(W + a_src[J] + k0, (FH_LDS void*)(st + (wave * A_PER_WAVE + J) * 1024));
     } else {
       constexpr int JB = J - A_PER_WAVE;
-      const int ih = b_ih[JB] + ld_kh, iw = b_iw[JB] + ld_kw;
+      const int kh_ = C8 ? c8_kh[JB] : ld_kh, kw_ = C8 ? c8_kw[JB] : ld_kw;
+      const int ih = b_ih[JB] + kh_, iw = b_iw[JB] + kw_;
       const bool inside = static_cast<unsigned>(ih) < static_cast<unsigned>(args.h) &&
-                          static_cast<unsigned>(iw) < static_cast<unsigned>(args.w_in);
+                          static_cast<unsigned>(iw) < static_cast<unsigned>(args.w_in) && (!C8 || kh_ < args.kh);
       // computed unconditionally so the padding case is a select, not a branch
-      const uint32_t at = static_cast<uint32_t>(b_org[JB] + ld_off) * 2u;
+      const int off = C8 ? (kh_ * args.w_in + kw_) * cin : ld_off;
+      const uint32_t at = static_cast<uint32_t>(b_org[JB] + off) * 2u;
       const uint32_t voff = inside ? at : 0x80000000u;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (FH_LDS void*)(st + A_BYTES + (wave * B_PER_WAVE + JB) * 1024), 16,
                                                static_cast<int>(voff), 0, 0, 0);
@@ -326,25 +360,26 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
   }
 }
 
-template <typename T, int BM, int BN, int WAVES_M, int WAVES_N>
+template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, bool C8>
 fh_status launch_conv(ConvNhwcArgs a, hipStream_t stream) {
   a.tiles_m = (a.cout + BM - 1) / BM;
   a.tiles_n = static_cast<int32_t>((a.p + BN - 1) / BN);
   const dim3 grid(static_cast<uint32_t>(a.tiles_m) * static_cast<uint32_t>(a.tiles_n));
-  hipLaunchKernelGGL((conv_nhwc_kernel<T, BM, BN, WAVES_M, WAVES_N>), grid, dim3(WAVES_M * WAVES_N * 64), 0, stream, a);
+  hipLaunchKernelGGL((conv_nhwc_kernel<T, BM, BN, WAVES_M, WAVES_N, C8>), grid, dim3(WAVES_M * WAVES_N * 64), 0, stream,
+                     a);
   return launch_status("conv_nhwc_kernel launch");
 }
 
 // Largest tile that still gives every CU a workgroup; otherwise the one with the most workgroups.
-template <typename T>
+template <typename T, bool C8>
 fh_status dispatch_conv(const ConvNhwcArgs& a, hipStream_t stream) {
   const int64_t cus = device_cu_count();
   auto tiles = [&](int64_t bm, int64_t bn) { return ((a.cout + bm - 1) / bm) * ((a.p + bn - 1) / bn); };
-  if (a.cout >= 128 && tiles(128, 256) >= cus) return launch_conv<T, 128, 256, 2, 4>(a, stream);
-  if (a.cout >= 128 && tiles(128, 128) >= cus) return launch_conv<T, 128, 128, 2, 4>(a, stream);
-  if (tiles(64, 256) >= cus) return launch_conv<T, 64, 256, 1, 4>(a, stream);
-  if (tiles(64, 128) >= cus) return launch_conv<T, 64, 128, 2, 2>(a, stream);
-  return launch_conv<T, 64, 64, 2, 2>(a, stream);
+  if (a.cout >= 128 && tiles(128, 256) >= cus) return launch_conv<T, 128, 256, 2, 4, C8>(a, stream);
+  if (a.cout >= 128 && tiles(128, 128) >= cus) return launch_conv<T, 128, 128, 2, 4, C8>(a, stream);
+  if (tiles(64, 256) >= cus) return launch_conv<T, 64, 256, 1, 4, C8>(a, stream);
+  if (tiles(64, 128) >= cus) return launch_conv<T, 64, 128, 2, 2, C8>(a, stream);
+  return launch_conv<T, 64, 64, 2, 2, C8>(a, stream);
 }
 
 // Batched transpose through a 64 x 64 LDS tile: y[b][c][r] = x[b][r][c]; reads and writes are coalesced.
@@ -370,12 +405,42 @@ __global__ __launch_bounds__(256) void transpose_batched_kernel(const E* __restr
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
+// K of a C8 filter: KH*KW positions of 8 channels, rounded up to whole stages.
+int64_t conv_c8_filter_k(int64_t kh, int64_t kw) { return (kh * kw * 8 + kBK - 1) / kBK * kBK; }
+
+// x [N][C][HW] (C <= 8) -> y [N][HW][8], channels C..7 zero. One thread per pixel, one 16-byte store.
+__global__ __launch_bounds__(256) void pack_input_c8_kernel(const uint16_t* __restrict__ x, uint4* __restrict__ y,
+                                                            int64_t n, int32_t c, int64_t hw) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n * hw; i += stride) {
+    const int64_t img = i / hw, pix = i - img * hw;
+    uint16_t v[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (int ch = 0; ch < c; ++ch) v[ch] = x[(img * c + ch) * hw + pix];
+    uint4 o;
+    __builtin_memcpy(&o, v, 16);
+    y[i] = o;
+  }
+}
+
+// w [Cout][C][KH*KW] (C <= 8) -> y [Cout][K] with y[co][pos*8 + ci] = w[co][ci][pos], zeros elsewhere.
+__global__ __launch_bounds__(256) void pack_filter_c8_kernel(const uint16_t* __restrict__ w, uint16_t* __restrict__ y,
+                                                             int32_t cout, int32_t c, int32_t khw, int32_t k) {
+  const int64_t total = static_cast<int64_t>(cout) * k;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < total; i += static_cast<int64_t>(gridDim.x) * 256) {
+    const int64_t co = i / k;
+    const int q = static_cast<int>(i - co * k), pos = q / 8, ci = q % 8;
+    y[i] = (pos < khw && ci < c) ? w[(co * c + ci) * khw + pos] : uint16_t{0};
+  }
+}
+
 // Geometry accepted by the channels-last MFMA path.
 bool nhwc_supported(int32_t dtype, const int64_t* g) {
   if (dtype != FH_BF16 && dtype != FH_F16) return false;
   const int64_t n = g[0], cin = g[1], h = g[2], w = g[3], cout = g[4], kh = g[5], kw = g[6], sh = g[7], sw = g[8],
                 ph = g[9], pw = g[10], groups = g[11];
-  if (groups != 1 || cin % kBK != 0 || n <= 0 || h <= 0 || w <= 0 || cout <= 0 || kh <= 0 || kw <= 0) return false;
+  // Cin % 32 == 0, or Cin == 8: the C8 layout (a conv with fewer channels is packed to 8 first)
+  if (groups != 1 || (cin % kBK != 0 && cin != 8) || n <= 0 || h <= 0 || w <= 0 || cout <= 0 || kh <= 0 || kw <= 0)
+    return false;
   if (sh <= 0 || sw <= 0 || ph < 0 || pw < 0 || h + 2 * ph < kh || w + 2 * pw < kw) return false;
   const int64_t oh = (h + 2 * ph - kh) / sh + 1, ow = (w + 2 * pw - kw) / sw + 1;
   // 32-bit offsets inside the kernel: input bytes, window origins and filter rows
@@ -436,6 +501,7 @@ extern "C" fh_status fh_conv2d_nhwc_fwd(int32_t dtype, const void* x_nhwc, const
   a.h = static_cast<int32_t>(geom[2]);
   a.w_in = static_cast<int32_t>(geom[3]);
   a.cout = static_cast<int32_t>(geom[4]);
+  a.kh = static_cast<int32_t>(geom[5]);
   a.kw = static_cast<int32_t>(geom[6]);
   a.sh = static_cast<int32_t>(geom[7]);
   a.sw = static_cast<int32_t>(geom[8]);
@@ -445,7 +511,8 @@ extern "C" fh_status fh_conv2d_nhwc_fwd(int32_t dtype, const void* x_nhwc, const
   const int64_t ow = (geom[3] + 2 * geom[10] - geom[6]) / geom[8] + 1;
   a.wo = static_cast<int32_t>(ow);
   a.howo = static_cast<int32_t>(oh * ow);
-  a.k = static_cast<int32_t>(geom[5] * geom[6] * geom[1]);
+  const bool c8 = geom[1] == 8;
+  a.k = static_cast<int32_t>(c8 ? conv_c8_filter_k(geom[5], geom[6]) : geom[5] * geom[6] * geom[1]);
   a.p = geom[0] * oh * ow;
   a.x_bytes = static_cast<uint32_t>(geom[0] * geom[2] * geom[3] * geom[1] * 2);
   if (epilogue != nullptr) {
@@ -468,5 +535,31 @@ extern "C" fh_status fh_conv2d_nhwc_fwd(int32_t dtype, const void* x_nhwc, const
   a.vec_store = vec ? 1 : 0;
   if (a.p == 0) return FH_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  return dtype == FH_BF16 ? dispatch_conv<bf16_t>(a, s) : dispatch_conv<f16_t>(a, s);
+  if (c8) return dtype == FH_BF16 ? dispatch_conv<bf16_t, true>(a, s) : dispatch_conv<f16_t, true>(a, s);
+  return dtype == FH_BF16 ? dispatch_conv<bf16_t, false>(a, s) : dispatch_conv<f16_t, false>(a, s);
+}
+
+extern "C" fh_status fh_conv_pack_input_c8(const void* x, void* y, int64_t n, int32_t c, int64_t hw, void* stream) {
+  if (n < 0 || hw < 0 || c < 1 || c > 8) return fail(FH_INVALID_ARGUMENT, "fh_conv_pack_input_c8: needs 1 <= C <= 8");
+  if (n * hw == 0) return FH_OK;
+  if (x == nullptr || y == nullptr || !aligned16(y)) return fail(FH_INVALID_ARGUMENT, "fh_conv_pack_input_c8: bad pointer");
+  int64_t blocks = (n * hw + 255) / 256;
+  blocks = blocks > 256LL * 16 ? 256LL * 16 : blocks;
+  hipLaunchKernelGGL(pack_input_c8_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x), static_cast<uint4*>(y), n, c, hw);
+  return launch_status("pack_input_c8_kernel launch");
+}
+
+extern "C" int64_t fh_conv_c8_filter_k(int64_t kh, int64_t kw) { return conv_c8_filter_k(kh, kw); }
+
+extern "C" fh_status fh_conv_pack_filter_c8(const void* w, void* y, int32_t cout, int32_t c, int32_t kh, int32_t kw,
+                                            void* stream) {
+  if (cout < 1 || c < 1 || c > 8 || kh < 1 || kw < 1) return fail(FH_INVALID_ARGUMENT, "fh_conv_pack_filter_c8: bad shape");
+  if (w == nullptr || y == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_conv_pack_filter_c8: null pointer");
+  const int32_t k = static_cast<int32_t>(conv_c8_filter_k(kh, kw));
+  const int64_t total = static_cast<int64_t>(cout) * k;
+  hipLaunchKernelGGL(pack_filter_c8_kernel, dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(w), static_cast<uint16_t*>(y), cout, c,
+                     kh * kw, k);
+  return launch_status("pack_filter_c8_kernel launch");
 }

@@ -117,6 +117,9 @@ inline constexpr std::string_view kConvEpilogueOp = "hip_conv2d_epilogue_interna
 inline constexpr std::string_view kChannelsLastOp = "hip_channels_last_internal";
 // conv2d (optionally with an epilogue program) on channels-last operands; output NCHW.
 inline constexpr std::string_view kConvNhwcOp = "hip_conv2d_nhwc_internal";
+// Cin <= 8: x [N,C,H,W] -> [N,H,W,8] zero-padded; w [Cout,C,KH,KW] -> [Cout, K8] (see fh_conv_pack_*_c8).
+inline constexpr std::string_view kPackInputC8Op = "hip_pack_input_c8_internal";
+inline constexpr std::string_view kPackFilterC8Op = "hip_pack_filter_c8_internal";
 
 // Elementwise op name -> fh_ew_op code (0 when the op has no device code).
 uint8_t ew_code(std::string_view op);

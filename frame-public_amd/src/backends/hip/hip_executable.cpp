@@ -146,18 +146,40 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
         const int64_t geom[12] = {xt.shape.dim(0), xt.shape.dim(1), xt.shape.dim(2), xt.shape.dim(3),
                                   wt.shape.dim(0), wt.shape.dim(2), wt.shape.dim(3), (*stride)[0],
                                   (*stride)[1],    (*pad)[0],       (*pad)[1],       *groups};
-        if (wt.shape.dim(1) == xt.shape.dim(1) && fh_conv2d_nhwc_supported(dt, geom) == 1) {
-          Result<ir::Value*> x_cl = channels_last(ins[0]);
-          if (!x_cl.is_ok()) return x_cl.status();
-          Result<ir::Value*> w_cl = channels_last(ins[1]);
-          if (!w_cl.is_ok()) return w_cl.status();
+        // Cin <= 8 goes through the C8 layout (channels padded to 8, four filter positions per k-stage)
+        const bool c8 = xt.shape.dim(1) <= 8 && *groups == 1;
+        int64_t geom_k[12];
+        std::copy(geom, geom + 12, geom_k);
+        if (c8) geom_k[1] = 8;
+        if (wt.shape.dim(1) == xt.shape.dim(1) && fh_conv2d_nhwc_supported(dt, geom_k) == 1) {
+          ir::Value* x_cl = nullptr;
+          ir::Value* w_cl = nullptr;
+          if (c8) {
+            ir::TensorType tx = ins[0]->type(), tw = ins[1]->type();
+            tx.shape = Shape({geom[0], geom[2], geom[3], 8});
+            tw.shape = Shape({geom[4], fh_conv_c8_filter_k(geom[5], geom[6])});
+            Result<ir::Node*> px = out.create_node(std::string(kPackInputC8Op), {ins[0]}, {tx});
+            if (!px.is_ok()) return px.status();
+            Result<ir::Node*> pw = out.create_node(std::string(kPackFilterC8Op), {ins[1]}, {tw});
+            if (!pw.is_ok()) return pw.status();
+            x_cl = px.value()->output(0);
+            w_cl = pw.value()->output(0);
+          } else {
+            Result<ir::Value*> xv = channels_last(ins[0]);
+            if (!xv.is_ok()) return xv.status();
+            Result<ir::Value*> wv = channels_last(ins[1]);
+            if (!wv.is_ok()) return wv.status();
+            x_cl = xv.value();
+            w_cl = wv.value();
+          }
           std::vector<ir::Value*> conv_ins = ins;
-          conv_ins[0] = x_cl.value();
-          conv_ins[1] = w_cl.value();
+          conv_ins[0] = x_cl;
+          conv_ins[1] = w_cl;
           Result<ir::Node*> c = out.create_node(std::string(kConvNhwcOp), std::move(conv_ins), {n->outputs()[0].type()});
           if (!c.is_ok()) return c.status();
           for (const auto& [k, v] : n->attrs()) c.value()->set_attr(k, v);
           if (n->op() == "conv2d") c.value()->set_attr("n_main_inputs", ir::AttrValue{static_cast<int64_t>(ins.size())});
+          c.value()->set_attr("filter_hw", ir::AttrValue{std::vector<int64_t>{geom[5], geom[6]}});
           map[&n->outputs()[0]] = c.value()->output(0);
           lowered = true;
         }

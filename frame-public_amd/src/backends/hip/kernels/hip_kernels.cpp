@@ -204,15 +204,23 @@ Status conv_nhwc_kernel(KernelContext& ctx) {
   const auto* groups = attr<int64_t>(ctx, "groups");
   if (stride == nullptr || pad == nullptr || groups == nullptr || stride->size() != 2 || pad->size() != 2)
     return invalid(op, "missing or malformed stride/padding/groups attributes");
-  if (x.shape().rank() != 4 || w.shape().rank() != 4 || y.shape().rank() != 4) return invalid(op, "operands must be rank-4");
+  if (x.shape().rank() != 4 || (w.shape().rank() != 4 && w.shape().rank() != 2) || y.shape().rank() != 4)
+    return invalid(op, "x and y must be rank-4, the filter rank-4 or rank-2 (C8)");
   for (size_t i = 0; i < n_main; ++i)
     if (!(ctx.inputs[i].dtype() == y.dtype())) return invalid(op, "operand dtypes differ");
   Result<int32_t> dt = float_code(op, y.dtype());
   if (!dt.is_ok()) return dt.status();
+  // filter [Cout,KH,KW,Cin], or the C8 layout [Cout, K8] (Cin == 8) with KH, KW in the filter_hw attribute
+  const auto* fhw = attr<std::vector<int64_t>>(ctx, "filter_hw");
+  const bool c8 = w.shape().rank() == 2;
+  if (c8 && (fhw == nullptr || fhw->size() != 2 || x.shape().dim(3) != 8))
+    return invalid(op, "C8 filter needs filter_hw and an input with 8 channels");
+  const int64_t kh = c8 ? (*fhw)[0] : w.shape().dim(1), kw = c8 ? (*fhw)[1] : w.shape().dim(2);
   const int64_t geom[12] = {x.shape().dim(0), x.shape().dim(3), x.shape().dim(1), x.shape().dim(2),
-                            w.shape().dim(0), w.shape().dim(1), w.shape().dim(2), (*stride)[0],
+                            w.shape().dim(0), kh,               kw,               (*stride)[0],
                             (*stride)[1],     (*pad)[0],        (*pad)[1],        *groups};
-  if (w.shape().dim(3) != geom[1]) return invalid(op, "filter channels do not match the input's");
+  if (c8 ? w.shape().dim(1) != fh_conv_c8_filter_k(kh, kw) : w.shape().dim(3) != geom[1])
+    return invalid(op, "filter shape does not match the input's channels");
   const int64_t oh = (geom[2] + 2 * geom[9] - geom[5]) / geom[7] + 1;
   const int64_t ow = (geom[3] + 2 * geom[10] - geom[6]) / geom[8] + 1;
   if (y.shape() != Shape({geom[0], geom[4], oh, ow})) return invalid(op, "output shape " + y.shape().to_string() + " does not match the geometry");
@@ -237,6 +245,37 @@ Status channels_last_kernel(KernelContext& ctx) {
   if (y.shape() != Shape({s.dim(0), s.dim(2), s.dim(3), s.dim(1)})) return invalid(op, "output shape does not match [d0,d2,d3,d1]");
   FRAME_HIP_RETURN_IF_ERROR(fh_transpose_batched(static_cast<int32_t>(x.dtype().itemsize()), x.raw_data(), y.raw_data(),
                                                  s.dim(0), s.dim(1), s.dim(2) * s.dim(3), stream_handle(ctx)),
+                            "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
+// x [N,C,H,W] (C <= 8) -> [N,H,W,8]
+Status pack_input_c8_kernel(KernelContext& ctx) {
+  const std::string op(kPackInputC8Op);
+  FRAME_RETURN_IF_ERROR(arity(ctx, op, 1, 1));
+  const Tensor& x = ctx.inputs[0];
+  Tensor& y = ctx.outputs[0];
+  const Shape& s = x.shape();
+  if (s.rank() != 4 || x.dtype().itemsize() != 2 || y.shape() != Shape({s.dim(0), s.dim(2), s.dim(3), 8}))
+    return invalid(op, "expects a 16-bit [N,C,H,W] input and a [N,H,W,8] output");
+  FRAME_HIP_RETURN_IF_ERROR(fh_conv_pack_input_c8(x.raw_data(), y.raw_data(), s.dim(0), static_cast<int32_t>(s.dim(1)),
+                                                  s.dim(2) * s.dim(3), stream_handle(ctx)),
+                            "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
+// w [Cout,C,KH,KW] (C <= 8) -> [Cout, K8]
+Status pack_filter_c8_kernel(KernelContext& ctx) {
+  const std::string op(kPackFilterC8Op);
+  FRAME_RETURN_IF_ERROR(arity(ctx, op, 1, 1));
+  const Tensor& w = ctx.inputs[0];
+  Tensor& y = ctx.outputs[0];
+  const Shape& s = w.shape();
+  if (s.rank() != 4 || w.dtype().itemsize() != 2 || y.shape() != Shape({s.dim(0), fh_conv_c8_filter_k(s.dim(2), s.dim(3))}))
+    return invalid(op, "expects a 16-bit [Cout,C,KH,KW] filter and a [Cout,K8] output");
+  FRAME_HIP_RETURN_IF_ERROR(fh_conv_pack_filter_c8(w.raw_data(), y.raw_data(), static_cast<int32_t>(s.dim(0)),
+                                                   static_cast<int32_t>(s.dim(1)), static_cast<int32_t>(s.dim(2)),
+                                                   static_cast<int32_t>(s.dim(3)), stream_handle(ctx)),
                             "op '" + op + "' (hip)");
   return Status::ok();
 }
@@ -426,6 +465,8 @@ FRAME_REGISTER_KERNEL("conv2d", kHipBackendName, &conv2d_kernel);
 FRAME_REGISTER_KERNEL(kConvEpilogueOp, kHipBackendName, &conv_epilogue_kernel);
 FRAME_REGISTER_KERNEL(kConvNhwcOp, kHipBackendName, &conv_nhwc_kernel);
 FRAME_REGISTER_KERNEL(kChannelsLastOp, kHipBackendName, &channels_last_kernel);
+FRAME_REGISTER_KERNEL(kPackInputC8Op, kHipBackendName, &pack_input_c8_kernel);
+FRAME_REGISTER_KERNEL(kPackFilterC8Op, kHipBackendName, &pack_filter_c8_kernel);
 FRAME_REGISTER_KERNEL("softmax", kHipBackendName, &softmax_kernel);
 FRAME_REGISTER_KERNEL("layer_norm", kHipBackendName, &layer_norm_kernel);
 FRAME_REGISTER_KERNEL("max_pool2d", kHipBackendName, &pool_kernel<0>);

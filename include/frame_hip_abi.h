@@ -134,9 +134,20 @@ fh_status fh_conv2d_fwd(int32_t dtype, const void* x, const void* w, const void*
 fh_status fh_conv2d_nhwc_fwd(int32_t dtype, const void* x_nhwc, const void* w_khwc, const void* bias, void* y,
                              const int64_t geom[12], const fh_epilogue* epilogue, void* stream);
 
-/* 1 if fh_conv2d_nhwc_fwd accepts dtype and geom (bf16/f16, groups 1, Cin % 32 == 0, 32-bit offsets), else 0.
- * Host-only query used at graph compile time; no counterpart in the reference. */
+/* 1 if fh_conv2d_nhwc_fwd accepts dtype and geom (bf16/f16, groups 1, Cin % 32 == 0 or Cin == 8, 32-bit
+ * offsets), else 0. Host-only query used at graph compile time; no counterpart in the reference.
+ * With Cin == 8 the operands are in the C8 layout: x from fh_conv_pack_input_c8 and w from
+ * fh_conv_pack_filter_c8 ([Cout][fh_conv_c8_filter_k(KH, KW)]). */
 int32_t fh_conv2d_nhwc_supported(int32_t dtype, const int64_t geom[12]);
+
+/* C8 layout for convolutions with Cin <= 8 (e.g. an RGB stem): x NCHW [N][C][H*W] (16-bit) ->
+ * [N][H*W][8] with channels C..7 zero. No counterpart in the reference (cuDNN consumes NCHW). */
+fh_status fh_conv_pack_input_c8(const void* x, void* y, int64_t n, int32_t c, int64_t hw, void* stream);
+
+/* C8 filter: w [Cout][C][KH][KW] (16-bit, C <= 8) -> [Cout][K] with element (kh*KW + kw)*8 + ci, zeros for
+ * ci >= C and past KH*KW*8; K = fh_conv_c8_filter_k(KH, KW) = KH*KW*8 rounded up to 32. */
+fh_status fh_conv_pack_filter_c8(const void* w, void* y, int32_t cout, int32_t c, int32_t kh, int32_t kw, void* stream);
+int64_t fh_conv_c8_filter_k(int64_t kh, int64_t kw);
 
 /* Batched transpose y[b][c][r] = x[b][r][c] (b < batch, r < rows, c < cols), itemsize 2 or 4.
  * Lays out the channels-last conv operands: x NCHW -> NHWC is (batch N, rows Cin, cols H*W); w

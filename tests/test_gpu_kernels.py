@@ -382,3 +382,45 @@ def test_conv2d_nhwc_rejects_unsupported(hip):
         assert hip.lib().fh_conv2d_nhwc_supported(dtype, hip.i64_array(geom)) == 0
         status = hip.lib().fh_conv2d_nhwc_fwd(dtype, None, None, None, None, hip.i64_array(geom), None, None)
         assert status == 4, status  # FH_UNIMPLEMENTED
+
+
+C8_CASES = [
+    # N, Cin, H, W, Cout, KH, KW, sh, sw, ph, pw, groups, bias — Cin <= 8 through the C8 layout
+    ((2, 3, 32, 32, 64, 7, 7, 2, 2, 3, 3, 1), True),   # ResNet stem geometry at 32 px
+    ((1, 3, 15, 17, 40, 3, 3, 1, 1, 1, 1, 1), True),   # Ho*Wo not a multiple of 8, Cout ragged
+    ((2, 8, 9, 9, 64, 5, 5, 1, 1, 2, 2, 1), False),    # Cin exactly 8
+    ((1, 1, 12, 12, 64, 2, 2, 2, 2, 0, 0, 1), True),   # KW < 4: several filter rows per stage
+]
+
+
+@pytest.mark.parametrize("dtype", [BF16, F16])
+@pytest.mark.parametrize("geom,with_bias", C8_CASES)
+def test_conv2d_c8(hip, dtype, geom, with_bias):
+    say(f"conv c8 dtype={dtype} {geom} bias={with_bias}")
+    n, cin, h, w, cout, kh, kw = geom[:7]
+    g8 = list(geom)
+    g8[1] = 8
+    assert hip.lib().fh_conv2d_nhwc_supported(dtype, hip.i64_array(g8)) == 1
+    x = synth.tensor(131, (n, cin, h, w), dtype, "normal")
+    wt = synth.tensor(132, (cout, cin, kh, kw), dtype, "normal", (2.0 / (cin * kh * kw)) ** 0.5)
+    bias = synth.tensor(133, (cout,), dtype, "normal", 0.1) if with_bias else None
+    want = orc.conv2d(dtype, x, wt, bias, geom)
+    k8 = hip.lib().fh_conv_c8_filter_k(kh, kw)
+    dx, dw = dev(hip, x), dev(hip, wt)
+    xp, wp = hip.DeviceBuffer(n * h * w * 8 * 2), hip.DeviceBuffer(cout * k8 * 2)
+    hip.check(hip.lib().fh_conv_pack_input_c8(dx.value, xp.value, n, cin, h * w, None))
+    hip.check(hip.lib().fh_conv_pack_filter_c8(dw.value, wp.value, cout, cin, kh, kw, None))
+    # the packed layouts themselves, bit for bit
+    xh = xp.download((n, h * w, 8), np.uint16)
+    assert_bitwise(xh[:, :, :cin], np.ascontiguousarray(x.reshape(n, cin, h * w).transpose(0, 2, 1)), "packed input")
+    assert not xh[:, :, cin:].any()
+    wh = wp.download((cout, k8), np.uint16)
+    ref_w = np.zeros((cout, k8), np.uint16)
+    ref_w[:, :kh * kw * 8].reshape(cout, kh * kw, 8)[:, :, :cin] = wt.reshape(cout, cin, kh * kw).transpose(0, 2, 1)
+    assert_bitwise(wh, ref_w, "packed filter")
+    db = dev(hip, bias) if with_bias else None
+    dy = hip.DeviceBuffer(want.nbytes)
+    hip.check(hip.lib().fh_conv2d_nhwc_fwd(dtype, xp.value, wp.value, db.value if db else None, dy.value,
+                                           hip.i64_array(g8), None, None))
+    got = dy.download(want.shape, want.dtype)
+    assert_close(got, want, dtype, what=f"conv c8 {geom}")
