@@ -76,6 +76,9 @@ _SIGS = {
     "fh_conv_c8_filter_k": (c_int64, [c_int64, c_int64]),
     "fh_ew_program": (c_int32, [c_int32, c_int32, POINTER(c_uint8), POINTER(c_int8), POINTER(c_void_p), c_int32,
                                 c_void_p, c_int64, c_int32, c_void_p]),
+    "fh_attention_fwd": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
+                                   c_float, c_void_p]),
+    "fh_attention_supported": (c_int32, [c_int32, c_int64, c_int64]),
     "fh_softmax_rows": (c_int32, [c_int32, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "fh_layer_norm_rows": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_float,
                                      c_void_p]),

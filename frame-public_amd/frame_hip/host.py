@@ -61,6 +61,7 @@ _SIGS = {
     "frame_transform_text": (c_int32, [c_char_p, c_char_p, c_void_p, c_int64, POINTER(c_int64)]),
     "frame_roundtrip_text": (c_int32, [c_char_p, c_void_p, c_int64, POINTER(c_int64)]),
     "frame_memory_plan_text": (c_int32, [c_char_p, c_void_p, c_int64, POINTER(c_int64)]),
+    "frame_hip_lowered_text": (c_int32, [c_char_p, c_int32, c_void_p, c_int64, POINTER(c_int64)]),
     "frame_launch": (c_int32, [c_char_p, c_char_p, POINTER(c_void_p), c_int32, POINTER(c_void_p), c_int32, c_void_p]),
 }
 
@@ -113,6 +114,11 @@ def device_count(backend: str = "hip") -> int:
 
 def transform(ir_text: str, pass_name: str = "") -> str:
     return _text(lib().frame_transform_text, ir_text.encode(), pass_name.encode())
+
+
+def hip_lowered(ir_text: str, opt_level: int = 1) -> str:
+    """The graph the hip backend plans: standard pipeline, then HipBackend::compile's lowering (host only)."""
+    return _text(lib().frame_hip_lowered_text, ir_text.encode(), opt_level)
 
 
 def roundtrip(ir_text: str) -> str:

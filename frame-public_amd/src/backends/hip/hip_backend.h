@@ -19,6 +19,7 @@
 #include <frame/hal/event.h>
 #include <frame/hal/executable.h>
 #include <frame/hal/stream.h>
+#include <frame/ir/graph.h>
 #include <frame/ops/kernel_registry.h>
 
 #include "frame_hip_abi.h"
@@ -120,6 +121,14 @@ inline constexpr std::string_view kConvNhwcOp = "hip_conv2d_nhwc_internal";
 // Cin <= 8: x [N,C,H,W] -> [N,H,W,8] zero-padded; w [Cout,C,KH,KW] -> [Cout, K8] (see fh_conv_pack_*_c8).
 inline constexpr std::string_view kPackInputC8Op = "hip_pack_input_c8_internal";
 inline constexpr std::string_view kPackFilterC8Op = "hip_pack_filter_c8_internal";
+// attention(q, k, v) [batch*seq, heads*dh] -> [batch*seq, heads*dh]: the per-(batch, head) slice / matmul / mul /
+// softmax / matmul / concat decomposition in one kernel (attrs batch, seq, heads, dh, scale; see fh_attention_fwd).
+inline constexpr std::string_view kAttentionOp = "hip_attention_internal";
+
+// The graph HipBackend::compile plans for `graph` (already through the pass pipeline): attention, epilogue
+// (opt_level >= 1) and channels-last conv lowering applied to a copy. Host-only; used by compile and by
+// frame_hip_lowered_text.
+Result<ir::Graph> lower_for_hip(const ir::Graph& graph, int32_t opt_level);
 
 // Elementwise op name -> fh_ew_op code (0 when the op has no device code).
 uint8_t ew_code(std::string_view op);

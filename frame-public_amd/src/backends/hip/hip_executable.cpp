@@ -7,6 +7,8 @@
 //  * constants are materialised on the device once, at compile time.
 //
 // Lowering (allowed inside Backend::compile by the HAL contract, include/frame/hal/backend.h:45-63):
+//  * attention (every opt_level): the per-(batch, head) decomposition of multi-head attention becomes one
+// attention node (see lower_attention);
 //  * epilogue fusion (opt_level >= 1): a matmul
 // or conv2d whose only consumer is an elementwise node (add, mul, relu, square, gelu or a fused chain) that
 // takes the contraction result as its first operand is replaced by one internal node that applies the
@@ -18,7 +20,9 @@
 #include <algorithm>
 #include <cstring>
 #include <mutex>
+#include <optional>
 #include <string>
+#include <string_view>
 #include <unordered_map>
 #include <unordered_set>
 #include <utility>
@@ -197,6 +201,214 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
   return out;
 }
 
+// ---- attention ---------------------------------------------------------------------------------------------
+
+template <typename T>
+const T* attr_of(const ir::Node* n, const char* key) {
+  auto it = n->attrs().find(key);
+  return it == n->attrs().end() ? nullptr : std::get_if<T>(&it->second);
+}
+
+const ir::Node* producer_op(const ir::Value* v, std::string_view op, size_t n_inputs) {
+  const ir::Node* p = v->producer();
+  return p != nullptr && p->op() == op && p->inputs().size() == n_inputs && p->outputs().size() == 1 ? p : nullptr;
+}
+
+// x when v = slice(x) {axis, start, stop} with exactly these attributes, else nullptr.
+const ir::Node* slice_of(const ir::Value* v, int64_t axis, int64_t start, int64_t stop) {
+  const ir::Node* s = producer_op(v, "slice", 1);
+  if (s == nullptr) return nullptr;
+  const int64_t* a = attr_of<int64_t>(s, "axis");
+  const int64_t* b = attr_of<int64_t>(s, "start");
+  const int64_t* e = attr_of<int64_t>(s, "stop");
+  return a && b && e && *a == axis && *b == start && *e == stop ? s : nullptr;
+}
+
+// Value of a constant node whose payload is one repeated number, narrowed to `dtype` the way
+// fill_tensor_from_constant_attrs narrows it (double -> float -> dtype, round to nearest even).
+std::optional<float> splat_value(const ir::Node* c, DType dtype) {
+  if (c == nullptr || c->op() != ops::kConstantOpName || !c->inputs().empty()) return std::nullopt;
+  const auto* vals = attr_of<std::vector<double>>(c, "value");
+  if (vals == nullptr || vals->empty()) return std::nullopt;
+  for (double x : *vals)
+    if (!(x == vals->front())) return std::nullopt;
+  const float f = static_cast<float>(vals->front());
+  if (dtype.code() == DTypeCode::kBFloat16) return bfloat16_to_float(float_to_bfloat16(f));
+  if (dtype.code() == DTypeCode::kFloat16) return float16_to_float(float_to_float16(f));
+  return std::nullopt;
+}
+
+struct AttentionMatch {
+  ir::Value* q = nullptr;
+  ir::Value* k = nullptr;
+  ir::Value* v = nullptr;
+  int64_t batch = 0, seq = 0, heads = 0, dh = 0;
+  float scale = 0.0f;
+  std::vector<const ir::Node*> absorbed;  // every node of the decomposition, the batch concat included
+};
+
+// Matches the decomposition the reference's MultiHeadAttention emits (reference: src/nn/layers.cpp:1014-1080),
+// rooted at the batch concat `root`:
+//   root = concat_axis0_b( concat_axis1_h( matmul(softmax(mul(matmul(Qbh, transpose(Kbh, [1,0])), C)), Vbh) ) )
+//   Xbh  = slice_axis1[h*dh, (h+1)*dh)( slice_axis0[b*seq, (b+1)*seq)(X) )   for X in Q, K, V
+// with C a constant splat (either mul operand) and Q, K, V of shape [batch*seq, heads*dh].
+std::optional<AttentionMatch> match_attention(const ir::Node* root) {
+  if (root->op() != "concat" || root->outputs().size() != 1 || root->inputs().empty()) return std::nullopt;
+  const int64_t* axis0 = attr_of<int64_t>(root, "axis");
+  const ir::TensorType& ot = root->outputs()[0].type();
+  if (axis0 == nullptr || *axis0 != 0 || ot.shape.rank() != 2) return std::nullopt;
+  const int32_t dt = ot.dtype.code() == DTypeCode::kBFloat16 ? FH_BF16 : ot.dtype.code() == DTypeCode::kFloat16 ? FH_F16 : -1;
+  if (dt < 0) return std::nullopt;
+  AttentionMatch m;
+  m.batch = static_cast<int64_t>(root->inputs().size());
+  const ir::Node* c1 = root->inputs()[0]->producer();
+  if (c1 == nullptr || c1->op() != "concat" || c1->inputs().empty()) return std::nullopt;
+  m.heads = static_cast<int64_t>(c1->inputs().size());
+  const Shape& head_shape = c1->inputs()[0]->type().shape;
+  if (head_shape.rank() != 2) return std::nullopt;
+  m.seq = head_shape.dim(0);
+  m.dh = head_shape.dim(1);
+  if (ot.shape != Shape({m.batch * m.seq, m.heads * m.dh}) || fh_attention_supported(dt, m.seq, m.dh) != 1)
+    return std::nullopt;
+  std::optional<float> scale;
+  m.absorbed.push_back(root);
+  for (int64_t b = 0; b < m.batch; ++b) {
+    const ir::Value* ob = root->inputs()[static_cast<size_t>(b)];
+    const ir::Node* cb = producer_op(ob, "concat", static_cast<size_t>(m.heads));
+    if (cb == nullptr || attr_of<int64_t>(cb, "axis") == nullptr || *attr_of<int64_t>(cb, "axis") != 1) return std::nullopt;
+    m.absorbed.push_back(cb);
+    const int64_t r0 = b * m.seq, r1 = r0 + m.seq;
+    // the row slices of Q, K, V for this batch (shared by its heads)
+    const ir::Node* rows[3] = {nullptr, nullptr, nullptr};
+    for (int64_t h = 0; h < m.heads; ++h) {
+      const int64_t c0 = h * m.dh, c1h = c0 + m.dh;
+      const ir::Node* pv = producer_op(cb->inputs()[static_cast<size_t>(h)], "matmul", 2);
+      if (pv == nullptr) return std::nullopt;
+      const ir::Node* sm = producer_op(pv->inputs()[0], "softmax", 1);
+      if (sm == nullptr) return std::nullopt;
+      const ir::Node* mul = producer_op(sm->inputs()[0], "mul", 2);
+      if (mul == nullptr) return std::nullopt;
+      const ir::Value* s = mul->inputs()[0];
+      std::optional<float> sc = splat_value(mul->inputs()[1]->producer(), ot.dtype);
+      if (!sc) {
+        s = mul->inputs()[1];
+        sc = splat_value(mul->inputs()[0]->producer(), ot.dtype);
+      }
+      if (!sc || (scale && *scale != *sc)) return std::nullopt;
+      scale = sc;
+      const ir::Node* qk = producer_op(s, "matmul", 2);
+      if (qk == nullptr) return std::nullopt;
+      const ir::Node* kt = producer_op(qk->inputs()[1], "transpose", 1);
+      const auto* perm = kt ? attr_of<std::vector<int64_t>>(kt, "perm") : nullptr;
+      if (perm == nullptr || *perm != std::vector<int64_t>{1, 0}) return std::nullopt;
+      const ir::Value* heads_in[3] = {qk->inputs()[0], kt->inputs()[0], pv->inputs()[1]};
+      for (int i = 0; i < 3; ++i) {
+        const ir::Node* col = slice_of(heads_in[i], 1, c0, c1h);
+        if (col == nullptr) return std::nullopt;
+        const ir::Node* row = slice_of(col->inputs()[0], 0, r0, r1);
+        if (row == nullptr || (rows[i] != nullptr && rows[i] != row)) return std::nullopt;
+        ir::Value* x = row->inputs()[0];
+        ir::Value*& want = i == 0 ? m.q : i == 1 ? m.k : m.v;
+        if (want != nullptr && want != x) return std::nullopt;
+        want = x;
+        if (rows[i] == nullptr) m.absorbed.push_back(row);
+        rows[i] = row;
+        m.absorbed.push_back(col);
+      }
+      m.absorbed.insert(m.absorbed.end(), {pv, sm, mul, qk, kt});
+    }
+  }
+  for (const ir::Value* x : {m.q, m.k, m.v})
+    if (x->type().shape != ot.shape || !(x->type().dtype == ot.dtype)) return std::nullopt;
+  m.scale = *scale;
+  return m;
+}
+
+// Replaces every matched attention decomposition by one kAttentionOp node. Nodes of a decomposition whose
+// results are also used outside it (or are graph outputs) keep the decomposition as it is. The graph is rebuilt in
+// topological order without the nodes the rewrite leaves unused (the shared scale constant among them).
+Status lower_attention(ir::Graph& g) {
+  std::unordered_map<const ir::Value*, std::vector<const ir::Node*>> users;
+  for (const ir::Node* n : g.topological_order())
+    for (const ir::Value* v : n->inputs()) users[v].push_back(n);
+  std::unordered_set<const ir::Value*> graph_outputs(g.outputs().begin(), g.outputs().end());
+
+  std::unordered_map<const ir::Node*, AttentionMatch> roots;
+  std::unordered_set<const ir::Node*> absorbed;
+  for (const ir::Node* n : g.topological_order()) {
+    std::optional<AttentionMatch> m = match_attention(n);
+    if (!m) continue;
+    const std::unordered_set<const ir::Node*> mine(m->absorbed.begin(), m->absorbed.end());
+    bool closed = true;
+    for (const ir::Node* a : m->absorbed) {
+      if (absorbed.count(a)) closed = false;
+      if (a == n) continue;
+      for (const ir::Value& o : a->outputs()) {
+        if (graph_outputs.count(&o)) closed = false;
+        for (const ir::Node* u : users[&o])
+          if (!mine.count(u)) closed = false;
+      }
+    }
+    if (!closed) continue;
+    absorbed.insert(m->absorbed.begin(), m->absorbed.end());
+    roots.emplace(n, std::move(*m));
+  }
+  if (roots.empty()) return Status::ok();
+
+  // Liveness after the rewrite: a matched root reads q, k, v instead of its own inputs.
+  const std::vector<ir::Node*> order = g.topological_order();
+  std::unordered_set<const ir::Node*> live;
+  for (const ir::Value* o : g.outputs())
+    if (o->producer()) live.insert(o->producer());
+  for (auto it = order.rbegin(); it != order.rend(); ++it) {
+    const ir::Node* n = *it;
+    if (!live.count(n)) continue;
+    if (auto r = roots.find(n); r != roots.end()) {
+      for (const ir::Value* x : {r->second.q, r->second.k, r->second.v})
+        if (x->producer()) live.insert(x->producer());
+      continue;
+    }
+    for (const ir::Value* x : n->inputs())
+      if (x->producer()) live.insert(x->producer());
+  }
+
+  std::unordered_map<const ir::Value*, ir::Value*> map;
+  ir::Graph out{std::string(g.name())};
+  for (const ir::Node* n : order) {
+    if (n->op() == ir::kGraphInputOp) {
+      Result<ir::Value*> v = out.add_graph_input(n->outputs()[0].type());
+      if (!v.is_ok()) return v.status();
+      map[&n->outputs()[0]] = v.value();
+      continue;
+    }
+    if (!live.count(n)) continue;
+    if (auto r = roots.find(n); r != roots.end()) {
+      const AttentionMatch& m = r->second;
+      Result<ir::Node*> a = out.create_node(std::string(kAttentionOp), {map.at(m.q), map.at(m.k), map.at(m.v)},
+                                            {n->outputs()[0].type()});
+      if (!a.is_ok()) return a.status();
+      a.value()->set_attr("batch", ir::AttrValue{m.batch});
+      a.value()->set_attr("seq", ir::AttrValue{m.seq});
+      a.value()->set_attr("heads", ir::AttrValue{m.heads});
+      a.value()->set_attr("dh", ir::AttrValue{m.dh});
+      a.value()->set_attr("scale", ir::AttrValue{static_cast<double>(m.scale)});
+      map[&n->outputs()[0]] = a.value()->output(0);
+      continue;
+    }
+    std::vector<ir::Value*> ins;
+    for (const ir::Value* in : n->inputs()) ins.push_back(map.at(in));
+    std::vector<ir::TensorType> types;
+    for (const ir::Value& o : n->outputs()) types.push_back(o.type());
+    Result<ir::Node*> c = out.create_node(std::string(n->op()), std::move(ins), std::move(types));
+    if (!c.is_ok()) return c.status();
+    for (const auto& [k, v] : n->attrs()) c.value()->set_attr(k, v);
+    for (size_t i = 0; i < n->outputs().size(); ++i) map[&n->outputs()[i]] = c.value()->output(static_cast<int32_t>(i));
+  }
+  for (const ir::Value* o : g.outputs()) FRAME_RETURN_IF_ERROR(out.mark_output(map.at(o)));
+  g = std::move(out);
+  return Status::ok();
+}
+
 class HipExecutable final : public hal::Executable {
  public:
   HipExecutable(ops::ExecutablePlan plan, HipAllocator& alloc, Device device, hal::CompileOptions options)
@@ -323,13 +535,19 @@ class HipExecutable final : public hal::Executable {
 
 }  // namespace
 
-Result<std::unique_ptr<hal::Executable>> compile_hip_executable(const ir::Graph& graph, const hal::CompileOptions& options,
-                                                                 HipAllocator& allocator, Device device) {
+Result<ir::Graph> lower_for_hip(const ir::Graph& graph, int32_t opt_level) {
   Result<ir::Graph> work = ir::clone_graph(graph);
   if (!work.is_ok()) return work.status();
-  if (options.opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_epilogues(work.value()));
+  // Attention runs at every level (like the conv lowering), before the epilogue fusion would claim its matmuls.
+  FRAME_RETURN_IF_ERROR(lower_attention(work.value()));
+  if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_epilogues(work.value()));
   // Channels-last conv lowering runs at every level, so the conv numerics do not depend on the level.
-  Result<ir::Graph> lowered = lower_convs(work.value());
+  return lower_convs(work.value());
+}
+
+Result<std::unique_ptr<hal::Executable>> compile_hip_executable(const ir::Graph& graph, const hal::CompileOptions& options,
+                                                                 HipAllocator& allocator, Device device) {
+  Result<ir::Graph> lowered = lower_for_hip(graph, options.opt_level);
   if (!lowered.is_ok()) return lowered.status();
   Result<ops::ExecutablePlan> plan = ops::build_executable_plan(lowered.value(), kHipBackendName);
   if (!plan.is_ok()) return plan.status();

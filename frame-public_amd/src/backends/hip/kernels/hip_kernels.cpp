@@ -305,6 +305,31 @@ Status softmax_kernel(KernelContext& ctx) {
   return Status::ok();
 }
 
+// Fused attention produced by HipBackend::compile from the per-(batch, head) decomposition
+// (reference: src/nn/layers.cpp:1014-1080); q, k, v, out are [batch*seq, heads*dh].
+Status attention_kernel(KernelContext& ctx) {
+  const std::string op(kAttentionOp);
+  FRAME_RETURN_IF_ERROR(arity(ctx, op, 3, 1));
+  FRAME_RETURN_IF_ERROR(same_dtype(ctx, op));
+  const auto* batch = attr<int64_t>(ctx, "batch");
+  const auto* seq = attr<int64_t>(ctx, "seq");
+  const auto* heads = attr<int64_t>(ctx, "heads");
+  const auto* dh = attr<int64_t>(ctx, "dh");
+  const auto* scale = attr<double>(ctx, "scale");
+  if (!batch || !seq || !heads || !dh || !scale) return invalid(op, "missing batch/seq/heads/dh/scale attributes");
+  const Shape want({*batch * *seq, *heads * *dh});
+  for (const Tensor& t : ctx.inputs)
+    if (t.shape() != want) return invalid(op, "q, k, v must be [batch*seq, heads*dh]");
+  if (ctx.outputs[0].shape() != want) return invalid(op, "out must be [batch*seq, heads*dh]");
+  Result<int32_t> dt = float_code(op, ctx.outputs[0].dtype());
+  if (!dt.is_ok()) return dt.status();
+  FRAME_HIP_RETURN_IF_ERROR(fh_attention_fwd(dt.value(), ctx.inputs[0].raw_data(), ctx.inputs[1].raw_data(),
+                                             ctx.inputs[2].raw_data(), ctx.outputs[0].raw_data(), *batch, *seq, *heads,
+                                             *dh, static_cast<float>(*scale), stream_handle(ctx)),
+                            "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
 Status layer_norm_kernel(KernelContext& ctx) {
   FRAME_RETURN_IF_ERROR(arity(ctx, "layer_norm", 3, 1));
   FRAME_RETURN_IF_ERROR(same_dtype(ctx, "layer_norm"));
@@ -468,6 +493,7 @@ FRAME_REGISTER_KERNEL(kChannelsLastOp, kHipBackendName, &channels_last_kernel);
 FRAME_REGISTER_KERNEL(kPackInputC8Op, kHipBackendName, &pack_input_c8_kernel);
 FRAME_REGISTER_KERNEL(kPackFilterC8Op, kHipBackendName, &pack_filter_c8_kernel);
 FRAME_REGISTER_KERNEL("softmax", kHipBackendName, &softmax_kernel);
+FRAME_REGISTER_KERNEL(kAttentionOp, kHipBackendName, &attention_kernel);
 FRAME_REGISTER_KERNEL("layer_norm", kHipBackendName, &layer_norm_kernel);
 FRAME_REGISTER_KERNEL("max_pool2d", kHipBackendName, &pool_kernel<0>);
 FRAME_REGISTER_KERNEL("avg_pool2d", kHipBackendName, &pool_kernel<1>);

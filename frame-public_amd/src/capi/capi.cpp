@@ -21,6 +21,8 @@
 #include <frame/ir/serialization.h>
 #include <frame/runtime/compile.h>
 
+#include "backends/hip/hip_backend.h"
+
 struct frame_tensor {
   frame::Tensor t;
   frame::hal::Backend* backend;
@@ -225,6 +227,18 @@ int frame_transform_text(const char* ir_text, const char* pass_name, char* out, 
   frame::Status s = pm.run(g.value());
   if (!s.is_ok()) return fail(s);
   return text_out(frame::ir::dump_text(g.value()), out, cap, needed);
+}
+
+int frame_hip_lowered_text(const char* ir_text, int32_t opt_level, char* out, int64_t cap, int64_t* needed) {
+  auto g = frame::ir::parse_text(ir_text);
+  if (!g.is_ok()) return fail(g.status());
+  auto p = frame::compiler::standard_pipeline(frame::kHipBackendName);
+  if (!p.is_ok()) return fail(p.status());
+  frame::Status s = p.value().run(g.value());
+  if (!s.is_ok()) return fail(s);
+  auto lowered = frame::backends::hip::lower_for_hip(g.value(), opt_level);
+  if (!lowered.is_ok()) return fail(lowered.status());
+  return text_out(frame::ir::dump_text(lowered.value()), out, cap, needed);
 }
 
 int frame_roundtrip_text(const char* ir_text, char* out, int64_t cap, int64_t* needed) {

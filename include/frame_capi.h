@@ -74,6 +74,11 @@ int frame_transform_text(const char* ir_text, const char* pass_name, char* out, 
 int frame_roundtrip_text(const char* ir_text, char* out, int64_t cap, int64_t* needed);
 int frame_memory_plan_text(const char* ir_text, char* out, int64_t cap, int64_t* needed);
 
+/* The graph the hip backend plans for `ir_text`: the standard pipeline for "hip", then HipBackend::compile's
+ * lowering (fused attention, matmul/conv epilogues at opt_level >= 1, channels-last conv), as IR text.
+ * Host-only (no device needed); no counterpart in the reference, which has no backend lowering to inspect. */
+int frame_hip_lowered_text(const char* ir_text, int32_t opt_level, char* out, int64_t cap, int64_t* needed);
+
 /* Eager single-op launch (Backend::launch) of the one operator node in `node_ir_text` (a graph whose
  * non-input nodes are exactly one op) on the given tensors. */
 int frame_launch(const char* node_ir_text, const char* backend, frame_tensor* const* inputs, int32_t n_in,

@@ -175,6 +175,21 @@ fh_status fh_softmax_rows(int32_t dtype, const void* x, void* y, int64_t rows, i
 fh_status fh_layer_norm_rows(int32_t dtype, const void* x, const void* gamma, const void* beta, void* y,
                              int64_t rows, int64_t cols, float eps, void* stream);
 
+/* Fused scaled dot-product attention over Frame's per-(batch, head) decomposition (reference:
+ * src/nn/layers.cpp:1014-1080): q, k, v and out are [batch*seq, heads*dh] row-major; for each (b, h)
+ *   out[b*seq.., h*dh..] = round(softmax(round(round(Q_bh K_bh^T) * scale)) V_bh)
+ * with every intermediate rounded to the storage dtype where the reference's matmul, mul, softmax and matmul
+ * nodes round it. `scale` is the value of the graph's 1/sqrt(dh) constant splat after narrowing to dtype.
+ * Replaces, per (b, h), two cuBLASLt matmuls (reference: src/backends/cuda/kernels/matmul.cpp:90-276), a
+ * transpose (src/backends/cuda/kernels/shape.cu:65-192), an elementwise mul (elementwise.cu:139-360), a
+ * cudnnSoftmaxForward (sequence.cpp:108-178) and the slice/concat copies (shape.cpp:52-355): HipBackend::compile
+ * rewrites the whole decomposition into one call. bf16/f16, dh = 64, seq a multiple of 64 up to 512. */
+fh_status fh_attention_fwd(int32_t dtype, const void* q, const void* k, const void* v, void* out, int64_t batch,
+                           int64_t seq, int64_t heads, int64_t dh, float scale, void* stream);
+
+/* 1 if fh_attention_fwd accepts (dtype, seq, dh), else 0. Host-only query; no counterpart in the reference. */
+int32_t fh_attention_supported(int32_t dtype, int64_t seq, int64_t dh);
+
 /* 2-D pooling, NCHW. mode 0 = max (-inf padding, first max wins), 1 = average (include padding).
  * geom = {N, C, H, W, KH, KW, stride_h, stride_w, pad_h, pad_w}.
  * Replaces cudnnPoolingForward (reference: src/backends/cuda/kernels/pool.cpp:172-244);

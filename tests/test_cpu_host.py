@@ -170,3 +170,67 @@ def test_shape_inference_rejects_inconsistent_types():
     with pytest.raises(host.FrameError) as e:
         host.transform(g.text())
     assert "contraction dimension mismatch" in str(e.value)
+
+
+# ---- attention lowering (host only: the graph HipBackend::compile plans) ----------------------------------
+
+def attention_graph(batch=2, seq=64, heads=2, dh=64, dtype=3, swap_mul=False, head_order=None, leak=False,
+                    scale=None):
+    """Q, K, V inputs -> the reference's per-(batch, head) decomposition (src/nn/layers.cpp:1014-1080)."""
+    g = graphs.Graph("hip")
+    rows, width = batch * seq, heads * dh
+    q, k, v = (g.input(dtype, (rows, width)) for _ in range(3))
+    c = g.constant_splat(dtype, (seq, seq), (1.0 / dh ** 0.5) if scale is None else scale)
+    per_batch = []
+    for b in range(batch):
+        qr, kr, vr = (g.slice(t, 0, b * seq, (b + 1) * seq) for t in (q, k, v))
+        outs = []
+        for h in (head_order or range(heads)):
+            qh, kh, vh = (g.slice(t, 1, h * dh, (h + 1) * dh) for t in (qr, kr, vr))
+            s = g.matmul(qh, g.transpose(kh, (1, 0)))
+            s = g.mul(c, s) if swap_mul else g.mul(s, c)
+            p = g.softmax(s)
+            if leak and b == 0 and h == 0:
+                g.output(p)
+            outs.append(g.matmul(p, vh))
+        per_batch.append(g.concat(outs, 1))
+    g.output(g.concat(per_batch, 0))
+    return g
+
+
+def test_attention_decomposition_lowers_to_one_node():
+    for opt in (0, 1, 2):
+        out = host.hip_lowered(attention_graph().text(), opt)
+        ops = re.findall(r"= (\w+)\(", out)
+        assert ops == ["graph_input"] * 3 + ["hip_attention_internal"], out
+        assert "batch=2" in out and "seq=64" in out and "heads=2" in out and "dh=64" in out and "scale=0.125" in out
+
+
+def test_attention_lowering_accepts_either_mul_operand_order():
+    assert "hip_attention_internal" in host.hip_lowered(attention_graph(swap_mul=True).text())
+
+
+def test_attention_scale_is_the_constant_narrowed_to_the_dtype():
+    # 0.1 is not a bfloat16; the kernel must see the value the constant node stores (0.10009765625)
+    out = host.hip_lowered(attention_graph(scale=0.1).text())
+    assert "scale=0.10009765625" in out, out
+
+
+@pytest.mark.parametrize("kwargs", [
+    {"leak": True},                 # a probability matrix is also a graph output
+    {"head_order": [1, 0]},         # heads concatenated out of order
+    {"dh": 32, "heads": 4},         # head dim the kernel does not take
+    {"seq": 48},                    # sequence not a multiple of 64
+    {"seq": 576, "batch": 1},       # sequence beyond 512
+    {"dtype": 0},                   # float32 keeps the decomposition
+])
+def test_attention_lowering_keeps_the_decomposition_when_it_cannot_apply(kwargs):
+    out = host.hip_lowered(attention_graph(**kwargs).text())
+    assert "hip_attention_internal" not in out and "softmax" in out
+
+
+def test_attention_support_query_is_host_only():
+    lib = abi.lib()
+    assert lib.fh_attention_supported(3, 512, 64) == 1 and lib.fh_attention_supported(2, 64, 64) == 1
+    assert lib.fh_attention_supported(0, 512, 64) == 0 and lib.fh_attention_supported(3, 512, 128) == 0
+    assert lib.fh_attention_supported(3, 100, 64) == 0 and lib.fh_attention_supported(3, 1024, 64) == 0

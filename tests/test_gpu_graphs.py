@@ -194,6 +194,19 @@ def test_c5_transformer_small_full(dev):
     assert_close(got, want, BF16, what="transformer small")
 
 
+@pytest.mark.parametrize("opt_level", [0, 1])
+def test_c5_transformer_fused_attention(dev, opt_level):
+    # head dim 64, so HipBackend::compile replaces the per-(batch, head) decomposition with one attention kernel
+    say(f"C5 transformer bf16 batch=2 seq=128 heads=2 (fused attention) opt={opt_level}")
+    g, shapes = graphs.transformer_block(batch=2, seq=128, d_model=128, heads=2, ffn=256, dtype=BF16, device="hip")
+    lowered = host.hip_lowered(g.text(), opt_level)
+    assert "hip_attention_internal" in lowered and "softmax" not in lowered
+    ins = graphs.transformer_inputs(shapes, rows=256, d_model=128, dtype=BF16)
+    (got,) = run_hip(g, ins, opt_level)
+    (want,) = orc.run_graph_cpu(retarget(g, "cpu"), ins)
+    assert_close(got, want, BF16, what="transformer with fused attention")
+
+
 def test_c5_transformer_full_rows(dev):
     say("C5 transformer bf16 batch=8 seq=512 (sequence 0 checked)")
     g, shapes = graphs.transformer_block(dtype=BF16, device="hip")

@@ -424,3 +424,65 @@ def test_conv2d_c8(hip, dtype, geom, with_bias):
                                            hip.i64_array(g8), None, None))
     got = dy.download(want.shape, want.dtype)
     assert_close(got, want, dtype, what=f"conv c8 {geom}")
+
+
+# ---- fused attention ------------------------------------------------------------------------------------
+
+def attention_oracle(dtype, q, k, v, batch, seq, heads, dh):
+    """The reference's per-(batch, head) decomposition (src/nn/layers.cpp:1014-1080) evaluated node by node
+    with the oracle: matmul(Q_bh, K_bh^T) -> mul by the 1/sqrt(dh) splat -> softmax -> matmul(., V_bh)."""
+    scale = synth.to_storage(np.full((seq, seq), 1.0 / np.sqrt(dh), np.float32), dtype)
+    out = np.empty_like(q)
+    for b in range(batch):
+        rows = slice(b * seq, (b + 1) * seq)
+        for h in range(heads):
+            cols = slice(h * dh, (h + 1) * dh)
+            qh = np.ascontiguousarray(q[rows, cols])
+            kt = np.ascontiguousarray(k[rows, cols].T)
+            vh = np.ascontiguousarray(v[rows, cols])
+            s = orc.matmul(dtype, qh, kt)
+            s = orc.ew_program(dtype, [2], [2], [s, scale])  # fh_ew_op 2 = mul
+            out[rows, cols] = orc.matmul(dtype, orc.softmax(dtype, s), vh)
+    return out
+
+
+ATTENTION_CASES = [
+    # dtype, batch, seq, heads, input std
+    (BF16, 2, 64, 2, 1.0),    # one 64-key tile per wave half; score-row swizzle over 8 chunks
+    (BF16, 1, 128, 3, 1.0),   # 16 chunks per score row
+    (BF16, 2, 192, 2, 1.0),   # 24 chunks: not a multiple of 16
+    (BF16, 1, 320, 1, 1.0),   # 40 chunks
+    (BF16, 1, 512, 2, 1.0),   # the largest sequence (C5's)
+    (BF16, 1, 256, 2, 3.0),   # wide score range: most probabilities underflow to 0
+    (F16, 2, 256, 2, 1.0),
+    (F16, 1, 512, 1, 0.5),
+]
+
+
+@pytest.mark.parametrize("dtype,batch,seq,heads,std", ATTENTION_CASES)
+def test_attention_matches_decomposition(hip, dtype, batch, seq, heads, std):
+    dh = 64
+    say(f"attention dtype={dtype} batch={batch} seq={seq} heads={heads} std={std}")
+    assert hip.lib().fh_attention_supported(dtype, seq, dh) == 1
+    shape = (batch * seq, heads * dh)
+    q = synth.tensor(141, shape, dtype, "normal", std)
+    k = synth.tensor(142, shape, dtype, "normal", std)
+    v = synth.tensor(143, shape, dtype, "normal")
+    want = attention_oracle(dtype, q, k, v, batch, seq, heads, dh)
+    dq, dk, dv = dev(hip, q), dev(hip, k), dev(hip, v)
+    dout = hip.DeviceBuffer(want.nbytes)
+    scale = float(synth.to_float(synth.to_storage(np.array([1.0 / np.sqrt(dh)], np.float32), dtype), dtype)[0])
+    hip.check(hip.lib().fh_attention_fwd(dtype, dq.value, dk.value, dv.value, dout.value, batch, seq, heads, dh,
+                                         scale, None), "fh_attention_fwd")
+    got = dout.download(want.shape, want.dtype)
+    stats = assert_close(got, want, dtype, what=f"attention b={batch} s={seq} h={heads}")
+    same = float(np.mean(got == want))
+    print(f"  bit-identical fraction {same:.4f}, max abs err {stats['max_abs']:.3g} (rms {stats['rms']:.3g})")
+
+
+def test_attention_rejects_unsupported(hip):
+    # shapes outside the kernel's envelope are refused without a launch
+    for dtype, seq, dh in [(F32, 128, 64), (BF16, 128, 32), (BF16, 96, 64), (BF16, 576, 64), (BF16, 0, 64)]:
+        assert hip.lib().fh_attention_supported(dtype, seq, dh) == 0
+        rc = hip.lib().fh_attention_fwd(dtype, None, None, None, None, 1, seq, 1, dh, 0.125, None)
+        assert rc != 0, (dtype, seq, dh)
