@@ -123,13 +123,16 @@ def _time_graph(graph_text, input_sets, steps, warmup):
     return start.elapsed_ms(stop) / steps
 
 
-def extras(steps):
-    """Each entry: the config, its work, and the measured rate; failures are reported, not raised."""
+def extras(steps, only=None):
+    """Each entry: the config, its work, and the measured rate; failures are reported, not raised.
+    `only` names one entry to run by itself (for per-workload profiles)."""
     from frame_hip import graphs, synth
 
     out = {}
 
     def guard(name, fn):
+        if only is not None and name != only:
+            return
         try:
             out[name] = fn()
         except Exception as e:  # a secondary measurement must not cost the bench line
@@ -224,6 +227,8 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=128)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="only the headline GEMM (and the CPU baseline)")
+    ap.add_argument("--only", default=None,
+                    help="run just this secondary measurement (e.g. c5_transformer) and print it, no headline")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="only run the known-size copy used to scale HBM traffic counters")
     args = ap.parse_args()
@@ -232,6 +237,9 @@ def main():
         sys.exit(2)
     if args.copy_calibration_mib > 0:
         copy_calibration(args.copy_calibration_mib, args.steps)
+        return
+    if args.only:
+        print(json.dumps({args.only: extras(args.steps, args.only).get(args.only, {"error": "no such entry"})}), flush=True)
         return
 
     ms, wall = run_gpu(args.steps, args.warmup)

@@ -8,9 +8,9 @@
 //   y      = conv2d_nhwc(x_nhwc, w_khwc, bias)   (y written NCHW)
 // so the transposed tensors are ordinary arena intermediates of the memory plan.
 //
-// GEMM view: M = Cout, N = P = batch*Ho*Wo output pixels, K = KH*KW*Cin ordered (kh, kw, ci). With
-// Cin % 32 == 0 every BK = 32 stage is one filter position (kh, kw) and 32 consecutive channels, so both
-// operands are k-contiguous 64-byte rows:
+// GEMM view: M = Cout, N = P = batch*Ho*Wo output pixels, K = KH*KW*Cin ordered (kh, kw, ci). Every stage is
+// one 64-byte row per operand row: 32 channels (bf16/f16, Cin % 32 == 0) or 16 (fp32, Cin % 16 == 0) of one
+// filter position (kh, kw), so both operands are k-contiguous 64-byte rows:
 //  * A rows = w_khwc[co] (row-major [Cout][K]), loaded with global_load_lds_dwordx4 like the GEMM's A;
 //  * B rows = one output pixel's receptive-field slice x_nhwc[img, oh*sh-ph+kh, ow*sw-pw+kw, ci0..ci0+31],
 //    loaded with buffer_load_dwordx4 ... lds. Positions in the zero padding get an offset past the buffer's
@@ -31,6 +31,7 @@
 // when Ho*Wo % 8 == 0, element stores otherwise.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <string>
 #include <utility>
 
@@ -74,7 +75,7 @@ __device__ __forceinline__ void fence_kfragments(KFragments<TM, TN>& f) {
 
 template <typename T>
 __device__ __forceinline__ float apply_epilogue_one(const EpilogueArgs& ep, float v, int64_t idx) {
-  using S = uint16_t;
+  using S = typename Io<T>::storage;
   for (int s = 0; s < ep.nseg; ++s) {
     const uint8_t op = ep.ops[s];
     if (ew_is_binary(op)) {
@@ -89,12 +90,16 @@ __device__ __forceinline__ float apply_epilogue_one(const EpilogueArgs& ep, floa
 
 template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, bool C8>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNhwcArgs args) {
-  using S = uint16_t;
+  using S = typename Io<T>::storage;
+  constexpr int ES = static_cast<int>(sizeof(S));
+  constexpr int EPC = 16 / ES;     // elements per 16-byte chunk
+  constexpr int KBK = 64 / ES;     // k per stage: one 64-byte row per operand row
+  static_assert(!C8 || ES == 2, "the C8 layout is 16-bit");
   constexpr int NW = WAVES_M * WAVES_N;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int A_BYTES = BM * kBK * 2;
-  constexpr int B_BYTES = BN * kBK * 2;
+  constexpr int A_BYTES = BM * 64;
+  constexpr int B_BYTES = BN * 64;
   constexpr int STAGE = A_BYTES + B_BYTES;
   constexpr int A_PER_WAVE = A_BYTES / 1024 / NW;
   constexpr int B_PER_WAVE = B_BYTES / 1024 / NW;
@@ -125,7 +130,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
 
   const S* __restrict__ W = static_cast<const S*>(args.w);
   const int cin = args.cin, K = args.k;
-  const int KT = K / kBK;
+  const int KT = K / KBK;
 
   // ---- A (filter) sources: row co, clamped to the last channel ----
   int64_t a_src[A_PER_WAVE];
@@ -133,7 +138,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
   for (int j = 0; j < A_PER_WAVE; ++j) {
     const int row = (wave * A_PER_WAVE + j) * 16 + (lane >> 2);
     const int chunk = (lane & 3) ^ a_swizzle(row);
-    a_src[j] = static_cast<int64_t>(min(m0 + row, args.cout - 1)) * K + chunk * 8;
+    a_src[j] = static_cast<int64_t>(min(m0 + row, args.cout - 1)) * K + chunk * EPC;
   }
   // ---- B (im2col) sources: per load row, the pixel's window origin (element offset in x_nhwc, possibly
   // outside the image) and its top-left input coordinates ----
@@ -148,7 +153,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
     const int oh = rem / args.wo, ow = rem - (rem / args.wo) * args.wo;
     b_ih[j] = oh * args.sh - args.ph;
     b_iw[j] = ow * args.sw - args.pw;
-    b_org[j] = ((img * args.h + b_ih[j]) * args.w_in + b_iw[j]) * cin + (C8 ? 0 : chunk * 8);
+    b_org[j] = ((img * args.h + b_ih[j]) * args.w_in + b_iw[j]) * cin + (C8 ? 0 : chunk * EPC);
   }
   // C8 mode: filter position (kh, kw) of this lane's chunk in each B load, for the next stage to load
   // (stage s, chunk c -> position 4s + c); c8_live is false once the position is past KH*KW.
@@ -187,7 +192,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
         }
         return;
       }
-      ld_ci += kBK;
+      ld_ci += KBK;
       if (ld_ci == cin) {
         ld_ci = 0;
         if (++ld_kw == args.kw) {
@@ -203,7 +208,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
   auto load_one = [&]<int J>(int kt) {
     unsigned char* st = ring + (kt & (kStages - 1)) * STAGE;
     if constexpr (J < A_PER_WAVE) {
-      const int64_t k0 = static_cast<int64_t>(min(kt, KT - 1)) * kBK;
+      const int64_t k0 = static_cast<int64_t>(min(kt, KT - 1)) * KBK;
       global_to_lds16(W + a_src[J] + k0, (FH_LDS void*)(st + (wave * A_PER_WAVE + J) * 1024));
     } else {
       constexpr int JB = J - A_PER_WAVE;
@@ -213,7 +218,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
                           static_cast<unsigned>(iw) < static_cast<unsigned>(args.w_in) && (!C8 || kh_ < args.kh);
       // computed unconditionally so the padding case is a select, not a branch
       const int off = C8 ? (kh_ * args.w_in + kw_) * cin : ld_off;
-      const uint32_t at = static_cast<uint32_t>(b_org[JB] + off) * 2u;
+      const uint32_t at = static_cast<uint32_t>(b_org[JB] + off) * static_cast<uint32_t>(ES);
       const uint32_t voff = inside ? at : 0x80000000u;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (FH_LDS void*)(st + A_BYTES + (wave * B_PER_WAVE + JB) * 1024), 16,
                                                static_cast<int>(voff), 0, 0, 0);
@@ -313,7 +318,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
   wait_vmcnt<0>();
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __syncthreads();
-  constexpr int WTILE_BYTES = WM * WN * 2;
+  constexpr int WTILE_BYTES = WM * WN * ES;
   static_assert(NW * WTILE_BYTES <= kStages * STAGE, "the wave tiles fit in the ring");
   S* wl = reinterpret_cast<S*>(ring + wave * WTILE_BYTES);
   const S* bias = static_cast<const S*>(args.bias);
@@ -328,7 +333,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
     }
   __builtin_amdgcn_s_waitcnt(0xc07f);
   __builtin_amdgcn_wave_barrier();
-  constexpr int V = 8;
+  constexpr int V = EPC;
   constexpr int LPR = WN / V;
   constexpr int RPI = 64 / LPR;
   static_assert(64 % LPR == 0 && WM % RPI == 0, "epilogue access shape");
@@ -346,7 +351,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
       if (args.ep.nseg > 0) packed = apply_epilogue_vec<T>(args.ep, packed, idx);
       *reinterpret_cast<uint4*>(Y + idx) = packed;
     } else {
-      S vals[8];
+      S vals[V];
       __builtin_memcpy(vals, &packed, 16);
       for (int e = 0; e < V && p0 + e < args.p; ++e) {
         const int64_t p = p0 + e;
@@ -375,7 +380,10 @@ template <typename T, bool C8>
 fh_status dispatch_conv(const ConvNhwcArgs& a, hipStream_t stream) {
   const int64_t cus = device_cu_count();
   auto tiles = [&](int64_t bm, int64_t bn) { return ((a.cout + bm - 1) / bm) * ((a.p + bn - 1) / bn); };
-  if (a.cout >= 128 && tiles(128, 256) >= cus) return launch_conv<T, 128, 256, 2, 4, C8>(a, stream);
+  // fp32 wave tiles of 64x64 would not fit the ring for staging the epilogue: no 128x256 tile for fp32
+  if constexpr (sizeof(typename Io<T>::storage) == 2) {
+    if (a.cout >= 128 && tiles(128, 256) >= cus) return launch_conv<T, 128, 256, 2, 4, C8>(a, stream);
+  }
   if (a.cout >= 128 && tiles(128, 128) >= cus) return launch_conv<T, 128, 128, 2, 4, C8>(a, stream);
   if (tiles(64, 256) >= cus) return launch_conv<T, 64, 256, 1, 4, C8>(a, stream);
   if (tiles(64, 128) >= cus) return launch_conv<T, 64, 128, 2, 2, C8>(a, stream);
@@ -400,6 +408,55 @@ __global__ __launch_bounds__(256) void transpose_batched_kernel(const E* __restr
   for (int c = ty; c < 64; c += 4) {
     const int64_t gc = c0 + c, gr = r0 + tx;
     if (gc < cols && gr < rows) yb[gc * rows + gr] = tile[tx][c];
+  }
+}
+
+// 16-bit batched transpose with 16-byte global accesses (rows % 8 == 0, cols % 8 == 0, 16-byte aligned): a
+// 64 x 64 tile is read as 16-byte row chunks into LDS (chunk cc of tile row r stored at cc ^ ((r >> 3) & 7), which
+// keeps the column reads below free of bank conflicts), and each thread then gathers 8 consecutive rows of one
+// column and writes them as one 16-byte chunk of the output row.
+__global__ __launch_bounds__(256) void transpose_wide_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
+                                                             int64_t rows, int64_t cols) {
+  __shared__ __attribute__((aligned(16))) uint16_t tile[64 * 64];
+  const int64_t b = blockIdx.z;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64, c0 = static_cast<int64_t>(blockIdx.x) * 64;
+  const uint16_t* xb = x + b * rows * cols;
+  uint16_t* yb = y + b * rows * cols;
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int id = t + 256 * j, r = id >> 3, cc = id & 7;
+    const int64_t gr = r0 + r, gc = c0 + 8 * cc;
+    uint4 v = make_uint4(0, 0, 0, 0);
+    if (gr < rows && gc < cols) v = *reinterpret_cast<const uint4*>(xb + gr * cols + gc);
+    *reinterpret_cast<uint4*>(tile + r * 64 + ((cc ^ ((r >> 3) & 7)) * 8)) = v;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int id = t + 256 * j, c = id >> 3, rc = id & 7;
+    const int64_t gc = c0 + c, gr = r0 + 8 * rc;
+    uint16_t o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = tile[(8 * rc + i) * 64 + (((c >> 3) ^ rc) * 8) + (c & 7)];
+    if (gc < cols && gr < rows) {
+      uint4 v;
+      __builtin_memcpy(&v, o, 16);
+      *reinterpret_cast<uint4*>(yb + gc * rows + gr) = v;
+    }
+  }
+}
+
+// Small or thin batched transposes (a filter's [Cin][KH*KW] planes, late-stage activations): one thread per
+// output element, consecutive threads along the output row (writes coalesced, reads at stride `cols`).
+template <typename E>
+__global__ __launch_bounds__(256) void transpose_gather_kernel(const E* __restrict__ x, E* __restrict__ y, int64_t batch,
+                                                               int64_t rows, int64_t cols) {
+  const int64_t total = batch * rows * cols;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  for (int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; o < total; o += stride) {
+    const int64_t r = o % rows, bc = o / rows, c = bc % cols, b = bc / cols;
+    y[o] = x[(b * rows + r) * cols + c];
   }
 }
 
@@ -435,16 +492,19 @@ __global__ __launch_bounds__(256) void pack_filter_c8_kernel(const uint16_t* __r
 
 // Geometry accepted by the channels-last MFMA path.
 bool nhwc_supported(int32_t dtype, const int64_t* g) {
-  if (dtype != FH_BF16 && dtype != FH_F16) return false;
+  if (dtype != FH_BF16 && dtype != FH_F16 && dtype != FH_F32) return false;
   const int64_t n = g[0], cin = g[1], h = g[2], w = g[3], cout = g[4], kh = g[5], kw = g[6], sh = g[7], sw = g[8],
                 ph = g[9], pw = g[10], groups = g[11];
-  // Cin % 32 == 0, or Cin == 8: the C8 layout (a conv with fewer channels is packed to 8 first)
-  if (groups != 1 || (cin % kBK != 0 && cin != 8) || n <= 0 || h <= 0 || w <= 0 || cout <= 0 || kh <= 0 || kw <= 0)
+  const int64_t es = dtype == FH_F32 ? 4 : 2, stage_k = 64 / es;
+  // 16-bit: Cin % 32 == 0, or Cin == 8 (the C8 layout; a conv with fewer channels is packed to 8 first).
+  // fp32: Cin % 16 == 0 (one 64-byte row of channels per stage).
+  const bool c8 = es == 2 && cin == 8;
+  if (groups != 1 || (cin % stage_k != 0 && !c8) || n <= 0 || h <= 0 || w <= 0 || cout <= 0 || kh <= 0 || kw <= 0)
     return false;
   if (sh <= 0 || sw <= 0 || ph < 0 || pw < 0 || h + 2 * ph < kh || w + 2 * pw < kw) return false;
   const int64_t oh = (h + 2 * ph - kh) / sh + 1, ow = (w + 2 * pw - kw) / sw + 1;
   // 32-bit offsets inside the kernel: input bytes, window origins and filter rows
-  if (n * h * w * cin * 2 >= (int64_t{1} << 31)) return false;
+  if (n * h * w * cin * es >= (int64_t{1} << 31)) return false;
   if (kh * kw * cin >= (int64_t{1} << 24) || n * oh * ow >= (int64_t{1} << 31)) return false;
   return true;
 }
@@ -464,6 +524,25 @@ extern "C" fh_status fh_transpose_batched(int32_t itemsize, const void* x, void*
   const dim3 grid(static_cast<uint32_t>((cols + 63) / 64), static_cast<uint32_t>((rows + 63) / 64),
                   static_cast<uint32_t>(batch));
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (rows < 64 || cols < 64) {
+    const int64_t total = batch * rows * cols;
+    const uint32_t blocks = static_cast<uint32_t>(std::min<int64_t>((total + 255) / 256, 65536));
+    if (itemsize == 2) {
+      hipLaunchKernelGGL(transpose_gather_kernel<uint16_t>, dim3(blocks), dim3(256), 0, s, static_cast<const uint16_t*>(x),
+                         static_cast<uint16_t*>(y), batch, rows, cols);
+    } else if (itemsize == 4) {
+      hipLaunchKernelGGL(transpose_gather_kernel<uint32_t>, dim3(blocks), dim3(256), 0, s, static_cast<const uint32_t*>(x),
+                         static_cast<uint32_t*>(y), batch, rows, cols);
+    } else {
+      return fail(FH_INVALID_ARGUMENT, "fh_transpose_batched: itemsize must be 2 or 4");
+    }
+    return launch_status("transpose_gather_kernel launch");
+  }
+  if (itemsize == 2 && rows % 8 == 0 && cols % 8 == 0 && aligned16(x) && aligned16(y)) {
+    hipLaunchKernelGGL(transpose_wide_kernel, grid, dim3(256), 0, s, static_cast<const uint16_t*>(x),
+                       static_cast<uint16_t*>(y), rows, cols);
+    return launch_status("transpose_wide_kernel launch");
+  }
   switch (itemsize) {
     case 2:
       hipLaunchKernelGGL(transpose_batched_kernel<uint16_t>, grid, dim3(256), 0, s, static_cast<const uint16_t*>(x),
@@ -488,7 +567,8 @@ extern "C" fh_status fh_conv2d_nhwc_fwd(int32_t dtype, const void* x_nhwc, const
   if (geom == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd: null geometry");
   if (!nhwc_supported(dtype, geom))
     return fail(FH_UNIMPLEMENTED, "fh_conv2d_nhwc_fwd: geometry or dtype not supported by the channels-last path "
-                                  "(needs bf16/f16, groups 1, Cin % 32 == 0)");
+                                  "(needs groups 1 and bf16/f16 with Cin % 32 == 0 or Cin == 8, or fp32 with "
+                                  "Cin % 16 == 0)");
   if (x_nhwc == nullptr || w_khwc == nullptr || y == nullptr)
     return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd: null pointer");
   if (!aligned16(x_nhwc) || !aligned16(w_khwc)) return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd: operands must be 16-byte aligned");
@@ -511,10 +591,11 @@ extern "C" fh_status fh_conv2d_nhwc_fwd(int32_t dtype, const void* x_nhwc, const
   const int64_t ow = (geom[3] + 2 * geom[10] - geom[6]) / geom[8] + 1;
   a.wo = static_cast<int32_t>(ow);
   a.howo = static_cast<int32_t>(oh * ow);
-  const bool c8 = geom[1] == 8;
+  const bool c8 = geom[1] == 8 && dtype != FH_F32;
   a.k = static_cast<int32_t>(c8 ? conv_c8_filter_k(geom[5], geom[6]) : geom[5] * geom[6] * geom[1]);
   a.p = geom[0] * oh * ow;
-  a.x_bytes = static_cast<uint32_t>(geom[0] * geom[2] * geom[3] * geom[1] * 2);
+  const int64_t es = dtype == FH_F32 ? 4 : 2;
+  a.x_bytes = static_cast<uint32_t>(geom[0] * geom[2] * geom[3] * geom[1] * es);
   if (epilogue != nullptr) {
     if (epilogue->nseg < 0 || epilogue->nseg > FH_MAX_SEGMENTS)
       return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd: epilogue nseg out of range");
@@ -535,6 +616,7 @@ extern "C" fh_status fh_conv2d_nhwc_fwd(int32_t dtype, const void* x_nhwc, const
   a.vec_store = vec ? 1 : 0;
   if (a.p == 0) return FH_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == FH_F32) return dispatch_conv<float, false>(a, s);
   if (c8) return dtype == FH_BF16 ? dispatch_conv<bf16_t, true>(a, s) : dispatch_conv<f16_t, true>(a, s);
   return dtype == FH_BF16 ? dispatch_conv<bf16_t, false>(a, s) : dispatch_conv<f16_t, false>(a, s);
 }

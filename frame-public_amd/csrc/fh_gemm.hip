@@ -324,53 +324,79 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(GemmArgs args) {
   }
 }
 
-// Generic fallback for shapes the tile kernel does not accept (unaligned rows, N or K not a multiple of the
-// chunk width). Plain fp32 arithmetic with k summed in increasing order, like the reference CPU kernel.
+// Small and unaligned GEMMs (few output tiles, or rows/columns the tile kernels cannot take): one thread per
+// output of a 16 x 16 tile, its k loop strictly sequential like the reference CPU kernel (fp32 products and sums,
+// no contraction, one rounding), so the result is bit-identical to it. K is staged through LDS in chunks of kKC as
+// fp32, A row-major and B transposed, both k-contiguous so each step reads 4 k-values per operand with one
+// 16-byte LDS read; the next chunk's global loads are in flight while the current one is consumed.
+constexpr int kSeqT = 16;   // output tile edge
+constexpr int kKC = 128;    // k per LDS chunk
+constexpr int kKP = kKC + 4;  // padded row: 16 consecutive B rows hit distinct 16-byte bank groups
+
 template <typename T>
-__global__ __launch_bounds__(256) void gemm_generic_kernel(GemmArgs args) {
+__global__ __launch_bounds__(256) void gemm_seq_kernel(GemmArgs args) {
   using S = typename Io<T>::storage;
-  constexpr int TB = 64, KB = 16;
-  __shared__ float As[KB][TB + 1];
-  __shared__ float Bs[KB][TB + 1];
-  const S* A = static_cast<const S*>(args.A) + blockIdx.z * args.stride_a;
-  const S* B = static_cast<const S*>(args.B) + blockIdx.z * args.stride_b;
-  S* C = static_cast<S*>(args.C) + blockIdx.z * args.stride_c;
-  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * TB;
-  const int64_t n0 = static_cast<int64_t>(blockIdx.x) * TB;
-  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-  float acc[4][4] = {};
-  for (int64_t k0 = 0; k0 < args.K; k0 += KB) {
-    for (int e = threadIdx.x; e < KB * TB; e += 256) {
-      const int kk = e / TB, mm = e % TB;
-      const int64_t gm = m0 + mm, gk = k0 + kk;
-      As[kk][mm] = (gm < args.M && gk < args.K) ? Io<T>::load(A[gm * args.lda + gk]) : 0.0f;
-      const int nn = e % TB;
-      const int64_t gn = n0 + nn;
-      Bs[kk][nn] = (gk < args.K && gn < args.N) ? Io<T>::load(B[gk * args.ldb + gn]) : 0.0f;
-    }
-    __syncthreads();
-    const int kmax = static_cast<int>(min<int64_t>(KB, args.K - k0));
-    for (int kk = 0; kk < kmax; ++kk) {
+  __shared__ __attribute__((aligned(16))) float As[2][kSeqT * kKP];
+  __shared__ __attribute__((aligned(16))) float Bt[2][kSeqT * kKP];
+  const S* __restrict__ A = static_cast<const S*>(args.A) + blockIdx.z * args.stride_a;
+  const S* __restrict__ B = static_cast<const S*>(args.B) + blockIdx.z * args.stride_b;
+  S* __restrict__ C = static_cast<S*>(args.C) + blockIdx.z * args.stride_c;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kSeqT, n0 = static_cast<int64_t>(blockIdx.x) * kSeqT;
+  const int64_t M = args.M, N = args.N, K = args.K;
+  const int t = threadIdx.x;
+  const int r = t >> 4, c = t & 15;
+
+  // chunk loads: A[16][kKC] (thread -> row t/16, k t%16 + 16 i) and B[kKC][16] (thread -> k t/16 + 16 i, col t%16)
+  float la[8], lb[8];
+  auto load_chunk = [&](int64_t k0) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] += As[kk][ty * 4 + i] * Bs[kk][tx * 4 + j];
+    for (int i = 0; i < 8; ++i) {
+      const int64_t gm = m0 + r, gk = k0 + c + 16 * i;
+      la[i] = (gm < M && gk < K) ? Io<T>::load(A[gm * args.lda + gk]) : 0.0f;
+      const int64_t bk = k0 + r + 16 * i, bn = n0 + c;
+      lb[i] = (bk < K && bn < N) ? Io<T>::load(B[bk * args.ldb + bn]) : 0.0f;
     }
+  };
+  auto store_chunk = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      As[buf][r * kKP + c + 16 * i] = la[i];
+      Bt[buf][c * kKP + r + 16 * i] = lb[i];
+    }
+  };
+
+  float acc = 0.0f;
+  const int chunks = static_cast<int>((K + kKC - 1) / kKC);
+  if (chunks > 0) {
+    load_chunk(0);
+    store_chunk(0);
+  }
+  __syncthreads();
+  for (int ch = 0; ch < chunks; ++ch) {
+    const int buf = ch & 1;
+    if (ch + 1 < chunks) load_chunk(static_cast<int64_t>(ch + 1) * kKC);
+    const int kn = static_cast<int>(min<int64_t>(kKC, K - static_cast<int64_t>(ch) * kKC));
+    const float* ar = &As[buf][r * kKP];
+    const float* br = &Bt[buf][c * kKP];
+    int kk = 0;
+    for (; kk + 4 <= kn; kk += 4) {
+      const float4 a = *reinterpret_cast<const float4*>(ar + kk);
+      const float4 b = *reinterpret_cast<const float4*>(br + kk);
+      acc = acc + a.x * b.x;
+      acc = acc + a.y * b.y;
+      acc = acc + a.z * b.z;
+      acc = acc + a.w * b.w;
+    }
+    for (; kk < kn; ++kk) acc = acc + ar[kk] * br[kk];
+    if (ch + 1 < chunks) store_chunk(buf ^ 1);
     __syncthreads();
   }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t row = m0 + ty * 4 + i;
-    if (row >= args.M) continue;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int64_t col = n0 + tx * 4 + j;
-      if (col >= args.N) continue;
-      float v = Io<T>::round(acc[i][j]);
-      const int64_t idx = row * args.ldc + col;
-      if (args.ep.nseg > 0) v = apply_epilogue<T>(args.ep, v, idx);
-      C[idx] = Io<T>::store(v);
-    }
+  const int64_t row = m0 + r, col = n0 + c;
+  if (row < M && col < N) {
+    float v = Io<T>::round(acc);
+    const int64_t idx = row * args.ldc + col;
+    if (args.ep.nseg > 0) v = apply_epilogue<T>(args.ep, v, idx);
+    C[idx] = Io<T>::store(v);
   }
 }
 
@@ -399,9 +425,14 @@ bool epilogue_aligned(const EpilogueArgs& ep) {
 template <typename T>
 fh_status dispatch_gemm(GemmArgs args, int64_t batch, hipStream_t stream) {
   constexpr int E = GemmTraits<T>::E;
+  const int cus = device_cu_count();
+  // Few 64 x 64 tiles (less than a quarter of the CUs busy): the sequential kernel, whose 16 x 16 tiles spread
+  // further and whose latency is a handful of K chunks.
+  const int64_t tiles64 = ((args.M + 63) / 64) * ((args.N + 63) / 64) * batch;
+  const bool small = tiles64 * 4 < cus && args.K <= 16384;
   if constexpr (!std::is_same_v<T, float>) {
     fh_status st = FH_OK;
-    if (gemm16_try_launch(std::is_same_v<T, bf16_t> ? FH_BF16 : FH_F16, args, batch, stream, &st)) return st;
+    if (!small && gemm16_try_launch(std::is_same_v<T, bf16_t> ? FH_BF16 : FH_F16, args, batch, stream, &st)) return st;
   }
   const size_t esz = sizeof(typename Io<T>::storage);
   const bool aligned = (reinterpret_cast<uintptr_t>(args.A) % 16 == 0) &&
@@ -410,13 +441,15 @@ fh_status dispatch_gemm(GemmArgs args, int64_t batch, hipStream_t stream) {
                        ((args.stride_a * esz) % 16 == 0) && ((args.stride_b * esz) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(args.C) % 16 == 0) && (args.ldc % E == 0) &&
                        ((args.stride_c * esz) % 16 == 0) && epilogue_aligned(args.ep);
-  if (!aligned) {
-    dim3 grid(static_cast<uint32_t>((args.N + 63) / 64), static_cast<uint32_t>((args.M + 63) / 64),
+  // small problems, or operands the tile kernels cannot take
+  if (!aligned || small) {
+    if ((args.M + kSeqT - 1) / kSeqT > 65535 || batch > 65535)
+      return fail(FH_UNIMPLEMENTED, "fh_gemm: unaligned operands with more than 1,048,560 rows or 65,535 batches");
+    dim3 grid(static_cast<uint32_t>((args.N + kSeqT - 1) / kSeqT), static_cast<uint32_t>((args.M + kSeqT - 1) / kSeqT),
               static_cast<uint32_t>(batch));
-    hipLaunchKernelGGL((gemm_generic_kernel<T>), grid, dim3(256), 0, stream, args);
-    return launch_status("gemm_generic_kernel launch");
+    hipLaunchKernelGGL((gemm_seq_kernel<T>), grid, dim3(256), 0, stream, args);
+    return launch_status("gemm_seq_kernel launch");
   }
-  const int cus = device_cu_count();
   auto tiles = [&](int64_t t) { return ((args.M + t - 1) / t) * ((args.N + t - 1) / t) * batch; };
   if (tiles(256) >= cus) return launch_tile<T, 256, 256>(args, batch, stream);
   if (tiles(128) >= cus / 2) return launch_tile<T, 128, 128>(args, batch, stream);

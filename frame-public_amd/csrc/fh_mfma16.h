@@ -1,4 +1,4 @@
-// Device helpers shared by the 16-bit MFMA kernels (fh_gemm16.hip, fh_conv_igemm.hip): MFMA wrapper, explicit
+// Device helpers shared by the MFMA kernels (fh_gemm16.hip, fh_conv_igemm.hip, fh_attention.hip): MFMA wrapper, explicit
 // wait counts, LDS fragment reads, direct-to-LDS loads, the elementwise epilogue on 16-byte vectors, LDS
 // swizzles and the in-loop instruction spreading used by the software pipelines.
 #pragma once
@@ -24,9 +24,17 @@ typedef unsigned int u32x2_t __attribute__((ext_vector_type(2)));
 constexpr int kBK = 32;      // k per stage
 constexpr int kStages = 4;   // LDS ring depth
 
+// One k-slice of the 32x32 MFMA tile from a 16-byte fragment per lane (lane half h holds k-chunk h of the
+// slice). 16-bit: the chunk is 8 k-values, one 32x32x16 instruction. fp32: the chunk is 4 k-values; four 32x32x2
+// instructions take component j of both halves' chunks, and since both operands use the same k assignment the
+// slice's 8 products are all summed.
 template <typename T>
 __device__ __forceinline__ void mfma32(const u32x4_t& a, const u32x4_t& b, f32x16_t& acc) {
-  if constexpr (std::is_same_v<T, bf16_t>) {
+  if constexpr (std::is_same_v<T, float>) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__uint_as_float(a[j]), __uint_as_float(b[j]), acc, 0, 0, 0);
+  } else if constexpr (std::is_same_v<T, bf16_t>) {
     acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
                                                   acc, 0, 0, 0);
   } else {
@@ -73,31 +81,32 @@ __device__ __forceinline__ void global_to_lds16(const void* g, FH_LDS void* lds_
 // Runs the epilogue program on 8 rounded outputs (one 16-byte vector) at flat output index idx.
 template <typename T>
 __device__ __forceinline__ uint4 apply_epilogue_vec(const EpilogueArgs& ep, uint4 packed, int64_t idx) {
-  using S = uint16_t;
-  S vals[8];
+  using S = typename Io<T>::storage;
+  constexpr int V = 16 / static_cast<int>(sizeof(S));
+  S vals[V];
   __builtin_memcpy(vals, &packed, 16);
-  float v[8];
+  float v[V];
 #pragma unroll
-  for (int x = 0; x < 8; ++x) v[x] = Io<T>::load(vals[x]);
+  for (int x = 0; x < V; ++x) v[x] = Io<T>::load(vals[x]);
   for (int sg = 0; sg < ep.nseg; ++sg) {
     const uint8_t op = ep.ops[sg];
     if (ew_is_binary(op)) {
       const uint4 in = *reinterpret_cast<const uint4*>(static_cast<const S*>(ep.ins[sg]) + idx);
-      S iv[8];
+      S iv[V];
       __builtin_memcpy(iv, &in, 16);
 #pragma unroll
-      for (int x = 0; x < 8; ++x) v[x] = ew_binary(op, v[x], Io<T>::load(iv[x]));
+      for (int x = 0; x < V; ++x) v[x] = ew_binary(op, v[x], Io<T>::load(iv[x]));
     } else {
 #pragma unroll
-      for (int x = 0; x < 8; ++x) v[x] = ew_unary(op, v[x]);
+      for (int x = 0; x < V; ++x) v[x] = ew_unary(op, v[x]);
     }
     if (ep.round_between) {
 #pragma unroll
-      for (int x = 0; x < 8; ++x) v[x] = Io<T>::round(v[x]);
+      for (int x = 0; x < V; ++x) v[x] = Io<T>::round(v[x]);
     }
   }
 #pragma unroll
-  for (int x = 0; x < 8; ++x) vals[x] = Io<T>::store(v[x]);
+  for (int x = 0; x < V; ++x) vals[x] = Io<T>::store(v[x]);
   __builtin_memcpy(&packed, vals, 16);
   return packed;
 }

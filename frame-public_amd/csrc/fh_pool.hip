@@ -1,5 +1,5 @@
 // 2-D pooling over NCHW, one thread per output element (the operation is a small gather; its cost is the
-// read of the input once and the write of the output once).
+// read of the input once and the write of the output once). The per-plane kernel keeps index math in 32 bits.
 //
 // max_pool2d (reference: src/backends/cpu/kernels/pool.cpp:178-237): padding never wins (treated as -inf),
 // the window is scanned kh-outer / kw-inner and a later value replaces the best only if strictly greater,
@@ -51,9 +51,68 @@ __global__ __launch_bounds__(256) void pool2d_kernel(const typename Io<T>::stora
   }
 }
 
+// Same semantics with one grid row per (image, channel) plane and 32-bit index math inside the plane (the 64-bit
+// divisions of the general kernel dominate its run time). Used when a plane has fewer than 2^31 elements and
+// there are at most 65535 * 65535 planes' worth of grid.
+struct PlaneGeom {
+  int32_t h, w, kh, kw, sh, sw, ph, pw, oh, ow;
+};
+
+template <typename T, int MODE>
+__global__ __launch_bounds__(256) void pool2d_plane_kernel(const typename Io<T>::storage* __restrict__ x,
+                                                           typename Io<T>::storage* __restrict__ y, PlaneGeom g) {
+  const int p = blockIdx.x * 256 + threadIdx.x;
+  const int ohw = g.oh * g.ow;
+  if (p >= ohw) return;
+  const int64_t plane_id = static_cast<int64_t>(blockIdx.z) * gridDim.y + blockIdx.y;
+  const int oh = p / g.ow, ow = p - (p / g.ow) * g.ow;
+  const auto* plane = x + plane_id * g.h * g.w;
+  const float denom = static_cast<float>(g.kh * g.kw);
+  float acc = 0.0f;
+  bool found = false;
+  const int ih0 = oh * g.sh - g.ph, iw0 = ow * g.sw - g.pw;
+  for (int a = 0; a < g.kh; ++a) {
+    const int ih = ih0 + a;
+    if (ih < 0 || ih >= g.h) continue;
+    const auto* rowp = plane + ih * g.w;
+    for (int b = 0; b < g.kw; ++b) {
+      const int iw = iw0 + b;
+      if (iw < 0 || iw >= g.w) continue;
+      const float v = Io<T>::load(rowp[iw]);
+      if (MODE == 0) {
+        if (!found || v > acc) acc = v;
+        found = true;
+      } else {
+        acc += v;
+      }
+    }
+  }
+  y[plane_id * ohw + p] = Io<T>::store(MODE == 0 ? acc : acc / denom);
+}
+
 template <typename T>
 fh_status launch_pool(int32_t mode, const void* x, void* y, const PoolGeom& g, hipStream_t s) {
   using S = typename Io<T>::storage;
+  const int64_t planes = g.n * g.c;
+  if (g.h * g.w < (int64_t{1} << 31) && g.oh * g.ow < (int64_t{1} << 31) && planes <= int64_t{65535} * 65535) {
+    const PlaneGeom pg{static_cast<int32_t>(g.h),  static_cast<int32_t>(g.w),  static_cast<int32_t>(g.kh),
+                       static_cast<int32_t>(g.kw), static_cast<int32_t>(g.sh), static_cast<int32_t>(g.sw),
+                       static_cast<int32_t>(g.ph), static_cast<int32_t>(g.pw), static_cast<int32_t>(g.oh),
+                       static_cast<int32_t>(g.ow)};
+    // planes = gy * gz exactly: gy the largest divisor of planes not above 65535
+    int64_t gy = planes <= 65535 ? planes : 65535;
+    while (planes % gy != 0) --gy;
+    const int64_t gz = planes / gy;
+    if (gz <= 65535) {
+      const dim3 grid(static_cast<uint32_t>((g.oh * g.ow + 255) / 256), static_cast<uint32_t>(gy), static_cast<uint32_t>(gz));
+      if (mode == 0) {
+        hipLaunchKernelGGL((pool2d_plane_kernel<T, 0>), grid, dim3(256), 0, s, static_cast<const S*>(x), static_cast<S*>(y), pg);
+      } else {
+        hipLaunchKernelGGL((pool2d_plane_kernel<T, 1>), grid, dim3(256), 0, s, static_cast<const S*>(x), static_cast<S*>(y), pg);
+      }
+      return launch_status("pool2d_plane_kernel launch");
+    }
+  }
   const int64_t total = g.n * g.c * g.oh * g.ow;
   int64_t blocks = (total + 255) / 256;
   const int64_t cap = static_cast<int64_t>(device_cu_count()) * 16;

@@ -34,6 +34,8 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 constexpr int kRowsPerBlock = 4;  // 4 waves, one row each
 
+typedef unsigned int u4_t __attribute__((ext_vector_type(4)));
+
 template <typename T, int PER>
 __global__ __launch_bounds__(256) void softmax_wave_kernel(const typename Io<T>::storage* __restrict__ x,
                                                            typename Io<T>::storage* __restrict__ y, int64_t rows,
@@ -138,6 +140,72 @@ __global__ __launch_bounds__(256) void layer_norm_wave_kernel(const typename Io<
   }
 }
 
+// Same arithmetic with 16-byte accesses, for rows of exactly 64 * PER elements (PER a multiple of the vector
+// width): lane l owns the contiguous elements [V*l + 64*V*t, +V) for t < PER / V. Every load (x, gamma, beta)
+// is issued before the first reduction, so one memory latency covers the row.
+template <typename T, int PER>
+__global__ __launch_bounds__(256) void layer_norm_vec_kernel(const typename Io<T>::storage* __restrict__ x,
+                                                             const typename Io<T>::storage* __restrict__ gamma,
+                                                             const typename Io<T>::storage* __restrict__ beta,
+                                                             typename Io<T>::storage* __restrict__ y, int64_t rows,
+                                                             float eps) {
+  using S = typename Io<T>::storage;
+  constexpr int V = 16 / static_cast<int>(sizeof(S));
+  constexpr int NV = PER / V;
+  constexpr int64_t COLS = 64 * PER;
+  static_assert(PER % V == 0, "whole vectors per lane");
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const u4_t* xr = reinterpret_cast<const u4_t*>(x + row * COLS);
+  const u4_t* gr = reinterpret_cast<const u4_t*>(gamma);
+  const u4_t* br = reinterpret_cast<const u4_t*>(beta);
+  u4_t* yr = reinterpret_cast<u4_t*>(y + row * COLS);
+  u4_t xv[NV], gv[NV], bv[NV];
+#pragma unroll
+  for (int t = 0; t < NV; ++t) xv[t] = __builtin_nontemporal_load(xr + lane + 64 * t);
+#pragma unroll
+  for (int t = 0; t < NV; ++t) {
+    gv[t] = gr[lane + 64 * t];
+    bv[t] = br[lane + 64 * t];
+  }
+  float v[PER];
+  float sum = 0.0f;
+#pragma unroll
+  for (int t = 0; t < NV; ++t) {
+    S e[V];
+    __builtin_memcpy(e, &xv[t], 16);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      v[t * V + i] = Io<T>::load(e[i]);
+      sum += v[t * V + i];
+    }
+  }
+  const float mean = wave_sum(sum) / static_cast<float>(COLS);
+  float var_sum = 0.0f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const float c = v[i] - mean;
+    var_sum += c * c;
+  }
+  const float variance = wave_sum(var_sum) / static_cast<float>(COLS);
+  const float r = 1.0f / sqrtf(variance + eps);
+#pragma unroll
+  for (int t = 0; t < NV; ++t) {
+    S g[V], b[V], o[V];
+    __builtin_memcpy(g, &gv[t], 16);
+    __builtin_memcpy(b, &bv[t], 16);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float xhat = (v[t * V + i] - mean) * r;
+      o[i] = Io<T>::store(Io<T>::load(g[i]) * xhat + Io<T>::load(b[i]));
+    }
+    u4_t w;
+    __builtin_memcpy(&w, o, 16);
+    __builtin_nontemporal_store(w, yr + lane + 64 * t);
+  }
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void layer_norm_block_kernel(const typename Io<T>::storage* __restrict__ x,
                                                                const typename Io<T>::storage* __restrict__ gamma,
@@ -205,10 +273,29 @@ fh_status softmax_typed(const void* x, void* y, int64_t rows, int64_t cols, hipS
   return launch_status("softmax_block_kernel launch");
 }
 
+template <typename T, int PER>
+fh_status launch_layer_norm_vec(const void* x, const void* g, const void* b, void* y, int64_t rows, float eps,
+                                hipStream_t s) {
+  using S = typename Io<T>::storage;
+  const dim3 grid(static_cast<uint32_t>((rows + kRowsPerBlock - 1) / kRowsPerBlock));
+  hipLaunchKernelGGL((layer_norm_vec_kernel<T, PER>), grid, dim3(256), 0, s, static_cast<const S*>(x),
+                     static_cast<const S*>(g), static_cast<const S*>(b), static_cast<S*>(y), rows, eps);
+  return launch_status("layer_norm_vec_kernel launch");
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 template <typename T>
 fh_status layer_norm_typed(const void* x, const void* g, const void* b, void* y, int64_t rows, int64_t cols,
                            float eps, hipStream_t s) {
   using S = typename Io<T>::storage;
+  if (aligned16(x) && aligned16(g) && aligned16(b) && aligned16(y)) {
+    constexpr int V = 16 / static_cast<int>(sizeof(S));
+    if (cols == 64 * V) return launch_layer_norm_vec<T, V>(x, g, b, y, rows, eps, s);
+    if (cols == 64 * 2 * V) return launch_layer_norm_vec<T, 2 * V>(x, g, b, y, rows, eps, s);
+    if (cols == 64 * 4 * V) return launch_layer_norm_vec<T, 4 * V>(x, g, b, y, rows, eps, s);
+    if (V == 4 && cols == 64 * 8 * V) return launch_layer_norm_vec<T, 8 * V>(x, g, b, y, rows, eps, s);
+  }
   if (cols <= 64 * 32) return by_width<T, LayerNormLaunch>(cols, x, g, b, y, rows, cols, eps, s);
   hipLaunchKernelGGL(layer_norm_block_kernel<T>, dim3(static_cast<uint32_t>(rows)), dim3(256), 0, s,
                      static_cast<const S*>(x), static_cast<const S*>(g), static_cast<const S*>(b), static_cast<S*>(y),

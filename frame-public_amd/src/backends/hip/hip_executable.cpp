@@ -14,7 +14,7 @@
 // takes the contraction result as its first operand is replaced by one internal node that applies the
 // consumer's program in the contraction's epilogue. The epilogue rounds to the storage dtype after the
 // product and after every segment, so results equal the unfused graph's bit for bit.
-//  * channels-last conv (every opt_level): a bf16/f16 conv that the MFMA implicit-GEMM path accepts becomes
+//  * channels-last conv (every opt_level): a conv that the MFMA implicit-GEMM path accepts becomes
 // channels_last(x), channels_last(w) and conv2d_nhwc (see lower_convs).
 // The rewrites run on a private copy of the graph before planning, so the memory plan sees the real lifetimes.
 #include <algorithm>
@@ -144,6 +144,7 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
       const auto* groups = get("groups") ? std::get_if<int64_t>(get("groups")) : nullptr;
       const int32_t dt = xt.dtype.code() == DTypeCode::kBFloat16  ? FH_BF16
                          : xt.dtype.code() == DTypeCode::kFloat16 ? FH_F16
+                         : xt.dtype.code() == DTypeCode::kFloat32 ? FH_F32
                                                                   : -1;
       if (stride && pad && groups && stride->size() == 2 && pad->size() == 2 && dt >= 0 && xt.shape.rank() == 4 &&
           wt.shape.rank() == 4 && wt.dtype == xt.dtype) {
@@ -151,7 +152,7 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
                                   wt.shape.dim(0), wt.shape.dim(2), wt.shape.dim(3), (*stride)[0],
                                   (*stride)[1],    (*pad)[0],       (*pad)[1],       *groups};
         // Cin <= 8 goes through the C8 layout (channels padded to 8, four filter positions per k-stage)
-        const bool c8 = xt.shape.dim(1) <= 8 && *groups == 1;
+        const bool c8 = xt.shape.dim(1) <= 8 && *groups == 1 && dt != FH_F32;
         int64_t geom_k[12];
         std::copy(geom, geom + 12, geom_k);
         if (c8) geom_k[1] = 8;

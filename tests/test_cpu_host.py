@@ -234,3 +234,16 @@ def test_attention_support_query_is_host_only():
     assert lib.fh_attention_supported(3, 512, 64) == 1 and lib.fh_attention_supported(2, 64, 64) == 1
     assert lib.fh_attention_supported(0, 512, 64) == 0 and lib.fh_attention_supported(3, 512, 128) == 0
     assert lib.fh_attention_supported(3, 100, 64) == 0 and lib.fh_attention_supported(3, 1024, 64) == 0
+
+
+@pytest.mark.parametrize("dtype,cin,lowered", [(3, 64, "hip_conv2d_nhwc_internal"), (0, 64, "hip_conv2d_nhwc_internal"),
+                                               (3, 3, "hip_pack_input_c8_internal"), (0, 3, "conv2d"),
+                                               (0, 24, "conv2d")])
+def test_conv_lowering_by_dtype_and_channels(dtype, cin, lowered):
+    # bf16 and fp32 with a stage-aligned channel count go channels-last; a bf16 stem takes the C8 packing;
+    # fp32 with 3 or 24 channels keeps the direct conv
+    g = graphs.conv(dtype, device="hip", n=1, cin=cin, h=12, w=12, cout=32, k=3)
+    out = host.hip_lowered(g.text(), 1)
+    assert lowered in out, out
+    if lowered == "conv2d":
+        assert "hip_conv2d_nhwc_internal" not in out

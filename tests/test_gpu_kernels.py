@@ -69,6 +69,31 @@ def test_gemm_matches_oracle(hip, dtype, shape):
     assert_close(got, want, dtype, what=f"gemm {shape}")
 
 
+# Small problems (fewer 64x64 tiles than a quarter of the CUs) and unaligned operands run the sequential kernel:
+# one output per thread with k summed in order in fp32, like the reference CPU kernel, so it matches bit for bit.
+SEQ_SHAPES = [
+    (64, 784, 256),   # C1 layer 1
+    (64, 256, 10),    # C1 layer 2
+    (64, 512, 1000),  # C4 classifier
+    (128, 128, 128),
+    (300, 264, 200),  # ragged tiles
+    (512, 512, 64),
+    (1, 8, 8),
+    (3, 1, 5),        # K = 1
+    (7, 131, 3),      # K tail shorter than one 4-wide step
+]
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16, F16])
+@pytest.mark.parametrize("shape", SEQ_SHAPES)
+def test_gemm_small_bit_exact(hip, dtype, shape):
+    m, k, n = shape
+    say(f"gemm small dtype={dtype} m={m} k={k} n={n}")
+    a = synth.tensor(13, (m, k), dtype, "uniform")
+    b = synth.tensor(14, (k, n), dtype, "uniform")
+    assert_bitwise(run_gemm(hip, dtype, a, b), orc.matmul(dtype, a, b), f"small gemm {shape}")
+
+
 def test_gemm_known_answer(hip):
     # reference: tests/cpp/ops/test_op_matmul.cpp:208-230 — [[1,2],[3,4]]·[[5,6],[7,8]] = [[19,22],[43,50]]
     a = np.array([[1, 2], [3, 4]], np.float32)
@@ -212,7 +237,10 @@ def test_softmax_known_answer(hip):
     np.testing.assert_allclose(got, [[0.26894142, 0.73105858]] * 2, rtol=1e-6)
 
 
-@pytest.mark.parametrize("dtype,rows,cols", [(F32, 2, 5), (BF16, 4096, 1024), (F32, 3, 5000), (BF16, 7, 33)])
+# (BF16, 4096, 1024), (BF16, 5, 512), (F16, 9, 2048), (F32, 6, 256/1024/2048) take the 16-byte vector kernel
+@pytest.mark.parametrize("dtype,rows,cols", [(F32, 2, 5), (BF16, 4096, 1024), (F32, 3, 5000), (BF16, 7, 33),
+                                             (BF16, 5, 512), (F16, 9, 2048), (F32, 6, 256), (F32, 6, 1024),
+                                             (F32, 3, 2048)])
 def test_layer_norm(hip, dtype, rows, cols):
     say(f"layer_norm dtype={dtype} {rows}x{cols}")
     x = synth.tensor(71, (rows, cols), dtype, "normal")
@@ -231,6 +259,9 @@ def test_layer_norm(hip, dtype, rows, cols):
     (0, (1, 2, 9, 9, 3, 3, 2, 2, 1, 1)),
     (1, (2, 8, 7, 7, 7, 7, 1, 1, 0, 0)),       # global average pool
     (1, (1, 2, 6, 6, 3, 3, 2, 2, 1, 1)),       # average with padding counted
+    (0, (2, 35000, 2, 2, 2, 2, 2, 2, 0, 0)),   # 70,000 planes: grid rows split over y and z
+    (1, (1, 65537, 2, 2, 2, 2, 2, 2, 0, 0)),   # a prime plane count above 65,535: the general kernel
+    (0, (1, 3, 300, 290, 3, 3, 2, 2, 1, 1)),   # planes spanning several 256-output blocks
 ])
 def test_pool2d(hip, dtype, mode, geom):
     say(f"pool mode={mode} dtype={dtype} {geom}")
@@ -309,7 +340,10 @@ def test_conv2d(hip, dtype, geom, with_bias):
     assert_close(got, want, dtype, what=f"conv {geom}")
 
 
-@pytest.mark.parametrize("itemsize,shape", [(2, (3, 64, 3136)), (2, (5, 70, 9)), (4, (2, 33, 130)), (2, (64, 64, 9))])
+# paths: 16-byte tiles (16-bit, rows and cols multiples of 8; full and partial tiles), gather (rows or cols
+# below 64: filters, thin planes), element tiles (everything else)
+@pytest.mark.parametrize("itemsize,shape", [(2, (3, 64, 3136)), (2, (2, 72, 200)), (2, (5, 70, 9)), (4, (2, 33, 130)),
+                                            (2, (64, 64, 9)), (4, (2, 96, 100)), (2, (2, 70, 130))])
 def test_transpose_batched(hip, itemsize, shape):
     b, r, c = shape
     say(f"transpose_batched itemsize={itemsize} {shape}")
@@ -336,8 +370,16 @@ def to_nhwc(x):
     return np.ascontiguousarray(x.transpose(0, 2, 3, 1))
 
 
-@pytest.mark.parametrize("dtype", [BF16, F16])
-@pytest.mark.parametrize("geom,with_bias", NHWC_CASES)
+# fp32 takes Cin % 16 == 0 (16 channels of 4 bytes per stage): these only it accepts
+NHWC_F32_CASES = [
+    ((1, 16, 10, 10, 48, 3, 3, 1, 1, 1, 1, 1), True),
+    ((2, 48, 7, 9, 64, 3, 3, 2, 1, 1, 1, 1), False),
+]
+
+
+@pytest.mark.parametrize("dtype,geom,with_bias",
+                         [(d, g, b) for d in (BF16, F16, F32) for g, b in NHWC_CASES] +
+                         [(F32, g, b) for g, b in NHWC_F32_CASES])
 def test_conv2d_nhwc(hip, dtype, geom, with_bias):
     say(f"conv nhwc dtype={dtype} {geom} bias={with_bias}")
     n, cin, h, w, cout, kh, kw = geom[:7]
@@ -355,7 +397,7 @@ def test_conv2d_nhwc(hip, dtype, geom, with_bias):
     assert_close(got, want, dtype, what=f"conv nhwc {geom}")
 
 
-@pytest.mark.parametrize("dtype", [BF16])
+@pytest.mark.parametrize("dtype", [BF16, F32])
 def test_conv2d_nhwc_epilogue_add_relu(hip, dtype):
     # conv + bias, then the residual add;relu of a ResNet basic block, rounded between segments
     geom = (2, 64, 14, 14, 64, 3, 3, 1, 1, 1, 1, 1)
@@ -376,9 +418,11 @@ def test_conv2d_nhwc_epilogue_add_relu(hip, dtype):
 
 
 def test_conv2d_nhwc_rejects_unsupported(hip):
-    # Cin % 32 != 0, grouped and fp32 convolutions stay on the direct path
+    # channel counts the stage width does not divide (and no C8 layout for fp32) and grouped convolutions stay
+    # on the direct path
     for dtype, geom in [(BF16, (1, 3, 9, 9, 4, 3, 3, 1, 1, 1, 1, 1)), (BF16, (1, 64, 9, 9, 64, 3, 3, 1, 1, 1, 1, 2)),
-                        (F32, (1, 64, 9, 9, 64, 3, 3, 1, 1, 1, 1, 1))]:
+                        (BF16, (1, 48, 9, 9, 64, 3, 3, 1, 1, 1, 1, 1)), (F32, (1, 24, 9, 9, 64, 3, 3, 1, 1, 1, 1, 1)),
+                        (F32, (1, 8, 9, 9, 64, 3, 3, 1, 1, 1, 1, 1))]:
         assert hip.lib().fh_conv2d_nhwc_supported(dtype, hip.i64_array(geom)) == 0
         status = hip.lib().fh_conv2d_nhwc_fwd(dtype, None, None, None, None, hip.i64_array(geom), None, None)
         assert status == 4, status  # FH_UNIMPLEMENTED
