@@ -43,14 +43,25 @@ class _NativeStream:
         self.ptr = ptr
 
 
-def run_gpu(steps: int, warmup: int):
+def gemm_operands(data: str):
+    """The headline's operands: U(-1,1) (the configuration's data), or all zeros / all ones for the
+    data-dependence check of the engine clock (same kernel, same work, less switching)."""
+    from frame_hip import graphs, synth
+
+    if data == "uniform":
+        return graphs.gemm_inputs(N, BF16)
+    value = 0.0 if data == "zeros" else 1.0
+    return [synth.to_storage(np.full((N, N), value, np.float32), BF16) for _ in range(2)]
+
+
+def run_gpu(steps: int, warmup: int, data: str = "uniform"):
     """Times `steps` runs of the compiled GEMM graph (runtime::compile(graph, "hip") -> Executable::run) on one
     persistent stream, inputs and outputs resident in HBM."""
     from frame_hip import abi, graphs, host
 
     g = graphs.gemm(N, BF16, device="hip")
     exe = host.compile(g, "hip")
-    ins = exe.upload_inputs(graphs.gemm_inputs(N, BF16))
+    ins = exe.upload_inputs(gemm_operands(data))
     outs = exe.alloc_outputs()
     stream = host.Stream("hip")
     native = _NativeStream(stream.native)
@@ -227,6 +238,9 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=128)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="only the headline GEMM (and the CPU baseline)")
+    ap.add_argument("--gemm-data", choices=["uniform", "zeros", "ones"], default="uniform",
+                    help="headline operands; anything but the default (U(-1,1), the configuration's data) is a "
+                         "diagnostic of data-dependent clocks and is labelled as such in the output")
     ap.add_argument("--only", default=None,
                     help="run just this secondary measurement (e.g. c5_transformer) and print it, no headline")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
@@ -242,7 +256,7 @@ def main():
         print(json.dumps({args.only: extras(args.steps, args.only).get(args.only, {"error": "no such entry"})}), flush=True)
         return
 
-    ms, wall = run_gpu(args.steps, args.warmup)
+    ms, wall = run_gpu(args.steps, args.warmup, args.gemm_data)
     tflops = gemm_flops(N, N, N) / (ms * 1e-3) / 1e12
     line = {
         "metric": "GEMM/Conv2d TFLOP/s & % MFMA peak; fused-op GB/s; compiled-graph fwd latency",
@@ -256,7 +270,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic",
+        "data": "synthetic" if args.gemm_data == "uniform" else f"synthetic, diagnostic all-{args.gemm_data} operands",
         "config": {"workload": "dense GEMM C=A·B, M=N=K=4096, bf16 in/out, fp32 accumulate (configs[1])",
                    "M": N, "N": N, "K": N},
         "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
