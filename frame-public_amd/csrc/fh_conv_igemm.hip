@@ -447,16 +447,20 @@ __global__ __launch_bounds__(256) void transpose_wide_kernel(const uint16_t* __r
   }
 }
 
-// Small or thin batched transposes (a filter's [Cin][KH*KW] planes, late-stage activations): one thread per
-// output element, consecutive threads along the output row (writes coalesced, reads at stride `cols`).
+// Small planes (rows * cols <= kPlaneMax, e.g. a filter's [Cin][KH*KW]): one workgroup per batch item moves the
+// whole plane through LDS, reading and writing it contiguously.
+constexpr int kPlaneMax = 8192;
 template <typename E>
-__global__ __launch_bounds__(256) void transpose_gather_kernel(const E* __restrict__ x, E* __restrict__ y, int64_t batch,
-                                                               int64_t rows, int64_t cols) {
-  const int64_t total = batch * rows * cols;
-  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
-  for (int64_t o = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; o < total; o += stride) {
-    const int64_t r = o % rows, bc = o / rows, c = bc % cols, b = bc / cols;
-    y[o] = x[(b * rows + r) * cols + c];
+__global__ __launch_bounds__(256) void transpose_plane_kernel(const E* __restrict__ x, E* __restrict__ y, int32_t rows,
+                                                              int32_t cols) {
+  __shared__ E plane[kPlaneMax];
+  const int n = rows * cols;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * n;
+  for (int i = threadIdx.x; i < n; i += 256) plane[i] = x[base + i];
+  __syncthreads();
+  for (int o = threadIdx.x; o < n; o += 256) {
+    const int c = o / rows, r = o - (o / rows) * rows;
+    y[base + o] = plane[r * cols + c];
   }
 }
 
@@ -524,19 +528,19 @@ extern "C" fh_status fh_transpose_batched(int32_t itemsize, const void* x, void*
   const dim3 grid(static_cast<uint32_t>((cols + 63) / 64), static_cast<uint32_t>((rows + 63) / 64),
                   static_cast<uint32_t>(batch));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (rows < 64 || cols < 64) {
-    const int64_t total = batch * rows * cols;
-    const uint32_t blocks = static_cast<uint32_t>(std::min<int64_t>((total + 255) / 256, 65536));
+  if (rows * cols <= kPlaneMax && batch <= 0x7fffffffLL) {
     if (itemsize == 2) {
-      hipLaunchKernelGGL(transpose_gather_kernel<uint16_t>, dim3(blocks), dim3(256), 0, s, static_cast<const uint16_t*>(x),
-                         static_cast<uint16_t*>(y), batch, rows, cols);
+      hipLaunchKernelGGL(transpose_plane_kernel<uint16_t>, dim3(static_cast<uint32_t>(batch)), dim3(256), 0, s,
+                         static_cast<const uint16_t*>(x), static_cast<uint16_t*>(y), static_cast<int32_t>(rows),
+                         static_cast<int32_t>(cols));
     } else if (itemsize == 4) {
-      hipLaunchKernelGGL(transpose_gather_kernel<uint32_t>, dim3(blocks), dim3(256), 0, s, static_cast<const uint32_t*>(x),
-                         static_cast<uint32_t*>(y), batch, rows, cols);
+      hipLaunchKernelGGL(transpose_plane_kernel<uint32_t>, dim3(static_cast<uint32_t>(batch)), dim3(256), 0, s,
+                         static_cast<const uint32_t*>(x), static_cast<uint32_t*>(y), static_cast<int32_t>(rows),
+                         static_cast<int32_t>(cols));
     } else {
       return fail(FH_INVALID_ARGUMENT, "fh_transpose_batched: itemsize must be 2 or 4");
     }
-    return launch_status("transpose_gather_kernel launch");
+    return launch_status("transpose_plane_kernel launch");
   }
   if (itemsize == 2 && rows % 8 == 0 && cols % 8 == 0 && aligned16(x) && aligned16(y)) {
     hipLaunchKernelGGL(transpose_wide_kernel, grid, dim3(256), 0, s, static_cast<const uint16_t*>(x),

@@ -90,11 +90,80 @@ __global__ __launch_bounds__(256) void pool2d_plane_kernel(const typename Io<T>:
   y[plane_id * ohw + p] = Io<T>::store(MODE == 0 ? acc : acc / denom);
 }
 
+// Max pool 3x3, stride 2, padding 1 on 16-bit data (ResNet's stem pool), W % 16 == 0: one thread per 8
+// consecutive outputs of a row. Each of the 3 input rows is read as two 16-byte vectors (columns 2*ow0 ..
+// 2*ow0 + 15) plus the element left of them, and every window is scanned in the general kernel's order
+// (kh outer, kw inner, strictly greater replaces), so the selected values are the same bits.
+template <typename T>
+__global__ __launch_bounds__(256) void maxpool3s2_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
+                                                         int32_t h, int32_t w, int32_t oh, int32_t ow, int32_t total) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= total) return;
+  const int qn = ow / 8;
+  const int q = idx % qn, t2 = idx / qn;
+  const int o_h = t2 % oh;
+  const int64_t plane = t2 / oh;
+  const int c0 = 16 * q;  // first input column of the 8 windows' centres - 1 ... (2 * ow0)
+  const uint16_t* px = x + plane * h * w;
+  float acc[8];
+  bool found[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    acc[j] = 0.0f;
+    found[j] = false;
+  }
+#pragma unroll
+  for (int a = 0; a < 3; ++a) {
+    const int ih = 2 * o_h - 1 + a;
+    if (ih < 0 || ih >= h) continue;
+    const uint16_t* row = px + static_cast<int64_t>(ih) * w + c0;
+    const uint4 v0 = *reinterpret_cast<const uint4*>(row);
+    const uint4 v1 = *reinterpret_cast<const uint4*>(row + 8);
+    uint16_t e[17];  // e[0] = column c0 - 1, e[1 + k] = column c0 + k
+    __builtin_memcpy(e + 1, &v0, 16);
+    __builtin_memcpy(e + 9, &v1, 16);
+    const bool left = c0 > 0;
+    e[0] = left ? row[-1] : uint16_t{0};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+#pragma unroll
+      for (int b = 0; b < 3; ++b) {
+        const int k = 2 * j + b;  // index into e: column c0 + 2j - 1 + b
+        if (k == 0 && !left) continue;
+        const float v = Io<T>::load(e[k]);
+        if (!found[j] || v > acc[j]) acc[j] = v;
+        found[j] = true;
+      }
+    }
+  }
+  uint16_t o[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j] = Io<T>::store(acc[j]);
+  uint4 out;
+  __builtin_memcpy(&out, o, 16);
+  *reinterpret_cast<uint4*>(y + (plane * oh + o_h) * ow + 8 * q) = out;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
+
 template <typename T>
 fh_status launch_pool(int32_t mode, const void* x, void* y, const PoolGeom& g, hipStream_t s) {
   using S = typename Io<T>::storage;
   const int64_t planes = g.n * g.c;
-  if (g.h * g.w < (int64_t{1} << 31) && g.oh * g.ow < (int64_t{1} << 31) && planes <= int64_t{65535} * 65535) {
+  if constexpr (sizeof(S) == 2) {
+    const int64_t total = planes * g.oh * (g.ow / 8);
+    if (mode == 0 && g.kh == 3 && g.kw == 3 && g.sh == 2 && g.sw == 2 && g.ph == 1 && g.pw == 1 && g.w % 16 == 0 &&
+        g.ow % 8 == 0 && g.ow * 2 == g.w && aligned16(x) && aligned16(y) && total < (int64_t{1} << 31)) {
+      hipLaunchKernelGGL((maxpool3s2_kernel<T>), dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256), 0, s,
+                         static_cast<const uint16_t*>(x), static_cast<uint16_t*>(y), static_cast<int32_t>(g.h),
+                         static_cast<int32_t>(g.w), static_cast<int32_t>(g.oh), static_cast<int32_t>(g.ow),
+                         static_cast<int32_t>(total));
+      return launch_status("maxpool3s2_kernel launch");
+    }
+  }
+  // per-plane grid rows only when a plane fills most of a 256-thread block (a global pool would idle 255 of 256)
+  if (g.oh * g.ow >= 192 && g.h * g.w < (int64_t{1} << 31) && g.oh * g.ow < (int64_t{1} << 31) &&
+      planes <= int64_t{65535} * 65535) {
     const PlaneGeom pg{static_cast<int32_t>(g.h),  static_cast<int32_t>(g.w),  static_cast<int32_t>(g.kh),
                        static_cast<int32_t>(g.kw), static_cast<int32_t>(g.sh), static_cast<int32_t>(g.sw),
                        static_cast<int32_t>(g.ph), static_cast<int32_t>(g.pw), static_cast<int32_t>(g.oh),

@@ -262,6 +262,9 @@ def test_layer_norm(hip, dtype, rows, cols):
     (0, (2, 35000, 2, 2, 2, 2, 2, 2, 0, 0)),   # 70,000 planes: grid rows split over y and z
     (1, (1, 65537, 2, 2, 2, 2, 2, 2, 0, 0)),   # a prime plane count above 65,535: the general kernel
     (0, (1, 3, 300, 290, 3, 3, 2, 2, 1, 1)),   # planes spanning several 256-output blocks
+    (0, (2, 4, 32, 32, 3, 3, 2, 2, 1, 1)),     # 16-bit: the vectorized 3x3 stride-2 kernel
+    (0, (1, 3, 17, 48, 3, 3, 2, 2, 1, 1)),     # same, odd height: the last window's bottom row is padding
+    (1, (2, 64, 7, 7, 7, 7, 1, 1, 0, 0)),      # global average pool, many planes
 ])
 def test_pool2d(hip, dtype, mode, geom):
     say(f"pool mode={mode} dtype={dtype} {geom}")
@@ -284,6 +287,22 @@ def test_maxpool_ties_and_neg_inf_padding(hip):
     dx, dy = dev(hip, x), hip.DeviceBuffer(want.nbytes)
     hip.check(hip.lib().fh_pool2d(F32, 0, dx.value, dy.value, hip.i64_array(geom), None))
     assert_bitwise(dy.download(want.shape, np.float32), want, "maxpool ties")
+
+
+@pytest.mark.parametrize("dtype", [BF16, F16])
+def test_maxpool3s2_signed_zero_and_nan_selection(hip, dtype):
+    # the vectorized 3x3 stride-2 kernel keeps the scan order: of equal +0/-0 the first stays, NaN first stays
+    x = synth.tensor(85, (1, 2, 16, 32), dtype, "normal")
+    neg0, pos0, nan = (synth.to_storage(np.array([v], np.float32), dtype)[0] for v in (-0.0, 0.0, np.nan))
+    x[0, 0] = pos0
+    x[0, 0, 0::2, 0::2] = neg0        # window origins -0: later +0 must not replace them
+    x[0, 1, :4, :4] = nan             # NaN scanned first in its windows
+    x[0, 1, 5, 7] = nan
+    geom = (1, 2, 16, 32, 3, 3, 2, 2, 1, 1)
+    want = orc.pool2d(dtype, 0, x, geom)
+    dx, dy = dev(hip, x), hip.DeviceBuffer(want.nbytes)
+    hip.check(hip.lib().fh_pool2d(dtype, 0, dx.value, dy.value, hip.i64_array(geom), None))
+    assert_bitwise(dy.download(want.shape, want.dtype), want, "maxpool3s2 ties")
 
 
 def test_permute_copy_fill(hip):
@@ -340,10 +359,11 @@ def test_conv2d(hip, dtype, geom, with_bias):
     assert_close(got, want, dtype, what=f"conv {geom}")
 
 
-# paths: 16-byte tiles (16-bit, rows and cols multiples of 8; full and partial tiles), gather (rows or cols
-# below 64: filters, thin planes), element tiles (everything else)
+# paths: whole planes through LDS (rows * cols <= 8192: filters), 16-byte tiles (16-bit, rows and cols multiples
+# of 8; full and partial tiles), element tiles (everything else, e.g. thin late-stage activations)
 @pytest.mark.parametrize("itemsize,shape", [(2, (3, 64, 3136)), (2, (2, 72, 200)), (2, (5, 70, 9)), (4, (2, 33, 130)),
-                                            (2, (64, 64, 9)), (4, (2, 96, 100)), (2, (2, 70, 130))])
+                                            (2, (64, 64, 9)), (4, (2, 96, 100)), (2, (2, 70, 130)),
+                                            (2, (2, 512, 49)), (2, (3, 64, 128)), (4, (3, 512, 9))])
 def test_transpose_batched(hip, itemsize, shape):
     b, r, c = shape
     say(f"transpose_batched itemsize={itemsize} {shape}")
