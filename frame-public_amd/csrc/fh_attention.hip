@@ -6,15 +6,20 @@
 //   O  = round(P · V_bh)                 (matmul)
 // and O lands at rows [b*seq, (b+1)*seq), columns [h*dh, (h+1)*dh) of the output: the layout of the reference's
 // head concat (axis 1) and batch concat (axis 0). Every intermediate is rounded where the reference rounds it;
-// only the summation order (MFMA blocks, a tree for the softmax sum) and the exp routine differ.
+// the summation orders (MFMA blocks, per-lane partial sums), the exp routine and e * (1/s) in place of e / s
+// differ, each well inside one rounding of the stored probabilities.
 //
-// One workgroup (4 waves) per (64-row block, head, batch). LDS: the Q block [64][64], K_bh then V_bh [seq][64]
-// (the same buffer, reused), and the score / probability rows [64][seq], all bf16/f16:
-//   1. Q block and K_bh -> LDS (global_load_lds_dwordx4), rows k-contiguous, 16-byte chunks swizzled by row.
-//   2. S: waves 2 x 2 (32 rows x seq/2 keys each) on v_mfma_f32_32x32x16; both operands k-contiguous in LDS.
-//      Rounded twice (product, scale) into the score rows.
-//   3. V_bh -> LDS (overlapping the softmax); softmax per row, one row per wave at a time, wave reductions.
-//   4. O: waves 2 x 2 (32 rows x 32 columns), A = probability rows, B = V through ds_read_b64_tr_b16.
+// One wave owns 32 queries and all seq keys; a workgroup is W waves (4, or 2 when seq is not a multiple of 128).
+//  1. Scores transposed, Sᵀ = K·Qᵀ on v_mfma_f32_32x32x16, per 64-key block: K blocks stream through a
+//     double-buffered 8 KB LDS ring (global_load_lds_dwordx4, 16-byte chunks swizzled by row), the Q fragments
+//     stay in registers. Each lane's accumulator then holds one query and 16 keys of a 32-key tile; they are
+//     rounded, scaled, rounded and kept as packed bf16/f16 in registers (seq/2 values per lane), with the
+//     running maximum.
+//  2. m and s = sum exp(S2 - m) per query: the lane's values plus its partner lane (lane ^ 32, same query).
+//  3. Oᵀ = Vᵀ·Pᵀ: p = round(exp(S2 - m) * (1/s)) is produced in registers already in the B-operand layout
+//     (k = the lane's 8 keys of one query, in the accumulator's key order); the A operand (Vᵀ) comes from V
+//     blocks in LDS through ds_read_b64_tr_b16 in the same key order. V streams like K did.
+// LDS: 32 KB per workgroup (two K and two V blocks), so two workgroups share a CU.
 #include <hip/hip_runtime.h>
 
 #include <string>
@@ -29,168 +34,180 @@ namespace {
 using namespace mfma16;
 
 constexpr int kDh = 64;      // head dim
-constexpr int kRows = 64;    // query rows per workgroup
 constexpr int kMaxSeq = 512;
 
 typedef short s16x4_t __attribute__((ext_vector_type(4)));
 
-// 16-byte chunk swizzles: Q/K rows (8 chunks) by row & 7; score rows (seq/8 chunks) by row & pmask, pmask = 15
-// when the chunk count is a multiple of 16 (16 rows of one ds_read_b128 phase hit 16 distinct 16-byte bank
-// groups), else 7 (the count is a multiple of 8, so the swizzled chunk stays inside the row); V rows (8 chunks)
-// for transpose reads as in the GEMM.
-__device__ __forceinline__ int qk_chunk(int row, int c) { return c ^ (row & 7); }
-__device__ __forceinline__ int p_chunk(int row, int c, int pmask) { return c ^ (row & pmask); }
-__device__ __forceinline__ int v_chunk(int krow, int c) { return c ^ (2 * (krow & 3)); }
+// 16-byte chunk swizzles of a 128-byte LDS row: K rows by row & 7 (the 32 rows of one fragment read spread over
+// the banks); V rows by 2 * (row & 3) for the transpose reads (4 consecutive rows hit disjoint 32-byte windows).
+__device__ __forceinline__ int k_chunk(int row, int c) { return c ^ (row & 7); }
+__device__ __forceinline__ int v_chunk(int row, int c) { return c ^ (2 * (row & 3)); }
 
 template <typename T>
-__global__ __launch_bounds__(256) void attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
-                                                        const uint16_t* __restrict__ v, uint16_t* __restrict__ out,
-                                                        int seq, int heads, float scale) {
-  __shared__ __attribute__((aligned(1024))) unsigned char qs[kRows * kDh * 2];
-  __shared__ __attribute__((aligned(1024))) unsigned char kv[kMaxSeq * kDh * 2];
-  __shared__ __attribute__((aligned(1024))) unsigned char ps[kRows * kMaxSeq * 2];
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return static_cast<uint32_t>(Io<T>::store(lo)) | (static_cast<uint32_t>(Io<T>::store(hi)) << 16);
+}
+template <typename T>
+__device__ __forceinline__ float lo16(uint32_t v) { return Io<T>::load(static_cast<uint16_t>(v & 0xffffu)); }
+template <typename T>
+__device__ __forceinline__ float hi16(uint32_t v) { return Io<T>::load(static_cast<uint16_t>(v >> 16)); }
+
+template <typename T, int NB, int W>
+__global__ __launch_bounds__(W * 64, 2) void attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
+                                                              const uint16_t* __restrict__ v, uint16_t* __restrict__ out,
+                                                              int heads, float scale) {
+  constexpr int SEQ = NB * 64;
+  constexpr int NT = SEQ / 32;  // 32-key tiles
+  constexpr int BLK = 64 * 128;  // one 64-key block of K or V, bytes
+  constexpr int LOADS = 8 / W;   // 1 KB global->LDS instructions per wave and block
+  __shared__ __attribute__((aligned(1024))) unsigned char kb[2 * BLK];
+  __shared__ __attribute__((aligned(1024))) unsigned char vb[2 * BLK];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave >> 1, wn = wave & 1;
   const int l32 = lane & 31, hi = lane >> 5;
-  const int r0 = blockIdx.x * kRows, h = blockIdx.y, b = blockIdx.z;
-  const int64_t ld = static_cast<int64_t>(heads) * kDh;        // row stride of q/k/v/out (elements)
-  const int64_t base = (static_cast<int64_t>(b) * seq) * ld + static_cast<int64_t>(h) * kDh;
-  const int pchunks = seq / 8;                                  // 16-byte chunks per score row
-  const int pmask = (pchunks & 15) == 0 ? 15 : 7;
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int q0 = blockIdx.x * (32 * W) + wave * 32;
+  const int64_t ld = static_cast<int64_t>(heads) * kDh;
+  const int64_t base = (static_cast<int64_t>(b) * SEQ) * ld + static_cast<int64_t>(h) * kDh;
 
-  // ---- 1. Q block and K_bh into LDS: one wave instruction = 8 rows of 128 B ----
-  {
-    const int row_in = lane >> 3, pc = lane & 7;  // lane -> (row within the 8, physical chunk)
-    for (int i = wave; i < kRows / 8; i += 4) {
-      const int row = i * 8 + row_in;
-      const uint16_t* src = q + base + static_cast<int64_t>(r0 + row) * ld + qk_chunk(row, pc) * 8;
-      __builtin_amdgcn_global_load_lds(src, (FH_LDS void*)(qs + i * 1024), 16, 0, 0);
-    }
-    for (int i = wave; i < seq / 8; i += 4) {
-      const int row = i * 8 + row_in;
-      const uint16_t* src = k + base + static_cast<int64_t>(row) * ld + qk_chunk(row, pc) * 8;
-      __builtin_amdgcn_global_load_lds(src, (FH_LDS void*)(kv + i * 1024), 16, 0, 0);
-    }
-  }
-  wait_vmcnt<0>();
-  __syncthreads();
+  // Q fragments (B operand of Sᵀ = K·Qᵀ): lane -> query q0 + l32, d = 16 s + 8 hi .. + 7
+  u32x4_t qf[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    qf[s] = *reinterpret_cast<const u32x4_t*>(q + base + static_cast<int64_t>(q0 + l32) * ld + 16 * s + 8 * hi);
 
-  // ---- 2. S = Q K^T for rows wm*32.., keys wn*(seq/2).. ; rounded, scaled, rounded, into the score rows ----
-  {
-    const int keys_per_wave = seq / 2;
-    const int tiles = keys_per_wave / 32;  // <= 8
-    f32x16_t acc[8];
+  // block loaders: instruction i of a block = rows 8i .. 8i + 7, lane -> (row 8i + lane / 8, physical chunk lane % 8)
+  auto load_block = [&](const uint16_t* src, unsigned char* ring, int blk, int buf, bool is_v) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < LOADS; ++j) {
+      const int i = wave + W * j;
+      const int row = 8 * i + (lane >> 3), pc = lane & 7;
+      const int c = is_v ? v_chunk(row, pc) : k_chunk(row, pc);
+      const uint16_t* g = src + base + static_cast<int64_t>(blk * 64 + row) * ld + c * 8;
+      __builtin_amdgcn_global_load_lds(g, (FH_LDS void*)(ring + buf * BLK + i * 1024), 16, 0, 0);
+    }
+  };
+
+  load_block(k, kb, 0, 0, false);
+  if (NB > 1) load_block(k, kb, 1, 1, false);
+
+  // ---- 1. scores, kept as packed 16-bit values: s2[t][j] = keys (x = 2j, 2j + 1) of tile t ----
+  uint32_t s2[NT][8];
+  float m = -__builtin_inff();
 #pragma unroll
-      for (int x = 0; x < 16; ++x) acc[j][x] = 0.0f;
-    const int arow = wm * 32 + l32;
+  for (int blk = 0; blk < NB; ++blk) {
+    if (blk + 1 < NB) wait_vmcnt<LOADS>(); else wait_vmcnt<0>();
+    __syncthreads();
+    const unsigned char* kr = kb + (blk & 1) * BLK;
+    f32x16_t acc[2];
 #pragma unroll
-    for (int s = 0; s < kDh / 16; ++s) {
-      const u32x4_t a = *reinterpret_cast<const u32x4_t*>(qs + arow * 128 + qk_chunk(arow, 2 * s + hi) * 16);
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int x = 0; x < 16; ++x) acc[t][x] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int row = 32 * t + l32;
+        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(kr + row * 128 + k_chunk(row, 2 * s + hi) * 16);
+        mfma32<T>(a, qf[s], acc[t]);
+      }
+    }
+    __syncthreads();  // every wave is done with this K buffer
+    if (blk + 2 < NB) load_block(k, kb, blk + 2, blk & 1, false);
+    if (blk + 1 == NB) {  // the K stream is over: start V
+      load_block(v, vb, 0, 0, true);
+      if (NB > 1) load_block(v, vb, 1, 1, true);
+    }
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        if (j < tiles) {
-          const int key = wn * keys_per_wave + j * 32 + l32;
-          const u32x4_t bf = *reinterpret_cast<const u32x4_t*>(kv + key * 128 + qk_chunk(key, 2 * s + hi) * 16);
-          mfma32<T>(a, bf, acc[j]);
+        const float a0 = Io<T>::round(Io<T>::round(acc[t][2 * j]) * scale);
+        const float a1 = Io<T>::round(Io<T>::round(acc[t][2 * j + 1]) * scale);
+        m = fmaxf(m, fmaxf(a0, a1));
+        s2[2 * blk + t][j] = pack2<T>(a0, a1);
+        asm volatile("" : "+v"(s2[2 * blk + t][j]));  // later passes unpack; nothing of a0, a1 stays live
+      }
+  }
+  m = fmaxf(m, __shfl_xor(m, 32));
+
+  // ---- 2. row sums ----
+  float sum = 0.0f;
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sum += __expf(lo16<T>(s2[t][j]) - m) + __expf(hi16<T>(s2[t][j]) - m);
+  sum += __shfl_xor(sum, 32);
+  const float r = 1.0f / sum;
+  // The packed scores are all pass 3 reads: tie them so the compiler recomputes the unpacking and exp there
+  // instead of keeping pass 2's seq/2 float values alive (which would not fit the register file).
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(s2[t][j]));
+
+  // ---- 3. Oᵀ = Vᵀ·Pᵀ, two 32-row d tiles ----
+  f32x16_t acc_o[2];
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int x = 0; x < 16; ++x) acc_o[dt][x] = 0.0f;
+  // transpose reads: group g = lane / 16 covers d columns 16 (g & 1) .. + 15 of a d tile and the key half
+  // g >> 1; source lane qd + 4 e of the group points at key row (kbase + e), columns n0 + 4 qd .. + 3
+  const int g = lane >> 4, rr = lane & 15, qd = rr & 3, e = rr >> 2;
+#pragma unroll
+  for (int blk = 0; blk < NB; ++blk) {
+    if (blk + 1 < NB) wait_vmcnt<LOADS>(); else wait_vmcnt<0>();
+    __syncthreads();
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+      const int t = 2 * blk + tt;
+      u32x4_t pf[2];
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          uint32_t w = s2[t][4 * hf + j];
+          asm volatile("" : "+v"(w));  // keeps the exp of this tile here, after the block's barrier
+          pf[hf][j] = pack2<T>(__expf(lo16<T>(w) - m) * r, __expf(hi16<T>(w) - m) * r);
+        }
+#pragma unroll
+      for (int dt = 0; dt < 2; ++dt) {
+        const int n0 = 32 * dt + 16 * (g & 1) + 4 * qd;
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) {
+          // keys of this MFMA for k-half g >> 1: 32 tt + 16 hf + 4 (g >> 1) + {0..3, 8..11}
+          u32x4_t a;
+#pragma unroll
+          for (int part = 0; part < 2; ++part) {
+            const int krow = 32 * tt + 16 * hf + 4 * (g >> 1) + 8 * part + e;
+            const uint32_t off = krow * 128 + v_chunk(krow, n0 >> 3) * 16 + (n0 & 7) * 2;
+            const s16x4_t tr = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FH_LDS s16x4_t*)(vb + (blk & 1) * BLK + off));
+            const u32x2_t t2 = __builtin_bit_cast(u32x2_t, tr);
+            a[2 * part] = t2[0];
+            a[2 * part + 1] = t2[1];
+          }
+          mfma32<T>(a, pf[hf], acc_o[dt]);
         }
       }
     }
-    uint16_t* prow = reinterpret_cast<uint16_t*>(ps);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      if (j < tiles) {
-        const int col = wn * keys_per_wave + j * 32 + l32;
-#pragma unroll
-        for (int x = 0; x < 16; ++x) {
-          const int row = wm * 32 + 8 * (x >> 2) + 4 * hi + (x & 3);
-          const float s1 = Io<T>::round(acc[j][x]);
-          prow[row * seq + p_chunk(row, col >> 3, pmask) * 8 + (col & 7)] = Io<T>::store(s1 * scale);
-        }
-      }
-    }
+    __syncthreads();
+    if (blk + 2 < NB) load_block(v, vb, blk + 2, blk & 1, true);
   }
-  __syncthreads();  // score rows complete; K no longer read
 
-  // ---- 3. V_bh into LDS (rows = keys, n-contiguous, chunks swizzled for transpose reads), then softmax ----
-  {
-    const int row_in = lane >> 3, pc = lane & 7;
-    for (int i = wave; i < seq / 8; i += 4) {
-      const int row = i * 8 + row_in;
-      const uint16_t* src = v + base + static_cast<int64_t>(row) * ld + v_chunk(row, pc) * 8;
-      __builtin_amdgcn_global_load_lds(src, (FH_LDS void*)(kv + i * 1024), 16, 0, 0);
+  // ---- output: acc_o[dt][x] = O[query q0 + l32][d = 32 dt + 8 (x / 4) + 4 hi + x % 4] ----
+  uint16_t* orow = out + base + static_cast<int64_t>(q0 + l32) * ld;
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      u32x2_t w;
+      w[0] = pack2<T>(acc_o[dt][4 * gq], acc_o[dt][4 * gq + 1]);
+      w[1] = pack2<T>(acc_o[dt][4 * gq + 2], acc_o[dt][4 * gq + 3]);
+      *reinterpret_cast<u32x2_t*>(orow + 32 * dt + 8 * gq + 4 * hi) = w;
     }
-  }
-  {
-    uint16_t* prow = reinterpret_cast<uint16_t*>(ps);
-    for (int row = wave; row < kRows; row += 4) {
-      float e[8];
-      const bool mine = lane < pchunks;
-      uint4 w = make_uint4(0, 0, 0, 0);
-      if (mine) w = *reinterpret_cast<const uint4*>(prow + row * seq + p_chunk(row, lane, pmask) * 8);
-      uint16_t raw[8];
-      __builtin_memcpy(raw, &w, 16);
-      float m = -__builtin_inff();
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        e[i] = Io<T>::load(raw[i]);
-        if (mine) m = fmaxf(m, e[i]);
-      }
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) m = fmaxf(m, __shfl_xor(m, off));
-      float sum = 0.0f;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        e[i] = mine ? expf(e[i] - m) : 0.0f;
-        sum += e[i];
-      }
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off);
-      if (mine) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) raw[i] = Io<T>::store(e[i] / sum);
-        __builtin_memcpy(&w, raw, 16);
-        *reinterpret_cast<uint4*>(prow + row * seq + p_chunk(row, lane, pmask) * 8) = w;
-      }
-    }
-  }
-  wait_vmcnt<0>();  // this wave's V rows have landed
-  __syncthreads();
-
-  // ---- 4. O = P V: rows wm*32.., columns wn*32.. ----
-  {
-    f32x16_t acc;
-#pragma unroll
-    for (int x = 0; x < 16; ++x) acc[x] = 0.0f;
-    const int arow = wm * 32 + l32;
-    // transpose reads: group g = lane/16 covers 16 columns and 4 k; lane r = qd + 4e of the group points at
-    // row (kbase + e), columns n + 4 qd .. n + 4 qd + 3
-    const int g = lane >> 4, r = lane & 15, qd = r & 3, e = r >> 2;
-    const int ncol = wn * 32 + 16 * (g & 1) + 4 * qd;
-    for (int t = 0; t < seq / 16; ++t) {
-      const u32x4_t a = *reinterpret_cast<const u32x4_t*>(ps + arow * seq * 2 + p_chunk(arow, 2 * t + hi, pmask) * 16);
-      u32x4_t bf;
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const int krow = 16 * t + 8 * (g >> 1) + 4 * half + e;
-        const int off = krow * 128 + v_chunk(krow, ncol >> 3) * 16 + (ncol & 7) * 2;
-        const s16x4_t tr = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FH_LDS s16x4_t*)(kv + off));
-        const u32x2_t t2 = __builtin_bit_cast(u32x2_t, tr);
-        bf[2 * half] = t2[0];
-        bf[2 * half + 1] = t2[1];
-      }
-      mfma32<T>(a, bf, acc);
-    }
-    const int col = h * kDh + wn * 32 + l32;
-#pragma unroll
-    for (int x = 0; x < 16; ++x) {
-      const int row = r0 + wm * 32 + 8 * (x >> 2) + 4 * hi + (x & 3);
-      out[(static_cast<int64_t>(b) * seq + row) * ld + col] = Io<T>::store(acc[x]);
-    }
-  }
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -201,7 +218,7 @@ bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 
 using namespace fh;
 
 extern "C" int32_t fh_attention_supported(int32_t dtype, int64_t seq, int64_t dh) {
-  return (dtype == FH_BF16 || dtype == FH_F16) && dh == kDh && seq >= kRows && seq <= kMaxSeq && seq % kRows == 0 ? 1 : 0;
+  return (dtype == FH_BF16 || dtype == FH_F16) && dh == kDh && seq >= 64 && seq <= kMaxSeq && seq % 64 == 0 ? 1 : 0;
 }
 
 extern "C" fh_status fh_attention_fwd(int32_t dtype, const void* q, const void* k, const void* v, void* out, int64_t batch,
@@ -212,18 +229,34 @@ extern "C" fh_status fh_attention_fwd(int32_t dtype, const void* q, const void* 
   if (batch == 0) return FH_OK;
   if (q == nullptr || k == nullptr || v == nullptr || out == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_attention_fwd: null pointer");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v)) return fail(FH_INVALID_ARGUMENT, "fh_attention_fwd: q/k/v must be 16-byte aligned");
-  const dim3 grid(static_cast<uint32_t>(seq / kRows), static_cast<uint32_t>(heads), static_cast<uint32_t>(batch));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const auto* qq = static_cast<const uint16_t*>(q);
   const auto* kk = static_cast<const uint16_t*>(k);
   const auto* vv = static_cast<const uint16_t*>(v);
   auto* oo = static_cast<uint16_t*>(out);
-  if (dtype == FH_BF16) {
-    hipLaunchKernelGGL(attention_kernel<bf16_t>, grid, dim3(256), 0, s, qq, kk, vv, oo, static_cast<int>(seq),
-                       static_cast<int>(heads), scale);
-  } else {
-    hipLaunchKernelGGL(attention_kernel<f16_t>, grid, dim3(256), 0, s, qq, kk, vv, oo, static_cast<int>(seq),
-                       static_cast<int>(heads), scale);
+  const int nb = static_cast<int>(seq / 64);
+  const int w = seq % 128 == 0 ? 4 : 2;
+  const dim3 grid(static_cast<uint32_t>(seq / (32 * w)), static_cast<uint32_t>(heads), static_cast<uint32_t>(batch));
+  const bool bf = dtype == FH_BF16;
+  const int hd = static_cast<int>(heads);
+  auto go = [&]<int NB>() {
+    constexpr int W = (NB * 64) % 128 == 0 ? 4 : 2;
+    if (bf) {
+      hipLaunchKernelGGL((attention_kernel<bf16_t, NB, W>), grid, dim3(W * 64), 0, s, qq, kk, vv, oo, hd, scale);
+    } else {
+      hipLaunchKernelGGL((attention_kernel<f16_t, NB, W>), grid, dim3(W * 64), 0, s, qq, kk, vv, oo, hd, scale);
+    }
+  };
+  switch (nb) {
+    case 1: go.template operator()<1>(); break;
+    case 2: go.template operator()<2>(); break;
+    case 3: go.template operator()<3>(); break;
+    case 4: go.template operator()<4>(); break;
+    case 5: go.template operator()<5>(); break;
+    case 6: go.template operator()<6>(); break;
+    case 7: go.template operator()<7>(); break;
+    default: go.template operator()<8>(); break;
   }
+  (void)w;
   return launch_status("attention_kernel launch");
 }

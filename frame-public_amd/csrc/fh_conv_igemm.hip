@@ -375,18 +375,29 @@ fh_status launch_conv(ConvNhwcArgs a, hipStream_t stream) {
   return launch_status("conv_nhwc_kernel launch");
 }
 
-// Largest tile that still gives every CU a workgroup; otherwise the one with the most workgroups.
+// Tile choice, from measurements of the ResNet layer shapes on an MI355X (bf16, 3x3, batch 64): by output
+// channels M and output pixels P, the per-layer best of {64x256, 64x128, 64x64, 128x128, 128x256}:
+//   M <= 64: 64x128 when P >= 150K (56x56 at batch 64: 35.4 us vs 37.5 for 64x256), else 64x256 (C3: 20.7 vs 22.2);
+//   M == 128: 128x256 (28x28: 22.9 us vs 25.5 for 128x128);  M in (128, 256]: 128x128 (14x14: 31.0 vs 34.9);
+//   larger M: 64x64 (7x7 at 512 channels: 40.1 us vs 42.0 for 64x128).
+// Every choice keeps at least as many tiles as a quarter of the CUs; otherwise the smallest tile.
 template <typename T, bool C8>
 fh_status dispatch_conv(const ConvNhwcArgs& a, hipStream_t stream) {
   const int64_t cus = device_cu_count();
   auto tiles = [&](int64_t bm, int64_t bn) { return ((a.cout + bm - 1) / bm) * ((a.p + bn - 1) / bn); };
-  // fp32 wave tiles of 64x64 would not fit the ring for staging the epilogue: no 128x256 tile for fp32
-  if constexpr (sizeof(typename Io<T>::storage) == 2) {
-    if (a.cout >= 128 && tiles(128, 256) >= cus) return launch_conv<T, 128, 256, 2, 4, C8>(a, stream);
+  auto enough = [&](int64_t bm, int64_t bn) { return tiles(bm, bn) * 4 >= cus; };
+  constexpr bool k16 = sizeof(typename Io<T>::storage) == 2;  // fp32 wave tiles of 64x64 do not fit the ring
+  if (a.cout <= 64) {
+    if (a.p < 150000 && enough(64, 256)) return launch_conv<T, 64, 256, 1, 4, C8>(a, stream);
+    if (enough(64, 128)) return launch_conv<T, 64, 128, 2, 2, C8>(a, stream);
+  } else if (a.cout <= 128) {
+    if constexpr (k16) {
+      if (enough(128, 256)) return launch_conv<T, 128, 256, 2, 4, C8>(a, stream);
+    }
+    if (enough(128, 128)) return launch_conv<T, 128, 128, 2, 4, C8>(a, stream);
+  } else if (a.cout <= 256) {
+    if (enough(128, 128)) return launch_conv<T, 128, 128, 2, 4, C8>(a, stream);
   }
-  if (a.cout >= 128 && tiles(128, 128) >= cus) return launch_conv<T, 128, 128, 2, 4, C8>(a, stream);
-  if (tiles(64, 256) >= cus) return launch_conv<T, 64, 256, 1, 4, C8>(a, stream);
-  if (tiles(64, 128) >= cus) return launch_conv<T, 64, 128, 2, 2, C8>(a, stream);
   return launch_conv<T, 64, 64, 2, 2, C8>(a, stream);
 }
 
