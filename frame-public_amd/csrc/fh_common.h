@@ -116,6 +116,28 @@ struct Io<f16_t> {
   __device__ static float round(float v) { return f16_bits_to_float(float_to_f16_bits(v)); }
 };
 
+// gelu(x) = 0.5 x (1 + erf(x / sqrt 2)), with 1 + erf(z) = 2 - erfc(|z|) for x >= 0 and erfc(|z|) for x < 0, and
+// erfc from the Chebyshev fit of Numerical Recipes in C (2nd ed., section 6.2, erfcc; fractional error below
+// 1.2e-7 for all z): erfc(z) = t exp(-z^2 + P(t)), t = 1 / (1 + z / 2). In fp32 the result is within 1e-6
+// relative of the exact function for |x| < 5 (7e-6 at x = -10, where exp(-z^2) itself limits), and it keeps
+// relative accuracy in the negative tail, where 1 + erff(z) cancels to zero. About 20 instructions, no branch.
+__device__ inline float gelu_erfc(float x) {
+  const float z = __builtin_fabsf(x) * 0.70710678118654752440f;
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.5f, z, 1.0f));
+  float p = 0.17087277f;
+  p = __builtin_fmaf(p, t, -0.82215223f);
+  p = __builtin_fmaf(p, t, 1.48851587f);
+  p = __builtin_fmaf(p, t, -1.13520398f);
+  p = __builtin_fmaf(p, t, 0.27886807f);
+  p = __builtin_fmaf(p, t, -0.18628806f);
+  p = __builtin_fmaf(p, t, 0.09678418f);
+  p = __builtin_fmaf(p, t, 0.37409196f);
+  p = __builtin_fmaf(p, t, 1.00002368f);
+  p = __builtin_fmaf(p, t, -1.26551223f);
+  const float erfc_z = t * __expf(__builtin_fmaf(-z, z, p));
+  return 0.5f * x * (x >= 0.0f ? 2.0f - erfc_z : erfc_z);
+}
+
 // Elementwise sub-op semantics, all in fp32 (reference: src/backends/cpu/kernels/elementwise.cpp:146-331).
 // relu keeps NaN and -0.0 exactly like std::max(x, 0.0f): returns x unless x < 0.
 __device__ inline float ew_unary(uint8_t op, float x) {
@@ -125,7 +147,7 @@ __device__ inline float ew_unary(uint8_t op, float x) {
     case FH_EW_SQUARE:
       return x * x;
     case FH_EW_GELU:
-      return 0.5f * x * (1.0f + erff(x * 0.70710678118654752440f));
+      return gelu_erfc(x);
     default:
       return x;
   }
@@ -136,6 +158,73 @@ __device__ inline float ew_binary(uint8_t op, float a, float b) {
 }
 
 __host__ __device__ inline bool ew_is_binary(uint8_t op) { return op == FH_EW_ADD || op == FH_EW_MUL; }
+
+// The fused elementwise program of a GEMM / conv epilogue (EpilogueArgs, ConvEpilogue: nseg, round_between,
+// ops[], ins[]): segment s applies ops[s] to the running value, a binary op taking its second operand from
+// ins[s] at the output's index, rounding to T after each segment when round_between is set. The op codes are
+// read as one scalar word and the segments are unrolled with static indices: a runtime-indexed ops[s] / ins[s]
+// would load the kernel argument from memory for every value.
+template <typename EP>
+__device__ __forceinline__ uint64_t epilogue_ops_word(const EP& ep) {
+  static_assert(sizeof(ep.ops) == sizeof(uint64_t), "eight one-byte op codes");
+  uint64_t w;
+  __builtin_memcpy(&w, ep.ops, sizeof(w));
+  return w;
+}
+
+template <typename T, typename EP>
+__device__ __forceinline__ float epilogue_one(const EP& ep, float v, int64_t idx) {
+  using S = typename Io<T>::storage;
+  const uint64_t opw = epilogue_ops_word(ep);
+#pragma unroll
+  for (int s = 0; s < FH_MAX_SEGMENTS; ++s) {
+    if (s >= ep.nseg) break;
+    const uint8_t op = static_cast<uint8_t>(opw >> (8 * s));
+    if (ew_is_binary(op)) {
+      v = ew_binary(op, v, Io<T>::load(static_cast<const S*>(ep.ins[s])[idx]));
+    } else {
+      v = ew_unary(op, v);
+    }
+    if (ep.round_between) v = Io<T>::round(v);
+  }
+  return v;
+}
+
+// Same program on one 16-byte vector of consecutive outputs starting at index idx (16-byte aligned operands).
+template <typename T, typename EP>
+__device__ __forceinline__ uint4 epilogue_vec(const EP& ep, uint4 packed, int64_t idx) {
+  using S = typename Io<T>::storage;
+  constexpr int V = 16 / static_cast<int>(sizeof(S));
+  S vals[V];
+  __builtin_memcpy(vals, &packed, 16);
+  float v[V];
+#pragma unroll
+  for (int x = 0; x < V; ++x) v[x] = Io<T>::load(vals[x]);
+  const uint64_t opw = epilogue_ops_word(ep);
+#pragma unroll
+  for (int s = 0; s < FH_MAX_SEGMENTS; ++s) {
+    if (s >= ep.nseg) break;
+    const uint8_t op = static_cast<uint8_t>(opw >> (8 * s));
+    if (ew_is_binary(op)) {
+      const uint4 in = *reinterpret_cast<const uint4*>(static_cast<const S*>(ep.ins[s]) + idx);
+      S iv[V];
+      __builtin_memcpy(iv, &in, 16);
+#pragma unroll
+      for (int x = 0; x < V; ++x) v[x] = ew_binary(op, v[x], Io<T>::load(iv[x]));
+    } else {
+#pragma unroll
+      for (int x = 0; x < V; ++x) v[x] = ew_unary(op, v[x]);
+    }
+    if (ep.round_between) {
+#pragma unroll
+      for (int x = 0; x < V; ++x) v[x] = Io<T>::round(v[x]);
+    }
+  }
+#pragma unroll
+  for (int x = 0; x < V; ++x) vals[x] = Io<T>::store(v[x]);
+  __builtin_memcpy(&packed, vals, 16);
+  return packed;
+}
 
 inline int device_cu_count() {
   static int cached = 0;

@@ -21,17 +21,7 @@ struct ConvEpilogue {
 // Runs the epilogue program on one rounded conv output value at flat output index `idx` (NCHW).
 template <typename T>
 __device__ __forceinline__ float conv_epilogue(const ConvEpilogue& ep, float v, int64_t idx) {
-  using S = typename Io<T>::storage;
-  for (int s = 0; s < ep.nseg; ++s) {
-    const uint8_t op = ep.ops[s];
-    if (ew_is_binary(op)) {
-      v = ew_binary(op, v, Io<T>::load(static_cast<const S*>(ep.ins[s])[idx]));
-    } else {
-      v = ew_unary(op, v);
-    }
-    if (ep.round_between) v = Io<T>::round(v);
-  }
-  return v;
+  return epilogue_one<T>(ep, v, idx);
 }
 
 }  // namespace fh

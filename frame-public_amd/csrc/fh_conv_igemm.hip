@@ -73,21 +73,6 @@ __device__ __forceinline__ void fence_kfragments(KFragments<TM, TN>& f) {
   for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(f.b[j]));
 }
 
-template <typename T>
-__device__ __forceinline__ float apply_epilogue_one(const EpilogueArgs& ep, float v, int64_t idx) {
-  using S = typename Io<T>::storage;
-  for (int s = 0; s < ep.nseg; ++s) {
-    const uint8_t op = ep.ops[s];
-    if (ew_is_binary(op)) {
-      v = ew_binary(op, v, Io<T>::load(static_cast<const S*>(ep.ins[s])[idx]));
-    } else {
-      v = ew_unary(op, v);
-    }
-    if (ep.round_between) v = Io<T>::round(v);
-  }
-  return v;
-}
-
 template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, bool C8>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNhwcArgs args) {
   using S = typename Io<T>::storage;
@@ -348,7 +333,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
     if (args.vec_store && p0 + V <= args.p) {
       const int64_t img = p0 / args.howo;
       const int64_t idx = (img * args.cout + co) * args.howo + (p0 - img * args.howo);
-      if (args.ep.nseg > 0) packed = apply_epilogue_vec<T>(args.ep, packed, idx);
+      if (args.ep.nseg > 0) packed = epilogue_vec<T>(args.ep, packed, idx);
       *reinterpret_cast<uint4*>(Y + idx) = packed;
     } else {
       S vals[V];
@@ -358,7 +343,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
         const int64_t img = p / args.howo;
         const int64_t idx = (img * args.cout + co) * args.howo + (p - img * args.howo);
         S v = vals[e];
-        if (args.ep.nseg > 0) v = Io<T>::store(apply_epilogue_one<T>(args.ep, Io<T>::load(v), idx));
+        if (args.ep.nseg > 0) v = Io<T>::store(epilogue_one<T>(args.ep, Io<T>::load(v), idx));
         Y[idx] = v;
       }
     }

@@ -47,23 +47,6 @@ struct GemmTraits<float> {
 
 __device__ __forceinline__ int swz(int row, int chunk) { return chunk ^ ((row ^ (row >> 3)) & 7); }
 
-// Applies the epilogue program to one rounded product value at (row, col).
-template <typename T>
-__device__ __forceinline__ float apply_epilogue(const EpilogueArgs& ep, float v, int64_t idx) {
-  using S = typename Io<T>::storage;
-  for (int s = 0; s < ep.nseg; ++s) {
-    const uint8_t op = ep.ops[s];
-    if (ew_is_binary(op)) {
-      const float e = Io<T>::load(static_cast<const S*>(ep.ins[s])[idx]);
-      v = ew_binary(op, v, e);
-    } else {
-      v = ew_unary(op, v);
-    }
-    if (ep.round_between) v = Io<T>::round(v);
-  }
-  return v;
-}
-
 // Transposes an E x E block of 16-bit values held as E rows of 16 bytes.
 __device__ __forceinline__ void transpose8x8_u16(const uint4 (&in)[8], uint4 (&out)[8]) {
   const uint32_t* src = reinterpret_cast<const uint32_t*>(in);  // src[r*4 + d]
@@ -291,33 +274,7 @@ __global__ __launch_bounds__(256) void gemm_tile_kernel(GemmArgs args) {
       if (kGuard && (row >= M || col >= N)) continue;
       uint4 packed = *reinterpret_cast<const uint4*>(wl + rr * WN + c);
       const int64_t idx = row * ldc + col;
-      if (args.ep.nseg > 0) {
-        S vals[V];
-        __builtin_memcpy(vals, &packed, 16);
-        float v[V];
-#pragma unroll
-        for (int e = 0; e < V; ++e) v[e] = Io<T>::load(vals[e]);
-        for (int s = 0; s < args.ep.nseg; ++s) {
-          const uint8_t op = args.ep.ops[s];
-          if (ew_is_binary(op)) {
-            const uint4 in = *reinterpret_cast<const uint4*>(static_cast<const S*>(args.ep.ins[s]) + idx);
-            S ivals[V];
-            __builtin_memcpy(ivals, &in, 16);
-#pragma unroll
-            for (int e = 0; e < V; ++e) v[e] = ew_binary(op, v[e], Io<T>::load(ivals[e]));
-          } else {
-#pragma unroll
-            for (int e = 0; e < V; ++e) v[e] = ew_unary(op, v[e]);
-          }
-          if (args.ep.round_between) {
-#pragma unroll
-            for (int e = 0; e < V; ++e) v[e] = Io<T>::round(v[e]);
-          }
-        }
-#pragma unroll
-        for (int e = 0; e < V; ++e) vals[e] = Io<T>::store(v[e]);
-        __builtin_memcpy(&packed, vals, 16);
-      }
+      if (args.ep.nseg > 0) packed = epilogue_vec<T>(args.ep, packed, idx);
       *reinterpret_cast<uint4*>(C + idx) = packed;
     }
     if (p + 1 < PASSES) __syncthreads();
@@ -395,7 +352,7 @@ __global__ __launch_bounds__(256) void gemm_seq_kernel(GemmArgs args) {
   if (row < M && col < N) {
     float v = Io<T>::round(acc);
     const int64_t idx = row * args.ldc + col;
-    if (args.ep.nseg > 0) v = apply_epilogue<T>(args.ep, v, idx);
+    if (args.ep.nseg > 0) v = epilogue_one<T>(args.ep, v, idx);
     C[idx] = Io<T>::store(v);
   }
 }

@@ -277,7 +277,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
     if (row < M && col < N) {
       uint4 packed = *reinterpret_cast<const uint4*>(wl + rr * WN + c);
       const int64_t idx = row * ldc + col;
-      if (args.ep.nseg > 0) packed = apply_epilogue_vec<T>(args.ep, packed, idx);
+      if (args.ep.nseg > 0) packed = epilogue_vec<T>(args.ep, packed, idx);
       *reinterpret_cast<uint4*>(C + idx) = packed;
     }
   }

@@ -1,5 +1,5 @@
 // Device helpers shared by the MFMA kernels (fh_gemm16.hip, fh_conv_igemm.hip, fh_attention.hip): MFMA wrapper, explicit
-// wait counts, LDS fragment reads, direct-to-LDS loads, the elementwise epilogue on 16-byte vectors, LDS
+// wait counts, LDS fragment reads, direct-to-LDS loads, LDS
 // swizzles and the in-loop instruction spreading used by the software pipelines.
 #pragma once
 
@@ -79,38 +79,6 @@ __device__ __forceinline__ void global_to_lds16(const void* g, FH_LDS void* lds_
 }
 
 // Runs the epilogue program on 8 rounded outputs (one 16-byte vector) at flat output index idx.
-template <typename T>
-__device__ __forceinline__ uint4 apply_epilogue_vec(const EpilogueArgs& ep, uint4 packed, int64_t idx) {
-  using S = typename Io<T>::storage;
-  constexpr int V = 16 / static_cast<int>(sizeof(S));
-  S vals[V];
-  __builtin_memcpy(vals, &packed, 16);
-  float v[V];
-#pragma unroll
-  for (int x = 0; x < V; ++x) v[x] = Io<T>::load(vals[x]);
-  for (int sg = 0; sg < ep.nseg; ++sg) {
-    const uint8_t op = ep.ops[sg];
-    if (ew_is_binary(op)) {
-      const uint4 in = *reinterpret_cast<const uint4*>(static_cast<const S*>(ep.ins[sg]) + idx);
-      S iv[V];
-      __builtin_memcpy(iv, &in, 16);
-#pragma unroll
-      for (int x = 0; x < V; ++x) v[x] = ew_binary(op, v[x], Io<T>::load(iv[x]));
-    } else {
-#pragma unroll
-      for (int x = 0; x < V; ++x) v[x] = ew_unary(op, v[x]);
-    }
-    if (ep.round_between) {
-#pragma unroll
-      for (int x = 0; x < V; ++x) v[x] = Io<T>::round(v[x]);
-    }
-  }
-#pragma unroll
-  for (int x = 0; x < V; ++x) vals[x] = Io<T>::store(v[x]);
-  __builtin_memcpy(&packed, vals, 16);
-  return packed;
-}
-
 // XOR swizzles of the 16-byte chunks of an LDS row (gfx950 LDS: 64 banks of 4 bytes, 256 B per cycle).
 // A rows are 64 B (4 chunks); XOR with (row >> 2) & 3 makes the ds_read_b128 fragment reads (32 consecutive
 // rows, one chunk each) conflict-free. B rows are BN*2 B: the 4 consecutive k rows of one transpose-read group
