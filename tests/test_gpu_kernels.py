@@ -417,6 +417,37 @@ def test_conv2d_nhwc(hip, dtype, geom, with_bias):
     assert_close(got, want, dtype, what=f"conv nhwc {geom}")
 
 
+# Shapes large enough for each tile configuration of the dispatch table (64x256, 64x128, 128x256, 128x128;
+# the small cases above take 64x64), checked on 4,096 sampled outputs recomputed by the oracle's per-element
+# formula (the full single-threaded oracle would take minutes here).
+LARGE_NHWC_CASES = [
+    (BF16, (8, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1)),     # 64x256
+    (BF16, (4, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1)),     # 64x128
+    (BF16, (32, 128, 28, 28, 128, 3, 3, 1, 1, 1, 1, 1)),  # 128x256
+    (BF16, (64, 256, 14, 14, 256, 3, 3, 1, 1, 1, 1, 1)),  # 128x128
+    (F32, (8, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1)),      # 64x256
+    (F32, (32, 128, 28, 28, 128, 3, 3, 1, 1, 1, 1, 1)),   # 128x128 (no 128x256 for fp32)
+]
+
+
+@pytest.mark.parametrize("dtype,geom", LARGE_NHWC_CASES)
+def test_conv2d_nhwc_large_tiles_sampled(hip, dtype, geom):
+    say(f"conv nhwc large dtype={dtype} {geom}")
+    n, cin, h, w, cout, kh, kw = geom[:7]
+    x = synth.tensor(141, (n, cin, h, w), dtype, "normal")
+    wt = synth.tensor(142, (cout, cin, kh, kw), dtype, "normal", (2.0 / (cin * kh * kw)) ** 0.5)
+    bias = synth.tensor(143, (cout,), dtype, "normal", 0.1)
+    oh, ow = orc.conv_out_hw(geom)
+    dx, dw, db = dev(hip, to_nhwc(x)), dev(hip, to_nhwc(wt)), dev(hip, bias)
+    dy = hip.DeviceBuffer(n * cout * oh * ow * x.itemsize)
+    hip.check(hip.lib().fh_conv2d_nhwc_fwd(dtype, dx.value, dw.value, db.value, dy.value, hip.i64_array(geom),
+                                           None, None))
+    got = dy.download((n, cout, oh, ow), x.dtype).reshape(-1)
+    idx = np.random.default_rng(7).integers(0, got.size, 4096)
+    want = orc.conv2d_sample(dtype, x, wt, bias, geom, idx)
+    assert_close(got[idx], want, dtype, what=f"conv nhwc large {geom}")
+
+
 @pytest.mark.parametrize("dtype", [BF16, F32])
 def test_conv2d_nhwc_epilogue_add_relu(hip, dtype):
     # conv + bias, then the residual add;relu of a ResNet basic block, rounded between segments
