@@ -407,10 +407,12 @@ __global__ __launch_bounds__(256) void transpose_batched_kernel(const E* __restr
   }
 }
 
-// 16-bit batched transpose with 16-byte global accesses (rows % 8 == 0, cols % 8 == 0, 16-byte aligned): a
-// 64 x 64 tile is read as 16-byte row chunks into LDS (chunk cc of tile row r stored at cc ^ ((r >> 3) & 7), which
-// keeps the column reads below free of bank conflicts), and each thread then gathers 8 consecutive rows of one
-// column and writes them as one 16-byte chunk of the output row.
+// 16-bit batched transpose with 16-byte writes (rows % 8 == 0, 16-byte aligned output) and, when cols % 8 == 0
+// and the input is aligned too, 16-byte reads (otherwise one element per lane, still coalesced along a row): a
+// 64 x 64 tile goes through LDS (chunk cc of tile row r stored at cc ^ ((r >> 3) & 7), which keeps the column
+// reads below free of bank conflicts), and each thread then gathers 8 consecutive rows of one column and writes
+// them as one 16-byte chunk of the output row.
+template <bool WIDE_READ>
 __global__ __launch_bounds__(256) void transpose_wide_kernel(const uint16_t* __restrict__ x, uint16_t* __restrict__ y,
                                                              int64_t rows, int64_t cols) {
   __shared__ __attribute__((aligned(16))) uint16_t tile[64 * 64];
@@ -419,13 +421,25 @@ __global__ __launch_bounds__(256) void transpose_wide_kernel(const uint16_t* __r
   const uint16_t* xb = x + b * rows * cols;
   uint16_t* yb = y + b * rows * cols;
   const int t = threadIdx.x;
+  if constexpr (WIDE_READ) {
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int id = t + 256 * j, r = id >> 3, cc = id & 7;
-    const int64_t gr = r0 + r, gc = c0 + 8 * cc;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (gr < rows && gc < cols) v = *reinterpret_cast<const uint4*>(xb + gr * cols + gc);
-    *reinterpret_cast<uint4*>(tile + r * 64 + ((cc ^ ((r >> 3) & 7)) * 8)) = v;
+    for (int j = 0; j < 2; ++j) {
+      const int id = t + 256 * j, r = id >> 3, cc = id & 7;
+      const int64_t gr = r0 + r, gc = c0 + 8 * cc;
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (gr < rows && gc < cols) v = *reinterpret_cast<const uint4*>(xb + gr * cols + gc);
+      *reinterpret_cast<uint4*>(tile + r * 64 + ((cc ^ ((r >> 3) & 7)) * 8)) = v;
+    }
+  } else {
+    // lane -> column t % 64 of rows t / 64 + 4 i: reads coalesced along the input row
+    const int c = t & 63;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int r = (t >> 6) + 4 * i;
+      const int64_t gr = r0 + r, gc = c0 + c;
+      const uint16_t v = (gr < rows && gc < cols) ? xb[gr * cols + gc] : uint16_t{0};
+      tile[r * 64 + (((c >> 3) ^ ((r >> 3) & 7)) * 8) + (c & 7)] = v;
+    }
   }
   __syncthreads();
 #pragma unroll
@@ -457,6 +471,33 @@ __global__ __launch_bounds__(256) void transpose_plane_kernel(const E* __restric
   for (int o = threadIdx.x; o < n; o += 256) {
     const int c = o / rows, r = o - (o / rows) * rows;
     y[base + o] = plane[r * cols + c];
+  }
+}
+
+// Up to kMultiMax small batched transposes in one launch (a graph's filters, [Cout][Cin][KH*KW] ->
+// [Cout][KH*KW][Cin]): blockIdx.y picks the tensor, blockIdx.x the plane, each plane as in
+// transpose_plane_kernel. One launch instead of one per layer: each of these is too small to be more than
+// launch and memory latency on its own.
+constexpr int kMultiMax = 32;
+struct PlaneBatch {
+  const void* x[kMultiMax];
+  void* y[kMultiMax];
+  int32_t batch[kMultiMax], rows[kMultiMax], cols[kMultiMax];
+};
+template <typename E>
+__global__ __launch_bounds__(256) void transpose_planes_multi_kernel(PlaneBatch a) {
+  __shared__ E plane[kPlaneMax];
+  const int ti = blockIdx.y;
+  if (static_cast<int32_t>(blockIdx.x) >= a.batch[ti]) return;
+  const int rows = a.rows[ti], cols = a.cols[ti], n = rows * cols;
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * n;
+  const E* x = static_cast<const E*>(a.x[ti]) + base;
+  E* y = static_cast<E*>(a.y[ti]) + base;
+  for (int i = threadIdx.x; i < n; i += 256) plane[i] = x[i];
+  __syncthreads();
+  for (int o = threadIdx.x; o < n; o += 256) {
+    const int c = o / rows, r = o - (o / rows) * rows;
+    y[o] = plane[r * cols + c];
   }
 }
 
@@ -538,9 +579,14 @@ extern "C" fh_status fh_transpose_batched(int32_t itemsize, const void* x, void*
     }
     return launch_status("transpose_plane_kernel launch");
   }
-  if (itemsize == 2 && rows % 8 == 0 && cols % 8 == 0 && aligned16(x) && aligned16(y)) {
-    hipLaunchKernelGGL(transpose_wide_kernel, grid, dim3(256), 0, s, static_cast<const uint16_t*>(x),
-                       static_cast<uint16_t*>(y), rows, cols);
+  if (itemsize == 2 && rows % 8 == 0 && aligned16(y)) {
+    if (cols % 8 == 0 && aligned16(x)) {
+      hipLaunchKernelGGL(transpose_wide_kernel<true>, grid, dim3(256), 0, s, static_cast<const uint16_t*>(x),
+                         static_cast<uint16_t*>(y), rows, cols);
+    } else {
+      hipLaunchKernelGGL(transpose_wide_kernel<false>, grid, dim3(256), 0, s, static_cast<const uint16_t*>(x),
+                         static_cast<uint16_t*>(y), rows, cols);
+    }
     return launch_status("transpose_wide_kernel launch");
   }
   switch (itemsize) {
@@ -556,6 +602,39 @@ extern "C" fh_status fh_transpose_batched(int32_t itemsize, const void* x, void*
       return fail(FH_INVALID_ARGUMENT, "fh_transpose_batched: itemsize must be 2 or 4");
   }
   return launch_status("transpose_batched_kernel launch");
+}
+
+extern "C" fh_status fh_transpose_planes_multi(int32_t itemsize, int32_t n, const void* const* xs, void* const* ys,
+                                               const int64_t* batch, const int64_t* rows, const int64_t* cols,
+                                               void* stream) {
+  if (n < 0 || n > kMultiMax) return fail(FH_INVALID_ARGUMENT, "fh_transpose_planes_multi: 0 to 32 tensors");
+  if (n == 0) return FH_OK;
+  if (xs == nullptr || ys == nullptr || batch == nullptr || rows == nullptr || cols == nullptr)
+    return fail(FH_INVALID_ARGUMENT, "fh_transpose_planes_multi: null argument");
+  if (itemsize != 2 && itemsize != 4) return fail(FH_INVALID_ARGUMENT, "fh_transpose_planes_multi: itemsize must be 2 or 4");
+  PlaneBatch a{};
+  int64_t max_batch = 0;
+  for (int i = 0; i < n; ++i) {
+    if (batch[i] < 0 || rows[i] < 0 || cols[i] < 0 || rows[i] * cols[i] > kPlaneMax || batch[i] > 0x7fffffffLL)
+      return fail(FH_INVALID_ARGUMENT, "fh_transpose_planes_multi: planes of at most 8192 elements");
+    if (batch[i] * rows[i] * cols[i] > 0 && (xs[i] == nullptr || ys[i] == nullptr))
+      return fail(FH_INVALID_ARGUMENT, "fh_transpose_planes_multi: null tensor");
+    a.x[i] = xs[i];
+    a.y[i] = ys[i];
+    a.batch[i] = rows[i] * cols[i] == 0 ? 0 : static_cast<int32_t>(batch[i]);
+    a.rows[i] = static_cast<int32_t>(rows[i]);
+    a.cols[i] = static_cast<int32_t>(cols[i]);
+    max_batch = std::max<int64_t>(max_batch, a.batch[i]);
+  }
+  if (max_batch == 0) return FH_OK;
+  const dim3 grid(static_cast<uint32_t>(max_batch), static_cast<uint32_t>(n));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (itemsize == 2) {
+    hipLaunchKernelGGL(transpose_planes_multi_kernel<uint16_t>, grid, dim3(256), 0, s, a);
+  } else {
+    hipLaunchKernelGGL(transpose_planes_multi_kernel<uint32_t>, grid, dim3(256), 0, s, a);
+  }
+  return launch_status("transpose_planes_multi_kernel launch");
 }
 
 extern "C" int32_t fh_conv2d_nhwc_supported(int32_t dtype, const int64_t geom[12]) {

@@ -74,6 +74,8 @@ _SIGS = {
     "fh_conv_pack_input_c8": (c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_int64, c_void_p]),
     "fh_conv_pack_filter_c8": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p]),
     "fh_conv_c8_filter_k": (c_int64, [c_int64, c_int64]),
+    "fh_transpose_planes_multi": (c_int32, [c_int32, c_int32, POINTER(c_void_p), POINTER(c_void_p), POINTER(c_int64),
+                                            POINTER(c_int64), POINTER(c_int64), c_void_p]),
     "fh_ew_program": (c_int32, [c_int32, c_int32, POINTER(c_uint8), POINTER(c_int8), POINTER(c_void_p), c_int32,
                                 c_void_p, c_int64, c_int32, c_void_p]),
     "fh_attention_fwd": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,

@@ -118,6 +118,11 @@ inline constexpr std::string_view kConvEpilogueOp = "hip_conv2d_epilogue_interna
 inline constexpr std::string_view kChannelsLastOp = "hip_channels_last_internal";
 // conv2d (optionally with an epilogue program) on channels-last operands; output NCHW.
 inline constexpr std::string_view kConvNhwcOp = "hip_conv2d_nhwc_internal";
+// channels_last of up to kMultiMaxTensors tensors in one step (a graph's filters; each [d0,d1,d2,d3] ->
+// [d0,d2,d3,d1] with d1*d2*d3 <= kMultiPlaneMax), see fh_transpose_planes_multi.
+inline constexpr std::string_view kChannelsLastMultiOp = "hip_channels_last_multi_internal";
+inline constexpr size_t kMultiMaxTensors = 32;
+inline constexpr int64_t kMultiPlaneMax = 8192;
 // Cin <= 8: x [N,C,H,W] -> [N,H,W,8] zero-padded; w [Cout,C,KH,KW] -> [Cout, K8] (see fh_conv_pack_*_c8).
 inline constexpr std::string_view kPackInputC8Op = "hip_pack_input_c8_internal";
 inline constexpr std::string_view kPackFilterC8Op = "hip_pack_filter_c8_internal";

@@ -106,91 +106,155 @@ Status lower_epilogues(ir::Graph& g) {
   return Status::ok();
 }
 
+// Whether the channels-last MFMA path takes conv node `n` (conv2d or conv epilogue), with its geometry
+// {N, Cin, H, W, Cout, KH, KW, sh, sw, ph, pw, groups} and whether it goes through the C8 layout (Cin <= 8, 16-bit).
+struct ConvLowering {
+  bool ok = false;
+  bool c8 = false;
+  int64_t geom[12] = {};
+};
+
+ConvLowering plan_conv(const ir::Node* n) {
+  ConvLowering p;
+  const bool is_conv = n->op() == "conv2d" || n->op() == kConvEpilogueOp;
+  if (!is_conv || n->outputs().size() != 1 || n->inputs().size() < 2) return p;
+  const ir::TensorType& xt = n->inputs()[0]->type();
+  const ir::TensorType& wt = n->inputs()[1]->type();
+  auto get = [&](const char* k) -> const ir::AttrValue* {
+    auto it = n->attrs().find(k);
+    return it == n->attrs().end() ? nullptr : &it->second;
+  };
+  const auto* stride = get("stride") ? std::get_if<std::vector<int64_t>>(get("stride")) : nullptr;
+  const auto* pad = get("padding") ? std::get_if<std::vector<int64_t>>(get("padding")) : nullptr;
+  const auto* groups = get("groups") ? std::get_if<int64_t>(get("groups")) : nullptr;
+  const int32_t dt = xt.dtype.code() == DTypeCode::kBFloat16  ? FH_BF16
+                     : xt.dtype.code() == DTypeCode::kFloat16 ? FH_F16
+                     : xt.dtype.code() == DTypeCode::kFloat32 ? FH_F32
+                                                              : -1;
+  if (!stride || !pad || !groups || stride->size() != 2 || pad->size() != 2 || dt < 0 || xt.shape.rank() != 4 ||
+      wt.shape.rank() != 4 || !(wt.dtype == xt.dtype) || wt.shape.dim(1) != xt.shape.dim(1))
+    return p;
+  const int64_t geom[12] = {xt.shape.dim(0), xt.shape.dim(1), xt.shape.dim(2), xt.shape.dim(3),
+                            wt.shape.dim(0), wt.shape.dim(2), wt.shape.dim(3), (*stride)[0],
+                            (*stride)[1],    (*pad)[0],       (*pad)[1],       *groups};
+  // Cin <= 8 goes through the C8 layout (channels padded to 8, four filter positions per k-stage)
+  p.c8 = xt.shape.dim(1) <= 8 && *groups == 1 && dt != FH_F32;
+  int64_t geom_k[12];
+  std::copy(geom, geom + 12, geom_k);
+  if (p.c8) geom_k[1] = 8;
+  std::copy(geom, geom + 12, p.geom);
+  p.ok = fh_conv2d_nhwc_supported(dt, geom_k) == 1;
+  return p;
+}
+
 // Lowers every conv2d / conv epilogue node that the channels-last MFMA path accepts (fh_conv2d_nhwc_supported)
 // to  x_nhwc = channels_last(x); w_khwc = channels_last(w); y = conv2d_nhwc(x_nhwc, w_khwc, bias?, ep...).
-// The graph is rebuilt in topological order with the three nodes emitted in the conv's place, so the transposed
+// The filters that are graph inputs (weights fed per run) are transposed together by one
+// channels_last_multi node, emitted before the first conv that needs one, instead of one launch per layer.
+// The graph is rebuilt in topological order with the new nodes emitted in the conv's place, so the transposed
 // operands become ordinary intermediates that the memory plan places and recycles.
 Result<ir::Graph> lower_convs(const ir::Graph& src) {
   std::unordered_map<const ir::Value*, ir::Value*> map;
   ir::Graph out{std::string(src.name())};
-  auto channels_last = [&](ir::Value* v) -> Result<ir::Value*> {
+  auto channels_last_type = [](const ir::Value* v) {
     ir::TensorType t = v->type();
     const Shape& s = t.shape;
     t.shape = Shape({s.dim(0), s.dim(2), s.dim(3), s.dim(1)});
-    Result<ir::Node*> n = out.create_node(std::string(kChannelsLastOp), {v}, {t});
+    return t;
+  };
+  auto channels_last = [&](ir::Value* v) -> Result<ir::Value*> {
+    Result<ir::Node*> n = out.create_node(std::string(kChannelsLastOp), {v}, {channels_last_type(v)});
     if (!n.is_ok()) return n.status();
     return n.value()->output(0);
   };
-  for (const ir::Node* n : src.topological_order()) {
-    if (n->op() == ir::kGraphInputOp) {
-      Result<ir::Value*> v = out.add_graph_input(n->outputs()[0].type());
-      if (!v.is_ok()) return v.status();
-      map[&n->outputs()[0]] = v.value();
-      continue;
+
+  // graph-input filters of the non-C8 lowered convs, in first-use order, each once
+  std::vector<const ir::Value*> batched;
+  {
+    std::unordered_set<const ir::Value*> seen;
+    for (const ir::Node* n : src.topological_order()) {
+      const ConvLowering p = plan_conv(n);
+      const ir::Value* w = p.ok && !p.c8 ? n->inputs()[1] : nullptr;
+      if (w == nullptr || w->producer() == nullptr || w->producer()->op() != ir::kGraphInputOp || seen.count(w)) continue;
+      if (w->type().shape.dim(1) * w->type().shape.dim(2) * w->type().shape.dim(3) > kMultiPlaneMax) continue;
+      seen.insert(w);
+      batched.push_back(w);
     }
+  }
+  std::unordered_map<const ir::Value*, ir::Value*> batched_out;  // source filter -> its transposed value
+  bool batched_emitted = false;
+  auto emit_batched = [&]() -> Status {
+    batched_emitted = true;
+    std::vector<const ir::Value*> ready;
+    for (const ir::Value* w : batched)
+      if (map.count(w)) ready.push_back(w);
+    for (size_t i0 = 0; i0 < ready.size(); i0 += kMultiMaxTensors) {
+      const size_t i1 = std::min(ready.size(), i0 + kMultiMaxTensors);
+      if (i1 - i0 < 2) break;  // a single filter keeps its own channels_last node
+      std::vector<ir::Value*> ins;
+      std::vector<ir::TensorType> types;
+      for (size_t i = i0; i < i1; ++i) {
+        ins.push_back(map.at(ready[i]));
+        types.push_back(channels_last_type(ready[i]));
+      }
+      Result<ir::Node*> n = out.create_node(std::string(kChannelsLastMultiOp), std::move(ins), std::move(types));
+      if (!n.is_ok()) return n.status();
+      for (size_t i = i0; i < i1; ++i) batched_out[ready[i]] = n.value()->output(static_cast<int32_t>(i - i0));
+    }
+    return Status::ok();
+  };
+
+  // Graph inputs first (same order, so the same signature; they have no operands, so the order stays
+  // topological): every filter is defined before the first conv, where the batched transpose goes.
+  for (const ir::Node* n : src.topological_order()) {
+    if (n->op() != ir::kGraphInputOp) continue;
+    Result<ir::Value*> v = out.add_graph_input(n->outputs()[0].type());
+    if (!v.is_ok()) return v.status();
+    map[&n->outputs()[0]] = v.value();
+  }
+  for (const ir::Node* n : src.topological_order()) {
+    if (n->op() == ir::kGraphInputOp) continue;
     std::vector<ir::Value*> ins;
     for (const ir::Value* in : n->inputs()) ins.push_back(map.at(in));
-    const bool is_conv = n->op() == "conv2d" || n->op() == kConvEpilogueOp;
-    bool lowered = false;
-    if (is_conv && n->outputs().size() == 1 && ins.size() >= 2) {
-      const ir::TensorType& xt = n->inputs()[0]->type();
-      const ir::TensorType& wt = n->inputs()[1]->type();
-      auto get = [&](const char* k) -> const ir::AttrValue* {
-        auto it = n->attrs().find(k);
-        return it == n->attrs().end() ? nullptr : &it->second;
-      };
-      const auto* stride = get("stride") ? std::get_if<std::vector<int64_t>>(get("stride")) : nullptr;
-      const auto* pad = get("padding") ? std::get_if<std::vector<int64_t>>(get("padding")) : nullptr;
-      const auto* groups = get("groups") ? std::get_if<int64_t>(get("groups")) : nullptr;
-      const int32_t dt = xt.dtype.code() == DTypeCode::kBFloat16  ? FH_BF16
-                         : xt.dtype.code() == DTypeCode::kFloat16 ? FH_F16
-                         : xt.dtype.code() == DTypeCode::kFloat32 ? FH_F32
-                                                                  : -1;
-      if (stride && pad && groups && stride->size() == 2 && pad->size() == 2 && dt >= 0 && xt.shape.rank() == 4 &&
-          wt.shape.rank() == 4 && wt.dtype == xt.dtype) {
-        const int64_t geom[12] = {xt.shape.dim(0), xt.shape.dim(1), xt.shape.dim(2), xt.shape.dim(3),
-                                  wt.shape.dim(0), wt.shape.dim(2), wt.shape.dim(3), (*stride)[0],
-                                  (*stride)[1],    (*pad)[0],       (*pad)[1],       *groups};
-        // Cin <= 8 goes through the C8 layout (channels padded to 8, four filter positions per k-stage)
-        const bool c8 = xt.shape.dim(1) <= 8 && *groups == 1 && dt != FH_F32;
-        int64_t geom_k[12];
-        std::copy(geom, geom + 12, geom_k);
-        if (c8) geom_k[1] = 8;
-        if (wt.shape.dim(1) == xt.shape.dim(1) && fh_conv2d_nhwc_supported(dt, geom_k) == 1) {
-          ir::Value* x_cl = nullptr;
-          ir::Value* w_cl = nullptr;
-          if (c8) {
-            ir::TensorType tx = ins[0]->type(), tw = ins[1]->type();
-            tx.shape = Shape({geom[0], geom[2], geom[3], 8});
-            tw.shape = Shape({geom[4], fh_conv_c8_filter_k(geom[5], geom[6])});
-            Result<ir::Node*> px = out.create_node(std::string(kPackInputC8Op), {ins[0]}, {tx});
-            if (!px.is_ok()) return px.status();
-            Result<ir::Node*> pw = out.create_node(std::string(kPackFilterC8Op), {ins[1]}, {tw});
-            if (!pw.is_ok()) return pw.status();
-            x_cl = px.value()->output(0);
-            w_cl = pw.value()->output(0);
-          } else {
-            Result<ir::Value*> xv = channels_last(ins[0]);
-            if (!xv.is_ok()) return xv.status();
-            Result<ir::Value*> wv = channels_last(ins[1]);
-            if (!wv.is_ok()) return wv.status();
-            x_cl = xv.value();
-            w_cl = wv.value();
-          }
-          std::vector<ir::Value*> conv_ins = ins;
-          conv_ins[0] = x_cl;
-          conv_ins[1] = w_cl;
-          Result<ir::Node*> c = out.create_node(std::string(kConvNhwcOp), std::move(conv_ins), {n->outputs()[0].type()});
-          if (!c.is_ok()) return c.status();
-          for (const auto& [k, v] : n->attrs()) c.value()->set_attr(k, v);
-          if (n->op() == "conv2d") c.value()->set_attr("n_main_inputs", ir::AttrValue{static_cast<int64_t>(ins.size())});
-          c.value()->set_attr("filter_hw", ir::AttrValue{std::vector<int64_t>{geom[5], geom[6]}});
-          map[&n->outputs()[0]] = c.value()->output(0);
-          lowered = true;
+    const ConvLowering p = plan_conv(n);
+    if (p.ok) {
+      const int64_t* geom = p.geom;
+      ir::Value* x_cl = nullptr;
+      ir::Value* w_cl = nullptr;
+      if (p.c8) {
+        ir::TensorType tx = ins[0]->type(), tw = ins[1]->type();
+        tx.shape = Shape({geom[0], geom[2], geom[3], 8});
+        tw.shape = Shape({geom[4], fh_conv_c8_filter_k(geom[5], geom[6])});
+        Result<ir::Node*> px = out.create_node(std::string(kPackInputC8Op), {ins[0]}, {tx});
+        if (!px.is_ok()) return px.status();
+        Result<ir::Node*> pw = out.create_node(std::string(kPackFilterC8Op), {ins[1]}, {tw});
+        if (!pw.is_ok()) return pw.status();
+        x_cl = px.value()->output(0);
+        w_cl = pw.value()->output(0);
+      } else {
+        if (!batched_emitted) FRAME_RETURN_IF_ERROR(emit_batched());
+        Result<ir::Value*> xv = channels_last(ins[0]);
+        if (!xv.is_ok()) return xv.status();
+        x_cl = xv.value();
+        if (auto it = batched_out.find(n->inputs()[1]); it != batched_out.end()) {
+          w_cl = it->second;
+        } else {
+          Result<ir::Value*> wv = channels_last(ins[1]);
+          if (!wv.is_ok()) return wv.status();
+          w_cl = wv.value();
         }
       }
+      std::vector<ir::Value*> conv_ins = ins;
+      conv_ins[0] = x_cl;
+      conv_ins[1] = w_cl;
+      Result<ir::Node*> c = out.create_node(std::string(kConvNhwcOp), std::move(conv_ins), {n->outputs()[0].type()});
+      if (!c.is_ok()) return c.status();
+      for (const auto& [k, v] : n->attrs()) c.value()->set_attr(k, v);
+      if (n->op() == "conv2d") c.value()->set_attr("n_main_inputs", ir::AttrValue{static_cast<int64_t>(ins.size())});
+      c.value()->set_attr("filter_hw", ir::AttrValue{std::vector<int64_t>{geom[5], geom[6]}});
+      map[&n->outputs()[0]] = c.value()->output(0);
+      continue;
     }
-    if (lowered) continue;
     std::vector<ir::TensorType> types;
     for (const ir::Value& o : n->outputs()) types.push_back(o.type());
     Result<ir::Node*> c = out.create_node(std::string(n->op()), std::move(ins), std::move(types));

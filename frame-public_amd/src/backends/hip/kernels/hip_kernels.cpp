@@ -249,6 +249,36 @@ Status channels_last_kernel(KernelContext& ctx) {
   return Status::ok();
 }
 
+// channels_last of several tensors in one launch ([d0,d1,d2,d3] -> [d0,d2,d3,d1] each)
+Status channels_last_multi_kernel(KernelContext& ctx) {
+  const std::string op(kChannelsLastMultiOp);
+  const size_t n = ctx.inputs.size();
+  if (n == 0 || n > kMultiMaxTensors || ctx.outputs.size() != n) return invalid(op, "expects 1 to 32 inputs and as many outputs");
+  std::vector<const void*> xs(n);
+  std::vector<void*> ys(n);
+  std::vector<int64_t> batch(n), rows(n), cols(n);
+  const size_t itemsize = ctx.inputs[0].dtype().itemsize();
+  for (size_t i = 0; i < n; ++i) {
+    const Tensor& x = ctx.inputs[i];
+    Tensor& y = ctx.outputs[i];
+    const Shape& s = x.shape();
+    if (s.rank() != 4 || !(x.dtype() == y.dtype()) || x.dtype().itemsize() != itemsize)
+      return invalid(op, "expects rank-4 inputs of one item size, outputs of the same dtype");
+    if (y.shape() != Shape({s.dim(0), s.dim(2), s.dim(3), s.dim(1)})) return invalid(op, "output shape does not match [d0,d2,d3,d1]");
+    if (s.dim(1) * s.dim(2) * s.dim(3) > kMultiPlaneMax) return invalid(op, "planes above 8192 elements");
+    xs[i] = x.raw_data();
+    ys[i] = y.raw_data();
+    batch[i] = s.dim(0);
+    rows[i] = s.dim(1);
+    cols[i] = s.dim(2) * s.dim(3);
+  }
+  FRAME_HIP_RETURN_IF_ERROR(fh_transpose_planes_multi(static_cast<int32_t>(itemsize), static_cast<int32_t>(n), xs.data(),
+                                                      ys.data(), batch.data(), rows.data(), cols.data(),
+                                                      stream_handle(ctx)),
+                            "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
 // x [N,C,H,W] (C <= 8) -> [N,H,W,8]
 Status pack_input_c8_kernel(KernelContext& ctx) {
   const std::string op(kPackInputC8Op);
@@ -490,6 +520,7 @@ FRAME_REGISTER_KERNEL("conv2d", kHipBackendName, &conv2d_kernel);
 FRAME_REGISTER_KERNEL(kConvEpilogueOp, kHipBackendName, &conv_epilogue_kernel);
 FRAME_REGISTER_KERNEL(kConvNhwcOp, kHipBackendName, &conv_nhwc_kernel);
 FRAME_REGISTER_KERNEL(kChannelsLastOp, kHipBackendName, &channels_last_kernel);
+FRAME_REGISTER_KERNEL(kChannelsLastMultiOp, kHipBackendName, &channels_last_multi_kernel);
 FRAME_REGISTER_KERNEL(kPackInputC8Op, kHipBackendName, &pack_input_c8_kernel);
 FRAME_REGISTER_KERNEL(kPackFilterC8Op, kHipBackendName, &pack_filter_c8_kernel);
 FRAME_REGISTER_KERNEL("softmax", kHipBackendName, &softmax_kernel);

@@ -156,6 +156,13 @@ int64_t fh_conv_c8_filter_k(int64_t kh, int64_t kw);
 fh_status fh_transpose_batched(int32_t itemsize, const void* x, void* y, int64_t batch, int64_t rows, int64_t cols,
                                void* stream);
 
+/* Several small batched transposes in one launch: for tensor i < n (n <= 32), ys[i][b][c][r] = xs[i][b][r][c] for
+ * b < batch[i], r < rows[i], c < cols[i], with rows[i] * cols[i] <= 8192. HipBackend::compile puts all the
+ * filters of a graph's channels-last convolutions into one such step. No counterpart in the reference (cuDNN
+ * consumes KCRS filters, reference: src/backends/cuda/kernels/conv.cpp:385-520). */
+fh_status fh_transpose_planes_multi(int32_t itemsize, int32_t n, const void* const* xs, void* const* ys,
+                                    const int64_t* batch, const int64_t* rows, const int64_t* cols, void* stream);
+
 /* One-pass fused elementwise program over `numel` elements.
  * ops/arities follow the fused_elementwise_internal attrs (reference: src/ops/fused_elementwise_utils.cpp:17-120);
  * ins are the node's external inputs in order. Single add/mul/relu nodes are programs with nseg = 1.

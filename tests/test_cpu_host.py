@@ -247,3 +247,13 @@ def test_conv_lowering_by_dtype_and_channels(dtype, cin, lowered):
     assert lowered in out, out
     if lowered == "conv2d":
         assert "hip_conv2d_nhwc_internal" not in out
+
+
+def test_resnet_filters_are_transposed_in_one_step():
+    # every non-stem conv filter is a graph input: one batched channels-last step instead of one per layer
+    g, _ = graphs.resnet18(batch=2, dtype=3, image=64)
+    ops = re.findall(r"= (\w+)\(", host.hip_lowered(g.text(), 1))
+    assert ops.count("hip_channels_last_multi_internal") == 1
+    assert ops.count("hip_conv2d_nhwc_internal") == 20
+    assert ops.count("hip_channels_last_internal") == 19  # the activations
+    assert ops.count("graph_input") == 43

@@ -375,6 +375,27 @@ def test_transpose_batched(hip, itemsize, shape):
     assert_bitwise(got, np.ascontiguousarray(x.transpose(0, 2, 1)), "batched transpose")
 
 
+@pytest.mark.parametrize("itemsize", [2, 4])
+def test_transpose_planes_multi(hip, itemsize):
+    # three tensors of different batch and plane shape (filters of a 3x3, a 1x1 and a 7-wide conv) in one launch
+    say(f"transpose_planes_multi itemsize={itemsize}")
+    dt = np.uint16 if itemsize == 2 else np.uint32
+    shapes = [(64, 64, 9), (128, 64, 1), (5, 33, 7)]
+    rng = np.random.default_rng(11)
+    xs = [rng.integers(0, np.iinfo(dt).max, size=s, dtype=dt) for s in shapes]
+    dxs = [dev(hip, x) for x in xs]
+    dys = [hip.DeviceBuffer(x.nbytes) for x in xs]
+    n = len(shapes)
+    ptrs_in = (ctypes.c_void_p * n)(*[d.value for d in dxs])
+    ptrs_out = (ctypes.c_void_p * n)(*[d.value for d in dys])
+    b = (ctypes.c_int64 * n)(*[s[0] for s in shapes])
+    r = (ctypes.c_int64 * n)(*[s[1] for s in shapes])
+    c = (ctypes.c_int64 * n)(*[s[2] for s in shapes])
+    hip.check(hip.lib().fh_transpose_planes_multi(itemsize, n, ptrs_in, ptrs_out, b, r, c, None))
+    for x, d, s in zip(xs, dys, shapes):
+        assert_bitwise(d.download((s[0], s[2], s[1]), dt), np.ascontiguousarray(x.transpose(0, 2, 1)), f"multi {s}")
+
+
 NHWC_CASES = [
     # N, Cin, H, W, Cout, KH, KW, sh, sw, ph, pw, groups, bias
     ((2, 64, 12, 12, 64, 3, 3, 1, 1, 1, 1, 1), True),
