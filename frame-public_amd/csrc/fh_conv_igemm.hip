@@ -54,7 +54,8 @@ struct ConvNhwcArgs {
   int64_t p;         // N*Ho*Wo
   uint32_t x_bytes;
   int32_t tiles_m, tiles_n;
-  int32_t vec_store;  // Ho*Wo % 8 == 0 and 16-byte aligned output / epilogue operands
+  int32_t vec_store;  // NCHW: Ho*Wo % V == 0; NHWC: Cout % V == 0; and 16-byte aligned output / epilogue operands
+  int32_t out_nhwc;   // 1: y (and the epilogue operands) are [N][Ho][Wo][Cout]
   EpilogueArgs ep;
 };
 
@@ -303,10 +304,71 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
   wait_vmcnt<0>();
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __syncthreads();
+  constexpr int V = EPC;
+  S* __restrict__ Y = static_cast<S*>(args.y);
+  const S* bias = static_cast<const S*>(args.bias);
+  if (args.out_nhwc) {
+    // Channels-last output. The wave tile is staged pixel-major: pixel pc's WM channels are a row of PITCH
+    // elements (padded by one 16-byte chunk so the 32 pixels of one accumulator register spread over the banks),
+    // written two channels at a time. Then lane -> (pixel, group g of V channels) with g fastest: each lane reads
+    // 16 contiguous bytes and consecutive lanes write consecutive 16-byte chunks of a pixel's channel run.
+    constexpr int PITCH = WM + V;
+    constexpr int GPW = WM / V;
+    static_assert((WN * GPW) % 64 == 0, "whole waves of (pixel, channel group) pairs");
+    // configurations whose pixel-major staging would not fit the ring are never launched with out_nhwc
+    // (launch_conv refuses them)
+    if constexpr (NW * WN * PITCH * ES <= kStages * STAGE) {
+    S* wl = reinterpret_cast<S*>(ring + wave * (WN * PITCH * ES));
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int x = 0; x < 16; x += 2) {
+        const int rr = i * 32 + 8 * (x >> 2) + 4 * hi + (x & 3);  // even: rows rr, rr + 1 are registers x, x + 1
+        const float b0 = bias != nullptr ? Io<T>::load(bias[min(m0 + wm * WM + rr, args.cout - 1)]) : 0.0f;
+        const float b1 = bias != nullptr ? Io<T>::load(bias[min(m0 + wm * WM + rr + 1, args.cout - 1)]) : 0.0f;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          S* dst = wl + (j * 32 + l32) * PITCH + rr;
+          if constexpr (ES == 2) {
+            const uint32_t w = static_cast<uint32_t>(Io<T>::store(acc[i][j][x] + b0)) |
+                               (static_cast<uint32_t>(Io<T>::store(acc[i][j][x + 1] + b1)) << 16);
+            *reinterpret_cast<uint32_t*>(dst) = w;
+          } else {
+            dst[0] = Io<T>::store(acc[i][j][x] + b0);
+            dst[1] = Io<T>::store(acc[i][j][x + 1] + b1);
+          }
+        }
+      }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll 2
+    for (int it = 0; it < WN * GPW / 64; ++it) {
+      const int id = it * 64 + lane;
+      const int g = id % GPW, pc = id / GPW;
+      const int co0 = m0 + wm * WM + g * V;
+      const int64_t p = n0 + wn * WN + pc;
+      if (co0 >= args.cout || p >= args.p) continue;
+      uint4 packed = *reinterpret_cast<const uint4*>(wl + pc * PITCH + g * V);
+      const int64_t idx = p * args.cout + co0;
+      if (args.vec_store && co0 + V <= args.cout) {
+        if (args.ep.nseg > 0) packed = epilogue_vec<T>(args.ep, packed, idx);
+        *reinterpret_cast<uint4*>(Y + idx) = packed;
+      } else {
+        S vals[V];
+        __builtin_memcpy(vals, &packed, 16);
+        for (int e = 0; e < V && co0 + e < args.cout; ++e) {
+          S v = vals[e];
+          if (args.ep.nseg > 0) v = Io<T>::store(epilogue_one<T>(args.ep, Io<T>::load(v), idx + e));
+          Y[idx + e] = v;
+        }
+      }
+    }
+    }
+    return;
+  }
   constexpr int WTILE_BYTES = WM * WN * ES;
   static_assert(NW * WTILE_BYTES <= kStages * STAGE, "the wave tiles fit in the ring");
   S* wl = reinterpret_cast<S*>(ring + wave * WTILE_BYTES);
-  const S* bias = static_cast<const S*>(args.bias);
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -318,11 +380,9 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
     }
   __builtin_amdgcn_s_waitcnt(0xc07f);
   __builtin_amdgcn_wave_barrier();
-  constexpr int V = EPC;
   constexpr int LPR = WN / V;
   constexpr int RPI = 64 / LPR;
   static_assert(64 % LPR == 0 && WM % RPI == 0, "epilogue access shape");
-  S* __restrict__ Y = static_cast<S*>(args.y);
   const int c = (lane % LPR) * V;
   const int64_t p0 = n0 + wn * WN + c;
   for (int it = 0; it < WM / RPI; ++it) {
@@ -350,8 +410,18 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
   }
 }
 
+// Whether a configuration can stage its wave tiles pixel-major (channels-last output) in its LDS ring.
+template <typename T, int BM, int BN, int WAVES_M, int WAVES_N>
+constexpr bool nhwc_out_fits() {
+  constexpr int es = static_cast<int>(sizeof(typename Io<T>::storage));
+  constexpr int wm = BM / WAVES_M, wn = BN / WAVES_N;
+  return WAVES_M * WAVES_N * wn * (wm + 16 / es) * es <= kStages * (BM + BN) * 64;
+}
+
 template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, bool C8>
 fh_status launch_conv(ConvNhwcArgs a, hipStream_t stream) {
+  if (a.out_nhwc && !nhwc_out_fits<T, BM, BN, WAVES_M, WAVES_N>())
+    return fail(FH_INTERNAL, "conv_nhwc_kernel: channels-last output does not fit this tile configuration");
   a.tiles_m = (a.cout + BM - 1) / BM;
   a.tiles_n = static_cast<int32_t>((a.p + BN - 1) / BN);
   const dim3 grid(static_cast<uint32_t>(a.tiles_m) * static_cast<uint32_t>(a.tiles_n));
@@ -379,9 +449,9 @@ fh_status dispatch_conv(const ConvNhwcArgs& a, hipStream_t stream) {
     if constexpr (k16) {
       if (enough(128, 256)) return launch_conv<T, 128, 256, 2, 4, C8>(a, stream);
     }
-    if (enough(128, 128)) return launch_conv<T, 128, 128, 2, 4, C8>(a, stream);
+    if (enough(128, 128) && (k16 || !a.out_nhwc)) return launch_conv<T, 128, 128, 2, 4, C8>(a, stream);
   } else if (a.cout <= 256) {
-    if (enough(128, 128)) return launch_conv<T, 128, 128, 2, 4, C8>(a, stream);
+    if (enough(128, 128) && (k16 || !a.out_nhwc)) return launch_conv<T, 128, 128, 2, 4, C8>(a, stream);
   }
   return launch_conv<T, 64, 64, 2, 2, C8>(a, stream);
 }
@@ -641,8 +711,19 @@ extern "C" int32_t fh_conv2d_nhwc_supported(int32_t dtype, const int64_t geom[12
   return geom != nullptr && nhwc_supported(dtype, geom) ? 1 : 0;
 }
 
+extern "C" fh_status fh_conv2d_nhwc_fwd_ex(int32_t dtype, const void* x_nhwc, const void* w_khwc, const void* bias,
+                                           void* y, const int64_t geom[12], const fh_epilogue* epilogue,
+                                           int32_t flags, void* stream);
+
 extern "C" fh_status fh_conv2d_nhwc_fwd(int32_t dtype, const void* x_nhwc, const void* w_khwc, const void* bias, void* y,
                                         const int64_t geom[12], const fh_epilogue* epilogue, void* stream) {
+  return fh_conv2d_nhwc_fwd_ex(dtype, x_nhwc, w_khwc, bias, y, geom, epilogue, 0, stream);
+}
+
+extern "C" fh_status fh_conv2d_nhwc_fwd_ex(int32_t dtype, const void* x_nhwc, const void* w_khwc, const void* bias,
+                                           void* y, const int64_t geom[12], const fh_epilogue* epilogue,
+                                           int32_t flags, void* stream) {
+  if ((flags & ~FH_CONV_OUT_NHWC) != 0) return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd_ex: unknown flags");
   if (geom == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd: null geometry");
   if (!nhwc_supported(dtype, geom))
     return fail(FH_UNIMPLEMENTED, "fh_conv2d_nhwc_fwd: geometry or dtype not supported by the channels-last path "
@@ -689,7 +770,9 @@ extern "C" fh_status fh_conv2d_nhwc_fwd(int32_t dtype, const void* x_nhwc, const
       a.ep.ins[s] = epilogue->ins[s];
     }
   }
-  bool vec = a.howo % 8 == 0 && aligned16(y);
+  a.out_nhwc = (flags & FH_CONV_OUT_NHWC) ? 1 : 0;
+  const int64_t vwidth = dtype == FH_F32 ? 4 : 8;  // elements per 16-byte vector
+  bool vec = (a.out_nhwc ? a.cout % vwidth == 0 : a.howo % vwidth == 0) && aligned16(y);
   for (int s = 0; s < a.ep.nseg; ++s)
     if (ew_is_binary(a.ep.ops[s]) && !aligned16(a.ep.ins[s])) vec = false;
   a.vec_store = vec ? 1 : 0;

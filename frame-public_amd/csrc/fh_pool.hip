@@ -196,30 +196,148 @@ fh_status launch_pool(int32_t mode, const void* x, void* y, const PoolGeom& g, h
   return launch_status("pool2d_kernel launch");
 }
 
+// Channels-last pooling, x [N][H][W][C] -> y [N][Ho][Wo][C]: one thread per output pixel and group of VW
+// consecutive channels (one 16-byte vector when C allows, else VW = 1), each channel with the NCHW kernel's
+// semantics and scan order. 32-bit index math (the launch checks the sizes); the positions of a window row are
+// loaded 8 at a time before they are folded in, in order, so the loads overlap.
+struct PoolGeom32 {
+  int32_t n, c, h, w, kh, kw, sh, sw, ph, pw, oh, ow;
+};
+
+template <typename T, int MODE, int VW>
+__global__ __launch_bounds__(256) void pool2d_nhwc_kernel(const typename Io<T>::storage* __restrict__ x,
+                                                          typename Io<T>::storage* __restrict__ y, PoolGeom32 g) {
+  using S = typename Io<T>::storage;
+  struct Vec {
+    S v[VW];
+  };
+  const int groups = g.c / VW;
+  const int total = g.n * g.oh * g.ow * groups;
+  const int stride = gridDim.x * blockDim.x;
+  const float denom = static_cast<float>(g.kh * g.kw);
+  for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int cg = i % groups, pix = i / groups;
+    const int ow = pix % g.ow, oh = (pix / g.ow) % g.oh, n = pix / (g.ow * g.oh);
+    float acc[VW];
+    bool found = false;
+#pragma unroll
+    for (int e = 0; e < VW; ++e) acc[e] = 0.0f;
+    for (int a = 0; a < g.kh; ++a) {
+      const int ih = oh * g.sh - g.ph + a;
+      if (ih < 0 || ih >= g.h) continue;
+      const S* row = x + (static_cast<int64_t>(n * g.h + ih) * g.w) * g.c + cg * VW;
+      for (int b0 = 0; b0 < g.kw; b0 += 8) {
+        Vec vals[8];
+        bool ok[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          const int iw = ow * g.sw - g.pw + b0 + u;
+          ok[u] = b0 + u < g.kw && iw >= 0 && iw < g.w;
+          const int iwc = iw < 0 ? 0 : (iw >= g.w ? g.w - 1 : iw);  // clamped: the load is unconditional
+          const S* src = row + static_cast<int64_t>(iwc) * g.c;
+          if constexpr (VW * sizeof(S) == 16) {
+            const uint4 w = *reinterpret_cast<const uint4*>(src);
+            __builtin_memcpy(vals[u].v, &w, 16);
+          } else {
+#pragma unroll
+            for (int e = 0; e < VW; ++e) vals[u].v[e] = src[e];
+          }
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+          if (!ok[u]) continue;
+#pragma unroll
+          for (int e = 0; e < VW; ++e) {
+            const float f = Io<T>::load(vals[u].v[e]);
+            if (MODE == 0) {
+              if (!found || f > acc[e]) acc[e] = f;
+            } else {
+              acc[e] += f;
+            }
+          }
+          found = true;
+        }
+      }
+    }
+    S o[VW];
+#pragma unroll
+    for (int e = 0; e < VW; ++e) o[e] = Io<T>::store(MODE == 0 ? acc[e] : acc[e] / denom);
+    S* dst = y + static_cast<int64_t>(pix) * g.c + cg * VW;
+    if constexpr (VW * sizeof(S) == 16) {
+      uint4 w;
+      __builtin_memcpy(&w, o, 16);
+      *reinterpret_cast<uint4*>(dst) = w;
+    } else {
+#pragma unroll
+      for (int e = 0; e < VW; ++e) dst[e] = o[e];
+    }
+  }
+}
+
+template <typename T>
+fh_status launch_pool_nhwc(int32_t mode, const void* x, void* y, const PoolGeom& g, hipStream_t s) {
+  using S = typename Io<T>::storage;
+  constexpr int V = 16 / static_cast<int>(sizeof(S));
+  const bool vec = g.c % V == 0 && aligned16(x) && aligned16(y);
+  const int64_t total = g.n * g.oh * g.ow * (vec ? g.c / V : g.c);
+  if (total >= (int64_t{1} << 31) || g.n * g.h * g.w >= (int64_t{1} << 31) || g.c >= (int64_t{1} << 31))
+    return fail(FH_UNIMPLEMENTED, "fh_pool2d_nhwc: more than 2^31 outputs or input pixels");
+  const PoolGeom32 g32{static_cast<int32_t>(g.n),  static_cast<int32_t>(g.c),  static_cast<int32_t>(g.h),
+                       static_cast<int32_t>(g.w),  static_cast<int32_t>(g.kh), static_cast<int32_t>(g.kw),
+                       static_cast<int32_t>(g.sh), static_cast<int32_t>(g.sw), static_cast<int32_t>(g.ph),
+                       static_cast<int32_t>(g.pw), static_cast<int32_t>(g.oh), static_cast<int32_t>(g.ow)};
+  int64_t blocks = (total + 255) / 256;
+  const int64_t cap = static_cast<int64_t>(device_cu_count()) * 16;
+  if (blocks > cap) blocks = cap;
+  const dim3 grid(static_cast<uint32_t>(blocks));
+  const auto* xs = static_cast<const S*>(x);
+  auto* ys = static_cast<S*>(y);
+  if (vec) {
+    if (mode == 0) hipLaunchKernelGGL((pool2d_nhwc_kernel<T, 0, V>), grid, dim3(256), 0, s, xs, ys, g32);
+    else hipLaunchKernelGGL((pool2d_nhwc_kernel<T, 1, V>), grid, dim3(256), 0, s, xs, ys, g32);
+  } else {
+    if (mode == 0) hipLaunchKernelGGL((pool2d_nhwc_kernel<T, 0, 1>), grid, dim3(256), 0, s, xs, ys, g32);
+    else hipLaunchKernelGGL((pool2d_nhwc_kernel<T, 1, 1>), grid, dim3(256), 0, s, xs, ys, g32);
+  }
+  return launch_status("pool2d_nhwc_kernel launch");
+}
+
 }  // namespace
 }  // namespace fh
 
 using namespace fh;
 
-extern "C" fh_status fh_pool2d(int32_t dtype, int32_t mode, const void* x, void* y, const int64_t geom[10],
-                               void* stream) {
-  if (!is_supported_float(dtype)) return fail(FH_UNIMPLEMENTED, "fh_pool2d: unsupported dtype");
-  if (mode != 0 && mode != 1) return fail(FH_INVALID_ARGUMENT, "fh_pool2d: mode must be 0 (max) or 1 (avg)");
-  if (geom == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_pool2d: null geometry");
-  PoolGeom g{geom[0], geom[1], geom[2], geom[3], geom[4], geom[5], geom[6], geom[7], geom[8], geom[9], 0, 0};
+namespace {
+
+// Shared argument checks of the pooling entry points; fills g (with Ho, Wo) or returns the error.
+fh_status check_pool(const char* who, int32_t dtype, int32_t mode, const int64_t* geom, PoolGeom& g) {
+  const std::string w(who);
+  if (!is_supported_float(dtype)) return fail(FH_UNIMPLEMENTED, w + ": unsupported dtype");
+  if (mode != 0 && mode != 1) return fail(FH_INVALID_ARGUMENT, w + ": mode must be 0 (max) or 1 (avg)");
+  if (geom == nullptr) return fail(FH_INVALID_ARGUMENT, w + ": null geometry");
+  g = PoolGeom{geom[0], geom[1], geom[2], geom[3], geom[4], geom[5], geom[6], geom[7], geom[8], geom[9], 0, 0};
   if (g.n < 0 || g.c < 0 || g.h < 0 || g.w < 0 || g.kh <= 0 || g.kw <= 0 || g.sh <= 0 || g.sw <= 0 || g.ph < 0 ||
       g.pw < 0)
-    return fail(FH_INVALID_ARGUMENT, "fh_pool2d: invalid geometry");
+    return fail(FH_INVALID_ARGUMENT, w + ": invalid geometry");
   if (g.h + 2 * g.ph < g.kh || g.w + 2 * g.pw < g.kw)
-    return fail(FH_INVALID_ARGUMENT, "fh_pool2d: window larger than the padded input");
+    return fail(FH_INVALID_ARGUMENT, w + ": window larger than the padded input");
   g.oh = (g.h + 2 * g.ph - g.kh) / g.sh + 1;
   g.ow = (g.w + 2 * g.pw - g.kw) / g.sw + 1;
   if (mode == 0) {
     // Every window must hold a valid position: the last window start must not lie beyond the input and the
     // first window must reach into it (reference rejects such windows with kInternal).
     if (g.ph >= g.kh || g.pw >= g.kw || (g.oh - 1) * g.sh - g.ph >= g.h || (g.ow - 1) * g.sw - g.pw >= g.w)
-      return fail(FH_INVALID_ARGUMENT, "fh_pool2d: a max-pool window has no valid (non-padding) position");
+      return fail(FH_INVALID_ARGUMENT, w + ": a max-pool window has no valid (non-padding) position");
   }
+  return FH_OK;
+}
+
+}  // namespace
+
+extern "C" fh_status fh_pool2d(int32_t dtype, int32_t mode, const void* x, void* y, const int64_t geom[10],
+                               void* stream) {
+  PoolGeom g{};
+  if (fh_status st = check_pool("fh_pool2d", dtype, mode, geom, g); st != FH_OK) return st;
   if (g.n * g.c * g.oh * g.ow == 0) return FH_OK;
   if (x == nullptr || y == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_pool2d: null pointer");
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -230,5 +348,22 @@ extern "C" fh_status fh_pool2d(int32_t dtype, int32_t mode, const void* x, void*
       return launch_pool<bf16_t>(mode, x, y, g, s);
     default:
       return launch_pool<f16_t>(mode, x, y, g, s);
+  }
+}
+
+extern "C" fh_status fh_pool2d_nhwc(int32_t dtype, int32_t mode, const void* x, void* y, const int64_t geom[10],
+                                    void* stream) {
+  PoolGeom g{};
+  if (fh_status st = check_pool("fh_pool2d_nhwc", dtype, mode, geom, g); st != FH_OK) return st;
+  if (g.n * g.c * g.oh * g.ow == 0) return FH_OK;
+  if (x == nullptr || y == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_pool2d_nhwc: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case FH_F32:
+      return launch_pool_nhwc<float>(mode, x, y, g, s);
+    case FH_BF16:
+      return launch_pool_nhwc<bf16_t>(mode, x, y, g, s);
+    default:
+      return launch_pool_nhwc<f16_t>(mode, x, y, g, s);
   }
 }

@@ -116,13 +116,17 @@ inline constexpr std::string_view kGemmEpilogueOp = "hip_matmul_epilogue_interna
 inline constexpr std::string_view kConvEpilogueOp = "hip_conv2d_epilogue_internal";
 // [d0, d1, d2, d3] -> [d0, d2, d3, d1]: NCHW activations to NHWC, [Cout][Cin][KH][KW] filters to [Cout][KH][KW][Cin].
 inline constexpr std::string_view kChannelsLastOp = "hip_channels_last_internal";
-// conv2d (optionally with an epilogue program) on channels-last operands; output NCHW.
+// conv2d (optionally with an epilogue program) on channels-last operands; output NCHW, or channels-last
+// [N,Ho,Wo,Cout] with attribute out_nhwc = 1.
 inline constexpr std::string_view kConvNhwcOp = "hip_conv2d_nhwc_internal";
 // channels_last of up to kMultiMaxTensors tensors in one step (a graph's filters; each [d0,d1,d2,d3] ->
 // [d0,d2,d3,d1] with d1*d2*d3 <= kMultiPlaneMax), see fh_transpose_planes_multi.
 inline constexpr std::string_view kChannelsLastMultiOp = "hip_channels_last_multi_internal";
 inline constexpr size_t kMultiMaxTensors = 32;
 inline constexpr int64_t kMultiPlaneMax = 8192;
+// max_pool2d / avg_pool2d on channels-last [N,H,W,C] activations (same attributes; see fh_pool2d_nhwc).
+inline constexpr std::string_view kMaxPoolNhwcOp = "hip_max_pool2d_nhwc_internal";
+inline constexpr std::string_view kAvgPoolNhwcOp = "hip_avg_pool2d_nhwc_internal";
 // Cin <= 8: x [N,C,H,W] -> [N,H,W,8] zero-padded; w [Cout,C,KH,KW] -> [Cout, K8] (see fh_conv_pack_*_c8).
 inline constexpr std::string_view kPackInputC8Op = "hip_pack_input_c8_internal";
 inline constexpr std::string_view kPackFilterC8Op = "hip_pack_filter_c8_internal";

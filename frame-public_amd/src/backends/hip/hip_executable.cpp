@@ -15,7 +15,8 @@
 // consumer's program in the contraction's epilogue. The epilogue rounds to the storage dtype after the
 // product and after every segment, so results equal the unfused graph's bit for bit.
 //  * channels-last conv (every opt_level): a conv that the MFMA implicit-GEMM path accepts becomes
-// channels_last(x), channels_last(w) and conv2d_nhwc (see lower_convs).
+// channels_last(x), channels_last(w) and conv2d_nhwc (see lower_convs); activations whose every use takes
+// channels-last data stay channels-last between convs (see plan_channels_last).
 // The rewrites run on a private copy of the graph before planning, so the memory plan sees the real lifetimes.
 #include <algorithm>
 #include <cstring>
@@ -39,6 +40,12 @@
 namespace frame::backends::hip {
 
 namespace {
+
+template <typename T>
+const T* attr_of(const ir::Node* n, const char* key) {
+  auto it = n->attrs().find(key);
+  return it == n->attrs().end() ? nullptr : std::get_if<T>(&it->second);
+}
 
 // Consumer program as fh_ew_op codes, or empty when the consumer cannot become an epilogue.
 // `operand_index` is the position of the contraction result among the consumer's inputs.
@@ -147,6 +154,89 @@ ConvLowering plan_conv(const ir::Node* n) {
   return p;
 }
 
+// Channels-last activations between convolutions. Values that must share a layout form groups (union-find):
+// an elementwise node's rank-4 operands and result, a pool's input and output, a lowered conv's result and its
+// epilogue operands. A group is kept channels-last ([N,H,W,C] in the lowered graph) when every member is produced
+// by a lowered conv, a pool or an elementwise node, and every use is one that takes channels-last data: input 0
+// of a lowered non-C8 conv, a conv epilogue operand, a pool, an elementwise node, or a reshape of a 1x1 plane
+// (the same bytes in either layout). Graph inputs and outputs stay NCHW, so nothing outside the backend sees it.
+std::unordered_set<const ir::Value*> plan_channels_last(const ir::Graph& src) {
+  std::unordered_map<const ir::Value*, const ir::Value*> parent;
+  auto find = [&](const ir::Value* v) {
+    const ir::Value* r = v;
+    while (parent.count(r) && parent[r] != r) r = parent[r];
+    while (parent.count(v) && parent[v] != r) {  // path compression
+      const ir::Value* next = parent[v];
+      parent[v] = r;
+      v = next;
+    }
+    return r;
+  };
+  auto add = [&](const ir::Value* v) {
+    if (!parent.count(v)) parent[v] = v;
+  };
+  auto unite = [&](const ir::Value* a, const ir::Value* b) {
+    add(a);
+    add(b);
+    const ir::Value *ra = find(a), *rb = find(b);
+    if (ra != rb) parent[ra] = rb;
+  };
+  auto is_ew = [](const ir::Node* n) { return ew_code(n->op()) != 0 || n->op() == ops::kFusedElementwiseOpName; };
+  auto is_pool = [](const ir::Node* n) { return n->op() == "max_pool2d" || n->op() == "avg_pool2d"; };
+  auto rank4 = [](const ir::Value* v) { return v->type().shape.rank() == 4; };
+
+  std::unordered_map<const ir::Value*, std::vector<std::pair<const ir::Node*, size_t>>> uses;
+  std::unordered_map<const ir::Node*, ConvLowering> convs;
+  for (const ir::Node* n : src.topological_order()) {
+    for (size_t i = 0; i < n->inputs().size(); ++i) uses[n->inputs()[i]].push_back({n, i});
+    const ConvLowering p = plan_conv(n);
+    if (p.ok) {
+      convs[n] = p;
+      add(&n->outputs()[0]);
+      if (n->op() == kConvEpilogueOp) {
+        const auto* nm = attr_of<int64_t>(n, "n_main_inputs");
+        for (size_t i = nm ? static_cast<size_t>(*nm) : 2; i < n->inputs().size(); ++i)
+          unite(&n->outputs()[0], n->inputs()[i]);
+      }
+    } else if ((is_ew(n) || is_pool(n)) && n->outputs().size() == 1 && rank4(&n->outputs()[0])) {
+      add(&n->outputs()[0]);
+      for (const ir::Value* in : n->inputs())
+        if (rank4(in)) unite(&n->outputs()[0], in);
+    }
+  }
+  std::unordered_set<const ir::Value*> bad;  // group roots that must stay NCHW
+  std::unordered_set<const ir::Value*> graph_outputs(src.outputs().begin(), src.outputs().end());
+  for (const auto& [v, unused] : parent) {
+    (void)unused;
+    const ir::Value* root = find(v);
+    const ir::Node* p = v->producer();
+    const bool producer_ok = p != nullptr && (convs.count(p) || is_ew(p) || is_pool(p));
+    bool uses_ok = !graph_outputs.count(v);
+    for (const auto& [c, idx] : uses[v]) {
+      if (!uses_ok) break;
+      if (auto it = convs.find(c); it != convs.end()) {
+        const auto* nm = attr_of<int64_t>(c, "n_main_inputs");
+        const size_t n_main = c->op() == kConvEpilogueOp ? (nm ? static_cast<size_t>(*nm) : 2) : c->inputs().size();
+        uses_ok = (idx == 0 && !it->second.c8) || idx >= n_main;
+      } else if (is_ew(c) || is_pool(c)) {
+        uses_ok = rank4(&c->outputs()[0]);
+      } else if (c->op() == "reshape") {
+        const Shape& sh = v->type().shape;
+        uses_ok = sh.rank() == 4 && sh.dim(2) == 1 && sh.dim(3) == 1;
+      } else {
+        uses_ok = false;
+      }
+    }
+    if (!producer_ok || !uses_ok || !rank4(v)) bad.insert(root);
+  }
+  std::unordered_set<const ir::Value*> nhwc;
+  for (const auto& [v, unused] : parent) {
+    (void)unused;
+    if (!bad.count(find(v))) nhwc.insert(v);
+  }
+  return nhwc;
+}
+
 // Lowers every conv2d / conv epilogue node that the channels-last MFMA path accepts (fh_conv2d_nhwc_supported)
 // to  x_nhwc = channels_last(x); w_khwc = channels_last(w); y = conv2d_nhwc(x_nhwc, w_khwc, bias?, ep...).
 // The filters that are graph inputs (weights fed per run) are transposed together by one
@@ -156,6 +246,16 @@ ConvLowering plan_conv(const ir::Node* n) {
 Result<ir::Graph> lower_convs(const ir::Graph& src) {
   std::unordered_map<const ir::Value*, ir::Value*> map;
   ir::Graph out{std::string(src.name())};
+  const std::unordered_set<const ir::Value*> nhwc = plan_channels_last(src);
+  // the lowered graph's type of a source value: [N,H,W,C] when it is kept channels-last
+  auto lowered_type = [&](const ir::Value* v) {
+    ir::TensorType t = v->type();
+    if (nhwc.count(v)) {
+      const Shape& s = t.shape;
+      t.shape = Shape({s.dim(0), s.dim(2), s.dim(3), s.dim(1)});
+    }
+    return t;
+  };
   auto channels_last_type = [](const ir::Value* v) {
     ir::TensorType t = v->type();
     const Shape& s = t.shape;
@@ -233,9 +333,13 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
         w_cl = pw.value()->output(0);
       } else {
         if (!batched_emitted) FRAME_RETURN_IF_ERROR(emit_batched());
-        Result<ir::Value*> xv = channels_last(ins[0]);
-        if (!xv.is_ok()) return xv.status();
-        x_cl = xv.value();
+        if (nhwc.count(n->inputs()[0])) {
+          x_cl = ins[0];  // already channels-last
+        } else {
+          Result<ir::Value*> xv = channels_last(ins[0]);
+          if (!xv.is_ok()) return xv.status();
+          x_cl = xv.value();
+        }
         if (auto it = batched_out.find(n->inputs()[1]); it != batched_out.end()) {
           w_cl = it->second;
         } else {
@@ -247,17 +351,23 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
       std::vector<ir::Value*> conv_ins = ins;
       conv_ins[0] = x_cl;
       conv_ins[1] = w_cl;
-      Result<ir::Node*> c = out.create_node(std::string(kConvNhwcOp), std::move(conv_ins), {n->outputs()[0].type()});
+      Result<ir::Node*> c = out.create_node(std::string(kConvNhwcOp), std::move(conv_ins), {lowered_type(&n->outputs()[0])});
       if (!c.is_ok()) return c.status();
       for (const auto& [k, v] : n->attrs()) c.value()->set_attr(k, v);
+      if (nhwc.count(&n->outputs()[0])) c.value()->set_attr("out_nhwc", ir::AttrValue{int64_t{1}});
       if (n->op() == "conv2d") c.value()->set_attr("n_main_inputs", ir::AttrValue{static_cast<int64_t>(ins.size())});
       c.value()->set_attr("filter_hw", ir::AttrValue{std::vector<int64_t>{geom[5], geom[6]}});
       map[&n->outputs()[0]] = c.value()->output(0);
       continue;
     }
     std::vector<ir::TensorType> types;
-    for (const ir::Value& o : n->outputs()) types.push_back(o.type());
-    Result<ir::Node*> c = out.create_node(std::string(n->op()), std::move(ins), std::move(types));
+    for (const ir::Value& o : n->outputs()) types.push_back(lowered_type(&o));
+    std::string op(n->op());
+    if (n->outputs().size() == 1 && nhwc.count(&n->outputs()[0])) {  // pools of channels-last activations
+      if (op == "max_pool2d") op = std::string(kMaxPoolNhwcOp);
+      if (op == "avg_pool2d") op = std::string(kAvgPoolNhwcOp);
+    }
+    Result<ir::Node*> c = out.create_node(op, std::move(ins), std::move(types));
     if (!c.is_ok()) return c.status();
     for (const auto& [k, v] : n->attrs()) c.value()->set_attr(k, v);
     for (size_t i = 0; i < n->outputs().size(); ++i) map[&n->outputs()[i]] = c.value()->output(static_cast<int32_t>(i));
@@ -267,12 +377,6 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
 }
 
 // ---- attention ---------------------------------------------------------------------------------------------
-
-template <typename T>
-const T* attr_of(const ir::Node* n, const char* key) {
-  auto it = n->attrs().find(key);
-  return it == n->attrs().end() ? nullptr : std::get_if<T>(&it->second);
-}
 
 const ir::Node* producer_op(const ir::Value* v, std::string_view op, size_t n_inputs) {
   const ir::Node* p = v->producer();

@@ -223,13 +223,17 @@ Status conv_nhwc_kernel(KernelContext& ctx) {
     return invalid(op, "filter shape does not match the input's channels");
   const int64_t oh = (geom[2] + 2 * geom[9] - geom[5]) / geom[7] + 1;
   const int64_t ow = (geom[3] + 2 * geom[10] - geom[6]) / geom[8] + 1;
-  if (y.shape() != Shape({geom[0], geom[4], oh, ow})) return invalid(op, "output shape " + y.shape().to_string() + " does not match the geometry");
+  // out_nhwc: y (and the epilogue operands) channels-last [N,Ho,Wo,Cout], else NCHW
+  const auto* out_nhwc_attr = attr<int64_t>(ctx, "out_nhwc");
+  const bool out_nhwc = out_nhwc_attr != nullptr && *out_nhwc_attr != 0;
+  const Shape want = out_nhwc ? Shape({geom[0], oh, ow, geom[4]}) : Shape({geom[0], geom[4], oh, ow});
+  if (y.shape() != want) return invalid(op, "output shape " + y.shape().to_string() + " does not match the geometry");
   if (bias != nullptr && (bias->shape().rank() != 1 || bias->shape().dim(0) != geom[4])) return invalid(op, "bias must be [Cout]");
   Result<fh_epilogue> ep = make_epilogue(ctx, op, n_main);
   if (!ep.is_ok()) return ep.status();
-  FRAME_HIP_RETURN_IF_ERROR(fh_conv2d_nhwc_fwd(dt.value(), x.raw_data(), w.raw_data(), bias ? bias->raw_data() : nullptr,
-                                               y.raw_data(), geom, ep.value().nseg > 0 ? &ep.value() : nullptr,
-                                               stream_handle(ctx)),
+  FRAME_HIP_RETURN_IF_ERROR(fh_conv2d_nhwc_fwd_ex(dt.value(), x.raw_data(), w.raw_data(), bias ? bias->raw_data() : nullptr,
+                                                  y.raw_data(), geom, ep.value().nseg > 0 ? &ep.value() : nullptr,
+                                                  out_nhwc ? FH_CONV_OUT_NHWC : 0, stream_handle(ctx)),
                             "op '" + op + "' (hip)");
   return Status::ok();
 }
@@ -400,6 +404,31 @@ Status pool_kernel(KernelContext& ctx) {
   return Status::ok();
 }
 
+// Channels-last pooling on [N,H,W,C] activations (internal ops of the channels-last lowering), same attributes.
+template <int Mode>
+Status pool_nhwc_kernel(KernelContext& ctx) {
+  const std::string op(Mode == 0 ? kMaxPoolNhwcOp : kAvgPoolNhwcOp);
+  FRAME_RETURN_IF_ERROR(arity(ctx, op, 1, 1));
+  FRAME_RETURN_IF_ERROR(same_dtype(ctx, op));
+  const auto* k = attr<std::vector<int64_t>>(ctx, "kernel");
+  const auto* s = attr<std::vector<int64_t>>(ctx, "stride");
+  const auto* p = attr<std::vector<int64_t>>(ctx, "padding");
+  if (!k || !s || !p || k->size() != 2 || s->size() != 2 || p->size() != 2) return invalid(op, "missing or malformed attributes");
+  const Tensor& x = ctx.inputs[0];
+  if (x.shape().rank() != 4) return invalid(op, "expects rank-4 input");
+  Result<int32_t> dt = float_code(op, x.dtype());
+  if (!dt.is_ok()) return dt.status();
+  const int64_t geom[10] = {x.shape().dim(0), x.shape().dim(3), x.shape().dim(1), x.shape().dim(2), (*k)[0],
+                            (*k)[1],          (*s)[0],          (*s)[1],          (*p)[0],          (*p)[1]};
+  const int64_t oh = (geom[2] + 2 * geom[8] - geom[4]) / geom[6] + 1;
+  const int64_t ow = (geom[3] + 2 * geom[9] - geom[5]) / geom[7] + 1;
+  if (ctx.outputs[0].shape() != Shape({geom[0], oh, ow, geom[1]})) return invalid(op, "output shape does not match the geometry");
+  FRAME_HIP_RETURN_IF_ERROR(fh_pool2d_nhwc(dt.value(), Mode, x.raw_data(), ctx.outputs[0].raw_data(), geom,
+                                           stream_handle(ctx)),
+                            "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
 // ---- data movement (bit-exact, any dtype) -----------------------------------------------------------------
 
 Status reshape_kernel(KernelContext& ctx) {
@@ -528,6 +557,8 @@ FRAME_REGISTER_KERNEL(kAttentionOp, kHipBackendName, &attention_kernel);
 FRAME_REGISTER_KERNEL("layer_norm", kHipBackendName, &layer_norm_kernel);
 FRAME_REGISTER_KERNEL("max_pool2d", kHipBackendName, &pool_kernel<0>);
 FRAME_REGISTER_KERNEL("avg_pool2d", kHipBackendName, &pool_kernel<1>);
+FRAME_REGISTER_KERNEL(kMaxPoolNhwcOp, kHipBackendName, &pool_nhwc_kernel<0>);
+FRAME_REGISTER_KERNEL(kAvgPoolNhwcOp, kHipBackendName, &pool_nhwc_kernel<1>);
 FRAME_REGISTER_KERNEL("reshape", kHipBackendName, &reshape_kernel);
 FRAME_REGISTER_KERNEL("transpose", kHipBackendName, &transpose_kernel);
 FRAME_REGISTER_KERNEL("slice", kHipBackendName, &slice_kernel);

@@ -134,6 +134,14 @@ fh_status fh_conv2d_fwd(int32_t dtype, const void* x, const void* w, const void*
 fh_status fh_conv2d_nhwc_fwd(int32_t dtype, const void* x_nhwc, const void* w_khwc, const void* bias, void* y,
                              const int64_t geom[12], const fh_epilogue* epilogue, void* stream);
 
+/* fh_conv2d_nhwc_fwd with flags: FH_CONV_OUT_NHWC writes y channels-last, [N,Ho,Wo,Cout], and reads the
+ * epilogue's binary operands in that layout too, so a conv can feed the next one without a layout step.
+ * HipBackend::compile uses it for activations whose every consumer takes channels-last data. No counterpart in
+ * the reference (NCHW throughout, reference: src/backends/cuda/kernels/conv.cpp:385-520). */
+#define FH_CONV_OUT_NHWC 1
+fh_status fh_conv2d_nhwc_fwd_ex(int32_t dtype, const void* x_nhwc, const void* w_khwc, const void* bias, void* y,
+                                const int64_t geom[12], const fh_epilogue* epilogue, int32_t flags, void* stream);
+
 /* 1 if fh_conv2d_nhwc_fwd accepts dtype and geom (bf16/f16, groups 1, Cin % 32 == 0 or Cin == 8, 32-bit
  * offsets), else 0. Host-only query used at graph compile time; no counterpart in the reference.
  * With Cin == 8 the operands are in the C8 layout: x from fh_conv_pack_input_c8 and w from
@@ -202,6 +210,11 @@ int32_t fh_attention_supported(int32_t dtype, int64_t seq, int64_t dh);
  * Replaces cudnnPoolingForward (reference: src/backends/cuda/kernels/pool.cpp:172-244);
  * semantics of pool.cpp (reference: src/backends/cpu/kernels/pool.cpp:8-350). */
 fh_status fh_pool2d(int32_t dtype, int32_t mode, const void* x, void* y, const int64_t geom[10], void* stream);
+
+/* fh_pool2d over channels-last data: x [N,H,W,C] -> y [N,Ho,Wo,C], same geom (N, C, H, W, ...), semantics and
+ * scan order per channel. For activations HipBackend::compile keeps channels-last between convolutions. No
+ * counterpart in the reference (NCHW only, reference: src/backends/cpu/kernels/pool.cpp:8-350). */
+fh_status fh_pool2d_nhwc(int32_t dtype, int32_t mode, const void* x, void* y, const int64_t geom[10], void* stream);
 
 /* out[i0..] = x[perm-gathered], rank <= 8, itemsize in {1,2,4,8}. out_dims are the output dims;
  * in_strides_permuted[d] is the input element stride of the input axis that output axis d reads.

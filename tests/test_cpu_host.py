@@ -249,11 +249,38 @@ def test_conv_lowering_by_dtype_and_channels(dtype, cin, lowered):
         assert "hip_conv2d_nhwc_internal" not in out
 
 
-def test_resnet_filters_are_transposed_in_one_step():
-    # every non-stem conv filter is a graph input: one batched channels-last step instead of one per layer
+def test_resnet_lowering_is_channels_last_throughout():
+    # every non-stem conv filter is a graph input: one batched channels-last step instead of one per layer; every
+    # activation is produced and consumed channels-last (convs, residual epilogues, both pools, the 1x1 reshape),
+    # so no activation transpose is left
     g, _ = graphs.resnet18(batch=2, dtype=3, image=64)
-    ops = re.findall(r"= (\w+)\(", host.hip_lowered(g.text(), 1))
+    out = host.hip_lowered(g.text(), 1)
+    ops = re.findall(r"= (\w+)\(", out)
     assert ops.count("hip_channels_last_multi_internal") == 1
     assert ops.count("hip_conv2d_nhwc_internal") == 20
-    assert ops.count("hip_channels_last_internal") == 19  # the activations
+    assert ops.count("hip_channels_last_internal") == 0
+    assert ops.count("hip_max_pool2d_nhwc_internal") == 1 and ops.count("hip_avg_pool2d_nhwc_internal") == 1
     assert ops.count("graph_input") == 43
+    assert out.count("out_nhwc=1") == 20
+
+
+def _conv_chain(last_is_output=True, softmax_tail=False):
+    g = graphs.Graph("hip")
+    x = g.input(3, (2, 32, 10, 10))
+    w1, w2 = g.input(3, (32, 32, 3, 3)), g.input(3, (32, 32, 3, 3))
+    a = g.relu(g.conv2d(x, w1, padding=(1, 1)))
+    b = g.conv2d(a, w2, padding=(1, 1))
+    if softmax_tail:
+        g.output(g.softmax(g.reshape(b, (2 * 32 * 10, 10))))
+    else:
+        g.output(b)
+    return g
+
+
+def test_channels_last_stops_at_graph_outputs_and_other_uses():
+    # the first conv's result feeds the second conv only: channels-last; the second is a graph output: NCHW
+    out = host.hip_lowered(_conv_chain().text(), 1)
+    assert out.count("out_nhwc=1") == 1 and "hip_channels_last_internal" in out  # x of the first conv
+    # a reshape of a non-1x1 plane needs NCHW order: the second conv stays NCHW
+    out = host.hip_lowered(_conv_chain(softmax_tail=True).text(), 1)
+    assert out.count("out_nhwc=1") == 1

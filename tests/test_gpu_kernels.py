@@ -469,6 +469,54 @@ def test_conv2d_nhwc_large_tiles_sampled(hip, dtype, geom):
     assert_close(got[idx], want, dtype, what=f"conv nhwc large {geom}")
 
 
+NHWC_OUT_CASES = [
+    (BF16, (2, 64, 12, 12, 64, 3, 3, 1, 1, 1, 1, 1)),
+    (BF16, (2, 64, 14, 14, 128, 1, 1, 2, 2, 0, 0, 1)),    # 1x1 stride-2 downsample
+    (BF16, (1, 32, 9, 11, 40, 3, 5, 1, 2, 2, 0, 1)),      # Cout 40: whole 8-channel vectors, 5 groups
+    (BF16, (1, 32, 9, 9, 36, 3, 3, 1, 1, 1, 1, 1)),       # Cout 36: element stores
+    (F32, (2, 48, 7, 9, 64, 3, 3, 2, 1, 1, 1, 1)),
+]
+
+
+@pytest.mark.parametrize("dtype,geom", NHWC_OUT_CASES)
+def test_conv2d_nhwc_channels_last_output(hip, dtype, geom):
+    # FH_CONV_OUT_NHWC: y [N,Ho,Wo,Cout] with the residual add;relu epilogue read channels-last as well
+    say(f"conv nhwc-out dtype={dtype} {geom}")
+    n, cin, h, w, cout, kh, kw = geom[:7]
+    x = synth.tensor(151, (n, cin, h, w), dtype, "normal")
+    wt = synth.tensor(152, (cout, cin, kh, kw), dtype, "normal", (2.0 / (cin * kh * kw)) ** 0.5)
+    bias = synth.tensor(153, (cout,), dtype, "normal", 0.1)
+    conv = orc.conv2d(dtype, x, wt, bias, geom)
+    res = synth.tensor(154, conv.shape, dtype, "normal")
+    want = to_nhwc(orc.ew_program(dtype, [1, 3], [2, 1], [conv, res]))
+    dx, dw, db, dr = dev(hip, to_nhwc(x)), dev(hip, to_nhwc(wt)), dev(hip, bias), dev(hip, to_nhwc(res))
+    dy = hip.DeviceBuffer(want.nbytes)
+    ep = hip.make_epilogue([(hip.EW_ADD, dr.value), (hip.EW_RELU, None)])
+    hip.check(hip.lib().fh_conv2d_nhwc_fwd_ex(dtype, dx.value, dw.value, db.value, dy.value, hip.i64_array(geom),
+                                              ctypes.byref(ep), 1, None))
+    got = dy.download(want.shape, want.dtype)
+    assert_close(got, want, dtype, what=f"conv nhwc-out {geom}")
+
+
+@pytest.mark.parametrize("dtype", [BF16, F32])
+@pytest.mark.parametrize("mode,geom", [
+    (0, (2, 64, 16, 16, 3, 3, 2, 2, 1, 1)),   # ResNet stem pool, channels-last
+    (1, (2, 64, 7, 7, 7, 7, 1, 1, 0, 0)),     # global average pool
+    (0, (1, 12, 9, 9, 3, 3, 2, 2, 1, 1)),     # C not a multiple of the vector width: one channel per lane
+    (1, (1, 16, 6, 6, 3, 3, 2, 2, 1, 1)),     # average with padding counted
+    (0, (1, 16, 12, 12, 10, 10, 1, 1, 0, 0)), # window rows wider than one batch of 8 loads
+    (1, (1, 24, 12, 12, 10, 9, 1, 1, 1, 0)),
+])
+def test_pool2d_nhwc(hip, dtype, mode, geom):
+    say(f"pool nhwc mode={mode} dtype={dtype} {geom}")
+    n, c, h, w = geom[:4]
+    x = synth.tensor(161, (n, c, h, w), dtype, "normal")
+    want = to_nhwc(orc.pool2d(dtype, mode, x, geom))
+    dx, dy = dev(hip, to_nhwc(x)), hip.DeviceBuffer(want.nbytes)
+    hip.check(hip.lib().fh_pool2d_nhwc(dtype, mode, dx.value, dy.value, hip.i64_array(geom), None))
+    assert_bitwise(dy.download(want.shape, want.dtype), want, f"pool nhwc mode={mode}")
+
+
 @pytest.mark.parametrize("dtype", [BF16, F32])
 def test_conv2d_nhwc_epilogue_add_relu(hip, dtype):
     # conv + bias, then the residual add;relu of a ResNet basic block, rounded between segments
