@@ -383,10 +383,11 @@ template <typename T>
 fh_status dispatch_gemm(GemmArgs args, int64_t batch, hipStream_t stream) {
   constexpr int E = GemmTraits<T>::E;
   const int cus = device_cu_count();
-  // Few 64 x 64 tiles (less than a quarter of the CUs busy): the sequential kernel, whose 16 x 16 tiles spread
-  // further and whose latency is a handful of K chunks.
+  // Few 64 x 64 tiles: the sequential kernel, whose 16 x 16 tiles spread further and whose latency is a handful
+  // of K chunks. fp32 below a quarter of the CUs; 16-bit only below 16 tiles (its MFMA kernel stays faster down
+  // to there: the C4 classifier, 16 tiles, 7.8 us there against 22 us sequential).
   const int64_t tiles64 = ((args.M + 63) / 64) * ((args.N + 63) / 64) * batch;
-  const bool small = tiles64 * 4 < cus && args.K <= 16384;
+  const bool small = (std::is_same_v<T, float> ? tiles64 * 4 < cus : tiles64 < 16) && args.K <= 16384;
   if constexpr (!std::is_same_v<T, float>) {
     fh_status st = FH_OK;
     if (!small && gemm16_try_launch(std::is_same_v<T, bf16_t> ? FH_BF16 : FH_F16, args, batch, stream, &st)) return st;

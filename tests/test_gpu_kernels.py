@@ -69,23 +69,26 @@ def test_gemm_matches_oracle(hip, dtype, shape):
     assert_close(got, want, dtype, what=f"gemm {shape}")
 
 
-# Small problems (fewer 64x64 tiles than a quarter of the CUs) and unaligned operands run the sequential kernel:
-# one output per thread with k summed in order in fp32, like the reference CPU kernel, so it matches bit for bit.
+# Small problems (fp32: fewer 64x64 tiles than a quarter of the CUs; 16-bit: fewer than 16) and unaligned operands
+# run the sequential kernel: one output per thread with k summed in order in fp32, like the reference CPU
+# kernel, so it matches bit for bit.
 SEQ_SHAPES = [
     (64, 784, 256),   # C1 layer 1
     (64, 256, 10),    # C1 layer 2
-    (64, 512, 1000),  # C4 classifier
     (128, 128, 128),
-    (300, 264, 200),  # ragged tiles
     (512, 512, 64),
     (1, 8, 8),
     (3, 1, 5),        # K = 1
     (7, 131, 3),      # K tail shorter than one 4-wide step
 ]
+SEQ_SHAPES_F32_ONLY = [
+    (64, 512, 1000),  # the C4 classifier shape (16 tiles: MFMA for 16-bit types)
+    (300, 264, 200),  # ragged tiles (20 tiles)
+]
 
 
-@pytest.mark.parametrize("dtype", [F32, BF16, F16])
-@pytest.mark.parametrize("shape", SEQ_SHAPES)
+@pytest.mark.parametrize("dtype,shape", [(d, s) for d in (F32, BF16, F16) for s in SEQ_SHAPES] +
+                         [(F32, s) for s in SEQ_SHAPES_F32_ONLY])
 def test_gemm_small_bit_exact(hip, dtype, shape):
     m, k, n = shape
     say(f"gemm small dtype={dtype} m={m} k={k} n={n}")
