@@ -154,10 +154,13 @@ __device__ inline float ew_unary(uint8_t op, float x) {
 }
 
 __device__ inline float ew_binary(uint8_t op, float a, float b) {
+  if (op == FH_EW_RELU_GRAD) return a > 0.0f ? b : 0.0f;
   return op == FH_EW_MUL ? a * b : a + b;
 }
 
-__host__ __device__ inline bool ew_is_binary(uint8_t op) { return op == FH_EW_ADD || op == FH_EW_MUL; }
+__host__ __device__ constexpr bool ew_is_binary(uint8_t op) {
+  return op == FH_EW_ADD || op == FH_EW_MUL || op == FH_EW_RELU_GRAD;
+}
 
 // The fused elementwise program of a GEMM / conv epilogue (EpilogueArgs, ConvEpilogue: nseg, round_between,
 // ops[], ins[]): segment s applies ops[s] to the running value, a binary op taking its second operand from

@@ -213,7 +213,8 @@ __global__ __launch_bounds__(kEwThreads) void ew_vec_kernel(EwArgs a) {
       const bool last = s + 1 == a.nseg;
       switch (op) {
         case FH_EW_ADD:
-        case FH_EW_MUL: {
+        case FH_EW_MUL:
+        case FH_EW_RELU_GRAD: {
           ew_u4 t = cur[0];
 #pragma unroll
           for (int k = 1; k < NIN; ++k)
@@ -223,6 +224,9 @@ __global__ __launch_bounds__(kEwThreads) void ew_vec_kernel(EwArgs a) {
           if (op == FH_EW_ADD) {
 #pragma unroll
             for (int e = 0; e < V; ++e) v[e] = v[e] + w[e];
+          } else if (op == FH_EW_RELU_GRAD) {
+#pragma unroll
+            for (int e = 0; e < V; ++e) v[e] = v[e] > 0.0f ? w[e] : 0.0f;
           } else {
 #pragma unroll
             for (int e = 0; e < V; ++e) v[e] = v[e] * w[e];
@@ -259,7 +263,7 @@ __global__ __launch_bounds__(kEwThreads) void ew_vec_kernel(EwArgs a) {
 // input fixed. OPS are fh_ew_op codes; NIN = 1 + the number of binary segments.
 template <uint8_t... OPS>
 constexpr int ew_inputs() {
-  return 1 + ((OPS == FH_EW_ADD || OPS == FH_EW_MUL ? 1 : 0) + ... + 0);
+  return 1 + ((ew_is_binary(OPS) ? 1 : 0) + ... + 0);
 }
 
 template <typename T, uint8_t... OPS>
@@ -283,17 +287,18 @@ __global__ __launch_bounds__(kEwThreads) void ew_fixed_kernel(EwArgs a) {
       (
           [&] {
             constexpr uint8_t op = ops[S];
-            constexpr bool binary = op == FH_EW_ADD || op == FH_EW_MUL;
+            constexpr bool binary = ew_is_binary(op);
             // input of segment S: 1 + the binary segments before it
             constexpr int in_idx = [] {
               int n = 1;
-              for (int q = 0; q < S; ++q) n += (ops[q] == FH_EW_ADD || ops[q] == FH_EW_MUL) ? 1 : 0;
+              for (int q = 0; q < S; ++q) n += ew_is_binary(ops[q]) ? 1 : 0;
               return n;
             }();
             if constexpr (binary) {
               L::unpack(cur[in_idx], w);
 #pragma unroll
-              for (int e = 0; e < V; ++e) v[e] = op == FH_EW_ADD ? v[e] + w[e] : v[e] * w[e];
+              for (int e = 0; e < V; ++e)
+                v[e] = op == FH_EW_ADD ? v[e] + w[e] : op == FH_EW_MUL ? v[e] * w[e] : (v[e] > 0.0f ? w[e] : 0.0f);
             } else if constexpr (op == FH_EW_RELU) {
 #pragma unroll
               for (int e = 0; e < V; ++e) v[e] = (v[e] < 0.0f) ? 0.0f : v[e];
@@ -334,6 +339,7 @@ bool launch_fixed(const EwArgs& a, dim3 grid, hipStream_t stream) {
       case FH_EW_RELU: FH_EW_FIXED(FH_EW_RELU);
       case FH_EW_GELU: FH_EW_FIXED(FH_EW_GELU);
       case FH_EW_SQUARE: FH_EW_FIXED(FH_EW_SQUARE);
+      case FH_EW_RELU_GRAD: FH_EW_FIXED(FH_EW_RELU_GRAD);
       default: return false;
     }
   }
@@ -471,7 +477,7 @@ extern "C" fh_status fh_ew_program(int32_t dtype, int32_t nseg, const uint8_t* o
   int expected = 0;
   for (int s = 0; s < nseg; ++s) {
     const uint8_t op = ops[s];
-    if (op < FH_EW_ADD || op > FH_EW_GELU)
+    if (op < FH_EW_ADD || op > FH_EW_RELU_GRAD)
       return fail(FH_INVALID_ARGUMENT, "fh_ew_program: unknown op code " + std::to_string(op));
     const int want = ew_is_binary(op) ? 2 : 1;
     if (arities[s] != want)

@@ -24,6 +24,9 @@ struct GemmArgs {
   int64_t stride_a, stride_b, stride_c;  // batch strides in elements (blockIdx.y)
   int32_t tiles_m, tiles_n;
   EpilogueArgs ep;
+  // Transposed operand storage, honoured by the sequential kernel only: A(m, k) = A[k * lda + m],
+  // B(k, n) = B[n * ldb + k].
+  int32_t trans_a, trans_b;
 };
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));

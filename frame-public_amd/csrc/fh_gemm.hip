@@ -309,9 +309,9 @@ __global__ __launch_bounds__(256) void gemm_seq_kernel(GemmArgs args) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const int64_t gm = m0 + r, gk = k0 + c + 16 * i;
-      la[i] = (gm < M && gk < K) ? Io<T>::load(A[gm * args.lda + gk]) : 0.0f;
+      la[i] = (gm < M && gk < K) ? Io<T>::load(A[args.trans_a ? gk * args.lda + gm : gm * args.lda + gk]) : 0.0f;
       const int64_t bk = k0 + r + 16 * i, bn = n0 + c;
-      lb[i] = (bk < K && bn < N) ? Io<T>::load(B[bk * args.ldb + bn]) : 0.0f;
+      lb[i] = (bk < K && bn < N) ? Io<T>::load(B[args.trans_b ? bn * args.ldb + bk : bk * args.ldb + bn]) : 0.0f;
     }
   };
   auto store_chunk = [&](int buf) {
@@ -504,4 +504,40 @@ extern "C" fh_status fh_gemm_batched(int32_t dtype, const void* A, const void* B
   args.stride_b = stride_b;
   args.stride_c = stride_c;
   return run_gemm(dtype, args, batch, static_cast<hipStream_t>(stream));
+}
+
+// matmul_grad_lhs_internal (rhs = 0): out [m,k] = gy [m,n] * b[k,n]^T; matmul_grad_rhs_internal (rhs = 1):
+// out [k,n] = a[m,k]^T * gy [m,n]. The sequential kernel reads the transposed operand in place, so every output is
+// one fp32 sum over the contraction index in ascending order (reference: src/backends/cpu/kernels/matmul.cpp:187-327).
+extern "C" fh_status fh_matmul_grad(int32_t dtype, int32_t rhs, const void* p, const void* q, void* out, int64_t m,
+                                    int64_t n, int64_t k, void* stream) {
+  using namespace fh;
+  if (!is_supported_float(dtype)) return fail(FH_UNIMPLEMENTED, "fh_matmul_grad: unsupported dtype");
+  if (m < 0 || n < 0 || k < 0) return fail(FH_INVALID_ARGUMENT, "fh_matmul_grad: negative dimension");
+  GemmArgs args{};
+  if (rhs == 0) {  // A = gy [m,n] (contraction n), B(j, c) = b[c * n + j]
+    args.A = p, args.B = q, args.M = m, args.N = k, args.K = n, args.lda = n, args.ldb = n, args.ldc = k;
+    args.trans_b = 1;
+  } else {  // A(c, i) = a[i * k + c], B = gy [m,n] (contraction m)
+    args.A = p, args.B = q, args.M = k, args.N = n, args.K = m, args.lda = k, args.ldb = n, args.ldc = n;
+    args.trans_a = 1;
+  }
+  args.C = out;
+  if (args.M == 0 || args.N == 0) return FH_OK;
+  if (p == nullptr || q == nullptr || out == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_matmul_grad: null pointer");
+  if ((args.M + kSeqT - 1) / kSeqT > 65535) return fail(FH_UNIMPLEMENTED, "fh_matmul_grad: more than 1,048,560 rows");
+  const dim3 grid(static_cast<uint32_t>((args.N + kSeqT - 1) / kSeqT), static_cast<uint32_t>((args.M + kSeqT - 1) / kSeqT), 1);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case FH_F32:
+      hipLaunchKernelGGL((gemm_seq_kernel<float>), grid, dim3(256), 0, s, args);
+      break;
+    case FH_BF16:
+      hipLaunchKernelGGL((gemm_seq_kernel<bf16_t>), grid, dim3(256), 0, s, args);
+      break;
+    default:
+      hipLaunchKernelGGL((gemm_seq_kernel<f16_t>), grid, dim3(256), 0, s, args);
+      break;
+  }
+  return launch_status("fh_matmul_grad");
 }

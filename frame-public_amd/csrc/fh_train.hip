@@ -1,0 +1,522 @@
+// Training-path kernels: the gradient-only ops of compiler::build_backward_graph's graphs (pool gradients, conv
+// gradients, sum and its gradient, mse_loss and its gradient). matmul_grad_{lhs,rhs} are lowered to a transpose
+// plus the GEMM kernels by the backend, relu_grad_internal is an elementwise program op (FH_EW_RELU_GRAD).
+//
+// Where a result is a per-element sequential sum in the reference (pool gradients, conv gradients), each output is
+// accumulated by one thread in the reference's order with the same fp32 operations, so fp32 results are
+// bit-identical and 16-bit ones differ only if the reference's single final rounding does (it does not: same
+// float, same rounding). sum and mse_loss are tree reductions in fp32 (deterministic, not in the reference's
+// order); their parity is a tolerance.
+#include "fh_common.h"
+
+namespace fh {
+namespace {
+
+constexpr int kThreads = 256;
+
+int64_t blocks_for(int64_t n, int per = kThreads) { return (n + per - 1) / per; }
+
+// ---- pool gradients (gather form) --------------------------------------------------------------------------
+
+struct PoolG {
+  int32_t n, c, h, w, kh, kw, sh, sw, ph, pw, oh, ow;
+};
+
+// One thread per input element. max: the covering windows in (oh, ow) ascending order, each window's argmax
+// recomputed exactly as the forward (first strict maximum in (kh, kw) order over non-padding taps), dy added
+// when the argmax is this element (reference: src/backends/cpu/kernels/pool.cpp:186-206, 358-388, where the
+// windows scatter in that order into a float buffer). avg: kh then kw ascending over the covering windows, sum of
+// dy, then / (KH*KW) (reference: pool.cpp:543-566).
+template <typename T, int MODE>
+__global__ __launch_bounds__(kThreads) void pool2d_grad_kernel(const typename Io<T>::storage* __restrict__ dy,
+                                                               const typename Io<T>::storage* __restrict__ x,
+                                                               typename Io<T>::storage* __restrict__ dx, PoolG g,
+                                                               int64_t total) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= total) return;
+  const int32_t iw = static_cast<int32_t>(i % g.w);
+  const int32_t ih = static_cast<int32_t>((i / g.w) % g.h);
+  const int64_t nc = i / (static_cast<int64_t>(g.w) * g.h);
+  const auto* dyp = dy + nc * g.oh * g.ow;
+  float acc = 0.0f;
+  if constexpr (MODE == 0) {
+    const auto* xp = x + nc * g.h * g.w;
+    // windows whose rows cover ih: oh*sh - ph <= ih <= oh*sh - ph + kh - 1
+    const int32_t th = ih + g.ph - g.kh + 1, tw = iw + g.pw - g.kw + 1;  // first window start reaching ih / iw
+    const int32_t oh_lo = th <= 0 ? 0 : (th + g.sh - 1) / g.sh;
+    const int32_t ow_lo = tw <= 0 ? 0 : (tw + g.sw - 1) / g.sw;
+    const int32_t oh_hi = min(g.oh - 1, (ih + g.ph) / g.sh);
+    const int32_t ow_hi = min(g.ow - 1, (iw + g.pw) / g.sw);
+    for (int32_t oh = oh_lo; oh <= oh_hi; ++oh) {
+      const int32_t h0 = oh * g.sh - g.ph;
+      if (ih < h0 || ih >= h0 + g.kh) continue;
+      for (int32_t ow = ow_lo; ow <= ow_hi; ++ow) {
+        const int32_t w0 = ow * g.sw - g.pw;
+        if (iw < w0 || iw >= w0 + g.kw) continue;
+        bool found = false;
+        float best = 0.0f;
+        int32_t at = -1;
+        for (int32_t a = 0; a < g.kh; ++a) {
+          const int32_t hh = h0 + a;
+          if (hh < 0 || hh >= g.h) continue;
+          for (int32_t b = 0; b < g.kw; ++b) {
+            const int32_t ww = w0 + b;
+            if (ww < 0 || ww >= g.w) continue;
+            const float v = Io<T>::load(xp[hh * g.w + ww]);
+            if (!found || v > best) {
+              found = true;
+              best = v;
+              at = hh * g.w + ww;
+            }
+          }
+        }
+        if (at == ih * g.w + iw) acc += Io<T>::load(dyp[oh * g.ow + ow]);
+      }
+    }
+    dx[i] = Io<T>::store(acc);
+  } else {
+    for (int32_t a = 0; a < g.kh; ++a) {
+      const int32_t nh = ih + g.ph - a;
+      if (nh < 0 || nh % g.sh != 0) continue;
+      const int32_t oh = nh / g.sh;
+      if (oh >= g.oh) continue;
+      for (int32_t b = 0; b < g.kw; ++b) {
+        const int32_t nw = iw + g.pw - b;
+        if (nw < 0 || nw % g.sw != 0) continue;
+        const int32_t ow = nw / g.sw;
+        if (ow >= g.ow) continue;
+        acc += Io<T>::load(dyp[oh * g.ow + ow]);
+      }
+    }
+    dx[i] = Io<T>::store(acc / static_cast<float>(g.kh * g.kw));
+  }
+}
+
+// ---- conv gradients (direct, reference order) ----------------------------------------------------------------
+
+struct ConvG {
+  int32_t n, cin, h, w, cout, kh, kw, sh, sw, ph, pw, groups, oh, ow;
+};
+
+// dx[n, cf, ih, iw] = sum over co of cf's group, kh, kw (ascending) of dy * w at the taps where ih + ph - kh is a
+// multiple of the stride inside dy (reference: src/backends/cpu/kernels/conv.cpp:320-352).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void conv_grad_input_kernel(const typename Io<T>::storage* __restrict__ dy,
+                                                                   const typename Io<T>::storage* __restrict__ wt,
+                                                                   typename Io<T>::storage* __restrict__ dx, ConvG g,
+                                                                   int64_t total) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= total) return;
+  const int32_t iw = static_cast<int32_t>(i % g.w);
+  const int32_t ih = static_cast<int32_t>((i / g.w) % g.h);
+  const int32_t cf = static_cast<int32_t>((i / (static_cast<int64_t>(g.w) * g.h)) % g.cin);
+  const int64_t n = i / (static_cast<int64_t>(g.w) * g.h * g.cin);
+  const int32_t cin_g = g.cin / g.groups, cout_g = g.cout / g.groups;
+  const int32_t grp = cf / cin_g, ci = cf - grp * cin_g;
+  float acc = 0.0f;
+  for (int32_t co = grp * cout_g; co < (grp + 1) * cout_g; ++co) {
+    const auto* dyc = dy + (n * g.cout + co) * g.oh * g.ow;
+    const auto* wc = wt + (static_cast<int64_t>(co) * cin_g + ci) * g.kh * g.kw;
+    for (int32_t a = 0; a < g.kh; ++a) {
+      const int32_t nh = ih + g.ph - a;
+      if (nh < 0 || nh % g.sh != 0) continue;
+      const int32_t oh = nh / g.sh;
+      if (oh >= g.oh) continue;
+      for (int32_t b = 0; b < g.kw; ++b) {
+        const int32_t nw = iw + g.pw - b;
+        if (nw < 0 || nw % g.sw != 0) continue;
+        const int32_t ow = nw / g.sw;
+        if (ow >= g.ow) continue;
+        acc += Io<T>::load(dyc[oh * g.ow + ow]) * Io<T>::load(wc[a * g.kw + b]);
+      }
+    }
+  }
+  dx[i] = Io<T>::store(acc);
+}
+
+// dw[co, ci, kh, kw] = sum over n, oh, ow (ascending) of x * dy, padding taps skipped
+// (reference: src/backends/cpu/kernels/conv.cpp:423-451).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void conv_grad_filter_kernel(const typename Io<T>::storage* __restrict__ x,
+                                                                    const typename Io<T>::storage* __restrict__ dy,
+                                                                    typename Io<T>::storage* __restrict__ dw, ConvG g,
+                                                                    int64_t total) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= total) return;
+  const int32_t cin_g = g.cin / g.groups, cout_g = g.cout / g.groups;
+  const int32_t b = static_cast<int32_t>(i % g.kw);
+  const int32_t a = static_cast<int32_t>((i / g.kw) % g.kh);
+  const int32_t ci = static_cast<int32_t>((i / (static_cast<int64_t>(g.kw) * g.kh)) % cin_g);
+  const int32_t co = static_cast<int32_t>(i / (static_cast<int64_t>(g.kw) * g.kh * cin_g));
+  const int32_t cf = (co / cout_g) * cin_g + ci;
+  float acc = 0.0f;
+  for (int32_t n = 0; n < g.n; ++n) {
+    const auto* xc = x + (static_cast<int64_t>(n) * g.cin + cf) * g.h * g.w;
+    const auto* dyc = dy + (static_cast<int64_t>(n) * g.cout + co) * g.oh * g.ow;
+    for (int32_t oh = 0; oh < g.oh; ++oh) {
+      const int32_t ih = oh * g.sh - g.ph + a;
+      if (ih < 0 || ih >= g.h) continue;
+      for (int32_t ow = 0; ow < g.ow; ++ow) {
+        const int32_t iw = ow * g.sw - g.pw + b;
+        if (iw < 0 || iw >= g.w) continue;
+        acc += Io<T>::load(xc[ih * g.w + iw]) * Io<T>::load(dyc[oh * g.ow + ow]);
+      }
+    }
+  }
+  dw[i] = Io<T>::store(acc);
+}
+
+// ---- sum / sum_grad_internal -------------------------------------------------------------------------------
+
+constexpr int kMaxDims = 8;
+
+// x's dims split into kept (output) and reduced groups, adjacent dims of the same kind merged. Offsets in x are
+// base(kept coordinates) + roff(reduced coordinates).
+struct ReduceG {
+  int32_t nk, nr;
+  int64_t kdim[kMaxDims], kstride[kMaxDims];
+  int64_t rdim[kMaxDims], rstride[kMaxDims];
+  int64_t nout, nred;
+};
+
+__device__ inline int64_t decompose(int64_t idx, int32_t nd, const int64_t* dim, const int64_t* stride) {
+  int64_t off = 0;
+  for (int32_t d = nd - 1; d >= 0; --d) {
+    const int64_t c = idx % dim[d];
+    idx /= dim[d];
+    off += c * stride[d];
+  }
+  return off;
+}
+
+constexpr int kSumThreads = 512;
+
+// One workgroup per output: fp32 partial sums strided over the reduced elements, then a fixed-shape tree.
+template <typename T>
+__global__ __launch_bounds__(kSumThreads) void sum_kernel(const typename Io<T>::storage* __restrict__ x,
+                                                          typename Io<T>::storage* __restrict__ out, ReduceG g) {
+  __shared__ float part[kSumThreads / 64];
+  const int64_t o = blockIdx.x;
+  const int64_t base = decompose(o, g.nk, g.kdim, g.kstride);
+  float acc = 0.0f;
+  if (g.nr == 1 && g.rstride[0] == 1) {
+    for (int64_t r = threadIdx.x; r < g.nred; r += kSumThreads) acc += Io<T>::load(x[base + r]);
+  } else {
+    for (int64_t r = threadIdx.x; r < g.nred; r += kSumThreads)
+      acc += Io<T>::load(x[base + decompose(r, g.nr, g.rdim, g.rstride)]);
+  }
+  for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float s = 0.0f;
+    for (int k = 0; k < kSumThreads / 64; ++k) s += part[k];
+    out[o] = Io<T>::store(s);
+  }
+}
+
+// gx[i] = gy[projection of i]: a copy of the storage bits.
+template <typename S>
+__global__ __launch_bounds__(kThreads) void sum_grad_kernel(const S* __restrict__ gy, S* __restrict__ gx, ReduceG g,
+                                                            int64_t total) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= total) return;
+  // kdim holds every dim of x and kstride the matching stride in gy (0 for a reduced dim)
+  gx[i] = gy[decompose(i, g.nk, g.kdim, g.kstride)];
+}
+
+// ---- mse_loss ----------------------------------------------------------------------------------------------
+
+constexpr int kLossThreads = 1024;
+
+template <typename T>
+__global__ __launch_bounds__(kLossThreads) void mse_loss_kernel(const typename Io<T>::storage* __restrict__ p,
+                                                                const typename Io<T>::storage* __restrict__ t,
+                                                                typename Io<T>::storage* __restrict__ out, int64_t n) {
+  __shared__ float part[kLossThreads / 64];
+  float acc = 0.0f;
+  for (int64_t i = threadIdx.x; i < n; i += kLossThreads) {
+    const float d = Io<T>::load(p[i]) - Io<T>::load(t[i]);
+    acc += d * d;
+  }
+  for (int m = 32; m >= 1; m >>= 1) acc += __shfl_xor(acc, m);
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float s = 0.0f;
+    for (int k = 0; k < kLossThreads / 64; ++k) s += part[k];
+    out[0] = Io<T>::store(s / static_cast<float>(n));
+  }
+}
+
+// gpred = (2 * gy / numel) * (pred - target), the reference's operations in its order
+// (reference: src/backends/cpu/kernels/loss.cpp:230-262).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void mse_loss_grad_kernel(const typename Io<T>::storage* __restrict__ p,
+                                                                 const typename Io<T>::storage* __restrict__ t,
+                                                                 const typename Io<T>::storage* __restrict__ gy,
+                                                                 typename Io<T>::storage* __restrict__ out, int64_t n) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= n) return;
+  const float c = 2.0f * Io<T>::load(gy[0]) / static_cast<float>(n);
+  out[i] = Io<T>::store(c * (Io<T>::load(p[i]) - Io<T>::load(t[i])));
+}
+
+// ---- host side ---------------------------------------------------------------------------------------------
+
+template <template <typename> class K, typename... A>
+fh_status dispatch(int32_t dtype, A&&... args) {
+  switch (dtype) {
+    case FH_F32:
+      return K<float>::run(args...);
+    case FH_BF16:
+      return K<bf16_t>::run(args...);
+    default:
+      return K<f16_t>::run(args...);
+  }
+}
+
+bool grid_ok(int64_t blocks) { return blocks <= 0x7fffffffLL; }
+
+template <typename T>
+struct PoolGradRun {
+  static fh_status run(int32_t mode, const void* dy, const void* x, void* dx, const PoolG& g, int64_t total,
+                       hipStream_t s) {
+    using S = typename Io<T>::storage;
+    const dim3 grid(static_cast<uint32_t>(blocks_for(total)));
+    if (mode == 0)
+      hipLaunchKernelGGL((pool2d_grad_kernel<T, 0>), grid, dim3(kThreads), 0, s, static_cast<const S*>(dy),
+                         static_cast<const S*>(x), static_cast<S*>(dx), g, total);
+    else
+      hipLaunchKernelGGL((pool2d_grad_kernel<T, 1>), grid, dim3(kThreads), 0, s, static_cast<const S*>(dy),
+                         static_cast<const S*>(x), static_cast<S*>(dx), g, total);
+    return launch_status("fh_pool2d_grad");
+  }
+};
+
+template <typename T>
+struct ConvGradRun {
+  static fh_status run(int filter, const void* p, const void* q, void* out, const ConvG& g, int64_t total, hipStream_t s) {
+    using S = typename Io<T>::storage;
+    const dim3 grid(static_cast<uint32_t>(blocks_for(total)));
+    if (filter)
+      hipLaunchKernelGGL((conv_grad_filter_kernel<T>), grid, dim3(kThreads), 0, s, static_cast<const S*>(p),
+                         static_cast<const S*>(q), static_cast<S*>(out), g, total);
+    else
+      hipLaunchKernelGGL((conv_grad_input_kernel<T>), grid, dim3(kThreads), 0, s, static_cast<const S*>(p),
+                         static_cast<const S*>(q), static_cast<S*>(out), g, total);
+    return launch_status(filter ? "fh_conv2d_grad_filter" : "fh_conv2d_grad_input");
+  }
+};
+
+template <typename T>
+struct SumRun {
+  static fh_status run(const void* x, void* out, const ReduceG& g, hipStream_t s) {
+    using S = typename Io<T>::storage;
+    hipLaunchKernelGGL((sum_kernel<T>), dim3(static_cast<uint32_t>(g.nout)), dim3(kSumThreads), 0, s,
+                       static_cast<const S*>(x), static_cast<S*>(out), g);
+    return launch_status("fh_sum");
+  }
+};
+
+template <typename T>
+struct MseRun {
+  static fh_status run(int grad, const void* p, const void* t, const void* gy, void* out, int64_t n, hipStream_t s) {
+    using S = typename Io<T>::storage;
+    if (grad)
+      hipLaunchKernelGGL((mse_loss_grad_kernel<T>), dim3(static_cast<uint32_t>(blocks_for(n))), dim3(kThreads), 0, s,
+                         static_cast<const S*>(p), static_cast<const S*>(t), static_cast<const S*>(gy), static_cast<S*>(out),
+                         n);
+    else
+      hipLaunchKernelGGL((mse_loss_kernel<T>), dim3(1), dim3(kLossThreads), 0, s, static_cast<const S*>(p),
+                         static_cast<const S*>(t), static_cast<S*>(out), n);
+    return launch_status(grad ? "fh_mse_loss_grad" : "fh_mse_loss");
+  }
+};
+
+fh_status conv_geom(const char* who, int32_t dtype, const int64_t* geom, ConvG& g) {
+  const std::string w(who);
+  if (!is_supported_float(dtype)) return fail(FH_UNIMPLEMENTED, w + ": unsupported dtype");
+  if (geom == nullptr) return fail(FH_INVALID_ARGUMENT, w + ": null geometry");
+  for (int k = 0; k < 12; ++k)
+    if (geom[k] < 0 || geom[k] > 0x7fffffffLL) return fail(FH_INVALID_ARGUMENT, w + ": geometry entry out of range");
+  g = ConvG{static_cast<int32_t>(geom[0]), static_cast<int32_t>(geom[1]), static_cast<int32_t>(geom[2]),
+            static_cast<int32_t>(geom[3]), static_cast<int32_t>(geom[4]), static_cast<int32_t>(geom[5]),
+            static_cast<int32_t>(geom[6]), static_cast<int32_t>(geom[7]), static_cast<int32_t>(geom[8]),
+            static_cast<int32_t>(geom[9]), static_cast<int32_t>(geom[10]), static_cast<int32_t>(geom[11]), 0, 0};
+  if (g.kh <= 0 || g.kw <= 0 || g.sh <= 0 || g.sw <= 0 || g.groups <= 0 || g.cin % g.groups != 0 ||
+      g.cout % g.groups != 0)
+    return fail(FH_INVALID_ARGUMENT, w + ": invalid geometry");
+  const int64_t oh = (static_cast<int64_t>(g.h) + 2 * g.ph - g.kh), ow = (static_cast<int64_t>(g.w) + 2 * g.pw - g.kw);
+  if (oh < 0 || ow < 0) return fail(FH_INVALID_ARGUMENT, w + ": filter larger than the padded input");
+  g.oh = static_cast<int32_t>(oh / g.sh + 1);
+  g.ow = static_cast<int32_t>(ow / g.sw + 1);
+  return FH_OK;
+}
+
+// Splits x's dims into merged kept / reduced groups (row-major strides).
+void build_reduce(int32_t rank, const int64_t* dims, const uint8_t* reduced, ReduceG& g) {
+  g = ReduceG{};
+  int64_t stride = 1;
+  int64_t kd[kMaxDims], ks[kMaxDims], rd[kMaxDims], rs[kMaxDims];
+  int nk = 0, nr = 0;
+  int last = -1;  // kind of the previous (inner) dim: 0 kept, 1 reduced
+  for (int32_t d = rank - 1; d >= 0; --d) {
+    const int kind = reduced[d] ? 1 : 0;
+    if (dims[d] == 1) {  // size-1 dims contribute nothing
+      continue;
+    }
+    if (kind == last) {  // merge with the adjacent inner dim of the same kind (contiguous in row-major order)
+      if (kind) rd[nr - 1] *= dims[d];
+      else kd[nk - 1] *= dims[d];
+    } else if (kind) {
+      rd[nr] = dims[d];
+      rs[nr] = stride;
+      ++nr;
+    } else {
+      kd[nk] = dims[d];
+      ks[nk] = stride;
+      ++nk;
+    }
+    last = kind;
+    stride *= dims[d];
+  }
+  // stored outermost first
+  g.nk = nk;
+  g.nr = nr;
+  g.nout = 1;
+  g.nred = 1;
+  for (int k = 0; k < nk; ++k) {
+    g.kdim[k] = kd[nk - 1 - k];
+    g.kstride[k] = ks[nk - 1 - k];
+    g.nout *= g.kdim[k];
+  }
+  for (int k = 0; k < nr; ++k) {
+    g.rdim[k] = rd[nr - 1 - k];
+    g.rstride[k] = rs[nr - 1 - k];
+    g.nred *= g.rdim[k];
+  }
+}
+
+fh_status check_reduce(const char* who, int32_t rank, const int64_t* dims, const uint8_t* reduced) {
+  const std::string w(who);
+  if (rank < 0 || rank > kMaxDims) return fail(FH_UNIMPLEMENTED, w + ": rank above 8");
+  if (rank > 0 && (dims == nullptr || reduced == nullptr)) return fail(FH_INVALID_ARGUMENT, w + ": null dims");
+  for (int32_t d = 0; d < rank; ++d)
+    if (dims[d] < 0) return fail(FH_INVALID_ARGUMENT, w + ": negative dimension");
+  return FH_OK;
+}
+
+}  // namespace
+}  // namespace fh
+
+using namespace fh;
+
+extern "C" fh_status fh_pool2d_grad(int32_t dtype, int32_t mode, const void* dy, const void* x, void* dx,
+                                    const int64_t geom[10], void* stream) {
+  if (!is_supported_float(dtype)) return fail(FH_UNIMPLEMENTED, "fh_pool2d_grad: unsupported dtype");
+  if (mode != 0 && mode != 1) return fail(FH_INVALID_ARGUMENT, "fh_pool2d_grad: mode must be 0 (max) or 1 (avg)");
+  if (geom == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_pool2d_grad: null geometry");
+  for (int k = 0; k < 10; ++k)
+    if (geom[k] < 0 || geom[k] > 0x7fffffffLL) return fail(FH_INVALID_ARGUMENT, "fh_pool2d_grad: geometry entry out of range");
+  PoolG g{static_cast<int32_t>(geom[0]), static_cast<int32_t>(geom[1]), static_cast<int32_t>(geom[2]),
+          static_cast<int32_t>(geom[3]), static_cast<int32_t>(geom[4]), static_cast<int32_t>(geom[5]),
+          static_cast<int32_t>(geom[6]), static_cast<int32_t>(geom[7]), static_cast<int32_t>(geom[8]),
+          static_cast<int32_t>(geom[9]), 0, 0};
+  if (g.kh <= 0 || g.kw <= 0 || g.sh <= 0 || g.sw <= 0 || g.h + 2 * g.ph < g.kh || g.w + 2 * g.pw < g.kw)
+    return fail(FH_INVALID_ARGUMENT, "fh_pool2d_grad: invalid geometry");
+  g.oh = (g.h + 2 * g.ph - g.kh) / g.sh + 1;
+  g.ow = (g.w + 2 * g.pw - g.kw) / g.sw + 1;
+  if (mode == 0 && (g.ph >= g.kh || g.pw >= g.kw || (g.oh - 1) * g.sh - g.ph >= g.h || (g.ow - 1) * g.sw - g.pw >= g.w))
+    return fail(FH_INVALID_ARGUMENT, "fh_pool2d_grad: a max-pool window has no valid (non-padding) position");
+  const int64_t total = static_cast<int64_t>(g.n) * g.c * g.h * g.w;
+  if (total == 0) return FH_OK;
+  if (dy == nullptr || dx == nullptr || (mode == 0 && x == nullptr))
+    return fail(FH_INVALID_ARGUMENT, "fh_pool2d_grad: null pointer");
+  if (!grid_ok(blocks_for(total))) return fail(FH_INVALID_ARGUMENT, "fh_pool2d_grad: tensor too large");
+  return dispatch<PoolGradRun>(dtype, mode, dy, x, dx, g, total, static_cast<hipStream_t>(stream));
+}
+
+extern "C" fh_status fh_conv2d_grad_input(int32_t dtype, const void* dy, const void* w, void* dx,
+                                          const int64_t geom[12], void* stream) {
+  ConvG g{};
+  if (fh_status st = conv_geom("fh_conv2d_grad_input", dtype, geom, g); st != FH_OK) return st;
+  const int64_t total = static_cast<int64_t>(g.n) * g.cin * g.h * g.w;
+  if (total == 0) return FH_OK;
+  if (dy == nullptr || w == nullptr || dx == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_conv2d_grad_input: null pointer");
+  if (!grid_ok(blocks_for(total))) return fail(FH_INVALID_ARGUMENT, "fh_conv2d_grad_input: tensor too large");
+  return dispatch<ConvGradRun>(dtype, 0, dy, w, dx, g, total, static_cast<hipStream_t>(stream));
+}
+
+extern "C" fh_status fh_conv2d_grad_filter(int32_t dtype, const void* x, const void* dy, void* dw,
+                                           const int64_t geom[12], void* stream) {
+  ConvG g{};
+  if (fh_status st = conv_geom("fh_conv2d_grad_filter", dtype, geom, g); st != FH_OK) return st;
+  const int64_t total = static_cast<int64_t>(g.cout) * (g.cin / g.groups) * g.kh * g.kw;
+  if (total == 0) return FH_OK;
+  if (x == nullptr || dy == nullptr || dw == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_conv2d_grad_filter: null pointer");
+  return dispatch<ConvGradRun>(dtype, 1, x, dy, dw, g, total, static_cast<hipStream_t>(stream));
+}
+
+extern "C" fh_status fh_sum(int32_t dtype, const void* x, void* out, int32_t rank, const int64_t* dims,
+                            const uint8_t* reduced, void* stream) {
+  if (!is_supported_float(dtype)) return fail(FH_UNIMPLEMENTED, "fh_sum: unsupported dtype");
+  if (fh_status st = check_reduce("fh_sum", rank, dims, reduced); st != FH_OK) return st;
+  uint8_t all[kMaxDims];
+  for (int32_t d = 0; d < rank; ++d) all[d] = reduced[d];
+  ReduceG g{};
+  build_reduce(rank, dims, all, g);
+  int64_t numel = 1;
+  for (int32_t d = 0; d < rank; ++d) numel *= dims[d];
+  if (g.nout == 0) return FH_OK;
+  if (x == nullptr || out == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_sum: null pointer");
+  if (numel == 0) g.nred = 0;  // an empty reduction writes zeros
+  if (!grid_ok(g.nout)) return fail(FH_INVALID_ARGUMENT, "fh_sum: too many outputs");
+  return dispatch<SumRun>(dtype, x, out, g, static_cast<hipStream_t>(stream));
+}
+
+extern "C" fh_status fh_sum_grad(int32_t dtype, const void* gy, void* gx, int32_t rank, const int64_t* dims,
+                                 const uint8_t* reduced, void* stream) {
+  if (!is_supported_float(dtype)) return fail(FH_UNIMPLEMENTED, "fh_sum_grad: unsupported dtype");
+  if (fh_status st = check_reduce("fh_sum_grad", rank, dims, reduced); st != FH_OK) return st;
+  // full dims of x with the output (gy) strides of each dim, reduced dims striding 0
+  ReduceG g{};
+  g.nk = rank;
+  int64_t total = 1, ostride = 1;
+  for (int32_t d = rank - 1; d >= 0; --d) {
+    g.kdim[d] = dims[d];
+    g.kstride[d] = reduced[d] ? 0 : ostride;
+    if (!reduced[d]) ostride *= dims[d];
+    total *= dims[d];
+  }
+  if (total == 0) return FH_OK;
+  if (gy == nullptr || gx == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_sum_grad: null pointer");
+  if (!grid_ok(blocks_for(total))) return fail(FH_INVALID_ARGUMENT, "fh_sum_grad: tensor too large");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<uint32_t>(blocks_for(total)));
+  if (dtype == FH_F32)
+    hipLaunchKernelGGL((sum_grad_kernel<uint32_t>), grid, dim3(kThreads), 0, s, static_cast<const uint32_t*>(gy),
+                       static_cast<uint32_t*>(gx), g, total);
+  else
+    hipLaunchKernelGGL((sum_grad_kernel<uint16_t>), grid, dim3(kThreads), 0, s, static_cast<const uint16_t*>(gy),
+                       static_cast<uint16_t*>(gx), g, total);
+  return launch_status("fh_sum_grad");
+}
+
+extern "C" fh_status fh_mse_loss(int32_t dtype, const void* pred, const void* target, void* out, int64_t numel,
+                                 void* stream) {
+  if (!is_supported_float(dtype)) return fail(FH_UNIMPLEMENTED, "fh_mse_loss: unsupported dtype");
+  if (numel <= 0) return fail(FH_INVALID_ARGUMENT, "fh_mse_loss: empty input (numel 0)");
+  if (pred == nullptr || target == nullptr || out == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_mse_loss: null pointer");
+  return dispatch<MseRun>(dtype, 0, pred, target, nullptr, out, numel, static_cast<hipStream_t>(stream));
+}
+
+extern "C" fh_status fh_mse_loss_grad(int32_t dtype, const void* pred, const void* target, const void* gy, void* out,
+                                      int64_t numel, void* stream) {
+  if (!is_supported_float(dtype)) return fail(FH_UNIMPLEMENTED, "fh_mse_loss_grad: unsupported dtype");
+  if (numel <= 0) return fail(FH_INVALID_ARGUMENT, "fh_mse_loss_grad: empty input (numel 0)");
+  if (pred == nullptr || target == nullptr || gy == nullptr || out == nullptr)
+    return fail(FH_INVALID_ARGUMENT, "fh_mse_loss_grad: null pointer");
+  if (!grid_ok(blocks_for(numel))) return fail(FH_INVALID_ARGUMENT, "fh_mse_loss_grad: tensor too large");
+  return dispatch<MseRun>(dtype, 1, pred, target, gy, out, numel, static_cast<hipStream_t>(stream));
+}

@@ -85,6 +85,14 @@ _SIGS = {
     "fh_layer_norm_rows": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_float,
                                      c_void_p]),
     "fh_pool2d_nhwc": (c_int32, [c_int32, c_int32, c_void_p, c_void_p, POINTER(c_int64), c_void_p]),
+    "fh_matmul_grad": (c_int32, [c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p]),
+    "fh_pool2d_grad": (c_int32, [c_int32, c_int32, c_void_p, c_void_p, c_void_p, POINTER(c_int64), c_void_p]),
+    "fh_conv2d_grad_input": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, POINTER(c_int64), c_void_p]),
+    "fh_conv2d_grad_filter": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, POINTER(c_int64), c_void_p]),
+    "fh_sum": (c_int32, [c_int32, c_void_p, c_void_p, c_int32, POINTER(c_int64), c_void_p, c_void_p]),
+    "fh_sum_grad": (c_int32, [c_int32, c_void_p, c_void_p, c_int32, POINTER(c_int64), c_void_p, c_void_p]),
+    "fh_mse_loss": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
+    "fh_mse_loss_grad": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
     "fh_conv2d_nhwc_fwd_ex": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_void_p, POINTER(c_int64), c_void_p,
                                         c_int32, c_void_p]),
     "fh_pool2d": (c_int32, [c_int32, c_int32, c_void_p, c_void_p, POINTER(c_int64), c_void_p]),

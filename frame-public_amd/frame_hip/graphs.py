@@ -150,6 +150,20 @@ class Graph:
         shape[axis] = sum(x.shape[axis] for x in xs)
         return self.op("concat", xs, shape, {"axis": axis})
 
+    def mse_loss(self, pred, target):
+        return self.op("mse_loss", [pred, target], ())
+
+    def sum(self, x, axes, keepdims=False):
+        red = set(range(len(x.shape))) if not axes else set(axes)
+        shape = tuple((1 if keepdims else None) if i in red else d for i, d in enumerate(x.shape))
+        attrs = {"axes": list(axes)}
+        if keepdims:
+            attrs["keepdims"] = True
+        return self.op("sum", [x], tuple(d for d in shape if d is not None), attrs)
+
+    def square(self, a):
+        return self.op("square", [a], a.shape)
+
     def constant_splat(self, dtype, shape, value):
         n = int(np.prod(shape))
         return self.op("constant", [], shape, {"value": [float(value)] * n, "shape": Shape(shape), "dtype": DType(dtype)},
@@ -177,6 +191,68 @@ def mlp_inputs(batch=64, dtype=F32, seed=1):
             synth.tensor(0, (batch, 256), dtype, "zeros"),
             synth.tensor(seed + 2, (256, 10), dtype, "normal", math.sqrt(2.0 / 256)),
             synth.tensor(0, (batch, 10), dtype, "zeros")]
+
+
+def mlp_train(batch=64, dtype=F32, device="hip", hidden=256, classes=10, features=784):
+    """C1's MLP as a training objective: mse_loss(logits, target). Inputs x, w1, b1, w2, b2, target; output the loss.
+    The parameters are graph inputs 1..4 (the wrt list of the backward graph)."""
+    g = Graph(device)
+    x = g.input(dtype, (batch, features))
+    w1 = g.input(dtype, (features, hidden))
+    b1 = g.input(dtype, (batch, hidden))
+    w2 = g.input(dtype, (hidden, classes))
+    b2 = g.input(dtype, (batch, classes))
+    t = g.input(dtype, (batch, classes))
+    h = g.relu(g.add(g.matmul(x, w1), b1))
+    g.output(g.mse_loss(g.add(g.matmul(h, w2), b2), t))
+    return g
+
+
+def mlp_train_inputs(batch=64, dtype=F32, seed=11, hidden=256, classes=10, features=784):
+    return [synth.tensor(seed, (batch, features), dtype, "normal"),
+            synth.tensor(seed + 1, (features, hidden), dtype, "normal", math.sqrt(2.0 / features)),
+            synth.tensor(seed + 2, (batch, hidden), dtype, "normal", 0.1),
+            synth.tensor(seed + 3, (hidden, classes), dtype, "normal", math.sqrt(2.0 / hidden)),
+            synth.tensor(seed + 4, (batch, classes), dtype, "normal", 0.1),
+            synth.tensor(seed + 5, (batch, classes), dtype, "normal")]
+
+
+def cnn_train(batch=8, dtype=F32, device="hip", cin=3, image=32, c1=32, c2=64, classes=10):
+    """A small CNN training objective over every gradient-path op: conv+bias, relu, 3x3/s2 max pool, strided conv,
+    residual add, square, global avg pool, reshape, matmul, add, mse_loss. Parameters are inputs 1..7."""
+    g = Graph(device)
+    x = g.input(dtype, (batch, cin, image, image))
+    w1 = g.input(dtype, (c1, cin, 3, 3))
+    b1 = g.input(dtype, (c1,))
+    w2 = g.input(dtype, (c2, c1, 3, 3))
+    w3 = g.input(dtype, (c2, c2, 1, 1))
+    wf = g.input(dtype, (c2, classes))
+    bf = g.input(dtype, (batch, classes))
+    scale = g.input(dtype, (batch, c2, image // 4, image // 4))
+    t = g.input(dtype, (batch, classes))
+    h = g.relu(g.conv2d(x, w1, b1, stride=(1, 1), padding=(1, 1)))
+    h = g.pool("max_pool2d", h, (3, 3), (2, 2), (1, 1))
+    h = g.relu(g.conv2d(h, w2, None, stride=(2, 2), padding=(1, 1)))
+    r = g.conv2d(h, w3, None, stride=(1, 1), padding=(0, 0))
+    h = g.relu(g.add(h, g.mul(g.square(r), scale)))
+    s = image // 4
+    h = g.pool("avg_pool2d", h, (s, s), (s, s), (0, 0))
+    h = g.reshape(h, (batch, c2))
+    g.output(g.mse_loss(g.add(g.matmul(h, wf), bf), t))
+    return g
+
+
+def cnn_train_inputs(batch=8, dtype=F32, seed=21, cin=3, image=32, c1=32, c2=64, classes=10):
+    s = image // 4
+    return [synth.tensor(seed, (batch, cin, image, image), dtype, "normal"),
+            synth.tensor(seed + 1, (c1, cin, 3, 3), dtype, "normal", math.sqrt(2.0 / (cin * 9))),
+            synth.tensor(seed + 2, (c1,), dtype, "normal", 0.1),
+            synth.tensor(seed + 3, (c2, c1, 3, 3), dtype, "normal", math.sqrt(2.0 / (c1 * 9))),
+            synth.tensor(seed + 4, (c2, c2, 1, 1), dtype, "normal", math.sqrt(1.0 / c2)),
+            synth.tensor(seed + 5, (c2, classes), dtype, "normal", math.sqrt(2.0 / c2)),
+            synth.tensor(seed + 6, (batch, classes), dtype, "normal", 0.1),
+            synth.tensor(seed + 7, (batch, c2, s, s), dtype, "normal", 0.1),
+            synth.tensor(seed + 8, (batch, classes), dtype, "normal")]
 
 
 # ---- C2: GEMM -------------------------------------------------------------------------------------------------

@@ -62,6 +62,8 @@ _SIGS = {
     "frame_roundtrip_text": (c_int32, [c_char_p, c_void_p, c_int64, POINTER(c_int64)]),
     "frame_memory_plan_text": (c_int32, [c_char_p, c_void_p, c_int64, POINTER(c_int64)]),
     "frame_hip_lowered_text": (c_int32, [c_char_p, c_int32, c_void_p, c_int64, POINTER(c_int64)]),
+    "frame_backward_text": (c_int32, [c_char_p, c_int32, c_void_p, c_int32, c_void_p, c_int64, POINTER(c_int64)]),
+    "frame_sgd_update_text": (c_int32, [c_char_p, c_void_p, c_int32, ctypes.c_double, c_void_p, c_int64, POINTER(c_int64)]),
     "frame_launch": (c_int32, [c_char_p, c_char_p, POINTER(c_void_p), c_int32, POINTER(c_void_p), c_int32, c_void_p]),
 }
 
@@ -121,6 +123,18 @@ def hip_lowered(ir_text: str, opt_level: int = 1) -> str:
     return _text(lib().frame_hip_lowered_text, ir_text.encode(), opt_level)
 
 
+def backward(ir_text: str, loss_index: int, wrt) -> str:
+    """compiler::build_backward_graph on IR text: forward outputs, then d(output loss_index)/d(inputs wrt)."""
+    idx = (ctypes.c_int32 * max(1, len(wrt)))(*wrt)
+    return _text(lib().frame_backward_text, ir_text.encode(), loss_index, idx, len(wrt))
+
+
+def sgd_update(ir_text: str, param_inputs, learning_rate: float) -> str:
+    """compiler::build_sgd_update_graph for the types of graph inputs `param_inputs` of `ir_text`."""
+    idx = (ctypes.c_int32 * max(1, len(param_inputs)))(*param_inputs)
+    return _text(lib().frame_sgd_update_text, ir_text.encode(), idx, len(param_inputs), learning_rate)
+
+
 def roundtrip(ir_text: str) -> str:
     return _text(lib().frame_roundtrip_text, ir_text.encode())
 
@@ -148,8 +162,8 @@ class Tensor:
 
     @classmethod
     def from_numpy(cls, backend: str, dtype: int, array: np.ndarray) -> "Tensor":
-        a = np.ascontiguousarray(array, dtype=_NP[dtype])
-        t = cls(backend, dtype, a.shape)
+        a = np.ascontiguousarray(array, dtype=_NP[dtype])  # (ndim >= 1: a rank-0 array comes back as [1])
+        t = cls(backend, dtype, np.shape(array))
         check(lib().frame_tensor_upload(t.handle, a.ctypes.data, a.nbytes), "frame_tensor_upload")
         return t
 

@@ -704,8 +704,67 @@ class HipExecutable final : public hal::Executable {
 
 }  // namespace
 
+// Whether a matmul_grad node's GEMM is large enough for the tiled kernels: the same threshold as fh_gemm's
+// dispatch on a 256-CU device (fp32 from 64 tiles of 64 x 64, 16-bit from 16). Smaller ones stay
+// matmul_grad_*_internal and run on fh_matmul_grad's sequential kernel, which reads the transposed operand in place.
+bool matmul_grad_wants_gemm(const ir::Node* n) {
+  const bool lhs = n->op() == "matmul_grad_lhs_internal";
+  if (!lhs && n->op() != "matmul_grad_rhs_internal") return false;
+  const Shape& p = n->inputs()[0]->type().shape;
+  const Shape& q = n->inputs()[1]->type().shape;
+  const int64_t M = lhs ? p.dim(0) : p.dim(1), N = lhs ? q.dim(0) : q.dim(1), K = lhs ? p.dim(1) : p.dim(0);
+  const int64_t tiles64 = ((M + 63) / 64) * ((N + 63) / 64);
+  const bool f32 = n->inputs()[0]->type().dtype.code() == DTypeCode::kFloat32;
+  return (f32 ? tiles64 >= 64 : tiles64 >= 16) || K > 16384;
+}
+
+// matmul_grad_lhs_internal(gy, b) = gy * b^T and matmul_grad_rhs_internal(a, gy) = a^T * gy, when large, become a
+// transpose of the transposed operand plus a plain matmul, so they run on the tiled GEMM kernels with the same
+// products and fp32 accumulation as the reference (src/backends/cpu/kernels/matmul.cpp:187-327). Returns a clone
+// of the source when no node qualifies.
+Result<ir::Graph> lower_matmul_grads(const ir::Graph& src) {
+  const auto& order = src.topological_order();
+  const bool any = std::any_of(order.begin(), order.end(), matmul_grad_wants_gemm);
+  if (!any) return ir::clone_graph(src);
+  std::unordered_map<const ir::Value*, ir::Value*> map;
+  ir::Graph out{std::string(src.name())};
+  for (const ir::Node* n : order) {
+    if (n->op() == ir::kGraphInputOp) {
+      Result<ir::Value*> v = out.add_graph_input(n->outputs()[0].type());
+      if (!v.is_ok()) return v.status();
+      map[&n->outputs()[0]] = v.value();
+      continue;
+    }
+    std::vector<ir::Value*> ins;
+    for (const ir::Value* in : n->inputs()) ins.push_back(map.at(in));
+    if (matmul_grad_wants_gemm(n)) {
+      const bool lhs = n->op() == "matmul_grad_lhs_internal";
+      ir::Value* t_in = lhs ? ins[1] : ins[0];  // b of gy*b^T, a of a^T*gy
+      ir::TensorType tt = t_in->type();
+      tt.shape = Shape({tt.shape.dim(1), tt.shape.dim(0)});
+      Result<ir::Node*> t = out.create_node("transpose", {t_in}, {tt});
+      if (!t.is_ok()) return t.status();
+      t.value()->set_attr("perm", ir::AttrValue{std::vector<int64_t>{1, 0}});
+      std::vector<ir::Value*> mm_in = lhs ? std::vector<ir::Value*>{ins[0], t.value()->output(0)}
+                                          : std::vector<ir::Value*>{t.value()->output(0), ins[1]};
+      Result<ir::Node*> mm = out.create_node("matmul", std::move(mm_in), {n->outputs()[0].type()});
+      if (!mm.is_ok()) return mm.status();
+      map[&n->outputs()[0]] = mm.value()->output(0);
+      continue;
+    }
+    std::vector<ir::TensorType> types;
+    for (const ir::Value& o : n->outputs()) types.push_back(o.type());
+    Result<ir::Node*> c = out.create_node(std::string(n->op()), std::move(ins), std::move(types));
+    if (!c.is_ok()) return c.status();
+    for (const auto& [k, v] : n->attrs()) c.value()->set_attr(k, v);
+    for (size_t j = 0; j < n->outputs().size(); ++j) map[&n->outputs()[j]] = c.value()->output(static_cast<int32_t>(j));
+  }
+  for (const ir::Value* o : src.outputs()) FRAME_RETURN_IF_ERROR(out.mark_output(map.at(o)));
+  return out;
+}
+
 Result<ir::Graph> lower_for_hip(const ir::Graph& graph, int32_t opt_level) {
-  Result<ir::Graph> work = ir::clone_graph(graph);
+  Result<ir::Graph> work = lower_matmul_grads(graph);
   if (!work.is_ok()) return work.status();
   // Attention runs at every level (like the conv lowering), before the epilogue fusion would claim its matmuls.
   FRAME_RETURN_IF_ERROR(lower_attention(work.value()));

@@ -2,6 +2,7 @@
 // libframe_hip_kernels.so on the context's stream. Registered with FRAME_REGISTER_KERNEL(op, "hip", fn) like
 // every Frame backend's kernels (reference: include/frame/ops/kernel_registry.h:104-107). The design analogs
 // replaced are the cuda kernels under src/backends/cuda/kernels/ (cuBLASLt, cuDNN and the .cu files).
+#include <array>
 #include <cstdint>
 #include <string>
 #include <vector>
@@ -76,7 +77,7 @@ Status run_program(const KernelContext& ctx, const std::string& op, const std::v
 
 template <uint8_t Code, int Arity>
 Status ew_kernel(KernelContext& ctx) {
-  static const std::string names[] = {"", "add", "mul", "relu", "square", "gelu"};
+  static const std::string names[] = {"", "add", "mul", "relu", "square", "gelu", "relu_grad_internal"};
   const std::string& op = names[Code];
   FRAME_RETURN_IF_ERROR(arity(ctx, op, Arity, 1));
   return run_program(ctx, op, {Code}, {static_cast<int8_t>(Arity)});
@@ -404,6 +405,151 @@ Status pool_kernel(KernelContext& ctx) {
   return Status::ok();
 }
 
+// ---- training path -----------------------------------------------------------------------------------------
+
+// Geometry array of fh_pool2d / fh_pool2d_grad for input dims `x` and the op's kernel/stride/padding attributes.
+Result<std::array<int64_t, 10>> pool_geom(KernelContext& ctx, const std::string& op, const Shape& x) {
+  const auto* k = attr<std::vector<int64_t>>(ctx, "kernel");
+  const auto* s = attr<std::vector<int64_t>>(ctx, "stride");
+  const auto* p = attr<std::vector<int64_t>>(ctx, "padding");
+  if (!k || !s || !p || k->size() != 2 || s->size() != 2 || p->size() != 2) return invalid(op, "missing or malformed attributes");
+  if (x.rank() != 4) return invalid(op, "expects a rank-4 input_shape");
+  return std::array<int64_t, 10>{x.dim(0), x.dim(1), x.dim(2), x.dim(3), (*k)[0], (*k)[1], (*s)[0], (*s)[1], (*p)[0], (*p)[1]};
+}
+
+// matmul_grad_lhs_internal (gy [m,n], b [k,n]) -> [m,k]; matmul_grad_rhs_internal (a [m,k], gy [m,n]) -> [k,n].
+template <int Rhs>
+Status matmul_grad_kernel(KernelContext& ctx) {
+  const std::string op = Rhs ? "matmul_grad_rhs_internal" : "matmul_grad_lhs_internal";
+  FRAME_RETURN_IF_ERROR(arity(ctx, op, 2, 1));
+  FRAME_RETURN_IF_ERROR(same_dtype(ctx, op));
+  const Shape& p = ctx.inputs[0].shape();
+  const Shape& q = ctx.inputs[1].shape();
+  if (p.rank() != 2 || q.rank() != 2) return invalid(op, "expects rank-2 operands");
+  const int64_t m = p.dim(0), n = Rhs ? q.dim(1) : p.dim(1), k = Rhs ? p.dim(1) : q.dim(0);
+  if ((Rhs ? q.dim(0) : q.dim(1)) != (Rhs ? m : n)) return invalid(op, "contraction dimension mismatch");
+  if (ctx.outputs[0].shape() != (Rhs ? Shape({k, n}) : Shape({m, k}))) return invalid(op, "output shape mismatch");
+  Result<int32_t> dt = float_code(op, ctx.outputs[0].dtype());
+  if (!dt.is_ok()) return dt.status();
+  FRAME_HIP_RETURN_IF_ERROR(fh_matmul_grad(dt.value(), Rhs, ctx.inputs[0].raw_data(), ctx.inputs[1].raw_data(),
+                                           ctx.outputs[0].raw_data(), m, n, k, stream_handle(ctx)),
+                            "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
+template <int Mode>
+Status pool_grad_kernel(KernelContext& ctx) {
+  const std::string op = Mode == 0 ? "max_pool2d_grad_internal" : "avg_pool2d_grad_internal";
+  FRAME_RETURN_IF_ERROR(arity(ctx, op, Mode == 0 ? 2 : 1, 1));
+  FRAME_RETURN_IF_ERROR(same_dtype(ctx, op));
+  const Shape* xs = attr<Shape>(ctx, "input_shape");
+  if (xs == nullptr) return invalid(op, "missing attribute 'input_shape'");
+  Result<std::array<int64_t, 10>> g = pool_geom(ctx, op, *xs);
+  if (!g.is_ok()) return g.status();
+  if (ctx.outputs[0].shape() != *xs) return invalid(op, "output shape does not match input_shape");
+  if (Mode == 0 && ctx.inputs[1].shape() != *xs) return invalid(op, "x shape does not match input_shape");
+  const auto& geom = g.value();
+  const int64_t oh = (geom[2] + 2 * geom[8] - geom[4]) / geom[6] + 1, ow = (geom[3] + 2 * geom[9] - geom[5]) / geom[7] + 1;
+  if (ctx.inputs[0].shape() != Shape({geom[0], geom[1], oh, ow})) return invalid(op, "dy shape does not match the geometry");
+  Result<int32_t> dt = float_code(op, ctx.outputs[0].dtype());
+  if (!dt.is_ok()) return dt.status();
+  FRAME_HIP_RETURN_IF_ERROR(fh_pool2d_grad(dt.value(), Mode, ctx.inputs[0].raw_data(),
+                                           Mode == 0 ? ctx.inputs[1].raw_data() : nullptr, ctx.outputs[0].raw_data(),
+                                           geom.data(), stream_handle(ctx)),
+                            "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
+// conv2d_grad_input_internal (dy, w) -> dx of input_shape; conv2d_grad_filter_internal (x, dy) -> dw of filter_shape.
+template <int Filter>
+Status conv_grad_kernel(KernelContext& ctx) {
+  const std::string op = Filter ? "conv2d_grad_filter_internal" : "conv2d_grad_input_internal";
+  FRAME_RETURN_IF_ERROR(arity(ctx, op, 2, 1));
+  FRAME_RETURN_IF_ERROR(same_dtype(ctx, op));
+  const Shape* fixed = attr<Shape>(ctx, Filter ? "filter_shape" : "input_shape");
+  const auto* s = attr<std::vector<int64_t>>(ctx, "stride");
+  const auto* p = attr<std::vector<int64_t>>(ctx, "padding");
+  const auto* grp = attr<int64_t>(ctx, "groups");
+  if (!fixed || !s || !p || !grp || s->size() != 2 || p->size() != 2) return invalid(op, "missing or malformed attributes");
+  const Shape& x = Filter ? ctx.inputs[0].shape() : *fixed;
+  const Shape& w = Filter ? *fixed : ctx.inputs[1].shape();
+  if (x.rank() != 4 || w.rank() != 4) return invalid(op, "expects rank-4 x and w");
+  if (ctx.outputs[0].shape() != *fixed) return invalid(op, "output shape does not match its shape attribute");
+  const int64_t geom[12] = {x.dim(0), x.dim(1), x.dim(2), x.dim(3), w.dim(0), w.dim(2), w.dim(3), (*s)[0], (*s)[1], (*p)[0], (*p)[1], *grp};
+  if (*grp <= 0 || (*s)[0] <= 0 || (*s)[1] <= 0) return invalid(op, "invalid stride or groups");
+  const int64_t oh = (geom[2] + 2 * geom[9] - geom[5]) / geom[7] + 1, ow = (geom[3] + 2 * geom[10] - geom[6]) / geom[8] + 1;
+  const Tensor& dy = ctx.inputs[Filter ? 1 : 0];
+  if (dy.shape() != Shape({geom[0], geom[4], oh, ow}) || w.dim(1) * *grp != x.dim(1))
+    return invalid(op, "dy / w shapes do not match the geometry");
+  Result<int32_t> dt = float_code(op, ctx.outputs[0].dtype());
+  if (!dt.is_ok()) return dt.status();
+  if (Filter)
+    FRAME_HIP_RETURN_IF_ERROR(fh_conv2d_grad_filter(dt.value(), ctx.inputs[0].raw_data(), dy.raw_data(), ctx.outputs[0].raw_data(),
+                                                    geom, stream_handle(ctx)),
+                              "op '" + op + "' (hip)");
+  else
+    FRAME_HIP_RETURN_IF_ERROR(fh_conv2d_grad_input(dt.value(), dy.raw_data(), ctx.inputs[1].raw_data(), ctx.outputs[0].raw_data(),
+                                                   geom, stream_handle(ctx)),
+                              "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
+// sum (x; axes[, keepdims]) and sum_grad_internal (gy; input_shape, axes): both index x's dims with a reduced mask.
+template <int Grad>
+Status sum_kernel(KernelContext& ctx) {
+  const std::string op = Grad ? "sum_grad_internal" : "sum";
+  FRAME_RETURN_IF_ERROR(arity(ctx, op, 1, 1));
+  FRAME_RETURN_IF_ERROR(same_dtype(ctx, op));
+  const auto* axes = attr<std::vector<int64_t>>(ctx, "axes");
+  const Shape* xs_attr = Grad ? attr<Shape>(ctx, "input_shape") : nullptr;
+  if (axes == nullptr || (Grad && xs_attr == nullptr)) return invalid(op, "missing attributes");
+  const Shape& xs = Grad ? *xs_attr : ctx.inputs[0].shape();
+  if (xs.rank() > 8) return Status::make(ErrorCode::kUnimplemented, "op '" + op + "' (hip): rank above 8");
+  std::vector<uint8_t> red(static_cast<size_t>(xs.rank()), axes->empty() ? 1 : 0);
+  for (int64_t a : *axes) {
+    if (a < 0 || a >= xs.rank()) return invalid(op, "axis out of range");
+    red[static_cast<size_t>(a)] = 1;
+  }
+  int64_t nout = 1;
+  for (int64_t d = 0; d < xs.rank(); ++d)
+    if (!red[static_cast<size_t>(d)]) nout *= xs.dim(d);
+  if (Grad ? (ctx.outputs[0].shape() != xs || ctx.inputs[0].numel() != nout) : ctx.outputs[0].numel() != nout)
+    return invalid(op, "input / output shapes do not match the axes");
+  Result<int32_t> dt = float_code(op, ctx.outputs[0].dtype());
+  if (!dt.is_ok()) return dt.status();
+  if (Grad)
+    FRAME_HIP_RETURN_IF_ERROR(fh_sum_grad(dt.value(), ctx.inputs[0].raw_data(), ctx.outputs[0].raw_data(),
+                                          static_cast<int32_t>(xs.rank()), xs.dims().data(), red.data(), stream_handle(ctx)),
+                              "op '" + op + "' (hip)");
+  else
+    FRAME_HIP_RETURN_IF_ERROR(fh_sum(dt.value(), ctx.inputs[0].raw_data(), ctx.outputs[0].raw_data(),
+                                     static_cast<int32_t>(xs.rank()), xs.dims().data(), red.data(), stream_handle(ctx)),
+                              "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
+template <int Grad>
+Status mse_kernel(KernelContext& ctx) {
+  const std::string op = Grad ? "mse_loss_grad_internal" : "mse_loss";
+  FRAME_RETURN_IF_ERROR(arity(ctx, op, Grad ? 3 : 2, 1));
+  FRAME_RETURN_IF_ERROR(same_dtype(ctx, op));
+  const Tensor& p = ctx.inputs[0];
+  if (ctx.inputs[1].shape() != p.shape()) return invalid(op, "pred and target shapes differ");
+  if (Grad ? (ctx.outputs[0].shape() != p.shape() || ctx.inputs[2].numel() != 1) : ctx.outputs[0].numel() != 1)
+    return invalid(op, "output / gy shapes do not match");
+  Result<int32_t> dt = float_code(op, p.dtype());
+  if (!dt.is_ok()) return dt.status();
+  if (Grad)
+    FRAME_HIP_RETURN_IF_ERROR(fh_mse_loss_grad(dt.value(), p.raw_data(), ctx.inputs[1].raw_data(), ctx.inputs[2].raw_data(),
+                                               ctx.outputs[0].raw_data(), p.numel(), stream_handle(ctx)),
+                              "op '" + op + "' (hip)");
+  else
+    FRAME_HIP_RETURN_IF_ERROR(fh_mse_loss(dt.value(), p.raw_data(), ctx.inputs[1].raw_data(), ctx.outputs[0].raw_data(),
+                                          p.numel(), stream_handle(ctx)),
+                              "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
 // Channels-last pooling on [N,H,W,C] activations (internal ops of the channels-last lowering), same attributes.
 template <int Mode>
 Status pool_nhwc_kernel(KernelContext& ctx) {
@@ -564,5 +710,16 @@ FRAME_REGISTER_KERNEL("transpose", kHipBackendName, &transpose_kernel);
 FRAME_REGISTER_KERNEL("slice", kHipBackendName, &slice_kernel);
 FRAME_REGISTER_KERNEL("concat", kHipBackendName, &concat_kernel);
 FRAME_REGISTER_KERNEL(ops::kConstantOpName, kHipBackendName, &constant_kernel);
+FRAME_REGISTER_KERNEL("relu_grad_internal", kHipBackendName, (&ew_kernel<FH_EW_RELU_GRAD, 2>));
+FRAME_REGISTER_KERNEL("matmul_grad_lhs_internal", kHipBackendName, &matmul_grad_kernel<0>);
+FRAME_REGISTER_KERNEL("matmul_grad_rhs_internal", kHipBackendName, &matmul_grad_kernel<1>);
+FRAME_REGISTER_KERNEL("max_pool2d_grad_internal", kHipBackendName, &pool_grad_kernel<0>);
+FRAME_REGISTER_KERNEL("avg_pool2d_grad_internal", kHipBackendName, &pool_grad_kernel<1>);
+FRAME_REGISTER_KERNEL("conv2d_grad_input_internal", kHipBackendName, &conv_grad_kernel<0>);
+FRAME_REGISTER_KERNEL("conv2d_grad_filter_internal", kHipBackendName, &conv_grad_kernel<1>);
+FRAME_REGISTER_KERNEL("sum", kHipBackendName, &sum_kernel<0>);
+FRAME_REGISTER_KERNEL("sum_grad_internal", kHipBackendName, &sum_kernel<1>);
+FRAME_REGISTER_KERNEL("mse_loss", kHipBackendName, &mse_kernel<0>);
+FRAME_REGISTER_KERNEL("mse_loss_grad_internal", kHipBackendName, &mse_kernel<1>);
 
 }  // namespace frame::backends::hip

@@ -9,6 +9,7 @@
 #include <string>
 #include <vector>
 
+#include <frame/compiler/autograd.h>
 #include <frame/compiler/pipeline.h>
 #include <frame/core/tensor.h>
 #include <frame/hal/allocator.h>
@@ -239,6 +240,33 @@ int frame_hip_lowered_text(const char* ir_text, int32_t opt_level, char* out, in
   auto lowered = frame::backends::hip::lower_for_hip(g.value(), opt_level);
   if (!lowered.is_ok()) return fail(lowered.status());
   return text_out(frame::ir::dump_text(lowered.value()), out, cap, needed);
+}
+
+int frame_backward_text(const char* ir_text, int32_t loss_output_index, const int32_t* wrt, int32_t n_wrt, char* out,
+                        int64_t cap, int64_t* needed) {
+  auto g = frame::ir::parse_text(ir_text);
+  if (!g.is_ok()) return fail(g.status());
+  std::span<const int32_t> idx(wrt, static_cast<size_t>(n_wrt < 0 ? 0 : n_wrt));
+  auto t = frame::compiler::build_backward_graph(g.value(), loss_output_index, idx);
+  if (!t.is_ok()) return fail(t.status());
+  return text_out(frame::ir::dump_text(t.value()), out, cap, needed);
+}
+
+int frame_sgd_update_text(const char* ir_text, const int32_t* param_inputs, int32_t n_params, double learning_rate,
+                          char* out, int64_t cap, int64_t* needed) {
+  auto g = frame::ir::parse_text(ir_text);
+  if (!g.is_ok()) return fail(g.status());
+  std::vector<frame::ir::TensorType> types;
+  for (int32_t i = 0; i < n_params; ++i) {
+    const int32_t k = param_inputs[i];
+    if (k < 0 || static_cast<size_t>(k) >= g.value().inputs().size())
+      return fail(frame::Status::make(frame::ErrorCode::kInvalidArgument,
+                                      "frame_sgd_update_text: param input index " + std::to_string(k) + " is out of range"));
+    types.push_back(g.value().inputs()[static_cast<size_t>(k)]->type());
+  }
+  auto u = frame::compiler::build_sgd_update_graph(types, learning_rate);
+  if (!u.is_ok()) return fail(u.status());
+  return text_out(frame::ir::dump_text(u.value()), out, cap, needed);
 }
 
 int frame_roundtrip_text(const char* ir_text, char* out, int64_t cap, int64_t* needed) {

@@ -20,6 +20,8 @@
 #include <frame/ops/fused_elementwise_utils.h>
 #include <frame/ops/op_registry.h>
 
+#include "gradients.h"
+
 namespace {
 
 using frame::DType;
@@ -285,7 +287,8 @@ FRAME_REGISTER_OP("add")
     .trait(OpTrait::kElementwise)
     .trait(OpTrait::kFusable)
     .trait(OpTrait::kCommutative)
-    .shape_infer(&binary_same);
+    .shape_infer(&binary_same)
+    .gradient(&frame::ops::schemas::add_gradient);
 
 FRAME_REGISTER_OP("mul")
     .input("lhs", "left operand")
@@ -294,21 +297,24 @@ FRAME_REGISTER_OP("mul")
     .trait(OpTrait::kElementwise)
     .trait(OpTrait::kFusable)
     .trait(OpTrait::kCommutative)
-    .shape_infer(&binary_same);
+    .shape_infer(&binary_same)
+    .gradient(&frame::ops::schemas::mul_gradient);
 
 FRAME_REGISTER_OP("relu")
     .input("x", "input")
     .output("out", "max(x, 0), NaN kept")
     .trait(OpTrait::kElementwise)
     .trait(OpTrait::kFusable)
-    .shape_infer(&unary_same);
+    .shape_infer(&unary_same)
+    .gradient(&frame::ops::schemas::relu_gradient);
 
 FRAME_REGISTER_OP("square")
     .input("x", "input")
     .output("out", "x * x")
     .trait(OpTrait::kElementwise)
     .trait(OpTrait::kFusable)
-    .shape_infer(&unary_same);
+    .shape_infer(&unary_same)
+    .gradient(&frame::ops::schemas::square_gradient);
 
 FRAME_REGISTER_OP("gelu")
     .input("x", "input")
@@ -325,7 +331,8 @@ FRAME_REGISTER_OP("matmul")
     .input("lhs", "rank-2 [m, k]")
     .input("rhs", "rank-2 [k, n]")
     .output("out", "rank-2 [m, n]")
-    .shape_infer(&infer_matmul);
+    .shape_infer(&infer_matmul)
+    .gradient(&frame::ops::schemas::matmul_gradient);
 
 FRAME_REGISTER_OP("conv2d")
     .input("x", "rank-4 [N, Cin, H, W]")
@@ -335,7 +342,8 @@ FRAME_REGISTER_OP("conv2d")
     .attr("padding", AttrType::kInt64Array, true)
     .attr("groups", AttrType::kInt64, true)
     .output("out", "rank-4 [N, Cout, out_h, out_w]")
-    .shape_infer(&infer_conv2d);
+    .shape_infer(&infer_conv2d)
+    .gradient(&frame::ops::schemas::conv2d_gradient);
 
 FRAME_REGISTER_OP("softmax").input("x", "rank-2 [N, D]").output("out", "softmax along the last axis").shape_infer(&infer_softmax);
 
@@ -353,7 +361,8 @@ FRAME_REGISTER_OP("max_pool2d")
     .attr("stride", AttrType::kInt64Array, true)
     .attr("padding", AttrType::kInt64Array, true)
     .output("out", "max pooling; padding is -inf")
-    .shape_infer(&infer_pool);
+    .shape_infer(&infer_pool)
+    .gradient(&frame::ops::schemas::max_pool2d_gradient);
 
 FRAME_REGISTER_OP("avg_pool2d")
     .input("x", "rank-4 [N, C, H, W]")
@@ -361,9 +370,11 @@ FRAME_REGISTER_OP("avg_pool2d")
     .attr("stride", AttrType::kInt64Array, true)
     .attr("padding", AttrType::kInt64Array, true)
     .output("out", "average pooling; denominator KH*KW")
-    .shape_infer(&infer_pool);
+    .shape_infer(&infer_pool)
+    .gradient(&frame::ops::schemas::avg_pool2d_gradient);
 
-FRAME_REGISTER_OP("reshape").input("x", "input").attr("target_shape", AttrType::kShape, true).output("out", "reshaped x").shape_infer(&infer_reshape);
+FRAME_REGISTER_OP("reshape").input("x", "input").attr("target_shape", AttrType::kShape, true).output("out", "reshaped x").shape_infer(&infer_reshape)
+    .gradient(&frame::ops::schemas::reshape_gradient);
 FRAME_REGISTER_OP("transpose").input("x", "input").attr("perm", AttrType::kInt64Array, true).output("out", "out.dims[i] = x.dims[perm[i]]").shape_infer(&infer_transpose);
 FRAME_REGISTER_OP("concat").variadic_input("xs", "tensors to concatenate", 1).attr("axis", AttrType::kInt64, true).output("out", "concatenation").shape_infer(&infer_concat);
 FRAME_REGISTER_OP("slice")

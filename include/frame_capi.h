@@ -74,6 +74,15 @@ int frame_transform_text(const char* ir_text, const char* pass_name, char* out, 
 int frame_roundtrip_text(const char* ir_text, char* out, int64_t cap, int64_t* needed);
 int frame_memory_plan_text(const char* ir_text, char* out, int64_t cap, int64_t* needed);
 
+/* Training-graph construction (compiler::build_backward_graph / build_sgd_update_graph, reference
+ * include/frame/compiler/autograd.h:45-67) on IR text. frame_backward_text: the forward graph's outputs, then the
+ * gradients of output `loss_output_index` w.r.t. graph inputs wrt[0..n_wrt). frame_sgd_update_text: the update graph
+ * for the types of graph inputs param_inputs[0..n_params) of `ir_text`. */
+int frame_backward_text(const char* ir_text, int32_t loss_output_index, const int32_t* wrt, int32_t n_wrt, char* out,
+                        int64_t cap, int64_t* needed);
+int frame_sgd_update_text(const char* ir_text, const int32_t* param_inputs, int32_t n_params, double learning_rate,
+                          char* out, int64_t cap, int64_t* needed);
+
 /* The graph the hip backend plans for `ir_text`: the standard pipeline for "hip", then HipBackend::compile's
  * lowering (fused attention, matmul/conv epilogues at opt_level >= 1, channels-last conv), as IR text.
  * Host-only (no device needed); no counterpart in the reference, which has no backend lowering to inspect. */

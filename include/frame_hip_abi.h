@@ -49,7 +49,10 @@ typedef enum fh_ew_op {
   FH_EW_MUL = 2,
   FH_EW_RELU = 3,
   FH_EW_SQUARE = 4,
-  FH_EW_GELU = 5
+  FH_EW_GELU = 5,
+  /* relu_grad_internal(x, gy): gy where x > 0, else 0 (reference: src/backends/cpu/kernels/elementwise.cpp:407-414);
+   * binary, the running value is x and the next input gy */
+  FH_EW_RELU_GRAD = 6
 } fh_ew_op;
 
 #define FH_MAX_SEGMENTS 8
@@ -231,6 +234,54 @@ fh_status fh_copy2d(void* dst, int64_t dst_pitch, const void* src, int64_t src_p
  * Used for constant materialisation (reference: src/backends/cuda/kernels/constant.cpp:23-73) and to clear
  * memory without hipMemsetAsync. */
 fh_status fh_fill(void* dst, int32_t itemsize, uint64_t pattern, int64_t count, void* stream);
+
+/* ---- training path (the gradient-only ops of compiler::build_backward_graph) ---- */
+
+/* matmul_grad_lhs_internal (rhs = 0): out [m,k] = p [m,n] * q[k,n]^T (p = gy, q = b); matmul_grad_rhs_internal
+ * (rhs = 1): out [k,n] = p[m,k]^T * q [m,n] (p = a, q = gy). Transposed operands are read in place; every output
+ * is one fp32 sum in the reference's order (src/backends/cpu/kernels/matmul.cpp:187-327), so results are
+ * bit-identical. HipBackend::compile lowers both ops to a transpose plus the GEMM kernels where those are faster;
+ * this entry serves eager launches. The CUDA backend has no kernel for either op (CPU fallback). */
+fh_status fh_matmul_grad(int32_t dtype, int32_t rhs, const void* p, const void* q, void* out, int64_t m, int64_t n,
+                         int64_t k, void* stream);
+
+/* max_pool2d_grad_internal (mode 0; x = the forward input) / avg_pool2d_grad_internal (mode 1; x unused), NCHW.
+ * geom as fh_pool2d (the forward input's dims). One thread per input element gathers its covering windows in the
+ * reference's order, so results are bit-identical to the CPU reference (src/backends/cpu/kernels/pool.cpp:186-206,
+ * 358-388, 543-566). Replaces the recompute-y + cudnnPoolingBackward of max_pool2d_grad_internal
+ * (reference: src/backends/cuda/kernels/pool.cpp:245-363) and avg_pool2d_grad_internal's kernel
+ * (reference: src/backends/cuda/kernels/pool.cu:250-320). */
+fh_status fh_pool2d_grad(int32_t dtype, int32_t mode, const void* dy, const void* x, void* dx, const int64_t geom[10],
+                         void* stream);
+
+/* conv2d_grad_input_internal: dx [N,Cin,H,W] from dy [N,Cout,Ho,Wo] and w [Cout,Cin/g,KH,KW];
+ * conv2d_grad_filter_internal: dw [Cout,Cin/g,KH,KW] from x and dy. geom as fh_conv2d_fwd (x's dims).
+ * Each output is one fp32 sum in the reference's order (src/backends/cpu/kernels/conv.cpp:320-452).
+ * Replace cudnnConvolutionBackwardData / cudnnConvolutionBackwardFilter
+ * (reference: src/backends/cuda/kernels/conv.cpp:560-789). */
+fh_status fh_conv2d_grad_input(int32_t dtype, const void* dy, const void* w, void* dx, const int64_t geom[12],
+                               void* stream);
+fh_status fh_conv2d_grad_filter(int32_t dtype, const void* x, const void* dy, void* dw, const int64_t geom[12],
+                                void* stream);
+
+/* sum over the axes flagged in reduced[0..rank) (rank <= 8; every axis for the reference's axes = []), output dense
+ * with the reduced axes dropped (keepdims only adds size-1 dims, same layout). fp32 tree per output.
+ * Replaces sum_cuda_kernel (reference: src/backends/cuda/kernels/reduction.cu:322-460). */
+fh_status fh_sum(int32_t dtype, const void* x, void* out, int32_t rank, const int64_t* dims, const uint8_t* reduced,
+                 void* stream);
+
+/* sum_grad_internal: gx (dims) = gy broadcast along the reduced axes, a copy of the stored bits
+ * (reference: src/backends/cpu/kernels/reduction.cpp:378-388; the CUDA backend has no kernel for it and falls
+ * back to the CPU). */
+fh_status fh_sum_grad(int32_t dtype, const void* gy, void* gx, int32_t rank, const int64_t* dims,
+                      const uint8_t* reduced, void* stream);
+
+/* mse_loss: out (one element) = mean((pred - target)^2), fp32 tree; mse_loss_grad_internal: out = 2 * gy / numel *
+ * (pred - target), bit-identical to the CPU reference (src/backends/cpu/kernels/loss.cpp:110-262; the CUDA backend
+ * has no kernel for either and falls back to the CPU). */
+fh_status fh_mse_loss(int32_t dtype, const void* pred, const void* target, void* out, int64_t numel, void* stream);
+fh_status fh_mse_loss_grad(int32_t dtype, const void* pred, const void* target, const void* gy, void* out,
+                           int64_t numel, void* stream);
 
 #ifdef __cplusplus
 }

@@ -242,6 +242,72 @@ Status concat_kernel(ops::KernelContext& c) {
 }
 Status constant_kernel(ops::KernelContext& c) { return ops::fill_tensor_from_constant_attrs(*c.attrs, c.outputs[0]); }
 
+// ---- training path ----
+template <int Rhs>
+Status matmul_grad_kernel(ops::KernelContext& c) {
+  const auto& p = c.inputs[0].shape();
+  const auto& q = c.inputs[1].shape();
+  // lhs: gy [m,n], b [k,n]; rhs: a [m,k], gy [m,n]
+  const int64_t m = p.dim(0), n = Rhs ? q.dim(1) : p.dim(1), k = Rhs ? p.dim(1) : q.dim(0);
+  return rc(oracle_matmul_grad(dcode(c.outputs[0].dtype()), Rhs, c.inputs[0].raw_data(), c.inputs[1].raw_data(),
+                               c.outputs[0].raw_data(), m, n, k),
+            "matmul_grad");
+}
+template <int Filter>
+Status conv_grad_kernel(ops::KernelContext& c) {
+  // input grad: (dy, w) -> dx of input_shape; filter grad: (x, dy) -> dw of filter_shape
+  const Shape x = Filter ? c.inputs[0].shape() : *attr<Shape>(c, "input_shape");
+  const Shape w = Filter ? *attr<Shape>(c, "filter_shape") : c.inputs[1].shape();
+  const auto* s = attr<std::vector<int64_t>>(c, "stride");
+  const auto* p = attr<std::vector<int64_t>>(c, "padding");
+  const auto* g = attr<int64_t>(c, "groups");
+  const int64_t geom[12] = {x.dim(0), x.dim(1), x.dim(2), x.dim(3), w.dim(0), w.dim(2), w.dim(3), (*s)[0], (*s)[1], (*p)[0], (*p)[1], *g};
+  const int dt = dcode(c.outputs[0].dtype());
+  if (Filter)
+    return rc(oracle_conv2d_grad_filter(dt, c.inputs[0].raw_data(), c.inputs[1].raw_data(), c.outputs[0].raw_data(), geom), "conv2d_grad_filter");
+  return rc(oracle_conv2d_grad_input(dt, c.inputs[0].raw_data(), c.inputs[1].raw_data(), c.outputs[0].raw_data(), geom), "conv2d_grad_input");
+}
+template <int Mode>
+Status pool_grad_kernel(ops::KernelContext& c) {
+  const Shape x = *attr<Shape>(c, "input_shape");
+  const auto* k = attr<std::vector<int64_t>>(c, "kernel");
+  const auto* s = attr<std::vector<int64_t>>(c, "stride");
+  const auto* p = attr<std::vector<int64_t>>(c, "padding");
+  const int64_t geom[10] = {x.dim(0), x.dim(1), x.dim(2), x.dim(3), (*k)[0], (*k)[1], (*s)[0], (*s)[1], (*p)[0], (*p)[1]};
+  return rc(oracle_pool2d_grad(dcode(c.outputs[0].dtype()), Mode, c.inputs[0].raw_data(),
+                               Mode == 0 ? c.inputs[1].raw_data() : nullptr, c.outputs[0].raw_data(), geom),
+            "pool2d_grad");
+}
+std::vector<uint8_t> reduced_mask(const Shape& x, const std::vector<int64_t>& axes) {
+  std::vector<uint8_t> r(static_cast<size_t>(x.rank()), axes.empty() ? 1 : 0);
+  for (int64_t a : axes) r[static_cast<size_t>(a)] = 1;
+  return r;
+}
+Status sum_kernel(ops::KernelContext& c) {
+  const Shape& x = c.inputs[0].shape();
+  const auto mask = reduced_mask(x, *attr<std::vector<int64_t>>(c, "axes"));
+  return rc(oracle_sum(dcode(c.outputs[0].dtype()), c.inputs[0].raw_data(), c.outputs[0].raw_data(), static_cast<int>(x.rank()),
+                       x.dims().data(), mask.data()),
+            "sum");
+}
+Status sum_grad_kernel(ops::KernelContext& c) {
+  const Shape x = *attr<Shape>(c, "input_shape");
+  const auto mask = reduced_mask(x, *attr<std::vector<int64_t>>(c, "axes"));
+  return rc(oracle_sum_grad(static_cast<int>(c.outputs[0].dtype().itemsize()), c.inputs[0].raw_data(), c.outputs[0].raw_data(),
+                            static_cast<int>(x.rank()), x.dims().data(), mask.data()),
+            "sum_grad");
+}
+Status mse_loss_kernel(ops::KernelContext& c) {
+  return rc(oracle_mse_loss(dcode(c.outputs[0].dtype()), c.inputs[0].raw_data(), c.inputs[1].raw_data(), c.outputs[0].raw_data(),
+                            c.inputs[0].numel()),
+            "mse_loss");
+}
+Status mse_loss_grad_kernel(ops::KernelContext& c) {
+  return rc(oracle_mse_loss_grad(dcode(c.outputs[0].dtype()), c.inputs[0].raw_data(), c.inputs[1].raw_data(), c.inputs[2].raw_data(),
+                                 c.outputs[0].raw_data(), c.inputs[0].numel()),
+            "mse_loss_grad");
+}
+
 }  // namespace oracle_cpu
 
 FRAME_REGISTER_BACKEND(frame::kCpuBackendName, oracle_cpu::CpuBackend);
@@ -262,3 +328,14 @@ FRAME_REGISTER_KERNEL("transpose", frame::kCpuBackendName, &oracle_cpu::transpos
 FRAME_REGISTER_KERNEL("slice", frame::kCpuBackendName, &oracle_cpu::slice_kernel);
 FRAME_REGISTER_KERNEL("concat", frame::kCpuBackendName, &oracle_cpu::concat_kernel);
 FRAME_REGISTER_KERNEL(frame::ops::kConstantOpName, frame::kCpuBackendName, &oracle_cpu::constant_kernel);
+FRAME_REGISTER_KERNEL("relu_grad_internal", frame::kCpuBackendName, (&oracle_cpu::ew_kernel<6, 2>));
+FRAME_REGISTER_KERNEL("matmul_grad_lhs_internal", frame::kCpuBackendName, &oracle_cpu::matmul_grad_kernel<0>);
+FRAME_REGISTER_KERNEL("matmul_grad_rhs_internal", frame::kCpuBackendName, &oracle_cpu::matmul_grad_kernel<1>);
+FRAME_REGISTER_KERNEL("conv2d_grad_input_internal", frame::kCpuBackendName, &oracle_cpu::conv_grad_kernel<0>);
+FRAME_REGISTER_KERNEL("conv2d_grad_filter_internal", frame::kCpuBackendName, &oracle_cpu::conv_grad_kernel<1>);
+FRAME_REGISTER_KERNEL("max_pool2d_grad_internal", frame::kCpuBackendName, &oracle_cpu::pool_grad_kernel<0>);
+FRAME_REGISTER_KERNEL("avg_pool2d_grad_internal", frame::kCpuBackendName, &oracle_cpu::pool_grad_kernel<1>);
+FRAME_REGISTER_KERNEL("sum", frame::kCpuBackendName, &oracle_cpu::sum_kernel);
+FRAME_REGISTER_KERNEL("sum_grad_internal", frame::kCpuBackendName, &oracle_cpu::sum_grad_kernel);
+FRAME_REGISTER_KERNEL("mse_loss", frame::kCpuBackendName, &oracle_cpu::mse_loss_kernel);
+FRAME_REGISTER_KERNEL("mse_loss_grad_internal", frame::kCpuBackendName, &oracle_cpu::mse_loss_grad_kernel);

@@ -117,8 +117,12 @@ float unary(uint8_t op, float x) {
       return x;
   }
 }
-float binary(uint8_t op, float a, float b) { return op == 2 ? a * b : a + b; }
-bool is_binary(uint8_t op) { return op == 1 || op == 2; }
+// op 6 is relu_grad_internal(x, gy): gy where x > 0, else 0 (reference: src/backends/cpu/kernels/elementwise.cpp:407-414).
+float binary(uint8_t op, float a, float b) {
+  if (op == 6) return a > 0.0f ? b : 0.0f;
+  return op == 2 ? a * b : a + b;
+}
+bool is_binary(uint8_t op) { return op == 1 || op == 2 || op == 6; }
 
 template <typename D>
 float matmul_element(const typename D::S* a, const typename D::S* b, int64_t n, int64_t k, int64_t i, int64_t j) {
@@ -439,6 +443,264 @@ int oracle_constant(int dtype, const double* values, int64_t nvalues, void* out,
   return with_dtype(dtype, [&](auto d) {
     using D = decltype(d);
     for (int64_t i = 0; i < numel; ++i) static_cast<typename D::S*>(out)[i] = D::st(static_cast<float>(values[i]));
+    return 0;
+  });
+}
+
+}  // extern "C"
+
+// ---- training path ----------------------------------------------------------------------------------------
+extern "C" {
+
+// reference: src/backends/cpu/kernels/matmul.cpp:187-231 (lhs: ga[i,p] = sum_j gy[i,j]*b[p,j]) and :285-327
+// (rhs: gb[p,j] = sum_i a[i,p]*gy[i,j]); float accumulator, contraction index ascending, one rounding at the store.
+int oracle_matmul_grad(int dtype, int rhs, const void* p, const void* q, void* out, int64_t m, int64_t n, int64_t k) {
+  return with_dtype(dtype, [&](auto d) {
+    using D = decltype(d);
+    using S = typename D::S;
+    const S* P = static_cast<const S*>(p);
+    const S* Q = static_cast<const S*>(q);
+    S* O = static_cast<S*>(out);
+    if (!rhs) {  // P = gy [m,n], Q = b [k,n] -> [m,k]
+      for (int64_t i = 0; i < m; ++i)
+        for (int64_t c = 0; c < k; ++c) {
+          float acc = 0.0f;
+          for (int64_t j = 0; j < n; ++j) acc += D::ld(P[i * n + j]) * D::ld(Q[c * n + j]);
+          O[i * k + c] = D::st(acc);
+        }
+    } else {  // P = a [m,k], Q = gy [m,n] -> [k,n]
+      for (int64_t c = 0; c < k; ++c)
+        for (int64_t j = 0; j < n; ++j) {
+          float acc = 0.0f;
+          for (int64_t i = 0; i < m; ++i) acc += D::ld(P[i * k + c]) * D::ld(Q[i * n + j]);
+          O[c * n + j] = D::st(acc);
+        }
+    }
+    return 0;
+  });
+}
+
+// reference: src/backends/cpu/kernels/conv.cpp:320-352. Per input element, products over co (of its group), kh,
+// kw ascending, taking only taps where (ih + pad - kh) is a multiple of the stride and lands inside dy.
+int oracle_conv2d_grad_input(int dtype, const void* dy, const void* w, void* dx, const int64_t* geom) {
+  ConvG p;
+  if (!read_conv(geom, p)) return 1;
+  return with_dtype(dtype, [&](auto d) {
+    using D = decltype(d);
+    using S = typename D::S;
+    const S* DY = static_cast<const S*>(dy);
+    const S* Wt = static_cast<const S*>(w);
+    S* DX = static_cast<S*>(dx);
+    const int64_t cin_g = p.cin / p.groups, cout_g = p.cout / p.groups;
+    for (int64_t n = 0; n < p.n; ++n)
+      for (int64_t cf = 0; cf < p.cin; ++cf) {
+        const int64_t g = cf / cin_g, ci = cf - g * cin_g;
+        for (int64_t ih = 0; ih < p.h; ++ih)
+          for (int64_t iw = 0; iw < p.w; ++iw) {
+            float acc = 0.0f;
+            for (int64_t co = g * cout_g; co < (g + 1) * cout_g; ++co)
+              for (int64_t a = 0; a < p.kh; ++a) {
+                const int64_t nh = ih + p.ph - a;
+                if (nh % p.sh != 0) continue;
+                const int64_t oh = nh / p.sh;
+                if (oh < 0 || oh >= p.oh) continue;
+                for (int64_t b = 0; b < p.kw; ++b) {
+                  const int64_t nw = iw + p.pw - b;
+                  if (nw % p.sw != 0) continue;
+                  const int64_t ow = nw / p.sw;
+                  if (ow < 0 || ow >= p.ow) continue;
+                  acc += D::ld(DY[((n * p.cout + co) * p.oh + oh) * p.ow + ow]) *
+                         D::ld(Wt[((co * cin_g + ci) * p.kh + a) * p.kw + b]);
+                }
+              }
+            DX[((n * p.cin + cf) * p.h + ih) * p.w + iw] = D::st(acc);
+          }
+      }
+    return 0;
+  });
+}
+
+// reference: src/backends/cpu/kernels/conv.cpp:423-451. Per filter element, products over n, oh, ow ascending,
+// skipping taps in the padding.
+int oracle_conv2d_grad_filter(int dtype, const void* x, const void* dy, void* dw, const int64_t* geom) {
+  ConvG p;
+  if (!read_conv(geom, p)) return 1;
+  return with_dtype(dtype, [&](auto d) {
+    using D = decltype(d);
+    using S = typename D::S;
+    const S* X = static_cast<const S*>(x);
+    const S* DY = static_cast<const S*>(dy);
+    S* DW = static_cast<S*>(dw);
+    const int64_t cin_g = p.cin / p.groups, cout_g = p.cout / p.groups;
+    for (int64_t co = 0; co < p.cout; ++co) {
+      const int64_t g = co / cout_g;
+      for (int64_t ci = 0; ci < cin_g; ++ci)
+        for (int64_t a = 0; a < p.kh; ++a)
+          for (int64_t b = 0; b < p.kw; ++b) {
+            float acc = 0.0f;
+            for (int64_t n = 0; n < p.n; ++n)
+              for (int64_t oh = 0; oh < p.oh; ++oh) {
+                const int64_t ih = oh * p.sh - p.ph + a;
+                if (ih < 0 || ih >= p.h) continue;
+                for (int64_t ow = 0; ow < p.ow; ++ow) {
+                  const int64_t iw = ow * p.sw - p.pw + b;
+                  if (iw < 0 || iw >= p.w) continue;
+                  acc += D::ld(X[((n * p.cin + g * cin_g + ci) * p.h + ih) * p.w + iw]) *
+                         D::ld(DY[((n * p.cout + co) * p.oh + oh) * p.ow + ow]);
+                }
+              }
+            DW[((co * cin_g + ci) * p.kh + a) * p.kw + b] = D::st(acc);
+          }
+    }
+    return 0;
+  });
+}
+
+// mode 0 = max_pool2d_grad_internal (reference: src/backends/cpu/kernels/pool.cpp:186-206 window argmax, first
+// strict maximum in (kh, kw) order; :358-388 windows in (n, c, oh, ow) order add dy into a float buffer at the
+// argmax, one rounding at the end). mode 1 = avg_pool2d_grad_internal (:543-566: per input element, kh then kw
+// ascending over covering windows, sum of dy, then / (KH*KW)). geom as oracle_pool2d (input dims).
+int oracle_pool2d_grad(int dtype, int mode, const void* dy, const void* x, void* dx, const int64_t* g) {
+  const int64_t N = g[0], C = g[1], H = g[2], W = g[3], KH = g[4], KW = g[5], SH = g[6], SW = g[7], PH = g[8],
+                PW = g[9];
+  if (SH <= 0 || SW <= 0 || KH <= 0 || KW <= 0) return 1;
+  const int64_t OH = (H + 2 * PH - KH) / SH + 1, OW = (W + 2 * PW - KW) / SW + 1;
+  return with_dtype(dtype, [&](auto d) {
+    using D = decltype(d);
+    using S = typename D::S;
+    const S* DY = static_cast<const S*>(dy);
+    const S* X = static_cast<const S*>(x);
+    S* DX = static_cast<S*>(dx);
+    if (mode == 0) {
+      std::vector<float> acc(static_cast<size_t>(N * C * H * W), 0.0f);
+      for (int64_t nc = 0; nc < N * C; ++nc)
+        for (int64_t oh = 0; oh < OH; ++oh)
+          for (int64_t ow = 0; ow < OW; ++ow) {
+            bool found = false;
+            float best = 0.0f;
+            int64_t at = 0;
+            for (int64_t a = 0; a < KH; ++a) {
+              const int64_t ih = oh * SH - PH + a;
+              if (ih < 0 || ih >= H) continue;
+              for (int64_t b = 0; b < KW; ++b) {
+                const int64_t iw = ow * SW - PW + b;
+                if (iw < 0 || iw >= W) continue;
+                const float v = D::ld(X[(nc * H + ih) * W + iw]);
+                if (!found || v > best) {
+                  found = true;
+                  best = v;
+                  at = ih * W + iw;
+                }
+              }
+            }
+            if (!found) return 2;
+            acc[static_cast<size_t>(nc * H * W + at)] += D::ld(DY[(nc * OH + oh) * OW + ow]);
+          }
+      for (size_t i = 0; i < acc.size(); ++i) DX[i] = D::st(acc[i]);
+      return 0;
+    }
+    const float denom = static_cast<float>(KH * KW);
+    for (int64_t nc = 0; nc < N * C; ++nc)
+      for (int64_t ih = 0; ih < H; ++ih)
+        for (int64_t iw = 0; iw < W; ++iw) {
+          float acc = 0.0f;
+          for (int64_t a = 0; a < KH; ++a) {
+            const int64_t nh = ih + PH - a;
+            if (nh % SH != 0) continue;
+            const int64_t oh = nh / SH;
+            if (oh < 0 || oh >= OH) continue;
+            for (int64_t b = 0; b < KW; ++b) {
+              const int64_t nw = iw + PW - b;
+              if (nw % SW != 0) continue;
+              const int64_t ow = nw / SW;
+              if (ow < 0 || ow >= OW) continue;
+              acc += D::ld(DY[(nc * OH + oh) * OW + ow]);
+            }
+          }
+          DX[(nc * H + ih) * W + iw] = D::st(acc / denom);
+        }
+    return 0;
+  });
+}
+
+namespace {
+// Linear index of x's element `i` in the reduced tensor (reduced axes dropped; reference:
+// src/backends/cpu/kernels/reduction.cpp:87-116).
+int64_t project(int rank, const int64_t* dims, const uint8_t* reduced, int64_t i) {
+  int64_t out = 0, stride = 1;
+  for (int d = rank - 1; d >= 0; --d) {
+    const int64_t sz = dims[d] > 0 ? dims[d] : 1;
+    const int64_t c = i % sz;
+    i /= sz;
+    if (!reduced[d]) {
+      out += c * stride;
+      stride *= dims[d];
+    }
+  }
+  return out;
+}
+}  // namespace
+
+// reference: src/backends/cpu/kernels/reduction.cpp:215-241 — one float accumulator per output, x visited in
+// row-major order, one rounding per output. reduced[d] != 0 marks a reduced axis (every axis for axes = []).
+int oracle_sum(int dtype, const void* x, void* out, int rank, const int64_t* dims, const uint8_t* reduced) {
+  int64_t numel = 1, nout = 1;
+  for (int d = 0; d < rank; ++d) {
+    numel *= dims[d];
+    if (!reduced[d]) nout *= dims[d];
+  }
+  return with_dtype(dtype, [&](auto dd) {
+    using D = decltype(dd);
+    using S = typename D::S;
+    const S* X = static_cast<const S*>(x);
+    S* O = static_cast<S*>(out);
+    std::vector<float> acc(static_cast<size_t>(nout), 0.0f);
+    for (int64_t i = 0; i < numel; ++i) acc[static_cast<size_t>(project(rank, dims, reduced, i))] += D::ld(X[i]);
+    for (int64_t j = 0; j < nout; ++j) O[j] = D::st(acc[static_cast<size_t>(j)]);
+    return 0;
+  });
+}
+
+// reference: src/backends/cpu/kernels/reduction.cpp:378-388 — gx[i] = gy[project(i)], a bit copy.
+int oracle_sum_grad(int itemsize, const void* gy, void* gx, int rank, const int64_t* dims, const uint8_t* reduced) {
+  int64_t numel = 1;
+  for (int d = 0; d < rank; ++d) numel *= dims[d];
+  const auto* G = static_cast<const unsigned char*>(gy);
+  auto* O = static_cast<unsigned char*>(gx);
+  for (int64_t i = 0; i < numel; ++i)
+    std::memcpy(O + i * itemsize, G + project(rank, dims, reduced, i) * itemsize, static_cast<size_t>(itemsize));
+  return 0;
+}
+
+// reference: src/backends/cpu/kernels/loss.cpp:110-147 — sum of (p - t)^2 in index order, then / numel, one rounding.
+int oracle_mse_loss(int dtype, const void* pred, const void* target, void* out, int64_t numel) {
+  if (numel <= 0) return 1;
+  return with_dtype(dtype, [&](auto d) {
+    using D = decltype(d);
+    using S = typename D::S;
+    const S* P = static_cast<const S*>(pred);
+    const S* T = static_cast<const S*>(target);
+    float acc = 0.0f;
+    for (int64_t i = 0; i < numel; ++i) {
+      const float diff = D::ld(P[i]) - D::ld(T[i]);
+      acc += diff * diff;
+    }
+    static_cast<S*>(out)[0] = D::st(acc / static_cast<float>(numel));
+    return 0;
+  });
+}
+
+// reference: src/backends/cpu/kernels/loss.cpp:230-262 — c = 2 * gy / numel (in that order), out = c * (p - t).
+int oracle_mse_loss_grad(int dtype, const void* pred, const void* target, const void* gy, void* out, int64_t numel) {
+  if (numel <= 0) return 1;
+  return with_dtype(dtype, [&](auto d) {
+    using D = decltype(d);
+    using S = typename D::S;
+    const S* P = static_cast<const S*>(pred);
+    const S* T = static_cast<const S*>(target);
+    const float c = 2.0f * D::ld(static_cast<const S*>(gy)[0]) / static_cast<float>(numel);
+    S* O = static_cast<S*>(out);
+    for (int64_t i = 0; i < numel; ++i) O[i] = D::st(c * (D::ld(P[i]) - D::ld(T[i])));
     return 0;
   });
 }

@@ -45,7 +45,7 @@ int oracle_conv2d_sample(int dtype, const void* x, const void* w, const void* bi
 
 /* Fused elementwise chain (reference: src/ops/fused_elementwise_utils.cpp:122-206 for segment order and
  * per-segment rounding; sub-op arithmetic: src/backends/cpu/kernels/elementwise.cpp:146-331).
- * op codes: 1 add, 2 mul, 3 relu, 4 square, 5 gelu. */
+ * op codes: 1 add, 2 mul, 3 relu, 4 square, 5 gelu, 6 relu_grad (binary: x > 0 ? gy : 0). */
 int oracle_ew_program(int dtype, int nseg, const uint8_t* ops, const int8_t* arities, const void* const* ins,
                       int nin, void* out, int64_t numel);
 
@@ -72,6 +72,29 @@ int oracle_concat(int itemsize, const void* const* xs, int count, void* y, int r
 
 /* constant materialisation: value[i % nvalues] cast to dtype (reference: src/ops/constant_utils.cpp) */
 int oracle_constant(int dtype, const double* values, int64_t nvalues, void* out, int64_t numel);
+
+/* ---- training path ---- */
+/* matmul_grad_{lhs,rhs}_internal (reference: src/backends/cpu/kernels/matmul.cpp:187-327).
+ * rhs = 0: p = gy [m,n], q = b [k,n], out [m,k]; rhs = 1: p = a [m,k], q = gy [m,n], out [k,n]. */
+int oracle_matmul_grad(int dtype, int rhs, const void* p, const void* q, void* out, int64_t m, int64_t n, int64_t k);
+
+/* conv2d_grad_{input,filter}_internal (reference: src/backends/cpu/kernels/conv.cpp:320-452); geom as
+ * oracle_conv2d with x's dims. */
+int oracle_conv2d_grad_input(int dtype, const void* dy, const void* w, void* dx, const int64_t* geom);
+int oracle_conv2d_grad_filter(int dtype, const void* x, const void* dy, void* dw, const int64_t* geom);
+
+/* max (mode 0, x required) / avg (mode 1, x unused) pool gradients (reference: src/backends/cpu/kernels/pool.cpp:
+ * 186-206, 358-388, 543-566); geom as oracle_pool2d. Returns 2 when a max window is empty. */
+int oracle_pool2d_grad(int dtype, int mode, const void* dy, const void* x, void* dx, const int64_t* geom);
+
+/* sum over the axes flagged in reduced[] and its gradient (reference: src/backends/cpu/kernels/reduction.cpp:
+ * 87-116, 215-241, 378-388). */
+int oracle_sum(int dtype, const void* x, void* out, int rank, const int64_t* dims, const uint8_t* reduced);
+int oracle_sum_grad(int itemsize, const void* gy, void* gx, int rank, const int64_t* dims, const uint8_t* reduced);
+
+/* mse_loss and mse_loss_grad_internal (reference: src/backends/cpu/kernels/loss.cpp:110-147, 230-262). */
+int oracle_mse_loss(int dtype, const void* pred, const void* target, void* out, int64_t numel);
+int oracle_mse_loss_grad(int dtype, const void* pred, const void* target, const void* gy, void* out, int64_t numel);
 
 #ifdef __cplusplus
 }

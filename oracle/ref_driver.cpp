@@ -5,10 +5,12 @@
 #include <cstdint>
 #include <cstring>
 #include <memory>
+#include <span>
 #include <sstream>
 #include <string>
 #include <vector>
 
+#include <frame/compiler/autograd.h>
 #include <frame/compiler/pass.h>
 #include <frame/compiler/pipeline.h>
 #include <frame/core/dtype.h>
@@ -124,6 +126,28 @@ int ref_transform_text(const char* ir_text, const char* pass_name, char* out, in
 }
 
 // Round-trips the text through parse_text + dump_text.
+// The reference's compile-time autograd on IR text (compiler::build_backward_graph / build_sgd_update_graph).
+int ref_backward_text(const char* ir_text, int32_t loss_output_index, const int32_t* wrt, int32_t n_wrt, char* out,
+                      int64_t cap, int64_t* needed) {
+  frame::Result<frame::ir::Graph> parsed = frame::ir::parse_text(ir_text);
+  if (!parsed.is_ok()) return set_err(parsed.status());
+  auto t = frame::compiler::build_backward_graph(parsed.value(), loss_output_index,
+                                                 std::span<const int32_t>(wrt, static_cast<size_t>(n_wrt)));
+  if (!t.is_ok()) return set_err(t.status());
+  return copy_text(frame::ir::dump_text(t.value()), out, cap, needed);
+}
+
+int ref_sgd_update_text(const char* ir_text, const int32_t* param_inputs, int32_t n_params, double learning_rate,
+                        char* out, int64_t cap, int64_t* needed) {
+  frame::Result<frame::ir::Graph> parsed = frame::ir::parse_text(ir_text);
+  if (!parsed.is_ok()) return set_err(parsed.status());
+  std::vector<frame::ir::TensorType> types;
+  for (int32_t i = 0; i < n_params; ++i) types.push_back(parsed.value().inputs()[static_cast<size_t>(param_inputs[i])]->type());
+  auto u = frame::compiler::build_sgd_update_graph(types, learning_rate);
+  if (!u.is_ok()) return set_err(u.status());
+  return copy_text(frame::ir::dump_text(u.value()), out, cap, needed);
+}
+
 int ref_roundtrip_text(const char* ir_text, char* out, int64_t cap, int64_t* needed) {
   frame::Result<frame::ir::Graph> parsed = frame::ir::parse_text(ir_text);
   if (!parsed.is_ok()) return set_err(parsed.status());

@@ -93,6 +93,10 @@ def ref() -> ctypes.CDLL:
             "ref_transform_text": (c_int, [c_char_p, c_char_p, c_void_p, c_int64, POINTER(c_int64)]),
             "ref_roundtrip_text": (c_int, [c_char_p, c_void_p, c_int64, POINTER(c_int64)]),
             "ref_memory_plan_text": (c_int, [c_char_p, c_void_p, c_int64, POINTER(c_int64)]),
+            "ref_backward_text": (c_int, [c_char_p, ctypes.c_int32, c_void_p, ctypes.c_int32, c_void_p, c_int64,
+                                          POINTER(c_int64)]),
+            "ref_sgd_update_text": (c_int, [c_char_p, c_void_p, ctypes.c_int32, ctypes.c_double, c_void_p, c_int64,
+                                            POINTER(c_int64)]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(lib, name)
@@ -134,6 +138,18 @@ def _text_call(fn, *args) -> str:
 
 def ref_transform(ir_text: str, pass_name: str = "") -> str:
     return _text_call(ref().ref_transform_text, ir_text.encode(), pass_name.encode())
+
+
+def ref_backward(ir_text: str, loss_index: int, wrt) -> str:
+    """The reference's build_backward_graph on IR text."""
+    idx = (ctypes.c_int32 * max(1, len(wrt)))(*wrt)
+    return _text_call(ref().ref_backward_text, ir_text.encode(), loss_index, idx, len(wrt))
+
+
+def ref_sgd_update(ir_text: str, param_inputs, learning_rate: float) -> str:
+    """The reference's build_sgd_update_graph for the types of the given graph inputs of `ir_text`."""
+    idx = (ctypes.c_int32 * max(1, len(param_inputs)))(*param_inputs)
+    return _text_call(ref().ref_sgd_update_text, ir_text.encode(), idx, len(param_inputs), learning_rate)
 
 
 def ref_roundtrip(ir_text: str) -> str:

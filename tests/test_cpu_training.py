@@ -1,0 +1,269 @@
+"""Training path, host side (no GPU): the training-graph construction and the oracle's gradient kernels.
+
+* build_backward_graph / build_sgd_update_graph on IR text: identical text to the reference's own autograd
+  (oracle/_ref, the reference compiled from its sources), before and after the standard pipeline, and the same
+  error codes for the reference's rejection cases (src/compiler/autograd.cpp:118-300).
+* The oracle's restatement of every gradient-only op (oracle/cpu_kernels.cpp, training section): bit-identical to
+  the reference build on seeded inputs, per op and through whole training graphs.
+* Independent pins from the mathematics (no reference code involved): each gradient op is the adjoint of its
+  forward linear map, <f(x), y> = <x, f^T(y)>, checked in float64 on the oracle's float32 outputs; the max-pool
+  gradient against a numpy scatter with numpy's own argmax; mse_loss and its gradient against their closed forms;
+  the backward of the MLP against central finite differences of the loss.
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as orc
+from frame_hip import graphs, host, synth
+
+F32, F16, BF16 = 0, 2, 3
+needs_ref = pytest.mark.skipif(not orc.ref_available(), reason="reference build (oracle/_ref) not present")
+
+
+@pytest.fixture(autouse=True)
+def _cpu_backend():
+    orc.load_cpu_backend()  # the oracle's `cpu` backend: the pipeline's backend_lowering pass needs it registered
+
+
+def cpu_graph(name, in_shapes, out_shape, attrs=None, dtype=F32):
+    g = graphs.Graph("cpu")
+    vals = [g.input(dtype, s) for s in in_shapes]
+    g.output(g.op(name, vals, out_shape, attrs))
+    return g.text()
+
+
+def run(text, ins):
+    return orc.run_graph_cpu(text, ins)
+
+
+def run_ref(text, ins, outs):
+    return orc.ref_run_graph(text, ins, outs)
+
+
+def bits(a):
+    return np.ascontiguousarray(a).reshape(-1).view(np.uint8)
+
+
+# ---- graph construction -------------------------------------------------------------------------------------
+
+GRAPHS = [("mlp", graphs.mlp_train, dict(batch=4), [1, 2, 3, 4]),
+          ("cnn", graphs.cnn_train, dict(batch=2, image=16), [1, 2, 3, 4, 5, 6]),
+          ("cnn-partial", graphs.cnn_train, dict(batch=2, image=16), [6, 0, 2])]
+
+
+@needs_ref
+@pytest.mark.parametrize("dtype", [F32, BF16, F16])
+@pytest.mark.parametrize("name,mk,kw,wrt", GRAPHS)
+def test_backward_graph_text_matches_reference(name, mk, kw, wrt, dtype):
+    fwd = mk(dtype=dtype, device="cpu", **kw).text()
+    mine = host.backward(fwd, 0, wrt)
+    assert mine == orc.ref_backward(fwd, 0, wrt)
+    # and after the nine-pass pipeline (fusion, CSE, dead nodes, memory plan)
+    assert host.transform(mine) == orc.ref_transform(mine)
+
+
+@needs_ref
+def test_sgd_graph_text_matches_reference():
+    fwd = graphs.cnn_train(dtype=BF16, device="cpu", batch=2, image=16).text()
+    for lr in (0.1, 1e-3):
+        assert host.sgd_update(fwd, [1, 2, 3], lr) == orc.ref_sgd_update(fwd, [1, 2, 3], lr)
+
+
+def test_unreached_wrt_input_gets_zero_gradient():
+    fwd = graphs.mlp_train(batch=2, features=3, hidden=4, classes=2, device="cpu").text()
+    text = host.backward(fwd, 0, [5])  # the target: reached (mse_loss is differentiable in it)
+    assert "mse_loss_grad_internal" in text
+    g = graphs.Graph("cpu")
+    x = g.input(F32, (2, 3))
+    g.input(F32, (3, 3))  # unused input
+    g.output(g.mse_loss(x, x))
+    text = host.backward(g.text(), 0, [1])
+    assert "value=[0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0]" in text
+
+
+@needs_ref
+@pytest.mark.parametrize("case", ["nonscalar", "loss_range", "wrt_range", "wrt_dup", "no_gradient"])
+def test_backward_errors_match_reference(case):
+    g = graphs.Graph("cpu")
+    x = g.input(F32, (4, 8))
+    w = g.input(F32, (8, 3))
+    y = g.matmul(x, w)
+    if case == "no_gradient":  # fused_elementwise_internal has no GradientFn in either build
+        g.output(g.sum(g.op("fused_elementwise_internal", [y], y.shape, {"ops": "relu", "arities": [1]}), []))
+    elif case == "nonscalar":
+        g.output(y)
+    else:
+        g.output(g.sum(y, []))
+    loss, wrt = {"loss_range": (1, [1]), "wrt_range": (0, [2]), "wrt_dup": (0, [1, 1])}.get(case, (0, [1]))
+    with pytest.raises(host.FrameError) as mine:
+        host.backward(g.text(), loss, wrt)
+    with pytest.raises(RuntimeError) as ref:
+        orc.ref_backward(g.text(), loss, wrt)
+    import re
+    ref_code = int(re.search(r"reference call failed \((\d+)\)", str(ref.value)).group(1))
+    assert mine.value.code == ref_code  # frame::ErrorCode ordinals on both sides
+    assert ref_code == (host.CODES["unimplemented"] if case == "no_gradient" else host.CODES["invalid_argument"])
+
+
+# ---- oracle vs the reference build -----------------------------------------------------------------------------
+
+@needs_ref
+@pytest.mark.parametrize("dtype", [F32, BF16, F16])
+@pytest.mark.parametrize("name,mk,kw,wrt", GRAPHS[:2])
+def test_oracle_training_graph_bit_identical_to_reference(name, mk, kw, wrt, dtype):
+    fwd = mk(dtype=dtype, device="cpu", **kw).text()
+    text = host.backward(fwd, 0, wrt)
+    ins = (graphs.mlp_train_inputs if name == "mlp" else graphs.cnn_train_inputs)(dtype=dtype, **kw)
+    mine = run(text, ins)
+    ref = run_ref(text, ins, [(o.shape, o.dtype) for o in mine])
+    for i, (a, b) in enumerate(zip(mine, ref)):
+        assert np.array_equal(bits(a), bits(b)), f"output {i}"
+
+
+OP_CASES = [
+    ("relu_grad_internal", [(5, 33), (5, 33)], (5, 33), None),
+    ("matmul_grad_lhs_internal", [(7, 5), (9, 5)], (7, 9), None),
+    ("matmul_grad_rhs_internal", [(7, 9), (7, 5)], (9, 5), None),
+    ("conv2d_grad_input_internal", [(2, 6, 4, 5), (6, 4, 3, 3)], (2, 4, 8, 9),
+     {"input_shape": graphs.Shape((2, 4, 8, 9)), "stride": [2, 2], "padding": [1, 1], "groups": 1}),
+    ("conv2d_grad_filter_internal", [(2, 4, 8, 9), (2, 6, 4, 5)], (6, 4, 3, 3),
+     {"filter_shape": graphs.Shape((6, 4, 3, 3)), "stride": [2, 2], "padding": [1, 1], "groups": 1}),
+    ("conv2d_grad_input_internal", [(2, 6, 8, 8), (6, 2, 3, 3)], (2, 4, 8, 8),
+     {"input_shape": graphs.Shape((2, 4, 8, 8)), "stride": [1, 1], "padding": [1, 1], "groups": 2}),
+    ("max_pool2d_grad_internal", [(2, 3, 5, 5), (2, 3, 9, 9)], (2, 3, 9, 9),
+     {"input_shape": graphs.Shape((2, 3, 9, 9)), "kernel": [3, 3], "stride": [2, 2], "padding": [1, 1]}),
+    ("avg_pool2d_grad_internal", [(2, 3, 5, 5)], (2, 3, 9, 9),
+     {"input_shape": graphs.Shape((2, 3, 9, 9)), "kernel": [3, 3], "stride": [2, 2], "padding": [1, 1]}),
+    ("sum", [(3, 4, 5, 6)], (4,), {"axes": [0, 2, 3]}),
+    ("sum", [(3, 4, 5)], (1, 4, 1), {"axes": [0, 2], "keepdims": True}),
+    ("sum", [(300, 7)], (), {"axes": []}),
+    ("sum_grad_internal", [(4,)], (3, 4, 5, 6), {"axes": [0, 2, 3], "input_shape": graphs.Shape((3, 4, 5, 6))}),
+    ("mse_loss", [(33, 7), (33, 7)], (), None),
+    ("mse_loss_grad_internal", [(33, 7), (33, 7), ()], (33, 7), None),
+]
+
+
+@needs_ref
+@pytest.mark.parametrize("dtype", [F32, BF16, F16])
+@pytest.mark.parametrize("case", OP_CASES, ids=lambda c: c[0] + str(c[2]))
+def test_oracle_op_bit_identical_to_reference(case, dtype):
+    name, ins_s, out_s, attrs = case
+    text = cpu_graph(name, ins_s, out_s, attrs, dtype)
+    ins = [synth.tensor(90 + i, s, dtype).reshape(s) for i, s in enumerate(ins_s)]
+    if name.startswith("max_pool"):
+        ins[1].reshape(-1)[::5] = ins[1].reshape(-1)[2]  # ties
+    (mine,) = run(text, ins)
+    (ref,) = run_ref(text, ins, [(mine.shape, mine.dtype)])
+    assert np.array_equal(bits(mine), bits(ref))
+
+
+# ---- pins from the mathematics ---------------------------------------------------------------------------------
+
+def f64(a):
+    return np.asarray(a, dtype=np.float64)
+
+
+def conv_ref64(x, w, s, p):
+    """float64 direct convolution (groups 1), written from the definition."""
+    n, cin, h, wd = x.shape
+    cout, _, kh, kw = w.shape
+    oh, ow = (h + 2 * p - kh) // s + 1, (wd + 2 * p - kw) // s + 1
+    xp = np.zeros((n, cin, h + 2 * p, wd + 2 * p))
+    xp[:, :, p:p + h, p:p + wd] = x
+    y = np.zeros((n, cout, oh, ow))
+    for a in range(kh):
+        for b in range(kw):
+            patch = xp[:, :, a:a + s * oh:s, b:b + s * ow:s]  # [n, cin, oh, ow]
+            y += np.einsum("nchw,oc->nohw", patch, w[:, :, a, b])
+    return y
+
+
+@pytest.mark.parametrize("s,p,k", [(1, 1, 3), (2, 1, 3), (2, 0, 1), (2, 3, 7)])
+def test_conv_grads_are_adjoints(s, p, k):
+    rng = np.random.default_rng(5)
+    n, cin, h, w, cout = 2, 3, 11, 10, 4
+    x = rng.standard_normal((n, cin, h, w)).astype(np.float32)
+    wt = rng.standard_normal((cout, cin, k, k)).astype(np.float32)
+    y = conv_ref64(f64(x), f64(wt), s, p)
+    dy = rng.standard_normal(y.shape).astype(np.float32)
+    common = {"stride": [s, s], "padding": [p, p], "groups": 1}
+    (gx,) = run(cpu_graph("conv2d_grad_input_internal", [dy.shape, wt.shape], x.shape,
+                          dict(common, input_shape=graphs.Shape(x.shape))), [dy, wt])
+    (gw,) = run(cpu_graph("conv2d_grad_filter_internal", [x.shape, dy.shape], wt.shape,
+                          dict(common, filter_shape=graphs.Shape(wt.shape))), [x, dy])
+    lhs = np.sum(y * f64(dy))
+    np.testing.assert_allclose(np.sum(f64(x) * f64(gx)), lhs, rtol=1e-5)
+    np.testing.assert_allclose(np.sum(f64(wt) * f64(gw)), lhs, rtol=1e-5)
+
+
+def test_avg_pool_grad_is_adjoint_and_max_pool_grad_scatters_to_argmax():
+    rng = np.random.default_rng(6)
+    xs, k, s, p = (2, 3, 9, 8), 3, 2, 1
+    x = rng.standard_normal(xs).astype(np.float32)
+    oh, ow = (9 + 2 * p - k) // s + 1, (8 + 2 * p - k) // s + 1
+    dy = rng.standard_normal((2, 3, oh, ow)).astype(np.float32)
+    attrs = {"kernel": [k, k], "stride": [s, s], "padding": [p, p], "input_shape": graphs.Shape(xs)}
+    (ga,) = run(cpu_graph("avg_pool2d_grad_internal", [dy.shape], xs, attrs), [dy])
+    xp = np.zeros((2, 3, 9 + 2 * p, 8 + 2 * p))
+    xp[:, :, p:p + 9, p:p + 8] = x
+    avg = np.zeros(dy.shape)
+    for a in range(k):
+        for b in range(k):
+            avg += xp[:, :, a:a + s * oh:s, b:b + s * ow:s]
+    avg /= k * k
+    np.testing.assert_allclose(np.sum(f64(x) * f64(ga)), np.sum(avg * f64(dy)), rtol=1e-5)
+    (gm,) = run(cpu_graph("max_pool2d_grad_internal", [dy.shape, xs], xs, attrs), [dy, x])
+    want = np.zeros(xs)
+    for nn in range(2):
+        for c in range(3):
+            for i in range(oh):
+                for j in range(ow):
+                    h0, w0 = i * s - p, j * s - p
+                    hs, ws = max(h0, 0), max(w0, 0)
+                    win = x[nn, c, hs:h0 + k, ws:w0 + k]
+                    r, q = np.unravel_index(np.argmax(win), win.shape)  # first maximum in row-major order
+                    want[nn, c, hs + r, ws + q] += dy[nn, c, i, j]
+    np.testing.assert_allclose(f64(gm), want, rtol=1e-6, atol=1e-6)
+
+
+def test_matmul_sum_and_mse_closed_forms():
+    rng = np.random.default_rng(7)
+    m, n, k = 9, 5, 7
+    gy = rng.standard_normal((m, n)).astype(np.float32)
+    b = rng.standard_normal((k, n)).astype(np.float32)
+    a = rng.standard_normal((m, k)).astype(np.float32)
+    (ga,) = run(cpu_graph("matmul_grad_lhs_internal", [(m, n), (k, n)], (m, k)), [gy, b])
+    (gb,) = run(cpu_graph("matmul_grad_rhs_internal", [(m, k), (m, n)], (k, n)), [a, gy])
+    np.testing.assert_allclose(ga, f64(gy) @ f64(b).T, rtol=1e-5, atol=1e-5)
+    np.testing.assert_allclose(gb, f64(a).T @ f64(gy), rtol=1e-5, atol=1e-5)
+    x = rng.standard_normal((3, 4, 5, 6)).astype(np.float32)
+    (sx,) = run(cpu_graph("sum", [x.shape], (4,), {"axes": [0, 2, 3]}), [x])
+    np.testing.assert_allclose(sx, f64(x).sum(axis=(0, 2, 3)), rtol=1e-5, atol=1e-5)
+    g = rng.standard_normal((4,)).astype(np.float32)
+    (gx,) = run(cpu_graph("sum_grad_internal", [(4,)], x.shape, {"axes": [0, 2, 3], "input_shape": graphs.Shape(x.shape)}), [g])
+    assert np.array_equal(gx, np.broadcast_to(g.reshape(1, 4, 1, 1), x.shape))
+    pr, t = rng.standard_normal((33, 7)).astype(np.float32), rng.standard_normal((33, 7)).astype(np.float32)
+    (loss,) = run(cpu_graph("mse_loss", [pr.shape, t.shape], ()), [pr, t])
+    np.testing.assert_allclose(float(loss), np.mean((f64(pr) - f64(t)) ** 2), rtol=1e-5)
+    gyl = np.array(0.75, dtype=np.float32)
+    (gp,) = run(cpu_graph("mse_loss_grad_internal", [pr.shape, t.shape, ()], pr.shape), [pr, t, gyl])
+    np.testing.assert_allclose(gp, 2 * 0.75 / pr.size * (f64(pr) - f64(t)), rtol=1e-5, atol=1e-7)
+
+
+def test_mlp_backward_matches_finite_differences():
+    kw = dict(batch=3, features=5, hidden=6, classes=4)
+    fwd = graphs.mlp_train(device="cpu", **kw).text()
+    ins = graphs.mlp_train_inputs(**kw)
+    ins = [i.astype(np.float32) for i in ins]
+    grads = run(host.backward(fwd, 0, [1, 2, 3, 4]), ins)[1:]
+    rng = np.random.default_rng(8)
+    eps = 1e-2
+    for pi, g in zip([1, 2, 3, 4], grads):
+        for _ in range(3):
+            idx = tuple(rng.integers(0, d) for d in ins[pi].shape)
+            plus = [i.copy() for i in ins]
+            minus = [i.copy() for i in ins]
+            plus[pi][idx] += eps
+            minus[pi][idx] -= eps
+            fd = (float(run(fwd, plus)[0]) - float(run(fwd, minus)[0])) / (2 * eps)
+            assert abs(fd - float(g[idx])) <= 2e-3 * max(1.0, abs(fd)), (pi, idx, fd, float(g[idx]))

@@ -1,0 +1,251 @@
+"""Training path on the MI355X: the gradient-only ops of compiler::build_backward_graph, each compiled for `hip`
+(runtime::compile -> HipBackend::compile -> HipExecutable::run) and compared with the same graph on the oracle's
+`cpu` backend, then whole training graphs (backward of an MLP and of a small CNN, and the SGD update graph).
+
+Bit-exact where the hip kernel keeps the reference's per-element summation order (relu_grad, pool gradients, conv
+gradients, matmul gradients below the tiled-GEMM threshold, sum_grad, mse_loss_grad); rtol 1e-5 (float32) /
+1e-2 (16-bit) with atol = rtol * rms(expected) where the kernel reduces in another order (sum, mse_loss, matmul
+gradients on the tiled GEMM) or the graph contains such ops (tests/tolerance.py).
+"""
+import numpy as np
+import pytest
+
+import oracle_lib as orc
+from frame_hip import graphs, host, synth
+from tolerance import assert_bitwise, assert_close
+
+pytestmark = pytest.mark.gpu
+F32, F16, BF16 = 0, 2, 3
+DTYPES = [F32, BF16, F16]
+
+
+def say(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert host.device_count("hip") >= 1, "no hip device"
+    orc.load_cpu_backend()
+
+
+def both(g, ins):
+    """(hip outputs, oracle cpu outputs) of graph g (built for device 'hip')."""
+    got = host.compile(g.text(), "hip", 1).run(ins)
+    want = orc.run_graph_cpu(g.text().replace("@hip:0", "@cpu:0"), ins)
+    return got, want
+
+
+def one_op(name, ins_specs, out_shape, attrs=None, dtype=F32):
+    g = graphs.Graph("hip")
+    vals = [g.input(dtype, s) for s in ins_specs]
+    g.output(g.op(name, vals, out_shape, attrs))
+    return g
+
+
+def tensors(seed, shapes, dtype, kind="normal"):
+    return [synth.tensor(seed + i, s, dtype, kind).reshape(s) for i, s in enumerate(shapes)]
+
+
+def conv_out(h, k, s, p):
+    return (h + 2 * p - k) // s + 1
+
+
+# ---- elementwise ---------------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_relu_grad(dev, dtype):
+    say(f"relu_grad dtype={dtype}")
+    shape = (3, 1000, 17)
+    x, gy = tensors(1, [shape, shape], dtype)
+    x.reshape(-1)[:40] = 0  # x == 0 takes the zero branch
+    got, want = both(one_op("relu_grad_internal", [shape, shape], shape, dtype=dtype), [x, gy])
+    assert_bitwise(got[0], want[0], "relu_grad")
+
+
+# ---- matmul gradients ----------------------------------------------------------------------------------------
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("m,n,k", [(64, 10, 256), (64, 256, 784), (3, 5, 7), (130, 33, 70)])
+def test_matmul_grads_sequential_exact(dev, dtype, m, n, k):
+    # small: fh_matmul_grad's sequential kernel reads the transposed operand in place -> bit-exact
+    say(f"matmul_grad small m={m} n={n} k={k} dtype={dtype}")
+    gy, b, a = tensors(10, [(m, n), (k, n), (m, k)], dtype)
+    got, want = both(one_op("matmul_grad_lhs_internal", [(m, n), (k, n)], (m, k), dtype=dtype), [gy, b])
+    assert_bitwise(got[0], want[0], "matmul_grad_lhs")
+    got, want = both(one_op("matmul_grad_rhs_internal", [(m, k), (m, n)], (k, n), dtype=dtype), [a, gy])
+    assert_bitwise(got[0], want[0], "matmul_grad_rhs")
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16])
+def test_matmul_grads_tiled(dev, dtype):
+    # large: lowered to transpose + matmul on the tiled / MFMA GEMM kernels -> tolerance
+    m, n, k = 1024, 512, 768
+    say(f"matmul_grad tiled dtype={dtype}")
+    assert "transpose" in host.hip_lowered(one_op("matmul_grad_lhs_internal", [(m, n), (k, n)], (m, k), dtype=dtype).text())
+    gy, b, a = tensors(20, [(m, n), (k, n), (m, k)], dtype)
+    got, want = both(one_op("matmul_grad_lhs_internal", [(m, n), (k, n)], (m, k), dtype=dtype), [gy, b])
+    assert_close(got[0], want[0], dtype, what="matmul_grad_lhs tiled")
+    got, want = both(one_op("matmul_grad_rhs_internal", [(m, k), (m, n)], (k, n), dtype=dtype), [a, gy])
+    assert_close(got[0], want[0], dtype, what="matmul_grad_rhs tiled")
+
+
+def test_matmul_grad_eager_launch(dev):
+    say("matmul_grad eager launch")
+    m, n, k = 40, 24, 56
+    g = one_op("matmul_grad_rhs_internal", [(m, k), (m, n)], (k, n))
+    a, gy = tensors(30, [(m, k), (m, n)], F32)
+    ta, tg = host.Tensor.from_numpy("hip", F32, a), host.Tensor.from_numpy("hip", F32, gy)
+    out = host.Tensor("hip", F32, (k, n))
+    s = host.Stream("hip")
+    host.launch(g.text(), "hip", [ta, tg], [out], s)
+    s.synchronize()
+    (want,) = orc.run_graph_cpu(g.text().replace("@hip:0", "@cpu:0"), [a, gy])
+    assert_bitwise(out.numpy(), want, "eager matmul_grad_rhs")
+
+
+# ---- conv gradients ------------------------------------------------------------------------------------------
+
+CONV_CASES = [
+    # (N, Cin, H, W, Cout, K, stride, pad, groups)
+    (2, 8, 9, 9, 16, 3, 1, 1, 1),
+    (2, 8, 9, 10, 16, 3, 2, 1, 1),
+    (3, 16, 8, 8, 8, 1, 2, 0, 1),
+    (2, 3, 15, 15, 8, 7, 2, 3, 1),
+    (2, 8, 6, 6, 8, 3, 1, 0, 2),
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("case", CONV_CASES)
+def test_conv_grads(dev, dtype, case):
+    n, cin, h, w, cout, kk, s, p, grp = case
+    say(f"conv grads {case} dtype={dtype}")
+    oh, ow = conv_out(h, kk, s, p), conv_out(w, kk, s, p)
+    xs, ws, dys = (n, cin, h, w), (cout, cin // grp, kk, kk), (n, cout, oh, ow)
+    x, wt, dy = tensors(40, [xs, ws, dys], dtype)
+    common = {"stride": [s, s], "padding": [p, p], "groups": grp}
+    gi = one_op("conv2d_grad_input_internal", [dys, ws], xs, dict(common, input_shape=graphs.Shape(xs)), dtype)
+    got, want = both(gi, [dy, wt])
+    assert_bitwise(got[0], want[0], "conv2d_grad_input")
+    gf = one_op("conv2d_grad_filter_internal", [xs, dys], ws, dict(common, filter_shape=graphs.Shape(ws)), dtype)
+    got, want = both(gf, [x, dy])
+    assert_bitwise(got[0], want[0], "conv2d_grad_filter")
+
+
+# ---- pool gradients ------------------------------------------------------------------------------------------
+
+POOL_CASES = [
+    # (N, C, H, W, K, stride, pad)
+    (2, 4, 17, 16, 3, 2, 1),
+    (2, 3, 8, 8, 2, 2, 0),
+    (1, 5, 7, 7, 7, 7, 0),
+    (2, 2, 9, 9, 3, 1, 1),
+]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("case", POOL_CASES)
+def test_pool_grads(dev, dtype, case):
+    n, c, h, w, kk, s, p = case
+    say(f"pool grads {case} dtype={dtype}")
+    oh, ow = conv_out(h, kk, s, p), conv_out(w, kk, s, p)
+    xs, dys = (n, c, h, w), (n, c, oh, ow)
+    x, dy = tensors(50, [xs, dys], dtype)
+    x.reshape(-1)[::7] = x.reshape(-1)[3]  # repeated values: ties resolve to the first maximum
+    attrs = {"kernel": [kk, kk], "stride": [s, s], "padding": [p, p], "input_shape": graphs.Shape(xs)}
+    got, want = both(one_op("max_pool2d_grad_internal", [dys, xs], xs, attrs, dtype), [dy, x])
+    assert_bitwise(got[0], want[0], "max_pool2d_grad")
+    got, want = both(one_op("avg_pool2d_grad_internal", [dys], xs, attrs, dtype), [dy])
+    assert_bitwise(got[0], want[0], "avg_pool2d_grad")
+
+
+# ---- sum, sum_grad, mse_loss -----------------------------------------------------------------------------------
+
+SUM_CASES = [((4, 6, 5, 7), [0, 2, 3], False), ((4, 6, 5, 7), [], False), ((33, 1000), [1], True),
+             ((33, 1000), [0], False), ((8, 3, 300), [0, 2], False), ((1 << 20,), [], False)]
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape,axes,keep", SUM_CASES)
+def test_sum_and_sum_grad(dev, dtype, shape, axes, keep):
+    say(f"sum {shape} axes={axes} keepdims={keep} dtype={dtype}")
+    red = set(range(len(shape))) if not axes else set(axes)
+    out = tuple((1 if keep else None) if i in red else d for i, d in enumerate(shape))
+    out = tuple(d for d in out if d is not None)
+    attrs = {"axes": list(axes)}
+    if keep:
+        attrs["keepdims"] = True
+    (x,) = tensors(60, [shape], dtype)
+    got, want = both(one_op("sum", [shape], out, attrs, dtype), [x])
+    # fp32 tree vs the reference's sequential sum: bound by the sum of magnitudes
+    mag = np.abs(x.astype(np.float32) if dtype == F32 else synth.to_float(x, dtype)).sum(
+        axis=tuple(sorted(red)), keepdims=keep).reshape(out)
+    g32 = got[0] if dtype == F32 else synth.to_float(got[0], dtype)
+    w32 = want[0] if dtype == F32 else synth.to_float(want[0], dtype)
+    tol = (2e-6 * mag) if dtype == F32 else (1e-2 * np.abs(w32) + 1e-5 * mag)
+    assert np.all(np.abs(g32 - w32) <= tol), f"sum: max excess {np.max(np.abs(g32 - w32) - tol)}"
+    (gy,) = tensors(61, [out], dtype)
+    gattrs = {"axes": list(axes), "input_shape": graphs.Shape(shape)}
+    got, want = both(one_op("sum_grad_internal", [out], shape, gattrs, dtype), [gy])
+    assert_bitwise(got[0], want[0], "sum_grad")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(64, 10), (1000, 513), (7,)])
+def test_mse_loss_and_grad(dev, dtype, shape):
+    say(f"mse_loss {shape} dtype={dtype}")
+    p, t = tensors(70, [shape, shape], dtype)
+    got, want = both(one_op("mse_loss", [shape, shape], (), None, dtype), [p, t])
+    assert_close(np.asarray(got[0]).reshape(1), np.asarray(want[0]).reshape(1), dtype, what="mse_loss")
+    (gy,) = tensors(72, [()], dtype)
+    got, want = both(one_op("mse_loss_grad_internal", [shape, shape, ()], shape, None, dtype), [p, t, gy])
+    assert_bitwise(got[0], want[0], "mse_loss_grad")
+
+
+# ---- whole training graphs -----------------------------------------------------------------------------------
+
+def check_outputs(got, want, dtype, what):
+    assert len(got) == len(want)
+    for i, (a, b) in enumerate(zip(got, want)):
+        assert_close(np.asarray(a).reshape(-1), np.asarray(b).reshape(-1), dtype, what=f"{what} output {i}")
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16])
+def test_mlp_training_step(dev, dtype):
+    # C1's MLP under mse_loss: loss, d/dw1, d/db1, d/dw2, d/db2
+    say(f"mlp training step dtype={dtype}")
+    g = graphs.mlp_train(batch=64, dtype=dtype, device="hip")
+    text = host.backward(g.text(), 0, [1, 2, 3, 4])
+    ins = graphs.mlp_train_inputs(batch=64, dtype=dtype)
+    got = host.compile(text, "hip", 1).run(ins)
+    want = orc.run_graph_cpu(text.replace("@hip:0", "@cpu:0"), ins)
+    check_outputs(got, want, dtype, "mlp training")
+    if dtype == F32:
+        # below the tiled threshold every GEMM keeps the reference's order: the gradients are bit-exact
+        for i in range(1, 5):
+            assert_bitwise(got[i], want[i], f"mlp gradient {i}")
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16])
+def test_cnn_training_step(dev, dtype):
+    say(f"cnn training step dtype={dtype}")
+    g = graphs.cnn_train(batch=4, dtype=dtype, device="hip")
+    text = host.backward(g.text(), 0, [1, 2, 3, 4, 5, 6])
+    ins = graphs.cnn_train_inputs(batch=4, dtype=dtype)
+    got = host.compile(text, "hip", 1).run(ins)
+    want = orc.run_graph_cpu(text.replace("@hip:0", "@cpu:0"), ins)
+    check_outputs(got, want, dtype, "cnn training")
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16])
+def test_sgd_update(dev, dtype):
+    say(f"sgd update dtype={dtype}")
+    g = graphs.mlp_train(batch=64, dtype=dtype, device="hip")
+    text = host.sgd_update(g.text(), [1, 2, 3, 4], 0.05)
+    params = graphs.mlp_train_inputs(batch=64, dtype=dtype)[1:5]
+    grads = [synth.tensor(80 + i, p.shape, dtype) for i, p in enumerate(params)]
+    got = host.compile(text, "hip", 1).run(params + grads)
+    want = orc.run_graph_cpu(text.replace("@hip:0", "@cpu:0"), params + grads)
+    for i in range(4):
+        assert_bitwise(got[i], want[i], f"sgd param {i}")
