@@ -67,14 +67,18 @@ def test_relu_grad(dev, dtype):
 
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("m,n,k", [(64, 10, 256), (64, 256, 784), (3, 5, 7), (130, 33, 70)])
-def test_matmul_grads_sequential_exact(dev, dtype, m, n, k):
-    # small: fh_matmul_grad's sequential kernel reads the transposed operand in place -> bit-exact
+def test_matmul_grads_small(dev, dtype, m, n, k):
+    # below the tiled threshold fh_matmul_grad's sequential kernel reads the transposed operand in place ->
+    # bit-exact; above it (16-bit [784,256] here) the backend lowers to transpose + MFMA GEMM -> tolerance
     say(f"matmul_grad small m={m} n={n} k={k} dtype={dtype}")
     gy, b, a = tensors(10, [(m, n), (k, n), (m, k)], dtype)
-    got, want = both(one_op("matmul_grad_lhs_internal", [(m, n), (k, n)], (m, k), dtype=dtype), [gy, b])
-    assert_bitwise(got[0], want[0], "matmul_grad_lhs")
-    got, want = both(one_op("matmul_grad_rhs_internal", [(m, k), (m, n)], (k, n), dtype=dtype), [a, gy])
-    assert_bitwise(got[0], want[0], "matmul_grad_rhs")
+    for g, ins, what in [(one_op("matmul_grad_lhs_internal", [(m, n), (k, n)], (m, k), dtype=dtype), [gy, b], "lhs"),
+                         (one_op("matmul_grad_rhs_internal", [(m, k), (m, n)], (k, n), dtype=dtype), [a, gy], "rhs")]:
+        got, want = both(g, ins)
+        if "transpose" in host.hip_lowered(g.text()):
+            assert_close(got[0], want[0], dtype, what=f"matmul_grad_{what} (tiled)")
+        else:
+            assert_bitwise(got[0], want[0], f"matmul_grad_{what}")
 
 
 @pytest.mark.parametrize("dtype", [F32, BF16])
@@ -197,7 +201,15 @@ def test_mse_loss_and_grad(dev, dtype, shape):
     say(f"mse_loss {shape} dtype={dtype}")
     p, t = tensors(70, [shape, shape], dtype)
     got, want = both(one_op("mse_loss", [shape, shape], (), None, dtype), [p, t])
-    assert_close(np.asarray(got[0]).reshape(1), np.asarray(want[0]).reshape(1), dtype, what="mse_loss")
+    # The reference sums sequentially in fp32 (its error grows with numel: 1.7e-4 relative at 513k terms); the
+    # kernel's tree is checked against the float64 value of the same storage inputs, and must be at least as close
+    # to it as the reference is, up to the tolerance.
+    truth = float(np.mean((synth.to_float(p, dtype).astype(np.float64) - synth.to_float(t, dtype).astype(np.float64)) ** 2))
+    g = float(synth.to_float(np.asarray(got[0]).reshape(1), dtype)[0])
+    w = float(synth.to_float(np.asarray(want[0]).reshape(1), dtype)[0])
+    rtol = {F32: 1e-5, BF16: 8e-3, F16: 1e-3}[dtype]
+    assert abs(g - truth) <= rtol * truth, (g, truth)
+    assert abs(g - w) <= abs(w - truth) + rtol * truth, (g, w, truth)
     (gy,) = tensors(72, [()], dtype)
     got, want = both(one_op("mse_loss_grad_internal", [shape, shape, ()], shape, None, dtype), [p, t, gy])
     assert_bitwise(got[0], want[0], "mse_loss_grad")
