@@ -1,0 +1,250 @@
+// conv2d_grad_filter_internal on MFMA (bf16 / f16): the filter gradient as a GEMM over the batch-spatial positions,
+//   dW[co][(a,b,ci)] = sum over p = (n, oh, ow) of dy[p][co] * x[n][oh*sh - ph + a][ow*sw - pw + b][ci],
+// M = Cout, N = KH*KW*Cin, K = N*Ho*Wo, with both operands channels-last (dy [P][Cout], x [N][H][W][Cin]). K is
+// the long dimension (batch times the output plane) and M*N is small, so K is split across workgroups: each
+// writes an fp32 partial tile into a workspace, and a second kernel sums the partials in split order and writes
+// dW in the reference's [Cout][Cin][KH][KW] layout with one rounding.
+//
+// Both operands are k-major (rows of p), so both MFMA fragments come from ds_read_b64_tr_b16 transpose reads of
+// [BK][cols] LDS tiles (the B-operand path of the GEMM kernel, used for A as well). Tiles: 64 (co) x 128 (a,b,ci)
+// per workgroup, 4 waves of 32 x 64 (two 32x32x16 MFMA tiles), 32 p-rows per stage, register-staged loads with
+// zero fill for rows past the split and taps in the padding, two LDS stages.
+#include <algorithm>
+
+#include "fh_mfma16.h"
+
+namespace fh {
+namespace {
+
+using namespace mfma16;
+
+constexpr int kWM = 64, kWN = 128, kWK = 32;  // workgroup tile
+constexpr int kWThreads = 256;
+
+struct WgradArgs {
+  const void* x;   // [N][H][W][Cin] (Cin % 8 == 0)
+  const void* dy;  // [P][Cout] (Cout % 8 == 0)
+  float* part;     // [splits][Cout][NC]
+  int32_t h, w, cin, cout, kw, sh, sw, ph, pw, oh, ow, nc, tiles_n;
+  int64_t p, rows_per_split;
+};
+
+__device__ __forceinline__ int swz8(int krow) { return 2 * (krow & 3); }
+__device__ __forceinline__ int swz16(int krow) { return (2 * (krow & 3)) ^ (8 * (krow & 1)); }
+
+template <typename T>
+__global__ __launch_bounds__(kWThreads) void conv_wgrad_kernel(WgradArgs a) {
+  using S = typename Io<T>::storage;
+  __shared__ __attribute__((aligned(16))) S As[2][kWK * kWM];
+  __shared__ __attribute__((aligned(16))) S Bs[2][kWK * kWN];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tm = blockIdx.x / a.tiles_n, tn = blockIdx.x % a.tiles_n;
+  const int m0 = tm * kWM, n0 = tn * kWN;
+  const int64_t p_begin = static_cast<int64_t>(blockIdx.y) * a.rows_per_split;
+  const int64_t p_end = min(a.p, p_begin + a.rows_per_split);
+  const S* __restrict__ X = static_cast<const S*>(a.x);
+  const S* __restrict__ DY = static_cast<const S*>(a.dy);
+
+  // A loads: one 16-byte chunk per thread, row t/8, column chunk t%8
+  const int a_row = tid >> 3, a_chunk = tid & 7;
+  const bool a_col_ok = m0 + 8 * a_chunk < a.cout;
+  // B loads: two chunks per thread, rows t/16 and t/16 + 16, column chunk t%16 (a fixed filter tap and ci block)
+  const int b_row = tid >> 4, b_chunk = tid & 15;
+  const int ncol = n0 + 8 * b_chunk;
+  const bool b_col_ok = ncol < a.nc;
+  const int tap = b_col_ok ? ncol / a.cin : 0;
+  const int ci = b_col_ok ? ncol - tap * a.cin : 0;
+  const int ta = tap / a.kw, tb = tap - ta * a.kw;
+  const int plane = a.oh * a.ow;
+
+  uint4 ra, rb[2];
+  auto load = [&](int64_t p0) {
+    {
+      const int64_t p = p0 + a_row;
+      ra = (p < p_end && a_col_ok) ? *reinterpret_cast<const uint4*>(DY + p * a.cout + m0 + 8 * a_chunk)
+                                   : uint4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int64_t p = p0 + b_row + 16 * i;
+      uint4 v{0, 0, 0, 0};
+      if (p < p_end && b_col_ok) {
+        const int32_t n = static_cast<int32_t>(p / plane);
+        const int32_t rem = static_cast<int32_t>(p - static_cast<int64_t>(n) * plane);
+        const int32_t oh = rem / a.ow, ow = rem - oh * a.ow;
+        const int32_t ih = oh * a.sh - a.ph + ta, iw = ow * a.sw - a.pw + tb;
+        if (ih >= 0 && ih < a.h && iw >= 0 && iw < a.w)
+          v = *reinterpret_cast<const uint4*>(X + ((static_cast<int64_t>(n) * a.h + ih) * a.w + iw) * a.cin + ci);
+      }
+      rb[i] = v;
+    }
+  };
+  auto store = [&](int buf) {
+    *reinterpret_cast<uint4*>(&As[buf][a_row * kWM + ((a_chunk ^ swz8(a_row)) * 8)]) = ra;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = b_row + 16 * i;
+      *reinterpret_cast<uint4*>(&Bs[buf][r * kWN + ((b_chunk ^ swz16(r)) * 8)]) = rb[i];
+    }
+  };
+
+  // transpose-read addressing (bytes within a tile): lane group g = lane/16 covers 16 columns and 4 k rows;
+  // lane q + 4e of the group points at row (kbase + e), columns 4q .. 4q+3 of the group's 16
+  const int wm = wave >> 1, wn = wave & 1;
+  const int g = lane >> 4, r16 = lane & 15, q = r16 & 3, e = r16 >> 2;
+  const int krow0 = 8 * (g >> 1) + e;  // + 16 s + 4 h: krow & 3 and krow & 1 unchanged
+  int a_off, b_off[2];
+  {
+    const int col = wm * 32 + 16 * (g & 1) + 4 * q;
+    a_off = krow0 * (kWM * 2) + ((col >> 3) ^ swz8(krow0)) * 16 + (col & 7) * 2;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int c = wn * 64 + 32 * j + 16 * (g & 1) + 4 * q;
+      b_off[j] = krow0 * (kWN * 2) + ((c >> 3) ^ swz16(krow0)) * 16 + (c & 7) * 2;
+    }
+  }
+
+  f32x16_t acc[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int x = 0; x < 16; ++x) acc[j][x] = 0.0f;
+
+  const int64_t steps = (p_end - p_begin + kWK - 1) / kWK;
+  if (steps > 0) {
+    load(p_begin);
+    store(0);
+  }
+  __syncthreads();
+  asm volatile("" ::: "memory");  // the transpose reads below are asm: keep them after the barrier
+  for (int64_t it = 0; it < steps; ++it) {
+    const int buf = static_cast<int>(it & 1);
+    if (it + 1 < steps) load(p_begin + (it + 1) * kWK);
+    const uint32_t abase = lds_addr((const FH_LDS void*)&As[buf][0]);
+    const uint32_t bbase = lds_addr((const FH_LDS void*)&Bs[buf][0]);
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      u32x2_t al, ah, bl[2], bh[2];
+      if (s == 0) {
+        al = lds_read_tr16_b64<0>(abase + a_off);
+        ah = lds_read_tr16_b64<4 * kWM * 2>(abase + a_off);
+        bl[0] = lds_read_tr16_b64<0>(bbase + b_off[0]);
+        bh[0] = lds_read_tr16_b64<4 * kWN * 2>(bbase + b_off[0]);
+        bl[1] = lds_read_tr16_b64<0>(bbase + b_off[1]);
+        bh[1] = lds_read_tr16_b64<4 * kWN * 2>(bbase + b_off[1]);
+      } else {
+        al = lds_read_tr16_b64<16 * kWM * 2>(abase + a_off);
+        ah = lds_read_tr16_b64<20 * kWM * 2>(abase + a_off);
+        bl[0] = lds_read_tr16_b64<16 * kWN * 2>(bbase + b_off[0]);
+        bh[0] = lds_read_tr16_b64<20 * kWN * 2>(bbase + b_off[0]);
+        bl[1] = lds_read_tr16_b64<16 * kWN * 2>(bbase + b_off[1]);
+        bh[1] = lds_read_tr16_b64<20 * kWN * 2>(bbase + b_off[1]);
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(al), "+v"(ah), "+v"(bl[0]), "+v"(bh[0]), "+v"(bl[1]), "+v"(bh[1]));
+      const u32x4_t af{al[0], al[1], ah[0], ah[1]};
+#pragma unroll
+      for (int j = 0; j < 2; ++j) mfma32<T>(af, u32x4_t{bl[j][0], bl[j][1], bh[j][0], bh[j][1]}, acc[j]);
+    }
+    // buf^1 was last read in the previous iteration, before its closing barrier: safe to refill now
+    if (it + 1 < steps) store(buf ^ 1);
+    __syncthreads();
+    asm volatile("" ::: "memory");
+  }
+
+  // fp32 partial tile: row m = 8*(x/4) + 4*(lane/32) + x%4 of the wave's 32, column lane%32 of each 32-wide tile
+  float* out = a.part + static_cast<int64_t>(blockIdx.y) * a.cout * a.nc;
+  const int hi = lane >> 5, l32 = lane & 31;
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int col = n0 + wn * 64 + 32 * j + l32;
+    if (col >= a.nc) continue;
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      const int row = m0 + wm * 32 + 8 * (x >> 2) + 4 * hi + (x & 3);
+      if (row < a.cout) out[static_cast<int64_t>(row) * a.nc + col] = acc[j][x];
+    }
+  }
+}
+
+// dw[co][ci][kh][kw] = round(sum over splits, in order, of part[s][co][(kh*KW + kw)*cin_pad + ci]), ci < cin.
+template <typename T>
+__global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* __restrict__ part, typename Io<T>::storage* __restrict__ dw,
+                                                           int32_t splits, int32_t cout, int32_t cin, int32_t cin_pad,
+                                                           int32_t kh, int32_t kw, int64_t nc, int64_t total) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= total) return;
+  const int32_t b = static_cast<int32_t>(i % kw);
+  int64_t r = i / kw;
+  const int32_t a = static_cast<int32_t>(r % kh);
+  r /= kh;
+  const int32_t ci = static_cast<int32_t>(r % cin);
+  const int32_t co = static_cast<int32_t>(r / cin);
+  const int64_t col = static_cast<int64_t>(co) * nc + (static_cast<int64_t>(a) * kw + b) * cin_pad + ci;
+  const int64_t stride = static_cast<int64_t>(cout) * nc;
+  float s = 0.0f;
+  for (int32_t k = 0; k < splits; ++k) s += part[k * stride + col];
+  dw[i] = Io<T>::store(s);
+}
+
+template <typename T>
+fh_status run_wgrad(const WgradArgs& args, int32_t splits, int32_t cin_real, int32_t kh, void* dw, hipStream_t s) {
+  const int tiles = ((args.cout + kWM - 1) / kWM) * args.tiles_n;
+  hipLaunchKernelGGL((conv_wgrad_kernel<T>), dim3(static_cast<uint32_t>(tiles), static_cast<uint32_t>(splits)),
+                     dim3(kWThreads), 0, s, args);
+  if (fh_status st = launch_status("conv_wgrad_kernel"); st != FH_OK) return st;
+  const int64_t total = static_cast<int64_t>(args.cout) * cin_real * kh * args.kw;
+  hipLaunchKernelGGL((wgrad_reduce_kernel<T>), dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256), 0, s,
+                     args.part, static_cast<typename Io<T>::storage*>(dw), splits, args.cout, cin_real, args.cin, kh,
+                     args.kw, static_cast<int64_t>(args.nc), total);
+  return launch_status("wgrad_reduce_kernel");
+}
+
+}  // namespace
+}  // namespace fh
+
+using namespace fh;
+
+extern "C" int64_t fh_conv2d_wgrad_workspace(int32_t dtype, const int64_t geom[12], int32_t cin_pad, int32_t* splits) {
+  if (dtype != FH_BF16 && dtype != FH_F16) return -1;
+  if (geom == nullptr || geom[11] != 1 || cin_pad % 8 != 0 || cin_pad < geom[1] || geom[4] % 8 != 0) return -1;
+  const int64_t oh = (geom[2] + 2 * geom[9] - geom[5]) / geom[7] + 1, ow = (geom[3] + 2 * geom[10] - geom[6]) / geom[8] + 1;
+  const int64_t p = geom[0] * oh * ow, nc = geom[5] * geom[6] * cin_pad;
+  if (p <= 0 || nc <= 0 || p > (int64_t{1} << 40) || nc > (1 << 30)) return -1;
+  const int64_t tiles = ((geom[4] + kWM - 1) / kWM) * ((nc + kWN - 1) / kWN);
+  // enough workgroups to fill the device twice over, each at least 512 p-rows, the workspace within 256 MiB
+  int64_t sp = (2 * 256 + tiles - 1) / tiles;
+  sp = std::min<int64_t>(sp, std::max<int64_t>(1, p / 512));
+  sp = std::min<int64_t>(sp, std::max<int64_t>(1, (int64_t{256} << 20) / (4 * geom[4] * nc)));
+  sp = std::max<int64_t>(1, std::min<int64_t>(sp, 65535));
+  if (splits != nullptr) *splits = static_cast<int32_t>(sp);
+  return sp * geom[4] * nc * 4;
+}
+
+extern "C" fh_status fh_conv2d_wgrad_nhwc(int32_t dtype, const void* x, const void* dy, void* dw, void* workspace,
+                                          int64_t workspace_bytes, const int64_t geom[12], int32_t cin_pad, void* stream) {
+  int32_t splits = 0;
+  const int64_t need = fh_conv2d_wgrad_workspace(dtype, geom, cin_pad, &splits);
+  if (need < 0) return fail(FH_UNIMPLEMENTED, "fh_conv2d_wgrad_nhwc: unsupported dtype or geometry");
+  if (workspace_bytes < need) return fail(FH_INVALID_ARGUMENT, "fh_conv2d_wgrad_nhwc: workspace too small");
+  for (int k = 0; k < 12; ++k)
+    if (geom[k] < 0 || geom[k] > 0x7fffffffLL) return fail(FH_INVALID_ARGUMENT, "fh_conv2d_wgrad_nhwc: geometry out of range");
+  if (x == nullptr || dy == nullptr || dw == nullptr || workspace == nullptr)
+    return fail(FH_INVALID_ARGUMENT, "fh_conv2d_wgrad_nhwc: null pointer");
+  WgradArgs a{};
+  a.x = x, a.dy = dy, a.part = static_cast<float*>(workspace);
+  a.h = static_cast<int32_t>(geom[2]), a.w = static_cast<int32_t>(geom[3]), a.cin = cin_pad;
+  a.cout = static_cast<int32_t>(geom[4]), a.kw = static_cast<int32_t>(geom[6]);
+  a.sh = static_cast<int32_t>(geom[7]), a.sw = static_cast<int32_t>(geom[8]);
+  a.ph = static_cast<int32_t>(geom[9]), a.pw = static_cast<int32_t>(geom[10]);
+  a.oh = static_cast<int32_t>((geom[2] + 2 * geom[9] - geom[5]) / geom[7] + 1);
+  a.ow = static_cast<int32_t>((geom[3] + 2 * geom[10] - geom[6]) / geom[8] + 1);
+  a.nc = static_cast<int32_t>(geom[5] * geom[6] * cin_pad);
+  a.tiles_n = (a.nc + kWN - 1) / kWN;
+  a.p = geom[0] * a.oh * a.ow;
+  a.rows_per_split = ((a.p + splits - 1) / splits + kWK - 1) / kWK * kWK;
+  if (!(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(dy) % 16 == 0))
+    return fail(FH_INVALID_ARGUMENT, "fh_conv2d_wgrad_nhwc: operands must be 16-byte aligned");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == FH_BF16) return run_wgrad<bf16_t>(a, splits, static_cast<int32_t>(geom[1]), static_cast<int32_t>(geom[5]), dw, s);
+  return run_wgrad<f16_t>(a, splits, static_cast<int32_t>(geom[1]), static_cast<int32_t>(geom[5]), dw, s);
+}

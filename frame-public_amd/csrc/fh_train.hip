@@ -166,6 +166,43 @@ __global__ __launch_bounds__(kThreads) void conv_grad_filter_kernel(const typena
   dw[i] = Io<T>::store(acc);
 }
 
+// ---- operands of the transposed convolution (conv2d_grad_input on the implicit-GEMM conv) -----------------------
+
+// out[ci][a][b][co] = w[co][ci][KH-1-a][KW-1-b]: the filter of dx = conv(dy, w') in the conv kernel's channels-last
+// filter layout [Cout'][KH][KW][Cin'] with Cout' = Cin, Cin' = Cout.
+template <typename S>
+__global__ __launch_bounds__(kThreads) void filter_flip_kernel(const S* __restrict__ w, S* __restrict__ out, int32_t cout,
+                                                               int32_t cin, int32_t kh, int32_t kw, int64_t total) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= total) return;
+  const int32_t co = static_cast<int32_t>(i % cout);
+  int64_t r = i / cout;
+  const int32_t b = static_cast<int32_t>(r % kw);
+  r /= kw;
+  const int32_t a = static_cast<int32_t>(r % kh);
+  const int32_t ci = static_cast<int32_t>(r / kh);
+  out[i] = w[((static_cast<int64_t>(co) * cin + ci) * kh + (kh - 1 - a)) * kw + (kw - 1 - b)];
+}
+
+// NCHW x [N,C,H,W] -> channels-last [N,Hu,Wu,C] with x[n][c][h][w] at (h*sh, w*sw) and zeros elsewhere.
+template <typename S>
+__global__ __launch_bounds__(kThreads) void dilate_nhwc_kernel(const S* __restrict__ x, S* __restrict__ out, int32_t c,
+                                                               int32_t h, int32_t w, int32_t sh, int32_t sw, int32_t hu,
+                                                               int32_t wu, int64_t total) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= total) return;
+  const int32_t ch = static_cast<int32_t>(i % c);
+  int64_t r = i / c;
+  const int32_t xw = static_cast<int32_t>(r % wu);
+  r /= wu;
+  const int32_t yh = static_cast<int32_t>(r % hu);
+  const int64_t n = r / hu;
+  S v{};
+  if (yh % sh == 0 && xw % sw == 0 && yh / sh < h && xw / sw < w)
+    v = x[((n * c + ch) * h + yh / sh) * w + xw / sw];
+  out[i] = v;
+}
+
 // ---- sum / sum_grad_internal -------------------------------------------------------------------------------
 
 constexpr int kMaxDims = 8;
@@ -519,4 +556,51 @@ extern "C" fh_status fh_mse_loss_grad(int32_t dtype, const void* pred, const voi
     return fail(FH_INVALID_ARGUMENT, "fh_mse_loss_grad: null pointer");
   if (!grid_ok(blocks_for(numel))) return fail(FH_INVALID_ARGUMENT, "fh_mse_loss_grad: tensor too large");
   return dispatch<MseRun>(dtype, 1, pred, target, gy, out, numel, static_cast<hipStream_t>(stream));
+}
+
+extern "C" fh_status fh_conv_filter_flip(int32_t dtype, const void* w, void* out, int64_t cout, int64_t cin, int64_t kh,
+                                         int64_t kw, void* stream) {
+  if (!is_supported_float(dtype)) return fail(FH_UNIMPLEMENTED, "fh_conv_filter_flip: unsupported dtype");
+  if (cout < 0 || cin < 0 || kh < 0 || kw < 0 || cout > 0x7fffffffLL || cin > 0x7fffffffLL || kh > 0x7fffffffLL ||
+      kw > 0x7fffffffLL)
+    return fail(FH_INVALID_ARGUMENT, "fh_conv_filter_flip: invalid dims");
+  const int64_t total = cout * cin * kh * kw;
+  if (total == 0) return FH_OK;
+  if (w == nullptr || out == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_conv_filter_flip: null pointer");
+  if (!grid_ok(blocks_for(total))) return fail(FH_INVALID_ARGUMENT, "fh_conv_filter_flip: tensor too large");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<uint32_t>(blocks_for(total)));
+  const int32_t a = static_cast<int32_t>(cout), b = static_cast<int32_t>(cin), c = static_cast<int32_t>(kh),
+                d = static_cast<int32_t>(kw);
+  if (dtype == FH_F32)
+    hipLaunchKernelGGL((filter_flip_kernel<uint32_t>), grid, dim3(kThreads), 0, s, static_cast<const uint32_t*>(w),
+                       static_cast<uint32_t*>(out), a, b, c, d, total);
+  else
+    hipLaunchKernelGGL((filter_flip_kernel<uint16_t>), grid, dim3(kThreads), 0, s, static_cast<const uint16_t*>(w),
+                       static_cast<uint16_t*>(out), a, b, c, d, total);
+  return launch_status("fh_conv_filter_flip");
+}
+
+extern "C" fh_status fh_dilate_nhwc(int32_t dtype, const void* x, void* out, int64_t n, int64_t c, int64_t h, int64_t w,
+                                    int64_t sh, int64_t sw, int64_t hu, int64_t wu, void* stream) {
+  if (!is_supported_float(dtype)) return fail(FH_UNIMPLEMENTED, "fh_dilate_nhwc: unsupported dtype");
+  const int64_t dims[] = {n, c, h, w, sh, sw, hu, wu};
+  for (int64_t v : dims)
+    if (v < 0 || v > 0x7fffffffLL) return fail(FH_INVALID_ARGUMENT, "fh_dilate_nhwc: invalid dims");
+  if (sh == 0 || sw == 0) return fail(FH_INVALID_ARGUMENT, "fh_dilate_nhwc: zero stride");
+  const int64_t total = n * hu * wu * c;
+  if (total == 0) return FH_OK;
+  if (x == nullptr || out == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_dilate_nhwc: null pointer");
+  if (!grid_ok(blocks_for(total))) return fail(FH_INVALID_ARGUMENT, "fh_dilate_nhwc: tensor too large");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<uint32_t>(blocks_for(total)));
+  const int32_t args[] = {static_cast<int32_t>(c), static_cast<int32_t>(h), static_cast<int32_t>(w), static_cast<int32_t>(sh),
+                          static_cast<int32_t>(sw), static_cast<int32_t>(hu), static_cast<int32_t>(wu)};
+  if (dtype == FH_F32)
+    hipLaunchKernelGGL((dilate_nhwc_kernel<uint32_t>), grid, dim3(kThreads), 0, s, static_cast<const uint32_t*>(x),
+                       static_cast<uint32_t*>(out), args[0], args[1], args[2], args[3], args[4], args[5], args[6], total);
+  else
+    hipLaunchKernelGGL((dilate_nhwc_kernel<uint16_t>), grid, dim3(kThreads), 0, s, static_cast<const uint16_t*>(x),
+                       static_cast<uint16_t*>(out), args[0], args[1], args[2], args[3], args[4], args[5], args[6], total);
+  return launch_status("fh_dilate_nhwc");
 }

@@ -295,8 +295,10 @@ def conv_inputs(dtype, seed=101, n=32, cin=64, h=56, w=56, cout=64, k=3):
 
 # ---- C4: ResNet-18 --------------------------------------------------------------------------------------------
 
-def resnet18(batch=64, dtype=BF16, device="hip", image=224, classes=1000):
-    """Returns (graph, parameter specs [(shape, fan_in or None for bias)] in input order after x)."""
+def resnet18(batch=64, dtype=BF16, device="hip", image=224, classes=1000, train=False):
+    """Returns (graph, parameter specs [(shape, fan_in or None for bias)] in input order after x). With train=True
+    the graph takes one more input, the target [batch, classes], and outputs mse_loss(logits, target); the
+    parameters are then graph inputs 1..len(specs)."""
     g = Graph(device)
     specs = []
     x = g.input(dtype, (batch, 3, image, image))
@@ -326,7 +328,11 @@ def resnet18(batch=64, dtype=BF16, device="hip", image=224, classes=1000):
     h = g.reshape(h, (batch, h.shape[1]))
     w = param((h.shape[1], classes), h.shape[1])
     b = param((batch, classes), None)
-    g.output(g.add(g.matmul(h, w), b))
+    logits = g.add(g.matmul(h, w), b)
+    if train:
+        g.output(g.mse_loss(logits, g.input(dtype, (batch, classes))))
+    else:
+        g.output(logits)
     return g, specs
 
 

@@ -130,6 +130,15 @@ inline constexpr std::string_view kAvgPoolNhwcOp = "hip_avg_pool2d_nhwc_internal
 // Cin <= 8: x [N,C,H,W] -> [N,H,W,8] zero-padded; w [Cout,C,KH,KW] -> [Cout, K8] (see fh_conv_pack_*_c8).
 inline constexpr std::string_view kPackInputC8Op = "hip_pack_input_c8_internal";
 inline constexpr std::string_view kPackFilterC8Op = "hip_pack_filter_c8_internal";
+// conv2d_grad_input_internal as a stride-1 convolution on the implicit-GEMM kernel: the flipped channels-last
+// filter [Cin][KH][KW][Cout] (fh_conv_filter_flip) and dy zero-dilated by the stride into channels-last
+// [N,Hu,Wu,Cout] (fh_dilate_nhwc; attribute stride).
+inline constexpr std::string_view kFilterFlipOp = "hip_conv_filter_flip_internal";
+inline constexpr std::string_view kDilateNhwcOp = "hip_dilate_nhwc_internal";
+// conv2d_grad_filter_internal on MFMA: inputs x channels-last [N,H,W,cin_pad] and dy channels-last [N,Ho,Wo,Cout];
+// outputs dw [Cout,Cin,KH,KW] and an fp32 split-K workspace (see fh_conv2d_wgrad_nhwc); attrs stride, padding,
+// groups, filter_shape.
+inline constexpr std::string_view kConvWgradOp = "hip_conv2d_wgrad_nhwc_internal";
 // attention(q, k, v) [batch*seq, heads*dh] -> [batch*seq, heads*dh]: the per-(batch, head) slice / matmul / mul /
 // softmax / matmul / concat decomposition in one kernel (attrs batch, seq, heads, dh, scale; see fh_attention_fwd).
 inline constexpr std::string_view kAttentionOp = "hip_attention_internal";

@@ -154,6 +154,82 @@ ConvLowering plan_conv(const ir::Node* n) {
   return p;
 }
 
+// conv2d_grad_input_internal(dy, w) as dx = conv(dilate(dy, stride), flip(w)) with stride 1 and padding
+// KH-1-pad on the implicit-GEMM kernel: the transposed convolution. dy is dilated to Hu = (Ho-1)*s + 1 + r rows,
+// r = (H + 2 pad - KH) mod s (the rows the forward's floor dropped), so the output is exactly [N,Cin,H,W]. Only
+// groups == 1 and pad <= K-1, and geometries the kernel takes; others keep the direct kernel.
+struct GradInputLowering {
+  bool ok = false;
+  int64_t n = 0, cout = 0, cin = 0, hu = 0, wu = 0, kh = 0, kw = 0, sh = 1, sw = 1, ph = 0, pw = 0;
+};
+
+GradInputLowering plan_grad_input(const ir::Node* n) {
+  GradInputLowering g;
+  if (n->op() != "conv2d_grad_input_internal" || n->inputs().size() != 2) return g;
+  const ir::TensorType& dy = n->inputs()[0]->type();
+  const ir::TensorType& w = n->inputs()[1]->type();
+  auto get = [&](const char* k) -> const ir::AttrValue* {
+    auto it = n->attrs().find(k);
+    return it == n->attrs().end() ? nullptr : &it->second;
+  };
+  const auto* xs = get("input_shape") ? std::get_if<Shape>(get("input_shape")) : nullptr;
+  const auto* stride = get("stride") ? std::get_if<std::vector<int64_t>>(get("stride")) : nullptr;
+  const auto* pad = get("padding") ? std::get_if<std::vector<int64_t>>(get("padding")) : nullptr;
+  const auto* groups = get("groups") ? std::get_if<int64_t>(get("groups")) : nullptr;
+  const int32_t dt = dy.dtype.code() == DTypeCode::kBFloat16  ? FH_BF16
+                     : dy.dtype.code() == DTypeCode::kFloat16 ? FH_F16
+                     : dy.dtype.code() == DTypeCode::kFloat32 ? FH_F32
+                                                              : -1;
+  if (!xs || !stride || !pad || !groups || stride->size() != 2 || pad->size() != 2 || *groups != 1 || dt < 0 ||
+      xs->rank() != 4 || dy.shape.rank() != 4 || w.shape.rank() != 4)
+    return g;
+  g.n = xs->dim(0), g.cin = xs->dim(1), g.cout = w.shape.dim(0), g.kh = w.shape.dim(2), g.kw = w.shape.dim(3);
+  g.sh = (*stride)[0], g.sw = (*stride)[1], g.ph = (*pad)[0], g.pw = (*pad)[1];
+  if (g.sh < 1 || g.sw < 1 || g.ph > g.kh - 1 || g.pw > g.kw - 1) return g;
+  const int64_t eh = xs->dim(2) + 2 * g.ph - g.kh, ew = xs->dim(3) + 2 * g.pw - g.kw;
+  if (eh < 0 || ew < 0) return g;
+  g.hu = (dy.shape.dim(2) - 1) * g.sh + 1 + eh % g.sh;
+  g.wu = (dy.shape.dim(3) - 1) * g.sw + 1 + ew % g.sw;
+  const int64_t geom[12] = {g.n, g.cout, g.hu, g.wu, g.cin, g.kh, g.kw, 1, 1, g.kh - 1 - g.ph, g.kw - 1 - g.pw, 1};
+  // the transposed conv's input channels are the forward's Cout: the plain (not C8) channels-last layout only
+  g.ok = g.cout % (dt == FH_F32 ? 16 : 32) == 0 && fh_conv2d_nhwc_supported(dt, geom) == 1;
+  return g;
+}
+
+// conv2d_grad_filter_internal(x, dy) on the MFMA filter-gradient kernel: x channels-last (the C8 pack when
+// Cin <= 8), dy channels-last, plus the kernel's split-K workspace as a second, planned output.
+struct GradFilterLowering {
+  bool ok = false, c8 = false;
+  int64_t workspace = 0;
+};
+
+GradFilterLowering plan_grad_filter(const ir::Node* n) {
+  GradFilterLowering g;
+  if (n->op() != "conv2d_grad_filter_internal" || n->inputs().size() != 2) return g;
+  const ir::TensorType& x = n->inputs()[0]->type();
+  const ir::TensorType& dy = n->inputs()[1]->type();
+  auto get = [&](const char* k) -> const ir::AttrValue* {
+    auto it = n->attrs().find(k);
+    return it == n->attrs().end() ? nullptr : &it->second;
+  };
+  const auto* ws = get("filter_shape") ? std::get_if<Shape>(get("filter_shape")) : nullptr;
+  const auto* stride = get("stride") ? std::get_if<std::vector<int64_t>>(get("stride")) : nullptr;
+  const auto* pad = get("padding") ? std::get_if<std::vector<int64_t>>(get("padding")) : nullptr;
+  const auto* groups = get("groups") ? std::get_if<int64_t>(get("groups")) : nullptr;
+  const int32_t dt = x.dtype.code() == DTypeCode::kBFloat16 ? FH_BF16 : x.dtype.code() == DTypeCode::kFloat16 ? FH_F16 : -1;
+  if (!ws || !stride || !pad || !groups || stride->size() != 2 || pad->size() != 2 || dt < 0 || x.shape.rank() != 4 ||
+      dy.shape.rank() != 4 || ws->rank() != 4)
+    return g;
+  const int64_t geom[12] = {x.shape.dim(0), x.shape.dim(1), x.shape.dim(2), x.shape.dim(3), ws->dim(0), ws->dim(2),
+                            ws->dim(3),     (*stride)[0],   (*stride)[1],   (*pad)[0],      (*pad)[1],  *groups};
+  g.c8 = x.shape.dim(1) <= 8;
+  const int64_t cin_pad = g.c8 ? 8 : x.shape.dim(1);
+  if (!g.c8 && cin_pad % 8 != 0) return g;
+  g.workspace = fh_conv2d_wgrad_workspace(dt, geom, static_cast<int32_t>(cin_pad), nullptr);
+  g.ok = g.workspace > 0;
+  return g;
+}
+
 // Channels-last activations between convolutions. Values that must share a layout form groups (union-find):
 // an elementwise node's rank-4 operands and result, a pool's input and output, a lowered conv's result and its
 // epilogue operands. A group is kept channels-last ([N,H,W,C] in the lowered graph) when every member is produced
@@ -316,6 +392,58 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
     if (n->op() == ir::kGraphInputOp) continue;
     std::vector<ir::Value*> ins;
     for (const ir::Value* in : n->inputs()) ins.push_back(map.at(in));
+    if (const GradInputLowering gi = plan_grad_input(n); gi.ok) {
+      ir::TensorType wt = ins[1]->type(), dt = ins[0]->type();
+      wt.shape = Shape({gi.cin, gi.kh, gi.kw, gi.cout});
+      Result<ir::Node*> flip = out.create_node(std::string(kFilterFlipOp), {ins[1]}, {wt});
+      if (!flip.is_ok()) return flip.status();
+      ir::Value* dy_cl = nullptr;
+      if (gi.sh == 1 && gi.sw == 1) {
+        Result<ir::Value*> v = channels_last(ins[0]);
+        if (!v.is_ok()) return v.status();
+        dy_cl = v.value();
+      } else {
+        dt.shape = Shape({gi.n, gi.hu, gi.wu, gi.cout});
+        Result<ir::Node*> d = out.create_node(std::string(kDilateNhwcOp), {ins[0]}, {dt});
+        if (!d.is_ok()) return d.status();
+        d.value()->set_attr("stride", ir::AttrValue{std::vector<int64_t>{gi.sh, gi.sw}});
+        dy_cl = d.value()->output(0);
+      }
+      Result<ir::Node*> c = out.create_node(std::string(kConvNhwcOp), {dy_cl, flip.value()->output(0)}, {n->outputs()[0].type()});
+      if (!c.is_ok()) return c.status();
+      c.value()->set_attr("stride", ir::AttrValue{std::vector<int64_t>{1, 1}});
+      c.value()->set_attr("padding", ir::AttrValue{std::vector<int64_t>{gi.kh - 1 - gi.ph, gi.kw - 1 - gi.pw}});
+      c.value()->set_attr("groups", ir::AttrValue{int64_t{1}});
+      c.value()->set_attr("n_main_inputs", ir::AttrValue{int64_t{2}});
+      c.value()->set_attr("filter_hw", ir::AttrValue{std::vector<int64_t>{gi.kh, gi.kw}});
+      map[&n->outputs()[0]] = c.value()->output(0);
+      continue;
+    }
+    if (const GradFilterLowering gf = plan_grad_filter(n); gf.ok) {
+      ir::Value* x_cl = nullptr;
+      if (gf.c8) {
+        ir::TensorType tx = ins[0]->type();
+        const Shape& xs = tx.shape;
+        tx.shape = Shape({xs.dim(0), xs.dim(2), xs.dim(3), 8});
+        Result<ir::Node*> px = out.create_node(std::string(kPackInputC8Op), {ins[0]}, {tx});
+        if (!px.is_ok()) return px.status();
+        x_cl = px.value()->output(0);
+      } else {
+        Result<ir::Value*> v = channels_last(ins[0]);
+        if (!v.is_ok()) return v.status();
+        x_cl = v.value();
+      }
+      Result<ir::Value*> dy_cl = channels_last(ins[1]);
+      if (!dy_cl.is_ok()) return dy_cl.status();
+      ir::TensorType wst = n->outputs()[0].type();
+      wst.dtype = DType::of<float>();
+      wst.shape = Shape({gf.workspace / 4});
+      Result<ir::Node*> c = out.create_node(std::string(kConvWgradOp), {x_cl, dy_cl.value()}, {n->outputs()[0].type(), wst});
+      if (!c.is_ok()) return c.status();
+      for (const auto& [k, v] : n->attrs()) c.value()->set_attr(k, v);
+      map[&n->outputs()[0]] = c.value()->output(0);
+      continue;
+    }
     const ConvLowering p = plan_conv(n);
     if (p.ok) {
       const int64_t* geom = p.geom;

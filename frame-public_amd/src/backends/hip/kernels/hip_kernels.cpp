@@ -222,6 +222,8 @@ Status conv_nhwc_kernel(KernelContext& ctx) {
                             (*stride)[1],     (*pad)[0],        (*pad)[1],        *groups};
   if (c8 ? w.shape().dim(1) != fh_conv_c8_filter_k(kh, kw) : w.shape().dim(3) != geom[1])
     return invalid(op, "filter shape does not match the input's channels");
+  // 16-bit with 8 input channels is the C8 kernel, which reads the packed [Cout, K8] filter only
+  if (!c8 && geom[1] == 8 && dt.value() != FH_F32) return invalid(op, "an 8-channel 16-bit input needs the packed C8 filter");
   const int64_t oh = (geom[2] + 2 * geom[9] - geom[5]) / geom[7] + 1;
   const int64_t ow = (geom[3] + 2 * geom[10] - geom[6]) / geom[8] + 1;
   // out_nhwc: y (and the epilogue operands) channels-last [N,Ho,Wo,Cout], else NCHW
@@ -494,6 +496,68 @@ Status conv_grad_kernel(KernelContext& ctx) {
   return Status::ok();
 }
 
+// conv2d_grad_filter on MFMA over channels-last operands (kConvWgradOp); output 1 is the split-K workspace.
+Status conv_wgrad_kernel(KernelContext& ctx) {
+  const std::string op(kConvWgradOp);
+  if (ctx.inputs.size() != 2 || ctx.outputs.size() != 2) return invalid(op, "expects 2 inputs and 2 outputs");
+  const Shape* ws = attr<Shape>(ctx, "filter_shape");
+  const auto* s = attr<std::vector<int64_t>>(ctx, "stride");
+  const auto* p = attr<std::vector<int64_t>>(ctx, "padding");
+  const auto* grp = attr<int64_t>(ctx, "groups");
+  if (!ws || !s || !p || !grp || s->size() != 2 || p->size() != 2 || ws->rank() != 4) return invalid(op, "missing attributes");
+  const Shape& x = ctx.inputs[0].shape();   // [N,H,W,cin_pad]
+  const Shape& dy = ctx.inputs[1].shape();  // [N,Ho,Wo,Cout]
+  if (x.rank() != 4 || dy.rank() != 4 || ctx.outputs[0].shape() != *ws) return invalid(op, "operand shapes");
+  if (!(ctx.inputs[0].dtype() == ctx.outputs[0].dtype()) || !(ctx.inputs[1].dtype() == ctx.outputs[0].dtype()))
+    return invalid(op, "operand dtypes differ");
+  const int64_t geom[12] = {x.dim(0), ws->dim(1), x.dim(1), x.dim(2), ws->dim(0), ws->dim(2), ws->dim(3), (*s)[0], (*s)[1], (*p)[0], (*p)[1], *grp};
+  const int64_t oh = (geom[2] + 2 * geom[9] - geom[5]) / geom[7] + 1, ow = (geom[3] + 2 * geom[10] - geom[6]) / geom[8] + 1;
+  if (dy != Shape({geom[0], oh, ow, geom[4]}) || x.dim(3) < ws->dim(1)) return invalid(op, "dy / x shapes do not match the geometry");
+  Result<int32_t> dt = float_code(op, ctx.outputs[0].dtype());
+  if (!dt.is_ok()) return dt.status();
+  const int64_t bytes = ctx.outputs[1].numel() * 4;
+  FRAME_HIP_RETURN_IF_ERROR(fh_conv2d_wgrad_nhwc(dt.value(), ctx.inputs[0].raw_data(), ctx.inputs[1].raw_data(),
+                                                 ctx.outputs[0].raw_data(), ctx.outputs[1].raw_data(), bytes, geom,
+                                                 static_cast<int32_t>(x.dim(3)), stream_handle(ctx)),
+                            "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
+// Operands of the lowered conv2d_grad_input (see kFilterFlipOp / kDilateNhwcOp).
+Status filter_flip_kernel(KernelContext& ctx) {
+  const std::string op(kFilterFlipOp);
+  FRAME_RETURN_IF_ERROR(arity(ctx, op, 1, 1));
+  FRAME_RETURN_IF_ERROR(same_dtype(ctx, op));
+  const Shape& w = ctx.inputs[0].shape();
+  if (w.rank() != 4 || ctx.outputs[0].shape() != Shape({w.dim(1), w.dim(2), w.dim(3), w.dim(0)}))
+    return invalid(op, "expects w [Cout,Cin,KH,KW] -> [Cin,KH,KW,Cout]");
+  Result<int32_t> dt = float_code(op, ctx.outputs[0].dtype());
+  if (!dt.is_ok()) return dt.status();
+  FRAME_HIP_RETURN_IF_ERROR(fh_conv_filter_flip(dt.value(), ctx.inputs[0].raw_data(), ctx.outputs[0].raw_data(), w.dim(0),
+                                                w.dim(1), w.dim(2), w.dim(3), stream_handle(ctx)),
+                            "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
+Status dilate_nhwc_kernel(KernelContext& ctx) {
+  const std::string op(kDilateNhwcOp);
+  FRAME_RETURN_IF_ERROR(arity(ctx, op, 1, 1));
+  FRAME_RETURN_IF_ERROR(same_dtype(ctx, op));
+  const auto* s = attr<std::vector<int64_t>>(ctx, "stride");
+  const Shape& x = ctx.inputs[0].shape();
+  const Shape& y = ctx.outputs[0].shape();
+  if (s == nullptr || s->size() != 2 || (*s)[0] < 1 || (*s)[1] < 1) return invalid(op, "missing or malformed stride");
+  if (x.rank() != 4 || y.rank() != 4 || y.dim(0) != x.dim(0) || y.dim(3) != x.dim(1) || y.dim(1) < (x.dim(2) - 1) * (*s)[0] + 1 ||
+      y.dim(2) < (x.dim(3) - 1) * (*s)[1] + 1)
+    return invalid(op, "output shape does not match the dilated input");
+  Result<int32_t> dt = float_code(op, ctx.outputs[0].dtype());
+  if (!dt.is_ok()) return dt.status();
+  FRAME_HIP_RETURN_IF_ERROR(fh_dilate_nhwc(dt.value(), ctx.inputs[0].raw_data(), ctx.outputs[0].raw_data(), x.dim(0), x.dim(1),
+                                           x.dim(2), x.dim(3), (*s)[0], (*s)[1], y.dim(1), y.dim(2), stream_handle(ctx)),
+                            "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
 // sum (x; axes[, keepdims]) and sum_grad_internal (gy; input_shape, axes): both index x's dims with a reduced mask.
 template <int Grad>
 Status sum_kernel(KernelContext& ctx) {
@@ -717,6 +781,9 @@ FRAME_REGISTER_KERNEL("max_pool2d_grad_internal", kHipBackendName, &pool_grad_ke
 FRAME_REGISTER_KERNEL("avg_pool2d_grad_internal", kHipBackendName, &pool_grad_kernel<1>);
 FRAME_REGISTER_KERNEL("conv2d_grad_input_internal", kHipBackendName, &conv_grad_kernel<0>);
 FRAME_REGISTER_KERNEL("conv2d_grad_filter_internal", kHipBackendName, &conv_grad_kernel<1>);
+FRAME_REGISTER_KERNEL(kFilterFlipOp, kHipBackendName, &filter_flip_kernel);
+FRAME_REGISTER_KERNEL(kConvWgradOp, kHipBackendName, &conv_wgrad_kernel);
+FRAME_REGISTER_KERNEL(kDilateNhwcOp, kHipBackendName, &dilate_nhwc_kernel);
 FRAME_REGISTER_KERNEL("sum", kHipBackendName, &sum_kernel<0>);
 FRAME_REGISTER_KERNEL("sum_grad_internal", kHipBackendName, &sum_kernel<1>);
 FRAME_REGISTER_KERNEL("mse_loss", kHipBackendName, &mse_kernel<0>);

@@ -264,6 +264,27 @@ fh_status fh_conv2d_grad_input(int32_t dtype, const void* dy, const void* w, voi
 fh_status fh_conv2d_grad_filter(int32_t dtype, const void* x, const void* dy, void* dw, const int64_t geom[12],
                                 void* stream);
 
+/* conv2d_grad_filter_internal on MFMA (bf16 / f16, groups 1): x channels-last [N,H,W,cin_pad] (cin_pad % 8 == 0,
+ * channels past geom's Cin zero, e.g. the C8 pack of a 3-channel stem), dy channels-last [N,Ho,Wo,Cout]
+ * (Cout % 8 == 0), dw [Cout][Cin][KH][KW] as the reference lays it out. geom as fh_conv2d_fwd. The long
+ * contraction (N*Ho*Wo) is split across workgroups into fp32 partials in `workspace`, summed in split order;
+ * fh_conv2d_wgrad_workspace returns the bytes needed (and the split count), or -1 where this path does not
+ * apply (then fh_conv2d_grad_filter). Replaces cudnnConvolutionBackwardFilter
+ * (reference: src/backends/cuda/kernels/conv.cpp:700-789). */
+int64_t fh_conv2d_wgrad_workspace(int32_t dtype, const int64_t geom[12], int32_t cin_pad, int32_t* splits);
+fh_status fh_conv2d_wgrad_nhwc(int32_t dtype, const void* x, const void* dy, void* dw, void* workspace,
+                               int64_t workspace_bytes, const int64_t geom[12], int32_t cin_pad, void* stream);
+
+/* Operands of conv2d_grad_input as a stride-1 convolution on the implicit-GEMM kernel (dx = conv(dilate(dy),
+ * flip(w)), padding KH-1-pad): fh_conv_filter_flip writes out[ci][a][b][co] = w[co][ci][KH-1-a][KW-1-b] (the
+ * channels-last filter [Cin][KH][KW][Cout] of that convolution); fh_dilate_nhwc writes the channels-last
+ * [N,Hu,Wu,C] tensor holding x[n][c][h][w] (NCHW) at (h*sh, w*sw) and zeros elsewhere. No counterpart in the
+ * reference (cudnnConvolutionBackwardData does this inside the library). */
+fh_status fh_conv_filter_flip(int32_t dtype, const void* w, void* out, int64_t cout, int64_t cin, int64_t kh, int64_t kw,
+                              void* stream);
+fh_status fh_dilate_nhwc(int32_t dtype, const void* x, void* out, int64_t n, int64_t c, int64_t h, int64_t w, int64_t sh,
+                         int64_t sw, int64_t hu, int64_t wu, void* stream);
+
 /* sum over the axes flagged in reduced[0..rank) (rank <= 8; every axis for the reference's axes = []), output dense
  * with the reduced axes dropped (keepdims only adds size-1 dims, same layout). fp32 tree per output.
  * Replaces sum_cuda_kernel (reference: src/backends/cuda/kernels/reduction.cu:322-460). */

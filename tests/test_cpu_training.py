@@ -267,3 +267,24 @@ def test_mlp_backward_matches_finite_differences():
             minus[pi][idx] -= eps
             fd = (float(run(fwd, plus)[0]) - float(run(fwd, minus)[0])) / (2 * eps)
             assert abs(fd - float(g[idx])) <= 2e-3 * max(1.0, abs(fd)), (pi, idx, fd, float(g[idx]))
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16])
+def test_grad_input_lowering(dtype):
+    """conv2d_grad_input_internal becomes flip(w) + channels-last dy (dilated by the stride) + a stride-1 NHWC conv
+    with padding K-1-pad where the implicit-GEMM kernel takes the geometry; groups > 1 keeps the direct kernel."""
+    def lowered(xs, ws, s, p, groups=1):
+        oh, ow = (xs[2] + 2 * p - ws[2]) // s + 1, (xs[3] + 2 * p - ws[3]) // s + 1
+        g = graphs.Graph("hip")
+        a, b = g.input(dtype, (xs[0], ws[0], oh, ow)), g.input(dtype, ws)
+        g.output(g.op("conv2d_grad_input_internal", [a, b], xs,
+                      {"input_shape": graphs.Shape(xs), "stride": [s, s], "padding": [p, p], "groups": groups}))
+        return host.hip_lowered(g.text())
+    t = lowered((8, 64, 56, 56), (128, 64, 3, 3), 2, 1)
+    assert "hip_dilate_nhwc_internal(%0) {stride=[2, 2]}" in t and "bfloat16[8,56,56,128]" in t.replace("float32", "bfloat16")
+    assert "padding=[1, 1], stride=[1, 1]" in t and "hip_conv_filter_flip_internal" in t
+    t = lowered((8, 64, 56, 56), (64, 64, 3, 3), 1, 1)
+    assert "hip_channels_last_internal(%0)" in t and "hip_dilate_nhwc_internal" not in t
+    t = lowered((8, 64, 57, 57), (128, 64, 1, 1), 2, 0)  # odd size: one trailing zero row/column in the dilation
+    assert "[8,57,57,128]" in t
+    assert "conv2d_grad_input_internal" in lowered((8, 64, 56, 56), (64, 32, 3, 3), 1, 1, groups=2)
