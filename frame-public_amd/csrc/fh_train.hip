@@ -92,6 +92,65 @@ __global__ __launch_bounds__(kThreads) void pool2d_grad_kernel(const typename Io
   }
 }
 
+// max_pool2d_grad for the 3x3 / stride 2 / padding 1 window (the ResNet stem pool): one thread per 2x2 input block
+// (rows 2i, 2i+1, columns 2j, 2j+1), whose covering windows are exactly (oh, ow) in {i, i+1} x {j, j+1}. Each of
+// the four windows' argmax is found once (first strict maximum in (kh, kw) order, as the forward) and every input of
+// the block adds the dy of the windows that chose it in (oh, ow) order: the same sums as the generic kernel.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void maxpool3s2_grad_kernel(const typename Io<T>::storage* __restrict__ dy,
+                                                                   const typename Io<T>::storage* __restrict__ x,
+                                                                   typename Io<T>::storage* __restrict__ dx, int32_t h,
+                                                                   int32_t w, int32_t oh, int32_t ow, int32_t bh,
+                                                                   int32_t bw, int64_t total) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (t >= total) return;
+  const int32_t bj = static_cast<int32_t>(t % bw);
+  const int64_t r = t / bw;
+  const int32_t bi = static_cast<int32_t>(r % bh);
+  const int64_t nc = r / bh;
+  const auto* xp = x + nc * h * w;
+  const auto* dyp = dy + nc * oh * ow;
+  int32_t arg[4];
+  float g[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int32_t wh = bi + (k >> 1), ww = bj + (k & 1);
+    arg[k] = -1;
+    g[k] = 0.0f;
+    if (wh >= oh || ww >= ow) continue;
+    bool found = false;
+    float best = 0.0f;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      const int32_t hh = 2 * wh - 1 + a;
+      if (hh < 0 || hh >= h) continue;
+#pragma unroll
+      for (int b = 0; b < 3; ++b) {
+        const int32_t cc = 2 * ww - 1 + b;
+        if (cc < 0 || cc >= w) continue;
+        const float v = Io<T>::load(xp[hh * w + cc]);
+        if (!found || v > best) {
+          found = true;
+          best = v;
+          arg[k] = hh * w + cc;
+        }
+      }
+    }
+    g[k] = Io<T>::load(dyp[wh * ow + ww]);
+  }
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    const int32_t ih = 2 * bi + (d >> 1), iw = 2 * bj + (d & 1);
+    if (ih >= h || iw >= w) continue;
+    const int32_t at = ih * w + iw;
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (arg[k] == at) acc += g[k];
+    dx[nc * h * w + at] = Io<T>::store(acc);
+  }
+}
+
 // ---- conv gradients (direct, reference order) ----------------------------------------------------------------
 
 struct ConvG {
@@ -228,16 +287,40 @@ __device__ inline int64_t decompose(int64_t idx, int32_t nd, const int64_t* dim,
 
 constexpr int kSumThreads = 512;
 
-// One workgroup per output: fp32 partial sums strided over the reduced elements, then a fixed-shape tree.
+// One workgroup per output: fp32 partial sums strided over the reduced elements, then a fixed-shape tree. The
+// reduced set is walked as (outer reduced coordinates) x (innermost reduced run): when that run is contiguous in x
+// (the bias gradient's H*W planes, a row sum) each lane reads 16-byte vectors of it, and the outer coordinates are
+// decoded once per run instead of once per element.
 template <typename T>
 __global__ __launch_bounds__(kSumThreads) void sum_kernel(const typename Io<T>::storage* __restrict__ x,
                                                           typename Io<T>::storage* __restrict__ out, ReduceG g) {
+  using S = typename Io<T>::storage;
+  constexpr int V = 16 / sizeof(S);
   __shared__ float part[kSumThreads / 64];
   const int64_t o = blockIdx.x;
   const int64_t base = decompose(o, g.nk, g.kdim, g.kstride);
   float acc = 0.0f;
-  if (g.nr == 1 && g.rstride[0] == 1) {
-    for (int64_t r = threadIdx.x; r < g.nred; r += kSumThreads) acc += Io<T>::load(x[base + r]);
+  const bool inner_run = g.nr >= 1 && g.rstride[g.nr - 1] == 1;
+  if (inner_run) {
+    const int64_t len = g.rdim[g.nr - 1];
+    const int64_t outer = len > 0 ? g.nred / len : 0;
+    const bool vec = len % V == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0 && (base % V) == 0;
+    for (int64_t q = 0; q < outer; ++q) {
+      const int64_t off = base + (g.nr > 1 ? decompose(q, g.nr - 1, g.rdim, g.rstride) : 0);
+      if (vec && off % V == 0) {
+        const uint4* row = reinterpret_cast<const uint4*>(x + off);
+        for (int64_t v = threadIdx.x; v < len / V; v += kSumThreads) {
+          const uint4 w = row[v];
+          const S* e = reinterpret_cast<const S*>(&w);
+#pragma unroll
+          for (int k = 0; k < V; ++k) acc += Io<T>::load(e[k]);
+        }
+      } else {
+        for (int64_t r = threadIdx.x; r < len; r += kSumThreads) acc += Io<T>::load(x[off + r]);
+      }
+    }
+  } else if (g.nr == 1) {
+    for (int64_t r = threadIdx.x; r < g.nred; r += kSumThreads) acc += Io<T>::load(x[base + r * g.rstride[0]]);
   } else {
     for (int64_t r = threadIdx.x; r < g.nred; r += kSumThreads)
       acc += Io<T>::load(x[base + decompose(r, g.nr, g.rdim, g.rstride)]);
@@ -321,7 +404,13 @@ struct PoolGradRun {
                        hipStream_t s) {
     using S = typename Io<T>::storage;
     const dim3 grid(static_cast<uint32_t>(blocks_for(total)));
-    if (mode == 0)
+    if (mode == 0 && g.kh == 3 && g.kw == 3 && g.sh == 2 && g.sw == 2 && g.ph == 1 && g.pw == 1) {
+      const int32_t bh = (g.h + 1) / 2, bw = (g.w + 1) / 2;
+      const int64_t blocks = static_cast<int64_t>(g.n) * g.c * bh * bw;
+      hipLaunchKernelGGL((maxpool3s2_grad_kernel<T>), dim3(static_cast<uint32_t>(blocks_for(blocks))), dim3(kThreads), 0, s,
+                         static_cast<const S*>(dy), static_cast<const S*>(x), static_cast<S*>(dx), g.h, g.w, g.oh, g.ow,
+                         bh, bw, blocks);
+    } else if (mode == 0)
       hipLaunchKernelGGL((pool2d_grad_kernel<T, 0>), grid, dim3(kThreads), 0, s, static_cast<const S*>(dy),
                          static_cast<const S*>(x), static_cast<S*>(dx), g, total);
     else

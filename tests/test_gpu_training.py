@@ -180,7 +180,8 @@ def test_pool_grads(dev, dtype, case):
 # ---- sum, sum_grad, mse_loss -----------------------------------------------------------------------------------
 
 SUM_CASES = [((4, 6, 5, 7), [0, 2, 3], False), ((4, 6, 5, 7), [], False), ((33, 1000), [1], True),
-             ((33, 1000), [0], False), ((8, 3, 300), [0, 2], False), ((1 << 20,), [], False)]
+             ((33, 1000), [0], False), ((8, 3, 300), [0, 2], False), ((1 << 20,), [], False),
+             ((8, 64, 28, 28), [0, 2, 3], False), ((3, 5, 9, 9), [0, 2, 3], True)]
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
