@@ -151,6 +151,90 @@ __global__ __launch_bounds__(kThreads) void maxpool3s2_grad_kernel(const typenam
   }
 }
 
+// The same gradient on 2 x 8 input blocks when W % 8 == 0: the ten covering windows (oh in {i, i+1}, ow in
+// 4j .. 4j+4) are evaluated from one register tile of the 5 x 11 inputs they span (16-byte loads for the middle
+// eight columns), and the block is written with two 16-byte stores.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void maxpool3s2_grad8_kernel(const typename Io<T>::storage* __restrict__ dy,
+                                                                    const typename Io<T>::storage* __restrict__ x,
+                                                                    typename Io<T>::storage* __restrict__ dx, int32_t h,
+                                                                    int32_t w, int32_t oh, int32_t ow, int32_t bh,
+                                                                    int32_t bw, int64_t total) {
+  using S = typename Io<T>::storage;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (t >= total) return;
+  const int32_t bj = static_cast<int32_t>(t % bw);
+  const int64_t r0 = t / bw;
+  const int32_t bi = static_cast<int32_t>(r0 % bh);
+  const int64_t nc = r0 / bh;
+  const S* xp = x + nc * h * w;
+  const S* dyp = dy + nc * oh * ow;
+  const int32_t row0 = 2 * bi - 1, col0 = 8 * bj - 1;  // local (0, 0)
+  float v[5][11];
+  bool rv[5], cv[11];
+#pragma unroll
+  for (int c = 0; c < 11; ++c) cv[c] = col0 + c >= 0 && col0 + c < w;
+#pragma unroll
+  for (int r = 0; r < 5; ++r) {
+    const int32_t gr = row0 + r;
+    rv[r] = gr >= 0 && gr < h;
+#pragma unroll
+    for (int c = 0; c < 11; ++c) v[r][c] = 0.0f;
+    if (!rv[r]) continue;
+    const S* rowp = xp + static_cast<int64_t>(gr) * w;
+    const uint4 mid = *reinterpret_cast<const uint4*>(rowp + 8 * bj);
+    const S* m = reinterpret_cast<const S*>(&mid);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) v[r][c + 1] = Io<T>::load(m[c]);
+    if (cv[0]) v[r][0] = Io<T>::load(rowp[col0]);
+    if (cv[9]) v[r][9] = Io<T>::load(rowp[col0 + 9]);
+    if (cv[10]) v[r][10] = Io<T>::load(rowp[col0 + 10]);
+  }
+  int arg[10];
+  float g[10];
+#pragma unroll
+  for (int k = 0; k < 10; ++k) {
+    const int wr = k / 5, wc = k % 5;
+    const int32_t woh = bi + wr, wow = 4 * bj + wc;
+    arg[k] = -1;
+    g[k] = 0.0f;
+    if (woh >= oh || wow >= ow) continue;
+    bool found = false;
+    float best = 0.0f;
+#pragma unroll
+    for (int a = 0; a < 3; ++a)
+#pragma unroll
+      for (int b = 0; b < 3; ++b) {
+        const int lr = 2 * wr + a, lc = 2 * wc + b;
+        if (!rv[lr] || !cv[lc]) continue;
+        const float val = v[lr][lc];
+        if (!found || val > best) {
+          found = true;
+          best = val;
+          arg[k] = lr * 11 + lc;
+        }
+      }
+    g[k] = Io<T>::load(dyp[woh * ow + wow]);
+  }
+#pragma unroll
+  for (int rr = 0; rr < 2; ++rr) {
+    const int32_t gr = 2 * bi + rr;
+    if (gr >= h) continue;
+    uint4 packed;
+    S* o = reinterpret_cast<S*>(&packed);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const int at = (rr + 1) * 11 + (c + 1);
+      float acc = 0.0f;
+#pragma unroll
+      for (int k = 0; k < 10; ++k)
+        if (arg[k] == at) acc += g[k];
+      o[c] = Io<T>::store(acc);
+    }
+    *reinterpret_cast<uint4*>(dx + nc * h * w + static_cast<int64_t>(gr) * w + 8 * bj) = packed;
+  }
+}
+
 // ---- conv gradients (direct, reference order) ----------------------------------------------------------------
 
 struct ConvG {
@@ -285,7 +369,7 @@ __device__ inline int64_t decompose(int64_t idx, int32_t nd, const int64_t* dim,
   return off;
 }
 
-constexpr int kSumThreads = 512;
+constexpr int kSumThreads = 1024;
 
 // One workgroup per output: fp32 partial sums strided over the reduced elements, then a fixed-shape tree. The
 // reduced set is walked as (outer reduced coordinates) x (innermost reduced run): when that run is contiguous in x
@@ -304,18 +388,38 @@ __global__ __launch_bounds__(kSumThreads) void sum_kernel(const typename Io<T>::
   if (inner_run) {
     const int64_t len = g.rdim[g.nr - 1];
     const int64_t outer = len > 0 ? g.nred / len : 0;
-    const bool vec = len % V == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0 && (base % V) == 0;
-    for (int64_t q = 0; q < outer; ++q) {
-      const int64_t off = base + (g.nr > 1 ? decompose(q, g.nr - 1, g.rdim, g.rstride) : 0);
-      if (vec && off % V == 0) {
-        const uint4* row = reinterpret_cast<const uint4*>(x + off);
-        for (int64_t v = threadIdx.x; v < len / V; v += kSumThreads) {
-          const uint4 w = row[v];
-          const S* e = reinterpret_cast<const S*>(&w);
+    const bool vec = len % V == 0 && (reinterpret_cast<uintptr_t>(x) % 16) == 0 && (base % V) == 0 &&
+                     (g.nr == 1 || g.rstride[g.nr - 2] % V == 0);
+    if (vec && g.nr <= 2) {
+      // flat index over (outer coordinate, vector within the run); four independent 16-byte loads in flight per
+      // lane before they are accumulated (in index order)
+      const int64_t per_row = len / V, total = outer * per_row;
+      const int64_t ostride = g.nr == 2 ? g.rstride[0] : 0;
+      auto at = [&](int64_t f) {
+        const int64_t q = f / per_row;
+        return reinterpret_cast<const uint4*>(x + base + q * ostride + (f - q * per_row) * V);
+      };
+      int64_t f = threadIdx.x;
+      for (; f + 3 * kSumThreads < total; f += 4 * kSumThreads) {
+        uint4 w[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) w[u] = *at(f + u * kSumThreads);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const S* e = reinterpret_cast<const S*>(&w[u]);
 #pragma unroll
           for (int k = 0; k < V; ++k) acc += Io<T>::load(e[k]);
         }
-      } else {
+      }
+      for (; f < total; f += kSumThreads) {
+        const uint4 w = *at(f);
+        const S* e = reinterpret_cast<const S*>(&w);
+#pragma unroll
+        for (int k = 0; k < V; ++k) acc += Io<T>::load(e[k]);
+      }
+    } else {
+      for (int64_t q = 0; q < outer; ++q) {
+        const int64_t off = base + (g.nr > 1 ? decompose(q, g.nr - 1, g.rdim, g.rstride) : 0);
         for (int64_t r = threadIdx.x; r < len; r += kSumThreads) acc += Io<T>::load(x[off + r]);
       }
     }
@@ -404,7 +508,15 @@ struct PoolGradRun {
                        hipStream_t s) {
     using S = typename Io<T>::storage;
     const dim3 grid(static_cast<uint32_t>(blocks_for(total)));
-    if (mode == 0 && g.kh == 3 && g.kw == 3 && g.sh == 2 && g.sw == 2 && g.ph == 1 && g.pw == 1) {
+    const bool aligned = reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(dx) % 16 == 0;
+    if (mode == 0 && g.kh == 3 && g.kw == 3 && g.sh == 2 && g.sw == 2 && g.ph == 1 && g.pw == 1 && g.w % 8 == 0 &&
+        (sizeof(S) == 2) && aligned) {
+      const int32_t bh = (g.h + 1) / 2, bw = g.w / 8;
+      const int64_t blocks = static_cast<int64_t>(g.n) * g.c * bh * bw;
+      hipLaunchKernelGGL((maxpool3s2_grad8_kernel<T>), dim3(static_cast<uint32_t>(blocks_for(blocks))), dim3(kThreads), 0,
+                         s, static_cast<const S*>(dy), static_cast<const S*>(x), static_cast<S*>(dx), g.h, g.w, g.oh, g.ow,
+                         bh, bw, blocks);
+    } else if (mode == 0 && g.kh == 3 && g.kw == 3 && g.sh == 2 && g.sw == 2 && g.ph == 1 && g.pw == 1) {
       const int32_t bh = (g.h + 1) / 2, bw = (g.w + 1) / 2;
       const int64_t blocks = static_cast<int64_t>(g.n) * g.c * bh * bw;
       hipLaunchKernelGGL((maxpool3s2_grad_kernel<T>), dim3(static_cast<uint32_t>(blocks_for(blocks))), dim3(kThreads), 0, s,

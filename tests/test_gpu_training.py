@@ -158,6 +158,8 @@ POOL_CASES = [
     (2, 3, 8, 8, 2, 2, 0),
     (1, 5, 7, 7, 7, 7, 0),
     (2, 2, 9, 9, 3, 1, 1),
+    (2, 8, 24, 32, 3, 2, 1),  # 3x3/s2/p1 with W % 8 == 0: the 2x8-block kernel
+    (1, 3, 13, 13, 3, 2, 1),  # ... and the 2x2-block kernel
 ]
 
 
