@@ -7,8 +7,8 @@
 //
 // Both operands are k-major (rows of p), so both MFMA fragments come from ds_read_b64_tr_b16 transpose reads of
 // [BK][cols] LDS tiles (the B-operand path of the GEMM kernel, used for A as well). Tiles: 64 (co) x 128 (a,b,ci)
-// per workgroup, 4 waves of 32 x 64 (two 32x32x16 MFMA tiles), 32 p-rows per stage, register-staged loads with
-// zero fill for rows past the split and taps in the padding, two LDS stages.
+// per workgroup, 4 waves of 32 x 64 (two 32x32x16 MFMA tiles), register-staged loads with
+// zero fill for rows past the split and taps in the padding, two LDS stages of 64 p-rows.
 #include <algorithm>
 
 #include "fh_mfma16.h"
@@ -18,7 +18,7 @@ namespace {
 
 using namespace mfma16;
 
-constexpr int kWM = 64, kWN = 128, kWK = 32;  // workgroup tile
+constexpr int kWM = 64, kWN = 128, kWK = 64;  // workgroup tile
 constexpr int kWThreads = 256;
 
 struct WgradArgs {
@@ -40,37 +40,40 @@ __global__ __launch_bounds__(kWThreads) void conv_wgrad_kernel(WgradArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int tm = blockIdx.x / a.tiles_n, tn = blockIdx.x % a.tiles_n;
   const int m0 = tm * kWM, n0 = tn * kWN;
-  const int64_t p_begin = static_cast<int64_t>(blockIdx.y) * a.rows_per_split;
-  const int64_t p_end = min(a.p, p_begin + a.rows_per_split);
+  // p fits 32 bits (checked by the host)
+  const int32_t p_begin = static_cast<int32_t>(static_cast<int64_t>(blockIdx.y) * a.rows_per_split);
+  const int32_t p_end = static_cast<int32_t>(min(a.p, static_cast<int64_t>(p_begin) + a.rows_per_split));
   const S* __restrict__ X = static_cast<const S*>(a.x);
   const S* __restrict__ DY = static_cast<const S*>(a.dy);
 
-  // A loads: one 16-byte chunk per thread, row t/8, column chunk t%8
+  // A loads: kWK*8 chunks, rows t/8 + 32 i, column chunk t%8; B loads: kWK*16 chunks, rows t/16 + 16 i, column
+  // chunk t%16 (a fixed filter tap and ci block per thread)
+  constexpr int A_LOADS = kWK * (kWM / 8) / kWThreads, B_LOADS = kWK * (kWN / 8) / kWThreads;
   const int a_row = tid >> 3, a_chunk = tid & 7;
   const bool a_col_ok = m0 + 8 * a_chunk < a.cout;
-  // B loads: two chunks per thread, rows t/16 and t/16 + 16, column chunk t%16 (a fixed filter tap and ci block)
   const int b_row = tid >> 4, b_chunk = tid & 15;
   const int ncol = n0 + 8 * b_chunk;
   const bool b_col_ok = ncol < a.nc;
   const int tap = b_col_ok ? ncol / a.cin : 0;
   const int ci = b_col_ok ? ncol - tap * a.cin : 0;
   const int ta = tap / a.kw, tb = tap - ta * a.kw;
-  const int plane = a.oh * a.ow;
+  const int32_t plane = a.oh * a.ow;
 
-  uint4 ra, rb[2];
-  auto load = [&](int64_t p0) {
-    {
-      const int64_t p = p0 + a_row;
-      ra = (p < p_end && a_col_ok) ? *reinterpret_cast<const uint4*>(DY + p * a.cout + m0 + 8 * a_chunk)
-                                   : uint4{0, 0, 0, 0};
+  uint4 ra[A_LOADS], rb[B_LOADS];
+  auto load = [&](int32_t p0) {
+#pragma unroll
+    for (int i = 0; i < A_LOADS; ++i) {
+      const int32_t p = p0 + a_row + 32 * i;
+      ra[i] = (p < p_end && a_col_ok) ? *reinterpret_cast<const uint4*>(DY + static_cast<int64_t>(p) * a.cout + m0 + 8 * a_chunk)
+                                      : uint4{0, 0, 0, 0};
     }
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int64_t p = p0 + b_row + 16 * i;
+    for (int i = 0; i < B_LOADS; ++i) {
+      const int32_t p = p0 + b_row + 16 * i;
       uint4 v{0, 0, 0, 0};
       if (p < p_end && b_col_ok) {
-        const int32_t n = static_cast<int32_t>(p / plane);
-        const int32_t rem = static_cast<int32_t>(p - static_cast<int64_t>(n) * plane);
+        const int32_t n = p / plane;
+        const int32_t rem = p - n * plane;
         const int32_t oh = rem / a.ow, ow = rem - oh * a.ow;
         const int32_t ih = oh * a.sh - a.ph + ta, iw = ow * a.sw - a.pw + tb;
         if (ih >= 0 && ih < a.h && iw >= 0 && iw < a.w)
@@ -80,9 +83,13 @@ __global__ __launch_bounds__(kWThreads) void conv_wgrad_kernel(WgradArgs a) {
     }
   };
   auto store = [&](int buf) {
-    *reinterpret_cast<uint4*>(&As[buf][a_row * kWM + ((a_chunk ^ swz8(a_row)) * 8)]) = ra;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < A_LOADS; ++i) {
+      const int r = a_row + 32 * i;
+      *reinterpret_cast<uint4*>(&As[buf][r * kWM + ((a_chunk ^ swz8(r)) * 8)]) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_LOADS; ++i) {
       const int r = b_row + 16 * i;
       *reinterpret_cast<uint4*>(&Bs[buf][r * kWN + ((b_chunk ^ swz16(r)) * 8)]) = rb[i];
     }
@@ -110,41 +117,36 @@ __global__ __launch_bounds__(kWThreads) void conv_wgrad_kernel(WgradArgs a) {
 #pragma unroll
     for (int x = 0; x < 16; ++x) acc[j][x] = 0.0f;
 
-  const int64_t steps = (p_end - p_begin + kWK - 1) / kWK;
+  const int32_t steps = (p_end - p_begin + kWK - 1) / kWK;
   if (steps > 0) {
     load(p_begin);
     store(0);
   }
   __syncthreads();
   asm volatile("" ::: "memory");  // the transpose reads below are asm: keep them after the barrier
-  for (int64_t it = 0; it < steps; ++it) {
-    const int buf = static_cast<int>(it & 1);
+  for (int32_t it = 0; it < steps; ++it) {
+    const int buf = it & 1;
     if (it + 1 < steps) load(p_begin + (it + 1) * kWK);
     const uint32_t abase = lds_addr((const FH_LDS void*)&As[buf][0]);
     const uint32_t bbase = lds_addr((const FH_LDS void*)&Bs[buf][0]);
+    [&]<int... K_>(std::integer_sequence<int, K_...>) {
+      (
+          [&] {
+            constexpr int s = K_;  // 16-row k-step within the stage
+            u32x2_t al, ah, bl[2], bh[2];
+            al = lds_read_tr16_b64<(16 * s) * kWM * 2>(abase + a_off);
+            ah = lds_read_tr16_b64<(16 * s + 4) * kWM * 2>(abase + a_off);
+            bl[0] = lds_read_tr16_b64<(16 * s) * kWN * 2>(bbase + b_off[0]);
+            bh[0] = lds_read_tr16_b64<(16 * s + 4) * kWN * 2>(bbase + b_off[0]);
+            bl[1] = lds_read_tr16_b64<(16 * s) * kWN * 2>(bbase + b_off[1]);
+            bh[1] = lds_read_tr16_b64<(16 * s + 4) * kWN * 2>(bbase + b_off[1]);
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(al), "+v"(ah), "+v"(bl[0]), "+v"(bh[0]), "+v"(bl[1]), "+v"(bh[1]));
+            const u32x4_t af{al[0], al[1], ah[0], ah[1]};
 #pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      u32x2_t al, ah, bl[2], bh[2];
-      if (s == 0) {
-        al = lds_read_tr16_b64<0>(abase + a_off);
-        ah = lds_read_tr16_b64<4 * kWM * 2>(abase + a_off);
-        bl[0] = lds_read_tr16_b64<0>(bbase + b_off[0]);
-        bh[0] = lds_read_tr16_b64<4 * kWN * 2>(bbase + b_off[0]);
-        bl[1] = lds_read_tr16_b64<0>(bbase + b_off[1]);
-        bh[1] = lds_read_tr16_b64<4 * kWN * 2>(bbase + b_off[1]);
-      } else {
-        al = lds_read_tr16_b64<16 * kWM * 2>(abase + a_off);
-        ah = lds_read_tr16_b64<20 * kWM * 2>(abase + a_off);
-        bl[0] = lds_read_tr16_b64<16 * kWN * 2>(bbase + b_off[0]);
-        bh[0] = lds_read_tr16_b64<20 * kWN * 2>(bbase + b_off[0]);
-        bl[1] = lds_read_tr16_b64<16 * kWN * 2>(bbase + b_off[1]);
-        bh[1] = lds_read_tr16_b64<20 * kWN * 2>(bbase + b_off[1]);
-      }
-      asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(al), "+v"(ah), "+v"(bl[0]), "+v"(bh[0]), "+v"(bl[1]), "+v"(bh[1]));
-      const u32x4_t af{al[0], al[1], ah[0], ah[1]};
-#pragma unroll
-      for (int j = 0; j < 2; ++j) mfma32<T>(af, u32x4_t{bl[j][0], bl[j][1], bh[j][0], bh[j][1]}, acc[j]);
-    }
+            for (int j = 0; j < 2; ++j) mfma32<T>(af, u32x4_t{bl[j][0], bl[j][1], bh[j][0], bh[j][1]}, acc[j]);
+          }(),
+          ...);
+    }(std::make_integer_sequence<int, kWK / 16>{});
     // buf^1 was last read in the previous iteration, before its closing barrier: safe to refill now
     if (it + 1 < steps) store(buf ^ 1);
     __syncthreads();
@@ -166,24 +168,24 @@ __global__ __launch_bounds__(kWThreads) void conv_wgrad_kernel(WgradArgs a) {
   }
 }
 
-// dw[co][ci][kh][kw] = round(sum over splits, in order, of part[s][co][(kh*KW + kw)*cin_pad + ci]), ci < cin.
+// dw[co][ci][kh][kw] = round(sum over splits, in order, of part[s][co][(kh*KW + kw)*cin_pad + ci]), ci < cin. One
+// thread per workspace column in its natural (co, tap, ci) order, so the split-strided reads of a wave are
+// contiguous; the scattered 2-byte writes are the small side.
 template <typename T>
 __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* __restrict__ part, typename Io<T>::storage* __restrict__ dw,
                                                            int32_t splits, int32_t cout, int32_t cin, int32_t cin_pad,
-                                                           int32_t kh, int32_t kw, int64_t nc, int64_t total) {
+                                                           int32_t taps, int64_t nc, int64_t total) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= total) return;
-  const int32_t b = static_cast<int32_t>(i % kw);
-  int64_t r = i / kw;
-  const int32_t a = static_cast<int32_t>(r % kh);
-  r /= kh;
-  const int32_t ci = static_cast<int32_t>(r % cin);
-  const int32_t co = static_cast<int32_t>(r / cin);
-  const int64_t col = static_cast<int64_t>(co) * nc + (static_cast<int64_t>(a) * kw + b) * cin_pad + ci;
+  const int32_t ci = static_cast<int32_t>(i % cin_pad);
+  const int64_t r = i / cin_pad;
+  const int32_t tap = static_cast<int32_t>(r % taps);
+  const int32_t co = static_cast<int32_t>(r / taps);
+  if (ci >= cin) return;
   const int64_t stride = static_cast<int64_t>(cout) * nc;
   float s = 0.0f;
-  for (int32_t k = 0; k < splits; ++k) s += part[k * stride + col];
-  dw[i] = Io<T>::store(s);
+  for (int32_t k = 0; k < splits; ++k) s += part[k * stride + i];
+  dw[(static_cast<int64_t>(co) * cin + ci) * taps + tap] = Io<T>::store(s);
 }
 
 template <typename T>
@@ -192,10 +194,10 @@ fh_status run_wgrad(const WgradArgs& args, int32_t splits, int32_t cin_real, int
   hipLaunchKernelGGL((conv_wgrad_kernel<T>), dim3(static_cast<uint32_t>(tiles), static_cast<uint32_t>(splits)),
                      dim3(kWThreads), 0, s, args);
   if (fh_status st = launch_status("conv_wgrad_kernel"); st != FH_OK) return st;
-  const int64_t total = static_cast<int64_t>(args.cout) * cin_real * kh * args.kw;
+  const int64_t total = static_cast<int64_t>(args.cout) * args.nc;  // every workspace column (co, tap, ci_pad)
   hipLaunchKernelGGL((wgrad_reduce_kernel<T>), dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256), 0, s,
-                     args.part, static_cast<typename Io<T>::storage*>(dw), splits, args.cout, cin_real, args.cin, kh,
-                     args.kw, static_cast<int64_t>(args.nc), total);
+                     args.part, static_cast<typename Io<T>::storage*>(dw), splits, args.cout, cin_real, args.cin,
+                     kh * args.kw, static_cast<int64_t>(args.nc), total);
   return launch_status("wgrad_reduce_kernel");
 }
 
@@ -209,7 +211,7 @@ extern "C" int64_t fh_conv2d_wgrad_workspace(int32_t dtype, const int64_t geom[1
   if (geom == nullptr || geom[11] != 1 || cin_pad % 8 != 0 || cin_pad < geom[1] || geom[4] % 8 != 0) return -1;
   const int64_t oh = (geom[2] + 2 * geom[9] - geom[5]) / geom[7] + 1, ow = (geom[3] + 2 * geom[10] - geom[6]) / geom[8] + 1;
   const int64_t p = geom[0] * oh * ow, nc = geom[5] * geom[6] * cin_pad;
-  if (p <= 0 || nc <= 0 || p > (int64_t{1} << 40) || nc > (1 << 30)) return -1;
+  if (p <= 0 || nc <= 0 || p >= (int64_t{1} << 31) - (int64_t{1} << 23) || nc > (1 << 30)) return -1;  // rows fit int32
   const int64_t tiles = ((geom[4] + kWM - 1) / kWM) * ((nc + kWN - 1) / kWN);
   // enough workgroups to fill the device twice over, each at least 512 p-rows, the workspace within 256 MiB
   int64_t sp = (2 * 256 + tiles - 1) / tiles;
