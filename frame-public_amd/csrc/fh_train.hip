@@ -327,6 +327,71 @@ __global__ __launch_bounds__(kThreads) void filter_flip_kernel(const S* __restri
   out[i] = w[((static_cast<int64_t>(co) * cin + ci) * kh + (kh - 1 - a)) * kw + (kw - 1 - b)];
 }
 
+// channels-last x [N,H,W,C] -> [N,Hu,Wu,C], the same placement, 16-byte vectors of channels (C % 8 == 0).
+template <typename S>
+__global__ __launch_bounds__(kThreads) void dilate_nhwc_vec_kernel(const S* __restrict__ x, S* __restrict__ out, int32_t c,
+                                                                   int32_t h, int32_t w, int32_t sh, int32_t sw,
+                                                                   int32_t hu, int32_t wu, int64_t total) {
+  constexpr int V = 16 / sizeof(S);
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;  // vector index
+  if (i >= total) return;
+  const int32_t cv = c / V;
+  const int32_t ch = static_cast<int32_t>(i % cv) * V;
+  int64_t r = i / cv;
+  const int32_t xw = static_cast<int32_t>(r % wu);
+  r /= wu;
+  const int32_t yh = static_cast<int32_t>(r % hu);
+  const int64_t n = r / hu;
+  uint4 v{0, 0, 0, 0};
+  if (yh % sh == 0 && xw % sw == 0 && yh / sh < h && xw / sw < w)
+    v = *reinterpret_cast<const uint4*>(x + ((n * h + yh / sh) * w + xw / sw) * c + ch);
+  *reinterpret_cast<uint4*>(out + ((n * hu + yh) * wu + xw) * c + ch) = v;
+}
+
+// avg_pool2d_grad_internal on channels-last dy [N,Ho,Wo,C] -> dx [N,H,W,C]: per input element the covering windows
+// in the reference's (kh, kw) order, sum of dy, then / (KH*KW), for a 16-byte vector of channels per lane.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void avgpool_grad_nhwc_kernel(const typename Io<T>::storage* __restrict__ dy,
+                                                                     typename Io<T>::storage* __restrict__ dx, PoolG g,
+                                                                     int64_t total) {
+  using S = typename Io<T>::storage;
+  constexpr int V = 16 / sizeof(S);
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (i >= total) return;
+  const int32_t cv = g.c / V;
+  const int32_t ch = static_cast<int32_t>(i % cv) * V;
+  int64_t r = i / cv;
+  const int32_t iw = static_cast<int32_t>(r % g.w);
+  r /= g.w;
+  const int32_t ih = static_cast<int32_t>(r % g.h);
+  const int64_t n = r / g.h;
+  float acc[V];
+#pragma unroll
+  for (int k = 0; k < V; ++k) acc[k] = 0.0f;
+  for (int32_t a = 0; a < g.kh; ++a) {
+    const int32_t nh = ih + g.ph - a;
+    if (nh < 0 || nh % g.sh != 0) continue;
+    const int32_t oh = nh / g.sh;
+    if (oh >= g.oh) continue;
+    for (int32_t b = 0; b < g.kw; ++b) {
+      const int32_t nw = iw + g.pw - b;
+      if (nw < 0 || nw % g.sw != 0) continue;
+      const int32_t ow = nw / g.sw;
+      if (ow >= g.ow) continue;
+      const uint4 v = *reinterpret_cast<const uint4*>(dy + ((n * g.oh + oh) * g.ow + ow) * g.c + ch);
+      const S* e = reinterpret_cast<const S*>(&v);
+#pragma unroll
+      for (int k = 0; k < V; ++k) acc[k] += Io<T>::load(e[k]);
+    }
+  }
+  const float denom = static_cast<float>(g.kh * g.kw);
+  uint4 o;
+  S* oe = reinterpret_cast<S*>(&o);
+#pragma unroll
+  for (int k = 0; k < V; ++k) oe[k] = Io<T>::store(acc[k] / denom);
+  *reinterpret_cast<uint4*>(dx + ((n * g.h + ih) * g.w + iw) * g.c + ch) = o;
+}
+
 // NCHW x [N,C,H,W] -> channels-last [N,Hu,Wu,C] with x[n][c][h][w] at (h*sh, w*sw) and zeros elsewhere.
 template <typename S>
 __global__ __launch_bounds__(kThreads) void dilate_nhwc_kernel(const S* __restrict__ x, S* __restrict__ out, int32_t c,
@@ -782,8 +847,8 @@ extern "C" fh_status fh_conv_filter_flip(int32_t dtype, const void* w, void* out
   return launch_status("fh_conv_filter_flip");
 }
 
-extern "C" fh_status fh_dilate_nhwc(int32_t dtype, const void* x, void* out, int64_t n, int64_t c, int64_t h, int64_t w,
-                                    int64_t sh, int64_t sw, int64_t hu, int64_t wu, void* stream) {
+extern "C" fh_status fh_dilate_nhwc(int32_t dtype, int32_t in_nhwc, const void* x, void* out, int64_t n, int64_t c,
+                                    int64_t h, int64_t w, int64_t sh, int64_t sw, int64_t hu, int64_t wu, void* stream) {
   if (!is_supported_float(dtype)) return fail(FH_UNIMPLEMENTED, "fh_dilate_nhwc: unsupported dtype");
   const int64_t dims[] = {n, c, h, w, sh, sw, hu, wu};
   for (int64_t v : dims)
@@ -794,9 +859,23 @@ extern "C" fh_status fh_dilate_nhwc(int32_t dtype, const void* x, void* out, int
   if (x == nullptr || out == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_dilate_nhwc: null pointer");
   if (!grid_ok(blocks_for(total))) return fail(FH_INVALID_ARGUMENT, "fh_dilate_nhwc: tensor too large");
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<uint32_t>(blocks_for(total)));
   const int32_t args[] = {static_cast<int32_t>(c), static_cast<int32_t>(h), static_cast<int32_t>(w), static_cast<int32_t>(sh),
                           static_cast<int32_t>(sw), static_cast<int32_t>(hu), static_cast<int32_t>(wu)};
+  if (in_nhwc) {
+    const int64_t vw = 16 / dtype_size(dtype);
+    if (c % vw != 0 || reinterpret_cast<uintptr_t>(x) % 16 != 0 || reinterpret_cast<uintptr_t>(out) % 16 != 0)
+      return fail(FH_UNIMPLEMENTED, "fh_dilate_nhwc: a channels-last input needs 16-byte channel vectors");
+    const int64_t vt = total / vw;
+    const dim3 vgrid(static_cast<uint32_t>(blocks_for(vt)));
+    if (dtype == FH_F32)
+      hipLaunchKernelGGL((dilate_nhwc_vec_kernel<uint32_t>), vgrid, dim3(kThreads), 0, s, static_cast<const uint32_t*>(x),
+                         static_cast<uint32_t*>(out), args[0], args[1], args[2], args[3], args[4], args[5], args[6], vt);
+    else
+      hipLaunchKernelGGL((dilate_nhwc_vec_kernel<uint16_t>), vgrid, dim3(kThreads), 0, s, static_cast<const uint16_t*>(x),
+                         static_cast<uint16_t*>(out), args[0], args[1], args[2], args[3], args[4], args[5], args[6], vt);
+    return launch_status("fh_dilate_nhwc");
+  }
+  const dim3 grid(static_cast<uint32_t>(blocks_for(total)));
   if (dtype == FH_F32)
     hipLaunchKernelGGL((dilate_nhwc_kernel<uint32_t>), grid, dim3(kThreads), 0, s, static_cast<const uint32_t*>(x),
                        static_cast<uint32_t*>(out), args[0], args[1], args[2], args[3], args[4], args[5], args[6], total);
@@ -804,4 +883,43 @@ extern "C" fh_status fh_dilate_nhwc(int32_t dtype, const void* x, void* out, int
     hipLaunchKernelGGL((dilate_nhwc_kernel<uint16_t>), grid, dim3(kThreads), 0, s, static_cast<const uint16_t*>(x),
                        static_cast<uint16_t*>(out), args[0], args[1], args[2], args[3], args[4], args[5], args[6], total);
   return launch_status("fh_dilate_nhwc");
+}
+
+extern "C" fh_status fh_avg_pool2d_grad_nhwc(int32_t dtype, const void* dy, void* dx, const int64_t geom[10], void* stream) {
+  if (!is_supported_float(dtype)) return fail(FH_UNIMPLEMENTED, "fh_avg_pool2d_grad_nhwc: unsupported dtype");
+  if (geom == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_avg_pool2d_grad_nhwc: null geometry");
+  for (int k = 0; k < 10; ++k)
+    if (geom[k] < 0 || geom[k] > 0x7fffffffLL) return fail(FH_INVALID_ARGUMENT, "fh_avg_pool2d_grad_nhwc: geometry entry out of range");
+  PoolG g{static_cast<int32_t>(geom[0]), static_cast<int32_t>(geom[1]), static_cast<int32_t>(geom[2]),
+          static_cast<int32_t>(geom[3]), static_cast<int32_t>(geom[4]), static_cast<int32_t>(geom[5]),
+          static_cast<int32_t>(geom[6]), static_cast<int32_t>(geom[7]), static_cast<int32_t>(geom[8]),
+          static_cast<int32_t>(geom[9]), 0, 0};
+  if (g.kh <= 0 || g.kw <= 0 || g.sh <= 0 || g.sw <= 0 || g.h + 2 * g.ph < g.kh || g.w + 2 * g.pw < g.kw)
+    return fail(FH_INVALID_ARGUMENT, "fh_avg_pool2d_grad_nhwc: invalid geometry");
+  g.oh = (g.h + 2 * g.ph - g.kh) / g.sh + 1;
+  g.ow = (g.w + 2 * g.pw - g.kw) / g.sw + 1;
+  const int64_t vw = 16 / dtype_size(dtype);
+  if (g.c % vw != 0 || reinterpret_cast<uintptr_t>(dy) % 16 != 0 || reinterpret_cast<uintptr_t>(dx) % 16 != 0)
+    return fail(FH_UNIMPLEMENTED, "fh_avg_pool2d_grad_nhwc: needs 16-byte channel vectors");
+  const int64_t total = static_cast<int64_t>(g.n) * g.h * g.w * (g.c / vw);
+  if (total == 0) return FH_OK;
+  if (dy == nullptr || dx == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_avg_pool2d_grad_nhwc: null pointer");
+  if (!grid_ok(blocks_for(total))) return fail(FH_INVALID_ARGUMENT, "fh_avg_pool2d_grad_nhwc: tensor too large");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<uint32_t>(blocks_for(total)));
+  switch (dtype) {
+    case FH_F32:
+      hipLaunchKernelGGL((avgpool_grad_nhwc_kernel<float>), grid, dim3(kThreads), 0, s, static_cast<const float*>(dy),
+                         static_cast<float*>(dx), g, total);
+      break;
+    case FH_BF16:
+      hipLaunchKernelGGL((avgpool_grad_nhwc_kernel<bf16_t>), grid, dim3(kThreads), 0, s, static_cast<const uint16_t*>(dy),
+                         static_cast<uint16_t*>(dx), g, total);
+      break;
+    default:
+      hipLaunchKernelGGL((avgpool_grad_nhwc_kernel<f16_t>), grid, dim3(kThreads), 0, s, static_cast<const uint16_t*>(dy),
+                         static_cast<uint16_t*>(dx), g, total);
+      break;
+  }
+  return launch_status("fh_avg_pool2d_grad_nhwc");
 }

@@ -134,7 +134,9 @@ inline constexpr std::string_view kPackFilterC8Op = "hip_pack_filter_c8_internal
 // filter [Cin][KH][KW][Cout] (fh_conv_filter_flip) and dy zero-dilated by the stride into channels-last
 // [N,Hu,Wu,Cout] (fh_dilate_nhwc; attribute stride).
 inline constexpr std::string_view kFilterFlipOp = "hip_conv_filter_flip_internal";
-inline constexpr std::string_view kDilateNhwcOp = "hip_dilate_nhwc_internal";
+inline constexpr std::string_view kDilateNhwcOp = "hip_dilate_nhwc_internal";  // attr in_nhwc = 1: dy channels-last
+// avg_pool2d_grad_internal on channels-last dy / dx (same attributes; see fh_avg_pool2d_grad_nhwc).
+inline constexpr std::string_view kAvgPoolGradNhwcOp = "hip_avg_pool2d_grad_nhwc_internal";
 // conv2d_grad_filter_internal on MFMA: inputs x channels-last [N,H,W,cin_pad] and dy channels-last [N,Ho,Wo,Cout];
 // outputs dw [Cout,Cin,KH,KW] and an fp32 split-K workspace (see fh_conv2d_wgrad_nhwc); attrs stride, padding,
 // groups, filter_shape.

@@ -236,6 +236,34 @@ GradFilterLowering plan_grad_filter(const ir::Node* n) {
 // by a lowered conv, a pool or an elementwise node, and every use is one that takes channels-last data: input 0
 // of a lowered non-C8 conv, a conv epilogue operand, a pool, an elementwise node, or a reshape of a 1x1 plane
 // (the same bytes in either layout). Graph inputs and outputs stay NCHW, so nothing outside the backend sees it.
+// A rank-4 `sum` whose input can be channels-last: without keepdims, and with its kept axes in the same order in
+// both layouts (NCHW axis 0,1,2,3 is NHWC axis 0,3,1,2), so the output is the same tensor. Returns the axes for
+// the channels-last input.
+std::optional<std::vector<int64_t>> nhwc_sum_axes(const ir::Node* n) {
+  if (n->op() != "sum" || n->inputs()[0]->type().shape.rank() != 4) return std::nullopt;
+  const auto* axes = attr_of<std::vector<int64_t>>(n, "axes");
+  const auto* kd = attr_of<bool>(n, "keepdims");
+  if (axes == nullptr || (kd != nullptr && *kd)) return std::nullopt;
+  static constexpr int64_t to_nhwc[4] = {0, 3, 1, 2};
+  bool reduced[4] = {axes->empty(), axes->empty(), axes->empty(), axes->empty()};
+  for (int64_t a : *axes) {
+    if (a < 0 || a > 3) return std::nullopt;
+    reduced[a] = true;
+  }
+  int64_t last = -1;
+  std::vector<int64_t> out;
+  for (int64_t a = 0; a < 4; ++a) {
+    if (reduced[a]) {
+      out.push_back(to_nhwc[a]);
+      continue;
+    }
+    if (to_nhwc[a] < last) return std::nullopt;
+    last = to_nhwc[a];
+  }
+  std::sort(out.begin(), out.end());
+  return out;
+}
+
 std::unordered_set<const ir::Value*> plan_channels_last(const ir::Graph& src) {
   std::unordered_map<const ir::Value*, const ir::Value*> parent;
   auto find = [&](const ir::Value* v) {
@@ -257,9 +285,17 @@ std::unordered_set<const ir::Value*> plan_channels_last(const ir::Graph& src) {
     const ir::Value *ra = find(a), *rb = find(b);
     if (ra != rb) parent[ra] = rb;
   };
-  auto is_ew = [](const ir::Node* n) { return ew_code(n->op()) != 0 || n->op() == ops::kFusedElementwiseOpName; };
+  auto is_ew = [](const ir::Node* n) {
+    return ew_code(n->op()) != 0 || n->op() == ops::kFusedElementwiseOpName || n->op() == "relu_grad_internal";
+  };
   auto is_pool = [](const ir::Node* n) { return n->op() == "max_pool2d" || n->op() == "avg_pool2d"; };
   auto rank4 = [](const ir::Value* v) { return v->type().shape.rank() == 4; };
+  // training-graph nodes that read or write channels-last operands once lowered
+  auto is_grad_input = [](const ir::Node* n) { return plan_grad_input(n).ok; };
+  auto is_avg_pool_grad = [](const ir::Node* n) {
+    return n->op() == "avg_pool2d_grad_internal" && n->outputs()[0].type().shape.rank() == 4 &&
+           n->outputs()[0].type().shape.dim(1) * static_cast<int64_t>(n->outputs()[0].type().dtype.itemsize()) % 16 == 0;
+  };
 
   std::unordered_map<const ir::Value*, std::vector<std::pair<const ir::Node*, size_t>>> uses;
   std::unordered_map<const ir::Node*, ConvLowering> convs;
@@ -278,6 +314,13 @@ std::unordered_set<const ir::Value*> plan_channels_last(const ir::Graph& src) {
       add(&n->outputs()[0]);
       for (const ir::Value* in : n->inputs())
         if (rank4(in)) unite(&n->outputs()[0], in);
+    } else if (is_grad_input(n)) {
+      add(&n->outputs()[0]);
+    } else if (is_avg_pool_grad(n)) {
+      unite(&n->outputs()[0], n->inputs()[0]);
+    } else if (n->op() == "reshape" && rank4(&n->outputs()[0]) && n->outputs()[0].type().shape.dim(2) == 1 &&
+               n->outputs()[0].type().shape.dim(3) == 1) {
+      add(&n->outputs()[0]);  // [N,C,1,1]: the same bytes in either layout
     }
   }
   std::unordered_set<const ir::Value*> bad;  // group roots that must stay NCHW
@@ -286,7 +329,9 @@ std::unordered_set<const ir::Value*> plan_channels_last(const ir::Graph& src) {
     (void)unused;
     const ir::Value* root = find(v);
     const ir::Node* p = v->producer();
-    const bool producer_ok = p != nullptr && (convs.count(p) || is_ew(p) || is_pool(p));
+    const bool plane1 = rank4(v) && v->type().shape.dim(2) == 1 && v->type().shape.dim(3) == 1;
+    const bool producer_ok = p != nullptr && (convs.count(p) || is_ew(p) || is_pool(p) || is_grad_input(p) ||
+                                              is_avg_pool_grad(p) || (p->op() == "reshape" && plane1));
     bool uses_ok = !graph_outputs.count(v);
     for (const auto& [c, idx] : uses[v]) {
       if (!uses_ok) break;
@@ -299,6 +344,14 @@ std::unordered_set<const ir::Value*> plan_channels_last(const ir::Graph& src) {
       } else if (c->op() == "reshape") {
         const Shape& sh = v->type().shape;
         uses_ok = sh.rank() == 4 && sh.dim(2) == 1 && sh.dim(3) == 1;
+      } else if (is_grad_input(c)) {
+        uses_ok = idx == 0;  // dy
+      } else if (const GradFilterLowering gf = plan_grad_filter(c); gf.ok) {
+        uses_ok = idx == 1 || !gf.c8;  // dy, or x when it needs no C8 pack
+      } else if (is_avg_pool_grad(c)) {
+        uses_ok = true;
+      } else if (c->op() == "sum") {
+        uses_ok = nhwc_sum_axes(c).has_value();
       } else {
         uses_ok = false;
       }
@@ -398,19 +451,27 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
       Result<ir::Node*> flip = out.create_node(std::string(kFilterFlipOp), {ins[1]}, {wt});
       if (!flip.is_ok()) return flip.status();
       ir::Value* dy_cl = nullptr;
+      const bool dy_nhwc = nhwc.count(n->inputs()[0]) != 0;
       if (gi.sh == 1 && gi.sw == 1) {
-        Result<ir::Value*> v = channels_last(ins[0]);
-        if (!v.is_ok()) return v.status();
-        dy_cl = v.value();
+        if (dy_nhwc) {
+          dy_cl = ins[0];
+        } else {
+          Result<ir::Value*> v = channels_last(ins[0]);
+          if (!v.is_ok()) return v.status();
+          dy_cl = v.value();
+        }
       } else {
         dt.shape = Shape({gi.n, gi.hu, gi.wu, gi.cout});
         Result<ir::Node*> d = out.create_node(std::string(kDilateNhwcOp), {ins[0]}, {dt});
         if (!d.is_ok()) return d.status();
         d.value()->set_attr("stride", ir::AttrValue{std::vector<int64_t>{gi.sh, gi.sw}});
+        if (dy_nhwc) d.value()->set_attr("in_nhwc", ir::AttrValue{int64_t{1}});
         dy_cl = d.value()->output(0);
       }
-      Result<ir::Node*> c = out.create_node(std::string(kConvNhwcOp), {dy_cl, flip.value()->output(0)}, {n->outputs()[0].type()});
+      Result<ir::Node*> c =
+          out.create_node(std::string(kConvNhwcOp), {dy_cl, flip.value()->output(0)}, {lowered_type(&n->outputs()[0])});
       if (!c.is_ok()) return c.status();
+      if (nhwc.count(&n->outputs()[0])) c.value()->set_attr("out_nhwc", ir::AttrValue{int64_t{1}});
       c.value()->set_attr("stride", ir::AttrValue{std::vector<int64_t>{1, 1}});
       c.value()->set_attr("padding", ir::AttrValue{std::vector<int64_t>{gi.kh - 1 - gi.ph, gi.kw - 1 - gi.pw}});
       c.value()->set_attr("groups", ir::AttrValue{int64_t{1}});
@@ -428,12 +489,14 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
         Result<ir::Node*> px = out.create_node(std::string(kPackInputC8Op), {ins[0]}, {tx});
         if (!px.is_ok()) return px.status();
         x_cl = px.value()->output(0);
+      } else if (nhwc.count(n->inputs()[0])) {
+        x_cl = ins[0];
       } else {
         Result<ir::Value*> v = channels_last(ins[0]);
         if (!v.is_ok()) return v.status();
         x_cl = v.value();
       }
-      Result<ir::Value*> dy_cl = channels_last(ins[1]);
+      Result<ir::Value*> dy_cl = nhwc.count(n->inputs()[1]) ? Result<ir::Value*>(ins[1]) : channels_last(ins[1]);
       if (!dy_cl.is_ok()) return dy_cl.status();
       ir::TensorType wst = n->outputs()[0].type();
       wst.dtype = DType::of<float>();
@@ -494,10 +557,15 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
     if (n->outputs().size() == 1 && nhwc.count(&n->outputs()[0])) {  // pools of channels-last activations
       if (op == "max_pool2d") op = std::string(kMaxPoolNhwcOp);
       if (op == "avg_pool2d") op = std::string(kAvgPoolNhwcOp);
+      if (op == "avg_pool2d_grad_internal") op = std::string(kAvgPoolGradNhwcOp);
     }
+    const bool sum_nhwc = op == "sum" && nhwc.count(n->inputs()[0]);
     Result<ir::Node*> c = out.create_node(op, std::move(ins), std::move(types));
     if (!c.is_ok()) return c.status();
     for (const auto& [k, v] : n->attrs()) c.value()->set_attr(k, v);
+    if (sum_nhwc) c.value()->set_attr("axes", ir::AttrValue{*nhwc_sum_axes(n)});
+    if (op == "reshape" && nhwc.count(&n->outputs()[0]))  // [N,C,1,1] kept as [N,1,1,C]: same bytes
+      c.value()->set_attr("target_shape", ir::AttrValue{lowered_type(&n->outputs()[0]).shape});
     for (size_t i = 0; i < n->outputs().size(); ++i) map[&n->outputs()[i]] = c.value()->output(static_cast<int32_t>(i));
   }
   for (const ir::Value* o : src.outputs()) FRAME_RETURN_IF_ERROR(out.mark_output(map.at(o)));

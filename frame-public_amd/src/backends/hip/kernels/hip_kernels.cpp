@@ -496,6 +496,28 @@ Status conv_grad_kernel(KernelContext& ctx) {
   return Status::ok();
 }
 
+// avg_pool2d_grad_internal on channels-last dy [N,Ho,Wo,C] -> dx [N,H,W,C] (kAvgPoolGradNhwcOp).
+Status avg_pool_grad_nhwc_kernel(KernelContext& ctx) {
+  const std::string op(kAvgPoolGradNhwcOp);
+  FRAME_RETURN_IF_ERROR(arity(ctx, op, 1, 1));
+  FRAME_RETURN_IF_ERROR(same_dtype(ctx, op));
+  const Shape* xs = attr<Shape>(ctx, "input_shape");  // NCHW input_shape of the forward
+  if (xs == nullptr) return invalid(op, "missing attribute 'input_shape'");
+  Result<std::array<int64_t, 10>> g = pool_geom(ctx, op, *xs);
+  if (!g.is_ok()) return g.status();
+  const auto& geom = g.value();
+  const int64_t oh = (geom[2] + 2 * geom[8] - geom[4]) / geom[6] + 1, ow = (geom[3] + 2 * geom[9] - geom[5]) / geom[7] + 1;
+  if (ctx.outputs[0].shape() != Shape({geom[0], geom[2], geom[3], geom[1]}) ||
+      ctx.inputs[0].shape() != Shape({geom[0], oh, ow, geom[1]}))
+    return invalid(op, "channels-last shapes do not match the geometry");
+  Result<int32_t> dt = float_code(op, ctx.outputs[0].dtype());
+  if (!dt.is_ok()) return dt.status();
+  FRAME_HIP_RETURN_IF_ERROR(fh_avg_pool2d_grad_nhwc(dt.value(), ctx.inputs[0].raw_data(), ctx.outputs[0].raw_data(), geom.data(),
+                                                    stream_handle(ctx)),
+                            "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
 // conv2d_grad_filter on MFMA over channels-last operands (kConvWgradOp); output 1 is the split-K workspace.
 Status conv_wgrad_kernel(KernelContext& ctx) {
   const std::string op(kConvWgradOp);
@@ -547,13 +569,17 @@ Status dilate_nhwc_kernel(KernelContext& ctx) {
   const Shape& x = ctx.inputs[0].shape();
   const Shape& y = ctx.outputs[0].shape();
   if (s == nullptr || s->size() != 2 || (*s)[0] < 1 || (*s)[1] < 1) return invalid(op, "missing or malformed stride");
-  if (x.rank() != 4 || y.rank() != 4 || y.dim(0) != x.dim(0) || y.dim(3) != x.dim(1) || y.dim(1) < (x.dim(2) - 1) * (*s)[0] + 1 ||
-      y.dim(2) < (x.dim(3) - 1) * (*s)[1] + 1)
-    return invalid(op, "output shape does not match the dilated input");
+  if (x.rank() != 4 || y.rank() != 4 || y.dim(0) != x.dim(0)) return invalid(op, "expects rank-4 tensors of one batch");
   Result<int32_t> dt = float_code(op, ctx.outputs[0].dtype());
   if (!dt.is_ok()) return dt.status();
-  FRAME_HIP_RETURN_IF_ERROR(fh_dilate_nhwc(dt.value(), ctx.inputs[0].raw_data(), ctx.outputs[0].raw_data(), x.dim(0), x.dim(1),
-                                           x.dim(2), x.dim(3), (*s)[0], (*s)[1], y.dim(1), y.dim(2), stream_handle(ctx)),
+  const auto* in_nhwc = attr<int64_t>(ctx, "in_nhwc");
+  const bool cl = in_nhwc != nullptr && *in_nhwc != 0;
+  // x NCHW [N,C,H,W], or channels-last [N,H,W,C]
+  const int64_t xn = x.dim(0), xc = cl ? x.dim(3) : x.dim(1), xh = cl ? x.dim(1) : x.dim(2), xw = cl ? x.dim(2) : x.dim(3);
+  if (y.dim(3) != xc || y.dim(1) < (xh - 1) * (*s)[0] + 1 || y.dim(2) < (xw - 1) * (*s)[1] + 1)
+    return invalid(op, "output shape does not match the dilated input");
+  FRAME_HIP_RETURN_IF_ERROR(fh_dilate_nhwc(dt.value(), cl ? 1 : 0, ctx.inputs[0].raw_data(), ctx.outputs[0].raw_data(), xn, xc,
+                                           xh, xw, (*s)[0], (*s)[1], y.dim(1), y.dim(2), stream_handle(ctx)),
                             "op '" + op + "' (hip)");
   return Status::ok();
 }
@@ -783,6 +809,7 @@ FRAME_REGISTER_KERNEL("conv2d_grad_input_internal", kHipBackendName, &conv_grad_
 FRAME_REGISTER_KERNEL("conv2d_grad_filter_internal", kHipBackendName, &conv_grad_kernel<1>);
 FRAME_REGISTER_KERNEL(kFilterFlipOp, kHipBackendName, &filter_flip_kernel);
 FRAME_REGISTER_KERNEL(kConvWgradOp, kHipBackendName, &conv_wgrad_kernel);
+FRAME_REGISTER_KERNEL(kAvgPoolGradNhwcOp, kHipBackendName, &avg_pool_grad_nhwc_kernel);
 FRAME_REGISTER_KERNEL(kDilateNhwcOp, kHipBackendName, &dilate_nhwc_kernel);
 FRAME_REGISTER_KERNEL("sum", kHipBackendName, &sum_kernel<0>);
 FRAME_REGISTER_KERNEL("sum_grad_internal", kHipBackendName, &sum_kernel<1>);

@@ -278,12 +278,18 @@ fh_status fh_conv2d_wgrad_nhwc(int32_t dtype, const void* x, const void* dy, voi
 /* Operands of conv2d_grad_input as a stride-1 convolution on the implicit-GEMM kernel (dx = conv(dilate(dy),
  * flip(w)), padding KH-1-pad): fh_conv_filter_flip writes out[ci][a][b][co] = w[co][ci][KH-1-a][KW-1-b] (the
  * channels-last filter [Cin][KH][KW][Cout] of that convolution); fh_dilate_nhwc writes the channels-last
- * [N,Hu,Wu,C] tensor holding x[n][c][h][w] (NCHW) at (h*sh, w*sw) and zeros elsewhere. No counterpart in the
- * reference (cudnnConvolutionBackwardData does this inside the library). */
+ * [N,Hu,Wu,C] tensor holding x's element (n, c, h, w) at (h*sh, w*sw) and zeros elsewhere, x NCHW (in_nhwc 0) or
+ * channels-last [N,H,W,C] (in_nhwc 1, C*itemsize % 16 == 0). No counterpart in the reference
+ * (cudnnConvolutionBackwardData does this inside the library). */
 fh_status fh_conv_filter_flip(int32_t dtype, const void* w, void* out, int64_t cout, int64_t cin, int64_t kh, int64_t kw,
                               void* stream);
-fh_status fh_dilate_nhwc(int32_t dtype, const void* x, void* out, int64_t n, int64_t c, int64_t h, int64_t w, int64_t sh,
-                         int64_t sw, int64_t hu, int64_t wu, void* stream);
+fh_status fh_dilate_nhwc(int32_t dtype, int32_t in_nhwc, const void* x, void* out, int64_t n, int64_t c, int64_t h,
+                         int64_t w, int64_t sh, int64_t sw, int64_t hu, int64_t wu, void* stream);
+
+/* avg_pool2d_grad_internal on channels-last dy [N,Ho,Wo,C] -> dx [N,H,W,C] (C*itemsize % 16 == 0), geom as fh_pool2d;
+ * the reference's summation order, bit-identical to fh_pool2d_grad mode 1. For backward graphs whose activations
+ * stay channels-last; no counterpart in the reference. */
+fh_status fh_avg_pool2d_grad_nhwc(int32_t dtype, const void* dy, void* dx, const int64_t geom[10], void* stream);
 
 /* sum over the axes flagged in reduced[0..rank) (rank <= 8; every axis for the reference's axes = []), output dense
  * with the reduced axes dropped (keepdims only adds size-1 dims, same layout). fp32 tree per output.

@@ -288,3 +288,18 @@ def test_grad_input_lowering(dtype):
     t = lowered((8, 64, 57, 57), (128, 64, 1, 1), 2, 0)  # odd size: one trailing zero row/column in the dilation
     assert "[8,57,57,128]" in t
     assert "conv2d_grad_input_internal" in lowered((8, 64, 56, 56), (64, 32, 3, 3), 1, 1, groups=2)
+
+
+def test_resnet_training_graph_stays_channels_last():
+    """The backward of ResNet-18 reads and writes channels-last activations: conv gradients take NHWC x / dy, the
+    transposed convolutions write NHWC, relu_grad / add / bias sums run on NHWC, the global average-pool gradient
+    has an NHWC kernel. What is left NCHW is the stem (its max-pool gradient kernel is NCHW) and graph inputs."""
+    g, specs = graphs.resnet18(batch=8, dtype=BF16, image=64, train=True)
+    low = host.hip_lowered(host.backward(g.text(), 0, list(range(1, len(specs) + 1))), 1)
+    assert low.count("hip_channels_last_internal(") <= 13, low.count("hip_channels_last_internal(")
+    assert "hip_avg_pool2d_grad_nhwc_internal" in low
+    assert low.count("hip_conv2d_wgrad_nhwc_internal") == 20
+    assert 'in_nhwc=1' in low  # strided grad_input dilates a channels-last dy
+    sums = [l for l in low.splitlines() if " = sum(" in l]
+    # bias gradients over N, H, W of NHWC data; the stem's (NCHW) keeps [0, 2, 3]
+    assert len(sums) == 17 and sum("axes=[0, 1, 2]" in l for l in sums) >= 16  # 17 convs carry a bias
