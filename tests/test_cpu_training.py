@@ -301,5 +301,5 @@ def test_resnet_training_graph_stays_channels_last():
     assert low.count("hip_conv2d_wgrad_nhwc_internal") == 20
     assert 'in_nhwc=1' in low  # strided grad_input dilates a channels-last dy
     sums = [l for l in low.splitlines() if " = sum(" in l]
-    # bias gradients over N, H, W of NHWC data; the stem's (NCHW) keeps [0, 2, 3]
-    assert len(sums) == 17 and sum("axes=[0, 1, 2]" in l for l in sums) >= 16  # 17 convs carry a bias
+    # bias gradients over N, H, W of NHWC data; the stem region (NCHW, next to the max-pool gradient) keeps [0, 2, 3]
+    assert len(sums) == 17 and sum("axes=[0, 1, 2]" in l for l in sums) >= 14  # 17 biased convs; stem region NCHW
