@@ -7,6 +7,8 @@
 // bit-identical and 16-bit ones differ only if the reference's single final rounding does (it does not: same
 // float, same rounding). sum and mse_loss are tree reductions in fp32 (deterministic, not in the reference's
 // order); their parity is a tolerance.
+#include <algorithm>
+
 #include "fh_common.h"
 
 namespace fh {
@@ -504,6 +506,67 @@ __global__ __launch_bounds__(kSumThreads) void sum_kernel(const typename Io<T>::
   }
 }
 
+// Column sums of a dense [rows, cols] tensor (cols * itemsize % 16 == 0): the bias gradient of channels-last data.
+// Stage 1: workgroup w sums rows [w*R, (w+1)*R) for every column, lanes holding 16-byte column vectors and striding
+// over rows, then a fixed LDS tree over the lanes that share a column vector; fp32 partials to part[w][cols].
+// Stage 2: out[c] = round(sum over w in order of part[w][c]).
+template <typename T>
+__global__ __launch_bounds__(kThreads) void sum_rows_partial_kernel(const typename Io<T>::storage* __restrict__ x,
+                                                                    float* __restrict__ part, int64_t rows, int32_t cols,
+                                                                    int64_t rows_per_wg) {
+  using S = typename Io<T>::storage;
+  constexpr int V = 16 / sizeof(S);
+  __shared__ float red[kThreads * V];
+  const int32_t cv = cols / V;                       // column vectors
+  const int32_t lanes_per_row = min(cv, kThreads);   // threads covering one row
+  const int32_t row_step = kThreads / lanes_per_row;  // rows in flight per iteration
+  const int32_t t = threadIdx.x;
+  const int32_t rsub = t / lanes_per_row, vcol = t % lanes_per_row;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * rows_per_wg, r1 = min(rows, r0 + rows_per_wg);
+  // the same trip count for every thread (the loop holds barriers)
+  for (int32_t base = 0; base < cv; base += lanes_per_row) {
+    const int32_t vc = base + vcol;
+    const bool col_ok = vc < cv;
+    float acc[V];
+#pragma unroll
+    for (int k = 0; k < V; ++k) acc[k] = 0.0f;
+    if (rsub < row_step && col_ok) {
+      for (int64_t r = r0 + rsub; r < r1; r += row_step) {
+        const uint4 w = *reinterpret_cast<const uint4*>(x + r * cols + static_cast<int64_t>(vc) * V);
+        const S* e = reinterpret_cast<const S*>(&w);
+#pragma unroll
+        for (int k = 0; k < V; ++k) acc[k] += Io<T>::load(e[k]);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < V; ++k) red[t * V + k] = acc[k];
+    __syncthreads();
+    if (rsub == 0 && col_ok) {
+      // lanes rsub = 0 .. row_step-1 with this vcol, added in rsub order
+      for (int k = 0; k < V; ++k) {
+        float s = 0.0f;
+        for (int32_t q = 0; q < row_step; ++q) s += red[(q * lanes_per_row + vcol) * V + k];
+        part[static_cast<int64_t>(blockIdx.x) * cols + static_cast<int64_t>(vc) * V + k] = s;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// One wave per column: lane l adds partials l, l+64, ... in order, then a fixed xor-shuffle tree.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void sum_rows_final_kernel(const float* __restrict__ part,
+                                                                  typename Io<T>::storage* __restrict__ out, int32_t wgs,
+                                                                  int32_t cols) {
+  const int32_t c = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
+  const int32_t lane = threadIdx.x & 63;
+  if (c >= cols) return;
+  float s = 0.0f;
+  for (int32_t w = lane; w < wgs; w += 64) s += part[static_cast<int64_t>(w) * cols + c];
+  for (int m = 32; m >= 1; m >>= 1) s += __shfl_xor(s, m);
+  if (lane == 0) out[c] = Io<T>::store(s);
+}
+
 // gx[i] = gy[projection of i]: a copy of the storage bits.
 template <typename S>
 __global__ __launch_bounds__(kThreads) void sum_grad_kernel(const S* __restrict__ gy, S* __restrict__ gx, ReduceG g,
@@ -922,4 +985,51 @@ extern "C" fh_status fh_avg_pool2d_grad_nhwc(int32_t dtype, const void* dy, void
       break;
   }
   return launch_status("fh_avg_pool2d_grad_nhwc");
+}
+
+namespace {
+// rows per stage-1 workgroup: about 256 workgroups, 64 .. 65536 rows each
+int64_t sum_rows_per_wg(int64_t rows) { return std::min<int64_t>(65536, std::max<int64_t>(64, (rows + 255) / 256)); }
+}  // namespace
+
+extern "C" int64_t fh_sum_rows_workspace(int32_t dtype, int64_t rows, int64_t cols) {
+  if (!is_supported_float(dtype) || rows <= 0 || cols <= 0 || (cols * dtype_size(dtype)) % 16 != 0 || cols > (1 << 24))
+    return -1;
+  const int64_t per = sum_rows_per_wg(rows);
+  const int64_t wgs = (rows + per - 1) / per;
+  if (wgs > 0x7fffffffLL) return -1;
+  return wgs * cols * 4;
+}
+
+extern "C" fh_status fh_sum_rows(int32_t dtype, const void* x, void* out, int64_t rows, int64_t cols, void* workspace,
+                                 int64_t workspace_bytes, void* stream) {
+  const int64_t need = fh_sum_rows_workspace(dtype, rows, cols);
+  if (need < 0) return fail(FH_UNIMPLEMENTED, "fh_sum_rows: unsupported dtype or shape (cols*itemsize % 16 != 0)");
+  if (workspace_bytes < need) return fail(FH_INVALID_ARGUMENT, "fh_sum_rows: workspace too small");
+  if (x == nullptr || out == nullptr || workspace == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_sum_rows: null pointer");
+  if (reinterpret_cast<uintptr_t>(x) % 16 != 0) return fail(FH_INVALID_ARGUMENT, "fh_sum_rows: x must be 16-byte aligned");
+  const int64_t per = sum_rows_per_wg(rows);
+  const int32_t wgs = static_cast<int32_t>((rows + per - 1) / per);
+  const int32_t c = static_cast<int32_t>(cols);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  float* part = static_cast<float*>(workspace);
+  const dim3 fgrid(static_cast<uint32_t>((cols + kThreads / 64 - 1) / (kThreads / 64)));
+  switch (dtype) {
+    case FH_F32:
+      hipLaunchKernelGGL((sum_rows_partial_kernel<float>), dim3(wgs), dim3(kThreads), 0, s, static_cast<const float*>(x), part,
+                         rows, c, per);
+      hipLaunchKernelGGL((sum_rows_final_kernel<float>), fgrid, dim3(kThreads), 0, s, part, static_cast<float*>(out), wgs, c);
+      break;
+    case FH_BF16:
+      hipLaunchKernelGGL((sum_rows_partial_kernel<bf16_t>), dim3(wgs), dim3(kThreads), 0, s, static_cast<const uint16_t*>(x),
+                         part, rows, c, per);
+      hipLaunchKernelGGL((sum_rows_final_kernel<bf16_t>), fgrid, dim3(kThreads), 0, s, part, static_cast<uint16_t*>(out), wgs, c);
+      break;
+    default:
+      hipLaunchKernelGGL((sum_rows_partial_kernel<f16_t>), dim3(wgs), dim3(kThreads), 0, s, static_cast<const uint16_t*>(x),
+                         part, rows, c, per);
+      hipLaunchKernelGGL((sum_rows_final_kernel<f16_t>), fgrid, dim3(kThreads), 0, s, part, static_cast<uint16_t*>(out), wgs, c);
+      break;
+  }
+  return launch_status("fh_sum_rows");
 }

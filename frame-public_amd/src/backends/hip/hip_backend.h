@@ -135,6 +135,9 @@ inline constexpr std::string_view kPackFilterC8Op = "hip_pack_filter_c8_internal
 // [N,Hu,Wu,Cout] (fh_dilate_nhwc; attribute stride).
 inline constexpr std::string_view kFilterFlipOp = "hip_conv_filter_flip_internal";
 inline constexpr std::string_view kDilateNhwcOp = "hip_dilate_nhwc_internal";  // attr in_nhwc = 1: dy channels-last
+// sum over every axis but the last (the bias gradient of channels-last data or of [rows, features]): outputs the
+// sum and an fp32 workspace of per-workgroup partials (see fh_sum_rows).
+inline constexpr std::string_view kSumRowsOp = "hip_sum_rows_internal";
 // avg_pool2d_grad_internal on channels-last dy / dx (same attributes; see fh_avg_pool2d_grad_nhwc).
 inline constexpr std::string_view kAvgPoolGradNhwcOp = "hip_avg_pool2d_grad_nhwc_internal";
 // conv2d_grad_filter_internal on MFMA: inputs x channels-last [N,H,W,cin_pad] and dy channels-last [N,Ho,Wo,Cout];

@@ -560,6 +560,31 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
       if (op == "avg_pool2d_grad_internal") op = std::string(kAvgPoolGradNhwcOp);
     }
     const bool sum_nhwc = op == "sum" && nhwc.count(n->inputs()[0]);
+    if (op == "sum") {
+      // every axis but the last of the (lowered) input reduced: the two-pass column sum
+      const Shape& xs = ins[0]->type().shape;
+      const auto* ax = attr_of<std::vector<int64_t>>(n, "axes");
+      const auto* kd = attr_of<bool>(n, "keepdims");
+      std::vector<int64_t> axes = sum_nhwc ? *nhwc_sum_axes(n) : (ax ? *ax : std::vector<int64_t>{});
+      bool rows_form = ax != nullptr && !(kd && *kd) && xs.rank() >= 2 && static_cast<int64_t>(axes.size()) == xs.rank() - 1;
+      for (size_t i = 0; rows_form && i < axes.size(); ++i) rows_form = axes[i] == static_cast<int64_t>(i);
+      const ir::TensorType& xt = ins[0]->type();
+      const int32_t dt = xt.dtype.code() == DTypeCode::kBFloat16  ? FH_BF16
+                         : xt.dtype.code() == DTypeCode::kFloat16 ? FH_F16
+                         : xt.dtype.code() == DTypeCode::kFloat32 ? FH_F32
+                                                                  : -1;
+      const int64_t cols = rows_form ? xs.dim(xs.rank() - 1) : 0;
+      const int64_t ws = rows_form && dt >= 0 ? fh_sum_rows_workspace(dt, xs.numel() / std::max<int64_t>(cols, 1), cols) : -1;
+      if (ws > 0 && xs.numel() / cols >= 256) {
+        ir::TensorType wst = types[0];
+        wst.dtype = DType::of<float>();
+        wst.shape = Shape({ws / 4});
+        Result<ir::Node*> c = out.create_node(std::string(kSumRowsOp), std::move(ins), {types[0], wst});
+        if (!c.is_ok()) return c.status();
+        map[&n->outputs()[0]] = c.value()->output(0);
+        continue;
+      }
+    }
     Result<ir::Node*> c = out.create_node(op, std::move(ins), std::move(types));
     if (!c.is_ok()) return c.status();
     for (const auto& [k, v] : n->attrs()) c.value()->set_attr(k, v);

@@ -496,6 +496,22 @@ Status conv_grad_kernel(KernelContext& ctx) {
   return Status::ok();
 }
 
+// Sum over every axis but the last (kSumRowsOp); output 1 is the partials workspace.
+Status sum_rows_kernel(KernelContext& ctx) {
+  const std::string op(kSumRowsOp);
+  if (ctx.inputs.size() != 1 || ctx.outputs.size() != 2) return invalid(op, "expects 1 input and 2 outputs");
+  const Shape& x = ctx.inputs[0].shape();
+  if (x.rank() < 1 || !(ctx.inputs[0].dtype() == ctx.outputs[0].dtype())) return invalid(op, "operand shapes");
+  const int64_t cols = x.dim(x.rank() - 1);
+  if (ctx.outputs[0].numel() != cols) return invalid(op, "output must hold one value per column");
+  Result<int32_t> dt = float_code(op, ctx.outputs[0].dtype());
+  if (!dt.is_ok()) return dt.status();
+  FRAME_HIP_RETURN_IF_ERROR(fh_sum_rows(dt.value(), ctx.inputs[0].raw_data(), ctx.outputs[0].raw_data(), x.numel() / cols, cols,
+                                        ctx.outputs[1].raw_data(), ctx.outputs[1].numel() * 4, stream_handle(ctx)),
+                            "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
 // avg_pool2d_grad_internal on channels-last dy [N,Ho,Wo,C] -> dx [N,H,W,C] (kAvgPoolGradNhwcOp).
 Status avg_pool_grad_nhwc_kernel(KernelContext& ctx) {
   const std::string op(kAvgPoolGradNhwcOp);
@@ -810,6 +826,7 @@ FRAME_REGISTER_KERNEL("conv2d_grad_filter_internal", kHipBackendName, &conv_grad
 FRAME_REGISTER_KERNEL(kFilterFlipOp, kHipBackendName, &filter_flip_kernel);
 FRAME_REGISTER_KERNEL(kConvWgradOp, kHipBackendName, &conv_wgrad_kernel);
 FRAME_REGISTER_KERNEL(kAvgPoolGradNhwcOp, kHipBackendName, &avg_pool_grad_nhwc_kernel);
+FRAME_REGISTER_KERNEL(kSumRowsOp, kHipBackendName, &sum_rows_kernel);
 FRAME_REGISTER_KERNEL(kDilateNhwcOp, kHipBackendName, &dilate_nhwc_kernel);
 FRAME_REGISTER_KERNEL("sum", kHipBackendName, &sum_kernel<0>);
 FRAME_REGISTER_KERNEL("sum_grad_internal", kHipBackendName, &sum_kernel<1>);

@@ -297,6 +297,14 @@ fh_status fh_avg_pool2d_grad_nhwc(int32_t dtype, const void* dy, void* dx, const
 fh_status fh_sum(int32_t dtype, const void* x, void* out, int32_t rank, const int64_t* dims, const uint8_t* reduced,
                  void* stream);
 
+/* sum over every axis but the last of a dense tensor viewed as [rows, cols] (cols*itemsize % 16 == 0): the bias
+ * gradient of channels-last activations. Per-workgroup fp32 partials (about 256 workgroups) in `workspace`
+ * (fh_sum_rows_workspace bytes, -1 if unsupported), then summed in workgroup order; deterministic. Replaces
+ * sum_cuda_kernel for that shape (reference: src/backends/cuda/kernels/reduction.cu:322-460). */
+int64_t fh_sum_rows_workspace(int32_t dtype, int64_t rows, int64_t cols);
+fh_status fh_sum_rows(int32_t dtype, const void* x, void* out, int64_t rows, int64_t cols, void* workspace,
+                      int64_t workspace_bytes, void* stream);
+
 /* sum_grad_internal: gx (dims) = gy broadcast along the reduced axes, a copy of the stored bits
  * (reference: src/backends/cpu/kernels/reduction.cpp:378-388; the CUDA backend has no kernel for it and falls
  * back to the CPU). */

@@ -183,7 +183,9 @@ def test_pool_grads(dev, dtype, case):
 
 SUM_CASES = [((4, 6, 5, 7), [0, 2, 3], False), ((4, 6, 5, 7), [], False), ((33, 1000), [1], True),
              ((33, 1000), [0], False), ((8, 3, 300), [0, 2], False), ((1 << 20,), [], False),
-             ((8, 64, 28, 28), [0, 2, 3], False), ((3, 5, 9, 9), [0, 2, 3], True)]
+             ((8, 64, 28, 28), [0, 2, 3], False), ((3, 5, 9, 9), [0, 2, 3], True),
+             # every axis but the last, >= 256 rows: the two-pass column sum (hip_sum_rows_internal)
+             ((5000, 64), [0], False), ((4096, 24), [0], False), ((300, 8, 8), [0, 1], False)]
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
