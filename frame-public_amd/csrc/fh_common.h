@@ -121,7 +121,8 @@ struct Io<f16_t> {
 // 1.2e-7 for all z): erfc(z) = t exp(-z^2 + P(t)), t = 1 / (1 + z / 2). In fp32 the result is within 1e-6
 // relative of the exact function for |x| < 5 (7e-6 at x = -10, where exp(-z^2) itself limits), and it keeps
 // relative accuracy in the negative tail, where 1 + erff(z) cancels to zero. About 20 instructions, no branch.
-__device__ inline float gelu_erfc(float x) {
+// erfc(|x| / sqrt 2) by the Numerical Recipes erfcc fit (see above).
+__device__ inline float erfc_scaled_abs(float x) {
   const float z = __builtin_fabsf(x) * 0.70710678118654752440f;
   const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.5f, z, 1.0f));
   float p = 0.17087277f;
@@ -134,7 +135,11 @@ __device__ inline float gelu_erfc(float x) {
   p = __builtin_fmaf(p, t, 0.37409196f);
   p = __builtin_fmaf(p, t, 1.00002368f);
   p = __builtin_fmaf(p, t, -1.26551223f);
-  const float erfc_z = t * __expf(__builtin_fmaf(-z, z, p));
+  return t * __expf(__builtin_fmaf(-z, z, p));
+}
+
+__device__ inline float gelu_erfc(float x) {
+  const float erfc_z = erfc_scaled_abs(x);
   return 0.5f * x * (x >= 0.0f ? 2.0f - erfc_z : erfc_z);
 }
 
@@ -148,18 +153,40 @@ __device__ inline float ew_unary(uint8_t op, float x) {
       return x * x;
     case FH_EW_GELU:
       return gelu_erfc(x);
+    case FH_EW_SIGMOID:
+      if (x >= 0.0f) return 1.0f / (1.0f + __expf(-x));
+      return __expf(x) / (1.0f + __expf(x));
+    case FH_EW_TANH:
+      return tanhf(x);
+    case FH_EW_RSQRT:
+      return 1.0f / sqrtf(x);  // both correctly rounded: the reference's 1.0f / std::sqrt(x)
     default:
       return x;
   }
 }
 
+// d/dx gelu(x) = Phi(x) + x phi(x), Phi from the same erfc fit as gelu_erfc (1 + erf(z) = 2 - erfc(|z|) or
+// erfc(|z|)), phi(x) = exp(-x^2/2) / sqrt(2 pi).
+__device__ inline float gelu_grad(float x, float gy) {
+  const float erfc_z = erfc_scaled_abs(x);
+  const float cdf = x >= 0.0f ? 1.0f - 0.5f * erfc_z : 0.5f * erfc_z;
+  return gy * (cdf + x * (__expf(-0.5f * x * x) * 0.39894228040143267794f));
+}
+
 __device__ inline float ew_binary(uint8_t op, float a, float b) {
   if (op == FH_EW_RELU_GRAD) return a > 0.0f ? b : 0.0f;
+  if (op == FH_EW_GELU_GRAD) return gelu_grad(a, b);
   return op == FH_EW_MUL ? a * b : a + b;
 }
 
+// Ops a GEMM / conv epilogue program may hold: add, mul and the unary ops (the gradient ops never follow a
+// contraction in epilogue position).
+__host__ __device__ constexpr bool epilogue_op_ok(uint8_t op) {
+  return (op >= FH_EW_ADD && op <= FH_EW_GELU) || (op >= FH_EW_SIGMOID && op <= FH_EW_RSQRT);
+}
+
 __host__ __device__ constexpr bool ew_is_binary(uint8_t op) {
-  return op == FH_EW_ADD || op == FH_EW_MUL || op == FH_EW_RELU_GRAD;
+  return op == FH_EW_ADD || op == FH_EW_MUL || op == FH_EW_RELU_GRAD || op == FH_EW_GELU_GRAD;
 }
 
 // The fused elementwise program of a GEMM / conv epilogue (EpilogueArgs, ConvEpilogue: nseg, round_between,

@@ -108,7 +108,7 @@ extern "C" fh_status fh_conv2d_fwd(int32_t dtype, const void* x, const void* w, 
     ep.nseg = epilogue->nseg;
     ep.round_between = epilogue->round_between;
     for (int s = 0; s < ep.nseg; ++s) {
-      if (epilogue->ops[s] < FH_EW_ADD || epilogue->ops[s] > FH_EW_GELU)
+      if (!epilogue_op_ok(epilogue->ops[s]))
         return fail(FH_INVALID_ARGUMENT, "fh_conv2d_fwd: unknown epilogue op");
       if (ew_is_binary(epilogue->ops[s]) && epilogue->ins[s] == nullptr)
         return fail(FH_INVALID_ARGUMENT, "fh_conv2d_fwd: binary epilogue segment without operand");

@@ -763,7 +763,7 @@ extern "C" fh_status fh_conv2d_nhwc_fwd_ex(int32_t dtype, const void* x_nhwc, co
     a.ep.round_between = epilogue->round_between;
     for (int s = 0; s < a.ep.nseg; ++s) {
       const uint8_t op = epilogue->ops[s];
-      if (op < FH_EW_ADD || op > FH_EW_GELU) return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd: unknown epilogue op");
+      if (!epilogue_op_ok(op)) return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd: unknown epilogue op");
       if (ew_is_binary(op) && epilogue->ins[s] == nullptr)
         return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd: binary epilogue segment without operand");
       a.ep.ops[s] = op;

@@ -214,7 +214,8 @@ __global__ __launch_bounds__(kEwThreads) void ew_vec_kernel(EwArgs a) {
       switch (op) {
         case FH_EW_ADD:
         case FH_EW_MUL:
-        case FH_EW_RELU_GRAD: {
+        case FH_EW_RELU_GRAD:
+        case FH_EW_GELU_GRAD: {
           ew_u4 t = cur[0];
 #pragma unroll
           for (int k = 1; k < NIN; ++k)
@@ -224,9 +225,9 @@ __global__ __launch_bounds__(kEwThreads) void ew_vec_kernel(EwArgs a) {
           if (op == FH_EW_ADD) {
 #pragma unroll
             for (int e = 0; e < V; ++e) v[e] = v[e] + w[e];
-          } else if (op == FH_EW_RELU_GRAD) {
+          } else if (op != FH_EW_MUL) {
 #pragma unroll
-            for (int e = 0; e < V; ++e) v[e] = v[e] > 0.0f ? w[e] : 0.0f;
+            for (int e = 0; e < V; ++e) v[e] = ew_binary(op, v[e], w[e]);
           } else {
 #pragma unroll
             for (int e = 0; e < V; ++e) v[e] = v[e] * w[e];
@@ -298,7 +299,7 @@ __global__ __launch_bounds__(kEwThreads) void ew_fixed_kernel(EwArgs a) {
               L::unpack(cur[in_idx], w);
 #pragma unroll
               for (int e = 0; e < V; ++e)
-                v[e] = op == FH_EW_ADD ? v[e] + w[e] : op == FH_EW_MUL ? v[e] * w[e] : (v[e] > 0.0f ? w[e] : 0.0f);
+                v[e] = op == FH_EW_ADD ? v[e] + w[e] : op == FH_EW_MUL ? v[e] * w[e] : ew_binary(op, v[e], w[e]);
             } else if constexpr (op == FH_EW_RELU) {
 #pragma unroll
               for (int e = 0; e < V; ++e) v[e] = (v[e] < 0.0f) ? 0.0f : v[e];
@@ -340,6 +341,10 @@ bool launch_fixed(const EwArgs& a, dim3 grid, hipStream_t stream) {
       case FH_EW_GELU: FH_EW_FIXED(FH_EW_GELU);
       case FH_EW_SQUARE: FH_EW_FIXED(FH_EW_SQUARE);
       case FH_EW_RELU_GRAD: FH_EW_FIXED(FH_EW_RELU_GRAD);
+      case FH_EW_GELU_GRAD: FH_EW_FIXED(FH_EW_GELU_GRAD);
+      case FH_EW_SIGMOID: FH_EW_FIXED(FH_EW_SIGMOID);
+      case FH_EW_TANH: FH_EW_FIXED(FH_EW_TANH);
+      case FH_EW_RSQRT: FH_EW_FIXED(FH_EW_RSQRT);
       default: return false;
     }
   }
@@ -477,7 +482,7 @@ extern "C" fh_status fh_ew_program(int32_t dtype, int32_t nseg, const uint8_t* o
   int expected = 0;
   for (int s = 0; s < nseg; ++s) {
     const uint8_t op = ops[s];
-    if (op < FH_EW_ADD || op > FH_EW_RELU_GRAD)
+    if (op < FH_EW_ADD || op > FH_EW_GELU_GRAD)
       return fail(FH_INVALID_ARGUMENT, "fh_ew_program: unknown op code " + std::to_string(op));
     const int want = ew_is_binary(op) ? 2 : 1;
     if (arities[s] != want)

@@ -436,7 +436,7 @@ fh_status copy_epilogue(const fh_epilogue* in, EpilogueArgs& out) {
   out.round_between = in->round_between;
   for (int s = 0; s < in->nseg; ++s) {
     const uint8_t op = in->ops[s];
-    if (op < FH_EW_ADD || op > FH_EW_GELU)
+    if (!epilogue_op_ok(op))
       return fail(FH_INVALID_ARGUMENT, "epilogue: unknown op code " + std::to_string(op));
     if (ew_is_binary(op) && in->ins[s] == nullptr)
       return fail(FH_INVALID_ARGUMENT, "epilogue: binary segment " + std::to_string(s) + " has no operand");

@@ -348,7 +348,10 @@ def resnet18_inputs(specs, batch=64, dtype=BF16, image=224, seed=401):
 
 # ---- C5: transformer encoder block (pre-LN, GELU) ---------------------------------------------------------------
 
-def transformer_block(batch=8, seq=512, d_model=1024, heads=16, ffn=4096, dtype=BF16, device="hip"):
+def transformer_block(batch=8, seq=512, d_model=1024, heads=16, ffn=4096, dtype=BF16, device="hip", act="gelu",
+                      train=False):
+    """C5's pre-LN block. act selects the FFN activation ("relu" gives a block the reference can also build);
+    train=True adds a target input [rows, d_model] after the parameters and outputs mse_loss(y, target)."""
     g = Graph(device)
     rows = batch * seq
     dh = d_model // heads
@@ -379,9 +382,13 @@ def transformer_block(batch=8, seq=512, d_model=1024, heads=16, ffn=4096, dtype=
     o = g.add(g.matmul(attn, p["wo"]), p["bo"])
     h = g.add(o, x)
     h2 = g.layer_norm(h, p["ln2_g"], p["ln2_b"])
-    f = g.gelu(g.add(g.matmul(h2, p["w1"]), p["b1"]))
+    pre = g.add(g.matmul(h2, p["w1"]), p["b1"])
+    f = g.gelu(pre) if act == "gelu" else g.relu(pre)
     y = g.add(g.add(g.matmul(f, p["w2"]), p["b2"]), h)
-    g.output(y)
+    if train:
+        g.output(g.mse_loss(y, g.input(dtype, (rows, d_model))))
+    else:
+        g.output(y)
     return g, shapes
 
 

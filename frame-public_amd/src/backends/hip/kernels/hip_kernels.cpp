@@ -77,7 +77,8 @@ Status run_program(const KernelContext& ctx, const std::string& op, const std::v
 
 template <uint8_t Code, int Arity>
 Status ew_kernel(KernelContext& ctx) {
-  static const std::string names[] = {"", "add", "mul", "relu", "square", "gelu", "relu_grad_internal"};
+  static const std::string names[] = {"",        "add",  "mul",   "relu", "square", "gelu", "relu_grad_internal",
+                                      "sigmoid", "tanh", "rsqrt", "gelu_grad_internal"};
   const std::string& op = names[Code];
   FRAME_RETURN_IF_ERROR(arity(ctx, op, Arity, 1));
   return run_program(ctx, op, {Code}, {static_cast<int8_t>(Arity)});
@@ -817,6 +818,10 @@ FRAME_REGISTER_KERNEL("slice", kHipBackendName, &slice_kernel);
 FRAME_REGISTER_KERNEL("concat", kHipBackendName, &concat_kernel);
 FRAME_REGISTER_KERNEL(ops::kConstantOpName, kHipBackendName, &constant_kernel);
 FRAME_REGISTER_KERNEL("relu_grad_internal", kHipBackendName, (&ew_kernel<FH_EW_RELU_GRAD, 2>));
+FRAME_REGISTER_KERNEL("gelu_grad_internal", kHipBackendName, (&ew_kernel<FH_EW_GELU_GRAD, 2>));
+FRAME_REGISTER_KERNEL("sigmoid", kHipBackendName, (&ew_kernel<FH_EW_SIGMOID, 1>));
+FRAME_REGISTER_KERNEL("tanh", kHipBackendName, (&ew_kernel<FH_EW_TANH, 1>));
+FRAME_REGISTER_KERNEL("rsqrt", kHipBackendName, (&ew_kernel<FH_EW_RSQRT, 1>));
 FRAME_REGISTER_KERNEL("matmul_grad_lhs_internal", kHipBackendName, &matmul_grad_kernel<0>);
 FRAME_REGISTER_KERNEL("matmul_grad_rhs_internal", kHipBackendName, &matmul_grad_kernel<1>);
 FRAME_REGISTER_KERNEL("max_pool2d_grad_internal", kHipBackendName, &pool_grad_kernel<0>);

@@ -106,7 +106,7 @@ bool fold_scalar(std::string_view op, const std::vector<float>& in, float& out) 
   else if (op == "relu") out = std::max(in[0], 0.0f);
   else if (op == "square") out = in[0] * in[0];
   else if (op == "gelu") out = 0.5f * in[0] * (1.0f + std::erf(in[0] * 0.70710678118654752440f));
-  else if (op == "sigmoid") out = 1.0f / (1.0f + std::exp(-in[0]));
+  else if (op == "sigmoid") out = in[0] >= 0.0f ? 1.0f / (1.0f + std::exp(-in[0])) : std::exp(in[0]) / (1.0f + std::exp(in[0]));
   else if (op == "tanh") out = std::tanh(in[0]);
   else if (op == "rsqrt") out = 1.0f / std::sqrt(in[0]);
   else return false;

@@ -6,7 +6,10 @@
 //   pool gradients + grad ops       src/ops/schemas/pool.cpp:230-420, 596-655
 //   sum / sum_grad_internal         src/ops/schemas/reduction.cpp:30-301
 //   mse_loss / mse_loss_grad        src/ops/schemas/loss.cpp:30-279
-//   reshape gradient                src/ops/schemas/shape.cpp (reshape_gradient)
+//   reshape / transpose / slice / concat gradients   src/ops/schemas/shape.cpp:60-410
+//   softmax / layer_norm gradients and their row-statistics helpers   src/ops/schemas/sequence.cpp:255-615
+//   sigmoid / tanh / rsqrt gradients   src/ops/schemas/elementwise.cpp:401-660
+// gelu and gelu_grad_internal are this build's own (the reference has no gelu).
 // Only first-order gradients are registered: the gradient-only ops carry no GradientFn here, so differentiating
 // a training graph a second time reports kUnimplemented naming the op.
 #include "gradients.h"
@@ -63,6 +66,11 @@ class Micro {
     Result<ir::Node*> n = create_node_with_inferred_types(g_, name, std::move(ins), attrs);
     if (!n.is_ok()) st_ = n.status();
     return n.is_ok() ? n.value()->output(0) : nullptr;
+  }
+  ir::Value* splat_shape(const ir::TensorType& like, const Shape& shape, double v) {
+    ir::TensorType t = like;
+    t.shape = shape;
+    return splat(t, v);
   }
   ir::Value* splat(const ir::TensorType& like, double v) {
     if (!st_.is_ok()) return nullptr;
@@ -330,6 +338,29 @@ Result<ir::Graph> mse_loss_gradient(const NodeContext& c) {
   return m.finish({gpred, gtarget});
 }
 
+// Row-statistics helpers of the softmax / layer_norm gradients (reference: src/ops/schemas/sequence.cpp:255-330):
+// mean over axis 1 = sum * splat(1/d); a per-row [n] vector broadcast to [n,d] = reshape [n,1] @ ones [1,d]; a
+// per-column [d] vector broadcast = ones [n,1] @ reshape [1,d]; a - b = a + (-1) * b.
+ir::Value* mean_axis1(Micro& m, ir::Value* x, const ir::TensorType& t, int64_t n, int64_t d) {
+  ir::Value* s = m.op("sum", {x}, {{"axes", std::vector<int64_t>{1}}});
+  ir::Value* r = m.splat_shape(t, Shape({n}), 1.0 / static_cast<double>(d));
+  return m.op("mul", {s, r});
+}
+ir::Value* bcast_col(Micro& m, ir::Value* v, const ir::TensorType& t, int64_t n, int64_t d) {
+  ir::Value* col = m.op("reshape", {v}, {{"target_shape", Shape({n, 1})}});
+  ir::Value* ones = m.splat_shape(t, Shape({1, d}), 1.0);
+  return m.op("matmul", {col, ones});
+}
+ir::Value* bcast_row(Micro& m, ir::Value* v, const ir::TensorType& t, int64_t n, int64_t d) {
+  ir::Value* row = m.op("reshape", {v}, {{"target_shape", Shape({1, d})}});
+  ir::Value* ones = m.splat_shape(t, Shape({n, 1}), 1.0);
+  return m.op("matmul", {ones, row});
+}
+ir::Value* minus(Micro& m, ir::Value* a, ir::Value* b, const ir::TensorType& t) {
+  ir::Value* neg = m.splat(t, -1.0);
+  return m.op("add", {a, m.op("mul", {neg, b})});
+}
+
 }  // namespace
 
 Result<ir::Graph> add_gradient(const NodeContext& c) {
@@ -411,6 +442,167 @@ Result<ir::Graph> reshape_gradient(const NodeContext& c) {
   Micro m("reshape_gradient");
   Fwd f = forward_inputs(m, c);
   return m.finish({m.op("reshape", {f.gy}, {{"target_shape", c.input_types[0].shape}})});
+}
+
+// softmax (reference: src/ops/schemas/sequence.cpp:358-406): t = softmax(x) recomputed,
+// gx = t * (gy - bcast_col(sum(t * gy, axis 1))).
+Result<ir::Graph> softmax_gradient(const NodeContext& c) {
+  FRAME_RETURN_IF_ERROR(expect(c, 1, "1 input"));
+  Micro m("softmax_gradient");
+  Fwd f = forward_inputs(m, c);
+  const ir::TensorType& t = c.input_types[0];
+  const int64_t n = t.shape.dim(0), d = t.shape.dim(1);
+  ir::Value* sm = m.op("softmax", {f.x[0]});
+  ir::Value* tg = m.op("mul", {sm, f.gy});
+  ir::Value* s = m.op("sum", {tg}, {{"axes", std::vector<int64_t>{1}}});
+  ir::Value* sb = bcast_col(m, s, t, n, d);
+  ir::Value* diff = minus(m, f.gy, sb, t);
+  return m.finish({m.op("mul", {sm, diff})});
+}
+
+// layer_norm (reference: src/ops/schemas/sequence.cpp:479-615): mean / variance / rsqrt recomputed from x, then
+// gx = r * ((a - mean(a)) - xhat * mean(a * xhat)) with a = gamma * gy; ggamma = sum(gy * xhat, axis 0);
+// gbeta = sum(gy, axis 0).
+Result<ir::Graph> layer_norm_gradient(const NodeContext& c) {
+  FRAME_RETURN_IF_ERROR(expect(c, 3, "3 inputs (x, gamma, beta)"));
+  const auto* eps = c.attr<double>("eps");
+  if (eps == nullptr) return bad("layer_norm", "gradient is missing attribute 'eps'");
+  Micro m("layer_norm_gradient");
+  Fwd f = forward_inputs(m, c);
+  const ir::TensorType& t = c.input_types[0];
+  const int64_t n = t.shape.dim(0), d = t.shape.dim(1);
+  ir::Value* mu = mean_axis1(m, f.x[0], t, n, d);
+  ir::Value* mub = bcast_col(m, mu, t, n, d);
+  ir::Value* cen = minus(m, f.x[0], mub, t);
+  ir::Value* sq = m.op("mul", {cen, cen});
+  ir::Value* var = mean_axis1(m, sq, t, n, d);
+  ir::Value* epsv = m.splat_shape(t, Shape({n}), *eps);
+  ir::Value* ve = m.op("add", {var, epsv});
+  ir::Value* r = m.op("rsqrt", {ve});
+  ir::Value* rb = bcast_col(m, r, t, n, d);
+  ir::Value* xhat = m.op("mul", {cen, rb});
+  ir::Value* gb = bcast_row(m, f.x[1], t, n, d);
+  ir::Value* a = m.op("mul", {gb, f.gy});
+  ir::Value* ma = mean_axis1(m, a, t, n, d);
+  ir::Value* mab = bcast_col(m, ma, t, n, d);
+  ir::Value* ax = m.op("mul", {a, xhat});
+  ir::Value* max = mean_axis1(m, ax, t, n, d);
+  ir::Value* maxb = bcast_col(m, max, t, n, d);
+  ir::Value* term1 = minus(m, a, mab, t);
+  ir::Value* xm = m.op("mul", {xhat, maxb});
+  ir::Value* term = minus(m, term1, xm, t);
+  ir::Value* gx = m.op("mul", {rb, term});
+  ir::Value* gyx = m.op("mul", {f.gy, xhat});
+  ir::Value* gg = m.op("sum", {gyx}, {{"axes", std::vector<int64_t>{0}}});
+  ir::Value* gbeta = m.op("sum", {f.gy}, {{"axes", std::vector<int64_t>{0}}});
+  return m.finish({gx, gg, gbeta});
+}
+
+// transpose (reference: src/ops/schemas/shape.cpp:150-185): transpose of gy by the inverse permutation.
+Result<ir::Graph> transpose_gradient(const NodeContext& c) {
+  FRAME_RETURN_IF_ERROR(expect(c, 1, "1 input"));
+  const auto* perm = c.attr<std::vector<int64_t>>("perm");
+  if (perm == nullptr) return bad("transpose", "gradient is missing attribute 'perm'");
+  std::vector<int64_t> inv(perm->size());
+  for (size_t i = 0; i < perm->size(); ++i) inv[static_cast<size_t>((*perm)[i])] = static_cast<int64_t>(i);
+  Micro m("transpose_gradient");
+  Fwd f = forward_inputs(m, c);
+  return m.finish({m.op("transpose", {f.gy}, {{"perm", inv}})});
+}
+
+// concat (reference: src/ops/schemas/shape.cpp:240-290): each input's gradient is its slice of gy along the axis.
+Result<ir::Graph> concat_gradient(const NodeContext& c) {
+  if (c.input_types.empty()) return bad("concat", "gradient expects at least 1 input, got 0");
+  const auto* axis = c.attr<int64_t>("axis");
+  if (axis == nullptr) return bad("concat", "gradient is missing attribute 'axis'");
+  Micro m("concat_gradient");
+  Fwd f = forward_inputs(m, c);
+  std::vector<ir::Value*> outs;
+  int64_t start = 0;
+  for (const auto& t : c.input_types) {
+    const int64_t stop = start + t.shape.dim(*axis);
+    outs.push_back(m.op("slice", {f.gy}, {{"axis", *axis}, {"start", start}, {"stop", stop}}));
+    start = stop;
+  }
+  return m.finish(outs);
+}
+
+// slice (reference: src/ops/schemas/shape.cpp:352-410): gy concatenated between zero blocks of the cut-off parts.
+Result<ir::Graph> slice_gradient(const NodeContext& c) {
+  FRAME_RETURN_IF_ERROR(expect(c, 1, "1 input"));
+  const auto* axis = c.attr<int64_t>("axis");
+  const auto* start = c.attr<int64_t>("start");
+  const auto* stop = c.attr<int64_t>("stop");
+  if (axis == nullptr || start == nullptr || stop == nullptr) return bad("slice", "gradient is missing attributes");
+  Micro m("slice_gradient");
+  Fwd f = forward_inputs(m, c);
+  const ir::TensorType& t = c.input_types[0];
+  const int64_t dim = t.shape.dim(*axis);
+  std::vector<ir::Value*> parts;
+  if (*start > 0) {
+    std::vector<int64_t> dims = t.shape.dims();
+    dims[static_cast<size_t>(*axis)] = *start;
+    parts.push_back(m.splat_shape(t, Shape(dims), 0.0));
+  }
+  parts.push_back(f.gy);
+  if (*stop < dim) {
+    std::vector<int64_t> dims = t.shape.dims();
+    dims[static_cast<size_t>(*axis)] = dim - *stop;
+    parts.push_back(m.splat_shape(t, Shape(dims), 0.0));
+  }
+  return m.finish({m.op("concat", parts, {{"axis", *axis}})});
+}
+
+// sigmoid (reference: src/ops/schemas/elementwise.cpp:401-470): s = sigmoid(x) recomputed, gx = gy * (s * (1 - s)).
+Result<ir::Graph> sigmoid_gradient(const NodeContext& c) {
+  FRAME_RETURN_IF_ERROR(expect(c, 1, "1 input"));
+  Micro m("sigmoid_gradient");
+  Fwd f = forward_inputs(m, c);
+  const ir::TensorType& t = c.input_types[0];
+  ir::Value* s = m.op("sigmoid", {f.x[0]});
+  ir::Value* one = m.splat(t, 1.0);
+  ir::Value* neg = m.splat(t, -1.0);
+  ir::Value* ns = m.op("mul", {neg, s});
+  ir::Value* oms = m.op("add", {one, ns});
+  ir::Value* ss = m.op("mul", {s, oms});
+  return m.finish({m.op("mul", {f.gy, ss})});
+}
+
+// tanh (reference: src/ops/schemas/elementwise.cpp:550-605): gx = gy * (1 - tanh(x)^2).
+Result<ir::Graph> tanh_gradient(const NodeContext& c) {
+  FRAME_RETURN_IF_ERROR(expect(c, 1, "1 input"));
+  Micro m("tanh_gradient");
+  Fwd f = forward_inputs(m, c);
+  const ir::TensorType& t = c.input_types[0];
+  ir::Value* th = m.op("tanh", {f.x[0]});
+  ir::Value* t2 = m.op("mul", {th, th});
+  ir::Value* neg = m.splat(t, -1.0);
+  ir::Value* nt2 = m.op("mul", {neg, t2});
+  ir::Value* one = m.splat(t, 1.0);
+  ir::Value* omt = m.op("add", {one, nt2});
+  return m.finish({m.op("mul", {f.gy, omt})});
+}
+
+// rsqrt (reference: src/ops/schemas/elementwise.cpp:612-660): gx = gy * (-0.5 * r^3), r = rsqrt(x) recomputed.
+Result<ir::Graph> rsqrt_gradient(const NodeContext& c) {
+  FRAME_RETURN_IF_ERROR(expect(c, 1, "1 input"));
+  Micro m("rsqrt_gradient");
+  Fwd f = forward_inputs(m, c);
+  const ir::TensorType& t = c.input_types[0];
+  ir::Value* r = m.op("rsqrt", {f.x[0]});
+  ir::Value* r2 = m.op("mul", {r, r});
+  ir::Value* r3 = m.op("mul", {r2, r});
+  ir::Value* nh = m.splat(t, -0.5);
+  ir::Value* coeff = m.op("mul", {nh, r3});
+  return m.finish({m.op("mul", {f.gy, coeff})});
+}
+
+// gelu (this build's op; no reference counterpart): gx = gelu_grad_internal(x, gy) = gy * (Phi(x) + x * phi(x)).
+Result<ir::Graph> gelu_gradient(const NodeContext& c) {
+  FRAME_RETURN_IF_ERROR(expect(c, 1, "1 input"));
+  Micro m("gelu_gradient");
+  Fwd f = forward_inputs(m, c);
+  return m.finish({m.op("gelu_grad_internal", {f.x[0], f.gy})});
 }
 
 }  // namespace frame::ops::schemas
@@ -505,3 +697,9 @@ FRAME_REGISTER_OP("mse_loss_grad_internal")
     .input("gy", "upstream gradient of mse_loss's scalar output")
     .output("gpred", "2 * gy / numel * (pred - target)")
     .shape_infer(&fs::infer_mse_loss_grad);
+
+FRAME_REGISTER_OP("gelu_grad_internal")
+    .input("x", "gelu's original input")
+    .input("gy", "upstream gradient of gelu's output (same shape/dtype as x)")
+    .output("gx", "gy * (Phi(x) + x * phi(x)), the derivative of 0.5 x (1 + erf(x / sqrt 2))")
+    .shape_infer(&fs::infer_relu_grad);

@@ -16,5 +16,14 @@ Result<ir::Graph> conv2d_gradient(const NodeContext& ctx);
 Result<ir::Graph> max_pool2d_gradient(const NodeContext& ctx);
 Result<ir::Graph> avg_pool2d_gradient(const NodeContext& ctx);
 Result<ir::Graph> reshape_gradient(const NodeContext& ctx);
+Result<ir::Graph> softmax_gradient(const NodeContext& ctx);
+Result<ir::Graph> layer_norm_gradient(const NodeContext& ctx);
+Result<ir::Graph> transpose_gradient(const NodeContext& ctx);
+Result<ir::Graph> concat_gradient(const NodeContext& ctx);
+Result<ir::Graph> slice_gradient(const NodeContext& ctx);
+Result<ir::Graph> sigmoid_gradient(const NodeContext& ctx);
+Result<ir::Graph> tanh_gradient(const NodeContext& ctx);
+Result<ir::Graph> rsqrt_gradient(const NodeContext& ctx);
+Result<ir::Graph> gelu_gradient(const NodeContext& ctx);
 
 }  // namespace frame::ops::schemas

@@ -321,11 +321,15 @@ FRAME_REGISTER_OP("gelu")
     .output("out", "0.5 * x * (1 + erf(x / sqrt(2)))")
     .trait(OpTrait::kElementwise)
     .trait(OpTrait::kFusable)
-    .shape_infer(&unary_same);
+    .shape_infer(&unary_same)
+    .gradient(&frame::ops::schemas::gelu_gradient);
 
-FRAME_REGISTER_OP("sigmoid").input("x", "input").output("out", "1 / (1 + exp(-x))").trait(OpTrait::kElementwise).shape_infer(&unary_same);
-FRAME_REGISTER_OP("tanh").input("x", "input").output("out", "tanh(x)").trait(OpTrait::kElementwise).shape_infer(&unary_same);
-FRAME_REGISTER_OP("rsqrt").input("x", "input").output("out", "1 / sqrt(x)").trait(OpTrait::kElementwise).shape_infer(&unary_same);
+FRAME_REGISTER_OP("sigmoid").input("x", "input").output("out", "1 / (1 + exp(-x))").trait(OpTrait::kElementwise).shape_infer(&unary_same)
+    .gradient(&frame::ops::schemas::sigmoid_gradient);
+FRAME_REGISTER_OP("tanh").input("x", "input").output("out", "tanh(x)").trait(OpTrait::kElementwise).shape_infer(&unary_same)
+    .gradient(&frame::ops::schemas::tanh_gradient);
+FRAME_REGISTER_OP("rsqrt").input("x", "input").output("out", "1 / sqrt(x)").trait(OpTrait::kElementwise).shape_infer(&unary_same)
+    .gradient(&frame::ops::schemas::rsqrt_gradient);
 
 FRAME_REGISTER_OP("matmul")
     .input("lhs", "rank-2 [m, k]")
@@ -345,7 +349,8 @@ FRAME_REGISTER_OP("conv2d")
     .shape_infer(&infer_conv2d)
     .gradient(&frame::ops::schemas::conv2d_gradient);
 
-FRAME_REGISTER_OP("softmax").input("x", "rank-2 [N, D]").output("out", "softmax along the last axis").shape_infer(&infer_softmax);
+FRAME_REGISTER_OP("softmax").input("x", "rank-2 [N, D]").output("out", "softmax along the last axis").shape_infer(&infer_softmax)
+    .gradient(&frame::ops::schemas::softmax_gradient);
 
 FRAME_REGISTER_OP("layer_norm")
     .input("x", "rank-2 [N, D]")
@@ -353,7 +358,8 @@ FRAME_REGISTER_OP("layer_norm")
     .input("beta", "rank-1 [D]")
     .attr("eps", AttrType::kDouble, true)
     .output("out", "row-wise layer normalisation with affine")
-    .shape_infer(&infer_layer_norm);
+    .shape_infer(&infer_layer_norm)
+    .gradient(&frame::ops::schemas::layer_norm_gradient);
 
 FRAME_REGISTER_OP("max_pool2d")
     .input("x", "rank-4 [N, C, H, W]")
@@ -375,15 +381,18 @@ FRAME_REGISTER_OP("avg_pool2d")
 
 FRAME_REGISTER_OP("reshape").input("x", "input").attr("target_shape", AttrType::kShape, true).output("out", "reshaped x").shape_infer(&infer_reshape)
     .gradient(&frame::ops::schemas::reshape_gradient);
-FRAME_REGISTER_OP("transpose").input("x", "input").attr("perm", AttrType::kInt64Array, true).output("out", "out.dims[i] = x.dims[perm[i]]").shape_infer(&infer_transpose);
-FRAME_REGISTER_OP("concat").variadic_input("xs", "tensors to concatenate", 1).attr("axis", AttrType::kInt64, true).output("out", "concatenation").shape_infer(&infer_concat);
+FRAME_REGISTER_OP("transpose").input("x", "input").attr("perm", AttrType::kInt64Array, true).output("out", "out.dims[i] = x.dims[perm[i]]").shape_infer(&infer_transpose)
+    .gradient(&frame::ops::schemas::transpose_gradient);
+FRAME_REGISTER_OP("concat").variadic_input("xs", "tensors to concatenate", 1).attr("axis", AttrType::kInt64, true).output("out", "concatenation").shape_infer(&infer_concat)
+    .gradient(&frame::ops::schemas::concat_gradient);
 FRAME_REGISTER_OP("slice")
     .input("x", "input")
     .attr("axis", AttrType::kInt64, true)
     .attr("start", AttrType::kInt64, true)
     .attr("stop", AttrType::kInt64, true)
     .output("out", "x[start:stop] along axis")
-    .shape_infer(&infer_slice);
+    .shape_infer(&infer_slice)
+    .gradient(&frame::ops::schemas::slice_gradient);
 
 FRAME_REGISTER_OP(frame::ops::kConstantOpName)
     .attr("value", AttrType::kDoubleArray, true)

@@ -52,7 +52,13 @@ typedef enum fh_ew_op {
   FH_EW_GELU = 5,
   /* relu_grad_internal(x, gy): gy where x > 0, else 0 (reference: src/backends/cpu/kernels/elementwise.cpp:407-414);
    * binary, the running value is x and the next input gy */
-  FH_EW_RELU_GRAD = 6
+  FH_EW_RELU_GRAD = 6,
+  /* unary, the reference's formulas (src/backends/cpu/kernels/elementwise.cpp:342-405) */
+  FH_EW_SIGMOID = 7,
+  FH_EW_TANH = 8,
+  FH_EW_RSQRT = 9,
+  /* gelu_grad_internal(x, gy) = gy * (Phi(x) + x phi(x)): binary like FH_EW_RELU_GRAD; no reference counterpart */
+  FH_EW_GELU_GRAD = 10
 } fh_ew_op;
 
 #define FH_MAX_SEGMENTS 8

@@ -329,6 +329,10 @@ FRAME_REGISTER_KERNEL("slice", frame::kCpuBackendName, &oracle_cpu::slice_kernel
 FRAME_REGISTER_KERNEL("concat", frame::kCpuBackendName, &oracle_cpu::concat_kernel);
 FRAME_REGISTER_KERNEL(frame::ops::kConstantOpName, frame::kCpuBackendName, &oracle_cpu::constant_kernel);
 FRAME_REGISTER_KERNEL("relu_grad_internal", frame::kCpuBackendName, (&oracle_cpu::ew_kernel<6, 2>));
+FRAME_REGISTER_KERNEL("sigmoid", frame::kCpuBackendName, (&oracle_cpu::ew_kernel<7, 1>));
+FRAME_REGISTER_KERNEL("tanh", frame::kCpuBackendName, (&oracle_cpu::ew_kernel<8, 1>));
+FRAME_REGISTER_KERNEL("rsqrt", frame::kCpuBackendName, (&oracle_cpu::ew_kernel<9, 1>));
+FRAME_REGISTER_KERNEL("gelu_grad_internal", frame::kCpuBackendName, (&oracle_cpu::ew_kernel<10, 2>));
 FRAME_REGISTER_KERNEL("matmul_grad_lhs_internal", frame::kCpuBackendName, &oracle_cpu::matmul_grad_kernel<0>);
 FRAME_REGISTER_KERNEL("matmul_grad_rhs_internal", frame::kCpuBackendName, &oracle_cpu::matmul_grad_kernel<1>);
 FRAME_REGISTER_KERNEL("conv2d_grad_input_internal", frame::kCpuBackendName, &oracle_cpu::conv_grad_kernel<0>);

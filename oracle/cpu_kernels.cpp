@@ -113,16 +113,26 @@ float unary(uint8_t op, float x) {
       return x * x;
     case 5:
       return 0.5f * x * (1.0f + std::erf(x * 0.70710678118654752440f));
+    case 7:  // sigmoid, the reference's overflow-free two-branch form (elementwise.cpp:342-353)
+      if (x >= 0.0f) return 1.0f / (1.0f + std::exp(-x));
+      return std::exp(x) / (1.0f + std::exp(x));
+    case 8:  // tanh (elementwise.cpp:397)
+      return std::tanh(x);
+    case 9:  // rsqrt (elementwise.cpp:405)
+      return 1.0f / std::sqrt(x);
     default:
       return x;
   }
 }
 // op 6 is relu_grad_internal(x, gy): gy where x > 0, else 0 (reference: src/backends/cpu/kernels/elementwise.cpp:407-414).
+// op 10 is gelu_grad_internal(x, gy) = gy * (Phi(x) + x * phi(x)), this build's gelu derivative (no reference).
 float binary(uint8_t op, float a, float b) {
   if (op == 6) return a > 0.0f ? b : 0.0f;
+  if (op == 10)
+    return b * (0.5f * (1.0f + std::erf(a * 0.70710678118654752440f)) + a * (std::exp(-0.5f * a * a) * 0.39894228040143267794f));
   return op == 2 ? a * b : a + b;
 }
-bool is_binary(uint8_t op) { return op == 1 || op == 2 || op == 6; }
+bool is_binary(uint8_t op) { return op == 1 || op == 2 || op == 6 || op == 10; }
 
 template <typename D>
 float matmul_element(const typename D::S* a, const typename D::S* b, int64_t n, int64_t k, int64_t i, int64_t j) {

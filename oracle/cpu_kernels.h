@@ -45,7 +45,8 @@ int oracle_conv2d_sample(int dtype, const void* x, const void* w, const void* bi
 
 /* Fused elementwise chain (reference: src/ops/fused_elementwise_utils.cpp:122-206 for segment order and
  * per-segment rounding; sub-op arithmetic: src/backends/cpu/kernels/elementwise.cpp:146-331).
- * op codes: 1 add, 2 mul, 3 relu, 4 square, 5 gelu, 6 relu_grad (binary: x > 0 ? gy : 0). */
+ * op codes: 1 add, 2 mul, 3 relu, 4 square, 5 gelu, 6 relu_grad (binary: x > 0 ? gy : 0), 7 sigmoid, 8 tanh,
+ * 9 rsqrt, 10 gelu_grad (binary: gy * gelu'(x)). */
 int oracle_ew_program(int dtype, int nseg, const uint8_t* ops, const int8_t* arities, const void* const* ins,
                       int nin, void* out, int64_t numel);
 

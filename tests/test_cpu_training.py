@@ -304,3 +304,61 @@ def test_resnet_training_graph_stays_channels_last():
     # bias gradients over N, H, W of NHWC data; the stem region (NCHW, next to the max-pool gradient) keeps [0, 2, 3]
     assert len(sums) + low.count("hip_sum_rows_internal") == 17  # 17 biased convs
     assert sum("axes=[0, 1, 2]" in l for l in sums) + low.count("hip_sum_rows_internal") >= 14  # stem region NCHW
+
+
+TINY_BLOCK = dict(batch=2, seq=8, d_model=16, heads=2, ffn=32)
+
+
+@needs_ref
+@pytest.mark.parametrize("dtype", [F32, BF16])
+def test_transformer_training_graph_matches_reference(dtype):
+    """softmax, layer_norm, transpose, slice, concat gradients (and rsqrt, matmul broadcasts, sums in their
+    micrographs): the training graph of C5's block (relu FFN: the reference has no gelu) has the reference's IR text,
+    and the oracle runs it bit-identically to the reference build."""
+    g, shapes = graphs.transformer_block(dtype=dtype, device="cpu", act="relu", train=True, **TINY_BLOCK)
+    wrt = list(range(1, len(shapes) + 1))
+    text = host.backward(g.text(), 0, wrt)
+    assert text == orc.ref_backward(g.text(), 0, wrt)
+    assert host.transform(text) == orc.ref_transform(text)
+    rows = TINY_BLOCK["batch"] * TINY_BLOCK["seq"]
+    ins = graphs.transformer_inputs(shapes, rows=rows, d_model=16, dtype=dtype) + [synth.tensor(77, (rows, 16), dtype)]
+    mine = run(text, ins)
+    ref = run_ref(text, ins, [(o.shape, o.dtype) for o in mine])
+    for i, (a, b) in enumerate(zip(mine, ref)):
+        assert np.array_equal(bits(a), bits(b)), f"output {i}"
+
+
+@needs_ref
+@pytest.mark.parametrize("op", ["sigmoid", "tanh", "rsqrt"])
+def test_unary_ops_and_gradients_match_reference(op):
+    g = graphs.Graph("cpu")
+    x = g.input(F32, (6, 50))
+    y = g.op(op, [x], (6, 50))
+    g.output(g.sum(g.mul(y, y), []))
+    text = host.backward(g.text(), 0, [0])
+    assert text == orc.ref_backward(g.text(), 0, [0])
+    xs = np.abs(synth.tensor(5, (6, 50), F32)).astype(np.float32) + (0.1 if op == "rsqrt" else 0.0)
+    if op != "rsqrt":
+        xs = synth.tensor(5, (6, 50), F32) * 4
+    mine = run(text, [xs])
+    ref = run_ref(text, [xs], [(o.shape, o.dtype) for o in mine])
+    for a, b in zip(mine, ref):
+        assert np.array_equal(bits(a), bits(b))
+
+
+def test_gelu_gradient_matches_the_derivative():
+    # gelu has no reference counterpart: its gradient op is pinned by central differences of the exact function
+    import math
+    xs = np.linspace(-6, 6, 241).astype(np.float32)
+    gy = np.ones_like(xs)
+    (gx,) = run(cpu_graph("gelu_grad_internal", [xs.shape, xs.shape], xs.shape), [xs, gy])
+    def gelu(v):
+        return 0.5 * v * (1 + math.erf(v / math.sqrt(2)))
+    h = 1e-4
+    for v, got in zip(xs.astype(np.float64), gx):
+        want = (gelu(v + h) - gelu(v - h)) / (2 * h)
+        assert abs(float(got) - want) <= 1e-5 * max(1.0, abs(want)), (v, got, want)
+    g = graphs.Graph("cpu")
+    x = g.input(F32, (4, 5))
+    g.output(g.sum(g.gelu(x), []))
+    assert "gelu_grad_internal(%0, " in host.backward(g.text(), 0, [0])

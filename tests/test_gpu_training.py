@@ -279,3 +279,42 @@ def test_sgd_update(dev, dtype):
     want = orc.run_graph_cpu(text.replace("@hip:0", "@cpu:0"), params + grads)
     for i in range(4):
         assert_bitwise(got[i], want[i], f"sgd param {i}")
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16])
+@pytest.mark.parametrize("act", ["gelu", "relu"])
+def test_transformer_training_step(dev, dtype, act):
+    # C5's block at a small size: gradients of layer_norm, softmax, slice / concat / transpose, gelu or relu
+    say(f"transformer training step act={act} dtype={dtype}")
+    shape = dict(batch=2, seq=64, d_model=128, heads=2, ffn=256)
+    g, shapes = graphs.transformer_block(dtype=dtype, act=act, train=True, **shape)
+    text = host.backward(g.text(), 0, list(range(1, len(shapes) + 1)))
+    rows = shape["batch"] * shape["seq"]
+    ins = graphs.transformer_inputs(shapes, rows=rows, d_model=128, dtype=dtype) + [synth.tensor(77, (rows, 128), dtype)]
+    got = host.compile(text, "hip", 1).run(ins)
+    want = orc.run_graph_cpu(text.replace("@hip:0", "@cpu:0"), ins)
+    check_outputs(got, want, dtype, f"transformer training ({act})")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("op", ["sigmoid", "tanh", "rsqrt"])
+def test_unary_ops(dev, dtype, op):
+    say(f"{op} dtype={dtype}")
+    shape = (37, 129)
+    (x,) = tensors(90, [shape], dtype)
+    if op == "rsqrt":
+        x = synth.to_storage(np.abs(synth.to_float(x, dtype)) + 0.05, dtype)
+    got, want = both(one_op(op, [shape], shape, None, dtype), [x])
+    if op == "rsqrt" or dtype != F32:
+        assert_bitwise(got[0], want[0], op)  # correctly rounded sqrt / divide; 16-bit rounding absorbs the rest
+    else:
+        assert_close(got[0], want[0], dtype, what=op)  # device expf / tanhf vs the C library: a few ulp
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_gelu_grad(dev, dtype):
+    say(f"gelu_grad dtype={dtype}")
+    shape = (64, 513)
+    x, gy = tensors(95, [shape, shape], dtype)
+    got, want = both(one_op("gelu_grad_internal", [shape, shape], shape, None, dtype), [x, gy])
+    assert_close(got[0], want[0], dtype, what="gelu_grad")
