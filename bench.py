@@ -134,6 +134,38 @@ def _time_graph(graph_text, input_sets, steps, warmup):
     return start.elapsed_ms(stop) / steps
 
 
+def _time_train_step(fwd_text, n_params, inputs, lr, steps, warmup):
+    """ms per training step of the forward graph `fwd_text` whose inputs 1..n_params are the parameters: the
+    backward graph (forward outputs + gradients, compiler::build_backward_graph) then the SGD update graph,
+    parameters ping-ponging between two buffer sets on one stream; HIP events around `steps` steps."""
+    from frame_hip import abi, host
+
+    wrt = list(range(1, n_params + 1))
+    train = host.compile(host.backward(fwd_text, 0, wrt), "hip")
+    sgd = host.compile(host.sgd_update(fwd_text, wrt, lr), "hip")
+    ins = train.upload_inputs(inputs)
+    outs = train.alloc_outputs()
+    params = [ins[1:n_params + 1], sgd.alloc_outputs()]
+    stream = host.Stream("hip")
+    native = _NativeStream(stream.native)
+    start, stop = abi.Event(), abi.Event()
+
+    def step(i):
+        cur, nxt = params[i % 2], params[(i + 1) % 2]
+        train.run_tensors([ins[0]] + cur + ins[n_params + 1:], outs, stream)
+        sgd.run_tensors(cur + outs[1:], nxt, stream)
+
+    for i in range(warmup):
+        step(i)
+    stream.synchronize()
+    start.record(native)
+    for i in range(steps):
+        step(warmup + i)
+    stop.record(native)
+    stop.synchronize()
+    return start.elapsed_ms(stop) / steps
+
+
 def extras(steps, only=None):
     """Each entry: the config, its work, and the measured rate; failures are reported, not raised.
     `only` names one entry to run by itself (for per-workload profiles)."""
@@ -191,6 +223,35 @@ def extras(steps, only=None):
         return {"workload": "C5 transformer block bf16 8x512x1024, 16 heads, FFN 4096, compiled graph", "ms": round(ms, 3),
                 "TFLOP/s": round(111.67e9 / (ms * 1e-3) / 1e12, 1)}
 
+    def mlp_train():
+        g = graphs.mlp_train(batch=64, dtype=F32)
+        ms = _time_train_step(g.text(), 4, graphs.mlp_train_inputs(batch=64, dtype=F32), 0.01, max(50, steps), 10)
+        return {"workload": "C1 MLP f32 batch 64 training step (mse_loss, backward graph + SGD update graph)",
+                "us": round(ms * 1e3, 1)}
+
+    def resnet_train():
+        g, specs = graphs.resnet18(batch=64, dtype=BF16, train=True)
+        ins = graphs.resnet18_inputs(specs, batch=64, dtype=BF16) + [synth.tensor(499, (64, 1000), BF16, "normal")]
+        ms = _time_train_step(g.text(), len(specs), ins, 1e-3, max(2, steps // 25), 1)
+        return {"workload": "C4 ResNet-18 bf16 batch 64 224px training step (mse_loss, backward + SGD graphs)",
+                "ms": round(ms, 3), "TFLOP/s": round(3 * 232.2e9 / (ms * 1e-3) / 1e12, 1)}
+
+    def conv_grads(dtype):
+        # C3's conv: both gradients at [32,64,56,56] * [64,64,3,3], 7.399 GFLOP each
+        geo = dict(stride=[1, 1], padding=[1, 1], groups=1)
+        xs, ws = (32, 64, 56, 56), (64, 64, 3, 3)
+        res = {}
+        for name, ins_s, out_s, extra in [("grad_input", [xs, ws], xs, {"input_shape": graphs.Shape(xs)}),
+                                          ("grad_filter", [xs, xs], ws, {"filter_shape": graphs.Shape(ws)})]:
+            g = graphs.Graph("hip")
+            vals = [g.input(dtype, sh) for sh in ins_s]
+            g.output(g.op(f"conv2d_{name}_internal", vals, out_s, dict(geo, **extra)))
+            ins = [synth.tensor(700 + i, sh, dtype, "normal") for i, sh in enumerate(ins_s)]
+            ms = _time_graph(g.text(), [ins], max(3, steps // 10), 1)
+            res[name] = {"us": round(ms * 1e3, 1), "TFLOP/s": round(7.399e9 / (ms * 1e-3) / 1e12, 1)}
+        res["workload"] = f"C3 conv gradients {'bf16' if dtype == BF16 else 'f32'} [32,64,56,56]*[64,64,3,3]"
+        return res
+
     guard("fused_elementwise", fused)
     guard("conv_c3_bf16", lambda: conv(BF16))
     guard("conv_c3_f32", lambda: conv(F32))
@@ -201,6 +262,9 @@ def extras(steps, only=None):
     guard("c1_mlp_latency", mlp)
     guard("c4_resnet18", resnet)
     guard("c5_transformer", transformer)
+    guard("c1_mlp_train_step", mlp_train)
+    guard("conv_c3_grads_bf16", lambda: conv_grads(BF16))
+    guard("c4_resnet18_train_step", resnet_train)
     return out
 
 

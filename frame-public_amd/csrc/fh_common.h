@@ -145,6 +145,22 @@ __device__ inline float gelu_erfc(float x) {
 
 // Elementwise sub-op semantics, all in fp32 (reference: src/backends/cpu/kernels/elementwise.cpp:146-331).
 // relu keeps NaN and -0.0 exactly like std::max(x, 0.0f): returns x unless x < 0.
+// The ops a GEMM / conv epilogue program may hold (epilogue_op_ok); kept apart from the rest so the contraction
+// kernels' epilogues do not carry the code of the other ops.
+__device__ inline float epi_unary(uint8_t op, float x) {
+  switch (op) {
+    case FH_EW_RELU:
+      return (x < 0.0f) ? 0.0f : x;
+    case FH_EW_SQUARE:
+      return x * x;
+    case FH_EW_GELU:
+      return gelu_erfc(x);
+    default:
+      return x;
+  }
+}
+__device__ inline float epi_binary(uint8_t op, float a, float b) { return op == FH_EW_MUL ? a * b : a + b; }
+
 __device__ inline float ew_unary(uint8_t op, float x) {
   switch (op) {
     case FH_EW_RELU:
@@ -179,11 +195,8 @@ __device__ inline float ew_binary(uint8_t op, float a, float b) {
   return op == FH_EW_MUL ? a * b : a + b;
 }
 
-// Ops a GEMM / conv epilogue program may hold: add, mul and the unary ops (the gradient ops never follow a
-// contraction in epilogue position).
-__host__ __device__ constexpr bool epilogue_op_ok(uint8_t op) {
-  return (op >= FH_EW_ADD && op <= FH_EW_GELU) || (op >= FH_EW_SIGMOID && op <= FH_EW_RSQRT);
-}
+// Ops a GEMM / conv epilogue program may hold: add, mul, relu, square, gelu.
+__host__ __device__ constexpr bool epilogue_op_ok(uint8_t op) { return op >= FH_EW_ADD && op <= FH_EW_GELU; }
 
 __host__ __device__ constexpr bool ew_is_binary(uint8_t op) {
   return op == FH_EW_ADD || op == FH_EW_MUL || op == FH_EW_RELU_GRAD || op == FH_EW_GELU_GRAD;
@@ -211,9 +224,9 @@ __device__ __forceinline__ float epilogue_one(const EP& ep, float v, int64_t idx
     if (s >= ep.nseg) break;
     const uint8_t op = static_cast<uint8_t>(opw >> (8 * s));
     if (ew_is_binary(op)) {
-      v = ew_binary(op, v, Io<T>::load(static_cast<const S*>(ep.ins[s])[idx]));
+      v = epi_binary(op, v, Io<T>::load(static_cast<const S*>(ep.ins[s])[idx]));
     } else {
-      v = ew_unary(op, v);
+      v = epi_unary(op, v);
     }
     if (ep.round_between) v = Io<T>::round(v);
   }
@@ -240,10 +253,10 @@ __device__ __forceinline__ uint4 epilogue_vec(const EP& ep, uint4 packed, int64_
       S iv[V];
       __builtin_memcpy(iv, &in, 16);
 #pragma unroll
-      for (int x = 0; x < V; ++x) v[x] = ew_binary(op, v[x], Io<T>::load(iv[x]));
+      for (int x = 0; x < V; ++x) v[x] = epi_binary(op, v[x], Io<T>::load(iv[x]));
     } else {
 #pragma unroll
-      for (int x = 0; x < V; ++x) v[x] = ew_unary(op, v[x]);
+      for (int x = 0; x < V; ++x) v[x] = epi_unary(op, v[x]);
     }
     if (ep.round_between) {
 #pragma unroll

@@ -136,6 +136,42 @@ fh_status fh_stream_synchronize(void* stream) {
   return FH_OK;
 }
 
+// Stream capture into a HIP graph (thread-local mode: other threads' HIP calls are unaffected) and replay.
+fh_status fh_graph_begin_capture(void* stream) {
+  if (stream == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_graph_begin_capture: the null stream cannot be captured");
+  FH_HIP_CHECK(hipStreamBeginCapture(static_cast<hipStream_t>(stream), hipStreamCaptureModeThreadLocal));
+  return FH_OK;
+}
+
+fh_status fh_graph_end_capture(void* stream, int32_t keep, void** exec) {
+  if (stream == nullptr || exec == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_graph_end_capture: null argument");
+  *exec = nullptr;
+  hipGraph_t g = nullptr;
+  FH_HIP_CHECK(hipStreamEndCapture(static_cast<hipStream_t>(stream), &g));
+  if (!keep) {
+    if (g != nullptr) FH_HIP_CHECK(hipGraphDestroy(g));
+    return FH_OK;
+  }
+  hipGraphExec_t e = nullptr;
+  const hipError_t err = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
+  (void)hipGraphDestroy(g);
+  if (err != hipSuccess) return fh::check_hip(err, "hipGraphInstantiate");
+  *exec = e;
+  return FH_OK;
+}
+
+fh_status fh_graph_launch(void* exec, void* stream) {
+  if (exec == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_graph_launch: null graph");
+  FH_HIP_CHECK(hipGraphLaunch(static_cast<hipGraphExec_t>(exec), static_cast<hipStream_t>(stream)));
+  return FH_OK;
+}
+
+fh_status fh_graph_destroy(void* exec) {
+  if (exec == nullptr) return FH_OK;
+  FH_HIP_CHECK(hipGraphExecDestroy(static_cast<hipGraphExec_t>(exec)));
+  return FH_OK;
+}
+
 fh_status fh_device_synchronize(void) {
   FH_HIP_CHECK(hipDeviceSynchronize());
   return FH_OK;

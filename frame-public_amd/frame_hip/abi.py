@@ -84,6 +84,10 @@ _SIGS = {
     "fh_softmax_rows": (c_int32, [c_int32, c_void_p, c_void_p, c_int64, c_int64, c_void_p]),
     "fh_layer_norm_rows": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_float,
                                      c_void_p]),
+    "fh_graph_begin_capture": (c_int32, [c_void_p]),
+    "fh_graph_end_capture": (c_int32, [c_void_p, c_int32, POINTER(c_void_p)]),
+    "fh_graph_launch": (c_int32, [c_void_p, c_void_p]),
+    "fh_graph_destroy": (c_int32, [c_void_p]),
     "fh_pool2d_nhwc": (c_int32, [c_int32, c_int32, c_void_p, c_void_p, POINTER(c_int64), c_void_p]),
     "fh_matmul_grad": (c_int32, [c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p]),
     "fh_pool2d_grad": (c_int32, [c_int32, c_int32, c_void_p, c_void_p, c_void_p, POINTER(c_int64), c_void_p]),

@@ -26,9 +26,6 @@ uint8_t ew_code(std::string_view op) {
   if (op == "relu") return FH_EW_RELU;
   if (op == "square") return FH_EW_SQUARE;
   if (op == "gelu") return FH_EW_GELU;
-  if (op == "sigmoid") return FH_EW_SIGMOID;
-  if (op == "tanh") return FH_EW_TANH;
-  if (op == "rsqrt") return FH_EW_RSQRT;
   return 0;
 }
 

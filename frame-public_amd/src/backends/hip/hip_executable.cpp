@@ -19,6 +19,7 @@
 // channels-last data stay channels-last between convs (see plan_channels_last).
 // The rewrites run on a private copy of the graph before planning, so the memory plan sees the real lifetimes.
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <optional>
@@ -851,6 +852,62 @@ class HipExecutable final : public hal::Executable {
       }
       arena = a;
     }
+    // Replay (opt-in, FRAME_HIP_GRAPHS=1): the second run on a stream with the same input and output addresses
+    // captures the step sequence into a HIP graph, and later runs with those addresses launch that graph instead
+    // of every step; other addresses run the steps directly. Off by default: on this ROCm a graph launch costs
+    // ~10 us more than launching its kernels (measured: C1 forward 23.8 -> 29.8 us, a 1024^3 GEMM 7 -> 18.5 us),
+    // and every workload here keeps the GPU busy without it.
+    if (sh == nullptr || !graphs_enabled()) return run_steps(inputs, outputs, stream, arena);
+    std::vector<const void*> key;
+    for (const Tensor& t : inputs) key.push_back(t.raw_data());
+    for (const Tensor& t : outputs) key.push_back(t.raw_data());
+    bool capture = false;
+    {
+      std::lock_guard<std::mutex> lock(mu_);
+      GraphCache& gc = graphs_[sh];
+      if (gc.exec != nullptr && gc.key == key) {
+        FRAME_HIP_RETURN_IF_ERROR(fh_graph_launch(gc.exec, sh), "HipExecutable: graph replay");
+        return Status::ok();
+      }
+      if (gc.key != key) {
+        if (gc.exec != nullptr) (void)fh_graph_destroy(gc.exec);
+        gc.exec = nullptr;
+        gc.key = key;
+      } else {
+        capture = !gc.failed;
+      }
+    }
+    if (!capture) return run_steps(inputs, outputs, stream, arena);
+    FRAME_HIP_RETURN_IF_ERROR(fh_graph_begin_capture(sh), "HipExecutable: graph capture");
+    const Status st = run_steps(inputs, outputs, stream, arena);
+    void* exec = nullptr;
+    const fh_status end = fh_graph_end_capture(sh, st.is_ok() ? 1 : 0, &exec);
+    std::lock_guard<std::mutex> lock(mu_);
+    GraphCache& gc = graphs_[sh];
+    if (!st.is_ok() || end != FH_OK || exec == nullptr) {
+      gc.failed = true;  // something in the steps cannot be captured: this executable runs them directly
+      if (!st.is_ok()) return st;
+      return run_steps(inputs, outputs, stream, arena);
+    }
+    gc.exec = exec;
+    FRAME_HIP_RETURN_IF_ERROR(fh_graph_launch(exec, sh), "HipExecutable: graph replay");
+    return Status::ok();
+  }
+
+  ~HipExecutable() override {
+    for (auto& [s, gc] : graphs_)
+      if (gc.exec != nullptr) (void)fh_graph_destroy(gc.exec);
+  }
+
+ private:
+  static bool graphs_enabled() {
+    const char* v = std::getenv("FRAME_HIP_GRAPHS");
+    return v != nullptr && v[0] == '1';
+  }
+
+  Status run_steps(std::span<const Tensor> inputs, std::span<Tensor> outputs, hal::Stream& stream,
+                   const std::shared_ptr<Storage>& arena) {
+    void* sh = stream.native_handle();
     std::vector<Tensor> slots(static_cast<size_t>(plan_.slot_count));
     for (size_t i = 0; i < inputs.size(); ++i) slots[i] = inputs[i];
     // A slot that is a graph output is produced directly in the first caller tensor naming it.
@@ -909,10 +966,17 @@ class HipExecutable final : public hal::Executable {
     return Status::ok();
   }
 
+
+ public:
   std::vector<hal::IoSpec> input_signature() const override { return in_sig_; }
   std::vector<hal::IoSpec> output_signature() const override { return out_sig_; }
 
  private:
+  struct GraphCache {
+    std::vector<const void*> key;  // input then output addresses of the captured run
+    void* exec = nullptr;          // instantiated graph, or null
+    bool failed = false;           // capture failed once: run steps directly from now on
+  };
   ops::ExecutablePlan plan_;
   HipAllocator* alloc_;
   Device device_;
@@ -921,6 +985,7 @@ class HipExecutable final : public hal::Executable {
   std::unordered_map<size_t, Tensor> constants_;  // step index -> device tensor
   std::mutex mu_;
   std::unordered_map<void*, std::shared_ptr<Storage>> arenas_;  // per stream
+  std::unordered_map<void*, GraphCache> graphs_;                 // per stream
 };
 
 }  // namespace

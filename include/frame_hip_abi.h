@@ -90,6 +90,13 @@ fh_status fh_stream_create(void** stream, int32_t device);
 fh_status fh_stream_destroy(void* stream);
 fh_status fh_stream_synchronize(void* stream);
 fh_status fh_device_synchronize(void);
+/* Replay of a captured step sequence (hipStreamBeginCapture / EndCapture / hipGraphInstantiate / hipGraphLaunch).
+ * end_capture with keep = 0 discards the capture (after a failure inside it). No counterpart in the reference,
+ * whose executables launch every step each run (src/backends/cuda/cuda_executable.cpp:55-95). */
+fh_status fh_graph_begin_capture(void* stream);
+fh_status fh_graph_end_capture(void* stream, int32_t keep, void** exec);
+fh_status fh_graph_launch(void* exec, void* stream);
+fh_status fh_graph_destroy(void* exec);
 fh_status fh_event_create(void** event, int32_t device);
 fh_status fh_event_destroy(void* event);
 fh_status fh_event_record(void* event, void* stream);

@@ -219,3 +219,45 @@ def test_c5_transformer_full_rows(dev):
     ins1 = [a[:512] if i in per_row else a for i, a in enumerate(ins)]
     (want,) = orc.run_graph_cpu(g1, ins1)
     assert_close(got[:512], want, BF16, what="transformer sequence 0")
+
+
+# ---- graph replay (HipExecutable captures its steps on the second run with the same addresses) -----------------
+
+@pytest.mark.parametrize("which", ["c1", "c5_small", "cnn_train"])
+def test_graph_replay_matches_eager(dev, which):
+    """With FRAME_HIP_GRAPHS=1, run 1 is eager, run 2 captures a HIP graph and launches it, runs 3+ replay it. Between replays: new input
+    values uploaded into the same tensors, another executable's eager work on the same stream, host syncs. Every
+    replay must equal a fresh eager run of the same inputs bit for bit."""
+    say(f"graph replay {which}")
+    import os
+    os.environ["FRAME_HIP_GRAPHS"] = "1"  # replay is opt-in
+    if which == "c1":
+        text = graphs.mlp(batch=64, dtype=F32, device="hip").text()
+        make = lambda seed: graphs.mlp_inputs(batch=64, dtype=F32, seed=seed)
+    elif which == "c5_small":
+        g, shapes = graphs.transformer_block(batch=2, seq=128, d_model=256, heads=4, ffn=512, dtype=BF16)
+        text = g.text()
+        make = lambda seed: graphs.transformer_inputs(shapes, rows=256, d_model=256, dtype=BF16, seed=seed)
+    else:
+        g = graphs.cnn_train(batch=4, dtype=BF16)
+        text = host.backward(g.text(), 0, [1, 2, 3, 4, 5, 6])
+        make = lambda seed: graphs.cnn_train_inputs(batch=4, dtype=BF16, seed=seed)
+    exe = host.compile(text, "hip")
+    other = host.compile(graphs.gemm(256, BF16, device="hip").text(), "hip")
+    other_ins = other.upload_inputs(graphs.gemm_inputs(256, BF16))
+    other_outs = other.alloc_outputs()
+    stream = host.Stream("hip")
+    ins = exe.upload_inputs(make(11))
+    outs = exe.alloc_outputs()
+    for run in range(6):
+        values = make(11 + run)
+        for t, a in zip(ins, values):
+            host.check(host.lib().frame_tensor_upload(t.handle, np.ascontiguousarray(a).ctypes.data, a.nbytes))
+        exe.run_tensors(ins, outs, stream)  # eager, capture + launch, then replays
+        other.run_tensors(other_ins, other_outs, stream)  # unrelated eager work on the same stream
+        stream.synchronize()
+        got = [o.numpy() for o in outs]
+        want = host.compile(text, "hip").run(values)  # a fresh executable: eager
+        for i, (a, b) in enumerate(zip(got, want)):
+            assert_bitwise(a, b, f"{which} run {run} output {i}")
+    os.environ.pop("FRAME_HIP_GRAPHS", None)
