@@ -172,10 +172,10 @@ __global__ __launch_bounds__(kWThreads) void conv_wgrad_kernel(WgradArgs a) {
 // thread per workspace column in its natural (co, tap, ci) order, so the split-strided reads of a wave are
 // contiguous; the scattered 2-byte writes are the small side.
 template <typename T>
-__global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* __restrict__ part, typename Io<T>::storage* __restrict__ dw,
+__global__ __launch_bounds__(64) void wgrad_reduce_kernel(const float* __restrict__ part, typename Io<T>::storage* __restrict__ dw,
                                                            int32_t splits, int32_t cout, int32_t cin, int32_t cin_pad,
                                                            int32_t taps, int64_t nc, int64_t total) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 64 + threadIdx.x;
   if (i >= total) return;
   const int32_t ci = static_cast<int32_t>(i % cin_pad);
   const int64_t r = i / cin_pad;
@@ -183,8 +183,18 @@ __global__ __launch_bounds__(256) void wgrad_reduce_kernel(const float* __restri
   const int32_t co = static_cast<int32_t>(r / taps);
   if (ci >= cin) return;
   const int64_t stride = static_cast<int64_t>(cout) * nc;
+  // Sixteen partials in flight per batch, summed in split order (the order does not depend on the batching).
+  constexpr int32_t kB = 16;
   float s = 0.0f;
-  for (int32_t k = 0; k < splits; ++k) s += part[k * stride + i];
+  int32_t k = 0;
+  for (; k + kB <= splits; k += kB) {
+    float t[kB];
+#pragma unroll
+    for (int32_t u = 0; u < kB; ++u) t[u] = part[(k + u) * stride + i];
+#pragma unroll
+    for (int32_t u = 0; u < kB; ++u) s += t[u];
+  }
+  for (; k < splits; ++k) s += part[k * stride + i];
   dw[(static_cast<int64_t>(co) * cin + ci) * taps + tap] = Io<T>::store(s);
 }
 
@@ -195,7 +205,8 @@ fh_status run_wgrad(const WgradArgs& args, int32_t splits, int32_t cin_real, int
                      dim3(kWThreads), 0, s, args);
   if (fh_status st = launch_status("conv_wgrad_kernel"); st != FH_OK) return st;
   const int64_t total = static_cast<int64_t>(args.cout) * args.nc;  // every workspace column (co, tap, ci_pad)
-  hipLaunchKernelGGL((wgrad_reduce_kernel<T>), dim3(static_cast<uint32_t>((total + 255) / 256)), dim3(256), 0, s,
+  // 64-lane workgroups: the small layers' few thousand columns still spread over every CU
+  hipLaunchKernelGGL((wgrad_reduce_kernel<T>), dim3(static_cast<uint32_t>((total + 63) / 64)), dim3(64), 0, s,
                      args.part, static_cast<typename Io<T>::storage*>(dw), splits, args.cout, cin_real, args.cin,
                      kh * args.kw, static_cast<int64_t>(args.nc), total);
   return launch_status("wgrad_reduce_kernel");
@@ -246,6 +257,9 @@ extern "C" fh_status fh_conv2d_wgrad_nhwc(int32_t dtype, const void* x, const vo
   a.rows_per_split = ((a.p + splits - 1) / splits + kWK - 1) / kWK * kWK;
   if (!(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(dy) % 16 == 0))
     return fail(FH_INVALID_ARGUMENT, "fh_conv2d_wgrad_nhwc: operands must be 16-byte aligned");
+  if ((geom[4] * static_cast<int64_t>(a.nc) + 63) / 64 > 0xffffffffLL ||
+      (geom[4] + kWM - 1) / kWM * static_cast<int64_t>(a.tiles_n) > 0xffffffffLL)
+    return fail(FH_INVALID_ARGUMENT, "fh_conv2d_wgrad_nhwc: filter too large for one launch");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == FH_BF16) return run_wgrad<bf16_t>(a, splits, static_cast<int32_t>(geom[1]), static_cast<int32_t>(geom[5]), dw, s);
   return run_wgrad<f16_t>(a, splits, static_cast<int32_t>(geom[1]), static_cast<int32_t>(geom[5]), dw, s);

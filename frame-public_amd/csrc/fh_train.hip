@@ -329,6 +329,33 @@ __global__ __launch_bounds__(kThreads) void filter_flip_kernel(const S* __restri
   out[i] = w[((static_cast<int64_t>(co) * cin + ci) * kh + (kh - 1 - a)) * kw + (kw - 1 - b)];
 }
 
+// The same permutation through LDS: a workgroup owns 64 output channels co and kFlipCi input channels ci. Each co's
+// kFlipCi * taps source elements are one contiguous run of w, and each (ci, tap) destination row holds the 64 co
+// contiguously, so both the global reads and the global writes are coalesced (the gather form above reads with a
+// stride of cin * taps elements).
+constexpr int kFlipCo = 64, kFlipCi = 8;
+template <typename S>
+__global__ __launch_bounds__(kThreads) void filter_flip_tiled_kernel(const S* __restrict__ w, S* __restrict__ out,
+                                                                     int32_t cout, int32_t cin, int32_t taps) {
+  extern __shared__ uint32_t flip_smem[];
+  S* tile = reinterpret_cast<S*>(flip_smem);
+  const int32_t co0 = static_cast<int32_t>(blockIdx.x) * kFlipCo, ci0 = static_cast<int32_t>(blockIdx.y) * kFlipCi;
+  const int32_t nco = min(kFlipCo, cout - co0), nci = min(kFlipCi, cin - ci0);
+  const int32_t run = nci * taps, pitch = kFlipCi * taps + 1;
+  const S* src = w + static_cast<int64_t>(co0) * cin * taps + static_cast<int64_t>(ci0) * taps;
+  for (int32_t e = threadIdx.x; e < nco * run; e += kThreads) {
+    const int32_t c = e / run, j = e - c * run;
+    tile[c * pitch + j] = src[static_cast<int64_t>(c) * cin * taps + j];
+  }
+  __syncthreads();
+  // out[(ci * taps + t) * cout + co] = w[co][ci][taps - 1 - t] (the (a, b) flip is the tap reversal)
+  for (int32_t e = threadIdx.x; e < run * nco; e += kThreads) {
+    const int32_t q = e / nco, c = e - q * nco;
+    const int32_t cl = q / taps, t = q - cl * taps;
+    out[(static_cast<int64_t>(ci0 + cl) * taps + t) * cout + co0 + c] = tile[c * pitch + cl * taps + (taps - 1 - t)];
+  }
+}
+
 // channels-last x [N,H,W,C] -> [N,Hu,Wu,C], the same placement, 16-byte vectors of channels (C % 8 == 0).
 template <typename S>
 __global__ __launch_bounds__(kThreads) void dilate_nhwc_vec_kernel(const S* __restrict__ x, S* __restrict__ out, int32_t c,
@@ -901,6 +928,21 @@ extern "C" fh_status fh_conv_filter_flip(int32_t dtype, const void* w, void* out
   const dim3 grid(static_cast<uint32_t>(blocks_for(total)));
   const int32_t a = static_cast<int32_t>(cout), b = static_cast<int32_t>(cin), c = static_cast<int32_t>(kh),
                 d = static_cast<int32_t>(kw);
+  const int64_t taps = kh * kw, esize = dtype_size(dtype);
+  const int64_t lds = kFlipCo * (kFlipCi * taps + 1) * esize;
+  const int64_t gy = (cin + kFlipCi - 1) / kFlipCi;
+  if (lds <= 64 * 1024 && gy <= 65535) {
+    const dim3 tgrid(static_cast<uint32_t>((cout + kFlipCo - 1) / kFlipCo), static_cast<uint32_t>(gy));
+    const size_t shm = static_cast<size_t>((lds + 3) / 4 * 4);
+    const int32_t t = static_cast<int32_t>(taps);
+    if (dtype == FH_F32)
+      hipLaunchKernelGGL((filter_flip_tiled_kernel<uint32_t>), tgrid, dim3(kThreads), shm, s,
+                         static_cast<const uint32_t*>(w), static_cast<uint32_t*>(out), a, b, t);
+    else
+      hipLaunchKernelGGL((filter_flip_tiled_kernel<uint16_t>), tgrid, dim3(kThreads), shm, s,
+                         static_cast<const uint16_t*>(w), static_cast<uint16_t*>(out), a, b, t);
+    return launch_status("fh_conv_filter_flip");
+  }
   if (dtype == FH_F32)
     hipLaunchKernelGGL((filter_flip_kernel<uint32_t>), grid, dim3(kThreads), 0, s, static_cast<const uint32_t*>(w),
                        static_cast<uint32_t*>(out), a, b, c, d, total);

@@ -653,3 +653,19 @@ def test_attention_rejects_unsupported(hip):
         assert hip.lib().fh_attention_supported(dtype, seq, dh) == 0
         rc = hip.lib().fh_attention_fwd(dtype, None, None, None, None, 1, seq, 1, dh, 0.125, None)
         assert rc != 0, (dtype, seq, dh)
+
+
+# out[ci][a][b][co] = w[co][ci][K-1-a][K-1-b]; (100, 13, 3, 3) and (64, 64, 3, 3) take the LDS-tiled form (ragged
+# and whole 64 x 8 tiles), (70, 9, 11, 11) f32 the gather form (its tile would need more than 64 KB of LDS)
+@pytest.mark.parametrize("itemsize,shape", [(2, (100, 13, 3, 3)), (2, (64, 64, 3, 3)), (4, (33, 17, 1, 1)),
+                                            (2, (512, 256, 3, 3)), (4, (70, 9, 11, 11)), (2, (8, 3, 7, 5))])
+def test_conv_filter_flip(hip, itemsize, shape):
+    say(f"conv_filter_flip itemsize={itemsize} {shape}")
+    dt = np.uint16 if itemsize == 2 else np.uint32
+    dtype = 3 if itemsize == 2 else 0
+    w = np.random.default_rng(5).integers(0, np.iinfo(dt).max, size=shape, dtype=dt)
+    dw, dout = dev(hip, w), hip.DeviceBuffer(w.nbytes)
+    co, ci, kh, kw = shape
+    hip.check(hip.lib().fh_conv_filter_flip(dtype, dw.value, dout.value, co, ci, kh, kw, None))
+    want = np.ascontiguousarray(w[:, :, ::-1, ::-1].transpose(1, 2, 3, 0))
+    assert_bitwise(dout.download((ci, kh, kw, co), dt), want, f"filter flip {shape}")
