@@ -356,6 +356,62 @@ __global__ __launch_bounds__(kThreads) void filter_flip_tiled_kernel(const S* __
   }
 }
 
+// out_i = x_i + round(s_i * y_i) for up to FH_AXPY_MAX tensors: workgroups are dealt to the tensors by
+// first_block (a prefix over each tensor's workgroup count), each workgroup covers kAxpyVecs 16-byte vectors per
+// thread. The product is rounded to the storage type before the add, as the separate mul node stores it.
+constexpr int kAxpyVecs = 4;
+struct AxpyBatch {
+  const void* x[FH_AXPY_MAX];
+  const void* y[FH_AXPY_MAX];
+  void* out[FH_AXPY_MAX];
+  int64_t n[FH_AXPY_MAX];
+  float s[FH_AXPY_MAX];
+  int32_t first_block[FH_AXPY_MAX + 1];
+  int32_t count;
+  uint32_t aligned;  // bit i: tensor i's three pointers are 16-byte aligned
+};
+
+template <typename T>
+__device__ __forceinline__ typename Io<T>::storage axpy_one(typename Io<T>::storage x, typename Io<T>::storage y, float s) {
+  const float step = Io<T>::load(Io<T>::store(s * Io<T>::load(y)));
+  return Io<T>::store(Io<T>::load(x) + step);
+}
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void axpy_multi_kernel(const AxpyBatch b) {
+  using S = typename Io<T>::storage;
+  constexpr int V = 16 / sizeof(S);
+  const int32_t blk = static_cast<int32_t>(blockIdx.x);
+  int32_t t = 0;
+  while (t + 1 < b.count && b.first_block[t + 1] <= blk) ++t;
+  const S* x = static_cast<const S*>(b.x[t]);
+  const S* y = static_cast<const S*>(b.y[t]);
+  S* out = static_cast<S*>(b.out[t]);
+  const int64_t n = b.n[t];
+  const float s = b.s[t];
+  const bool vec = (b.aligned >> t) & 1u;
+  const int64_t v0 = static_cast<int64_t>(blk - b.first_block[t]) * kThreads * kAxpyVecs + threadIdx.x;
+#pragma unroll
+  for (int u = 0; u < kAxpyVecs; ++u) {
+    const int64_t e0 = (v0 + static_cast<int64_t>(u) * kThreads) * V;
+    if (e0 >= n) break;
+    if (vec && e0 + V <= n) {
+      const uint4 xq = *reinterpret_cast<const uint4*>(x + e0), yq = *reinterpret_cast<const uint4*>(y + e0);
+      S xs[V], ys[V], os[V];
+      __builtin_memcpy(xs, &xq, 16);
+      __builtin_memcpy(ys, &yq, 16);
+#pragma unroll
+      for (int e = 0; e < V; ++e) os[e] = axpy_one<T>(xs[e], ys[e], s);
+      uint4 oq;
+      __builtin_memcpy(&oq, os, 16);
+      *reinterpret_cast<uint4*>(out + e0) = oq;
+    } else {
+      const int64_t end = min(e0 + V, n);
+      for (int64_t e = e0; e < end; ++e) out[e] = axpy_one<T>(x[e], y[e], s);
+    }
+  }
+}
+
 // channels-last x [N,H,W,C] -> [N,Hu,Wu,C], the same placement, 16-byte vectors of channels (C % 8 == 0).
 template <typename S>
 __global__ __launch_bounds__(kThreads) void dilate_nhwc_vec_kernel(const S* __restrict__ x, S* __restrict__ out, int32_t c,
@@ -950,6 +1006,41 @@ extern "C" fh_status fh_conv_filter_flip(int32_t dtype, const void* w, void* out
     hipLaunchKernelGGL((filter_flip_kernel<uint16_t>), grid, dim3(kThreads), 0, s, static_cast<const uint16_t*>(w),
                        static_cast<uint16_t*>(out), a, b, c, d, total);
   return launch_status("fh_conv_filter_flip");
+}
+
+extern "C" fh_status fh_axpy_multi(int32_t dtype, int32_t count, const void* const* x, const void* const* y,
+                                   void* const* out, const int64_t* numel, const float* scales, void* stream) {
+  if (!is_supported_float(dtype)) return fail(FH_UNIMPLEMENTED, "fh_axpy_multi: unsupported dtype");
+  if (count < 0 || count > FH_AXPY_MAX) return fail(FH_INVALID_ARGUMENT, "fh_axpy_multi: count out of range");
+  if (count == 0) return FH_OK;
+  if (x == nullptr || y == nullptr || out == nullptr || numel == nullptr || scales == nullptr)
+    return fail(FH_INVALID_ARGUMENT, "fh_axpy_multi: null pointer");
+  const int64_t esize = dtype_size(dtype), per_block = int64_t{kThreads} * kAxpyVecs * (16 / esize);
+  AxpyBatch b{};
+  int64_t blocks = 0;
+  for (int32_t i = 0; i < count; ++i) {
+    if (numel[i] < 0) return fail(FH_INVALID_ARGUMENT, "fh_axpy_multi: negative numel");
+    if (numel[i] > 0 && (x[i] == nullptr || y[i] == nullptr || out[i] == nullptr))
+      return fail(FH_INVALID_ARGUMENT, "fh_axpy_multi: null tensor pointer");
+    b.x[i] = x[i], b.y[i] = y[i], b.out[i] = out[i], b.n[i] = numel[i], b.s[i] = scales[i];
+    b.first_block[i] = static_cast<int32_t>(blocks);
+    const bool al = reinterpret_cast<uintptr_t>(x[i]) % 16 == 0 && reinterpret_cast<uintptr_t>(y[i]) % 16 == 0 &&
+                    reinterpret_cast<uintptr_t>(out[i]) % 16 == 0;
+    if (al) b.aligned |= 1u << i;
+    blocks += (numel[i] + per_block - 1) / per_block;
+    if (blocks > 0x7fffffffLL) return fail(FH_INVALID_ARGUMENT, "fh_axpy_multi: tensors too large for one launch");
+  }
+  b.first_block[count] = static_cast<int32_t>(blocks);
+  b.count = count;
+  if (blocks == 0) return FH_OK;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const dim3 grid(static_cast<uint32_t>(blocks));
+  switch (dtype) {
+    case FH_F32: hipLaunchKernelGGL((axpy_multi_kernel<float>), grid, dim3(kThreads), 0, s, b); break;
+    case FH_BF16: hipLaunchKernelGGL((axpy_multi_kernel<bf16_t>), grid, dim3(kThreads), 0, s, b); break;
+    default: hipLaunchKernelGGL((axpy_multi_kernel<f16_t>), grid, dim3(kThreads), 0, s, b); break;
+  }
+  return launch_status("fh_axpy_multi");
 }
 
 extern "C" fh_status fh_dilate_nhwc(int32_t dtype, int32_t in_nhwc, const void* x, void* out, int64_t n, int64_t c,

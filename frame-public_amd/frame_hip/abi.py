@@ -96,6 +96,7 @@ _SIGS = {
     "fh_conv2d_wgrad_workspace": (c_int64, [c_int32, POINTER(c_int64), c_int32, POINTER(c_int32)]),
     "fh_conv2d_wgrad_nhwc": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, POINTER(c_int64), c_int32,
                                        c_void_p]),
+    "fh_axpy_multi": (c_int32, [c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "fh_conv_filter_flip": (c_int32, [c_int32, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p]),
     "fh_dilate_nhwc": (c_int32, [c_int32, c_int32, c_void_p, c_void_p] + [c_int64] * 8 + [c_void_p]),
     "fh_avg_pool2d_grad_nhwc": (c_int32, [c_int32, c_void_p, c_void_p, POINTER(c_int64), c_void_p]),

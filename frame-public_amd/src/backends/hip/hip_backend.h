@@ -138,6 +138,9 @@ inline constexpr std::string_view kDilateNhwcOp = "hip_dilate_nhwc_internal";  /
 // sum over every axis but the last (the bias gradient of channels-last data or of [rows, features]): outputs the
 // sum and an fp32 workspace of per-workgroup partials (see fh_sum_rows).
 inline constexpr std::string_view kSumRowsOp = "hip_sum_rows_internal";
+// out_i = add(x_i, mul(constant s_i, y_i)) for up to FH_AXPY_MAX pairs in one launch (the SGD update graph's
+// parameter updates; see fh_axpy_multi): inputs [x_0, y_0, x_1, y_1, ...], one output per pair, attr scales.
+inline constexpr std::string_view kAxpyMultiOp = "hip_axpy_multi_internal";
 // avg_pool2d_grad_internal on channels-last dy / dx (same attributes; see fh_avg_pool2d_grad_nhwc).
 inline constexpr std::string_view kAvgPoolGradNhwcOp = "hip_avg_pool2d_grad_nhwc_internal";
 // conv2d_grad_filter_internal on MFMA: inputs x channels-last [N,H,W,cin_pad] and dy channels-last [N,Ho,Wo,Cout];

@@ -21,6 +21,7 @@
 #include <algorithm>
 #include <cstdlib>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <optional>
 #include <string>
@@ -1049,12 +1050,92 @@ Result<ir::Graph> lower_matmul_grads(const ir::Graph& src) {
   return out;
 }
 
+// add(x, mul(constant s, y)) with x and y graph inputs of one shape and dtype (either operand order), the mul used only by that add: the
+// SGD update graph's parameter updates (reference: src/compiler/autograd.cpp:418-440). Runs of up to FH_AXPY_MAX
+// such pairs of one dtype become one kAxpyMultiOp node (one launch instead of two per parameter); the constant
+// goes with them when nothing else reads it. Results are bit-identical: the product is rounded as the mul node
+// stores it, then added in the add node's operand order.
+Status lower_scaled_adds(ir::Graph& g) {
+  std::unordered_map<const ir::Value*, int> uses;
+  for (const ir::Node* n : g.topological_order())
+    for (const ir::Value* v : n->inputs()) ++uses[v];
+  for (const ir::Value* v : g.outputs()) uses[v] += 1000;
+  struct Pair {
+    ir::Node* add;
+    ir::Node* mul;
+    ir::Node* c;
+    ir::Value* x;
+    ir::Value* y;
+    float s;
+  };
+  std::map<int, std::vector<Pair>> by_dtype;
+  for (ir::Node* a : g.topological_order()) {
+    if (a->op() != "add" || a->inputs().size() != 2 || a->outputs().size() != 1) continue;
+    // canonicalize may have swapped the operands of either node; both are commutative in IEEE arithmetic
+    auto made_by = [](const ir::Value* v, std::string_view op) { return v->producer() != nullptr && v->producer()->op() == op; };
+    const int mi = made_by(a->inputs()[1], "mul") ? 1 : 0;
+    ir::Value* x = a->inputs()[1 - mi];
+    ir::Value* m = a->inputs()[mi];
+    ir::Node* mul = m->producer();
+    if (!made_by(x, ir::kGraphInputOp) || !made_by(m, "mul") || mul->inputs().size() != 2 || uses[m] != 1) continue;
+    const int ci = made_by(mul->inputs()[0], ops::kConstantOpName) ? 0 : 1;
+    ir::Node* c = mul->inputs()[ci]->producer();
+    ir::Value* y = mul->inputs()[1 - ci];
+    if (!made_by(mul->inputs()[ci], ops::kConstantOpName) || !made_by(y, ir::kGraphInputOp)) continue;
+    const ir::TensorType& t = a->outputs()[0].type();
+    if (!(x->type().dtype == t.dtype) || !(y->type().dtype == t.dtype) || !(mul->inputs()[ci]->type().dtype == t.dtype) ||
+        x->type().shape != t.shape || y->type().shape != t.shape || mul->inputs()[ci]->type().shape != t.shape)
+      continue;
+    const int dt = t.dtype.code() == DTypeCode::kFloat32 ? FH_F32 : t.dtype.code() == DTypeCode::kBFloat16 ? FH_BF16
+                   : t.dtype.code() == DTypeCode::kFloat16 ? FH_F16 : -1;
+    if (dt < 0) continue;
+    std::optional<float> sv;
+    if (dt == FH_F32) {
+      const auto* vals = c != nullptr && c->op() == ops::kConstantOpName && c->inputs().empty()
+                             ? attr_of<std::vector<double>>(c, "value") : nullptr;
+      if (vals != nullptr && !vals->empty() &&
+          std::all_of(vals->begin(), vals->end(), [&](double v) { return v == vals->front(); }))
+        sv = static_cast<float>(vals->front());
+    } else {
+      sv = splat_value(c, t.dtype);
+    }
+    if (!sv) continue;
+    by_dtype[dt].push_back({a, mul, c, x, y, *sv});
+  }
+  for (auto& [dt, pairs] : by_dtype) {
+    for (size_t first = 0; first < pairs.size(); first += FH_AXPY_MAX) {
+      const size_t last = std::min(pairs.size(), first + FH_AXPY_MAX);
+      if (last - first < 2) break;  // a single pair keeps its two nodes
+      std::vector<ir::Value*> ins;
+      std::vector<ir::TensorType> types;
+      std::vector<double> scales;
+      for (size_t i = first; i < last; ++i) {
+        ins.push_back(pairs[i].x);
+        ins.push_back(pairs[i].y);
+        types.push_back(pairs[i].add->outputs()[0].type());
+        scales.push_back(pairs[i].s);
+      }
+      Result<ir::Node*> f = g.create_node(std::string(kAxpyMultiOp), std::move(ins), std::move(types));
+      if (!f.is_ok()) return f.status();
+      f.value()->set_attr("scales", ir::AttrValue{scales});
+      for (size_t i = first; i < last; ++i) {
+        FRAME_RETURN_IF_ERROR(g.replace_all_uses(pairs[i].add->output(0), f.value()->output(static_cast<int>(i - first))));
+        FRAME_RETURN_IF_ERROR(g.erase_node(pairs[i].add));
+        FRAME_RETURN_IF_ERROR(g.erase_node(pairs[i].mul));
+        if (--uses[pairs[i].c->output(0)] == 0) FRAME_RETURN_IF_ERROR(g.erase_node(pairs[i].c));
+      }
+    }
+  }
+  return Status::ok();
+}
+
 Result<ir::Graph> lower_for_hip(const ir::Graph& graph, int32_t opt_level) {
   Result<ir::Graph> work = lower_matmul_grads(graph);
   if (!work.is_ok()) return work.status();
   // Attention runs at every level (like the conv lowering), before the epilogue fusion would claim its matmuls.
   FRAME_RETURN_IF_ERROR(lower_attention(work.value()));
   if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_epilogues(work.value()));
+  if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_scaled_adds(work.value()));
   // Channels-last conv lowering runs at every level, so the conv numerics do not depend on the level.
   return lower_convs(work.value());
 }

@@ -513,6 +513,35 @@ Status sum_rows_kernel(KernelContext& ctx) {
   return Status::ok();
 }
 
+// out_i = x_i + s_i * y_i over the pairs of kAxpyMultiOp (inputs [x_0, y_0, x_1, y_1, ...]), one launch.
+Status axpy_multi_kernel(KernelContext& ctx) {
+  const std::string op(kAxpyMultiOp);
+  const size_t n = ctx.outputs.size();
+  if (n == 0 || n > FH_AXPY_MAX || ctx.inputs.size() != 2 * n) return invalid(op, "expects 2 inputs per output, at most 32 outputs");
+  const auto* scales = attr<std::vector<double>>(ctx, "scales");
+  if (scales == nullptr || scales->size() != n) return invalid(op, "attribute 'scales' must hold one value per output");
+  Result<int32_t> dt = float_code(op, ctx.outputs[0].dtype());
+  if (!dt.is_ok()) return dt.status();
+  const void* xs[FH_AXPY_MAX];
+  const void* ys[FH_AXPY_MAX];
+  void* outs[FH_AXPY_MAX];
+  int64_t numel[FH_AXPY_MAX];
+  float sv[FH_AXPY_MAX];
+  for (size_t i = 0; i < n; ++i) {
+    const Tensor& x = ctx.inputs[2 * i];
+    const Tensor& y = ctx.inputs[2 * i + 1];
+    Tensor& o = ctx.outputs[i];
+    if (!(x.dtype() == o.dtype()) || !(y.dtype() == o.dtype()) || !(o.dtype() == ctx.outputs[0].dtype()) ||
+        x.shape() != o.shape() || y.shape() != o.shape())
+      return invalid(op, "every pair must match its output's dtype and shape");
+    xs[i] = x.raw_data(), ys[i] = y.raw_data(), outs[i] = o.raw_data();
+    numel[i] = o.numel(), sv[i] = static_cast<float>((*scales)[i]);
+  }
+  FRAME_HIP_RETURN_IF_ERROR(fh_axpy_multi(dt.value(), static_cast<int32_t>(n), xs, ys, outs, numel, sv, stream_handle(ctx)),
+                            "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
 // avg_pool2d_grad_internal on channels-last dy [N,Ho,Wo,C] -> dx [N,H,W,C] (kAvgPoolGradNhwcOp).
 Status avg_pool_grad_nhwc_kernel(KernelContext& ctx) {
   const std::string op(kAvgPoolGradNhwcOp);
@@ -832,6 +861,7 @@ FRAME_REGISTER_KERNEL(kFilterFlipOp, kHipBackendName, &filter_flip_kernel);
 FRAME_REGISTER_KERNEL(kConvWgradOp, kHipBackendName, &conv_wgrad_kernel);
 FRAME_REGISTER_KERNEL(kAvgPoolGradNhwcOp, kHipBackendName, &avg_pool_grad_nhwc_kernel);
 FRAME_REGISTER_KERNEL(kSumRowsOp, kHipBackendName, &sum_rows_kernel);
+FRAME_REGISTER_KERNEL(kAxpyMultiOp, kHipBackendName, &axpy_multi_kernel);
 FRAME_REGISTER_KERNEL(kDilateNhwcOp, kHipBackendName, &dilate_nhwc_kernel);
 FRAME_REGISTER_KERNEL("sum", kHipBackendName, &sum_kernel<0>);
 FRAME_REGISTER_KERNEL("sum_grad_internal", kHipBackendName, &sum_kernel<1>);

@@ -318,6 +318,15 @@ int64_t fh_sum_rows_workspace(int32_t dtype, int64_t rows, int64_t cols);
 fh_status fh_sum_rows(int32_t dtype, const void* x, void* out, int64_t rows, int64_t cols, void* workspace,
                       int64_t workspace_bytes, void* stream);
 
+/* out_i = x_i + s_i * y_i over up to FH_AXPY_MAX same-dtype tensors in one launch, with the product rounded to the
+ * storage type before the add: the SGD update graph's `add(param, mul(constant(-lr), grad))` pairs, bit-identical to
+ * the two elementwise nodes it replaces (reference: src/compiler/autograd.cpp:418-440 builds them; the CPU mul and
+ * add are src/backends/cpu/kernels/elementwise.cpp:146-331). numel[i] elements each; s_i is the value the constant
+ * holds (already narrowed to the storage type). Any alignment; 16-byte aligned tensors move in 16-byte vectors. */
+#define FH_AXPY_MAX 32
+fh_status fh_axpy_multi(int32_t dtype, int32_t count, const void* const* x, const void* const* y, void* const* out,
+                        const int64_t* numel, const float* scales, void* stream);
+
 /* sum_grad_internal: gx (dims) = gy broadcast along the reduced axes, a copy of the stored bits
  * (reference: src/backends/cpu/kernels/reduction.cpp:378-388; the CUDA backend has no kernel for it and falls
  * back to the CPU). */

@@ -362,3 +362,16 @@ def test_gelu_gradient_matches_the_derivative():
     x = g.input(F32, (4, 5))
     g.output(g.sum(g.gelu(x), []))
     assert "gelu_grad_internal(%0, " in host.backward(g.text(), 0, [0])
+
+
+def test_sgd_update_lowers_to_multi_tensor_launches():
+    """The SGD update graph's add(param, mul(constant(-lr), grad)) pairs become hip_axpy_multi_internal nodes of
+    at most 32 pairs each (42 ResNet-18 parameters: 32 + 10); no mul, add or constant is left. At opt level 0 the
+    graph keeps its nodes."""
+    g, specs = graphs.resnet18(batch=8, dtype=BF16, image=64, train=True)
+    sgd = host.sgd_update(g.text(), list(range(1, len(specs) + 1)), 0.01)
+    low = host.hip_lowered(sgd, 1)
+    assert low.count("hip_axpy_multi_internal(") == 2, low
+    assert " mul(" not in low and " add(" not in low and "constant(" not in low
+    assert "scales=[" in low
+    assert host.hip_lowered(sgd, 0).count(" mul(") == len(specs)

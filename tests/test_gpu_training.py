@@ -318,3 +318,47 @@ def test_gelu_grad(dev, dtype):
     x, gy = tensors(95, [shape, shape], dtype)
     got, want = both(one_op("gelu_grad_internal", [shape, shape], shape, None, dtype), [x, gy])
     assert_close(got[0], want[0], dtype, what="gelu_grad")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_sgd_update_many_params(dev, dtype):
+    # 40 parameters (two multi-tensor launches of 32 + 8 pairs), sizes with ragged 16-byte tails and one element
+    say(f"sgd update 40 params dtype={dtype}")
+    shapes = [(1,), (13,), (8,), (1000,), (64, 3, 7, 7), (4099,), (7, 9), (512, 512, 3, 3)] * 5
+    g = graphs.Graph("hip")
+    vals = [g.input(dtype, s) for s in shapes]
+    g.output(g.op("relu", [vals[0]], shapes[0]))
+    text = host.sgd_update(g.text(), list(range(len(shapes))), 0.03)
+    assert host.hip_lowered(text).count("hip_axpy_multi_internal(") == 2
+    params = [synth.tensor(200 + i, s, dtype).reshape(s) for i, s in enumerate(shapes)]
+    grads = [synth.tensor(300 + i, s, dtype).reshape(s) for i, s in enumerate(shapes)]
+    got = host.compile(text, "hip", 1).run(params + grads)
+    want = orc.run_graph_cpu(text.replace("@hip:0", "@cpu:0"), params + grads)
+    for i in range(len(shapes)):
+        assert_bitwise(got[i], want[i], f"sgd param {i} {shapes[i]}")
+
+
+def test_axpy_multi_unaligned(dev):
+    # fh_axpy_multi directly: tensors starting 4 bytes into their buffers take the element path
+    from frame_hip import abi
+    import ctypes
+    say("axpy_multi unaligned f32")
+    rng = np.random.default_rng(9)
+    sizes, scales = [37, 1024, 5], [-0.5, 0.25, 3.0]
+    xs = [rng.standard_normal(n + 1).astype(np.float32) for n in sizes]
+    ys = [rng.standard_normal(n + 1).astype(np.float32) for n in sizes]
+    dx = [host.Tensor.from_numpy("hip", F32, a) for a in xs]
+    dy = [host.Tensor.from_numpy("hip", F32, a) for a in ys]
+    do = [host.Tensor("hip", F32, (n + 1,)) for n in sizes]
+    off = [0, 1, 1]  # tensor 0 aligned, tensors 1 and 2 shifted by one element
+    k = len(sizes)
+    P = ctypes.c_void_p * k
+    xp = P(*[t.data_ptr + 4 * o for t, o in zip(dx, off)])
+    yp = P(*[t.data_ptr + 4 * o for t, o in zip(dy, off)])
+    op = P(*[t.data_ptr + 4 * o for t, o in zip(do, off)])
+    abi.check(abi.lib().fh_axpy_multi(F32, k, xp, yp, op, (ctypes.c_int64 * k)(*sizes), (ctypes.c_float * k)(*scales), None))
+    abi.check(abi.lib().fh_device_synchronize())
+    for i, n in enumerate(sizes):
+        o = off[i]
+        want = xs[i][o:o + n] + (np.float32(scales[i]) * ys[i][o:o + n])
+        assert_bitwise(do[i].numpy()[o:o + n], want, f"axpy tensor {i}")
