@@ -331,9 +331,10 @@ __global__ __launch_bounds__(kThreads) void filter_flip_kernel(const S* __restri
 
 // The same permutation through LDS: a workgroup owns 64 output channels co and kFlipCi input channels ci. Each co's
 // kFlipCi * taps source elements are one contiguous run of w, and each (ci, tap) destination row holds the 64 co
-// contiguously, so both the global reads and the global writes are coalesced (the gather form above reads with a
-// stride of cin * taps elements).
-constexpr int kFlipCo = 64, kFlipCi = 8;
+// contiguously, so the global writes are coalesced and neighbouring workgroups read neighbouring runs (the gather
+// form above reads with a stride of cin * taps elements). One ci per workgroup: a 64x64x3x3 filter still spreads
+// over 64 workgroups (with eight, its eight workgroups took longer than the gather form).
+constexpr int kFlipCo = 64, kFlipCi = 1;
 template <typename S>
 __global__ __launch_bounds__(kThreads) void filter_flip_tiled_kernel(const S* __restrict__ w, S* __restrict__ out,
                                                                      int32_t cout, int32_t cin, int32_t taps) {

@@ -656,9 +656,9 @@ def test_attention_rejects_unsupported(hip):
 
 
 # out[ci][a][b][co] = w[co][ci][K-1-a][K-1-b]; (100, 13, 3, 3) and (64, 64, 3, 3) take the LDS-tiled form (ragged
-# and whole 64 x 8 tiles), (70, 9, 11, 11) f32 the gather form (its tile would need more than 64 KB of LDS)
+# and whole 64-channel tiles), (70, 9, 17, 17) f32 the gather form (its tile would need more than 64 KB of LDS)
 @pytest.mark.parametrize("itemsize,shape", [(2, (100, 13, 3, 3)), (2, (64, 64, 3, 3)), (4, (33, 17, 1, 1)),
-                                            (2, (512, 256, 3, 3)), (4, (70, 9, 11, 11)), (2, (8, 3, 7, 5))])
+                                            (2, (512, 256, 3, 3)), (4, (70, 9, 17, 17)), (4, (70, 9, 11, 11)), (2, (8, 3, 7, 5))])
 def test_conv_filter_flip(hip, itemsize, shape):
     say(f"conv_filter_flip itemsize={itemsize} {shape}")
     dt = np.uint16 if itemsize == 2 else np.uint32
