@@ -27,7 +27,22 @@ struct WgradArgs {
   float* part;     // [splits][Cout][NC]
   int32_t h, w, cin, cout, kw, sh, sw, ph, pw, oh, ow, nc, tiles_n;
   int64_t p, rows_per_split;
+  uint64_t plane_m, ow_m;  // multiply-shift dividers for Ho*Wo and Wo (make_divider)
+  uint32_t plane_s, ow_s;
 };
+
+// Division of 0 <= n < 2^31 by a fixed d >= 1 as floor(n * m / 2^s) (Granlund and Montgomery, "Division by
+// invariant integers using multiplication", 1994, theorem 4.2 with N = 31): l = ceil(log2 d), s = 31 + l,
+// m = floor(2^s / d) + 1, so 2^s < m d <= 2^s + 2^l and the quotient is exact. m <= 2^32, so n * m < 2^63.
+inline void make_divider(int64_t d, uint64_t& m, uint32_t& s) {
+  int l = 0;
+  while ((int64_t{1} << l) < d) ++l;
+  s = static_cast<uint32_t>(31 + l);
+  m = (uint64_t{1} << s) / static_cast<uint64_t>(d) + 1;
+}
+__device__ __forceinline__ int32_t div_by(int32_t n, uint64_t m, uint32_t s) {
+  return static_cast<int32_t>((static_cast<uint64_t>(static_cast<uint32_t>(n)) * m) >> s);
+}
 
 __device__ __forceinline__ int swz8(int krow) { return 2 * (krow & 3); }
 __device__ __forceinline__ int swz16(int krow) { return (2 * (krow & 3)) ^ (8 * (krow & 1)); }
@@ -72,9 +87,9 @@ __global__ __launch_bounds__(kWThreads) void conv_wgrad_kernel(WgradArgs a) {
       const int32_t p = p0 + b_row + 16 * i;
       uint4 v{0, 0, 0, 0};
       if (p < p_end && b_col_ok) {
-        const int32_t n = p / plane;
+        const int32_t n = div_by(p, a.plane_m, a.plane_s);
         const int32_t rem = p - n * plane;
-        const int32_t oh = rem / a.ow, ow = rem - oh * a.ow;
+        const int32_t oh = div_by(rem, a.ow_m, a.ow_s), ow = rem - oh * a.ow;
         const int32_t ih = oh * a.sh - a.ph + ta, iw = ow * a.sw - a.pw + tb;
         if (ih >= 0 && ih < a.h && iw >= 0 && iw < a.w)
           v = *reinterpret_cast<const uint4*>(X + ((static_cast<int64_t>(n) * a.h + ih) * a.w + iw) * a.cin + ci);
@@ -255,6 +270,9 @@ extern "C" fh_status fh_conv2d_wgrad_nhwc(int32_t dtype, const void* x, const vo
   a.tiles_n = (a.nc + kWN - 1) / kWN;
   a.p = geom[0] * a.oh * a.ow;
   a.rows_per_split = ((a.p + splits - 1) / splits + kWK - 1) / kWK * kWK;
+  if (a.oh <= 0 || a.ow <= 0) return fail(FH_INVALID_ARGUMENT, "fh_conv2d_wgrad_nhwc: empty output plane");
+  make_divider(static_cast<int64_t>(a.oh) * a.ow, a.plane_m, a.plane_s);
+  make_divider(a.ow, a.ow_m, a.ow_s);
   if (!(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(dy) % 16 == 0))
     return fail(FH_INVALID_ARGUMENT, "fh_conv2d_wgrad_nhwc: operands must be 16-byte aligned");
   if ((geom[4] * static_cast<int64_t>(a.nc) + 63) / 64 > 0xffffffffLL ||
