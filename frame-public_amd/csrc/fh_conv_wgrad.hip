@@ -6,9 +6,11 @@
 // dW in the reference's [Cout][Cin][KH][KW] layout with one rounding.
 //
 // Both operands are k-major (rows of p), so both MFMA fragments come from ds_read_b64_tr_b16 transpose reads of
-// [BK][cols] LDS tiles (the B-operand path of the GEMM kernel, used for A as well). Tiles: 64 (co) x 128 (a,b,ci)
-// per workgroup, 4 waves of 32 x 64 (two 32x32x16 MFMA tiles), register-staged loads with
-// zero fill for rows past the split and taps in the padding, two LDS stages of 64 p-rows.
+// [BK][cols] LDS tiles (the B-operand path of the GEMM kernel, used for A as well). Tiles: WM (co) x 128 (a,b,ci)
+// per workgroup with WM = 128 when Cout >= 128 (4 waves of 64 x 64, four 32x32x16 MFMA tiles each) and WM = 64
+// otherwise (4 waves of 32 x 64, two tiles), register-staged loads with zero fill for rows past the split and
+// taps in the padding, two LDS stages of 64 p-rows. The larger tile loads 1.5x fewer bytes per MFMA, which is
+// what limits this kernel: operands come from L2 (x is read once per filter tap).
 #include <algorithm>
 
 #include "fh_mfma16.h"
@@ -18,7 +20,7 @@ namespace {
 
 using namespace mfma16;
 
-constexpr int kWM = 64, kWN = 128, kWK = 64;  // workgroup tile
+constexpr int kWN = 128, kWK = 64;  // workgroup tile columns and rows per stage (WM is a template argument)
 constexpr int kWThreads = 256;
 
 struct WgradArgs {
@@ -47,8 +49,13 @@ __device__ __forceinline__ int32_t div_by(int32_t n, uint64_t m, uint32_t s) {
 __device__ __forceinline__ int swz8(int krow) { return 2 * (krow & 3); }
 __device__ __forceinline__ int swz16(int krow) { return (2 * (krow & 3)) ^ (8 * (krow & 1)); }
 
-template <typename T>
+// Workgroup tile rows for a filter of cout output channels (the host's and the kernel's choice must agree).
+inline int wgrad_wm(int64_t cout) { return cout >= 128 ? 128 : 64; }
+
+template <typename T, int kWM>
 __global__ __launch_bounds__(kWThreads) void conv_wgrad_kernel(WgradArgs a) {
+  static_assert(kWM == 64 || kWM == 128, "tile rows");
+  constexpr int MT = kWM / 64;  // 32-row MFMA tiles per wave
   using S = typename Io<T>::storage;
   __shared__ __attribute__((aligned(16))) S As[2][kWK * kWM];
   __shared__ __attribute__((aligned(16))) S Bs[2][kWK * kWN];
@@ -61,10 +68,13 @@ __global__ __launch_bounds__(kWThreads) void conv_wgrad_kernel(WgradArgs a) {
   const S* __restrict__ X = static_cast<const S*>(a.x);
   const S* __restrict__ DY = static_cast<const S*>(a.dy);
 
-  // A loads: kWK*8 chunks, rows t/8 + 32 i, column chunk t%8; B loads: kWK*16 chunks, rows t/16 + 16 i, column
-  // chunk t%16 (a fixed filter tap and ci block per thread)
-  constexpr int A_LOADS = kWK * (kWM / 8) / kWThreads, B_LOADS = kWK * (kWN / 8) / kWThreads;
-  const int a_row = tid >> 3, a_chunk = tid & 7;
+  // A loads: kWK*(WM/8) chunks, rows t/(WM/8) + A_STEP i, column chunk t%(WM/8); B loads: kWK*16 chunks, rows
+  // t/16 + 16 i, column chunk t%16 (a fixed filter tap and ci block per thread)
+  constexpr int A_CH = kWM / 8, A_STEP = kWThreads / A_CH;
+  // A rows of 8 chunks swizzle like the GEMM's A, rows of 16 chunks like B
+  auto swza = [](int krow) { return kWM == 64 ? swz8(krow) : swz16(krow); };
+  constexpr int A_LOADS = kWK * A_CH / kWThreads, B_LOADS = kWK * (kWN / 8) / kWThreads;
+  const int a_row = tid / A_CH, a_chunk = tid % A_CH;
   const bool a_col_ok = m0 + 8 * a_chunk < a.cout;
   const int b_row = tid >> 4, b_chunk = tid & 15;
   const int ncol = n0 + 8 * b_chunk;
@@ -78,7 +88,7 @@ __global__ __launch_bounds__(kWThreads) void conv_wgrad_kernel(WgradArgs a) {
   auto load = [&](int32_t p0) {
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i) {
-      const int32_t p = p0 + a_row + 32 * i;
+      const int32_t p = p0 + a_row + A_STEP * i;
       ra[i] = (p < p_end && a_col_ok) ? *reinterpret_cast<const uint4*>(DY + static_cast<int64_t>(p) * a.cout + m0 + 8 * a_chunk)
                                       : uint4{0, 0, 0, 0};
     }
@@ -100,8 +110,8 @@ __global__ __launch_bounds__(kWThreads) void conv_wgrad_kernel(WgradArgs a) {
   auto store = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i) {
-      const int r = a_row + 32 * i;
-      *reinterpret_cast<uint4*>(&As[buf][r * kWM + ((a_chunk ^ swz8(r)) * 8)]) = ra[i];
+      const int r = a_row + A_STEP * i;
+      *reinterpret_cast<uint4*>(&As[buf][r * kWM + ((a_chunk ^ swza(r)) * 8)]) = ra[i];
     }
 #pragma unroll
     for (int i = 0; i < B_LOADS; ++i) {
@@ -115,10 +125,13 @@ __global__ __launch_bounds__(kWThreads) void conv_wgrad_kernel(WgradArgs a) {
   const int wm = wave >> 1, wn = wave & 1;
   const int g = lane >> 4, r16 = lane & 15, q = r16 & 3, e = r16 >> 2;
   const int krow0 = 8 * (g >> 1) + e;  // + 16 s + 4 h: krow & 3 and krow & 1 unchanged
-  int a_off, b_off[2];
+  int a_off[MT], b_off[2];
   {
-    const int col = wm * 32 + 16 * (g & 1) + 4 * q;
-    a_off = krow0 * (kWM * 2) + ((col >> 3) ^ swz8(krow0)) * 16 + (col & 7) * 2;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int col = wm * (kWM / 2) + 32 * mt + 16 * (g & 1) + 4 * q;
+      a_off[mt] = krow0 * (kWM * 2) + ((col >> 3) ^ swza(krow0)) * 16 + (col & 7) * 2;
+    }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int c = wn * 64 + 32 * j + 16 * (g & 1) + 4 * q;
@@ -126,11 +139,13 @@ __global__ __launch_bounds__(kWThreads) void conv_wgrad_kernel(WgradArgs a) {
     }
   }
 
-  f32x16_t acc[2];
+  f32x16_t acc[MT][2];
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int x = 0; x < 16; ++x) acc[j][x] = 0.0f;
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int x = 0; x < 16; ++x) acc[mt][j][x] = 0.0f;
 
   const int32_t steps = (p_end - p_begin + kWK - 1) / kWK;
   if (steps > 0) {
@@ -148,17 +163,28 @@ __global__ __launch_bounds__(kWThreads) void conv_wgrad_kernel(WgradArgs a) {
       (
           [&] {
             constexpr int s = K_;  // 16-row k-step within the stage
-            u32x2_t al, ah, bl[2], bh[2];
-            al = lds_read_tr16_b64<(16 * s) * kWM * 2>(abase + a_off);
-            ah = lds_read_tr16_b64<(16 * s + 4) * kWM * 2>(abase + a_off);
+            u32x2_t al[MT], ah[MT], bl[2], bh[2];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+              al[mt] = lds_read_tr16_b64<(16 * s) * kWM * 2>(abase + a_off[mt]);
+              ah[mt] = lds_read_tr16_b64<(16 * s + 4) * kWM * 2>(abase + a_off[mt]);
+            }
             bl[0] = lds_read_tr16_b64<(16 * s) * kWN * 2>(bbase + b_off[0]);
             bh[0] = lds_read_tr16_b64<(16 * s + 4) * kWN * 2>(bbase + b_off[0]);
             bl[1] = lds_read_tr16_b64<(16 * s) * kWN * 2>(bbase + b_off[1]);
             bh[1] = lds_read_tr16_b64<(16 * s + 4) * kWN * 2>(bbase + b_off[1]);
-            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(al), "+v"(ah), "+v"(bl[0]), "+v"(bh[0]), "+v"(bl[1]), "+v"(bh[1]));
-            const u32x4_t af{al[0], al[1], ah[0], ah[1]};
+            if constexpr (MT == 1)
+              asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(al[0]), "+v"(ah[0]), "+v"(bl[0]), "+v"(bh[0]), "+v"(bl[1]), "+v"(bh[1]));
+            else
+              asm volatile("s_waitcnt lgkmcnt(0)"
+                           : "+v"(al[0]), "+v"(ah[0]), "+v"(al[1]), "+v"(ah[1]), "+v"(bl[0]), "+v"(bh[0]), "+v"(bl[1]),
+                             "+v"(bh[1]));
 #pragma unroll
-            for (int j = 0; j < 2; ++j) mfma32<T>(af, u32x4_t{bl[j][0], bl[j][1], bh[j][0], bh[j][1]}, acc[j]);
+            for (int mt = 0; mt < MT; ++mt) {
+              const u32x4_t af{al[mt][0], al[mt][1], ah[mt][0], ah[mt][1]};
+#pragma unroll
+              for (int j = 0; j < 2; ++j) mfma32<T>(af, u32x4_t{bl[j][0], bl[j][1], bh[j][0], bh[j][1]}, acc[mt][j]);
+            }
           }(),
           ...);
     }(std::make_integer_sequence<int, kWK / 16>{});
@@ -172,15 +198,17 @@ __global__ __launch_bounds__(kWThreads) void conv_wgrad_kernel(WgradArgs a) {
   float* out = a.part + static_cast<int64_t>(blockIdx.y) * a.cout * a.nc;
   const int hi = lane >> 5, l32 = lane & 31;
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int col = n0 + wn * 64 + 32 * j + l32;
-    if (col >= a.nc) continue;
+  for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-    for (int x = 0; x < 16; ++x) {
-      const int row = m0 + wm * 32 + 8 * (x >> 2) + 4 * hi + (x & 3);
-      if (row < a.cout) out[static_cast<int64_t>(row) * a.nc + col] = acc[j][x];
+    for (int j = 0; j < 2; ++j) {
+      const int col = n0 + wn * 64 + 32 * j + l32;
+      if (col >= a.nc) continue;
+#pragma unroll
+      for (int x = 0; x < 16; ++x) {
+        const int row = m0 + wm * (kWM / 2) + 32 * mt + 8 * (x >> 2) + 4 * hi + (x & 3);
+        if (row < a.cout) out[static_cast<int64_t>(row) * a.nc + col] = acc[mt][j][x];
+      }
     }
-  }
 }
 
 // dw[co][ci][kh][kw] = round(sum over splits, in order, of part[s][co][(kh*KW + kw)*cin_pad + ci]), ci < cin. One
@@ -215,9 +243,13 @@ __global__ __launch_bounds__(64) void wgrad_reduce_kernel(const float* __restric
 
 template <typename T>
 fh_status run_wgrad(const WgradArgs& args, int32_t splits, int32_t cin_real, int32_t kh, void* dw, hipStream_t s) {
-  const int tiles = ((args.cout + kWM - 1) / kWM) * args.tiles_n;
-  hipLaunchKernelGGL((conv_wgrad_kernel<T>), dim3(static_cast<uint32_t>(tiles), static_cast<uint32_t>(splits)),
-                     dim3(kWThreads), 0, s, args);
+  const int wm = wgrad_wm(args.cout);
+  const int tiles = ((args.cout + wm - 1) / wm) * args.tiles_n;
+  const dim3 grid(static_cast<uint32_t>(tiles), static_cast<uint32_t>(splits));
+  if (wm == 128)
+    hipLaunchKernelGGL((conv_wgrad_kernel<T, 128>), grid, dim3(kWThreads), 0, s, args);
+  else
+    hipLaunchKernelGGL((conv_wgrad_kernel<T, 64>), grid, dim3(kWThreads), 0, s, args);
   if (fh_status st = launch_status("conv_wgrad_kernel"); st != FH_OK) return st;
   const int64_t total = static_cast<int64_t>(args.cout) * args.nc;  // every workspace column (co, tap, ci_pad)
   // 64-lane workgroups: the small layers' few thousand columns still spread over every CU
@@ -238,7 +270,8 @@ extern "C" int64_t fh_conv2d_wgrad_workspace(int32_t dtype, const int64_t geom[1
   const int64_t oh = (geom[2] + 2 * geom[9] - geom[5]) / geom[7] + 1, ow = (geom[3] + 2 * geom[10] - geom[6]) / geom[8] + 1;
   const int64_t p = geom[0] * oh * ow, nc = geom[5] * geom[6] * cin_pad;
   if (p <= 0 || nc <= 0 || p >= (int64_t{1} << 31) - (int64_t{1} << 23) || nc > (1 << 30)) return -1;  // rows fit int32
-  const int64_t tiles = ((geom[4] + kWM - 1) / kWM) * ((nc + kWN - 1) / kWN);
+  const int64_t wm = wgrad_wm(geom[4]);
+  const int64_t tiles = ((geom[4] + wm - 1) / wm) * ((nc + kWN - 1) / kWN);
   // enough workgroups to fill the device twice over, each at least 512 p-rows, the workspace within 256 MiB
   int64_t sp = (2 * 256 + tiles - 1) / tiles;
   sp = std::min<int64_t>(sp, std::max<int64_t>(1, p / 512));
@@ -276,7 +309,7 @@ extern "C" fh_status fh_conv2d_wgrad_nhwc(int32_t dtype, const void* x, const vo
   if (!(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(dy) % 16 == 0))
     return fail(FH_INVALID_ARGUMENT, "fh_conv2d_wgrad_nhwc: operands must be 16-byte aligned");
   if ((geom[4] * static_cast<int64_t>(a.nc) + 63) / 64 > 0xffffffffLL ||
-      (geom[4] + kWM - 1) / kWM * static_cast<int64_t>(a.tiles_n) > 0xffffffffLL)
+      (geom[4] + wgrad_wm(geom[4]) - 1) / wgrad_wm(geom[4]) * static_cast<int64_t>(a.tiles_n) > 0xffffffffLL)
     return fail(FH_INVALID_ARGUMENT, "fh_conv2d_wgrad_nhwc: filter too large for one launch");
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == FH_BF16) return run_wgrad<bf16_t>(a, splits, static_cast<int32_t>(geom[1]), static_cast<int32_t>(geom[5]), dw, s);

@@ -115,6 +115,7 @@ CONV_CASES = [
     # transposed convolution on the implicit-GEMM kernel (tolerance), otherwise on the direct kernel (bit-exact)
     (2, 32, 9, 9, 64, 3, 1, 1, 1),
     (2, 64, 10, 11, 128, 3, 2, 1, 1),
+    (2, 16, 9, 9, 160, 3, 1, 1, 1),   # Cout >= 128 with a partial 128-row filter-gradient tile
     (2, 64, 10, 10, 128, 1, 2, 0, 1),
     (2, 16, 15, 15, 64, 7, 2, 3, 1),
     (2, 3, 20, 20, 64, 7, 2, 3, 1),
