@@ -267,6 +267,10 @@ using namespace fh;
 extern "C" int64_t fh_conv2d_wgrad_workspace(int32_t dtype, const int64_t geom[12], int32_t cin_pad, int32_t* splits) {
   if (dtype != FH_BF16 && dtype != FH_F16) return -1;
   if (geom == nullptr || geom[11] != 1 || cin_pad % 8 != 0 || cin_pad < geom[1] || geom[4] % 8 != 0) return -1;
+  // every extent positive, strides positive, padding non-negative, each 31-bit; the padded input covers the filter
+  for (int k = 0; k < 11; ++k)
+    if (geom[k] < (k >= 9 ? 0 : 1) || geom[k] > 0x7fffffffLL) return -1;
+  if (geom[2] + 2 * geom[9] < geom[5] || geom[3] + 2 * geom[10] < geom[6]) return -1;
   const int64_t oh = (geom[2] + 2 * geom[9] - geom[5]) / geom[7] + 1, ow = (geom[3] + 2 * geom[10] - geom[6]) / geom[8] + 1;
   const int64_t p = geom[0] * oh * ow, nc = geom[5] * geom[6] * cin_pad;
   if (p <= 0 || nc <= 0 || p >= (int64_t{1} << 31) - (int64_t{1} << 23) || nc > (1 << 30)) return -1;  // rows fit int32

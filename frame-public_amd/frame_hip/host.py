@@ -65,6 +65,10 @@ _SIGS = {
     "frame_backward_text": (c_int32, [c_char_p, c_int32, c_void_p, c_int32, c_void_p, c_int64, POINTER(c_int64)]),
     "frame_sgd_update_text": (c_int32, [c_char_p, c_void_p, c_int32, ctypes.c_double, c_void_p, c_int64, POINTER(c_int64)]),
     "frame_launch": (c_int32, [c_char_p, c_char_p, POINTER(c_void_p), c_int32, POINTER(c_void_p), c_int32, c_void_p]),
+    "frame_backend_compile": (c_int32, [c_char_p, c_char_p, c_int32, POINTER(c_void_p)]),
+    "frame_backend_copy": (c_int32, [c_char_p, c_void_p, c_char_p, c_int32, c_void_p, c_char_p, c_int32, c_size_t,
+                                     c_void_p]),
+    "frame_hip_allocator_stats": (c_int32, [c_int32, POINTER(ctypes.c_uint64)]),
 }
 
 
@@ -264,6 +268,32 @@ class Executable:
                 self.handle = None
         except Exception:
             pass
+
+
+def backend_compile(graph, backend: str, opt_level: int = 1) -> Executable:
+    """Backend::compile of the graph as given (no pass pipeline, no compile cache)."""
+    text = graph if isinstance(graph, str) else graph.text()
+    exe = Executable.__new__(Executable)
+    exe.backend = backend
+    exe.handle = c_void_p()
+    check(lib().frame_backend_compile(text.encode(), backend.encode(), opt_level, ctypes.byref(exe.handle)),
+          f"Backend::compile for {backend}")
+    return exe
+
+
+def backend_copy(backend: str, dst: int, dst_backend: str, src: int, src_backend: str, nbytes: int,
+                 stream: "Stream | None" = None) -> None:
+    """Backend::copy between raw addresses; "cpu" names host memory."""
+    check(lib().frame_backend_copy(backend.encode(), c_void_p(dst), dst_backend.encode(), 0, c_void_p(src),
+                                   src_backend.encode(), 0, nbytes, stream.handle if stream else None),
+          "Backend::copy")
+
+
+def allocator_stats(device: int = 0) -> dict:
+    """The hip caching allocator's counters (bytes live / reusable / waiting for the device, allocations, waits)."""
+    out = (ctypes.c_uint64 * 5)()
+    check(lib().frame_hip_allocator_stats(device, out), "frame_hip_allocator_stats")
+    return dict(zip(("live", "cached", "pending", "device_allocations", "device_syncs"), [int(v) for v in out]))
 
 
 def compile(graph, backend: str, opt_level: int = 1) -> Executable:

@@ -3,8 +3,10 @@
 // src/backends/cuda/cuda_backend.cpp:42-320, cuda_allocator.cpp:26-66).
 #include "hip_backend.h"
 
+#include <atomic>
 #include <bit>
 #include <string>
+#include <unordered_set>
 
 #include <frame/ir/graph.h>
 #include <frame/ops/kernel_registry.h>
@@ -31,7 +33,29 @@ uint8_t ew_code(std::string_view op) {
 
 // ---- stream / event ---------------------------------------------------------------------------------------
 
-HipStream::~HipStream() { (void)fh_stream_destroy(handle_); }
+namespace {
+std::mutex g_streams_mu;
+std::unordered_set<uint64_t> g_live_streams;
+std::atomic<uint64_t> g_next_stream_id{1};
+}  // namespace
+
+bool hip_stream_alive(uint64_t id) {
+  std::lock_guard<std::mutex> lock(g_streams_mu);
+  return g_live_streams.count(id) != 0;
+}
+
+HipStream::HipStream(void* handle, int32_t device) : handle_(handle), device_(device), id_(g_next_stream_id++) {
+  std::lock_guard<std::mutex> lock(g_streams_mu);
+  g_live_streams.insert(id_);
+}
+
+HipStream::~HipStream() {
+  {
+    std::lock_guard<std::mutex> lock(g_streams_mu);
+    g_live_streams.erase(id_);
+  }
+  (void)fh_stream_destroy(handle_);
+}
 
 Status HipStream::synchronize() {
   FRAME_HIP_RETURN_IF_ERROR(fh_stream_synchronize(handle_), "HipStream::synchronize");
@@ -79,9 +103,31 @@ size_t HipAllocator::size_class(size_t bytes) {
 }
 
 HipAllocator::~HipAllocator() {
-  // Process teardown: return cached blocks. Live blocks belong to Storage objects that may outlive us.
-  for (auto& [cls, list] : free_lists_)
-    for (void* p : list) (void)fh_free(p);
+  // Process teardown: return cached blocks (hipFree waits for the device). Live blocks belong to Storage objects
+  // that may outlive us.
+  for (auto* lists : {&free_lists_, &pending_})
+    for (auto& [cls, list] : *lists)
+      for (void* p : list) (void)fh_free(p);
+}
+
+Status HipAllocator::release_pending_locked() {
+  if (pending_.empty()) return Status::ok();
+  FRAME_HIP_RETURN_IF_ERROR(fh_set_device(device_), "HipAllocator: set device");
+  FRAME_HIP_RETURN_IF_ERROR(fh_device_synchronize(), "HipAllocator: wait for work on freed blocks");
+  ++stats_.device_syncs;
+  for (auto& [cls, list] : pending_) {
+    auto& dst = free_lists_[cls];
+    dst.insert(dst.end(), list.begin(), list.end());
+    stats_.pending_bytes -= cls * list.size();
+    stats_.cached_bytes += cls * list.size();
+  }
+  pending_.clear();
+  return Status::ok();
+}
+
+HipAllocator::Stats HipAllocator::stats() {
+  std::lock_guard<std::mutex> lock(mu_);
+  return stats_;
 }
 
 Result<void*> HipAllocator::allocate(size_t bytes, size_t alignment) {
@@ -94,24 +140,38 @@ Result<void*> HipAllocator::allocate(size_t bytes, size_t alignment) {
                                                          " exceeds the guaranteed " + std::to_string(kGuaranteedAlignment));
   const size_t cls = size_class(bytes);
   std::lock_guard<std::mutex> lock(mu_);
-  auto it = free_lists_.find(cls);
-  if (it != free_lists_.end() && !it->second.empty()) {
+  auto take = [&]() -> void* {
+    auto it = free_lists_.find(cls);
+    if (it == free_lists_.end() || it->second.empty()) return nullptr;
     void* p = it->second.back();
     it->second.pop_back();
-    live_.emplace(p, cls);
+    stats_.cached_bytes -= cls;
     return p;
+  };
+  void* p = take();
+  if (p == nullptr) {
+    auto pend = pending_.find(cls);
+    if (pend != pending_.end() && !pend->second.empty()) {
+      FRAME_RETURN_IF_ERROR(release_pending_locked());
+      p = take();
+    }
   }
-  void* p = nullptr;
-  fh_status st = fh_malloc(&p, cls, device_);
-  if (st == FH_OUT_OF_MEMORY) {
-    // Give the cache back to the device and retry once.
-    for (auto& [c, list] : free_lists_)
-      for (void* q : list) (void)fh_free(q);
-    free_lists_.clear();
-    st = fh_malloc(&p, cls, device_);
+  if (p == nullptr) {
+    fh_status st = fh_malloc(&p, cls, device_);
+    if (st == FH_OUT_OF_MEMORY) {
+      // Give the whole cache back to the device (pending blocks once their work is done) and retry once.
+      FRAME_RETURN_IF_ERROR(release_pending_locked());
+      for (auto& [c, list] : free_lists_)
+        for (void* q : list) (void)fh_free(q);
+      free_lists_.clear();
+      stats_.cached_bytes = 0;
+      st = fh_malloc(&p, cls, device_);
+    }
+    if (st != FH_OK) return from_fh(st, "HipAllocator::allocate(" + std::to_string(bytes) + " bytes)");
+    ++stats_.device_allocations;
   }
-  if (st != FH_OK) return from_fh(st, "HipAllocator::allocate(" + std::to_string(bytes) + " bytes)");
   live_.emplace(p, cls);
+  stats_.live_bytes += cls;
   return p;
 }
 
@@ -120,7 +180,9 @@ void HipAllocator::deallocate(void* ptr) {
   std::lock_guard<std::mutex> lock(mu_);
   auto it = live_.find(ptr);
   if (it == live_.end()) return;  // not ours: ignore rather than corrupt the cache
-  free_lists_[it->second].push_back(ptr);
+  pending_[it->second].push_back(ptr);
+  stats_.live_bytes -= it->second;
+  stats_.pending_bytes += it->second;
   live_.erase(it);
 }
 

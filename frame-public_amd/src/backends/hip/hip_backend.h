@@ -37,18 +37,24 @@ Status from_fh(fh_status code, std::string_view what);
 
 class HipStream final : public hal::Stream {
  public:
-  HipStream(void* handle, int32_t device) : handle_(handle), device_(device) {}
+  HipStream(void* handle, int32_t device);
   ~HipStream() override;
   Status synchronize() override;
   Status record(hal::Event& event) override;
   Status wait(const hal::Event& event) override;
   void* native_handle() override { return handle_; }
   int32_t device() const { return device_; }
+  // Process-unique, never reused (unlike the hipStream_t address): what executables key per-stream state by.
+  uint64_t id() const { return id_; }
 
  private:
   void* handle_;
   int32_t device_;
+  uint64_t id_;
 };
+
+// Whether the HipStream with this id still exists (ids of destroyed streams are never handed out again).
+bool hip_stream_alive(uint64_t id);
 
 class HipEvent final : public hal::Event {
  public:
@@ -66,10 +72,13 @@ class HipEvent final : public hal::Event {
   bool recorded_ = false;  // an event never recorded counts as complete
 };
 
-// Device memory with a size-class cache: freed blocks go back to per-size free lists and are handed out again
-// without calling hipMalloc. Memory returned to the cache may be reused by the next allocate(); callers free a
-// block only after the work that uses it is ordered before any later use (same stream or synchronised), which
-// is how the executor and the runtime use it.
+// Device memory with a size-class cache, so repeated runs do not call hipMalloc. deallocate() carries no stream
+// (hal::Allocator), and kernels queued on any stream before the free may still read or write the block, so a
+// freed block first goes to a pending list. Pending blocks become reusable only after a device-wide
+// synchronisation, which allocate() performs once, when a request of that size class finds no reusable block but
+// pending ones exist; every pending block is released by that one wait. A block is therefore never handed out
+// while work queued before its free can still touch it (the reference gets this from cudaFree, which synchronises
+// on every free, src/backends/cuda/cuda_allocator.cpp:55-66).
 class HipAllocator final : public hal::Allocator {
  public:
   explicit HipAllocator(int32_t device) : device_(device) {}
@@ -78,12 +87,22 @@ class HipAllocator final : public hal::Allocator {
   void deallocate(void* ptr) override;
   static constexpr size_t kGuaranteedAlignment = 256;
 
- private:
+  // Bytes held by the cache (reusable + pending) and by live blocks; for tests of memory growth.
+  struct Stats {
+    size_t live_bytes = 0, cached_bytes = 0, pending_bytes = 0;
+    uint64_t device_allocations = 0, device_syncs = 0;
+  };
+  Stats stats();
   static size_t size_class(size_t bytes);
+
+ private:
+  Status release_pending_locked();  // device-wide wait, then pending -> reusable
   int32_t device_;
   std::mutex mu_;
   std::unordered_map<void*, size_t> live_;           // pointer -> size class
-  std::map<size_t, std::vector<void*>> free_lists_;  // size class -> cached blocks
+  std::map<size_t, std::vector<void*>> free_lists_;  // size class -> reusable blocks
+  std::map<size_t, std::vector<void*>> pending_;     // size class -> freed, not yet known to be idle
+  Stats stats_;
 };
 
 class HipBackend final : public hal::Backend {

@@ -842,30 +842,40 @@ class HipExecutable final : public hal::Executable {
     FRAME_RETURN_IF_ERROR(hal::validate_tensor_devices(inputs, device_, "HipExecutable::run: input"));
     FRAME_RETURN_IF_ERROR(hal::validate_tensor_devices(outputs, device_, "HipExecutable::run: output"));
     void* sh = stream.native_handle();
+    // Per-stream state is keyed by the HipStream's process-unique id (a destroyed stream's handle address can come
+    // back for a new stream). A stream of another backend gets no cached state: a transient arena for this run.
+    auto* hs = dynamic_cast<HipStream*>(&stream);
+    const uint64_t sid = hs != nullptr ? hs->id() : 0;
     std::shared_ptr<Storage> arena;
-    if (plan_.arena_total_bytes > 0) {
+    {
       std::lock_guard<std::mutex> lock(mu_);
-      auto& a = arenas_[sh];
-      if (!a) {
-        Result<std::shared_ptr<Storage>> st = Storage::allocate(*alloc_, plan_.arena_total_bytes, kDefaultAlignment, device_);
-        if (!st.is_ok()) return st.status();
-        a = st.value();
+      prune_stream_state_locked(sid);
+      if (plan_.arena_total_bytes > 0) {
+        StreamArena* a = sid != 0 ? &arenas_[sid] : nullptr;
+        if (a == nullptr || !a->storage) {
+          Result<std::shared_ptr<Storage>> st = Storage::allocate(*alloc_, plan_.arena_total_bytes, kDefaultAlignment, device_);
+          if (!st.is_ok()) return st.status();
+          if (a != nullptr) a->storage = st.value();
+          arena = st.value();
+        } else {
+          arena = a->storage;
+        }
+        if (a != nullptr) a->last_use = ++use_clock_;
       }
-      arena = a;
     }
     // Replay (opt-in, FRAME_HIP_GRAPHS=1): the second run on a stream with the same input and output addresses
     // captures the step sequence into a HIP graph, and later runs with those addresses launch that graph instead
     // of every step; other addresses run the steps directly. Off by default: on this ROCm a graph launch costs
     // ~10 us more than launching its kernels (measured: C1 forward 23.8 -> 29.8 us, a 1024^3 GEMM 7 -> 18.5 us),
     // and every workload here keeps the GPU busy without it.
-    if (sh == nullptr || !graphs_enabled()) return run_steps(inputs, outputs, stream, arena);
+    if (sh == nullptr || sid == 0 || !graphs_enabled()) return run_steps(inputs, outputs, stream, arena);
     std::vector<const void*> key;
     for (const Tensor& t : inputs) key.push_back(t.raw_data());
     for (const Tensor& t : outputs) key.push_back(t.raw_data());
     bool capture = false;
     {
       std::lock_guard<std::mutex> lock(mu_);
-      GraphCache& gc = graphs_[sh];
+      GraphCache& gc = graphs_[sid];
       if (gc.exec != nullptr && gc.key == key) {
         FRAME_HIP_RETURN_IF_ERROR(fh_graph_launch(gc.exec, sh), "HipExecutable: graph replay");
         return Status::ok();
@@ -884,7 +894,7 @@ class HipExecutable final : public hal::Executable {
     void* exec = nullptr;
     const fh_status end = fh_graph_end_capture(sh, st.is_ok() ? 1 : 0, &exec);
     std::lock_guard<std::mutex> lock(mu_);
-    GraphCache& gc = graphs_[sh];
+    GraphCache& gc = graphs_[sid];
     if (!st.is_ok() || end != FH_OK || exec == nullptr) {
       gc.failed = true;  // something in the steps cannot be captured: this executable runs them directly
       if (!st.is_ok()) return st;
@@ -898,6 +908,36 @@ class HipExecutable final : public hal::Executable {
   ~HipExecutable() override {
     for (auto& [s, gc] : graphs_)
       if (gc.exec != nullptr) (void)fh_graph_destroy(gc.exec);
+  }
+
+ private:
+  // Drops the arenas and graphs of destroyed streams (their memory returns to the allocator, which reuses it only
+  // once the device is idle), and keeps at most kMaxStreamArenas arenas, evicting the least recently used, so an
+  // executable run on ever new streams (run_with_allocated_outputs creates one per call) holds bounded memory.
+  void prune_stream_state_locked(uint64_t current) {
+    for (auto it = arenas_.begin(); it != arenas_.end();)
+      it = (it->first != current && !hip_stream_alive(it->first)) ? arenas_.erase(it) : std::next(it);
+    for (auto it = graphs_.begin(); it != graphs_.end();) {
+      if (it->first != current && !hip_stream_alive(it->first)) {
+        if (it->second.exec != nullptr) (void)fh_graph_destroy(it->second.exec);
+        it = graphs_.erase(it);
+      } else {
+        ++it;
+      }
+    }
+    while (arenas_.size() > kMaxStreamArenas) {
+      auto lru = arenas_.end();
+      for (auto it = arenas_.begin(); it != arenas_.end(); ++it)
+        if (it->first != current && (lru == arenas_.end() || it->second.last_use < lru->second.last_use)) lru = it;
+      if (lru == arenas_.end()) break;
+      arenas_.erase(lru);
+    }
+  }
+
+ public:
+  size_t cached_arena_count() {
+    std::lock_guard<std::mutex> lock(mu_);
+    return arenas_.size();
   }
 
  private:
@@ -984,9 +1024,15 @@ class HipExecutable final : public hal::Executable {
   hal::CompileOptions options_;
   std::vector<hal::IoSpec> in_sig_, out_sig_;
   std::unordered_map<size_t, Tensor> constants_;  // step index -> device tensor
+  struct StreamArena {
+    std::shared_ptr<Storage> storage;
+    uint64_t last_use = 0;
+  };
+  static constexpr size_t kMaxStreamArenas = 4;
   std::mutex mu_;
-  std::unordered_map<void*, std::shared_ptr<Storage>> arenas_;  // per stream
-  std::unordered_map<void*, GraphCache> graphs_;                 // per stream
+  uint64_t use_clock_ = 0;
+  std::unordered_map<uint64_t, StreamArena> arenas_;  // HipStream id -> arena
+  std::unordered_map<uint64_t, GraphCache> graphs_;   // HipStream id -> captured step list
 };
 
 }  // namespace

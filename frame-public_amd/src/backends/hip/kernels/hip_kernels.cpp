@@ -2,12 +2,14 @@
 // libframe_hip_kernels.so on the context's stream. Registered with FRAME_REGISTER_KERNEL(op, "hip", fn) like
 // every Frame backend's kernels (reference: include/frame/ops/kernel_registry.h:104-107). The design analogs
 // replaced are the cuda kernels under src/backends/cuda/kernels/ (cuBLASLt, cuDNN and the .cu files).
+#include <algorithm>
 #include <array>
 #include <cstdint>
 #include <string>
 #include <vector>
 
 #include <frame/core/tensor.h>
+#include <frame/hal/backend.h>
 #include <frame/ops/constant_utils.h>
 #include <frame/ops/fused_elementwise_utils.h>
 #include <frame/ops/kernel_registry.h>
@@ -159,6 +161,49 @@ Status gemm_epilogue_kernel(KernelContext& ctx) {
   return gemm_impl(ctx, std::string(kGemmEpilogueOp), n_main ? static_cast<size_t>(*n_main) : 2);
 }
 
+// An NCHW conv2d (an eager Backend::launch, or a node HipBackend::compile did not lower) whose geometry the
+// implicit-GEMM kernel accepts runs on MFMA: channels-last copies of x and w (or their C8 packs when Cin <= 8,
+// 16-bit) go to device temporaries from the backend's allocator, then the MFMA conv writes y NCHW with the bias
+// and epilogue. The temporaries go back to the allocator when this call returns; it hands them out again only
+// after the device has gone idle, so the queued kernels still own them. Returns false when the geometry is
+// outside that kernel's envelope (the caller then runs the direct kernel).
+Result<bool> conv_via_channels_last(const KernelContext& ctx, const std::string& op, int32_t dt, const int64_t geom[12],
+                                    const Tensor* bias, const fh_epilogue& ep) {
+  const Tensor& x = ctx.inputs[0];
+  const Tensor& w = ctx.inputs[1];
+  const bool c8 = dt != FH_F32 && geom[1] <= 8 && geom[11] == 1;
+  int64_t g[12];
+  std::copy(geom, geom + 12, g);
+  if (c8) g[1] = 8;
+  if (fh_conv2d_nhwc_supported(dt, g) == 0) return false;
+  Result<hal::Backend*> be = hal::BackendRegistry::instance().get(kHipBackendName);
+  if (!be.is_ok()) return be.status();
+  hal::Allocator* alloc = be.value()->allocator(ctx.device);
+  if (alloc == nullptr) return Status::make(ErrorCode::kInternal, "op '" + op + "' (hip): no allocator for the device");
+  const int64_t n = geom[0], cin = geom[1], h = geom[2], wd = geom[3], cout = geom[4], kh = geom[5], kw = geom[6];
+  Result<Tensor> xt = Tensor::empty(Shape({n, h, wd, c8 ? 8 : cin}), x.dtype(), ctx.device, *alloc);
+  if (!xt.is_ok()) return xt.status();
+  Result<Tensor> wt = c8 ? Tensor::empty(Shape({cout, fh_conv_c8_filter_k(kh, kw)}), w.dtype(), ctx.device, *alloc)
+                         : Tensor::empty(Shape({cout, kh, kw, cin}), w.dtype(), ctx.device, *alloc);
+  if (!wt.is_ok()) return wt.status();
+  void* s = stream_handle(ctx);
+  const std::string what = "op '" + op + "' (hip)";
+  if (c8) {
+    FRAME_HIP_RETURN_IF_ERROR(fh_conv_pack_input_c8(x.raw_data(), xt.value().raw_data(), n, static_cast<int32_t>(cin), h * wd, s), what);
+    FRAME_HIP_RETURN_IF_ERROR(fh_conv_pack_filter_c8(w.raw_data(), wt.value().raw_data(), static_cast<int32_t>(cout),
+                                                     static_cast<int32_t>(cin), static_cast<int32_t>(kh),
+                                                     static_cast<int32_t>(kw), s), what);
+  } else {
+    const int32_t es = static_cast<int32_t>(x.dtype().itemsize());
+    FRAME_HIP_RETURN_IF_ERROR(fh_transpose_batched(es, x.raw_data(), xt.value().raw_data(), n, cin, h * wd, s), what);
+    FRAME_HIP_RETURN_IF_ERROR(fh_transpose_batched(es, w.raw_data(), wt.value().raw_data(), cout, cin, kh * kw, s), what);
+  }
+  FRAME_HIP_RETURN_IF_ERROR(fh_conv2d_nhwc_fwd_ex(dt, xt.value().raw_data(), wt.value().raw_data(),
+                                                  bias ? bias->raw_data() : nullptr, ctx.outputs[0].raw_data(), g,
+                                                  ep.nseg > 0 ? &ep : nullptr, 0, s), what);
+  return true;
+}
+
 Status conv_impl(KernelContext& ctx, const std::string& op, size_t n_main) {
   if (ctx.inputs.size() < n_main || n_main < 2 || n_main > 3 || ctx.outputs.size() != 1) return invalid(op, "bad operand count");
   const Tensor& x = ctx.inputs[0];
@@ -185,6 +230,11 @@ Status conv_impl(KernelContext& ctx, const std::string& op, size_t n_main) {
   if (bias != nullptr && (bias->shape().rank() != 1 || bias->shape().dim(0) != geom[4])) return invalid(op, "bias must be [Cout]");
   Result<fh_epilogue> ep = make_epilogue(ctx, op, n_main);
   if (!ep.is_ok()) return ep.status();
+  if (y.numel() > 0) {
+    Result<bool> done = conv_via_channels_last(ctx, op, dt.value(), geom, bias, ep.value());
+    if (!done.is_ok()) return done.status();
+    if (done.value()) return Status::ok();
+  }
   FRAME_HIP_RETURN_IF_ERROR(fh_conv2d_fwd(dt.value(), x.raw_data(), w.raw_data(), bias ? bias->raw_data() : nullptr,
                                           y.raw_data(), geom, ep.value().nseg > 0 ? &ep.value() : nullptr, stream_handle(ctx)),
                             "op '" + op + "' (hip)");

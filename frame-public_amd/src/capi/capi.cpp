@@ -173,6 +173,20 @@ int frame_compile(const char* ir_text, const char* backend, int32_t opt_level, f
   return 0;
 }
 
+int frame_backend_compile(const char* ir_text, const char* backend, int32_t opt_level, frame_executable** out) {
+  if (ir_text == nullptr || backend == nullptr || out == nullptr) return fail_msg("frame_backend_compile: null argument");
+  auto g = frame::ir::parse_text(ir_text);
+  if (!g.is_ok()) return fail(g.status());
+  auto b = backend_of(backend);
+  if (!b.is_ok()) return fail(b.status());
+  frame::hal::CompileOptions opts;
+  opts.opt_level = opt_level;
+  auto e = b.value()->compile(g.value(), opts);
+  if (!e.is_ok()) return fail(e.status());
+  *out = new frame_executable{std::shared_ptr<frame::hal::Executable>(std::move(e.value())), backend};
+  return 0;
+}
+
 void frame_executable_free(frame_executable* e) { delete e; }
 int32_t frame_executable_num_inputs(const frame_executable* e) {
   return static_cast<int32_t>(e->exe->input_signature().size());
@@ -305,6 +319,39 @@ int frame_launch(const char* node_ir_text, const char* backend, frame_tensor* co
   frame::hal::KernelInvocation inv{node->op(), ins, outs, &node->attrs(), frame::Device{b.value()->name(), 0}};
   frame::Status s = b.value()->launch(inv, stream ? stream->s.get() : nullptr);
   return s.is_ok() ? 0 : fail(s);
+}
+
+int frame_backend_copy(const char* backend, void* dst, const char* dst_backend, int32_t dst_index, const void* src,
+                       const char* src_backend, int32_t src_index, size_t bytes, frame_stream* stream) {
+  auto b = backend_of(backend);
+  if (!b.is_ok()) return fail(b.status());
+  auto dev = [](const char* name, int32_t index) -> frame::Result<frame::Device> {
+    if (name == nullptr) return frame::Status::make(frame::ErrorCode::kInvalidArgument, "device backend is null");
+    const std::string_view n(name);
+    if (n == frame::kCpuBackendName) return frame::Device{frame::kCpuBackendName, index};
+    if (n == frame::kHipBackendName) return frame::Device{frame::kHipBackendName, index};
+    return frame::Status::make(frame::ErrorCode::kInvalidArgument, "unknown device backend '" + std::string(n) + "'");
+  };
+  auto d = dev(dst_backend, dst_index);
+  if (!d.is_ok()) return fail(d.status());
+  auto s = dev(src_backend, src_index);
+  if (!s.is_ok()) return fail(s.status());
+  frame::Status st = b.value()->copy(dst, d.value(), src, s.value(), bytes, stream ? stream->s.get() : nullptr);
+  return st.is_ok() ? 0 : fail(st);
+}
+
+int frame_hip_allocator_stats(int32_t device, uint64_t out[5]) {
+  auto b = backend_of(frame::kHipBackendName.data());
+  if (!b.is_ok()) return fail(b.status());
+  auto* a = dynamic_cast<frame::backends::hip::HipAllocator*>(b.value()->allocator(frame::Device{frame::kHipBackendName, device}));
+  if (a == nullptr) return fail_msg("frame_hip_allocator_stats: no hip allocator for device " + std::to_string(device));
+  const auto st = a->stats();
+  out[0] = st.live_bytes;
+  out[1] = st.cached_bytes;
+  out[2] = st.pending_bytes;
+  out[3] = st.device_allocations;
+  out[4] = st.device_syncs;
+  return 0;
 }
 
 }  // extern "C"

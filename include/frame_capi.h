@@ -53,6 +53,10 @@ int frame_event_synchronize(frame_event* e);
 
 /* runtime::compile of IR text for `backend` (opt_level as hal::CompileOptions::opt_level). */
 int frame_compile(const char* ir_text, const char* backend, int32_t opt_level, frame_executable** out);
+/* Backend::compile (include/frame/hal/backend.h:104-105) of the graph as given: no pass pipeline, no cache. An op
+ * without a kernel on the backend fails with kUnimplemented naming the op (the HAL conformance contract,
+ * reference tests/cpp/hal_conformance/test_hal_conformance.cpp:249-269). */
+int frame_backend_compile(const char* ir_text, const char* backend, int32_t opt_level, frame_executable** out);
 void frame_executable_free(frame_executable* e);
 int32_t frame_executable_num_inputs(const frame_executable* e);
 int32_t frame_executable_num_outputs(const frame_executable* e);
@@ -87,6 +91,17 @@ int frame_sgd_update_text(const char* ir_text, const int32_t* param_inputs, int3
  * lowering (fused attention, matmul/conv epilogues at opt_level >= 1, channels-last conv), as IR text.
  * Host-only (no device needed); no counterpart in the reference, which has no backend lowering to inspect. */
 int frame_hip_lowered_text(const char* ir_text, int32_t opt_level, char* out, int64_t cap, int64_t* needed);
+
+/* Backend::copy (include/frame/hal/backend.h:100-102) between two devices named by backend and index; "cpu" means
+ * host memory. The direction follows the two devices; asynchronous on `stream` when it is non-null, synchronous
+ * otherwise (the reference's contract, src/backends/cuda/cuda_backend.cpp:185-204). */
+int frame_backend_copy(const char* backend, void* dst, const char* dst_backend, int32_t dst_index, const void* src,
+                       const char* src_backend, int32_t src_index, size_t bytes, frame_stream* stream);
+
+/* Counters of the hip backend's caching allocator for `device`: out[0] live bytes, out[1] reusable cached bytes,
+ * out[2] freed bytes waiting for the device to go idle, out[3] device allocations made, out[4] device-wide waits.
+ * No counterpart in the reference (its allocator caches nothing); for tests of memory growth. */
+int frame_hip_allocator_stats(int32_t device, uint64_t out[5]);
 
 /* Eager single-op launch (Backend::launch) of the one operator node in `node_ir_text` (a graph whose
  * non-input nodes are exactly one op) on the given tensors. */

@@ -240,6 +240,24 @@ def test_attention_support_query_is_host_only():
     assert lib.fh_attention_supported(3, 100, 64) == 0 and lib.fh_attention_supported(3, 1024, 64) == 0
 
 
+def test_wgrad_workspace_rejects_invalid_geometry_on_the_host():
+    """fh_conv2d_wgrad_workspace validates before it divides: zero strides, negative padding, zero extents and a
+    filter larger than the padded input give -1 (no SIGFPE, no truncated output size); host-only."""
+    lib = abi.lib()
+
+    def ws(geom):
+        return lib.fh_conv2d_wgrad_workspace(3, abi.i64_array(geom), 64, None)
+
+    good = [32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1]
+    assert ws(good) > 0
+    for k, v in [(7, 0), (8, 0), (7, -1), (9, -1), (10, -2), (0, 0), (2, 0), (5, 0)]:
+        bad = list(good)
+        bad[k] = v
+        assert ws(bad) == -1, (k, v)
+    assert ws([1, 64, 2, 2, 64, 5, 5, 1, 1, 1, 1, 1]) == -1  # h + 2p < kh
+    assert ws([1, 64, 8, 2, 64, 3, 5, 1, 1, 1, 1, 1]) == -1  # w + 2p < kw
+
+
 @pytest.mark.parametrize("dtype,cin,lowered", [(3, 64, "hip_conv2d_nhwc_internal"), (0, 64, "hip_conv2d_nhwc_internal"),
                                                (3, 3, "hip_pack_input_c8_internal"), (0, 3, "conv2d"),
                                                (0, 24, "conv2d")])
