@@ -12,6 +12,8 @@
 // taps in the padding, two LDS stages of 64 p-rows. The larger tile loads 1.5x fewer bytes per MFMA, which is
 // what limits this kernel: operands come from L2 (x is read once per filter tap).
 #include <algorithm>
+#include <mutex>
+#include <string>
 
 #include "fh_mfma16.h"
 
@@ -259,6 +261,37 @@ fh_status run_wgrad(const WgradArgs& args, int32_t splits, int32_t cin_real, int
   return launch_status("wgrad_reduce_kernel");
 }
 
+// ---- no-allocation variant -----------------------------------------------------------------------------------
+// The split-K partials of fh_conv2d_wgrad_nhwc_noalloc live in this file-scope device array. Each device the
+// library runs on holds its own copy until the process ends. In host code the name `scratch` is only a host-side
+// stand-in: its device address is looked up once per device (hipGetSymbolAddress with that device current) and
+// only that address is handed to kernels. Nothing in it needs to start at zero: the main kernel writes every
+// partial of every split before the reduction reads it.
+constexpr int64_t kWgradScratchBytes = int64_t{64} << 20;
+constexpr int kScratchMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kWgradScratchBytes];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchMaxDevices] = {};
+
+fh_status scratch_of_current_device(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess) return fail(FH_DEVICE_ERROR, "fh_conv2d_wgrad_nhwc_noalloc: hipGetDevice failed");
+  if (dev < 0 || dev >= kScratchMaxDevices)
+    return fail(FH_UNIMPLEMENTED, "fh_conv2d_wgrad_nhwc_noalloc: device index above 63");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(FH_DEVICE_ERROR, std::string("fh_conv2d_wgrad_nhwc_noalloc: hipGetSymbolAddress(scratch): ") +
+                                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return FH_OK;
+}
+
 }  // namespace
 }  // namespace fh
 
@@ -318,4 +351,17 @@ extern "C" fh_status fh_conv2d_wgrad_nhwc(int32_t dtype, const void* x, const vo
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == FH_BF16) return run_wgrad<bf16_t>(a, splits, static_cast<int32_t>(geom[1]), static_cast<int32_t>(geom[5]), dw, s);
   return run_wgrad<f16_t>(a, splits, static_cast<int32_t>(geom[1]), static_cast<int32_t>(geom[5]), dw, s);
+}
+
+extern "C" fh_status fh_conv2d_wgrad_nhwc_noalloc(int32_t dtype, const void* x, const void* dy, void* dw,
+                                                  const int64_t geom[12], int32_t cin_pad, void* stream) {
+  const int64_t need = fh_conv2d_wgrad_workspace(dtype, geom, cin_pad, nullptr);
+  if (need < 0) return fail(FH_UNIMPLEMENTED, "fh_conv2d_wgrad_nhwc_noalloc: unsupported dtype or geometry");
+  if (need > kWgradScratchBytes)
+    return fail(FH_INVALID_ARGUMENT, "fh_conv2d_wgrad_nhwc_noalloc: the split-K partials need " + std::to_string(need) +
+                                         " bytes, above the " + std::to_string(kWgradScratchBytes) +
+                                         "-byte no-allocation scratch (use fh_conv2d_wgrad_nhwc with a workspace)");
+  void* ws = nullptr;
+  if (fh_status st = scratch_of_current_device(&ws); st != FH_OK) return st;
+  return fh_conv2d_wgrad_nhwc(dtype, x, dy, dw, ws, need, geom, cin_pad, stream);
 }

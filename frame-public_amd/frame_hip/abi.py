@@ -94,6 +94,8 @@ _SIGS = {
     "fh_conv2d_grad_input": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, POINTER(c_int64), c_void_p]),
     "fh_conv2d_grad_filter": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, POINTER(c_int64), c_void_p]),
     "fh_conv2d_wgrad_workspace": (c_int64, [c_int32, POINTER(c_int64), c_int32, POINTER(c_int32)]),
+    "fh_conv2d_wgrad_nhwc_noalloc": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, POINTER(c_int64), c_int32,
+                                               c_void_p]),
     "fh_conv2d_wgrad_nhwc": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, POINTER(c_int64), c_int32,
                                        c_void_p]),
     "fh_axpy_multi": (c_int32, [c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),

@@ -287,6 +287,13 @@ fh_status fh_conv2d_grad_filter(int32_t dtype, const void* x, const void* dy, vo
 int64_t fh_conv2d_wgrad_workspace(int32_t dtype, const int64_t geom[12], int32_t cin_pad, int32_t* splits);
 fh_status fh_conv2d_wgrad_nhwc(int32_t dtype, const void* x, const void* dy, void* dw, void* workspace,
                                int64_t workspace_bytes, const int64_t geom[12], int32_t cin_pad, void* stream);
+/* fh_conv2d_wgrad_nhwc without a caller workspace and without any allocation: the split-K partials go to a
+ * 64 MiB file-scope device array that each device holds until the process ends. No counterpart in the
+ * reference; it is for callers that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Geometries whose partials (fh_conv2d_wgrad_workspace) exceed 64 MiB fail with
+ * FH_INVALID_ARGUMENT. Every call on a device shares that device's array: calls that overlap on one device race. */
+fh_status fh_conv2d_wgrad_nhwc_noalloc(int32_t dtype, const void* x, const void* dy, void* dw, const int64_t geom[12],
+                                       int32_t cin_pad, void* stream);
 
 /* Operands of conv2d_grad_input as a stride-1 convolution on the implicit-GEMM kernel (dx = conv(dilate(dy),
  * flip(w)), padding KH-1-pad): fh_conv_filter_flip writes out[ci][a][b][co] = w[co][ci][KH-1-a][KW-1-b] (the
