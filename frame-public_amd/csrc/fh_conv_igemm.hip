@@ -33,6 +33,7 @@
 
 #include <algorithm>
 #include <string>
+#include <type_traits>
 #include <utility>
 
 #include "fh_common.h"
@@ -74,7 +75,138 @@ __device__ __forceinline__ void fence_kfragments(KFragments<TM, TN>& f) {
   for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(f.b[j]));
 }
 
-template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, bool C8>
+// Writes one wave's accumulator tile (output channels m0w.. m0w+WM-1, output pixels n0w.. n0w+WN-1): bias added to
+// the fp32 sum, one rounding, the fused chain on the rounded value, stored NCHW or channels-last (args.out_nhwc),
+// staged through `lds` (LDS_BYTES of LDS the caller no longer needs; each wave uses its own slice).
+template <typename T, int E, int WM, int WN, int NW, int LDS_BYTES>
+__device__ __forceinline__ void conv_store_tile(const ConvNhwcArgs& args, f32x16_t (&acc)[WM / 32][WN / 32],
+                                                unsigned char* lds, int wave, int lane, int m0w, int64_t n0w,
+                                                const float* bias_lds = nullptr) {
+  using S = typename Io<T>::storage;
+  constexpr int ES = static_cast<int>(sizeof(S));
+  constexpr int V = 16 / ES;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  const int l32 = lane & 31, hi = lane >> 5;
+  S* __restrict__ Y = static_cast<S*>(args.y);
+  const S* bias = static_cast<const S*>(args.bias);
+  // The bias of every accumulator row of this lane. Lane l loads row l of the wave tile (one coalesced load per
+  // wave) and the rows each lane needs are exchanged across lanes. Every workgroup reads the same few bias lines:
+  // sixteen 2-byte gathers per lane, as a per-row load would issue, pile up on one L2 channel (measured: 5-15 us of
+  // a 30 us C3 conv spent waiting for them).
+  static_assert(WM <= 64, "one bias row per lane");
+  float bv[TM][16];
+  {
+    // bias_lds: the kernel staged the whole bias as floats in LDS (no global access in its epilogue)
+    const int brow = min(m0w + lane % WM, args.cout - 1);
+    const float mine = bias_lds != nullptr ? bias_lds[brow] : bias != nullptr ? Io<T>::load(bias[brow]) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int x = 0; x < 16; ++x) bv[i][x] = __shfl(mine, i * 32 + 8 * (x >> 2) + 4 * hi + (x & 3));
+  }
+  if (args.out_nhwc) {
+    // Channels-last output. The wave tile is staged pixel-major: pixel pc's WM channels are a row of PITCH
+    // elements (padded by one 16-byte chunk so the 32 pixels of one accumulator register spread over the banks),
+    // written two channels at a time. Then lane -> (pixel, group g of V channels) with g fastest: each lane reads
+    // 16 contiguous bytes and consecutive lanes write consecutive 16-byte chunks of a pixel's channel run.
+    constexpr int PITCH = WM + V;
+    constexpr int GPW = WM / V;
+    static_assert((WN * GPW) % 64 == 0, "whole waves of (pixel, channel group) pairs");
+    // configurations whose pixel-major staging would not fit the ring are never launched with out_nhwc
+    // (launch_conv refuses them)
+    if constexpr (NW * WN * PITCH * ES <= LDS_BYTES) {
+    S* wl = reinterpret_cast<S*>(lds + wave * (WN * PITCH * ES));
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int x = 0; x < 16; x += 2) {
+        const int rr = i * 32 + 8 * (x >> 2) + 4 * hi + (x & 3);  // even: rows rr, rr + 1 are registers x, x + 1
+        const float b0 = bv[i][x], b1 = bv[i][x + 1];
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          S* dst = wl + (j * 32 + l32) * PITCH + rr;
+          if constexpr (ES == 2) {
+            const uint32_t w = static_cast<uint32_t>(Io<T>::store(acc[i][j][x] + b0)) |
+                               (static_cast<uint32_t>(Io<T>::store(acc[i][j][x + 1] + b1)) << 16);
+            *reinterpret_cast<uint32_t*>(dst) = w;
+          } else {
+            dst[0] = Io<T>::store(acc[i][j][x] + b0);
+            dst[1] = Io<T>::store(acc[i][j][x + 1] + b1);
+          }
+        }
+      }
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll 2
+    for (int it = 0; it < WN * GPW / 64; ++it) {
+      const int id = it * 64 + lane;
+      const int g = id % GPW, pc = id / GPW;
+      const int co0 = m0w + g * V;
+      const int64_t p = n0w + pc;
+      if (co0 >= args.cout || p >= args.p) continue;
+      uint4 packed = *reinterpret_cast<const uint4*>(wl + pc * PITCH + g * V);
+      const int64_t idx = p * args.cout + co0;
+      if (args.vec_store && co0 + V <= args.cout) {
+        packed = epi_vec<E, T>(args.ep, packed, idx);
+        *reinterpret_cast<uint4*>(Y + idx) = packed;
+      } else {
+        S vals[V];
+        __builtin_memcpy(vals, &packed, 16);
+        for (int e = 0; e < V && co0 + e < args.cout; ++e) {
+          S v = vals[e];
+          if constexpr (E != kEpiNone) v = Io<T>::store(epi_one<E, T>(args.ep, Io<T>::load(v), idx + e));
+          Y[idx + e] = v;
+        }
+      }
+    }
+    }
+    return;
+  }
+  constexpr int WTILE_BYTES = WM * WN * ES;
+  static_assert(NW * WTILE_BYTES <= LDS_BYTES, "the wave tiles fit in the LDS space");
+  S* wl = reinterpret_cast<S*>(lds + wave * WTILE_BYTES);
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      const int rr = i * 32 + 8 * (x >> 2) + 4 * hi + (x & 3);
+#pragma unroll
+      for (int j = 0; j < TN; ++j) wl[rr * WN + j * 32 + l32] = Io<T>::store(acc[i][j][x] + bv[i][x]);
+    }
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __builtin_amdgcn_wave_barrier();
+  constexpr int LPR = WN / V;
+  constexpr int RPI = 64 / LPR;
+  static_assert(64 % LPR == 0 && WM % RPI == 0, "epilogue access shape");
+  const int c = (lane % LPR) * V;
+  const int64_t p0 = n0w + c;
+  for (int it = 0; it < WM / RPI; ++it) {
+    const int rr = it * RPI + lane / LPR;
+    const int co = m0w + rr;
+    if (co >= args.cout || p0 >= args.p) continue;
+    uint4 packed = *reinterpret_cast<const uint4*>(wl + rr * WN + c);
+    if (args.vec_store && p0 + V <= args.p) {
+      const uint32_t img = static_cast<uint32_t>(p0) / static_cast<uint32_t>(args.howo);  // P < 2^31
+      const int64_t idx = (static_cast<int64_t>(img) * args.cout + co) * args.howo +
+                          (static_cast<uint32_t>(p0) - img * static_cast<uint32_t>(args.howo));
+      packed = epi_vec<E, T>(args.ep, packed, idx);
+      *reinterpret_cast<uint4*>(Y + idx) = packed;
+    } else {
+      S vals[V];
+      __builtin_memcpy(vals, &packed, 16);
+      for (int e = 0; e < V && p0 + e < args.p; ++e) {
+        const int64_t p = p0 + e;
+        const int64_t img = p / args.howo;
+        const int64_t idx = (img * args.cout + co) * args.howo + (p - img * args.howo);
+        S v = vals[e];
+        if constexpr (E != kEpiNone) v = Io<T>::store(epi_one<E, T>(args.ep, Io<T>::load(v), idx));
+        Y[idx] = v;
+      }
+    }
+  }
+}
+
+template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, bool C8, int E>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNhwcArgs args) {
   using S = typename Io<T>::storage;
   constexpr int ES = static_cast<int>(sizeof(S));
@@ -304,110 +436,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
   wait_vmcnt<0>();
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __syncthreads();
-  constexpr int V = EPC;
-  S* __restrict__ Y = static_cast<S*>(args.y);
-  const S* bias = static_cast<const S*>(args.bias);
-  if (args.out_nhwc) {
-    // Channels-last output. The wave tile is staged pixel-major: pixel pc's WM channels are a row of PITCH
-    // elements (padded by one 16-byte chunk so the 32 pixels of one accumulator register spread over the banks),
-    // written two channels at a time. Then lane -> (pixel, group g of V channels) with g fastest: each lane reads
-    // 16 contiguous bytes and consecutive lanes write consecutive 16-byte chunks of a pixel's channel run.
-    constexpr int PITCH = WM + V;
-    constexpr int GPW = WM / V;
-    static_assert((WN * GPW) % 64 == 0, "whole waves of (pixel, channel group) pairs");
-    // configurations whose pixel-major staging would not fit the ring are never launched with out_nhwc
-    // (launch_conv refuses them)
-    if constexpr (NW * WN * PITCH * ES <= kStages * STAGE) {
-    S* wl = reinterpret_cast<S*>(ring + wave * (WN * PITCH * ES));
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int x = 0; x < 16; x += 2) {
-        const int rr = i * 32 + 8 * (x >> 2) + 4 * hi + (x & 3);  // even: rows rr, rr + 1 are registers x, x + 1
-        const float b0 = bias != nullptr ? Io<T>::load(bias[min(m0 + wm * WM + rr, args.cout - 1)]) : 0.0f;
-        const float b1 = bias != nullptr ? Io<T>::load(bias[min(m0 + wm * WM + rr + 1, args.cout - 1)]) : 0.0f;
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          S* dst = wl + (j * 32 + l32) * PITCH + rr;
-          if constexpr (ES == 2) {
-            const uint32_t w = static_cast<uint32_t>(Io<T>::store(acc[i][j][x] + b0)) |
-                               (static_cast<uint32_t>(Io<T>::store(acc[i][j][x + 1] + b1)) << 16);
-            *reinterpret_cast<uint32_t*>(dst) = w;
-          } else {
-            dst[0] = Io<T>::store(acc[i][j][x] + b0);
-            dst[1] = Io<T>::store(acc[i][j][x + 1] + b1);
-          }
-        }
-      }
-    __builtin_amdgcn_s_waitcnt(0xc07f);
-    __builtin_amdgcn_wave_barrier();
-#pragma unroll 2
-    for (int it = 0; it < WN * GPW / 64; ++it) {
-      const int id = it * 64 + lane;
-      const int g = id % GPW, pc = id / GPW;
-      const int co0 = m0 + wm * WM + g * V;
-      const int64_t p = n0 + wn * WN + pc;
-      if (co0 >= args.cout || p >= args.p) continue;
-      uint4 packed = *reinterpret_cast<const uint4*>(wl + pc * PITCH + g * V);
-      const int64_t idx = p * args.cout + co0;
-      if (args.vec_store && co0 + V <= args.cout) {
-        if (args.ep.nseg > 0) packed = epilogue_vec<T>(args.ep, packed, idx);
-        *reinterpret_cast<uint4*>(Y + idx) = packed;
-      } else {
-        S vals[V];
-        __builtin_memcpy(vals, &packed, 16);
-        for (int e = 0; e < V && co0 + e < args.cout; ++e) {
-          S v = vals[e];
-          if (args.ep.nseg > 0) v = Io<T>::store(epilogue_one<T>(args.ep, Io<T>::load(v), idx + e));
-          Y[idx + e] = v;
-        }
-      }
-    }
-    }
-    return;
-  }
-  constexpr int WTILE_BYTES = WM * WN * ES;
-  static_assert(NW * WTILE_BYTES <= kStages * STAGE, "the wave tiles fit in the ring");
-  S* wl = reinterpret_cast<S*>(ring + wave * WTILE_BYTES);
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int x = 0; x < 16; ++x) {
-      const int rr = i * 32 + 8 * (x >> 2) + 4 * hi + (x & 3);
-      const float bv = bias != nullptr ? Io<T>::load(bias[min(m0 + wm * WM + rr, args.cout - 1)]) : 0.0f;
-#pragma unroll
-      for (int j = 0; j < TN; ++j) wl[rr * WN + j * 32 + l32] = Io<T>::store(acc[i][j][x] + bv);
-    }
-  __builtin_amdgcn_s_waitcnt(0xc07f);
-  __builtin_amdgcn_wave_barrier();
-  constexpr int LPR = WN / V;
-  constexpr int RPI = 64 / LPR;
-  static_assert(64 % LPR == 0 && WM % RPI == 0, "epilogue access shape");
-  const int c = (lane % LPR) * V;
-  const int64_t p0 = n0 + wn * WN + c;
-  for (int it = 0; it < WM / RPI; ++it) {
-    const int rr = it * RPI + lane / LPR;
-    const int co = m0 + wm * WM + rr;
-    if (co >= args.cout || p0 >= args.p) continue;
-    uint4 packed = *reinterpret_cast<const uint4*>(wl + rr * WN + c);
-    if (args.vec_store && p0 + V <= args.p) {
-      const int64_t img = p0 / args.howo;
-      const int64_t idx = (img * args.cout + co) * args.howo + (p0 - img * args.howo);
-      if (args.ep.nseg > 0) packed = epilogue_vec<T>(args.ep, packed, idx);
-      *reinterpret_cast<uint4*>(Y + idx) = packed;
-    } else {
-      S vals[V];
-      __builtin_memcpy(vals, &packed, 16);
-      for (int e = 0; e < V && p0 + e < args.p; ++e) {
-        const int64_t p = p0 + e;
-        const int64_t img = p / args.howo;
-        const int64_t idx = (img * args.cout + co) * args.howo + (p - img * args.howo);
-        S v = vals[e];
-        if (args.ep.nseg > 0) v = Io<T>::store(epilogue_one<T>(args.ep, Io<T>::load(v), idx));
-        Y[idx] = v;
-      }
-    }
-  }
+  conv_store_tile<T, E, WM, WN, NW, kStages * STAGE>(args, acc, ring, wave, lane, m0 + wm * WM, n0 + wn * WN);
 }
 
 // Whether a configuration can stage its wave tiles pixel-major (channels-last output) in its LDS ring.
@@ -418,6 +447,34 @@ constexpr bool nhwc_out_fits() {
   return WAVES_M * WAVES_N * wn * (wm + 16 / es) * es <= kStages * (BM + BN) * 64;
 }
 
+// Runs f.template operator()<E>() with the fixed epilogue program of `kind` when bit E of MASK allows it, else
+// with kEpiAny (the instantiations each kernel family carries are listed by its MASK).
+template <unsigned MASK, typename F>
+fh_status with_epi(int kind, F&& f) {
+  switch (kind) {
+    case kEpiNone:
+      if constexpr ((MASK >> kEpiNone) & 1) return f.template operator()<kEpiNone>();
+      break;
+    case kEpiRelu:
+      if constexpr ((MASK >> kEpiRelu) & 1) return f.template operator()<kEpiRelu>();
+      break;
+    case kEpiAddRelu:
+      if constexpr ((MASK >> kEpiAddRelu) & 1) return f.template operator()<kEpiAddRelu>();
+      break;
+    default:
+      break;
+  }
+  return f.template operator()<kEpiAny>();
+}
+
+// bf16 (the configurations' type) gets the ResNet programs as their own kernels; other types the interpreter.
+template <typename T, bool C8>
+constexpr unsigned conv_epi_mask() {
+  if constexpr (!std::is_same_v<T, bf16_t>) return 0;
+  else if constexpr (C8) return 1u << kEpiRelu;
+  else return (1u << kEpiNone) | (1u << kEpiRelu) | (1u << kEpiAddRelu);
+}
+
 template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, bool C8>
 fh_status launch_conv(ConvNhwcArgs a, hipStream_t stream) {
   if (a.out_nhwc && !nhwc_out_fits<T, BM, BN, WAVES_M, WAVES_N>())
@@ -425,9 +482,574 @@ fh_status launch_conv(ConvNhwcArgs a, hipStream_t stream) {
   a.tiles_m = (a.cout + BM - 1) / BM;
   a.tiles_n = static_cast<int32_t>((a.p + BN - 1) / BN);
   const dim3 grid(static_cast<uint32_t>(a.tiles_m) * static_cast<uint32_t>(a.tiles_n));
-  hipLaunchKernelGGL((conv_nhwc_kernel<T, BM, BN, WAVES_M, WAVES_N, C8>), grid, dim3(WAVES_M * WAVES_N * 64), 0, stream,
-                     a);
-  return launch_status("conv_nhwc_kernel launch");
+  return with_epi<conv_epi_mask<T, C8>()>(epi_kind(a.ep), [&]<int E>() {
+    hipLaunchKernelGGL((conv_nhwc_kernel<T, BM, BN, WAVES_M, WAVES_N, C8, E>), grid, dim3(WAVES_M * WAVES_N * 64), 0,
+                       stream, a);
+    return launch_status("conv_nhwc_kernel launch");
+  });
+}
+
+// ---- 3x3 stride-1 convolutions with the input patch resident in LDS -------------------------------------------
+//
+// For KH = KW = 3, stride 1, padding 1 (output plane = input plane), 16-bit, Cin % 32 == 0, Cout <= 512. A tile is
+// 64 output channels x BN consecutive output pixels (flattened n, oh, ow). Those pixels cover a band of output
+// rows; the input they read is that band plus one halo row above and below, addressed by global input row
+// gi = n * H + ih, each row W + 2 positions wide (the two padding columns are zeros). For each chunk of 32 input
+// channels the workgroup loads the patch [rows][W + 2][32 ch] once and runs all 9 taps out of LDS: the B
+// fragment of output pixel (band row r, column c) for tap (kh, kw) is patch position (r + kh) * (W + 2) + c + kw.
+// The implicit GEMM streams one 64-byte im2col row per pixel and tap (every input byte crosses L2 -> LDS 9 times,
+// as half cache lines); here each crosses about (rows + 2) / rows times, in contiguous runs of whole lines. A tap
+// whose input row falls outside the pixel's own image (the first and last rows of every image; the patch holds
+// the neighbouring image's row there) reads three zero positions kept after the patch instead. Positions use the
+// A layout's 16-byte chunk swizzle.
+//
+// The kernel is persistent: one workgroup per CU walks tiles blockIdx.x, blockIdx.x + gridDim.x, ..., and its
+// (tile, chunk) steps form one double-buffered pipeline, so the next step's loads (the next tile's first patch
+// included) are in flight while a step is multiplied and while a finished tile is written out. RES_A (Cout <= 64,
+// Cin <= 64): the whole filter, [chunk][tap][64 rows][32 ch], is loaded once and stays in LDS; otherwise each step
+// also loads its 64 filter rows for the 9 taps of the chunk. The bias is staged in LDS once, so a tile's epilogue
+// reads no global memory and never waits behind the loads in flight.
+struct ConvHaloArgs {
+  ConvNhwcArgs c;
+  int32_t rw;          // W + 2: positions per patch row
+  int32_t p_loads;     // 1 KB LDS-DMA loads that fill the patch positions this geometry needs
+  int32_t rows_total;  // N * H: global input rows
+  int32_t tiles;       // tiles_m * tiles_n
+};
+
+constexpr int kHaloPatchBytes = 30 * 1024;
+
+constexpr int kHaloResidentCin = 64;  // RES_A: the filter of Cout <= 64, Cin <= 64 (72 KB) stays in LDS
+
+template <typename T, int BN, bool RES_A, int E>
+__global__ __launch_bounds__(512) void conv_halo_kernel(ConvHaloArgs ha) {
+  const ConvNhwcArgs& args = ha.c;
+  using S = typename Io<T>::storage;
+  static_assert(sizeof(S) == 2, "16-bit operands");
+  constexpr int BM = 64, WAVES_M = 2, WAVES_N = 4, NW = 8;
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int TAPS = 9;
+  constexpr int A_CHUNK = TAPS * BM * 64;                       // one chunk's filter rows
+  constexpr int A_RES = RES_A ? (kHaloResidentCin / 32) * A_CHUNK : 0;
+  constexpr int A_STEP = RES_A ? 0 : A_CHUNK;                   // filter bytes loaded with every step
+  constexpr int A_LOADS = A_CHUNK / 1024;
+  constexpr int A_PER_WAVE = (A_LOADS + NW - 1) / NW;
+  constexpr int P_MAX = kHaloPatchBytes / 1024;
+  constexpr int P_PER_WAVE = (P_MAX + NW - 1) / NW;
+  constexpr int STAGE_BYTES = NW * WN * (WM + 8) * 2;  // conv_store_tile's channels-last staging (the larger)
+  constexpr int SB_USED = A_STEP + kHaloPatchBytes > STAGE_BYTES ? A_STEP + kHaloPatchBytes : STAGE_BYTES;
+  // one step buffer: [filter rows (!RES_A)][patch] (or the epilogue's staging), then three zero positions at its
+  // end, which neither the loads nor the staging touch
+  constexpr int SB = (SB_USED + 3 * 64 + 1023) / 1024 * 1024;
+  constexpr int ZERO_OFF = SB - 256;
+  constexpr int ZERO_POS = (ZERO_OFF - A_STEP) / 64;  // patch position index of the zero positions
+  static_assert(ZERO_OFF >= SB_USED && (ZERO_OFF - A_STEP) % 64 == 0, "zero positions after loads and staging");
+  constexpr int NSTORE = WM * WN / 512;  // 16-byte stores per lane of a full tile (conv_store_tile, vector path)
+  constexpr int BIAS_OFF = A_RES + 2 * SB;
+  static_assert(A_CHUNK % 1024 == 0 && kHaloPatchBytes % 1024 == 0, "whole 1 KB loads");
+  static_assert(BIAS_OFF + 512 * 4 <= 160 * 1024, "LDS budget");
+
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[BIAS_OFF + 512 * 4];
+  float* bias_lds = reinterpret_cast<float*>(lds + BIAS_OFF);
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int W = args.w_in, H = args.h, cin = args.cin, rw = ha.rw;
+  const int nchunks = cin / 32;
+  const S* __restrict__ Wt = static_cast<const S*>(args.w);
+  const __amdgpu_buffer_rsrc_t xr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(args.x), static_cast<short>(0), static_cast<int>(args.x_bytes),
+                                        0x00020000);
+
+  // tile -> (m0, n0): channel tiles fastest, so consecutive tiles of a workgroup share pixels
+  auto tile_m0 = [&](int t) { return (t % args.tiles_m) * BM; };
+  auto tile_n0 = [&](int t) { return static_cast<int64_t>(t / args.tiles_m) * BN; };
+
+  // ---- load side: sources of this wave's loads for a (tile, chunk) step ----
+  // patch position of load i, lane: fixed over tiles; only the band's first global row changes
+  int p_r[P_PER_WAVE], p_c[P_PER_WAVE], p_ch[P_PER_WAVE];
+#pragma unroll
+  for (int i = 0; i < P_PER_WAVE; ++i) {
+    const int q = (wave + NW * i) * 16 + (lane >> 2);
+    p_ch[i] = ((lane & 3) ^ ((q >> 2) & 3)) * 8;
+    p_r[i] = q / rw;
+    p_c[i] = q - p_r[i] * rw;
+  }
+  auto a_row_src = [&](int j, int m0) {  // element offset (without ci0) of filter load j, this lane
+    const int tap = j / (BM / 16);
+    const int row = (j % (BM / 16)) * 16 + (lane >> 2);
+    const int gch = (lane & 3) ^ a_swizzle(row);
+    return (min(m0 + row, args.cout - 1) * TAPS + tap) * cin + gch * 8;
+  };
+  // issue the loads of step (tile t, chunk c) into step buffer b
+  auto issue_step = [&](int t, int c, int b) {
+    unsigned char* base = lds + A_RES + b * SB;
+    const int ci0 = c * 32;
+    if constexpr (!RES_A) {
+      const int m0 = tile_m0(t);
+#pragma unroll
+      for (int i = 0; i < A_PER_WAVE; ++i) {
+        const int j = wave + NW * i;
+        if (j < A_LOADS) global_to_lds16(Wt + a_row_src(j, m0) + ci0, (FH_LDS void*)(base + j * 1024));
+      }
+    }
+    const int gi_lo = static_cast<int>(tile_n0(t) / W) - 1;
+#pragma unroll
+    for (int i = 0; i < P_PER_WAVE; ++i) {
+      const int j = wave + NW * i;
+      if (j < ha.p_loads) {
+        const int gi = gi_lo + p_r[i];
+        const bool ok = gi >= 0 && gi < ha.rows_total && p_c[i] >= 1 && p_c[i] <= W;
+        const uint32_t voff = ok ? static_cast<uint32_t>((gi * W + p_c[i] - 1) * cin + p_ch[i] + ci0) * 2u : 0x80000000u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (FH_LDS void*)(base + A_STEP + j * 1024), 16,
+                                                 static_cast<int>(voff), 0, 0, 0);
+      }
+    }
+  };
+
+  // ---- compute side: fragment addresses of the tile being multiplied ----
+  int a_off[TM][2];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int arow = wm * WM + i * 32 + l32;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) a_off[i][h] = arow * 64 + (((2 * h + hi) ^ a_swizzle(arow)) * 16);
+  }
+  int rowpos[TN][3];
+  auto set_tile = [&](int t) {  // B: patch position of tap (kh, 0) per n-tile, or ZERO_POS outside the image
+    const int64_t n0 = tile_n0(t);
+    const int gr_first = static_cast<int>(n0 / W);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int64_t p = min(n0 + wn * WN + j * 32 + l32, args.p - 1);
+      const int gr = static_cast<int>(p / W);
+      const int ow = static_cast<int>(p - static_cast<int64_t>(gr) * W);
+      const int oh = gr % H;
+      const int pbase = (gr - gr_first) * rw + ow;
+#pragma unroll
+      for (int kh = 0; kh < 3; ++kh)
+        rowpos[j][kh] = static_cast<unsigned>(oh + kh - 1) < static_cast<unsigned>(H) ? pbase + kh * rw : ZERO_POS;
+    }
+  };
+
+  f32x16_t acc[TM][TN];
+  auto clear_acc = [&]() {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int x = 0; x < 16; ++x) acc[i][j][x] = 0.0f;
+  };
+
+  // ---- prologue: zero positions, bias, the resident filter, the first step ----
+  const int first = blockIdx.x;
+  if (first >= ha.tiles) return;
+  if (tid < 2 * 12) {
+    const int b = tid / 12, k = tid % 12;
+    *reinterpret_cast<uint4*>(lds + A_RES + b * SB + ZERO_OFF + k * 16) = uint4{0, 0, 0, 0};
+  }
+  if (tid < args.cout)
+    bias_lds[tid] = args.bias != nullptr ? Io<T>::load(static_cast<const S*>(args.bias)[tid]) : 0.0f;
+  if constexpr (RES_A) {
+    for (int c = 0; c < nchunks; ++c)
+#pragma unroll
+      for (int i = 0; i < A_PER_WAVE; ++i) {
+        const int j = wave + NW * i;
+        if (j < A_LOADS) global_to_lds16(Wt + a_row_src(j, 0) + c * 32, (FH_LDS void*)(lds + c * A_CHUNK + j * 1024));
+      }
+  }
+  issue_step(first, 0, 0);
+  wait_vmcnt<0>();
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+
+  const uint32_t lds_base = lds_addr((const FH_LDS void*)lds);
+  KFragments<TM, TN> f0, f1;
+  auto read_step = [&]<int STEP>(uint32_t ab, uint32_t pb, KFragments<TM, TN>& f) {
+    constexpr int tap = STEP / 2, h = STEP % 2, kh = tap / 3, kw = tap % 3;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) f.a[i] = lds_read_b128<tap * BM * 64>(ab + a_off[i][h]);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int pos = rowpos[j][kh] + kw;
+      f.b[j] = lds_read_b128<0>(pb + pos * 64 + ((((2 * h + hi) ^ ((pos >> 2) & 3))) * 16));
+    }
+  };
+  auto multiply = [&](KFragments<TM, TN>& f) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) mfma32<T>(f.a[i], f.b[j], acc[i][j]);
+  };
+
+  clear_acc();
+  set_tile(first);
+  int t = first, c = 0, buf = 0;
+  while (true) {
+    // next step: the next chunk of this tile, or the first chunk of the next tile
+    int nt = t, nc = c + 1;
+    if (nc == nchunks) {
+      nc = 0;
+      nt = t + static_cast<int>(gridDim.x);
+    }
+    const bool more = nt < ha.tiles;
+    if (more) issue_step(nt, nc, buf ^ 1);
+    const uint32_t sb = lds_base + A_RES + buf * SB;
+    const uint32_t ab = RES_A ? lds_base + c * A_CHUNK : sb;
+    const uint32_t pb = sb + A_STEP;
+    read_step.template operator()<0>(ab, pb, f0);
+    [&]<int... STEP>(std::integer_sequence<int, STEP...>) {
+      (
+          [&] {
+            constexpr int s = STEP;
+            KFragments<TM, TN>& cur = (s % 2 == 0) ? f0 : f1;
+            KFragments<TM, TN>& nxt = (s % 2 == 0) ? f1 : f0;
+            fence_kfragments(cur);
+            if constexpr (s + 1 < 2 * TAPS) read_step.template operator()<s + 1>(ab, pb, nxt);
+            multiply(cur);
+            __builtin_amdgcn_sched_barrier(0);
+          }(),
+          ...);
+    }(std::make_integer_sequence<int, 2 * TAPS>{});
+    fence_kfragments(f0);
+    fence_kfragments(f1);
+    bool exact = true;  // the vmcnt wait below may leave this tile's NSTORE stores in flight
+    if (c + 1 == nchunks) {
+      // tile done: every wave has finished reading this step buffer, which then stages the output
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      const int m0 = tile_m0(t);
+      const int64_t n0 = tile_n0(t);
+      conv_store_tile<T, E, WM, WN, NW, SB>(args, acc, lds + A_RES + buf * SB, wave, lane, m0 + wm * WM,
+                                            n0 + wn * WN, bias_lds);
+      exact = args.vec_store && m0 + BM <= args.cout && n0 + BN <= args.p;
+      clear_acc();
+      if (more) set_tile(nt);
+    }
+    if (!more) break;
+    if (exact) {
+      wait_vmcnt<NSTORE>();
+    } else {
+      wait_vmcnt<0>();
+    }
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    t = nt;
+    c = nc;
+    buf ^= 1;
+  }
+}
+
+// Channels-last output of a whole workgroup tile (BM = 64 channels x BN pixels): every wave stages its accumulators
+// pixel-major into one shared [BN][BM + 8] layout, then eight consecutive lanes write a pixel's 64 channels as one
+// 128-byte line. (Per-wave staging writes each pixel's channels in 32-channel halves from two different waves,
+// half cache lines that cost the C4 layers a third of their time.) Ends with every wave past a barrier.
+template <typename T, int E, int BM, int BN, int WAVES_N, int NW>
+__device__ __forceinline__ void conv_store_tile_wg_nhwc(const ConvNhwcArgs& args, f32x16_t (&acc)[BM / (NW / WAVES_N) / 32][BN / WAVES_N / 32],
+                                                        unsigned char* lds, int wave, int lane, int m0, int64_t n0) {
+  using S = typename Io<T>::storage;
+  static_assert(sizeof(S) == 2 && BM == 64, "16-bit, 64-channel tiles");
+  constexpr int WAVES_M = NW / WAVES_N;
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int PITCH = BM + 8;  // elements per staged pixel (one 16-byte pad chunk)
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const S* bias = static_cast<const S*>(args.bias);
+  float bv[TM][16];
+  {
+    const float mine = bias != nullptr ? Io<T>::load(bias[min(m0 + wm * WM + lane % WM, args.cout - 1)]) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int x = 0; x < 16; ++x) bv[i][x] = __shfl(mine, i * 32 + 8 * (x >> 2) + 4 * hi + (x & 3));
+  }
+  S* st = reinterpret_cast<S*>(lds);
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int x = 0; x < 16; x += 2) {
+      const int ch = wm * WM + i * 32 + 8 * (x >> 2) + 4 * hi + (x & 3);  // even; channels ch, ch + 1
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int pc = wn * WN + j * 32 + l32;
+        const uint32_t w = static_cast<uint32_t>(Io<T>::store(acc[i][j][x] + bv[i][x])) |
+                           (static_cast<uint32_t>(Io<T>::store(acc[i][j][x + 1] + bv[i][x + 1])) << 16);
+        *reinterpret_cast<uint32_t*>(st + pc * PITCH + ch) = w;
+      }
+    }
+  __builtin_amdgcn_s_waitcnt(0xc07f);
+  __syncthreads();
+  const int tid = wave * 64 + lane;
+#pragma unroll
+  for (int it = 0; it < BN * 8 / (NW * 64); ++it) {
+    const int id = it * NW * 64 + tid;
+    const int g = id & 7, pc = id >> 3;
+    const int co0 = m0 + g * 8;
+    const int64_t p = n0 + pc;
+    if (co0 >= args.cout || p >= args.p) continue;
+    uint4 packed = *reinterpret_cast<const uint4*>(st + pc * PITCH + g * 8);
+    const int64_t idx = p * args.cout + co0;
+    S* __restrict__ Y = static_cast<S*>(args.y);
+    if (args.vec_store && co0 + 8 <= args.cout) {
+      packed = epi_vec<E, T>(args.ep, packed, idx);
+      *reinterpret_cast<uint4*>(Y + idx) = packed;
+    } else {
+      S vals[8];
+      __builtin_memcpy(vals, &packed, 16);
+      for (int e = 0; e < 8 && co0 + e < args.cout; ++e) {
+        S v = vals[e];
+        if constexpr (E != kEpiNone) v = Io<T>::store(epi_one<E, T>(args.ep, Io<T>::load(v), idx + e));
+        Y[idx + e] = v;
+      }
+    }
+  }
+}
+
+// Single-buffered variant: one tile per workgroup, each (chunk) step loaded, waited for and multiplied in turn,
+// 66 KB of LDS, so two workgroups share a CU and each one's loads, barriers and epilogue overlap the other's
+// multiplications (the persistent kernel above keeps one workgroup per CU and has nothing to overlap them with).
+template <typename T, int BN, int E>
+__global__ __launch_bounds__(512, 2) void conv_halo1_kernel(ConvHaloArgs ha) {
+  const ConvNhwcArgs& args = ha.c;
+  using S = typename Io<T>::storage;
+  static_assert(sizeof(S) == 2, "16-bit operands");
+  constexpr int BM = 64, WAVES_M = 2, WAVES_N = 4, NW = 8;
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int TAPS = 9;
+  constexpr int A_CHUNK = TAPS * BM * 64;
+  constexpr int A_LOADS = A_CHUNK / 1024;
+  constexpr int A_PER_WAVE = (A_LOADS + NW - 1) / NW;
+  constexpr int P_MAX = kHaloPatchBytes / 1024;
+  constexpr int P_PER_WAVE = (P_MAX + NW - 1) / NW;
+  constexpr int STAGE_BYTES = NW * WN * (WM + 8) * 2;
+  constexpr int SB_USED = A_CHUNK + kHaloPatchBytes > STAGE_BYTES ? A_CHUNK + kHaloPatchBytes : STAGE_BYTES;
+  constexpr int SB = (SB_USED + 3 * 64 + 255) / 256 * 256;
+  constexpr int ZERO_OFF = SB - 256;
+  constexpr int ZERO_POS = (ZERO_OFF - A_CHUNK) / 64;
+  static_assert(ZERO_OFF >= SB_USED && (ZERO_OFF - A_CHUNK) % 64 == 0, "zero positions after loads and staging");
+  static_assert(2 * SB <= 160 * 1024, "two workgroups per CU");
+
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[SB];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int W = args.w_in, H = args.h, cin = args.cin, rw = ha.rw;
+  const int nchunks = cin / 32;
+  const S* __restrict__ Wt = static_cast<const S*>(args.w);
+  const __amdgpu_buffer_rsrc_t xr =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(args.x), static_cast<short>(0), static_cast<int>(args.x_bytes),
+                                        0x00020000);
+  // XCD-aware order: consecutive tiles (sharing halo rows and filter rows) on one XCD's L2
+  int t = blockIdx.x;
+  if ((ha.tiles & 7) == 0) t = (t & 7) * (ha.tiles >> 3) + (t >> 3);
+  const int m0 = (t % args.tiles_m) * BM;
+  const int64_t n0 = static_cast<int64_t>(t / args.tiles_m) * BN;
+  const int gr_first = static_cast<int>(n0 / W);
+  const int gi_lo = gr_first - 1;
+
+  int32_t a_src[A_PER_WAVE];
+#pragma unroll
+  for (int i = 0; i < A_PER_WAVE; ++i) {
+    const int j = wave + NW * i;
+    const int tap = j / (BM / 16);
+    const int row = (j % (BM / 16)) * 16 + (lane >> 2);
+    const int gch = (lane & 3) ^ a_swizzle(row);
+    a_src[i] = (min(m0 + row, args.cout - 1) * TAPS + tap) * cin + gch * 8;
+  }
+  int32_t p_src[P_PER_WAVE];
+#pragma unroll
+  for (int i = 0; i < P_PER_WAVE; ++i) {
+    const int q = (wave + NW * i) * 16 + (lane >> 2);
+    const int gch = (lane & 3) ^ ((q >> 2) & 3);
+    const int r = q / rw;
+    const int c = q - r * rw;
+    const int gi = gi_lo + r;
+    const bool ok = gi >= 0 && gi < ha.rows_total && c >= 1 && c <= W;
+    p_src[i] = ok ? (gi * W + c - 1) * cin + gch * 8 : -1;
+  }
+  auto issue_step = [&](int ci0) {
+#pragma unroll
+    for (int i = 0; i < A_PER_WAVE; ++i) {
+      const int j = wave + NW * i;
+      if (j < A_LOADS) global_to_lds16(Wt + a_src[i] + ci0, (FH_LDS void*)(lds + j * 1024));
+    }
+#pragma unroll
+    for (int i = 0; i < P_PER_WAVE; ++i) {
+      const int j = wave + NW * i;
+      if (j < ha.p_loads) {
+        const uint32_t voff = p_src[i] >= 0 ? static_cast<uint32_t>(p_src[i] + ci0) * 2u : 0x80000000u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (FH_LDS void*)(lds + A_CHUNK + j * 1024), 16,
+                                                 static_cast<int>(voff), 0, 0, 0);
+      }
+    }
+  };
+  int a_off[TM][2];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int arow = wm * WM + i * 32 + l32;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) a_off[i][h] = arow * 64 + (((2 * h + hi) ^ a_swizzle(arow)) * 16);
+  }
+  int rowpos[TN][3];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int64_t p = min(n0 + wn * WN + j * 32 + l32, args.p - 1);
+    const int gr = static_cast<int>(p / W);
+    const int ow = static_cast<int>(p - static_cast<int64_t>(gr) * W);
+    const int oh = gr % H;
+    const int pbase = (gr - gr_first) * rw + ow;
+#pragma unroll
+    for (int kh = 0; kh < 3; ++kh)
+      rowpos[j][kh] = static_cast<unsigned>(oh + kh - 1) < static_cast<unsigned>(H) ? pbase + kh * rw : ZERO_POS;
+  }
+  f32x16_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int x = 0; x < 16; ++x) acc[i][j][x] = 0.0f;
+
+  const uint32_t ab = lds_addr((const FH_LDS void*)lds);
+  const uint32_t pb = ab + A_CHUNK;
+  KFragments<TM, TN> f0, f1;
+  auto read_step = [&]<int STEP>(KFragments<TM, TN>& f) {
+    constexpr int tap = STEP / 2, h = STEP % 2, kh = tap / 3, kw = tap % 3;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) f.a[i] = lds_read_b128<tap * BM * 64>(ab + a_off[i][h]);
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int pos = rowpos[j][kh] + kw;
+      f.b[j] = lds_read_b128<0>(pb + pos * 64 + ((((2 * h + hi) ^ ((pos >> 2) & 3))) * 16));
+    }
+  };
+  auto multiply = [&](KFragments<TM, TN>& f) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) mfma32<T>(f.a[i], f.b[j], acc[i][j]);
+  };
+
+  if (tid < 12) *reinterpret_cast<uint4*>(lds + ZERO_OFF + tid * 16) = uint4{0, 0, 0, 0};
+  for (int c = 0; c < nchunks; ++c) {
+    issue_step(c * 32);
+    wait_vmcnt<0>();
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    read_step.template operator()<0>(f0);
+    [&]<int... STEP>(std::integer_sequence<int, STEP...>) {
+      (
+          [&] {
+            constexpr int s = STEP;
+            KFragments<TM, TN>& cur = (s % 2 == 0) ? f0 : f1;
+            KFragments<TM, TN>& nxt = (s % 2 == 0) ? f1 : f0;
+            fence_kfragments(cur);
+            if constexpr (s + 1 < 2 * TAPS) read_step.template operator()<s + 1>(nxt);
+            multiply(cur);
+            __builtin_amdgcn_sched_barrier(0);
+          }(),
+          ...);
+    }(std::make_integer_sequence<int, 2 * TAPS>{});
+    fence_kfragments(f0);
+    fence_kfragments(f1);
+    // every wave is done with this step's operands before the next step (or the epilogue) overwrites them
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  }
+  if (args.out_nhwc) {
+    static_assert(BN * (BM + 8) * 2 <= SB, "workgroup staging fits");
+    conv_store_tile_wg_nhwc<T, E, BM, BN, WAVES_N, NW>(args, acc, lds, wave, lane, m0, n0);
+  } else {
+    conv_store_tile<T, E, WM, WN, NW, SB>(args, acc, lds, wave, lane, m0 + wm * WM, n0 + wn * WN);
+  }
+}
+
+// Whether the resident-patch kernel takes this geometry: patch rows of a BN-pixel tile (at most (BN - 1) / W + 2
+// output rows plus the two halo rows) must fit kHaloPatchBytes; p_loads = the 1 KB loads that fill them.
+bool halo_supported(int32_t dtype, const int64_t* g, int bn, int32_t* p_loads) {
+  if (dtype != FH_BF16 && dtype != FH_F16) return false;
+  if (g[11] != 1 || g[5] != 3 || g[6] != 3 || g[7] != 1 || g[8] != 1 || g[9] != 1 || g[10] != 1) return false;
+  if (g[1] % 32 != 0 || g[2] < 1 || g[3] < 1 || g[4] < 1 || g[4] > 512) return false;
+  const int64_t rows = (bn - 1) / g[3] + 2 + 2;
+  const int64_t positions = rows * (g[3] + 2);
+  if (positions * 64 > kHaloPatchBytes) return false;
+  // 32-bit element offsets: the whole input, the filter
+  if (g[0] * g[2] * g[3] * g[1] >= (int64_t{1} << 30) || g[4] * 9 * g[1] >= (int64_t{1} << 30)) return false;
+  if (p_loads != nullptr) *p_loads = static_cast<int32_t>((positions + 15) / 16);
+  return true;
+}
+
+template <typename T, int BN>
+fh_status launch_halo1(ConvHaloArgs a, hipStream_t stream) {
+  a.c.tiles_m = (a.c.cout + 63) / 64;
+  a.c.tiles_n = static_cast<int32_t>((a.c.p + BN - 1) / BN);
+  a.tiles = a.c.tiles_m * a.c.tiles_n;
+  return with_epi<conv_epi_mask<T, false>()>(epi_kind(a.c.ep), [&]<int E>() {
+    hipLaunchKernelGGL((conv_halo1_kernel<T, BN, E>), dim3(static_cast<uint32_t>(a.tiles)), dim3(512), 0, stream, a);
+    return launch_status("conv_halo1_kernel launch");
+  });
+}
+
+template <typename T, int BN>
+fh_status launch_halo(ConvHaloArgs a, hipStream_t stream) {
+  a.c.tiles_m = (a.c.cout + 63) / 64;
+  a.c.tiles_n = static_cast<int32_t>((a.c.p + BN - 1) / BN);
+  a.tiles = a.c.tiles_m * a.c.tiles_n;
+  const dim3 grid(static_cast<uint32_t>(std::min<int64_t>(a.tiles, device_cu_count())));
+  const bool res_a = a.c.cout <= 64 && a.c.cin <= kHaloResidentCin;
+  return with_epi<conv_epi_mask<T, false>()>(epi_kind(a.c.ep), [&]<int E>() {
+    if (res_a)
+      hipLaunchKernelGGL((conv_halo_kernel<T, BN, true, E>), grid, dim3(512), 0, stream, a);
+    else
+      hipLaunchKernelGGL((conv_halo_kernel<T, BN, false, E>), grid, dim3(512), 0, stream, a);
+    return launch_status("conv_halo_kernel launch");
+  });
+}
+
+// Which resident-patch kernel, from measurements of C3 and the ResNet-18 3x3 stride-1 layers on an MI355X (bf16,
+// relu epilogue, batch 64; us per launch, implicit GEMM in brackets):
+//   NCHW output (a graph output, C3):        single-buffered, two per CU    C3 16.3 (20.6)
+//   channels-last output, Cout <= 64:        persistent, resident filter    56x56x64 34.2 (41.9)
+//   channels-last output, 64 < Cout <= 256:  single-buffered                28x28x128 31.1 (32.8), 14x14x256 32.1 (36.2)
+//   Cout > 256 (7x7x512):                    the implicit GEMM (31.6; 43.8 here)
+// Single-buffered tiles: 256 pixels when that still makes 1.5 workgroups per CU slot pair, else 128; persistent:
+// 256 when the tiles fill the device 1.5 times over, else 128.
+template <typename T>
+fh_status dispatch_halo(const ConvNhwcArgs& c, const int64_t* geom, hipStream_t stream, bool* launched) {
+  *launched = false;
+  if (c.out_nhwc && c.cout > 256) return FH_OK;
+  const int64_t cus = device_cu_count();
+  const int64_t tiles_m = (c.cout + 63) / 64;
+  const bool persistent = c.out_nhwc && c.cout <= 64;
+  ConvHaloArgs a{};
+  a.c = c;
+  a.rw = c.w_in + 2;
+  a.rows_total = static_cast<int32_t>(geom[0] * geom[2]);
+  int32_t loads = 0;
+  if (2 * tiles_m * ((c.p + 255) / 256) >= 3 * cus && halo_supported(FH_BF16, geom, 256, &loads)) {
+    a.p_loads = loads;
+    *launched = true;
+    return persistent ? launch_halo<T, 256>(a, stream) : launch_halo1<T, 256>(a, stream);
+  }
+  if (halo_supported(FH_BF16, geom, 128, &loads)) {
+    a.p_loads = loads;
+    *launched = true;
+    return persistent ? launch_halo<T, 128>(a, stream) : launch_halo1<T, 128>(a, stream);
+  }
+  return FH_OK;
 }
 
 // Tile choice, from measurements of the ResNet layer shapes on an MI355X (bf16, 3x3, batch 64): by output
@@ -723,7 +1345,8 @@ extern "C" fh_status fh_conv2d_nhwc_fwd(int32_t dtype, const void* x_nhwc, const
 extern "C" fh_status fh_conv2d_nhwc_fwd_ex(int32_t dtype, const void* x_nhwc, const void* w_khwc, const void* bias,
                                            void* y, const int64_t geom[12], const fh_epilogue* epilogue,
                                            int32_t flags, void* stream) {
-  if ((flags & ~FH_CONV_OUT_NHWC) != 0) return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd_ex: unknown flags");
+  if ((flags & ~(FH_CONV_OUT_NHWC | FH_CONV_IMPLICIT_GEMM)) != 0)
+    return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd_ex: unknown flags");
   if (geom == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd: null geometry");
   if (!nhwc_supported(dtype, geom))
     return fail(FH_UNIMPLEMENTED, "fh_conv2d_nhwc_fwd: geometry or dtype not supported by the channels-last path "
@@ -778,6 +1401,12 @@ extern "C" fh_status fh_conv2d_nhwc_fwd_ex(int32_t dtype, const void* x_nhwc, co
   a.vec_store = vec ? 1 : 0;
   if (a.p == 0) return FH_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if ((dtype == FH_BF16 || dtype == FH_F16) && !c8 && (flags & FH_CONV_IMPLICIT_GEMM) == 0) {
+    bool launched = false;
+    const fh_status st = dtype == FH_BF16 ? dispatch_halo<bf16_t>(a, geom, s, &launched)
+                                          : dispatch_halo<f16_t>(a, geom, s, &launched);
+    if (launched || st != FH_OK) return st;
+  }
   if (dtype == FH_F32) return dispatch_conv<float, false>(a, s);
   if (c8) return dtype == FH_BF16 ? dispatch_conv<bf16_t, true>(a, s) : dispatch_conv<f16_t, true>(a, s);
   return dtype == FH_BF16 ? dispatch_conv<bf16_t, false>(a, s) : dispatch_conv<f16_t, false>(a, s);

@@ -155,6 +155,10 @@ fh_status fh_conv2d_nhwc_fwd(int32_t dtype, const void* x_nhwc, const void* w_kh
  * HipBackend::compile uses it for activations whose every consumer takes channels-last data. No counterpart in
  * the reference (NCHW throughout, reference: src/backends/cuda/kernels/conv.cpp:385-520). */
 #define FH_CONV_OUT_NHWC 1
+/* FH_CONV_IMPLICIT_GEMM selects the implicit-GEMM kernel (one im2col row per pixel and tap per stage) even where the
+ * resident-patch kernel for 3x3 stride-1 convolutions would run; both compute the same sums, so tests use it to
+ * cover both kernels on one geometry. */
+#define FH_CONV_IMPLICIT_GEMM 2
 fh_status fh_conv2d_nhwc_fwd_ex(int32_t dtype, const void* x_nhwc, const void* w_khwc, const void* bias, void* y,
                                 const int64_t geom[12], const fh_epilogue* epilogue, int32_t flags, void* stream);
 

@@ -441,9 +441,10 @@ def test_conv2d_nhwc(hip, dtype, geom, with_bias):
     assert_close(got, want, dtype, what=f"conv nhwc {geom}")
 
 
-# Shapes large enough for each tile configuration of the dispatch table (64x256, 64x128, 128x256, 128x128;
-# the small cases above take 64x64), checked on 4,096 sampled outputs recomputed by the oracle's per-element
-# formula (the full single-threaded oracle would take minutes here).
+# Shapes large enough for each tile configuration of the implicit-GEMM dispatch table (64x256, 64x128, 128x256,
+# 128x128; the small cases above take 64x64; FH_CONV_IMPLICIT_GEMM keeps these 3x3 stride-1 convs off the
+# resident-patch kernel), checked on 4,096 sampled outputs recomputed by the oracle's per-element formula (the
+# full single-threaded oracle would take minutes here).
 LARGE_NHWC_CASES = [
     (BF16, (8, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1)),     # 64x256
     (BF16, (4, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1)),     # 64x128
@@ -464,12 +465,68 @@ def test_conv2d_nhwc_large_tiles_sampled(hip, dtype, geom):
     oh, ow = orc.conv_out_hw(geom)
     dx, dw, db = dev(hip, to_nhwc(x)), dev(hip, to_nhwc(wt)), dev(hip, bias)
     dy = hip.DeviceBuffer(n * cout * oh * ow * x.itemsize)
-    hip.check(hip.lib().fh_conv2d_nhwc_fwd(dtype, dx.value, dw.value, db.value, dy.value, hip.i64_array(geom),
-                                           None, None))
+    hip.check(hip.lib().fh_conv2d_nhwc_fwd_ex(dtype, dx.value, dw.value, db.value, dy.value, hip.i64_array(geom),
+                                              None, 2, None))  # 2 = FH_CONV_IMPLICIT_GEMM
     got = dy.download((n, cout, oh, ow), x.dtype).reshape(-1)
     idx = np.random.default_rng(7).integers(0, got.size, 4096)
     want = orc.conv2d_sample(dtype, x, wt, bias, geom, idx)
     assert_close(got[idx], want, dtype, what=f"conv nhwc large {geom}")
+
+
+# The resident-patch kernel (3x3, stride 1, padding 1, 16-bit, Cin % 32 == 0): 256-pixel tiles where they still
+# fill the device, 128 otherwise; tiles that straddle images (7x7 and 14x14 planes hold several images per tile),
+# Cout below and above the 64-channel tile, channels-last output with the residual epilogue; sampled outputs
+# everywhere in the batch (first and last images included) plus the full first and last images.
+HALO_CASES = [
+    # NCHW output: the single-buffered kernel (two workgroups per CU)
+    (BF16, (32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1), 0),    # C3: 256-pixel tiles
+    (F16, (32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1), 0),
+    (BF16, (3, 96, 9, 13, 40, 3, 3, 1, 1, 1, 1, 1), 0),      # Cout 40, odd plane, 128-pixel tiles
+    # channels-last output with the residual add;relu, 64 < Cout <= 256: single-buffered, workgroup-wide staging
+    (BF16, (16, 128, 28, 28, 128, 3, 3, 1, 1, 1, 1, 1), 1),
+    (BF16, (64, 256, 14, 14, 256, 3, 3, 1, 1, 1, 1, 1), 1),
+    (BF16, (8, 256, 7, 7, 256, 3, 3, 1, 1, 1, 1, 1), 1),     # ~2.6 images per tile
+    (BF16, (5, 32, 3, 5, 100, 3, 3, 1, 1, 1, 1, 1), 1),      # Cout 100 over two channel tiles, 3-row images
+    # channels-last output, Cout <= 64: the persistent kernel (filter resident when Cin <= 64)
+    (BF16, (64, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1), 1),    # ResNet layer 1: 256-pixel tiles, two per CU
+    (BF16, (4, 32, 10, 12, 48, 3, 3, 1, 1, 1, 1, 1), 1),     # one chunk, Cout 48, 128-pixel tiles
+    (BF16, (6, 128, 14, 14, 64, 3, 3, 1, 1, 1, 1, 1), 1),    # Cin 128: filter streamed with each step
+    (F16, (2, 64, 12, 12, 64, 3, 3, 1, 1, 1, 1, 1), 1),
+]
+
+
+@pytest.mark.parametrize("dtype,geom,nhwc_out", HALO_CASES)
+def test_conv2d_resident_patch(hip, dtype, geom, nhwc_out):
+    say(f"conv resident patch dtype={dtype} {geom} nhwc_out={nhwc_out}")
+    n, cin, h, w, cout, kh, kw = geom[:7]
+    x = synth.tensor(171, (n, cin, h, w), dtype, "normal")
+    wt = synth.tensor(172, (cout, cin, kh, kw), dtype, "normal", (2.0 / (cin * kh * kw)) ** 0.5)
+    bias = synth.tensor(173, (cout,), dtype, "normal", 0.1)
+    res = synth.tensor(174, (n, cout, h, w), dtype, "normal") if nhwc_out else None
+    dx, dw, db = dev(hip, to_nhwc(x)), dev(hip, to_nhwc(wt)), dev(hip, bias)
+    dy = hip.DeviceBuffer(n * cout * h * w * x.itemsize)
+    ep = None
+    if nhwc_out:
+        dr = dev(hip, to_nhwc(res))
+        ep = hip.make_epilogue([(hip.EW_ADD, dr.value), (hip.EW_RELU, None)])
+    hip.check(hip.lib().fh_conv2d_nhwc_fwd_ex(dtype, dx.value, dw.value, db.value, dy.value, hip.i64_array(geom),
+                                              ctypes.byref(ep) if ep else None, nhwc_out, None))
+    got = dy.download((n, h, w, cout) if nhwc_out else (n, cout, h, w), x.dtype)
+    if nhwc_out:
+        got = np.ascontiguousarray(got.transpose(0, 3, 1, 2))
+
+    def expect(conv, r):
+        return orc.ew_program(dtype, [1, 3], [2, 1], [conv, r]) if nhwc_out else conv
+
+    for img in sorted({0, n - 1}):  # whole first and last images
+        conv = orc.conv2d(dtype, x[img:img + 1], wt, bias, (1,) + geom[1:])
+        assert_close(got[img:img + 1], expect(conv, res[img:img + 1] if nhwc_out else None), dtype,
+                     what=f"resident patch {geom} image {img}")
+    flat = got.reshape(-1)
+    idx = np.random.default_rng(9).integers(0, flat.size, 4096)
+    conv = orc.conv2d_sample(dtype, x, wt, bias, geom, idx)
+    want = orc.ew_program(dtype, [1, 3], [2, 1], [conv, res.reshape(-1)[idx]]) if nhwc_out else conv
+    assert_close(flat[idx], want, dtype, what=f"resident patch {geom} sampled")
 
 
 NHWC_OUT_CASES = [
