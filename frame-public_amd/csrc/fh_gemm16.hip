@@ -66,7 +66,7 @@ __device__ __forceinline__ void fence_fragments(Fragments<TM, TN>& f) {
 // refilled after the barrier of step kt held stage kt-1, whose reads every wave fenced (lgkmcnt(0)) before
 // arriving at that barrier. Stages past the end re-load the last stage (nobody reads them), so every step
 // issues the same number of loads and the vmcnt counts hold on every path.
-template <typename T, int BM, int BN, int WAVES_M, int WAVES_N>
+template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, int E>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs args) {
   using S = uint16_t;
   constexpr int NW = WAVES_M * WAVES_N;
@@ -277,7 +277,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
     if (row < M && col < N) {
       uint4 packed = *reinterpret_cast<const uint4*>(wl + rr * WN + c);
       const int64_t idx = row * ldc + col;
-      if (args.ep.nseg > 0) packed = epilogue_vec<T>(args.ep, packed, idx);
+      packed = epi_vec<E, T>(args.ep, packed, idx);
       *reinterpret_cast<uint4*>(C + idx) = packed;
     }
   }
@@ -288,8 +288,23 @@ fh_status launch(GemmArgs args, int64_t batch, hipStream_t stream) {
   args.tiles_m = static_cast<int32_t>((args.M + BM - 1) / BM);
   args.tiles_n = static_cast<int32_t>((args.N + BN - 1) / BN);
   dim3 grid(static_cast<uint32_t>(args.tiles_m) * static_cast<uint32_t>(args.tiles_n), static_cast<uint32_t>(batch));
-  hipLaunchKernelGGL((gemm16_kernel<T, BM, BN, WAVES_M, WAVES_N>), grid, dim3(WAVES_M * WAVES_N * 64), 0, stream, args);
-  return launch_status("gemm16_kernel launch");
+  auto go = [&]<int E>() {
+    hipLaunchKernelGGL((gemm16_kernel<T, BM, BN, WAVES_M, WAVES_N, E>), grid, dim3(WAVES_M * WAVES_N * 64), 0, stream,
+                       args);
+    return launch_status("gemm16_kernel launch");
+  };
+  // bf16 (the configurations' type): the programs of C1-C5's GEMMs as kernels of their own; the rest (and f16)
+  // take the interpreter (see EpiKind)
+  if constexpr (std::is_same_v<T, bf16_t>) {
+    switch (epi_kind(args.ep)) {
+      case kEpiNone: return go.template operator()<kEpiNone>();
+      case kEpiAdd: return go.template operator()<kEpiAdd>();
+      case kEpiAddGelu: return go.template operator()<kEpiAddGelu>();
+      case kEpiAddAdd: return go.template operator()<kEpiAddAdd>();
+      default: break;
+    }
+  }
+  return go.template operator()<kEpiAny>();
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
