@@ -69,6 +69,15 @@ _SIGS = {
     "frame_backend_copy": (c_int32, [c_char_p, c_void_p, c_char_p, c_int32, c_void_p, c_char_p, c_int32, c_size_t,
                                      c_void_p]),
     "frame_hip_allocator_stats": (c_int32, [c_int32, POINTER(ctypes.c_uint64)]),
+    "frame_save_onnx_weights": (c_int32, [c_char_p, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
+    "frame_load_onnx_weights": (c_int32, [c_char_p, POINTER(c_void_p)]),
+    "frame_onnx_count": (c_int32, [c_void_p]),
+    "frame_onnx_name": (c_char_p, [c_void_p, c_int32]),
+    "frame_onnx_dtype": (c_int32, [c_void_p, c_int32]),
+    "frame_onnx_rank": (c_int32, [c_void_p, c_int32]),
+    "frame_onnx_dim": (c_int64, [c_void_p, c_int32, c_int32]),
+    "frame_onnx_data": (c_void_p, [c_void_p, c_int32]),
+    "frame_onnx_free": (None, [c_void_p]),
 }
 
 
@@ -294,6 +303,44 @@ def allocator_stats(device: int = 0) -> dict:
     out = (ctypes.c_uint64 * 5)()
     check(lib().frame_hip_allocator_stats(device, out), "frame_hip_allocator_stats")
     return dict(zip(("live", "cached", "pending", "device_allocations", "device_syncs"), [int(v) for v in out]))
+
+
+def onnx_arrays(weights):
+    """(names, dtypes, dims, ranks, data) ctypes arrays for {name: (dtype, numpy array)} (kept alive by the caller)."""
+    names = list(weights)
+    # (np.ascontiguousarray would turn a rank-0 array into rank 1)
+    arrs = [np.asarray(weights[n][1]).copy(order="C") for n in names]
+    dims = [(c_int64 * max(1, a.ndim))(*a.shape) for a in arrs]
+    c_names = (c_char_p * max(1, len(names)))(*[n.encode() for n in names])
+    c_dtypes = (c_int32 * max(1, len(names)))(*[int(weights[n][0]) for n in names])
+    c_dims = (c_void_p * max(1, len(names)))(*[ctypes.addressof(d) for d in dims])
+    c_ranks = (c_int32 * max(1, len(names)))(*[a.ndim for a in arrs])
+    c_data = (c_void_p * max(1, len(names)))(*[a.ctypes.data for a in arrs])
+    return (c_names, c_dtypes, c_dims, c_ranks, c_data), (arrs, dims)
+
+
+def save_onnx_weights(path: str, weights) -> None:
+    """interop::save_onnx_weights: weights = {name: (dtype code, numpy array of its storage)}, in order."""
+    args, keep = onnx_arrays(weights)
+    check(lib().frame_save_onnx_weights(path.encode(), len(weights), *args), "save_onnx_weights")
+
+
+def load_onnx_weights(path: str) -> dict:
+    """interop::load_onnx_weights: {name: (dtype code, numpy array)} in file order."""
+    h = c_void_p()
+    check(lib().frame_load_onnx_weights(path.encode(), ctypes.byref(h)), "load_onnx_weights")
+    try:
+        out = {}
+        for i in range(lib().frame_onnx_count(h)):
+            dt = lib().frame_onnx_dtype(h, i)
+            shape = tuple(lib().frame_onnx_dim(h, i, k) for k in range(lib().frame_onnx_rank(h, i)))
+            a = np.empty(shape, dtype=_NP[dt])
+            if a.nbytes:
+                ctypes.memmove(a.ctypes.data, lib().frame_onnx_data(h, i), a.nbytes)
+            out[lib().frame_onnx_name(h, i).decode()] = (dt, a)
+        return out
+    finally:
+        lib().frame_onnx_free(h)
 
 
 def compile(graph, backend: str, opt_level: int = 1) -> Executable:

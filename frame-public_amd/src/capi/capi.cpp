@@ -3,6 +3,7 @@
 #include "frame_capi.h"
 #pragma GCC visibility pop
 
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 #include <sstream>
@@ -19,6 +20,7 @@
 #include <frame/hal/stream.h>
 #include <frame/ir/graph.h>
 #include <frame/ir/memory_plan.h>
+#include <frame/interop/onnx_weights.h>
 #include <frame/ir/serialization.h>
 #include <frame/runtime/compile.h>
 
@@ -34,12 +36,35 @@ struct frame_stream {
 struct frame_event {
   std::unique_ptr<frame::hal::Event> e;
 };
+struct frame_onnx_weights {
+  std::vector<frame::interop::NamedTensor> items;
+};
 struct frame_executable {
   std::shared_ptr<frame::hal::Executable> exe;
   std::string backend;
 };
 
 namespace {
+
+// Host memory for cpu tensors (ONNX weights): 64-byte aligned blocks from the C library. The hip plugin's library
+// registers no cpu backend, so the C API brings its own host allocator.
+class HostAllocator final : public frame::hal::Allocator {
+ public:
+  frame::Result<void*> allocate(size_t bytes, size_t alignment) override {
+    if (bytes == 0) return frame::Status::make(frame::ErrorCode::kInvalidArgument, "host allocate: 0 bytes");
+    if (alignment == 0 || (alignment & (alignment - 1)) != 0 || alignment > 64)
+      return frame::Status::make(frame::ErrorCode::kInvalidArgument, "host allocate: bad alignment");
+    void* p = std::aligned_alloc(64, (bytes + 63) / 64 * 64);
+    if (p == nullptr) return frame::Status::make(frame::ErrorCode::kOutOfMemory, "host allocate failed");
+    return p;
+  }
+  void deallocate(void* p) override { std::free(p); }
+};
+
+HostAllocator& host_allocator() {
+  static HostAllocator a;  // process lifetime: tensors it backs may be released at any time
+  return a;
+}
 
 thread_local std::string g_error;
 
@@ -320,6 +345,47 @@ int frame_launch(const char* node_ir_text, const char* backend, frame_tensor* co
   frame::Status s = b.value()->launch(inv, stream ? stream->s.get() : nullptr);
   return s.is_ok() ? 0 : fail(s);
 }
+
+int frame_save_onnx_weights(const char* path, int32_t n, const char* const* names, const int32_t* dtypes,
+                            const int64_t* const* dims, const int32_t* ranks, const void* const* data) {
+  if (path == nullptr || n < 0 || (n > 0 && (names == nullptr || dtypes == nullptr || dims == nullptr ||
+                                             ranks == nullptr || data == nullptr)))
+    return fail_msg("frame_save_onnx_weights: null argument");
+  std::vector<frame::interop::NamedTensor> ws;
+  for (int32_t i = 0; i < n; ++i) {
+    if (ranks[i] < 0 || (ranks[i] > 0 && dims[i] == nullptr)) return fail_msg("frame_save_onnx_weights: bad shape");
+    std::vector<int64_t> d(dims[i], dims[i] + ranks[i]);
+    auto t = frame::Tensor::empty(frame::Shape(d), frame::DType(static_cast<frame::DTypeCode>(dtypes[i])),
+                                  frame::cpu_device(), host_allocator());
+    if (!t.is_ok()) return fail(t.status());
+    const size_t nbytes = static_cast<size_t>(t.value().numel()) * t.value().dtype().itemsize();
+    if (nbytes > 0) std::memcpy(t.value().raw_data(), data[i], nbytes);
+    ws.push_back(frame::interop::NamedTensor{names[i], t.value()});
+  }
+  frame::Status st = frame::interop::save_onnx_weights(path, ws);
+  return st.is_ok() ? 0 : fail(st);
+}
+
+int frame_load_onnx_weights(const char* path, frame_onnx_weights** out) {
+  if (path == nullptr || out == nullptr) return fail_msg("frame_load_onnx_weights: null argument");
+  auto r = frame::interop::load_onnx_weights(path, host_allocator());
+  if (!r.is_ok()) return fail(r.status());
+  *out = new frame_onnx_weights{std::move(r.value())};
+  return 0;
+}
+int32_t frame_onnx_count(const frame_onnx_weights* w) { return static_cast<int32_t>(w->items.size()); }
+const char* frame_onnx_name(const frame_onnx_weights* w, int32_t i) { return w->items[static_cast<size_t>(i)].name.c_str(); }
+int32_t frame_onnx_dtype(const frame_onnx_weights* w, int32_t i) {
+  return static_cast<int32_t>(w->items[static_cast<size_t>(i)].tensor.dtype().code());
+}
+int32_t frame_onnx_rank(const frame_onnx_weights* w, int32_t i) {
+  return static_cast<int32_t>(w->items[static_cast<size_t>(i)].tensor.shape().rank());
+}
+int64_t frame_onnx_dim(const frame_onnx_weights* w, int32_t i, int32_t k) {
+  return w->items[static_cast<size_t>(i)].tensor.shape().dim(k);
+}
+const void* frame_onnx_data(const frame_onnx_weights* w, int32_t i) { return w->items[static_cast<size_t>(i)].tensor.raw_data(); }
+void frame_onnx_free(frame_onnx_weights* w) { delete w; }
 
 int frame_backend_copy(const char* backend, void* dst, const char* dst_backend, int32_t dst_index, const void* src,
                        const char* src_backend, int32_t src_index, size_t bytes, frame_stream* stream) {

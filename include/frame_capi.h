@@ -103,6 +103,23 @@ int frame_backend_copy(const char* backend, void* dst, const char* dst_backend, 
  * No counterpart in the reference (its allocator caches nothing); for tests of memory growth. */
 int frame_hip_allocator_stats(int32_t device, uint64_t out[5]);
 
+/* ONNX weight exchange (interop::save_onnx_weights / load_onnx_weights, reference
+ * include/frame/interop/onnx_weights.h:38,47): the graph.initializer subset of an ONNX ModelProto, dtypes
+ * float32 / float16 / bfloat16 (DTypeCode ordinals 0 / 2 / 3), host buffers. frame_load_onnx_weights parses `path`
+ * into host tensors owned by *out, read back with the frame_onnx_* accessors (file order) and released with
+ * frame_onnx_free. */
+typedef struct frame_onnx_weights frame_onnx_weights;
+int frame_save_onnx_weights(const char* path, int32_t n, const char* const* names, const int32_t* dtypes,
+                            const int64_t* const* dims, const int32_t* ranks, const void* const* data);
+int frame_load_onnx_weights(const char* path, frame_onnx_weights** out);
+int32_t frame_onnx_count(const frame_onnx_weights* w);
+const char* frame_onnx_name(const frame_onnx_weights* w, int32_t i);
+int32_t frame_onnx_dtype(const frame_onnx_weights* w, int32_t i);
+int32_t frame_onnx_rank(const frame_onnx_weights* w, int32_t i);
+int64_t frame_onnx_dim(const frame_onnx_weights* w, int32_t i, int32_t k);
+const void* frame_onnx_data(const frame_onnx_weights* w, int32_t i);
+void frame_onnx_free(frame_onnx_weights* w);
+
 /* Eager single-op launch (Backend::launch) of the one operator node in `node_ir_text` (a graph whose
  * non-input nodes are exactly one op) on the given tensors. */
 int frame_launch(const char* node_ir_text, const char* backend, frame_tensor* const* inputs, int32_t n_in,

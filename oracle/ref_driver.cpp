@@ -17,6 +17,7 @@
 #include <frame/hal/allocator.h>
 #include <frame/hal/backend.h>
 #include <frame/hal/executable.h>
+#include <frame/interop/onnx_weights.h>
 #include <frame/ir/graph.h>
 #include <frame/ir/memory_plan.h>
 #include <frame/ir/serialization.h>
@@ -168,6 +169,43 @@ int ref_memory_plan_text(const char* ir_text, char* out, int64_t cap, int64_t* n
   os << "total " << plan.value().total_bytes << '\n';
   return copy_text(os.str(), out, cap, needed);
 }
+
+// ONNX weight exchange through the reference's own codec (src/interop/onnx_weights.cpp): save host buffers; load
+// into a thread-local list read back with the ref_onnx_* accessors.
+thread_local std::vector<frame::interop::NamedTensor> g_onnx;
+
+int ref_save_onnx_weights(const char* path, int32_t n, const char* const* names, const int32_t* dtypes,
+                          const int64_t* const* dims, const int32_t* ranks, const void* const* data) {
+  auto b = frame::hal::BackendRegistry::instance().get(frame::kCpuBackendName);
+  if (!b.is_ok()) return set_err(b.status());
+  frame::hal::Allocator* alloc = b.value()->allocator(frame::cpu_device());
+  std::vector<frame::interop::NamedTensor> ws;
+  for (int32_t i = 0; i < n; ++i) {
+    std::vector<int64_t> d(dims[i], dims[i] + ranks[i]);
+    auto t = frame::Tensor::empty(frame::Shape(d), frame::DType(static_cast<frame::DTypeCode>(dtypes[i])),
+                                  frame::cpu_device(), *alloc);
+    if (!t.is_ok()) return set_err(t.status());
+    std::memcpy(t.value().raw_data(), data[i], static_cast<size_t>(t.value().numel()) * t.value().dtype().itemsize());
+    ws.push_back(frame::interop::NamedTensor{names[i], t.value()});
+  }
+  frame::Status st = frame::interop::save_onnx_weights(path, ws);
+  return st.is_ok() ? 0 : set_err(st);
+}
+
+int ref_load_onnx_weights(const char* path) {
+  auto b = frame::hal::BackendRegistry::instance().get(frame::kCpuBackendName);
+  if (!b.is_ok()) return set_err(b.status());
+  auto r = frame::interop::load_onnx_weights(path, *b.value()->allocator(frame::cpu_device()));
+  if (!r.is_ok()) return set_err(r.status());
+  g_onnx = std::move(r.value());
+  return 0;
+}
+int32_t ref_onnx_count(void) { return static_cast<int32_t>(g_onnx.size()); }
+const char* ref_onnx_name(int32_t i) { return g_onnx[static_cast<size_t>(i)].name.c_str(); }
+int32_t ref_onnx_dtype(int32_t i) { return static_cast<int32_t>(g_onnx[static_cast<size_t>(i)].tensor.dtype().code()); }
+int32_t ref_onnx_rank(int32_t i) { return static_cast<int32_t>(g_onnx[static_cast<size_t>(i)].tensor.shape().rank()); }
+int64_t ref_onnx_dim(int32_t i, int32_t k) { return g_onnx[static_cast<size_t>(i)].tensor.shape().dim(k); }
+const void* ref_onnx_data(int32_t i) { return g_onnx[static_cast<size_t>(i)].tensor.raw_data(); }
 
 }  // extern "C"
 #pragma GCC visibility pop

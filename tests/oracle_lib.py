@@ -97,6 +97,15 @@ def ref() -> ctypes.CDLL:
                                           POINTER(c_int64)]),
             "ref_sgd_update_text": (c_int, [c_char_p, c_void_p, ctypes.c_int32, ctypes.c_double, c_void_p, c_int64,
                                             POINTER(c_int64)]),
+            "ref_save_onnx_weights": (c_int, [c_char_p, ctypes.c_int32, c_void_p, c_void_p, c_void_p, c_void_p,
+                                              c_void_p]),
+            "ref_load_onnx_weights": (c_int, [c_char_p]),
+            "ref_onnx_count": (ctypes.c_int32, []),
+            "ref_onnx_name": (c_char_p, [ctypes.c_int32]),
+            "ref_onnx_dtype": (ctypes.c_int32, [ctypes.c_int32]),
+            "ref_onnx_rank": (ctypes.c_int32, [ctypes.c_int32]),
+            "ref_onnx_dim": (c_int64, [ctypes.c_int32, ctypes.c_int32]),
+            "ref_onnx_data": (c_void_p, [ctypes.c_int32]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(lib, name)
@@ -241,3 +250,28 @@ def pool2d(dtype, mode, x, geom):
     if rc != 0:
         raise ValueError(f"oracle_pool2d rc={rc}")
     return y
+
+
+def ref_save_onnx_weights(path: str, weights) -> None:
+    """The reference's interop::save_onnx_weights on {name: (dtype code, numpy array)}."""
+    from frame_hip import host
+
+    args, keep = host.onnx_arrays(weights)
+    if ref().ref_save_onnx_weights(path.encode(), len(weights), *args) != 0:
+        raise RuntimeError(f"reference save_onnx_weights failed: {ref_error()}")
+
+
+def ref_load_onnx_weights(path: str) -> dict:
+    """The reference's interop::load_onnx_weights: {name: (dtype code, numpy array)} in file order."""
+    r = ref()
+    if r.ref_load_onnx_weights(path.encode()) != 0:
+        raise RuntimeError(f"reference load_onnx_weights failed: {ref_error()}")
+    out = {}
+    for i in range(r.ref_onnx_count()):
+        dt = r.ref_onnx_dtype(i)
+        shape = tuple(r.ref_onnx_dim(i, k) for k in range(r.ref_onnx_rank(i)))
+        a = np.empty(shape, dtype=storage_np(dt))
+        if a.nbytes:
+            ctypes.memmove(a.ctypes.data, r.ref_onnx_data(i), a.nbytes)
+        out[r.ref_onnx_name(i).decode()] = (dt, a)
+    return out
