@@ -54,9 +54,15 @@ def gemm_operands(data: str):
     return [synth.to_storage(np.full((N, N), value, np.float32), BF16) for _ in range(2)]
 
 
-def run_gpu(steps: int, warmup: int, data: str = "uniform"):
+def run_gpu(steps: int, warmup: int, data: str = "uniform", settle_ms: float = 300.0):
     """Times `steps` runs of the compiled GEMM graph (runtime::compile(graph, "hip") -> Executable::run) on one
-    persistent stream, inputs and outputs resident in HBM."""
+    persistent stream, inputs and outputs resident in HBM.
+
+    After the `warmup` steps, further untimed steps run until `settle_ms` of wall time has passed since the
+    first one: the MI355X raises its engine clock over the first ~10 ms of sustained MFMA load (50 back-to-back
+    launches of this GEMM time ~15 % slower from a cold start than the same 50 a few milliseconds later), so a
+    few warmup steps alone time the clock ramp instead of the kernel. Returns (ms per step, wall seconds of the
+    timed region, settle steps run)."""
     from frame_hip import abi, graphs, host
 
     g = graphs.gemm(N, BF16, device="hip")
@@ -66,9 +72,16 @@ def run_gpu(steps: int, warmup: int, data: str = "uniform"):
     stream = host.Stream("hip")
     native = _NativeStream(stream.native)
     start, stop = abi.Event(), abi.Event()
+    t_start = time.perf_counter()
     for _ in range(warmup):
         exe.run_tensors(ins, outs, stream)
     stream.synchronize()
+    settle = 0
+    while (time.perf_counter() - t_start) * 1e3 < settle_ms:
+        for _ in range(20):
+            exe.run_tensors(ins, outs, stream)
+        stream.synchronize()
+        settle += 20
     abi.check(abi.lib().fh_device_synchronize())
     t0 = time.perf_counter()
     start.record(native)
@@ -79,7 +92,7 @@ def run_gpu(steps: int, warmup: int, data: str = "uniform"):
     stream.synchronize()
     wall = time.perf_counter() - t0
     ms = start.elapsed_ms(stop) / steps
-    return ms, wall
+    return ms, wall, settle
 
 
 TRAFFIC_SUMMARY = os.path.join(REPO, "profiles", "gemm16_bf16_4096_hbm_traffic.md")
@@ -299,6 +312,8 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--settle-ms", type=float, default=300.0,
+                    help="untimed steps after the warmup until this much wall time has passed (engine clock ramp)")
     ap.add_argument("--cpu-rows", type=int, default=128)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extras", action="store_true", help="only the headline GEMM (and the CPU baseline)")
@@ -320,7 +335,7 @@ def main():
         print(json.dumps({args.only: extras(args.steps, args.only).get(args.only, {"error": "no such entry"})}), flush=True)
         return
 
-    ms, wall = run_gpu(args.steps, args.warmup, args.gemm_data)
+    ms, wall, settle = run_gpu(args.steps, args.warmup, args.gemm_data, args.settle_ms)
     tflops = gemm_flops(N, N, N) / (ms * 1e-3) / 1e12
     line = {
         "metric": "GEMM/Conv2d TFLOP/s & % MFMA peak; fused-op GB/s; compiled-graph fwd latency",
@@ -329,6 +344,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle": {"ms": args.settle_ms, "untimed_steps": settle},
         "ms_per_step": round(ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
