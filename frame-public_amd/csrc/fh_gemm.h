@@ -15,6 +15,8 @@ struct EpilogueArgs {
   const void* ins[FH_MAX_SEGMENTS];
 };
 
+constexpr int kGemmMaxGroups = FH_GEMM_MAX_GROUPS;
+
 struct GemmArgs {
   const void* A;
   const void* B;
@@ -27,6 +29,14 @@ struct GemmArgs {
   // Transposed operand storage, honoured by the sequential kernel only: A(m, k) = A[k * lda + m],
   // B(k, n) = B[n * ldb + k].
   int32_t trans_a, trans_b;
+  // FH_GEMM_ANY_ORDER: the k-sum may be reassociated (small problems then take the split-k kernel).
+  int32_t any_order;
+  // groups > 0 (16-bit MFMA kernel only): blockIdx.y = g selects B, C and the epilogue operands from these
+  // arrays instead of the batch strides; A is shared (stride_a = 0).
+  int32_t groups;
+  const void* group_b[kGemmMaxGroups];
+  void* group_c[kGemmMaxGroups];
+  const void* group_ins[kGemmMaxGroups][FH_MAX_SEGMENTS];
 };
 
 typedef float f32x16_t __attribute__((ext_vector_type(16)));

@@ -357,6 +357,95 @@ __global__ __launch_bounds__(256) void gemm_seq_kernel(GemmArgs args) {
   }
 }
 
+// Small GEMMs whose k-sum may be reassociated (FH_GEMM_ANY_ORDER): the sequential kernel's few 16 x 16 tiles leave
+// most CUs idle, and each output's k loop is one long dependent chain. Here a workgroup of four waves owns a
+// 4 x 16 output tile (four times as many workgroups), K is staged through LDS in chunks of kSplitKC as fp32 (A
+// row-major, B transposed, double-buffered, the next chunk's global loads in flight during the current one), and
+// within every chunk wave w sums its own quarter of the k, one output per lane, products and sums in fp32 without
+// contraction like the sequential kernel. The four partial sums are added in wave order, so the result is
+// deterministic; it differs from the sequential order by fp32 reassociation only.
+constexpr int kSplitTM = 4, kSplitTN = 16, kSplitKC = 256, kSplitKP = kSplitKC + 4;
+
+template <typename T>
+__global__ __launch_bounds__(256) void gemm_split_kernel(GemmArgs args) {
+  using S = typename Io<T>::storage;
+  __shared__ __attribute__((aligned(16))) float As[2][kSplitTM * kSplitKP];
+  __shared__ __attribute__((aligned(16))) float Bt[2][kSplitTN * kSplitKP];
+  __shared__ float part[4][kSplitTM * kSplitTN];
+  const S* __restrict__ A = static_cast<const S*>(args.A) + blockIdx.z * args.stride_a;
+  const S* __restrict__ B = static_cast<const S*>(args.B) + blockIdx.z * args.stride_b;
+  S* __restrict__ C = static_cast<S*>(args.C) + blockIdx.z * args.stride_c;
+  const int64_t m0 = static_cast<int64_t>(blockIdx.y) * kSplitTM, n0 = static_cast<int64_t>(blockIdx.x) * kSplitTN;
+  const int64_t M = args.M, N = args.N, K = args.K;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int r = lane >> 4, c = lane & 15;  // this lane's output: (m0 + r, n0 + c)
+
+  // chunk loads: A[4][kSplitKC] (thread -> row t / 64, k t % 64 + 64 i) and B[kSplitKC][16] (thread -> k t / 16
+  // + 16 i, column t % 16), zero past the edges (never summed: the k loops stop at the chunk's length)
+  constexpr int AL = kSplitTM * kSplitKC / 256, BL = kSplitTN * kSplitKC / 256;
+  float la[AL], lb[BL];
+  auto load_chunk = [&](int64_t k0) {
+#pragma unroll
+    for (int i = 0; i < AL; ++i) {
+      const int64_t gm = m0 + (t >> 6), gk = k0 + (t & 63) + 64 * i;
+      la[i] = (gm < M && gk < K) ? Io<T>::load(A[gm * args.lda + gk]) : 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < BL; ++i) {
+      const int64_t gk = k0 + (t >> 4) + 16 * i, gn = n0 + (t & 15);
+      lb[i] = (gk < K && gn < N) ? Io<T>::load(B[gk * args.ldb + gn]) : 0.0f;
+    }
+  };
+  auto store_chunk = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < AL; ++i) As[buf][(t >> 6) * kSplitKP + (t & 63) + 64 * i] = la[i];
+#pragma unroll
+    for (int i = 0; i < BL; ++i) Bt[buf][(t & 15) * kSplitKP + (t >> 4) + 16 * i] = lb[i];
+  };
+
+  float acc = 0.0f;
+  const int chunks = static_cast<int>((K + kSplitKC - 1) / kSplitKC);
+  if (chunks > 0) {
+    load_chunk(0);
+    store_chunk(0);
+  }
+  __syncthreads();
+  constexpr int KQ = kSplitKC / 4;  // k per wave and chunk
+  for (int ch = 0; ch < chunks; ++ch) {
+    const int buf = ch & 1;
+    if (ch + 1 < chunks) load_chunk(static_cast<int64_t>(ch + 1) * kSplitKC);
+    const int kn = static_cast<int>(min<int64_t>(kSplitKC, K - static_cast<int64_t>(ch) * kSplitKC));
+    const int q0 = wave * KQ;
+    const int qn = max(0, min(KQ, kn - q0));
+    const float* ar = &As[buf][r * kSplitKP + q0];
+    const float* br = &Bt[buf][c * kSplitKP + q0];
+    int kk = 0;
+    for (; kk + 4 <= qn; kk += 4) {
+      const float4 a = *reinterpret_cast<const float4*>(ar + kk);
+      const float4 b = *reinterpret_cast<const float4*>(br + kk);
+      acc = acc + a.x * b.x;
+      acc = acc + a.y * b.y;
+      acc = acc + a.z * b.z;
+      acc = acc + a.w * b.w;
+    }
+    for (; kk < qn; ++kk) acc = acc + ar[kk] * br[kk];
+    if (ch + 1 < chunks) store_chunk(buf ^ 1);
+    __syncthreads();
+  }
+  part[wave][lane] = acc;
+  __syncthreads();
+  if (t < kSplitTM * kSplitTN) {
+    const int64_t row = m0 + (t >> 4), col = n0 + (t & 15);
+    if (row < M && col < N) {
+      const float sum = ((part[0][t] + part[1][t]) + part[2][t]) + part[3][t];
+      float v = Io<T>::round(sum);
+      const int64_t idx = row * args.ldc + col;
+      if (args.ep.nseg > 0) v = epilogue_one<T>(args.ep, v, idx);
+      C[idx] = Io<T>::store(v);
+    }
+  }
+}
+
 template <typename T, int BM, int BN>
 fh_status launch_tile(GemmArgs args, int64_t batch, hipStream_t stream) {
   args.tiles_m = static_cast<int32_t>((args.M + BM - 1) / BM);
@@ -399,6 +488,13 @@ fh_status dispatch_gemm(GemmArgs args, int64_t batch, hipStream_t stream) {
                        ((args.stride_a * esz) % 16 == 0) && ((args.stride_b * esz) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(args.C) % 16 == 0) && (args.ldc % E == 0) &&
                        ((args.stride_c * esz) % 16 == 0) && epilogue_aligned(args.ep);
+  if (small && args.any_order && !args.trans_a && !args.trans_b && (args.M + kSplitTM - 1) / kSplitTM <= 65535 &&
+      batch <= 65535) {
+    dim3 grid(static_cast<uint32_t>((args.N + kSplitTN - 1) / kSplitTN),
+              static_cast<uint32_t>((args.M + kSplitTM - 1) / kSplitTM), static_cast<uint32_t>(batch));
+    hipLaunchKernelGGL((gemm_split_kernel<T>), grid, dim3(256), 0, stream, args);
+    return launch_status("gemm_split_kernel launch");
+  }
   // small problems, or operands the tile kernels cannot take
   if (!aligned || small) {
     if ((args.M + kSeqT - 1) / kSeqT > 65535 || batch > 65535)
@@ -449,7 +545,8 @@ fh_status copy_epilogue(const fh_epilogue* in, EpilogueArgs& out) {
 }  // namespace
 
 fh_status gemm_with_epilogue_args(int32_t dtype, const void* A, const void* B, void* C, int64_t M, int64_t N,
-                                  int64_t K, const fh_epilogue* epilogue, hipStream_t stream) {
+                                  int64_t K, const fh_epilogue* epilogue, hipStream_t stream, int32_t flags) {
+  if ((flags & ~FH_GEMM_ANY_ORDER) != 0) return fail(FH_INVALID_ARGUMENT, "fh_gemm_ex: unknown flags " + std::to_string(flags));
   if (!is_supported_float(dtype)) return fail(FH_UNIMPLEMENTED, "fh_gemm: unsupported dtype");
   if (M < 0 || N < 0 || K < 0) return fail(FH_INVALID_ARGUMENT, "fh_gemm: negative dimension");
   if (M == 0 || N == 0) return FH_OK;
@@ -466,6 +563,7 @@ fh_status gemm_with_epilogue_args(int32_t dtype, const void* A, const void* B, v
   args.lda = K;
   args.ldb = N;
   args.ldc = N;
+  args.any_order = (flags & FH_GEMM_ANY_ORDER) != 0;
   fh_status st = copy_epilogue(epilogue, args.ep);
   if (st != FH_OK) return st;
   return run_gemm(dtype, args, 1, stream);
@@ -473,9 +571,68 @@ fh_status gemm_with_epilogue_args(int32_t dtype, const void* A, const void* B, v
 
 }  // namespace fh
 
+extern "C" fh_status fh_gemm_ex(int32_t dtype, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
+                                const fh_epilogue* epilogue, int32_t flags, void* stream) {
+  return fh::gemm_with_epilogue_args(dtype, A, B, C, M, N, K, epilogue, static_cast<hipStream_t>(stream), flags);
+}
+
+extern "C" fh_status fh_gemm_grouped(int32_t dtype, const void* A, int32_t groups, const void* const* B, void* const* C,
+                                     int64_t M, int64_t N, int64_t K, const fh_epilogue* epilogues, int32_t flags,
+                                     void* stream) {
+  using namespace fh;
+  if (groups < 1 || groups > kGemmMaxGroups)
+    return fail(FH_INVALID_ARGUMENT, "fh_gemm_grouped: groups must be in [1, " + std::to_string(kGemmMaxGroups) + "]");
+  if (B == nullptr || C == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_gemm_grouped: null operand arrays");
+  if ((flags & ~FH_GEMM_ANY_ORDER) != 0) return fail(FH_INVALID_ARGUMENT, "fh_gemm_grouped: unknown flags");
+  // every group must carry the same epilogue program (one kernel instance serves them all)
+  for (int g = 1; g < groups && epilogues != nullptr; ++g) {
+    if (epilogues[g].nseg != epilogues[0].nseg || epilogues[g].round_between != epilogues[0].round_between)
+      return fail(FH_INVALID_ARGUMENT, "fh_gemm_grouped: groups with different epilogue programs");
+    for (int s = 0; s < epilogues[0].nseg && s < FH_MAX_SEGMENTS; ++s)
+      if (epilogues[g].ops[s] != epilogues[0].ops[s])
+        return fail(FH_INVALID_ARGUMENT, "fh_gemm_grouped: groups with different epilogue programs");
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool sixteen = dtype == FH_BF16 || dtype == FH_F16;
+  if (sixteen && M > 0 && N > 0 && K > 0 && A != nullptr) {
+    GemmArgs args{};
+    args.A = A;
+    args.B = B[0];
+    args.C = C[0];
+    args.M = M;
+    args.N = N;
+    args.K = K;
+    args.lda = K;
+    args.ldb = N;
+    args.ldc = N;
+    args.any_order = (flags & FH_GEMM_ANY_ORDER) != 0;
+    fh_status st = copy_epilogue(epilogues, args.ep);
+    if (st != FH_OK) return st;
+    args.groups = groups;
+    for (int g = 0; g < groups; ++g) {
+      if (B[g] == nullptr || C[g] == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_gemm_grouped: null operand");
+      args.group_b[g] = B[g];
+      args.group_c[g] = C[g];
+      EpilogueArgs eg{};
+      if (epilogues != nullptr && (st = copy_epilogue(&epilogues[g], eg)) != FH_OK) return st;
+      for (int sg = 0; sg < FH_MAX_SEGMENTS; ++sg) args.group_ins[g][sg] = eg.ins[sg];
+    }
+    // the MFMA kernel takes the groups as its second grid axis when the problem is one it accepts and is not small
+    const int64_t tiles64 = ((M + 63) / 64) * ((N + 63) / 64) * groups;
+    if (tiles64 >= 16 && gemm16_try_launch(dtype, args, groups, s, &st)) return st;
+  }
+  // otherwise: one GEMM per group
+  for (int g = 0; g < groups; ++g) {
+    const fh_status st = fh_gemm_ex(dtype, A, B[g], C[g], M, N, K, epilogues != nullptr ? &epilogues[g] : nullptr,
+                                    flags, stream);
+    if (st != FH_OK) return st;
+  }
+  return FH_OK;
+}
+
 extern "C" fh_status fh_gemm(int32_t dtype, const void* A, const void* B, void* C, int64_t M, int64_t N,
                              int64_t K, const fh_epilogue* epilogue, void* stream) {
-  return fh::gemm_with_epilogue_args(dtype, A, B, C, M, N, K, epilogue, static_cast<hipStream_t>(stream));
+  return fh::gemm_with_epilogue_args(dtype, A, B, C, M, N, K, epilogue, static_cast<hipStream_t>(stream), 0);
 }
 
 extern "C" fh_status fh_gemm_batched(int32_t dtype, const void* A, const void* B, void* C, int64_t M,

@@ -106,8 +106,10 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
   const int64_t n0 = static_cast<int64_t>(tn) * BN;
 
   const S* __restrict__ A = static_cast<const S*>(args.A) + blockIdx.y * args.stride_a;
-  const S* __restrict__ B = static_cast<const S*>(args.B) + blockIdx.y * args.stride_b;
-  S* __restrict__ C = static_cast<S*>(args.C) + blockIdx.y * args.stride_c;
+  const bool grouped = args.groups > 0;
+  const S* __restrict__ B = grouped ? static_cast<const S*>(args.group_b[blockIdx.y])
+                                    : static_cast<const S*>(args.B) + blockIdx.y * args.stride_b;
+  S* __restrict__ C = grouped ? static_cast<S*>(args.group_c[blockIdx.y]) : static_cast<S*>(args.C) + blockIdx.y * args.stride_c;
   const int64_t M = args.M, N = args.N;
   const int64_t lda = args.lda, ldb = args.ldb, ldc = args.ldc;
   const int KT = static_cast<int>(args.K / kBK);
@@ -271,13 +273,17 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
   static_assert(64 % LPR == 0 && WM % RPI == 0, "epilogue access shape");
   const int c = (lane % LPR) * V;
   const int64_t col = n0 + wn * WN + c;
+  EpilogueArgs ep = args.ep;
+  if (grouped)
+#pragma unroll
+    for (int sg = 0; sg < FH_MAX_SEGMENTS; ++sg) ep.ins[sg] = args.group_ins[blockIdx.y][sg];
   for (int it = 0; it < WM / RPI; ++it) {
     const int rr = it * RPI + lane / LPR;
     const int64_t row = m0 + wm * WM + rr;
     if (row < M && col < N) {
       uint4 packed = *reinterpret_cast<const uint4*>(wl + rr * WN + c);
       const int64_t idx = row * ldc + col;
-      packed = epi_vec<E, T>(args.ep, packed, idx);
+      packed = epi_vec<E, T>(ep, packed, idx);
       *reinterpret_cast<uint4*>(C + idx) = packed;
     }
   }
@@ -332,6 +338,11 @@ bool gemm16_try_launch(int32_t dtype, const GemmArgs& args, int64_t batch, hipSt
   if ((args.stride_a * esz) % 16 || (args.stride_b * esz) % 16 || (args.stride_c * esz) % 16) return false;
   for (int s = 0; s < args.ep.nseg; ++s)
     if (ew_is_binary(args.ep.ops[s]) && !aligned16(args.ep.ins[s])) return false;
+  for (int g = 0; g < args.groups; ++g) {
+    if (!aligned16(args.group_b[g]) || !aligned16(args.group_c[g])) return false;
+    for (int s = 0; s < args.ep.nseg; ++s)
+      if (ew_is_binary(args.ep.ops[s]) && !aligned16(args.group_ins[g][s])) return false;
+  }
   *status = dtype == FH_BF16 ? dispatch<bf16_t>(args, batch, stream) : dispatch<f16_t>(args, batch, stream);
   return true;
 }

@@ -19,6 +19,7 @@ KERNELS_LIB = os.path.join(LIB_DIR, "libframe_hip_kernels.so")
 FH_OK = 0
 F32, F16, BF16 = 0, 2, 3
 EW_ADD, EW_MUL, EW_RELU, EW_SQUARE, EW_GELU = 1, 2, 3, 4, 5
+GEMM_ANY_ORDER = 1
 H2H, H2D, D2H, D2D = 0, 1, 2, 3
 MAX_SEGMENTS = 8
 
@@ -63,6 +64,10 @@ _SIGS = {
     "fh_event_elapsed_ms": (c_int32, [c_void_p, c_void_p, POINTER(c_float)]),
     "fh_gemm": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, POINTER(Epilogue),
                           c_void_p]),
+    "fh_gemm_ex": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, POINTER(Epilogue),
+                             c_int32, c_void_p]),
+    "fh_gemm_grouped": (c_int32, [c_int32, c_void_p, c_int32, POINTER(c_void_p), POINTER(c_void_p), c_int64, c_int64,
+                                  c_int64, POINTER(Epilogue), c_int32, c_void_p]),
     "fh_gemm_batched": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64,
                                   c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p]),
     "fh_conv2d_fwd": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_void_p, POINTER(c_int64),

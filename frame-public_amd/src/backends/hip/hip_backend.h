@@ -133,6 +133,10 @@ inline void* stream_handle(const ops::KernelContext& ctx) {
 // Internal op names produced by HipBackend::compile's lowering (never user-visible).
 inline constexpr std::string_view kGemmEpilogueOp = "hip_matmul_epilogue_internal";
 inline constexpr std::string_view kConvEpilogueOp = "hip_conv2d_epilogue_internal";
+// Up to FH_GEMM_MAX_GROUPS matmuls (each optionally with the same epilogue program) that read one A operand, as one
+// fh_gemm_grouped launch: inputs [A, B_0 .. B_{g-1}, epilogue operands of group 0, of group 1, ...], outputs C_0 ..
+// C_{g-1}; attrs groups, ep_ops (possibly empty), any_order.
+inline constexpr std::string_view kGemmGroupedOp = "hip_matmul_grouped_internal";
 // [d0, d1, d2, d3] -> [d0, d2, d3, d1]: NCHW activations to NHWC, [Cout][Cin][KH][KW] filters to [Cout][KH][KW][Cin].
 inline constexpr std::string_view kChannelsLastOp = "hip_channels_last_internal";
 // conv2d (optionally with an epilogue program) on channels-last operands; output NCHW, or channels-last

@@ -13,7 +13,12 @@
 // or conv2d whose only consumer is an elementwise node (add, mul, relu, square, gelu or a fused chain) that
 // takes the contraction result as its first operand is replaced by one internal node that applies the
 // consumer's program in the contraction's epilogue. The epilogue rounds to the storage dtype after the
-// product and after every segment, so results equal the unfused graph's bit for bit.
+// product and after every segment, exactly as the unfused consumer does. The fused matmul also carries
+// any_order = 1: small problems may then sum k in a reassociated order (the split-k kernel), within the fp32
+// tolerance; opt_level 0 keeps the sequential order, bit-identical to the reference CPU kernel.
+//  * grouped GEMMs (opt_level >= 1): 16-bit matmuls (fused or not) that read the same A with equal B shapes,
+// output types and epilogue programs (the Q/K/V projections of an attention block) become one grouped node
+// launched as one kernel (see lower_grouped_gemms).
 //  * channels-last conv (every opt_level): a conv that the MFMA implicit-GEMM path accepts becomes
 // channels_last(x), channels_last(w) and conv2d_nhwc (see lower_convs); activations whose every use takes
 // channels-last data stay channels-last between convs (see plan_channels_last).
@@ -104,6 +109,7 @@ Status lower_epilogues(ir::Graph& g) {
       for (const auto& [k, a] : p->attrs()) f.value()->set_attr(k, a);
       f.value()->set_attr("ep_ops", ir::AttrValue{prog});
       f.value()->set_attr("n_main_inputs", ir::AttrValue{static_cast<int64_t>(n_main)});
+      if (is_mm) f.value()->set_attr("any_order", ir::AttrValue{int64_t{1}});
       FRAME_RETURN_IF_ERROR(g.replace_all_uses(c->output(0), f.value()->output(0)));
       FRAME_RETURN_IF_ERROR(g.erase_node(c));
       FRAME_RETURN_IF_ERROR(g.erase_node(p));
@@ -1175,12 +1181,78 @@ Status lower_scaled_adds(ir::Graph& g) {
   return Status::ok();
 }
 
+// Matmuls (plain, or epilogue nodes with two main inputs) of a 16-bit dtype that read the same A value, with equal
+// B shapes, output types and epilogue programs, merged in groups of up to FH_GEMM_MAX_GROUPS into one
+// kGemmGroupedOp node, when every operand of the group is produced before the group's first member (so the
+// merged node can take that member's place and no member depends on another).
+Status lower_grouped_gemms(ir::Graph& g) {
+  struct Member {
+    ir::Node* node;
+    size_t pos;
+  };
+  std::unordered_map<const ir::Node*, size_t> pos;
+  {
+    const auto& order = g.topological_order();
+    for (size_t i = 0; i < order.size(); ++i) pos[order[i]] = i;
+  }
+  auto program = [](const ir::Node* n) -> std::vector<int64_t> {
+    const auto* p = attr_of<std::vector<int64_t>>(n, "ep_ops");
+    return p != nullptr ? *p : std::vector<int64_t>{};
+  };
+  std::map<std::string, std::vector<Member>> groups;  // key -> members in topological order
+  for (ir::Node* n : g.topological_order()) {
+    const bool mm = n->op() == "matmul" && n->inputs().size() == 2;
+    const auto* n_main = attr_of<int64_t>(n, "n_main_inputs");
+    const bool epi = n->op() == kGemmEpilogueOp && n_main != nullptr && *n_main == 2;
+    if ((!mm && !epi) || n->outputs().size() != 1) continue;
+    const ir::TensorType& ot = n->outputs()[0].type();
+    if (ot.dtype.code() != DTypeCode::kBFloat16 && ot.dtype.code() != DTypeCode::kFloat16) continue;
+    const ir::TensorType& bt = n->inputs()[1]->type();
+    if (bt.shape.rank() != 2 || ot.shape.rank() != 2) continue;
+    std::string key = std::to_string(reinterpret_cast<uintptr_t>(n->inputs()[0])) + "|" + bt.shape.to_string() + "|" +
+                      ot.shape.to_string() + "|" + std::to_string(static_cast<int>(ot.dtype.code())) + "|";
+    for (int64_t c : program(n)) key += std::to_string(c) + ",";
+    groups[key].push_back({n, pos[n]});
+  }
+  for (auto& [key, members] : groups) {
+    for (size_t start = 0; start + 1 < members.size(); start += FH_GEMM_MAX_GROUPS) {
+      const size_t count = std::min<size_t>(FH_GEMM_MAX_GROUPS, members.size() - start);
+      if (count < 2) break;
+      std::vector<Member> part(members.begin() + static_cast<std::ptrdiff_t>(start),
+                               members.begin() + static_cast<std::ptrdiff_t>(start + count));
+      const size_t first = part.front().pos;
+      bool ok = true;
+      for (const Member& m : part)
+        for (const ir::Value* v : m.node->inputs())
+          if (v->producer() != nullptr && pos[v->producer()] >= first) ok = false;
+      if (!ok) continue;
+      std::vector<ir::Value*> ins{part.front().node->inputs()[0]};
+      for (const Member& m : part) ins.push_back(m.node->inputs()[1]);
+      for (const Member& m : part)
+        for (size_t j = 2; j < m.node->inputs().size(); ++j) ins.push_back(m.node->inputs()[j]);
+      std::vector<ir::TensorType> types;
+      for (const Member& m : part) types.push_back(m.node->outputs()[0].type());
+      Result<ir::Node*> f = g.create_node(std::string(kGemmGroupedOp), ins, types);
+      if (!f.is_ok()) return f.status();
+      f.value()->set_attr("groups", ir::AttrValue{static_cast<int64_t>(count)});
+      f.value()->set_attr("ep_ops", ir::AttrValue{program(part.front().node)});
+      f.value()->set_attr("any_order", ir::AttrValue{int64_t{1}});
+      for (size_t i = 0; i < count; ++i) {
+        FRAME_RETURN_IF_ERROR(g.replace_all_uses(part[i].node->output(0), f.value()->output(static_cast<int32_t>(i))));
+        FRAME_RETURN_IF_ERROR(g.erase_node(part[i].node));
+      }
+    }
+  }
+  return Status::ok();
+}
+
 Result<ir::Graph> lower_for_hip(const ir::Graph& graph, int32_t opt_level) {
   Result<ir::Graph> work = lower_matmul_grads(graph);
   if (!work.is_ok()) return work.status();
   // Attention runs at every level (like the conv lowering), before the epilogue fusion would claim its matmuls.
   FRAME_RETURN_IF_ERROR(lower_attention(work.value()));
   if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_epilogues(work.value()));
+  if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_grouped_gemms(work.value()));
   if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_scaled_adds(work.value()));
   // Channels-last conv lowering runs at every level, so the conv numerics do not depend on the level.
   return lower_convs(work.value());

@@ -145,8 +145,67 @@ Status gemm_impl(KernelContext& ctx, const std::string& op, size_t n_main) {
   if (!dt.is_ok()) return dt.status();
   Result<fh_epilogue> ep = make_epilogue(ctx, op, n_main);
   if (!ep.is_ok()) return ep.status();
-  FRAME_HIP_RETURN_IF_ERROR(fh_gemm(dt.value(), a.raw_data(), b.raw_data(), c.raw_data(), m, n, k,
-                                    ep.value().nseg > 0 ? &ep.value() : nullptr, stream_handle(ctx)),
+  const auto* any = attr<int64_t>(ctx, "any_order");
+  const int32_t flags = (any != nullptr && *any != 0) ? FH_GEMM_ANY_ORDER : 0;
+  FRAME_HIP_RETURN_IF_ERROR(fh_gemm_ex(dt.value(), a.raw_data(), b.raw_data(), c.raw_data(), m, n, k,
+                                       ep.value().nseg > 0 ? &ep.value() : nullptr, flags, stream_handle(ctx)),
+                            "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
+// kGemmGroupedOp: inputs [A, B_0 .. B_{g-1}, epilogue operands group by group], outputs C_0 .. C_{g-1}.
+Status gemm_grouped_kernel(KernelContext& ctx) {
+  const std::string op(kGemmGroupedOp);
+  const auto* groups_attr = attr<int64_t>(ctx, "groups");
+  if (groups_attr == nullptr || *groups_attr < 1 || *groups_attr > FH_GEMM_MAX_GROUPS) return invalid(op, "bad groups attribute");
+  const size_t g = static_cast<size_t>(*groups_attr);
+  if (ctx.outputs.size() != g || ctx.inputs.size() < 1 + g) return invalid(op, "bad operand count");
+  const Tensor& a = ctx.inputs[0];
+  if (a.shape().rank() != 2) return invalid(op, "A must be rank-2");
+  const int64_t m = a.shape().dim(0), k = a.shape().dim(1);
+  const Tensor& b0 = ctx.inputs[1];
+  if (b0.shape().rank() != 2 || b0.shape().dim(0) != k) return invalid(op, "B shape mismatch");
+  const int64_t n = b0.shape().dim(1);
+  FRAME_RETURN_IF_ERROR(same_dtype(ctx, op));
+  Result<int32_t> dt = float_code(op, a.dtype());
+  if (!dt.is_ok()) return dt.status();
+  const auto* prog = attr<std::vector<int64_t>>(ctx, "ep_ops");
+  size_t binary = 0;
+  if (prog != nullptr) {
+    if (prog->size() > FH_MAX_SEGMENTS) return invalid(op, "epilogue longer than " + std::to_string(FH_MAX_SEGMENTS) + " segments");
+    for (int64_t c : *prog) binary += (c == FH_EW_ADD || c == FH_EW_MUL) ? 1 : 0;
+  }
+  if (ctx.inputs.size() != 1 + g + g * binary) return invalid(op, "epilogue operand count does not match the program");
+  std::vector<const void*> bs(g);
+  std::vector<void*> cs(g);
+  std::vector<fh_epilogue> eps(g);
+  size_t next = 1 + g;
+  for (size_t i = 0; i < g; ++i) {
+    const Tensor& b = ctx.inputs[1 + i];
+    Tensor& c = ctx.outputs[i];
+    if (b.shape().rank() != 2 || b.shape().dim(0) != k || b.shape().dim(1) != n || c.shape().rank() != 2 ||
+        c.shape().dim(0) != m || c.shape().dim(1) != n)
+      return invalid(op, "group " + std::to_string(i) + ": shape mismatch");
+    bs[i] = b.raw_data();
+    cs[i] = c.raw_data();
+    eps[i] = fh_epilogue{};
+    if (prog != nullptr) {
+      eps[i].nseg = static_cast<int32_t>(prog->size());
+      eps[i].round_between = 1;
+      for (size_t s = 0; s < prog->size(); ++s) {
+        eps[i].ops[s] = static_cast<uint8_t>((*prog)[s]);
+        if (eps[i].ops[s] == FH_EW_ADD || eps[i].ops[s] == FH_EW_MUL) {
+          const Tensor& t = ctx.inputs[next++];
+          if (t.numel() != m * n || !(t.dtype() == c.dtype())) return invalid(op, "epilogue operand has the wrong shape or dtype");
+          eps[i].ins[s] = t.raw_data();
+        }
+      }
+    }
+  }
+  const auto* any = attr<int64_t>(ctx, "any_order");
+  const int32_t flags = (any != nullptr && *any != 0) ? FH_GEMM_ANY_ORDER : 0;
+  FRAME_HIP_RETURN_IF_ERROR(fh_gemm_grouped(dt.value(), a.raw_data(), static_cast<int32_t>(g), bs.data(), cs.data(), m, n,
+                                            k, eps.data(), flags, stream_handle(ctx)),
                             "op '" + op + "' (hip)");
   return Status::ok();
 }
@@ -877,6 +936,7 @@ FRAME_REGISTER_KERNEL("gelu", kHipBackendName, (&ew_kernel<FH_EW_GELU, 1>));
 FRAME_REGISTER_KERNEL(ops::kFusedElementwiseOpName, kHipBackendName, &fused_kernel);
 FRAME_REGISTER_KERNEL("matmul", kHipBackendName, &matmul_kernel);
 FRAME_REGISTER_KERNEL(kGemmEpilogueOp, kHipBackendName, &gemm_epilogue_kernel);
+FRAME_REGISTER_KERNEL(kGemmGroupedOp, kHipBackendName, &gemm_grouped_kernel);
 FRAME_REGISTER_KERNEL("conv2d", kHipBackendName, &conv2d_kernel);
 FRAME_REGISTER_KERNEL(kConvEpilogueOp, kHipBackendName, &conv_epilogue_kernel);
 FRAME_REGISTER_KERNEL(kConvNhwcOp, kHipBackendName, &conv_nhwc_kernel);

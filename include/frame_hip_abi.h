@@ -128,6 +128,22 @@ typedef struct fh_epilogue {
 fh_status fh_gemm(int32_t dtype, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
                   const fh_epilogue* epilogue, void* stream);
 
+/* fh_gemm with flags. FH_GEMM_ANY_ORDER: the sum over k may be taken in any order (the host passes it at
+ * opt_level >= 1, where results are checked within tolerance rather than bit for bit); small problems then run
+ * a split-k kernel instead of the sequential-order one. No reference counterpart beyond fh_gemm's. */
+#define FH_GEMM_ANY_ORDER 1
+fh_status fh_gemm_ex(int32_t dtype, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
+                     const fh_epilogue* epilogue, int32_t flags, void* stream);
+
+/* `groups` GEMMs sharing A[M,K] and one shape, in one launch: C_g[M,N] = A · B_g[K,N], then epilogues[g]
+ * (every group the same program, its own operands). Used where HipBackend::compile merges the Q/K/V
+ * projections of an attention block, which read the same normalised input (the reference runs three
+ * Linear layers, reference: src/nn/layers.cpp:1014-1080). */
+#define FH_GEMM_MAX_GROUPS 4
+fh_status fh_gemm_grouped(int32_t dtype, const void* A, int32_t groups, const void* const* B, void* const* C,
+                          int64_t M, int64_t N, int64_t K, const fh_epilogue* epilogues, int32_t flags,
+                          void* stream);
+
 /* Batched GEMM over `batch` independent problems with element strides between problems.
  * Used by the fused attention lowering of per-(batch, head) matmuls (no reference counterpart in one
  * call: the reference launches one matmul per (batch, head), reference: src/nn/layers.cpp:1014-1080). */

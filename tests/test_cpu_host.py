@@ -3,6 +3,7 @@ reference's own golden IR fixtures (tests/golden/compiler, copied from the refer
 tests/cpp/compiler/testdata) and against the reference pipeline itself, the memory plan, the compile cache and
 the error contract. No GPU is touched: graphs here live on the oracle's `cpu` backend, and hip graphs stop
 before Backend::compile."""
+import ctypes
 import os
 import re
 import subprocess
@@ -306,3 +307,63 @@ def test_channels_last_stops_at_graph_outputs_and_other_uses():
     # a reshape of a non-1x1 plane needs NCHW order: the second conv stays NCHW
     out = host.hip_lowered(_conv_chain(softmax_tail=True).text(), 1)
     assert out.count("out_nhwc=1") == 1
+
+
+def test_qkv_projections_become_one_grouped_gemm():
+    # the three projections of the attention block read the LN1 output: one grouped node at opt_level 1, with the
+    # bias adds as per-group epilogues; opt_level 0 keeps three matmuls; fp32 is left alone
+    g, _ = graphs.transformer_block(batch=2, seq=128, d_model=128, heads=2, ffn=256, dtype=3)
+    out = host.hip_lowered(g.text(), 1)
+    ops = re.findall(r"= (\w+)\(", out)
+    assert ops.count("hip_matmul_grouped_internal") == 1, out
+    line = [l for l in out.splitlines() if "hip_matmul_grouped_internal" in l][0]
+    assert "groups=3" in line and "ep_ops=[1]" in line and "any_order=1" in line
+    assert line.count("bfloat16[256,128]") == 3  # three outputs
+    assert ops.count("hip_matmul_epilogue_internal") == 3  # output projection, FFN up, FFN down
+    assert "hip_matmul_grouped_internal" not in host.hip_lowered(g.text(), 0)
+    g32, _ = graphs.transformer_block(batch=1, seq=64, d_model=128, heads=2, ffn=256, dtype=0)
+    assert "hip_matmul_grouped_internal" not in host.hip_lowered(g32.text(), 1)
+
+
+def test_grouping_skips_members_that_depend_on_each_other():
+    # y2's bias is y1 itself: merging would make the group read its own output, so the two stay apart
+    g = graphs.Graph("hip")
+    x, w1, w2, b1 = g.input(3, (64, 64)), g.input(3, (64, 64)), g.input(3, (64, 64)), g.input(3, (64, 64))
+    y1 = g.add(g.matmul(x, w1), b1)
+    y2 = g.add(g.matmul(x, w2), y1)
+    g.output(y2)
+    out = host.hip_lowered(g.text(), 1)
+    assert "hip_matmul_grouped_internal" not in out
+    # independent members with equal shapes and programs do merge, up to four per node
+    g = graphs.Graph("hip")
+    x = g.input(3, (64, 64))
+    ws = [g.input(3, (64, 32)) for _ in range(5)]  # operands must precede the first member in topological order
+    ys = [g.relu(g.matmul(x, w)) for w in ws]
+    for y in ys:
+        g.output(y)
+    out = host.hip_lowered(g.text(), 1)
+    ops = re.findall(r"= (\w+)\(", out)
+    assert ops.count("hip_matmul_grouped_internal") == 1 and "groups=4" in out
+    assert ops.count("hip_matmul_epilogue_internal") == 1  # the fifth
+
+
+def test_small_fused_gemms_are_marked_any_order_only_above_opt0():
+    g = graphs.mlp(64, 0)
+    assert host.hip_lowered(g.text(), 1).count("any_order=1") == 2
+    assert "any_order" not in host.hip_lowered(g.text(), 0)
+
+
+def test_gemm_grouped_and_ex_argument_checks():
+    # validation happens before any device call, so it runs without a GPU
+    lib = abi.lib()
+    ptrs = (ctypes.c_void_p * 4)(8, 8, 8, 8)
+    eps = (abi.Epilogue * 4)()
+    for groups in (0, 5):
+        assert lib.fh_gemm_grouped(3, 8, groups, ptrs, ptrs, 64, 64, 64, eps, 1, None) == 1  # invalid_argument
+    eps[0] = abi.make_epilogue([(abi.EW_ADD, 8)])
+    eps[1] = abi.make_epilogue([(abi.EW_MUL, 8)])
+    assert lib.fh_gemm_grouped(3, 8, 2, ptrs, ptrs, 64, 64, 64, eps, 1, None) == 1
+    assert b"different epilogue programs" in lib.fh_last_error()
+    assert lib.fh_gemm_grouped(3, 8, 2, ptrs, ptrs, 64, 64, 64, eps, 4, None) == 1  # unknown flag
+    assert lib.fh_gemm_ex(3, 8, 8, 8, 64, 64, 64, None, 6, None) == 1
+    assert b"unknown flags" in lib.fh_last_error()

@@ -176,6 +176,96 @@ def test_gemm_epilogue_add_relu(hip, dtype):
     assert_close(got, want, dtype, what="gemm epilogue")
 
 
+def run_gemm_ex(hip, dtype, a, b, epilogue_segments=None, flags=1):
+    """fh_gemm_ex (flags 1 = FH_GEMM_ANY_ORDER)."""
+    m, k = a.shape
+    n = b.shape[1]
+    da, db = dev(hip, a), dev(hip, b)
+    dc = hip.DeviceBuffer(m * n * a.itemsize)
+    keep, segs = [], []
+    for op, operand in epilogue_segments or []:
+        if operand is None:
+            segs.append((op, None))
+        else:
+            keep.append(dev(hip, operand))
+            segs.append((op, keep[-1].value))
+    ep = ctypes.byref(hip.make_epilogue(segs)) if segs else None
+    hip.check(hip.lib().fh_gemm_ex(dtype, da.value, db.value, dc.value, m, n, k, ep, flags, None), "fh_gemm_ex")
+    hip.check(hip.lib().fh_device_synchronize())
+    return dc.download((m, n), a.dtype)
+
+
+# Small GEMMs with FH_GEMM_ANY_ORDER (what the host passes at opt_level >= 1) run the split-k kernel: k summed in
+# four interleaved quarters per 256-k chunk, the quarters added in order. Within the rule against the oracle,
+# deterministic, and its epilogue is exact (fused == plain split-k GEMM followed by the elementwise program).
+SPLIT_SHAPES = [
+    (64, 784, 256),   # C1 layer 1
+    (64, 256, 10),    # C1 layer 2
+    (1, 8, 8),
+    (100, 1000, 37),  # ragged rows, columns and chunks
+    (4, 300, 16),
+    (33, 5, 50),      # k below one wave's quarter
+]
+
+
+@pytest.mark.parametrize("dtype", [F32, BF16, F16])
+@pytest.mark.parametrize("shape", SPLIT_SHAPES)
+def test_gemm_split_k_matches_oracle(hip, dtype, shape):
+    m, k, n = shape
+    say(f"split-k gemm dtype={dtype} m={m} k={k} n={n}")
+    a = synth.tensor(61, (m, k), dtype, "normal")
+    b = synth.tensor(62, (k, n), dtype, "normal", 0.1)
+    bias = synth.tensor(63, (m, n), dtype, "normal")
+    got = run_gemm_ex(hip, dtype, a, b)
+    assert_close(got, orc.matmul(dtype, a, b), dtype, what=f"split-k gemm {shape}")
+    assert_bitwise(run_gemm_ex(hip, dtype, a, b), got, "split-k gemm, second call")
+    fused = run_gemm_ex(hip, dtype, a, b, [(hip.EW_ADD, bias), (hip.EW_RELU, None)])
+    assert_bitwise(fused, run_ew(hip, dtype, [1, 3], [2, 1], [got, bias]), "split-k epilogue vs separate program")
+
+
+def run_gemm_grouped(hip, dtype, a, bs, biases):
+    m, k = a.shape
+    n = bs[0].shape[1]
+    g = len(bs)
+    da = dev(hip, a)
+    dbs = [dev(hip, b) for b in bs]
+    dcs = [hip.DeviceBuffer(m * n * a.itemsize) for _ in range(g)]
+    dbias = [dev(hip, x) for x in biases] if biases else []
+    eps = (hip.Epilogue * g)()
+    for i in range(g):
+        if biases:
+            eps[i] = hip.make_epilogue([(hip.EW_ADD, dbias[i].value)])
+    bp = (ctypes.c_void_p * g)(*[d.value for d in dbs])
+    cp = (ctypes.c_void_p * g)(*[d.value for d in dcs])
+    hip.check(hip.lib().fh_gemm_grouped(dtype, da.value, g, bp, cp, m, n, k, eps, 1, None), "fh_gemm_grouped")
+    hip.check(hip.lib().fh_device_synchronize())
+    return [d.download((m, n), a.dtype) for d in dcs]
+
+
+@pytest.mark.parametrize("dtype", [BF16, F16])
+@pytest.mark.parametrize("shape,groups,with_bias", [((512, 256, 256), 3, True), ((256, 128, 512), 2, False),
+                                                     ((300, 96, 264), 4, True), ((4096, 1024, 1024), 3, True)])
+def test_gemm_grouped_equals_separate_gemms(hip, dtype, shape, groups, with_bias):
+    """fh_gemm_grouped (C5's merged Q/K/V projections) against one fh_gemm per group: the same MFMA kernel
+    family sums every output in the same k order, so the results agree bit for bit (every shape here has at least
+    16 tiles of 64 x 64 per group, so the single GEMMs take the MFMA kernel too); small shapes also against the
+    oracle."""
+    m, k, n = shape
+    say(f"grouped gemm dtype={dtype} m={m} k={k} n={n} groups={groups} bias={with_bias}")
+    a = synth.tensor(71, (m, k), dtype, "uniform")
+    bs = [synth.tensor(72 + i, (k, n), dtype, "uniform") for i in range(groups)]
+    biases = [synth.tensor(80 + i, (m, n), dtype, "normal") for i in range(groups)] if with_bias else None
+    got = run_gemm_grouped(hip, dtype, a, bs, biases)
+    for i in range(groups):
+        segs = [(hip.EW_ADD, biases[i])] if with_bias else None
+        assert_bitwise(got[i], run_gemm(hip, dtype, a, bs[i], segs), f"group {i} vs fh_gemm")
+        if m * n * k <= (1 << 24):
+            want = orc.matmul(dtype, a, bs[i])
+            if with_bias:
+                want = orc.ew_program(dtype, [1], [2], [want, biases[i]])
+            assert_close(got[i], want, dtype, what=f"group {i} vs oracle")
+
+
 def run_ew(hip, dtype, ops, arities, ins):
     dins = [dev(hip, x) for x in ins]
     out = hip.DeviceBuffer(ins[0].nbytes)
