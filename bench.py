@@ -265,6 +265,59 @@ def extras(steps, only=None):
         res["workload"] = f"C3 conv gradients {'bf16' if dtype == BF16 else 'f32'} [32,64,56,56]*[64,64,3,3]"
         return res
 
+    def graph_replay():
+        # eager step launches against the captured-hipGraph replay (FRAME_HIP_GRAPHS=1) of the same executable
+        cfgs = {"c1_mlp": (graphs.mlp(64, F32).text(), [graphs.mlp_inputs(64, F32)], 200, 20)}
+        g4, specs = graphs.resnet18(batch=64, dtype=BF16)
+        cfgs["c4_resnet18"] = (g4.text(), [graphs.resnet18_inputs(specs, batch=64, dtype=BF16)], 20, 5)
+        g5, shapes = graphs.transformer_block(dtype=BF16)
+        cfgs["c5_transformer"] = (g5.text(), [graphs.transformer_inputs(shapes, dtype=BF16)], 40, 5)
+        res = {}
+        for name, (text, sets, n, w) in cfgs.items():
+            row = {}
+            for mode in ("eager", "replay", "eager_again"):
+                if mode == "replay":
+                    os.environ["FRAME_HIP_GRAPHS"] = "1"
+                else:
+                    os.environ.pop("FRAME_HIP_GRAPHS", None)
+                row[mode + "_us"] = round(_time_graph(text, sets, n, w) * 1e3, 1)
+            os.environ.pop("FRAME_HIP_GRAPHS", None)
+            res[name] = row
+        return res
+
+    def cpu_baselines():
+        # the reference CPU backend (oracle/_ref, one thread) on a bounded sample of each configuration, scaled to
+        # the configuration (every op here computes each image / sequence independently, so the scale is exact)
+        import oracle_lib as orc
+
+        if not orc.ref_available():
+            return {"error": "oracle/_ref is not built"}
+        res = {"cores": 1, "nproc": os.cpu_count(), "cpu_model": _cpu_model()}
+
+        def timed(text, ins, out_specs, reps=1):
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                orc.ref_run_graph(text.replace("@hip:0", "@cpu:0"), ins, out_specs)
+            return (time.perf_counter() - t0) / reps
+
+        t = timed(graphs.mlp(64, F32).text(), graphs.mlp_inputs(64, F32), [((64, 10), np.float32)], reps=20)
+        res["c1_mlp"] = {"sample": "the whole batch-64 forward, 20 runs", "ms": round(t * 1e3, 3)}
+        t = timed(graphs.conv(BF16, n=1).text(), graphs.conv_inputs(BF16, n=1), [((1, 64, 56, 56), np.uint16)])
+        res["conv_c3_bf16"] = {"sample": "image 1 of 32", "ms": round(t * 32 * 1e3, 1),
+                               "TFLOP/s": round(7.399e9 / (t * 32) / 1e12, 6)}
+        g, specs = graphs.resnet18(batch=1, dtype=BF16)
+        t = timed(g.text(), graphs.resnet18_inputs(specs, batch=1, dtype=BF16), [((1, 1000), np.uint16)])
+        res["c4_resnet18"] = {"sample": "image 1 of 64", "ms": round(t * 64 * 1e3, 1),
+                              "TFLOP/s": round(232.2e9 / (t * 64) / 1e12, 6)}
+        g, shapes = graphs.transformer_block(batch=1, dtype=BF16, act="relu")
+        t = timed(g.text(), graphs.transformer_inputs(shapes, rows=512, dtype=BF16), [((512, 1024), np.uint16)])
+        res["c5_transformer"] = {"sample": "sequence 1 of 8, relu in place of gelu (the reference has no gelu op)",
+                                 "ms": round(t * 8 * 1e3, 1), "TFLOP/s": round(111.67e9 / (t * 8) / 1e12, 6)}
+        return res
+
+    if only is not None:
+        guard("graph_replay", graph_replay)
+        guard("cpu_baselines", cpu_baselines)
     guard("fused_elementwise", fused)
     guard("conv_c3_bf16", lambda: conv(BF16))
     guard("conv_c3_f32", lambda: conv(F32))
@@ -279,6 +332,17 @@ def extras(steps, only=None):
     guard("conv_c3_grads_bf16", lambda: conv_grads(BF16))
     guard("c4_resnet18_train_step", resnet_train)
     return out
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
 
 def cpu_baseline(rows: int):

@@ -31,6 +31,8 @@ struct GemmArgs {
   int32_t trans_a, trans_b;
   // FH_GEMM_ANY_ORDER: the k-sum may be reassociated (small problems then take the split-k kernel).
   int32_t any_order;
+  // FH_GEMM_ROW_SOFTMAX: softmax over every output row after the epilogue (split-k kernel, N <= 16).
+  int32_t row_softmax;
   // groups > 0 (16-bit MFMA kernel only): blockIdx.y = g selects B, C and the epilogue operands from these
   // arrays instead of the batch strides; A is shared (stride_a = 0).
   int32_t groups;

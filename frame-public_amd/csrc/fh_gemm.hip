@@ -358,20 +358,26 @@ __global__ __launch_bounds__(256) void gemm_seq_kernel(GemmArgs args) {
 }
 
 // Small GEMMs whose k-sum may be reassociated (FH_GEMM_ANY_ORDER): the sequential kernel's few 16 x 16 tiles leave
-// most CUs idle, and each output's k loop is one long dependent chain. Here a workgroup of four waves owns a
-// 4 x 16 output tile (four times as many workgroups), K is staged through LDS in chunks of kSplitKC as fp32 (A
-// row-major, B transposed, double-buffered, the next chunk's global loads in flight during the current one), and
-// within every chunk wave w sums its own quarter of the k, one output per lane, products and sums in fp32 without
-// contraction like the sequential kernel. The four partial sums are added in wave order, so the result is
-// deterministic; it differs from the sequential order by fp32 reassociation only.
-constexpr int kSplitTM = 4, kSplitTN = 16, kSplitKC = 256, kSplitKP = kSplitKC + 4;
+// most CUs idle, and each output's k loop is one long dependent chain. Here a workgroup of 16 waves owns a 4 x 16
+// output tile (four times as many workgroups) and splits K 16 ways. K is staged through LDS as fp32 in chunks of
+// up to kSplitKC = 1024 (A row-major, B transposed; every global load of a chunk in flight at once, so C1's layers
+// pay one memory latency); within a chunk wave w sums its own contiguous sixteenth of the k, one output per lane,
+// products and sums in fp32 without contraction like the sequential kernel. The 16 partial sums are then added in
+// wave order: deterministic, and different from the sequential order by fp32 reassociation only. (Measured at
+// C1's shapes on MI355X: 64x784x256 6.4 us and 64x256x10 3.4 us against 10.2 / 4.4 us with 4 waves and 16.3 /
+// 6.1 us sequential; a launch of any kernel costs ~3 us there.)
+// With row_softmax (N <= 16, so every output row lies in one workgroup), the rounded outputs of each row then
+// go through softmax exactly as fh_softmax_rows computes it (m = max, e = exp(x - m), s = sum e, y = round(e / s);
+// the sum taken over 16 lanes instead of 64).
+constexpr int kSplitTM = 4, kSplitTN = 16, kSplitKC = 1024, kSplitKP = kSplitKC + 4, kSplitWaves = 16;
 
 template <typename T>
-__global__ __launch_bounds__(256) void gemm_split_kernel(GemmArgs args) {
+__global__ __launch_bounds__(kSplitWaves * 64) void gemm_split_kernel(GemmArgs args) {
   using S = typename Io<T>::storage;
-  __shared__ __attribute__((aligned(16))) float As[2][kSplitTM * kSplitKP];
-  __shared__ __attribute__((aligned(16))) float Bt[2][kSplitTN * kSplitKP];
-  __shared__ float part[4][kSplitTM * kSplitTN];
+  __shared__ __attribute__((aligned(16))) float As[kSplitTM * kSplitKP];
+  __shared__ __attribute__((aligned(16))) float Bt[kSplitTN * kSplitKP];
+  __shared__ float part[kSplitWaves][kSplitTM * kSplitTN];
+  constexpr int NT = kSplitWaves * 64;
   const S* __restrict__ A = static_cast<const S*>(args.A) + blockIdx.z * args.stride_a;
   const S* __restrict__ B = static_cast<const S*>(args.B) + blockIdx.z * args.stride_b;
   S* __restrict__ C = static_cast<S*>(args.C) + blockIdx.z * args.stride_c;
@@ -380,69 +386,51 @@ __global__ __launch_bounds__(256) void gemm_split_kernel(GemmArgs args) {
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   const int r = lane >> 4, c = lane & 15;  // this lane's output: (m0 + r, n0 + c)
 
-  // chunk loads: A[4][kSplitKC] (thread -> row t / 64, k t % 64 + 64 i) and B[kSplitKC][16] (thread -> k t / 16
-  // + 16 i, column t % 16), zero past the edges (never summed: the k loops stop at the chunk's length)
-  constexpr int AL = kSplitTM * kSplitKC / 256, BL = kSplitTN * kSplitKC / 256;
-  float la[AL], lb[BL];
-  auto load_chunk = [&](int64_t k0) {
-#pragma unroll
-    for (int i = 0; i < AL; ++i) {
-      const int64_t gm = m0 + (t >> 6), gk = k0 + (t & 63) + 64 * i;
-      la[i] = (gm < M && gk < K) ? Io<T>::load(A[gm * args.lda + gk]) : 0.0f;
-    }
-#pragma unroll
-    for (int i = 0; i < BL; ++i) {
-      const int64_t gk = k0 + (t >> 4) + 16 * i, gn = n0 + (t & 15);
-      lb[i] = (gk < K && gn < N) ? Io<T>::load(B[gk * args.ldb + gn]) : 0.0f;
-    }
-  };
-  auto store_chunk = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < AL; ++i) As[buf][(t >> 6) * kSplitKP + (t & 63) + 64 * i] = la[i];
-#pragma unroll
-    for (int i = 0; i < BL; ++i) Bt[buf][(t & 15) * kSplitKP + (t >> 4) + 16 * i] = lb[i];
-  };
-
   float acc = 0.0f;
-  const int chunks = static_cast<int>((K + kSplitKC - 1) / kSplitKC);
-  if (chunks > 0) {
-    load_chunk(0);
-    store_chunk(0);
-  }
-  __syncthreads();
-  constexpr int KQ = kSplitKC / 4;  // k per wave and chunk
-  for (int ch = 0; ch < chunks; ++ch) {
-    const int buf = ch & 1;
-    if (ch + 1 < chunks) load_chunk(static_cast<int64_t>(ch + 1) * kSplitKC);
-    const int kn = static_cast<int>(min<int64_t>(kSplitKC, K - static_cast<int64_t>(ch) * kSplitKC));
-    const int q0 = wave * KQ;
-    const int qn = max(0, min(KQ, kn - q0));
-    const float* ar = &As[buf][r * kSplitKP + q0];
-    const float* br = &Bt[buf][c * kSplitKP + q0];
-    int kk = 0;
-    for (; kk + 4 <= qn; kk += 4) {
-      const float4 a = *reinterpret_cast<const float4*>(ar + kk);
-      const float4 b = *reinterpret_cast<const float4*>(br + kk);
-      acc = acc + a.x * b.x;
-      acc = acc + a.y * b.y;
-      acc = acc + a.z * b.z;
-      acc = acc + a.w * b.w;
+  for (int64_t k0 = 0; k0 < K; k0 += kSplitKC) {
+    const int kn = static_cast<int>(min<int64_t>(kSplitKC, K - k0));
+    if (k0 > 0) __syncthreads();  // the previous chunk has been read
+    for (int i = t; i < kSplitTM * kn; i += NT) {
+      const int row = i / kn, kk = i - row * kn;
+      As[row * kSplitKP + kk] = (m0 + row < M) ? Io<T>::load(A[(m0 + row) * args.lda + k0 + kk]) : 0.0f;
     }
-    for (; kk < qn; ++kk) acc = acc + ar[kk] * br[kk];
-    if (ch + 1 < chunks) store_chunk(buf ^ 1);
+    for (int i = t; i < kSplitTN * kn; i += NT) {
+      const int kk = i >> 4, cc = i & 15;
+      Bt[cc * kSplitKP + kk] = (n0 + cc < N) ? Io<T>::load(B[(k0 + kk) * args.ldb + n0 + cc]) : 0.0f;
+    }
     __syncthreads();
+    const int per = (kn + kSplitWaves - 1) / kSplitWaves;
+    const int q0 = wave * per;
+    const int qn = max(0, min(per, kn - q0));
+    const float* ar = &As[r * kSplitKP + q0];
+    const float* br = &Bt[c * kSplitKP + q0];
+    for (int kk = 0; kk < qn; ++kk) acc = acc + ar[kk] * br[kk];
   }
   part[wave][lane] = acc;
   __syncthreads();
   if (t < kSplitTM * kSplitTN) {
     const int64_t row = m0 + (t >> 4), col = n0 + (t & 15);
-    if (row < M && col < N) {
-      const float sum = ((part[0][t] + part[1][t]) + part[2][t]) + part[3][t];
-      float v = Io<T>::round(sum);
-      const int64_t idx = row * args.ldc + col;
-      if (args.ep.nseg > 0) v = epilogue_one<T>(args.ep, v, idx);
-      C[idx] = Io<T>::store(v);
+    const bool live = row < M && col < N;
+    float sum = part[0][t];
+#pragma unroll
+    for (int w = 1; w < kSplitWaves; ++w) sum = sum + part[w][t];
+    float v = Io<T>::round(sum);
+    const int64_t idx = row * args.ldc + col;
+    if (live && args.ep.nseg > 0) v = epilogue_one<T>(args.ep, v, idx);
+    if (args.row_softmax) {  // N <= 16: the row's outputs are the 16 lanes of this lane's group
+      float m = live ? v : -__builtin_inff();
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) {
+        const float other = __shfl_xor(m, o, 16);
+        m = (other > m) ? other : m;
+      }
+      const float e = live ? expf(v - m) : 0.0f;
+      float s = e;
+#pragma unroll
+      for (int o = 8; o > 0; o >>= 1) s += __shfl_xor(s, o, 16);
+      v = e / s;
     }
+    if (live) C[idx] = Io<T>::store(v);
   }
 }
 
@@ -488,11 +476,15 @@ fh_status dispatch_gemm(GemmArgs args, int64_t batch, hipStream_t stream) {
                        ((args.stride_a * esz) % 16 == 0) && ((args.stride_b * esz) % 16 == 0) &&
                        (reinterpret_cast<uintptr_t>(args.C) % 16 == 0) && (args.ldc % E == 0) &&
                        ((args.stride_c * esz) % 16 == 0) && epilogue_aligned(args.ep);
-  if (small && args.any_order && !args.trans_a && !args.trans_b && (args.M + kSplitTM - 1) / kSplitTM <= 65535 &&
-      batch <= 65535) {
+  const bool split_ok = args.any_order && !args.trans_a && !args.trans_b &&
+                        (args.M + kSplitTM - 1) / kSplitTM <= 65535 && batch <= 65535;
+  if (args.row_softmax && (!split_ok || args.N > kSplitTN))
+    return fail(FH_INVALID_ARGUMENT, "fh_gemm_ex: FH_GEMM_ROW_SOFTMAX needs FH_GEMM_ANY_ORDER, N <= 16 and at most "
+                                     "262,140 rows");
+  if ((small || args.row_softmax) && split_ok) {
     dim3 grid(static_cast<uint32_t>((args.N + kSplitTN - 1) / kSplitTN),
               static_cast<uint32_t>((args.M + kSplitTM - 1) / kSplitTM), static_cast<uint32_t>(batch));
-    hipLaunchKernelGGL((gemm_split_kernel<T>), grid, dim3(256), 0, stream, args);
+    hipLaunchKernelGGL((gemm_split_kernel<T>), grid, dim3(kSplitWaves * 64), 0, stream, args);
     return launch_status("gemm_split_kernel launch");
   }
   // small problems, or operands the tile kernels cannot take
@@ -546,7 +538,8 @@ fh_status copy_epilogue(const fh_epilogue* in, EpilogueArgs& out) {
 
 fh_status gemm_with_epilogue_args(int32_t dtype, const void* A, const void* B, void* C, int64_t M, int64_t N,
                                   int64_t K, const fh_epilogue* epilogue, hipStream_t stream, int32_t flags) {
-  if ((flags & ~FH_GEMM_ANY_ORDER) != 0) return fail(FH_INVALID_ARGUMENT, "fh_gemm_ex: unknown flags " + std::to_string(flags));
+  if ((flags & ~(FH_GEMM_ANY_ORDER | FH_GEMM_ROW_SOFTMAX)) != 0)
+    return fail(FH_INVALID_ARGUMENT, "fh_gemm_ex: unknown flags " + std::to_string(flags));
   if (!is_supported_float(dtype)) return fail(FH_UNIMPLEMENTED, "fh_gemm: unsupported dtype");
   if (M < 0 || N < 0 || K < 0) return fail(FH_INVALID_ARGUMENT, "fh_gemm: negative dimension");
   if (M == 0 || N == 0) return FH_OK;
@@ -564,6 +557,7 @@ fh_status gemm_with_epilogue_args(int32_t dtype, const void* A, const void* B, v
   args.ldb = N;
   args.ldc = N;
   args.any_order = (flags & FH_GEMM_ANY_ORDER) != 0;
+  args.row_softmax = (flags & FH_GEMM_ROW_SOFTMAX) != 0;
   fh_status st = copy_epilogue(epilogue, args.ep);
   if (st != FH_OK) return st;
   return run_gemm(dtype, args, 1, stream);

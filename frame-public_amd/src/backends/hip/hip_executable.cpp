@@ -19,6 +19,8 @@
 //  * grouped GEMMs (opt_level >= 1): 16-bit matmuls (fused or not) that read the same A with equal B shapes,
 // output types and epilogue programs (the Q/K/V projections of an attention block) become one grouped node
 // launched as one kernel (see lower_grouped_gemms).
+//  * GEMM + softmax (opt_level >= 1): a softmax over the rows of a fused matmul of at most 16 columns runs in
+// the GEMM's launch (see lower_gemm_softmax).
 //  * channels-last conv (every opt_level): a conv that the MFMA implicit-GEMM path accepts becomes
 // channels_last(x), channels_last(w) and conv2d_nhwc (see lower_convs); activations whose every use takes
 // channels-last data stay channels-last between convs (see plan_channels_last).
@@ -1181,6 +1183,34 @@ Status lower_scaled_adds(ir::Graph& g) {
   return Status::ok();
 }
 
+// A softmax whose input is a fused matmul (any_order) of at most 16 columns, used by nothing else, runs in that
+// GEMM's launch: the matmul node gets row_softmax = 1 (fh_gemm_ex with FH_GEMM_ROW_SOFTMAX) and the softmax node
+// goes. C1's classifier layer (matmul, bias add, softmax over 10 classes) becomes one kernel.
+Status lower_gemm_softmax(ir::Graph& g) {
+  std::unordered_map<const ir::Value*, int> uses;
+  for (const ir::Node* n : g.topological_order())
+    for (const ir::Value* v : n->inputs()) ++uses[v];
+  for (const ir::Value* v : g.outputs()) uses[v] += 1000;
+  const std::vector<ir::Node*> snapshot = g.topological_order();
+  for (ir::Node* sm : snapshot) {
+    if (sm->op() != "softmax" || sm->inputs().size() != 1 || sm->outputs().size() != 1) continue;
+    ir::Value* v = sm->inputs()[0];
+    ir::Node* p = v->producer();
+    if (p == nullptr || p->op() != kGemmEpilogueOp || uses[v] != 1) continue;
+    const auto* any = attr_of<int64_t>(p, "any_order");
+    const auto* n_main = attr_of<int64_t>(p, "n_main_inputs");
+    if (any == nullptr || *any == 0 || n_main == nullptr || *n_main != 2) continue;
+    const ir::TensorType& ot = p->outputs()[0].type();
+    if (ot.shape.rank() != 2 || ot.shape.dim(1) > 16 || ot.shape.dim(0) > 262140) continue;
+    const ir::TensorType& st = sm->outputs()[0].type();
+    if (!(ot.shape == st.shape) || !(ot.dtype == st.dtype)) continue;
+    p->set_attr("row_softmax", ir::AttrValue{int64_t{1}});
+    FRAME_RETURN_IF_ERROR(g.replace_all_uses(sm->output(0), p->output(0)));
+    FRAME_RETURN_IF_ERROR(g.erase_node(sm));
+  }
+  return Status::ok();
+}
+
 // Matmuls (plain, or epilogue nodes with two main inputs) of a 16-bit dtype that read the same A value, with equal
 // B shapes, output types and epilogue programs, merged in groups of up to FH_GEMM_MAX_GROUPS into one
 // kGemmGroupedOp node, when every operand of the group is produced before the group's first member (so the
@@ -1204,7 +1234,7 @@ Status lower_grouped_gemms(ir::Graph& g) {
     const bool mm = n->op() == "matmul" && n->inputs().size() == 2;
     const auto* n_main = attr_of<int64_t>(n, "n_main_inputs");
     const bool epi = n->op() == kGemmEpilogueOp && n_main != nullptr && *n_main == 2;
-    if ((!mm && !epi) || n->outputs().size() != 1) continue;
+    if ((!mm && !epi) || n->outputs().size() != 1 || attr_of<int64_t>(n, "row_softmax") != nullptr) continue;
     const ir::TensorType& ot = n->outputs()[0].type();
     if (ot.dtype.code() != DTypeCode::kBFloat16 && ot.dtype.code() != DTypeCode::kFloat16) continue;
     const ir::TensorType& bt = n->inputs()[1]->type();
@@ -1252,6 +1282,7 @@ Result<ir::Graph> lower_for_hip(const ir::Graph& graph, int32_t opt_level) {
   // Attention runs at every level (like the conv lowering), before the epilogue fusion would claim its matmuls.
   FRAME_RETURN_IF_ERROR(lower_attention(work.value()));
   if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_epilogues(work.value()));
+  if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_gemm_softmax(work.value()));
   if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_grouped_gemms(work.value()));
   if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_scaled_adds(work.value()));
   // Channels-last conv lowering runs at every level, so the conv numerics do not depend on the level.

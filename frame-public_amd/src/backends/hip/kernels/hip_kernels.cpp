@@ -146,7 +146,9 @@ Status gemm_impl(KernelContext& ctx, const std::string& op, size_t n_main) {
   Result<fh_epilogue> ep = make_epilogue(ctx, op, n_main);
   if (!ep.is_ok()) return ep.status();
   const auto* any = attr<int64_t>(ctx, "any_order");
-  const int32_t flags = (any != nullptr && *any != 0) ? FH_GEMM_ANY_ORDER : 0;
+  const auto* row_softmax = attr<int64_t>(ctx, "row_softmax");
+  const int32_t flags = ((any != nullptr && *any != 0) ? FH_GEMM_ANY_ORDER : 0) |
+                        ((row_softmax != nullptr && *row_softmax != 0) ? FH_GEMM_ROW_SOFTMAX : 0);
   FRAME_HIP_RETURN_IF_ERROR(fh_gemm_ex(dt.value(), a.raw_data(), b.raw_data(), c.raw_data(), m, n, k,
                                        ep.value().nseg > 0 ? &ep.value() : nullptr, flags, stream_handle(ctx)),
                             "op '" + op + "' (hip)");

@@ -132,6 +132,10 @@ fh_status fh_gemm(int32_t dtype, const void* A, const void* B, void* C, int64_t 
  * opt_level >= 1, where results are checked within tolerance rather than bit for bit); small problems then run
  * a split-k kernel instead of the sequential-order one. No reference counterpart beyond fh_gemm's. */
 #define FH_GEMM_ANY_ORDER 1
+/* FH_GEMM_ROW_SOFTMAX (with FH_GEMM_ANY_ORDER, N <= 16): every output row, after the epilogue and its rounding,
+ * goes through softmax in the same launch (HipBackend::compile fuses a softmax that reads such a GEMM, e.g. C1's
+ * classifier layer; the reference runs softmax as its own op, reference: src/backends/cpu/kernels/sequence.cpp:111-160). */
+#define FH_GEMM_ROW_SOFTMAX 2
 fh_status fh_gemm_ex(int32_t dtype, const void* A, const void* B, void* C, int64_t M, int64_t N, int64_t K,
                      const fh_epilogue* epilogue, int32_t flags, void* stream);
 

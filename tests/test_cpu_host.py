@@ -348,9 +348,26 @@ def test_grouping_skips_members_that_depend_on_each_other():
 
 
 def test_small_fused_gemms_are_marked_any_order_only_above_opt0():
+    # C1 at opt_level 1: two fused GEMMs that may reassociate k, the classifier's softmax folded into the second
     g = graphs.mlp(64, 0)
-    assert host.hip_lowered(g.text(), 1).count("any_order=1") == 2
-    assert "any_order" not in host.hip_lowered(g.text(), 0)
+    out = host.hip_lowered(g.text(), 1)
+    assert out.count("any_order=1") == 2 and out.count("row_softmax=1") == 1 and "softmax(" not in out, out
+    out0 = host.hip_lowered(g.text(), 0)
+    assert "any_order" not in out0 and "row_softmax" not in out0 and "softmax(" in out0
+
+
+def test_softmax_fold_needs_a_narrow_single_use_gemm():
+    def build(n, extra_use):
+        g = graphs.Graph("hip")
+        x, w, b = g.input(0, (8, 32)), g.input(0, (32, n)), g.input(0, (8, n))
+        y = g.add(g.matmul(x, w), b)
+        g.output(g.softmax(y))
+        if extra_use:
+            g.output(y)
+        return host.hip_lowered(g.text(), 1)
+    assert "row_softmax=1" in build(16, False)
+    assert "row_softmax" not in build(17, False)  # wider than one split-k tile
+    assert "row_softmax" not in build(10, True)   # the GEMM result is also a graph output
 
 
 def test_gemm_grouped_and_ex_argument_checks():

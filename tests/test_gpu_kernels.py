@@ -223,6 +223,33 @@ def test_gemm_split_k_matches_oracle(hip, dtype, shape):
     assert_bitwise(fused, run_ew(hip, dtype, [1, 3], [2, 1], [got, bias]), "split-k epilogue vs separate program")
 
 
+@pytest.mark.parametrize("dtype", [F32, BF16, F16])
+@pytest.mark.parametrize("shape", [(64, 256, 10), (7, 40, 16), (300, 1500, 3)])
+def test_gemm_row_softmax(hip, dtype, shape):
+    """FH_GEMM_ROW_SOFTMAX: the split-k GEMM with its bias epilogue, then softmax over each row, in one launch;
+    against the split-k GEMM alone followed by the oracle's softmax (and the oracle end to end)."""
+    m, k, n = shape
+    say(f"gemm + row softmax dtype={dtype} m={m} k={k} n={n}")
+    a = synth.tensor(91, (m, k), dtype, "normal")
+    b = synth.tensor(92, (k, n), dtype, "normal", 0.1)
+    bias = synth.tensor(93, (m, n), dtype, "normal")
+    fused = run_gemm_ex(hip, dtype, a, b, [(hip.EW_ADD, bias)], flags=3)
+    logits = run_gemm_ex(hip, dtype, a, b, [(hip.EW_ADD, bias)], flags=1)
+    assert_close(fused, orc.softmax(dtype, logits), dtype, what="fused softmax vs softmax of the same logits")
+    want = orc.softmax(dtype, orc.ew_program(dtype, [1], [2], [orc.matmul(dtype, a, b), bias]))
+    assert_close(fused, want, dtype, what="gemm + bias + softmax vs oracle")
+
+
+def test_gemm_row_softmax_argument_checks(hip):
+    a = dev(hip, np.zeros((8, 32), np.float32))
+    b = dev(hip, np.zeros((32, 17), np.float32))
+    c = hip.DeviceBuffer(8 * 17 * 4)
+    lib = hip.lib()
+    assert lib.fh_gemm_ex(F32, a.value, b.value, c.value, 8, 17, 32, None, 3, None) == 1  # N > 16
+    assert lib.fh_gemm_ex(F32, a.value, b.value, c.value, 8, 16, 32, None, 2, None) == 1  # without any-order
+    assert b"FH_GEMM_ROW_SOFTMAX" in lib.fh_last_error()
+
+
 def run_gemm_grouped(hip, dtype, a, bs, biases):
     m, k = a.shape
     n = bs[0].shape[1]

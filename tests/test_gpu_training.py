@@ -253,9 +253,11 @@ def test_mlp_training_step(dev, dtype):
     want = orc.run_graph_cpu(text.replace("@hip:0", "@cpu:0"), ins)
     check_outputs(got, want, dtype, "mlp training")
     if dtype == F32:
-        # below the tiled threshold every GEMM keeps the reference's order: the gradients are bit-exact
+        # at opt_level 0 every GEMM below the tiled threshold keeps the reference's order: the gradients are
+        # bit-exact (opt_level 1 lets the forward's fused small GEMMs reassociate k, checked within tolerance above)
+        got0 = host.compile(text, "hip", 0).run(ins)
         for i in range(1, 5):
-            assert_bitwise(got[i], want[i], f"mlp gradient {i}")
+            assert_bitwise(got0[i], want[i], f"mlp gradient {i} at opt_level 0")
 
 
 @pytest.mark.parametrize("dtype", [F32, BF16])
