@@ -515,6 +515,7 @@ struct ConvHaloArgs {
   int32_t p_loads;     // 1 KB LDS-DMA loads that fill the patch positions this geometry needs
   int32_t rows_total;  // N * H: global input rows
   int32_t tiles;       // tiles_m * tiles_n
+  int32_t patch_rows;  // rows of the patch a BN-pixel tile reads (NCHW input fill)
 };
 
 constexpr int kHaloPatchBytes = 30 * 1024;
@@ -816,8 +817,14 @@ __device__ __forceinline__ void conv_store_tile_wg_nhwc(const ConvNhwcArgs& args
 // Single-buffered variant: one tile per workgroup, each (chunk) step loaded, waited for and multiplied in turn,
 // 66 KB of LDS, so two workgroups share a CU and each one's loads, barriers and epilogue overlap the other's
 // multiplications (the persistent kernel above keeps one workgroup per CU and has nothing to overlap them with).
-template <typename T, int BN, int E>
-__global__ __launch_bounds__(512, 2) void conv_halo1_kernel(ConvHaloArgs ha) {
+//
+// NCHW_IN: x is NCHW [N][Cin][H][W] (W % 8 == 0), the layout a graph input arrives in, so no channels-last copy of
+// the activations is made first. The patch of a chunk is then filled through registers: a thread takes 8
+// channels x 8 consecutive pixels of one patch row (8 loads of 16 bytes, one per channel plane), transposes the
+// 8 x 8 block of 16-bit values in registers, and writes 8 positions' 16-byte chunks of the channels-last patch;
+// other threads zero the two padding positions of every row. Everything after the patch fill is unchanged.
+template <typename T, int BN, int E, bool NCHW_IN>
+__global__ __launch_bounds__(512, 4) void conv_halo1_kernel(ConvHaloArgs ha) {
   const ConvNhwcArgs& args = ha.c;
   using S = typename Io<T>::storage;
   static_assert(sizeof(S) == 2, "16-bit operands");
@@ -879,19 +886,64 @@ __global__ __launch_bounds__(512, 2) void conv_halo1_kernel(ConvHaloArgs ha) {
     const bool ok = gi >= 0 && gi < ha.rows_total && c >= 1 && c <= W;
     p_src[i] = ok ? (gi * W + c - 1) * cin + gch * 8 : -1;
   }
+  // NCHW_IN: this thread's 8 x 8 block (patch row nr, 8-channel group ncg of the chunk, 8-pixel group npg) or
+  // padding position. Recomputed at every chunk from an opaque copy of the thread id, so none of it stays live
+  // (in registers) across the multiply loop, which keeps the kernel within 128 VGPRs (two workgroups per CU).
+  auto fill_nchw = [&](int ci0) {
+    int tq = tid;
+    asm volatile("" : "+v"(tq));
+    const int pgroups = W / 8;
+    const int blocks = ha.patch_rows * 4 * pgroups;
+    const int nr = tq / (4 * pgroups), ncg = tq % 4, npg = (tq / 4) % pgroups;
+    const int ngi = gi_lo + nr;
+    const bool nblock = tq < blocks && ngi >= 0 && ngi < ha.rows_total;
+    const S* __restrict__ Xn = static_cast<const S*>(args.x);
+    const int64_t plane = static_cast<int64_t>(H) * W;
+    const int64_t nsrc =
+        nblock ? ((static_cast<int64_t>(ngi / H) * cin + 8 * ncg + ci0) * H + ngi % H) * W + 8 * npg : 0;
+    if (tq < blocks) {
+      uint4 v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        v[e] = uint4{0, 0, 0, 0};
+        if (nblock) v[e] = *reinterpret_cast<const uint4*>(Xn + nsrc + e * plane);
+      }
+      // o[i] = the 8 channels of pixel i: dword k holds channels 2k (low half) and 2k + 1 (high half)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        uint32_t d[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          const uint32_t lo = reinterpret_cast<const uint32_t*>(&v[2 * k])[i / 2];
+          const uint32_t hi = reinterpret_cast<const uint32_t*>(&v[2 * k + 1])[i / 2];
+          d[k] = (i % 2 == 0) ? ((lo & 0xffffu) | (hi << 16)) : ((lo >> 16) | (hi & 0xffff0000u));
+        }
+        const int q = nr * rw + 1 + 8 * npg + i;
+        *reinterpret_cast<uint4*>(lds + A_CHUNK + q * 64 + ((ncg ^ ((q >> 2) & 3)) * 16)) = uint4{d[0], d[1], d[2], d[3]};
+      }
+    } else if (tq < blocks + ha.patch_rows * 8) {  // the padding positions (columns 0 and W + 1), 4 chunks each
+      const int z = tq - blocks;
+      const int q = (z >> 3) * rw + ((z >> 2) & 1) * (W + 1);
+      *reinterpret_cast<uint4*>(lds + A_CHUNK + q * 64 + (z & 3) * 16) = uint4{0, 0, 0, 0};
+    }
+  };
   auto issue_step = [&](int ci0) {
 #pragma unroll
     for (int i = 0; i < A_PER_WAVE; ++i) {
       const int j = wave + NW * i;
       if (j < A_LOADS) global_to_lds16(Wt + a_src[i] + ci0, (FH_LDS void*)(lds + j * 1024));
     }
+    if constexpr (NCHW_IN) {
+      fill_nchw(ci0);
+    } else {
 #pragma unroll
-    for (int i = 0; i < P_PER_WAVE; ++i) {
-      const int j = wave + NW * i;
-      if (j < ha.p_loads) {
-        const uint32_t voff = p_src[i] >= 0 ? static_cast<uint32_t>(p_src[i] + ci0) * 2u : 0x80000000u;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (FH_LDS void*)(lds + A_CHUNK + j * 1024), 16,
-                                                 static_cast<int>(voff), 0, 0, 0);
+      for (int i = 0; i < P_PER_WAVE; ++i) {
+        const int j = wave + NW * i;
+        if (j < ha.p_loads) {
+          const uint32_t voff = p_src[i] >= 0 ? static_cast<uint32_t>(p_src[i] + ci0) * 2u : 0x80000000u;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (FH_LDS void*)(lds + A_CHUNK + j * 1024), 16,
+                                                   static_cast<int>(voff), 0, 0, 0);
+        }
       }
     }
   };
@@ -979,7 +1031,7 @@ __global__ __launch_bounds__(512, 2) void conv_halo1_kernel(ConvHaloArgs ha) {
 
 // Whether the resident-patch kernel takes this geometry: patch rows of a BN-pixel tile (at most (BN - 1) / W + 2
 // output rows plus the two halo rows) must fit kHaloPatchBytes; p_loads = the 1 KB loads that fill them.
-bool halo_supported(int32_t dtype, const int64_t* g, int bn, int32_t* p_loads) {
+bool halo_supported(int32_t dtype, const int64_t* g, int bn, int32_t* p_loads, int32_t* patch_rows = nullptr) {
   if (dtype != FH_BF16 && dtype != FH_F16) return false;
   if (g[11] != 1 || g[5] != 3 || g[6] != 3 || g[7] != 1 || g[8] != 1 || g[9] != 1 || g[10] != 1) return false;
   if (g[1] % 32 != 0 || g[2] < 1 || g[3] < 1 || g[4] < 1 || g[4] > 512) return false;
@@ -989,16 +1041,26 @@ bool halo_supported(int32_t dtype, const int64_t* g, int bn, int32_t* p_loads) {
   // 32-bit element offsets: the whole input, the filter
   if (g[0] * g[2] * g[3] * g[1] >= (int64_t{1} << 30) || g[4] * 9 * g[1] >= (int64_t{1} << 30)) return false;
   if (p_loads != nullptr) *p_loads = static_cast<int32_t>((positions + 15) / 16);
+  if (patch_rows != nullptr) *patch_rows = static_cast<int32_t>(rows);
   return true;
 }
 
-template <typename T, int BN>
+// NCHW input for the single-buffered kernel: whole 8-pixel groups per row, and one thread per 8 x 8 block plus
+// the padding positions.
+bool halo_nchw_supported(int32_t dtype, const int64_t* g) {
+  int32_t loads = 0, rows = 0;
+  if (!halo_supported(dtype, g, 128, &loads, &rows) || g[3] % 8 != 0) return false;
+  return rows * 4 * (g[3] / 8) + rows * 8 <= 512;
+}
+
+template <typename T, int BN, bool NCHW_IN = false>
 fh_status launch_halo1(ConvHaloArgs a, hipStream_t stream) {
   a.c.tiles_m = (a.c.cout + 63) / 64;
   a.c.tiles_n = static_cast<int32_t>((a.c.p + BN - 1) / BN);
   a.tiles = a.c.tiles_m * a.c.tiles_n;
   return with_epi<conv_epi_mask<T, false>()>(epi_kind(a.c.ep), [&]<int E>() {
-    hipLaunchKernelGGL((conv_halo1_kernel<T, BN, E>), dim3(static_cast<uint32_t>(a.tiles)), dim3(512), 0, stream, a);
+    hipLaunchKernelGGL((conv_halo1_kernel<T, BN, E, NCHW_IN>), dim3(static_cast<uint32_t>(a.tiles)), dim3(512), 0,
+                       stream, a);
     return launch_status("conv_halo1_kernel launch");
   });
 }
@@ -1028,25 +1090,31 @@ fh_status launch_halo(ConvHaloArgs a, hipStream_t stream) {
 // Single-buffered tiles: 256 pixels when that still makes 1.5 workgroups per CU slot pair, else 128; persistent:
 // 256 when the tiles fill the device 1.5 times over, else 128.
 template <typename T>
-fh_status dispatch_halo(const ConvNhwcArgs& c, const int64_t* geom, hipStream_t stream, bool* launched) {
+fh_status dispatch_halo(const ConvNhwcArgs& c, const int64_t* geom, hipStream_t stream, bool* launched,
+                        bool nchw_in = false) {
   *launched = false;
-  if (c.out_nhwc && c.cout > 256) return FH_OK;
+  if (c.out_nhwc && c.cout > 256 && !nchw_in) return FH_OK;
   const int64_t cus = device_cu_count();
   const int64_t tiles_m = (c.cout + 63) / 64;
-  const bool persistent = c.out_nhwc && c.cout <= 64;
+  const bool persistent = c.out_nhwc && c.cout <= 64 && !nchw_in;
   ConvHaloArgs a{};
   a.c = c;
   a.rw = c.w_in + 2;
   a.rows_total = static_cast<int32_t>(geom[0] * geom[2]);
-  int32_t loads = 0;
-  if (2 * tiles_m * ((c.p + 255) / 256) >= 3 * cus && halo_supported(FH_BF16, geom, 256, &loads)) {
+  int32_t loads = 0, rows = 0;
+  if (2 * tiles_m * ((c.p + 255) / 256) >= 3 * cus && halo_supported(FH_BF16, geom, 256, &loads, &rows) &&
+      (!nchw_in || rows * 4 * (geom[3] / 8) + rows * 8 <= 512)) {
     a.p_loads = loads;
+    a.patch_rows = rows;
     *launched = true;
+    if (nchw_in) return launch_halo1<T, 256, true>(a, stream);
     return persistent ? launch_halo<T, 256>(a, stream) : launch_halo1<T, 256>(a, stream);
   }
-  if (halo_supported(FH_BF16, geom, 128, &loads)) {
+  if (halo_supported(FH_BF16, geom, 128, &loads, &rows)) {
     a.p_loads = loads;
+    a.patch_rows = rows;
     *launched = true;
+    if (nchw_in) return launch_halo1<T, 128, true>(a, stream);
     return persistent ? launch_halo<T, 128>(a, stream) : launch_halo1<T, 128>(a, stream);
   }
   return FH_OK;
@@ -1333,6 +1401,10 @@ extern "C" int32_t fh_conv2d_nhwc_supported(int32_t dtype, const int64_t geom[12
   return geom != nullptr && nhwc_supported(dtype, geom) ? 1 : 0;
 }
 
+extern "C" int32_t fh_conv2d_nchw_in_supported(int32_t dtype, const int64_t geom[12]) {
+  return geom != nullptr && nhwc_supported(dtype, geom) && halo_nchw_supported(dtype, geom) ? 1 : 0;
+}
+
 extern "C" fh_status fh_conv2d_nhwc_fwd_ex(int32_t dtype, const void* x_nhwc, const void* w_khwc, const void* bias,
                                            void* y, const int64_t geom[12], const fh_epilogue* epilogue,
                                            int32_t flags, void* stream);
@@ -1345,9 +1417,14 @@ extern "C" fh_status fh_conv2d_nhwc_fwd(int32_t dtype, const void* x_nhwc, const
 extern "C" fh_status fh_conv2d_nhwc_fwd_ex(int32_t dtype, const void* x_nhwc, const void* w_khwc, const void* bias,
                                            void* y, const int64_t geom[12], const fh_epilogue* epilogue,
                                            int32_t flags, void* stream) {
-  if ((flags & ~(FH_CONV_OUT_NHWC | FH_CONV_IMPLICIT_GEMM)) != 0)
+  if ((flags & ~(FH_CONV_OUT_NHWC | FH_CONV_IMPLICIT_GEMM | FH_CONV_IN_NCHW)) != 0)
     return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd_ex: unknown flags");
   if (geom == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd: null geometry");
+  const bool nchw_in = (flags & FH_CONV_IN_NCHW) != 0;
+  if (nchw_in && ((flags & FH_CONV_IMPLICIT_GEMM) != 0 || !halo_nchw_supported(dtype, geom)))
+    return fail(FH_UNIMPLEMENTED, "fh_conv2d_nhwc_fwd_ex: FH_CONV_IN_NCHW needs the resident-patch geometry (bf16/f16, "
+                                  "3x3, stride 1, padding 1, groups 1, Cin % 32 == 0, W % 8 == 0, a patch of at most "
+                                  "30 KB) and excludes FH_CONV_IMPLICIT_GEMM");
   if (!nhwc_supported(dtype, geom))
     return fail(FH_UNIMPLEMENTED, "fh_conv2d_nhwc_fwd: geometry or dtype not supported by the channels-last path "
                                   "(needs groups 1 and bf16/f16 with Cin % 32 == 0 or Cin == 8, or fp32 with "
@@ -1403,9 +1480,10 @@ extern "C" fh_status fh_conv2d_nhwc_fwd_ex(int32_t dtype, const void* x_nhwc, co
   hipStream_t s = static_cast<hipStream_t>(stream);
   if ((dtype == FH_BF16 || dtype == FH_F16) && !c8 && (flags & FH_CONV_IMPLICIT_GEMM) == 0) {
     bool launched = false;
-    const fh_status st = dtype == FH_BF16 ? dispatch_halo<bf16_t>(a, geom, s, &launched)
-                                          : dispatch_halo<f16_t>(a, geom, s, &launched);
+    const fh_status st = dtype == FH_BF16 ? dispatch_halo<bf16_t>(a, geom, s, &launched, nchw_in)
+                                          : dispatch_halo<f16_t>(a, geom, s, &launched, nchw_in);
     if (launched || st != FH_OK) return st;
+    if (nchw_in) return fail(FH_INTERNAL, "fh_conv2d_nhwc_fwd_ex: NCHW input accepted but no kernel launched");
   }
   if (dtype == FH_F32) return dispatch_conv<float, false>(a, s);
   if (c8) return dtype == FH_BF16 ? dispatch_conv<bf16_t, true>(a, s) : dispatch_conv<f16_t, true>(a, s);

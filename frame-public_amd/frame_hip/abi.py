@@ -64,6 +64,7 @@ _SIGS = {
     "fh_event_elapsed_ms": (c_int32, [c_void_p, c_void_p, POINTER(c_float)]),
     "fh_gemm": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, POINTER(Epilogue),
                           c_void_p]),
+    "fh_conv2d_nchw_in_supported": (c_int32, [c_int32, POINTER(c_int64)]),
     "fh_gemm_ex": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, POINTER(Epilogue),
                              c_int32, c_void_p]),
     "fh_gemm_grouped": (c_int32, [c_int32, c_void_p, c_int32, POINTER(c_void_p), POINTER(c_void_p), c_int64, c_int64,

@@ -123,6 +123,13 @@ Status lower_epilogues(ir::Graph& g) {
   return Status::ok();
 }
 
+int32_t conv_dtype_code(const ir::TensorType& t) {
+  return t.dtype.code() == DTypeCode::kBFloat16  ? FH_BF16
+         : t.dtype.code() == DTypeCode::kFloat16 ? FH_F16
+         : t.dtype.code() == DTypeCode::kFloat32 ? FH_F32
+                                                 : -1;
+}
+
 // Whether the channels-last MFMA path takes conv node `n` (conv2d or conv epilogue), with its geometry
 // {N, Cin, H, W, Cout, KH, KW, sh, sw, ph, pw, groups} and whether it goes through the C8 layout (Cin <= 8, 16-bit).
 struct ConvLowering {
@@ -522,6 +529,7 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
       const int64_t* geom = p.geom;
       ir::Value* x_cl = nullptr;
       ir::Value* w_cl = nullptr;
+      bool in_nchw = false;
       if (p.c8) {
         ir::TensorType tx = ins[0]->type(), tw = ins[1]->type();
         tx.shape = Shape({geom[0], geom[2], geom[3], 8});
@@ -536,6 +544,9 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
         if (!batched_emitted) FRAME_RETURN_IF_ERROR(emit_batched());
         if (nhwc.count(n->inputs()[0])) {
           x_cl = ins[0];  // already channels-last
+        } else if (fh_conv2d_nchw_in_supported(conv_dtype_code(ins[0]->type()), geom) != 0) {
+          x_cl = ins[0];  // NCHW, read by the resident-patch kernel itself (FH_CONV_IN_NCHW)
+          in_nchw = true;
         } else {
           Result<ir::Value*> xv = channels_last(ins[0]);
           if (!xv.is_ok()) return xv.status();
@@ -556,6 +567,7 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
       if (!c.is_ok()) return c.status();
       for (const auto& [k, v] : n->attrs()) c.value()->set_attr(k, v);
       if (nhwc.count(&n->outputs()[0])) c.value()->set_attr("out_nhwc", ir::AttrValue{int64_t{1}});
+      if (in_nchw) c.value()->set_attr("in_nchw", ir::AttrValue{int64_t{1}});
       if (n->op() == "conv2d") c.value()->set_attr("n_main_inputs", ir::AttrValue{static_cast<int64_t>(ins.size())});
       c.value()->set_attr("filter_hw", ir::AttrValue{std::vector<int64_t>{geom[5], geom[6]}});
       map[&n->outputs()[0]] = c.value()->output(0);

@@ -242,7 +242,9 @@ Result<bool> conv_via_channels_last(const KernelContext& ctx, const std::string&
   hal::Allocator* alloc = be.value()->allocator(ctx.device);
   if (alloc == nullptr) return Status::make(ErrorCode::kInternal, "op '" + op + "' (hip): no allocator for the device");
   const int64_t n = geom[0], cin = geom[1], h = geom[2], wd = geom[3], cout = geom[4], kh = geom[5], kw = geom[6];
-  Result<Tensor> xt = Tensor::empty(Shape({n, h, wd, c8 ? 8 : cin}), x.dtype(), ctx.device, *alloc);
+  // the resident-patch kernel reads NCHW activations itself where the geometry allows; otherwise a channels-last copy
+  const bool nchw_in = !c8 && fh_conv2d_nchw_in_supported(dt, g) != 0;
+  Result<Tensor> xt = Tensor::empty(nchw_in ? Shape({1}) : Shape({n, h, wd, c8 ? 8 : cin}), x.dtype(), ctx.device, *alloc);
   if (!xt.is_ok()) return xt.status();
   Result<Tensor> wt = c8 ? Tensor::empty(Shape({cout, fh_conv_c8_filter_k(kh, kw)}), w.dtype(), ctx.device, *alloc)
                          : Tensor::empty(Shape({cout, kh, kw, cin}), w.dtype(), ctx.device, *alloc);
@@ -256,12 +258,13 @@ Result<bool> conv_via_channels_last(const KernelContext& ctx, const std::string&
                                                      static_cast<int32_t>(kw), s), what);
   } else {
     const int32_t es = static_cast<int32_t>(x.dtype().itemsize());
-    FRAME_HIP_RETURN_IF_ERROR(fh_transpose_batched(es, x.raw_data(), xt.value().raw_data(), n, cin, h * wd, s), what);
+    if (!nchw_in)
+      FRAME_HIP_RETURN_IF_ERROR(fh_transpose_batched(es, x.raw_data(), xt.value().raw_data(), n, cin, h * wd, s), what);
     FRAME_HIP_RETURN_IF_ERROR(fh_transpose_batched(es, w.raw_data(), wt.value().raw_data(), cout, cin, kh * kw, s), what);
   }
-  FRAME_HIP_RETURN_IF_ERROR(fh_conv2d_nhwc_fwd_ex(dt, xt.value().raw_data(), wt.value().raw_data(),
+  FRAME_HIP_RETURN_IF_ERROR(fh_conv2d_nhwc_fwd_ex(dt, nchw_in ? x.raw_data() : xt.value().raw_data(), wt.value().raw_data(),
                                                   bias ? bias->raw_data() : nullptr, ctx.outputs[0].raw_data(), g,
-                                                  ep.nseg > 0 ? &ep : nullptr, 0, s), what);
+                                                  ep.nseg > 0 ? &ep : nullptr, nchw_in ? FH_CONV_IN_NCHW : 0, s), what);
   return true;
 }
 
@@ -329,9 +332,13 @@ Status conv_nhwc_kernel(KernelContext& ctx) {
   if (c8 && (fhw == nullptr || fhw->size() != 2 || x.shape().dim(3) != 8))
     return invalid(op, "C8 filter needs filter_hw and an input with 8 channels");
   const int64_t kh = c8 ? (*fhw)[0] : w.shape().dim(1), kw = c8 ? (*fhw)[1] : w.shape().dim(2);
-  const int64_t geom[12] = {x.shape().dim(0), x.shape().dim(3), x.shape().dim(1), x.shape().dim(2),
-                            w.shape().dim(0), kh,               kw,               (*stride)[0],
-                            (*stride)[1],     (*pad)[0],        (*pad)[1],        *groups};
+  // in_nchw: x is NCHW [N,Cin,H,W] (FH_CONV_IN_NCHW), else channels-last [N,H,W,Cin]
+  const auto* in_nchw_attr = attr<int64_t>(ctx, "in_nchw");
+  const bool in_nchw = in_nchw_attr != nullptr && *in_nchw_attr != 0;
+  if (in_nchw && c8) return invalid(op, "NCHW input with the C8 filter");
+  const int64_t geom[12] = {x.shape().dim(0), x.shape().dim(in_nchw ? 1 : 3), x.shape().dim(in_nchw ? 2 : 1),
+                            x.shape().dim(in_nchw ? 3 : 2), w.shape().dim(0), kh, kw, (*stride)[0],
+                            (*stride)[1], (*pad)[0], (*pad)[1], *groups};
   if (c8 ? w.shape().dim(1) != fh_conv_c8_filter_k(kh, kw) : w.shape().dim(3) != geom[1])
     return invalid(op, "filter shape does not match the input's channels");
   // 16-bit with 8 input channels is the C8 kernel, which reads the packed [Cout, K8] filter only
@@ -348,7 +355,8 @@ Status conv_nhwc_kernel(KernelContext& ctx) {
   if (!ep.is_ok()) return ep.status();
   FRAME_HIP_RETURN_IF_ERROR(fh_conv2d_nhwc_fwd_ex(dt.value(), x.raw_data(), w.raw_data(), bias ? bias->raw_data() : nullptr,
                                                   y.raw_data(), geom, ep.value().nseg > 0 ? &ep.value() : nullptr,
-                                                  out_nhwc ? FH_CONV_OUT_NHWC : 0, stream_handle(ctx)),
+                                                  (out_nhwc ? FH_CONV_OUT_NHWC : 0) | (in_nchw ? FH_CONV_IN_NCHW : 0),
+                                                  stream_handle(ctx)),
                             "op '" + op + "' (hip)");
   return Status::ok();
 }

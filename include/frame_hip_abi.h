@@ -179,6 +179,10 @@ fh_status fh_conv2d_nhwc_fwd(int32_t dtype, const void* x_nhwc, const void* w_kh
  * resident-patch kernel for 3x3 stride-1 convolutions would run; both compute the same sums, so tests use it to
  * cover both kernels on one geometry. */
 #define FH_CONV_IMPLICIT_GEMM 2
+/* FH_CONV_IN_NCHW: x is NCHW [N][Cin][H][W] instead of channels-last (the filter stays [Cout][KH][KW][Cin]); the
+ * resident-patch kernel transposes it on the way into LDS, so a graph-input activation needs no channels-last
+ * copy. Only where fh_conv2d_nchw_in_supported says so. */
+#define FH_CONV_IN_NCHW 4
 fh_status fh_conv2d_nhwc_fwd_ex(int32_t dtype, const void* x_nhwc, const void* w_khwc, const void* bias, void* y,
                                 const int64_t geom[12], const fh_epilogue* epilogue, int32_t flags, void* stream);
 
@@ -187,6 +191,10 @@ fh_status fh_conv2d_nhwc_fwd_ex(int32_t dtype, const void* x_nhwc, const void* w
  * With Cin == 8 the operands are in the C8 layout: x from fh_conv_pack_input_c8 and w from
  * fh_conv_pack_filter_c8 ([Cout][fh_conv_c8_filter_k(KH, KW)]). */
 int32_t fh_conv2d_nhwc_supported(int32_t dtype, const int64_t geom[12]);
+
+/* 1 if fh_conv2d_nhwc_fwd_ex takes dtype and geom with FH_CONV_IN_NCHW (bf16/f16, 3x3, stride 1, padding 1,
+ * groups 1, Cin % 32 == 0, W % 8 == 0, a resident patch of at most 30 KB), else 0. Host-only query. */
+int32_t fh_conv2d_nchw_in_supported(int32_t dtype, const int64_t geom[12]);
 
 /* C8 layout for convolutions with Cin <= 8 (e.g. an RGB stem): x NCHW [N][C][H*W] (16-bit) ->
  * [N][H*W][8] with channels C..7 zero. No counterpart in the reference (cuDNN consumes NCHW). */

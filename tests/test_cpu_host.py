@@ -384,3 +384,16 @@ def test_gemm_grouped_and_ex_argument_checks():
     assert lib.fh_gemm_grouped(3, 8, 2, ptrs, ptrs, 64, 64, 64, eps, 4, None) == 1  # unknown flag
     assert lib.fh_gemm_ex(3, 8, 8, 8, 64, 64, 64, None, 6, None) == 1
     assert b"unknown flags" in lib.fh_last_error()
+
+
+def test_nchw_graph_input_conv_reads_nchw_directly():
+    # C3: the 3x3 stride-1 conv of a graph-input activation reads it NCHW (no channels-last copy of x, only of the
+    # filter); a width the 8-pixel groups do not divide keeps the copy
+    out = host.hip_lowered(graphs.conv(3).text(), 1)
+    assert out.count("hip_channels_last_internal(") == 1 and "in_nchw=1" in out, out
+    out = host.hip_lowered(graphs.conv(3, w=57).text(), 1)
+    assert out.count("hip_channels_last_internal(") == 2 and "in_nchw" not in out, out
+    lib = abi.lib()
+    assert lib.fh_conv2d_nchw_in_supported(3, abi.i64_array([32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1])) == 1
+    assert lib.fh_conv2d_nchw_in_supported(3, abi.i64_array([32, 64, 56, 57, 64, 3, 3, 1, 1, 1, 1, 1])) == 0
+    assert lib.fh_conv2d_nchw_in_supported(0, abi.i64_array([32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1])) == 0

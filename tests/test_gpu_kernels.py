@@ -646,6 +646,60 @@ def test_conv2d_resident_patch(hip, dtype, geom, nhwc_out):
     assert_close(flat[idx], want, dtype, what=f"resident patch {geom} sampled")
 
 
+NCHW_IN_CASES = [
+    (BF16, (32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1), 0),    # C3: 256-pixel tiles, 8 patch rows
+    (F16, (32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1), 0),
+    (BF16, (3, 96, 9, 16, 40, 3, 3, 1, 1, 1, 1, 1), 0),      # Cout 40, three chunks, 128-pixel tiles
+    (BF16, (5, 32, 3, 8, 100, 3, 3, 1, 1, 1, 1, 1), 1),      # 3-row images, one 8-pixel group per row
+    (BF16, (4, 64, 14, 24, 64, 3, 3, 1, 1, 1, 1, 1), 1),     # channels-last output from NCHW input
+    (BF16, (2, 64, 7, 8, 320, 3, 3, 1, 1, 1, 1, 1), 1),      # Cout > 256 with channels-last output
+]
+
+
+@pytest.mark.parametrize("dtype,geom,nhwc_out", NCHW_IN_CASES)
+def test_conv2d_nchw_input(hip, dtype, geom, nhwc_out):
+    """FH_CONV_IN_NCHW: the single-buffered resident-patch kernel fills its patch from NCHW activations through
+    registers. Same kernel, same k order as the channels-last input, so the two agree bit for bit; and both images
+    at the ends of the batch against the oracle."""
+    say(f"conv nchw input dtype={dtype} {geom} nhwc_out={nhwc_out}")
+    n, cin, h, w, cout, kh, kw = geom[:7]
+    assert hip.lib().fh_conv2d_nchw_in_supported(dtype, hip.i64_array(geom)) == 1
+    x = synth.tensor(181, (n, cin, h, w), dtype, "normal")
+    wt = synth.tensor(182, (cout, cin, kh, kw), dtype, "normal", (2.0 / (cin * kh * kw)) ** 0.5)
+    bias = synth.tensor(183, (cout,), dtype, "normal", 0.1)
+    dxn, dxc, dw, db = dev(hip, x), dev(hip, to_nhwc(x)), dev(hip, to_nhwc(wt)), dev(hip, bias)
+    ep = hip.make_epilogue([(hip.EW_RELU, None)])
+    outs = []
+    for xin, flag in ((dxn, 4), (dxc, 0)):
+        dy = hip.DeviceBuffer(n * cout * h * w * x.itemsize)
+        hip.check(hip.lib().fh_conv2d_nhwc_fwd_ex(dtype, xin.value, dw.value, db.value, dy.value, hip.i64_array(geom),
+                                                  ctypes.byref(ep), flag | nhwc_out, None))
+        got = dy.download((n, h, w, cout) if nhwc_out else (n, cout, h, w), x.dtype)
+        outs.append(np.ascontiguousarray(got.transpose(0, 3, 1, 2)) if nhwc_out else got)
+    # with channels-last output, a channels-last input takes the persistent kernel for Cout <= 64 and the implicit
+    # GEMM above 256; elsewhere both inputs run the same kernel
+    if not (nhwc_out and (cout <= 64 or cout > 256)):
+        assert_bitwise(outs[0], outs[1], f"NCHW vs channels-last input {geom}")
+    else:
+        assert_close(outs[0], outs[1], dtype, what=f"NCHW vs channels-last input {geom}")
+    for img in sorted({0, n - 1}):
+        conv = orc.conv2d(dtype, x[img:img + 1], wt, bias, (1,) + geom[1:])
+        assert_close(outs[0][img:img + 1], orc.ew_program(dtype, [3], [1], [conv]), dtype,
+                     what=f"NCHW input {geom} image {img}")
+
+
+def test_conv2d_nchw_input_rejections(hip):
+    lib = hip.lib()
+    for geom in [(1, 64, 8, 12, 64, 3, 3, 1, 1, 1, 1, 1),     # W % 8 != 0
+                 (1, 64, 8, 16, 64, 3, 3, 2, 2, 1, 1, 1),     # stride 2
+                 (1, 48, 8, 16, 64, 3, 3, 1, 1, 1, 1, 1)]:    # Cin % 32 != 0
+        g = hip.i64_array(geom)
+        assert lib.fh_conv2d_nchw_in_supported(BF16, g) == 0, geom
+        x = hip.DeviceBuffer(64 * 8 * 16 * 2)
+        assert lib.fh_conv2d_nhwc_fwd_ex(BF16, x.value, x.value, None, x.value, g, None, 4, None) == 4  # unimplemented
+    assert lib.fh_conv2d_nchw_in_supported(F32, hip.i64_array((1, 64, 8, 16, 64, 3, 3, 1, 1, 1, 1, 1))) == 0
+
+
 NHWC_OUT_CASES = [
     (BF16, (2, 64, 12, 12, 64, 3, 3, 1, 1, 1, 1, 1)),
     (BF16, (2, 64, 14, 14, 128, 1, 1, 2, 2, 0, 0, 1)),    # 1x1 stride-2 downsample
