@@ -206,6 +206,27 @@ def extras(steps, only=None):
         return {"workload": "fused add;relu bf16 [64,64,56,56], cold (8 rotating input sets)", "us": round(ms * 1e3, 2),
                 "GB/s": round(by / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(by / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
 
+    def rows_op(kind):
+        # C5's row reductions as standalone ops: softmax over the [8*16*512, 512] per-head score rows, LayerNorm
+        # over the [4096, 1024] activations; bf16, 8 rotating input sets so every run reads from HBM
+        g = graphs.Graph("hip")
+        if kind == "softmax":
+            shape = (65536, 512)
+            x = g.input(BF16, shape)
+            g.output(g.softmax(x))
+            sets = [[synth.tensor(920 + i, shape, BF16, "normal", 2.0)] for i in range(8)]
+            by = 2 * int(np.prod(shape)) * 2
+        else:
+            shape = (4096, 1024)
+            x, ga, be = g.input(BF16, shape), g.input(BF16, (1024,)), g.input(BF16, (1024,))
+            g.output(g.layer_norm(x, ga, be))
+            sets = [[synth.tensor(930 + i, shape, BF16), synth.tensor(940, (1024,), BF16), synth.tensor(941, (1024,), BF16)]
+                    for i in range(8)]
+            by = 2 * int(np.prod(shape)) * 2 + 2 * 1024 * 2
+        ms = _time_graph(g.text(), sets, max(steps, 40), 8)
+        return {"workload": f"{kind} bf16 {list(shape)}, cold (8 rotating input sets)", "us": round(ms * 1e3, 2),
+                "GB/s": round(by / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(by / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+
     def conv(dtype):
         flops = 2 * 32 * 64 * 56 * 56 * 64 * 9
         ms = _time_graph(graphs.conv(dtype).text(), [graphs.conv_inputs(dtype)], max(3, steps // 5), 2)
@@ -319,6 +340,8 @@ def extras(steps, only=None):
         guard("graph_replay", graph_replay)
         guard("cpu_baselines", cpu_baselines)
     guard("fused_elementwise", fused)
+    guard("softmax_c5", lambda: rows_op("softmax"))
+    guard("layer_norm_c5", lambda: rows_op("layer_norm"))
     guard("conv_c3_bf16", lambda: conv(BF16))
     guard("conv_c3_f32", lambda: conv(F32))
     for n in (1024, 2048):

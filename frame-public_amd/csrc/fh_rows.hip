@@ -69,6 +69,57 @@ __global__ __launch_bounds__(256) void softmax_wave_kernel(const typename Io<T>:
   }
 }
 
+// Rows of 64 * PER elements with 16-byte aligned rows, one wave per row: lane l owns the contiguous elements
+// [V*l + 64*V*t, +V) for t < PER / V, all loaded (16-byte accesses) before the max reduction. The arithmetic is
+// softmax_wave_kernel's (m = max, e = expf(x - m), s = sum e, y = round(e / s)); only the order of the terms of
+// the lane's partial sum differs.
+template <typename T, int PER>
+__global__ __launch_bounds__(256) void softmax_vec_kernel(const typename Io<T>::storage* __restrict__ x,
+                                                         typename Io<T>::storage* __restrict__ y, int64_t rows) {
+  using S = typename Io<T>::storage;
+  constexpr int V = 16 / static_cast<int>(sizeof(S));
+  constexpr int NV = PER / V;
+  constexpr int64_t COLS = 64 * PER;
+  static_assert(PER % V == 0, "whole vectors per lane");
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * kRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const u4_t* xr = reinterpret_cast<const u4_t*>(x + row * COLS);
+  u4_t* yr = reinterpret_cast<u4_t*>(y + row * COLS);
+  u4_t xv[NV];
+#pragma unroll
+  for (int t = 0; t < NV; ++t) xv[t] = __builtin_nontemporal_load(xr + lane + 64 * t);
+  float v[PER];
+  float m = -__builtin_inff();
+#pragma unroll
+  for (int t = 0; t < NV; ++t) {
+    S e[V];
+    __builtin_memcpy(e, &xv[t], 16);
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      v[t * V + i] = Io<T>::load(e[i]);
+      m = (v[t * V + i] > m) ? v[t * V + i] : m;
+    }
+  }
+  m = wave_max(m);
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    v[i] = expf(v[i] - m);
+    s += v[i];
+  }
+  s = wave_sum(s);
+#pragma unroll
+  for (int t = 0; t < NV; ++t) {
+    S o[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) o[i] = Io<T>::store(v[t * V + i] / s);
+    u4_t w;
+    __builtin_memcpy(&w, o, 16);
+    __builtin_nontemporal_store(w, yr + lane + 64 * t);
+  }
+}
+
 __device__ float block_reduce(float v, bool is_max, float* scratch) {
   v = is_max ? wave_max(v) : wave_sum(v);
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
@@ -264,9 +315,26 @@ struct LayerNormLaunch {
   }
 };
 
+template <typename T, int PER>
+fh_status launch_softmax_vec(const void* x, void* y, int64_t rows, hipStream_t s) {
+  using S = typename Io<T>::storage;
+  const dim3 grid(static_cast<uint32_t>((rows + kRowsPerBlock - 1) / kRowsPerBlock));
+  hipLaunchKernelGGL((softmax_vec_kernel<T, PER>), grid, dim3(256), 0, s, static_cast<const S*>(x),
+                     static_cast<S*>(y), rows);
+  return launch_status("softmax_vec_kernel launch");
+}
+
+bool aligned16(const void* p);
+
 template <typename T>
 fh_status softmax_typed(const void* x, void* y, int64_t rows, int64_t cols, hipStream_t s) {
   using S = typename Io<T>::storage;
+  constexpr int V = 16 / static_cast<int>(sizeof(S));
+  if (aligned16(x) && aligned16(y)) {
+    if (cols == 64 * V) return launch_softmax_vec<T, V>(x, y, rows, s);
+    if (cols == 64 * 2 * V) return launch_softmax_vec<T, 2 * V>(x, y, rows, s);
+    if (cols == 64 * 4 * V) return launch_softmax_vec<T, 4 * V>(x, y, rows, s);
+  }
   if (cols <= 64 * 32) return by_width<T, SoftmaxLaunch>(cols, x, y, rows, cols, s);
   hipLaunchKernelGGL(softmax_block_kernel<T>, dim3(static_cast<uint32_t>(rows)), dim3(256), 0, s,
                      static_cast<const S*>(x), static_cast<S*>(y), cols);

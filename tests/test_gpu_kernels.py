@@ -336,8 +336,10 @@ def test_gelu(hip, dtype):
     assert_close(got, want, dtype, rtol=1e-5 if dtype == F32 else 1e-2, atol=1e-6, what="gelu")
 
 
+# (BF16, 512, 512), (BF16, 33, 1024), (F16, 5, 2048), (F32, 7, 256 / 512 / 1024) take the 16-byte vector kernel
 @pytest.mark.parametrize("dtype,rows,cols", [(F32, 64, 10), (BF16, 512, 512), (F32, 3, 3000), (BF16, 8, 1),
-                                             (F32, 2, 2)])
+                                             (F32, 2, 2), (BF16, 33, 1024), (F16, 5, 2048), (F32, 7, 256),
+                                             (F32, 7, 512), (F32, 7, 1024), (BF16, 65536, 512)])
 def test_softmax(hip, dtype, rows, cols):
     say(f"softmax dtype={dtype} {rows}x{cols}")
     x = synth.tensor(61, (rows, cols), dtype, "normal", 2.0)
