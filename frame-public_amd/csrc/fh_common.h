@@ -366,6 +366,61 @@ __device__ __forceinline__ uint4 epi_vec(const EP& ep, uint4 packed, int64_t idx
   }
 }
 
+// Split form of epi_vec for the fixed programs, so a caller can issue the operand loads of several output vectors
+// before using any of them (one memory latency per batch instead of one per vector): epi_operands<E>() 16-byte
+// operand vectors per output vector, epi_load fetches them, epi_apply runs the program on them. kEpiAny reads its
+// own operands (epi_operands = 0; use epi_vec).
+template <int E>
+__host__ __device__ constexpr int epi_operands() {
+  return (E == kEpiAddRelu || E == kEpiAdd || E == kEpiAddGelu) ? 1 : E == kEpiAddAdd ? 2 : 0;
+}
+
+template <int E, typename T, typename EP>
+__device__ __forceinline__ void epi_load(const EP& ep, int64_t idx, uint4* in) {
+  using S = typename Io<T>::storage;
+#pragma unroll
+  for (int s = 0; s < epi_operands<E>(); ++s) in[s] = *reinterpret_cast<const uint4*>(static_cast<const S*>(ep.ins[s]) + idx);
+}
+
+template <int E, typename T, typename EP>
+__device__ __forceinline__ uint4 epi_apply(const EP& ep, uint4 packed, const uint4* in) {
+  using S = typename Io<T>::storage;
+  static_assert(E != kEpiAny, "the interpreter reads its own operands");
+  if constexpr (E == kEpiNone) {
+    return packed;
+  } else {
+    using P = EpiProgram<E>;
+    constexpr int V = 16 / static_cast<int>(sizeof(S));
+    const uint8_t ops[2] = {P::op0, P::op1};
+    S vals[V];
+    __builtin_memcpy(vals, &packed, 16);
+    float v[V];
+#pragma unroll
+    for (int x = 0; x < V; ++x) v[x] = Io<T>::load(vals[x]);
+    int next = 0;
+#pragma unroll
+    for (int s = 0; s < P::n; ++s) {
+      if (ew_is_binary(ops[s])) {
+        S iv[V];
+        __builtin_memcpy(iv, &in[next++], 16);
+#pragma unroll
+        for (int x = 0; x < V; ++x) v[x] = epi_binary(ops[s], v[x], Io<T>::load(iv[x]));
+      } else {
+#pragma unroll
+        for (int x = 0; x < V; ++x) v[x] = epi_unary(ops[s], v[x]);
+      }
+      if (ep.round_between) {
+#pragma unroll
+        for (int x = 0; x < V; ++x) v[x] = Io<T>::round(v[x]);
+      }
+    }
+#pragma unroll
+    for (int x = 0; x < V; ++x) vals[x] = Io<T>::store(v[x]);
+    __builtin_memcpy(&packed, vals, 16);
+    return packed;
+  }
+}
+
 inline int device_cu_count() {
   static int cached = 0;
   if (cached == 0) {

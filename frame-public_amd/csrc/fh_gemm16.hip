@@ -277,14 +277,43 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
   if (grouped)
 #pragma unroll
     for (int sg = 0; sg < FH_MAX_SEGMENTS; ++sg) ep.ins[sg] = args.group_ins[blockIdx.y][sg];
-  for (int it = 0; it < WM / RPI; ++it) {
-    const int rr = it * RPI + lane / LPR;
-    const int64_t row = m0 + wm * WM + rr;
-    if (row < M && col < N) {
-      uint4 packed = *reinterpret_cast<const uint4*>(wl + rr * WN + c);
-      const int64_t idx = row * ldc + col;
-      packed = epi_vec<E, T>(ep, packed, idx);
-      *reinterpret_cast<uint4*>(C + idx) = packed;
+  constexpr int ITERS = WM / RPI;
+  constexpr int NOP = epi_operands<E>();
+  if constexpr (NOP == 0) {
+    for (int it = 0; it < ITERS; ++it) {
+      const int rr = it * RPI + lane / LPR;
+      const int64_t row = m0 + wm * WM + rr;
+      if (row < M && col < N) {
+        uint4 packed = *reinterpret_cast<const uint4*>(wl + rr * WN + c);
+        const int64_t idx = row * ldc + col;
+        packed = epi_vec<E, T>(ep, packed, idx);
+        *reinterpret_cast<uint4*>(C + idx) = packed;
+      }
+    }
+  } else {
+    // programs with operands: the operand loads of a batch of rows are all issued before the first is used, so the
+    // epilogue waits for memory once per batch rather than once per row. Rows and columns past the edge load the
+    // last valid vector instead (never used), which keeps the loads free of branches the wait-count tracking
+    // would have to join.
+    constexpr int BATCH = ITERS < 8 ? ITERS : 8;
+    const int64_t col_c = col < N ? col : N - V;
+    for (int it0 = 0; it0 < ITERS; it0 += BATCH) {
+      uint4 in[BATCH][NOP];
+#pragma unroll
+      for (int b = 0; b < BATCH; ++b) {
+        const int64_t row = m0 + wm * WM + (it0 + b) * RPI + lane / LPR;
+        epi_load<E, T>(ep, (row < M ? row : M - 1) * ldc + col_c, in[b]);
+      }
+#pragma unroll
+      for (int b = 0; b < BATCH; ++b) {
+        const int rr = (it0 + b) * RPI + lane / LPR;
+        const int64_t row = m0 + wm * WM + rr;
+        if (row < M && col < N) {
+          const uint4 packed = *reinterpret_cast<const uint4*>(wl + rr * WN + c);
+          const int64_t idx = row * ldc + col;
+          *reinterpret_cast<uint4*>(C + idx) = epi_apply<E, T>(ep, packed, in[b]);
+        }
+      }
     }
   }
 }
