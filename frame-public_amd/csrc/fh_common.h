@@ -366,6 +366,24 @@ __device__ __forceinline__ uint4 epi_vec(const EP& ep, uint4 packed, int64_t idx
   }
 }
 
+// The value an epilogue stages for output x (the fp32 sum plus bias): rounded to the storage type and, for the
+// relu-only program, already through relu. relu of a rounded value is itself a storage value and rounds to itself,
+// so applying it here equals applying it after the staging round trip; the readback then runs
+// epi_after_stage<E>() instead of E (no program for relu), which saves an unpack, compare and repack per element.
+template <int E, typename T>
+__device__ __forceinline__ typename Io<T>::storage epi_stage(float x) {
+  if constexpr (E == kEpiRelu) {
+    const float r = Io<T>::round(x);
+    return Io<T>::store(r < 0.0f ? 0.0f : r);
+  } else {
+    return Io<T>::store(x);
+  }
+}
+template <int E>
+__host__ __device__ constexpr int epi_after_stage() {
+  return E == kEpiRelu ? kEpiNone : E;
+}
+
 // Split form of epi_vec for the fixed programs, so a caller can issue the operand loads of several output vectors
 // before using any of them (one memory latency per batch instead of one per vector): epi_operands<E>() 16-byte
 // operand vectors per output vector, epi_load fetches them, epi_apply runs the program on them. kEpiAny reads its

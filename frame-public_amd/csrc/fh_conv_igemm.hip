@@ -126,12 +126,12 @@ __device__ __forceinline__ void conv_store_tile(const ConvNhwcArgs& args, f32x16
         for (int j = 0; j < TN; ++j) {
           S* dst = wl + (j * 32 + l32) * PITCH + rr;
           if constexpr (ES == 2) {
-            const uint32_t w = static_cast<uint32_t>(Io<T>::store(acc[i][j][x] + b0)) |
-                               (static_cast<uint32_t>(Io<T>::store(acc[i][j][x + 1] + b1)) << 16);
+            const uint32_t w = static_cast<uint32_t>(epi_stage<E, T>(acc[i][j][x] + b0)) |
+                               (static_cast<uint32_t>(epi_stage<E, T>(acc[i][j][x + 1] + b1)) << 16);
             *reinterpret_cast<uint32_t*>(dst) = w;
           } else {
-            dst[0] = Io<T>::store(acc[i][j][x] + b0);
-            dst[1] = Io<T>::store(acc[i][j][x + 1] + b1);
+            dst[0] = epi_stage<E, T>(acc[i][j][x] + b0);
+            dst[1] = epi_stage<E, T>(acc[i][j][x + 1] + b1);
           }
         }
       }
@@ -146,15 +146,16 @@ __device__ __forceinline__ void conv_store_tile(const ConvNhwcArgs& args, f32x16
       if (co0 >= args.cout || p >= args.p) continue;
       uint4 packed = *reinterpret_cast<const uint4*>(wl + pc * PITCH + g * V);
       const int64_t idx = p * args.cout + co0;
+      constexpr int EA = epi_after_stage<E>();
       if (args.vec_store && co0 + V <= args.cout) {
-        packed = epi_vec<E, T>(args.ep, packed, idx);
+        packed = epi_vec<EA, T>(args.ep, packed, idx);
         *reinterpret_cast<uint4*>(Y + idx) = packed;
       } else {
         S vals[V];
         __builtin_memcpy(vals, &packed, 16);
         for (int e = 0; e < V && co0 + e < args.cout; ++e) {
           S v = vals[e];
-          if constexpr (E != kEpiNone) v = Io<T>::store(epi_one<E, T>(args.ep, Io<T>::load(v), idx + e));
+          if constexpr (EA != kEpiNone) v = Io<T>::store(epi_one<EA, T>(args.ep, Io<T>::load(v), idx + e));
           Y[idx + e] = v;
         }
       }
@@ -171,7 +172,7 @@ __device__ __forceinline__ void conv_store_tile(const ConvNhwcArgs& args, f32x16
     for (int x = 0; x < 16; ++x) {
       const int rr = i * 32 + 8 * (x >> 2) + 4 * hi + (x & 3);
 #pragma unroll
-      for (int j = 0; j < TN; ++j) wl[rr * WN + j * 32 + l32] = Io<T>::store(acc[i][j][x] + bv[i][x]);
+      for (int j = 0; j < TN; ++j) wl[rr * WN + j * 32 + l32] = epi_stage<E, T>(acc[i][j][x] + bv[i][x]);
     }
   __builtin_amdgcn_s_waitcnt(0xc07f);
   __builtin_amdgcn_wave_barrier();
@@ -180,16 +181,19 @@ __device__ __forceinline__ void conv_store_tile(const ConvNhwcArgs& args, f32x16
   static_assert(64 % LPR == 0 && WM % RPI == 0, "epilogue access shape");
   const int c = (lane % LPR) * V;
   const int64_t p0 = n0w + c;
+  constexpr int EA = epi_after_stage<E>();
+  // the lane's 8 pixels lie in one image (vector path: Ho*Wo % 8 == 0): its output offset without the channel term
+  const uint32_t img0 = static_cast<uint32_t>(p0) / static_cast<uint32_t>(args.howo);  // P < 2^31
+  const int64_t base0 = static_cast<int64_t>(img0) * args.cout * args.howo +
+                        (static_cast<uint32_t>(p0) - img0 * static_cast<uint32_t>(args.howo));
   for (int it = 0; it < WM / RPI; ++it) {
     const int rr = it * RPI + lane / LPR;
     const int co = m0w + rr;
     if (co >= args.cout || p0 >= args.p) continue;
     uint4 packed = *reinterpret_cast<const uint4*>(wl + rr * WN + c);
     if (args.vec_store && p0 + V <= args.p) {
-      const uint32_t img = static_cast<uint32_t>(p0) / static_cast<uint32_t>(args.howo);  // P < 2^31
-      const int64_t idx = (static_cast<int64_t>(img) * args.cout + co) * args.howo +
-                          (static_cast<uint32_t>(p0) - img * static_cast<uint32_t>(args.howo));
-      packed = epi_vec<E, T>(args.ep, packed, idx);
+      const int64_t idx = base0 + static_cast<int64_t>(co) * args.howo;
+      packed = epi_vec<EA, T>(args.ep, packed, idx);
       *reinterpret_cast<uint4*>(Y + idx) = packed;
     } else {
       S vals[V];
@@ -199,7 +203,7 @@ __device__ __forceinline__ void conv_store_tile(const ConvNhwcArgs& args, f32x16
         const int64_t img = p / args.howo;
         const int64_t idx = (img * args.cout + co) * args.howo + (p - img * args.howo);
         S v = vals[e];
-        if constexpr (E != kEpiNone) v = Io<T>::store(epi_one<E, T>(args.ep, Io<T>::load(v), idx));
+        if constexpr (EA != kEpiNone) v = Io<T>::store(epi_one<EA, T>(args.ep, Io<T>::load(v), idx));
         Y[idx] = v;
       }
     }
@@ -781,8 +785,8 @@ __device__ __forceinline__ void conv_store_tile_wg_nhwc(const ConvNhwcArgs& args
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int pc = wn * WN + j * 32 + l32;
-        const uint32_t w = static_cast<uint32_t>(Io<T>::store(acc[i][j][x] + bv[i][x])) |
-                           (static_cast<uint32_t>(Io<T>::store(acc[i][j][x + 1] + bv[i][x + 1])) << 16);
+        const uint32_t w = static_cast<uint32_t>(epi_stage<E, T>(acc[i][j][x] + bv[i][x])) |
+                           (static_cast<uint32_t>(epi_stage<E, T>(acc[i][j][x + 1] + bv[i][x + 1])) << 16);
         *reinterpret_cast<uint32_t*>(st + pc * PITCH + ch) = w;
       }
     }
@@ -799,15 +803,16 @@ __device__ __forceinline__ void conv_store_tile_wg_nhwc(const ConvNhwcArgs& args
     uint4 packed = *reinterpret_cast<const uint4*>(st + pc * PITCH + g * 8);
     const int64_t idx = p * args.cout + co0;
     S* __restrict__ Y = static_cast<S*>(args.y);
+    constexpr int EA = epi_after_stage<E>();
     if (args.vec_store && co0 + 8 <= args.cout) {
-      packed = epi_vec<E, T>(args.ep, packed, idx);
+      packed = epi_vec<EA, T>(args.ep, packed, idx);
       *reinterpret_cast<uint4*>(Y + idx) = packed;
     } else {
       S vals[8];
       __builtin_memcpy(vals, &packed, 16);
       for (int e = 0; e < 8 && co0 + e < args.cout; ++e) {
         S v = vals[e];
-        if constexpr (E != kEpiNone) v = Io<T>::store(epi_one<E, T>(args.ep, Io<T>::load(v), idx + e));
+        if constexpr (EA != kEpiNone) v = Io<T>::store(epi_one<EA, T>(args.ep, Io<T>::load(v), idx + e));
         Y[idx + e] = v;
       }
     }
