@@ -137,8 +137,39 @@ __device__ __forceinline__ void conv_store_tile(const ConvNhwcArgs& args, f32x16
       }
     __builtin_amdgcn_s_waitcnt(0xc07f);
     __builtin_amdgcn_wave_barrier();
+    constexpr int EA = epi_after_stage<E>();
+    constexpr int ITERS = WN * GPW / 64;
+    if constexpr (EA != kEpiAny) {
+      if (args.vec_store) {
+        // every operand load issued before the first is used and no wait between the stores (a wait for one
+        // iteration's operand would also wait for the previous iteration's store)
+        constexpr int NOP = epi_operands<EA>() > 0 ? epi_operands<EA>() : 1;
+        uint4 in[ITERS][NOP];
+        if constexpr (epi_operands<EA>() > 0) {
+#pragma unroll
+          for (int it = 0; it < ITERS; ++it) {
+            const int id = it * 64 + lane;
+            const int co0 = min(m0w + (id % GPW) * V, args.cout - V);
+            const int64_t p = min(n0w + id / GPW, args.p - 1);
+            epi_load<EA, T>(args.ep, p * args.cout + co0, in[it]);
+          }
+        }
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+          const int id = it * 64 + lane;
+          const int g = id % GPW, pc = id / GPW;
+          const int co0 = m0w + g * V;
+          const int64_t p = n0w + pc;
+          if (co0 < args.cout && p < args.p) {
+            const uint4 packed = *reinterpret_cast<const uint4*>(wl + pc * PITCH + g * V);
+            *reinterpret_cast<uint4*>(Y + p * args.cout + co0) = epi_apply<EA, T>(args.ep, packed, in[it]);
+          }
+        }
+        return;
+      }
+    }
 #pragma unroll 2
-    for (int it = 0; it < WN * GPW / 64; ++it) {
+    for (int it = 0; it < ITERS; ++it) {
       const int id = it * 64 + lane;
       const int g = id % GPW, pc = id / GPW;
       const int co0 = m0w + g * V;
@@ -146,7 +177,6 @@ __device__ __forceinline__ void conv_store_tile(const ConvNhwcArgs& args, f32x16
       if (co0 >= args.cout || p >= args.p) continue;
       uint4 packed = *reinterpret_cast<const uint4*>(wl + pc * PITCH + g * V);
       const int64_t idx = p * args.cout + co0;
-      constexpr int EA = epi_after_stage<E>();
       if (args.vec_store && co0 + V <= args.cout) {
         packed = epi_vec<EA, T>(args.ep, packed, idx);
         *reinterpret_cast<uint4*>(Y + idx) = packed;
@@ -186,7 +216,33 @@ __device__ __forceinline__ void conv_store_tile(const ConvNhwcArgs& args, f32x16
   const uint32_t img0 = static_cast<uint32_t>(p0) / static_cast<uint32_t>(args.howo);  // P < 2^31
   const int64_t base0 = static_cast<int64_t>(img0) * args.cout * args.howo +
                         (static_cast<uint32_t>(p0) - img0 * static_cast<uint32_t>(args.howo));
-  for (int it = 0; it < WM / RPI; ++it) {
+  constexpr int ITERS = WM / RPI;
+  if constexpr (EA != kEpiAny) {
+    if (args.vec_store && p0 + V <= args.p) {
+      // operand loads first, then the stores with no wait between them (see the channels-last path)
+      constexpr int NOP = epi_operands<EA>() > 0 ? epi_operands<EA>() : 1;
+      uint4 in[ITERS][NOP];
+      if constexpr (epi_operands<EA>() > 0) {
+#pragma unroll
+        for (int it = 0; it < ITERS; ++it) {
+          const int co = min(m0w + it * RPI + lane / LPR, args.cout - 1);
+          epi_load<EA, T>(args.ep, base0 + static_cast<int64_t>(co) * args.howo, in[it]);
+        }
+      }
+#pragma unroll
+      for (int it = 0; it < ITERS; ++it) {
+        const int rr = it * RPI + lane / LPR;
+        const int co = m0w + rr;
+        if (co < args.cout) {
+          const uint4 packed = *reinterpret_cast<const uint4*>(wl + rr * WN + c);
+          *reinterpret_cast<uint4*>(Y + base0 + static_cast<int64_t>(co) * args.howo) =
+              epi_apply<EA, T>(args.ep, packed, in[it]);
+        }
+      }
+      return;
+    }
+  }
+  for (int it = 0; it < ITERS; ++it) {
     const int rr = it * RPI + lane / LPR;
     const int co = m0w + rr;
     if (co >= args.cout || p0 >= args.p) continue;
@@ -793,8 +849,39 @@ __device__ __forceinline__ void conv_store_tile_wg_nhwc(const ConvNhwcArgs& args
   __builtin_amdgcn_s_waitcnt(0xc07f);
   __syncthreads();
   const int tid = wave * 64 + lane;
+  constexpr int ITERS = BN * 8 / (NW * 64);
+  if constexpr (epi_after_stage<E>() != kEpiAny) {
+    if (args.vec_store) {
+      // operand loads first, then the stores with no wait between them (see conv_store_tile)
+      constexpr int EA = epi_after_stage<E>();
+      constexpr int NOP = epi_operands<EA>() > 0 ? epi_operands<EA>() : 1;
+      S* __restrict__ Y = static_cast<S*>(args.y);
+      uint4 in[ITERS][NOP];
+      if constexpr (epi_operands<EA>() > 0) {
 #pragma unroll
-  for (int it = 0; it < BN * 8 / (NW * 64); ++it) {
+        for (int it = 0; it < ITERS; ++it) {
+          const int id = it * NW * 64 + tid;
+          const int co0 = min(m0 + (id & 7) * 8, args.cout - 8);
+          const int64_t p = min(n0 + (id >> 3), args.p - 1);
+          epi_load<EA, T>(args.ep, p * args.cout + co0, in[it]);
+        }
+      }
+#pragma unroll
+      for (int it = 0; it < ITERS; ++it) {
+        const int id = it * NW * 64 + tid;
+        const int g = id & 7, pc = id >> 3;
+        const int co0 = m0 + g * 8;
+        const int64_t p = n0 + pc;
+        if (co0 < args.cout && p < args.p) {
+          const uint4 packed = *reinterpret_cast<const uint4*>(st + pc * PITCH + g * 8);
+          *reinterpret_cast<uint4*>(Y + p * args.cout + co0) = epi_apply<EA, T>(args.ep, packed, in[it]);
+        }
+      }
+      return;
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
     const int id = it * NW * 64 + tid;
     const int g = id & 7, pc = id >> 3;
     const int co0 = m0 + g * 8;
