@@ -5,20 +5,27 @@
 //   P  = softmax rows of S2, rounded     (m = max, e = exp(x - m), s = sum e, y = round(e / s))
 //   O  = round(P · V_bh)                 (matmul)
 // and O lands at rows [b*seq, (b+1)*seq), columns [h*dh, (h+1)*dh) of the output: the layout of the reference's
-// head concat (axis 1) and batch concat (axis 0). Every intermediate is rounded where the reference rounds it;
-// the summation orders (MFMA blocks, per-lane partial sums), the exp routine and e * (1/s) in place of e / s
-// differ, each well inside one rounding of the stored probabilities.
+// head concat (axis 1) and batch concat (axis 0). S and S2 are rounded where the reference rounds them and m is
+// the exact row maximum of S2. The normalisation moves behind the second product: the kernel multiplies
+// round(e) (not round(e / s)) by V and scales the fp32 sums by 1/s before the one output rounding, so every
+// exponential is evaluated once. That, the summation orders (MFMA blocks, per-lane partial sums) and the exp
+// routine (v_exp_f32 of x log2(e) - m log2(e)) differ from the decomposition, each well inside one rounding of
+// the stored probabilities.
 //
 // One wave owns 32 queries and all seq keys; a workgroup is W waves (4, or 2 when seq is not a multiple of 128).
+// The work is VALU-bound (about 11 VALU operations per score against two MFMA k-steps per 32 x 32 tile), so the
+// per-score code is kept short.
 //  1. Scores transposed, Sᵀ = K·Qᵀ on v_mfma_f32_32x32x16, per 64-key block: K blocks stream through a
 //     double-buffered 8 KB LDS ring (global_load_lds_dwordx4, 16-byte chunks swizzled by row), the Q fragments
 //     stay in registers. Each lane's accumulator then holds one query and 16 keys of a 32-key tile; they are
-//     rounded, scaled, rounded and kept as packed bf16/f16 in registers (seq/2 values per lane), with the
-//     running maximum.
-//  2. m and s = sum exp(S2 - m) per query: the lane's values plus its partner lane (lane ^ 32, same query).
-//  3. Oᵀ = Vᵀ·Pᵀ: p = round(exp(S2 - m) * (1/s)) is produced in registers already in the B-operand layout
-//     (k = the lane's 8 keys of one query, in the accumulator's key order); the A operand (Vᵀ) comes from V
-//     blocks in LDS through ds_read_b64_tr_b16 in the same key order. V streams like K did.
+//     rounded, scaled, rounded and kept as packed bf16/f16 in registers (seq/2 values per lane). The running
+//     maximum is taken over the scaled values before their rounding: rounding is monotonic, so the rounded
+//     maximum is the maximum of the rounded values.
+//  2. m per query: the lane's maximum and its partner lane's (lane ^ 32, same query).
+//  3. Oᵀ = Vᵀ·Pᵀ: p = round(exp(S2 - m)) is produced in registers already in the B-operand layout (k = the
+//     lane's 8 keys of one query, in the accumulator's key order) while the lane sums the unrounded e; the A
+//     operand (Vᵀ) comes from V blocks in LDS through ds_read_b64_tr_b16 in the same key order. V streams like
+//     K did. The output is round(acc * (1/s)), s = the lane's sum plus its partner's.
 // LDS: 32 KB per workgroup (two K and two V blocks), so two workgroups share a CU.
 #include <hip/hip_runtime.h>
 
@@ -44,13 +51,11 @@ __device__ __forceinline__ int k_chunk(int row, int c) { return c ^ (row & 7); }
 __device__ __forceinline__ int v_chunk(int row, int c) { return c ^ (2 * (row & 3)); }
 
 template <typename T>
-__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  return static_cast<uint32_t>(Io<T>::store(lo)) | (static_cast<uint32_t>(Io<T>::store(hi)) << 16);
-}
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) { return store2<T>(lo, hi); }
 template <typename T>
-__device__ __forceinline__ float lo16(uint32_t v) { return Io<T>::load(static_cast<uint16_t>(v & 0xffffu)); }
+__device__ __forceinline__ float lo16(uint32_t v) { return load_lo<T>(v); }
 template <typename T>
-__device__ __forceinline__ float hi16(uint32_t v) { return Io<T>::load(static_cast<uint16_t>(v >> 16)); }
+__device__ __forceinline__ float hi16(uint32_t v) { return load_hi<T>(v); }
 
 template <typename T, int NB, int W>
 __global__ __launch_bounds__(W * 64, 2) void attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
@@ -94,7 +99,7 @@ __global__ __launch_bounds__(W * 64, 2) void attention_kernel(const uint16_t* __
 
   // ---- 1. scores, kept as packed 16-bit values: s2[t][j] = keys (x = 2j, 2j + 1) of tile t ----
   uint32_t s2[NT][8];
-  float m = -__builtin_inff();
+  float mraw = -__builtin_inff();  // maximum of the scaled scores before their rounding
 #pragma unroll
   for (int blk = 0; blk < NB; ++blk) {
     if (blk + 1 < NB) wait_vmcnt<LOADS>(); else wait_vmcnt<0>();
@@ -124,29 +129,18 @@ __global__ __launch_bounds__(W * 64, 2) void attention_kernel(const uint16_t* __
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const float a0 = Io<T>::round(Io<T>::round(acc[t][2 * j]) * scale);
-        const float a1 = Io<T>::round(Io<T>::round(acc[t][2 * j + 1]) * scale);
-        m = fmaxf(m, fmaxf(a0, a1));
-        s2[2 * blk + t][j] = pack2<T>(a0, a1);
-        asm volatile("" : "+v"(s2[2 * blk + t][j]));  // later passes unpack; nothing of a0, a1 stays live
+        const uint32_t sr = pack2<T>(acc[t][2 * j], acc[t][2 * j + 1]);  // round(S), two keys
+        const float a0 = lo16<T>(sr) * scale, a1 = hi16<T>(sr) * scale;
+        mraw = fmaxf(mraw, fmaxf(a0, a1));
+        s2[2 * blk + t][j] = pack2<T>(a0, a1);                         // round(S * scale)
+        asm volatile("" : "+v"(s2[2 * blk + t][j]));  // pass 3 unpacks; nothing of a0, a1 stays live
       }
   }
-  m = fmaxf(m, __shfl_xor(m, 32));
 
-  // ---- 2. row sums ----
-  float sum = 0.0f;
-#pragma unroll
-  for (int t = 0; t < NT; ++t)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) sum += __expf(lo16<T>(s2[t][j]) - m) + __expf(hi16<T>(s2[t][j]) - m);
-  sum += __shfl_xor(sum, 32);
-  const float r = 1.0f / sum;
-  // The packed scores are all pass 3 reads: tie them so the compiler recomputes the unpacking and exp there
-  // instead of keeping pass 2's seq/2 float values alive (which would not fit the register file).
-#pragma unroll
-  for (int t = 0; t < NT; ++t)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) asm volatile("" : "+v"(s2[t][j]));
+  // ---- 2. row maximum ----
+  const float m = Io<T>::round(fmaxf(mraw, __shfl_xor(mraw, 32)));
+  constexpr float kLog2e = 1.44269504088896340736f;
+  const float ml = m * kLog2e;  // exp(x - m) = exp2(x log2(e) - ml)
 
   // ---- 3. Oᵀ = Vᵀ·Pᵀ, two 32-row d tiles ----
   f32x16_t acc_o[2];
@@ -157,6 +151,7 @@ __global__ __launch_bounds__(W * 64, 2) void attention_kernel(const uint16_t* __
   // transpose reads: group g = lane / 16 covers d columns 16 (g & 1) .. + 15 of a d tile and the key half
   // g >> 1; source lane qd + 4 e of the group points at key row (kbase + e), columns n0 + 4 qd .. + 3
   const int g = lane >> 4, rr = lane & 15, qd = rr & 3, e = rr >> 2;
+  float sum = 0.0f;
 #pragma unroll
   for (int blk = 0; blk < NB; ++blk) {
     if (blk + 1 < NB) wait_vmcnt<LOADS>(); else wait_vmcnt<0>();
@@ -165,14 +160,21 @@ __global__ __launch_bounds__(W * 64, 2) void attention_kernel(const uint16_t* __
     for (int tt = 0; tt < 2; ++tt) {
       const int t = 2 * blk + tt;
       u32x4_t pf[2];
+      float part[8];
 #pragma unroll
       for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           uint32_t w = s2[t][4 * hf + j];
           asm volatile("" : "+v"(w));  // keeps the exp of this tile here, after the block's barrier
-          pf[hf][j] = pack2<T>(__expf(lo16<T>(w) - m) * r, __expf(hi16<T>(w) - m) * r);
+          const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(lo16<T>(w), kLog2e, -ml));
+          const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(hi16<T>(w), kLog2e, -ml));
+          part[4 * hf + j] = e0 + e1;
+          pf[hf][j] = pack2<T>(e0, e1);
         }
+      // the tile's sum joins the running sum here (tied), so no tile's exponentials outlive the tile
+      sum += ((part[0] + part[1]) + (part[2] + part[3])) + ((part[4] + part[5]) + (part[6] + part[7]));
+      asm volatile("" : "+v"(sum));
 #pragma unroll
       for (int dt = 0; dt < 2; ++dt) {
         const int n0 = 32 * dt + 16 * (g & 1) + 4 * qd;
@@ -198,14 +200,16 @@ __global__ __launch_bounds__(W * 64, 2) void attention_kernel(const uint16_t* __
   }
 
   // ---- output: acc_o[dt][x] = O[query q0 + l32][d = 32 dt + 8 (x / 4) + 4 hi + x % 4] ----
+  sum += __shfl_xor(sum, 32);
+  const float r = 1.0f / sum;
   uint16_t* orow = out + base + static_cast<int64_t>(q0 + l32) * ld;
 #pragma unroll
   for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
     for (int gq = 0; gq < 4; ++gq) {
       u32x2_t w;
-      w[0] = pack2<T>(acc_o[dt][4 * gq], acc_o[dt][4 * gq + 1]);
-      w[1] = pack2<T>(acc_o[dt][4 * gq + 2], acc_o[dt][4 * gq + 3]);
+      w[0] = pack2<T>(acc_o[dt][4 * gq] * r, acc_o[dt][4 * gq + 1] * r);
+      w[1] = pack2<T>(acc_o[dt][4 * gq + 2] * r, acc_o[dt][4 * gq + 3] * r);
       *reinterpret_cast<u32x2_t*>(orow + 32 * dt + 8 * gq + 4 * hi) = w;
     }
 }

@@ -7,6 +7,7 @@
 #include <cstdint>
 #include <cstring>
 #include <string>
+#include <type_traits>
 
 #include "frame_hip_abi.h"
 
@@ -115,6 +116,67 @@ struct Io<f16_t> {
   __device__ static uint16_t store(float v) { return float_to_f16_bits(v); }
   __device__ static float round(float v) { return f16_bits_to_float(float_to_f16_bits(v)); }
 };
+
+// Two values narrowed to T's 16-bit storage and packed in one word, lo in bits 0-15. bf16 takes one
+// v_cvt_pk_bf16_f32 for the pair (the narrowing of Io<bf16_t>::store); f16 narrows each half.
+template <typename T>
+__device__ __forceinline__ uint32_t store2(float lo, float hi) {
+  if constexpr (std::is_same_v<T, bf16_t>) {
+    typedef float f2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 b2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f2{lo, hi}, b2));
+  } else {
+    return static_cast<uint32_t>(Io<T>::store(lo)) | (static_cast<uint32_t>(Io<T>::store(hi)) << 16);
+  }
+}
+template <typename T>
+__device__ __forceinline__ float load_lo(uint32_t w) { return Io<T>::load(static_cast<uint16_t>(w & 0xffffu)); }
+template <typename T>
+__device__ __forceinline__ float load_hi(uint32_t w) { return Io<T>::load(static_cast<uint16_t>(w >> 16)); }
+// a, b <- round(a), round(b) through T's storage (Io<T>::round on each; identity for fp32)
+template <typename T>
+__device__ __forceinline__ void round_pair(float& a, float& b) {
+  if constexpr (!std::is_same_v<T, float>) {
+    const uint32_t w = store2<T>(a, b);
+    a = load_lo<T>(w);
+    b = load_hi<T>(w);
+  }
+}
+
+// One 16-byte vector of T's storage <-> 16 / sizeof(storage) floats; the narrowing goes pairwise through store2.
+template <typename T, int V>
+__device__ __forceinline__ void unpack_vec(const uint4& w, float (&v)[V]) {
+  static_assert(V * sizeof(typename Io<T>::storage) == 16, "one 16-byte vector");
+  const uint32_t u[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    if constexpr (std::is_same_v<T, float>) {
+      v[d] = __uint_as_float(u[d]);
+    } else {
+      v[2 * d] = load_lo<T>(u[d]);
+      v[2 * d + 1] = load_hi<T>(u[d]);
+    }
+  }
+}
+template <typename T, int V>
+__device__ __forceinline__ uint4 pack_vec(const float (&v)[V]) {
+  static_assert(V * sizeof(typename Io<T>::storage) == 16, "one 16-byte vector");
+  uint32_t u[4];
+#pragma unroll
+  for (int d = 0; d < 4; ++d) {
+    if constexpr (std::is_same_v<T, float>) {
+      u[d] = __float_as_uint(v[d]);
+    } else {
+      u[d] = store2<T>(v[2 * d], v[2 * d + 1]);
+    }
+  }
+  return uint4{u[0], u[1], u[2], u[3]};
+}
+template <typename T, int V>
+__device__ __forceinline__ void round_vec(float (&v)[V]) {
+#pragma unroll
+  for (int x = 0; x + 1 < V; x += 2) round_pair<T>(v[x], v[x + 1]);
+}
 
 // gelu(x) = 0.5 x (1 + erf(x / sqrt 2)), with 1 + erf(z) = 2 - erfc(|z|) for x >= 0 and erfc(|z|) for x < 0, and
 // erfc from the Chebyshev fit of Numerical Recipes in C (2nd ed., section 6.2, erfcc; fractional error below
@@ -326,57 +388,34 @@ __device__ __forceinline__ float epi_one(const EP& ep, float v, int64_t idx) {
   }
 }
 
-template <int E, typename T, typename EP>
-__device__ __forceinline__ uint4 epi_vec(const EP& ep, uint4 packed, int64_t idx) {
-  using S = typename Io<T>::storage;
-  if constexpr (E == kEpiNone) {
-    return packed;
-  } else if constexpr (E == kEpiAny) {
-    return ep.nseg > 0 ? epilogue_vec<T>(ep, packed, idx) : packed;
-  } else {
-    using P = EpiProgram<E>;
-    constexpr int V = 16 / static_cast<int>(sizeof(S));
-    const uint8_t ops[2] = {P::op0, P::op1};
-    S vals[V];
-    __builtin_memcpy(vals, &packed, 16);
-    float v[V];
-#pragma unroll
-    for (int x = 0; x < V; ++x) v[x] = Io<T>::load(vals[x]);
-#pragma unroll
-    for (int s = 0; s < P::n; ++s) {
-      if (ew_is_binary(ops[s])) {
-        const uint4 in = *reinterpret_cast<const uint4*>(static_cast<const S*>(ep.ins[s]) + idx);
-        S iv[V];
-        __builtin_memcpy(iv, &in, 16);
-#pragma unroll
-        for (int x = 0; x < V; ++x) v[x] = epi_binary(ops[s], v[x], Io<T>::load(iv[x]));
-      } else {
-#pragma unroll
-        for (int x = 0; x < V; ++x) v[x] = epi_unary(ops[s], v[x]);
-      }
-      if (ep.round_between) {
-#pragma unroll
-        for (int x = 0; x < V; ++x) v[x] = Io<T>::round(v[x]);
-      }
-    }
-#pragma unroll
-    for (int x = 0; x < V; ++x) vals[x] = Io<T>::store(v[x]);
-    __builtin_memcpy(&packed, vals, 16);
-    return packed;
-  }
-}
-
 // The value an epilogue stages for output x (the fp32 sum plus bias): rounded to the storage type and, for the
 // relu-only program, already through relu. relu of a rounded value is itself a storage value and rounds to itself,
 // so applying it here equals applying it after the staging round trip; the readback then runs
 // epi_after_stage<E>() instead of E (no program for relu), which saves an unpack, compare and repack per element.
+//
+// relu(round(x)) is computed as round(x < -lim ? 0 : x), lim = half of T's smallest denormal (2^-134 for bf16,
+// 2^-25 for f16, 0 for fp32): round(x) < 0 exactly when x < -lim (x in [-lim, 0) rounds to -0.0, the tie at -lim
+// to even, and relu keeps -0.0), and NaN compares false and rounds to NaN as relu keeps it.
+template <typename T>
+__device__ __forceinline__ float relu_before_round(float x) {
+  constexpr float lim = std::is_same_v<T, bf16_t> ? 0x1p-134f : std::is_same_v<T, f16_t> ? 0x1p-25f : 0.0f;
+  return x < -lim ? 0.0f : x;
+}
 template <int E, typename T>
 __device__ __forceinline__ typename Io<T>::storage epi_stage(float x) {
   if constexpr (E == kEpiRelu) {
-    const float r = Io<T>::round(x);
-    return Io<T>::store(r < 0.0f ? 0.0f : r);
+    return Io<T>::store(relu_before_round<T>(x));
   } else {
     return Io<T>::store(x);
+  }
+}
+// Two adjacent staged values packed in one word (16-bit storage), one narrowing for the pair on bf16.
+template <int E, typename T>
+__device__ __forceinline__ uint32_t epi_stage2(float x0, float x1) {
+  if constexpr (E == kEpiRelu) {
+    return store2<T>(relu_before_round<T>(x0), relu_before_round<T>(x1));
+  } else {
+    return store2<T>(x0, x1);
   }
 }
 template <int E>
@@ -402,40 +441,43 @@ __device__ __forceinline__ void epi_load(const EP& ep, int64_t idx, uint4* in) {
 
 template <int E, typename T, typename EP>
 __device__ __forceinline__ uint4 epi_apply(const EP& ep, uint4 packed, const uint4* in) {
-  using S = typename Io<T>::storage;
   static_assert(E != kEpiAny, "the interpreter reads its own operands");
   if constexpr (E == kEpiNone) {
     return packed;
   } else {
     using P = EpiProgram<E>;
-    constexpr int V = 16 / static_cast<int>(sizeof(S));
+    constexpr int V = 16 / static_cast<int>(sizeof(typename Io<T>::storage));
     const uint8_t ops[2] = {P::op0, P::op1};
-    S vals[V];
-    __builtin_memcpy(vals, &packed, 16);
     float v[V];
-#pragma unroll
-    for (int x = 0; x < V; ++x) v[x] = Io<T>::load(vals[x]);
+    unpack_vec<T>(packed, v);
     int next = 0;
 #pragma unroll
     for (int s = 0; s < P::n; ++s) {
       if (ew_is_binary(ops[s])) {
-        S iv[V];
-        __builtin_memcpy(iv, &in[next++], 16);
+        float iv[V];
+        unpack_vec<T>(in[next++], iv);
 #pragma unroll
-        for (int x = 0; x < V; ++x) v[x] = epi_binary(ops[s], v[x], Io<T>::load(iv[x]));
+        for (int x = 0; x < V; ++x) v[x] = epi_binary(ops[s], v[x], iv[x]);
       } else {
 #pragma unroll
         for (int x = 0; x < V; ++x) v[x] = epi_unary(ops[s], v[x]);
       }
-      if (ep.round_between) {
-#pragma unroll
-        for (int x = 0; x < V; ++x) v[x] = Io<T>::round(v[x]);
-      }
+      if (ep.round_between) round_vec<T>(v);
     }
-#pragma unroll
-    for (int x = 0; x < V; ++x) vals[x] = Io<T>::store(v[x]);
-    __builtin_memcpy(&packed, vals, 16);
+    return pack_vec<T>(v);
+  }
+}
+
+template <int E, typename T, typename EP>
+__device__ __forceinline__ uint4 epi_vec(const EP& ep, uint4 packed, int64_t idx) {
+  if constexpr (E == kEpiNone) {
     return packed;
+  } else if constexpr (E == kEpiAny) {
+    return ep.nseg > 0 ? epilogue_vec<T>(ep, packed, idx) : packed;
+  } else {
+    uint4 in[epi_operands<E>() > 0 ? epi_operands<E>() : 1];
+    epi_load<E, T>(ep, idx, in);
+    return epi_apply<E, T>(ep, packed, in);
   }
 }
 

@@ -126,9 +126,7 @@ __device__ __forceinline__ void conv_store_tile(const ConvNhwcArgs& args, f32x16
         for (int j = 0; j < TN; ++j) {
           S* dst = wl + (j * 32 + l32) * PITCH + rr;
           if constexpr (ES == 2) {
-            const uint32_t w = static_cast<uint32_t>(epi_stage<E, T>(acc[i][j][x] + b0)) |
-                               (static_cast<uint32_t>(epi_stage<E, T>(acc[i][j][x + 1] + b1)) << 16);
-            *reinterpret_cast<uint32_t*>(dst) = w;
+            *reinterpret_cast<uint32_t*>(dst) = epi_stage2<E, T>(acc[i][j][x] + b0, acc[i][j][x + 1] + b1);
           } else {
             dst[0] = epi_stage<E, T>(acc[i][j][x] + b0);
             dst[1] = epi_stage<E, T>(acc[i][j][x + 1] + b1);
@@ -841,9 +839,7 @@ __device__ __forceinline__ void conv_store_tile_wg_nhwc(const ConvNhwcArgs& args
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const int pc = wn * WN + j * 32 + l32;
-        const uint32_t w = static_cast<uint32_t>(epi_stage<E, T>(acc[i][j][x] + bv[i][x])) |
-                           (static_cast<uint32_t>(epi_stage<E, T>(acc[i][j][x + 1] + bv[i][x + 1])) << 16);
-        *reinterpret_cast<uint32_t*>(st + pc * PITCH + ch) = w;
+        *reinterpret_cast<uint32_t*>(st + pc * PITCH + ch) = epi_stage2<E, T>(acc[i][j][x] + bv[i][x], acc[i][j][x + 1] + bv[i][x + 1]);
       }
     }
   __builtin_amdgcn_s_waitcnt(0xc07f);
