@@ -27,6 +27,7 @@ import numpy as np  # noqa: E402
 PEAK_BF16_TFLOPS = 2516.6  # dense bf16 MFMA, 256 CU x 2.4 GHz x 4096 FLOP/clk/CU
 PEAK_F32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
+GRAPH_SETTLE_MS = 200.0  # untimed wall time each secondary measurement runs before its timed region
 
 N = 4096
 F32, BF16 = 0, 3
@@ -125,9 +126,11 @@ def copy_calibration(mib: int, reps: int):
 
 # ---- secondary measurements of the same metric (GEMM/Conv2d TFLOP/s, fused-op GB/s, graph latency) --
 
-def _time_graph(graph_text, input_sets, steps, warmup):
+def _time_graph(graph_text, input_sets, steps, warmup, settle_ms=GRAPH_SETTLE_MS):
     """ms per Executable::run of the compiled graph, rotating over input_sets (lists of numpy arrays), HIP events
-    on the executable's own stream."""
+    on the executable's own stream. After the warm-up runs the graph keeps running, untimed, for settle_ms of
+    wall time, so the timed runs see the settled engine clock rather than its ramp from idle (a short graph
+    such as C1 otherwise measures up to 2.5x its settled time on a cold GPU)."""
     from frame_hip import abi, host
 
     exe = host.compile(graph_text, "hip")
@@ -138,6 +141,14 @@ def _time_graph(graph_text, input_sets, steps, warmup):
     start, stop = abi.Event(), abi.Event()
     for i in range(warmup):
         exe.run_tensors(sets[i % len(sets)], outs, stream)
+    stream.synchronize()
+    t_end = time.perf_counter() + settle_ms * 1e-3
+    i = 0
+    while time.perf_counter() < t_end:
+        exe.run_tensors(sets[i % len(sets)], outs, stream)
+        i += 1
+        if i % 16 == 0:
+            stream.synchronize()
     stream.synchronize()
     start.record(native)
     for i in range(steps):
@@ -171,6 +182,11 @@ def _time_train_step(fwd_text, n_params, inputs, lr, steps, warmup):
     for i in range(warmup):
         step(i)
     stream.synchronize()
+    t_end = time.perf_counter() + GRAPH_SETTLE_MS * 1e-3  # settled clock, as in _time_graph
+    while time.perf_counter() < t_end:
+        step(warmup)
+        warmup += 1
+        stream.synchronize()
     start.record(native)
     for i in range(steps):
         step(warmup + i)
@@ -447,6 +463,7 @@ def main():
         line["cpu_baseline"] = cpu_baseline(args.cpu_rows)
     if not args.no_extras:
         line["extras"] = extras(args.steps)
+        line["extras_settle_ms"] = GRAPH_SETTLE_MS
     print(json.dumps(line), flush=True)
 
 

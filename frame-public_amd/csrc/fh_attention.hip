@@ -29,6 +29,7 @@
 // LDS: 32 KB per workgroup (two K and two V blocks), so two workgroups share a CU.
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <string>
 
 #include "fh_common.h"
@@ -57,7 +58,12 @@ __device__ __forceinline__ float lo16(uint32_t v) { return load_lo<T>(v); }
 template <typename T>
 __device__ __forceinline__ float hi16(uint32_t v) { return load_hi<T>(v); }
 
-template <typename T, int NB, int W>
+// POW2: scale is a power of two (1/sqrt(dh) for dh = 64, 256, ...). Then round(S) * scale is exact, so
+// round(round(S) * scale) = round(S) * scale: pass 1 keeps round(S) and the maximum of the fp32 sums, and the
+// scale moves into the exponent's constant, scale log2(e) = scale * round(log2(e)) exactly, which gives the same
+// fma arguments bit for bit. (Products that fall into T's denormal range are the exception: they lose bits in
+// the reference's rounding; their exponentials are 1 to within an fp32 rounding either way.)
+template <typename T, int NB, int W, bool POW2>
 __global__ __launch_bounds__(W * 64, 2) void attention_kernel(const uint16_t* __restrict__ q, const uint16_t* __restrict__ k,
                                                               const uint16_t* __restrict__ v, uint16_t* __restrict__ out,
                                                               int heads, float scale) {
@@ -99,7 +105,7 @@ __global__ __launch_bounds__(W * 64, 2) void attention_kernel(const uint16_t* __
 
   // ---- 1. scores, kept as packed 16-bit values: s2[t][j] = keys (x = 2j, 2j + 1) of tile t ----
   uint32_t s2[NT][8];
-  float mraw = -__builtin_inff();  // maximum of the scaled scores before their rounding
+  float mraw = -__builtin_inff();  // maximum of the scaled scores (POW2: of the sums) before their rounding
 #pragma unroll
   for (int blk = 0; blk < NB; ++blk) {
     if (blk + 1 < NB) wait_vmcnt<LOADS>(); else wait_vmcnt<0>();
@@ -130,17 +136,24 @@ __global__ __launch_bounds__(W * 64, 2) void attention_kernel(const uint16_t* __
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const uint32_t sr = pack2<T>(acc[t][2 * j], acc[t][2 * j + 1]);  // round(S), two keys
-        const float a0 = lo16<T>(sr) * scale, a1 = hi16<T>(sr) * scale;
-        mraw = fmaxf(mraw, fmaxf(a0, a1));
-        s2[2 * blk + t][j] = pack2<T>(a0, a1);                         // round(S * scale)
+        if constexpr (POW2) {
+          mraw = fmaxf(mraw, fmaxf(acc[t][2 * j], acc[t][2 * j + 1]));
+          s2[2 * blk + t][j] = sr;
+        } else {
+          const float a0 = lo16<T>(sr) * scale, a1 = hi16<T>(sr) * scale;
+          mraw = fmaxf(mraw, fmaxf(a0, a1));
+          s2[2 * blk + t][j] = pack2<T>(a0, a1);                         // round(S * scale)
+        }
         asm volatile("" : "+v"(s2[2 * blk + t][j]));  // pass 3 unpacks; nothing of a0, a1 stays live
       }
   }
 
   // ---- 2. row maximum ----
-  const float m = Io<T>::round(fmaxf(mraw, __shfl_xor(mraw, 32)));
   constexpr float kLog2e = 1.44269504088896340736f;
-  const float ml = m * kLog2e;  // exp(x - m) = exp2(x log2(e) - ml)
+  const float mr = Io<T>::round(fmaxf(mraw, __shfl_xor(mraw, 32)));
+  const float m = POW2 ? mr * scale : mr;
+  const float ml = m * kLog2e;                      // exp(x - m) = exp2(x log2(e) - ml)
+  const float c = POW2 ? scale * kLog2e : kLog2e;   // x = c-scaled stored value
 
   // ---- 3. Oᵀ = Vᵀ·Pᵀ, two 32-row d tiles ----
   f32x16_t acc_o[2];
@@ -167,8 +180,8 @@ __global__ __launch_bounds__(W * 64, 2) void attention_kernel(const uint16_t* __
         for (int j = 0; j < 4; ++j) {
           uint32_t w = s2[t][4 * hf + j];
           asm volatile("" : "+v"(w));  // keeps the exp of this tile here, after the block's barrier
-          const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(lo16<T>(w), kLog2e, -ml));
-          const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(hi16<T>(w), kLog2e, -ml));
+          const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(lo16<T>(w), c, -ml));
+          const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(hi16<T>(w), c, -ml));
           part[4 * hf + j] = e0 + e1;
           pf[hf][j] = pack2<T>(e0, e1);
         }
@@ -243,12 +256,17 @@ extern "C" fh_status fh_attention_fwd(int32_t dtype, const void* q, const void* 
   const dim3 grid(static_cast<uint32_t>(seq / (32 * w)), static_cast<uint32_t>(heads), static_cast<uint32_t>(batch));
   const bool bf = dtype == FH_BF16;
   const int hd = static_cast<int>(heads);
+  int e2 = 0;
+  const bool pow2 = std::isfinite(scale) && scale > 0.0f && std::frexp(scale, &e2) == 0.5f && e2 > -60 && e2 < 60;
   auto go = [&]<int NB>() {
     constexpr int W = (NB * 64) % 128 == 0 ? 4 : 2;
+    auto launch = [&]<typename T, bool P>() {
+      hipLaunchKernelGGL((attention_kernel<T, NB, W, P>), grid, dim3(W * 64), 0, s, qq, kk, vv, oo, hd, scale);
+    };
     if (bf) {
-      hipLaunchKernelGGL((attention_kernel<bf16_t, NB, W>), grid, dim3(W * 64), 0, s, qq, kk, vv, oo, hd, scale);
+      if (pow2) launch.template operator()<bf16_t, true>(); else launch.template operator()<bf16_t, false>();
     } else {
-      hipLaunchKernelGGL((attention_kernel<f16_t, NB, W>), grid, dim3(W * 64), 0, s, qq, kk, vv, oo, hd, scale);
+      if (pow2) launch.template operator()<f16_t, true>(); else launch.template operator()<f16_t, false>();
     }
   };
   switch (nb) {

@@ -825,10 +825,11 @@ def test_conv2d_c8(hip, dtype, geom, with_bias):
 
 # ---- fused attention ------------------------------------------------------------------------------------
 
-def attention_oracle(dtype, q, k, v, batch, seq, heads, dh):
+def attention_oracle(dtype, q, k, v, batch, seq, heads, dh, scale_value=None):
     """The reference's per-(batch, head) decomposition (src/nn/layers.cpp:1014-1080) evaluated node by node
     with the oracle: matmul(Q_bh, K_bh^T) -> mul by the 1/sqrt(dh) splat -> softmax -> matmul(., V_bh)."""
-    scale = synth.to_storage(np.full((seq, seq), 1.0 / np.sqrt(dh), np.float32), dtype)
+    sv = 1.0 / np.sqrt(dh) if scale_value is None else scale_value
+    scale = synth.to_storage(np.full((seq, seq), sv, np.float32), dtype)
     out = np.empty_like(q)
     for b in range(batch):
         rows = slice(b * seq, (b + 1) * seq)
@@ -844,7 +845,8 @@ def attention_oracle(dtype, q, k, v, batch, seq, heads, dh):
 
 
 ATTENTION_CASES = [
-    # dtype, batch, seq, heads, input std
+    # dtype, batch, seq, heads, input std[, scale]: 1/sqrt(64) = 0.125 is a power of two, which the kernel
+    # folds into the exponent; the cases with 0.1 take its general path (round(round(S) * scale))
     (BF16, 2, 64, 2, 1.0),    # one 64-key tile per wave half; score-row swizzle over 8 chunks
     (BF16, 1, 128, 3, 1.0),   # 16 chunks per score row
     (BF16, 2, 192, 2, 1.0),   # 24 chunks: not a multiple of 16
@@ -853,22 +855,28 @@ ATTENTION_CASES = [
     (BF16, 1, 256, 2, 3.0),   # wide score range: most probabilities underflow to 0
     (F16, 2, 256, 2, 1.0),
     (F16, 1, 512, 1, 0.5),
+    (BF16, 1, 512, 2, 1.0, 0.1),
+    (BF16, 2, 192, 1, 3.0, 0.1),
+    (F16, 1, 320, 2, 1.0, 0.1),
 ]
 
 
-@pytest.mark.parametrize("dtype,batch,seq,heads,std", ATTENTION_CASES)
-def test_attention_matches_decomposition(hip, dtype, batch, seq, heads, std):
+@pytest.mark.parametrize("case", ATTENTION_CASES, ids=lambda c: "-".join(str(x) for x in c))
+def test_attention_matches_decomposition(hip, case):
+    dtype, batch, seq, heads, std = case[:5]
+    scale_value = case[5] if len(case) > 5 else None
     dh = 64
-    say(f"attention dtype={dtype} batch={batch} seq={seq} heads={heads} std={std}")
+    say(f"attention dtype={dtype} batch={batch} seq={seq} heads={heads} std={std} scale={scale_value}")
     assert hip.lib().fh_attention_supported(dtype, seq, dh) == 1
     shape = (batch * seq, heads * dh)
     q = synth.tensor(141, shape, dtype, "normal", std)
     k = synth.tensor(142, shape, dtype, "normal", std)
     v = synth.tensor(143, shape, dtype, "normal")
-    want = attention_oracle(dtype, q, k, v, batch, seq, heads, dh)
+    want = attention_oracle(dtype, q, k, v, batch, seq, heads, dh, scale_value)
     dq, dk, dv = dev(hip, q), dev(hip, k), dev(hip, v)
     dout = hip.DeviceBuffer(want.nbytes)
-    scale = float(synth.to_float(synth.to_storage(np.array([1.0 / np.sqrt(dh)], np.float32), dtype), dtype)[0])
+    sv = 1.0 / np.sqrt(dh) if scale_value is None else scale_value
+    scale = float(synth.to_float(synth.to_storage(np.array([sv], np.float32), dtype), dtype)[0])
     hip.check(hip.lib().fh_attention_fwd(dtype, dq.value, dk.value, dv.value, dout.value, batch, seq, heads, dh,
                                          scale, None), "fh_attention_fwd")
     got = dout.download(want.shape, want.dtype)
