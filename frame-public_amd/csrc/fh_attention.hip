@@ -31,6 +31,7 @@
 
 #include <cmath>
 #include <string>
+#include <utility>
 
 #include "fh_common.h"
 #include "fh_gemm.h"
@@ -71,8 +72,10 @@ __global__ __launch_bounds__(W * 64, 2) void attention_kernel(const uint16_t* __
   constexpr int NT = SEQ / 32;  // 32-key tiles
   constexpr int BLK = 64 * 128;  // one 64-key block of K or V, bytes
   constexpr int LOADS = 8 / W;   // 1 KB global->LDS instructions per wave and block
-  __shared__ __attribute__((aligned(1024))) unsigned char kb[2 * BLK];
-  __shared__ __attribute__((aligned(1024))) unsigned char vb[2 * BLK];
+  static_assert(LOADS * NB < 64, "vmcnt range");
+  // Slot b holds K block b, then V block b: every K block is requested at the start, and V block b goes into
+  // slot b as soon as every wave has read K block b, so V is resident well before pass 3 reads it.
+  __shared__ __attribute__((aligned(1024))) unsigned char kv[NB * BLK];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -87,66 +90,90 @@ __global__ __launch_bounds__(W * 64, 2) void attention_kernel(const uint16_t* __
 #pragma unroll
   for (int s = 0; s < 4; ++s)
     qf[s] = *reinterpret_cast<const u32x4_t*>(q + base + static_cast<int64_t>(q0 + l32) * ld + 16 * s + 8 * hi);
+  // the vmcnt counts below count the K / V loads only: the Q loads stay ahead of them (loads retire in order)
+  asm volatile("" ::: "memory");
 
   // block loaders: instruction i of a block = rows 8i .. 8i + 7, lane -> (row 8i + lane / 8, physical chunk lane % 8)
-  auto load_block = [&](const uint16_t* src, unsigned char* ring, int blk, int buf, bool is_v) {
+  auto load_block = [&](const uint16_t* src, int blk, bool is_v) {
 #pragma unroll
     for (int j = 0; j < LOADS; ++j) {
       const int i = wave + W * j;
       const int row = 8 * i + (lane >> 3), pc = lane & 7;
       const int c = is_v ? v_chunk(row, pc) : k_chunk(row, pc);
       const uint16_t* g = src + base + static_cast<int64_t>(blk * 64 + row) * ld + c * 8;
-      __builtin_amdgcn_global_load_lds(g, (FH_LDS void*)(ring + buf * BLK + i * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(g, (FH_LDS void*)(kv + blk * BLK + i * 1024), 16, 0, 0);
     }
   };
+  // The LDS reads below are inline asm the compiler does not order against the LDS-DMA loads (its own tracking
+  // would wait for every load in flight at each read or barrier), so the kernel orders them itself: a block is
+  // read after this wave's vmcnt wait for it and an s_barrier (every wave's share landed), and a slot is
+  // refilled only after a barrier that every wave reached with its reads of the slot complete (lgkmcnt(0)).
+  auto barrier = [] {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  const uint32_t kv_addr = lds_addr((const FH_LDS void*)kv);
 
-  load_block(k, kb, 0, 0, false);
-  if (NB > 1) load_block(k, kb, 1, 1, false);
+#pragma unroll
+  for (int blk = 0; blk < NB; ++blk) load_block(k, blk, false);
+
+  // K fragment of (k-slice s, key tile t) for this lane: row 32 t + l32, chunk 2 s + hi; the swizzle uses row & 7
+  // = l32 & 7 only, so tile t adds 32 rows = 4096 bytes
+  uint32_t k_off[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) k_off[s] = kv_addr + l32 * 128 + k_chunk(l32, 2 * s + hi) * 16;
 
   // ---- 1. scores, kept as packed 16-bit values: s2[t][j] = keys (x = 2j, 2j + 1) of tile t ----
   uint32_t s2[NT][8];
   float mraw = -__builtin_inff();  // maximum of the scaled scores (POW2: of the sums) before their rounding
+  [&]<int... B_>(std::integer_sequence<int, B_...>) {
+    (
+        [&] {
+          constexpr int blk = B_;
+          // this wave's loads of K block blk have landed when no more than the ones issued after them are in
+          // flight: K blocks blk+1 .. NB-1 and V blocks 0 .. blk-2
+          wait_vmcnt<LOADS * ((NB - 1 - blk) + (blk >= 2 ? blk - 1 : 0))>();
+          barrier();
+          if constexpr (blk >= 1) load_block(v, blk - 1, true);  // every wave has read K block blk - 1
+          u32x4_t kf[4][2];
 #pragma unroll
-  for (int blk = 0; blk < NB; ++blk) {
-    if (blk + 1 < NB) wait_vmcnt<LOADS>(); else wait_vmcnt<0>();
-    __syncthreads();
-    const unsigned char* kr = kb + (blk & 1) * BLK;
-    f32x16_t acc[2];
+          for (int s = 0; s < 4; ++s) {
+            kf[s][0] = lds_read_b128<blk * BLK>(k_off[s]);
+            kf[s][1] = lds_read_b128<blk * BLK + 4096>(k_off[s]);
+          }
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+          for (int s = 0; s < 4; ++s) asm volatile("" : "+v"(kf[s][0]), "+v"(kf[s][1]));
+          f32x16_t acc[2];
 #pragma unroll
-      for (int x = 0; x < 16; ++x) acc[t][x] = 0.0f;
+          for (int t = 0; t < 2; ++t)
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
+            for (int x = 0; x < 16; ++x) acc[t][x] = 0.0f;
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int row = 32 * t + l32;
-        const u32x4_t a = *reinterpret_cast<const u32x4_t*>(kr + row * 128 + k_chunk(row, 2 * s + hi) * 16);
-        mfma32<T>(a, qf[s], acc[t]);
-      }
-    }
-    __syncthreads();  // every wave is done with this K buffer
-    if (blk + 2 < NB) load_block(k, kb, blk + 2, blk & 1, false);
-    if (blk + 1 == NB) {  // the K stream is over: start V
-      load_block(v, vb, 0, 0, true);
-      if (NB > 1) load_block(v, vb, 1, 1, true);
-    }
+          for (int s = 0; s < 4; ++s)
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
+            for (int t = 0; t < 2; ++t) mfma32<T>(kf[s][t], qf[s], acc[t]);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const uint32_t sr = pack2<T>(acc[t][2 * j], acc[t][2 * j + 1]);  // round(S), two keys
-        if constexpr (POW2) {
-          mraw = fmaxf(mraw, fmaxf(acc[t][2 * j], acc[t][2 * j + 1]));
-          s2[2 * blk + t][j] = sr;
-        } else {
-          const float a0 = lo16<T>(sr) * scale, a1 = hi16<T>(sr) * scale;
-          mraw = fmaxf(mraw, fmaxf(a0, a1));
-          s2[2 * blk + t][j] = pack2<T>(a0, a1);                         // round(S * scale)
-        }
-        asm volatile("" : "+v"(s2[2 * blk + t][j]));  // pass 3 unpacks; nothing of a0, a1 stays live
-      }
-  }
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const uint32_t sr = pack2<T>(acc[t][2 * j], acc[t][2 * j + 1]);  // round(S), two keys
+              if constexpr (POW2) {
+                mraw = fmaxf(mraw, fmaxf(acc[t][2 * j], acc[t][2 * j + 1]));
+                s2[2 * blk + t][j] = sr;
+              } else {
+                const float a0 = lo16<T>(sr) * scale, a1 = hi16<T>(sr) * scale;
+                mraw = fmaxf(mraw, fmaxf(a0, a1));
+                s2[2 * blk + t][j] = pack2<T>(a0, a1);  // round(S * scale)
+              }
+              asm volatile("" : "+v"(s2[2 * blk + t][j]));  // pass 3 unpacks; nothing of a0, a1 stays live
+            }
+        }(),
+        ...);
+  }(std::make_integer_sequence<int, NB>{});
+  barrier();  // every wave has read K block NB - 1
+  load_block(v, NB - 1, true);
 
   // ---- 2. row maximum ----
   constexpr float kLog2e = 1.44269504088896340736f;
@@ -162,55 +189,72 @@ __global__ __launch_bounds__(W * 64, 2) void attention_kernel(const uint16_t* __
 #pragma unroll
     for (int x = 0; x < 16; ++x) acc_o[dt][x] = 0.0f;
   // transpose reads: group g = lane / 16 covers d columns 16 (g & 1) .. + 15 of a d tile and the key half
-  // g >> 1; source lane qd + 4 e of the group points at key row (kbase + e), columns n0 + 4 qd .. + 3
+  // g >> 1; source lane qd + 4 e of the group points at key row (kbase + e), columns n0 + 4 qd .. + 3. The key
+  // row is 32 tt + 16 hf + 4 (g >> 1) + 8 part + e, so its swizzle (row & 3 = e) is the same for every read and
+  // tt, hf, part add whole rows.
   const int g = lane >> 4, rr = lane & 15, qd = rr & 3, e = rr >> 2;
-  float sum = 0.0f;
+  uint32_t v_off[2];
 #pragma unroll
-  for (int blk = 0; blk < NB; ++blk) {
-    if (blk + 1 < NB) wait_vmcnt<LOADS>(); else wait_vmcnt<0>();
-    __syncthreads();
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-      const int t = 2 * blk + tt;
-      u32x4_t pf[2];
-      float part[8];
-#pragma unroll
-      for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          uint32_t w = s2[t][4 * hf + j];
-          asm volatile("" : "+v"(w));  // keeps the exp of this tile here, after the block's barrier
-          const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(lo16<T>(w), c, -ml));
-          const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(hi16<T>(w), c, -ml));
-          part[4 * hf + j] = e0 + e1;
-          pf[hf][j] = pack2<T>(e0, e1);
-        }
-      // the tile's sum joins the running sum here (tied), so no tile's exponentials outlive the tile
-      sum += ((part[0] + part[1]) + (part[2] + part[3])) + ((part[4] + part[5]) + (part[6] + part[7]));
-      asm volatile("" : "+v"(sum));
-#pragma unroll
-      for (int dt = 0; dt < 2; ++dt) {
-        const int n0 = 32 * dt + 16 * (g & 1) + 4 * qd;
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf) {
-          // keys of this MFMA for k-half g >> 1: 32 tt + 16 hf + 4 (g >> 1) + {0..3, 8..11}
-          u32x4_t a;
-#pragma unroll
-          for (int part = 0; part < 2; ++part) {
-            const int krow = 32 * tt + 16 * hf + 4 * (g >> 1) + 8 * part + e;
-            const uint32_t off = krow * 128 + v_chunk(krow, n0 >> 3) * 16 + (n0 & 7) * 2;
-            const s16x4_t tr = __builtin_amdgcn_ds_read_tr16_b64_v4i16((FH_LDS s16x4_t*)(vb + (blk & 1) * BLK + off));
-            const u32x2_t t2 = __builtin_bit_cast(u32x2_t, tr);
-            a[2 * part] = t2[0];
-            a[2 * part + 1] = t2[1];
-          }
-          mfma32<T>(a, pf[hf], acc_o[dt]);
-        }
-      }
-    }
-    __syncthreads();
-    if (blk + 2 < NB) load_block(v, vb, blk + 2, blk & 1, true);
+  for (int dt = 0; dt < 2; ++dt) {
+    const int n0 = 32 * dt + 16 * (g & 1) + 4 * qd;
+    const int krow = 4 * (g >> 1) + e;
+    v_off[dt] = kv_addr + krow * 128 + v_chunk(krow, n0 >> 3) * 16 + (n0 & 7) * 2;
   }
+  float sum = 0.0f;
+  wait_vmcnt<LOADS>();  // this wave's V blocks 0 .. NB-2
+  barrier();
+  [&]<int... B_>(std::integer_sequence<int, B_...>) {
+    (
+        [&] {
+          constexpr int blk = B_;
+          if constexpr (blk == NB - 1) {
+            wait_vmcnt<0>();
+            barrier();
+          }
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt) {
+            const int t = 2 * blk + tt;
+            // this tile's V fragments first, so the exponentials below run while they are in flight
+            u32x2_t vf[2][2][2];
+            [&]<int... R_>(std::integer_sequence<int, R_...>) {
+              (
+                  [&] {
+                    constexpr int dt = R_ / 4, hf = (R_ / 2) % 2, part = R_ % 2;
+                    constexpr int off = blk * BLK + (16 * hf + 8 * part) * 128;
+                    vf[dt][hf][part] = lds_read_tr16_b64<off>(v_off[dt] + tt * 32 * 128);
+                  }(),
+                  ...);
+            }(std::make_integer_sequence<int, 8>{});
+            u32x4_t pf[2];
+            float part[8];
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                uint32_t w = s2[t][4 * hf + j];
+                asm volatile("" : "+v"(w));  // keeps the exp of this tile here, after the block's barrier
+                const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(lo16<T>(w), c, -ml));
+                const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(hi16<T>(w), c, -ml));
+                part[4 * hf + j] = e0 + e1;
+                pf[hf][j] = pack2<T>(e0, e1);
+              }
+            // the tile's sum joins the running sum here (tied), so no tile's exponentials outlive the tile
+            sum += ((part[0] + part[1]) + (part[2] + part[3])) + ((part[4] + part[5]) + (part[6] + part[7]));
+            asm volatile("" : "+v"(sum));
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+              for (int hf = 0; hf < 2; ++hf) {
+                asm volatile("" : "+v"(vf[dt][hf][0]), "+v"(vf[dt][hf][1]));
+                // keys of this MFMA for k-half g >> 1: 32 tt + 16 hf + 4 (g >> 1) + {0..3, 8..11}
+                const u32x4_t a{vf[dt][hf][0][0], vf[dt][hf][0][1], vf[dt][hf][1][0], vf[dt][hf][1][1]};
+                mfma32<T>(a, pf[hf], acc_o[dt]);
+              }
+          }
+        }(),
+        ...);
+  }(std::make_integer_sequence<int, NB>{});
 
   // ---- output: acc_o[dt][x] = O[query q0 + l32][d = 32 dt + 8 (x / 4) + 4 hi + x % 4] ----
   sum += __shfl_xor(sum, 32);
