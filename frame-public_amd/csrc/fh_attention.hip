@@ -160,7 +160,11 @@ __global__ __launch_bounds__(W * 64, 2) void attention_kernel(const uint16_t* __
             for (int j = 0; j < 8; ++j) {
               const uint32_t sr = pack2<T>(acc[t][2 * j], acc[t][2 * j + 1]);  // round(S), two keys
               if constexpr (POW2) {
-                mraw = fmaxf(mraw, fmaxf(acc[t][2 * j], acc[t][2 * j + 1]));
+                // max(mraw, a, b) in one instruction: fmaxf on the raw MFMA results would first canonicalise
+                // each of them (the compiler cannot prove an MFMA result is not a signalling NaN; it never is)
+                float mx;
+                asm("v_max3_f32 %0, %1, %2, %3" : "=v"(mx) : "v"(mraw), "v"(acc[t][2 * j]), "v"(acc[t][2 * j + 1]));
+                mraw = mx;
                 s2[2 * blk + t][j] = sr;
               } else {
                 const float a0 = lo16<T>(sr) * scale, a1 = hi16<T>(sr) * scale;
