@@ -219,17 +219,20 @@ def test_c5_transformer_fused_attention(dev, opt_level):
 
 
 def test_c5_transformer_full_rows(dev):
-    say("C5 transformer bf16 batch=8 seq=512 (sequence 0 checked)")
+    say("C5 transformer bf16 batch=8 seq=512 (sequences 0 and 7 checked)")
     g, shapes = graphs.transformer_block(dtype=BF16, device="hip")
     ins = graphs.transformer_inputs(shapes, dtype=BF16)
     (got,) = run_hip(g, ins)
     assert got.shape == (4096, 1024) and np.isfinite(synth.to_float(got, BF16)).all()
     g1, shapes1 = graphs.transformer_block(batch=1, dtype=BF16, device="cpu")
-    # x and the full-shape biases (bq, bk, bv, bo, b1, b2) are per-row; weights and LayerNorm parameters are shared
+    # x and the full-shape biases (bq, bk, bv, bo, b1, b2) are per-row; weights and LayerNorm parameters are shared.
+    # The first and the last sequence: the attention's and the biases' batch offsets are exercised at both ends.
     per_row = {0, 4, 6, 8, 10, 14, 16}
-    ins1 = [a[:512] if i in per_row else a for i, a in enumerate(ins)]
-    (want,) = orc.run_graph_cpu(g1, ins1)
-    assert_close(got[:512], want, BF16, what="transformer sequence 0")
+    for sq in (0, 7):
+        rows = slice(512 * sq, 512 * (sq + 1))
+        ins1 = [a[rows] if i in per_row else a for i, a in enumerate(ins)]
+        (want,) = orc.run_graph_cpu(g1, ins1)
+        assert_close(got[rows], want, BF16, what=f"transformer sequence {sq}")
 
 
 # ---- graph replay (HipExecutable captures its steps on the second run with the same addresses) -----------------
