@@ -1368,6 +1368,21 @@ __global__ __launch_bounds__(256) void pack_input_c8_kernel(const uint16_t* __re
   }
 }
 
+// The same packing with the image from blockIdx.y: 32-bit, division-free index math; a wave's plane loads
+// and its 16-byte stores are each one contiguous run.
+__global__ __launch_bounds__(256) void pack_input_c8_2d_kernel(const uint16_t* __restrict__ x, uint4* __restrict__ y,
+                                                               int32_t c, int32_t hw) {
+  const int32_t pix = static_cast<int32_t>(blockIdx.x) * 256 + static_cast<int32_t>(threadIdx.x);
+  if (pix >= hw) return;
+  const int64_t img = blockIdx.y;
+  const uint16_t* src = x + img * c * hw + pix;
+  uint32_t d[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int ch = 0; ch < 8; ++ch)
+    if (ch < c) d[ch / 2] |= static_cast<uint32_t>(src[static_cast<int64_t>(ch) * hw]) << (16 * (ch % 2));
+  y[img * hw + pix] = uint4{d[0], d[1], d[2], d[3]};
+}
+
 // w [Cout][C][KH*KW] (C <= 8) -> y [Cout][K] with y[co][pos*8 + ci] = w[co][ci][pos], zeros elsewhere.
 __global__ __launch_bounds__(256) void pack_filter_c8_kernel(const uint16_t* __restrict__ w, uint16_t* __restrict__ y,
                                                              int32_t cout, int32_t c, int32_t khw, int32_t k) {
@@ -1582,6 +1597,12 @@ extern "C" fh_status fh_conv_pack_input_c8(const void* x, void* y, int64_t n, in
   if (n < 0 || hw < 0 || c < 1 || c > 8) return fail(FH_INVALID_ARGUMENT, "fh_conv_pack_input_c8: needs 1 <= C <= 8");
   if (n * hw == 0) return FH_OK;
   if (x == nullptr || y == nullptr || !aligned16(y)) return fail(FH_INVALID_ARGUMENT, "fh_conv_pack_input_c8: bad pointer");
+  if (n <= 65535 && hw < (int64_t{1} << 31)) {
+    const dim3 grid(static_cast<uint32_t>((hw + 255) / 256), static_cast<uint32_t>(n));
+    hipLaunchKernelGGL(pack_input_c8_2d_kernel, grid, dim3(256), 0, static_cast<hipStream_t>(stream),
+                       static_cast<const uint16_t*>(x), static_cast<uint4*>(y), c, static_cast<int32_t>(hw));
+    return launch_status("pack_input_c8_2d_kernel launch");
+  }
   int64_t blocks = (n * hw + 255) / 256;
   blocks = blocks > 256LL * 16 ? 256LL * 16 : blocks;
   hipLaunchKernelGGL(pack_input_c8_kernel, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0,

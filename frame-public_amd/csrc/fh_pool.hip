@@ -204,7 +204,9 @@ struct PoolGeom32 {
   int32_t n, c, h, w, kh, kw, sh, sw, ph, pw, oh, ow;
 };
 
-template <typename T, int MODE, int VW>
+// KWF: the window width when it is fixed at compile time (3 for the ResNet stem pool), so a row takes exactly
+// that many loads; 0: any width, loaded 8 columns at a time.
+template <typename T, int MODE, int VW, int KWF = 0>
 __global__ __launch_bounds__(256) void pool2d_nhwc_kernel(const typename Io<T>::storage* __restrict__ x,
                                                           typename Io<T>::storage* __restrict__ y, PoolGeom32 g) {
   using S = typename Io<T>::storage;
@@ -226,11 +228,12 @@ __global__ __launch_bounds__(256) void pool2d_nhwc_kernel(const typename Io<T>::
       const int ih = oh * g.sh - g.ph + a;
       if (ih < 0 || ih >= g.h) continue;
       const S* row = x + (static_cast<int64_t>(n * g.h + ih) * g.w) * g.c + cg * VW;
-      for (int b0 = 0; b0 < g.kw; b0 += 8) {
-        Vec vals[8];
-        bool ok[8];
+      constexpr int U = KWF > 0 ? KWF : 8;
+      for (int b0 = 0; b0 < g.kw; b0 += U) {
+        Vec vals[U];
+        bool ok[U];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < U; ++u) {
           const int iw = ow * g.sw - g.pw + b0 + u;
           ok[u] = b0 + u < g.kw && iw >= 0 && iw < g.w;
           const int iwc = iw < 0 ? 0 : (iw >= g.w ? g.w - 1 : iw);  // clamped: the load is unconditional
@@ -244,7 +247,7 @@ __global__ __launch_bounds__(256) void pool2d_nhwc_kernel(const typename Io<T>::
           }
         }
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
+        for (int u = 0; u < U; ++u) {
           if (!ok[u]) continue;
 #pragma unroll
           for (int e = 0; e < VW; ++e) {
@@ -292,7 +295,10 @@ fh_status launch_pool_nhwc(int32_t mode, const void* x, void* y, const PoolGeom&
   const dim3 grid(static_cast<uint32_t>(blocks));
   const auto* xs = static_cast<const S*>(x);
   auto* ys = static_cast<S*>(y);
-  if (vec) {
+  if (vec && g.kw == 3) {
+    if (mode == 0) hipLaunchKernelGGL((pool2d_nhwc_kernel<T, 0, V, 3>), grid, dim3(256), 0, s, xs, ys, g32);
+    else hipLaunchKernelGGL((pool2d_nhwc_kernel<T, 1, V, 3>), grid, dim3(256), 0, s, xs, ys, g32);
+  } else if (vec) {
     if (mode == 0) hipLaunchKernelGGL((pool2d_nhwc_kernel<T, 0, V>), grid, dim3(256), 0, s, xs, ys, g32);
     else hipLaunchKernelGGL((pool2d_nhwc_kernel<T, 1, V>), grid, dim3(256), 0, s, xs, ys, g32);
   } else {

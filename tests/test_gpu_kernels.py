@@ -739,6 +739,7 @@ def test_conv2d_nhwc_channels_last_output(hip, dtype, geom):
     (1, (1, 16, 6, 6, 3, 3, 2, 2, 1, 1)),     # average with padding counted
     (0, (1, 16, 12, 12, 10, 10, 1, 1, 0, 0)), # window rows wider than one batch of 8 loads
     (1, (1, 24, 12, 12, 10, 9, 1, 1, 1, 0)),
+    (0, (2, 8, 17, 15, 3, 3, 2, 2, 1, 1)),    # 3-wide rows (the fixed-width kernel), odd sizes: padded edges
 ])
 def test_pool2d_nhwc(hip, dtype, mode, geom):
     say(f"pool nhwc mode={mode} dtype={dtype} {geom}")
@@ -748,6 +749,35 @@ def test_pool2d_nhwc(hip, dtype, mode, geom):
     dx, dy = dev(hip, to_nhwc(x)), hip.DeviceBuffer(want.nbytes)
     hip.check(hip.lib().fh_pool2d_nhwc(dtype, mode, dx.value, dy.value, hip.i64_array(geom), None))
     assert_bitwise(dy.download(want.shape, want.dtype), want, f"pool nhwc mode={mode}")
+
+
+@pytest.mark.parametrize("dtype", [BF16, F16])
+def test_maxpool_nhwc_signed_zero_and_nan_selection(hip, dtype):
+    # the channels-last 3x3 stride-2 kernel keeps the reference's scan order: of equal +0/-0 the first stays, a
+    # NaN stays only where it is scanned first, otherwise the comparisons skip it
+    geom = (1, 16, 10, 12, 3, 3, 2, 2, 1, 1)
+    x = synth.tensor(87, geom[:4], dtype, "normal")
+    neg0, pos0, nan = (synth.to_storage(np.array([v], np.float32), dtype)[0] for v in (-0.0, 0.0, np.nan))
+    x[0, :8] = pos0
+    x[0, :8, 0::2, 0::2] = neg0
+    x[0, 8:, 3, 5] = nan
+    x[0, 8:, 0, 0] = nan
+    want = to_nhwc(orc.pool2d(dtype, 0, x, geom))
+    dx, dy = dev(hip, to_nhwc(x)), hip.DeviceBuffer(want.nbytes)
+    hip.check(hip.lib().fh_pool2d_nhwc(dtype, 0, dx.value, dy.value, hip.i64_array(geom), None))
+    assert_bitwise(dy.download(want.shape, want.dtype), want, "maxpool nhwc special values")
+
+
+@pytest.mark.parametrize("n,c,hw", [(3, 3, 224 * 8), (2, 1, 64), (1, 8, 40), (2, 3, 50), (1, 5, 7), (4, 3, 300)])
+def test_conv_pack_input_c8(hip, n, c, hw):
+    # [N][C][HW] -> [N][HW][8] with channels C..7 zero (one pixel per thread, the image from the grid's y)
+    say(f"pack input c8 n={n} c={c} hw={hw}")
+    x = np.random.default_rng(hw + c).integers(0, 65536, size=(n, c, hw), dtype=np.uint16)
+    want = np.zeros((n, hw, 8), np.uint16)
+    want[:, :, :c] = x.transpose(0, 2, 1)
+    dx, dy = dev(hip, x), hip.DeviceBuffer(want.nbytes)
+    hip.check(hip.lib().fh_conv_pack_input_c8(dx.value, dy.value, n, c, hw, None))
+    assert_bitwise(dy.download(want.shape, np.uint16), want, "pack c8")
 
 
 @pytest.mark.parametrize("dtype", [BF16, F32])
