@@ -13,8 +13,8 @@
 // the stored probabilities.
 //
 // One wave owns 32 queries and all seq keys; a workgroup is W waves (4, or 2 when seq is not a multiple of 128).
-// The work is VALU-bound (about 11 VALU operations per score against two MFMA k-steps per 32 x 32 tile), so the
-// per-score code is kept short.
+// The work is bound by its VALU instruction stream (about 7 VALU instructions per score, one of them the
+// quarter-rate exponential, against two MFMA k-steps per 32 x 32 tile), so the per-score code is kept short.
 //  1. Scores transposed, Sᵀ = K·Qᵀ on v_mfma_f32_32x32x16, per 64-key block: K blocks stream through a
 //     double-buffered 8 KB LDS ring (global_load_lds_dwordx4, 16-byte chunks swizzled by row), the Q fragments
 //     stay in registers. Each lane's accumulator then holds one query and 16 keys of a 32-key tile; they are
