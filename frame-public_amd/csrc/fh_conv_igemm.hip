@@ -1117,6 +1117,280 @@ __global__ __launch_bounds__(512, 4) void conv_halo1_kernel(ConvHaloArgs ha) {
   }
 }
 
+// ---- 3x3 stride-1 convolutions over bands of whole output rows, NCHW in and out ---------------------------------
+//
+// For Cin = 64, Cout <= 64, NCHW input and output (a conv on a graph input whose result is a graph output). One
+// workgroup per band of R consecutive output rows of one image, R chosen so the bands spread evenly over the CUs
+// (C3, 32 x 56 rows: R = 7 gives 256 bands of 392 pixels, one per CU; the 256-pixel tiles of the kernel above make
+// 392 tiles, two on some CUs and one on the others). The whole filter (2 chunks x 9 taps x 64 rows x 64 B = 72 KB)
+// and both 32-channel chunks of the band's patch ((R + 2) x (W + 2) positions each) are resident in LDS. Chunk 1's
+// input is loaded into registers before chunk 0 is multiplied and written to LDS after it, so its load overlaps
+// the first multiplications. Patch rows outside the image and the two padding columns hold zeros.
+// The band's pixels (R * W <= 512) go in two phases of 32-pixel tiles, one tile per wave and phase, all 64 output
+// channels each: band pixels 0-255, then 256 onwards (waves without a tile skip the phase). A tile's result is
+// written from registers as soon as its phase ends, so phase 0's stores drain while phase 1 multiplies (no LDS
+// staging, which would need space the resident operands fill). The products and their order per output are
+// those of the kernels above (chunk, tap, k16 half), so the result is the same bit for bit.
+constexpr int kBandPatchBytes = 34 * 1024;  // one chunk's patch: (R + 2) * (W + 2) positions of 64 B
+
+struct ConvBandArgs {
+  ConvNhwcArgs c;
+  int32_t rows;           // R: output rows per band, a divisor of H
+  int32_t bands_per_img;  // H / R
+};
+
+template <typename T, int E>
+__global__ __launch_bounds__(512) void conv_band_kernel(ConvBandArgs ba) {
+  const ConvNhwcArgs& args = ba.c;
+  using S = typename Io<T>::storage;
+  static_assert(sizeof(S) == 2, "16-bit operands");
+  constexpr int BM = 64, NW = 8, TM = 2, TAPS = 9;
+  constexpr int A_CHUNK = TAPS * BM * 64;  // [tap][64 rows][32 channels] of one chunk
+  constexpr int A_BYTES = 2 * A_CHUNK;     // Cin = 64: two chunks
+  constexpr int A_PER_WAVE = A_BYTES / 1024 / NW;
+  constexpr int PB = kBandPatchBytes;
+  constexpr int LDS_BYTES = A_BYTES + 2 * PB;
+  static_assert((A_BYTES / 1024) % NW == 0, "filter loads split evenly over the waves");
+  static_assert(LDS_BYTES <= 160 * 1024, "filter and both patches fit the LDS");
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[LDS_BYTES];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int W = args.w_in, H = args.h, R = ba.rows, rw = W + 2;
+  const int npx = R * W;
+  // XCD-aware order: consecutive bands (sharing halo rows) on one XCD's L2
+  int b = blockIdx.x;
+  if ((gridDim.x & 7) == 0) b = (b & 7) * static_cast<int>(gridDim.x >> 3) + (b >> 3);
+  const int img = b / ba.bands_per_img;
+  const int r0 = (b - img * ba.bands_per_img) * R;
+  const int64_t n0 = (static_cast<int64_t>(img) * H + r0) * W;  // first output pixel (flattened n, oh, ow)
+
+  // the filter: 1 KB load j covers chunk j / 36, tap (j / 4) % 9, rows 16 * (j % 4) .. + 15
+  const S* __restrict__ Wt = static_cast<const S*>(args.w);
+#pragma unroll
+  for (int i = 0; i < A_PER_WAVE; ++i) {
+    const int j = wave + NW * i;
+    const int ch = j / (TAPS * 4), tap = (j / 4) % TAPS;
+    const int row = (j % 4) * 16 + (lane >> 2);
+    const int gch = (lane & 3) ^ a_swizzle(row);
+    global_to_lds16(Wt + (min(row, args.cout - 1) * TAPS + tap) * 64 + ch * 32 + gch * 8,
+                    (FH_LDS void*)(lds + j * 1024));
+  }
+  // the padding columns (positions 0 and W + 1 of every patch row) of both patches
+  if (tid < 2 * (R + 2) * 8) {
+    const int buf = tid / ((R + 2) * 8), z = tid % ((R + 2) * 8);
+    const int q = (z >> 3) * rw + ((z >> 2) & 1) * (W + 1);
+    *reinterpret_cast<uint4*>(lds + A_BYTES + buf * PB + q * 64 + (z & 3) * 16) = uint4{0, 0, 0, 0};
+  }
+  // NCHW fill: thread -> (8-channel group ncg, patch row nr, 8-pixel group npg), npg fastest, so the lanes of one
+  // load instruction read one channel plane's (R + 2) band rows, which are contiguous in memory.
+  const int pgroups = W / 8;
+  const int per_cg = (R + 2) * pgroups;
+  const int ncg = tid / per_cg, nr = (tid % per_cg) / pgroups, npg = tid % pgroups;
+  const int ih = r0 - 1 + nr;
+  const bool filler = tid < 4 * per_cg;
+  const bool inside = filler && ih >= 0 && ih < H;
+  const S* __restrict__ Xn = static_cast<const S*>(args.x);
+  const int64_t plane = static_cast<int64_t>(H) * W;
+  const int64_t src = inside ? ((static_cast<int64_t>(img) * 64 + 8 * ncg) * H + ih) * W + 8 * npg : 0;
+  auto load_chunk = [&](int ci0, uint4 (&v)[8]) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      v[e] = uint4{0, 0, 0, 0};
+      if (inside) v[e] = *reinterpret_cast<const uint4*>(Xn + src + (ci0 + e) * plane);
+    }
+  };
+  // transposes the 8 x 8 block in registers and writes 8 positions' 16-byte chunks (zeros outside the image)
+  auto store_chunk = [&](const uint4 (&v)[8], unsigned char* patch) {
+    if (!filler) return;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      uint32_t d[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t lo = reinterpret_cast<const uint32_t*>(&v[2 * k])[i / 2];
+        const uint32_t hi2 = reinterpret_cast<const uint32_t*>(&v[2 * k + 1])[i / 2];
+        d[k] = (i % 2 == 0) ? ((lo & 0xffffu) | (hi2 << 16)) : ((lo >> 16) | (hi2 & 0xffff0000u));
+      }
+      const int q = nr * rw + 1 + 8 * npg + i;
+      *reinterpret_cast<uint4*>(patch + q * 64 + ((ncg ^ ((q >> 2) & 3)) * 16)) = uint4{d[0], d[1], d[2], d[3]};
+    }
+  };
+
+  // filter fragment offsets: channel row 32 i + l32, k-chunk 2 h + hi of the stage
+  int a_off[TM][2];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int arow = i * 32 + l32;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) a_off[i][h] = arow * 64 + (((2 * h + hi) ^ a_swizzle(arow)) * 16);
+  }
+  // the bias of this lane's output channels (32 i + l32), fetched with the first fill
+  const S* bias_g = static_cast<const S*>(args.bias);
+  float bias_v[TM];
+#pragma unroll
+  for (int i = 0; i < TM; ++i) bias_v[i] = bias_g != nullptr ? Io<T>::load(bias_g[min(i * 32 + l32, args.cout - 1)]) : 0.0f;
+
+  const uint32_t ab = lds_addr((const FH_LDS void*)lds);
+  // One chunk of the pixel tile whose tap-(0, 0) patch position for this lane is pb. The MFMA's A operand is the
+  // patch (rows = the tile's 32 pixels) and B the filter (columns = 32 channels), so each lane ends with one
+  // channel's values for runs of four consecutive pixels (see store_tile).
+  auto chunk = [&](f32x16_t (&acc)[TM], int pb, uint32_t a_base, uint32_t p_base) {
+    KFragments<TM, 1> f0, f1;
+    auto read_step = [&]<int STEP>(KFragments<TM, 1>& f) {
+      constexpr int tap = STEP / 2, h = STEP % 2, kh = tap / 3, kw = tap % 3;
+#pragma unroll
+      for (int i = 0; i < TM; ++i) f.a[i] = lds_read_b128<tap * BM * 64>(a_base + a_off[i][h]);
+      const int pos = pb + kh * rw + kw;
+      f.b[0] = lds_read_b128<0>(p_base + pos * 64 + ((((2 * h + hi) ^ ((pos >> 2) & 3))) * 16));
+    };
+    read_step.template operator()<0>(f0);
+    [&]<int... STEP>(std::integer_sequence<int, STEP...>) {
+      (
+          [&] {
+            constexpr int s = STEP;
+            KFragments<TM, 1>& cur = (s % 2 == 0) ? f0 : f1;
+            KFragments<TM, 1>& nxt = (s % 2 == 0) ? f1 : f0;
+            fence_kfragments(cur);
+            if constexpr (s + 1 < 2 * TAPS) read_step.template operator()<s + 1>(nxt);
+#pragma unroll
+            for (int i = 0; i < TM; ++i) mfma32<T>(cur.b[0], cur.a[i], acc[i]);
+            __builtin_amdgcn_sched_barrier(0);
+          }(),
+          ...);
+    }(std::make_integer_sequence<int, 2 * TAPS>{});
+    fence_kfragments(f0);
+    fence_kfragments(f1);
+  };
+  // Writes the pixel tile px0 .. px0 + 31 of the band from registers. Register x of a lane holds pixel
+  // px0 + 8 (x >> 2) + 4 hi + (x & 3) of channel 32 i + l32: the lanes l32 and l32 + 32 exchange one 4-pixel
+  // run each (hi = 0 keeps pixels 0-3 and takes 4-7, hi = 1 takes 8-11 and keeps 12-15; likewise for 16-31),
+  // after which every lane holds two 8-pixel vectors of its channel and writes them with 16-byte stores.
+  S* __restrict__ Y = static_cast<S*>(args.y);
+  const int64_t ybase = static_cast<int64_t>(img) * args.cout * args.howo + static_cast<int64_t>(r0) * W;
+  constexpr int EA = epi_after_stage<E>();
+  auto store_tile = [&](f32x16_t (&acc)[TM], int px0) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int co = i * 32 + l32;
+      const float b = bias_v[i];
+      // runs 2 half and 2 half + 1 (registers 8 half .. 8 half + 7): pixels 16 half + 4 hi + 0..3 and
+      // 16 half + 8 + 4 hi + 0..3, packed pairwise, exchanged into the 8-pixel vector 16 half + 8 hi + 0..7
+      auto vector = [&](int x0) {
+        const uint32_t a0 = epi_stage2<E, T>(acc[i][x0] + b, acc[i][x0 + 1] + b);
+        const uint32_t a1 = epi_stage2<E, T>(acc[i][x0 + 2] + b, acc[i][x0 + 3] + b);
+        const uint32_t c0 = epi_stage2<E, T>(acc[i][x0 + 4] + b, acc[i][x0 + 5] + b);
+        const uint32_t c1 = epi_stage2<E, T>(acc[i][x0 + 6] + b, acc[i][x0 + 7] + b);
+        const uint32_t r0v = static_cast<uint32_t>(__shfl_xor(static_cast<int>(hi ? a0 : c0), 32));
+        const uint32_t r1v = static_cast<uint32_t>(__shfl_xor(static_cast<int>(hi ? a1 : c1), 32));
+        return hi ? uint4{r0v, r1v, c0, c1} : uint4{a0, a1, r0v, r1v};
+      };
+      const uint4 v0 = vector(0), v1 = vector(8);
+      if (co < args.cout) {
+        const int64_t idx = ybase + static_cast<int64_t>(co) * args.howo + px0 + 8 * hi;
+        if (px0 + 8 * hi < npx) *reinterpret_cast<uint4*>(Y + idx) = epi_vec<EA, T>(args.ep, v0, idx);
+        if (px0 + 16 + 8 * hi < npx) *reinterpret_cast<uint4*>(Y + idx + 16) = epi_vec<EA, T>(args.ep, v1, idx + 16);
+      }
+    }
+  };
+  auto zero = [](f32x16_t (&acc)[TM]) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int x = 0; x < 16; ++x) acc[i][x] = 0.0f;
+  };
+  auto patch_pos = [&](int px0) {
+    const int bp = min(px0 + l32, npx - 1);
+    const int r = bp / W;
+    return r * rw + (bp - r * W);
+  };
+
+  // phase 0: pixels 32 wave .. + 31 (band pixels 0-255), both chunks; chunk 1's fill lands in between
+  uint4 v[8];
+  load_chunk(0, v);
+  wait_vmcnt<0>();  // chunk 0's input, the whole filter and the bias
+  store_chunk(v, lds + A_BYTES);
+  load_chunk(32, v);  // chunk 1 stays in flight during chunk 0's multiplications
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  {
+    const int px0 = wave * 32;
+    const bool active = px0 < npx;  // uniform
+    const int pb = patch_pos(px0);
+    f32x16_t acc[TM];
+    zero(acc);
+    if (active) chunk(acc, pb, ab, ab + A_BYTES);
+    wait_vmcnt<0>();
+    store_chunk(v, lds + A_BYTES + PB);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (active) {
+      chunk(acc, pb, ab + A_CHUNK, ab + A_BYTES + PB);
+      store_tile(acc, px0);
+    }
+  }
+  // phase 1: pixels 256 + 32 wave .. (the LDS operands are read-only from here; phase 0's stores drain meanwhile)
+  {
+    const int px0 = 256 + wave * 32;
+    if (px0 < npx) {
+      const int pb = patch_pos(px0);
+      f32x16_t acc[TM];
+      zero(acc);
+      chunk(acc, pb, ab, ab + A_BYTES);
+      chunk(acc, pb, ab + A_CHUNK, ab + A_BYTES + PB);
+      store_tile(acc, px0);
+    }
+  }
+}
+
+// Rows per band for the band kernel, or 0 when it does not take this geometry (NCHW input and output, Cin = 64,
+// Cout <= 64, W % 8 == 0, 16-byte aligned output and epilogue operands) or would not finish sooner than the 256-pixel tiles: the divisor R of H with the least
+// pixels per CU (rounds of one band per CU x R x W), R * W <= 512, both patches within kBandPatchBytes and one
+// fill thread per 8 x 8 block.
+int conv_band_rows(const ConvNhwcArgs& c, const int64_t* g, int64_t cus) {
+  if (c.out_nhwc || !c.vec_store || g[1] != 64 || g[4] > 64 || g[3] % 8 != 0) return 0;
+  const int64_t n = g[0], h = g[2], w = g[3];
+  int best = 0;
+  int64_t best_px = 0;
+  for (int64_t r = 1; r <= h && r * w <= 512; ++r) {
+    if (h % r != 0 || (r + 2) * (w + 2) * 64 > kBandPatchBytes || 4 * (r + 2) * (w / 8) > 512) continue;
+    const int64_t bands = n * h / r;
+    const int64_t px = (bands + cus - 1) / cus * r * w;
+    if (best == 0 || px <= best_px) {
+      best = static_cast<int>(r);
+      best_px = px;
+    }
+  }
+  // the single-buffered kernel at two 256-pixel tiles per CU slot pair
+  const int64_t tiles = (c.p + 255) / 256;
+  const int64_t halo_px = (tiles + 2 * cus - 1) / (2 * cus) * 2 * 256;
+  return best != 0 && best_px < halo_px ? best : 0;
+}
+
+// bf16 with the fixed programs (none, relu, add;relu) only: other programs and f16 take the single-buffered kernel
+// (the interpreted epilogue would need scratch memory here).
+bool band_program(int kind) { return kind == kEpiNone || kind == kEpiRelu || kind == kEpiAddRelu; }
+
+fh_status launch_band(ConvNhwcArgs c, int rows, hipStream_t stream) {
+  ConvBandArgs a{};
+  a.c = c;
+  a.rows = rows;
+  a.bands_per_img = c.h / rows;
+  const dim3 grid(static_cast<uint32_t>(c.p / (static_cast<int64_t>(rows) * c.w_in)));
+  switch (epi_kind(c.ep)) {
+    case kEpiNone: hipLaunchKernelGGL((conv_band_kernel<bf16_t, kEpiNone>), grid, dim3(512), 0, stream, a); break;
+    case kEpiRelu: hipLaunchKernelGGL((conv_band_kernel<bf16_t, kEpiRelu>), grid, dim3(512), 0, stream, a); break;
+    case kEpiAddRelu: hipLaunchKernelGGL((conv_band_kernel<bf16_t, kEpiAddRelu>), grid, dim3(512), 0, stream, a); break;
+    default: return fail(FH_INTERNAL, "conv_band_kernel: epilogue program without a band instance");
+  }
+  return launch_status("conv_band_kernel launch");
+}
+
 // Whether the resident-patch kernel takes this geometry: patch rows of a BN-pixel tile (at most (BN - 1) / W + 2
 // output rows plus the two halo rows) must fit kHaloPatchBytes; p_loads = the 1 KB loads that fill them.
 bool halo_supported(int32_t dtype, const int64_t* g, int bn, int32_t* p_loads, int32_t* patch_rows = nullptr) {
@@ -1171,6 +1445,8 @@ fh_status launch_halo(ConvHaloArgs a, hipStream_t stream) {
 
 // Which resident-patch kernel, from measurements of C3 and the ResNet-18 3x3 stride-1 layers on an MI355X (bf16,
 // relu epilogue, batch 64; us per launch, implicit GEMM in brackets):
+//   NCHW input and output, Cin 64, bf16:     the band kernel when its bands spread more evenly (C3 13.5; 16.2
+//                                            single-buffered)
 //   NCHW output (a graph output, C3):        single-buffered, two per CU    C3 16.3 (20.6)
 //   channels-last output, Cout <= 64:        persistent, resident filter    56x56x64 34.2 (41.9)
 //   channels-last output, 64 < Cout <= 256:  single-buffered                28x28x128 31.1 (32.8), 14x14x256 32.1 (36.2)
@@ -1183,6 +1459,13 @@ fh_status dispatch_halo(const ConvNhwcArgs& c, const int64_t* geom, hipStream_t 
   *launched = false;
   if (c.out_nhwc && c.cout > 256 && !nchw_in) return FH_OK;
   const int64_t cus = device_cu_count();
+  if (nchw_in && std::is_same_v<T, bf16_t> && band_program(epi_kind(c.ep))) {
+    const int band_rows = conv_band_rows(c, geom, cus);
+    if (band_rows > 0) {
+      *launched = true;
+      return launch_band(c, band_rows, stream);
+    }
+  }
   const int64_t tiles_m = (c.cout + 63) / 64;
   const bool persistent = c.out_nhwc && c.cout <= 64 && !nchw_in;
   ConvHaloArgs a{};

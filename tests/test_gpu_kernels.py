@@ -649,8 +649,14 @@ def test_conv2d_resident_patch(hip, dtype, geom, nhwc_out):
 
 
 NCHW_IN_CASES = [
-    (BF16, (32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1), 0),    # C3: 256-pixel tiles, 8 patch rows
-    (F16, (32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1), 0),
+    # NCHW output, Cin 64, Cout <= 64, bf16: the band kernel (whole output rows per workgroup, filter resident)
+    (BF16, (32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1), 0),    # C3: 7-row bands, 256 of them
+    (F16, (32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1), 0),     # f16: the single-buffered kernel
+    (BF16, (16, 64, 32, 56, 64, 3, 3, 1, 1, 1, 1, 1), 0),    # 2-row bands
+    (BF16, (256, 64, 16, 16, 64, 3, 3, 1, 1, 1, 1, 1), 0),   # whole-image bands: both halo rows zero, 4 waves idle
+    (BF16, (64, 64, 8, 64, 40, 3, 3, 1, 1, 1, 1, 1), 0),     # Cout 40, W 64
+    (BF16, (3, 64, 12, 40, 48, 3, 3, 1, 1, 1, 1, 1), 0),     # 1-row bands (fewer rows than CUs)
+    # the single-buffered kernel
     (BF16, (3, 96, 9, 16, 40, 3, 3, 1, 1, 1, 1, 1), 0),      # Cout 40, three chunks, 128-pixel tiles
     (BF16, (5, 32, 3, 8, 100, 3, 3, 1, 1, 1, 1, 1), 1),      # 3-row images, one 8-pixel group per row
     (BF16, (4, 64, 14, 24, 64, 3, 3, 1, 1, 1, 1, 1), 1),     # channels-last output from NCHW input
@@ -688,6 +694,33 @@ def test_conv2d_nchw_input(hip, dtype, geom, nhwc_out):
         conv = orc.conv2d(dtype, x[img:img + 1], wt, bias, (1,) + geom[1:])
         assert_close(outs[0][img:img + 1], orc.ew_program(dtype, [3], [1], [conv]), dtype,
                      what=f"NCHW input {geom} image {img}")
+
+
+@pytest.mark.parametrize("geom", [(32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1), (64, 64, 8, 64, 40, 3, 3, 1, 1, 1, 1, 1),
+                                  (3, 64, 12, 40, 48, 3, 3, 1, 1, 1, 1, 1)])
+def test_conv2d_band_residual(hip, geom):
+    """The band kernel (NCHW input and output) with the residual add;relu program and no bias: both images at the
+    ends of the batch and 4,096 sampled outputs against the oracle."""
+    say(f"conv band kernel add;relu {geom}")
+    n, cin, h, w, cout, kh, kw = geom[:7]
+    x = synth.tensor(191, (n, cin, h, w), BF16, "normal")
+    wt = synth.tensor(192, (cout, cin, kh, kw), BF16, "normal", (2.0 / (cin * kh * kw)) ** 0.5)
+    res = synth.tensor(193, (n, cout, h, w), BF16, "normal")
+    dx, dw, dr = dev(hip, x), dev(hip, to_nhwc(wt)), dev(hip, res)
+    dy = hip.DeviceBuffer(n * cout * h * w * 2)
+    ep = hip.make_epilogue([(hip.EW_ADD, dr.value), (hip.EW_RELU, None)])
+    hip.check(hip.lib().fh_conv2d_nhwc_fwd_ex(BF16, dx.value, dw.value, None, dy.value, hip.i64_array(geom),
+                                              ctypes.byref(ep), 4, None))
+    got = dy.download((n, cout, h, w), x.dtype)
+    for img in sorted({0, n - 1}):
+        conv = orc.conv2d(BF16, x[img:img + 1], wt, None, (1,) + geom[1:])
+        want = orc.ew_program(BF16, [1, 3], [2, 1], [conv, res[img:img + 1]])
+        assert_close(got[img:img + 1], want, BF16, what=f"band add;relu {geom} image {img}")
+    flat = got.reshape(-1)
+    idx = np.random.default_rng(11).integers(0, flat.size, 4096)
+    conv = orc.conv2d_sample(BF16, x, wt, None, geom, idx)
+    want = orc.ew_program(BF16, [1, 3], [2, 1], [conv, res.reshape(-1)[idx]])
+    assert_close(flat[idx], want, BF16, what=f"band add;relu {geom} sampled")
 
 
 def test_conv2d_nchw_input_rejections(hip):
