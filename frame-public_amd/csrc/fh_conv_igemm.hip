@@ -1139,7 +1139,7 @@ struct ConvBandArgs {
   int32_t bands_per_img;  // H / R
 };
 
-template <typename T, int E>
+template <typename T, int E, bool W_OIHW>
 __global__ __launch_bounds__(512) void conv_band_kernel(ConvBandArgs ba) {
   const ConvNhwcArgs& args = ba.c;
   using S = typename Io<T>::storage;
@@ -1165,19 +1165,46 @@ __global__ __launch_bounds__(512) void conv_band_kernel(ConvBandArgs ba) {
   if ((gridDim.x & 7) == 0) b = (b & 7) * static_cast<int>(gridDim.x >> 3) + (b >> 3);
   const int img = b / ba.bands_per_img;
   const int r0 = (b - img * ba.bands_per_img) * R;
-  const int64_t n0 = (static_cast<int64_t>(img) * H + r0) * W;  // first output pixel (flattened n, oh, ow)
 
-  // the filter: 1 KB load j covers chunk j / 36, tap (j / 4) % 9, rows 16 * (j % 4) .. + 15
+  // the filter, [chunk][tap][64 rows][32 channels] in LDS (16-byte chunks of a row swizzled)
   const S* __restrict__ Wt = static_cast<const S*>(args.w);
+  uint4 wv[TAPS];  // W_OIHW: this thread's 8 input channels x 9 taps of one output channel
+  if constexpr (!W_OIHW) {
+    // [Cout][3][3][64]: 1 KB load j covers chunk j / 36, tap (j / 4) % 9, rows 16 * (j % 4) .. + 15
 #pragma unroll
-  for (int i = 0; i < A_PER_WAVE; ++i) {
-    const int j = wave + NW * i;
-    const int ch = j / (TAPS * 4), tap = (j / 4) % TAPS;
-    const int row = (j % 4) * 16 + (lane >> 2);
-    const int gch = (lane & 3) ^ a_swizzle(row);
-    global_to_lds16(Wt + (min(row, args.cout - 1) * TAPS + tap) * 64 + ch * 32 + gch * 8,
-                    (FH_LDS void*)(lds + j * 1024));
+    for (int i = 0; i < A_PER_WAVE; ++i) {
+      const int j = wave + NW * i;
+      const int ch = j / (TAPS * 4), tap = (j / 4) % TAPS;
+      const int row = (j % 4) * 16 + (lane >> 2);
+      const int gch = (lane & 3) ^ a_swizzle(row);
+      global_to_lds16(Wt + (min(row, args.cout - 1) * TAPS + tap) * 64 + ch * 32 + gch * 8,
+                      (FH_LDS void*)(lds + j * 1024));
+    }
+  } else {
+    // [Cout][64][3][3] (the graph's own layout): thread = (output channel tid / 8, input channels 8 (tid % 8) ..
+    // + 7), whose 72 filter values are 144 contiguous bytes; transposed in registers after they land
+    const int co = min(tid >> 3, args.cout - 1);
+    const uint4* src = reinterpret_cast<const uint4*>(Wt + (co * 64 + (tid & 7) * 8) * TAPS);
+#pragma unroll
+    for (int q = 0; q < TAPS; ++q) wv[q] = src[q];
   }
+  // W_OIHW: writes the thread's 9 taps x 8 channels as 9 16-byte chunks (channel pairs packed per dword)
+  auto store_filter = [&]() {
+    if constexpr (W_OIHW) {
+      const int row = tid >> 3, cg = tid & 7;
+      uint16_t e[8 * TAPS];  // e[ci * 9 + tap]
+      __builtin_memcpy(e, wv, sizeof(e));
+      unsigned char* dst = lds + (cg >> 2) * A_CHUNK + row * 64 + (((cg & 3) ^ a_swizzle(row)) * 16);
+#pragma unroll
+      for (int tap = 0; tap < TAPS; ++tap) {
+        uint32_t d[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+          d[k] = static_cast<uint32_t>(e[(2 * k) * TAPS + tap]) | (static_cast<uint32_t>(e[(2 * k + 1) * TAPS + tap]) << 16);
+        *reinterpret_cast<uint4*>(dst + tap * BM * 64) = uint4{d[0], d[1], d[2], d[3]};
+      }
+    }
+  };
   // the padding columns (positions 0 and W + 1 of every patch row) of both patches
   if (tid < 2 * (R + 2) * 8) {
     const int buf = tid / ((R + 2) * 8), z = tid % ((R + 2) * 8);
@@ -1311,6 +1338,7 @@ __global__ __launch_bounds__(512) void conv_band_kernel(ConvBandArgs ba) {
   uint4 v[8];
   load_chunk(0, v);
   wait_vmcnt<0>();  // chunk 0's input, the whole filter and the bias
+  store_filter();
   store_chunk(v, lds + A_BYTES);
   load_chunk(32, v);  // chunk 1 stays in flight during chunk 0's multiplications
   __builtin_amdgcn_sched_barrier(0);
@@ -1376,6 +1404,15 @@ int conv_band_rows(const ConvNhwcArgs& c, const int64_t* g, int64_t cus) {
 // (the interpreted epilogue would need scratch memory here).
 bool band_program(int kind) { return kind == kEpiNone || kind == kEpiRelu || kind == kEpiAddRelu; }
 
+bool halo_nchw_supported(int32_t dtype, const int64_t* g);
+
+// Rows per band when the band kernel takes (dtype, geometry, program) with NCHW input and output, else 0.
+int band_rows_for(int32_t dtype, const ConvNhwcArgs& c, const int64_t* g) {
+  if (dtype != FH_BF16 || !band_program(epi_kind(c.ep)) || !halo_nchw_supported(dtype, g)) return 0;
+  return conv_band_rows(c, g, device_cu_count());
+}
+
+template <bool W_OIHW>
 fh_status launch_band(ConvNhwcArgs c, int rows, hipStream_t stream) {
   ConvBandArgs a{};
   a.c = c;
@@ -1383,9 +1420,15 @@ fh_status launch_band(ConvNhwcArgs c, int rows, hipStream_t stream) {
   a.bands_per_img = c.h / rows;
   const dim3 grid(static_cast<uint32_t>(c.p / (static_cast<int64_t>(rows) * c.w_in)));
   switch (epi_kind(c.ep)) {
-    case kEpiNone: hipLaunchKernelGGL((conv_band_kernel<bf16_t, kEpiNone>), grid, dim3(512), 0, stream, a); break;
-    case kEpiRelu: hipLaunchKernelGGL((conv_band_kernel<bf16_t, kEpiRelu>), grid, dim3(512), 0, stream, a); break;
-    case kEpiAddRelu: hipLaunchKernelGGL((conv_band_kernel<bf16_t, kEpiAddRelu>), grid, dim3(512), 0, stream, a); break;
+    case kEpiNone:
+      hipLaunchKernelGGL((conv_band_kernel<bf16_t, kEpiNone, W_OIHW>), grid, dim3(512), 0, stream, a);
+      break;
+    case kEpiRelu:
+      hipLaunchKernelGGL((conv_band_kernel<bf16_t, kEpiRelu, W_OIHW>), grid, dim3(512), 0, stream, a);
+      break;
+    case kEpiAddRelu:
+      hipLaunchKernelGGL((conv_band_kernel<bf16_t, kEpiAddRelu, W_OIHW>), grid, dim3(512), 0, stream, a);
+      break;
     default: return fail(FH_INTERNAL, "conv_band_kernel: epilogue program without a band instance");
   }
   return launch_status("conv_band_kernel launch");
@@ -1459,11 +1502,11 @@ fh_status dispatch_halo(const ConvNhwcArgs& c, const int64_t* geom, hipStream_t 
   *launched = false;
   if (c.out_nhwc && c.cout > 256 && !nchw_in) return FH_OK;
   const int64_t cus = device_cu_count();
-  if (nchw_in && std::is_same_v<T, bf16_t> && band_program(epi_kind(c.ep))) {
-    const int band_rows = conv_band_rows(c, geom, cus);
+  if (nchw_in && std::is_same_v<T, bf16_t>) {
+    const int band_rows = band_rows_for(FH_BF16, c, geom);
     if (band_rows > 0) {
       *launched = true;
-      return launch_band(c, band_rows, stream);
+      return launch_band<false>(c, band_rows, stream);
     }
   }
   const int64_t tiles_m = (c.cout + 63) / 64;
@@ -1795,6 +1838,23 @@ extern "C" fh_status fh_conv2d_nhwc_fwd_ex(int32_t dtype, const void* x_nhwc, co
                                            void* y, const int64_t geom[12], const fh_epilogue* epilogue,
                                            int32_t flags, void* stream);
 
+extern "C" int32_t fh_conv2d_w_oihw_supported(int32_t dtype, const int64_t geom[12], const fh_epilogue* epilogue) {
+  if (geom == nullptr || !nhwc_supported(dtype, geom) || !halo_nchw_supported(dtype, geom)) return 0;
+  if (epilogue != nullptr && (epilogue->nseg < 0 || epilogue->nseg > FH_MAX_SEGMENTS)) return 0;
+  ConvNhwcArgs a{};
+  a.cout = static_cast<int32_t>(geom[4]);
+  a.p = geom[0] * geom[2] * geom[3];  // 3x3, stride 1, padding 1: the output plane is the input plane
+  a.vec_store = 1;
+  if (epilogue != nullptr) {
+    a.ep.nseg = epilogue->nseg;
+    for (int s = 0; s < a.ep.nseg; ++s) {
+      if (!epilogue_op_ok(epilogue->ops[s])) return 0;
+      a.ep.ops[s] = epilogue->ops[s];
+    }
+  }
+  return band_rows_for(dtype, a, geom) > 0 ? 1 : 0;
+}
+
 extern "C" fh_status fh_conv2d_nhwc_fwd(int32_t dtype, const void* x_nhwc, const void* w_khwc, const void* bias, void* y,
                                         const int64_t geom[12], const fh_epilogue* epilogue, void* stream) {
   return fh_conv2d_nhwc_fwd_ex(dtype, x_nhwc, w_khwc, bias, y, geom, epilogue, 0, stream);
@@ -1803,8 +1863,11 @@ extern "C" fh_status fh_conv2d_nhwc_fwd(int32_t dtype, const void* x_nhwc, const
 extern "C" fh_status fh_conv2d_nhwc_fwd_ex(int32_t dtype, const void* x_nhwc, const void* w_khwc, const void* bias,
                                            void* y, const int64_t geom[12], const fh_epilogue* epilogue,
                                            int32_t flags, void* stream) {
-  if ((flags & ~(FH_CONV_OUT_NHWC | FH_CONV_IMPLICIT_GEMM | FH_CONV_IN_NCHW)) != 0)
+  if ((flags & ~(FH_CONV_OUT_NHWC | FH_CONV_IMPLICIT_GEMM | FH_CONV_IN_NCHW | FH_CONV_W_OIHW)) != 0)
     return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd_ex: unknown flags");
+  const bool w_oihw = (flags & FH_CONV_W_OIHW) != 0;
+  if (w_oihw && (flags & (FH_CONV_IN_NCHW | FH_CONV_OUT_NHWC | FH_CONV_IMPLICIT_GEMM)) != FH_CONV_IN_NCHW)
+    return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd_ex: FH_CONV_W_OIHW goes with FH_CONV_IN_NCHW and NCHW output only");
   if (geom == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd: null geometry");
   const bool nchw_in = (flags & FH_CONV_IN_NCHW) != 0;
   if (nchw_in && ((flags & FH_CONV_IMPLICIT_GEMM) != 0 || !halo_nchw_supported(dtype, geom)))
@@ -1862,8 +1925,17 @@ extern "C" fh_status fh_conv2d_nhwc_fwd_ex(int32_t dtype, const void* x_nhwc, co
   for (int s = 0; s < a.ep.nseg; ++s)
     if (ew_is_binary(a.ep.ops[s]) && !aligned16(a.ep.ins[s])) vec = false;
   a.vec_store = vec ? 1 : 0;
-  if (a.p == 0) return FH_OK;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (w_oihw) {
+    const int rows = band_rows_for(dtype, a, geom);
+    if (rows == 0)
+      return fail(FH_UNIMPLEMENTED, "fh_conv2d_nhwc_fwd_ex: FH_CONV_W_OIHW needs the band kernel (bf16, 3x3 stride 1 "
+                                    "padding 1, Cin 64, Cout <= 64, W % 8 == 0, 16-byte aligned output and operands, "
+                                    "no epilogue, relu or add;relu); see fh_conv2d_w_oihw_supported");
+    if (a.p == 0) return FH_OK;
+    return launch_band<true>(a, rows, s);
+  }
+  if (a.p == 0) return FH_OK;
   if ((dtype == FH_BF16 || dtype == FH_F16) && !c8 && (flags & FH_CONV_IMPLICIT_GEMM) == 0) {
     bool launched = false;
     const fh_status st = dtype == FH_BF16 ? dispatch_halo<bf16_t>(a, geom, s, &launched, nchw_in)

@@ -65,6 +65,7 @@ _SIGS = {
     "fh_gemm": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, POINTER(Epilogue),
                           c_void_p]),
     "fh_conv2d_nchw_in_supported": (c_int32, [c_int32, POINTER(c_int64)]),
+    "fh_conv2d_w_oihw_supported": (c_int32, [c_int32, POINTER(c_int64), POINTER(Epilogue)]),
     "fh_gemm_ex": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, POINTER(Epilogue),
                              c_int32, c_void_p]),
     "fh_gemm_grouped": (c_int32, [c_int32, c_void_p, c_int32, POINTER(c_void_p), POINTER(c_void_p), c_int64, c_int64,

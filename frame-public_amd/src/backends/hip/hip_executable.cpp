@@ -414,13 +414,30 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
     return n.value()->output(0);
   };
 
-  // graph-input filters of the non-C8 lowered convs, in first-use order, each once
+  // Whether a lowered conv reads its NCHW activation (FH_CONV_IN_NCHW) and, writing NCHW, takes its filter in the
+  // graph's own [Cout][Cin][KH][KW] layout too (FH_CONV_W_OIHW, the band kernel): then neither operand is copied.
+  auto reads_nchw = [&](const ir::Node* n, const ConvLowering& p) {
+    return p.ok && !p.c8 && !nhwc.count(n->inputs()[0]) &&
+           fh_conv2d_nchw_in_supported(conv_dtype_code(n->inputs()[0]->type()), p.geom) != 0;
+  };
+  auto takes_oihw = [&](const ir::Node* n, const ConvLowering& p) {
+    if (!reads_nchw(n, p) || nhwc.count(&n->outputs()[0])) return false;
+    fh_epilogue qe{};
+    if (const auto* prog = attr_of<std::vector<int64_t>>(n, "ep_ops")) {
+      if (prog->size() > FH_MAX_SEGMENTS) return false;
+      qe.nseg = static_cast<int32_t>(prog->size());
+      for (size_t s = 0; s < prog->size(); ++s) qe.ops[s] = static_cast<uint8_t>((*prog)[s]);
+    }
+    return fh_conv2d_w_oihw_supported(conv_dtype_code(n->inputs()[0]->type()), p.geom, &qe) != 0;
+  };
+
+  // graph-input filters of the non-C8 lowered convs that need a channels-last copy, in first-use order, each once
   std::vector<const ir::Value*> batched;
   {
     std::unordered_set<const ir::Value*> seen;
     for (const ir::Node* n : src.topological_order()) {
       const ConvLowering p = plan_conv(n);
-      const ir::Value* w = p.ok && !p.c8 ? n->inputs()[1] : nullptr;
+      const ir::Value* w = p.ok && !p.c8 && !takes_oihw(n, p) ? n->inputs()[1] : nullptr;
       if (w == nullptr || w->producer() == nullptr || w->producer()->op() != ir::kGraphInputOp || seen.count(w)) continue;
       if (w->type().shape.dim(1) * w->type().shape.dim(2) * w->type().shape.dim(3) > kMultiPlaneMax) continue;
       seen.insert(w);
@@ -529,7 +546,7 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
       const int64_t* geom = p.geom;
       ir::Value* x_cl = nullptr;
       ir::Value* w_cl = nullptr;
-      bool in_nchw = false;
+      bool in_nchw = false, w_oihw = false;
       if (p.c8) {
         ir::TensorType tx = ins[0]->type(), tw = ins[1]->type();
         tx.shape = Shape({geom[0], geom[2], geom[3], 8});
@@ -544,15 +561,18 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
         if (!batched_emitted) FRAME_RETURN_IF_ERROR(emit_batched());
         if (nhwc.count(n->inputs()[0])) {
           x_cl = ins[0];  // already channels-last
-        } else if (fh_conv2d_nchw_in_supported(conv_dtype_code(ins[0]->type()), geom) != 0) {
+        } else if (reads_nchw(n, p)) {
           x_cl = ins[0];  // NCHW, read by the resident-patch kernel itself (FH_CONV_IN_NCHW)
           in_nchw = true;
+          w_oihw = takes_oihw(n, p);
         } else {
           Result<ir::Value*> xv = channels_last(ins[0]);
           if (!xv.is_ok()) return xv.status();
           x_cl = xv.value();
         }
-        if (auto it = batched_out.find(n->inputs()[1]); it != batched_out.end()) {
+        if (w_oihw) {
+          w_cl = ins[1];  // [Cout][Cin][KH][KW], transposed by the band kernel on its way into LDS
+        } else if (auto it = batched_out.find(n->inputs()[1]); it != batched_out.end()) {
           w_cl = it->second;
         } else {
           Result<ir::Value*> wv = channels_last(ins[1]);
@@ -568,6 +588,7 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
       for (const auto& [k, v] : n->attrs()) c.value()->set_attr(k, v);
       if (nhwc.count(&n->outputs()[0])) c.value()->set_attr("out_nhwc", ir::AttrValue{int64_t{1}});
       if (in_nchw) c.value()->set_attr("in_nchw", ir::AttrValue{int64_t{1}});
+      if (w_oihw) c.value()->set_attr("w_oihw", ir::AttrValue{int64_t{1}});
       if (n->op() == "conv2d") c.value()->set_attr("n_main_inputs", ir::AttrValue{static_cast<int64_t>(ins.size())});
       c.value()->set_attr("filter_hw", ir::AttrValue{std::vector<int64_t>{geom[5], geom[6]}});
       map[&n->outputs()[0]] = c.value()->output(0);

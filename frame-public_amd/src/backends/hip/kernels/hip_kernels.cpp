@@ -305,7 +305,8 @@ Status conv_impl(KernelContext& ctx, const std::string& op, size_t n_main) {
   return Status::ok();
 }
 
-// x_nhwc [N,H,W,Cin], w_khwc [Cout,KH,KW,Cin], optional bias [Cout], then the epilogue operands; y NCHW.
+// x_nhwc [N,H,W,Cin] (or NCHW, in_nchw), w_khwc [Cout,KH,KW,Cin] (or [Cout,Cin,KH,KW], w_oihw), optional bias
+// [Cout], then the epilogue operands; y NCHW (or channels-last, out_nhwc).
 Status conv_nhwc_kernel(KernelContext& ctx) {
   const std::string op(kConvNhwcOp);
   const auto* n_main_attr = attr<int64_t>(ctx, "n_main_inputs");
@@ -331,15 +332,19 @@ Status conv_nhwc_kernel(KernelContext& ctx) {
   const bool c8 = w.shape().rank() == 2;
   if (c8 && (fhw == nullptr || fhw->size() != 2 || x.shape().dim(3) != 8))
     return invalid(op, "C8 filter needs filter_hw and an input with 8 channels");
-  const int64_t kh = c8 ? (*fhw)[0] : w.shape().dim(1), kw = c8 ? (*fhw)[1] : w.shape().dim(2);
-  // in_nchw: x is NCHW [N,Cin,H,W] (FH_CONV_IN_NCHW), else channels-last [N,H,W,Cin]
+  // in_nchw: x is NCHW [N,Cin,H,W] (FH_CONV_IN_NCHW), else channels-last [N,H,W,Cin]; w_oihw: the filter is
+  // [Cout,Cin,KH,KW] (FH_CONV_W_OIHW, with in_nchw only)
   const auto* in_nchw_attr = attr<int64_t>(ctx, "in_nchw");
   const bool in_nchw = in_nchw_attr != nullptr && *in_nchw_attr != 0;
+  const auto* w_oihw_attr = attr<int64_t>(ctx, "w_oihw");
+  const bool w_oihw = w_oihw_attr != nullptr && *w_oihw_attr != 0;
   if (in_nchw && c8) return invalid(op, "NCHW input with the C8 filter");
+  if (w_oihw && !in_nchw) return invalid(op, "the [Cout,Cin,KH,KW] filter goes with NCHW input only");
+  const int64_t kh = c8 ? (*fhw)[0] : w.shape().dim(w_oihw ? 2 : 1), kw = c8 ? (*fhw)[1] : w.shape().dim(w_oihw ? 3 : 2);
   const int64_t geom[12] = {x.shape().dim(0), x.shape().dim(in_nchw ? 1 : 3), x.shape().dim(in_nchw ? 2 : 1),
                             x.shape().dim(in_nchw ? 3 : 2), w.shape().dim(0), kh, kw, (*stride)[0],
                             (*stride)[1], (*pad)[0], (*pad)[1], *groups};
-  if (c8 ? w.shape().dim(1) != fh_conv_c8_filter_k(kh, kw) : w.shape().dim(3) != geom[1])
+  if (c8 ? w.shape().dim(1) != fh_conv_c8_filter_k(kh, kw) : w.shape().dim(w_oihw ? 1 : 3) != geom[1])
     return invalid(op, "filter shape does not match the input's channels");
   // 16-bit with 8 input channels is the C8 kernel, which reads the packed [Cout, K8] filter only
   if (!c8 && geom[1] == 8 && dt.value() != FH_F32) return invalid(op, "an 8-channel 16-bit input needs the packed C8 filter");
@@ -355,7 +360,8 @@ Status conv_nhwc_kernel(KernelContext& ctx) {
   if (!ep.is_ok()) return ep.status();
   FRAME_HIP_RETURN_IF_ERROR(fh_conv2d_nhwc_fwd_ex(dt.value(), x.raw_data(), w.raw_data(), bias ? bias->raw_data() : nullptr,
                                                   y.raw_data(), geom, ep.value().nseg > 0 ? &ep.value() : nullptr,
-                                                  (out_nhwc ? FH_CONV_OUT_NHWC : 0) | (in_nchw ? FH_CONV_IN_NCHW : 0),
+                                                  (out_nhwc ? FH_CONV_OUT_NHWC : 0) | (in_nchw ? FH_CONV_IN_NCHW : 0) |
+                                                      (w_oihw ? FH_CONV_W_OIHW : 0),
                                                   stream_handle(ctx)),
                             "op '" + op + "' (hip)");
   return Status::ok();

@@ -183,6 +183,11 @@ fh_status fh_conv2d_nhwc_fwd(int32_t dtype, const void* x_nhwc, const void* w_kh
  * resident-patch kernel transposes it on the way into LDS, so a graph-input activation needs no channels-last
  * copy. Only where fh_conv2d_nchw_in_supported says so. */
 #define FH_CONV_IN_NCHW 4
+/* FH_CONV_W_OIHW (with FH_CONV_IN_NCHW and NCHW output): the filter is [Cout][Cin][KH][KW], the layout Frame's
+ * conv2d takes it in (reference: src/backends/cpu/kernels/conv.cpp:223-314, filter index ((co*Cin + ci)*KH + kh)*KW
+ * + kw), so a graph-input filter needs no transposed copy either: the band kernel transposes it on its way into
+ * LDS. Only where fh_conv2d_w_oihw_supported says so. */
+#define FH_CONV_W_OIHW 8
 fh_status fh_conv2d_nhwc_fwd_ex(int32_t dtype, const void* x_nhwc, const void* w_khwc, const void* bias, void* y,
                                 const int64_t geom[12], const fh_epilogue* epilogue, int32_t flags, void* stream);
 
@@ -195,6 +200,13 @@ int32_t fh_conv2d_nhwc_supported(int32_t dtype, const int64_t geom[12]);
 /* 1 if fh_conv2d_nhwc_fwd_ex takes dtype and geom with FH_CONV_IN_NCHW (bf16/f16, 3x3, stride 1, padding 1,
  * groups 1, Cin % 32 == 0, W % 8 == 0, a resident patch of at most 30 KB), else 0. Host-only query. */
 int32_t fh_conv2d_nchw_in_supported(int32_t dtype, const int64_t geom[12]);
+
+/* 1 if fh_conv2d_nhwc_fwd_ex takes dtype, geom and the epilogue program (nseg and ops of `epilogue`; NULL for
+ * none) with FH_CONV_IN_NCHW | FH_CONV_W_OIHW, given a 16-byte aligned output and epilogue operands: bf16, 3x3,
+ * stride 1, padding 1, Cin 64, Cout <= 64, W % 8 == 0, no epilogue, relu or add;relu, and a geometry whose bands of
+ * whole output rows spread over the CUs more evenly than 256-pixel tiles; else 0. Host-only query; no
+ * counterpart in the reference. */
+int32_t fh_conv2d_w_oihw_supported(int32_t dtype, const int64_t geom[12], const fh_epilogue* epilogue);
 
 /* C8 layout for convolutions with Cin <= 8 (e.g. an RGB stem): x NCHW [N][C][H*W] (16-bit) ->
  * [N][H*W][8] with channels C..7 zero. No counterpart in the reference (cuDNN consumes NCHW). */

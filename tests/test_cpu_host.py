@@ -389,11 +389,23 @@ def test_gemm_grouped_and_ex_argument_checks():
 def test_nchw_graph_input_conv_reads_nchw_directly():
     # C3: the 3x3 stride-1 conv of a graph-input activation reads it NCHW (no channels-last copy of x, only of the
     # filter); a width the 8-pixel groups do not divide keeps the copy
+    # and its filter in the graph's [Cout,Cin,KH,KW] layout too (the band kernel: no channels-last copy at all)
     out = host.hip_lowered(graphs.conv(3).text(), 1)
-    assert out.count("hip_channels_last_internal(") == 1 and "in_nchw=1" in out, out
+    assert out.count("hip_channels_last_internal(") == 0 and "in_nchw=1" in out and "w_oihw=1" in out, out
     out = host.hip_lowered(graphs.conv(3, w=57).text(), 1)
-    assert out.count("hip_channels_last_internal(") == 2 and "in_nchw" not in out, out
+    assert out.count("hip_channels_last_internal(") == 2 and "in_nchw" not in out and "w_oihw" not in out, out
     lib = abi.lib()
     assert lib.fh_conv2d_nchw_in_supported(3, abi.i64_array([32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1])) == 1
     assert lib.fh_conv2d_nchw_in_supported(3, abi.i64_array([32, 64, 56, 57, 64, 3, 3, 1, 1, 1, 1, 1])) == 0
     assert lib.fh_conv2d_nchw_in_supported(0, abi.i64_array([32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1])) == 0
+    c3 = abi.i64_array([32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1])
+    relu = abi.make_epilogue([(abi.EW_RELU, None)])
+    gelu = abi.make_epilogue([(abi.EW_GELU, None)])
+    assert lib.fh_conv2d_w_oihw_supported(3, c3, None) == 1
+    assert lib.fh_conv2d_w_oihw_supported(3, c3, ctypes.byref(relu)) == 1
+    assert lib.fh_conv2d_w_oihw_supported(3, c3, ctypes.byref(gelu)) == 0     # a program without a band instance
+    assert lib.fh_conv2d_w_oihw_supported(2, c3, None) == 0                   # f16
+    for g in ([32, 96, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1],                        # Cin 96
+              [32, 64, 56, 56, 128, 3, 3, 1, 1, 1, 1, 1],                       # Cout 128
+              [32, 64, 56, 57, 64, 3, 3, 1, 1, 1, 1, 1]):                       # W % 8 != 0
+        assert lib.fh_conv2d_w_oihw_supported(3, abi.i64_array(g), None) == 0, g

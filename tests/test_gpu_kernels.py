@@ -723,6 +723,65 @@ def test_conv2d_band_residual(hip, geom):
     assert_close(flat[idx], want, BF16, what=f"band add;relu {geom} sampled")
 
 
+BAND_GEOMS = [(32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1), (16, 64, 32, 56, 64, 3, 3, 1, 1, 1, 1, 1),
+              (256, 64, 16, 16, 64, 3, 3, 1, 1, 1, 1, 1), (64, 64, 8, 64, 40, 3, 3, 1, 1, 1, 1, 1),
+              (3, 64, 12, 40, 48, 3, 3, 1, 1, 1, 1, 1)]
+
+
+@pytest.mark.parametrize("geom", BAND_GEOMS)
+@pytest.mark.parametrize("program", ["none", "relu", "add;relu"])
+def test_conv2d_band_filter_oihw(hip, geom, program):
+    """FH_CONV_W_OIHW: the band kernel takes the filter in the graph's own [Cout,Cin,KH,KW] layout and transposes it
+    in registers on its way into LDS. The LDS image and the k order are those of the channels-last filter, so the
+    two agree bit for bit; the first image against the oracle as well."""
+    say(f"conv band kernel OIHW filter {geom} {program}")
+    n, cin, h, w, cout, kh, kw = geom[:7]
+    lib = hip.lib()
+    x = synth.tensor(201, (n, cin, h, w), BF16, "normal")
+    wt = synth.tensor(202, (cout, cin, kh, kw), BF16, "normal", (2.0 / (cin * kh * kw)) ** 0.5)
+    bias = None if program == "add;relu" else synth.tensor(203, (cout,), BF16, "normal", 0.1)
+    res = synth.tensor(204, (n, cout, h, w), BF16, "normal")
+    dx, dwo, dwc, dr = dev(hip, x), dev(hip, wt), dev(hip, to_nhwc(wt)), dev(hip, res)
+    db = dev(hip, bias) if bias is not None else None
+    segs = {"none": [], "relu": [(hip.EW_RELU, None)], "add;relu": [(hip.EW_ADD, dr.value), (hip.EW_RELU, None)]}
+    ep = hip.make_epilogue(segs[program]) if segs[program] else None
+    g = hip.i64_array(geom)
+    assert lib.fh_conv2d_w_oihw_supported(BF16, g, ctypes.byref(ep) if ep else None) == 1
+    outs = []
+    for wbuf, flags in ((dwo, 4 | 8), (dwc, 4)):
+        dy = hip.DeviceBuffer(n * cout * h * w * 2)
+        hip.check(lib.fh_conv2d_nhwc_fwd_ex(BF16, dx.value, wbuf.value, db.value if db else None, dy.value, g,
+                                            ctypes.byref(ep) if ep else None, flags, None))
+        outs.append(dy.download((n, cout, h, w), x.dtype))
+    assert_bitwise(outs[0], outs[1], f"OIHW vs channels-last filter {geom} {program}")
+    conv = orc.conv2d(BF16, x[:1], wt, bias, (1,) + geom[1:])
+    if program == "relu":
+        conv = orc.ew_program(BF16, [3], [1], [conv])
+    elif program == "add;relu":
+        conv = orc.ew_program(BF16, [1, 3], [2, 1], [conv, res[:1]])
+    assert_close(outs[0][:1], conv, BF16, what=f"band OIHW filter {geom} {program} image 0")
+
+
+def test_conv2d_band_filter_oihw_rejections(hip):
+    lib = hip.lib()
+    c3 = (32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1)
+    n, cin, h, w, cout = c3[:5]
+    dx, dw, dy = hip.DeviceBuffer(n * cin * h * w * 2), hip.DeviceBuffer(cout * cin * 9 * 2), \
+        hip.DeviceBuffer(n * cout * h * w * 2)
+    gelu = hip.make_epilogue([(hip.EW_GELU, None)])
+    # FH_CONV_W_OIHW without FH_CONV_IN_NCHW, or with channels-last output: invalid argument
+    for flags in (8, 8 | 4 | 1):
+        assert lib.fh_conv2d_nhwc_fwd_ex(BF16, dx.value, dw.value, None, dy.value, hip.i64_array(c3), None, flags,
+                                         None) == 1
+    # a program without a band instance, f16, Cin 96: unimplemented, nothing launched
+    assert lib.fh_conv2d_nhwc_fwd_ex(BF16, dx.value, dw.value, None, dy.value, hip.i64_array(c3), ctypes.byref(gelu),
+                                     12, None) == 4
+    assert lib.fh_conv2d_nhwc_fwd_ex(F16, dx.value, dw.value, None, dy.value, hip.i64_array(c3), None, 12, None) == 4
+    g96 = (8, 96, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1)
+    assert lib.fh_conv2d_nhwc_fwd_ex(BF16, dx.value, dw.value, None, dy.value, hip.i64_array(g96), None, 12,
+                                     None) == 4
+
+
 def test_conv2d_nchw_input_rejections(hip):
     lib = hip.lib()
     for geom in [(1, 64, 8, 12, 64, 3, 3, 1, 1, 1, 1, 1),     # W % 8 != 0
