@@ -74,6 +74,25 @@ __device__ __forceinline__ void fence_kfragments(KFragments<TM, TN>& f) {
 #pragma unroll
   for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(f.b[j]));
 }
+// Word j (a constant after unrolling) of a 16-byte vector.
+__device__ __forceinline__ uint32_t uint4_word(const uint4& v, int j) {
+  return j == 0 ? v.x : j == 1 ? v.y : j == 2 ? v.z : v.w;
+}
+// Ties the fragment registers to the preceding wait (no consumer is scheduled above it), as fence_kfragments does
+// after its full wait.
+template <int TM, int TN>
+__device__ __forceinline__ void tie_kfragments(KFragments<TM, TN>& f) {
+#pragma unroll
+  for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(f.a[i]));
+#pragma unroll
+  for (int j = 0; j < TN; ++j) asm volatile("" : "+v"(f.b[j]));
+}
+// s_waitcnt with only lgkmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[15:14]).
+template <int N>
+__device__ __forceinline__ void wait_lgkmcnt() {
+  static_assert(N >= 0 && N < 16, "lgkmcnt range");
+  __builtin_amdgcn_s_waitcnt(0xc07f | (N << 8));
+}
 
 // Writes one wave's accumulator tile (output channels m0w.. m0w+WM-1, output pixels n0w.. n0w+WN-1): bias added to
 // the fp32 sum, one rounding, the fused chain on the rounded value, stored NCHW or channels-last (args.out_nhwc),
@@ -1180,18 +1199,23 @@ __global__ __launch_bounds__(512) void conv_band_kernel(ConvBandArgs ba) {
       global_to_lds16(Wt + (min(row, args.cout - 1) * TAPS + tap) * 64 + ch * 32 + gch * 8,
                       (FH_LDS void*)(lds + j * 1024));
     }
-  } else {
-    // [Cout][64][3][3] (the graph's own layout): thread = (output channel tid / 8, input channels 8 (tid % 8) ..
-    // + 7), whose 72 filter values are 144 contiguous bytes; transposed in registers after they land
-    const int co = min(tid >> 3, args.cout - 1);
-    const uint4* src = reinterpret_cast<const uint4*>(Wt + (co * 64 + (tid & 7) * 8) * TAPS);
+  }
+  // W_OIHW: thread = (output channel row, input channels 8 cg .. 8 cg + 7) with tid bits [cg & 3 | row & 3 | cg >> 2 |
+  // row >> 2], so the 16 lanes of one LDS write cover 4 rows x 4 chunks of one 32-channel half: 16 distinct 16-byte
+  // bank slots (row & 3 picks the 64-byte quarter of a 256-byte bank row, the swizzled chunk the slot in it)
+  const int f_row = ((tid >> 5) << 2) | ((tid >> 2) & 3), f_cg = (((tid >> 4) & 1) << 2) | (tid & 3);
+  if constexpr (W_OIHW) {
+    // [Cout][64][3][3] (the graph's own layout): the thread's 72 filter values are 144 contiguous bytes,
+    // transposed in registers after they land
+    const int co = min(f_row, args.cout - 1);
+    const uint4* src = reinterpret_cast<const uint4*>(Wt + (co * 64 + f_cg * 8) * TAPS);
 #pragma unroll
     for (int q = 0; q < TAPS; ++q) wv[q] = src[q];
   }
   // W_OIHW: writes the thread's 9 taps x 8 channels as 9 16-byte chunks (channel pairs packed per dword)
   auto store_filter = [&]() {
     if constexpr (W_OIHW) {
-      const int row = tid >> 3, cg = tid & 7;
+      const int row = f_row, cg = f_cg;
       uint16_t e[8 * TAPS];  // e[ci * 9 + tap]
       __builtin_memcpy(e, wv, sizeof(e));
       unsigned char* dst = lds + (cg >> 2) * A_CHUNK + row * 64 + (((cg & 3) ^ a_swizzle(row)) * 16);
@@ -1237,8 +1261,8 @@ __global__ __launch_bounds__(512) void conv_band_kernel(ConvBandArgs ba) {
       uint32_t d[4];
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
-        const uint32_t lo = reinterpret_cast<const uint32_t*>(&v[2 * k])[i / 2];
-        const uint32_t hi2 = reinterpret_cast<const uint32_t*>(&v[2 * k + 1])[i / 2];
+        const uint32_t lo = uint4_word(v[2 * k], i / 2);
+        const uint32_t hi2 = uint4_word(v[2 * k + 1], i / 2);
         d[k] = (i % 2 == 0) ? ((lo & 0xffffu) | (hi2 << 16)) : ((lo >> 16) | (hi2 & 0xffff0000u));
       }
       const int q = nr * rw + 1 + 8 * npg + i;
@@ -1265,7 +1289,7 @@ __global__ __launch_bounds__(512) void conv_band_kernel(ConvBandArgs ba) {
   // patch (rows = the tile's 32 pixels) and B the filter (columns = 32 channels), so each lane ends with one
   // channel's values for runs of four consecutive pixels (see store_tile).
   auto chunk = [&](f32x16_t (&acc)[TM], int pb, uint32_t a_base, uint32_t p_base) {
-    KFragments<TM, 1> f0, f1;
+    KFragments<TM, 1> f0, f1, f2;
     auto read_step = [&]<int STEP>(KFragments<TM, 1>& f) {
       constexpr int tap = STEP / 2, h = STEP % 2, kh = tap / 3, kw = tap % 3;
 #pragma unroll
@@ -1273,15 +1297,23 @@ __global__ __launch_bounds__(512) void conv_band_kernel(ConvBandArgs ba) {
       const int pos = pb + kh * rw + kw;
       f.b[0] = lds_read_b128<0>(p_base + pos * 64 + ((((2 * h + hi) ^ ((pos >> 2) & 3))) * 16));
     };
+    // fragments read two steps ahead (three buffers): before step s's MFMAs, every LDS read but step s+1's (the
+    // last TM + 1 issued; LDS reads complete in order) has landed
     read_step.template operator()<0>(f0);
+    read_step.template operator()<1>(f1);
     [&]<int... STEP>(std::integer_sequence<int, STEP...>) {
       (
           [&] {
             constexpr int s = STEP;
-            KFragments<TM, 1>& cur = (s % 2 == 0) ? f0 : f1;
-            KFragments<TM, 1>& nxt = (s % 2 == 0) ? f1 : f0;
-            fence_kfragments(cur);
-            if constexpr (s + 1 < 2 * TAPS) read_step.template operator()<s + 1>(nxt);
+            KFragments<TM, 1>& cur = (s % 3 == 0) ? f0 : (s % 3 == 1) ? f1 : f2;
+            KFragments<TM, 1>& ahead = (s % 3 == 0) ? f2 : (s % 3 == 1) ? f0 : f1;
+            if constexpr (s + 1 < 2 * TAPS) {
+              wait_lgkmcnt<TM + 1>();
+            } else {
+              wait_lgkmcnt<0>();
+            }
+            tie_kfragments(cur);
+            if constexpr (s + 2 < 2 * TAPS) read_step.template operator()<s + 2>(ahead);
 #pragma unroll
             for (int i = 0; i < TM; ++i) mfma32<T>(cur.b[0], cur.a[i], acc[i]);
             __builtin_amdgcn_sched_barrier(0);
@@ -1290,6 +1322,7 @@ __global__ __launch_bounds__(512) void conv_band_kernel(ConvBandArgs ba) {
     }(std::make_integer_sequence<int, 2 * TAPS>{});
     fence_kfragments(f0);
     fence_kfragments(f1);
+    fence_kfragments(f2);
   };
   // Writes the pixel tile px0 .. px0 + 31 of the band from registers. Register x of a lane holds pixel
   // px0 + 8 (x >> 2) + 4 hi + (x & 3) of channel 32 i + l32: the lanes l32 and l32 + 32 exchange one 4-pixel
