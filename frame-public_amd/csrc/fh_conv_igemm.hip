@@ -748,7 +748,7 @@ __global__ __launch_bounds__(512) void conv_halo_kernel(ConvHaloArgs ha) {
   asm volatile("" ::: "memory");
 
   const uint32_t lds_base = lds_addr((const FH_LDS void*)lds);
-  KFragments<TM, TN> f0, f1;
+  KFragments<TM, TN> f0, f1, f2;
   auto read_step = [&]<int STEP>(uint32_t ab, uint32_t pb, KFragments<TM, TN>& f) {
     constexpr int tap = STEP / 2, h = STEP % 2, kh = tap / 3, kw = tap % 3;
 #pragma unroll
@@ -781,15 +781,23 @@ __global__ __launch_bounds__(512) void conv_halo_kernel(ConvHaloArgs ha) {
     const uint32_t sb = lds_base + A_RES + buf * SB;
     const uint32_t ab = RES_A ? lds_base + c * A_CHUNK : sb;
     const uint32_t pb = sb + A_STEP;
+    // fragments read two steps ahead (three buffers): before step s's MFMAs every LDS operation but step s+1's
+    // reads (the last TM + TN issued; LDS operations complete in order) has completed
     read_step.template operator()<0>(ab, pb, f0);
+    read_step.template operator()<1>(ab, pb, f1);
     [&]<int... STEP>(std::integer_sequence<int, STEP...>) {
       (
           [&] {
             constexpr int s = STEP;
-            KFragments<TM, TN>& cur = (s % 2 == 0) ? f0 : f1;
-            KFragments<TM, TN>& nxt = (s % 2 == 0) ? f1 : f0;
-            fence_kfragments(cur);
-            if constexpr (s + 1 < 2 * TAPS) read_step.template operator()<s + 1>(ab, pb, nxt);
+            KFragments<TM, TN>& cur = (s % 3 == 0) ? f0 : (s % 3 == 1) ? f1 : f2;
+            KFragments<TM, TN>& ahead = (s % 3 == 0) ? f2 : (s % 3 == 1) ? f0 : f1;
+            if constexpr (s + 1 < 2 * TAPS) {
+              wait_lgkmcnt<TM + TN>();
+            } else {
+              wait_lgkmcnt<0>();
+            }
+            tie_kfragments(cur);
+            if constexpr (s + 2 < 2 * TAPS) read_step.template operator()<s + 2>(ab, pb, ahead);
             multiply(cur);
             __builtin_amdgcn_sched_barrier(0);
           }(),
@@ -797,6 +805,7 @@ __global__ __launch_bounds__(512) void conv_halo_kernel(ConvHaloArgs ha) {
     }(std::make_integer_sequence<int, 2 * TAPS>{});
     fence_kfragments(f0);
     fence_kfragments(f1);
+    fence_kfragments(f2);
     bool exact = true;  // the vmcnt wait below may leave this tile's NSTORE stores in flight
     if (c + 1 == nchunks) {
       // tile done: every wave has finished reading this step buffer, which then stages the output
@@ -1108,6 +1117,8 @@ __global__ __launch_bounds__(512, 4) void conv_halo1_kernel(ConvHaloArgs ha) {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    // one step ahead: at two workgroups per CU this kernel is held to 128 VGPRs, where a third fragment buffer
+    // measured 1-2 % slower
     read_step.template operator()<0>(f0);
     [&]<int... STEP>(std::integer_sequence<int, STEP...>) {
       (
