@@ -277,6 +277,54 @@ __global__ __launch_bounds__(256) void pool2d_nhwc_kernel(const typename Io<T>::
   }
 }
 
+// Pooling over whole planes (a 1 x 1 output, the window the plane, no padding; ResNet's global average pool):
+// thread = (image, pair of channels). All the pair's plane positions are loaded before the first is used, then
+// folded in the plane's row-major order, the order of pool2d_nhwc_kernel, so the results are the same bit for
+// bit. Two channels per thread (4-byte loads, 64 lanes on 256 contiguous bytes of a pixel) give 32 x more
+// threads than 16-byte vectors and one memory latency per thread.
+constexpr int kGlobalPoolMax = 64;  // plane positions per thread
+template <typename T, int MODE>
+__global__ __launch_bounds__(256) void pool_global_nhwc_kernel(const typename Io<T>::storage* __restrict__ x,
+                                                               typename Io<T>::storage* __restrict__ y, int32_t n,
+                                                               int32_t c, int32_t hw) {
+  using S = typename Io<T>::storage;
+  constexpr int VW = sizeof(S) == 2 ? 2 : 1;
+  struct Vec {
+    S v[VW];
+  };
+  const int pairs = c / VW;
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n * pairs) return;
+  const int img = i / pairs, cp = i - img * pairs;
+  const Vec* src = reinterpret_cast<const Vec*>(x + static_cast<int64_t>(img) * hw * c) + cp;
+  // every load unconditional (positions past the plane re-read its last one, never used), so none waits behind a
+  // branch and all are in flight together
+  Vec vals[kGlobalPoolMax];
+#pragma unroll
+  for (int p = 0; p < kGlobalPoolMax; ++p) vals[p] = src[static_cast<int64_t>(min(p, hw - 1)) * pairs];
+  float acc[VW];
+#pragma unroll
+  for (int e = 0; e < VW; ++e) acc[e] = 0.0f;
+#pragma unroll
+  for (int p = 0; p < kGlobalPoolMax; ++p) {
+    if (p >= hw) continue;  // uniform; no break, so the loop unrolls and vals keeps constant indices (registers)
+#pragma unroll
+    for (int e = 0; e < VW; ++e) {
+      const float f = Io<T>::load(vals[p].v[e]);
+      if (MODE == 0) {
+        if (p == 0 || f > acc[e]) acc[e] = f;
+      } else {
+        acc[e] += f;
+      }
+    }
+  }
+  const float denom = static_cast<float>(hw);
+  Vec o;
+#pragma unroll
+  for (int e = 0; e < VW; ++e) o.v[e] = Io<T>::store(MODE == 0 ? acc[e] : acc[e] / denom);
+  reinterpret_cast<Vec*>(y + static_cast<int64_t>(img) * c)[cp] = o;
+}
+
 template <typename T>
 fh_status launch_pool_nhwc(int32_t mode, const void* x, void* y, const PoolGeom& g, hipStream_t s) {
   using S = typename Io<T>::storage;
@@ -289,6 +337,18 @@ fh_status launch_pool_nhwc(int32_t mode, const void* x, void* y, const PoolGeom&
                        static_cast<int32_t>(g.w),  static_cast<int32_t>(g.kh), static_cast<int32_t>(g.kw),
                        static_cast<int32_t>(g.sh), static_cast<int32_t>(g.sw), static_cast<int32_t>(g.ph),
                        static_cast<int32_t>(g.pw), static_cast<int32_t>(g.oh), static_cast<int32_t>(g.ow)};
+  if (g.oh == 1 && g.ow == 1 && g.ph == 0 && g.pw == 0 && g.kh == g.h && g.kw == g.w && g.h * g.w <= kGlobalPoolMax &&
+      g.c % (sizeof(S) == 2 ? 2 : 1) == 0 && (reinterpret_cast<uintptr_t>(x) & 3) == 0 &&
+      (reinterpret_cast<uintptr_t>(y) & 3) == 0) {
+    const int32_t hw = static_cast<int32_t>(g.h * g.w), pairs = static_cast<int32_t>(g.c / (sizeof(S) == 2 ? 2 : 1));
+    const dim3 grid(static_cast<uint32_t>((g.n * pairs + 255) / 256));
+    const auto* xs = static_cast<const S*>(x);
+    auto* ys = static_cast<S*>(y);
+    const int32_t n32 = static_cast<int32_t>(g.n), c32 = static_cast<int32_t>(g.c);
+    if (mode == 0) hipLaunchKernelGGL((pool_global_nhwc_kernel<T, 0>), grid, dim3(256), 0, s, xs, ys, n32, c32, hw);
+    else hipLaunchKernelGGL((pool_global_nhwc_kernel<T, 1>), grid, dim3(256), 0, s, xs, ys, n32, c32, hw);
+    return launch_status("pool_global_nhwc_kernel launch");
+  }
   int64_t blocks = (total + 255) / 256;
   const int64_t cap = static_cast<int64_t>(device_cu_count()) * 16;
   if (blocks > cap) blocks = cap;

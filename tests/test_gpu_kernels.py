@@ -832,6 +832,12 @@ def test_conv2d_nhwc_channels_last_output(hip, dtype, geom):
     (0, (1, 16, 12, 12, 10, 10, 1, 1, 0, 0)), # window rows wider than one batch of 8 loads
     (1, (1, 24, 12, 12, 10, 9, 1, 1, 1, 0)),
     (0, (2, 8, 17, 15, 3, 3, 2, 2, 1, 1)),    # 3-wide rows (the fixed-width kernel), odd sizes: padded edges
+    # whole-plane windows (the whole-plane kernel: a channel pair per thread, all positions loaded first)
+    (1, (64, 512, 7, 7, 7, 7, 1, 1, 0, 0)),   # C4's global average pool
+    (0, (3, 10, 5, 5, 5, 5, 1, 1, 0, 0)),     # global max
+    (1, (2, 6, 8, 8, 8, 8, 1, 1, 0, 0)),      # 64 positions, the most the kernel holds
+    (1, (2, 6, 9, 9, 9, 9, 1, 1, 0, 0)),      # 81 positions: the general kernel
+    (1, (3, 7, 4, 4, 4, 4, 1, 1, 0, 0)),      # odd C: 16-bit pairs do not divide it, the general kernel
 ])
 def test_pool2d_nhwc(hip, dtype, mode, geom):
     say(f"pool nhwc mode={mode} dtype={dtype} {geom}")
