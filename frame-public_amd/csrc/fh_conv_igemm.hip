@@ -1719,6 +1719,41 @@ __global__ __launch_bounds__(256) void transpose_planes_multi_kernel(PlaneBatch 
   }
 }
 
+// 16-bit filters whose every plane is [Cin][9] or [Cin][1] with Cin % 8 == 0 (a ResNet's 3x3 and 1x1 convs), in
+// 16-byte vectors: thread = (tensor blockIdx.y, output channel, 8 input channels); a 3x3 thread loads its 8 x 9
+// values (144 contiguous bytes) and writes 9 vectors of 8 channels, one per tap; a 1x1 plane is its own
+// transpose (a copy). Lanes of one store write consecutive 16-byte vectors.
+__global__ __launch_bounds__(256) void transpose_filters_vec_kernel(PlaneBatch a) {
+  const int ti = blockIdx.y;
+  const int rows = a.rows[ti], cols = a.cols[ti], groups = rows / 8;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= static_cast<int64_t>(a.batch[ti]) * groups) return;
+  const int64_t co = i / groups, cg = i - co * groups;
+  const uint16_t* x = static_cast<const uint16_t*>(a.x[ti]);
+  uint16_t* y = static_cast<uint16_t*>(a.y[ti]);
+  if (cols == 1) {
+    *reinterpret_cast<uint4*>(y + co * rows + cg * 8) = *reinterpret_cast<const uint4*>(x + co * rows + cg * 8);
+    return;
+  }
+  const uint4* src = reinterpret_cast<const uint4*>(x + (co * rows + cg * 8) * 9);
+  uint4 v[9];
+#pragma unroll
+  for (int q = 0; q < 9; ++q) v[q] = src[q];
+  // value (channel c, tap t) is element c * 9 + t of the 72 loaded
+  auto value = [&](int f) -> uint32_t {
+    const uint32_t w = uint4_word(v[f / 8], (f % 8) / 2);
+    return (f % 2 == 0) ? (w & 0xffffu) : (w >> 16);
+  };
+  uint16_t* dst = y + co * 9 * rows + cg * 8;
+#pragma unroll
+  for (int t = 0; t < 9; ++t) {
+    uint32_t d[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) d[k] = value((2 * k) * 9 + t) | (value((2 * k + 1) * 9 + t) << 16);
+    *reinterpret_cast<uint4*>(dst + t * rows) = uint4{d[0], d[1], d[2], d[3]};
+  }
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
 // K of a C8 filter: KH*KW positions of 8 channels, rounded up to whole stages.
@@ -1860,8 +1895,20 @@ extern "C" fh_status fh_transpose_planes_multi(int32_t itemsize, int32_t n, cons
     max_batch = std::max<int64_t>(max_batch, a.batch[i]);
   }
   if (max_batch == 0) return FH_OK;
-  const dim3 grid(static_cast<uint32_t>(max_batch), static_cast<uint32_t>(n));
   hipStream_t s = static_cast<hipStream_t>(stream);
+  bool vec = itemsize == 2;
+  int64_t max_threads = 0;
+  for (int i = 0; i < n && vec; ++i) {
+    if (a.batch[i] == 0) continue;
+    vec = a.rows[i] % 8 == 0 && (a.cols[i] == 1 || a.cols[i] == 9) && aligned16(xs[i]) && aligned16(ys[i]);
+    max_threads = std::max<int64_t>(max_threads, static_cast<int64_t>(a.batch[i]) * (a.rows[i] / 8));
+  }
+  if (vec) {
+    const dim3 vgrid(static_cast<uint32_t>((max_threads + 255) / 256), static_cast<uint32_t>(n));
+    hipLaunchKernelGGL(transpose_filters_vec_kernel, vgrid, dim3(256), 0, s, a);
+    return launch_status("transpose_filters_vec_kernel launch");
+  }
+  const dim3 grid(static_cast<uint32_t>(max_batch), static_cast<uint32_t>(n));
   if (itemsize == 2) {
     hipLaunchKernelGGL(transpose_planes_multi_kernel<uint16_t>, grid, dim3(256), 0, s, a);
   } else {

@@ -498,11 +498,15 @@ def test_transpose_batched(hip, itemsize, shape):
 
 
 @pytest.mark.parametrize("itemsize", [2, 4])
-def test_transpose_planes_multi(hip, itemsize):
-    # three tensors of different batch and plane shape (filters of a 3x3, a 1x1 and a 7-wide conv) in one launch
-    say(f"transpose_planes_multi itemsize={itemsize}")
+@pytest.mark.parametrize("shapes", [
+    [(64, 64, 9), (128, 64, 1), (5, 33, 7)],     # a 7-wide plane and 33 channels: the per-plane LDS kernel
+    [(64, 64, 9), (128, 64, 1), (512, 512, 9)],  # 16-bit 3x3 and 1x1 with Cin % 8 == 0: the 16-byte vector kernel
+    [(3, 8, 9), (1, 8, 9), (7, 16, 1)],          # one or two 8-channel groups per plane
+])
+def test_transpose_planes_multi(hip, itemsize, shapes):
+    # tensors of different batch and plane shape (filters of 3x3, 1x1 and other convs) in one launch
+    say(f"transpose_planes_multi itemsize={itemsize} {shapes}")
     dt = np.uint16 if itemsize == 2 else np.uint32
-    shapes = [(64, 64, 9), (128, 64, 1), (5, 33, 7)]
     rng = np.random.default_rng(11)
     xs = [rng.integers(0, np.iinfo(dt).max, size=s, dtype=dt) for s in shapes]
     dxs = [dev(hip, x) for x in xs]
