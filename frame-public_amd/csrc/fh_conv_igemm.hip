@@ -1299,17 +1299,26 @@ __global__ __launch_bounds__(512) void conv_band_kernel(ConvBandArgs ba) {
   // One chunk of the pixel tile whose tap-(0, 0) patch position for this lane is pb. The MFMA's A operand is the
   // patch (rows = the tile's 32 pixels) and B the filter (columns = 32 channels), so each lane ends with one
   // channel's values for runs of four consecutive pixels (see store_tile).
-  auto chunk = [&](f32x16_t (&acc)[TM], int pb, uint32_t a_base, uint32_t p_base) {
+  // ONLY: -1 multiplies both 32-channel halves of the tile, 0 or 1 that half alone (one filter fragment and one
+  // MFMA per step; acc[ONLY] is the only accumulator written).
+  auto chunk = [&]<int ONLY>(f32x16_t (&acc)[TM], int pb, uint32_t a_base, uint32_t p_base) {
+    constexpr int I0 = ONLY < 0 ? 0 : ONLY, I1 = ONLY < 0 ? TM : ONLY + 1;
+    constexpr int READS = I1 - I0 + 1;  // LDS reads per step
     KFragments<TM, 1> f0, f1, f2;
     auto read_step = [&]<int STEP>(KFragments<TM, 1>& f) {
       constexpr int tap = STEP / 2, h = STEP % 2, kh = tap / 3, kw = tap % 3;
 #pragma unroll
-      for (int i = 0; i < TM; ++i) f.a[i] = lds_read_b128<tap * BM * 64>(a_base + a_off[i][h]);
+      for (int i = I0; i < I1; ++i) f.a[i] = lds_read_b128<tap * BM * 64>(a_base + a_off[i][h]);
       const int pos = pb + kh * rw + kw;
       f.b[0] = lds_read_b128<0>(p_base + pos * 64 + ((((2 * h + hi) ^ ((pos >> 2) & 3))) * 16));
     };
+    auto tie = [&](KFragments<TM, 1>& f) {
+#pragma unroll
+      for (int i = I0; i < I1; ++i) asm volatile("" : "+v"(f.a[i]));
+      asm volatile("" : "+v"(f.b[0]));
+    };
     // fragments read two steps ahead (three buffers): before step s's MFMAs, every LDS read but step s+1's (the
-    // last TM + 1 issued; LDS reads complete in order) has landed
+    // last READS issued; LDS reads complete in order) has landed
     read_step.template operator()<0>(f0);
     read_step.template operator()<1>(f1);
     [&]<int... STEP>(std::integer_sequence<int, STEP...>) {
@@ -1319,21 +1328,22 @@ __global__ __launch_bounds__(512) void conv_band_kernel(ConvBandArgs ba) {
             KFragments<TM, 1>& cur = (s % 3 == 0) ? f0 : (s % 3 == 1) ? f1 : f2;
             KFragments<TM, 1>& ahead = (s % 3 == 0) ? f2 : (s % 3 == 1) ? f0 : f1;
             if constexpr (s + 1 < 2 * TAPS) {
-              wait_lgkmcnt<TM + 1>();
+              wait_lgkmcnt<READS>();
             } else {
               wait_lgkmcnt<0>();
             }
-            tie_kfragments(cur);
+            tie(cur);
             if constexpr (s + 2 < 2 * TAPS) read_step.template operator()<s + 2>(ahead);
 #pragma unroll
-            for (int i = 0; i < TM; ++i) mfma32<T>(cur.b[0], cur.a[i], acc[i]);
+            for (int i = I0; i < I1; ++i) mfma32<T>(cur.b[0], cur.a[i], acc[i]);
             __builtin_amdgcn_sched_barrier(0);
           }(),
           ...);
     }(std::make_integer_sequence<int, 2 * TAPS>{});
-    fence_kfragments(f0);
-    fence_kfragments(f1);
-    fence_kfragments(f2);
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    tie(f0);
+    tie(f1);
+    tie(f2);
   };
   // Writes the pixel tile px0 .. px0 + 31 of the band from registers. Register x of a lane holds pixel
   // px0 + 8 (x >> 2) + 4 hi + (x & 3) of channel 32 i + l32: the lanes l32 and l32 + 32 exchange one 4-pixel
@@ -1342,9 +1352,9 @@ __global__ __launch_bounds__(512) void conv_band_kernel(ConvBandArgs ba) {
   S* __restrict__ Y = static_cast<S*>(args.y);
   const int64_t ybase = static_cast<int64_t>(img) * args.cout * args.howo + static_cast<int64_t>(r0) * W;
   constexpr int EA = epi_after_stage<E>();
-  auto store_tile = [&](f32x16_t (&acc)[TM], int px0) {
+  auto store_tile = [&]<int ONLY>(f32x16_t (&acc)[TM], int px0) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
+    for (int i = ONLY < 0 ? 0 : ONLY; i < (ONLY < 0 ? TM : ONLY + 1); ++i) {
       const int co = i * 32 + l32;
       const float b = bias_v[i];
       // runs 2 half and 2 half + 1 (registers 8 half .. 8 half + 7): pixels 16 half + 4 hi + 0..3 and
@@ -1395,27 +1405,53 @@ __global__ __launch_bounds__(512) void conv_band_kernel(ConvBandArgs ba) {
     const int pb = patch_pos(px0);
     f32x16_t acc[TM];
     zero(acc);
-    if (active) chunk(acc, pb, ab, ab + A_BYTES);
+    if (active) chunk.template operator()<-1>(acc, pb, ab, ab + A_BYTES);
     wait_vmcnt<0>();
     store_chunk(v, lds + A_BYTES + PB);
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     if (active) {
-      chunk(acc, pb, ab + A_CHUNK, ab + A_BYTES + PB);
-      store_tile(acc, px0);
+      chunk.template operator()<-1>(acc, pb, ab + A_CHUNK, ab + A_BYTES + PB);
+      store_tile.template operator()<-1>(acc, px0);
     }
   }
-  // phase 1: pixels 256 + 32 wave .. (the LDS operands are read-only from here; phase 0's stores drain meanwhile)
+  // phase 1: tiles 8 .. ntiles - 1 (pixels from 256; the LDS operands are read-only from here, phase 0's stores
+  // drain meanwhile). Wave w runs on SIMD w % 4, and phase 0 gave every SIMD two tiles. When the phase holds
+  // 4 k + 1 tiles, its last tile goes to waves n1 and n1 + 1 (SIMDs 1 and 2) as two 32-channel halves instead of
+  // to wave n1 - 1 (SIMD 0) whole: C3's bands of 13 tiles then hold 3.5 tiles on their busiest SIMD, not 4.
   {
-    const int px0 = 256 + wave * 32;
-    if (px0 < npx) {
+    const int ntiles = (npx + 31) / 32, n1 = ntiles - 8;
+    const bool split = n1 > 0 && (n1 & 3) == 1;
+    int tile = -1, half = -1;  // uniform per wave
+    if (split) {
+      if (wave < n1 - 1) {
+        tile = 8 + wave;
+      } else if (wave == n1 || wave == n1 + 1) {
+        tile = 8 + n1 - 1;
+        half = wave - n1;
+      }
+    } else if (wave < n1) {
+      tile = 8 + wave;
+    }
+    if (tile >= 0) {
+      const int px0 = tile * 32;
       const int pb = patch_pos(px0);
       f32x16_t acc[TM];
       zero(acc);
-      chunk(acc, pb, ab, ab + A_BYTES);
-      chunk(acc, pb, ab + A_CHUNK, ab + A_BYTES + PB);
-      store_tile(acc, px0);
+      if (half < 0) {
+        chunk.template operator()<-1>(acc, pb, ab, ab + A_BYTES);
+        chunk.template operator()<-1>(acc, pb, ab + A_CHUNK, ab + A_BYTES + PB);
+        store_tile.template operator()<-1>(acc, px0);
+      } else if (half == 0) {
+        chunk.template operator()<0>(acc, pb, ab, ab + A_BYTES);
+        chunk.template operator()<0>(acc, pb, ab + A_CHUNK, ab + A_BYTES + PB);
+        store_tile.template operator()<0>(acc, px0);
+      } else {
+        chunk.template operator()<1>(acc, pb, ab, ab + A_BYTES);
+        chunk.template operator()<1>(acc, pb, ab + A_CHUNK, ab + A_BYTES + PB);
+        store_tile.template operator()<1>(acc, px0);
+      }
     }
   }
 }

@@ -660,6 +660,7 @@ NCHW_IN_CASES = [
     (BF16, (256, 64, 16, 16, 64, 3, 3, 1, 1, 1, 1, 1), 0),   # whole-image bands: both halo rows zero, 4 waves idle
     (BF16, (64, 64, 8, 64, 40, 3, 3, 1, 1, 1, 1, 1), 0),     # Cout 40, W 64
     (BF16, (3, 64, 12, 40, 48, 3, 3, 1, 1, 1, 1, 1), 0),     # 1-row bands (fewer rows than CUs)
+    (BF16, (128, 64, 12, 48, 64, 3, 3, 1, 1, 1, 1, 1), 0),   # 6-row bands of 9 tiles: the 9th split in channel halves
     # the single-buffered kernel
     (BF16, (3, 96, 9, 16, 40, 3, 3, 1, 1, 1, 1, 1), 0),      # Cout 40, three chunks, 128-pixel tiles
     (BF16, (5, 32, 3, 8, 100, 3, 3, 1, 1, 1, 1, 1), 1),      # 3-row images, one 8-pixel group per row
@@ -701,7 +702,7 @@ def test_conv2d_nchw_input(hip, dtype, geom, nhwc_out):
 
 
 @pytest.mark.parametrize("geom", [(32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1), (64, 64, 8, 64, 40, 3, 3, 1, 1, 1, 1, 1),
-                                  (3, 64, 12, 40, 48, 3, 3, 1, 1, 1, 1, 1)])
+                                  (3, 64, 12, 40, 48, 3, 3, 1, 1, 1, 1, 1), (128, 64, 12, 48, 64, 3, 3, 1, 1, 1, 1, 1)])
 def test_conv2d_band_residual(hip, geom):
     """The band kernel (NCHW input and output) with the residual add;relu program and no bias: both images at the
     ends of the batch and 4,096 sampled outputs against the oracle."""
@@ -729,7 +730,7 @@ def test_conv2d_band_residual(hip, geom):
 
 BAND_GEOMS = [(32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1), (16, 64, 32, 56, 64, 3, 3, 1, 1, 1, 1, 1),
               (256, 64, 16, 16, 64, 3, 3, 1, 1, 1, 1, 1), (64, 64, 8, 64, 40, 3, 3, 1, 1, 1, 1, 1),
-              (3, 64, 12, 40, 48, 3, 3, 1, 1, 1, 1, 1)]
+              (3, 64, 12, 40, 48, 3, 3, 1, 1, 1, 1, 1), (128, 64, 12, 48, 64, 3, 3, 1, 1, 1, 1, 1)]
 
 
 @pytest.mark.parametrize("geom", BAND_GEOMS)
