@@ -272,19 +272,29 @@ def test_conv_lowering_by_dtype_and_channels(dtype, cin, lowered):
         assert "hip_conv2d_nhwc_internal" not in out
 
 
-def test_resnet_lowering_is_channels_last_throughout():
-    # every non-stem conv filter is a graph input: one batched channels-last step instead of one per layer; every
-    # activation is produced and consumed channels-last (convs, residual epilogues, both pools, the 1x1 reshape),
-    # so no activation transpose is left
+def test_resnet_lowering_layouts():
+    # every conv filter that needs it is transposed in one batched channels-last step; the 56x56 (here 16x16) layer's
+    # four convs are band convs (Cin 64, Cout 64, 3x3): that layer, the stem's output and the max pool stay NCHW and
+    # those convs read their filters as they are (w_oihw); everything after it is channels-last, with one
+    # channels-last copy of the layer's output for the next layer's two convs
     g, _ = graphs.resnet18(batch=2, dtype=3, image=64)
     out = host.hip_lowered(g.text(), 1)
     ops = re.findall(r"= (\w+)\(", out)
     assert ops.count("hip_channels_last_multi_internal") == 1
     assert ops.count("hip_conv2d_nhwc_internal") == 20
-    assert ops.count("hip_channels_last_internal") == 0
-    assert ops.count("hip_max_pool2d_nhwc_internal") == 1 and ops.count("hip_avg_pool2d_nhwc_internal") == 1
+    assert out.count("w_oihw=1") == 4 and out.count("in_nchw=1") == 4
+    assert ops.count("hip_channels_last_internal") == 1
+    assert ops.count("max_pool2d") == 1 and ops.count("hip_avg_pool2d_nhwc_internal") == 1
     assert ops.count("graph_input") == 43
-    assert out.count("out_nhwc=1") == 20
+    assert out.count("out_nhwc=1") == 15
+
+
+def test_training_lowering_keeps_band_layer_channels_last():
+    # the NCHW preference for band convs applies to forward graphs only: a training graph's layout plan is unchanged
+    g, specs = graphs.resnet18(batch=2, dtype=3, image=64, train=True)
+    text = host.backward(g.text(), 0, list(range(1, len(specs) + 1)))
+    out = host.hip_lowered(text, 1)
+    assert "w_oihw=1" not in out
 
 
 def _conv_chain(last_is_output=True, softmax_tail=False):
