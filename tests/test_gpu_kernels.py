@@ -871,7 +871,8 @@ def test_maxpool_nhwc_signed_zero_and_nan_selection(hip, dtype):
     assert_bitwise(dy.download(want.shape, want.dtype), want, "maxpool nhwc special values")
 
 
-@pytest.mark.parametrize("n,c,hw", [(3, 3, 224 * 8), (2, 1, 64), (1, 8, 40), (2, 3, 50), (1, 5, 7), (4, 3, 300)])
+@pytest.mark.parametrize("n,c,hw", [(3, 3, 224 * 8), (2, 1, 64), (1, 8, 40), (2, 3, 50), (1, 5, 7), (4, 3, 300),
+                                    (2, 3, 224 * 224), (1, 7, 1028), (3, 2, 4)])  # a whole 224x224 plane, odd C
 def test_conv_pack_input_c8(hip, n, c, hw):
     # [N][C][HW] -> [N][HW][8] with channels C..7 zero (one pixel per thread, the image from the grid's y)
     say(f"pack input c8 n={n} c={c} hw={hw}")
