@@ -442,6 +442,30 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
     t.shape = Shape({s.dim(0), s.dim(2), s.dim(3), s.dim(1)});
     return t;
   };
+  // A channels-last pool to a 1x1 plane whose only use is a reshape to [N, C] (ResNet's global pool before the
+  // FC): [N,1,1,C] and [N,C] are the same bytes, so the pool writes the reshape's type and the reshape (a device
+  // copy and a launch) goes away.
+  std::unordered_map<const ir::Node*, const ir::Node*> reshaped_pool;  // pool -> its reshape
+  std::unordered_set<const ir::Node*> folded_reshape;
+  {
+    std::unordered_map<const ir::Value*, int> n_uses;
+    for (const ir::Node* n : src.topological_order())
+      for (const ir::Value* in : n->inputs()) ++n_uses[in];
+    std::unordered_set<const ir::Value*> outs(src.outputs().begin(), src.outputs().end());
+    for (const ir::Node* r : src.topological_order()) {
+      if (r->op() != "reshape" || r->inputs().size() != 1 || r->outputs().size() != 1) continue;
+      const ir::Value* v = r->inputs()[0];
+      const ir::Node* p = v->producer();
+      if (p == nullptr || (p->op() != "max_pool2d" && p->op() != "avg_pool2d") || p->outputs().size() != 1) continue;
+      const Shape& vs = v->type().shape;
+      const Shape& rs = r->outputs()[0].type().shape;
+      if (!nhwc.count(v) || outs.count(v) || n_uses[v] != 1 || vs.rank() != 4 || vs.dim(2) != 1 || vs.dim(3) != 1 ||
+          rs.rank() != 2 || rs.dim(0) != vs.dim(0) || rs.dim(1) != vs.dim(1) || nhwc.count(&r->outputs()[0]))
+        continue;
+      reshaped_pool[p] = r;
+      folded_reshape.insert(r);
+    }
+  }
   std::unordered_map<const ir::Value*, ir::Value*> cl_copies;  // one channels-last copy per value
   auto channels_last = [&](ir::Value* v) -> Result<ir::Value*> {
     if (auto it = cl_copies.find(v); it != cl_copies.end()) return it->second;
@@ -631,8 +655,13 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
       map[&n->outputs()[0]] = c.value()->output(0);
       continue;
     }
+    if (auto it = folded_reshape.find(n); it != folded_reshape.end()) {  // the pool below already has its type
+      map[&n->outputs()[0]] = map.at(n->inputs()[0]);
+      continue;
+    }
     std::vector<ir::TensorType> types;
     for (const ir::Value& o : n->outputs()) types.push_back(lowered_type(&o));
+    if (auto it = reshaped_pool.find(n); it != reshaped_pool.end()) types[0] = it->second->outputs()[0].type();
     std::string op(n->op());
     if (n->outputs().size() == 1 && nhwc.count(&n->outputs()[0])) {  // pools of channels-last activations
       if (op == "max_pool2d") op = std::string(kMaxPoolNhwcOp);

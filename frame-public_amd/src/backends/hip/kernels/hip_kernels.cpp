@@ -829,7 +829,10 @@ Status pool_nhwc_kernel(KernelContext& ctx) {
                             (*k)[1],          (*s)[0],          (*s)[1],          (*p)[0],          (*p)[1]};
   const int64_t oh = (geom[2] + 2 * geom[8] - geom[4]) / geom[6] + 1;
   const int64_t ow = (geom[3] + 2 * geom[9] - geom[5]) / geom[7] + 1;
-  if (ctx.outputs[0].shape() != Shape({geom[0], oh, ow, geom[1]})) return invalid(op, "output shape does not match the geometry");
+  // a 1x1 output plane may come typed [N, C] (the same bytes; a reshape folded into the pool)
+  const bool flat = oh == 1 && ow == 1 && ctx.outputs[0].shape() == Shape({geom[0], geom[1]});
+  if (!flat && ctx.outputs[0].shape() != Shape({geom[0], oh, ow, geom[1]}))
+    return invalid(op, "output shape does not match the geometry");
   FRAME_HIP_RETURN_IF_ERROR(fh_pool2d_nhwc(dt.value(), Mode, x.raw_data(), ctx.outputs[0].raw_data(), geom,
                                            stream_handle(ctx)),
                             "op '" + op + "' (hip)");
