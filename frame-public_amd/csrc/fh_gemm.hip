@@ -389,14 +389,31 @@ __global__ __launch_bounds__(kSplitWaves * 64) void gemm_split_kernel(GemmArgs a
   float acc = 0.0f;
   for (int64_t k0 = 0; k0 < K; k0 += kSplitKC) {
     const int kn = static_cast<int>(min<int64_t>(kSplitKC, K - k0));
-    if (k0 > 0) __syncthreads();  // the previous chunk has been read
-    for (int i = t; i < kSplitTM * kn; i += NT) {
-      const int row = i / kn, kk = i - row * kn;
-      As[row * kSplitKP + kk] = (m0 + row < M) ? Io<T>::load(A[(m0 + row) * args.lda + k0 + kk]) : 0.0f;
+    // every element of the chunk this thread stages is loaded into registers before the first is written to LDS,
+    // so the loads overlap (a load-then-store loop waits for each load in turn)
+    constexpr int AJ = kSplitTM * kSplitKC / NT, BJ = kSplitTN * kSplitKC / NT;
+    static_assert(kSplitTM * kSplitKC % NT == 0 && kSplitTN * kSplitKC % NT == 0, "whole staging rounds");
+    float av[AJ], bv[BJ];
+#pragma unroll
+    for (int j = 0; j < AJ; ++j) {
+      const int i = t + j * NT, row = i / kSplitKC, kk = i - row * kSplitKC;
+      av[j] = (kk < kn && m0 + row < M) ? Io<T>::load(A[(m0 + row) * args.lda + k0 + kk]) : 0.0f;
     }
-    for (int i = t; i < kSplitTN * kn; i += NT) {
-      const int kk = i >> 4, cc = i & 15;
-      Bt[cc * kSplitKP + kk] = (n0 + cc < N) ? Io<T>::load(B[(k0 + kk) * args.ldb + n0 + cc]) : 0.0f;
+#pragma unroll
+    for (int j = 0; j < BJ; ++j) {
+      const int i = t + j * NT, kk = i >> 4, cc = i & 15;
+      bv[j] = (kk < kn && n0 + cc < N) ? Io<T>::load(B[(k0 + kk) * args.ldb + n0 + cc]) : 0.0f;
+    }
+    if (k0 > 0) __syncthreads();  // the previous chunk has been read
+#pragma unroll
+    for (int j = 0; j < AJ; ++j) {
+      const int i = t + j * NT, row = i / kSplitKC, kk = i - row * kSplitKC;
+      if (kk < kn) As[row * kSplitKP + kk] = av[j];
+    }
+#pragma unroll
+    for (int j = 0; j < BJ; ++j) {
+      const int i = t + j * NT, kk = i >> 4, cc = i & 15;
+      if (kk < kn) Bt[cc * kSplitKP + kk] = bv[j];
     }
     __syncthreads();
     const int per = (kn + kSplitWaves - 1) / kSplitWaves;
