@@ -481,15 +481,16 @@ __device__ __forceinline__ uint4 epi_vec(const EP& ep, uint4 packed, int64_t idx
   }
 }
 
+// CUs of the device current at the first call (256, MI355X's count, when no device is visible), read once per
+// process under the function-local static's thread-safe initialisation. Launch shapes and the band conv's
+// geometry choice depend on it, so the lowering (and the lowered text) of a graph does too.
 inline int device_cu_count() {
-  static int cached = 0;
-  if (cached == 0) {
-    int dev = 0;
-    (void)hipGetDevice(&dev);
+  static const int cached = [] {
+    int dev = 0, cus = 0;
     hipDeviceProp_t prop;
-    if (hipGetDeviceProperties(&prop, dev) == hipSuccess) cached = prop.multiProcessorCount;
-    if (cached <= 0) cached = 256;
-  }
+    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess) cus = prop.multiProcessorCount;
+    return cus > 0 ? cus : 256;
+  }();
   return cached;
 }
 

@@ -1240,9 +1240,10 @@ __global__ __launch_bounds__(512) void conv_band_kernel(ConvBandArgs ba) {
       }
     }
   };
-  // the padding columns (positions 0 and W + 1 of every patch row) of both patches
-  if (tid < 2 * (R + 2) * 8) {
-    const int buf = tid / ((R + 2) * 8), z = tid % ((R + 2) * 8);
+  // the padding columns (positions 0 and W + 1 of every patch row) of both patches: 2 (R + 2) 8 16-byte slots,
+  // more than the 512 threads when R > 30 (W = 8 allows R up to 62)
+  for (int t = tid; t < 2 * (R + 2) * 8; t += 512) {
+    const int buf = t / ((R + 2) * 8), z = t % ((R + 2) * 8);
     const int q = (z >> 3) * rw + ((z >> 2) & 1) * (W + 1);
     *reinterpret_cast<uint4*>(lds + A_BYTES + buf * PB + q * 64 + (z & 3) * 16) = uint4{0, 0, 0, 0};
   }

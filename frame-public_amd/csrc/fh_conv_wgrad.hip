@@ -271,23 +271,35 @@ constexpr int64_t kWgradScratchBytes = int64_t{64} << 20;
 constexpr int kScratchMaxDevices = 64;
 static __device__ __align__(256) unsigned char scratch[kWgradScratchBytes];
 
+// Calls on one device are ordered through the array: each call's stream first waits for the event the previous
+// call recorded after its kernels (on whatever stream that was), and the call records it again after its own.
+// g_scratch_mu is held from the wait to the record, so the order is the order in which the host made the calls.
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kScratchMaxDevices] = {};
+hipEvent_t g_scratch_done[kScratchMaxDevices] = {};
 
-fh_status scratch_of_current_device(void** out) {
+// Set-up, once per device with that device current (g_scratch_mu held): the array's device address and the
+// ordering event. No device memory is allocated.
+fh_status scratch_of_current_device_locked(int* dev_out, void** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess) return fail(FH_DEVICE_ERROR, "fh_conv2d_wgrad_nhwc_noalloc: hipGetDevice failed");
   if (dev < 0 || dev >= kScratchMaxDevices)
     return fail(FH_UNIMPLEMENTED, "fh_conv2d_wgrad_nhwc_noalloc: device index above 63");
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
     void* p = nullptr;
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || p == nullptr)
       return fail(FH_DEVICE_ERROR, std::string("fh_conv2d_wgrad_nhwc_noalloc: hipGetSymbolAddress(scratch): ") +
                                        hipGetErrorString(e));
+    hipEvent_t ev = nullptr;
+    const hipError_t ee = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (ee != hipSuccess)
+      return fail(FH_DEVICE_ERROR, std::string("fh_conv2d_wgrad_nhwc_noalloc: hipEventCreateWithFlags: ") +
+                                       hipGetErrorString(ee));
+    g_scratch_done[dev] = ev;
     g_scratch_ptr[dev] = p;
   }
+  *dev_out = dev;
   *out = g_scratch_ptr[dev];
   return FH_OK;
 }
@@ -361,7 +373,18 @@ extern "C" fh_status fh_conv2d_wgrad_nhwc_noalloc(int32_t dtype, const void* x, 
     return fail(FH_INVALID_ARGUMENT, "fh_conv2d_wgrad_nhwc_noalloc: the split-K partials need " + std::to_string(need) +
                                          " bytes, above the " + std::to_string(kWgradScratchBytes) +
                                          "-byte no-allocation scratch (use fh_conv2d_wgrad_nhwc with a workspace)");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
   void* ws = nullptr;
-  if (fh_status st = scratch_of_current_device(&ws); st != FH_OK) return st;
-  return fh_conv2d_wgrad_nhwc(dtype, x, dy, dw, ws, need, geom, cin_pad, stream);
+  int dev = -1;
+  if (fh_status st = scratch_of_current_device_locked(&dev, &ws); st != FH_OK) return st;
+  // Under graph capture the graph's own dependencies order the work (an event recorded outside the capture is not
+  // waited on there): overlapping replays of such graphs on one device race.
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  FH_HIP_CHECK(hipStreamIsCapturing(s, &cap));
+  const bool order = cap == hipStreamCaptureStatusNone;
+  if (order) FH_HIP_CHECK(hipStreamWaitEvent(s, g_scratch_done[dev], 0));
+  if (fh_status st = fh_conv2d_wgrad_nhwc(dtype, x, dy, dw, ws, need, geom, cin_pad, stream); st != FH_OK) return st;
+  if (order) FH_HIP_CHECK(hipEventRecord(g_scratch_done[dev], s));
+  return FH_OK;
 }

@@ -125,6 +125,14 @@ fh_status fh_stream_create(void** stream, int32_t device) {
   return FH_OK;
 }
 
+fh_status fh_stream_capturing(void* stream, int32_t* capturing) {
+  if (capturing == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_stream_capturing: capturing is null");
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  FH_HIP_CHECK(hipStreamIsCapturing(static_cast<hipStream_t>(stream), &st));
+  *capturing = st == hipStreamCaptureStatusNone ? 0 : 1;
+  return FH_OK;
+}
+
 fh_status fh_stream_destroy(void* stream) {
   if (stream == nullptr) return FH_OK;
   FH_HIP_CHECK(hipStreamDestroy(static_cast<hipStream_t>(stream)));

@@ -36,6 +36,8 @@ _SIGS = {
     "frame_backends": (c_int32, [c_void_p, c_int64, POINTER(c_int64)]),
     "frame_device_count": (c_int32, [c_char_p, POINTER(c_int32)]),
     "frame_tensor_empty": (c_int32, [c_char_p, c_int32, c_int32, POINTER(c_int64), c_int32, POINTER(c_void_p)]),
+    "frame_tensor_empty_at": (c_int32, [c_char_p, c_int32, c_int32, POINTER(c_int64), c_int32, c_int64,
+                                        POINTER(c_void_p)]),
     "frame_tensor_free": (None, [c_void_p]),
     "frame_tensor_data": (c_void_p, [c_void_p]),
     "frame_tensor_nbytes": (c_int64, [c_void_p]),
@@ -163,20 +165,25 @@ def compile_cache_size() -> int:
 class Tensor:
     """A frame::Tensor allocated by a backend's allocator (device memory for hip)."""
 
-    def __init__(self, backend: str, dtype: int, shape, device: int = 0, _handle=None):
+    def __init__(self, backend: str, dtype: int, shape, device: int = 0, _handle=None, byte_offset: int = 0):
+        """byte_offset > 0: a view that starts that many bytes into its own block (Tensor::from_storage_slice)."""
         self.backend, self.dtype, self.shape = backend, int(dtype), tuple(int(d) for d in shape)
         if _handle is None:
             h = c_void_p()
             dims = (c_int64 * max(1, len(self.shape)))(*self.shape)
-            check(lib().frame_tensor_empty(backend.encode(), device, self.dtype, dims, len(self.shape), ctypes.byref(h)),
-                  "frame_tensor_empty")
+            if byte_offset:
+                check(lib().frame_tensor_empty_at(backend.encode(), device, self.dtype, dims, len(self.shape),
+                                                  byte_offset, ctypes.byref(h)), "frame_tensor_empty_at")
+            else:
+                check(lib().frame_tensor_empty(backend.encode(), device, self.dtype, dims, len(self.shape),
+                                               ctypes.byref(h)), "frame_tensor_empty")
             _handle = h
         self.handle = _handle
 
     @classmethod
-    def from_numpy(cls, backend: str, dtype: int, array: np.ndarray) -> "Tensor":
+    def from_numpy(cls, backend: str, dtype: int, array: np.ndarray, byte_offset: int = 0) -> "Tensor":
         a = np.ascontiguousarray(array, dtype=_NP[dtype])  # (ndim >= 1: a rank-0 array comes back as [1])
-        t = cls(backend, dtype, np.shape(array))
+        t = cls(backend, dtype, np.shape(array), byte_offset=byte_offset)
         check(lib().frame_tensor_upload(t.handle, a.ctypes.data, a.nbytes), "frame_tensor_upload")
         return t
 
@@ -299,10 +306,12 @@ def backend_copy(backend: str, dst: int, dst_backend: str, src: int, src_backend
 
 
 def allocator_stats(device: int = 0) -> dict:
-    """The hip caching allocator's counters (bytes live / reusable / waiting for the device, allocations, waits)."""
-    out = (ctypes.c_uint64 * 5)()
+    """The hip caching allocator's counters (bytes live / reusable / freed with work possibly queued, allocations,
+    device-wide waits, waits on one freed block's fence)."""
+    out = (ctypes.c_uint64 * 6)()
     check(lib().frame_hip_allocator_stats(device, out), "frame_hip_allocator_stats")
-    return dict(zip(("live", "cached", "pending", "device_allocations", "device_syncs"), [int(v) for v in out]))
+    return dict(zip(("live", "cached", "pending", "device_allocations", "device_syncs", "fence_waits"),
+                    [int(v) for v in out]))
 
 
 def onnx_arrays(weights):

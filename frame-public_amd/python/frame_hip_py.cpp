@@ -30,17 +30,25 @@ namespace py = pybind11;
 
 namespace {
 
-// Status -> Python exception (the reference's translate_status.cpp maps codes to exception types the same way:
-// invalid argument -> ValueError, not found -> KeyError, unimplemented -> NotImplementedError, else RuntimeError).
-[[noreturn]] void raise(const frame::Status& st) {
-  const std::string msg(st.message());
-  switch (st.code()) {
-    case frame::ErrorCode::kInvalidArgument: throw py::value_error(msg);
-    case frame::ErrorCode::kNotFound: throw py::key_error(msg);
-    case frame::ErrorCode::kUnimplemented: throw py::type_error("unimplemented: " + msg);
-    default: throw std::runtime_error(msg);
+// Status -> Python exception, with the status message as the exception's text unchanged. The exception types are
+// the reference binding's (python/src/translate_status.cpp:29-47): invalid argument -> ValueError, not found ->
+// KeyError, unimplemented -> NotImplementedError, out of memory -> MemoryError, every other code -> RuntimeError.
+PyObject* exception_type(frame::ErrorCode code) {
+  switch (code) {
+    case frame::ErrorCode::kInvalidArgument: return PyExc_ValueError;
+    case frame::ErrorCode::kNotFound: return PyExc_KeyError;
+    case frame::ErrorCode::kUnimplemented: return PyExc_NotImplementedError;
+    case frame::ErrorCode::kOutOfMemory: return PyExc_MemoryError;
+    default: return PyExc_RuntimeError;
   }
 }
+// Thrown where a Status fails (possibly with the GIL released, inside compile and run) and turned into the Python
+// exception by the translator registered in the module, which runs with the GIL held.
+struct StatusError {
+  frame::ErrorCode code;
+  std::string message;
+};
+[[noreturn]] void raise(const frame::Status& st) { throw StatusError{st.code(), std::string(st.message())}; }
 template <typename T>
 T unwrap(frame::Result<T> r) {
   if (!r.is_ok()) raise(r.status());
@@ -122,6 +130,13 @@ struct BoundExecutable {
 
 PYBIND11_MODULE(frame_hip_py, m) {
   m.doc() = "Frame's compiled-graph path from Python: compile(graph_text, backend).run(inputs)";
+  py::register_exception_translator([](std::exception_ptr p) {
+    try {
+      if (p) std::rethrow_exception(p);
+    } catch (const StatusError& e) {
+      PyErr_SetString(exception_type(e.code), e.message.c_str());
+    }
+  });
   py::class_<frame::Tensor>(m, "Tensor")
       .def_static("from_numpy", &tensor_from_numpy, py::arg("backend"), py::arg("dtype"), py::arg("array"))
       .def("numpy", &tensor_to_numpy)
@@ -155,4 +170,12 @@ PYBIND11_MODULE(frame_hip_py, m) {
           return out;
         },
         py::arg("path"));
+  // Test hook: raises what a Status of `code` (a frame::ErrorCode ordinal) with `message` turns into; 0 returns.
+  m.def("_raise_status",
+        [](int code, const std::string& message) {
+          if (code < 0 || code > static_cast<int>(frame::ErrorCode::kDeviceError)) throw py::value_error("bad error code");
+          const frame::Status st = frame::Status::make(static_cast<frame::ErrorCode>(code), message);
+          if (!st.is_ok()) raise(st);
+        },
+        py::arg("code"), py::arg("message"));
 }

@@ -5,7 +5,9 @@
 
 #include <atomic>
 #include <bit>
+#include <functional>
 #include <string>
+#include <unordered_map>
 #include <unordered_set>
 
 #include <frame/ir/graph.h>
@@ -35,7 +37,13 @@ uint8_t ew_code(std::string_view op) {
 
 namespace {
 std::mutex g_streams_mu;
-std::unordered_set<uint64_t> g_live_streams;
+std::unordered_set<uint64_t> g_live_streams;  // ids of live HipStreams
+struct LiveStream {
+  uint64_t id;
+  void* handle;
+  int32_t device;
+};
+std::unordered_map<const hal::Stream*, LiveStream> g_live_stream_objects;  // live HipStream objects
 std::atomic<uint64_t> g_next_stream_id{1};
 }  // namespace
 
@@ -44,15 +52,30 @@ bool hip_stream_alive(uint64_t id) {
   return g_live_streams.count(id) != 0;
 }
 
+uint64_t hip_stream_id(const hal::Stream& stream) {
+  std::lock_guard<std::mutex> lock(g_streams_mu);
+  auto it = g_live_stream_objects.find(&stream);
+  return it != g_live_stream_objects.end() ? it->second.id : 0;
+}
+
+bool for_each_live_stream(int32_t device, const std::function<bool(void*)>& fn) {
+  std::lock_guard<std::mutex> lock(g_streams_mu);  // no stream of the list is destroyed meanwhile
+  for (const auto& [obj, ls] : g_live_stream_objects)
+    if (ls.device == device && !fn(ls.handle)) return false;
+  return true;
+}
+
 HipStream::HipStream(void* handle, int32_t device) : handle_(handle), device_(device), id_(g_next_stream_id++) {
   std::lock_guard<std::mutex> lock(g_streams_mu);
   g_live_streams.insert(id_);
+  g_live_stream_objects.emplace(this, LiveStream{id_, handle_, device_});
 }
 
 HipStream::~HipStream() {
   {
     std::lock_guard<std::mutex> lock(g_streams_mu);
     g_live_streams.erase(id_);
+    g_live_stream_objects.erase(this);
   }
   (void)fh_stream_destroy(handle_);
 }
@@ -103,11 +126,44 @@ size_t HipAllocator::size_class(size_t bytes) {
 }
 
 HipAllocator::~HipAllocator() {
-  // Process teardown: return cached blocks (hipFree waits for the device). Live blocks belong to Storage objects
-  // that may outlive us.
-  for (auto* lists : {&free_lists_, &pending_})
-    for (auto& [cls, list] : *lists)
-      for (void* p : list) (void)fh_free(p);
+  // Process teardown: return cached blocks (hipFree waits for the device) and the fence events. Live blocks belong
+  // to Storage objects that may outlive us.
+  for (auto& [cls, list] : free_lists_)
+    for (void* p : list) (void)fh_free(p);
+  for (auto& [cls, list] : pending_)
+    for (PendingBlock& b : list) {
+      (void)fh_free(b.ptr);
+      for (void* e : b.fence) (void)fh_event_destroy(e);
+    }
+  for (void* e : event_pool_) (void)fh_event_destroy(e);
+}
+
+// Events recorded now on every live stream of the device and on the null stream: once they have all completed,
+// every kernel or copy queued before this point (on any of those streams) has finished. False when a stream is
+// being captured into a graph (nothing is recorded then; the caller falls back to a device-wide wait) or when an
+// event cannot be had.
+bool HipAllocator::record_fence_locked(std::vector<void*>& fence) {
+  auto not_capturing = [](void* s) {
+    int32_t capturing = 1;
+    return fh_stream_capturing(s, &capturing) == FH_OK && capturing == 0;
+  };
+  auto record = [&](void* s) {
+    void* e = nullptr;
+    if (!event_pool_.empty()) {
+      e = event_pool_.back();
+      event_pool_.pop_back();
+    } else if (fh_event_create(&e, device_) != FH_OK) {
+      return false;
+    }
+    fence.push_back(e);
+    return fh_event_record(e, s) == FH_OK;
+  };
+  return for_each_live_stream(device_, not_capturing) && for_each_live_stream(device_, record) && record(nullptr);
+}
+
+void HipAllocator::recycle_fence_locked(std::vector<void*>& fence) {
+  event_pool_.insert(event_pool_.end(), fence.begin(), fence.end());
+  fence.clear();
 }
 
 Status HipAllocator::release_pending_locked() {
@@ -117,12 +173,45 @@ Status HipAllocator::release_pending_locked() {
   ++stats_.device_syncs;
   for (auto& [cls, list] : pending_) {
     auto& dst = free_lists_[cls];
-    dst.insert(dst.end(), list.begin(), list.end());
+    for (PendingBlock& b : list) {
+      dst.push_back(b.ptr);
+      recycle_fence_locked(b.fence);
+    }
     stats_.pending_bytes -= cls * list.size();
     stats_.cached_bytes += cls * list.size();
   }
   pending_.clear();
   return Status::ok();
+}
+
+// The oldest pending block of a size class, once the work queued before its free has finished: a wait on its
+// fence's events (usually complete already), which leaves work queued after the free running. Blocks freed while
+// a stream was being captured carry no fence and take the device-wide wait.
+Result<void*> HipAllocator::take_pending_locked(size_t cls) {
+  auto it = pending_.find(cls);
+  if (it == pending_.end() || it->second.empty()) return static_cast<void*>(nullptr);
+  PendingBlock& b = it->second.front();
+  if (!b.fenced) {
+    FRAME_RETURN_IF_ERROR(release_pending_locked());
+    auto& list = free_lists_[cls];
+    void* p = list.back();
+    list.pop_back();
+    stats_.cached_bytes -= cls;
+    return p;
+  }
+  for (void* e : b.fence) {
+    int32_t done = 0;
+    FRAME_HIP_RETURN_IF_ERROR(fh_event_query(e, &done), "HipAllocator: fence query");
+    if (!done) {
+      FRAME_HIP_RETURN_IF_ERROR(fh_event_synchronize(e), "HipAllocator: wait for work on a freed block");
+      ++stats_.fence_waits;
+    }
+  }
+  void* p = b.ptr;
+  recycle_fence_locked(b.fence);
+  it->second.pop_front();
+  stats_.pending_bytes -= cls;
+  return p;
 }
 
 HipAllocator::Stats HipAllocator::stats() {
@@ -150,11 +239,9 @@ Result<void*> HipAllocator::allocate(size_t bytes, size_t alignment) {
   };
   void* p = take();
   if (p == nullptr) {
-    auto pend = pending_.find(cls);
-    if (pend != pending_.end() && !pend->second.empty()) {
-      FRAME_RETURN_IF_ERROR(release_pending_locked());
-      p = take();
-    }
+    Result<void*> r = take_pending_locked(cls);
+    if (!r.is_ok()) return r.status();
+    p = r.value();
   }
   if (p == nullptr) {
     fh_status st = fh_malloc(&p, cls, device_);
@@ -180,7 +267,10 @@ void HipAllocator::deallocate(void* ptr) {
   std::lock_guard<std::mutex> lock(mu_);
   auto it = live_.find(ptr);
   if (it == live_.end()) return;  // not ours: ignore rather than corrupt the cache
-  pending_[it->second].push_back(ptr);
+  PendingBlock b{ptr, {}, false};
+  b.fenced = record_fence_locked(b.fence);
+  if (!b.fenced) recycle_fence_locked(b.fence);
+  pending_[it->second].push_back(std::move(b));
   stats_.live_bytes -= it->second;
   stats_.pending_bytes += it->second;
   live_.erase(it);

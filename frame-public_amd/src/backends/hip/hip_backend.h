@@ -5,6 +5,8 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <deque>
+#include <functional>
 #include <map>
 #include <memory>
 #include <mutex>
@@ -55,6 +57,12 @@ class HipStream final : public hal::Stream {
 
 // Whether the HipStream with this id still exists (ids of destroyed streams are never handed out again).
 bool hip_stream_alive(uint64_t id);
+// Calls fn(hipStream_t) for each live HipStream of `device` while holding the registry's lock (so none of them is
+// destroyed meanwhile), until fn returns false; returns whether every call returned true.
+bool for_each_live_stream(int32_t device, const std::function<bool(void*)>& fn);
+// The id of `stream` if it is a live HipStream, else 0 (a stream of another backend): a lookup among the live
+// HipStream objects, which needs no RTTI (the reference's sources are built without dynamic_cast / typeid).
+uint64_t hip_stream_id(const hal::Stream& stream);
 
 class HipEvent final : public hal::Event {
  public:
@@ -74,11 +82,13 @@ class HipEvent final : public hal::Event {
 
 // Device memory with a size-class cache, so repeated runs do not call hipMalloc. deallocate() carries no stream
 // (hal::Allocator), and kernels queued on any stream before the free may still read or write the block, so a
-// freed block first goes to a pending list. Pending blocks become reusable only after a device-wide
-// synchronisation, which allocate() performs once, when a request of that size class finds no reusable block but
-// pending ones exist; every pending block is released by that one wait. A block is therefore never handed out
-// while work queued before its free can still touch it (the reference gets this from cudaFree, which synchronises
-// on every free, src/backends/cuda/cuda_allocator.cpp:55-66).
+// freed block first goes to a pending list with a fence: an event recorded at the free on every live stream of the
+// device and on the null stream. A request of that size class that finds no reusable block takes the oldest
+// pending one after waiting for its fence's events (work queued after the free keeps running); a block freed
+// while a stream was being captured has no fence and is released by one device-wide synchronisation, as is the
+// whole pending list before a retry on out-of-memory. A block is therefore never handed out while work queued
+// before its free can still touch it (the reference gets this from cudaFree, which synchronises on every free,
+// src/backends/cuda/cuda_allocator.cpp:55-66).
 class HipAllocator final : public hal::Allocator {
  public:
   explicit HipAllocator(int32_t device) : device_(device) {}
@@ -90,18 +100,27 @@ class HipAllocator final : public hal::Allocator {
   // Bytes held by the cache (reusable + pending) and by live blocks; for tests of memory growth.
   struct Stats {
     size_t live_bytes = 0, cached_bytes = 0, pending_bytes = 0;
-    uint64_t device_allocations = 0, device_syncs = 0;
+    uint64_t device_allocations = 0, device_syncs = 0, fence_waits = 0;
   };
   Stats stats();
   static size_t size_class(size_t bytes);
 
  private:
-  Status release_pending_locked();  // device-wide wait, then pending -> reusable
+  struct PendingBlock {
+    void* ptr;
+    std::vector<void*> fence;  // events recorded at the free
+    bool fenced;               // false: freed during a capture, released by a device-wide wait only
+  };
+  bool record_fence_locked(std::vector<void*>& fence);
+  void recycle_fence_locked(std::vector<void*>& fence);
+  Status release_pending_locked();               // device-wide wait, then every pending block -> reusable
+  Result<void*> take_pending_locked(size_t cls);  // oldest pending block of the class once its fence passed
   int32_t device_;
   std::mutex mu_;
-  std::unordered_map<void*, size_t> live_;           // pointer -> size class
-  std::map<size_t, std::vector<void*>> free_lists_;  // size class -> reusable blocks
-  std::map<size_t, std::vector<void*>> pending_;     // size class -> freed, not yet known to be idle
+  std::unordered_map<void*, size_t> live_;                // pointer -> size class
+  std::map<size_t, std::vector<void*>> free_lists_;       // size class -> reusable blocks
+  std::map<size_t, std::deque<PendingBlock>> pending_;    // size class -> freed, oldest first
+  std::vector<void*> event_pool_;                         // fence events ready for reuse
   Stats stats_;
 };
 

@@ -26,6 +26,7 @@
 // channels-last data stay channels-last between convs (see plan_channels_last).
 // The rewrites run on a private copy of the graph before planning, so the memory plan sees the real lifetimes.
 #include <algorithm>
+#include <cstdint>
 #include <cstdlib>
 #include <cstring>
 #include <map>
@@ -951,8 +952,7 @@ class HipExecutable final : public hal::Executable {
     void* sh = stream.native_handle();
     // Per-stream state is keyed by the HipStream's process-unique id (a destroyed stream's handle address can come
     // back for a new stream). A stream of another backend gets no cached state: a transient arena for this run.
-    auto* hs = dynamic_cast<HipStream*>(&stream);
-    const uint64_t sid = hs != nullptr ? hs->id() : 0;
+    const uint64_t sid = hip_stream_id(stream);
     std::shared_ptr<Storage> arena;
     {
       std::lock_guard<std::mutex> lock(mu_);
@@ -975,7 +975,8 @@ class HipExecutable final : public hal::Executable {
     // of every step; other addresses run the steps directly. Off by default: on this ROCm a graph launch costs
     // ~10 us more than launching its kernels (measured: C1 forward 23.8 -> 29.8 us, a 1024^3 GEMM 7 -> 18.5 us),
     // and every workload here keeps the GPU busy without it.
-    if (sh == nullptr || sid == 0 || !graphs_enabled()) return run_steps(inputs, outputs, stream, arena);
+    if (sh == nullptr || sid == 0 || !graphs_enabled() || any_unaligned(inputs, outputs))
+      return run_steps(inputs, outputs, stream, arena);
     std::vector<const void*> key;
     for (const Tensor& t : inputs) key.push_back(t.raw_data());
     for (const Tensor& t : outputs) key.push_back(t.raw_data());
@@ -1053,14 +1054,40 @@ class HipExecutable final : public hal::Executable {
     return v != nullptr && v[0] == '1';
   }
 
+  // The kernels read and write 16-byte vectors where their operands allow it and some (the band conv with its
+  // filter kept in the graph's layout) require it. Arena slices and allocator blocks are aligned; a caller's
+  // tensor that is a view at an odd offset is not.
+  static bool unaligned(const Tensor& t) {
+    return t.numel() > 0 && (reinterpret_cast<uintptr_t>(t.raw_data()) & 15) != 0;
+  }
+  static bool any_unaligned(std::span<const Tensor> inputs, std::span<Tensor> outputs) {
+    for (const Tensor& t : inputs)
+      if (unaligned(t)) return true;
+    for (const Tensor& t : outputs)
+      if (unaligned(t)) return true;
+    return false;
+  }
+
   Status run_steps(std::span<const Tensor> inputs, std::span<Tensor> outputs, hal::Stream& stream,
                    const std::shared_ptr<Storage>& arena) {
     void* sh = stream.native_handle();
     std::vector<Tensor> slots(static_cast<size_t>(plan_.slot_count));
-    for (size_t i = 0; i < inputs.size(); ++i) slots[i] = inputs[i];
-    // A slot that is a graph output is produced directly in the first caller tensor naming it.
+    for (size_t i = 0; i < inputs.size(); ++i) {
+      slots[i] = inputs[i];
+      if (!unaligned(inputs[i])) continue;
+      // an input at an unaligned address is copied (stream-ordered) to an aligned block first
+      Result<Tensor> e = Tensor::empty(inputs[i].shape(), inputs[i].dtype(), device_, *alloc_);
+      if (!e.is_ok()) return e.status();
+      const size_t bytes = static_cast<size_t>(inputs[i].numel()) * inputs[i].dtype().itemsize();
+      FRAME_HIP_RETURN_IF_ERROR(fh_memcpy(e.value().raw_data(), inputs[i].raw_data(), bytes, FH_D2D, sh),
+                                "HipExecutable: unaligned input copy");
+      slots[i] = e.value();
+    }
+    // A slot that is a graph output is produced directly in the first caller tensor naming it, if that tensor is
+    // 16-byte aligned; otherwise in a block of its own, copied out at the end like a passed-through input.
     std::unordered_map<int32_t, size_t> direct;
-    for (size_t i = 0; i < plan_.output_slots.size(); ++i) direct.try_emplace(plan_.output_slots[i], i);
+    for (size_t i = 0; i < plan_.output_slots.size(); ++i)
+      if (!unaligned(outputs[i])) direct.try_emplace(plan_.output_slots[i], i);
 
     std::vector<Tensor> step_in, step_out;
     for (size_t si = 0; si < plan_.steps.size(); ++si) {
@@ -1366,6 +1393,9 @@ Status lower_grouped_gemms(ir::Graph& g) {
       f.value()->set_attr("groups", ir::AttrValue{static_cast<int64_t>(count)});
       f.value()->set_attr("ep_ops", ir::AttrValue{program(part.front().node)});
       f.value()->set_attr("any_order", ir::AttrValue{int64_t{1}});
+      // Every operand of the merged node is produced before its first member, so it can stand at that position:
+      // a later group reading one of its outputs compares against that position, not against a missing entry.
+      pos[f.value()] = first;
       for (size_t i = 0; i < count; ++i) {
         FRAME_RETURN_IF_ERROR(g.replace_all_uses(part[i].node->output(0), f.value()->output(static_cast<int32_t>(i))));
         FRAME_RETURN_IF_ERROR(g.erase_node(part[i].node));

@@ -135,6 +135,28 @@ int frame_tensor_empty(const char* backend, int32_t device, int32_t dtype, const
   return 0;
 }
 
+int frame_tensor_empty_at(const char* backend, int32_t device, int32_t dtype, const int64_t* dims, int32_t rank,
+                          int64_t byte_offset, frame_tensor** out) {
+  if (out == nullptr || rank < 0 || (rank > 0 && dims == nullptr) || byte_offset < 0)
+    return fail_msg("frame_tensor_empty_at: bad arguments");
+  if (dtype < 0 || dtype >= static_cast<int32_t>(frame::DTypeCode::kCount)) return fail_msg("frame_tensor_empty_at: bad dtype");
+  const frame::DType dt(static_cast<frame::DTypeCode>(dtype));
+  if (byte_offset % static_cast<int64_t>(dt.itemsize()) != 0)
+    return fail_msg("frame_tensor_empty_at: byte_offset is not a multiple of the element size");
+  auto b = backend_of(backend);
+  if (!b.is_ok()) return fail(b.status());
+  const frame::Device dev{b.value()->name(), device};
+  frame::hal::Allocator* a = b.value()->allocator(dev);
+  if (a == nullptr) return fail_msg("frame_tensor_empty_at: backend has no allocator for device " + std::to_string(device));
+  const frame::Shape shape(std::vector<int64_t>(dims, dims + rank));
+  const size_t bytes = static_cast<size_t>(shape.numel()) * dt.itemsize() + static_cast<size_t>(byte_offset);
+  auto st = frame::Storage::allocate(*a, bytes == 0 ? 1 : bytes, frame::kDefaultAlignment, dev);
+  if (!st.is_ok()) return fail(st.status());
+  *out = new frame_tensor{frame::Tensor::from_storage_slice(st.value(), static_cast<size_t>(byte_offset), shape, dt, dev),
+                          b.value()};
+  return 0;
+}
+
 void frame_tensor_free(frame_tensor* t) { delete t; }
 void* frame_tensor_data(frame_tensor* t) { return t == nullptr ? nullptr : t->t.raw_data(); }
 int64_t frame_tensor_nbytes(const frame_tensor* t) {
@@ -354,11 +376,18 @@ int frame_save_onnx_weights(const char* path, int32_t n, const char* const* name
   std::vector<frame::interop::NamedTensor> ws;
   for (int32_t i = 0; i < n; ++i) {
     if (ranks[i] < 0 || (ranks[i] > 0 && dims[i] == nullptr)) return fail_msg("frame_save_onnx_weights: bad shape");
+    if (names[i] == nullptr) return fail_msg("frame_save_onnx_weights: null name");
+    if (dtypes[i] != static_cast<int32_t>(frame::DTypeCode::kFloat32) &&
+        dtypes[i] != static_cast<int32_t>(frame::DTypeCode::kFloat16) &&
+        dtypes[i] != static_cast<int32_t>(frame::DTypeCode::kBFloat16))
+      return fail_msg("frame_save_onnx_weights: dtype code " + std::to_string(dtypes[i]) +
+                      " is not float32 (0), float16 (2) or bfloat16 (3)");
     std::vector<int64_t> d(dims[i], dims[i] + ranks[i]);
     auto t = frame::Tensor::empty(frame::Shape(d), frame::DType(static_cast<frame::DTypeCode>(dtypes[i])),
                                   frame::cpu_device(), host_allocator());
     if (!t.is_ok()) return fail(t.status());
     const size_t nbytes = static_cast<size_t>(t.value().numel()) * t.value().dtype().itemsize();
+    if (nbytes > 0 && data[i] == nullptr) return fail_msg("frame_save_onnx_weights: null data for a non-empty tensor");
     if (nbytes > 0) std::memcpy(t.value().raw_data(), data[i], nbytes);
     ws.push_back(frame::interop::NamedTensor{names[i], t.value()});
   }
@@ -406,7 +435,7 @@ int frame_backend_copy(const char* backend, void* dst, const char* dst_backend, 
   return st.is_ok() ? 0 : fail(st);
 }
 
-int frame_hip_allocator_stats(int32_t device, uint64_t out[5]) {
+int frame_hip_allocator_stats(int32_t device, uint64_t out[6]) {
   auto b = backend_of(frame::kHipBackendName.data());
   if (!b.is_ok()) return fail(b.status());
   auto* a = dynamic_cast<frame::backends::hip::HipAllocator*>(b.value()->allocator(frame::Device{frame::kHipBackendName, device}));
@@ -417,6 +446,7 @@ int frame_hip_allocator_stats(int32_t device, uint64_t out[5]) {
   out[2] = st.pending_bytes;
   out[3] = st.device_allocations;
   out[4] = st.device_syncs;
+  out[5] = st.fence_waits;
   return 0;
 }
 

@@ -35,6 +35,11 @@ int frame_device_count(const char* backend, int32_t* count);
 /* Tensors: dtype codes are frame::DTypeCode ordinals (0 float32, 2 float16, 3 bfloat16, ...). */
 int frame_tensor_empty(const char* backend, int32_t device, int32_t dtype, const int64_t* dims, int32_t rank,
                        frame_tensor** out);
+/* A tensor that starts `byte_offset` bytes into a fresh block (a multiple of the element size): the view
+ * Tensor::from_storage_slice makes (reference include/frame/core/tensor.h:30-45), e.g. to hand an executable
+ * operands that are not 16-byte aligned. */
+int frame_tensor_empty_at(const char* backend, int32_t device, int32_t dtype, const int64_t* dims, int32_t rank,
+                          int64_t byte_offset, frame_tensor** out);
 void frame_tensor_free(frame_tensor* t);
 void* frame_tensor_data(frame_tensor* t);
 int64_t frame_tensor_nbytes(const frame_tensor* t);
@@ -99,9 +104,10 @@ int frame_backend_copy(const char* backend, void* dst, const char* dst_backend, 
                        const char* src_backend, int32_t src_index, size_t bytes, frame_stream* stream);
 
 /* Counters of the hip backend's caching allocator for `device`: out[0] live bytes, out[1] reusable cached bytes,
- * out[2] freed bytes waiting for the device to go idle, out[3] device allocations made, out[4] device-wide waits.
- * No counterpart in the reference (its allocator caches nothing); for tests of memory growth. */
-int frame_hip_allocator_stats(int32_t device, uint64_t out[5]);
+ * out[2] freed bytes whose queued work may still run, out[3] device allocations made, out[4] device-wide waits,
+ * out[5] waits for one freed block's fence events. No counterpart in the reference (its allocator caches
+ * nothing); for tests of memory growth and reuse. */
+int frame_hip_allocator_stats(int32_t device, uint64_t out[6]);
 
 /* ONNX weight exchange (interop::save_onnx_weights / load_onnx_weights, reference
  * include/frame/interop/onnx_weights.h:38,47): the graph.initializer subset of an ONNX ModelProto, dtypes

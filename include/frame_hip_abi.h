@@ -90,6 +90,9 @@ fh_status fh_stream_create(void** stream, int32_t device);
 fh_status fh_stream_destroy(void* stream);
 fh_status fh_stream_synchronize(void* stream);
 fh_status fh_device_synchronize(void);
+/* *capturing = 1 while `stream` is being captured into a graph (hipStreamIsCapturing), else 0. For the allocator,
+ * which records no fence event on a capturing stream. No counterpart in the reference. */
+fh_status fh_stream_capturing(void* stream, int32_t* capturing);
 /* Replay of a captured step sequence (hipStreamBeginCapture / EndCapture / hipGraphInstantiate / hipGraphLaunch).
  * end_capture with keep = 0 discards the capture (after a failure inside it). No counterpart in the reference,
  * whose executables launch every step each run (src/backends/cuda/cuda_executable.cpp:55-95). */
@@ -204,8 +207,9 @@ int32_t fh_conv2d_nchw_in_supported(int32_t dtype, const int64_t geom[12]);
 /* 1 if fh_conv2d_nhwc_fwd_ex takes dtype, geom and the epilogue program (nseg and ops of `epilogue`; NULL for
  * none) with FH_CONV_IN_NCHW | FH_CONV_W_OIHW, given a 16-byte aligned output and epilogue operands: bf16, 3x3,
  * stride 1, padding 1, Cin 64, Cout <= 64, W % 8 == 0, no epilogue, relu or add;relu, and a geometry whose bands of
- * whole output rows spread over the CUs more evenly than 256-pixel tiles; else 0. Host-only query; no
- * counterpart in the reference. */
+ * whole output rows spread over the CUs more evenly than 256-pixel tiles; else 0. Host-only query (it launches
+ * nothing, but reads the current device's CU count once per process, 256 when no device is visible, so the answer
+ * depends on the device); no counterpart in the reference. */
 int32_t fh_conv2d_w_oihw_supported(int32_t dtype, const int64_t geom[12], const fh_epilogue* epilogue);
 
 /* C8 layout for convolutions with Cin <= 8 (e.g. an RGB stem): x NCHW [N][C][H*W] (16-bit) ->
@@ -335,7 +339,10 @@ fh_status fh_conv2d_wgrad_nhwc(int32_t dtype, const void* x, const void* dy, voi
  * 64 MiB file-scope device array that each device holds until the process ends. No counterpart in the
  * reference; it is for callers that cannot allocate (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). Geometries whose partials (fh_conv2d_wgrad_workspace) exceed 64 MiB fail with
- * FH_INVALID_ARGUMENT. Every call on a device shares that device's array: calls that overlap on one device race. */
+ * FH_INVALID_ARGUMENT. Every call on a device shares that device's array; calls on one device are ordered by it in
+ * the order the host makes them (each call's stream waits for an event the previous call recorded after its
+ * kernels, whatever stream that was), except under graph capture, where the graph's own order applies and
+ * overlapping replays on one device race. */
 fh_status fh_conv2d_wgrad_nhwc_noalloc(int32_t dtype, const void* x, const void* dy, void* dw, const int64_t geom[12],
                                        int32_t cin_pad, void* stream);
 

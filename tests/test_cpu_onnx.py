@@ -123,3 +123,28 @@ def test_error_cases_match_the_reference_contract(tmp_path):
     expect_error(lambda: host.save_onnx_weights(str(tmp_path / "i.onnx"), {"i": (I32, np.zeros(3, np.int32))}),
                  "invalid_argument", "i")
     expect_error(lambda: host.save_onnx_weights(str(tmp_path / "no_dir" / "x.onnx"), weights()), "invalid_argument")
+
+
+def test_save_rejects_null_name_null_data_and_bad_dtype(tmp_path):
+    """frame_save_onnx_weights checks each entry before reading it: a null name, null data for a non-empty tensor
+    and a dtype code other than float32 / float16 / bfloat16 are invalid arguments (code 1) that write no file."""
+    import ctypes
+    lib = host.lib()
+    path = str(tmp_path / "bad.onnx")
+    data = np.arange(4, dtype=np.float32)
+    dims = (ctypes.c_int64 * 1)(4)
+    dims_pp = (ctypes.c_void_p * 1)(ctypes.cast(dims, ctypes.c_void_p))
+    ranks = (ctypes.c_int32 * 1)(1)
+    good_name = (ctypes.c_char_p * 1)(b"w")
+    null_name = (ctypes.c_char_p * 1)(None)
+    good_data = (ctypes.c_void_p * 1)(data.ctypes.data)
+    null_data = (ctypes.c_void_p * 1)(None)
+    for names, dtype, ptrs, what in ((null_name, F32, good_data, "null name"), (good_name, F32, null_data, "null data"),
+                                     (good_name, I32, good_data, "int32"), (good_name, 17, good_data, "code 17")):
+        dt = (ctypes.c_int32 * 1)(dtype)
+        rc = lib.frame_save_onnx_weights(path.encode(), 1, names, dt, dims_pp, ranks, ptrs)
+        assert rc == 1, (what, rc)
+        assert not os.path.exists(path), what
+    dt = (ctypes.c_int32 * 1)(F32)
+    assert lib.frame_save_onnx_weights(path.encode(), 1, good_name, dt, dims_pp, ranks, good_data) == 0
+    assert os.path.exists(path)

@@ -39,3 +39,18 @@ def test_compile_without_a_device_raises():
     text = "%0 = graph_input() : float32[4]@hip:0\n%1 = relu(%0) : float32[4]@hip:0\ngraph_output(%1)\n"
     with pytest.raises(ValueError):
         fp.compile(text, "hip")
+
+
+@pytest.mark.parametrize("code,exc", [(1, ValueError), (2, KeyError), (3, RuntimeError), (4, NotImplementedError),
+                                      (5, MemoryError), (6, RuntimeError), (7, RuntimeError)])
+def test_status_codes_map_to_the_reference_exceptions(code, exc):
+    """Every frame::ErrorCode becomes the exception type of the reference binding (python/src/translate_status.cpp:
+    29-47: kInvalidArgument ValueError, kNotFound KeyError, kUnimplemented NotImplementedError, kOutOfMemory
+    MemoryError, the rest RuntimeError) with the status message verbatim."""
+    msg = f"status message {code}: op 'x' kernel failed"
+    with pytest.raises(exc) as info:
+        fp._raise_status(code, msg)
+    assert type(info.value) is exc
+    text = info.value.args[0] if info.value.args else ""
+    assert text == msg, (text, msg)
+    fp._raise_status(0, "ok")  # kOk raises nothing

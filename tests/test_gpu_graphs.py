@@ -238,13 +238,12 @@ def test_c5_transformer_full_rows(dev):
 # ---- graph replay (HipExecutable captures its steps on the second run with the same addresses) -----------------
 
 @pytest.mark.parametrize("which", ["c1", "c5_small", "cnn_train"])
-def test_graph_replay_matches_eager(dev, which):
+def test_graph_replay_matches_eager(dev, which, monkeypatch):
     """With FRAME_HIP_GRAPHS=1, run 1 is eager, run 2 captures a HIP graph and launches it, runs 3+ replay it. Between replays: new input
     values uploaded into the same tensors, another executable's eager work on the same stream, host syncs. Every
     replay must equal a fresh eager run of the same inputs bit for bit."""
     say(f"graph replay {which}")
-    import os
-    os.environ["FRAME_HIP_GRAPHS"] = "1"  # replay is opt-in
+    monkeypatch.setenv("FRAME_HIP_GRAPHS", "1")  # replay is opt-in; restored however the test ends
     if which == "c1":
         text = graphs.mlp(batch=64, dtype=F32, device="hip").text()
         make = lambda seed: graphs.mlp_inputs(batch=64, dtype=F32, seed=seed)
@@ -274,7 +273,30 @@ def test_graph_replay_matches_eager(dev, which):
         want = host.compile(text, "hip").run(values)  # a fresh executable: eager
         for i, (a, b) in enumerate(zip(got, want)):
             assert_bitwise(a, b, f"{which} run {run} output {i}")
-        if which != "cnn_train" and run in (2, 5):  # replays, checked against the oracle as well
-            for a, e in zip(got, orc.run_graph_cpu(text.replace("@hip:0", "@cpu:0"), values)):
-                assert_close(a, e, F32 if which == "c1" else BF16, what=f"{which} replay {run} vs oracle")
-    os.environ.pop("FRAME_HIP_GRAPHS", None)
+        if run in (2, 5):  # replays, checked against the oracle as well
+            for i, (a, e) in enumerate(zip(got, orc.run_graph_cpu(text.replace("@hip:0", "@cpu:0"), values))):
+                assert_close(np.asarray(a).reshape(-1), np.asarray(e).reshape(-1), F32 if which == "c1" else BF16,
+                             what=f"{which} replay {run} output {i} vs oracle")
+
+
+@pytest.mark.parametrize("offset", [2, 6])
+def test_unaligned_caller_tensors(dev, offset):
+    """Caller tensors that are views at an odd offset (Tensor::from_storage_slice): HipExecutable copies such inputs
+    to aligned blocks and produces such outputs in blocks of its own, so C3 (the band conv, whose graph-layout filter
+    path needs 16-byte aligned operands) and C1 give the same bits as with aligned tensors."""
+    for name, g, ins in (("c3", graphs.conv(BF16, device="hip", n=2, cin=64, h=16, w=16, cout=64, k=3),
+                          graphs.conv_inputs(BF16, n=2, cin=64, h=16, w=16, cout=64, k=3)),
+                         ("c1", graphs.mlp(batch=64, dtype=F32, device="hip"), graphs.mlp_inputs(batch=64, dtype=F32))):
+        say(f"unaligned caller tensors {name} offset {offset}")
+        exe = host.compile(g, "hip")
+        want = exe.run(ins)
+        dt = [sp[0] for sp in exe.input_specs()]
+        t_in = [host.Tensor.from_numpy("hip", d, a, byte_offset=offset) for d, a in zip(dt, ins)]
+        t_out = [host.Tensor("hip", d, shape, byte_offset=offset) for d, shape in exe.output_specs()]
+        assert all(t.data_ptr % 16 != 0 for t in t_in + t_out)
+        stream = host.Stream("hip")
+        for _ in range(2):
+            exe.run_tensors(t_in, t_out, stream)
+            stream.synchronize()
+            for i, (o, w) in enumerate(zip(t_out, want)):
+                assert_bitwise(o.numpy(), w, f"{name} unaligned output {i}")

@@ -702,7 +702,9 @@ def test_conv2d_nchw_input(hip, dtype, geom, nhwc_out):
 
 
 @pytest.mark.parametrize("geom", [(32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1), (64, 64, 8, 64, 40, 3, 3, 1, 1, 1, 1, 1),
-                                  (3, 64, 12, 40, 48, 3, 3, 1, 1, 1, 1, 1), (128, 64, 12, 48, 64, 3, 3, 1, 1, 1, 1, 1)])
+                                  (3, 64, 12, 40, 48, 3, 3, 1, 1, 1, 1, 1), (128, 64, 12, 48, 64, 3, 3, 1, 1, 1, 1, 1),
+              # W = 8 bands of R = 32 and R = 52 rows: more padding slots (2 (R + 2) 8) than threads
+              (256, 64, 32, 8, 64, 3, 3, 1, 1, 1, 1, 1), (256, 64, 52, 8, 64, 3, 3, 1, 1, 1, 1, 1)])
 def test_conv2d_band_residual(hip, geom):
     """The band kernel (NCHW input and output) with the residual add;relu program and no bias: both images at the
     ends of the batch and 4,096 sampled outputs against the oracle."""
@@ -730,7 +732,9 @@ def test_conv2d_band_residual(hip, geom):
 
 BAND_GEOMS = [(32, 64, 56, 56, 64, 3, 3, 1, 1, 1, 1, 1), (16, 64, 32, 56, 64, 3, 3, 1, 1, 1, 1, 1),
               (256, 64, 16, 16, 64, 3, 3, 1, 1, 1, 1, 1), (64, 64, 8, 64, 40, 3, 3, 1, 1, 1, 1, 1),
-              (3, 64, 12, 40, 48, 3, 3, 1, 1, 1, 1, 1), (128, 64, 12, 48, 64, 3, 3, 1, 1, 1, 1, 1)]
+              (3, 64, 12, 40, 48, 3, 3, 1, 1, 1, 1, 1), (128, 64, 12, 48, 64, 3, 3, 1, 1, 1, 1, 1),
+              # W = 8 bands of R = 32 and R = 52 rows: more padding slots (2 (R + 2) 8) than threads
+              (256, 64, 32, 8, 64, 3, 3, 1, 1, 1, 1, 1), (256, 64, 52, 8, 64, 3, 3, 1, 1, 1, 1, 1)]
 
 
 @pytest.mark.parametrize("geom", BAND_GEOMS)

@@ -181,12 +181,14 @@ def test_run_with_allocated_outputs_keeps_device_memory_flat(dev):
 
 def test_freed_block_is_not_reused_while_queued_work_writes_it(dev):
     """An output freed while the kernels writing it are still queued: the next allocation of that size must not
-    receive the block until the device is idle, so a synchronous upload into the new tensor survives."""
+    receive the block before those kernels finish, so a synchronous upload into the new tensor survives. The wait
+    is on the block's own fence events, not a device-wide synchronisation."""
     g = graphs.gemm(4096, BF16)
     exe = host.compile(g, "hip")
     ins = exe.upload_inputs(graphs.gemm_inputs(4096, BF16))
     stream = host.Stream("hip")
     pattern = synth.to_storage(np.full((4096, 4096), 0.5, np.float32), BF16)
+    syncs0 = host.allocator_stats()["device_syncs"]
     for trial in range(3):
         (t1,) = exe.alloc_outputs()
         addr = t1.data_ptr
@@ -198,6 +200,9 @@ def test_freed_block_is_not_reused_while_queued_work_writes_it(dev):
         assert_bitwise(t2.numpy(), pattern, f"trial {trial}: block reused under queued writes (t1 {addr:#x}, "
                                             f"t2 {t2.data_ptr:#x})")
         del t2
+    st = host.allocator_stats()
+    say(f"allocator after the trials: {st}")
+    assert st["device_syncs"] == syncs0, st
 
 
 def test_per_stream_arenas_are_bounded(dev):

@@ -61,3 +61,31 @@ def test_noalloc_wgrad_rejects_partials_above_the_scratch():
     rc = lib.fh_conv2d_wgrad_nhwc_noalloc(BF16, tiny.ptr, tiny.ptr, tiny.ptr, abi.i64_array(geom), 2048, None)
     assert rc == 1, rc  # FH_INVALID_ARGUMENT, before anything is launched
     assert b"no-allocation scratch" in lib.fh_last_error()
+
+
+def test_noalloc_wgrad_calls_on_two_streams_are_ordered():
+    """Two calls on two streams with no synchronisation between them share the device's scratch array: the second
+    call's stream waits for the first call's kernels, so both gradients equal the workspace entry point's."""
+    geom = (16, 64, 28, 28, 128, 3, 3, 1, 1, 1, 1, 1)
+    n, cin, h, w, cout, kh, kw = geom[:7]
+    lib = abi.lib()
+    g = abi.i64_array(geom)
+    need = lib.fh_conv2d_wgrad_workspace(BF16, g, cin, None)
+    ws = abi.DeviceBuffer(need)
+    cases = []
+    for seed in (81, 83):
+        x = abi.to_device(nhwc(synth.tensor(seed, (n, cin, h, w), BF16, "normal")))
+        dy = abi.to_device(nhwc(synth.tensor(seed + 1, (n, cout, h, w), BF16, "normal")))
+        cases.append((x, dy, abi.DeviceBuffer(cout * cin * kh * kw * 2), abi.DeviceBuffer(cout * cin * kh * kw * 2)))
+    s_ref, s1, s2 = abi.Stream(), abi.Stream(), abi.Stream()
+    for x, dy, ref, _ in cases:
+        abi.check(lib.fh_conv2d_wgrad_nhwc(BF16, x.ptr, dy.ptr, ref.ptr, ws.ptr, need, g, cin, s_ref.ptr), "wgrad")
+        s_ref.synchronize()
+    say("two no-alloc calls on two streams, back to back")
+    for (x, dy, _, out), s in zip(cases, (s1, s2)):
+        abi.check(lib.fh_conv2d_wgrad_nhwc_noalloc(BF16, x.ptr, dy.ptr, out.ptr, g, cin, s.ptr), "wgrad noalloc")
+    s1.synchronize()
+    s2.synchronize()
+    shape = (cout, cin, kh, kw)
+    for i, (_, _, ref, out) in enumerate(cases):
+        assert_bitwise(out.download(shape, np.uint16), ref.download(shape, np.uint16), f"stream {i + 1}")
