@@ -483,9 +483,11 @@ extern "C" fh_status fh_ew_program(int32_t dtype, int32_t nseg, const uint8_t* o
   if (!is_supported_float(dtype)) return fail(FH_UNIMPLEMENTED, "fh_ew_program: unsupported dtype");
   if (nseg < 1 || nseg > FH_MAX_SEGMENTS)
     return fail(FH_INVALID_ARGUMENT, "fh_ew_program: segment count out of range: " + std::to_string(nseg));
-  if (ops == nullptr || arities == nullptr || ins == nullptr || out == nullptr)
+  if (ops == nullptr || arities == nullptr || ins == nullptr)
     return fail(FH_INVALID_ARGUMENT, "fh_ew_program: null argument");
   if (numel < 0) return fail(FH_INVALID_ARGUMENT, "fh_ew_program: negative numel");
+  // empty tensors have no storage (null data): the program is still checked, nothing is launched
+  if (out == nullptr && numel > 0) return fail(FH_INVALID_ARGUMENT, "fh_ew_program: null output");
   EwArgs a{};
   a.nseg = nseg;
   a.round_between = round_between;
@@ -506,7 +508,7 @@ extern "C" fh_status fh_ew_program(int32_t dtype, int32_t nseg, const uint8_t* o
     return fail(FH_INVALID_ARGUMENT, "fh_ew_program: arities imply " + std::to_string(expected) +
                                          " inputs, got " + std::to_string(nin));
   for (int k = 0; k < nin; ++k) {
-    if (ins[k] == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_ew_program: null input");
+    if (ins[k] == nullptr && numel > 0) return fail(FH_INVALID_ARGUMENT, "fh_ew_program: null input");
     a.ins[k] = ins[k];
   }
   a.out = out;

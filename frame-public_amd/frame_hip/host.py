@@ -36,6 +36,9 @@ _SIGS = {
     "frame_backends": (c_int32, [c_void_p, c_int64, POINTER(c_int64)]),
     "frame_device_count": (c_int32, [c_char_p, POINTER(c_int32)]),
     "frame_tensor_empty": (c_int32, [c_char_p, c_int32, c_int32, POINTER(c_int64), c_int32, POINTER(c_void_p)]),
+    "frame_hip_run_tapped": (c_int32, [c_void_p, POINTER(c_void_p), c_int32, POINTER(c_void_p), c_int32, c_void_p, c_int32,
+                                       POINTER(c_int32), POINTER(c_int32), POINTER(c_void_p), POINTER(c_int64)]),
+    "frame_hip_executable_steps": (c_int32, [c_void_p, c_char_p, c_int64, POINTER(c_int64)]),
     "frame_tensor_empty_at": (c_int32, [c_char_p, c_int32, c_int32, POINTER(c_int64), c_int32, c_int64,
                                         POINTER(c_void_p)]),
     "frame_tensor_free": (None, [c_void_p]),
@@ -263,6 +266,21 @@ class Executable:
     def run_tensors(self, inputs, outputs, stream: Stream) -> None:
         check(lib().frame_executable_run(self.handle, _ptrs(inputs), len(inputs), _ptrs(outputs), len(outputs),
                                          stream.handle), "Executable.run")
+
+    def steps(self) -> list[str]:
+        """The hip executable's plan steps: the op of each non-input node of the lowered graph, in order."""
+        return [line.split(" ", 1)[1] for line in _text(lib().frame_hip_executable_steps, self.handle).splitlines()]
+
+    def run_tapped(self, inputs, outputs, stream: Stream, taps) -> None:
+        """frame_hip_run_tapped: taps = [(step, output index, numpy array sized like that output)]; each array is
+        filled with the step's output as it was produced."""
+        n = len(taps)
+        steps = (c_int32 * max(1, n))(*[t[0] for t in taps])
+        outs = (c_int32 * max(1, n))(*[t[1] for t in taps])
+        hosts = (c_void_p * max(1, n))(*[t[2].ctypes.data for t in taps])
+        sizes = (c_int64 * max(1, n))(*[t[2].nbytes for t in taps])
+        check(lib().frame_hip_run_tapped(self.handle, _ptrs(inputs), len(inputs), _ptrs(outputs), len(outputs),
+                                         stream.handle, n, steps, outs, hosts, sizes), "frame_hip_run_tapped")
 
     def run(self, inputs):
         """Inputs as numpy arrays (storage form) or Tensors; returns numpy outputs."""

@@ -10,6 +10,7 @@
 #include <map>
 #include <memory>
 #include <mutex>
+#include <span>
 #include <string>
 #include <unordered_map>
 #include <vector>
@@ -123,6 +124,19 @@ class HipAllocator final : public hal::Allocator {
   std::vector<void*> event_pool_;                         // fence events ready for reuse
   Stats stats_;
 };
+
+// Test hooks behind the C API's frame_hip_run_tapped / frame_hip_executable_steps (no counterpart in the
+// reference). `exe` must be an executable HipBackend::compile returned. Step i is the i-th non-input node of the
+// lowered graph (frame_hip_lowered_text prints it).
+struct HipStepTap {
+  size_t step;    // plan step index
+  size_t output;  // output index of that step
+  void* host;     // destination, `bytes` long
+  size_t bytes;   // must equal the output's size
+};
+Status hip_run_tapped(hal::Executable& exe, std::span<const Tensor> inputs, std::span<Tensor> outputs, hal::Stream& stream,
+                      std::span<const HipStepTap> taps);
+std::string hip_executable_steps(const hal::Executable& exe);
 
 class HipBackend final : public hal::Backend {
  public:

@@ -1013,6 +1013,32 @@ class HipExecutable final : public hal::Executable {
     return Status::ok();
   }
 
+  // Test hook: a run on a transient arena, eager, with the given step outputs copied to host memory as they are
+  // produced.
+  Status run_tapped(std::span<const Tensor> inputs, std::span<Tensor> outputs, hal::Stream& stream,
+                    std::span<const HipStepTap> taps) {
+    FRAME_RETURN_IF_ERROR(hal::validate_io_signature(inputs, in_sig_, "HipExecutable::run: input"));
+    FRAME_RETURN_IF_ERROR(hal::validate_io_signature(outputs, out_sig_, "HipExecutable::run: output"));
+    FRAME_RETURN_IF_ERROR(hal::validate_tensor_devices(inputs, device_, "HipExecutable::run: input"));
+    FRAME_RETURN_IF_ERROR(hal::validate_tensor_devices(outputs, device_, "HipExecutable::run: output"));
+    std::shared_ptr<Storage> arena;
+    if (plan_.arena_total_bytes > 0) {
+      Result<std::shared_ptr<Storage>> st = Storage::allocate(*alloc_, plan_.arena_total_bytes, kDefaultAlignment, device_);
+      if (!st.is_ok()) return st.status();
+      arena = st.value();
+    }
+    FRAME_RETURN_IF_ERROR(run_steps(inputs, outputs, stream, arena, taps));
+    FRAME_HIP_RETURN_IF_ERROR(fh_stream_synchronize(stream.native_handle()), "step tap: final drain");
+    return Status::ok();
+  }
+
+  // One line per plan step: "index op" (the lowered graph's non-input nodes in order).
+  std::string step_list() const {
+    std::string out;
+    for (size_t i = 0; i < plan_.steps.size(); ++i) out += std::to_string(i) + " " + plan_.steps[i].op + "\n";
+    return out;
+  }
+
   ~HipExecutable() override {
     for (auto& [s, gc] : graphs_)
       if (gc.exec != nullptr) (void)fh_graph_destroy(gc.exec);
@@ -1069,8 +1095,24 @@ class HipExecutable final : public hal::Executable {
   }
 
   Status run_steps(std::span<const Tensor> inputs, std::span<Tensor> outputs, hal::Stream& stream,
-                   const std::shared_ptr<Storage>& arena) {
+                   const std::shared_ptr<Storage>& arena, std::span<const HipStepTap> taps = {}) {
     void* sh = stream.native_handle();
+    // After step si: the tapped outputs go to host memory (the stream is drained first, since the arena
+    // slice may be reused by a later step).
+    auto tap = [&](size_t si, std::span<const Tensor> produced) -> Status {
+      for (const HipStepTap& t : taps) {
+        if (t.step != si) continue;
+        if (t.output >= produced.size()) return Status::make(ErrorCode::kInvalidArgument, "step tap: output index out of range");
+        const Tensor& o = produced[t.output];
+        const size_t bytes = static_cast<size_t>(o.numel()) * o.dtype().itemsize();
+        if (bytes != t.bytes)
+          return Status::make(ErrorCode::kInvalidArgument, "step tap: step " + std::to_string(si) + " output holds " +
+                                                               std::to_string(bytes) + " bytes, not " + std::to_string(t.bytes));
+        FRAME_HIP_RETURN_IF_ERROR(fh_stream_synchronize(sh), "step tap: drain");
+        if (bytes > 0) FRAME_HIP_RETURN_IF_ERROR(fh_memcpy(t.host, o.raw_data(), bytes, FH_D2H, nullptr), "step tap: copy");
+      }
+      return Status::ok();
+    };
     std::vector<Tensor> slots(static_cast<size_t>(plan_.slot_count));
     for (size_t i = 0; i < inputs.size(); ++i) {
       slots[i] = inputs[i];
@@ -1104,6 +1146,7 @@ class HipExecutable final : public hal::Executable {
                                     "HipExecutable: constant output copy");
           slots[static_cast<size_t>(slot)] = dst;
         }
+        if (!taps.empty()) FRAME_RETURN_IF_ERROR(tap(si, std::span<const Tensor>(&slots[static_cast<size_t>(slot)], 1)));
         continue;
       }
       step_in.clear();
@@ -1127,6 +1170,7 @@ class HipExecutable final : public hal::Executable {
       if (!st.is_ok())
         return Status::make(st.code(), "HipExecutable::run: op '" + s.op + "' kernel failed: " + std::string(st.message()));
       for (size_t j = 0; j < s.output_slots.size(); ++j) slots[static_cast<size_t>(s.output_slots[j])] = step_out[j];
+      if (!taps.empty()) FRAME_RETURN_IF_ERROR(tap(si, step_out));
     }
     // Outputs that were not written in place: graph inputs passed through, or a value listed twice.
     for (size_t i = 0; i < plan_.output_slots.size(); ++i) {
@@ -1417,6 +1461,13 @@ Result<ir::Graph> lower_for_hip(const ir::Graph& graph, int32_t opt_level) {
   // Channels-last conv lowering runs at every level, so the conv numerics do not depend on the level.
   return lower_convs(work.value());
 }
+
+Status hip_run_tapped(hal::Executable& exe, std::span<const Tensor> inputs, std::span<Tensor> outputs, hal::Stream& stream,
+                      std::span<const HipStepTap> taps) {
+  return static_cast<HipExecutable&>(exe).run_tapped(inputs, outputs, stream, taps);
+}
+
+std::string hip_executable_steps(const hal::Executable& exe) { return static_cast<const HipExecutable&>(exe).step_list(); }
 
 Result<std::unique_ptr<hal::Executable>> compile_hip_executable(const ir::Graph& graph, const hal::CompileOptions& options,
                                                                  HipAllocator& allocator, Device device) {

@@ -43,10 +43,16 @@ Status arity(const KernelContext& ctx, const std::string& op, size_t n_in, size_
   return Status::ok();
 }
 
+// Element-type comparisons and sizes for the argument checks below.
+bool same_elem_type(const Tensor& a, const Tensor& b) { return a.dtype() == b.dtype(); }
+bool same_elem_type(const Tensor& a, DType b) { return a.dtype() == b; }
+size_t elem_bytes(const Tensor& t) { return t.dtype().itemsize(); }
+
 Status same_dtype(const KernelContext& ctx, const std::string& op) {
   const DType d = ctx.outputs[0].dtype();
   for (const Tensor& t : ctx.inputs)
-    if (!(t.dtype() == d)) return invalid(op, "input dtype '" + std::string(t.dtype().name()) + "' differs from output dtype '" + std::string(d.name()) + "'");
+    if (!same_elem_type(t, d))
+      return invalid(op, "input dtype '" + std::string(t.dtype().name()) + "' differs from output dtype '" + std::string(d.name()) + "'");
   return Status::ok();
 }
 
@@ -123,7 +129,8 @@ Result<fh_epilogue> make_epilogue(const KernelContext& ctx, const std::string& o
     if (ep.ops[s] == FH_EW_ADD || ep.ops[s] == FH_EW_MUL) {
       if (next >= ctx.inputs.size()) return invalid(op, "epilogue operand missing");
       const Tensor& t = ctx.inputs[next++];
-      if (t.numel() != n || !(t.dtype() == ctx.outputs[0].dtype())) return invalid(op, "epilogue operand has the wrong shape or dtype");
+      if (t.numel() != n || !same_elem_type(t, ctx.outputs[0]))
+        return invalid(op, "epilogue operand has the wrong shape or dtype");
       ep.ins[s] = t.raw_data();
     }
   }
@@ -198,7 +205,8 @@ Status gemm_grouped_kernel(KernelContext& ctx) {
         eps[i].ops[s] = static_cast<uint8_t>((*prog)[s]);
         if (eps[i].ops[s] == FH_EW_ADD || eps[i].ops[s] == FH_EW_MUL) {
           const Tensor& t = ctx.inputs[next++];
-          if (t.numel() != m * n || !(t.dtype() == c.dtype())) return invalid(op, "epilogue operand has the wrong shape or dtype");
+          if (t.numel() != m * n || !same_elem_type(t, c))
+            return invalid(op, "epilogue operand has the wrong shape or dtype");
           eps[i].ins[s] = t.raw_data();
         }
       }
@@ -281,7 +289,8 @@ Status conv_impl(KernelContext& ctx, const std::string& op, size_t n_main) {
     return invalid(op, "missing or malformed stride/padding/groups attributes");
   if (x.shape().rank() != 4 || w.shape().rank() != 4 || y.shape().rank() != 4) return invalid(op, "operands must be rank-4");
   for (size_t i = 0; i < n_main; ++i)
-    if (!(ctx.inputs[i].dtype() == y.dtype())) return invalid(op, "operand dtypes differ");
+    if (!same_elem_type(ctx.inputs[i], y))
+      return invalid(op, "operand dtypes differ");
   Result<int32_t> dt = float_code(op, y.dtype());
   if (!dt.is_ok()) return dt.status();
   const int64_t geom[12] = {x.shape().dim(0), x.shape().dim(1), x.shape().dim(2), x.shape().dim(3),
@@ -324,7 +333,8 @@ Status conv_nhwc_kernel(KernelContext& ctx) {
   if (x.shape().rank() != 4 || (w.shape().rank() != 4 && w.shape().rank() != 2) || y.shape().rank() != 4)
     return invalid(op, "x and y must be rank-4, the filter rank-4 or rank-2 (C8)");
   for (size_t i = 0; i < n_main; ++i)
-    if (!(ctx.inputs[i].dtype() == y.dtype())) return invalid(op, "operand dtypes differ");
+    if (!same_elem_type(ctx.inputs[i], y))
+      return invalid(op, "operand dtypes differ");
   Result<int32_t> dt = float_code(op, y.dtype());
   if (!dt.is_ok()) return dt.status();
   // filter [Cout,KH,KW,Cin], or the C8 layout [Cout, K8] (Cin == 8) with KH, KW in the filter_hw attribute
@@ -373,7 +383,8 @@ Status channels_last_kernel(KernelContext& ctx) {
   FRAME_RETURN_IF_ERROR(arity(ctx, op, 1, 1));
   const Tensor& x = ctx.inputs[0];
   Tensor& y = ctx.outputs[0];
-  if (x.shape().rank() != 4 || !(x.dtype() == y.dtype())) return invalid(op, "expects a rank-4 input of the output's dtype");
+  if (x.shape().rank() != 4 || !same_elem_type(x, y))
+    return invalid(op, "expects a rank-4 input of the output's dtype");
   const Shape& s = x.shape();
   if (y.shape() != Shape({s.dim(0), s.dim(2), s.dim(3), s.dim(1)})) return invalid(op, "output shape does not match [d0,d2,d3,d1]");
   FRAME_HIP_RETURN_IF_ERROR(fh_transpose_batched(static_cast<int32_t>(x.dtype().itemsize()), x.raw_data(), y.raw_data(),
@@ -395,7 +406,7 @@ Status channels_last_multi_kernel(KernelContext& ctx) {
     const Tensor& x = ctx.inputs[i];
     Tensor& y = ctx.outputs[i];
     const Shape& s = x.shape();
-    if (s.rank() != 4 || !(x.dtype() == y.dtype()) || x.dtype().itemsize() != itemsize)
+    if (s.rank() != 4 || !same_elem_type(x, y) || elem_bytes(x) != itemsize)
       return invalid(op, "expects rank-4 inputs of one item size, outputs of the same dtype");
     if (y.shape() != Shape({s.dim(0), s.dim(2), s.dim(3), s.dim(1)})) return invalid(op, "output shape does not match [d0,d2,d3,d1]");
     if (s.dim(1) * s.dim(2) * s.dim(3) > kMultiPlaneMax) return invalid(op, "planes above 8192 elements");
@@ -419,7 +430,7 @@ Status pack_input_c8_kernel(KernelContext& ctx) {
   const Tensor& x = ctx.inputs[0];
   Tensor& y = ctx.outputs[0];
   const Shape& s = x.shape();
-  if (s.rank() != 4 || x.dtype().itemsize() != 2 || y.shape() != Shape({s.dim(0), s.dim(2), s.dim(3), 8}))
+  if (s.rank() != 4 || elem_bytes(x) != 2 || y.shape() != Shape({s.dim(0), s.dim(2), s.dim(3), 8}))
     return invalid(op, "expects a 16-bit [N,C,H,W] input and a [N,H,W,8] output");
   FRAME_HIP_RETURN_IF_ERROR(fh_conv_pack_input_c8(x.raw_data(), y.raw_data(), s.dim(0), static_cast<int32_t>(s.dim(1)),
                                                   s.dim(2) * s.dim(3), stream_handle(ctx)),
@@ -434,7 +445,7 @@ Status pack_filter_c8_kernel(KernelContext& ctx) {
   const Tensor& w = ctx.inputs[0];
   Tensor& y = ctx.outputs[0];
   const Shape& s = w.shape();
-  if (s.rank() != 4 || w.dtype().itemsize() != 2 || y.shape() != Shape({s.dim(0), fh_conv_c8_filter_k(s.dim(2), s.dim(3))}))
+  if (s.rank() != 4 || elem_bytes(w) != 2 || y.shape() != Shape({s.dim(0), fh_conv_c8_filter_k(s.dim(2), s.dim(3))}))
     return invalid(op, "expects a 16-bit [Cout,C,KH,KW] filter and a [Cout,K8] output");
   FRAME_HIP_RETURN_IF_ERROR(fh_conv_pack_filter_c8(w.raw_data(), y.raw_data(), static_cast<int32_t>(s.dim(0)),
                                                    static_cast<int32_t>(s.dim(1)), static_cast<int32_t>(s.dim(2)),
@@ -627,7 +638,7 @@ Status sum_rows_kernel(KernelContext& ctx) {
   const std::string op(kSumRowsOp);
   if (ctx.inputs.size() != 1 || ctx.outputs.size() != 2) return invalid(op, "expects 1 input and 2 outputs");
   const Shape& x = ctx.inputs[0].shape();
-  if (x.rank() < 1 || !(ctx.inputs[0].dtype() == ctx.outputs[0].dtype())) return invalid(op, "operand shapes");
+  if (x.rank() < 1 || !same_elem_type(ctx.inputs[0], ctx.outputs[0])) return invalid(op, "operand shapes");
   const int64_t cols = x.dim(x.rank() - 1);
   if (ctx.outputs[0].numel() != cols) return invalid(op, "output must hold one value per column");
   Result<int32_t> dt = float_code(op, ctx.outputs[0].dtype());
@@ -656,7 +667,7 @@ Status axpy_multi_kernel(KernelContext& ctx) {
     const Tensor& x = ctx.inputs[2 * i];
     const Tensor& y = ctx.inputs[2 * i + 1];
     Tensor& o = ctx.outputs[i];
-    if (!(x.dtype() == o.dtype()) || !(y.dtype() == o.dtype()) || !(o.dtype() == ctx.outputs[0].dtype()) ||
+    if (!same_elem_type(x, o) || !same_elem_type(y, o) || !same_elem_type(o, ctx.outputs[0]) ||
         x.shape() != o.shape() || y.shape() != o.shape())
       return invalid(op, "every pair must match its output's dtype and shape");
     xs[i] = x.raw_data(), ys[i] = y.raw_data(), outs[i] = o.raw_data();
@@ -701,7 +712,7 @@ Status conv_wgrad_kernel(KernelContext& ctx) {
   const Shape& x = ctx.inputs[0].shape();   // [N,H,W,cin_pad]
   const Shape& dy = ctx.inputs[1].shape();  // [N,Ho,Wo,Cout]
   if (x.rank() != 4 || dy.rank() != 4 || ctx.outputs[0].shape() != *ws) return invalid(op, "operand shapes");
-  if (!(ctx.inputs[0].dtype() == ctx.outputs[0].dtype()) || !(ctx.inputs[1].dtype() == ctx.outputs[0].dtype()))
+  if (!same_elem_type(ctx.inputs[0], ctx.outputs[0]) || !same_elem_type(ctx.inputs[1], ctx.outputs[0]))
     return invalid(op, "operand dtypes differ");
   const int64_t geom[12] = {x.dim(0), ws->dim(1), x.dim(1), x.dim(2), ws->dim(0), ws->dim(2), ws->dim(3), (*s)[0], (*s)[1], (*p)[0], (*p)[1], *grp};
   const int64_t oh = (geom[2] + 2 * geom[9] - geom[5]) / geom[7] + 1, ow = (geom[3] + 2 * geom[10] - geom[6]) / geom[8] + 1;
@@ -845,7 +856,8 @@ Status reshape_kernel(KernelContext& ctx) {
   FRAME_RETURN_IF_ERROR(arity(ctx, "reshape", 1, 1));
   const Tensor& x = ctx.inputs[0];
   Tensor& y = ctx.outputs[0];
-  if (x.numel() != y.numel() || !(x.dtype() == y.dtype())) return invalid("reshape", "element count or dtype differs");
+  if (x.numel() != y.numel() || !same_elem_type(x, y))
+    return invalid("reshape", "element count or dtype differs");
   FRAME_HIP_RETURN_IF_ERROR(fh_memcpy(y.raw_data(), x.raw_data(), static_cast<size_t>(x.numel()) * x.dtype().itemsize(),
                                       FH_D2D, stream_handle(ctx)),
                             "op 'reshape' (hip)");
@@ -895,7 +907,7 @@ Status slice_kernel(KernelContext& ctx) {
   split_at_axis(x.shape(), *axis, x.dtype().itemsize(), outer, inner);
   const int64_t src_pitch = x.shape().dim(*axis) * inner;
   const int64_t width = (*stop - *start) * inner;
-  if (ctx.outputs[0].numel() * static_cast<int64_t>(x.dtype().itemsize()) != outer * width) return invalid("slice", "output size mismatch");
+  if (ctx.outputs[0].numel() * static_cast<int64_t>(elem_bytes(x)) != outer * width) return invalid("slice", "output size mismatch");
   FRAME_HIP_RETURN_IF_ERROR(fh_copy2d(ctx.outputs[0].raw_data(), width, static_cast<const char*>(x.raw_data()) + *start * inner,
                                       src_pitch, width, outer, stream_handle(ctx)),
                             "op 'slice' (hip)");
@@ -912,7 +924,8 @@ Status concat_kernel(KernelContext& ctx) {
   const int64_t dst_pitch = y.shape().dim(*axis) * inner;
   int64_t offset = 0;
   for (const Tensor& x : ctx.inputs) {
-    if (!(x.dtype() == y.dtype()) || x.shape().rank() != y.shape().rank()) return invalid("concat", "operand dtype/rank differs");
+    if (!same_elem_type(x, y) || x.shape().rank() != y.shape().rank())
+      return invalid("concat", "operand dtype/rank differs");
     const int64_t width = x.shape().dim(*axis) * inner;
     if (offset + width > dst_pitch) return invalid("concat", "operands exceed the output along the axis");
     if (width > 0 && outer > 0)

@@ -273,6 +273,31 @@ int frame_run_with_allocated_outputs(frame_executable* e, frame_tensor* const* i
   return 0;
 }
 
+int frame_hip_run_tapped(frame_executable* e, frame_tensor* const* inputs, int32_t n_in, frame_tensor* const* outputs,
+                         int32_t n_out, frame_stream* stream, int32_t n_taps, const int32_t* steps,
+                         const int32_t* output_index, void* const* host, const int64_t* bytes) {
+  if (e == nullptr || stream == nullptr || n_taps < 0 ||
+      (n_taps > 0 && (steps == nullptr || output_index == nullptr || host == nullptr || bytes == nullptr)))
+    return fail_msg("frame_hip_run_tapped: null argument");
+  if (e->backend != frame::kHipBackendName) return fail_msg("frame_hip_run_tapped: not a hip executable");
+  std::vector<frame::backends::hip::HipStepTap> taps;
+  for (int32_t i = 0; i < n_taps; ++i) {
+    if (steps[i] < 0 || output_index[i] < 0 || bytes[i] < 0 || (bytes[i] > 0 && host[i] == nullptr))
+      return fail_msg("frame_hip_run_tapped: bad tap " + std::to_string(i));
+    taps.push_back({static_cast<size_t>(steps[i]), static_cast<size_t>(output_index[i]), host[i],
+                    static_cast<size_t>(bytes[i])});
+  }
+  std::vector<frame::Tensor> ins = unwrap(inputs, n_in), outs = unwrap(outputs, n_out);
+  frame::Status s = frame::backends::hip::hip_run_tapped(*e->exe, ins, outs, *stream->s, taps);
+  return s.is_ok() ? 0 : fail(s);
+}
+
+int frame_hip_executable_steps(const frame_executable* e, char* out, int64_t cap, int64_t* needed) {
+  if (e == nullptr) return fail_msg("frame_hip_executable_steps: null argument");
+  if (e->backend != frame::kHipBackendName) return fail_msg("frame_hip_executable_steps: not a hip executable");
+  return text_out(frame::backends::hip::hip_executable_steps(*e->exe), out, cap, needed);
+}
+
 int64_t frame_compile_cache_size(void) { return static_cast<int64_t>(frame::runtime::compilation_cache_size()); }
 
 int frame_transform_text(const char* ir_text, const char* pass_name, char* out, int64_t cap, int64_t* needed) {

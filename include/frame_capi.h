@@ -74,6 +74,17 @@ int frame_executable_run(frame_executable* e, frame_tensor* const* inputs, int32
 /* runtime::run_with_allocated_outputs: allocates outputs on device 0 of the backend, runs, synchronises. */
 int frame_run_with_allocated_outputs(frame_executable* e, frame_tensor* const* inputs, int32_t n_in,
                                      frame_tensor** outputs, int32_t n_out);
+/* Test hooks for per-op parity inside a whole compiled graph (no counterpart in the reference). A hip executable's
+ * plan step i is the i-th non-input node of the lowered graph (frame_hip_lowered_text of the same IR text and
+ * opt_level); frame_hip_executable_steps lists them as lines "i op". frame_hip_run_tapped runs the executable like
+ * frame_executable_run (on a transient arena, eager, synchronised at the end) and, after each step steps[t], copies
+ * its output output_index[t] into host[t], which holds bytes[t] bytes (the output's exact size, else
+ * kInvalidArgument). */
+int frame_hip_run_tapped(frame_executable* e, frame_tensor* const* inputs, int32_t n_in, frame_tensor* const* outputs,
+                         int32_t n_out, frame_stream* stream, int32_t n_taps, const int32_t* steps,
+                         const int32_t* output_index, void* const* host, const int64_t* bytes);
+int frame_hip_executable_steps(const frame_executable* e, char* out, int64_t cap, int64_t* needed);
+
 /* Number of entries in the compile cache. */
 int64_t frame_compile_cache_size(void);
 

@@ -1,0 +1,103 @@
+"""The hip plugin as a drop-in for the reference tree, host-only.
+
+* Lint: the plugin's sources, placed where INTEGRATION.md puts them (src/backends/hip/), pass the rules of the
+  reference's CI script that apply to a backend directory (scripts/check_iron_rules.sh:102-112 no dynamic_cast /
+  typeid, :178-188 no runtime dtype branch in kernels/, :190-201 no throw, :158-176 tagged to-do markers,
+  :203-221 no Backend::launch call outside src/runtime/, :242-256 no include of another backend or of a core
+  layer's internal headers). The patterns are restated here, comment lines excluded as the script excludes them.
+* Compile: the same sources compile with -fsyntax-only against the reference's own include/ (with the one edit a
+  maintainer makes, kHipBackendName beside the other backend names), where /root/reference exists.
+* Library: oracle/_ref/libframe_dropin.so (the reference's runtime linked with those plugin objects) registers
+  `hip` beside `cpu`, runs a graph through the reference's cpu backend, and refuses a hip compile without a device
+  with an error rather than a crash.
+"""
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+import dropin_lib as dl
+from frame_hip import graphs, synth
+
+REPO = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PLUGIN = os.path.join(REPO, "frame-public_amd", "src", "backends", "hip")
+SOURCES = ["hip_backend.h", "hip_backend.cpp", "hip_executable.cpp", os.path.join("kernels", "hip_kernels.cpp")]
+REFERENCE = "/root/reference"
+COMMENT = re.compile(r"^\s*(//|/\*|\*)")
+F32 = 0
+
+
+def code_lines(rel):
+    with open(os.path.join(PLUGIN, rel)) as f:
+        for i, line in enumerate(f, 1):
+            if not COMMENT.match(line):
+                yield i, line
+
+
+@pytest.mark.parametrize("rule,pattern,where", [
+    ("CPP-011 RTTI", r"\b(dynamic_cast|typeid)\b", None),
+    ("CPP-020 throw", r"\bthrow\b", None),
+    ("CPP-012 dtype branch in kernels/", r"switch *\(.*dtype|if *\(.*dtype", "kernels"),
+    ("ARCH-011 Backend::launch call", r"(->|\.)launch *\(", None),
+    ("ARCH-002 foreign include", r'^\s*#\s*include\s*[<"][^">]*(backends/(?!hip/)|src/(core|ir|compiler|runtime)/)',
+     None),
+])
+def test_plugin_sources_pass_the_reference_lint(rule, pattern, where):
+    rx = re.compile(pattern)
+    hits = [f"{rel}:{i}: {line.strip()}" for rel in SOURCES if where is None or rel.startswith(where)
+            for i, line in code_lines(rel) if rx.search(line)]
+    assert not hits, f"{rule}:\n" + "\n".join(hits)
+
+
+def test_plugin_to_do_markers_are_tagged():
+    marker = re.compile("(" + "TO" + "DO|FIX" + "ME|XX" + "X)")
+    tagged = re.compile("TO" + r"DO\(FRAME-(IMPL|DESIGN|TEST|DOC|PERF|DEP)\):")
+    hits = []
+    for rel in SOURCES:
+        with open(os.path.join(PLUGIN, rel)) as f:
+            hits += [f"{rel}:{i}" for i, line in enumerate(f, 1) if marker.search(line) and not tagged.search(line)]
+    assert not hits, hits
+
+
+@pytest.mark.skipif(not os.path.isdir(os.path.join(REFERENCE, "include")), reason="the reference tree is absent")
+def test_plugin_compiles_against_the_reference_headers():
+    header = os.path.join(REPO, "oracle", "_ref", "dropin", "include", "frame", "core", "device.h")
+    subprocess.run(["make", "-s", "-C", os.path.join(REPO, "oracle"), "_ref/dropin/include/frame/core/device.h"],
+                   check=True)
+    assert 'kHipBackendName = "hip"' in open(header).read()
+    for rel in SOURCES[1:]:
+        cmd = ["g++", "-std=c++20", "-fsyntax-only", "-Wall", "-Wextra", "-Wno-unused-parameter", "-Werror",
+               "-I" + os.path.dirname(os.path.dirname(os.path.dirname(header))), "-I" + REFERENCE + "/include",
+               "-I" + os.path.join(REPO, "include"), os.path.join(PLUGIN, rel)]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        assert r.returncode == 0, f"{rel} against the reference headers:\n{r.stderr[-4000:]}"
+
+
+@pytest.mark.skipif(not dl.available(), reason="oracle/_ref/libframe_dropin.so is not built (no reference tree)")
+def test_dropin_library_registers_hip_beside_cpu():
+    names = dl.backends()
+    assert "hip" in names and "cpu" in names, names
+    # the reference's own cpu backend through the same runtime: add of two vectors
+    g = graphs.Graph("cpu")
+    x, y = g.input(F32, (1000,)), g.input(F32, (1000,))
+    g.output(g.add(x, y))
+    a, b = synth.tensor(1, (1000,), F32), synth.tensor(2, (1000,), F32)
+    (got,) = dl.Executable(g.text(), "cpu").run([a, b])
+    assert got.tobytes() == (a + b).tobytes()
+
+
+@pytest.mark.skipif(not dl.available(), reason="oracle/_ref/libframe_dropin.so is not built (no reference tree)")
+def test_dropin_hip_compile_without_a_device_is_an_error():
+    try:
+        n = dl.device_count("hip")
+    except dl.DropinError:
+        n = 0
+    if n > 0:
+        pytest.skip("a hip device is present")
+    g = graphs.Graph("hip")
+    x = g.input(F32, (4,))
+    g.output(g.relu(x))
+    with pytest.raises(dl.DropinError):
+        dl.Executable(g.text(), "hip")
