@@ -80,6 +80,10 @@ _SIGS = {
     "fh_transpose_batched": (c_int32, [c_int32, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p]),
     "fh_conv_pack_input_c8": (c_int32, [c_void_p, c_void_p, c_int64, c_int32, c_int64, c_void_p]),
     "fh_conv_pack_filter_c8": (c_int32, [c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_void_p]),
+    "fh_conv2d_stem_pool_supported": (c_int32, [c_int32, POINTER(c_int64), POINTER(c_int64)]),
+    "fh_conv2d_stem_pool": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_void_p, POINTER(c_int64),
+                                      POINTER(c_int64), c_int32, c_void_p]),
+    "fh_stream_capturing": (c_int32, [c_void_p, POINTER(c_int32)]),
     "fh_conv_c8_filter_k": (c_int64, [c_int64, c_int64]),
     "fh_transpose_planes_multi": (c_int32, [c_int32, c_int32, POINTER(c_void_p), POINTER(c_void_p), POINTER(c_int64),
                                             POINTER(c_int64), POINTER(c_int64), c_void_p]),

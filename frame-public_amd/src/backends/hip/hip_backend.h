@@ -183,6 +183,9 @@ inline constexpr int64_t kMultiPlaneMax = 8192;
 // max_pool2d / avg_pool2d on channels-last [N,H,W,C] activations (same attributes; see fh_pool2d_nhwc).
 inline constexpr std::string_view kMaxPoolNhwcOp = "hip_max_pool2d_nhwc_internal";
 inline constexpr std::string_view kAvgPoolNhwcOp = "hip_avg_pool2d_nhwc_internal";
+// conv2d 7x7/2 (Cin <= 3, Cout 64) [-> relu] -> max_pool2d 3x3/2 as one launch, NCHW in and out (fh_conv2d_stem_pool):
+// inputs x, w[, bias]; attrs stride, padding, groups (the conv's), kernel, pool_stride, pool_padding, relu.
+inline constexpr std::string_view kConvStemPoolOp = "hip_conv2d_stem_pool_internal";
 // Cin <= 8: x [N,C,H,W] -> [N,H,W,8] zero-padded; w [Cout,C,KH,KW] -> [Cout, K8] (see fh_conv_pack_*_c8).
 inline constexpr std::string_view kPackInputC8Op = "hip_pack_input_c8_internal";
 inline constexpr std::string_view kPackFilterC8Op = "hip_pack_filter_c8_internal";

@@ -124,6 +124,85 @@ Status lower_epilogues(ir::Graph& g) {
   return Status::ok();
 }
 
+int32_t conv_dtype_code(const ir::TensorType& t);
+
+// A 7x7 stride-2 convolution (plain conv2d, or a conv epilogue node whose program is relu alone) whose result's only
+// use is a 3x3 stride-2 max_pool2d, directly or through a relu whose only use is the pool, becomes one
+// kConvStemPoolOp node that produces the pool's output (fh_conv2d_stem_pool takes the geometry): ResNet's stem
+// without its 4x larger convolution output ever reaching memory. Runs at every opt level, like the conv lowering.
+Status lower_stem_pools(ir::Graph& g) {
+  std::unordered_map<const ir::Value*, int> uses;
+  for (const ir::Node* n : g.topological_order())
+    for (const ir::Value* v : n->inputs()) ++uses[v];
+  for (const ir::Value* v : g.outputs()) uses[v] += 1000;  // graph outputs are never folded away
+  const std::vector<ir::Node*> snapshot = g.topological_order();
+  std::unordered_set<const ir::Node*> erased;
+  for (ir::Node* pool : snapshot) {
+    if (erased.count(pool) || pool->op() != "max_pool2d" || pool->inputs().size() != 1 || pool->outputs().size() != 1)
+      continue;
+    ir::Value* v = pool->inputs()[0];
+    ir::Node* p = v->producer();
+    if (p == nullptr || uses[v] != 1) continue;
+    ir::Node* relu_node = nullptr;
+    if (p->op() == "relu" && p->inputs().size() == 1) {
+      relu_node = p;
+      v = p->inputs()[0];
+      p = v->producer();
+      if (p == nullptr || uses[v] != 1) continue;
+    }
+    bool relu = relu_node != nullptr;
+    size_t n_main = p->inputs().size();
+    if (p->op() == kConvEpilogueOp) {
+      const auto* prog = attr_of<std::vector<int64_t>>(p, "ep_ops");
+      const auto* nm = attr_of<int64_t>(p, "n_main_inputs");
+      if (prog == nullptr || *prog != std::vector<int64_t>{FH_EW_RELU} || nm == nullptr) continue;
+      n_main = static_cast<size_t>(*nm);
+      relu = true;  // relu(relu(x)) == relu(x)
+    } else if (p->op() != "conv2d") {
+      continue;
+    }
+    if ((n_main != 2 && n_main != 3) || n_main != p->inputs().size()) continue;
+    const auto* stride = attr_of<std::vector<int64_t>>(p, "stride");
+    const auto* pad = attr_of<std::vector<int64_t>>(p, "padding");
+    const auto* groups = attr_of<int64_t>(p, "groups");
+    const auto* pk = attr_of<std::vector<int64_t>>(pool, "kernel");
+    const auto* ps = attr_of<std::vector<int64_t>>(pool, "stride");
+    const auto* pp = attr_of<std::vector<int64_t>>(pool, "padding");
+    if (stride == nullptr || pad == nullptr || groups == nullptr || pk == nullptr || ps == nullptr || pp == nullptr ||
+        stride->size() != 2 || pad->size() != 2 || pk->size() != 2 || ps->size() != 2 || pp->size() != 2)
+      continue;
+    const ir::TensorType& xt = p->inputs()[0]->type();
+    const ir::TensorType& wt = p->inputs()[1]->type();
+    const ir::TensorType& yt = pool->outputs()[0].type();
+    if (xt.shape.rank() != 4 || wt.shape.rank() != 4 || !(xt.dtype == yt.dtype) || !(wt.dtype == yt.dtype)) continue;
+    const int64_t geom[12] = {xt.shape.dim(0), xt.shape.dim(1), xt.shape.dim(2), xt.shape.dim(3), wt.shape.dim(0),
+                              wt.shape.dim(2),  wt.shape.dim(3),  (*stride)[0],    (*stride)[1],    (*pad)[0],
+                              (*pad)[1],        *groups};
+    const int64_t pgeom[6] = {(*pk)[0], (*pk)[1], (*ps)[0], (*ps)[1], (*pp)[0], (*pp)[1]};
+    if (wt.shape.dim(1) != geom[1] || fh_conv2d_stem_pool_supported(conv_dtype_code(yt), geom, pgeom) == 0) continue;
+    std::vector<ir::Value*> ins(p->inputs().begin(), p->inputs().end());
+    Result<ir::Node*> f = g.create_node(std::string(kConvStemPoolOp), ins, {yt});
+    if (!f.is_ok()) return f.status();
+    f.value()->set_attr("stride", ir::AttrValue{*stride});
+    f.value()->set_attr("padding", ir::AttrValue{*pad});
+    f.value()->set_attr("groups", ir::AttrValue{*groups});
+    f.value()->set_attr("kernel", ir::AttrValue{*pk});
+    f.value()->set_attr("pool_stride", ir::AttrValue{*ps});
+    f.value()->set_attr("pool_padding", ir::AttrValue{*pp});
+    f.value()->set_attr("relu", ir::AttrValue{static_cast<int64_t>(relu ? 1 : 0)});
+    FRAME_RETURN_IF_ERROR(g.replace_all_uses(pool->output(0), f.value()->output(0)));
+    FRAME_RETURN_IF_ERROR(g.erase_node(pool));
+    erased.insert(pool);
+    if (relu_node != nullptr) {
+      FRAME_RETURN_IF_ERROR(g.erase_node(relu_node));
+      erased.insert(relu_node);
+    }
+    FRAME_RETURN_IF_ERROR(g.erase_node(p));
+    erased.insert(p);
+  }
+  return Status::ok();
+}
+
 int32_t conv_dtype_code(const ir::TensorType& t) {
   return t.dtype.code() == DTypeCode::kBFloat16  ? FH_BF16
          : t.dtype.code() == DTypeCode::kFloat16 ? FH_F16
@@ -1458,6 +1537,7 @@ Result<ir::Graph> lower_for_hip(const ir::Graph& graph, int32_t opt_level) {
   if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_gemm_softmax(work.value()));
   if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_grouped_gemms(work.value()));
   if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_scaled_adds(work.value()));
+  FRAME_RETURN_IF_ERROR(lower_stem_pools(work.value()));
   // Channels-last conv lowering runs at every level, so the conv numerics do not depend on the level.
   return lower_convs(work.value());
 }

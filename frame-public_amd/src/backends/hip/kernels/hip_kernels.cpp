@@ -377,6 +377,43 @@ Status conv_nhwc_kernel(KernelContext& ctx) {
   return Status::ok();
 }
 
+// The stem chain conv2d 7x7/2 + bias [+ relu] + max_pool2d 3x3/2 as one launch (fh_conv2d_stem_pool).
+Status conv_stem_pool_kernel(KernelContext& ctx) {
+  const std::string op(kConvStemPoolOp);
+  if (ctx.inputs.size() < 2 || ctx.inputs.size() > 3 || ctx.outputs.size() != 1)
+    return invalid(op, "expects x, w[, bias] and one output");
+  const Tensor &x = ctx.inputs[0], &w = ctx.inputs[1];
+  Tensor& y = ctx.outputs[0];
+  const Tensor* bias = ctx.inputs.size() == 3 ? &ctx.inputs[2] : nullptr;
+  const auto* stride = attr<std::vector<int64_t>>(ctx, "stride");
+  const auto* pad = attr<std::vector<int64_t>>(ctx, "padding");
+  const auto* groups = attr<int64_t>(ctx, "groups");
+  const auto* pk = attr<std::vector<int64_t>>(ctx, "kernel");
+  const auto* ps = attr<std::vector<int64_t>>(ctx, "pool_stride");
+  const auto* pp = attr<std::vector<int64_t>>(ctx, "pool_padding");
+  const auto* relu = attr<int64_t>(ctx, "relu");
+  if (stride == nullptr || pad == nullptr || groups == nullptr || pk == nullptr || ps == nullptr || pp == nullptr ||
+      relu == nullptr || stride->size() != 2 || pad->size() != 2 || pk->size() != 2 || ps->size() != 2 || pp->size() != 2)
+    return invalid(op, "missing or malformed attributes");
+  if (x.shape().rank() != 4 || w.shape().rank() != 4 || y.shape().rank() != 4) return invalid(op, "x, w and y must be rank-4");
+  for (const Tensor& t : ctx.inputs)
+    if (!same_elem_type(t, y)) return invalid(op, "operand dtypes differ");
+  Result<int32_t> dt = float_code(op, y.dtype());
+  if (!dt.is_ok()) return dt.status();
+  const int64_t geom[12] = {x.shape().dim(0), x.shape().dim(1), x.shape().dim(2), x.shape().dim(3), w.shape().dim(0),
+                            w.shape().dim(2), w.shape().dim(3), (*stride)[0], (*stride)[1], (*pad)[0], (*pad)[1], *groups};
+  const int64_t pool[6] = {(*pk)[0], (*pk)[1], (*ps)[0], (*ps)[1], (*pp)[0], (*pp)[1]};
+  if (w.shape().dim(1) != geom[1]) return invalid(op, "filter channels differ from the input's");
+  if (bias != nullptr && (bias->shape().rank() != 1 || bias->shape().dim(0) != geom[4])) return invalid(op, "bias must be [Cout]");
+  const int64_t oh = (geom[2] + 2 * geom[9] - geom[5]) / geom[7] + 1, ow = (geom[3] + 2 * geom[10] - geom[6]) / geom[8] + 1;
+  const int64_t ph = (oh + 2 * pool[4] - pool[0]) / pool[2] + 1, pw = (ow + 2 * pool[5] - pool[1]) / pool[3] + 1;
+  if (y.shape() != Shape({geom[0], geom[4], ph, pw})) return invalid(op, "output shape does not match the geometry");
+  FRAME_HIP_RETURN_IF_ERROR(fh_conv2d_stem_pool(dt.value(), x.raw_data(), w.raw_data(), bias ? bias->raw_data() : nullptr,
+                                                y.raw_data(), geom, pool, *relu != 0 ? 1 : 0, stream_handle(ctx)),
+                            "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
 // [d0, d1, d2, d3] -> [d0, d2, d3, d1]
 Status channels_last_kernel(KernelContext& ctx) {
   const std::string op(kChannelsLastOp);
@@ -974,6 +1011,7 @@ FRAME_REGISTER_KERNEL(kConvEpilogueOp, kHipBackendName, &conv_epilogue_kernel);
 FRAME_REGISTER_KERNEL(kConvNhwcOp, kHipBackendName, &conv_nhwc_kernel);
 FRAME_REGISTER_KERNEL(kChannelsLastOp, kHipBackendName, &channels_last_kernel);
 FRAME_REGISTER_KERNEL(kChannelsLastMultiOp, kHipBackendName, &channels_last_multi_kernel);
+FRAME_REGISTER_KERNEL(kConvStemPoolOp, kHipBackendName, &conv_stem_pool_kernel);
 FRAME_REGISTER_KERNEL(kPackInputC8Op, kHipBackendName, &pack_input_c8_kernel);
 FRAME_REGISTER_KERNEL(kPackFilterC8Op, kHipBackendName, &pack_filter_c8_kernel);
 FRAME_REGISTER_KERNEL("softmax", kHipBackendName, &softmax_kernel);

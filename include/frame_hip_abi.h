@@ -212,6 +212,20 @@ int32_t fh_conv2d_nchw_in_supported(int32_t dtype, const int64_t geom[12]);
  * depends on the device); no counterpart in the reference. */
 int32_t fh_conv2d_w_oihw_supported(int32_t dtype, const int64_t geom[12], const fh_epilogue* epilogue);
 
+/* A network stem in one launch: y = max_pool2d(act(conv2d(x, w) + bias)), NCHW x [N][Cin][H][W], w [64][Cin][7][7],
+ * bias [64] or NULL, y [N][64][PH][PW]; the convolution 7x7, stride 2, padding 3 (geom as fh_conv2d_fwd; act relu
+ * when relu != 0, else identity on the rounded convolution), the pool 3x3, stride 2, padding 1 (pool = {kh, kw,
+ * sh, sw, ph, pw}). The convolution output is never stored. Each convolution value is rounded once (bias inside the
+ * fp32 sum, MFMA order: within tolerance of the reference's sequential sum); relu and the pool's selection are the
+ * reference's bit for bit on those values (reference: src/backends/cpu/kernels/conv.cpp:223-314,
+ * elementwise.cpp:329-331, pool.cpp:187-234, first valid element of the window in (kh, kw) order, then a strictly
+ * greater one). Replaces the reference's conv2d + relu + max_pool2d chain (cuDNN calls in
+ * src/backends/cuda/kernels/conv.cpp:385-520 and pool.cpp:172-244). fh_conv2d_stem_pool_supported: bf16 / f16,
+ * Cin <= 3, Cout 64, W % 8 == 0, W <= 224; host-only query. x and y 16-byte aligned. */
+int32_t fh_conv2d_stem_pool_supported(int32_t dtype, const int64_t geom[12], const int64_t pool[6]);
+fh_status fh_conv2d_stem_pool(int32_t dtype, const void* x, const void* w, const void* bias, void* y,
+                              const int64_t geom[12], const int64_t pool[6], int32_t relu, void* stream);
+
 /* C8 layout for convolutions with Cin <= 8 (e.g. an RGB stem): x NCHW [N][C][H*W] (16-bit) ->
  * [N][H*W][8] with channels C..7 zero. No counterpart in the reference (cuDNN consumes NCHW). */
 fh_status fh_conv_pack_input_c8(const void* x, void* y, int64_t n, int32_t c, int64_t hw, void* stream);

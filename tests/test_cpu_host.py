@@ -281,13 +281,34 @@ def test_resnet_lowering_layouts():
     out = host.hip_lowered(g.text(), 1)
     ops = re.findall(r"= (\w+)\(", out)
     assert ops.count("hip_channels_last_multi_internal") == 1
-    assert ops.count("hip_conv2d_nhwc_internal") == 20
+    assert ops.count("hip_conv2d_nhwc_internal") == 19  # the stem conv is fused with its relu and max pool
+    assert ops.count("hip_conv2d_stem_pool_internal") == 1 and "relu=1" in out
     assert out.count("w_oihw=1") == 4 and out.count("in_nchw=1") == 4
     assert ops.count("hip_channels_last_internal") == 1
-    assert ops.count("max_pool2d") == 1 and ops.count("hip_avg_pool2d_nhwc_internal") == 1
+    assert ops.count("max_pool2d") == 0 and ops.count("hip_avg_pool2d_nhwc_internal") == 1
     assert ops.count("reshape") == 0  # the global pool writes [N, C] itself
     assert ops.count("graph_input") == 43
     assert out.count("out_nhwc=1") == 15
+
+
+@pytest.mark.parametrize("opt_level", [0, 1])
+def test_stem_pool_lowering(opt_level):
+    # conv2d 7x7/2 -> relu -> max_pool2d 3x3/2 becomes one fused node at every opt level (bf16, Cin 3, Cout 64);
+    # fp32 keeps the three nodes, and so does a graph that also outputs the conv result
+    def stem(dtype, also_output=False):
+        g = graphs.Graph("hip")
+        x = g.input(dtype, (2, 3, 64, 64))
+        w, b = g.input(dtype, (64, 3, 7, 7)), g.input(dtype, (64,))
+        c = g.conv2d(x, w, b, (2, 2), (3, 3))
+        r = g.relu(c)
+        g.output(g.pool("max_pool2d", r, (3, 3), (2, 2), (1, 1)))
+        if also_output:
+            g.output(c)
+        return host.hip_lowered(g.text(), opt_level)
+    out = stem(3)
+    assert "hip_conv2d_stem_pool_internal" in out and "relu=1" in out and "max_pool2d(" not in out, out
+    assert "hip_conv2d_stem_pool_internal" not in stem(0)
+    assert "hip_conv2d_stem_pool_internal" not in stem(3, also_output=True)
 
 
 def test_training_lowering_keeps_band_layer_channels_last():

@@ -6,8 +6,8 @@ correct bf16 evaluations compound over 20 conv layers. This file holds every op 
 on images 0 and 63 of the batch (every op on the path computes each image independently), two ways:
 
 * test_c4_full_graph_every_step_at_1e2: the real 224 px, batch-64 executable, i.e. the kernels C4 itself runs
-  (channels-last convs with out_nhwc epilogues, the band and resident-patch NCHW convs, the C8 stem, the NHWC
-  whole-plane average pool, the classifier GEMM with its bias epilogue). Every step's output is tapped as it is
+  (the fused stem conv + relu + max pool, channels-last convs with out_nhwc epilogues, the band NCHW convs, the
+  NHWC whole-plane average pool, the classifier GEMM with its bias epilogue). Every step's output is tapped as it is
   produced (frame_hip_run_tapped); each compute step is recomputed by the oracle from the tapped hip values of its
   operands (channels-last values converted on the host) and compared; the layout steps (C8 packs, filter and
   activation transposes) must equal their host counterparts bit for bit, and max pooling is a selection, so it
@@ -238,6 +238,19 @@ def test_c4_full_graph_every_step_at_1e2():
                    f"{'w_oihw ' if attrs.get('w_oihw') else ''}{layout[out]} out, epilogue {prog}")
             st = assert_close(nchw(out)[CHECK], want, BF16, what=f"C4 step %{out}: {tag}")
             say(f"  %{out} {tag}: max |err| {st['max_abs']:.3g} (atol {st['atol']:.3g})")
+        elif op == "hip_conv2d_stem_pool_internal":
+            # the stem conv 7x7/2 + bias, relu and the 3x3/2 max pool in one kernel; the conv output is never stored
+            x, w, b = values[args[0]][CHECK], values[args[1]], values[args[2]]
+            (sh, sw), (ph, pw) = attrs["stride"], attrs["padding"]
+            geom = (len(CHECK), x.shape[1], x.shape[2], x.shape[3], w.shape[0], 7, 7, sh, sw, ph, pw, 1)
+            conv = orc.conv2d(BF16, np.ascontiguousarray(x), w, b, geom)
+            if attrs["relu"]:
+                conv = orc.ew_program(BF16, [EW_RELU], [1], [conv])
+            (kh, kw), (psh, psw), (pph, ppw) = attrs["kernel"], attrs["pool_stride"], attrs["pool_padding"]
+            want = orc.pool2d(BF16, 0, conv, conv.shape + (kh, kw, psh, psw, pph, ppw))
+            layout[out] = "nchw"
+            st = assert_close(values[out][CHECK], want, BF16, what=f"C4 step %{out}: stem conv + relu + max pool")
+            say(f"  %{out} stem conv 7x7/2 + relu + max pool 3x3/2: max |err| {st['max_abs']:.3g}")
         elif op in ("max_pool2d", "hip_max_pool2d_nhwc_internal"):
             x = nchw(args[0])[CHECK]
             (kh, kw), (sh, sw), (ph, pw) = attrs["kernel"], attrs["stride"], attrs["padding"]
@@ -263,6 +276,7 @@ def test_c4_full_graph_every_step_at_1e2():
         else:
             raise AssertionError(f"step {op} has no check")
     say(f"C4 full graph steps checked: {counts}")
-    assert counts.get("hip_conv2d_nhwc_internal", 0) == 20, counts
+    stem = counts.get("hip_conv2d_stem_pool_internal", 0)
+    assert counts.get("hip_conv2d_nhwc_internal", 0) + stem == 20, counts
     assert counts.get("hip_avg_pool2d_nhwc_internal", 0) == 1 and counts.get("hip_matmul_epilogue_internal", 0) == 1
-    assert counts.get("max_pool2d", 0) + counts.get("hip_max_pool2d_nhwc_internal", 0) == 1
+    assert counts.get("max_pool2d", 0) + counts.get("hip_max_pool2d_nhwc_internal", 0) + stem == 1

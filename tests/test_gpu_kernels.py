@@ -961,6 +961,92 @@ def test_conv2d_c8(hip, dtype, geom, with_bias):
     assert_close(got, want, dtype, what=f"conv c8 {geom}")
 
 
+# ---- fused stem: conv 7x7/2 + bias + relu + max pool 3x3/2 -------------------------------------------------
+
+STEM_CASES = [
+    (2, 3, 224, 224),  # C4's stem, two images: pool 56 x 56, 8 strips, 16-byte row stores
+    (3, 3, 32, 48),    # pool 8 x 12: the second strip ragged, element stores
+    (2, 1, 40, 64),    # one channel
+    (1, 2, 35, 16),    # odd height: the last pool window has two rows; two channels; one strip
+    (2, 3, 30, 112),   # pool 8 x 28
+]
+
+
+def stem_oracle(dtype, x, w, bias, relu):
+    n, cin, h, wd = x.shape
+    geom = (n, cin, h, wd, 64, 7, 7, 2, 2, 3, 3, 1)
+    y = orc.conv2d(dtype, x, w, bias, geom)
+    if relu:
+        y = orc.ew_program(dtype, [3], [1], [y])
+    oh, ow = y.shape[2], y.shape[3]
+    return orc.pool2d(dtype, 0, y, (n, 64, oh, ow, 3, 3, 2, 2, 1, 1))
+
+
+@pytest.mark.parametrize("dtype", [BF16, F16])
+@pytest.mark.parametrize("shape", STEM_CASES)
+def test_conv2d_stem_pool(hip, dtype, shape):
+    """fh_conv2d_stem_pool against the oracle's conv2d -> relu -> max_pool2d. The conv values differ from the
+    oracle's sequential sums within the tolerance, so the pooled values are held to the same rule; the selection
+    itself is exact (the test below checks it where the conv values are exact)."""
+    n, cin, h, wd = shape
+    say(f"stem conv+pool dtype={dtype} {shape}")
+    geom, pool = hip.i64_array((n, cin, h, wd, 64, 7, 7, 2, 2, 3, 3, 1)), hip.i64_array((3, 3, 2, 2, 1, 1))
+    assert hip.lib().fh_conv2d_stem_pool_supported(dtype, geom, pool) == 1
+    x = synth.tensor(141, (n, cin, h, wd), dtype, "normal")
+    w = synth.tensor(142, (64, cin, 7, 7), dtype, "normal", (2.0 / (cin * 49)) ** 0.5)
+    bias = synth.tensor(143, (64,), dtype, "normal", 0.1)
+    dx, dw, db = dev(hip, x), dev(hip, w), dev(hip, bias)  # held: the buffers must outlive the launch
+    for relu in (1, 0):
+        want = stem_oracle(dtype, x, w, bias, relu)
+        dy = hip.DeviceBuffer(want.nbytes)
+        hip.check(hip.lib().fh_conv2d_stem_pool(dtype, dx.value, dw.value, db.value, dy.value, geom, pool, relu, None))
+        got = dy.download(want.shape, want.dtype)
+        assert_close(got, want, dtype, what=f"stem {shape} relu={relu}")
+
+
+def test_conv2d_stem_pool_selection_is_exact(hip):
+    """Integer-valued operands (small integers in x, the filter and the bias: every product and partial sum is an
+    integer below 2^24, exact in fp32) make the fp32 sums identical in any summation order, so both sides round the
+    same value and the fused result must equal the oracle's conv -> relu -> max_pool2d bit for bit, including the NaN
+    rule of the reference's scan (a NaN in the input makes NaN conv values; a window whose first valid element is
+    NaN gives NaN, later NaNs are skipped)."""
+    rng = np.random.default_rng(7)
+    n, cin, h, wd = 2, 3, 36, 48
+    xf = rng.integers(-3, 4, (n, cin, h, wd)).astype(np.float32)
+    wf = rng.integers(-2, 3, (64, cin, 7, 7)).astype(np.float32)
+    bf = rng.integers(-4, 5, (64,)).astype(np.float32)
+    xf[0, 1, 10, 20] = np.nan  # NaN conv values around (5, 10) of image 0
+    xf[1, 0, 0, 0] = np.nan    # at the image corner: windows whose first element is NaN
+    x, w, b = (synth.to_storage(a, BF16) for a in (xf, wf, bf))
+    geom, pool = hip.i64_array((n, cin, h, wd, 64, 7, 7, 2, 2, 3, 3, 1)), hip.i64_array((3, 3, 2, 2, 1, 1))
+    dx, dw, db = dev(hip, x), dev(hip, w), dev(hip, b)  # held: the buffers must outlive the launch
+    for relu in (1, 0):
+        want = stem_oracle(BF16, x, w, b, relu)
+        dy = hip.DeviceBuffer(want.nbytes)
+        hip.check(hip.lib().fh_conv2d_stem_pool(BF16, dx.value, dw.value, db.value, dy.value, geom, pool, relu, None))
+        got = dy.download(want.shape, want.dtype)
+        # NaN positions must agree; the NaN's sign and payload are the matrix core's, not the CPU's
+        gnan, wnan = np.isnan(synth.to_float(got, BF16)), np.isnan(synth.to_float(want, BF16))
+        assert wnan.any() and (gnan == wnan).all(), f"relu={relu}: NaN positions differ at {np.count_nonzero(gnan != wnan)}"
+        assert_bitwise(np.where(wnan, 0, got), np.where(wnan, 0, want), f"stem exact relu={relu}")
+
+
+def test_conv2d_stem_pool_rejections(hip):
+    lib = hip.lib()
+    pool = hip.i64_array((3, 3, 2, 2, 1, 1))
+    ok = (2, 3, 224, 224, 64, 7, 7, 2, 2, 3, 3, 1)
+    assert lib.fh_conv2d_stem_pool_supported(BF16, hip.i64_array(ok), pool) == 1
+    assert lib.fh_conv2d_stem_pool_supported(F32, hip.i64_array(ok), pool) == 0
+    for k, v in [(1, 4), (4, 32), (5, 5), (7, 1), (9, 2), (3, 220), (3, 232), (11, 3)]:
+        bad = list(ok)
+        bad[k] = v
+        assert lib.fh_conv2d_stem_pool_supported(BF16, hip.i64_array(bad), pool) == 0, (k, v)
+    assert lib.fh_conv2d_stem_pool_supported(BF16, hip.i64_array(ok), hip.i64_array((2, 2, 2, 2, 0, 0))) == 0
+    dx = hip.DeviceBuffer(16)
+    assert lib.fh_conv2d_stem_pool(BF16, dx.value, dx.value, None, dx.value, hip.i64_array((2, 3, 224, 232, 64, 7, 7, 2,
+                                                                                         2, 3, 3, 1)), pool, 1, None) == 4
+
+
 # ---- fused attention ------------------------------------------------------------------------------------
 
 def attention_oracle(dtype, q, k, v, batch, seq, heads, dh, scale_value=None):
