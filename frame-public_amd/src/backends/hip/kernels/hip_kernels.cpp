@@ -397,7 +397,8 @@ Status conv_stem_pool_kernel(KernelContext& ctx) {
     return invalid(op, "missing or malformed attributes");
   if (x.shape().rank() != 4 || w.shape().rank() != 4 || y.shape().rank() != 4) return invalid(op, "x, w and y must be rank-4");
   for (const Tensor& t : ctx.inputs)
-    if (!same_elem_type(t, y)) return invalid(op, "operand dtypes differ");
+    if (!same_elem_type(t, y))
+      return invalid(op, "operand dtypes differ");
   Result<int32_t> dt = float_code(op, y.dtype());
   if (!dt.is_ok()) return dt.status();
   const int64_t geom[12] = {x.shape().dim(0), x.shape().dim(1), x.shape().dim(2), x.shape().dim(3), w.shape().dim(0),
