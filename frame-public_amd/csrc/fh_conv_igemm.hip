@@ -58,7 +58,14 @@ struct ConvNhwcArgs {
   int32_t vec_store;  // NCHW: Ho*Wo % V == 0; NHWC: Cout % V == 0; and 16-byte aligned output / epilogue operands
   int32_t out_nhwc;   // 1: y (and the epilogue operands) are [N][Ho][Wo][Cout]
   EpilogueArgs ep;
+  float* part;        // split K (kEpiSplitK instances): fp32 partial sums [gridDim.y][P][Cout]
+  int32_t kt_split;   // split K: k stages per split
 };
+
+// Epilogue "program" of the split-K instances: the workgroup of split s writes its fp32 sums over k stages
+// [s * kt_split, (s + 1) * kt_split) to part[s] instead of running an epilogue; conv_split_reduce_kernel sums the
+// splits in order and runs the real epilogue. Distinct from every EpiKind.
+constexpr int kEpiSplitK = 6;
 
 template <int TM, int TN>
 struct KFragments {
@@ -283,7 +290,9 @@ __device__ __forceinline__ void conv_store_tile(const ConvNhwcArgs& args, f32x16
   }
 }
 
-template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, bool C8, int E>
+// NS: LDS ring depth (stages in flight NS - 1); deeper rings for launches of one workgroup per CU, whose loads have
+// no other workgroup to hide behind.
+template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, bool C8, int E, int NS = kStages>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNhwcArgs args) {
   using S = typename Io<T>::storage;
   constexpr int ES = static_cast<int>(sizeof(S));
@@ -302,9 +311,10 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
   static_assert((A_BYTES / 1024) % NW == 0 && A_PER_WAVE >= 1, "A stage loads split evenly over waves");
   static_assert((B_BYTES / 1024) % NW == 0 && B_PER_WAVE >= 1, "B stage loads split evenly over waves");
   static_assert(TM >= 1 && TN >= 1, "wave tile at least 32x32");
-  static_assert(2 * LOADS <= 63, "vmcnt range");
+  static_assert((NS - 2) * LOADS <= 63, "vmcnt range");
+  static_assert(NS >= 4 && (NS & (NS - 1)) == 0, "ring depth a power of two");
 
-  __shared__ __attribute__((aligned(1024))) unsigned char ring[kStages * STAGE];
+  __shared__ __attribute__((aligned(1024))) unsigned char ring[NS * STAGE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -325,7 +335,10 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
 
   const S* __restrict__ W = static_cast<const S*>(args.w);
   const int cin = args.cin, K = args.k;
-  const int KT = K / KBK;
+  // stages [kt0, kt0 + KT) of the K / KBK: all of them, or this workgroup's split (kEpiSplitK)
+  const int kt0 = E == kEpiSplitK ? static_cast<int>(blockIdx.y) * args.kt_split : 0;
+  const int KT = E == kEpiSplitK ? min(args.kt_split, K / KBK - kt0) : K / KBK;
+  static_assert(E != kEpiSplitK || !C8, "split K walks the filter positions of whole-channel stages");
 
   // ---- A (filter) sources: row co, clamped to the last channel ----
   int64_t a_src[A_PER_WAVE];
@@ -373,6 +386,13 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
   // Filter position of the next stage to load; stays on the last stage once every stage has been issued.
   // ld_off = the stage's element offset from a window origin, (kh * W + kw) * Cin + ci0.
   int ld_kh = 0, ld_kw = 0, ld_ci = 0, ld_next = 0, ld_off = 0;
+  if constexpr (E == kEpiSplitK) {
+    const int k_first = kt0 * KBK, pos = k_first / cin;
+    ld_ci = k_first - pos * cin;
+    ld_kh = pos / args.kw;
+    ld_kw = pos - ld_kh * args.kw;
+    ld_off = (ld_kh * args.w_in + ld_kw) * cin + ld_ci;
+  }
   auto advance = [&]() {
     if (ld_next + 1 < KT) {
       ++ld_next;
@@ -401,9 +421,9 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
 
   // Load instruction J of this wave's share of stage kt (filter position = the ld_* counters).
   auto load_one = [&]<int J>(int kt) {
-    unsigned char* st = ring + (kt & (kStages - 1)) * STAGE;
+    unsigned char* st = ring + (kt & (NS - 1)) * STAGE;
     if constexpr (J < A_PER_WAVE) {
-      const int64_t k0 = static_cast<int64_t>(min(kt, KT - 1)) * KBK;
+      const int64_t k0 = static_cast<int64_t>(kt0 + min(kt, KT - 1)) * KBK;
       global_to_lds16(W + a_src[J] + k0, (FH_LDS void*)(st + (wave * A_PER_WAVE + J) * 1024));
     } else {
       constexpr int JB = J - A_PER_WAVE;
@@ -481,10 +501,9 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
     }(std::make_integer_sequence<int, NMFMA>{});
   };
 
-  issue_stage(0);
-  issue_stage(1);
-  issue_stage(2);
-  wait_vmcnt<2 * LOADS>();
+#pragma unroll
+  for (int st = 0; st < NS - 1; ++st) issue_stage(st);
+  wait_vmcnt<(NS - 2) * LOADS>();
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   [&]<int... R_>(std::integer_sequence<int, R_...>) {
@@ -492,16 +511,16 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
   }(std::make_integer_sequence<int, NREAD>{});
 
   for (int kt = 0; kt < KT; ++kt) {
-    const uint32_t cur = ring_addr + (kt & (kStages - 1)) * STAGE;
-    const uint32_t nxt = ring_addr + ((kt + 1) & (kStages - 1)) * STAGE;
+    const uint32_t cur = ring_addr + (kt & (NS - 1)) * STAGE;
+    const uint32_t nxt = ring_addr + ((kt + 1) & (NS - 1)) * STAGE;
     fence_kfragments(f0);
     multiply_and_read.template operator()<1, false>(f0, cur, f1, 0);
-    wait_vmcnt<LOADS>();
+    wait_vmcnt<(NS - 3) * LOADS>();
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     fence_kfragments(f1);
-    multiply_and_read.template operator()<0, true>(f1, nxt, f0, kt + kStages - 1);
+    multiply_and_read.template operator()<0, true>(f1, nxt, f0, kt + NS - 1);
     advance();
   }
   // The last step read the next half's fragments (past the end: unused). Those LDS reads are still in flight
@@ -511,9 +530,69 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void conv_nhwc_kernel(ConvNh
 
   // ---- epilogue ----
   wait_vmcnt<0>();
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __syncthreads();
-  conv_store_tile<T, E, WM, WN, NW, kStages * STAGE>(args, acc, ring, wave, lane, m0 + wm * WM, n0 + wn * WN);
+  if constexpr (E == kEpiSplitK) {
+    // fp32 partials, channels-last: registers 4q .. 4q + 3 of accumulator (i, j) are channels
+    // i * 32 + 8 q + 4 hi .. + 3 of pixel j * 32 + l32, one 16-byte store (Cout % 64 == 0: whole channel tiles)
+    float* __restrict__ part = args.part + static_cast<int64_t>(blockIdx.y) * args.p * args.cout;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int64_t p = n0 + wn * WN + j * 32 + l32;
+        if (p >= args.p) continue;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int co = m0 + wm * WM + i * 32 + 8 * q + 4 * hi;
+          *reinterpret_cast<float4*>(part + p * args.cout + co) =
+              make_float4(acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]);
+        }
+      }
+    return;
+  } else {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __syncthreads();
+    conv_store_tile<T, E, WM, WN, NW, NS * STAGE>(args, acc, ring, wave, lane, m0 + wm * WM, n0 + wn * WN);
+  }
+}
+
+// The second launch of a split-K convolution (16-bit, channels-last output): one thread per 8 channels of one
+// pixel sums the splits' fp32 partials in split order, adds the bias, rounds once and runs the epilogue program on
+// the rounded values, as conv_store_tile does for an unsplit tile.
+template <typename T, int E>
+__global__ __launch_bounds__(256) void conv_split_reduce_kernel(ConvNhwcArgs args, int32_t splits) {
+  using S = typename Io<T>::storage;
+  static_assert(sizeof(S) == 2, "16-bit outputs");
+  const int groups = args.cout / 8;
+  const int64_t gid = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (gid >= args.p * groups) return;
+  const int64_t p = gid / groups;
+  const int co0 = static_cast<int>(gid - p * groups) * 8;
+  const int64_t idx = p * args.cout + co0, stride = args.p * args.cout;
+  float v[8];
+  {
+    const float4* src = reinterpret_cast<const float4*>(args.part + idx);
+    const float4 a = src[0], b = src[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+  }
+  for (int s = 1; s < splits; ++s) {
+    const float4* src = reinterpret_cast<const float4*>(args.part + s * stride + idx);
+    const float4 a = src[0], b = src[1];
+    v[0] += a.x; v[1] += a.y; v[2] += a.z; v[3] += a.w; v[4] += b.x; v[5] += b.y; v[6] += b.z; v[7] += b.w;
+  }
+  if (args.bias != nullptr) {
+    const uint4 braw = *reinterpret_cast<const uint4*>(static_cast<const S*>(args.bias) + co0);
+    float bv[8];
+    unpack_vec<T>(braw, bv);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] += bv[e];
+  }
+  uint4 packed;
+  packed.x = epi_stage2<E, T>(v[0], v[1]);
+  packed.y = epi_stage2<E, T>(v[2], v[3]);
+  packed.z = epi_stage2<E, T>(v[4], v[5]);
+  packed.w = epi_stage2<E, T>(v[6], v[7]);
+  constexpr int EA = epi_after_stage<E>();
+  *reinterpret_cast<uint4*>(static_cast<S*>(args.y) + idx) = epi_vec<EA, T>(args.ep, packed, idx);
 }
 
 // Whether a configuration can stage its wave tiles pixel-major (channels-last output) in its LDS ring.
@@ -564,6 +643,33 @@ fh_status launch_conv(ConvNhwcArgs a, hipStream_t stream) {
                        stream, a);
     return launch_status("conv_nhwc_kernel launch");
   });
+}
+
+// Split-K launch (16-bit, channels-last output, Cout % BM == 0): gridDim.y = splits workgroups per tile, each over
+// kt_split consecutive k stages, then the reduction with the epilogue. The caller sized a.part for `splits`
+// (split_count below gives the count that leaves no split empty).
+template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, int NS = kStages>
+fh_status launch_conv_split(ConvNhwcArgs a, int32_t splits, hipStream_t stream) {
+  a.tiles_m = a.cout / BM;
+  a.tiles_n = static_cast<int32_t>((a.p + BN - 1) / BN);
+  const int32_t kt = a.k / 32;
+  a.kt_split = (kt + splits - 1) / splits;
+  hipLaunchKernelGGL((conv_nhwc_kernel<T, BM, BN, WAVES_M, WAVES_N, false, kEpiSplitK, NS>),
+                     dim3(static_cast<uint32_t>(a.tiles_m) * static_cast<uint32_t>(a.tiles_n), static_cast<uint32_t>(splits)),
+                     dim3(WAVES_M * WAVES_N * 64), 0, stream, a);
+  if (const fh_status st = launch_status("conv_nhwc_kernel launch (split K)"); st != FH_OK) return st;
+  const int64_t threads = a.p * (a.cout / 8);
+  return with_epi<conv_epi_mask<T, false>()>(epi_kind(a.ep), [&]<int E>() {
+    hipLaunchKernelGGL((conv_split_reduce_kernel<T, E>), dim3(static_cast<uint32_t>((threads + 255) / 256)), dim3(256), 0,
+                       stream, a, splits);
+    return launch_status("conv_split_reduce_kernel launch");
+  });
+}
+
+// Splits that leave none empty: ceil(kt / ceil(kt / want)).
+int32_t split_count(int32_t kt, int32_t want) {
+  const int32_t per = (kt + want - 1) / want;
+  return (kt + per - 1) / per;
 }
 
 // ---- 3x3 stride-1 convolutions with the input patch resident in LDS -------------------------------------------
@@ -1988,9 +2094,11 @@ extern "C" fh_status fh_conv2d_nhwc_fwd(int32_t dtype, const void* x_nhwc, const
   return fh_conv2d_nhwc_fwd_ex(dtype, x_nhwc, w_khwc, bias, y, geom, epilogue, 0, stream);
 }
 
-extern "C" fh_status fh_conv2d_nhwc_fwd_ex(int32_t dtype, const void* x_nhwc, const void* w_khwc, const void* bias,
-                                           void* y, const int64_t geom[12], const fh_epilogue* epilogue,
-                                           int32_t flags, void* stream) {
+namespace fh {
+namespace {
+// Checks the arguments of fh_conv2d_nhwc_fwd_ex and fills the kernel arguments (everything but the tiling).
+fh_status nhwc_args(int32_t dtype, const void* x_nhwc, const void* w_khwc, const void* bias, void* y,
+                    const int64_t geom[12], const fh_epilogue* epilogue, int32_t flags, ConvNhwcArgs* out) {
   if ((flags & ~(FH_CONV_OUT_NHWC | FH_CONV_IMPLICIT_GEMM | FH_CONV_IN_NCHW | FH_CONV_W_OIHW)) != 0)
     return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd_ex: unknown flags");
   const bool w_oihw = (flags & FH_CONV_W_OIHW) != 0;
@@ -2009,7 +2117,8 @@ extern "C" fh_status fh_conv2d_nhwc_fwd_ex(int32_t dtype, const void* x_nhwc, co
   if (x_nhwc == nullptr || w_khwc == nullptr || y == nullptr)
     return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd: null pointer");
   if (!aligned16(x_nhwc) || !aligned16(w_khwc)) return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd: operands must be 16-byte aligned");
-  ConvNhwcArgs a{};
+  ConvNhwcArgs& a = *out;
+  a = ConvNhwcArgs{};
   a.x = x_nhwc;
   a.w = w_khwc;
   a.bias = bias;
@@ -2053,6 +2162,18 @@ extern "C" fh_status fh_conv2d_nhwc_fwd_ex(int32_t dtype, const void* x_nhwc, co
   for (int s = 0; s < a.ep.nseg; ++s)
     if (ew_is_binary(a.ep.ops[s]) && !aligned16(a.ep.ins[s])) vec = false;
   a.vec_store = vec ? 1 : 0;
+  return FH_OK;
+}
+}  // namespace
+}  // namespace fh
+
+extern "C" fh_status fh_conv2d_nhwc_fwd_ex(int32_t dtype, const void* x_nhwc, const void* w_khwc, const void* bias,
+                                           void* y, const int64_t geom[12], const fh_epilogue* epilogue,
+                                           int32_t flags, void* stream) {
+  ConvNhwcArgs a{};
+  if (const fh_status st = nhwc_args(dtype, x_nhwc, w_khwc, bias, y, geom, epilogue, flags, &a); st != FH_OK) return st;
+  const bool w_oihw = (flags & FH_CONV_W_OIHW) != 0, nchw_in = (flags & FH_CONV_IN_NCHW) != 0;
+  const bool c8 = geom[1] == 8 && dtype != FH_F32;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (w_oihw) {
     const int rows = band_rows_for(dtype, a, geom);
@@ -2074,6 +2195,69 @@ extern "C" fh_status fh_conv2d_nhwc_fwd_ex(int32_t dtype, const void* x_nhwc, co
   if (dtype == FH_F32) return dispatch_conv<float, false>(a, s);
   if (c8) return dtype == FH_BF16 ? dispatch_conv<bf16_t, true>(a, s) : dispatch_conv<f16_t, true>(a, s);
   return dtype == FH_BF16 ? dispatch_conv<bf16_t, false>(a, s) : dispatch_conv<f16_t, false>(a, s);
+}
+
+namespace fh {
+namespace {
+// Split count of fh_conv2d_nhwc_fwd_split's planned form, or 0 where the unsplit kernels run. Measured on an MI355X
+// (ResNet-18 layer 4 at batch 64, bf16, 64 x 64 unsplit vs 128 x 128 tiles split in two): 3x3 stride 1, K = 4608:
+// 36.6 -> 30.4 us (add;relu), 34.0 -> 30.4 us (relu); 3x3 stride 2, K = 2304: 19.0 -> 21.3 us, so not split; more
+// splits than the CUs hold in one round of 128 x 128 tiles were slower (3: 34 us, 8: 43 us). So: 16-bit,
+// channels-last output of whole 128-channel tiles, not C8, a channel count the resident-patch kernels do not take
+// (Cout > 256), at least 128 k stages, and as many splits as whole rounds of tiles fit the CUs once (at least two).
+int32_t split_plan(int32_t dtype, const int64_t* g, int32_t flags) {
+  if ((dtype != FH_BF16 && dtype != FH_F16) || flags != FH_CONV_OUT_NHWC || !nhwc_supported(dtype, g)) return 0;
+  if (g[1] == 8 || g[4] % 128 != 0 || g[4] <= 256) return 0;
+  const int64_t oh = (g[2] + 2 * g[9] - g[5]) / g[7] + 1, ow = (g[3] + 2 * g[10] - g[6]) / g[8] + 1;
+  const int64_t tiles = g[4] / 128 * ((g[0] * oh * ow + 127) / 128);
+  const int64_t cus = device_cu_count();
+  const int32_t kt = static_cast<int32_t>(g[5] * g[6] * g[1] / 32);
+  if (kt < 128) return 0;
+  const int64_t want = std::min<int64_t>(cus / tiles, kt / 32);
+  return want >= 2 ? split_count(kt, static_cast<int32_t>(want)) : 0;
+}
+}  // namespace
+}  // namespace fh
+
+extern "C" int64_t fh_conv2d_nhwc_split_workspace(int32_t dtype, const int64_t geom[12], int32_t flags, int32_t* splits) {
+  if (geom == nullptr || splits == nullptr) return -1;
+  int32_t n = *splits;
+  if (n <= 0) {
+    n = split_plan(dtype, geom, flags);
+  } else {
+    if ((dtype != FH_BF16 && dtype != FH_F16) || flags != FH_CONV_OUT_NHWC || !nhwc_supported(dtype, geom) ||
+        geom[1] == 8 || geom[4] % 128 != 0)
+      return -1;
+    n = split_count(static_cast<int32_t>(geom[5] * geom[6] * geom[1] / 32), n);
+  }
+  *splits = n;
+  if (n <= 1) return 0;
+  const int64_t oh = (geom[2] + 2 * geom[9] - geom[5]) / geom[7] + 1, ow = (geom[3] + 2 * geom[10] - geom[6]) / geom[8] + 1;
+  return int64_t{n} * geom[0] * oh * ow * geom[4] * 4;
+}
+
+extern "C" fh_status fh_conv2d_nhwc_fwd_split(int32_t dtype, const void* x_nhwc, const void* w_khwc, const void* bias,
+                                              void* y, const int64_t geom[12], const fh_epilogue* epilogue,
+                                              int32_t flags, int32_t splits, void* workspace, int64_t workspace_bytes,
+                                              void* stream) {
+  if (geom == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd_split: null geometry");
+  int32_t n = splits;
+  const int64_t need = fh_conv2d_nhwc_split_workspace(dtype, geom, flags, &n);
+  if (need < 0)
+    return fail(FH_UNIMPLEMENTED, "fh_conv2d_nhwc_fwd_split: split K needs bf16/f16, FH_CONV_OUT_NHWC only, "
+                                  "Cin % 32 == 0 and Cout % 128 == 0");
+  if (need == 0) return fh_conv2d_nhwc_fwd_ex(dtype, x_nhwc, w_khwc, bias, y, geom, epilogue, flags, stream);
+  ConvNhwcArgs a{};
+  if (const fh_status st = nhwc_args(dtype, x_nhwc, w_khwc, bias, y, geom, epilogue, flags, &a); st != FH_OK) return st;
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd_split: workspace smaller than fh_conv2d_nhwc_split_workspace");
+  if (!aligned16(workspace) || (bias != nullptr && !aligned16(bias)) || !a.vec_store)
+    return fail(FH_INVALID_ARGUMENT, "fh_conv2d_nhwc_fwd_split: workspace, bias, y and the epilogue operands must be "
+                                     "16-byte aligned");
+  if (a.p == 0) return FH_OK;
+  a.part = static_cast<float*>(workspace);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  return dtype == FH_BF16 ? launch_conv_split<bf16_t, 128, 128, 2, 4>(a, n, s) : launch_conv_split<f16_t, 128, 128, 2, 4>(a, n, s);
 }
 
 extern "C" fh_status fh_conv_pack_input_c8(const void* x, void* y, int64_t n, int32_t c, int64_t hw, void* stream) {

@@ -121,6 +121,9 @@ _SIGS = {
     "fh_mse_loss_grad": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p]),
     "fh_conv2d_nhwc_fwd_ex": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_void_p, POINTER(c_int64), c_void_p,
                                         c_int32, c_void_p]),
+    "fh_conv2d_nhwc_split_workspace": (c_int64, [c_int32, POINTER(c_int64), c_int32, POINTER(c_int32)]),
+    "fh_conv2d_nhwc_fwd_split": (c_int32, [c_int32, c_void_p, c_void_p, c_void_p, c_void_p, POINTER(c_int64), c_void_p,
+                                           c_int32, c_int32, c_void_p, c_int64, c_void_p]),
     "fh_pool2d": (c_int32, [c_int32, c_int32, c_void_p, c_void_p, POINTER(c_int64), c_void_p]),
     "fh_permute": (c_int32, [c_int32, c_void_p, c_void_p, c_int32, POINTER(c_int64), POINTER(c_int64), c_void_p]),
     "fh_copy2d": (c_int32, [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_void_p]),

@@ -724,7 +724,19 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
       std::vector<ir::Value*> conv_ins = ins;
       conv_ins[0] = x_cl;
       conv_ins[1] = w_cl;
-      Result<ir::Node*> c = out.create_node(std::string(kConvNhwcOp), std::move(conv_ins), {lowered_type(&n->outputs()[0])});
+      std::vector<ir::TensorType> conv_outs{lowered_type(&n->outputs()[0])};
+      if (!p.c8 && !in_nchw && nhwc.count(&n->outputs()[0])) {
+        // split K (fh_conv2d_nhwc_fwd_split): its fp32 partials as a second, planned output
+        int32_t splits = 0;
+        const int64_t ws = fh_conv2d_nhwc_split_workspace(conv_dtype_code(n->inputs()[0]->type()), geom, FH_CONV_OUT_NHWC, &splits);
+        if (ws > 0) {
+          ir::TensorType wst = conv_outs[0];
+          wst.dtype = DType::of<float>();
+          wst.shape = Shape({ws / 4});
+          conv_outs.push_back(wst);
+        }
+      }
+      Result<ir::Node*> c = out.create_node(std::string(kConvNhwcOp), std::move(conv_ins), std::move(conv_outs));
       if (!c.is_ok()) return c.status();
       for (const auto& [k, v] : n->attrs()) c.value()->set_attr(k, v);
       if (nhwc.count(&n->outputs()[0])) c.value()->set_attr("out_nhwc", ir::AttrValue{int64_t{1}});

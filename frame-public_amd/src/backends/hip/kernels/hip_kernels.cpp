@@ -315,12 +315,14 @@ Status conv_impl(KernelContext& ctx, const std::string& op, size_t n_main) {
 }
 
 // x_nhwc [N,H,W,Cin] (or NCHW, in_nchw), w_khwc [Cout,KH,KW,Cin] (or [Cout,Cin,KH,KW], w_oihw), optional bias
-// [Cout], then the epilogue operands; y NCHW (or channels-last, out_nhwc).
+// [Cout], then the epilogue operands; y NCHW (or channels-last, out_nhwc). An optional second output is the fp32
+// workspace of the split-K form (channels-last output only; fh_conv2d_nhwc_split_workspace sized it).
 Status conv_nhwc_kernel(KernelContext& ctx) {
   const std::string op(kConvNhwcOp);
   const auto* n_main_attr = attr<int64_t>(ctx, "n_main_inputs");
   const size_t n_main = n_main_attr ? static_cast<size_t>(*n_main_attr) : 2;
-  if (ctx.inputs.size() < n_main || n_main < 2 || n_main > 3 || ctx.outputs.size() != 1) return invalid(op, "bad operand count");
+  if (ctx.inputs.size() < n_main || n_main < 2 || n_main > 3 || ctx.outputs.empty() || ctx.outputs.size() > 2)
+    return invalid(op, "bad operand count");
   const Tensor& x = ctx.inputs[0];
   const Tensor& w = ctx.inputs[1];
   const Tensor* bias = n_main == 3 ? &ctx.inputs[2] : nullptr;
@@ -368,6 +370,18 @@ Status conv_nhwc_kernel(KernelContext& ctx) {
   if (bias != nullptr && (bias->shape().rank() != 1 || bias->shape().dim(0) != geom[4])) return invalid(op, "bias must be [Cout]");
   Result<fh_epilogue> ep = make_epilogue(ctx, op, n_main);
   if (!ep.is_ok()) return ep.status();
+  if (ctx.outputs.size() == 2) {
+    Tensor& ws = ctx.outputs[1];
+    const bool ws_f32 = same_elem_type(ws, DType::of<float>());
+    if (!out_nhwc || in_nchw || c8 || !ws_f32)
+      return invalid(op, "the split-K workspace goes with a channels-last output and is float32");
+    FRAME_HIP_RETURN_IF_ERROR(fh_conv2d_nhwc_fwd_split(dt.value(), x.raw_data(), w.raw_data(), bias ? bias->raw_data() : nullptr,
+                                                       y.raw_data(), geom, ep.value().nseg > 0 ? &ep.value() : nullptr,
+                                                       FH_CONV_OUT_NHWC, 0, ws.raw_data(),
+                                                       ws.numel() * static_cast<int64_t>(sizeof(float)), stream_handle(ctx)),
+                              "op '" + op + "' (hip)");
+    return Status::ok();
+  }
   FRAME_HIP_RETURN_IF_ERROR(fh_conv2d_nhwc_fwd_ex(dt.value(), x.raw_data(), w.raw_data(), bias ? bias->raw_data() : nullptr,
                                                   y.raw_data(), geom, ep.value().nseg > 0 ? &ep.value() : nullptr,
                                                   (out_nhwc ? FH_CONV_OUT_NHWC : 0) | (in_nchw ? FH_CONV_IN_NCHW : 0) |

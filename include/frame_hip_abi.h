@@ -194,6 +194,24 @@ fh_status fh_conv2d_nhwc_fwd(int32_t dtype, const void* x_nhwc, const void* w_kh
 fh_status fh_conv2d_nhwc_fwd_ex(int32_t dtype, const void* x_nhwc, const void* w_khwc, const void* bias, void* y,
                                 const int64_t geom[12], const fh_epilogue* epilogue, int32_t flags, void* stream);
 
+/* Split-K form of fh_conv2d_nhwc_fwd_ex, for convolutions with few output tiles and a long reduction (ResNet's
+ * 7x7x512 layers at batch 64: 100 tiles of 128 x 128 for 256 CUs, K = 4608): each tile's K range is cut into
+ * `splits` consecutive ranges of k stages, one workgroup each, whose fp32 sums go to `workspace`
+ * ([splits][N*Ho*Wo][Cout] floats); a second launch sums them in split order, adds the bias, rounds once and runs
+ * the epilogue (same semantics as fh_conv2d_fwd; the fp32 sum is associated differently, hence not bit-identical
+ * to the unsplit kernels). bf16/f16, flags == FH_CONV_OUT_NHWC, Cin % 32 == 0, Cout % 128 == 0; the workspace,
+ * bias, y and epilogue operands 16-byte aligned.
+ * fh_conv2d_nhwc_split_workspace: with *splits <= 0, the planned count (0 where the unsplit kernels are used:
+ * Cout <= 256, fewer than 128 k stages, too many tiles to split in two) is written to *splits; with *splits > 0 that
+ * count is used (reduced so no split is empty, written back). Returns the workspace bytes (0: no split, the call
+ * runs fh_conv2d_nhwc_fwd_ex), or -1 where split K does not apply. fh_conv2d_nhwc_fwd_split takes the same
+ * `splits` argument. No counterpart in the reference (cuDNN picks its own algorithm and workspace:
+ * src/backends/cuda/kernels/conv.cpp:385-520). */
+int64_t fh_conv2d_nhwc_split_workspace(int32_t dtype, const int64_t geom[12], int32_t flags, int32_t* splits);
+fh_status fh_conv2d_nhwc_fwd_split(int32_t dtype, const void* x_nhwc, const void* w_khwc, const void* bias, void* y,
+                                   const int64_t geom[12], const fh_epilogue* epilogue, int32_t flags, int32_t splits,
+                                   void* workspace, int64_t workspace_bytes, void* stream);
+
 /* 1 if fh_conv2d_nhwc_fwd accepts dtype and geom (bf16/f16, groups 1, Cin % 32 == 0 or Cin == 8, 32-bit
  * offsets), else 0. Host-only query used at graph compile time; no counterpart in the reference.
  * With Cin == 8 the operands are in the C8 layout: x from fh_conv_pack_input_c8 and w from

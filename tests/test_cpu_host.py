@@ -259,6 +259,39 @@ def test_wgrad_workspace_rejects_invalid_geometry_on_the_host():
     assert ws([1, 64, 8, 2, 64, 3, 5, 1, 1, 1, 1, 1]) == -1  # w + 2p < kw
 
 
+def test_conv_split_k_plan_is_host_only():
+    """fh_conv2d_nhwc_split_workspace plans split K on the host: ResNet-18's 7x7x512 3x3 convs at batch 64 split in
+    two (100 tiles of 128 x 128 for 256 CUs, 144 k stages), the stride-2 one (72 stages), layer 3 (Cout 256) and
+    fp32 stay unsplit; an explicit count is reduced so no split is empty; NCHW output and Cout % 128 give -1."""
+    lib = abi.lib()
+    k = ctypes.c_int32(0)
+
+    def plan(geom, dtype=3, flags=1, splits=0):
+        k.value = splits
+        return lib.fh_conv2d_nhwc_split_workspace(dtype, abi.i64_array(geom), flags, ctypes.byref(k)), k.value
+
+    l4 = (64, 512, 7, 7, 512, 3, 3, 1, 1, 1, 1, 1)
+    assert plan(l4) == (2 * 3136 * 512 * 4, 2)
+    assert plan((64, 256, 14, 14, 512, 3, 3, 2, 2, 1, 1, 1)) == (0, 0)  # stride 2: K = 2304
+    assert plan((64, 256, 14, 14, 256, 3, 3, 1, 1, 1, 1, 1)) == (0, 0)
+    assert plan((256, 512, 7, 7, 512, 3, 3, 1, 1, 1, 1, 1)) == (0, 0)  # 392 tiles: no split fits one round
+    assert plan(l4, dtype=0) == (0, 0)
+    assert plan(l4, splits=5) == (5 * 3136 * 512 * 4, 5)
+    assert plan(l4, splits=100) == (72 * 3136 * 512 * 4, 72)  # 144 stages: 2 per split
+    assert plan(l4, flags=0, splits=2)[0] == -1 and plan(l4, dtype=0, splits=2)[0] == -1
+    assert plan((64, 512, 7, 7, 320, 3, 3, 1, 1, 1, 1, 1), splits=2)[0] == -1
+    assert lib.fh_conv2d_nhwc_split_workspace(3, None, 1, ctypes.byref(k)) == -1
+
+
+def test_resnet_layer4_lowers_with_split_k_workspaces():
+    # at batch 64 the three 3x3 stride-1 convs of layer 4 carry their fp32 partials as a second planned output
+    g, _ = graphs.resnet18(batch=64, dtype=3)
+    out = host.hip_lowered(g.text(), 1)
+    ws = [l for l in out.splitlines() if "hip_conv2d_nhwc_internal" in l and "float32[3211264]" in l]
+    assert len(ws) == 3, ws
+    assert all("out_nhwc=1" in l and "[64,7,7,512]" in l for l in ws)
+
+
 @pytest.mark.parametrize("dtype,cin,lowered", [(3, 64, "hip_conv2d_nhwc_internal"), (0, 64, "hip_conv2d_nhwc_internal"),
                                                (3, 3, "hip_pack_input_c8_internal"), (0, 3, "conv2d"),
                                                (0, 24, "conv2d")])

@@ -171,11 +171,11 @@ def test_c4_full_graph_every_step_at_1e2():
     assert exe.steps() == [op for _, op, _, _, _ in nodes], "plan steps differ from the lowered graph's nodes"
     say(f"C4 full graph: {len(nodes)} steps")
 
-    # every output of every step, tapped
+    # every output of every step, tapped (the float32 ones are split-K workspaces of layer-4 convs)
     values, taps = {}, []
     for step, (outs, op, _, _, types) in enumerate(nodes):
-        for j, (oid, (_, shape)) in enumerate(zip(outs, types)):
-            values[oid] = np.empty(shape, np.uint16)
+        for j, (oid, (dt, shape)) in enumerate(zip(outs, types)):
+            values[oid] = np.empty(shape, np.float32 if dt in ("f32", "float32") else np.uint16)
             taps.append((step, j, values[oid]))
     n_in = len(ins)
     for i, a in enumerate(ins):

@@ -908,6 +908,87 @@ def test_conv2d_nhwc_epilogue_add_relu(hip, dtype):
     assert_close(got, want, dtype, what="conv nhwc epilogue")
 
 
+SPLIT_CASES = [
+    # geometry, splits (0: the planned count), epilogue
+    ((64, 512, 7, 7, 512, 3, 3, 1, 1, 1, 1, 1), 0, "add;relu"),  # ResNet-18 layer 4 at batch 64 (planned: 2)
+    ((64, 512, 7, 7, 512, 3, 3, 1, 1, 1, 1, 1), 0, "relu"),
+    ((3, 512, 7, 7, 512, 3, 3, 1, 1, 1, 1, 1), 5, "add;relu"),   # 147 pixels (a ragged 128-pixel tile), 144 / 5
+    ((2, 256, 9, 7, 384, 3, 3, 2, 1, 1, 0, 1), 3, "none"),       # stride 2 x 1, asymmetric padding, no bias
+    ((1, 64, 5, 5, 128, 1, 1, 1, 1, 0, 0, 1), 2, "add;add"),      # 2 k stages, one per split; the interpreter
+]
+
+
+@pytest.mark.parametrize("geom,splits,program", SPLIT_CASES)
+def test_conv2d_nhwc_split_k(hip, geom, splits, program):
+    # fh_conv2d_nhwc_fwd_split: fp32 partials per K range, summed in split order by the reduction, which adds the
+    # bias, rounds once and runs the epilogue; checked against the oracle at 1e-2 and against the unsplit kernel
+    say(f"conv split-K {geom} splits={splits} {program}")
+    dtype = BF16
+    n, cin, h, w, cout, kh, kw = geom[:7]
+    x = synth.tensor(171, (n, cin, h, w), dtype, "normal")
+    wt = synth.tensor(172, (cout, cin, kh, kw), dtype, "normal", (2.0 / (cin * kh * kw)) ** 0.5)
+    with_bias = program != "none"
+    bias = synth.tensor(173, (cout,), dtype, "normal", 0.1) if with_bias else None
+    conv = orc.conv2d(dtype, x, wt, bias, geom)
+    res = synth.tensor(174, conv.shape, dtype, "normal")
+    res2 = synth.tensor(175, conv.shape, dtype, "normal")
+    ops = {"none": [], "relu": [hip.EW_RELU], "add;relu": [hip.EW_ADD, hip.EW_RELU], "add;add": [hip.EW_ADD, hip.EW_ADD]}[program]
+    operands, arity, inputs = [conv], [], []
+    dr, dr2 = dev(hip, to_nhwc(res)), dev(hip, to_nhwc(res2))
+    for i, op in enumerate(ops):
+        arity.append(2 if op == hip.EW_ADD else 1)
+        if op == hip.EW_ADD:
+            operands.append(res if len(operands) == 1 else res2)
+            inputs.append((op, (dr if len(inputs) == 0 else dr2).value))
+        else:
+            inputs.append((op, None))
+    want = to_nhwc(orc.ew_program(dtype, ops, arity, operands) if ops else conv)
+    lib = hip.lib()
+    g = hip.i64_array(geom)
+    k = ctypes.c_int32(splits)
+    ws = lib.fh_conv2d_nhwc_split_workspace(dtype, g, 1, ctypes.byref(k))
+    oh, ow = want.shape[1:3]
+    assert k.value >= 2 and ws == k.value * n * oh * ow * cout * 4, (ws, k.value)
+    if splits == 0:
+        assert k.value == 2, "the planned split of ResNet-18's layer 4 at batch 64 on 256 CUs"
+    dx, dw = dev(hip, to_nhwc(x)), dev(hip, to_nhwc(wt))
+    db = dev(hip, bias) if with_bias else None
+    dws, dy, dy1 = hip.DeviceBuffer(ws), hip.DeviceBuffer(want.nbytes), hip.DeviceBuffer(want.nbytes)
+    ep = hip.make_epilogue(inputs) if inputs else None
+    epp = ctypes.byref(ep) if ep is not None else None
+    hip.check(lib.fh_conv2d_nhwc_fwd_split(dtype, dx.value, dw.value, db.value if db else None, dy.value, g, epp, 1,
+                                           k.value, dws.value, ws, None))
+    hip.check(lib.fh_conv2d_nhwc_fwd_ex(dtype, dx.value, dw.value, db.value if db else None, dy1.value, g, epp, 1, None))
+    got, unsplit = dy.download(want.shape, want.dtype), dy1.download(want.shape, want.dtype)
+    assert_close(got, want, dtype, what=f"split-K conv {geom}")
+    assert_close(got, unsplit, dtype, what=f"split-K vs unsplit {geom}")
+
+
+def test_conv2d_nhwc_split_k_rejections(hip):
+    lib = hip.lib()
+    l4 = hip.i64_array((64, 512, 7, 7, 512, 3, 3, 1, 1, 1, 1, 1))
+    k = ctypes.c_int32(0)
+    for dtype, flags in [(F32, 1), (BF16, 0), (BF16, 3)]:  # fp32, NCHW output, with FH_CONV_IMPLICIT_GEMM
+        k.value = 0
+        assert lib.fh_conv2d_nhwc_split_workspace(dtype, l4, flags, ctypes.byref(k)) in (0, -1)
+    k.value = 2
+    assert lib.fh_conv2d_nhwc_split_workspace(BF16, hip.i64_array((64, 512, 7, 7, 192, 3, 3, 1, 1, 1, 1, 1)), 1,
+                                              ctypes.byref(k)) == -1  # Cout % 128 != 0
+    k.value = 0
+    assert lib.fh_conv2d_nhwc_split_workspace(BF16, hip.i64_array((64, 256, 14, 14, 256, 3, 3, 1, 1, 1, 1, 1)), 1,
+                                              ctypes.byref(k)) == 0 and k.value == 0  # layer 3 stays unsplit
+    need = lib.fh_conv2d_nhwc_split_workspace(BF16, l4, 1, ctypes.byref(k))
+    buf = hip.DeviceBuffer(need)
+    # a workspace one float short, a misaligned workspace
+    assert lib.fh_conv2d_nhwc_fwd_split(BF16, buf.value, buf.value, None, buf.value, l4, None, 1, 0, buf.value,
+                                        need - 4, None) == 1
+    assert lib.fh_conv2d_nhwc_fwd_split(BF16, buf.value, buf.value, None, buf.value, l4, None, 1, 0, buf.value + 8,
+                                        need - 8, None) == 1
+    # an explicit split count where split K does not apply (fp32); a planned count of 0 runs the unsplit kernels
+    assert lib.fh_conv2d_nhwc_fwd_split(F32, buf.value, buf.value, None, buf.value, l4, None, 1, 2, buf.value,
+                                        need, None) == 4
+
+
 def test_conv2d_nhwc_rejects_unsupported(hip):
     # channel counts the stage width does not divide (and no C8 layout for fp32) and grouped convolutions stay
     # on the direct path
