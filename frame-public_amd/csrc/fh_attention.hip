@@ -5,32 +5,36 @@
 //   P  = softmax rows of S2, rounded     (m = max, e = exp(x - m), s = sum e, y = round(e / s))
 //   O  = round(P · V_bh)                 (matmul)
 // and O lands at rows [b*seq, (b+1)*seq), columns [h*dh, (h+1)*dh) of the output: the layout of the reference's
-// head concat (axis 1) and batch concat (axis 0). S and S2 are rounded where the reference rounds them and m is
-// the exact row maximum of S2. The normalisation moves behind the second product: the kernel multiplies
-// round(e) (not round(e / s)) by V and scales the fp32 sums by 1/s before the one output rounding, so every
-// exponential is evaluated once. That, the summation orders (MFMA blocks, per-lane partial sums) and the exp
-// routine (v_exp_f32 of x log2(e) - m log2(e)) differ from the decomposition, each well inside one rounding of
-// the stored probabilities.
+// head concat (axis 1) and batch concat (axis 0). S and S2 are rounded where the reference rounds them, m is the
+// exact row maximum of S2, and the stored probabilities are round(e / s) as the reference's softmax stores them,
+// so P·V multiplies the same 16-bit P. What differs from the decomposition: the summation orders (MFMA blocks,
+// per-lane partial sums of e), the exponential (v_exp_f32 of x log2(e) - m log2(e) instead of expf(x - m), within
+// a few fp32 ulps), and e / s evaluated as e * (1 / s) (within one fp32 rounding); each changes a stored
+// probability only where the exact value lies that close to a 16-bit rounding boundary, and the tests report the
+// fraction of outputs that come out bit-identical (above 99.7 % at 512 keys).
 //
-// One wave owns 32 queries and all seq keys; a workgroup is W waves (4, or 2 when seq is not a multiple of 128).
-// The work is bound by its VALU instruction stream (about 7 VALU instructions per score, one of them the
-// quarter-rate exponential, against two MFMA k-steps per 32 x 32 tile), so the per-score code is kept short.
-//  1. Scores transposed, Sᵀ = K·Qᵀ on v_mfma_f32_32x32x16, per 64-key block: K blocks stream through a
-//     double-buffered 8 KB LDS ring (global_load_lds_dwordx4, 16-byte chunks swizzled by row), the Q fragments
+// attention_kernel: one wave owns 32 queries and all seq keys; a workgroup is W waves (4, or 2 when seq is not a
+// multiple of 128). attention_split_kernel (bf16, seq % 128 == 0) splits each query block's keys over two waves.
+// The work is bound by its VALU instruction stream (about 9 VALU instructions and two quarter-rate
+// exponentials per score, against two MFMA k-steps per 32 x 32 tile), so the per-score code is kept short.
+//  1. Scores transposed, Sᵀ = K·Qᵀ on v_mfma_f32_32x32x16, per 64-key block: K blocks go to LDS
+//     (global_load_lds_dwordx4, 16-byte chunks swizzled by row), all requested at the start; the Q fragments
 //     stay in registers. Each lane's accumulator then holds one query and 16 keys of a 32-key tile; they are
 //     rounded, scaled, rounded and kept as packed bf16/f16 in registers (seq/2 values per lane). The running
 //     maximum is taken over the scaled values before their rounding: rounding is monotonic, so the rounded
 //     maximum is the maximum of the rounded values.
-//  2. m per query: the lane's maximum and its partner lane's (lane ^ 32, same query).
-//  3. Oᵀ = Vᵀ·Pᵀ: p = round(exp(S2 - m)) is produced in registers already in the B-operand layout (k = the
-//     lane's 8 keys of one query, in the accumulator's key order) while the lane sums the unrounded e; the A
-//     operand (Vᵀ) comes from V blocks in LDS through ds_read_b64_tr_b16 in the same key order. V streams like
-//     K did. The output is round(acc * (1/s)), s = the lane's sum plus its partner's.
-// LDS: 32 KB per workgroup (two K and two V blocks), so two workgroups share a CU.
+//  2. m per query: the lane's maximum and its partner lane's (lane ^ 32, same query); then s, the sum of
+//     e = exp(S2 - m) over the lane's keys and its partner's.
+//  3. Oᵀ = Vᵀ·Pᵀ: p = round(e / s) is produced in registers already in the B-operand layout (k = the lane's 8
+//     keys of one query, in the accumulator's key order); the A operand (Vᵀ) comes from V blocks in LDS through
+//     ds_read_b64_tr_b16 in the same key order. V block b replaces K block b in LDS once every wave has read it.
+//     The output is round(acc).
+// LDS: seq x 128 bytes per workgroup (64 KB at seq 512), so two workgroups share a CU.
 #include <hip/hip_runtime.h>
 
 #include <cmath>
 #include <string>
+#include <type_traits>
 #include <utility>
 
 #include "fh_common.h"
@@ -204,7 +208,18 @@ __global__ __launch_bounds__(W * 64, 2) void attention_kernel(const uint16_t* __
     const int krow = 4 * (g >> 1) + e;
     v_off[dt] = kv_addr + krow * 128 + v_chunk(krow, n0 >> 3) * 16 + (n0 & 7) * 2;
   }
-  float sum = 0.0f;
+  // the sum of the exponentials first, so that pass 3 stores round(e / s) as the reference's softmax does (every
+  // exponential is evaluated here and again in pass 3); e / s as e * (1 / s), see attention_split_kernel
+  float esum = 0.0f;
+#pragma unroll
+  for (int t = 0; t < NT; ++t)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t w = s2[t][j];
+      esum += __builtin_amdgcn_exp2f(__builtin_fmaf(lo16<T>(w), c, -ml)) +
+              __builtin_amdgcn_exp2f(__builtin_fmaf(hi16<T>(w), c, -ml));
+    }
+  const float r = 1.0f / (esum + __shfl_xor(esum, 32));
   wait_vmcnt<LOADS>();  // this wave's V blocks 0 .. NB-2
   barrier();
   [&]<int... B_>(std::integer_sequence<int, B_...>) {
@@ -230,7 +245,6 @@ __global__ __launch_bounds__(W * 64, 2) void attention_kernel(const uint16_t* __
                   ...);
             }(std::make_integer_sequence<int, 8>{});
             u32x4_t pf[2];
-            float part[8];
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
@@ -239,12 +253,8 @@ __global__ __launch_bounds__(W * 64, 2) void attention_kernel(const uint16_t* __
                 asm volatile("" : "+v"(w));  // keeps the exp of this tile here, after the block's barrier
                 const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(lo16<T>(w), c, -ml));
                 const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(hi16<T>(w), c, -ml));
-                part[4 * hf + j] = e0 + e1;
-                pf[hf][j] = pack2<T>(e0, e1);
+                pf[hf][j] = pack2<T>(e0 * r, e1 * r);  // P = round(e / s)
               }
-            // the tile's sum joins the running sum here (tied), so no tile's exponentials outlive the tile
-            sum += ((part[0] + part[1]) + (part[2] + part[3])) + ((part[4] + part[5]) + (part[6] + part[7]));
-            asm volatile("" : "+v"(sum));
             asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
             for (int dt = 0; dt < 2; ++dt)
@@ -261,18 +271,266 @@ __global__ __launch_bounds__(W * 64, 2) void attention_kernel(const uint16_t* __
   }(std::make_integer_sequence<int, NB>{});
 
   // ---- output: acc_o[dt][x] = O[query q0 + l32][d = 32 dt + 8 (x / 4) + 4 hi + x % 4] ----
-  sum += __shfl_xor(sum, 32);
-  const float r = 1.0f / sum;
   uint16_t* orow = out + base + static_cast<int64_t>(q0 + l32) * ld;
 #pragma unroll
   for (int dt = 0; dt < 2; ++dt)
 #pragma unroll
     for (int gq = 0; gq < 4; ++gq) {
       u32x2_t w;
-      w[0] = pack2<T>(acc_o[dt][4 * gq] * r, acc_o[dt][4 * gq + 1] * r);
-      w[1] = pack2<T>(acc_o[dt][4 * gq + 2] * r, acc_o[dt][4 * gq + 3] * r);
+      w[0] = pack2<T>(acc_o[dt][4 * gq], acc_o[dt][4 * gq + 1]);
+      w[1] = pack2<T>(acc_o[dt][4 * gq + 2], acc_o[dt][4 * gq + 3]);
       *reinterpret_cast<u32x2_t*>(orow + 32 * dt + 8 * gq + 4 * hi) = w;
     }
+}
+
+// Key-split form for seq % 128 == 0. A workgroup is 8 waves over 128 queries: waves w and w + 4 own the same 32
+// queries, w < 4 the first half of the keys and w >= 4 the second. Each wave keeps the packed scores of seq / 2
+// keys (64 registers at seq 512 instead of 128), so four waves fit per SIMD (two workgroups per CU): twice the
+// waves of attention_kernel over the same work, which is bound by the latency of its instruction stream. The
+// blocks of K (then V) are loaded by all 8 waves, the halves' blocks in pairs (i, NB/2 + i) so both halves start
+// together. Per query the halves combine through LDS: the row maximum (exact either way), the sum of the
+// exponentials s = s_first + s_second, and the fp32 products P·V: half h writes the output's d tile h (32 columns)
+// as round((O_first + O_second) * (1/s)), taking the other half's partial from LDS. Everything else (roundings,
+// exponentials, key order inside a half) is attention_kernel's.
+template <typename T, int NB, bool POW2>
+__global__ __launch_bounds__(512, 2) void attention_split_kernel(const uint16_t* __restrict__ q,
+                                                                 const uint16_t* __restrict__ k,
+                                                                 const uint16_t* __restrict__ v,
+                                                                 uint16_t* __restrict__ out, int heads, float scale) {
+  constexpr int SEQ = NB * 64;
+  constexpr int H = NB / 2;        // 64-key blocks per half
+  constexpr int NTH = 2 * H;       // 32-key tiles per half
+  constexpr int BLK = 64 * 128;    // one 64-key block of K or V, bytes
+  static_assert(NB % 2 == 0 && 2 * NB < 64, "whole block pairs; vmcnt range");
+  // K / V blocks, then the halves' fp32 partial products: 8 waves x 64 lanes x 16 floats = 32 KB
+  constexpr int KV_BYTES = NB * BLK > 8 * 64 * 16 * 4 ? NB * BLK : 8 * 64 * 16 * 4;
+  __shared__ __attribute__((aligned(1024))) unsigned char kv[KV_BYTES];
+  __shared__ float xmax[8][64], xsum[8][64];
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int half = wave >> 2;
+  const int l32 = lane & 31, hi = lane >> 5;
+  // Workgroup -> (query block, head, batch), XCD-aware: consecutive workgroups go to the 8 XCDs in turn, so
+  // workgroup L runs on XCD L % 8; the (L / 8)-th workgroup of each XCD takes consecutive (head, batch) pairs with
+  // all their query blocks, and the 4 workgroups that read one pair's K and V share that XCD's L2.
+  const int nq = SEQ / 128, total = static_cast<int>(gridDim.x);
+  int idx = static_cast<int>(blockIdx.x);
+  if ((total & 7) == 0) idx = (idx & 7) * (total >> 3) + (idx >> 3);
+  const int qb = idx % nq, hb = idx / nq;
+  const int h = hb % heads, b = hb / heads;
+  const int q0 = qb * 128 + (wave & 3) * 32;
+  const int64_t ld = static_cast<int64_t>(heads) * kDh;
+  const int64_t base = (static_cast<int64_t>(b) * SEQ) * ld + static_cast<int64_t>(h) * kDh;
+
+  u32x4_t qf[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s)
+    qf[s] = *reinterpret_cast<const u32x4_t*>(q + base + static_cast<int64_t>(q0 + l32) * ld + 16 * s + 8 * hi);
+  asm volatile("" ::: "memory");
+
+  // one 1 KB instruction per wave and block: rows 8 wave .. 8 wave + 7
+  auto load_block = [&](const uint16_t* src, int blk, bool is_v) {
+    const int row = 8 * wave + (lane >> 3), pc = lane & 7;
+    const int c = is_v ? v_chunk(row, pc) : k_chunk(row, pc);
+    const uint16_t* g = src + base + static_cast<int64_t>(blk * 64 + row) * ld + c * 8;
+    __builtin_amdgcn_global_load_lds(g, (FH_LDS void*)(kv + blk * BLK + wave * 1024), 16, 0, 0);
+  };
+  auto barrier = [] {
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  const uint32_t kv_addr = lds_addr((const FH_LDS void*)kv);
+  const uint32_t half_addr = kv_addr + half * H * BLK;  // this half's first block
+
+#pragma unroll
+  for (int i = 0; i < H; ++i) {
+    load_block(k, i, false);
+    load_block(k, H + i, false);
+  }
+  uint32_t k_off[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) k_off[s] = half_addr + l32 * 128 + k_chunk(l32, 2 * s + hi) * 16;
+
+  // ---- 1. scores of this half's keys ----
+  uint32_t s2[NTH][8];
+  float mraw = -__builtin_inff();
+  [&]<int... B_>(std::integer_sequence<int, B_...>) {
+    (
+        [&] {
+          constexpr int i = B_;
+          // K pair i has landed when no more than the loads issued after it are in flight: K pairs i+1 .. H-1
+          // and V pairs 0 .. i-2
+          wait_vmcnt<2 * (H - 1 - i) + 2 * (i >= 2 ? i - 1 : 0)>();
+          barrier();
+          if constexpr (i >= 1) {  // every wave has read K pair i - 1
+            load_block(v, i - 1, true);
+            load_block(v, H + i - 1, true);
+          }
+          // one 32-key tile at a time: 16 fragment and 16 accumulator registers (the scores of the later blocks are
+          // still to come, but 4 waves per SIMD leave 128 registers per lane)
+          auto tile = [&]<int t>() {
+            u32x4_t kf[4];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) kf[s] = lds_read_b128<i * BLK + t * 4096>(k_off[s]);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+            for (int s = 0; s < 4; ++s) asm volatile("" : "+v"(kf[s]));
+            f32x16_t acc;
+#pragma unroll
+            for (int x = 0; x < 16; ++x) acc[x] = 0.0f;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) mfma32<T>(kf[s], qf[s], acc);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const uint32_t sr = pack2<T>(acc[2 * j], acc[2 * j + 1]);
+              if constexpr (POW2) {
+                float mx;
+                asm("v_max3_f32 %0, %1, %2, %3" : "=v"(mx) : "v"(mraw), "v"(acc[2 * j]), "v"(acc[2 * j + 1]));
+                mraw = mx;
+                s2[2 * i + t][j] = sr;
+              } else {
+                const float a0 = lo16<T>(sr) * scale, a1 = hi16<T>(sr) * scale;
+                mraw = fmaxf(mraw, fmaxf(a0, a1));
+                s2[2 * i + t][j] = pack2<T>(a0, a1);
+              }
+              asm volatile("" : "+v"(s2[2 * i + t][j]));
+            }
+          };
+          tile.template operator()<0>();
+          tile.template operator()<1>();
+        }(),
+        ...);
+  }(std::make_integer_sequence<int, H>{});
+
+  // ---- 2. row maximum over both halves ----
+  xmax[wave][lane] = fmaxf(mraw, __shfl_xor(mraw, 32));
+  barrier();  // also: every wave has read K pair H - 1
+  load_block(v, H - 1, true);
+  load_block(v, NB - 1, true);
+  const float mh0 = xmax[wave & 3][lane], mh1 = xmax[(wave & 3) + 4][lane];
+  constexpr float kLog2e = 1.44269504088896340736f;
+  const float mr = Io<T>::round(fmaxf(mh0, mh1));
+  const float m = POW2 ? mr * scale : mr;
+  const float ml = m * kLog2e;
+  const float c = POW2 ? scale * kLog2e : kLog2e;
+
+  // ---- 3. this half's share of Oᵀ = Vᵀ·Pᵀ ----
+  f32x16_t acc_o[2];
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt)
+#pragma unroll
+    for (int x = 0; x < 16; ++x) acc_o[dt][x] = 0.0f;
+  const int g = lane >> 4, rr = lane & 15, qd = rr & 3, e = rr >> 2;
+  uint32_t v_off[2];
+#pragma unroll
+  for (int dt = 0; dt < 2; ++dt) {
+    const int n0 = 32 * dt + 16 * (g & 1) + 4 * qd;
+    const int krow = 4 * (g >> 1) + e;
+    v_off[dt] = half_addr + krow * 128 + v_chunk(krow, n0 >> 3) * 16 + (n0 & 7) * 2;
+  }
+  // ---- 2b. the sum of the exponentials over both halves, so that pass 3 stores round(e / s) as the reference's
+  // softmax does (every exponential is evaluated here and again in pass 3) ----
+  float esum = 0.0f;
+#pragma unroll
+  for (int t = 0; t < NTH; ++t)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint32_t w = s2[t][j];
+      esum += __builtin_amdgcn_exp2f(__builtin_fmaf(lo16<T>(w), c, -ml)) +
+              __builtin_amdgcn_exp2f(__builtin_fmaf(hi16<T>(w), c, -ml));
+    }
+  xsum[wave][lane] = esum + __shfl_xor(esum, 32);
+  wait_vmcnt<2>();  // this wave's V pairs 0 .. H-2
+  barrier();
+  // e / s as e * (1 / s): the two differ by at most one fp32 rounding, which changes the stored 16-bit probability
+  // only when e / s lies within that rounding of a 16-bit rounding boundary
+  const float r = 1.0f / (xsum[wave & 3][lane] + xsum[(wave & 3) + 4][lane]);
+  [&]<int... B_>(std::integer_sequence<int, B_...>) {
+    (
+        [&] {
+          constexpr int i = B_;
+          if constexpr (i == H - 1) {
+            wait_vmcnt<0>();
+            barrier();
+          }
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt) {
+            const int t = 2 * i + tt;
+            // V fragments of one d tile at a time (8 registers): d tile 0's are read before the exponentials,
+            // d tile 1's while d tile 0's products run
+            auto read_v = [&]<int dt>(u32x2_t (&vf)[2][2]) {
+              [&]<int... R_>(std::integer_sequence<int, R_...>) {
+                (
+                    [&] {
+                      constexpr int hf = R_ / 2, part = R_ % 2;
+                      constexpr int off = i * BLK + (16 * hf + 8 * part) * 128;
+                      vf[hf][part] = lds_read_tr16_b64<off>(v_off[dt] + tt * 32 * 128);
+                    }(),
+                    ...);
+              }(std::make_integer_sequence<int, 4>{});
+            };
+            u32x2_t vf[2][2];
+            read_v.template operator()<0>(vf);
+            u32x4_t pf[2];
+#pragma unroll
+            for (int hf = 0; hf < 2; ++hf)
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                uint32_t w = s2[t][4 * hf + j];
+                asm volatile("" : "+v"(w));
+                const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(lo16<T>(w), c, -ml));
+                const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(hi16<T>(w), c, -ml));
+                pf[hf][j] = pack2<T>(e0 * r, e1 * r);  // P = round(e / s)
+              }
+            auto multiply = [&](u32x2_t (&f)[2][2], f32x16_t& acc) {
+#pragma unroll
+              for (int hf = 0; hf < 2; ++hf) {
+                asm volatile("" : "+v"(f[hf][0]), "+v"(f[hf][1]));
+                const u32x4_t a{f[hf][0][0], f[hf][0][1], f[hf][1][0], f[hf][1][1]};
+                mfma32<T>(a, pf[hf], acc);
+              }
+            };
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            multiply(vf, acc_o[0]);
+            read_v.template operator()<1>(vf);
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            multiply(vf, acc_o[1]);
+          }
+        }(),
+        ...);
+  }(std::make_integer_sequence<int, H>{});
+
+  // ---- output: half h writes d tile h from its partial and its partner's (kv is free: every V read is done) ----
+  float* xo = reinterpret_cast<float*>(kv);
+  {
+    const int other = 1 - half;
+    float4* dst = reinterpret_cast<float4*>(xo + (wave * 64 + lane) * 16);
+    barrier();  // every wave's V reads are complete before kv is overwritten
+#pragma unroll
+    for (int x4 = 0; x4 < 4; ++x4)
+      dst[x4] = make_float4(acc_o[other][4 * x4], acc_o[other][4 * x4 + 1], acc_o[other][4 * x4 + 2], acc_o[other][4 * x4 + 3]);
+  }
+  barrier();
+  const float4* src = reinterpret_cast<const float4*>(xo + ((wave ^ 4) * 64 + lane) * 16);
+  f32x16_t o = half == 0 ? acc_o[0] : acc_o[1];
+#pragma unroll
+  for (int x4 = 0; x4 < 4; ++x4) {
+    const float4 p = src[x4];
+    o[4 * x4] += p.x;
+    o[4 * x4 + 1] += p.y;
+    o[4 * x4 + 2] += p.z;
+    o[4 * x4 + 3] += p.w;
+  }
+  uint16_t* orow = out + base + static_cast<int64_t>(q0 + l32) * ld + 32 * half;
+#pragma unroll
+  for (int gq = 0; gq < 4; ++gq) {
+    u32x2_t w;
+    w[0] = pack2<T>(o[4 * gq], o[4 * gq + 1]);
+    w[1] = pack2<T>(o[4 * gq + 2], o[4 * gq + 3]);
+    *reinterpret_cast<u32x2_t*>(orow + 8 * gq + 4 * hi) = w;
+  }
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
@@ -309,6 +567,18 @@ extern "C" fh_status fh_attention_fwd(int32_t dtype, const void* q, const void* 
   auto go = [&]<int NB>() {
     constexpr int W = (NB * 64) % 128 == 0 ? 4 : 2;
     auto launch = [&]<typename T, bool P>() {
+      // bf16 takes the key-split form (8 waves over the same 128 queries) where seq % 128 == 0; f16's conversions
+      // need more registers than its four waves per SIMD allow, so f16 keeps the unsplit kernel
+      // (the split form's workgroups form one flat grid, hence the 2^31 bound)
+      const int64_t flat = int64_t{grid.x} * grid.y * grid.z;
+      if constexpr (NB % 2 == 0 && std::is_same_v<T, bf16_t>) {
+        if (flat <= 0x7fffffff) {
+          hipLaunchKernelGGL((attention_split_kernel<T, NB, P>), dim3(static_cast<uint32_t>(flat)), dim3(512), 0, s, qq,
+                             kk, vv, oo, hd, scale);
+          return;
+        }
+      }
+      (void)flat;
       hipLaunchKernelGGL((attention_kernel<T, NB, W, P>), grid, dim3(W * 64), 0, s, qq, kk, vv, oo, hd, scale);
     };
     if (bf) {

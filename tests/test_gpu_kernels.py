@@ -1151,12 +1151,14 @@ def attention_oracle(dtype, q, k, v, batch, seq, heads, dh, scale_value=None):
 
 ATTENTION_CASES = [
     # dtype, batch, seq, heads, input std[, scale]: 1/sqrt(64) = 0.125 is a power of two, which the kernel
-    # folds into the exponent; the cases with 0.1 take its general path (round(round(S) * scale))
+    # folds into the exponent; the cases with 0.1 take its general path (round(round(S) * scale)). bf16 with seq a
+    # multiple of 128 runs the key-split kernel (two waves per 32 queries), the rest the unsplit one
     (BF16, 2, 64, 2, 1.0),    # one 64-key tile per wave half; score-row swizzle over 8 chunks
     (BF16, 1, 128, 3, 1.0),   # 16 chunks per score row
     (BF16, 2, 192, 2, 1.0),   # 24 chunks: not a multiple of 16
     (BF16, 1, 320, 1, 1.0),   # 40 chunks
     (BF16, 1, 512, 2, 1.0),   # the largest sequence (C5's)
+    (BF16, 8, 512, 16, 1.0),  # C5's whole attention: 8 x 16 (batch, head) pairs, 512 workgroups
     (BF16, 1, 256, 2, 3.0),   # wide score range: most probabilities underflow to 0
     (F16, 2, 256, 2, 1.0),
     (F16, 1, 512, 1, 0.5),
