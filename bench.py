@@ -86,8 +86,7 @@ def run_gpu(steps: int, warmup: int, data: str = "uniform", settle_ms: float = 3
     abi.check(abi.lib().fh_device_synchronize())
     t0 = time.perf_counter()
     start.record(native)
-    for _ in range(steps):
-        exe.run_tensors(ins, outs, stream)
+    exe.run_repeat([ins], outs, stream, steps)  # the K timed runs, issued from native code
     stop.record(native)
     stop.synchronize()
     stream.synchronize()
@@ -143,16 +142,15 @@ def _time_graph(graph_text, input_sets, steps, warmup, settle_ms=GRAPH_SETTLE_MS
         exe.run_tensors(sets[i % len(sets)], outs, stream)
     stream.synchronize()
     t_end = time.perf_counter() + settle_ms * 1e-3
-    i = 0
     while time.perf_counter() < t_end:
-        exe.run_tensors(sets[i % len(sets)], outs, stream)
-        i += 1
-        if i % 16 == 0:
-            stream.synchronize()
+        exe.run_repeat(sets, outs, stream, 16)
+        stream.synchronize()
     stream.synchronize()
     start.record(native)
-    for i in range(steps):
-        exe.run_tensors(sets[i % len(sets)], outs, stream)
+    # the timed runs are issued from native code (frame_executable_run_repeat), as the reference's google-benchmark
+    # loops call Executable::run from C++ (benchmarks/bench_matmul.cpp): a Python loop costs more per run than a
+    # short graph's kernels (LayerNorm's one 4 us launch) and would time the interpreter instead
+    exe.run_repeat(sets, outs, stream, steps)
     stop.record(native)
     stop.synchronize()
     return start.elapsed_ms(stop) / steps

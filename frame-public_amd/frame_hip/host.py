@@ -61,6 +61,8 @@ _SIGS = {
     "frame_executable_io_spec": (c_int32, [c_void_p, c_int32, c_int32, POINTER(c_int32), POINTER(c_int64),
                                            POINTER(c_int32)]),
     "frame_executable_run": (c_int32, [c_void_p, POINTER(c_void_p), c_int32, POINTER(c_void_p), c_int32, c_void_p]),
+    "frame_executable_run_repeat": (c_int32, [c_void_p, POINTER(c_void_p), c_int32, c_int32, POINTER(c_void_p), c_int32,
+                                              c_void_p, c_int32]),
     "frame_run_with_allocated_outputs": (c_int32, [c_void_p, POINTER(c_void_p), c_int32, POINTER(c_void_p), c_int32]),
     "frame_compile_cache_size": (c_int64, []),
     "frame_transform_text": (c_int32, [c_char_p, c_char_p, c_void_p, c_int64, POINTER(c_int64)]),
@@ -266,6 +268,13 @@ class Executable:
     def run_tensors(self, inputs, outputs, stream: Stream) -> None:
         check(lib().frame_executable_run(self.handle, _ptrs(inputs), len(inputs), _ptrs(outputs), len(outputs),
                                          stream.handle), "Executable.run")
+
+    def run_repeat(self, input_sets, outputs, stream: Stream, iterations: int) -> None:
+        """frame_executable_run_repeat: `iterations` runs issued from native code, run i reading input_sets[i % n]."""
+        flat = [t for s in input_sets for t in s]
+        n_in = len(input_sets[0]) if input_sets else 0
+        check(lib().frame_executable_run_repeat(self.handle, _ptrs(flat), len(input_sets), n_in, _ptrs(outputs),
+                                                len(outputs), stream.handle, iterations), "Executable.run_repeat")
 
     def steps(self) -> list[str]:
         """The hip executable's plan steps: the op of each non-input node of the lowered graph, in order."""

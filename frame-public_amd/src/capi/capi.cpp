@@ -262,6 +262,21 @@ int frame_executable_run(frame_executable* e, frame_tensor* const* inputs, int32
   return s.is_ok() ? 0 : fail(s);
 }
 
+int frame_executable_run_repeat(frame_executable* e, frame_tensor* const* input_sets, int32_t n_sets, int32_t n_in,
+                                frame_tensor* const* outputs, int32_t n_out, frame_stream* stream, int32_t iterations) {
+  if (e == nullptr || stream == nullptr || n_sets < 1 || n_in < 0 || n_out < 0 || iterations < 0 ||
+      (n_in > 0 && input_sets == nullptr) || (n_out > 0 && outputs == nullptr))
+    return fail_msg("frame_executable_run_repeat: bad argument");
+  std::vector<std::vector<frame::Tensor>> sets;
+  for (int32_t k = 0; k < n_sets; ++k) sets.push_back(unwrap(input_sets + static_cast<size_t>(k) * n_in, n_in));
+  std::vector<frame::Tensor> outs = unwrap(outputs, n_out);
+  for (int32_t i = 0; i < iterations; ++i) {
+    frame::Status s = e->exe->run(sets[static_cast<size_t>(i % n_sets)], outs, *stream->s);
+    if (!s.is_ok()) return fail(s);
+  }
+  return 0;
+}
+
 int frame_run_with_allocated_outputs(frame_executable* e, frame_tensor* const* inputs, int32_t n_in,
                                      frame_tensor** outputs, int32_t n_out) {
   std::vector<frame::Tensor> ins = unwrap(inputs, n_in);

@@ -71,6 +71,13 @@ int frame_executable_io_spec(const frame_executable* e, int32_t is_output, int32
 /* Executable::run on `stream` (enqueue only). */
 int frame_executable_run(frame_executable* e, frame_tensor* const* inputs, int32_t n_in, frame_tensor* const* outputs,
                          int32_t n_out, frame_stream* stream);
+/* `iterations` back-to-back Executable::run calls on `stream` (enqueue only), run i reading input set i % n_sets
+ * (input_sets holds n_sets x n_in tensors, set-major) and writing `outputs`. The benchmark's timed loop: the runs
+ * are issued from native code, as the reference's google-benchmark loops call Executable::run from C++
+ * (benchmarks/bench_matmul.cpp), so a short graph is not timed at the speed of a Python loop. Stops at the first
+ * failing run and returns its status. */
+int frame_executable_run_repeat(frame_executable* e, frame_tensor* const* input_sets, int32_t n_sets, int32_t n_in,
+                                frame_tensor* const* outputs, int32_t n_out, frame_stream* stream, int32_t iterations);
 /* runtime::run_with_allocated_outputs: allocates outputs on device 0 of the backend, runs, synchronises. */
 int frame_run_with_allocated_outputs(frame_executable* e, frame_tensor* const* inputs, int32_t n_in,
                                      frame_tensor** outputs, int32_t n_out);

@@ -226,3 +226,26 @@ def test_per_stream_arenas_are_bounded(dev):
     live_after = host.allocator_stats()["live"]
     say(f"live bytes with 12 streams: {live_many}; after they are destroyed: {live_after}")
     assert live_after < live_many
+
+
+def test_run_repeat_rotates_input_sets_like_single_runs(dev):
+    """frame_executable_run_repeat (the benchmark's native timed loop): run i reads input set i % n; after 5 runs
+    over 2 sets the outputs are those of a single run on set 0, bit for bit, and match the oracle."""
+    g = graphs.mlp(batch=64, dtype=F32)
+    exe = host.compile(g, "hip")
+    sets_np = [graphs.mlp_inputs(batch=64, dtype=F32, seed=s) for s in (1, 2)]
+    sets = [exe.upload_inputs(s) for s in sets_np]
+    stream = host.Stream("hip")
+    outs = exe.alloc_outputs()
+    exe.run_repeat(sets, outs, stream, 5)
+    stream.synchronize()
+    got = outs[0].numpy()
+    single = exe.alloc_outputs()
+    exe.run_tensors(sets[0], single, stream)
+    stream.synchronize()
+    assert_bitwise(got, single[0].numpy(), "run_repeat vs a single run")
+    (want,) = orc.run_graph_cpu(graphs.mlp(batch=64, dtype=F32, device="cpu"), sets_np[0])
+    assert_close(got, want, F32, what="run_repeat vs oracle")
+    exe.run_repeat(sets, outs, stream, 0)  # zero runs: nothing enqueued
+    stream.synchronize()
+    assert_bitwise(outs[0].numpy(), got, "after zero runs")
