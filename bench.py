@@ -350,9 +350,44 @@ def extras(steps, only=None):
                                  "ms": round(t * 8 * 1e3, 1), "TFLOP/s": round(111.67e9 / (t * 8) / 1e12, 6)}
         return res
 
+    def vendor(shapes):
+        # Yardstick only, on request: the vendor GEMM (hipBLASLt through torch.matmul, and torch.addmm with a full-size
+        # C as the graphs' bias inputs are) on bf16 U(-1,1) operands, after the same kind of settle; nothing of this
+        # repository runs in it
+        import torch
+
+        torch.manual_seed(0)
+        res = {}
+        for (m, n, k) in shapes:
+            a = (torch.rand(m, k, device="cuda") * 2 - 1).to(torch.bfloat16)
+            b = (torch.rand(k, n, device="cuda") * 2 - 1).to(torch.bfloat16)
+            c = (torch.rand(m, n, device="cuda") * 2 - 1).to(torch.bfloat16)
+            entry = {}
+            for name, fn in (("matmul", lambda: a @ b), ("addmm", lambda: torch.addmm(c, a, b))):
+                fn()
+                torch.cuda.synchronize()
+                t_end = time.perf_counter() + GRAPH_SETTLE_MS * 1e-3
+                while time.perf_counter() < t_end:
+                    for _ in range(10):
+                        fn()
+                    torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(max(steps, 20)):
+                    fn()
+                e1.record()
+                e1.synchronize()
+                us = e0.elapsed_time(e1) / max(steps, 20) * 1e3
+                entry[name] = {"us": round(us, 2), "TFLOP/s": round(gemm_flops(m, n, k) / (us * 1e-6) / 1e12, 1)}
+            res[f"{m}x{n}x{k}"] = entry
+        return res
+
     if only is not None:
         guard("graph_replay", graph_replay)
         guard("cpu_baselines", cpu_baselines)
+        guard("vendor_gemm_4096", lambda: vendor([(4096, 4096, 4096)]))
+        guard("vendor_gemm_c5", lambda: vendor([(4096, 3072, 1024), (4096, 1024, 1024), (4096, 4096, 1024),
+                                                (4096, 1024, 4096)]))
     guard("fused_elementwise", fused)
     guard("softmax_c5", lambda: rows_op("softmax"))
     guard("layer_norm_c5", lambda: rows_op("layer_norm"))
