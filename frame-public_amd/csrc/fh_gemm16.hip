@@ -1,5 +1,5 @@
 // bf16 / f16 GEMM for gfx950: C[M,N] = A[M,K] · B[K,N], row-major, fp32 accumulation on
-// v_mfma_f32_32x32x16_{bf16,f16}, one round-to-nearest-even per output, then the optional elementwise epilogue
+// v_mfma_f32_16x16x32_{bf16,f16}, one round-to-nearest-even per output, then the optional elementwise epilogue
 // (semantics of Frame's matmul: reference src/backends/cpu/kernels/matmul.cpp:92-185).
 //
 // Data path (CDNA4-specific):
@@ -12,10 +12,15 @@
 //    column per lane; ds_read_b64_tr_b16 (gfx950 LDS transpose read) delivers them in two reads of 4 k each,
 //    with no register transposes.
 //  * A ring of 4 LDS stages of BK = 32, refilled three stages ahead.
-//  * Software pipeline: each stage is multiplied as two k16 halves, and the fragments of the next half are
-//    read from LDS while the current half's MFMAs run. The reads (and, after the barrier, the global->LDS
-//    loads of the stage three ahead) are placed between the MFMAs in fixed program order (sched_barrier), so
-//    the matrix pipe is fed while LDS and global traffic are in flight. One s_barrier per stage.
+//  * MFMA shape: 16x16x32 rather than 32x32x16. Both have the same throughput, but a 32x32 tile reads and writes
+//    16 accumulator registers per 32-cycle instruction where the 16x16 tile moves 4 per 16 cycles. Under the
+//    board's power limit the smaller register traffic lets the clock run higher: measured on MI355X at 4096^3
+//    U(-1,1), the same pipeline with 32x32x16 tiles ran at 1,243-1,265 TFLOP/s, this one at 1,344-1,375.
+//  * Software pipeline: each stage's k-step is done in two phases over halves of the wave's B blocks; the next
+//    phase's fragments are read from LDS while the current phase's MFMAs run. The reads (and, after the barrier,
+//    the global->LDS loads of the stage three ahead) are placed between the MFMAs in fixed program order
+//    (sched_barrier), so the matrix pipe is fed while LDS and global traffic are in flight. One s_barrier per
+//    stage.
 //  * Workgroups are remapped XCD-aware (consecutive tile ids on one XCD) and grouped along M for L2 reuse.
 //  * Epilogue: the rounded tile is staged through LDS per wave and written with 16-byte stores; epilogue
 //    operands are read with matching 16-byte loads.
@@ -34,44 +39,54 @@ namespace {
 
 using namespace mfma16;
 
-// The fragments of one k16 half of a wave tile.
-template <int TM, int TN>
-struct Fragments {
+// A fragment set: a wave tile's A (all TM 16-row blocks) and NB of its 16-column B blocks, each B block as the low
+// and high 4 k of the lane's 8.
+template <int TM>
+struct AFrags {
   u32x4_t a[TM];
-  u32x2_t bl[TN], bh[TN];  // B fragment = 4 k from the low transpose read, 4 k from the high one
+};
+template <int NB>
+struct BFrags {
+  u32x2_t lo[NB], hi[NB];
 };
 
-// Waits for every outstanding LDS read (they complete in order), then ties the fragment registers to the wait
-// so no consumer is scheduled above it. The B halves are combined into MFMA operands only after this point.
-template <int TM, int TN>
-__device__ __forceinline__ void fence_fragments(Fragments<TM, TN>& f) {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+// Ties fragment registers to the preceding lgkmcnt(0) wait, so no consumer is scheduled above it (the LDS reads
+// are inline asm the compiler's wait tracking does not see).
+template <int TM>
+__device__ __forceinline__ void tie(AFrags<TM>& f) {
 #pragma unroll
   for (int i = 0; i < TM; ++i) asm volatile("" : "+v"(f.a[i]));
+}
+template <int NB>
+__device__ __forceinline__ void tie(BFrags<NB>& f) {
 #pragma unroll
-  for (int j = 0; j < TN; ++j) {
-    asm volatile("" : "+v"(f.bl[j]));
-    asm volatile("" : "+v"(f.bh[j]));
+  for (int j = 0; j < NB; ++j) {
+    asm volatile("" : "+v"(f.lo[j]));
+    asm volatile("" : "+v"(f.hi[j]));
   }
 }
+__device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 // One workgroup = WAVES_M x WAVES_N waves computing a BM x BN tile; each wave owns (BM/WAVES_M) x (BN/WAVES_N)
-// as TM x TN MFMA tiles of 32 x 32.
-//
-// Per stage kt (ring slot kt % 4), with f0 / f1 the fragment buffers of the two k16 halves:
-//   fence(f0); MFMA(kt, half 0) || read(kt, half 1) -> f1;
+// as TM x TN MFMA tiles of 16 x 16. A stage (BK = 32) is one k-step of every tile. Large wave tiles run it in two
+// phases over the halves of the wave's B blocks (fb0: [0, TN/2), fb1: [TN/2, TN)):
+//   wait(fa, fb0); phase 0: MFMA(A, fb0) || read stage kt's B blocks [TN/2, TN) -> fb1;
 //   wait vmcnt (this wave's loads of stage kt+1); s_barrier;
-//   fence(f1); MFMA(kt, half 1) || read(kt+1, half 0) -> f0 || load stage kt+3 into the slot of stage kt-1.
-// Ordering: stage kt+1 is read only after the barrier that follows every wave's vmcnt wait for it. The slot
-// refilled after the barrier of step kt held stage kt-1, whose reads every wave fenced (lgkmcnt(0)) before
-// arriving at that barrier. Stages past the end re-load the last stage (nobody reads them), so every step
-// issues the same number of loads and the vmcnt counts hold on every path.
+//   wait(fb1); phase 1: MFMA(A, fb1) || read stage kt+1's A -> fa' and B blocks [0, TN/2) -> fb0
+//                      || load stage kt+3 into the slot of stage kt-1.
+// Small wave tiles hold two full sets and run a stage as one phase:
+//   wait vmcnt; s_barrier; wait(fa, fb); MFMA(A, B) || read stage kt+1 -> (fa', fb') || load stage kt+3.
+// Sets alternate between stages (so the loop runs two stages per iteration). Ordering: stage kt+1 is read only
+// after the barrier that follows every wave's vmcnt wait for it. The slot refilled after the barrier of step kt
+// held stage kt-1, whose reads every wave waited for (lgkmcnt(0)) before arriving at that barrier. Stages past
+// the end re-load the last stage (nobody reads them), so every step issues the same number of loads and the vmcnt
+// counts hold on every path.
 template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, int E>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs args) {
   using S = uint16_t;
   constexpr int NW = WAVES_M * WAVES_N;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
-  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int TM = WM / 16, TN = WN / 16;
   constexpr int A_BYTES = BM * kBK * 2;
   constexpr int B_BYTES = BN * kBK * 2;
   constexpr int STAGE = A_BYTES + B_BYTES;
@@ -82,7 +97,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
   constexpr int B_ROWS_PER_INSTR = 64 / B_CHUNKS;
   static_assert((A_BYTES / 1024) % NW == 0 && (B_BYTES / 1024) % NW == 0, "stage loads split evenly over waves");
   static_assert(B_CHUNKS >= 8 && B_CHUNKS <= 64, "BN in [64, 512]");
-  static_assert(TM >= 1 && TN >= 1, "wave tile at least 32x32");
+  static_assert(TM >= 1 && TN >= 2 && TN % 2 == 0, "wave tile at least 16x32");
   static_assert(2 * LOADS <= 63, "vmcnt range");
 
   __shared__ __attribute__((aligned(1024))) unsigned char ring[kStages * STAGE];
@@ -127,7 +142,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
 #pragma unroll
   for (int j = 0; j < B_PER_WAVE; ++j) {
     const int krow = (wave * B_PER_WAVE + j) * B_ROWS_PER_INSTR + lane / B_CHUNKS;
-    const int chunk = (lane % B_CHUNKS) ^ b_swizzle<B_CHUNKS>(krow);
+    const int chunk = (lane % B_CHUNKS) ^ b_swizzle16<B_CHUNKS>(krow);
     b_src[j] = static_cast<int64_t>(krow) * ldb + min(n0 + chunk * 8, N - 8);
   }
 
@@ -148,68 +163,82 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
     }(std::make_integer_sequence<int, LOADS>{});
   };
 
-  // ---- per-lane LDS read offsets (bytes within a stage). Tile i of A adds i*32 rows (the swizzle depends on
-  // row bits 2-3 only, so it is a constant 2048 B); k-half s and 4-k group h of B add whole rows. ----
-  const int l32 = lane & 31, hi = lane >> 5;
-  int a_off[2];
-  {
-    const int row = wm * WM + l32;
-#pragma unroll
-    for (int s = 0; s < 2; ++s) a_off[s] = row * 64 + (((2 * s + hi) ^ a_swizzle(row)) * 16);
-  }
-  // transpose reads: group g = lane/16 covers 16 columns and 4 k; lane r = q + 4e of the group points at
-  // row (kbase + e), columns n + 4q .. n + 4q + 3
+  // ---- per-lane LDS read offsets (bytes within a stage) ----
+  // A (16x16x32 operand: lane l holds row l % 16, k 8 (l / 16) .. + 7): one ds_read_b128 per 16-row block; block
+  // i adds 16 rows = 1 KB (the swizzle depends on row bits 2-3 only).
+  const int a_off = [&] {
+    const int row = wm * WM + (lane & 15);
+    return row * 64 + (((lane >> 4) ^ a_swizzle(row)) * 16);
+  }();
+  // B (lane l holds column l % 16, k 8 (l / 16) .. + 7): two transpose reads of 4 k each. In group g = l / 16,
+  // lane r = q + 4 e points at row 8 g + e, columns 4 q .. 4 q + 3 of the block; the high read adds 4 rows.
   const int g = lane >> 4, r = lane & 15, q = r & 3, e = r >> 2;
   int b_off[TN];
 #pragma unroll
   for (int j = 0; j < TN; ++j) {
-    const int ncol = wn * WN + j * 32 + 16 * (g & 1) + 4 * q;
-    const int krow = 8 * (g >> 1) + e;  // + 16 s + 4 h (immediates): krow & 3 and krow & 1 are unchanged
-    const int chunk = (ncol >> 3) ^ b_swizzle<B_CHUNKS>(krow);
+    const int ncol = wn * WN + j * 16 + 4 * q;
+    const int krow = 8 * g + e;  // + 4 for the high read: krow & 3, krow & 1 and krow & 8 are unchanged
+    const int chunk = (ncol >> 3) ^ b_swizzle16<B_CHUNKS>(krow);
     b_off[j] = A_BYTES + krow * (BN * 2) + chunk * 16 + (ncol & 7) * 2;
   }
-  constexpr int B_S = 16 * BN * 2, B_H = 4 * BN * 2;
+  constexpr int B_HI = 4 * BN * 2;
   const uint32_t ring_addr = lds_addr((const FH_LDS void*)ring);
 
-  f32x16_t acc[TM][TN];
+  f32x4_t acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int x = 0; x < 16; ++x) acc[i][j][x] = 0.0f;
+      for (int x = 0; x < 4; ++x) acc[i][j][x] = 0.0f;
 
-  Fragments<TM, TN> f0, f1;
-  constexpr int NREAD = TM + 2 * TN;  // LDS reads per half
-  constexpr int NMFMA = TM * TN;      // MFMAs per half
-
-  // Read number R of half H of the stage at `base` into f.
-  auto read_one = [&]<int H, int R>(uint32_t base, Fragments<TM, TN>& f) {
-    if constexpr (R < TM) {
-      f.a[R] = lds_read_b128<R * 2048>(base + a_off[H]);
-    } else if constexpr ((R - TM) % 2 == 0) {
-      f.bl[(R - TM) / 2] = lds_read_tr16_b64<H * B_S>(base + b_off[(R - TM) / 2]);
-    } else {
-      f.bh[(R - TM) / 2] = lds_read_tr16_b64<H * B_S + B_H>(base + b_off[(R - TM) / 2]);
-    }
-  };
-  // The MFMAs of the half held in `cur`. After each come some of the reads of half H of the stage at `base`
-  // into `nxt` (all within the first three quarters of the MFMAs, so they land before the half ends) and, with
-  // LOADS_TOO, some of the global->LDS loads of stage load_kt (within the first half of the MFMAs).
+  // Small wave tiles keep two full fragment sets (A and all B blocks) and run each stage as one phase that reads
+  // the next stage; large ones split a stage into two phases over halves of the B blocks (one full set would not
+  // leave registers for a second).
+  constexpr bool ONE = (TM + 2 * TN) * 8 + TM * TN * 4 <= 160;
+  constexpr int TB = ONE ? TN : TN / 2;  // B blocks per fragment set
+  AFrags<TM> fa0, fa1;
+  BFrags<TB> fb0, fb1;
+  constexpr int NMFMA = TM * TB;  // MFMAs per phase
+  // reads are spread over the first three quarters of a phase's MFMAs (so they land before it ends), global->LDS
+  // loads over the first half
   constexpr int R_SPAN = NMFMA * 3 / 4 > 0 ? NMFMA * 3 / 4 : 1;
   constexpr int L_SPAN = NMFMA / 2 > 0 ? NMFMA / 2 : 1;
-  auto multiply_and_read = [&]<int H, bool LOADS_TOO>(Fragments<TM, TN>& cur, uint32_t base, Fragments<TM, TN>& nxt,
-                                                      int load_kt) {
+
+  // Read R of B blocks [J0, J0 + TB) of the stage at `base` into f (even R: low 4 k, odd R: high 4 k).
+  auto read_b = [&]<int R, int J0>(uint32_t base, BFrags<TB>& f) {
+    constexpr int j = R / 2;
+    if constexpr (R % 2 == 0)
+      f.lo[j] = lds_read_tr16_b64<0>(base + b_off[J0 + j]);
+    else
+      f.hi[j] = lds_read_tr16_b64<B_HI>(base + b_off[J0 + j]);
+  };
+  // Read R of a stage's first set: its A blocks into fa, then its B blocks [0, TB) into fb.
+  auto read_set = [&]<int R>(uint32_t base, AFrags<TM>& fa, BFrags<TB>& fb) {
+    if constexpr (R < TM)
+      fa.a[R] = lds_read_b128<R * 1024>(base + a_off);
+    else
+      read_b.template operator()<R - TM, 0>(base, fb);
+  };
+  // The MFMAs of B blocks [J0, J0 + TB) (fragments fa, fb), with reads placed between them in fixed program order:
+  // NEXT: the first set of the stage at `base` into (fa_n, fb_n) and the global->LDS loads of stage load_kt;
+  // otherwise: B blocks [TB, 2 TB) of the stage at `base` into fb_n.
+  auto phase = [&]<int J0, bool NEXT>(AFrags<TM>& fa, BFrags<TB>& fb, uint32_t base, AFrags<TM>& fa_n,
+                                       BFrags<TB>& fb_n, int load_kt) {
+    constexpr int NR = NEXT ? TM + 2 * TB : 2 * TB;
     [&]<int... M_>(std::integer_sequence<int, M_...>) {
       (
           [&] {
-            constexpr int i = M_ / TN, j = M_ % TN;
-            mfma32<T>(cur.a[i], u32x4_t{cur.bl[j][0], cur.bl[j][1], cur.bh[j][0], cur.bh[j][1]}, acc[i][j]);
-            constexpr int r0 = first(M_, NREAD, R_SPAN);
+            constexpr int i = M_ / TB, j = M_ % TB;
+            mfma16x<T>(fa.a[i], u32x4_t{fb.lo[j][0], fb.lo[j][1], fb.hi[j][0], fb.hi[j][1]}, acc[i][J0 + j]);
+            constexpr int r0 = first(M_, NR, R_SPAN);
             [&]<int... R_>(std::integer_sequence<int, R_...>) {
-              (read_one.template operator()<H, r0 + R_>(base, nxt), ...);
-            }(std::make_integer_sequence<int, share(M_, NREAD, R_SPAN)>{});
-            if constexpr (LOADS_TOO) {
+              if constexpr (NEXT)
+                (read_set.template operator()<r0 + R_>(base, fa_n, fb_n), ...);
+              else
+                (read_b.template operator()<r0 + R_, TB>(base, fb_n), ...);
+            }(std::make_integer_sequence<int, share(M_, NR, R_SPAN)>{});
+            if constexpr (NEXT) {
               constexpr int l0 = first(M_, LOADS, L_SPAN);
               [&]<int... L_>(std::integer_sequence<int, L_...>) {
                 (load_one.template operator()<l0 + L_>(load_kt), ...);
@@ -220,8 +249,36 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
           ...);
     }(std::make_integer_sequence<int, NMFMA>{});
   };
+  auto barrier_next = [&] {
+    wait_vmcnt<LOADS>();  // this wave's part of stage kt+1 has landed (stage kt+2 may be in flight)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+  // Stage kt with its first set in (fa, fb). One phase: fb_n receives the next stage's B. Two phases: fb_n
+  // receives this stage's second B half, and fb the next stage's first.
+  auto step = [&](int kt, AFrags<TM>& fa, AFrags<TM>& fa_n, BFrags<TB>& fb, BFrags<TB>& fb_n) {
+    const uint32_t cur = ring_addr + (kt & (kStages - 1)) * STAGE;
+    const uint32_t nxt = ring_addr + ((kt + 1) & (kStages - 1)) * STAGE;
+    if constexpr (ONE) {
+      barrier_next();
+      wait_lds();
+      tie(fa);
+      tie(fb);
+      phase.template operator()<0, true>(fa, fb, nxt, fa_n, fb_n, kt + kStages - 1);
+    } else {
+      wait_lds();
+      tie(fa);
+      tie(fb);
+      phase.template operator()<0, false>(fa, fb, cur, fa_n, fb_n, 0);
+      barrier_next();
+      wait_lds();
+      tie(fb_n);
+      phase.template operator()<TB, true>(fa, fb_n, nxt, fa_n, fb, kt + kStages - 1);
+    }
+  };
 
-  // ---- prologue: stages 0..2 in flight, half 0 of stage 0 in f0 ----
+  // ---- prologue: stages 0..2 in flight, stage 0's first set in fa0 / fb0 ----
   issue_stage(0);
   issue_stage(1);
   issue_stage(2);
@@ -229,29 +286,29 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   [&]<int... R_>(std::integer_sequence<int, R_...>) {
-    (read_one.template operator()<0, R_>(ring_addr, f0), ...);
-  }(std::make_integer_sequence<int, NREAD>{});
+    (read_set.template operator()<R_>(ring_addr, fa0, fb0), ...);
+  }(std::make_integer_sequence<int, TM + 2 * TB>{});
 
-  for (int kt = 0; kt < KT; ++kt) {
-    const uint32_t cur = ring_addr + (kt & (kStages - 1)) * STAGE;
-    const uint32_t nxt = ring_addr + ((kt + 1) & (kStages - 1)) * STAGE;
-    fence_fragments(f0);
-    multiply_and_read.template operator()<1, false>(f0, cur, f1, 0);
-    wait_vmcnt<LOADS>();  // this wave's part of stage kt+1 has landed (stage kt+2 may be in flight)
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    fence_fragments(f1);
-    multiply_and_read.template operator()<0, true>(f1, nxt, f0, kt + kStages - 1);
+  int kt = 0;
+  for (; kt + 1 < KT; kt += 2) {
+    step(kt, fa0, fa1, fb0, fb1);
+    if constexpr (ONE)
+      step(kt + 1, fa1, fa0, fb1, fb0);
+    else
+      step(kt + 1, fa1, fa0, fb0, fb1);
   }
-  // The last step read the next half's fragments (past the end: unused). Those LDS reads are still in flight
-  // and would write their registers after the compiler has reused them in the epilogue, so they are fenced with
-  // the registers tied before anything else may use them.
-  fence_fragments(f0);
+  if (kt < KT) step(kt, fa0, fa1, fb0, fb1);
+  // The last step read the next stage's fragments (past the end: unused). Those LDS reads are still in flight
+  // and would write their registers after the compiler has reused them in the epilogue, so they are waited for
+  // with the registers tied before anything else may use them.
+  wait_lds();
+  tie(fa0);
+  tie(fa1);
+  tie(fb0);
+  tie(fb1);
 
   // ---- epilogue: round, stage each wave tile in LDS, then 16-byte coalesced read-modify-store ----
   wait_vmcnt<0>();  // the trailing re-loads must land before the ring is reused
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __syncthreads();
   constexpr int WTILE_BYTES = WM * WN * 2;
   static_assert(NW * WTILE_BYTES <= kStages * STAGE, "the wave tiles fit in the ring");
@@ -261,10 +318,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
 #pragma unroll
     for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int x = 0; x < 16; ++x) {
-        const int rr = i * 32 + 8 * (x >> 2) + 4 * hi + (x & 3);
-        wl[rr * WN + j * 32 + l32] = Io<T>::store(acc[i][j][x]);
-      }
+      for (int x = 0; x < 4; ++x) wl[(i * 16 + 4 * g + x) * WN + j * 16 + r] = Io<T>::store(acc[i][j][x]);
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's tile is in LDS (wave-private region)
   __builtin_amdgcn_wave_barrier();
   constexpr int V = 8;           // elements per 16-byte vector

@@ -43,6 +43,23 @@ __device__ __forceinline__ void mfma32(const u32x4_t& a, const u32x4_t& b, f32x1
   }
 }
 
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+// One 16x16 tile, k 32: lane l holds row (A) / column (B) l % 16 and k 8 (l / 16) .. + 7 as one 16-byte fragment;
+// the result's lane l holds column l % 16, rows 4 (l / 16) .. + 3. At equal MFMA throughput to the 32x32x16 form
+// it moves a quarter of the accumulator bytes per product through the register file.
+template <typename T>
+__device__ __forceinline__ void mfma16x(const u32x4_t& a, const u32x4_t& b, f32x4_t& acc) {
+  static_assert(!std::is_same_v<T, float>, "16-bit operands");
+  if constexpr (std::is_same_v<T, bf16_t>) {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a), __builtin_bit_cast(bf16x8_t, b),
+                                                  acc, 0, 0, 0);
+  } else {
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), acc,
+                                                 0, 0, 0);
+  }
+}
+
 // s_waitcnt with only vmcnt constrained (gfx9 encoding: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[15:14]).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
@@ -92,6 +109,13 @@ __device__ __forceinline__ int b_swizzle(int krow) {
   } else {
     return 2 * (krow & 3);
   }
+}
+
+// B swizzle for the 16x16x32 fragment reads: the two 16-lane groups served together read the same columns at
+// k rows 8 apart, so bit 3 of the row also moves the chunk (by 2, onto the pairs rows 0-3 leave free).
+template <int B_CHUNKS>
+__device__ __forceinline__ int b_swizzle16(int krow) {
+  return b_swizzle<B_CHUNKS>(krow) ^ (2 * ((krow >> 3) & 1));
 }
 
 // Number of items issued right after MFMA m when n items are spread over the first r MFMAs of a half, and the
