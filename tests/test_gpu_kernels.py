@@ -176,6 +176,24 @@ def test_gemm_epilogue_add_relu(hip, dtype):
     assert_close(got, want, dtype, what="gemm epilogue")
 
 
+@pytest.mark.parametrize("n", [256, 2048, 4096])  # 64x64, 128x128 and 256x256 tiles
+def test_gemm_add_gelu_every_bf16_input(hip, n):
+    # A.B = 0, so the add;gelu epilogue's gelu input is the operand itself, and the operand holds every bf16 pattern
+    # (both zeros, denormals, the table band's edges, infinities, NaN): the bf16 epilogue's gelu (a table over the
+    # band 2^-9 <= |x| < 8, closed forms outside it) equals the oracle's fp32 formula bit for bit, NaN as NaN
+    m, k = n, 32
+    say(f"gemm add;gelu over every bf16 pattern, {m}x{n}")
+    bias = np.resize(np.arange(65536, dtype=np.uint16), (m, n))
+    zeros_a = np.zeros((m, k), np.uint16)
+    zeros_b = np.zeros((k, n), np.uint16)
+    got = run_gemm(hip, BF16, zeros_a, zeros_b, [(hip.EW_ADD, bias), (hip.EW_GELU, None)])
+    want = orc.ew_program(BF16, [1, 5], [2, 1], [np.zeros((m, n), np.uint16), bias])
+    nan_got = (got & 0x7FFF) > 0x7F80
+    nan_want = (want & 0x7FFF) > 0x7F80
+    assert np.array_equal(nan_got, nan_want), "NaN positions differ"
+    assert_bitwise(np.where(nan_got, 0, got), np.where(nan_want, 0, want), "add;gelu over every bf16 input")
+
+
 def run_gemm_ex(hip, dtype, a, b, epilogue_segments=None, flags=1):
     """fh_gemm_ex (flags 1 = FH_GEMM_ANY_ORDER)."""
     m, k = a.shape
