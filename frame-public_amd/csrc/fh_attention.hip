@@ -15,8 +15,9 @@
 //
 // attention_kernel: one wave owns 32 queries and all seq keys; a workgroup is W waves (4, or 2 when seq is not a
 // multiple of 128). attention_split_kernel (bf16, seq % 128 == 0) splits each query block's keys over two waves.
-// The work is bound by its VALU instruction stream (about 9 VALU instructions and two quarter-rate
-// exponentials per score, against two MFMA k-steps per 32 x 32 tile), so the per-score code is kept short.
+// The unsplit kernel is bound by its VALU instruction stream (about 9 VALU instructions and two quarter-rate
+// exponentials per score, against two MFMA k-steps per 32 x 32 tile), so the per-score code is kept short; the
+// split kernel evaluates one exponential per score.
 //  1. Scores transposed, Sᵀ = K·Qᵀ on v_mfma_f32_32x32x16, per 64-key block: K blocks go to LDS
 //     (global_load_lds_dwordx4, 16-byte chunks swizzled by row), all requested at the start; the Q fragments
 //     stay in registers. Each lane's accumulator then holds one query and 16 keys of a 32-key tile; they are
@@ -285,15 +286,16 @@ __global__ __launch_bounds__(W * 64, 2) void attention_kernel(const uint16_t* __
 
 // Key-split form for seq % 128 == 0. A workgroup is 8 waves over 128 queries: waves w and w + 4 own the same 32
 // queries, w < 4 the first half of the keys and w >= 4 the second. Each wave keeps the packed scores of seq / 2
-// keys (64 registers at seq 512 instead of 128), so four waves fit per SIMD (two workgroups per CU): twice the
-// waves of attention_kernel over the same work, which is bound by the latency of its instruction stream. The
-// blocks of K (then V) are loaded by all 8 waves, the halves' blocks in pairs (i, NB/2 + i) so both halves start
-// together. Per query the halves combine through LDS: the row maximum (exact either way), the sum of the
-// exponentials s = s_first + s_second, and the fp32 products P·V: half h writes the output's d tile h (32 columns)
-// as round((O_first + O_second) * (1/s)), taking the other half's partial from LDS. Everything else (roundings,
-// exponentials, key order inside a half) is attention_kernel's.
+// keys (64 registers at seq 512) and, after the row maximum is known, their fp32 exponentials (128 registers), so
+// every exponential is evaluated once: the sum pass stores them and the P pass only scales and rounds them (at C5's
+// shape 21.1 us against 23.0 us when pass 3 evaluated them again with four waves per SIMD; the registers leave two
+// waves per SIMD, one workgroup per CU). The blocks of K (then V) are loaded by all 8 waves, the halves' blocks in
+// pairs (i, NB/2 + i) so both halves start together. Per query the halves combine through LDS: the row maximum
+// (exact either way), the sum of the exponentials s = s_first + s_second, and the fp32 products P·V: half h
+// writes the output's d tile h (32 columns) as round(O_first + O_second), taking the other half's partial from
+// LDS. Everything else (roundings, exponentials, key order inside a half) is attention_kernel's.
 template <typename T, int NB, bool POW2>
-__global__ __launch_bounds__(512, 2) void attention_split_kernel(const uint16_t* __restrict__ q,
+__global__ __launch_bounds__(512, 1) void attention_split_kernel(const uint16_t* __restrict__ q,
                                                                  const uint16_t* __restrict__ k,
                                                                  const uint16_t* __restrict__ v,
                                                                  uint16_t* __restrict__ out, int heads, float scale) {
@@ -368,8 +370,7 @@ __global__ __launch_bounds__(512, 2) void attention_split_kernel(const uint16_t*
             load_block(v, i - 1, true);
             load_block(v, H + i - 1, true);
           }
-          // one 32-key tile at a time: 16 fragment and 16 accumulator registers (the scores of the later blocks are
-          // still to come, but 4 waves per SIMD leave 128 registers per lane)
+          // one 32-key tile at a time: 16 fragment and 16 accumulator registers
           auto tile = [&]<int t>() {
             u32x4_t kf[4];
 #pragma unroll
@@ -430,16 +431,18 @@ __global__ __launch_bounds__(512, 2) void attention_split_kernel(const uint16_t*
     const int krow = 4 * (g >> 1) + e;
     v_off[dt] = half_addr + krow * 128 + v_chunk(krow, n0 >> 3) * 16 + (n0 & 7) * 2;
   }
-  // ---- 2b. the sum of the exponentials over both halves, so that pass 3 stores round(e / s) as the reference's
-  // softmax does (every exponential is evaluated here and again in pass 3) ----
+  // ---- 2b. the exponentials and their sum over both halves, so that pass 3 stores round(e / s) as the reference's
+  // softmax does ----
   float esum = 0.0f;
+  float ev[NTH][16];  // the exponentials, kept in fp32 for pass 3
 #pragma unroll
   for (int t = 0; t < NTH; ++t)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const uint32_t w = s2[t][j];
-      esum += __builtin_amdgcn_exp2f(__builtin_fmaf(lo16<T>(w), c, -ml)) +
-              __builtin_amdgcn_exp2f(__builtin_fmaf(hi16<T>(w), c, -ml));
+      ev[t][2 * j] = __builtin_amdgcn_exp2f(__builtin_fmaf(lo16<T>(w), c, -ml));
+      ev[t][2 * j + 1] = __builtin_amdgcn_exp2f(__builtin_fmaf(hi16<T>(w), c, -ml));
+      esum += ev[t][2 * j] + ev[t][2 * j + 1];
     }
   xsum[wave][lane] = esum + __shfl_xor(esum, 32);
   wait_vmcnt<2>();  // this wave's V pairs 0 .. H-2
@@ -477,13 +480,8 @@ __global__ __launch_bounds__(512, 2) void attention_split_kernel(const uint16_t*
 #pragma unroll
             for (int hf = 0; hf < 2; ++hf)
 #pragma unroll
-              for (int j = 0; j < 4; ++j) {
-                uint32_t w = s2[t][4 * hf + j];
-                asm volatile("" : "+v"(w));
-                const float e0 = __builtin_amdgcn_exp2f(__builtin_fmaf(lo16<T>(w), c, -ml));
-                const float e1 = __builtin_amdgcn_exp2f(__builtin_fmaf(hi16<T>(w), c, -ml));
-                pf[hf][j] = pack2<T>(e0 * r, e1 * r);  // P = round(e / s)
-              }
+              for (int j = 0; j < 4; ++j)
+                pf[hf][j] = pack2<T>(ev[t][8 * hf + 2 * j] * r, ev[t][8 * hf + 2 * j + 1] * r);  // P = round(e / s)
             auto multiply = [&](u32x2_t (&f)[2][2], f32x16_t& acc) {
 #pragma unroll
               for (int hf = 0; hf < 2; ++hf) {
