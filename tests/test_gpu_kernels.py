@@ -176,6 +176,30 @@ def test_gemm_epilogue_add_relu(hip, dtype):
     assert_close(got, want, dtype, what="gemm epilogue")
 
 
+# One round of 128x128 workgroups (256 tiles, a CU each) takes the instance that loads the epilogue operands into LDS
+# at the start (C5's O-projection and FFN-down with bias and residual, add only, ragged edges): the same program on
+# operands read from LDS instead of HBM, checked against the oracle on sampled outputs.
+@pytest.mark.parametrize("m,n,k,program", [
+    (4096, 1024, 1024, "add;add"),   # C5 O-projection + bias + residual
+    (4096, 1024, 4096, "add;add"),   # C5 FFN-down + bias + residual
+    (2048, 2048, 512, "add"),
+    (2000, 2000, 96, "add;add"),     # 16 x 16 tiles, the last row and column of tiles ragged
+])
+def test_gemm_single_round_epilogue_operands(hip, m, n, k, program):
+    say(f"gemm single-round epilogue {program} {m}x{n}x{k}")
+    a = synth.tensor(61, (m, k), BF16, "normal")
+    b = synth.tensor(62, (k, n), BF16, "normal", 0.05)
+    ins = [synth.tensor(63, (m, n), BF16, "normal"), synth.tensor(64, (m, n), BF16, "normal")]
+    nops = 2 if program == "add;add" else 1
+    got = run_gemm(hip, BF16, a, b, [(hip.EW_ADD, ins[i]) for i in range(nops)])
+    rng = np.random.default_rng(11)
+    rows = np.concatenate([rng.integers(0, m, 3000), np.full(64, m - 1)])
+    cols = np.concatenate([rng.integers(0, n, 3000), rng.integers(0, n, 64)])
+    mm = orc.matmul_sample(BF16, a, b, rows, cols)
+    want = orc.ew_program(BF16, [1] * nops, [2] * nops, [mm] + [x[rows, cols] for x in ins[:nops]])
+    assert_close(got[rows, cols], want, BF16, what=f"single-round epilogue {program}")
+
+
 @pytest.mark.parametrize("n", [256, 2048, 4096])  # 64x64, 128x128 and 256x256 tiles
 def test_gemm_add_gelu_every_bf16_input(hip, n):
     # A.B = 0, so the add;gelu epilogue's gelu input is the operand itself, and the operand holds every bf16 pattern
