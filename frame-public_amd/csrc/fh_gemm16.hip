@@ -116,7 +116,7 @@ __device__ __forceinline__ void wait_lds() { asm volatile("s_waitcnt lgkmcnt(0)"
 // held stage kt-1, whose reads every wave waited for (lgkmcnt(0)) before arriving at that barrier. Stages past
 // the end re-load the last stage (nobody reads them), so every step issues the same number of loads and the vmcnt
 // counts hold on every path.
-template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, int E, bool PREF>
+template <typename T, int BM, int BN, int WAVES_M, int WAVES_N, int E>
 __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs args) {
   using S = uint16_t;
   constexpr int NW = WAVES_M * WAVES_N;
@@ -133,23 +133,9 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
   static_assert((A_BYTES / 1024) % NW == 0 && (B_BYTES / 1024) % NW == 0, "stage loads split evenly over waves");
   static_assert(B_CHUNKS >= 8 && B_CHUNKS <= 64, "BN in [64, 512]");
   static_assert(TM >= 1 && TN >= 2 && TN % 2 == 0, "wave tile at least 16x32");
-  // epilogue access shape: each wave's rounded tile is read back as 16-byte vectors, LPR lanes per row, RPI rows
-  // per wave-wide access, ITERS accesses
-  constexpr int V = 8;           // elements per 16-byte vector
-  constexpr int LPR = WN / V;    // lanes per staged row
-  constexpr int RPI = 64 / LPR;  // rows per wave-wide access
-  constexpr int ITERS = WM / RPI;
-  static_assert(64 % LPR == 0 && WM % RPI == 0, "epilogue access shape");
-  constexpr int NOP = epi_operands<E>();
-  // PREF (one round of workgroups): the epilogue operands are loaded into LDS at the start, one 1 KB global->LDS
-  // instruction per operand and access, laid out as the epilogue reads them, so their HBM reads overlap the main
-  // loop instead of following it
-  static_assert(!PREF || NOP > 0, "prefetch needs operands");
-  constexpr int PLOADS = PREF ? NOP * ITERS : 0;
-  static_assert(2 * LOADS + PLOADS <= 63, "vmcnt range");
+  static_assert(2 * LOADS <= 63, "vmcnt range");
 
   __shared__ __attribute__((aligned(1024))) unsigned char ring[kStages * STAGE];
-  __shared__ __attribute__((aligned(1024))) unsigned char opnd_lds[PREF ? PLOADS * NW * 1024 : 16];
   // add;gelu on bf16: the gelu table, loaded at the start with the first stages (its loads are older than every
   // stage's, so the prologue's vmcnt wait covers them)
   constexpr bool GELU_TAB = E == kEpiAddGelu && std::is_same_v<T, bf16_t>;
@@ -302,13 +288,8 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
           ...);
     }(std::make_integer_sequence<int, NMFMA>{});
   };
-  auto barrier_next = [&](int kt) {
-    // this wave's part of stage kt+1 has landed (stage kt+2 may be in flight, and in steps 0 and 1 the operand
-    // prefetch, issued after stage 2)
-    if (PLOADS > 0 && kt < 2)
-      wait_vmcnt<LOADS + PLOADS>();
-    else
-      wait_vmcnt<LOADS>();
+  auto barrier_next = [&] {
+    wait_vmcnt<LOADS>();  // this wave's part of stage kt+1 has landed (stage kt+2 may be in flight)
     asm volatile("" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
@@ -319,7 +300,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
     const uint32_t cur = ring_addr + (kt & (kStages - 1)) * STAGE;
     const uint32_t nxt = ring_addr + ((kt + 1) & (kStages - 1)) * STAGE;
     if constexpr (ONE) {
-      barrier_next(kt);
+      barrier_next();
       wait_lds();
       tie(fa);
       tie(fb);
@@ -329,7 +310,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
       tie(fa);
       tie(fb);
       phase.template operator()<0, false>(fa, fb, cur, fa_n, fb_n, 0);
-      barrier_next(kt);
+      barrier_next();
       wait_lds();
       tie(fb_n);
       phase.template operator()<TB, true>(fa, fb_n, nxt, fa_n, fb, kt + kStages - 1);
@@ -344,19 +325,7 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
   issue_stage(0);
   issue_stage(1);
   issue_stage(2);
-  if constexpr (PREF) {
-    const int64_t col_p = min(n0 + wn * WN + (lane % LPR) * V, N - V);
-#pragma unroll
-    for (int sg = 0; sg < NOP; ++sg) {
-      const S* src = static_cast<const S*>(grouped ? args.group_ins[blockIdx.y][sg] : args.ep.ins[sg]);
-#pragma unroll
-      for (int it = 0; it < ITERS; ++it) {
-        const int64_t row = min(m0 + wm * WM + it * RPI + lane / LPR, M - 1);
-        global_to_lds16(src + row * ldc + col_p, (FH_LDS void*)(opnd_lds + ((sg * NW + wave) * ITERS + it) * 1024));
-      }
-    }
-  }
-  wait_vmcnt<2 * LOADS + PLOADS>();
+  wait_vmcnt<2 * LOADS>();
   asm volatile("" ::: "memory");
   __builtin_amdgcn_s_barrier();
   [&]<int... R_>(std::integer_sequence<int, R_...>) {
@@ -395,12 +364,18 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
       for (int x = 0; x < 4; ++x) wl[(i * 16 + 4 * g + x) * WN + j * 16 + r] = Io<T>::store(acc[i][j][x]);
   __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's tile is in LDS (wave-private region)
   __builtin_amdgcn_wave_barrier();
+  constexpr int V = 8;           // elements per 16-byte vector
+  constexpr int LPR = WN / V;    // lanes per staged row
+  constexpr int RPI = 64 / LPR;  // rows per wave-wide access
+  static_assert(64 % LPR == 0 && WM % RPI == 0, "epilogue access shape");
   const int c = (lane % LPR) * V;
   const int64_t col = n0 + wn * WN + c;
   EpilogueArgs ep = args.ep;
   if (grouped)
 #pragma unroll
     for (int sg = 0; sg < FH_MAX_SEGMENTS; ++sg) ep.ins[sg] = args.group_ins[blockIdx.y][sg];
+  constexpr int ITERS = WM / RPI;
+  constexpr int NOP = epi_operands<E>();
   if constexpr (NOP == 0) {
     for (int it = 0; it < ITERS; ++it) {
       const int rr = it * RPI + lane / LPR;
@@ -423,14 +398,8 @@ __global__ __launch_bounds__(WAVES_M* WAVES_N * 64) void gemm16_kernel(GemmArgs 
       uint4 in[BATCH][NOP];
 #pragma unroll
       for (int b = 0; b < BATCH; ++b) {
-        if constexpr (PREF) {
-#pragma unroll
-          for (int sg = 0; sg < NOP; ++sg)
-            in[b][sg] = *reinterpret_cast<const uint4*>(opnd_lds + ((sg * NW + wave) * ITERS + it0 + b) * 1024 + lane * 16);
-        } else {
-          const int64_t row = m0 + wm * WM + (it0 + b) * RPI + lane / LPR;
-          epi_load<E, T>(ep, (row < M ? row : M - 1) * ldc + col_c, in[b]);
-        }
+        const int64_t row = m0 + wm * WM + (it0 + b) * RPI + lane / LPR;
+        epi_load<E, T>(ep, (row < M ? row : M - 1) * ldc + col_c, in[b]);
       }
 #pragma unroll
       for (int b = 0; b < BATCH; ++b) {
@@ -456,19 +425,9 @@ fh_status launch(GemmArgs args, int64_t batch, hipStream_t stream) {
   args.tiles_m = static_cast<int32_t>((args.M + BM - 1) / BM);
   args.tiles_n = static_cast<int32_t>((args.N + BN - 1) / BN);
   dim3 grid(static_cast<uint32_t>(args.tiles_m) * static_cast<uint32_t>(args.tiles_n), static_cast<uint32_t>(batch));
-  // One round of 128x128 workgroups (every tile has a CU of its own): the prefetching instance, whose operand
-  // area takes the LDS a second workgroup on the CU would have used. (256x256 tiles leave no LDS for it.)
-  const bool one_round = static_cast<int64_t>(grid.x) * grid.y <= device_cu_count();
   auto go = [&]<int E>() {
-    if constexpr (epi_operands<E>() > 0 && BM == 128 && BN == 128) {
-      if (one_round) {
-        hipLaunchKernelGGL((gemm16_kernel<T, BM, BN, WAVES_M, WAVES_N, E, true>), grid, dim3(WAVES_M * WAVES_N * 64),
-                           0, stream, args);
-        return launch_status("gemm16_kernel launch");
-      }
-    }
-    hipLaunchKernelGGL((gemm16_kernel<T, BM, BN, WAVES_M, WAVES_N, E, false>), grid, dim3(WAVES_M * WAVES_N * 64), 0,
-                       stream, args);
+    hipLaunchKernelGGL((gemm16_kernel<T, BM, BN, WAVES_M, WAVES_N, E>), grid, dim3(WAVES_M * WAVES_N * 64), 0, stream,
+                       args);
     return launch_status("gemm16_kernel launch");
   };
   // bf16 (the configurations' type): the programs of C1-C5's GEMMs as kernels of their own; the rest (and f16)

@@ -176,9 +176,8 @@ def test_gemm_epilogue_add_relu(hip, dtype):
     assert_close(got, want, dtype, what="gemm epilogue")
 
 
-# One round of 128x128 workgroups (256 tiles, a CU each) takes the instance that loads the epilogue operands into LDS
-# at the start (C5's O-projection and FFN-down with bias and residual, add only, ragged edges): the same program on
-# operands read from LDS instead of HBM, checked against the oracle on sampled outputs.
+# C5's O-projection and FFN-down shapes with bias and residual (add;add), add only, and ragged edges, on 128x128
+# tiles (one round of 256 workgroups), checked against the oracle on sampled outputs.
 @pytest.mark.parametrize("m,n,k,program", [
     (4096, 1024, 1024, "add;add"),   # C5 O-projection + bias + residual
     (4096, 1024, 4096, "add;add"),   # C5 FFN-down + bias + residual
