@@ -289,7 +289,10 @@ __global__ __launch_bounds__(W * 64, 2) void attention_kernel(const uint16_t* __
 // keys (64 registers at seq 512) and, after the row maximum is known, their fp32 exponentials (128 registers), so
 // every exponential is evaluated once: the sum pass stores them and the P pass only scales and rounds them (at C5's
 // shape 21.1 us against 23.0 us when pass 3 evaluated them again with four waves per SIMD; the registers leave two
-// waves per SIMD, one workgroup per CU). The blocks of K (then V) are loaded by all 8 waves, the halves' blocks in
+// waves per SIMD, one workgroup per CU). With more tasks (128-query blocks) than CUs a workgroup runs two tasks
+// from two LDS buffers: the second task's Q fragments and K blocks are requested right after the first task's last
+// V blocks, so they arrive while the first task finishes (20.8 us against 21.2-21.4 us with the second task as a
+// second round of workgroups). The blocks of K (then V) are loaded by all 8 waves, the halves' blocks in
 // pairs (i, NB/2 + i) so both halves start together. Per query the halves combine through LDS: the row maximum
 // (exact either way), the sum of the exponentials s = s_first + s_second, and the fp32 products P·V: half h
 // writes the output's d tile h (32 columns) as round(O_first + O_second), taking the other half's partial from
@@ -298,7 +301,8 @@ template <typename T, int NB, bool POW2>
 __global__ __launch_bounds__(512, 1) void attention_split_kernel(const uint16_t* __restrict__ q,
                                                                  const uint16_t* __restrict__ k,
                                                                  const uint16_t* __restrict__ v,
-                                                                 uint16_t* __restrict__ out, int heads, float scale) {
+                                                                 uint16_t* __restrict__ out, int heads, float scale,
+                                                                 int tasks) {
   constexpr int SEQ = NB * 64;
   constexpr int H = NB / 2;        // 64-key blocks per half
   constexpr int NTH = 2 * H;       // 32-key tiles per half
@@ -306,228 +310,261 @@ __global__ __launch_bounds__(512, 1) void attention_split_kernel(const uint16_t*
   static_assert(NB % 2 == 0 && 2 * NB < 64, "whole block pairs; vmcnt range");
   // K / V blocks, then the halves' fp32 partial products: 8 waves x 64 lanes x 16 floats = 32 KB
   constexpr int KV_BYTES = NB * BLK > 8 * 64 * 16 * 4 ? NB * BLK : 8 * 64 * 16 * 4;
-  __shared__ __attribute__((aligned(1024))) unsigned char kv[KV_BYTES];
+  // two task buffers: the next task's K blocks land in one while the current task runs in the other
+  __shared__ __attribute__((aligned(1024))) unsigned char kvs[2][KV_BYTES];
   __shared__ float xmax[8][64], xsum[8][64];
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int half = wave >> 2;
   const int l32 = lane & 31, hi = lane >> 5;
-  // Workgroup -> (query block, head, batch), XCD-aware: consecutive workgroups go to the 8 XCDs in turn, so
-  // workgroup L runs on XCD L % 8; the (L / 8)-th workgroup of each XCD takes consecutive (head, batch) pairs with
-  // all their query blocks, and the 4 workgroups that read one pair's K and V share that XCD's L2.
-  const int nq = SEQ / 128, total = static_cast<int>(gridDim.x);
-  int idx = static_cast<int>(blockIdx.x);
-  if ((total & 7) == 0) idx = (idx & 7) * (total >> 3) + (idx >> 3);
-  const int qb = idx % nq, hb = idx / nq;
-  const int h = hb % heads, b = hb / heads;
-  const int q0 = qb * 128 + (wave & 3) * 32;
+  const int nq = SEQ / 128;
   const int64_t ld = static_cast<int64_t>(heads) * kDh;
-  const int64_t base = (static_cast<int64_t>(b) * SEQ) * ld + static_cast<int64_t>(h) * kDh;
-
-  u32x4_t qf[4];
+  // Task -> (query block, head, batch), XCD-aware: workgroup L runs on XCD L % 8 and takes tasks L and
+  // L + gridDim.x; the remap gives each XCD consecutive (head, batch) pairs with all their query blocks, so the
+  // 4 workgroups that read one pair's K and V share that XCD's L2 (tasks L and L + gridDim.x stay on L's XCD when
+  // gridDim.x is a multiple of 8).
+  auto geo = [&](int t, int64_t& base, int& q0) {
+    int idx = t;
+    if ((tasks & 7) == 0) idx = (idx & 7) * (tasks >> 3) + (idx >> 3);
+    const int qb = idx % nq, hb = idx / nq;
+    const int h = hb % heads, b = hb / heads;
+    q0 = qb * 128 + (wave & 3) * 32;
+    base = (static_cast<int64_t>(b) * SEQ) * ld + static_cast<int64_t>(h) * kDh;
+  };
+  auto load_q = [&](int64_t base, int q0, u32x4_t (&qf)[4]) {
 #pragma unroll
-  for (int s = 0; s < 4; ++s)
-    qf[s] = *reinterpret_cast<const u32x4_t*>(q + base + static_cast<int64_t>(q0 + l32) * ld + 16 * s + 8 * hi);
-  asm volatile("" ::: "memory");
-
+    for (int s = 0; s < 4; ++s)
+      qf[s] = *reinterpret_cast<const u32x4_t*>(q + base + static_cast<int64_t>(q0 + l32) * ld + 16 * s + 8 * hi);
+  };
   // one 1 KB instruction per wave and block: rows 8 wave .. 8 wave + 7
-  auto load_block = [&](const uint16_t* src, int blk, bool is_v) {
+  auto load_block_to = [&](unsigned char* buf, int64_t base, const uint16_t* src, int blk, bool is_v) {
     const int row = 8 * wave + (lane >> 3), pc = lane & 7;
     const int c = is_v ? v_chunk(row, pc) : k_chunk(row, pc);
     const uint16_t* g = src + base + static_cast<int64_t>(blk * 64 + row) * ld + c * 8;
-    __builtin_amdgcn_global_load_lds(g, (FH_LDS void*)(kv + blk * BLK + wave * 1024), 16, 0, 0);
+    __builtin_amdgcn_global_load_lds(g, (FH_LDS void*)(buf + blk * BLK + wave * 1024), 16, 0, 0);
+  };
+  auto issue_k = [&](unsigned char* buf, int64_t base) {
+#pragma unroll
+    for (int i = 0; i < H; ++i) {
+      load_block_to(buf, base, k, i, false);
+      load_block_to(buf, base, k, H + i, false);
+    }
   };
   auto barrier = [] {
     asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
   };
-  const uint32_t kv_addr = lds_addr((const FH_LDS void*)kv);
-  const uint32_t half_addr = kv_addr + half * H * BLK;  // this half's first block
+  // One task whose Q fragments and K blocks were requested before (their loads are the oldest outstanding ones).
+  // NEXT: request the next task's (4 + NB loads per wave) after this task's last V loads. PRIOR: the previous
+  // task's 4 output stores were issued after this task's K loads, so they are in flight during pass 1.
+  auto run = [&]<bool NEXT, bool PRIOR>(unsigned char* kv, int64_t base, int q0, u32x4_t (&qf)[4],
+                                        unsigned char* nbuf, int64_t nbase, int nq0, u32x4_t (&qfn)[4]) {
+    constexpr int NEXT_LOADS = NEXT ? 4 + NB : 0;
+    auto load_block = [&](const uint16_t* src, int blk, bool is_v) { load_block_to(kv, base, src, blk, is_v); };
+    const uint32_t kv_addr = lds_addr((const FH_LDS void*)kv);
+    const uint32_t half_addr = kv_addr + half * H * BLK;  // this half's first block
+    uint32_t k_off[4];
+  #pragma unroll
+    for (int s = 0; s < 4; ++s) k_off[s] = half_addr + l32 * 128 + k_chunk(l32, 2 * s + hi) * 16;
 
-#pragma unroll
-  for (int i = 0; i < H; ++i) {
-    load_block(k, i, false);
-    load_block(k, H + i, false);
-  }
-  uint32_t k_off[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) k_off[s] = half_addr + l32 * 128 + k_chunk(l32, 2 * s + hi) * 16;
-
-  // ---- 1. scores of this half's keys ----
-  uint32_t s2[NTH][8];
-  float mraw = -__builtin_inff();
-  [&]<int... B_>(std::integer_sequence<int, B_...>) {
-    (
-        [&] {
-          constexpr int i = B_;
-          // K pair i has landed when no more than the loads issued after it are in flight: K pairs i+1 .. H-1
-          // and V pairs 0 .. i-2
-          wait_vmcnt<2 * (H - 1 - i) + 2 * (i >= 2 ? i - 1 : 0)>();
-          barrier();
-          if constexpr (i >= 1) {  // every wave has read K pair i - 1
-            load_block(v, i - 1, true);
-            load_block(v, H + i - 1, true);
-          }
-          // one 32-key tile at a time: 16 fragment and 16 accumulator registers
-          auto tile = [&]<int t>() {
-            u32x4_t kf[4];
-#pragma unroll
-            for (int s = 0; s < 4; ++s) kf[s] = lds_read_b128<i * BLK + t * 4096>(k_off[s]);
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-#pragma unroll
-            for (int s = 0; s < 4; ++s) asm volatile("" : "+v"(kf[s]));
-            f32x16_t acc;
-#pragma unroll
-            for (int x = 0; x < 16; ++x) acc[x] = 0.0f;
-#pragma unroll
-            for (int s = 0; s < 4; ++s) mfma32<T>(kf[s], qf[s], acc);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              const uint32_t sr = pack2<T>(acc[2 * j], acc[2 * j + 1]);
-              if constexpr (POW2) {
-                float mx;
-                asm("v_max3_f32 %0, %1, %2, %3" : "=v"(mx) : "v"(mraw), "v"(acc[2 * j]), "v"(acc[2 * j + 1]));
-                mraw = mx;
-                s2[2 * i + t][j] = sr;
-              } else {
-                const float a0 = lo16<T>(sr) * scale, a1 = hi16<T>(sr) * scale;
-                mraw = fmaxf(mraw, fmaxf(a0, a1));
-                s2[2 * i + t][j] = pack2<T>(a0, a1);
-              }
-              asm volatile("" : "+v"(s2[2 * i + t][j]));
-            }
-          };
-          tile.template operator()<0>();
-          tile.template operator()<1>();
-        }(),
-        ...);
-  }(std::make_integer_sequence<int, H>{});
-
-  // ---- 2. row maximum over both halves ----
-  xmax[wave][lane] = fmaxf(mraw, __shfl_xor(mraw, 32));
-  barrier();  // also: every wave has read K pair H - 1
-  load_block(v, H - 1, true);
-  load_block(v, NB - 1, true);
-  const float mh0 = xmax[wave & 3][lane], mh1 = xmax[(wave & 3) + 4][lane];
-  constexpr float kLog2e = 1.44269504088896340736f;
-  const float mr = Io<T>::round(fmaxf(mh0, mh1));
-  const float m = POW2 ? mr * scale : mr;
-  const float ml = m * kLog2e;
-  const float c = POW2 ? scale * kLog2e : kLog2e;
-
-  // ---- 3. this half's share of Oᵀ = Vᵀ·Pᵀ ----
-  f32x16_t acc_o[2];
-#pragma unroll
-  for (int dt = 0; dt < 2; ++dt)
-#pragma unroll
-    for (int x = 0; x < 16; ++x) acc_o[dt][x] = 0.0f;
-  const int g = lane >> 4, rr = lane & 15, qd = rr & 3, e = rr >> 2;
-  uint32_t v_off[2];
-#pragma unroll
-  for (int dt = 0; dt < 2; ++dt) {
-    const int n0 = 32 * dt + 16 * (g & 1) + 4 * qd;
-    const int krow = 4 * (g >> 1) + e;
-    v_off[dt] = half_addr + krow * 128 + v_chunk(krow, n0 >> 3) * 16 + (n0 & 7) * 2;
-  }
-  // ---- 2b. the exponentials and their sum over both halves, so that pass 3 stores round(e / s) as the reference's
-  // softmax does ----
-  float esum = 0.0f;
-  float ev[NTH][16];  // the exponentials, kept in fp32 for pass 3
-#pragma unroll
-  for (int t = 0; t < NTH; ++t)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint32_t w = s2[t][j];
-      ev[t][2 * j] = __builtin_amdgcn_exp2f(__builtin_fmaf(lo16<T>(w), c, -ml));
-      ev[t][2 * j + 1] = __builtin_amdgcn_exp2f(__builtin_fmaf(hi16<T>(w), c, -ml));
-      esum += ev[t][2 * j] + ev[t][2 * j + 1];
-    }
-  xsum[wave][lane] = esum + __shfl_xor(esum, 32);
-  wait_vmcnt<2>();  // this wave's V pairs 0 .. H-2
-  barrier();
-  // e / s as e * (1 / s): the two differ by at most one fp32 rounding, which changes the stored 16-bit probability
-  // only when e / s lies within that rounding of a 16-bit rounding boundary
-  const float r = 1.0f / (xsum[wave & 3][lane] + xsum[(wave & 3) + 4][lane]);
-  [&]<int... B_>(std::integer_sequence<int, B_...>) {
-    (
-        [&] {
-          constexpr int i = B_;
-          if constexpr (i == H - 1) {
-            wait_vmcnt<0>();
+    // ---- 1. scores of this half's keys ----
+    uint32_t s2[NTH][8];
+    float mraw = -__builtin_inff();
+    [&]<int... B_>(std::integer_sequence<int, B_...>) {
+      (
+          [&] {
+            constexpr int i = B_;
+            // K pair i has landed when no more than the loads issued after it are in flight: K pairs i+1 .. H-1
+            // and V pairs 0 .. i-2
+            wait_vmcnt<2 * (H - 1 - i) + 2 * (i >= 2 ? i - 1 : 0) + (PRIOR ? 4 : 0)>();
             barrier();
-          }
-#pragma unroll
-          for (int tt = 0; tt < 2; ++tt) {
-            const int t = 2 * i + tt;
-            // V fragments of one d tile at a time (8 registers): d tile 0's are read before the exponentials,
-            // d tile 1's while d tile 0's products run
-            auto read_v = [&]<int dt>(u32x2_t (&vf)[2][2]) {
-              [&]<int... R_>(std::integer_sequence<int, R_...>) {
-                (
-                    [&] {
-                      constexpr int hf = R_ / 2, part = R_ % 2;
-                      constexpr int off = i * BLK + (16 * hf + 8 * part) * 128;
-                      vf[hf][part] = lds_read_tr16_b64<off>(v_off[dt] + tt * 32 * 128);
-                    }(),
-                    ...);
-              }(std::make_integer_sequence<int, 4>{});
-            };
-            u32x2_t vf[2][2];
-            read_v.template operator()<0>(vf);
-            u32x4_t pf[2];
-#pragma unroll
-            for (int hf = 0; hf < 2; ++hf)
-#pragma unroll
-              for (int j = 0; j < 4; ++j)
-                pf[hf][j] = pack2<T>(ev[t][8 * hf + 2 * j] * r, ev[t][8 * hf + 2 * j + 1] * r);  // P = round(e / s)
-            auto multiply = [&](u32x2_t (&f)[2][2], f32x16_t& acc) {
-#pragma unroll
-              for (int hf = 0; hf < 2; ++hf) {
-                asm volatile("" : "+v"(f[hf][0]), "+v"(f[hf][1]));
-                const u32x4_t a{f[hf][0][0], f[hf][0][1], f[hf][1][0], f[hf][1][1]};
-                mfma32<T>(a, pf[hf], acc);
+            if constexpr (i >= 1) {  // every wave has read K pair i - 1
+              load_block(v, i - 1, true);
+              load_block(v, H + i - 1, true);
+            }
+            // one 32-key tile at a time: 16 fragment and 16 accumulator registers
+            auto tile = [&]<int t>() {
+              u32x4_t kf[4];
+  #pragma unroll
+              for (int s = 0; s < 4; ++s) kf[s] = lds_read_b128<i * BLK + t * 4096>(k_off[s]);
+              asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  #pragma unroll
+              for (int s = 0; s < 4; ++s) asm volatile("" : "+v"(kf[s]));
+              f32x16_t acc;
+  #pragma unroll
+              for (int x = 0; x < 16; ++x) acc[x] = 0.0f;
+  #pragma unroll
+              for (int s = 0; s < 4; ++s) mfma32<T>(kf[s], qf[s], acc);
+  #pragma unroll
+              for (int j = 0; j < 8; ++j) {
+                const uint32_t sr = pack2<T>(acc[2 * j], acc[2 * j + 1]);
+                if constexpr (POW2) {
+                  float mx;
+                  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(mx) : "v"(mraw), "v"(acc[2 * j]), "v"(acc[2 * j + 1]));
+                  mraw = mx;
+                  s2[2 * i + t][j] = sr;
+                } else {
+                  const float a0 = lo16<T>(sr) * scale, a1 = hi16<T>(sr) * scale;
+                  mraw = fmaxf(mraw, fmaxf(a0, a1));
+                  s2[2 * i + t][j] = pack2<T>(a0, a1);
+                }
+                asm volatile("" : "+v"(s2[2 * i + t][j]));
               }
             };
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            multiply(vf, acc_o[0]);
-            read_v.template operator()<1>(vf);
-            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-            multiply(vf, acc_o[1]);
-          }
-        }(),
-        ...);
-  }(std::make_integer_sequence<int, H>{});
+            tile.template operator()<0>();
+            tile.template operator()<1>();
+          }(),
+          ...);
+    }(std::make_integer_sequence<int, H>{});
 
-  // ---- output: half h writes d tile h from its partial and its partner's (kv is free: every V read is done) ----
-  float* xo = reinterpret_cast<float*>(kv);
-  {
-    const int other = 1 - half;
-    float4* dst = reinterpret_cast<float4*>(xo + (wave * 64 + lane) * 16);
-    barrier();  // every wave's V reads are complete before kv is overwritten
-#pragma unroll
-    for (int x4 = 0; x4 < 4; ++x4)
-      dst[x4] = make_float4(acc_o[other][4 * x4], acc_o[other][4 * x4 + 1], acc_o[other][4 * x4 + 2], acc_o[other][4 * x4 + 3]);
-  }
-  barrier();
-  const float4* src = reinterpret_cast<const float4*>(xo + ((wave ^ 4) * 64 + lane) * 16);
-  f32x16_t o = half == 0 ? acc_o[0] : acc_o[1];
-#pragma unroll
-  for (int x4 = 0; x4 < 4; ++x4) {
-    const float4 p = src[x4];
-    o[4 * x4] += p.x;
-    o[4 * x4 + 1] += p.y;
-    o[4 * x4 + 2] += p.z;
-    o[4 * x4 + 3] += p.w;
-  }
-  uint16_t* orow = out + base + static_cast<int64_t>(q0 + l32) * ld + 32 * half;
-#pragma unroll
-  for (int gq = 0; gq < 4; ++gq) {
-    u32x2_t w;
-    w[0] = pack2<T>(o[4 * gq], o[4 * gq + 1]);
-    w[1] = pack2<T>(o[4 * gq + 2], o[4 * gq + 3]);
-    *reinterpret_cast<u32x2_t*>(orow + 8 * gq + 4 * hi) = w;
+    // ---- 2. row maximum over both halves ----
+    xmax[wave][lane] = fmaxf(mraw, __shfl_xor(mraw, 32));
+    barrier();  // also: every wave has read K pair H - 1
+    load_block(v, H - 1, true);
+    load_block(v, NB - 1, true);
+    if constexpr (NEXT) {  // the next task's Q fragments and K blocks, into the other buffer
+      load_q(nbase, nq0, qfn);
+      asm volatile("" ::: "memory");
+      issue_k(nbuf, nbase);
+    }
+    const float mh0 = xmax[wave & 3][lane], mh1 = xmax[(wave & 3) + 4][lane];
+    constexpr float kLog2e = 1.44269504088896340736f;
+    const float mr = Io<T>::round(fmaxf(mh0, mh1));
+    const float m = POW2 ? mr * scale : mr;
+    const float ml = m * kLog2e;
+    const float c = POW2 ? scale * kLog2e : kLog2e;
+
+    // ---- 3. this half's share of Oᵀ = Vᵀ·Pᵀ ----
+    f32x16_t acc_o[2];
+  #pragma unroll
+    for (int dt = 0; dt < 2; ++dt)
+  #pragma unroll
+      for (int x = 0; x < 16; ++x) acc_o[dt][x] = 0.0f;
+    const int g = lane >> 4, rr = lane & 15, qd = rr & 3, e = rr >> 2;
+    uint32_t v_off[2];
+  #pragma unroll
+    for (int dt = 0; dt < 2; ++dt) {
+      const int n0 = 32 * dt + 16 * (g & 1) + 4 * qd;
+      const int krow = 4 * (g >> 1) + e;
+      v_off[dt] = half_addr + krow * 128 + v_chunk(krow, n0 >> 3) * 16 + (n0 & 7) * 2;
+    }
+    // ---- 2b. the exponentials and their sum over both halves, so that pass 3 stores round(e / s) as the reference's
+    // softmax does ----
+    float esum = 0.0f;
+    float ev[NTH][16];  // the exponentials, kept in fp32 for pass 3
+  #pragma unroll
+    for (int t = 0; t < NTH; ++t)
+  #pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t w = s2[t][j];
+        ev[t][2 * j] = __builtin_amdgcn_exp2f(__builtin_fmaf(lo16<T>(w), c, -ml));
+        ev[t][2 * j + 1] = __builtin_amdgcn_exp2f(__builtin_fmaf(hi16<T>(w), c, -ml));
+        esum += ev[t][2 * j] + ev[t][2 * j + 1];
+      }
+    xsum[wave][lane] = esum + __shfl_xor(esum, 32);
+    wait_vmcnt<2 + NEXT_LOADS>();  // this wave's V pairs 0 .. H-2 (V pair H-1 and the next task's loads may be in flight)
+    barrier();
+    // e / s as e * (1 / s): the two differ by at most one fp32 rounding, which changes the stored 16-bit probability
+    // only when e / s lies within that rounding of a 16-bit rounding boundary
+    const float r = 1.0f / (xsum[wave & 3][lane] + xsum[(wave & 3) + 4][lane]);
+    [&]<int... B_>(std::integer_sequence<int, B_...>) {
+      (
+          [&] {
+            constexpr int i = B_;
+            if constexpr (i == H - 1) {
+              wait_vmcnt<NEXT_LOADS>();
+              barrier();
+            }
+  #pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+              const int t = 2 * i + tt;
+              // V fragments of one d tile at a time (8 registers): d tile 0's are read before the exponentials,
+              // d tile 1's while d tile 0's products run
+              auto read_v = [&]<int dt>(u32x2_t (&vf)[2][2]) {
+                [&]<int... R_>(std::integer_sequence<int, R_...>) {
+                  (
+                      [&] {
+                        constexpr int hf = R_ / 2, part = R_ % 2;
+                        constexpr int off = i * BLK + (16 * hf + 8 * part) * 128;
+                        vf[hf][part] = lds_read_tr16_b64<off>(v_off[dt] + tt * 32 * 128);
+                      }(),
+                      ...);
+                }(std::make_integer_sequence<int, 4>{});
+              };
+              u32x2_t vf[2][2];
+              read_v.template operator()<0>(vf);
+              u32x4_t pf[2];
+  #pragma unroll
+              for (int hf = 0; hf < 2; ++hf)
+  #pragma unroll
+                for (int j = 0; j < 4; ++j)
+                  pf[hf][j] = pack2<T>(ev[t][8 * hf + 2 * j] * r, ev[t][8 * hf + 2 * j + 1] * r);  // P = round(e / s)
+              auto multiply = [&](u32x2_t (&f)[2][2], f32x16_t& acc) {
+  #pragma unroll
+                for (int hf = 0; hf < 2; ++hf) {
+                  asm volatile("" : "+v"(f[hf][0]), "+v"(f[hf][1]));
+                  const u32x4_t a{f[hf][0][0], f[hf][0][1], f[hf][1][0], f[hf][1][1]};
+                  mfma32<T>(a, pf[hf], acc);
+                }
+              };
+              asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+              multiply(vf, acc_o[0]);
+              read_v.template operator()<1>(vf);
+              asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+              multiply(vf, acc_o[1]);
+            }
+          }(),
+          ...);
+    }(std::make_integer_sequence<int, H>{});
+
+    // ---- output: half h writes d tile h from its partial and its partner's (kv is free: every V read is done) ----
+    float* xo = reinterpret_cast<float*>(kv);
+    {
+      const int other = 1 - half;
+      float4* dst = reinterpret_cast<float4*>(xo + (wave * 64 + lane) * 16);
+      barrier();  // every wave's V reads are complete before kv is overwritten
+  #pragma unroll
+      for (int x4 = 0; x4 < 4; ++x4)
+        dst[x4] = make_float4(acc_o[other][4 * x4], acc_o[other][4 * x4 + 1], acc_o[other][4 * x4 + 2], acc_o[other][4 * x4 + 3]);
+    }
+    barrier();
+    const float4* src = reinterpret_cast<const float4*>(xo + ((wave ^ 4) * 64 + lane) * 16);
+    f32x16_t o = half == 0 ? acc_o[0] : acc_o[1];
+  #pragma unroll
+    for (int x4 = 0; x4 < 4; ++x4) {
+      const float4 p = src[x4];
+      o[4 * x4] += p.x;
+      o[4 * x4 + 1] += p.y;
+      o[4 * x4 + 2] += p.z;
+      o[4 * x4 + 3] += p.w;
+    }
+    uint16_t* orow = out + base + static_cast<int64_t>(q0 + l32) * ld + 32 * half;
+  #pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      u32x2_t w;
+      w[0] = pack2<T>(o[4 * gq], o[4 * gq + 1]);
+      w[1] = pack2<T>(o[4 * gq + 2], o[4 * gq + 3]);
+      *reinterpret_cast<u32x2_t*>(orow + 8 * gq + 4 * hi) = w;
+    }
+
+  };
+
+  const int t0 = static_cast<int>(blockIdx.x), t1 = t0 + static_cast<int>(gridDim.x);
+  int64_t base0, base1 = 0;
+  int q00, q01 = 0;
+  geo(t0, base0, q00);
+  u32x4_t qf0[4], qf1[4];
+  load_q(base0, q00, qf0);
+  asm volatile("" ::: "memory");
+  issue_k(kvs[0], base0);
+  if (t1 < tasks) {
+    geo(t1, base1, q01);
+    run.template operator()<true, false>(kvs[0], base0, q00, qf0, kvs[1], base1, q01, qf1);
+    run.template operator()<false, true>(kvs[1], base1, q01, qf1, kvs[0], 0, 0, qf0);
+  } else {
+    run.template operator()<false, false>(kvs[0], base0, q00, qf0, kvs[1], 0, 0, qf1);
   }
 }
 
@@ -571,8 +608,11 @@ extern "C" fh_status fh_attention_fwd(int32_t dtype, const void* q, const void* 
       const int64_t flat = int64_t{grid.x} * grid.y * grid.z;
       if constexpr (NB % 2 == 0 && std::is_same_v<T, bf16_t>) {
         if (flat <= 0x7fffffff) {
-          hipLaunchKernelGGL((attention_split_kernel<T, NB, P>), dim3(static_cast<uint32_t>(flat)), dim3(512), 0, s, qq,
-                             kk, vv, oo, hd, scale);
+          // more tasks than CUs: each workgroup runs two (one workgroup per CU fits), the second one's loads
+          // issued while the first finishes
+          const int64_t wgs = flat > device_cu_count() ? (flat + 1) / 2 : flat;
+          hipLaunchKernelGGL((attention_split_kernel<T, NB, P>), dim3(static_cast<uint32_t>(wgs)), dim3(512), 0, s, qq,
+                             kk, vv, oo, hd, scale, static_cast<int>(flat));
           return;
         }
       }

@@ -1199,7 +1199,9 @@ ATTENTION_CASES = [
     (BF16, 2, 192, 2, 1.0),   # 24 chunks: not a multiple of 16
     (BF16, 1, 320, 1, 1.0),   # 40 chunks
     (BF16, 1, 512, 2, 1.0),   # the largest sequence (C5's)
-    (BF16, 8, 512, 16, 1.0),  # C5's whole attention: 8 x 16 (batch, head) pairs, 512 workgroups
+    (BF16, 8, 512, 16, 1.0),  # C5's whole attention: 8 x 16 (batch, head) pairs, 512 tasks on 256 workgroups
+    (BF16, 1, 384, 87, 1.0),  # 261 tasks on 131 workgroups: the last one runs a single task; no XCD remap
+    (BF16, 3, 512, 30, 1.0, 0.1),  # 360 tasks on 180 workgroups, the general-scale path
     (BF16, 1, 256, 2, 3.0),   # wide score range: most probabilities underflow to 0
     (F16, 2, 256, 2, 1.0),
     (F16, 1, 512, 1, 0.5),
