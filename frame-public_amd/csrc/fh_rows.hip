@@ -7,10 +7,16 @@
 // softmax (reference: src/backends/cpu/kernels/sequence.cpp:114-174): m = max, e = exp(x - m), s = sum(e),
 // y = round(e / s). LayerNorm (reference: src/backends/cpu/kernels/sequence.cpp:182-279): two-pass mean and
 // variance, r = 1 / sqrt(var + eps), y = round(gamma * ((x - mean) * r) + beta). All arithmetic in fp32;
-// multiplies and adds are not contracted, division and sqrt are correctly rounded.
+// multiplies and adds are not contracted, division and sqrt are correctly rounded. For 16-bit outputs the softmax
+// of the register-resident kernels evaluates e as 2^((x - m) log2 e) on v_exp_f32 and y as round(e * (1 / s)): the
+// same d = x - m as the reference, an exponential within a few fp32 ulps of expf and a quotient within one, which
+// changes a stored 8- or 11-bit probability only where it lies that close to a rounding boundary. expf and the
+// correctly rounded division cost about 25 VALU instructions per element and made the [65536, 512] bf16 softmax
+// instruction-bound (30.7 us for 134 MB); fp32 outputs keep them.
 #include <hip/hip_runtime.h>
 
 #include <string>
+#include <type_traits>
 
 #include "fh_common.h"
 
@@ -33,6 +39,25 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 constexpr int kRowsPerBlock = 4;  // 4 waves, one row each
+
+// softmax's e = exp(d) for d = x - m: expf for fp32 outputs, 2^(d log2 e) on v_exp_f32 for 16-bit ones
+template <typename T>
+__device__ __forceinline__ float softmax_exp(float d) {
+  if constexpr (std::is_same_v<T, float>) {
+    return expf(d);
+  } else {
+    return __builtin_amdgcn_exp2f(d * 1.44269504088896340736f);
+  }
+}
+// y = e / s: correctly rounded for fp32 outputs, e * (1 / s) (r passed in) for 16-bit ones
+template <typename T>
+__device__ __forceinline__ float softmax_div(float e, float s, float r) {
+  if constexpr (std::is_same_v<T, float>) {
+    return e / s;
+  } else {
+    return e * r;
+  }
+}
 
 typedef unsigned int u4_t __attribute__((ext_vector_type(4)));
 
@@ -58,20 +83,21 @@ __global__ __launch_bounds__(256) void softmax_wave_kernel(const typename Io<T>:
 #pragma unroll
   for (int t = 0; t < PER; ++t) {
     const int64_t j = lane + 64 * t;
-    v[t] = (j < cols) ? expf(v[t] - m) : 0.0f;
+    v[t] = (j < cols) ? softmax_exp<T>(v[t] - m) : 0.0f;
     s += v[t];
   }
   s = wave_sum(s);
+  const float r = 1.0f / s;
 #pragma unroll
   for (int t = 0; t < PER; ++t) {
     const int64_t j = lane + 64 * t;
-    if (j < cols) yr[j] = Io<T>::store(v[t] / s);
+    if (j < cols) yr[j] = Io<T>::store(softmax_div<T>(v[t], s, r));
   }
 }
 
 // Rows of 64 * PER elements with 16-byte aligned rows, one wave per row: lane l owns the contiguous elements
 // [V*l + 64*V*t, +V) for t < PER / V, all loaded (16-byte accesses) before the max reduction. The arithmetic is
-// softmax_wave_kernel's (m = max, e = expf(x - m), s = sum e, y = round(e / s)); only the order of the terms of
+// softmax_wave_kernel's (m = max, e = exp(x - m), s = sum e, y = round(e / s)); only the order of the terms of
 // the lane's partial sum differs.
 template <typename T, int PER>
 __global__ __launch_bounds__(256) void softmax_vec_kernel(const typename Io<T>::storage* __restrict__ x,
@@ -105,15 +131,16 @@ __global__ __launch_bounds__(256) void softmax_vec_kernel(const typename Io<T>::
   float s = 0.0f;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
-    v[i] = expf(v[i] - m);
+    v[i] = softmax_exp<T>(v[i] - m);
     s += v[i];
   }
   s = wave_sum(s);
+  const float r = 1.0f / s;
 #pragma unroll
   for (int t = 0; t < NV; ++t) {
     S o[V];
 #pragma unroll
-    for (int i = 0; i < V; ++i) o[i] = Io<T>::store(v[t * V + i] / s);
+    for (int i = 0; i < V; ++i) o[i] = Io<T>::store(softmax_div<T>(v[t * V + i], s, r));
     u4_t w;
     __builtin_memcpy(&w, o, 16);
     __builtin_nontemporal_store(w, yr + lane + 64 * t);

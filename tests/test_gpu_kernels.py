@@ -389,6 +389,30 @@ def test_softmax(hip, dtype, rows, cols):
     got = dy.download(x.shape, x.dtype)
     want = orc.softmax(dtype, x)
     assert_close(got, want, dtype, atol=1e-7 if dtype == F32 else 1e-4, what="softmax")
+    say(f"  bit-identical fraction {np.mean(got == want):.4f}")
+
+
+@pytest.mark.parametrize("cols", [512, 200])  # the 16-byte vector kernel and the per-element one
+def test_softmax_16bit_special_rows(hip, cols):
+    # bf16 softmax on v_exp_f32 and e * (1 / s): rows whose results are exact keep the reference's values bit for
+    # bit (one-hot rows, ties), and infinities / NaN give NaN where the reference's arithmetic does
+    ninf, inf, nan = -np.inf, np.inf, np.nan
+    rows = [np.full(cols, ninf) for _ in range(6)]
+    rows[0][3] = 0.0                      # one finite entry: y = 1 there, 0 elsewhere
+    rows[1][:] = ninf                     # all -inf: x - m = NaN everywhere
+    rows[2][0], rows[2][1:] = inf, 0.0    # +inf: inf - inf = NaN, the sum is NaN
+    rows[3][:] = 1.0                      # ties: 1 / cols each
+    rows[3][5] = nan                      # NaN in the row: the max skips it, its e and the sum are NaN
+    rows[4][:] = 0.0                      # all equal: exactly 1 / cols (a power of two for 512)
+    rows[5][:2] = 7.0                     # two equal maxima among -inf: 0.5 each
+    x = synth.to_storage(np.stack(rows).astype(np.float32), BF16)
+    dx, dy = dev(hip, x), hip.DeviceBuffer(x.nbytes)
+    hip.check(hip.lib().fh_softmax_rows(BF16, dx.value, dy.value, len(rows), cols, None))
+    got = dy.download(x.shape, x.dtype)
+    want = orc.softmax(BF16, x)
+    nan_got, nan_want = (got & 0x7FFF) > 0x7F80, (want & 0x7FFF) > 0x7F80
+    assert np.array_equal(nan_got, nan_want), "NaN positions"
+    assert_bitwise(np.where(nan_got, 0, got), np.where(nan_want, 0, want), "softmax special rows")
 
 
 def test_softmax_known_answer(hip):
