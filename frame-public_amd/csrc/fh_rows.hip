@@ -263,24 +263,21 @@ __global__ __launch_bounds__(256) void layer_norm_vec_kernel(const typename Io<T
   float var_sum = 0.0f;
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
-    const float c = v[i] - mean;
-    var_sum += c * c;
+    v[i] -= mean;  // x - mean, kept for the normalisation (the same fp32 value the reference computes twice)
+    var_sum += v[i] * v[i];
   }
   const float variance = wave_sum(var_sum) / static_cast<float>(COLS);
   const float r = 1.0f / sqrtf(variance + eps);
 #pragma unroll
   for (int t = 0; t < NV; ++t) {
-    S g[V], b[V], o[V];
+    S g[V], b[V];
     __builtin_memcpy(g, &gv[t], 16);
     __builtin_memcpy(b, &bv[t], 16);
+    float o[V];
 #pragma unroll
-    for (int i = 0; i < V; ++i) {
-      const float xhat = (v[t * V + i] - mean) * r;
-      o[i] = Io<T>::store(Io<T>::load(g[i]) * xhat + Io<T>::load(b[i]));
-    }
-    u4_t w;
-    __builtin_memcpy(&w, o, 16);
-    __builtin_nontemporal_store(w, yr + lane + 64 * t);
+    for (int i = 0; i < V; ++i) o[i] = Io<T>::load(g[i]) * (v[t * V + i] * r) + Io<T>::load(b[i]);
+    const uint4 pw = pack_vec<T>(o);
+    __builtin_nontemporal_store(u4_t{pw.x, pw.y, pw.z, pw.w}, yr + lane + 64 * t);
   }
 }
 

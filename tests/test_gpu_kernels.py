@@ -438,6 +438,7 @@ def test_layer_norm(hip, dtype, rows, cols):
     got = dy.download(x.shape, x.dtype)
     want = orc.layer_norm(dtype, x, g, b, 1e-5)
     assert_close(got, want, dtype, what="layer_norm")
+    say(f"  bit-identical fraction {np.mean(got == want):.4f}")
 
 
 @pytest.mark.parametrize("dtype", [F32, BF16])
