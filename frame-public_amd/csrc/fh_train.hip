@@ -237,6 +237,133 @@ __global__ __launch_bounds__(kThreads) void maxpool3s2_grad8_kernel(const typena
   }
 }
 
+// The same 2 x 8 block gradient with one workgroup per (n, c) plane: the whole x plane and dy plane are first
+// copied into LDS with coalesced 16-byte loads (the per-thread form issues 5 x 4 loads, 15 of them 2-byte halo
+// columns, and 10 dy loads per block: ~130 us for ResNet's stem pool), then every block reads its 5 x 11 tile and
+// its ten dy values from LDS. Window scan, ties and the order of each input's sum are the per-thread kernel's.
+template <typename T>
+__global__ __launch_bounds__(kThreads) void maxpool3s2_grad8_plane_kernel(const typename Io<T>::storage* __restrict__ dy,
+                                                                          const typename Io<T>::storage* __restrict__ x,
+                                                                          typename Io<T>::storage* __restrict__ dx,
+                                                                          int32_t h, int32_t w, int32_t oh, int32_t ow,
+                                                                          int32_t bh, int32_t bw, int32_t dy_vec) {
+  using S = typename Io<T>::storage;
+  extern __shared__ __attribute__((aligned(16))) unsigned char plane_lds[];
+  S* xs = reinterpret_cast<S*>(plane_lds);
+  S* ds = xs + h * w;  // h * w % 8 == 0: 16-byte aligned
+  const int64_t nc = blockIdx.x;
+  const S* xp = x + nc * h * w;
+  const S* dyp = dy + nc * oh * ow;
+  for (int i = threadIdx.x; i < h * w / 8; i += kThreads)
+    reinterpret_cast<uint4*>(xs)[i] = reinterpret_cast<const uint4*>(xp)[i];
+  if (dy_vec) {
+    for (int i = threadIdx.x; i < oh * ow / 8; i += kThreads)
+      reinterpret_cast<uint4*>(ds)[i] = reinterpret_cast<const uint4*>(dyp)[i];
+  } else {
+    for (int i = threadIdx.x; i < oh * ow; i += kThreads) ds[i] = dyp[i];
+  }
+  __syncthreads();
+  // Blocks whose 5 x 11 tile and ten windows all lie inside the plane take a path with no validity logic; the
+  // rest (the plane's border blocks) the general one. Both are enumerated compactly, so a wave runs one path.
+  const int32_t bi_hi = min((h - 4) / 2, oh - 2), bj_hi = min((w - 10) / 8, (ow - 5) / 4);
+  const int32_t ni = bi_hi >= 1 ? bi_hi : 0, nj = bj_hi >= 1 ? bj_hi : 0;  // interior rows 1 .. bi_hi, cols 1 .. bj_hi
+  // one block: FULL = every tile position and window valid
+  auto block = [&]<bool FULL>(int32_t bi, int32_t bj) {
+    const int32_t row0 = 2 * bi - 1, col0 = 8 * bj - 1;  // local (0, 0)
+    float v[5][11];
+    bool rv[5], cv[11];
+#pragma unroll
+    for (int c = 0; c < 11; ++c) cv[c] = FULL || (col0 + c >= 0 && col0 + c < w);
+#pragma unroll
+    for (int r = 0; r < 5; ++r) {
+      const int32_t gr = row0 + r;
+      rv[r] = FULL || (gr >= 0 && gr < h);
+      const S* rowp = xs + (FULL ? gr : min(max(gr, 0), h - 1)) * w;
+      const uint4 mid = *reinterpret_cast<const uint4*>(rowp + 8 * bj);
+      const S* m = reinterpret_cast<const S*>(&mid);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) v[r][c + 1] = Io<T>::load(m[c]);
+      v[r][0] = Io<T>::load(rowp[FULL ? col0 : max(col0, 0)]);
+      v[r][9] = Io<T>::load(rowp[FULL ? col0 + 9 : min(col0 + 9, w - 1)]);
+      v[r][10] = Io<T>::load(rowp[FULL ? col0 + 10 : min(col0 + 10, w - 1)]);
+    }
+    // per window: the first valid position, then a later one only when strictly greater (the reference's scan),
+    // branch-free
+    int arg[10];
+    float g[10];
+#pragma unroll
+    for (int k = 0; k < 10; ++k) {
+      const int wr = k / 5, wc = k % 5;
+      const int32_t woh = bi + wr, wow = 4 * bj + wc;
+      const bool wvalid = FULL || (woh < oh && wow < ow);
+      bool found = false;
+      float best = 0.0f;
+      int at = -1;
+#pragma unroll
+      for (int a = 0; a < 3; ++a)
+#pragma unroll
+        for (int b = 0; b < 3; ++b) {
+          const int lr = 2 * wr + a, lc = 2 * wc + b;
+          const float val = v[lr][lc];
+          if constexpr (FULL) {
+            const bool take = (a == 0 && b == 0) || val > best;
+            best = take ? val : best;
+            at = take ? lr * 11 + lc : at;
+          } else {
+            const bool ok = rv[lr] && cv[lc];
+            const bool take = ok && (!found || val > best);
+            best = take ? val : best;
+            at = take ? lr * 11 + lc : at;
+            found = found || ok;
+          }
+        }
+      arg[k] = wvalid ? at : -1;
+      const float gv = Io<T>::load(ds[(FULL ? woh : min(woh, oh - 1)) * ow + (FULL ? wow : min(wow, ow - 1))]);
+      g[k] = wvalid ? gv : 0.0f;
+    }
+    // input (1 + rr, 1 + c) of the tile is covered by windows wr with 2 wr <= 1 + rr <= 2 wr + 2 and wc with
+    // 2 wc <= 1 + c <= 2 wc + 2; the others cannot have chosen it. Summed in window order; adding +0.0 for a
+    // window that chose another input leaves the sum unchanged (it starts at +0.0, so it is never -0.0).
+#pragma unroll
+    for (int rr = 0; rr < 2; ++rr) {
+      const int32_t gr = 2 * bi + rr;
+      if (!FULL && gr >= h) continue;
+      uint4 packed;
+      S* o = reinterpret_cast<S*>(&packed);
+#pragma unroll
+      for (int c = 0; c < 8; ++c) {
+        const int lr = rr + 1, lc = c + 1, at = lr * 11 + lc;
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 10; ++k) {
+          const int wr = k / 5, wc = k % 5;
+          if (2 * wr <= lr && lr <= 2 * wr + 2 && 2 * wc <= lc && lc <= 2 * wc + 2) acc += arg[k] == at ? g[k] : 0.0f;
+        }
+        o[c] = Io<T>::store(acc);
+      }
+      *reinterpret_cast<uint4*>(dx + nc * h * w + static_cast<int64_t>(gr) * w + 8 * bj) = packed;
+    }
+  };
+  for (int e = threadIdx.x; e < ni * nj; e += kThreads) block.template operator()<true>(1 + e / nj, 1 + e % nj);
+  // border blocks: rows 0 and bi_hi + 1 .. bh - 1 whole, the interior rows' columns 0 and bj_hi + 1 .. bw - 1
+  const int32_t top = 1 + (bh - 1 - ni);                   // whole rows: row 0 and the rows below the interior
+  const int32_t side = bw - nj;                            // border columns of an interior row
+  const int32_t nb = top * bw + ni * side;
+  for (int e = threadIdx.x; e < nb; e += kThreads) {
+    int32_t bi, bj;
+    if (e < top * bw) {
+      const int32_t r = e / bw;
+      bi = r == 0 ? 0 : ni + r;
+      bj = e % bw;
+    } else {
+      const int32_t f = e - top * bw, r = f / side, c = f % side;
+      bi = 1 + r;
+      bj = c == 0 ? 0 : nj + c;
+    }
+    block.template operator()<false>(bi, bj);
+  }
+}
+
 // ---- conv gradients (direct, reference order) ----------------------------------------------------------------
 
 struct ConvG {
@@ -724,10 +851,19 @@ struct PoolGradRun {
     if (mode == 0 && g.kh == 3 && g.kw == 3 && g.sh == 2 && g.sw == 2 && g.ph == 1 && g.pw == 1 && g.w % 8 == 0 &&
         (sizeof(S) == 2) && aligned) {
       const int32_t bh = (g.h + 1) / 2, bw = g.w / 8;
-      const int64_t blocks = static_cast<int64_t>(g.n) * g.c * bh * bw;
-      hipLaunchKernelGGL((maxpool3s2_grad8_kernel<T>), dim3(static_cast<uint32_t>(blocks_for(blocks))), dim3(kThreads), 0,
-                         s, static_cast<const S*>(dy), static_cast<const S*>(x), static_cast<S*>(dx), g.h, g.w, g.oh, g.ow,
-                         bh, bw, blocks);
+      const int64_t planes = static_cast<int64_t>(g.n) * g.c;
+      const int64_t plane_bytes = (static_cast<int64_t>(g.h) * g.w + static_cast<int64_t>(g.oh) * g.ow) * 2;
+      if (plane_bytes <= 64 * 1024 && planes <= 0x7fffffffLL) {
+        const int32_t dy_vec = (static_cast<int64_t>(g.oh) * g.ow) % 8 == 0 && reinterpret_cast<uintptr_t>(dy) % 16 == 0;
+        hipLaunchKernelGGL((maxpool3s2_grad8_plane_kernel<T>), dim3(static_cast<uint32_t>(planes)), dim3(kThreads),
+                           static_cast<uint32_t>(plane_bytes), s, static_cast<const S*>(dy), static_cast<const S*>(x),
+                           static_cast<S*>(dx), g.h, g.w, g.oh, g.ow, bh, bw, dy_vec);
+      } else {
+        const int64_t blocks = planes * bh * bw;
+        hipLaunchKernelGGL((maxpool3s2_grad8_kernel<T>), dim3(static_cast<uint32_t>(blocks_for(blocks))), dim3(kThreads),
+                           0, s, static_cast<const S*>(dy), static_cast<const S*>(x), static_cast<S*>(dx), g.h, g.w, g.oh,
+                           g.ow, bh, bw, blocks);
+      }
     } else if (mode == 0 && g.kh == 3 && g.kw == 3 && g.sh == 2 && g.sw == 2 && g.ph == 1 && g.pw == 1) {
       const int32_t bh = (g.h + 1) / 2, bw = (g.w + 1) / 2;
       const int64_t blocks = static_cast<int64_t>(g.n) * g.c * bh * bw;

@@ -159,7 +159,10 @@ POOL_CASES = [
     (2, 3, 8, 8, 2, 2, 0),
     (1, 5, 7, 7, 7, 7, 0),
     (2, 2, 9, 9, 3, 1, 1),
-    (2, 8, 24, 32, 3, 2, 1),  # 3x3/s2/p1 with W % 8 == 0: the 2x8-block kernel
+    (2, 8, 24, 32, 3, 2, 1),  # 3x3/s2/p1 with W % 8 == 0: the 2x8-block kernel, planes staged in LDS
+    (2, 4, 18, 24, 3, 2, 1),  # ... with a dy plane (9 x 12) that is not whole 16-byte vectors
+    (2, 3, 112, 112, 3, 2, 1),  # ResNet's stem pool plane
+    (1, 2, 192, 192, 3, 2, 1),  # planes too large for LDS: the per-thread 2x8-block kernel
     (1, 3, 13, 13, 3, 2, 1),  # ... and the 2x2-block kernel
 ]
 
