@@ -446,13 +446,16 @@ fh_status launch(GemmArgs args, int64_t batch, hipStream_t stream) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; }
 
-// Largest tile that still gives every CU a workgroup (measured on MI355X, bf16 U(-1,1), M=N=K:
-// 4096: 256x256/8 waves 1164 TFLOP/s; 2048: 128x128/8 waves 711-724; 1024: 64x64/4 waves 282).
+// Largest tile that still gives (nearly) every CU a workgroup (measured on MI355X, bf16 U(-1,1), M=N=K:
+// 4096: 256x256/8 waves 1164 TFLOP/s; 2048: 128x128/8 waves 711-724; 1024: 64x64/4 waves 282). A 256x256 tile
+// does the work of four 128x128 tiles at about 1.4 times their rate per CU, so it still wins with three quarters
+// of the CUs busy: 4096 x 3072 x 1024 (192 tiles) 31.8 us against 33.3-34.0 us on 128x128 tiles.
 template <typename T>
 fh_status dispatch(const GemmArgs& args, int64_t batch, hipStream_t stream) {
   const int cus = device_cu_count();
   auto tiles = [&](int64_t bm, int64_t bn) { return ((args.M + bm - 1) / bm) * ((args.N + bn - 1) / bn) * batch; };
-  if (args.M >= 256 && args.N >= 256 && tiles(256, 256) >= cus) return launch<T, 256, 256, 4, 2>(args, batch, stream);
+  if (args.M >= 256 && args.N >= 256 && tiles(256, 256) * 4 >= static_cast<int64_t>(cus) * 3)
+    return launch<T, 256, 256, 4, 2>(args, batch, stream);
   if (args.M >= 128 && args.N >= 128 && tiles(128, 128) >= cus) return launch<T, 128, 128, 2, 4>(args, batch, stream);
   if (args.N >= 128 && tiles(64, 128) >= cus) return launch<T, 64, 128, 2, 2>(args, batch, stream);
   return launch<T, 64, 64, 2, 2>(args, batch, stream);
