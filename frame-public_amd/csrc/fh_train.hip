@@ -462,12 +462,11 @@ __global__ __launch_bounds__(kThreads) void filter_flip_kernel(const S* __restri
 // form above reads with a stride of cin * taps elements). One ci per workgroup: a 64x64x3x3 filter still spreads
 // over 64 workgroups (with eight, its eight workgroups took longer than the gather form).
 constexpr int kFlipCo = 64, kFlipCi = 1;
+// Workgroup (bx, by) of one filter's flip: output channels [64 bx, 64 bx + 64), input channels [by, by + kFlipCi).
 template <typename S>
-__global__ __launch_bounds__(kThreads) void filter_flip_tiled_kernel(const S* __restrict__ w, S* __restrict__ out,
-                                                                     int32_t cout, int32_t cin, int32_t taps) {
-  extern __shared__ uint32_t flip_smem[];
-  S* tile = reinterpret_cast<S*>(flip_smem);
-  const int32_t co0 = static_cast<int32_t>(blockIdx.x) * kFlipCo, ci0 = static_cast<int32_t>(blockIdx.y) * kFlipCi;
+__device__ __forceinline__ void filter_flip_tile(const S* __restrict__ w, S* __restrict__ out, int32_t cout, int32_t cin,
+                                                 int32_t taps, int32_t bx, int32_t by, S* tile) {
+  const int32_t co0 = bx * kFlipCo, ci0 = by * kFlipCi;
   const int32_t nco = min(kFlipCo, cout - co0), nci = min(kFlipCi, cin - ci0);
   const int32_t run = nci * taps, pitch = kFlipCi * taps + 1;
   const S* src = w + static_cast<int64_t>(co0) * cin * taps + static_cast<int64_t>(ci0) * taps;
@@ -482,6 +481,39 @@ __global__ __launch_bounds__(kThreads) void filter_flip_tiled_kernel(const S* __
     const int32_t cl = q / taps, t = q - cl * taps;
     out[(static_cast<int64_t>(ci0 + cl) * taps + t) * cout + co0 + c] = tile[c * pitch + cl * taps + (taps - 1 - t)];
   }
+}
+
+template <typename S>
+__global__ __launch_bounds__(kThreads) void filter_flip_tiled_kernel(const S* __restrict__ w, S* __restrict__ out,
+                                                                     int32_t cout, int32_t cin, int32_t taps) {
+  extern __shared__ uint32_t flip_smem[];
+  filter_flip_tile<S>(w, out, cout, cin, taps, static_cast<int32_t>(blockIdx.x), static_cast<int32_t>(blockIdx.y),
+                      reinterpret_cast<S*>(flip_smem));
+}
+
+// Several filters' flips in one launch (a training graph's filters are all known before its first input gradient,
+// and each flip alone is too small to be more than launch and memory latency): workgroup g belongs to filter i with
+// first_block[i] <= g < first_block[i + 1] and runs that filter's workgroup (g - first_block[i]) of the tiled
+// flip, so each output is the single-filter launch's bit for bit.
+struct FlipBatch {
+  const void* w[FH_FLIP_MAX];
+  void* out[FH_FLIP_MAX];
+  int32_t cout[FH_FLIP_MAX], cin[FH_FLIP_MAX], taps[FH_FLIP_MAX];
+  int32_t first_block[FH_FLIP_MAX + 1];
+  int32_t count;
+};
+
+template <typename S>
+__global__ __launch_bounds__(kThreads) void filter_flip_multi_kernel(FlipBatch a) {
+  extern __shared__ uint32_t flip_smem[];
+  const int32_t g = static_cast<int32_t>(blockIdx.x);
+  int i = 0;
+  while (i + 1 < a.count && a.first_block[i + 1] <= g) ++i;
+  const int32_t local = g - a.first_block[i];
+  const int32_t tiles_co = (a.cout[i] + kFlipCo - 1) / kFlipCo;
+  const int32_t by = local / tiles_co, bx = local - by * tiles_co;
+  filter_flip_tile<S>(static_cast<const S*>(a.w[i]), static_cast<S*>(a.out[i]), a.cout[i], a.cin[i], a.taps[i], bx, by,
+                      reinterpret_cast<S*>(flip_smem));
 }
 
 // out_i = x_i + round(s_i * y_i) for up to FH_AXPY_MAX tensors: workgroups are dealt to the tensors by
@@ -1143,6 +1175,47 @@ extern "C" fh_status fh_conv_filter_flip(int32_t dtype, const void* w, void* out
     hipLaunchKernelGGL((filter_flip_kernel<uint16_t>), grid, dim3(kThreads), 0, s, static_cast<const uint16_t*>(w),
                        static_cast<uint16_t*>(out), a, b, c, d, total);
   return launch_status("fh_conv_filter_flip");
+}
+
+extern "C" fh_status fh_conv_filter_flip_multi(int32_t dtype, int32_t count, const void* const* w, void* const* out,
+                                               const int64_t* dims, void* stream) {
+  if (!is_supported_float(dtype)) return fail(FH_UNIMPLEMENTED, "fh_conv_filter_flip_multi: unsupported dtype");
+  if (count < 0 || count > FH_FLIP_MAX) return fail(FH_INVALID_ARGUMENT, "fh_conv_filter_flip_multi: count out of range");
+  if (count == 0) return FH_OK;
+  if (w == nullptr || out == nullptr || dims == nullptr)
+    return fail(FH_INVALID_ARGUMENT, "fh_conv_filter_flip_multi: null pointer");
+  const int64_t esize = dtype_size(dtype);
+  FlipBatch b{};
+  int64_t blocks = 0, max_taps = 0;
+  for (int32_t i = 0; i < count; ++i) {
+    const int64_t cout = dims[4 * i], cin = dims[4 * i + 1], kh = dims[4 * i + 2], kw = dims[4 * i + 3];
+    if (cout < 0 || cin < 0 || kh < 0 || kw < 0 || cout > 0x7fffffffLL || cin > 0x7fffffffLL)
+      return fail(FH_INVALID_ARGUMENT, "fh_conv_filter_flip_multi: invalid dims");
+    if (kh * kw > FH_FLIP_MAX_TAPS)
+      return fail(FH_INVALID_ARGUMENT, "fh_conv_filter_flip_multi: kh * kw above " + std::to_string(FH_FLIP_MAX_TAPS));
+    const int64_t total = cout * cin * kh * kw;
+    if (total > 0 && (w[i] == nullptr || out[i] == nullptr))
+      return fail(FH_INVALID_ARGUMENT, "fh_conv_filter_flip_multi: null tensor pointer");
+    b.w[i] = w[i], b.out[i] = out[i];
+    b.cout[i] = static_cast<int32_t>(cout), b.cin[i] = static_cast<int32_t>(cin);
+    b.taps[i] = static_cast<int32_t>(kh * kw);
+    b.first_block[i] = static_cast<int32_t>(blocks);
+    if (total > 0) {
+      blocks += (cout + kFlipCo - 1) / kFlipCo * ((cin + kFlipCi - 1) / kFlipCi);
+      max_taps = std::max(max_taps, kh * kw);
+    }
+    if (blocks > 0x7fffffffLL) return fail(FH_INVALID_ARGUMENT, "fh_conv_filter_flip_multi: filters too large for one launch");
+  }
+  b.first_block[count] = static_cast<int32_t>(blocks);
+  b.count = count;
+  if (blocks == 0) return FH_OK;
+  const size_t shm = static_cast<size_t>((kFlipCo * (kFlipCi * max_taps + 1) * esize + 3) / 4 * 4);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == FH_F32)
+    hipLaunchKernelGGL((filter_flip_multi_kernel<uint32_t>), dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), shm, s, b);
+  else
+    hipLaunchKernelGGL((filter_flip_multi_kernel<uint16_t>), dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), shm, s, b);
+  return launch_status("fh_conv_filter_flip_multi");
 }
 
 extern "C" fh_status fh_axpy_multi(int32_t dtype, int32_t count, const void* const* x, const void* const* y,

@@ -111,6 +111,7 @@ _SIGS = {
                                        c_void_p]),
     "fh_axpy_multi": (c_int32, [c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p]),
     "fh_conv_filter_flip": (c_int32, [c_int32, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p]),
+    "fh_conv_filter_flip_multi": (c_int32, [c_int32, c_int32, c_void_p, c_void_p, c_void_p, c_void_p]),
     "fh_dilate_nhwc": (c_int32, [c_int32, c_int32, c_void_p, c_void_p] + [c_int64] * 8 + [c_void_p]),
     "fh_avg_pool2d_grad_nhwc": (c_int32, [c_int32, c_void_p, c_void_p, POINTER(c_int64), c_void_p]),
     "fh_sum_rows_workspace": (c_int64, [c_int32, c_int64, c_int64]),

@@ -193,6 +193,9 @@ inline constexpr std::string_view kPackFilterC8Op = "hip_pack_filter_c8_internal
 // filter [Cin][KH][KW][Cout] (fh_conv_filter_flip) and dy zero-dilated by the stride into channels-last
 // [N,Hu,Wu,Cout] (fh_dilate_nhwc; attribute stride).
 inline constexpr std::string_view kFilterFlipOp = "hip_conv_filter_flip_internal";
+// the flips of up to FH_FLIP_MAX filters in one launch (fh_conv_filter_flip_multi): input i w_i [Cout,Cin,KH,KW],
+// output i [Cin,KH,KW,Cout]
+inline constexpr std::string_view kFilterFlipMultiOp = "hip_conv_filter_flip_multi_internal";
 inline constexpr std::string_view kDilateNhwcOp = "hip_dilate_nhwc_internal";  // attr in_nhwc = 1: dy channels-last
 // sum over every axis but the last (the bias gradient of channels-last data or of [rows, features]): outputs the
 // sum and an fp32 workspace of per-workgroup partials (see fh_sum_rows).

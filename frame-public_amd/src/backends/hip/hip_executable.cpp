@@ -608,6 +608,43 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
     return Status::ok();
   };
 
+  // graph-input filters of the lowered input gradients, in first-use order, each once: all of them are defined
+  // before the first input gradient, where one launch flips them all (fh_conv_filter_flip_multi)
+  std::vector<const ir::Value*> flip_batched;
+  {
+    std::unordered_set<const ir::Value*> seen;
+    for (const ir::Node* n : src.topological_order()) {
+      if (!plan_grad_input(n).ok) continue;
+      const ir::Value* w = n->inputs()[1];
+      if (w->producer() == nullptr || w->producer()->op() != ir::kGraphInputOp || seen.count(w)) continue;
+      if (w->type().shape.dim(2) * w->type().shape.dim(3) > FH_FLIP_MAX_TAPS) continue;
+      seen.insert(w);
+      flip_batched.push_back(w);
+    }
+  }
+  std::unordered_map<const ir::Value*, ir::Value*> flip_out;  // source filter -> its flipped value
+  bool flips_emitted = false;
+  auto emit_flips = [&]() -> Status {
+    flips_emitted = true;
+    for (size_t i0 = 0; i0 < flip_batched.size(); i0 += FH_FLIP_MAX) {
+      const size_t i1 = std::min(flip_batched.size(), i0 + size_t{FH_FLIP_MAX});
+      if (i1 - i0 < 2) break;  // a single filter keeps its own flip node
+      std::vector<ir::Value*> ins;
+      std::vector<ir::TensorType> types;
+      for (size_t i = i0; i < i1; ++i) {
+        ins.push_back(map.at(flip_batched[i]));
+        ir::TensorType t = flip_batched[i]->type();
+        const Shape& ws = t.shape;
+        t.shape = Shape({ws.dim(1), ws.dim(2), ws.dim(3), ws.dim(0)});
+        types.push_back(t);
+      }
+      Result<ir::Node*> n = out.create_node(std::string(kFilterFlipMultiOp), std::move(ins), std::move(types));
+      if (!n.is_ok()) return n.status();
+      for (size_t i = i0; i < i1; ++i) flip_out[flip_batched[i]] = n.value()->output(static_cast<int32_t>(i - i0));
+    }
+    return Status::ok();
+  };
+
   // Graph inputs first (same order, so the same signature; they have no operands, so the order stays
   // topological): every filter is defined before the first conv, where the batched transpose goes.
   for (const ir::Node* n : src.topological_order()) {
@@ -623,8 +660,15 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
     if (const GradInputLowering gi = plan_grad_input(n); gi.ok) {
       ir::TensorType wt = ins[1]->type(), dt = ins[0]->type();
       wt.shape = Shape({gi.cin, gi.kh, gi.kw, gi.cout});
-      Result<ir::Node*> flip = out.create_node(std::string(kFilterFlipOp), {ins[1]}, {wt});
-      if (!flip.is_ok()) return flip.status();
+      if (!flips_emitted) FRAME_RETURN_IF_ERROR(emit_flips());
+      ir::Value* flipped = nullptr;
+      if (auto it = flip_out.find(n->inputs()[1]); it != flip_out.end()) {
+        flipped = it->second;
+      } else {
+        Result<ir::Node*> flip = out.create_node(std::string(kFilterFlipOp), {ins[1]}, {wt});
+        if (!flip.is_ok()) return flip.status();
+        flipped = flip.value()->output(0);
+      }
       ir::Value* dy_cl = nullptr;
       const bool dy_nhwc = nhwc.count(n->inputs()[0]) != 0;
       if (gi.sh == 1 && gi.sw == 1) {
@@ -644,7 +688,7 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
         dy_cl = d.value()->output(0);
       }
       Result<ir::Node*> c =
-          out.create_node(std::string(kConvNhwcOp), {dy_cl, flip.value()->output(0)}, {lowered_type(&n->outputs()[0])});
+          out.create_node(std::string(kConvNhwcOp), {dy_cl, flipped}, {lowered_type(&n->outputs()[0])});
       if (!c.is_ok()) return c.status();
       if (nhwc.count(&n->outputs()[0])) c.value()->set_attr("out_nhwc", ir::AttrValue{int64_t{1}});
       c.value()->set_attr("stride", ir::AttrValue{std::vector<int64_t>{1, 1}});

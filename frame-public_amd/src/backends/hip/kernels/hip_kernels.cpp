@@ -795,6 +795,31 @@ Status filter_flip_kernel(KernelContext& ctx) {
   return Status::ok();
 }
 
+Status filter_flip_multi_kernel(KernelContext& ctx) {
+  const std::string op(kFilterFlipMultiOp);
+  const size_t n = ctx.inputs.size();
+  if (n == 0 || n > FH_FLIP_MAX || ctx.outputs.size() != n) return invalid(op, "expects 1 to 32 inputs and as many outputs");
+  Result<int32_t> dt = float_code(op, ctx.outputs[0].dtype());
+  if (!dt.is_ok()) return dt.status();
+  std::vector<const void*> ws(n);
+  std::vector<void*> outs(n);
+  std::vector<int64_t> dims(4 * n);
+  for (size_t i = 0; i < n; ++i) {
+    const Shape& w = ctx.inputs[i].shape();
+    if (!same_elem_type(ctx.inputs[i], ctx.outputs[i]) || !same_elem_type(ctx.outputs[i], ctx.outputs[0]))
+      return invalid(op, "expects inputs and outputs of one element type");
+    if (w.rank() != 4 || ctx.outputs[i].shape() != Shape({w.dim(1), w.dim(2), w.dim(3), w.dim(0)}))
+      return invalid(op, "expects w [Cout,Cin,KH,KW] -> [Cin,KH,KW,Cout]");
+    ws[i] = ctx.inputs[i].raw_data();
+    outs[i] = ctx.outputs[i].raw_data();
+    for (int d = 0; d < 4; ++d) dims[4 * i + d] = w.dim(d);
+  }
+  FRAME_HIP_RETURN_IF_ERROR(fh_conv_filter_flip_multi(dt.value(), static_cast<int32_t>(n), ws.data(), outs.data(),
+                                                      dims.data(), stream_handle(ctx)),
+                            "op '" + op + "' (hip)");
+  return Status::ok();
+}
+
 Status dilate_nhwc_kernel(KernelContext& ctx) {
   const std::string op(kDilateNhwcOp);
   FRAME_RETURN_IF_ERROR(arity(ctx, op, 1, 1));
@@ -1053,6 +1078,7 @@ FRAME_REGISTER_KERNEL("avg_pool2d_grad_internal", kHipBackendName, &pool_grad_ke
 FRAME_REGISTER_KERNEL("conv2d_grad_input_internal", kHipBackendName, &conv_grad_kernel<0>);
 FRAME_REGISTER_KERNEL("conv2d_grad_filter_internal", kHipBackendName, &conv_grad_kernel<1>);
 FRAME_REGISTER_KERNEL(kFilterFlipOp, kHipBackendName, &filter_flip_kernel);
+FRAME_REGISTER_KERNEL(kFilterFlipMultiOp, kHipBackendName, &filter_flip_multi_kernel);
 FRAME_REGISTER_KERNEL(kConvWgradOp, kHipBackendName, &conv_wgrad_kernel);
 FRAME_REGISTER_KERNEL(kAvgPoolGradNhwcOp, kHipBackendName, &avg_pool_grad_nhwc_kernel);
 FRAME_REGISTER_KERNEL(kSumRowsOp, kHipBackendName, &sum_rows_kernel);

@@ -389,6 +389,15 @@ fh_status fh_conv_filter_flip(int32_t dtype, const void* w, void* out, int64_t c
 fh_status fh_dilate_nhwc(int32_t dtype, int32_t in_nhwc, const void* x, void* out, int64_t n, int64_t c, int64_t h,
                          int64_t w, int64_t sh, int64_t sw, int64_t hu, int64_t wu, void* stream);
 
+/* fh_conv_filter_flip of up to FH_FLIP_MAX same-dtype filters in one launch: out[i] = flip(w[i]) with
+ * dims[4i .. 4i+3] = {cout, cin, kh, kw} (kh * kw <= FH_FLIP_MAX_TAPS), each output identical to a separate
+ * fh_conv_filter_flip call; the filters must not overlap the outputs. A training graph's filters are all known
+ * before its first input gradient, so one launch replaces one per convolution. No counterpart in the reference. */
+#define FH_FLIP_MAX 32
+#define FH_FLIP_MAX_TAPS 255
+fh_status fh_conv_filter_flip_multi(int32_t dtype, int32_t count, const void* const* w, void* const* out,
+                                    const int64_t* dims, void* stream);
+
 /* avg_pool2d_grad_internal on channels-last dy [N,Ho,Wo,C] -> dx [N,H,W,C] (C*itemsize % 16 == 0), geom as fh_pool2d;
  * the reference's summation order, bit-identical to fh_pool2d_grad mode 1. For backward graphs whose activations
  * stay channels-last; no counterpart in the reference. */

@@ -10,6 +10,8 @@
   gradient against a numpy scatter with numpy's own argmax; mse_loss and its gradient against their closed forms;
   the backward of the MLP against central finite differences of the loss.
 """
+import re
+
 import numpy as np
 import pytest
 
@@ -298,6 +300,10 @@ def test_resnet_training_graph_stays_channels_last():
     low = host.hip_lowered(host.backward(g.text(), 0, list(range(1, len(specs) + 1))), 1)
     assert low.count("hip_channels_last_internal(") <= 13, low.count("hip_channels_last_internal(")
     assert "hip_avg_pool2d_grad_nhwc_internal" in low
+    # the 19 input gradients' filters (every conv but the stem) are flipped in one batched step
+    assert low.count("hip_conv_filter_flip_multi_internal(") == 1 and "hip_conv_filter_flip_internal(" not in low
+    flips = re.search(r"= hip_conv_filter_flip_multi_internal\(([^)]*)\)", low)
+    assert flips is not None and len(flips.group(1).split(",")) == 19, low
     assert low.count("hip_conv2d_wgrad_nhwc_internal") == 20
     assert 'in_nhwc=1' in low  # strided grad_input dilates a channels-last dy
     sums = [l for l in low.splitlines() if " = sum(" in l]

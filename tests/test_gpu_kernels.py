@@ -1282,3 +1282,36 @@ def test_conv_filter_flip(hip, itemsize, shape):
     hip.check(hip.lib().fh_conv_filter_flip(dtype, dw.value, dout.value, co, ci, kh, kw, None))
     want = np.ascontiguousarray(w[:, :, ::-1, ::-1].transpose(1, 2, 3, 0))
     assert_bitwise(dout.download((ci, kh, kw, co), dt), want, f"filter flip {shape}")
+
+
+# the batched form: a training graph's mix (3x3 and 1x1, whole and ragged 64-channel tiles, a 7x7 and an empty
+# filter), each output against the permutation and against a single fh_conv_filter_flip call, bit for bit
+@pytest.mark.parametrize("itemsize", [2, 4])
+def test_conv_filter_flip_multi(hip, itemsize):
+    shapes = [(64, 64, 3, 3), (100, 13, 3, 3), (0, 8, 3, 3), (128, 64, 1, 1), (512, 256, 3, 3), (64, 3, 7, 7),
+              (33, 17, 1, 1), (8, 3, 7, 5)]
+    say(f"conv_filter_flip_multi itemsize={itemsize} {len(shapes)} filters")
+    dt = np.uint16 if itemsize == 2 else np.uint32
+    dtype = 3 if itemsize == 2 else 0
+    rng = np.random.default_rng(6)
+    ws = [rng.integers(0, np.iinfo(dt).max, size=sh, dtype=dt) for sh in shapes]
+    dws = [dev(hip, w) if w.size else hip.DeviceBuffer(16) for w in ws]
+    outs = [hip.DeviceBuffer(max(w.nbytes, 16)) for w in ws]
+    n = len(shapes)
+    wp = (ctypes.c_void_p * n)(*[d.value for d in dws])
+    op = (ctypes.c_void_p * n)(*[d.value for d in outs])
+    dims = (ctypes.c_int64 * (4 * n))(*[v for sh in shapes for v in sh])
+    hip.check(hip.lib().fh_conv_filter_flip_multi(dtype, n, wp, op, dims, None))
+    for w, dw, o, (co, ci, kh, kw) in zip(ws, dws, outs, shapes):
+        if w.size == 0:
+            continue
+        want = np.ascontiguousarray(w[:, :, ::-1, ::-1].transpose(1, 2, 3, 0))
+        got = o.download((ci, kh, kw, co), dt)
+        assert_bitwise(got, want, f"filter flip multi {w.shape}")
+        single = hip.DeviceBuffer(w.nbytes)
+        hip.check(hip.lib().fh_conv_filter_flip(dtype, dw.value, single.value, co, ci, kh, kw, None))
+        assert_bitwise(got, single.download((ci, kh, kw, co), dt), f"filter flip multi vs single {w.shape}")
+    # rejected before any launch: more than FH_FLIP_MAX filters, a filter above FH_FLIP_MAX_TAPS taps
+    assert hip.lib().fh_conv_filter_flip_multi(dtype, 33, wp, op, dims, None) != 0
+    big = (ctypes.c_int64 * 4)(8, 8, 16, 16)
+    assert hip.lib().fh_conv_filter_flip_multi(dtype, 1, wp, op, big, None) != 0
