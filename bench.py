@@ -238,8 +238,14 @@ def extras(steps, only=None):
                     for i in range(8)]
             by = 2 * int(np.prod(shape)) * 2 + 2 * 1024 * 2
         ms = _time_graph(g.text(), sets, max(steps, 40), 8)
+        # the copy floor at the same bytes: relu(x) of the same shape (one read, one write) through the fused
+        # elementwise kernel, timed the same way
+        gc = graphs.Graph("hip")
+        gc.output(gc.relu(gc.input(BF16, shape)))
+        copy_ms = _time_graph(gc.text(), [s_[:1] for s_ in sets], max(steps, 40), 8)
         return {"workload": f"{kind} bf16 {list(shape)}, cold (8 rotating input sets)", "us": round(ms * 1e3, 2),
-                "GB/s": round(by / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(by / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4)}
+                "GB/s": round(by / (ms * 1e-3) / 1e9, 1), "frac_hbm": round(by / (ms * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
+                "copy_us": round(copy_ms * 1e3, 2)}
 
     def conv(dtype):
         flops = 2 * 32 * 64 * 56 * 56 * 64 * 9
