@@ -303,22 +303,25 @@ __global__ __launch_bounds__(256) void gemm_seq_kernel(GemmArgs args) {
   const int t = threadIdx.x;
   const int r = t >> 4, c = t & 15;
 
-  // chunk loads: A[16][kKC] (thread -> row t/16, k t%16 + 16 i) and B[kKC][16] (thread -> k t/16 + 16 i, col t%16)
+  // chunk loads: A[16][kKC] and B[kKC][16], each with consecutive lanes on the operand's contiguous index: k for
+  // row-major A and transposed B (thread -> row / column t/16, k t%16 + 16 i), the row or column otherwise
+  // (thread -> k t/16 + 16 i, row / column t%16)
   float la[8], lb[8];
+  const bool ta = args.trans_a != 0, tb = args.trans_b != 0;
   auto load_chunk = [&](int64_t k0) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const int64_t gm = m0 + r, gk = k0 + c + 16 * i;
-      la[i] = (gm < M && gk < K) ? Io<T>::load(A[args.trans_a ? gk * args.lda + gm : gm * args.lda + gk]) : 0.0f;
-      const int64_t bk = k0 + r + 16 * i, bn = n0 + c;
-      lb[i] = (bk < K && bn < N) ? Io<T>::load(B[args.trans_b ? bn * args.ldb + bk : bk * args.ldb + bn]) : 0.0f;
+      const int64_t gm = m0 + (ta ? c : r), gk = k0 + (ta ? r : c) + 16 * i;
+      la[i] = (gm < M && gk < K) ? Io<T>::load(A[ta ? gk * args.lda + gm : gm * args.lda + gk]) : 0.0f;
+      const int64_t bk = k0 + (tb ? c : r) + 16 * i, bn = n0 + (tb ? r : c);
+      lb[i] = (bk < K && bn < N) ? Io<T>::load(B[tb ? bn * args.ldb + bk : bk * args.ldb + bn]) : 0.0f;
     }
   };
   auto store_chunk = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      As[buf][r * kKP + c + 16 * i] = la[i];
-      Bt[buf][c * kKP + r + 16 * i] = lb[i];
+      As[buf][ta ? c * kKP + r + 16 * i : r * kKP + c + 16 * i] = la[i];
+      Bt[buf][tb ? r * kKP + c + 16 * i : c * kKP + r + 16 * i] = lb[i];
     }
   };
 
