@@ -462,13 +462,14 @@ __global__ __launch_bounds__(kThreads) void filter_flip_kernel(const S* __restri
 // form above reads with a stride of cin * taps elements). One ci per workgroup: a 64x64x3x3 filter still spreads
 // over 64 workgroups (with eight, its eight workgroups took longer than the gather form).
 constexpr int kFlipCo = 64, kFlipCi = 1;
-// Workgroup (bx, by) of one filter's flip: output channels [64 bx, 64 bx + 64), input channels [by, by + kFlipCi).
+// Workgroup (bx, by) of one filter's flip: output channels [64 bx, 64 bx + 64), input channels
+// [ci_per by, ci_per by + ci_per); the tile takes kFlipCo * (ci_per * taps + 1) elements of LDS.
 template <typename S>
 __device__ __forceinline__ void filter_flip_tile(const S* __restrict__ w, S* __restrict__ out, int32_t cout, int32_t cin,
-                                                 int32_t taps, int32_t bx, int32_t by, S* tile) {
-  const int32_t co0 = bx * kFlipCo, ci0 = by * kFlipCi;
-  const int32_t nco = min(kFlipCo, cout - co0), nci = min(kFlipCi, cin - ci0);
-  const int32_t run = nci * taps, pitch = kFlipCi * taps + 1;
+                                                 int32_t taps, int32_t ci_per, int32_t bx, int32_t by, S* tile) {
+  const int32_t co0 = bx * kFlipCo, ci0 = by * ci_per;
+  const int32_t nco = min(kFlipCo, cout - co0), nci = min(ci_per, cin - ci0);
+  const int32_t run = nci * taps, pitch = ci_per * taps + 1;
   const S* src = w + static_cast<int64_t>(co0) * cin * taps + static_cast<int64_t>(ci0) * taps;
   for (int32_t e = threadIdx.x; e < nco * run; e += kThreads) {
     const int32_t c = e / run, j = e - c * run;
@@ -487,20 +488,21 @@ template <typename S>
 __global__ __launch_bounds__(kThreads) void filter_flip_tiled_kernel(const S* __restrict__ w, S* __restrict__ out,
                                                                      int32_t cout, int32_t cin, int32_t taps) {
   extern __shared__ uint32_t flip_smem[];
-  filter_flip_tile<S>(w, out, cout, cin, taps, static_cast<int32_t>(blockIdx.x), static_cast<int32_t>(blockIdx.y),
-                      reinterpret_cast<S*>(flip_smem));
+  filter_flip_tile<S>(w, out, cout, cin, taps, kFlipCi, static_cast<int32_t>(blockIdx.x),
+                      static_cast<int32_t>(blockIdx.y), reinterpret_cast<S*>(flip_smem));
 }
 
 // Several filters' flips in one launch (a training graph's filters are all known before its first input gradient,
 // and each flip alone is too small to be more than launch and memory latency): workgroup g belongs to filter i with
 // first_block[i] <= g < first_block[i + 1] and runs that filter's workgroup (g - first_block[i]) of the tiled
-// flip, so each output is the single-filter launch's bit for bit.
+// flip, over ci_per input channels (one launch has workgroups enough for larger tiles than a single small
+// filter's: the reads become runs of ci_per * taps elements); each output is the same permutation, bit for bit.
 struct FlipBatch {
   const void* w[FH_FLIP_MAX];
   void* out[FH_FLIP_MAX];
   int32_t cout[FH_FLIP_MAX], cin[FH_FLIP_MAX], taps[FH_FLIP_MAX];
   int32_t first_block[FH_FLIP_MAX + 1];
-  int32_t count;
+  int32_t count, ci_per;
 };
 
 template <typename S>
@@ -512,8 +514,8 @@ __global__ __launch_bounds__(kThreads) void filter_flip_multi_kernel(FlipBatch a
   const int32_t local = g - a.first_block[i];
   const int32_t tiles_co = (a.cout[i] + kFlipCo - 1) / kFlipCo;
   const int32_t by = local / tiles_co, bx = local - by * tiles_co;
-  filter_flip_tile<S>(static_cast<const S*>(a.w[i]), static_cast<S*>(a.out[i]), a.cout[i], a.cin[i], a.taps[i], bx, by,
-                      reinterpret_cast<S*>(flip_smem));
+  filter_flip_tile<S>(static_cast<const S*>(a.w[i]), static_cast<S*>(a.out[i]), a.cout[i], a.cin[i], a.taps[i],
+                      a.ci_per, bx, by, reinterpret_cast<S*>(flip_smem));
 }
 
 // out_i = x_i + round(s_i * y_i) for up to FH_AXPY_MAX tensors: workgroups are dealt to the tensors by
@@ -830,7 +832,18 @@ __global__ __launch_bounds__(kLossThreads) void mse_loss_kernel(const typename I
                                                                 typename Io<T>::storage* __restrict__ out, int64_t n) {
   __shared__ float part[kLossThreads / 64];
   float acc = 0.0f;
-  for (int64_t i = threadIdx.x; i < n; i += kLossThreads) {
+  // each thread sums elements threadIdx.x, + kLossThreads, ... in order; the loads of 16 of them are issued before
+  // their sum, so one memory latency covers 16 elements instead of one
+  constexpr int U = 16;
+  int64_t i = threadIdx.x;
+  for (; i + (U - 1) * kLossThreads < n; i += U * kLossThreads) {
+    float d[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) d[u] = Io<T>::load(p[i + u * kLossThreads]) - Io<T>::load(t[i + u * kLossThreads]);
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc += d[u] * d[u];
+  }
+  for (; i < n; i += kLossThreads) {
     const float d = Io<T>::load(p[i]) - Io<T>::load(t[i]);
     acc += d * d;
   }
@@ -1185,14 +1198,22 @@ extern "C" fh_status fh_conv_filter_flip_multi(int32_t dtype, int32_t count, con
   if (w == nullptr || out == nullptr || dims == nullptr)
     return fail(FH_INVALID_ARGUMENT, "fh_conv_filter_flip_multi: null pointer");
   const int64_t esize = dtype_size(dtype);
-  FlipBatch b{};
-  int64_t blocks = 0, max_taps = 0;
+  int64_t max_taps = 1;
   for (int32_t i = 0; i < count; ++i) {
     const int64_t cout = dims[4 * i], cin = dims[4 * i + 1], kh = dims[4 * i + 2], kw = dims[4 * i + 3];
     if (cout < 0 || cin < 0 || kh < 0 || kw < 0 || cout > 0x7fffffffLL || cin > 0x7fffffffLL)
       return fail(FH_INVALID_ARGUMENT, "fh_conv_filter_flip_multi: invalid dims");
     if (kh * kw > FH_FLIP_MAX_TAPS)
       return fail(FH_INVALID_ARGUMENT, "fh_conv_filter_flip_multi: kh * kw above " + std::to_string(FH_FLIP_MAX_TAPS));
+    if (cout * cin * kh * kw > 0) max_taps = std::max(max_taps, kh * kw);
+  }
+  // input channels per workgroup: up to 8, as many as keep the tile within 64 KB of LDS (at least one: 255 taps of
+  // fp32 take 64 KB)
+  const int32_t ci_per = static_cast<int32_t>(std::clamp<int64_t>((65536 / (kFlipCo * esize) - 1) / max_taps, 1, 8));
+  FlipBatch b{};
+  int64_t blocks = 0;
+  for (int32_t i = 0; i < count; ++i) {
+    const int64_t cout = dims[4 * i], cin = dims[4 * i + 1], kh = dims[4 * i + 2], kw = dims[4 * i + 3];
     const int64_t total = cout * cin * kh * kw;
     if (total > 0 && (w[i] == nullptr || out[i] == nullptr))
       return fail(FH_INVALID_ARGUMENT, "fh_conv_filter_flip_multi: null tensor pointer");
@@ -1200,16 +1221,14 @@ extern "C" fh_status fh_conv_filter_flip_multi(int32_t dtype, int32_t count, con
     b.cout[i] = static_cast<int32_t>(cout), b.cin[i] = static_cast<int32_t>(cin);
     b.taps[i] = static_cast<int32_t>(kh * kw);
     b.first_block[i] = static_cast<int32_t>(blocks);
-    if (total > 0) {
-      blocks += (cout + kFlipCo - 1) / kFlipCo * ((cin + kFlipCi - 1) / kFlipCi);
-      max_taps = std::max(max_taps, kh * kw);
-    }
+    if (total > 0) blocks += (cout + kFlipCo - 1) / kFlipCo * ((cin + ci_per - 1) / ci_per);
     if (blocks > 0x7fffffffLL) return fail(FH_INVALID_ARGUMENT, "fh_conv_filter_flip_multi: filters too large for one launch");
   }
   b.first_block[count] = static_cast<int32_t>(blocks);
   b.count = count;
+  b.ci_per = ci_per;
   if (blocks == 0) return FH_OK;
-  const size_t shm = static_cast<size_t>((kFlipCo * (kFlipCi * max_taps + 1) * esize + 3) / 4 * 4);
+  const size_t shm = static_cast<size_t>((kFlipCo * (ci_per * max_taps + 1) * esize + 3) / 4 * 4);
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == FH_F32)
     hipLaunchKernelGGL((filter_flip_multi_kernel<uint32_t>), dim3(static_cast<uint32_t>(blocks)), dim3(kThreads), shm, s, b);
