@@ -83,26 +83,67 @@ std::vector<int64_t> epilogue_program(const ir::Node* consumer, size_t operand_i
   return {};
 }
 
+// relu_grad_internal(x, gy) keeps gy where x > 0. Where the graph also computes r = relu(x), r > 0 exactly where
+// x > 0 (relu keeps every x > 0 and maps the rest, NaN included, to zero, -0 or NaN, none of which is > 0), so
+// relu_grad(r, gy) is the same tensor bit for bit and x loses a use: a conv or matmul (or the residual add after it)
+// whose result fed only the relu and its gradient can then take the relu into its epilogue, and a training graph's
+// forward fuses as the inference graph's does.
+Status lower_relu_grads(ir::Graph& g) {
+  std::unordered_map<const ir::Value*, ir::Value*> relu_of;  // x -> relu(x)
+  for (ir::Node* n : g.topological_order())
+    if (n->op() == "relu" && n->inputs().size() == 1 && n->outputs().size() == 1 &&
+        n->outputs()[0].type().dtype == n->inputs()[0]->type().dtype)
+      relu_of.emplace(n->inputs()[0], n->output(0));
+  if (relu_of.empty()) return Status::ok();
+  const std::vector<ir::Node*> snapshot = g.topological_order();
+  for (ir::Node* n : snapshot) {
+    if (n->op() != "relu_grad_internal" || n->inputs().size() != 2 || n->outputs().size() != 1) continue;
+    auto it = relu_of.find(n->inputs()[0]);
+    if (it == relu_of.end() || !(it->second->type().shape == n->inputs()[0]->type().shape)) continue;
+    Result<ir::Node*> r = g.create_node(std::string(n->op()), {it->second, n->inputs()[1]}, {n->outputs()[0].type()});
+    if (!r.is_ok()) return r.status();
+    for (const auto& [k, a] : n->attrs()) r.value()->set_attr(k, a);
+    FRAME_RETURN_IF_ERROR(g.replace_all_uses(n->output(0), r.value()->output(0)));
+    FRAME_RETURN_IF_ERROR(g.erase_node(n));
+  }
+  return Status::ok();
+}
+
+// A matmul or conv2d whose result's only use is an elementwise program (a single add/mul/relu/square/gelu node or a
+// fused chain of them) becomes one epilogue node; a second single-use elementwise consumer of that node's result
+// extends its program (conv -> add -> relu of a training graph, whose add and relu the fusion pass left apart while
+// the add's result also fed relu_grad, becomes the add;relu epilogue of the inference graph).
 Status lower_epilogues(ir::Graph& g) {
   std::unordered_map<const ir::Value*, int> uses;
   for (const ir::Node* n : g.topological_order())
     for (const ir::Value* v : n->inputs()) ++uses[v];
   for (const ir::Value* v : g.outputs()) uses[v] += 1000;  // graph outputs are never folded away
   const std::vector<ir::Node*> snapshot = g.topological_order();
+  // snapshot nodes fused away (checked only against snapshot nodes: an epilogue node created here may reuse the
+  // address of one erased before it; a producer reached through a live consumer's input is always live)
   std::unordered_set<const ir::Node*> erased;
   for (ir::Node* c : snapshot) {
     if (erased.count(c) || c->outputs().size() != 1) continue;
     for (size_t idx = 0; idx < std::min<size_t>(2, c->inputs().size()); ++idx) {
       ir::Value* v = c->inputs()[idx];
       ir::Node* p = v->producer();
-      if (p == nullptr || erased.count(p) || uses[v] != 1) continue;
-      const bool is_mm = p->op() == "matmul", is_conv = p->op() == "conv2d";
+      if (p == nullptr || uses[v] != 1) continue;
+      const bool chained = p->op() == kGemmEpilogueOp || p->op() == kConvEpilogueOp;
+      const bool is_mm = p->op() == "matmul" || p->op() == kGemmEpilogueOp;
+      const bool is_conv = p->op() == "conv2d" || p->op() == kConvEpilogueOp;
       if (!is_mm && !is_conv) continue;
       if (!(p->outputs()[0].type().dtype == c->outputs()[0].type().dtype)) continue;
       std::vector<int64_t> prog = epilogue_program(c, idx);
+      size_t n_main = p->inputs().size();
+      if (chained) {
+        const auto* before = attr_of<std::vector<int64_t>>(p, "ep_ops");
+        const auto* main = attr_of<int64_t>(p, "n_main_inputs");
+        if (before == nullptr || main == nullptr || prog.empty()) continue;
+        prog.insert(prog.begin(), before->begin(), before->end());
+        n_main = static_cast<size_t>(*main);
+      }
       if (prog.empty() || prog.size() > FH_MAX_SEGMENTS) continue;
       std::vector<ir::Value*> ins(p->inputs().begin(), p->inputs().end());
-      const size_t n_main = ins.size();
       for (size_t j = 0; j < c->inputs().size(); ++j)
         if (j != idx) ins.push_back(c->inputs()[j]);
       if (ins.size() - n_main > FH_MAX_SEGMENTS) continue;
@@ -113,6 +154,7 @@ Status lower_epilogues(ir::Graph& g) {
       f.value()->set_attr("ep_ops", ir::AttrValue{prog});
       f.value()->set_attr("n_main_inputs", ir::AttrValue{static_cast<int64_t>(n_main)});
       if (is_mm) f.value()->set_attr("any_order", ir::AttrValue{int64_t{1}});
+      uses[f.value()->output(0)] = uses[c->output(0)];
       FRAME_RETURN_IF_ERROR(g.replace_all_uses(c->output(0), f.value()->output(0)));
       FRAME_RETURN_IF_ERROR(g.erase_node(c));
       FRAME_RETURN_IF_ERROR(g.erase_node(p));
@@ -547,6 +589,18 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
     }
   }
   std::unordered_map<const ir::Value*, ir::Value*> cl_copies;  // one channels-last copy per value
+  // one C8 pack per value (a training graph's stem input feeds both the conv and its filter gradient)
+  std::unordered_map<const ir::Value*, ir::Value*> c8_packs;
+  auto pack_c8 = [&](ir::Value* v) -> Result<ir::Value*> {
+    if (auto it = c8_packs.find(v); it != c8_packs.end()) return it->second;
+    ir::TensorType tx = v->type();
+    const Shape& xs = tx.shape;
+    tx.shape = Shape({xs.dim(0), xs.dim(2), xs.dim(3), 8});
+    Result<ir::Node*> px = out.create_node(std::string(kPackInputC8Op), {v}, {tx});
+    if (!px.is_ok()) return px.status();
+    c8_packs[v] = px.value()->output(0);
+    return px.value()->output(0);
+  };
   auto channels_last = [&](ir::Value* v) -> Result<ir::Value*> {
     if (auto it = cl_copies.find(v); it != cl_copies.end()) return it->second;
     Result<ir::Node*> n = out.create_node(std::string(kChannelsLastOp), {v}, {channels_last_type(v)});
@@ -702,12 +756,9 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
     if (const GradFilterLowering gf = plan_grad_filter(n); gf.ok) {
       ir::Value* x_cl = nullptr;
       if (gf.c8) {
-        ir::TensorType tx = ins[0]->type();
-        const Shape& xs = tx.shape;
-        tx.shape = Shape({xs.dim(0), xs.dim(2), xs.dim(3), 8});
-        Result<ir::Node*> px = out.create_node(std::string(kPackInputC8Op), {ins[0]}, {tx});
+        Result<ir::Value*> px = pack_c8(ins[0]);
         if (!px.is_ok()) return px.status();
-        x_cl = px.value()->output(0);
+        x_cl = px.value();
       } else if (nhwc.count(n->inputs()[0])) {
         x_cl = ins[0];
       } else {
@@ -733,14 +784,13 @@ Result<ir::Graph> lower_convs(const ir::Graph& src) {
       ir::Value* w_cl = nullptr;
       bool in_nchw = false, w_oihw = false;
       if (p.c8) {
-        ir::TensorType tx = ins[0]->type(), tw = ins[1]->type();
-        tx.shape = Shape({geom[0], geom[2], geom[3], 8});
+        ir::TensorType tw = ins[1]->type();
         tw.shape = Shape({geom[4], fh_conv_c8_filter_k(geom[5], geom[6])});
-        Result<ir::Node*> px = out.create_node(std::string(kPackInputC8Op), {ins[0]}, {tx});
+        Result<ir::Value*> px = pack_c8(ins[0]);
         if (!px.is_ok()) return px.status();
         Result<ir::Node*> pw = out.create_node(std::string(kPackFilterC8Op), {ins[1]}, {tw});
         if (!pw.is_ok()) return pw.status();
-        x_cl = px.value()->output(0);
+        x_cl = px.value();
         w_cl = pw.value()->output(0);
       } else {
         if (!batched_emitted) FRAME_RETURN_IF_ERROR(emit_batched());
@@ -1589,6 +1639,7 @@ Result<ir::Graph> lower_for_hip(const ir::Graph& graph, int32_t opt_level) {
   if (!work.is_ok()) return work.status();
   // Attention runs at every level (like the conv lowering), before the epilogue fusion would claim its matmuls.
   FRAME_RETURN_IF_ERROR(lower_attention(work.value()));
+  if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_relu_grads(work.value()));
   if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_epilogues(work.value()));
   if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_gemm_softmax(work.value()));
   if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_grouped_gemms(work.value()));

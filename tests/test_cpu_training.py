@@ -292,6 +292,34 @@ def test_grad_input_lowering(dtype):
     assert "conv2d_grad_input_internal" in lowered((8, 64, 56, 56), (64, 32, 3, 3), 1, 1, groups=2)
 
 
+def test_relu_grad_reads_the_relu_output():
+    """relu_grad_internal(x, gy) keeps gy where x > 0, and relu(x) > 0 exactly where x > 0, so the lowering gives
+    relu_grad the relu's output: the residual block's conv -> add -> relu then becomes one add;relu conv epilogue,
+    and both gradients read it. The oracle check: on every bf16 bit pattern, relu_grad over relu(x) equals
+    relu_grad over x (NaN, -0, infinities and denormals included)."""
+    g = graphs.Graph("hip")
+    x, w, b = g.input(BF16, (2, 64, 8, 8)), g.input(BF16, (64, 64, 3, 3)), g.input(BF16, (64,))
+    skip, gy, w2 = g.input(BF16, (2, 64, 8, 8)), g.input(BF16, (2, 64, 8, 8)), g.input(BF16, (64, 64, 3, 3))
+    c = g.op("conv2d", [x, w, b], (2, 64, 8, 8), {"stride": [1, 1], "padding": [1, 1], "groups": 1})
+    a = g.add(c, skip)
+    r = g.relu(a)
+    g.output(g.op("conv2d", [r, w2], (2, 64, 8, 8), {"stride": [1, 1], "padding": [1, 1], "groups": 1}))
+    g.output(g.op("relu_grad_internal", [a, gy], (2, 64, 8, 8), {}))
+    g.output(g.op("relu_grad_internal", [r, gy], (2, 64, 8, 8), {}))
+    low = host.hip_lowered(g.text(), 1)
+    fused = re.search(r"(%\d+) = hip_conv2d_nhwc_internal\([^)]*\) \{ep_ops=\[1, 3\]", low)
+    assert fused is not None, low
+    grads = re.findall(r"= relu_grad_internal\((%\d+), ", low)
+    assert grads == [fused.group(1)] * 2, low
+    # at opt level 0 the graph keeps the reference's nodes
+    assert "= relu(" in host.hip_lowered(g.text(), 0)
+    bits = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    gy = np.random.default_rng(3).permutation(bits)
+    relu = orc.ew_program(BF16, [3], [1], [bits])
+    assert np.array_equal(orc.ew_program(BF16, [6], [2], [bits, gy]), orc.ew_program(BF16, [6], [2], [relu, gy]))
+    assert np.count_nonzero(orc.ew_program(BF16, [6], [2], [bits, gy]) != 0) > 30000  # gy passed where x > 0
+
+
 def test_resnet_training_graph_stays_channels_last():
     """The backward of ResNet-18 reads and writes channels-last activations: conv gradients take NHWC x / dy, the
     transposed convolutions write NHWC, relu_grad / add / bias sums run on NHWC, the global average-pool gradient
@@ -302,6 +330,12 @@ def test_resnet_training_graph_stays_channels_last():
     assert "hip_avg_pool2d_grad_nhwc_internal" in low
     # the 19 input gradients' filters (every conv but the stem) are flipped in one batched step
     assert low.count("hip_conv_filter_flip_multi_internal(") == 1 and "hip_conv_filter_flip_internal(" not in low
+    # relu_grad reads the relus' outputs, so every forward relu fuses into its conv as in the inference graph (the
+    # eight residual blocks as add;relu) and the stem's input is packed once for the conv and its filter gradient
+    ops = re.findall(r"= (\w+)\(", low)
+    assert "relu" not in ops and ops.count("relu_grad_internal") == 17
+    assert low.count("ep_ops=[1, 3]") == 8 and low.count("ep_ops=[3]") == 9
+    assert ops.count("hip_pack_input_c8_internal") == 1
     flips = re.search(r"= hip_conv_filter_flip_multi_internal\(([^)]*)\)", low)
     assert flips is not None and len(flips.group(1).split(",")) == 19, low
     assert low.count("hip_conv2d_wgrad_nhwc_internal") == 20
