@@ -776,8 +776,24 @@ __global__ __launch_bounds__(kThreads) void sum_rows_partial_kernel(const typena
 #pragma unroll
     for (int k = 0; k < V; ++k) acc[k] = 0.0f;
     if (rsub < row_step && col_ok) {
-      for (int64_t r = r0 + rsub; r < r1; r += row_step) {
-        const uint4 w = *reinterpret_cast<const uint4*>(x + r * cols + static_cast<int64_t>(vc) * V);
+      // rows r, r + row_step, ... added in order; the loads of 8 of them are issued before their sums, so one
+      // memory latency covers 8 rows instead of one
+      constexpr int U = 8;
+      const S* xc = x + static_cast<int64_t>(vc) * V;
+      int64_t r = r0 + rsub;
+      for (; r + (U - 1) * row_step < r1; r += U * row_step) {
+        uint4 w[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) w[u] = *reinterpret_cast<const uint4*>(xc + (r + u * row_step) * cols);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const S* e = reinterpret_cast<const S*>(&w[u]);
+#pragma unroll
+          for (int k = 0; k < V; ++k) acc[k] += Io<T>::load(e[k]);
+        }
+      }
+      for (; r < r1; r += row_step) {
+        const uint4 w = *reinterpret_cast<const uint4*>(xc + r * cols);
         const S* e = reinterpret_cast<const S*>(&w);
 #pragma unroll
         for (int k = 0; k < V; ++k) acc[k] += Io<T>::load(e[k]);
