@@ -28,7 +28,9 @@ struct PoolG {
 // recomputed exactly as the forward (first strict maximum in (kh, kw) order over non-padding taps), dy added
 // when the argmax is this element (reference: src/backends/cpu/kernels/pool.cpp:186-206, 358-388, where the
 // windows scatter in that order into a float buffer). avg: kh then kw ascending over the covering windows, sum of
-// dy, then / (KH*KW) (reference: pool.cpp:543-566).
+// dy, then / (KH*KW) (reference: pool.cpp:543-566). MODE 2 is max followed by relu_grad_internal against the
+// pool's input: dx = x > 0 ? max-pool gradient : 0 (elementwise.cpp:407-414), both values as the separate ops
+// store them.
 template <typename T, int MODE>
 __global__ __launch_bounds__(kThreads) void pool2d_grad_kernel(const typename Io<T>::storage* __restrict__ dy,
                                                                const typename Io<T>::storage* __restrict__ x,
@@ -41,7 +43,7 @@ __global__ __launch_bounds__(kThreads) void pool2d_grad_kernel(const typename Io
   const int64_t nc = i / (static_cast<int64_t>(g.w) * g.h);
   const auto* dyp = dy + nc * g.oh * g.ow;
   float acc = 0.0f;
-  if constexpr (MODE == 0) {
+  if constexpr (MODE != 1) {
     const auto* xp = x + nc * g.h * g.w;
     // windows whose rows cover ih: oh*sh - ph <= ih <= oh*sh - ph + kh - 1
     const int32_t th = ih + g.ph - g.kh + 1, tw = iw + g.pw - g.kw + 1;  // first window start reaching ih / iw
@@ -75,6 +77,7 @@ __global__ __launch_bounds__(kThreads) void pool2d_grad_kernel(const typename Io
         if (at == ih * g.w + iw) acc += Io<T>::load(dyp[oh * g.ow + ow]);
       }
     }
+    if constexpr (MODE == 2) acc = Io<T>::load(xp[ih * g.w + iw]) > 0.0f ? acc : 0.0f;
     dx[i] = Io<T>::store(acc);
   } else {
     for (int32_t a = 0; a < g.kh; ++a) {
@@ -98,7 +101,8 @@ __global__ __launch_bounds__(kThreads) void pool2d_grad_kernel(const typename Io
 // (rows 2i, 2i+1, columns 2j, 2j+1), whose covering windows are exactly (oh, ow) in {i, i+1} x {j, j+1}. Each of
 // the four windows' argmax is found once (first strict maximum in (kh, kw) order, as the forward) and every input of
 // the block adds the dy of the windows that chose it in (oh, ow) order: the same sums as the generic kernel.
-template <typename T>
+// RELU: then relu_grad against x (dx = x > 0 ? sum : 0), as pool2d_grad_kernel's MODE 2.
+template <typename T, bool RELU>
 __global__ __launch_bounds__(kThreads) void maxpool3s2_grad_kernel(const typename Io<T>::storage* __restrict__ dy,
                                                                    const typename Io<T>::storage* __restrict__ x,
                                                                    typename Io<T>::storage* __restrict__ dx, int32_t h,
@@ -149,14 +153,15 @@ __global__ __launch_bounds__(kThreads) void maxpool3s2_grad_kernel(const typenam
 #pragma unroll
     for (int k = 0; k < 4; ++k)
       if (arg[k] == at) acc += g[k];
+    if constexpr (RELU) acc = Io<T>::load(xp[at]) > 0.0f ? acc : 0.0f;
     dx[nc * h * w + at] = Io<T>::store(acc);
   }
 }
 
 // The same gradient on 2 x 8 input blocks when W % 8 == 0: the ten covering windows (oh in {i, i+1}, ow in
 // 4j .. 4j+4) are evaluated from one register tile of the 5 x 11 inputs they span (16-byte loads for the middle
-// eight columns), and the block is written with two 16-byte stores.
-template <typename T>
+// eight columns), and the block is written with two 16-byte stores. RELU as maxpool3s2_grad_kernel's.
+template <typename T, bool RELU>
 __global__ __launch_bounds__(kThreads) void maxpool3s2_grad8_kernel(const typename Io<T>::storage* __restrict__ dy,
                                                                     const typename Io<T>::storage* __restrict__ x,
                                                                     typename Io<T>::storage* __restrict__ dx, int32_t h,
@@ -231,6 +236,7 @@ __global__ __launch_bounds__(kThreads) void maxpool3s2_grad8_kernel(const typena
 #pragma unroll
       for (int k = 0; k < 10; ++k)
         if (arg[k] == at) acc += g[k];
+      if constexpr (RELU) acc = v[rr + 1][c + 1] > 0.0f ? acc : 0.0f;
       o[c] = Io<T>::store(acc);
     }
     *reinterpret_cast<uint4*>(dx + nc * h * w + static_cast<int64_t>(gr) * w + 8 * bj) = packed;
@@ -240,8 +246,9 @@ __global__ __launch_bounds__(kThreads) void maxpool3s2_grad8_kernel(const typena
 // The same 2 x 8 block gradient with one workgroup per (n, c) plane: the whole x plane and dy plane are first
 // copied into LDS with coalesced 16-byte loads (the per-thread form issues 5 x 4 loads, 15 of them 2-byte halo
 // columns, and 10 dy loads per block: ~130 us for ResNet's stem pool), then every block reads its 5 x 11 tile and
-// its ten dy values from LDS. Window scan, ties and the order of each input's sum are the per-thread kernel's.
-template <typename T>
+// its ten dy values from LDS. Window scan, ties and the order of each input's sum are the per-thread kernel's;
+// RELU as maxpool3s2_grad_kernel's (x is already in registers: the fused relu gradient reads nothing more).
+template <typename T, bool RELU>
 __global__ __launch_bounds__(kThreads) void maxpool3s2_grad8_plane_kernel(const typename Io<T>::storage* __restrict__ dy,
                                                                           const typename Io<T>::storage* __restrict__ x,
                                                                           typename Io<T>::storage* __restrict__ dx,
@@ -339,6 +346,7 @@ __global__ __launch_bounds__(kThreads) void maxpool3s2_grad8_plane_kernel(const 
           const int wr = k / 5, wc = k % 5;
           if (2 * wr <= lr && lr <= 2 * wr + 2 && 2 * wc <= lc && lc <= 2 * wc + 2) acc += arg[k] == at ? g[k] : 0.0f;
         }
+        if constexpr (RELU) acc = v[lr][lc] > 0.0f ? acc : 0.0f;
         o[c] = Io<T>::store(acc);
       }
       *reinterpret_cast<uint4*>(dx + nc * h * w + static_cast<int64_t>(gr) * w + 8 * bj) = packed;
@@ -909,30 +917,43 @@ struct PoolGradRun {
     using S = typename Io<T>::storage;
     const dim3 grid(static_cast<uint32_t>(blocks_for(total)));
     const bool aligned = reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(dx) % 16 == 0;
-    if (mode == 0 && g.kh == 3 && g.kw == 3 && g.sh == 2 && g.sw == 2 && g.ph == 1 && g.pw == 1 && g.w % 8 == 0 &&
+    const bool relu = mode == 2;
+    if (mode != 1 && g.kh == 3 && g.kw == 3 && g.sh == 2 && g.sw == 2 && g.ph == 1 && g.pw == 1 && g.w % 8 == 0 &&
         (sizeof(S) == 2) && aligned) {
       const int32_t bh = (g.h + 1) / 2, bw = g.w / 8;
       const int64_t planes = static_cast<int64_t>(g.n) * g.c;
       const int64_t plane_bytes = (static_cast<int64_t>(g.h) * g.w + static_cast<int64_t>(g.oh) * g.ow) * 2;
       if (plane_bytes <= 64 * 1024 && planes <= 0x7fffffffLL) {
         const int32_t dy_vec = (static_cast<int64_t>(g.oh) * g.ow) % 8 == 0 && reinterpret_cast<uintptr_t>(dy) % 16 == 0;
-        hipLaunchKernelGGL((maxpool3s2_grad8_plane_kernel<T>), dim3(static_cast<uint32_t>(planes)), dim3(kThreads),
-                           static_cast<uint32_t>(plane_bytes), s, static_cast<const S*>(dy), static_cast<const S*>(x),
-                           static_cast<S*>(dx), g.h, g.w, g.oh, g.ow, bh, bw, dy_vec);
+        auto go = [&]<bool R>() {
+          hipLaunchKernelGGL((maxpool3s2_grad8_plane_kernel<T, R>), dim3(static_cast<uint32_t>(planes)), dim3(kThreads),
+                             static_cast<uint32_t>(plane_bytes), s, static_cast<const S*>(dy), static_cast<const S*>(x),
+                             static_cast<S*>(dx), g.h, g.w, g.oh, g.ow, bh, bw, dy_vec);
+        };
+        relu ? go.template operator()<true>() : go.template operator()<false>();
       } else {
         const int64_t blocks = planes * bh * bw;
-        hipLaunchKernelGGL((maxpool3s2_grad8_kernel<T>), dim3(static_cast<uint32_t>(blocks_for(blocks))), dim3(kThreads),
-                           0, s, static_cast<const S*>(dy), static_cast<const S*>(x), static_cast<S*>(dx), g.h, g.w, g.oh,
-                           g.ow, bh, bw, blocks);
+        auto go = [&]<bool R>() {
+          hipLaunchKernelGGL((maxpool3s2_grad8_kernel<T, R>), dim3(static_cast<uint32_t>(blocks_for(blocks))),
+                             dim3(kThreads), 0, s, static_cast<const S*>(dy), static_cast<const S*>(x), static_cast<S*>(dx),
+                             g.h, g.w, g.oh, g.ow, bh, bw, blocks);
+        };
+        relu ? go.template operator()<true>() : go.template operator()<false>();
       }
-    } else if (mode == 0 && g.kh == 3 && g.kw == 3 && g.sh == 2 && g.sw == 2 && g.ph == 1 && g.pw == 1) {
+    } else if (mode != 1 && g.kh == 3 && g.kw == 3 && g.sh == 2 && g.sw == 2 && g.ph == 1 && g.pw == 1) {
       const int32_t bh = (g.h + 1) / 2, bw = (g.w + 1) / 2;
       const int64_t blocks = static_cast<int64_t>(g.n) * g.c * bh * bw;
-      hipLaunchKernelGGL((maxpool3s2_grad_kernel<T>), dim3(static_cast<uint32_t>(blocks_for(blocks))), dim3(kThreads), 0, s,
-                         static_cast<const S*>(dy), static_cast<const S*>(x), static_cast<S*>(dx), g.h, g.w, g.oh, g.ow,
-                         bh, bw, blocks);
+      auto go = [&]<bool R>() {
+        hipLaunchKernelGGL((maxpool3s2_grad_kernel<T, R>), dim3(static_cast<uint32_t>(blocks_for(blocks))), dim3(kThreads),
+                           0, s, static_cast<const S*>(dy), static_cast<const S*>(x), static_cast<S*>(dx), g.h, g.w, g.oh,
+                           g.ow, bh, bw, blocks);
+      };
+      relu ? go.template operator()<true>() : go.template operator()<false>();
     } else if (mode == 0)
       hipLaunchKernelGGL((pool2d_grad_kernel<T, 0>), grid, dim3(kThreads), 0, s, static_cast<const S*>(dy),
+                         static_cast<const S*>(x), static_cast<S*>(dx), g, total);
+    else if (mode == 2)
+      hipLaunchKernelGGL((pool2d_grad_kernel<T, 2>), grid, dim3(kThreads), 0, s, static_cast<const S*>(dy),
                          static_cast<const S*>(x), static_cast<S*>(dx), g, total);
     else
       hipLaunchKernelGGL((pool2d_grad_kernel<T, 1>), grid, dim3(kThreads), 0, s, static_cast<const S*>(dy),
@@ -1062,7 +1083,8 @@ using namespace fh;
 extern "C" fh_status fh_pool2d_grad(int32_t dtype, int32_t mode, const void* dy, const void* x, void* dx,
                                     const int64_t geom[10], void* stream) {
   if (!is_supported_float(dtype)) return fail(FH_UNIMPLEMENTED, "fh_pool2d_grad: unsupported dtype");
-  if (mode != 0 && mode != 1) return fail(FH_INVALID_ARGUMENT, "fh_pool2d_grad: mode must be 0 (max) or 1 (avg)");
+  if (mode < 0 || mode > 2)
+    return fail(FH_INVALID_ARGUMENT, "fh_pool2d_grad: mode must be 0 (max), 1 (avg) or 2 (max, then relu_grad by x)");
   if (geom == nullptr) return fail(FH_INVALID_ARGUMENT, "fh_pool2d_grad: null geometry");
   for (int k = 0; k < 10; ++k)
     if (geom[k] < 0 || geom[k] > 0x7fffffffLL) return fail(FH_INVALID_ARGUMENT, "fh_pool2d_grad: geometry entry out of range");
@@ -1074,11 +1096,11 @@ extern "C" fh_status fh_pool2d_grad(int32_t dtype, int32_t mode, const void* dy,
     return fail(FH_INVALID_ARGUMENT, "fh_pool2d_grad: invalid geometry");
   g.oh = (g.h + 2 * g.ph - g.kh) / g.sh + 1;
   g.ow = (g.w + 2 * g.pw - g.kw) / g.sw + 1;
-  if (mode == 0 && (g.ph >= g.kh || g.pw >= g.kw || (g.oh - 1) * g.sh - g.ph >= g.h || (g.ow - 1) * g.sw - g.pw >= g.w))
+  if (mode != 1 && (g.ph >= g.kh || g.pw >= g.kw || (g.oh - 1) * g.sh - g.ph >= g.h || (g.ow - 1) * g.sw - g.pw >= g.w))
     return fail(FH_INVALID_ARGUMENT, "fh_pool2d_grad: a max-pool window has no valid (non-padding) position");
   const int64_t total = static_cast<int64_t>(g.n) * g.c * g.h * g.w;
   if (total == 0) return FH_OK;
-  if (dy == nullptr || dx == nullptr || (mode == 0 && x == nullptr))
+  if (dy == nullptr || dx == nullptr || (mode != 1 && x == nullptr))
     return fail(FH_INVALID_ARGUMENT, "fh_pool2d_grad: null pointer");
   if (!grid_ok(blocks_for(total))) return fail(FH_INVALID_ARGUMENT, "fh_pool2d_grad: tensor too large");
   return dispatch<PoolGradRun>(dtype, mode, dy, x, dx, g, total, static_cast<hipStream_t>(stream));

@@ -197,6 +197,9 @@ inline constexpr std::string_view kFilterFlipOp = "hip_conv_filter_flip_internal
 // output i [Cin,KH,KW,Cout]
 inline constexpr std::string_view kFilterFlipMultiOp = "hip_conv_filter_flip_multi_internal";
 inline constexpr std::string_view kDilateNhwcOp = "hip_dilate_nhwc_internal";  // attr in_nhwc = 1: dy channels-last
+// relu_grad_internal(x, max_pool2d_grad_internal(dy, x)) as one launch (fh_pool2d_grad mode 2): inputs dy, x and
+// the pool gradient's attributes
+inline constexpr std::string_view kMaxPoolReluGradOp = "hip_max_pool2d_relu_grad_internal";
 // sum over every axis but the last (the bias gradient of channels-last data or of [rows, features]): outputs the
 // sum and an fp32 workspace of per-workgroup partials (see fh_sum_rows).
 inline constexpr std::string_view kSumRowsOp = "hip_sum_rows_internal";

@@ -109,6 +109,32 @@ Status lower_relu_grads(ir::Graph& g) {
   return Status::ok();
 }
 
+// relu_grad_internal(x, m) with m = max_pool2d_grad_internal(dy, x) used only there (the stem of a training graph
+// after lower_relu_grads, x the pool's input and the relu's output) becomes one kMaxPoolReluGradOp node: the pool
+// gradient kernel already holds x where it writes dx, so the mask costs no pass of its own.
+Status lower_pool_relu_grads(ir::Graph& g) {
+  std::unordered_map<const ir::Value*, int> uses;
+  for (const ir::Node* n : g.topological_order())
+    for (const ir::Value* v : n->inputs()) ++uses[v];
+  for (const ir::Value* v : g.outputs()) uses[v] += 1000;
+  const std::vector<ir::Node*> snapshot = g.topological_order();
+  for (ir::Node* n : snapshot) {
+    if (n->op() != "relu_grad_internal" || n->inputs().size() != 2 || n->outputs().size() != 1) continue;
+    ir::Value* m = n->inputs()[1];
+    ir::Node* p = m->producer();
+    if (p == nullptr || p->op() != "max_pool2d_grad_internal" || p->inputs().size() != 2 || uses[m] != 1) continue;
+    if (p->inputs()[1] != n->inputs()[0] || !(p->outputs()[0].type().dtype == n->outputs()[0].type().dtype)) continue;
+    Result<ir::Node*> f = g.create_node(std::string(kMaxPoolReluGradOp), {p->inputs()[0], p->inputs()[1]},
+                                        {n->outputs()[0].type()});
+    if (!f.is_ok()) return f.status();
+    for (const auto& [k, a] : p->attrs()) f.value()->set_attr(k, a);
+    FRAME_RETURN_IF_ERROR(g.replace_all_uses(n->output(0), f.value()->output(0)));
+    FRAME_RETURN_IF_ERROR(g.erase_node(n));
+    FRAME_RETURN_IF_ERROR(g.erase_node(p));
+  }
+  return Status::ok();
+}
+
 // A matmul or conv2d whose result's only use is an elementwise program (a single add/mul/relu/square/gelu node or a
 // fused chain of them) becomes one epilogue node; a second single-use elementwise consumer of that node's result
 // extends its program (conv -> add -> relu of a training graph, whose add and relu the fusion pass left apart while
@@ -1640,6 +1666,7 @@ Result<ir::Graph> lower_for_hip(const ir::Graph& graph, int32_t opt_level) {
   // Attention runs at every level (like the conv lowering), before the epilogue fusion would claim its matmuls.
   FRAME_RETURN_IF_ERROR(lower_attention(work.value()));
   if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_relu_grads(work.value()));
+  if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_pool_relu_grads(work.value()));
   if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_epilogues(work.value()));
   if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_gemm_softmax(work.value()));
   if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_grouped_gemms(work.value()));

@@ -630,22 +630,24 @@ Status matmul_grad_kernel(KernelContext& ctx) {
 
 template <int Mode>
 Status pool_grad_kernel(KernelContext& ctx) {
-  const std::string op = Mode == 0 ? "max_pool2d_grad_internal" : "avg_pool2d_grad_internal";
-  FRAME_RETURN_IF_ERROR(arity(ctx, op, Mode == 0 ? 2 : 1, 1));
+  const std::string op = Mode == 0 ? "max_pool2d_grad_internal"
+                         : Mode == 1 ? "avg_pool2d_grad_internal"
+                                     : std::string(kMaxPoolReluGradOp);
+  FRAME_RETURN_IF_ERROR(arity(ctx, op, Mode == 1 ? 1 : 2, 1));
   FRAME_RETURN_IF_ERROR(same_dtype(ctx, op));
   const Shape* xs = attr<Shape>(ctx, "input_shape");
   if (xs == nullptr) return invalid(op, "missing attribute 'input_shape'");
   Result<std::array<int64_t, 10>> g = pool_geom(ctx, op, *xs);
   if (!g.is_ok()) return g.status();
   if (ctx.outputs[0].shape() != *xs) return invalid(op, "output shape does not match input_shape");
-  if (Mode == 0 && ctx.inputs[1].shape() != *xs) return invalid(op, "x shape does not match input_shape");
+  if (Mode != 1 && ctx.inputs[1].shape() != *xs) return invalid(op, "x shape does not match input_shape");
   const auto& geom = g.value();
   const int64_t oh = (geom[2] + 2 * geom[8] - geom[4]) / geom[6] + 1, ow = (geom[3] + 2 * geom[9] - geom[5]) / geom[7] + 1;
   if (ctx.inputs[0].shape() != Shape({geom[0], geom[1], oh, ow})) return invalid(op, "dy shape does not match the geometry");
   Result<int32_t> dt = float_code(op, ctx.outputs[0].dtype());
   if (!dt.is_ok()) return dt.status();
   FRAME_HIP_RETURN_IF_ERROR(fh_pool2d_grad(dt.value(), Mode, ctx.inputs[0].raw_data(),
-                                           Mode == 0 ? ctx.inputs[1].raw_data() : nullptr, ctx.outputs[0].raw_data(),
+                                           Mode != 1 ? ctx.inputs[1].raw_data() : nullptr, ctx.outputs[0].raw_data(),
                                            geom.data(), stream_handle(ctx)),
                             "op '" + op + "' (hip)");
   return Status::ok();
@@ -1075,6 +1077,7 @@ FRAME_REGISTER_KERNEL("matmul_grad_lhs_internal", kHipBackendName, &matmul_grad_
 FRAME_REGISTER_KERNEL("matmul_grad_rhs_internal", kHipBackendName, &matmul_grad_kernel<1>);
 FRAME_REGISTER_KERNEL("max_pool2d_grad_internal", kHipBackendName, &pool_grad_kernel<0>);
 FRAME_REGISTER_KERNEL("avg_pool2d_grad_internal", kHipBackendName, &pool_grad_kernel<1>);
+FRAME_REGISTER_KERNEL(kMaxPoolReluGradOp, kHipBackendName, &pool_grad_kernel<2>);
 FRAME_REGISTER_KERNEL("conv2d_grad_input_internal", kHipBackendName, &conv_grad_kernel<0>);
 FRAME_REGISTER_KERNEL("conv2d_grad_filter_internal", kHipBackendName, &conv_grad_kernel<1>);
 FRAME_REGISTER_KERNEL(kFilterFlipOp, kHipBackendName, &filter_flip_kernel);

@@ -339,6 +339,8 @@ fh_status fh_matmul_grad(int32_t dtype, int32_t rhs, const void* p, const void* 
                          int64_t k, void* stream);
 
 /* max_pool2d_grad_internal (mode 0; x = the forward input) / avg_pool2d_grad_internal (mode 1; x unused), NCHW.
+ * Mode 2 (no reference counterpart) is mode 0 followed by relu_grad_internal against x, dx = x > 0 ? mode 0's dx
+ * : 0, bit for bit the two ops' result: the stem of a training graph, whose pool input is a relu's output.
  * geom as fh_pool2d (the forward input's dims). One thread per input element gathers its covering windows in the
  * reference's order, so results are bit-identical to the CPU reference (src/backends/cpu/kernels/pool.cpp:186-206,
  * 358-388, 543-566). Replaces the recompute-y + cudnnPoolingBackward of max_pool2d_grad_internal

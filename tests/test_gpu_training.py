@@ -183,6 +183,28 @@ def test_pool_grads(dev, dtype, case):
     assert_bitwise(got[0], want[0], "avg_pool2d_grad")
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("case", [c for c in POOL_CASES if c[4] == 3])
+def test_max_pool_relu_grad(dev, dtype, case):
+    """relu_grad_internal(x, max_pool2d_grad_internal(dy, x)) lowers to one fused launch (fh_pool2d_grad mode 2)
+    on hip; the oracle runs the two ops. x holds negatives, zeros and ties."""
+    n, c, h, w, kk, s, p = case
+    say(f"max_pool relu grad {case} dtype={dtype}")
+    oh, ow = conv_out(h, kk, s, p), conv_out(w, kk, s, p)
+    xs, dys = (n, c, h, w), (n, c, oh, ow)
+    x, dy = tensors(60, [xs, dys], dtype)
+    x.reshape(-1)[::7] = x.reshape(-1)[3]
+    x.reshape(-1)[::5] = 0
+    attrs = {"kernel": [kk, kk], "stride": [s, s], "padding": [p, p], "input_shape": graphs.Shape(xs)}
+    g = graphs.Graph("hip")
+    vdy, vx = g.input(dtype, dys), g.input(dtype, xs)
+    m = g.op("max_pool2d_grad_internal", [vdy, vx], xs, attrs)
+    g.output(g.op("relu_grad_internal", [vx, m], xs, {}))
+    assert "hip_max_pool2d_relu_grad_internal" in host.hip_lowered(g.text(), 1)
+    got, want = both(g, [dy, x])
+    assert_bitwise(got[0], want[0], "max_pool2d relu grad")
+
+
 # ---- sum, sum_grad, mse_loss -----------------------------------------------------------------------------------
 
 SUM_CASES = [((4, 6, 5, 7), [0, 2, 3], False), ((4, 6, 5, 7), [], False), ((33, 1000), [1], True),
