@@ -339,6 +339,23 @@ __global__ __launch_bounds__(256) void gemm_seq_kernel(GemmArgs args) {
     const float* ar = &As[buf][r * kKP];
     const float* br = &Bt[buf][c * kKP];
     int kk = 0;
+    // 16 k per step: the four LDS reads of each operand are issued before the sum uses them, so one LDS latency
+    // covers 16 k instead of 4 (the sum itself is the same chain, in the same order)
+    for (; kk + 16 <= kn; kk += 16) {
+      float4 a[4], b[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        a[u] = *reinterpret_cast<const float4*>(ar + kk + 4 * u);
+        b[u] = *reinterpret_cast<const float4*>(br + kk + 4 * u);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        acc = acc + a[u].x * b[u].x;
+        acc = acc + a[u].y * b[u].y;
+        acc = acc + a[u].z * b[u].z;
+        acc = acc + a[u].w * b[u].w;
+      }
+    }
     for (; kk + 4 <= kn; kk += 4) {
       const float4 a = *reinterpret_cast<const float4*>(ar + kk);
       const float4 b = *reinterpret_cast<const float4*>(br + kk);

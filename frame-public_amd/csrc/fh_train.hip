@@ -471,12 +471,16 @@ __global__ __launch_bounds__(kThreads) void filter_flip_kernel(const S* __restri
 // over 64 workgroups (with eight, its eight workgroups took longer than the gather form).
 constexpr int kFlipCo = 64, kFlipCi = 1;
 // Workgroup (bx, by) of one filter's flip: output channels [64 bx, 64 bx + 64), input channels
-// [ci_per by, ci_per by + ci_per); the tile takes kFlipCo * (ci_per * taps + 1) elements of LDS.
-template <typename S>
+// [ci_per by, ci_per by + ci_per); the tile takes kFlipCo * (ci_per * taps + 1) elements of LDS. TAPS and CIP > 0:
+// a whole tile (64 output and CIP input channels) of a TAPS-tap filter, whose index divisions become constant
+// ones (the runtime divisions made the kernel bound by integer instructions).
+template <typename S, int TAPS = 0, int CIP = 0>
 __device__ __forceinline__ void filter_flip_tile(const S* __restrict__ w, S* __restrict__ out, int32_t cout, int32_t cin,
-                                                 int32_t taps, int32_t ci_per, int32_t bx, int32_t by, S* tile) {
+                                                 int32_t taps_rt, int32_t ci_per_rt, int32_t bx, int32_t by, S* tile) {
+  constexpr bool FIXED = TAPS > 0 && CIP > 0;
+  const int32_t taps = FIXED ? TAPS : taps_rt, ci_per = FIXED ? CIP : ci_per_rt;
   const int32_t co0 = bx * kFlipCo, ci0 = by * ci_per;
-  const int32_t nco = min(kFlipCo, cout - co0), nci = min(ci_per, cin - ci0);
+  const int32_t nco = FIXED ? kFlipCo : min(kFlipCo, cout - co0), nci = FIXED ? CIP : min(ci_per, cin - ci0);
   const int32_t run = nci * taps, pitch = ci_per * taps + 1;
   const S* src = w + static_cast<int64_t>(co0) * cin * taps + static_cast<int64_t>(ci0) * taps;
   for (int32_t e = threadIdx.x; e < nco * run; e += kThreads) {
@@ -522,8 +526,16 @@ __global__ __launch_bounds__(kThreads) void filter_flip_multi_kernel(FlipBatch a
   const int32_t local = g - a.first_block[i];
   const int32_t tiles_co = (a.cout[i] + kFlipCo - 1) / kFlipCo;
   const int32_t by = local / tiles_co, bx = local - by * tiles_co;
-  filter_flip_tile<S>(static_cast<const S*>(a.w[i]), static_cast<S*>(a.out[i]), a.cout[i], a.cin[i], a.taps[i],
-                      a.ci_per, bx, by, reinterpret_cast<S*>(flip_smem));
+  const S* w = static_cast<const S*>(a.w[i]);
+  S* out = static_cast<S*>(a.out[i]);
+  S* tile = reinterpret_cast<S*>(flip_smem);
+  const bool whole = (bx + 1) * kFlipCo <= a.cout[i] && (by + 1) * a.ci_per <= a.cin[i] && a.ci_per == 8;
+  if (whole && a.taps[i] == 9)
+    filter_flip_tile<S, 9, 8>(w, out, a.cout[i], a.cin[i], 9, 8, bx, by, tile);
+  else if (whole && a.taps[i] == 1)
+    filter_flip_tile<S, 1, 8>(w, out, a.cout[i], a.cin[i], 1, 8, bx, by, tile);
+  else
+    filter_flip_tile<S>(w, out, a.cout[i], a.cin[i], a.taps[i], a.ci_per, bx, by, tile);
 }
 
 // out_i = x_i + round(s_i * y_i) for up to FH_AXPY_MAX tensors: workgroups are dealt to the tensors by
