@@ -253,6 +253,7 @@ __device__ inline float gelu_grad(float x, float gy) {
 
 __device__ inline float ew_binary(uint8_t op, float a, float b) {
   if (op == FH_EW_RELU_GRAD) return a > 0.0f ? b : 0.0f;
+  if (op == FH_EW_RELU_MASK) return b > 0.0f ? a : 0.0f;
   if (op == FH_EW_GELU_GRAD) return gelu_grad(a, b);
   return op == FH_EW_MUL ? a * b : a + b;
 }
@@ -261,7 +262,7 @@ __device__ inline float ew_binary(uint8_t op, float a, float b) {
 __host__ __device__ constexpr bool epilogue_op_ok(uint8_t op) { return op >= FH_EW_ADD && op <= FH_EW_GELU; }
 
 __host__ __device__ constexpr bool ew_is_binary(uint8_t op) {
-  return op == FH_EW_ADD || op == FH_EW_MUL || op == FH_EW_RELU_GRAD || op == FH_EW_GELU_GRAD;
+  return op == FH_EW_ADD || op == FH_EW_MUL || op == FH_EW_RELU_GRAD || op == FH_EW_GELU_GRAD || op == FH_EW_RELU_MASK;
 }
 
 // The fused elementwise program of a GEMM / conv epilogue (EpilogueArgs, ConvEpilogue: nseg, round_between,

@@ -218,7 +218,8 @@ __global__ __launch_bounds__(kEwThreads) void ew_vec_kernel(EwArgs a) {
         case FH_EW_ADD:
         case FH_EW_MUL:
         case FH_EW_RELU_GRAD:
-        case FH_EW_GELU_GRAD: {
+        case FH_EW_GELU_GRAD:
+        case FH_EW_RELU_MASK: {
           ew_u4 t = cur[0];
 #pragma unroll
           for (int k = 1; k < NIN; ++k)
@@ -363,6 +364,7 @@ bool launch_fixed(const EwArgs& a, dim3 grid, hipStream_t stream) {
     if (o0 == FH_EW_ADD && o1 == FH_EW_GELU) FH_EW_FIXED(FH_EW_ADD, FH_EW_GELU);
     if (o0 == FH_EW_ADD && o1 == FH_EW_ADD) FH_EW_FIXED(FH_EW_ADD, FH_EW_ADD);
     if (o0 == FH_EW_MUL && o1 == FH_EW_ADD) FH_EW_FIXED(FH_EW_MUL, FH_EW_ADD);
+    if (o0 == FH_EW_ADD && o1 == FH_EW_RELU_MASK) FH_EW_FIXED(FH_EW_ADD, FH_EW_RELU_MASK);
   }
 #undef FH_EW_FIXED
   return false;
@@ -494,7 +496,7 @@ extern "C" fh_status fh_ew_program(int32_t dtype, int32_t nseg, const uint8_t* o
   int expected = 0;
   for (int s = 0; s < nseg; ++s) {
     const uint8_t op = ops[s];
-    if (op < FH_EW_ADD || op > FH_EW_GELU_GRAD)
+    if (op < FH_EW_ADD || op > FH_EW_RELU_MASK)
       return fail(FH_INVALID_ARGUMENT, "fh_ew_program: unknown op code " + std::to_string(op));
     const int want = ew_is_binary(op) ? 2 : 1;
     if (arities[s] != want)

@@ -200,6 +200,9 @@ inline constexpr std::string_view kDilateNhwcOp = "hip_dilate_nhwc_internal";  /
 // relu_grad_internal(x, max_pool2d_grad_internal(dy, x)) as one launch (fh_pool2d_grad mode 2): inputs dy, x and
 // the pool gradient's attributes
 inline constexpr std::string_view kMaxPoolReluGradOp = "hip_max_pool2d_relu_grad_internal";
+// an elementwise program of fh_ew_op codes (attr ew_ops), inputs in program order: programs the reference's fused
+// chains cannot name (relu_grad(x, a + b) as add then FH_EW_RELU_MASK by x)
+inline constexpr std::string_view kEwProgramOp = "hip_ew_program_internal";
 // sum over every axis but the last (the bias gradient of channels-last data or of [rows, features]): outputs the
 // sum and an fp32 workspace of per-workgroup partials (see fh_sum_rows).
 inline constexpr std::string_view kSumRowsOp = "hip_sum_rows_internal";

@@ -135,6 +135,35 @@ Status lower_pool_relu_grads(ir::Graph& g) {
   return Status::ok();
 }
 
+// relu_grad_internal(x, s) with s = add(a, b) used only there (a residual block's gradient: the sum of its two
+// consumers' gradients, then the block relu's mask) becomes one kEwProgramOp node [add, FH_EW_RELU_MASK] over
+// (a, b, x): the sum is rounded as the add node stores it and masked as relu_grad does, bit for bit, in one pass.
+Status lower_masked_adds(ir::Graph& g) {
+  std::unordered_map<const ir::Value*, int> uses;
+  for (const ir::Node* n : g.topological_order())
+    for (const ir::Value* v : n->inputs()) ++uses[v];
+  for (const ir::Value* v : g.outputs()) uses[v] += 1000;
+  const std::vector<ir::Node*> snapshot = g.topological_order();
+  for (ir::Node* n : snapshot) {
+    if (n->op() != "relu_grad_internal" || n->inputs().size() != 2 || n->outputs().size() != 1) continue;
+    ir::Value* s = n->inputs()[1];
+    ir::Node* p = s->producer();
+    if (p == nullptr || p->op() != "add" || p->inputs().size() != 2 || uses[s] != 1) continue;
+    const ir::TensorType& t = n->outputs()[0].type();
+    bool same = true;
+    for (const ir::Value* v : {p->inputs()[0], p->inputs()[1], n->inputs()[0], s})
+      same = same && v->type().dtype == t.dtype && v->type().shape == t.shape;
+    if (!same) continue;
+    Result<ir::Node*> f = g.create_node(std::string(kEwProgramOp), {p->inputs()[0], p->inputs()[1], n->inputs()[0]}, {t});
+    if (!f.is_ok()) return f.status();
+    f.value()->set_attr("ew_ops", ir::AttrValue{std::vector<int64_t>{FH_EW_ADD, FH_EW_RELU_MASK}});
+    FRAME_RETURN_IF_ERROR(g.replace_all_uses(n->output(0), f.value()->output(0)));
+    FRAME_RETURN_IF_ERROR(g.erase_node(n));
+    FRAME_RETURN_IF_ERROR(g.erase_node(p));
+  }
+  return Status::ok();
+}
+
 // A matmul or conv2d whose result's only use is an elementwise program (a single add/mul/relu/square/gelu node or a
 // fused chain of them) becomes one epilogue node; a second single-use elementwise consumer of that node's result
 // extends its program (conv -> add -> relu of a training graph, whose add and relu the fusion pass left apart while
@@ -464,7 +493,8 @@ std::unordered_set<const ir::Value*> plan_channels_last(const ir::Graph& src) {
     if (ra != rb) parent[ra] = rb;
   };
   auto is_ew = [](const ir::Node* n) {
-    return ew_code(n->op()) != 0 || n->op() == ops::kFusedElementwiseOpName || n->op() == "relu_grad_internal";
+    return ew_code(n->op()) != 0 || n->op() == ops::kFusedElementwiseOpName || n->op() == "relu_grad_internal" ||
+           n->op() == kEwProgramOp;
   };
   auto is_pool = [](const ir::Node* n) { return n->op() == "max_pool2d" || n->op() == "avg_pool2d"; };
   auto rank4 = [](const ir::Value* v) { return v->type().shape.rank() == 4; };
@@ -1667,6 +1697,7 @@ Result<ir::Graph> lower_for_hip(const ir::Graph& graph, int32_t opt_level) {
   FRAME_RETURN_IF_ERROR(lower_attention(work.value()));
   if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_relu_grads(work.value()));
   if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_pool_relu_grads(work.value()));
+  if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_masked_adds(work.value()));
   if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_epilogues(work.value()));
   if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_gemm_softmax(work.value()));
   if (opt_level >= 1) FRAME_RETURN_IF_ERROR(lower_grouped_gemms(work.value()));

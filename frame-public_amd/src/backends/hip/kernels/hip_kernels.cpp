@@ -112,6 +112,26 @@ Status fused_kernel(KernelContext& ctx) {
   return run_program(ctx, op, codes, ar);
 }
 
+Status ew_program_kernel(KernelContext& ctx) {
+  const std::string op(kEwProgramOp);
+  if (ctx.outputs.size() != 1) return invalid(op, "expects 1 output");
+  const auto* prog = attr<std::vector<int64_t>>(ctx, "ew_ops");
+  if (prog == nullptr || prog->empty() || prog->size() > FH_MAX_SEGMENTS) return invalid(op, "missing or malformed ew_ops");
+  std::vector<uint8_t> codes;
+  std::vector<int8_t> ar;
+  size_t need = 0;
+  for (size_t i = 0; i < prog->size(); ++i) {
+    const int64_t c = (*prog)[i];
+    if (c < FH_EW_ADD || c > FH_EW_RELU_MASK) return invalid(op, "unknown op code " + std::to_string(c));
+    const bool binary = c == FH_EW_ADD || c == FH_EW_MUL || c == FH_EW_RELU_GRAD || c == FH_EW_GELU_GRAD || c == FH_EW_RELU_MASK;
+    codes.push_back(static_cast<uint8_t>(c));
+    ar.push_back(binary ? 2 : 1);
+    need += i == 0 ? (binary ? 2 : 1) : (binary ? 1 : 0);
+  }
+  if (ctx.inputs.size() != need) return invalid(op, "expects " + std::to_string(need) + " inputs");
+  return run_program(ctx, op, codes, ar);
+}
+
 // ---- contractions -----------------------------------------------------------------------------------------
 
 // Epilogue operands are ctx.inputs[first..]; binary segments consume them in order.
@@ -1045,6 +1065,7 @@ FRAME_REGISTER_KERNEL("relu", kHipBackendName, (&ew_kernel<FH_EW_RELU, 1>));
 FRAME_REGISTER_KERNEL("square", kHipBackendName, (&ew_kernel<FH_EW_SQUARE, 1>));
 FRAME_REGISTER_KERNEL("gelu", kHipBackendName, (&ew_kernel<FH_EW_GELU, 1>));
 FRAME_REGISTER_KERNEL(ops::kFusedElementwiseOpName, kHipBackendName, &fused_kernel);
+FRAME_REGISTER_KERNEL(kEwProgramOp, kHipBackendName, &ew_program_kernel);
 FRAME_REGISTER_KERNEL("matmul", kHipBackendName, &matmul_kernel);
 FRAME_REGISTER_KERNEL(kGemmEpilogueOp, kHipBackendName, &gemm_epilogue_kernel);
 FRAME_REGISTER_KERNEL(kGemmGroupedOp, kHipBackendName, &gemm_grouped_kernel);

@@ -58,7 +58,10 @@ typedef enum fh_ew_op {
   FH_EW_TANH = 8,
   FH_EW_RSQRT = 9,
   /* gelu_grad_internal(x, gy) = gy * (Phi(x) + x phi(x)): binary like FH_EW_RELU_GRAD; no reference counterpart */
-  FH_EW_GELU_GRAD = 10
+  FH_EW_GELU_GRAD = 10,
+  /* relu_grad_internal with its operands the other way round: the running value where the next input is > 0, else
+   * 0 (so a program can mask a sum it has just formed: add then mask = relu_grad(x, a + b)); no reference counterpart */
+  FH_EW_RELU_MASK = 11
 } fh_ew_op;
 
 #define FH_MAX_SEGMENTS 8

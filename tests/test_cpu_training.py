@@ -333,7 +333,11 @@ def test_resnet_training_graph_stays_channels_last():
     # relu_grad reads the relus' outputs, so every forward relu fuses into its conv as in the inference graph (the
     # eight residual blocks as add;relu) and the stem's input is packed once for the conv and its filter gradient
     ops = re.findall(r"= (\w+)\(", low)
-    assert "relu" not in ops and ops.count("relu_grad_internal") == 16
+    assert "relu" not in ops
+    # seven residual outputs' gradients (the sum of their two consumers' gradients, then the relu mask) are one
+    # add-then-mask program each; the eighth block output's sum feeds the stem's pool gradient
+    assert ops.count("hip_ew_program_internal") == 7 and low.count("ew_ops=[1, 11]") == 7
+    assert ops.count("relu_grad_internal") == 9 and ops.count("add") == 1
     # the stem's relu gradient is the max-pool gradient's mask (one launch; the pool input is the relu's output)
     assert ops.count("hip_max_pool2d_relu_grad_internal") == 1 and "max_pool2d_grad_internal" not in ops
     assert low.count("ep_ops=[1, 3]") == 8 and low.count("ep_ops=[3]") == 9

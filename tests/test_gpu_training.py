@@ -184,6 +184,22 @@ def test_pool_grads(dev, dtype, case):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("shape", [(2, 64, 9, 9), (3, 1000, 17), (5, 7)])
+def test_masked_gradient_sum(dev, dtype, shape):
+    """relu_grad_internal(x, add(a, b)) lowers to one add-then-mask program (FH_EW_RELU_MASK) on hip; the oracle
+    runs the add and the relu_grad. x holds zeros and negatives; odd sizes take the element tail."""
+    say(f"masked gradient sum {shape} dtype={dtype}")
+    a, b, x = tensors(70, [shape, shape, shape], dtype)
+    x.reshape(-1)[::4] = 0
+    g = graphs.Graph("hip")
+    va, vb, vx = g.input(dtype, shape), g.input(dtype, shape), g.input(dtype, shape)
+    g.output(g.op("relu_grad_internal", [vx, g.add(va, vb)], shape, {}))
+    assert "ew_ops=[1, 11]" in host.hip_lowered(g.text(), 1)
+    got, want = both(g, [a, b, x])
+    assert_bitwise(got[0], want[0], "masked gradient sum")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("case", [c for c in POOL_CASES if c[4] == 3])
 def test_max_pool_relu_grad(dev, dtype, case):
     """relu_grad_internal(x, max_pool2d_grad_internal(dy, x)) lowers to one fused launch (fh_pool2d_grad mode 2)
