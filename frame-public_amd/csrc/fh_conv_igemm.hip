@@ -1867,21 +1867,30 @@ __global__ __launch_bounds__(256) void transpose_planes_multi_kernel(PlaneBatch 
 // values (144 contiguous bytes) and writes 9 vectors of 8 channels, one per tap; a 1x1 plane is its own
 // transpose (a copy). Lanes of one store write consecutive 16-byte vectors.
 __global__ __launch_bounds__(256) void transpose_filters_vec_kernel(PlaneBatch a) {
+  __shared__ uint4 stage[256 * 9];
   const int ti = blockIdx.y;
   const int rows = a.rows[ti], cols = a.cols[ti], groups = rows / 8;
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= static_cast<int64_t>(a.batch[ti]) * groups) return;
+  const int64_t total = static_cast<int64_t>(a.batch[ti]) * groups;  // (co, 8-channel group) pairs
+  const int64_t i0 = static_cast<int64_t>(blockIdx.x) * 256, i = i0 + threadIdx.x;
+  if (i0 >= total) return;  // the whole workgroup
   const int64_t co = i / groups, cg = i - co * groups;
   const uint16_t* x = static_cast<const uint16_t*>(a.x[ti]);
   uint16_t* y = static_cast<uint16_t*>(a.y[ti]);
   if (cols == 1) {
-    *reinterpret_cast<uint4*>(y + co * rows + cg * 8) = *reinterpret_cast<const uint4*>(x + co * rows + cg * 8);
+    if (i < total)
+      *reinterpret_cast<uint4*>(y + co * rows + cg * 8) = *reinterpret_cast<const uint4*>(x + co * rows + cg * 8);
     return;
   }
-  const uint4* src = reinterpret_cast<const uint4*>(x + (co * rows + cg * 8) * 9);
+  // pair i's 72 values are the nine vectors 9i .. 9i + 8 of x, so the workgroup's pairs read one contiguous run:
+  // staged through LDS with consecutive lanes on consecutive vectors, then each thread takes its nine
+  const int32_t nvec = static_cast<int32_t>(min<int64_t>(256, total - i0)) * 9;
+  const uint4* src = reinterpret_cast<const uint4*>(x) + i0 * 9;
+  for (int32_t q = threadIdx.x; q < nvec; q += 256) stage[q] = src[q];
+  __syncthreads();
+  if (i >= total) return;
   uint4 v[9];
 #pragma unroll
-  for (int q = 0; q < 9; ++q) v[q] = src[q];
+  for (int q = 0; q < 9; ++q) v[q] = stage[threadIdx.x * 9 + q];
   // value (channel c, tap t) is element c * 9 + t of the 72 loaded
   auto value = [&](int f) -> uint32_t {
     const uint32_t w = uint4_word(v[f / 8], (f % 8) / 2);
