@@ -1,6 +1,6 @@
 """The hip plugin as a drop-in for the reference tree, host-only.
 
-* Lint: the plugin's sources, placed where INTEGRATION.md puts them (src/backends/hip/), pass the rules of the
+* Lint: the plugin's sources, placed where a drop-in puts them (src/backends/hip/), pass the rules of the
   reference's CI script that apply to a backend directory (scripts/check_iron_rules.sh:102-112 no dynamic_cast /
   typeid, :178-188 no runtime dtype branch in kernels/, :190-201 no throw, :158-176 tagged to-do markers,
   :203-221 no Backend::launch call outside src/runtime/, :242-256 no include of another backend or of a core
